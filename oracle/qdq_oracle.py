@@ -1,0 +1,218 @@
+"""CPU oracle for the fake-quantization (QuantizeDequantize) path — TEST INFRASTRUCTURE.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg use
+this module, and only as the checker / CPU baseline.  The product path never imports it.
+
+numpy restatement of aimet_torch's fake-quantization numerics, fp32 arithmetic with
+IEEE round-half-to-even (``np.rint``) and fp64 accumulation of encoding gradients:
+
+* ``qdq_frozen``      — torch.fake_quantize_per_{tensor,channel}_affine as called by the
+  frozen-encoding fast path (torch_builtins.py:287-361): ``q = rint(x * fl(1/s)) + zp``,
+  ``y = (clamp(q) - zp) * s``, NaN restored (:249), +-inf saturated (the grid contract of
+  tests/integration/test_native_qdq_alignment.py:139-147).
+* ``qdq_learnable``   — QuantDequantFunc.forward (torch_builtins.py:640-672).
+* ``qdq_learnable_backward`` — QuantDequantFunc.backward (:675-691) followed by the
+  reduction of the broadcast scale/offset gradients to the encoding shape.
+* ``quantize`` / ``quantize_backward`` — QuantizeFunc (:505-571).
+* ``dequantize`` / ``dequantize_backward`` — DequantizeFunc (:574-615).
+* ``minmax``          — _MinMaxObserver.collect_stats (encoding_analyzer.py:101-105).
+* ``compute_encodings_from_stats`` — MinMaxEncodingAnalyzer (encoding_analyzer.py:217-272).
+* ``scale_offset``    — get_scale / _get_offset (quantizer.py:345-403).
+
+Pinned by tests/test_qdq_oracle.py against: torch's own fake_quantize kernels (the
+reference's frozen path, third-party, exact); the reference's docstring tables
+(backends/__init__.py:169-187, 336-354); the ties-to-even, reciprocal and saturation
+tables of test_native_qdq_alignment.py:94-147; and an independent autograd derivation
+of the STE gradients (torch autograd through a straight-through surrogate).
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+f32 = np.float32
+
+
+def layout_view(x: np.ndarray, outer: int, C: int, inner: int) -> np.ndarray:
+    """View x as [outer, C, inner]."""
+    return x.reshape(outer, C, inner)
+
+
+def _bcast(v, C):
+    v = np.asarray(v, dtype=f32).reshape(-1)
+    if v.size == 1 and C != 1:
+        v = np.full(C, v[0], dtype=f32)
+    return v.reshape(1, C, 1)
+
+
+def _clamp_keep_nan(v, lo, hi):
+    out = np.where(v < lo, lo, np.where(v > hi, hi, v))
+    return out.astype(f32)
+
+
+def qdq_frozen(x, scale, offset, qmin, qmax, layout):
+    outer, C, inner = layout
+    xv = layout_view(np.asarray(x, dtype=f32), outer, C, inner)
+    s = _bcast(scale, C)
+    inv_s = (f32(1.0) / s).astype(f32)
+    zp = -np.trunc(_bcast(offset, C)).astype(f32)
+    with np.errstate(invalid="ignore", over="ignore"):
+        r = (np.rint((xv * inv_s).astype(f32)) + zp).astype(f32)
+        q = _clamp_keep_nan(r, f32(qmin), f32(qmax))
+        y = ((q - zp).astype(f32) * s).astype(f32)
+        mask = (r >= qmin) & (r <= qmax)
+    return y.reshape(np.shape(x)), mask.reshape(np.shape(x))
+
+
+def qdq_learnable(x, scale, offset, qmin, qmax, layout):
+    outer, C, inner = layout
+    xv = layout_view(np.asarray(x, dtype=f32), outer, C, inner)
+    s = _bcast(scale, C)
+    o = _bcast(offset, C)
+    with np.errstate(invalid="ignore", over="ignore", divide="ignore"):
+        r = (np.rint((xv / s).astype(f32)) - o).astype(f32)
+        mask = (r >= qmin) & (r <= qmax)
+        q = _clamp_keep_nan(r, f32(qmin), f32(qmax))
+        y = ((q + o).astype(f32) * s).astype(f32)
+    return y.reshape(np.shape(x)), mask.reshape(np.shape(x))
+
+
+def qdq_learnable_backward(x, g, scale, offset, qmin, qmax, layout):
+    """Return (dx, dscale[C], doffset[C]); sums accumulated in fp64."""
+    outer, C, inner = layout
+    xv = layout_view(np.asarray(x, dtype=f32), outer, C, inner)
+    gv = layout_view(np.asarray(g, dtype=f32), outer, C, inner)
+    s = _bcast(scale, C)
+    o = _bcast(offset, C)
+    with np.errstate(invalid="ignore", over="ignore", divide="ignore"):
+        xs = (xv / s).astype(f32)
+        rr = np.rint(xs).astype(f32)
+        r = (rr - o).astype(f32)
+        m = ((r >= qmin) & (r <= qmax)).astype(f32)
+        dx = (gv * m).astype(f32)
+        lo = (o + f32(qmin)).astype(f32)
+        hi = (o + f32(qmax)).astype(f32)
+        ds_el = (gv * (_clamp_keep_nan(rr, lo, hi) - (xs * m).astype(f32)).astype(f32)).astype(f32)
+        do_el = (gv * ((f32(1.0) - m) * s).astype(f32)).astype(f32)
+    ds = ds_el.astype(np.float64).sum(axis=(0, 2))
+    do = do_el.astype(np.float64).sum(axis=(0, 2))
+    return dx.reshape(np.shape(x)), ds.astype(f32), do.astype(f32)
+
+
+def qdq_frozen_backward(x, g, scale, offset, qmin, qmax, layout):
+    _, mask = qdq_frozen(x, scale, offset, qmin, qmax, layout)
+    return (np.asarray(g, dtype=f32) * mask.astype(f32)).astype(f32)
+
+
+def quantize(x, scale, offset, qmin, qmax, layout):
+    outer, C, inner = layout
+    xv = layout_view(np.asarray(x, dtype=f32), outer, C, inner)
+    s, o = _bcast(scale, C), _bcast(offset, C)
+    with np.errstate(invalid="ignore", over="ignore", divide="ignore"):
+        r = (np.rint((xv / s).astype(f32)) - o).astype(f32)
+        q = _clamp_keep_nan(r, f32(qmin), f32(qmax))
+    return q.reshape(np.shape(x))
+
+
+def quantize_backward(x, g, scale, offset, qmin, qmax, layout):
+    outer, C, inner = layout
+    xv = layout_view(np.asarray(x, dtype=f32), outer, C, inner)
+    gv = layout_view(np.asarray(g, dtype=f32), outer, C, inner)
+    s, o = _bcast(scale, C), _bcast(offset, C)
+    with np.errstate(invalid="ignore", over="ignore", divide="ignore"):
+        r = (np.rint((xv / s).astype(f32)) - o).astype(f32)
+        m = ((r >= qmin) & (r <= qmax)).astype(f32)
+        mg = (gv * m).astype(f32)
+        gs = (mg / s).astype(f32)
+        ds_el = (-gs * (xv / s).astype(f32)).astype(f32)
+    ds = ds_el.astype(np.float64).sum(axis=(0, 2))
+    do = (-mg).astype(np.float64).sum(axis=(0, 2))
+    return gs.reshape(np.shape(x)), ds.astype(f32), do.astype(f32)
+
+
+def dequantize(q, scale, offset, layout):
+    outer, C, inner = layout
+    qv = layout_view(np.asarray(q, dtype=f32), outer, C, inner)
+    s, o = _bcast(scale, C), _bcast(offset, C)
+    return ((qv + o).astype(f32) * s).astype(f32).reshape(np.shape(q))
+
+
+def dequantize_backward(q, g, scale, offset, layout):
+    outer, C, inner = layout
+    qv = layout_view(np.asarray(q, dtype=f32), outer, C, inner)
+    gv = layout_view(np.asarray(g, dtype=f32), outer, C, inner)
+    s, o = _bcast(scale, C), _bcast(offset, C)
+    gs = (gv * s).astype(f32)
+    ds = (gv * (qv + o).astype(f32)).astype(f32).astype(np.float64).sum(axis=(0, 2))
+    do = gs.astype(np.float64).sum(axis=(0, 2))
+    return gs.reshape(np.shape(q)), ds.astype(f32), do.astype(f32)
+
+
+def minmax(x, layout):
+    outer, C, inner = layout
+    xv = layout_view(np.asarray(x, dtype=f32), outer, C, inner)
+    # np.min/np.max propagate NaN like torch.min/torch.max.
+    return xv.min(axis=(0, 2)).astype(f32), xv.max(axis=(0, 2)).astype(f32)
+
+
+# ---------------------------------------------------------------------------------
+# Encoding math (fp32, same operation order as the reference)
+# ---------------------------------------------------------------------------------
+
+
+def minimum_scale(num_steps: int) -> float:
+    """aimet_common/quantsim.py:447-480."""
+    raw = min(float(np.finfo(np.float32).eps), 0.01 / num_steps)
+    return float(2.0 ** math.ceil(math.log2(raw)))
+
+
+def sdiv(a, b, gpu_scalar_div: bool):
+    """``tensor / python_scalar`` as PyTorch evaluates it: a true fp32 division on the
+    CPU, but a multiplication by the fp32 reciprocal fl(1/b) on the GPU (aten's
+    div_true kernel for a CPU-scalar divisor).  The reference's encoding math therefore
+    depends on the device its quantizer lives on; pass the device it ran on."""
+    a = np.asarray(a, dtype=f32)
+    if gpu_scalar_div:
+        return (a * f32(f32(1.0) / f32(b))).astype(f32)
+    return (a / f32(b)).astype(f32)
+
+
+def compute_encodings_from_stats(mn, mx, num_steps: int, is_symmetric: bool,
+                                 gpu_scalar_div: bool = False):
+    """MinMaxEncodingAnalyzer.compute_encodings_from_stats (encoding_analyzer.py:217-272)."""
+    mn = np.asarray(mn, dtype=f32)
+    mx = np.asarray(mx, dtype=f32)
+    ms = f32(minimum_scale(num_steps))
+    mn0 = np.minimum(mn, f32(0))
+    mx0 = np.maximum(mx, f32(0))
+    diff = sdiv(mx0 - mn0, num_steps, gpu_scalar_div)
+    adj = (ms * (diff < ms).astype(f32)).astype(f32)
+    if is_symmetric:
+        npos, nneg = num_steps // 2, -(-num_steps // 2)
+        umax = (mx0 + f32(npos) * adj).astype(f32)
+        umin = (mn0 - f32(nneg) * adj).astype(f32)
+        extra = 1 if num_steps == 3 else 0
+        delta = np.maximum(sdiv(umax, npos + extra, gpu_scalar_div),
+                           sdiv(-umin, nneg, gpu_scalar_div))
+        umin = (f32(-nneg) * delta).astype(f32)
+        umax = (f32(npos) * delta).astype(f32)
+    else:
+        umax = (mx0 + f32(num_steps) * adj).astype(f32)
+        umin = mn0
+    fmax = np.finfo(np.float32).max
+    return np.maximum(umin, -fmax).astype(f32), np.minimum(umax, fmax).astype(f32)
+
+
+def scale_offset(mn, mx, qmin: int, qmax: int, symmetric: bool, gpu_scalar_div: bool = False):
+    """get_scale / _get_offset of a min/max-parametrised quantizer (quantizer.py:345-403)."""
+    mn = np.asarray(mn, dtype=f32)
+    mx = np.asarray(mx, dtype=f32)
+    num_steps = qmax - qmin
+    s = np.abs(sdiv(mx - mn, num_steps, gpu_scalar_div))
+    s = np.maximum(s, f32(minimum_scale(num_steps))).astype(f32)
+    if symmetric:
+        o = np.full_like(s, f32(0 if qmin >= 0 else -round((qmin + qmax) / 2)))
+    else:
+        o = np.clip(np.rint((mn / s).astype(f32)) - f32(qmin), -qmax, -qmin).astype(f32)
+    return s, o

@@ -1,0 +1,101 @@
+"""ctypes binding of ``librxmet.so`` (the MI355X C ABI declared in ``include/*.h``).
+
+The library is the only compute path of this package: if it is missing, every entry
+point raises instead of falling back to anything else.  Calls pass raw device pointers
+(``tensor.data_ptr()``) and PyTorch's current HIP stream, so kernels are ordered with
+the caller's other work exactly like aten ops.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+from typing import Optional
+
+_PKG = Path(__file__).resolve().parent
+LIB_PATH = Path(os.environ.get("RXMET_LIB", _PKG / "librxmet.so"))
+
+_lib: Optional[ctypes.CDLL] = None
+
+c_i64 = ctypes.c_int64
+c_int = ctypes.c_int
+c_ptr = ctypes.c_void_p
+c_float = ctypes.c_float
+
+# name -> (restype, argtypes); mirrors include/rxmet_qdq.h and include/rxmet_gru.h
+_SIGNATURES = {
+    "rxmet_last_error": (ctypes.c_char_p, []),
+    "rxmet_abi_version": (c_int, []),
+    "rxmet_qdq_workspace_bytes": (c_i64, [c_i64, c_i64, c_i64]),
+    "rxmet_qdq_minmax": (c_int, [c_ptr, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_ptr, c_ptr]),
+    "rxmet_qdq_forward": (c_int, [c_ptr, c_ptr, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_i64, c_i64,
+                                  c_int, c_ptr]),
+    "rxmet_qdq_backward": (c_int, [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_ptr,
+                                   c_ptr, c_i64, c_i64, c_int, c_ptr, c_ptr]),
+    "rxmet_quantize_forward": (c_int, [c_ptr, c_ptr, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_i64,
+                                       c_i64, c_ptr]),
+    "rxmet_quantize_backward": (c_int, [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64,
+                                        c_ptr, c_ptr, c_i64, c_i64, c_ptr, c_ptr]),
+    "rxmet_dequantize_forward": (c_int, [c_ptr, c_ptr, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_ptr]),
+    "rxmet_dequantize_backward": (c_int, [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64,
+                                          c_ptr, c_ptr, c_ptr, c_ptr]),
+}
+
+# Symbols declared by the headers; tests check the built library exports all of them.
+EXPORTED = tuple(_SIGNATURES)
+
+
+class RxmetError(RuntimeError):
+    """Raised when a C-ABI call reports a failure (argument or HIP error)."""
+
+
+def load() -> ctypes.CDLL:
+    """Load and type the library once; raise if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RxmetError(
+            f"{LIB_PATH} is missing: build it with `python rx-met_amd/build.py` "
+            "(the MI355X kernels have no fallback)")
+    lib = ctypes.CDLL(str(LIB_PATH))
+    for name, (res, args) in _SIGNATURES.items():
+        try:
+            fn = getattr(lib, name)
+        except AttributeError as e:
+            raise RxmetError(f"{LIB_PATH} does not export {name}") from e
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def register(name: str, restype, argtypes) -> None:
+    """Add a signature (used by modules that extend the ABI)."""
+    _SIGNATURES[name] = (restype, argtypes)
+    if _lib is not None:
+        fn = getattr(_lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+
+
+def call(name: str, *args) -> int:
+    """Call ``name`` and raise RxmetError with the library's message on failure."""
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if isinstance(rc, int) and rc != 0:
+        msg = lib.rxmet_last_error().decode(errors="replace")
+        raise RxmetError(f"{name} failed ({rc}): {msg}")
+    return rc
+
+
+def ptr(t) -> Optional[int]:
+    """Device pointer of a tensor, or None for a missing optional argument."""
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(device) -> int:
+    """Handle of PyTorch's current HIP stream on ``device``."""
+    import torch
+
+    return torch.cuda.current_stream(device).cuda_stream

@@ -1,0 +1,40 @@
+"""The C-ABI library builds, loads and exports every entry point include/*.h declares."""
+import re
+from pathlib import Path
+
+import rxmet_lib
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared_symbols():
+    names = set()
+    for h in (ROOT / "include").glob("*.h"):
+        text = h.read_text()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names.update(re.findall(r"\b(rxmet_[a-z0-9_]+)\s*\(", text))
+    return names
+
+
+def test_headers_declare_entry_points():
+    names = declared_symbols()
+    assert "rxmet_qdq_forward" in names and "rxmet_last_error" in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = rxmet_lib.load()
+    missing = [n for n in sorted(declared_symbols()) if not hasattr(lib, n)]
+    assert not missing, f"librxmet.so lacks {missing}"
+
+
+def test_python_signatures_cover_headers():
+    assert declared_symbols() <= set(rxmet_lib.EXPORTED), \
+        sorted(declared_symbols() - set(rxmet_lib.EXPORTED))
+
+
+def test_host_only_calls_work_without_gpu():
+    lib = rxmet_lib.load()
+    assert lib.rxmet_abi_version() >= 1
+    # [8192, 8192] per-channel on dim 0: one partial per channel row
+    assert lib.rxmet_qdq_workspace_bytes(1, 8192, 8192) == 8192 * 16
+    assert lib.rxmet_qdq_workspace_bytes(1, 1, 8192 * 8192) == 8192 * 16

@@ -1,0 +1,242 @@
+"""GPU parity of the QDQ kernels (librxmet.so) against the pinned oracle.
+
+Bar: outputs, masks and dx bit-exact; encoding gradients (fp64-accumulated sums) within
+1e-6 relative of the oracle's fp64 sums; min/max exact.
+"""
+import numpy as np
+import pytest
+import torch
+
+import aimet_affine as A
+import mi355x_qdq as Q
+import qdq_oracle as O
+import rxmet_lib
+
+pytestmark = pytest.mark.gpu
+f32 = np.float32
+
+LAYOUTS = [
+    (1, 1, 100003),      # per-tensor, odd length (scalar tail path)
+    (1, 64, 1000),       # per-channel on dim 0, runs path, inner % 4 == 0
+    (1, 7, 1027),        # per-channel, runs path with unaligned runs
+    (40, 16, 1),         # per-channel on the last dim: column path
+    (3, 8, 50),          # per-channel on a middle dim: column path
+    (2, 5, 2048),        # outer > 1 with long runs
+    (1, 3, 20000),       # runs split into several chunks
+]
+
+
+def _data(n, seed):
+    g = np.random.default_rng(seed)
+    x = g.standard_normal(n).astype(f32)
+    m = g.random(n) < 0.01
+    x[m] = (g.standard_normal(int(m.sum())) * 10).astype(f32)
+    return x
+
+
+def _enc(C, seed, qmin, qmax, symmetric):
+    g = np.random.default_rng(seed)
+    mn = -(g.random(C) * 2 + 0.5).astype(f32)
+    mx = (g.random(C) * 2 + 0.5).astype(f32)
+    return O.scale_offset(mn, mx, qmin, qmax, symmetric)
+
+
+def _t(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _ws(layout, dev):
+    return torch.empty(max(16, rxmet_lib.load().rxmet_qdq_workspace_bytes(*layout)),
+                       dtype=torch.uint8, device=dev)
+
+
+def _stream(dev):
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
+@pytest.mark.parametrize("grid", [(-128, 127, True), (0, 255, False), (-8, 7, True),
+                                  (0, 65535, False)])
+@pytest.mark.parametrize("mode", [Q.LEARNABLE, Q.FROZEN])
+def test_forward_backward_match_oracle(cuda, layout, grid, mode):
+    qmin, qmax, sym = grid
+    outer, C, inner = layout
+    n = outer * C * inner
+    print(f"[qdq] layout={layout} grid={grid} mode={mode}", flush=True)
+    x = _data(n, 1)
+    x[:5] = [np.nan, np.inf, -np.inf, 0.0, -0.0] if n > 5 else x[:5]
+    g = np.random.default_rng(2).standard_normal(n).astype(f32)
+    s, o = _enc(C, 3, qmin, qmax, sym)
+    xd, gd, sd, od = _t(x, cuda), _t(g, cuda), _t(s, cuda), _t(o, cuda)
+    y = torch.empty_like(xd)
+    rxmet_lib.call("rxmet_qdq_forward", xd.data_ptr(), y.data_ptr(), outer, C, inner, sd.data_ptr(),
+                   od.data_ptr(), qmin, qmax, mode, _stream(cuda))
+    dx = torch.empty_like(xd)
+    learn = mode == Q.LEARNABLE
+    ds = torch.empty(C, device=cuda) if learn else None
+    do = torch.empty(C, device=cuda) if learn else None
+    rxmet_lib.call("rxmet_qdq_backward", xd.data_ptr(), gd.data_ptr(), dx.data_ptr(),
+                   rxmet_lib.ptr(ds), rxmet_lib.ptr(do), outer, C, inner, sd.data_ptr(),
+                   od.data_ptr(), qmin, qmax, mode, _ws(layout, cuda).data_ptr(), _stream(cuda))
+    torch.cuda.synchronize()
+    if learn:
+        ey, _ = O.qdq_learnable(x, s, o, qmin, qmax, layout)
+        edx, eds, edo = O.qdq_learnable_backward(x, g, s, o, qmin, qmax, layout)
+    else:
+        ey, _ = O.qdq_frozen(x, s, o, qmin, qmax, layout)
+        edx = O.qdq_frozen_backward(x, g, s, o, qmin, qmax, layout)
+    np.testing.assert_array_equal(y.cpu().numpy(), ey)
+    np.testing.assert_array_equal(dx.cpu().numpy(), edx)
+    if learn:
+        # NaN/inf inputs make the reference's scale gradient NaN for their encoding
+        np.testing.assert_allclose(ds.cpu().numpy(), eds, rtol=1e-6, atol=1e-6, equal_nan=True)
+        np.testing.assert_allclose(do.cpu().numpy(), edo, rtol=1e-6, atol=1e-6, equal_nan=True)
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
+def test_minmax_matches_oracle(cuda, layout):
+    outer, C, inner = layout
+    x = _data(outer * C * inner, 4)
+    mn = torch.empty(C, device=cuda)
+    mx = torch.empty(C, device=cuda)
+    xd = _t(x, cuda)
+    rxmet_lib.call("rxmet_qdq_minmax", xd.data_ptr(), outer, C, inner, mn.data_ptr(), mx.data_ptr(),
+                   _ws(layout, cuda).data_ptr(), _stream(cuda))
+    emn, emx = O.minmax(x, layout)
+    np.testing.assert_array_equal(mn.cpu().numpy(), emn)
+    np.testing.assert_array_equal(mx.cpu().numpy(), emx)
+    x[len(x) // 2] = np.nan
+    xd = _t(x, cuda)
+    rxmet_lib.call("rxmet_qdq_minmax", xd.data_ptr(), outer, C, inner, mn.data_ptr(), mx.data_ptr(),
+                   _ws(layout, cuda).data_ptr(), _stream(cuda))
+    emn, emx = O.minmax(x, layout)
+    np.testing.assert_array_equal(mn.cpu().numpy(), emn)
+    np.testing.assert_array_equal(mx.cpu().numpy(), emx)
+
+
+@pytest.mark.parametrize("layout", [(1, 1, 5001), (1, 4, 3000), (30, 6, 1)])
+def test_quantize_dequantize_kernels(cuda, layout):
+    outer, C, inner = layout
+    n = outer * C * inner
+    x = _data(n, 5)
+    g = np.random.default_rng(6).standard_normal(n).astype(f32)
+    s, o = _enc(C, 7, 0, 255, False)
+    xd, gd, sd, od = (_t(a, cuda) for a in (x, g, s, o))
+    q = torch.empty_like(xd)
+    rxmet_lib.call("rxmet_quantize_forward", xd.data_ptr(), q.data_ptr(), outer, C, inner,
+                   sd.data_ptr(), od.data_ptr(), 0, 255, _stream(cuda))
+    dx = torch.empty_like(xd)
+    ds, do = torch.empty(C, device=cuda), torch.empty(C, device=cuda)
+    rxmet_lib.call("rxmet_quantize_backward", xd.data_ptr(), gd.data_ptr(), dx.data_ptr(),
+                   ds.data_ptr(), do.data_ptr(), outer, C, inner, sd.data_ptr(), od.data_ptr(), 0,
+                   255, _ws(layout, cuda).data_ptr(), _stream(cuda))
+    eq = O.quantize(x, s, o, 0, 255, layout)
+    edx, eds, edo = O.quantize_backward(x, g, s, o, 0, 255, layout)
+    np.testing.assert_array_equal(q.cpu().numpy(), eq)
+    np.testing.assert_array_equal(dx.cpu().numpy(), edx)
+    np.testing.assert_allclose(ds.cpu().numpy(), eds, rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(do.cpu().numpy(), edo, rtol=1e-6, atol=1e-6)
+    y = torch.empty_like(xd)
+    rxmet_lib.call("rxmet_dequantize_forward", q.data_ptr(), y.data_ptr(), outer, C, inner,
+                   sd.data_ptr(), od.data_ptr(), _stream(cuda))
+    rxmet_lib.call("rxmet_dequantize_backward", q.data_ptr(), gd.data_ptr(), dx.data_ptr(),
+                   ds.data_ptr(), do.data_ptr(), outer, C, inner, sd.data_ptr(), od.data_ptr(),
+                   _ws(layout, cuda).data_ptr(), _stream(cuda))
+    ey = O.dequantize(eq, s, o, layout)
+    edq, eds, edo = O.dequantize_backward(eq, g, s, o, layout)
+    np.testing.assert_array_equal(y.cpu().numpy(), ey)
+    np.testing.assert_array_equal(dx.cpu().numpy(), edq)
+    np.testing.assert_allclose(ds.cpu().numpy(), eds, rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(do.cpu().numpy(), edo, rtol=1e-6, atol=1e-6)
+
+
+def test_empty_tensor(cuda):
+    x = torch.empty(0, device=cuda)
+    s = torch.ones(1, device=cuda)
+    y = Q.quantize_dequantize(x, s, torch.zeros(1, device=cuda), -128, 127)
+    assert y.numel() == 0
+
+
+def test_errors_are_raised(cuda):
+    x = torch.randn(10, device=cuda)
+    with pytest.raises(RuntimeError):
+        Q.quantize_dequantize(x, torch.ones(3, device=cuda), torch.zeros(3, device=cuda), 0, 255)
+    with pytest.raises(RuntimeError):
+        Q.quantize_dequantize(x, torch.ones(1, device=cuda), torch.zeros(1, device=cuda), 5, 1)
+
+
+def _module_case(cuda, shape, enc_shape, bits, symmetric, seed, learn=True):
+    """QuantizeDequantize through the aimet mirror vs the oracle pipeline."""
+    x = _data(int(np.prod(shape)), seed).reshape(shape)
+    g = np.random.default_rng(seed + 1).standard_normal(x.shape).astype(f32)
+    q = A.QuantizeDequantize(enc_shape, bits, symmetric).to(cuda)
+    xd = _t(x, cuda)
+    with q.compute_encodings():
+        q(xd)
+    if not learn:
+        q.requires_grad_(False)
+    xg = xd.clone().requires_grad_()
+    y = q(xg)
+    y.backward(_t(g, cuda))
+    layout = Q.kernel_layout(shape, enc_shape)
+    C = layout[1]
+    mn, mx = O.minmax(x, layout)
+    qmin, qmax = q.qmin, q.qmax
+    lo, hi = O.compute_encodings_from_stats(mn, mx, qmax - qmin, symmetric and qmin < 0,
+                                            gpu_scalar_div=True)
+    np.testing.assert_array_equal(q.min.detach().cpu().numpy().reshape(-1), lo)
+    np.testing.assert_array_equal(q.max.detach().cpu().numpy().reshape(-1), hi)
+    s, o = O.scale_offset(lo, hi, qmin, qmax, symmetric, gpu_scalar_div=True)
+    es, eo = q.get_encodings()
+    np.testing.assert_array_equal(es.detach().cpu().numpy().reshape(-1), s)
+    np.testing.assert_array_equal(eo.detach().cpu().numpy().reshape(-1), o)
+    if learn:
+        ey, _ = O.qdq_learnable(x, s, o, qmin, qmax, layout)
+        edx, eds, edo = O.qdq_learnable_backward(x, g, s, o, qmin, qmax, layout)
+    else:
+        ey, _ = O.qdq_frozen(x, s, o, qmin, qmax, layout)
+        edx = O.qdq_frozen_backward(x, g, s, o, qmin, qmax, layout)
+    np.testing.assert_array_equal(y.detach().cpu().numpy(), ey)
+    np.testing.assert_array_equal(xg.grad.cpu().numpy(), edx)
+    if learn:
+        # chain the oracle's encoding gradients through the same min/max -> (s, o) graph
+        pmn = torch.from_numpy(lo.reshape(enc_shape)).requires_grad_()
+        pmx = torch.from_numpy(hi.reshape(enc_shape)).requires_grad_()
+        ref = A.QuantizeDequantize(enc_shape, bits, symmetric)
+        ref.set_range(pmn.detach(), pmx.detach())
+        st = ref.get_scale()
+        ot = ref._get_offset(scale=st)
+        outs = [st] + ([ot] if ot.requires_grad else [])
+        grads = [torch.from_numpy(eds.reshape(st.shape))] + (
+            [torch.from_numpy(edo.reshape(ot.shape))] if ot.requires_grad else [])
+        torch.autograd.backward(outs, grads)
+        np.testing.assert_allclose(q.min.grad.cpu().numpy(), ref.min.grad.numpy(), rtol=1e-5,
+                                   atol=1e-3)
+        np.testing.assert_allclose(q.max.grad.cpu().numpy(), ref.max.grad.numpy(), rtol=1e-5,
+                                   atol=1e-3)
+    return C
+
+
+@pytest.mark.parametrize("learn", [True, False])
+def test_module_per_tensor_8bit_asym(cuda, learn):
+    _module_case(cuda, (512, 768), (), 8, False, 21, learn)
+
+
+@pytest.mark.parametrize("learn", [True, False])
+def test_module_per_channel_4bit_sym(cuda, learn):
+    _module_case(cuda, (512, 768), (512, 1), 4, True, 22, learn)
+
+
+def test_full_size_c2(cuda):
+    """c2 at its full shape [8192, 8192]: both modes against the oracle, plus frozen QDQ
+    against torch's own fake_quantize on the GPU."""
+    shape = (8192, 8192)
+    for enc_shape, bits, sym in (((), 8, False), ((8192, 1), 4, True)):
+        print(f"[qdq] full size enc={enc_shape} bits={bits}", flush=True)
+        _module_case(cuda, shape, enc_shape, bits, sym, 31, learn=True)
+    x = torch.from_numpy(_data(8192 * 8192, 33).reshape(shape)).to(cuda)
+    s = torch.tensor(0.0173, device=cuda)
+    y = Q.quantize_dequantize(x, s, torch.tensor(-3.0, device=cuda), -128, 127)
+    ref = torch.fake_quantize_per_tensor_affine(x, s, torch.tensor(3, dtype=torch.int32,
+                                                                   device=cuda), -128, 127)
+    assert torch.equal(y, ref)

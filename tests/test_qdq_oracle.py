@@ -1,0 +1,234 @@
+"""Pin the fake-quantization oracle (oracle/qdq_oracle.py) before trusting it.
+
+Checks, each chosen so a plausible mistake (wrong rounding mode, 1/s vs /s, sign of
+the offset, a dropped term of a gradient) fails:
+* frozen-encoding mode == torch.fake_quantize_per_{tensor,channel}_affine, the
+  third-party kernels the reference's fast path calls (torch_builtins.py:287-361);
+* the reference's docstring tables (backends/__init__.py:169-187, 336-354);
+* ties-to-even, decimal-reciprocal and NaN/inf tables of
+  tests/integration/test_native_qdq_alignment.py:94-147;
+* learnable-mode gradients == torch autograd through a straight-through surrogate of
+  QuantDequantFunc's forward (an independent derivation of torch_builtins.py:675-691);
+* the encoding analyzer's closed forms (encoding_analyzer.py:217-272, quantsim.py:463-470).
+"""
+import numpy as np
+import pytest
+import torch
+
+import qdq_oracle as O
+
+f32 = np.float32
+
+
+def _data(n, seed, outliers=True):
+    g = np.random.default_rng(seed)
+    x = g.standard_normal(n).astype(f32)
+    if outliers:
+        m = g.random(n) < 0.01
+        x[m] = (g.standard_normal(int(m.sum())) * 10).astype(f32)
+    return x
+
+
+@pytest.mark.parametrize("bits,signed", [(8, True), (8, False), (4, True), (16, True)])
+@pytest.mark.parametrize("scale", [0.0173, 1 / 15, 2.0 ** -5, 0.027019, 1 / 32767])
+def test_frozen_matches_torch_fake_quantize_per_tensor(bits, signed, scale):
+    qmin, qmax = (-(1 << (bits - 1)), (1 << (bits - 1)) - 1) if signed else (0, (1 << bits) - 1)
+    x = _data(20000, 1)
+    for offset in (0.0, float(-qmin - 3) if not signed else 0.0, -5.0 if not signed else 3.0):
+        zp = -int(offset)
+        if not (qmin <= zp <= qmax):
+            continue
+        y, mask = O.qdq_frozen(x, [scale], [offset], qmin, qmax, (1, 1, x.size))
+        xt = torch.from_numpy(x.copy()).requires_grad_()
+        ref = torch.fake_quantize_per_tensor_affine(
+            xt, torch.tensor(scale, dtype=torch.float32), torch.tensor(zp, dtype=torch.int32),
+            qmin, qmax)
+        np.testing.assert_array_equal(y, ref.detach().numpy())
+        ref.backward(torch.ones_like(ref))
+        np.testing.assert_array_equal(mask.astype(f32), xt.grad.numpy())
+
+
+def test_frozen_matches_torch_fake_quantize_per_channel():
+    x = _data(64 * 300, 2).reshape(64, 300)
+    g = np.random.default_rng(3)
+    scale = (g.random(64) * 0.05 + 0.001).astype(f32)
+    for qmin, qmax, offset in ((-8, 7, np.zeros(64, f32)), (0, 255, -np.full(64, 100, f32))):
+        y, mask = O.qdq_frozen(x, scale, offset, qmin, qmax, (1, 64, 300))
+        xt = torch.from_numpy(x.copy()).requires_grad_()
+        ref = torch.fake_quantize_per_channel_affine(
+            xt, torch.from_numpy(scale), torch.from_numpy(-offset).to(torch.int32), 0, qmin, qmax)
+        np.testing.assert_array_equal(y, ref.detach().numpy())
+        ref.backward(torch.ones_like(ref))
+        np.testing.assert_array_equal(mask.astype(f32), xt.grad.numpy())
+
+
+def test_docstring_tables():
+    # backends/__init__.py:169-187 and :336-354 (4-bit unsigned, scale 1/15, offset 0)
+    x = torch.arange(start=-0.3, end=1.3, step=0.05).numpy()
+    s = np.float32(torch.tensor(1 / 15).item())
+    q = O.quantize(x, [s], [0.0], 0, 15, (1, 1, x.size))
+    expect_q = [0, 0, 0, 0, 0, 0, -0, 1, 2, 2, 3, 4, 4, 5, 6, 7, 7, 8, 9, 10, 10, 11, 12, 13,
+                13, 14, 15, 15, 15, 15, 15, 15]
+    np.testing.assert_array_equal(q, np.array(expect_q, f32))
+    y, _ = O.qdq_learnable(x, [s], [0.0], 0, 15, (1, 1, x.size))
+    expect_y = [0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0667, 0.1333, 0.1333, 0.2000, 0.2667, 0.2667,
+                0.3333, 0.4000, 0.4667, 0.4667, 0.5333, 0.6000, 0.6667, 0.6667, 0.7333, 0.8000,
+                0.8667, 0.8667, 0.9333, 1.0000, 1.0000, 1.0000, 1.0000, 1.0000, 1.0000]
+    np.testing.assert_allclose(y, expect_y, atol=5e-5, rtol=0)
+
+
+@pytest.mark.parametrize("bits", [8, 16])
+@pytest.mark.parametrize("symmetric", [True, False])
+def test_ties_to_even_table(bits, symmetric):
+    # test_native_qdq_alignment.py:111-118
+    codes = np.array([-7.5, -3.5, -2.5, -1.5, -.5, .5, 1.5, 2.5, 3.5, 7.5], dtype=f32)
+    s = f32(2.0 ** -7 if bits == 8 else 2.0 ** -15)
+    x = (codes * s).astype(f32)
+    if symmetric:
+        qmin, qmax, off = -(1 << (bits - 1)), (1 << (bits - 1)) - 1, 0.0
+    else:
+        qmin, qmax, off = 0, (1 << bits) - 1, -13.0
+    expect = (np.rint(codes) * s).astype(f32)
+    for fn in (O.qdq_frozen, O.qdq_learnable):
+        y, _ = fn(x, [s], [off], qmin, qmax, (1, 1, x.size))
+        np.testing.assert_array_equal(y, expect)
+    assert list(np.rint(codes)) == [-8, -4, -2, -2, -0, 0, 2, 2, 4, 8]
+
+
+@pytest.mark.parametrize("scale", [1.0 / 32767, .013007, .027019])
+def test_decimal_scale_uses_float32_reciprocal(scale):
+    # test_native_qdq_alignment.py:120-124: frozen QDQ multiplies by fl(1/scale)
+    codes = np.arange(-63, 64, dtype=f32) + f32(.5)
+    x = (codes * f32(scale)).astype(f32)
+    y, _ = O.qdq_frozen(x, [scale], [0.0], -32768, 32767, (1, 1, x.size))
+    ref = torch.fake_quantize_per_tensor_affine(torch.from_numpy(x), torch.tensor(scale),
+                                                torch.tensor(0, dtype=torch.int32), -32768, 32767)
+    np.testing.assert_array_equal(y, ref.numpy())
+
+
+def test_nan_kept_and_infinity_saturates():
+    # test_native_qdq_alignment.py:126-137
+    for bits in (8, 16):
+        s = f32(2.0 ** -7 if bits == 8 else 2.0 ** -15)
+        qmin, qmax = -(1 << (bits - 1)), (1 << (bits - 1)) - 1
+        x = np.array([np.nan, -np.inf, -s, 0, s, np.inf], dtype=f32)
+        expect = np.array([np.nan, qmin * s, -s, 0, s, qmax * s], dtype=f32)
+        for fn in (O.qdq_frozen, O.qdq_learnable):
+            y, mask = fn(x, [s], [0.0], qmin, qmax, (1, 1, x.size))
+            np.testing.assert_array_equal(y, expect)
+            assert list(mask) == [False, False, True, True, True, False]
+
+
+def _surrogate_grads(x, g, s, o, qmin, qmax, layout):
+    """Autograd of y = (clamp(ste_round(x/s) - o) + o) * s, fp64 arithmetic with the
+    fp32 rounding decisions of the forward; independent of the oracle's formulas."""
+    outer, C, inner = layout
+    xt = torch.from_numpy(x.astype(np.float64)).view(outer, C, inner)
+    st = torch.from_numpy(np.asarray(s, np.float64)).view(1, C, 1).requires_grad_()
+    ot = torch.from_numpy(np.asarray(o, np.float64)).view(1, C, 1).requires_grad_()
+    xt = xt.requires_grad_()
+    xs32 = (x.reshape(outer, C, inner) / np.asarray(s, f32).reshape(1, C, 1)).astype(f32)
+    rounded = torch.from_numpy(np.rint(xs32).astype(np.float64))
+    xs = xt / st
+    r = xs + (rounded - xs).detach() - ot
+    q = torch.clamp(r, qmin, qmax)
+    y = (q + ot) * st
+    y.backward(torch.from_numpy(g.astype(np.float64)).view(outer, C, inner))
+    return xt.grad.numpy().reshape(x.shape), st.grad.numpy().reshape(-1), ot.grad.numpy().reshape(-1)
+
+
+@pytest.mark.parametrize("layout,qmin,qmax,asym", [((1, 1, 6000), -128, 127, False),
+                                                   ((1, 1, 6000), 0, 255, True),
+                                                   ((1, 16, 400), -8, 7, False),
+                                                   ((3, 8, 50), 0, 255, True)])
+def test_learnable_gradients_match_autograd_surrogate(layout, qmin, qmax, asym):
+    outer, C, inner = layout
+    n = outer * C * inner
+    x = _data(n, 7)
+    g = np.random.default_rng(8).standard_normal(n).astype(f32)
+    mn = np.full(C, -2.0, f32)
+    mx = np.full(C, 2.5, f32) * (1 + np.arange(C, dtype=f32) / C)
+    s, o = O.scale_offset(mn, mx, qmin, qmax, symmetric=not asym)
+    dx, ds, do = O.qdq_learnable_backward(x, g, s, o, qmin, qmax, layout)
+    sdx, sds, sdo = _surrogate_grads(x, g, s, o, qmin, qmax, layout)
+    np.testing.assert_array_equal(dx, sdx.astype(f32))
+    scale_ref = np.abs(g).reshape(outer, C, inner).sum(axis=(0, 2)) * 8
+    np.testing.assert_allclose(ds, sds, rtol=0, atol=1e-5 * scale_ref.max())
+    np.testing.assert_allclose(do, sdo, rtol=1e-5, atol=1e-5 * (s * np.abs(g).sum()).max())
+
+
+def test_quantize_dequantize_gradients_match_autograd():
+    layout = (1, 4, 500)
+    x = _data(2000, 11)
+    g = np.random.default_rng(12).standard_normal(2000).astype(f32)
+    s = np.array([0.01, 0.02, 0.03, 0.05], f32)
+    o = np.array([-100, -128, -10, -200], f32)
+    q = O.quantize(x, s, o, 0, 255, layout)
+    dq, dsd, dod = O.dequantize_backward(q, g, s, o, layout)
+    qt = torch.from_numpy(q.astype(np.float64)).view(1, 4, 500).requires_grad_()
+    st = torch.from_numpy(s.astype(np.float64)).view(1, 4, 1).requires_grad_()
+    ot = torch.from_numpy(o.astype(np.float64)).view(1, 4, 1).requires_grad_()
+    ((qt + ot) * st).backward(torch.from_numpy(g.astype(np.float64)).view(1, 4, 500))
+    np.testing.assert_allclose(dq, qt.grad.numpy().reshape(-1), rtol=1e-6)
+    np.testing.assert_allclose(dsd, st.grad.numpy().reshape(-1), rtol=1e-5)
+    np.testing.assert_allclose(dod, ot.grad.numpy().reshape(-1), rtol=1e-5)
+    y = O.dequantize(q, s, o, layout)
+    np.testing.assert_array_equal(y, ((q.reshape(1, 4, 500) + o.reshape(1, 4, 1)) *
+                                      s.reshape(1, 4, 1)).astype(f32).reshape(-1))
+
+
+def test_minimum_scale_table():
+    # quantsim.py:463-470
+    assert O.minimum_scale(15) == 2.0 ** -23
+    assert O.minimum_scale(255) == 2.0 ** -23
+    assert O.minimum_scale(65535) == 2.0 ** -23
+    assert O.minimum_scale(2 ** 32 - 1) == 2.0 ** -38
+
+
+def test_encoding_closed_forms():
+    mn = np.array([-1.0, 0.5, -3.0], f32)
+    mx = np.array([2.0, 4.0, -1.0], f32)
+    lo, hi = O.compute_encodings_from_stats(mn, mx, 255, False)
+    np.testing.assert_array_equal(lo, [-1.0, 0.0, -3.0])     # zero always inside
+    np.testing.assert_array_equal(hi, [2.0, 4.0, 0.0])
+    lo, hi = O.compute_encodings_from_stats(mn, mx, 255, True)
+    delta = np.maximum(np.maximum(mx, 0) / f32(127), -np.minimum(mn, 0) / f32(128)).astype(f32)
+    np.testing.assert_array_equal(lo, (-128 * delta).astype(f32))
+    np.testing.assert_array_equal(hi, (127 * delta).astype(f32))
+    # degenerate range gets the minimum-scale adjustment
+    lo, hi = O.compute_encodings_from_stats(np.zeros(1, f32), np.zeros(1, f32), 255, False)
+    assert hi[0] == f32(255 * 2.0 ** -23) and lo[0] == 0
+    s, o = O.scale_offset(np.array([-1.0], f32), np.array([2.0], f32), -128, 127, False)
+    assert s[0] == f32(3.0 / 255) and o[0] == f32(np.rint(-1.0 / s[0]) + 128)
+
+
+def test_encoding_math_matches_torch_on_cpu():
+    """The oracle's encoding math (CPU division) equals the torch expressions of
+    encoding_analyzer.py:226-268 / quantizer.py:359-368 evaluated on the CPU."""
+    g = np.random.default_rng(5)
+    mn = -(g.random(300) * 3).astype(f32)
+    mx = (g.random(300) * 3).astype(f32)
+    for n, sym in ((255, False), (255, True), (15, True), (65535, False), (3, True)):
+        lo, hi = O.compute_encodings_from_stats(mn, mx, n, sym)
+        tmn, tmx = torch.from_numpy(mn), torch.from_numpy(mx)
+        ms = O.minimum_scale(n)
+        m0, x0 = torch.clamp(tmn, max=0), torch.clamp(tmx, min=0)
+        adj = ms * ((x0 - m0) / n < ms)
+        if sym:
+            umax = x0 + (n // 2) * adj
+            umin = m0 - (-(-n // 2)) * adj
+            d = torch.maximum(umax / (n // 2 + (1 if n == 3 else 0)), -umin / (-(-n // 2)))
+            umin, umax = -1 * (-(-n // 2)) * d, (n // 2) * d
+        else:
+            umax, umin = x0 + n * adj, m0
+        np.testing.assert_array_equal(lo, umin.numpy())
+        np.testing.assert_array_equal(hi, umax.numpy())
+        s, o = O.scale_offset(lo, hi, 0, n, sym)
+        ts = ((torch.from_numpy(hi) - torch.from_numpy(lo)) / n).abs().clamp_min_(ms)
+        np.testing.assert_array_equal(s, ts.numpy())
+
+
+def test_gpu_scalar_division_is_reciprocal_multiply():
+    a = np.array([1.0, 3.0, 0.7, 1e-3], f32)
+    np.testing.assert_array_equal(O.sdiv(a, 255, True), (a * f32(f32(1) / f32(255))).astype(f32))
+    np.testing.assert_array_equal(O.sdiv(a, 255, False), (a / f32(255)).astype(f32))
