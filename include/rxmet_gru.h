@@ -1,0 +1,208 @@
+/*
+ * rxmet_gru.h — C ABI of the MI355X QuantGRU (FP32-carrier QAT) path.
+ *
+ * Replaces the entry points of the reference pybind module gru_interface_binding
+ * (operators/quant-gru/pytorch/lib/gru_interface_binding.cc:1331-1788) that the
+ * QAT path uses:
+ *   calculate_gru_quantitative_parameters -> rxmet_gru_make_params
+ *   forward_calibrate (MINMAX)            -> rxmet_gru_forward_calibrate
+ *   forward_quant_float_storage           -> rxmet_gru_forward_quant
+ *   backward_quant_float_storage          -> rxmet_gru_backward_quant
+ *   (LUT regeneration in GRUQuantParamsPy::to_cpp) -> rxmet_gru_make_luts
+ *
+ * Conventions (all as in the reference):
+ *   - Gate order inside a 3H block is (z, r, n) ("haste" order); W is [I, 3H], R is
+ *     [H, 3H], biases [3H]; x is [T, B, I], h0 [B, H] (row-major fp32).
+ *   - Quantized values are integer codes stored in fp32; masks are uint8 with
+ *     1 = keep gradient (value was not clamped).
+ *   - Boundary quantisation (x, h0, W, R, biases) and all dequantisation use the
+ *     effective scale decode(encode(scale)) (16-bit mantissa M * 2^-shift, or the
+ *     power of two itself); the in-loop rescales use ratios of the stored scales.
+ *
+ * Device entry points take device pointers and a hipStream_t (as void*), enqueue work on
+ * that stream and return 0 or a negative status (message in rxmet_last_error()).  They
+ * never allocate: scratch memory comes from a caller workspace of the size the matching
+ * *_workspace_bytes() function returns.
+ */
+#ifndef RXMET_GRU_H_
+#define RXMET_GRU_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Scalar operator grids, in this order (reference: quantize_param_types.h:65-142). */
+enum {
+  RXMET_GRU_X = 0,            /* input x                        */
+  RXMET_GRU_H = 1,            /* hidden state / output          */
+  RXMET_GRU_WX = 2,           /* weight_ih_linear = W x + bw    */
+  RXMET_GRU_RH = 3,           /* weight_hh_linear = R h + br    */
+  RXMET_GRU_Z_IN = 4,         /* update_gate_input              */
+  RXMET_GRU_R_IN = 5,         /* reset_gate_input               */
+  RXMET_GRU_N_IN = 6,         /* new_gate_input                 */
+  RXMET_GRU_Z_OUT = 7,        /* update_gate_output             */
+  RXMET_GRU_R_OUT = 8,        /* reset_gate_output              */
+  RXMET_GRU_N_OUT = 9,        /* new_gate_output                */
+  RXMET_GRU_MUL_RH = 10,      /* mul_reset_hidden               */
+  RXMET_GRU_MUL_NEW = 11,     /* mul_new_contribution           */
+  RXMET_GRU_MUL_OLD = 12,     /* mul_old_contribution           */
+  RXMET_GRU_NGRIDS = 13
+};
+
+/* Per-channel operators (weights / biases), in this order. */
+enum { RXMET_GRU_W = 0, RXMET_GRU_R = 1, RXMET_GRU_BW = 2, RXMET_GRU_BR = 3, RXMET_GRU_NCHAN = 4 };
+
+enum { RXMET_PER_TENSOR = 0, RXMET_PER_GATE = 1, RXMET_PER_CHANNEL = 2 };
+enum { RXMET_POT_ROUND = 0, RXMET_POT_COVER_RANGE = 1, RXMET_POT_FLOOR = 2 };
+
+/* Bit-width configuration of one operator (QuantBitWidth + symmetric flag). */
+typedef struct rxmet_bitspec {
+  int32_t bits;        /* 1..32 */
+  int32_t is_unsigned; /* 0: signed grid, 1: unsigned grid */
+  int32_t symmetric;   /* 1: zero point forced to 0 */
+  int32_t granularity; /* RXMET_PER_*; used by the per-channel operators only */
+} rxmet_bitspec;
+
+/* OperatorQuantConfig (quantize_bitwidth_config.h:56-122). */
+typedef struct rxmet_gru_config {
+  rxmet_bitspec op[RXMET_GRU_NGRIDS];
+  rxmet_bitspec chan[RXMET_GRU_NCHAN];
+  int32_t use_pot2;
+  int32_t pot_method;  /* RXMET_POT_* */
+  float pot_tolerance; /* default 0.02 */
+} rxmet_gru_config;
+
+/* GRUQuantizationRanges (gru_quantization_ranges.h): scalar min/max per grid and
+ * per-channel min/max arrays of length 3H (host memory). */
+typedef struct rxmet_gru_ranges {
+  int32_t hidden;
+  float min[RXMET_GRU_NGRIDS];
+  float max[RXMET_GRU_NGRIDS];
+  float *chan_min[RXMET_GRU_NCHAN];
+  float *chan_max[RXMET_GRU_NCHAN];
+} rxmet_gru_ranges;
+
+/* One operator grid: stored scale (continuous, or 2^-n in power-of-two mode), zero
+ * point and bit width. */
+typedef struct rxmet_grid {
+  float scale;
+  int32_t zero_point;
+  int32_t bits;
+  int32_t is_unsigned;
+} rxmet_grid;
+
+/* GRUQuantParams (quantize_param_types.h:88-118) without the LUTs; the per-channel
+ * scales live in host arrays chan_scale[k] of length 3H (zero points are 0). */
+typedef struct rxmet_gru_qparams {
+  int32_t hidden;
+  int32_t use_pot2;
+  rxmet_grid g[RXMET_GRU_NGRIDS];
+  int32_t chan_bits[RXMET_GRU_NCHAN];
+  int32_t chan_unsigned[RXMET_GRU_NCHAN];
+  float *chan_scale[RXMET_GRU_NCHAN];
+} rxmet_gru_qparams;
+
+/* One segment of a 16-segment piecewise-linear activation (SegmentParams,
+ * quantize_lut_types.h:20-25): y = rint((q_b * (q - zp_x)) * 2^-n) + c for q < threshold. */
+typedef struct rxmet_pwl_segment {
+  int32_t q_b;
+  int32_t n;
+  int32_t c;
+  int32_t threshold;
+} rxmet_pwl_segment;
+
+typedef struct rxmet_pwl_lut {
+  rxmet_pwl_segment seg[16];
+  int32_t zp_x;
+} rxmet_pwl_lut;
+
+/*
+ * Quantisation parameters from calibration ranges: calculateGRUQuantitativeParameters
+ * (operators/quant-gru/src/gru_host.cc:13-124) with encodeFromRange / calibrateBias /
+ * ensureMinRange (include/gru_calibration_helpers.h:15-61, calibration_utils.h:27-44).
+ * Host only.  out->chan_scale[k] must point at caller arrays of 3H floats.
+ * Weights and biases must be configured symmetric (gru_calibration_helpers.h:7-13).
+ */
+int rxmet_gru_make_params(const rxmet_gru_ranges *ranges, const rxmet_gru_config *config,
+                          rxmet_gru_qparams *out);
+
+/*
+ * The three activation LUTs the forward uses, rebuilt from the stored scales
+ * (generate_piecewise_linear_lut_to_params, src/quantize_lut.cc:16-48): out[0] sigmoid
+ * of the update gate, out[1] sigmoid of the reset gate, out[2] tanh of the new gate.
+ * Host only.
+ */
+int rxmet_gru_make_luts(const rxmet_gru_qparams *params, rxmet_pwl_lut out[3]);
+
+/* Effective scale the kernels use for a stored scale (decode(encode(s))). Host only. */
+float rxmet_gru_effective_scale(float scale, int32_t use_pot2);
+
+/* Workspace bytes of rxmet_gru_forward_quant / rxmet_gru_backward_quant. */
+int64_t rxmet_gru_forward_workspace_bytes(int32_t T, int32_t B, int32_t I, int32_t H);
+int64_t rxmet_gru_backward_workspace_bytes(int32_t T, int32_t B, int32_t I, int32_t H);
+
+/*
+ * Quantised forward, FP32 carrier: quantGRUForwardFP (src/gru_interface.cc:636-716)
+ * behind forward_quant_float_storage_wrapper (gru_interface_binding.cc:306-448).
+ * Outputs (device, caller-allocated, shapes as the binding returns them):
+ *   h [T+1, B, H] dequantised hidden states (h[0] = dequantised h0),
+ *   v [T, B, 4H]  dequantised (z, r, n, weight_hh_linear_n) per step,
+ *   W_q [I,3H], R_q [H,3H], bw_q [3H], br_q [3H], x_q [T,B,I] codes,
+ * and when is_training != 0 the uint8 masks (else they may be null):
+ *   x_mask [T,B,I], h0_mask [B,H] (null when h0 is null), W_mask [I,3H], R_mask [H,3H],
+ *   bw_mask [3H], br_mask [3H], ih_mask, hh_mask, gate_in_mask, gate_out_mask [T,B,3H],
+ *   h_mask [T,B,H].
+ * h0 may be null (state starts at the zero point of h).
+ */
+int rxmet_gru_forward_quant(int32_t is_training, int32_t T, int32_t B, int32_t I, int32_t H,
+                            const float *W, const float *R, const float *bw, const float *br,
+                            const float *x, const float *h0, const rxmet_gru_qparams *params,
+                            float *h, float *v, float *W_q, float *R_q, float *bw_q, float *br_q,
+                            float *x_q, uint8_t *x_mask, uint8_t *h0_mask, uint8_t *W_mask,
+                            uint8_t *R_mask, uint8_t *bw_mask, uint8_t *br_mask, uint8_t *ih_mask,
+                            uint8_t *hh_mask, uint8_t *gate_in_mask, uint8_t *gate_out_mask,
+                            uint8_t *h_mask, void *workspace, void *stream);
+
+/*
+ * Quantised backward: backward_quant_float_storage_wrapper
+ * (gru_interface_binding.cc:789-920) + quantGRUBackward / BackwardPassQuant::Run
+ * (src/gru_backward_gpu_quant.cu:379-493).  Inputs are the forward's outputs; unlike
+ * the reference the saved codes are not modified.  dh_new [T+1, B, H] is the upstream
+ * gradient of h (dh_new[0] unused).  Outputs (device, caller-allocated):
+ *   dx [T,B,I], dW [I,3H], dR [H,3H], dbw [3H], dbr [3H], dh0 [B,H].
+ * Mask pointers may be null (no masking for that tensor), as in the reference.
+ */
+int rxmet_gru_backward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const float *W_q,
+                             const float *R_q, const float *bw_q, const float *br_q,
+                             const float *x_q, const float *dh_new, const float *h,
+                             const float *v, const rxmet_gru_qparams *params,
+                             const uint8_t *x_mask, const uint8_t *h0_mask,
+                             const uint8_t *W_mask, const uint8_t *R_mask,
+                             const uint8_t *bw_mask, const uint8_t *br_mask,
+                             const uint8_t *ih_mask, const uint8_t *hh_mask,
+                             const uint8_t *gate_in_mask, const uint8_t *gate_out_mask,
+                             const uint8_t *h_mask, float *dx, float *dW, float *dR, float *dbw,
+                             float *dbr, float *dh0, void *workspace, void *stream);
+
+/*
+ * Float GRU forward with MinMax calibration statistics: forwardWithCalibrationGPU
+ * (src/gru_interface.cc:930-1024) / forwardWithCalibrationCPU
+ * (src/gru_forward_cpu.cc:58-151).  Writes h [T+1,B,H] and v [T,B,4H] (float values)
+ * and merges (min/max-accumulates) the statistics into stats, a device array of
+ * 2*13 + 8*3H floats laid out as: min[13], max[13], then for k in W,R,bw,br:
+ * chan_min_k[3H], chan_max_k[3H].  Initialise stats with +FLT_MAX / -FLT_MAX before the
+ * first call.  h0 may be null.  Non-finite values are ignored, as in the reference.
+ */
+int64_t rxmet_gru_calibrate_workspace_bytes(int32_t T, int32_t B, int32_t I, int32_t H);
+int rxmet_gru_forward_calibrate(int32_t T, int32_t B, int32_t I, int32_t H, const float *W,
+                                const float *R, const float *bw, const float *br,
+                                const float *x, const float *h0, float *h, float *v,
+                                float *stats, void *workspace, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RXMET_GRU_H_ */

@@ -41,8 +41,11 @@ _SIGNATURES = {
                                           c_ptr, c_ptr, c_ptr, c_ptr]),
 }
 
-# Symbols declared by the headers; tests check the built library exports all of them.
-EXPORTED = tuple(_SIGNATURES)
+
+
+def exported() -> tuple:
+    """Names of every typed entry point (tests check the library exports them all)."""
+    return tuple(_SIGNATURES)
 
 
 class RxmetError(RuntimeError):
