@@ -1,0 +1,582 @@
+// gru_fwd.hip — MI355X QuantGRU forward (FP32-carrier QAT), behind rxmet_gru_forward_quant.
+//
+// Reference path: quantGRUForwardFP (operators/quant-gru/src/gru_interface.cc:636-716):
+// four per-channel quantisation launches with a device sync each, x/h0 quantisation,
+// one cuBLAS SGEMM for the input projection, then a host loop of T iterations each
+// launching one SGEMM (R h) and one pointwise kernel (src/gru_forward_gpu_quant_fp.cu:
+// 604-801), and two in-place dequantisation passes over h and v.
+//
+// Here:
+//   1. quant_weights : one thread per channel column quantises W/R/bw/br, writes masks,
+//      the fp32 column sums of codes times the input zero points, and the bias terms
+//      rint(b_q * ratio) the pointwise step needs (they do not change over time);
+//   2. quant_input   : x and h0 quantisation (codes + masks), h[0] dequantised;
+//   3. code_gemm     : the time-parallel input projection W_q x_q summed exactly in
+//      int32 and rounded once to fp32;
+//   4. recurrence    : one persistent workgroup per 16 sequences runs all T steps.  The
+//      recurrent weights R_q live in VGPRs as int8 MFMA fragments for the whole kernel;
+//      h_t lives in LDS as int8 planes (16-bit codes are split into a high and a
+//      low byte plane); each step is 3 x (H/64) x planes v_mfma_i32_16x16x64_i8 per wave,
+//      exact in int32, followed by the fused pointwise update in registers (bias
+//      rescale, gate inputs, PWL sigmoid/tanh, hidden update, clamps and masks) and the
+//      dequantised outputs.  No host round trip and no grid barrier per step.
+#include <vector>
+
+#include "gru_internal.h"
+#include "mfma_frag.h"
+#include "rxmet_common.h"
+#include "rxmet_gru.h"
+
+namespace rxmet {
+namespace gru {
+
+constexpr int kTileB = 16;   // sequences per recurrent workgroup (MFMA N)
+constexpr int kMaxH = 256;   // 16 waves x 16 units
+constexpr int kChanParams = 7;  // igx, igh, wsum, rsum, btx, bth, rcol
+
+__device__ __forceinline__ float clamp_keep(float v, Bounds b, uint8_t &keep) {
+  keep = (v < b.lo || v > b.hi) ? 0 : 1;
+  return fmaxf(b.lo, fminf(v, b.hi));
+}
+
+// ---------------------------------------------------------------------------------
+// 1. weights
+// ---------------------------------------------------------------------------------
+struct WeightArgs {
+  const float *W, *R, *bw, *br;
+  const float *eff;  // 4 x C: W, R, bw, br effective scales
+  const float *ibx, *ibh;
+  Bounds bW, bR, bbw, bbr;
+  float zp_x, zp_h;
+  float *Wq, *Rq, *bwq, *brq;
+  uint8_t *Wm, *Rm, *bwm, *brm;
+  float *chan;  // kChanParams x C, fills wsum, rsum, btx, bth, rcol
+};
+
+__global__ __launch_bounds__(256) void quant_weights(int I, int H, WeightArgs a) {
+  const int C = 3 * H;
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= C) return;
+  uint8_t keep;
+  const float ew = a.eff[c], er = a.eff[C + c], ebw = a.eff[2 * C + c], ebr = a.eff[3 * C + c];
+  float s = 0.0f;
+  for (int k = 0; k < I; ++k) {
+    const size_t i = static_cast<size_t>(k) * C + c;
+    const float q = clamp_keep(rintf(a.W[i] / ew) + 0.0f, a.bW, keep);
+    a.Wq[i] = q;
+    if (a.Wm) a.Wm[i] = keep;
+    s += q;
+  }
+  a.chan[2 * C + c] = a.zp_x != 0.0f ? s * a.zp_x : 0.0f;  // wsum
+  s = 0.0f;
+  int exact = 0;
+  for (int k = 0; k < H; ++k) {
+    const size_t i = static_cast<size_t>(k) * C + c;
+    const float q = clamp_keep(rintf(a.R[i] / er) + 0.0f, a.bR, keep);
+    a.Rq[i] = q;
+    if (a.Rm) a.Rm[i] = keep;
+    s += q;
+    exact += static_cast<int>(q);
+  }
+  a.chan[3 * C + c] = a.zp_h != 0.0f ? s * a.zp_h : 0.0f;  // rsum
+  a.chan[6 * C + c] = static_cast<float>(exact);            // rcol (exact)
+  const float qbw = clamp_keep(rintf(a.bw[c] / ebw) + 0.0f, a.bbw, keep);
+  a.bwq[c] = qbw;
+  if (a.bwm) a.bwm[c] = keep;
+  const float qbr = clamp_keep(rintf(a.br[c] / ebr) + 0.0f, a.bbr, keep);
+  a.brq[c] = qbr;
+  if (a.brm) a.brm[c] = keep;
+  a.chan[4 * C + c] = rintf(qbw * a.ibx[c]);  // btx
+  a.chan[5 * C + c] = rintf(qbr * a.ibh[c]);  // bth
+}
+
+// ---------------------------------------------------------------------------------
+// 2. inputs
+// ---------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void quant_input(int64_t nx, int64_t nh, const float *x,
+                                                   const float *h0, float eff_x, float zp_x,
+                                                   Bounds bx, float eff_h, float zp_h, Bounds bh,
+                                                   float *xq, uint8_t *xm, float *h0codes,
+                                                   uint8_t *h0m, float *hout0) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  uint8_t keep;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < nx + nh;
+       i += stride) {
+    if (i < nx) {
+      xq[i] = clamp_keep(rintf(x[i] / eff_x) + zp_x, bx, keep);
+      if (xm) xm[i] = keep;
+    } else {
+      const int64_t j = i - nx;
+      float q = zp_h;
+      if (h0) {
+        q = clamp_keep(rintf(h0[j] / eff_h) + zp_h, bh, keep);
+        if (h0m) h0m[j] = keep;
+      }
+      h0codes[j] = q;
+      hout0[j] = (q - zp_h) * eff_h;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// 3. exact code GEMM  C[M][N] = A[M][K] * B[K][N]  (integer codes stored as fp32)
+// ---------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void code_gemm(int M, int N, int K, const float *__restrict__ A,
+                                                 const float *__restrict__ Bm,
+                                                 float *__restrict__ Cm) {
+  __shared__ int As[16][64 + 1];
+  __shared__ int Bs[16][64];
+  const int tm = blockIdx.y * 64, tn = blockIdx.x * 64;
+  const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
+  int acc[4][4] = {};
+  for (int k0 = 0; k0 < K; k0 += 16) {
+    for (int q = 0; q < 4; ++q) {
+      const int e = threadIdx.x + 256 * q;
+      const int row = e / 16, kk = e % 16;
+      const int gm = tm + row, gk = k0 + kk;
+      As[kk][row] = (gm < M && gk < K) ? static_cast<int>(A[static_cast<size_t>(gm) * K + gk]) : 0;
+      const int kb = e / 64, col = e % 64;
+      const int gkb = k0 + kb, gn = tn + col;
+      Bs[kb][col] = (gkb < K && gn < N) ? static_cast<int>(Bm[static_cast<size_t>(gkb) * N + gn]) : 0;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < 16; ++kk) {
+      int av[4], bv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) av[i] = As[kk][ty * 4 + i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bv[j] = Bs[kk][tx * 4 + j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] += av[i] * bv[j];
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int gm = tm + ty * 4 + i;
+    if (gm >= M) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int gn = tn + tx * 4 + j;
+      if (gn < N) Cm[static_cast<size_t>(gm) * N + gn] = static_cast<float>(acc[i][j]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// 4. persistent recurrence
+// ---------------------------------------------------------------------------------
+struct RecArgs {
+  int T, B, H, KS;          // KS = ceil(H / 64) MFMA K-steps
+  int training;
+  float h_offset;           // 0 (signed h grid) or 2^(bits-1) (unsigned): centred codes
+  const float *gih;         // [T, B, 3H] exact W_q x_q
+  const v4i *rfrag;         // R_q as int8 MFMA B fragments, [H/16][3][KS][64]
+  const float *chan;        // kChanParams x 3H
+  const float *h0codes;     // [B, H]
+  float *hout;              // [T+1, B, H] dequantised (row 0 written by quant_input)
+  float *v;                 // [T, B, 4H] dequantised
+  uint8_t *ih_m, *hh_m, *gin_m, *gout_m, *h_m;
+};
+
+// R_q [H][3H] (fp32 codes) -> int8 B fragments of v_mfma_i32_16x16x64_i8:
+// frag[((ut * 3 + g) * KS + s) * 64 + lane] holds R[k][c] for c = g*H + 16*ut + lane % 16,
+// k = 64*s + 16*(lane / 16) + 0..15 (zero beyond H).
+__global__ __launch_bounds__(64) void pack_r_frags(int H, int KS, const float *__restrict__ Rq,
+                                                   v4i *__restrict__ frag) {
+  const int lane = threadIdx.x;
+  const int idx = blockIdx.x;  // (ut * 3 + g) * KS + s
+  const int s = idx % KS, g = (idx / KS) % 3, ut = idx / (3 * KS);
+  const int C = 3 * H;
+  const int c = g * H + 16 * ut + lane % 16;
+  int wd[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    int by[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int k = 64 * s + 16 * (lane / 16) + 4 * q + e;
+      by[e] = k < H ? static_cast<int>(Rq[static_cast<size_t>(k) * C + c]) : 0;
+    }
+    wd[q] = pack4_i8(by[0], by[1], by[2], by[3]);
+  }
+  frag[static_cast<size_t>(idx) * 64 + lane] = v4i{wd[0], wd[1], wd[2], wd[3]};
+}
+
+// PWL activation on the carrier: segment = #thresholds <= q (capped at 15).
+__device__ __forceinline__ float pwl_eval(float q, const float *thr, const float *qb,
+                                          const int *nsh, const float *cc, float zp_x, Bounds ob,
+                                          uint8_t &keep) {
+  int idx = 0;
+#pragma unroll
+  for (int s = 8; s > 0; s >>= 1)
+    if (thr[idx + s - 1] <= q) idx += s;
+  const float prod = qb[idx] * (q - zp_x);
+  const float val = rintf(ldexpf(prod, -nsh[idx])) + cc[idx];
+  return clamp_keep(val, ob, keep);
+}
+
+// One workgroup = 16 sequences x all H units; wave w owns unit tiles 2w and 2w+1.
+// MFMA orientation: D[b][c] = h[b][:] . R[:, c]  (A = h planes from LDS, B = R_q fragments
+// resident in VGPRs), so lane l owns unit 16u + (l % 16) for batch rows 4 (l / 16) + r.
+template <int NPL>
+__global__ __launch_bounds__(512) void recurrence(RecArgs a, StepParams p) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int H = a.H, C = 3 * H, B = a.B;
+  const int ROW = a.KS * 64 + 16;  // plane row stride in bytes (conflict-free 16-B reads)
+  float *hcode = reinterpret_cast<float *>(smem);                      // 2 * 16 * H
+  float *lut_f = hcode + 2 * kTileB * H;                               // 3 * 16 * 3 (thr, qb, c)
+  int *lut_n = reinterpret_cast<int *>(lut_f + 3 * 16 * 3);            // 3 * 16
+  int8_t *plane = reinterpret_cast<int8_t *>(lut_n + 3 * 16);          // 2 * NPL * 16 * ROW
+
+  const int tid = threadIdx.x;
+  const int w = tid / 64, l = tid % 64;
+  const int b0 = blockIdx.x * kTileB;
+  const int nthreads = blockDim.x;
+
+  for (int i = tid; i < 3 * 16; i += nthreads) {
+    const int g = i / 16, s = i % 16;
+    lut_f[g * 48 + s] = p.lut[g].thr[s];
+    lut_f[g * 48 + 16 + s] = p.lut[g].qb[s];
+    lut_f[g * 48 + 32 + s] = p.lut[g].c[s];
+    lut_n[g * 16 + s] = p.lut[g].n[s];
+  }
+  for (int i = tid; i < 2 * NPL * kTileB * ROW / 4; i += nthreads)
+    reinterpret_cast<int *>(plane)[i] = 0;
+  __syncthreads();
+  for (int i = tid; i < kTileB * H; i += nthreads) {
+    const int n = i / H, j = i % H;
+    const int b = b0 + n;
+    const float q = b < B ? a.h0codes[static_cast<size_t>(b) * H + j] : p.zp_h;
+    hcode[i] = q;
+    const int hc = static_cast<int>(q - a.h_offset);
+    if (NPL == 1) {
+      plane[n * ROW + j] = static_cast<int8_t>(hc);
+    } else {
+      plane[n * ROW + j] = static_cast<int8_t>((hc & 255) - 128);            // low byte plane
+      plane[(kTileB + n) * ROW + j] = static_cast<int8_t>(hc >> 8);         // high byte plane
+    }
+  }
+
+  // R_q fragments (B operand) and per-channel constants of the two unit tiles.
+  v4i rfr[2][3][4];
+  float cst[2][3][kChanParams];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int unit = 16 * (2 * w + u) + (l % 16);
+#pragma unroll
+    for (int g = 0; g < 3; ++g) {
+      const int c = g * H + unit;
+#pragma unroll
+      for (int q = 0; q < kChanParams; ++q) cst[u][g][q] = unit < H ? a.chan[q * C + c] : 0.0f;
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        rfr[u][g][s] = (s < a.KS && unit < H)
+                           ? a.rfrag[(((2 * w + u) * 3 + g) * a.KS + s) * 64 + l]
+                           : v4i{0, 0, 0, 0};
+    }
+  }
+  __syncthreads();
+
+  const float plane_off = 128.0f + a.h_offset;  // added back with the column sums (NPL == 2)
+  const size_t TBH = static_cast<size_t>(B) * H;
+  const int nrow0 = 4 * (l / 16);                // first of the 4 batch rows owned
+
+  for (int t = 0; t < a.T; ++t) {
+    const int cur = t & 1, nxt = cur ^ 1;
+    const int8_t *pc = plane + cur * NPL * kTileB * ROW;
+    int8_t *pn = plane + nxt * NPL * kTileB * ROW;
+    const float *hc = hcode + cur * kTileB * H;
+    float *hn = hcode + nxt * kTileB * H;
+
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int j = 16 * (2 * w + u) + (l % 16);  // unit owned in this tile
+      if (16 * (2 * w + u) >= H) continue;
+      __builtin_amdgcn_sched_barrier(0);
+      v4i acc[3][NPL];
+#pragma unroll
+      for (int g = 0; g < 3; ++g)
+#pragma unroll
+        for (int q = 0; q < NPL; ++q) acc[g][q] = v4i{0, 0, 0, 0};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        if (s >= a.KS) break;
+        v4i hfr[NPL];  // A fragments: h planes of the 16 sequences
+#pragma unroll
+        for (int q = 0; q < NPL; ++q)
+          hfr[q] = *reinterpret_cast<const v4i *>(pc + (q * kTileB + l % 16) * ROW + 64 * s +
+                                                  16 * (l / 16));
+#pragma unroll
+        for (int g = 0; g < 3; ++g)
+#pragma unroll
+          for (int q = 0; q < NPL; ++q) acc[g][q] = mfma_i8(hfr[q], rfr[u][g][s], acc[g][q]);
+      }
+
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int nr = nrow0 + r;
+        const int b = b0 + nr;
+        const bool valid = b < B;
+        // 32-bit element offsets from uniform bases keep the per-row addressing cheap
+        const uint32_t oH = static_cast<uint32_t>(b) * H + j;          // [.., B, H]
+        const uint32_t oC = 3u * static_cast<uint32_t>(b) * H + j;     // [.., B, 3H]
+        const uint32_t o4 = 4u * static_cast<uint32_t>(b) * H + j;     // [.., B, 4H]
+        const uint32_t stepC = static_cast<uint32_t>(t) * B * C;
+        uint8_t k_ih[3], k_hh[3], k_gi[3], k_go[3], k_h;
+        float wx[3], rh[3];
+#pragma unroll
+        for (int g = 0; g < 3; ++g) {
+          // R_q h = 256 R hi + R lo' + (128 + offset) colsum(R); the exact result fits in
+          // int32, so the (modular) unsigned combination is exact.
+          const uint32_t col = static_cast<uint32_t>(static_cast<int>(cst[u][g][6]));
+          uint32_t v_u;
+          if (NPL == 2)
+            v_u = 256u * static_cast<uint32_t>(acc[g][1][r]) + static_cast<uint32_t>(acc[g][0][r]) +
+                  static_cast<uint32_t>(static_cast<int>(plane_off)) * col;
+          else
+            v_u = static_cast<uint32_t>(acc[g][0][r]) +
+                  static_cast<uint32_t>(static_cast<int>(a.h_offset)) * col;
+          const float ghh = static_cast<float>(static_cast<int>(v_u));
+          const float gi = valid ? a.gih[stepC + oC + g * H] : 0.0f;
+          float val = gi - cst[u][g][2];
+          wx[g] = clamp_keep(rintf((val + cst[u][g][4]) * cst[u][g][0]) + p.zp_wx, p.wx, k_ih[g]);
+          val = ghh - cst[u][g][3];
+          rh[g] = clamp_keep(rintf((val + cst[u][g][5]) * cst[u][g][1]) + p.zp_rh, p.rh, k_hh[g]);
+        }
+        // update gate
+        float in = rintf((wx[0] - p.zp_wx) * p.ih_to_zin) + rintf((rh[0] - p.zp_rh) * p.hh_to_zin);
+        in += p.zp_zin;
+        in = clamp_keep(in, p.zin, k_gi[0]);
+        const float z = pwl_eval(in, lut_f, lut_f + 16, lut_n, lut_f + 32, p.lut[0].zp_x, p.zout,
+                                 k_go[0]);
+        // reset gate
+        in = rintf((wx[1] - p.zp_wx) * p.ih_to_rin) + rintf((rh[1] - p.zp_rh) * p.hh_to_rin);
+        in += p.zp_rin;
+        in = clamp_keep(in, p.rin, k_gi[1]);
+        const float rr = pwl_eval(in, lut_f + 48, lut_f + 64, lut_n + 16, lut_f + 80, p.lut[1].zp_x,
+                                  p.rout, k_go[1]);
+        // new gate
+        const float rmul = (rr - p.zp_rout) * (rh[2] - p.zp_rh);
+        in = rintf((wx[2] - p.zp_wx) * p.ih_to_nin) + rintf(rmul * p.rmul_to_nin);
+        in += p.zp_nin;
+        in = clamp_keep(in, p.nin, k_gi[2]);
+        const float nn = pwl_eval(in, lut_f + 96, lut_f + 112, lut_n + 32, lut_f + 128,
+                                  p.lut[2].zp_x, p.nout, k_go[2]);
+        // hidden update
+        const float hold = hc[nr * H + j];
+        const float n_h = rintf((nn - p.zp_nout) * p.nout_to_h) + p.zp_h;
+        const float oldc = (z - p.zp_zout) * (hold - p.zp_h);
+        const float newc = (p.quant_one - z) * (n_h - p.zp_h);
+        float h2 = rintf((oldc + newc) * p.old_to_h) + p.zp_h;
+        h2 = clamp_keep(h2, p.h, k_h);
+
+        if (valid) {
+          const uint32_t stepH = static_cast<uint32_t>(t) * B * H;
+          a.hout[stepH + static_cast<uint32_t>(B) * H + oH] = (h2 - p.zp_h) * p.eff_h;
+          if (a.training) {
+            const uint32_t v0 = 4u * stepH + o4;
+            a.v[v0] = (z - p.zp_zout) * p.eff_zout;
+            a.v[v0 + H] = (rr - p.zp_rout) * p.eff_rout;
+            a.v[v0 + 2 * H] = (nn - p.zp_nout) * p.eff_nout;
+            a.v[v0 + 3 * H] = (rh[2] - p.zp_rh) * p.eff_rh;
+            const uint32_t m = stepC + oC;
+#pragma unroll
+            for (int g = 0; g < 3; ++g) {
+              a.ih_m[m + g * H] = k_ih[g];
+              a.hh_m[m + g * H] = k_hh[g];
+              a.gin_m[m + g * H] = k_gi[g];
+              a.gout_m[m + g * H] = k_go[g];
+            }
+            a.h_m[stepH + oH] = k_h;
+          }
+        }
+        // next state into LDS
+        hn[nr * H + j] = h2;
+        const int hcv = static_cast<int>(h2 - a.h_offset);
+        if (NPL == 1) {
+          pn[nr * ROW + j] = static_cast<int8_t>(hcv);
+        } else {
+          pn[nr * ROW + j] = static_cast<int8_t>((hcv & 255) - 128);
+          pn[(kTileB + nr) * ROW + j] = static_cast<int8_t>(hcv >> 8);
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+size_t recurrence_lds_bytes(int H, int KS, int npl) {
+  const int ROW = KS * 64 + 16;
+  return sizeof(float) * (2 * kTileB * H + 3 * 16 * 3) + sizeof(int) * 3 * 16 +
+         static_cast<size_t>(2) * npl * kTileB * ROW;
+}
+
+// Workspace layout of the forward (bytes, 256-aligned pieces).
+struct FwdWorkspace {
+  size_t gih, chan, h0codes, hostblk, rfrag, total;
+  FwdWorkspace(int T, int B, int I, int H) {
+    (void)I;
+    const size_t C = 3 * static_cast<size_t>(H);
+    auto al = [](size_t x) { return (x + 255) & ~static_cast<size_t>(255); };
+    size_t o = 0;
+    gih = o; o += al(sizeof(float) * static_cast<size_t>(T) * B * C);
+    chan = o; o += al(sizeof(float) * kChanParams * C);
+    h0codes = o; o += al(sizeof(float) * static_cast<size_t>(B) * H);
+    hostblk = o; o += al(sizeof(float) * 8 * C);  // eff[4C], ibx, ibh, igx, igh
+    rfrag = o; o += al(sizeof(v4i) * 64 * static_cast<size_t>(H / 16) * 3 * ((H + 63) / 64));
+    total = o;
+  }
+};
+
+static int host_bits_check(const rxmet_gru_qparams &p) {
+  RXMET_CHECK_ARG(p.chan_bits[RXMET_GRU_R] <= 8 && !p.chan_unsigned[RXMET_GRU_R],
+                  "recurrent weights wider than signed 8 bits are not supported by the MFMA "
+                  "recurrence");
+  RXMET_CHECK_ARG(p.g[RXMET_GRU_H].bits <= 16, "hidden-state grids wider than 16 bits are not supported");
+  RXMET_CHECK_ARG(p.g[RXMET_GRU_X].bits <= 16 && p.chan_bits[RXMET_GRU_W] <= 16,
+                  "input or input-weight grids wider than 16 bits are not supported");
+  return 0;
+}
+
+}  // namespace gru
+}  // namespace rxmet
+
+using namespace rxmet;
+using namespace rxmet::gru;
+
+extern "C" {
+
+int64_t rxmet_gru_forward_workspace_bytes(int32_t T, int32_t B, int32_t I, int32_t H) {
+  if (T < 0 || B < 0 || I < 0 || H < 0) return 0;
+  return static_cast<int64_t>(FwdWorkspace(T, B, I, H).total);
+}
+
+int rxmet_gru_forward_quant(int32_t is_training, int32_t T, int32_t B, int32_t I, int32_t H,
+                            const float *W, const float *R, const float *bw, const float *br,
+                            const float *x, const float *h0, const rxmet_gru_qparams *params,
+                            float *h, float *v, float *W_q, float *R_q, float *bw_q, float *br_q,
+                            float *x_q, uint8_t *x_mask, uint8_t *h0_mask, uint8_t *W_mask,
+                            uint8_t *R_mask, uint8_t *bw_mask, uint8_t *br_mask, uint8_t *ih_mask,
+                            uint8_t *hh_mask, uint8_t *gate_in_mask, uint8_t *gate_out_mask,
+                            uint8_t *h_mask, void *workspace, void *stream_) {
+  clear_error();
+  RXMET_CHECK_ARG(params != nullptr, "params must be non-null");
+  RXMET_CHECK_ARG(T >= 1 && B >= 1 && I >= 1 && H >= 1, "dimensions must be positive");
+  RXMET_CHECK_ARG(params->hidden == H, "params.hidden != hidden_size");
+  RXMET_CHECK_ARG(H % 16 == 0 && H <= kMaxH,
+                  "hidden_size must be a multiple of 16 and at most 256 for the MFMA recurrence");
+  RXMET_CHECK_ARG(W && R && bw && br && x && h && W_q && R_q && bw_q && br_q && x_q && workspace,
+                  "required pointer is null");
+  if (int rc = host_bits_check(*params)) return rc;
+  const bool training = is_training != 0;
+  if (training) {
+    RXMET_CHECK_ARG(v && x_mask && W_mask && R_mask && bw_mask && br_mask && ih_mask && hh_mask &&
+                        gate_in_mask && gate_out_mask && h_mask && (h0 == nullptr || h0_mask),
+                    "training needs v and every mask output");
+  }
+  {
+    // exact-int32 bound of the input projection
+    const double xmax = std::ldexp(1.0, params->g[RXMET_GRU_X].bits);
+    const double wmax = std::ldexp(1.0, params->chan_bits[RXMET_GRU_W] - 1);
+    RXMET_CHECK_ARG(xmax * wmax * I < 2147483647.0, "input projection would overflow int32");
+  }
+  RXMET_CHECK_ARG(static_cast<double>(T + 1) * B * 4 * H < 4294967295.0,
+                  "T*B*H too large for the recurrence's 32-bit element offsets");
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  const int C = 3 * H;
+  const FwdWorkspace ws(T, B, I, H);
+  char *wsb = static_cast<char *>(workspace);
+  float *gih = reinterpret_cast<float *>(wsb + ws.gih);
+  float *chan = reinterpret_cast<float *>(wsb + ws.chan);
+  float *h0codes = reinterpret_cast<float *>(wsb + ws.h0codes);
+  float *hostblk = reinterpret_cast<float *>(wsb + ws.hostblk);
+
+  StepParams sp;
+  std::vector<float> host(8 * static_cast<size_t>(C));
+  try {
+    make_step_params(*params, H, &sp);
+    // host block: eff[4C] | ibx | ibh | igx | igh
+    make_channel_factors(*params, H, host.data() + 6 * C, host.data() + 4 * C, host.data() + 7 * C,
+                         host.data() + 5 * C, host.data(), host.data() + C, host.data() + 2 * C,
+                         host.data() + 3 * C);
+  } catch (const std::exception &e) {
+    set_error(e.what());
+    return -22;
+  }
+  RXMET_CHECK_HIP(hipMemcpyAsync(hostblk, host.data(), sizeof(float) * host.size(),
+                                 hipMemcpyHostToDevice, stream));
+  // igx/igh go straight into the per-channel block
+  RXMET_CHECK_HIP(hipMemcpyAsync(chan, host.data() + 6 * C, sizeof(float) * C,
+                                 hipMemcpyHostToDevice, stream));
+  RXMET_CHECK_HIP(hipMemcpyAsync(chan + C, host.data() + 7 * C, sizeof(float) * C,
+                                 hipMemcpyHostToDevice, stream));
+  const rxmet_grid *g = params->g;
+  WeightArgs wa;
+  wa.W = W; wa.R = R; wa.bw = bw; wa.br = br;
+  wa.eff = hostblk;
+  wa.ibx = hostblk + 4 * C;
+  wa.ibh = hostblk + 5 * C;
+  wa.bW = bounds_of(params->chan_bits[RXMET_GRU_W], params->chan_unsigned[RXMET_GRU_W]);
+  wa.bR = bounds_of(params->chan_bits[RXMET_GRU_R], params->chan_unsigned[RXMET_GRU_R]);
+  wa.bbw = bounds_of(params->chan_bits[RXMET_GRU_BW], params->chan_unsigned[RXMET_GRU_BW]);
+  wa.bbr = bounds_of(params->chan_bits[RXMET_GRU_BR], params->chan_unsigned[RXMET_GRU_BR]);
+  wa.zp_x = static_cast<float>(g[RXMET_GRU_X].zero_point);
+  wa.zp_h = static_cast<float>(g[RXMET_GRU_H].zero_point);
+  wa.Wq = W_q; wa.Rq = R_q; wa.bwq = bw_q; wa.brq = br_q;
+  wa.Wm = training ? W_mask : nullptr;
+  wa.Rm = training ? R_mask : nullptr;
+  wa.bwm = training ? bw_mask : nullptr;
+  wa.brm = training ? br_mask : nullptr;
+  wa.chan = chan;
+  hipLaunchKernelGGL(quant_weights, dim3((C + 255) / 256), dim3(256), 0, stream, I, H, wa);
+  RXMET_CHECK_LAUNCH();
+
+  const int64_t nx = static_cast<int64_t>(T) * B * I, nh = static_cast<int64_t>(B) * H;
+  int64_t blocks = (nx + nh + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  hipLaunchKernelGGL(quant_input, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, nx, nh,
+                     x, h0, sp.eff_x, sp.zp_x, sp.x, sp.eff_h, sp.zp_h, sp.h, x_q,
+                     training ? x_mask : nullptr, h0codes, training ? h0_mask : nullptr, h);
+  RXMET_CHECK_LAUNCH();
+
+  const int M = T * B;
+  hipLaunchKernelGGL(code_gemm, dim3((C + 63) / 64, (M + 63) / 64), dim3(256), 0, stream, M, C, I,
+                     x_q, W_q, gih);
+  RXMET_CHECK_LAUNCH();
+
+  RecArgs ra;
+  ra.T = T; ra.B = B; ra.H = H; ra.KS = (H + 63) / 64;
+  v4i *rfrag = reinterpret_cast<v4i *>(wsb + ws.rfrag);
+  hipLaunchKernelGGL(pack_r_frags, dim3((H / 16) * 3 * ra.KS), dim3(64), 0, stream, H, ra.KS, R_q,
+                     rfrag);
+  RXMET_CHECK_LAUNCH();
+  ra.training = training ? 1 : 0;
+  const rxmet_grid &gh = g[RXMET_GRU_H];
+  const bool h_uns = gh.bits < 32 && gh.is_unsigned;
+  ra.h_offset = h_uns ? std::ldexp(1.0f, gh.bits - 1) : 0.0f;
+  const int npl = (gh.bits <= 8) ? 1 : 2;
+  ra.gih = gih; ra.rfrag = rfrag; ra.chan = chan; ra.h0codes = h0codes; ra.hout = h; ra.v = v;
+  ra.ih_m = ih_mask; ra.hh_m = hh_mask; ra.gin_m = gate_in_mask; ra.gout_m = gate_out_mask;
+  ra.h_m = h_mask;
+  const size_t lds = recurrence_lds_bytes(H, ra.KS, npl);
+  const dim3 grid((B + kTileB - 1) / kTileB), block(64 * ((H + 31) / 32));
+  if (npl == 1) {
+    RXMET_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&recurrence<1>),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        static_cast<int>(lds)));
+    hipLaunchKernelGGL(recurrence<1>, grid, block, lds, stream, ra, sp);
+  } else {
+    RXMET_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&recurrence<2>),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        static_cast<int>(lds)));
+    hipLaunchKernelGGL(recurrence<2>, grid, block, lds, stream, ra, sp);
+  }
+  RXMET_CHECK_LAUNCH();
+  return 0;
+}
+
+}  // extern "C"

@@ -39,6 +39,7 @@ _SIGNATURES = {
     "rxmet_dequantize_forward": (c_int, [c_ptr, c_ptr, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_ptr]),
     "rxmet_dequantize_backward": (c_int, [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64,
                                           c_ptr, c_ptr, c_ptr, c_ptr]),
+    "rxmet_selftest_mfma": (c_int, [c_int, c_ptr, c_ptr, c_ptr, c_ptr]),
 }
 
 

@@ -1,0 +1,123 @@
+"""GPU parity of the QuantGRU kernels against the pinned oracle (oracle/gru_oracle.c).
+
+Bar: every forward output (codes, masks, dequantised h and v) bit-exact; backward
+gradients within 1e-4 relative of the oracle (fp32 GEMM summation order differs from the
+oracle's fp64 sums).
+"""
+import numpy as np
+import pytest
+import torch
+
+import gru_ops
+import gru_oracle as GO
+import rxmet_gru_abi as A
+import rxmet_lib
+
+pytestmark = pytest.mark.gpu
+f32 = np.float32
+
+
+def test_mfma_layout_selftest(cuda):
+    g = np.random.default_rng(0)
+    a = g.integers(-128, 128, (16, 64), dtype=np.int8)
+    b = g.integers(-128, 128, (64, 16), dtype=np.int8)
+    d = torch.zeros((16, 16), dtype=torch.int32, device=cuda)
+    at, bt = torch.from_numpy(a).to(cuda), torch.from_numpy(b).to(cuda)
+    rxmet_lib.call("rxmet_selftest_mfma", 0, at.data_ptr(), bt.data_ptr(), d.data_ptr(),
+                   torch.cuda.current_stream().cuda_stream)
+    np.testing.assert_array_equal(d.cpu().numpy(), a.astype(np.int64) @ b.astype(np.int64))
+    a = g.integers(-100, 100, (16, 32)).astype(f32)
+    b = (g.integers(-100, 100, (32, 16)) / 64.0).astype(f32)
+    d = torch.zeros((16, 16), dtype=torch.float32, device=cuda)
+    at, bt = torch.from_numpy(a).to(cuda), torch.from_numpy(b).to(cuda)
+    rxmet_lib.call("rxmet_selftest_mfma", 1, at.data_ptr(), bt.data_ptr(), d.data_ptr(),
+                   torch.cuda.current_stream().cuda_stream)
+    np.testing.assert_array_equal(d.cpu().numpy(), (a.astype(np.float64) @ b).astype(f32))
+
+
+def _weights(I, H, seed, amp=None):
+    g = np.random.default_rng(seed)
+    k = amp if amp is not None else 1.0 / np.sqrt(H)
+    W = ((g.random((I, 3 * H)) * 2 - 1) * k).astype(f32)
+    R = ((g.random((H, 3 * H)) * 2 - 1) * k).astype(f32)
+    bw = ((g.random(3 * H) * 2 - 1) * k).astype(f32)
+    br = ((g.random(3 * H) * 2 - 1) * k).astype(f32)
+    return W, R, bw, br
+
+
+def _config(name):
+    if name == "8b-sym":
+        return A.default_config()
+    if name == "8b-asym":
+        return A.set_all_bitwidth(A.default_config(), 8, False)
+    if name == "c3":  # 8-bit per-channel weights, 8-bit activations, 16-bit hidden state
+        c = A.set_all_bitwidth(A.default_config(), 8, False)
+        c.op[A.GRID["h"]].bits = 16
+        return c
+    if name == "16b-act-pot2":
+        c = A.set_all_bitwidth(A.default_config(), 16, False)
+        c.chan[0].bits = c.chan[1].bits = 8
+        c.use_pot2 = 1
+        return c
+    if name == "h-unsigned":
+        c = A.set_all_bitwidth(A.default_config(), 8, False)
+        c.op[A.GRID["h"]].is_unsigned = 1
+        c.op[A.GRID["h"]].bits = 12
+        return c
+    raise KeyError(name)
+
+
+def _case(T, B, I, H, cfg_name, seed, with_h0):
+    W, R, bw, br = _weights(I, H, seed)
+    g = np.random.default_rng(seed + 100)
+    x = g.standard_normal((T, B, I)).astype(f32)
+    h0 = (g.standard_normal((B, H)) * 0.4).astype(f32) if with_h0 else None
+    _, _, stats = GO.forward_calibrate(W, R, bw, br, x, h0)
+    qp, _ = GO.make_params(A.make_ranges(stats, H), _config(cfg_name))
+    return W, R, bw, br, x, h0, qp
+
+
+def _gpu_forward(dev, W, R, bw, br, x, h0, qp, training):
+    T, B, I = x.shape
+    H = R.shape[0]
+    t = lambda a: None if a is None else torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    out = gru_ops.forward_quant_float_storage(
+        training, T, B, I, H, t(W), t(R), t(bw), t(br), t(x),
+        t(h0) if h0 is not None else torch.empty(0, device=dev), gru_ops.GRUQuantParams.from_struct(qp))
+    torch.cuda.synchronize()
+    return out
+
+
+NAMES = ("h", "v", "W_q", "R_q", "bw_q", "br_q", "x_q") + GO.MASKS
+
+
+@pytest.mark.parametrize("shape", [(5, 20, 7, 32), (4, 16, 80, 256), (3, 33, 40, 64),
+                                   (2, 5, 3, 16), (6, 48, 9, 48)])
+@pytest.mark.parametrize("cfg_name", ["8b-sym", "8b-asym", "c3", "16b-act-pot2", "h-unsigned"])
+@pytest.mark.parametrize("with_h0", [False, True])
+def test_forward_bit_exact(cuda, shape, cfg_name, with_h0):
+    T, B, I, H = shape
+    print(f"[gru fwd] shape={shape} cfg={cfg_name} h0={with_h0}", flush=True)
+    W, R, bw, br, x, h0, qp = _case(T, B, I, H, cfg_name, 1, with_h0)
+    exp = GO.forward_quant(W, R, bw, br, x, qp, h0=h0, training=True)
+    got = _gpu_forward(cuda, W, R, bw, br, x, h0, qp, True)
+    for name, tensor in zip(NAMES, got):
+        e = exp[name]
+        if e is None:
+            assert tensor.numel() == 0, name
+            continue
+        np.testing.assert_array_equal(tensor.cpu().numpy(), e, err_msg=name)
+
+
+def test_forward_eval_matches_training_h(cuda):
+    W, R, bw, br, x, h0, qp = _case(4, 16, 8, 32, "c3", 2, True)
+    tr = _gpu_forward(cuda, W, R, bw, br, x, h0, qp, True)
+    ev = _gpu_forward(cuda, W, R, bw, br, x, h0, qp, False)
+    assert torch.equal(tr[0], ev[0])
+    assert all(m.numel() == 0 for m in ev[7:])
+
+
+def test_forward_rejects_unsupported(cuda):
+    W, R, bw, br, x, h0, qp = _case(2, 4, 3, 20, "8b-sym", 3, False)  # H % 16 != 0
+    with pytest.raises(rxmet_lib.RxmetError, match="multiple of 16"):
+        _gpu_forward(cuda, W, R, bw, br, x, h0, qp, True)
