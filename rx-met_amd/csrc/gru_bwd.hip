@@ -1,0 +1,509 @@
+// gru_bwd.hip — MI355X QuantGRU backward (STE), behind rxmet_gru_backward_quant.
+//
+// Reference path: backward_quant_float_storage_wrapper (pytorch/lib/
+// gru_interface_binding.cc:789-920) dequantises the saved codes in place, transposes
+// x/W/R with torch copies, then BackwardPassQuant::Run (src/gru_backward_gpu_quant.cu:
+// 379-493) loops over t = T-1..0 from the host, launching PointwiseOperationsQuant
+// (:93-266, atomicAdd bias gradients) and an SGEMM dh += R dq per step, followed by three
+// SGEMMs (dx, dR, dW) and four mask passes.
+//
+// Here:
+//   1. prologue    : dequantised W and x for the weight-gradient GEMMs, R_q packed as
+//                    int8 MFMA fragments of the transposed product, row sums of R_q;
+//   2. recurrence  : one persistent workgroup per 16 sequences walks t = T-1..0.  Each
+//                    lane owns one hidden unit for four sequences (same layout as the
+//                    forward), so dh stays in registers between steps.  Per step: the
+//                    fused STE pointwise (all mask families), dp/dq written for the GEMMs,
+//                    bias gradients accumulated in fp64 registers; then
+//                    dh += R_deq dq on MFMA: dq * scale_R is written per sequence as a
+//                    22-bit block-fixed-point integer (exponent from the row maximum)
+//                    split into three int8 planes, so v_mfma_i32_16x16x64_i8 accumulates
+//                    exactly against the resident int8 R_q; the planes are recombined in
+//                    fp64 and rescaled (error <= 2^-22 of the row maximum per term, below
+//                    an fp32 SGEMM's rounding);
+//   3. bias fold   : per-workgroup fp64 partials summed in a fixed order (deterministic);
+//   4. dx, dW, dR  : rocBLAS SGEMMs on the dp/dq buffers, then one mask pass.
+#include <rocblas/rocblas.h>
+
+#include <mutex>
+#include <vector>
+
+#include "gru_internal.h"
+#include "mfma_frag.h"
+#include "rxmet_common.h"
+#include "rxmet_gru.h"
+
+namespace rxmet {
+namespace gru {
+
+constexpr int kBTile = 16;
+
+// ---------------------------------------------------------------------------------
+// 1. prologue
+// ---------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void dequant_inputs(int64_t nx, int64_t nw, int C,
+                                                      const float *__restrict__ xq, float eff_x,
+                                                      float zp_x, const float *__restrict__ Wq,
+                                                      const float *__restrict__ eff_w,
+                                                      float *__restrict__ xd,
+                                                      float *__restrict__ Wd) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < nx + nw;
+       i += stride) {
+    if (i < nx) {
+      xd[i] = (xq[i] - zp_x) * eff_x;
+    } else {
+      const int64_t k = i - nx;
+      Wd[k] = (Wq[k] - 0.0f) * eff_w[k % C];
+    }
+  }
+}
+
+// R_q [H][3H] -> B fragments of D[b][k] = sum_c A[b][c] R[k][c]:
+// frag[((ut * KS2) + s) * 64 + lane] holds R_q[k][c] for k = 16*ut + lane % 16,
+// c = 64*s + 16*(lane / 16) + 0..15 (zero beyond 3H).  rowsum[k] = sum_c R_q[k][c].
+__global__ __launch_bounds__(64) void pack_rt_frags(int H, int KS2, const float *__restrict__ Rq,
+                                                    v4i *__restrict__ frag,
+                                                    float *__restrict__ rowsum) {
+  const int lane = threadIdx.x;
+  const int idx = blockIdx.x;
+  const int s = idx % KS2, ut = idx / KS2;
+  const int C = 3 * H;
+  const int k = 16 * ut + lane % 16;
+  int wd[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    int by[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int c = 64 * s + 16 * (lane / 16) + 4 * q + e;
+      by[e] = (c < C && k < H) ? static_cast<int>(Rq[static_cast<size_t>(k) * C + c]) : 0;
+    }
+    wd[q] = pack4_i8(by[0], by[1], by[2], by[3]);
+  }
+  frag[static_cast<size_t>(idx) * 64 + lane] = v4i{wd[0], wd[1], wd[2], wd[3]};
+  if (s == 0 && lane < 16 && k < H) {
+    int sum = 0;
+    for (int c = 0; c < C; ++c) sum += static_cast<int>(Rq[static_cast<size_t>(k) * C + c]);
+    rowsum[k] = static_cast<float>(sum);
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// 2. backward recurrence
+// ---------------------------------------------------------------------------------
+struct BwdArgs {
+  int T, B, H, KS2;
+  const float *dh_new;       // [T+1, B, H]
+  const float *h;            // [T+1, B, H] dequantised
+  const float *v;            // [T, B, 4H] dequantised
+  const uint8_t *ih_m, *hh_m, *gin_m, *gout_m, *h_m;  // may be null
+  const uint8_t *bw_m, *br_m, *h0_m;                  // may be null
+  const v4i *rfrag;          // packed R_q fragments
+  const float *rowsum;       // [H]
+  const float *eff_r;        // [3H] effective per-channel scales of R
+  float *dp, *dq;            // [T, B, 3H]
+  double *bias_partial;      // [numWG][2][3H]
+  float *dh0;                // [B, H]
+};
+
+constexpr int kPlanes = 3;
+
+__global__ __launch_bounds__(512) void bwd_recurrence(BwdArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int H = a.H, C = 3 * H, B = a.B;
+  const int CP = a.KS2 * 64;          // padded channel count
+  const int ROW = CP + 16;            // plane row stride in bytes
+  float *dqs = reinterpret_cast<float *>(smem);                  // [16][CP] dq * scale_R
+  unsigned *rowmax = reinterpret_cast<unsigned *>(dqs + kBTile * CP);  // [16] |max| bits
+  int *rowexp = reinterpret_cast<int *>(rowmax + kBTile);              // [16]
+  int8_t *plane = reinterpret_cast<int8_t *>(rowexp + kBTile);          // [3][16][ROW]
+
+  const int tid = threadIdx.x, nthreads = blockDim.x;
+  const int w = tid / 64, l = tid % 64;
+  const int b0 = blockIdx.x * kBTile;
+
+  for (int i = tid; i < kBTile * CP; i += nthreads) dqs[i] = 0.0f;
+  for (int i = tid; i < kPlanes * kBTile * ROW / 4; i += nthreads) reinterpret_cast<int *>(plane)[i] = 0;
+  if (tid < kBTile) rowmax[tid] = 0u;
+
+  v4i rfr[2][12];
+  float rsum[2], effr[2][3];
+  uint8_t mbw[2][3], mbr[2][3];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int ut = 2 * w + u;
+    const int j = 16 * ut + l % 16;
+#pragma unroll
+    for (int s = 0; s < 12; ++s)
+      rfr[u][s] = (s < a.KS2 && 16 * ut < H) ? a.rfrag[(static_cast<size_t>(ut) * a.KS2 + s) * 64 + l]
+                                           : v4i{0, 0, 0, 0};
+    rsum[u] = j < H ? a.rowsum[j] : 0.0f;
+#pragma unroll
+    for (int g = 0; g < 3; ++g) {
+      effr[u][g] = j < H ? a.eff_r[g * H + j] : 0.0f;
+      mbw[u][g] = (j < H && a.bw_m) ? a.bw_m[g * H + j] : 1;
+      mbr[u][g] = (j < H && a.br_m) ? a.br_m[g * H + j] : 1;
+    }
+  }
+  float dh[2][4];
+  double sbw[2][3], sbr[2][3];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) dh[u][r] = 0.0f;
+#pragma unroll
+    for (int g = 0; g < 3; ++g) sbw[u][g] = sbr[u][g] = 0.0;
+  }
+  __syncthreads();
+
+  const int nrow0 = 4 * (l / 16);
+  const uint32_t BH = static_cast<uint32_t>(B) * H;
+
+  for (int t = a.T - 1; t >= 0; --t) {
+    // ---- pointwise STE backward (reference order of operations) ----
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int j = 16 * (2 * w + u) + l % 16;
+      if (16 * (2 * w + u) >= H) continue;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int nr = nrow0 + r, b = b0 + nr;
+        float dpv[3] = {0.f, 0.f, 0.f}, dqv[3] = {0.f, 0.f, 0.f};
+        if (b < B) {
+          const uint32_t oH = static_cast<uint32_t>(b) * H + j;
+          const uint32_t oC = 3u * static_cast<uint32_t>(b) * H + j;
+          const uint32_t tH = static_cast<uint32_t>(t) * BH;
+          const uint32_t tC = 3u * tH, v0 = 4u * tH + 4u * static_cast<uint32_t>(b) * H + j;
+          float dht = a.dh_new[tH + BH + oH] + dh[u][r];
+          if (a.h_m) dht *= static_cast<float>(a.h_m[tH + oH]);
+          const float z = a.v[v0], rr = a.v[v0 + H], g = a.v[v0 + 2 * H], qg = a.v[v0 + 3 * H];
+          dh[u][r] = z * dht;
+          const float dg = (1.0f - z) * dht;
+          const float dz = (a.h[tH + oH] - g) * dht;
+          const uint32_t m = tC + oC;
+          float dpg = (1.0f - g * g) * dg;
+          if (a.gout_m) dpg *= static_cast<float>(a.gout_m[m + 2 * H]);
+          if (a.gin_m) dpg *= static_cast<float>(a.gin_m[m + 2 * H]);
+          float dqg = dpg * rr;
+          const float dr = dpg * qg;
+          float dpr = rr * (1.0f - rr) * dr, dqr = dpr;
+          float dpz = z * (1.0f - z) * dz, dqz = dpz;
+          if (a.gout_m) {
+            const float mz = static_cast<float>(a.gout_m[m]), mr = static_cast<float>(a.gout_m[m + H]);
+            dpz *= mz; dqz *= mz; dpr *= mr; dqr *= mr;
+          }
+          if (a.gin_m) {
+            const float mz = static_cast<float>(a.gin_m[m]), mr = static_cast<float>(a.gin_m[m + H]);
+            dpz *= mz; dqz *= mz; dpr *= mr; dqr *= mr;
+          }
+          if (a.hh_m) {
+            dqz *= static_cast<float>(a.hh_m[m]);
+            dqr *= static_cast<float>(a.hh_m[m + H]);
+            dqg *= static_cast<float>(a.hh_m[m + 2 * H]);
+          }
+          if (a.ih_m) {
+            dpz *= static_cast<float>(a.ih_m[m]);
+            dpr *= static_cast<float>(a.ih_m[m + H]);
+            dpg *= static_cast<float>(a.ih_m[m + 2 * H]);
+          }
+          dpv[0] = dpz; dpv[1] = dpr; dpv[2] = dpg;
+          dqv[0] = dqz; dqv[1] = dqr; dqv[2] = dqg;
+#pragma unroll
+          for (int gg = 0; gg < 3; ++gg) {
+            a.dp[m + gg * H] = dpv[gg];
+            a.dq[m + gg * H] = dqv[gg];
+            sbw[u][gg] += static_cast<double>(dpv[gg] * static_cast<float>(mbw[u][gg]));
+            sbr[u][gg] += static_cast<double>(dqv[gg] * static_cast<float>(mbr[u][gg]));
+          }
+        }
+        // dq scaled by the per-channel dequantisation scale of R, staged for the GEMM
+        float mx = 0.0f;
+#pragma unroll
+        for (int gg = 0; gg < 3; ++gg) {
+          const float sv = dqv[gg] * effr[u][gg];
+          dqs[nr * CP + gg * H + j] = sv;
+          const float as = fabsf(sv);
+          mx = (as > mx || as != as) ? as : mx;  // keeps NaN
+        }
+        if (!(mx <= 3.0e38f)) mx = INFINITY;  // NaN/inf rows propagate below
+        atomicMax(&rowmax[nr], __float_as_uint(mx));
+      }
+    }
+    __syncthreads();
+    // ---- block fixed point: 22-bit integers split into three int8 planes ----
+    if (tid < kBTile) {
+      const float m = __uint_as_float(rowmax[tid]);
+      int ex = 0;
+      if (m > 0.0f && m <= 3.0e38f) frexpf(m, &ex);
+      rowexp[tid] = (m > 0.0f && m <= 3.0e38f) ? 22 - ex : (m == 0.0f ? 0 : 1000);
+    }
+    __syncthreads();
+    for (int i = tid; i < kBTile * CP; i += nthreads) {
+      const int nr = i / CP, c = i % CP;
+      const int e = rowexp[nr];
+      int q = 0;
+      if (e != 1000) q = static_cast<int>(rintf(ldexpf(dqs[i], e)));
+      const int uq = q + (1 << 23);
+      plane[(0 * kBTile + nr) * ROW + c] = static_cast<int8_t>((uq & 255) - 128);
+      plane[(1 * kBTile + nr) * ROW + c] = static_cast<int8_t>(((uq >> 8) & 255) - 128);
+      plane[(2 * kBTile + nr) * ROW + c] = static_cast<int8_t>((uq >> 16) - 128);
+    }
+    __syncthreads();
+    if (tid < kBTile) rowmax[tid] = 0u;
+    // ---- dh += R_deq dq on MFMA ----
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      if (16 * (2 * w + u) >= H) continue;
+      v4i acc[kPlanes];
+#pragma unroll
+      for (int q = 0; q < kPlanes; ++q) acc[q] = v4i{0, 0, 0, 0};
+#pragma unroll
+      for (int s = 0; s < 12; ++s) {
+        if (s < a.KS2) {
+#pragma unroll
+          for (int q = 0; q < kPlanes; ++q) {
+            const v4i afr = *reinterpret_cast<const v4i *>(plane + (q * kBTile + l % 16) * ROW +
+                                                           64 * s + 16 * (l / 16));
+            acc[q] = mfma_i8(afr, rfr[u][s], acc[q]);
+          }
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int e = rowexp[nrow0 + r];
+        const double comb = 65536.0 * acc[2][r] + 256.0 * acc[1][r] + static_cast<double>(acc[0][r]) +
+                            32896.0 * static_cast<double>(rsum[u]);
+        const float add = e == 1000 ? NAN : static_cast<float>(ldexp(comb, -e));
+        dh[u][r] = dh[u][r] + add;
+      }
+    }
+    __syncthreads();
+  }
+  // dh0 and bias partials
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int j = 16 * (2 * w + u) + l % 16;
+    if (16 * (2 * w + u) >= H) continue;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int b = b0 + nrow0 + r;
+      if (b < B) {
+        const uint32_t o = static_cast<uint32_t>(b) * H + j;
+        a.dh0[o] = a.h0_m ? dh[u][r] * static_cast<float>(a.h0_m[o]) : dh[u][r];
+      }
+    }
+    // sum the four row groups (lanes l, l^16, l^32, l^48 share the unit)
+#pragma unroll
+    for (int gg = 0; gg < 3; ++gg) {
+      double x = sbw[u][gg], y = sbr[u][gg];
+      x += __shfl_xor(x, 16, 64);
+      x += __shfl_xor(x, 32, 64);
+      y += __shfl_xor(y, 16, 64);
+      y += __shfl_xor(y, 32, 64);
+      if (l < 16) {
+        double *p = a.bias_partial + static_cast<size_t>(blockIdx.x) * 2 * C;
+        p[gg * H + j] = x;
+        p[C + gg * H + j] = y;
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void fold_bias(int nwg, int C, const double *__restrict__ part,
+                                                 float *__restrict__ dbw, float *__restrict__ dbr) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= C) return;
+  double x = 0.0, y = 0.0;
+  for (int k = 0; k < nwg; ++k) {
+    x += part[static_cast<size_t>(k) * 2 * C + c];
+    y += part[static_cast<size_t>(k) * 2 * C + C + c];
+  }
+  dbw[c] = static_cast<float>(x);
+  dbr[c] = static_cast<float>(y);
+}
+
+__global__ __launch_bounds__(256) void apply_masks(int64_t n0, int64_t n1, int64_t n2, float *d0,
+                                                   const uint8_t *m0, float *d1, const uint8_t *m1,
+                                                   float *d2, const uint8_t *m2) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n0 + n1 + n2;
+       i += stride) {
+    if (i < n0) {
+      if (m0) d0[i] *= static_cast<float>(m0[i]);
+    } else if (i < n0 + n1) {
+      if (m1) d1[i - n0] *= static_cast<float>(m1[i - n0]);
+    } else {
+      if (m2) d2[i - n0 - n1] *= static_cast<float>(m2[i - n0 - n1]);
+    }
+  }
+}
+
+size_t bwd_lds_bytes(int KS2) {
+  const int CP = KS2 * 64, ROW = CP + 16;
+  return sizeof(float) * kBTile * CP + sizeof(unsigned) * kBTile + sizeof(int) * kBTile +
+         static_cast<size_t>(kPlanes) * kBTile * ROW;
+}
+
+struct BwdWorkspace {
+  size_t dp, dq, xd, wd, rfrag, rowsum, effr, effw, bias, total;
+  BwdWorkspace(int T, int B, int I, int H) {
+    const size_t C = 3 * static_cast<size_t>(H);
+    const size_t KS2 = (C + 63) / 64;
+    const size_t nwg = (static_cast<size_t>(B) + kBTile - 1) / kBTile;
+    auto al = [](size_t x) { return (x + 255) & ~static_cast<size_t>(255); };
+    size_t o = 0;
+    dp = o; o += al(sizeof(float) * static_cast<size_t>(T) * B * C);
+    dq = o; o += al(sizeof(float) * static_cast<size_t>(T) * B * C);
+    xd = o; o += al(sizeof(float) * static_cast<size_t>(T) * B * I);
+    wd = o; o += al(sizeof(float) * static_cast<size_t>(I) * C);
+    rfrag = o; o += al(sizeof(v4i) * 64 * ((H + 15) / 16) * KS2);
+    rowsum = o; o += al(sizeof(float) * H);
+    effr = o; o += al(sizeof(float) * C);
+    effw = o; o += al(sizeof(float) * C);
+    bias = o; o += al(sizeof(double) * 2 * C * nwg);
+    total = o;
+  }
+};
+
+// rocBLAS handle per device, created once.
+static rocblas_handle blas_handle(int device) {
+  static std::mutex mu;
+  static std::vector<rocblas_handle> handles;
+  std::lock_guard<std::mutex> g(mu);
+  if (static_cast<int>(handles.size()) <= device) handles.resize(device + 1, nullptr);
+  if (!handles[device]) rocblas_create_handle(&handles[device]);
+  return handles[device];
+}
+
+// Row-major C[M][N] = op(A) op(B) with rocBLAS (column-major) arguments swapped.
+static rocblas_status gemm_rm(rocblas_handle h, bool ta, bool tb, int M, int N, int K,
+                              const float *A, int lda, const float *Bm, int ldb, float *Cm,
+                              int ldc) {
+  const float one = 1.0f, zero = 0.0f;
+  return rocblas_sgemm(h, tb ? rocblas_operation_transpose : rocblas_operation_none,
+                       ta ? rocblas_operation_transpose : rocblas_operation_none, N, M, K, &one, Bm,
+                       ldb, A, lda, &zero, Cm, ldc);
+}
+
+}  // namespace gru
+}  // namespace rxmet
+
+using namespace rxmet;
+using namespace rxmet::gru;
+
+extern "C" {
+
+int64_t rxmet_gru_backward_workspace_bytes(int32_t T, int32_t B, int32_t I, int32_t H) {
+  if (T < 0 || B < 0 || I < 0 || H < 0) return 0;
+  return static_cast<int64_t>(BwdWorkspace(T, B, I, H).total);
+}
+
+int rxmet_gru_backward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const float *W_q,
+                             const float *R_q, const float *bw_q, const float *br_q,
+                             const float *x_q, const float *dh_new, const float *h,
+                             const float *v, const rxmet_gru_qparams *params,
+                             const uint8_t *x_mask, const uint8_t *h0_mask,
+                             const uint8_t *W_mask, const uint8_t *R_mask,
+                             const uint8_t *bw_mask, const uint8_t *br_mask,
+                             const uint8_t *ih_mask, const uint8_t *hh_mask,
+                             const uint8_t *gate_in_mask, const uint8_t *gate_out_mask,
+                             const uint8_t *h_mask, float *dx, float *dW, float *dR, float *dbw,
+                             float *dbr, float *dh0, void *workspace, void *stream_) {
+  (void)bw_q;
+  (void)br_q;
+  clear_error();
+  RXMET_CHECK_ARG(params != nullptr, "params must be non-null");
+  RXMET_CHECK_ARG(T >= 1 && B >= 1 && I >= 1 && H >= 1, "dimensions must be positive");
+  RXMET_CHECK_ARG(params->hidden == H, "params.hidden != hidden_size");
+  RXMET_CHECK_ARG(H % 16 == 0 && H <= 256,
+                  "hidden_size must be a multiple of 16 and at most 256 for the MFMA recurrence");
+  RXMET_CHECK_ARG(W_q && R_q && x_q && dh_new && h && v && dx && dW && dR && dbw && dbr && dh0 &&
+                      workspace,
+                  "required pointer is null");
+  RXMET_CHECK_ARG(params->chan_bits[RXMET_GRU_R] <= 8 && !params->chan_unsigned[RXMET_GRU_R],
+                  "recurrent weights wider than signed 8 bits are not supported");
+  RXMET_CHECK_ARG(static_cast<double>(T + 1) * B * 4 * H < 4294967295.0,
+                  "T*B*H too large for the recurrence's 32-bit element offsets");
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  const int C = 3 * H;
+  const int KS2 = (C + 63) / 64;
+  const BwdWorkspace ws(T, B, I, H);
+  char *wsb = static_cast<char *>(workspace);
+  float *dp = reinterpret_cast<float *>(wsb + ws.dp);
+  float *dq = reinterpret_cast<float *>(wsb + ws.dq);
+  float *xd = reinterpret_cast<float *>(wsb + ws.xd);
+  float *wd = reinterpret_cast<float *>(wsb + ws.wd);
+  v4i *rfrag = reinterpret_cast<v4i *>(wsb + ws.rfrag);
+  float *rowsum = reinterpret_cast<float *>(wsb + ws.rowsum);
+  float *effr = reinterpret_cast<float *>(wsb + ws.effr);
+  float *effw = reinterpret_cast<float *>(wsb + ws.effw);
+  double *bias = reinterpret_cast<double *>(wsb + ws.bias);
+
+  std::vector<float> host(8 * static_cast<size_t>(C));
+  try {
+    make_channel_factors(*params, H, host.data() + 4 * C, host.data() + 5 * C, host.data() + 6 * C,
+                         host.data() + 7 * C, host.data(), host.data() + C, host.data() + 2 * C,
+                         host.data() + 3 * C);
+  } catch (const std::exception &e) {
+    set_error(e.what());
+    return -22;
+  }
+  RXMET_CHECK_HIP(hipMemcpyAsync(effw, host.data(), sizeof(float) * C, hipMemcpyHostToDevice, stream));
+  RXMET_CHECK_HIP(hipMemcpyAsync(effr, host.data() + C, sizeof(float) * C, hipMemcpyHostToDevice,
+                                 stream));
+  const float eff_x = effective_scale(params->g[RXMET_GRU_X].scale, params->use_pot2 != 0);
+  const float zp_x = static_cast<float>(params->g[RXMET_GRU_X].zero_point);
+
+  const int64_t nx = static_cast<int64_t>(T) * B * I, nw = static_cast<int64_t>(I) * C;
+  int64_t blocks = (nx + nw + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  hipLaunchKernelGGL(dequant_inputs, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, nx,
+                     nw, C, x_q, eff_x, zp_x, W_q, effw, xd, wd);
+  RXMET_CHECK_LAUNCH();
+  hipLaunchKernelGGL(pack_rt_frags, dim3((H / 16) * KS2), dim3(64), 0, stream, H, KS2, R_q, rfrag,
+                     rowsum);
+  RXMET_CHECK_LAUNCH();
+
+  BwdArgs ba;
+  ba.T = T; ba.B = B; ba.H = H; ba.KS2 = KS2;
+  ba.dh_new = dh_new; ba.h = h; ba.v = v;
+  ba.ih_m = ih_mask; ba.hh_m = hh_mask; ba.gin_m = gate_in_mask; ba.gout_m = gate_out_mask;
+  ba.h_m = h_mask; ba.bw_m = bw_mask; ba.br_m = br_mask; ba.h0_m = h0_mask;
+  ba.rfrag = rfrag; ba.rowsum = rowsum; ba.eff_r = effr;
+  ba.dp = dp; ba.dq = dq; ba.bias_partial = bias; ba.dh0 = dh0;
+  const int nwg = (B + kBTile - 1) / kBTile;
+  const size_t lds = bwd_lds_bytes(KS2);
+  RXMET_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&bwd_recurrence),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      static_cast<int>(lds)));
+  hipLaunchKernelGGL(bwd_recurrence, dim3(nwg), dim3(64 * ((H + 31) / 32)), lds, stream, ba);
+  RXMET_CHECK_LAUNCH();
+  hipLaunchKernelGGL(fold_bias, dim3((C + 255) / 256), dim3(256), 0, stream, nwg, C, bias, dbw, dbr);
+  RXMET_CHECK_LAUNCH();
+
+  int device = 0;
+  RXMET_CHECK_HIP(hipGetDevice(&device));
+  rocblas_handle bh = blas_handle(device);
+  RXMET_CHECK_ARG(bh != nullptr, "rocBLAS handle creation failed");
+  rocblas_set_stream(bh, stream);
+  const int M = T * B;
+  // dx[M][I] = dp[M][C] * W_deq^T
+  RXMET_CHECK_ARG(gemm_rm(bh, false, true, M, I, C, dp, C, wd, C, dx, I) == rocblas_status_success,
+                  "rocBLAS sgemm (dx) failed");
+  // dW[I][C] = x_deq^T * dp
+  RXMET_CHECK_ARG(gemm_rm(bh, true, false, I, C, M, xd, I, dp, C, dW, C) == rocblas_status_success,
+                  "rocBLAS sgemm (dW) failed");
+  // dR[H][C] = h_prev^T * dq   (h rows 0..T-1)
+  RXMET_CHECK_ARG(gemm_rm(bh, true, false, H, C, M, h, H, dq, C, dR, C) == rocblas_status_success,
+                  "rocBLAS sgemm (dR) failed");
+  const int64_t n0 = nx, n1 = nw, n2 = static_cast<int64_t>(H) * C;
+  blocks = (n0 + n1 + n2 + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  hipLaunchKernelGGL(apply_masks, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, n0, n1,
+                     n2, dx, x_mask, dW, W_mask, dR, R_mask);
+  RXMET_CHECK_LAUNCH();
+  return 0;
+}
+
+}  // extern "C"

@@ -121,3 +121,46 @@ def test_forward_rejects_unsupported(cuda):
     W, R, bw, br, x, h0, qp = _case(2, 4, 3, 20, "8b-sym", 3, False)  # H % 16 != 0
     with pytest.raises(rxmet_lib.RxmetError, match="multiple of 16"):
         _gpu_forward(cuda, W, R, bw, br, x, h0, qp, True)
+
+
+def _gpu_backward(dev, fwd, dh_new, qp, T, B, I, H):
+    (h, v, W_q, R_q, bw_q, br_q, x_q, *masks) = fwd
+    dh = torch.from_numpy(np.ascontiguousarray(dh_new)).to(dev)
+    out = gru_ops.backward_quant_float_storage(T, B, I, H, W_q, R_q, bw_q, br_q, x_q, dh, h, v,
+                                               gru_ops.GRUQuantParams.from_struct(qp), *masks)
+    torch.cuda.synchronize()
+    return [t.cpu().numpy() for t in out]
+
+
+@pytest.mark.parametrize("shape", [(5, 20, 7, 32), (4, 16, 80, 256), (3, 33, 40, 64),
+                                   (6, 48, 9, 48), (12, 64, 16, 128)])
+@pytest.mark.parametrize("cfg_name", ["8b-sym", "8b-asym", "c3", "16b-act-pot2"])
+@pytest.mark.parametrize("with_h0", [False, True])
+def test_backward_matches_oracle(cuda, shape, cfg_name, with_h0):
+    T, B, I, H = shape
+    print(f"[gru bwd] shape={shape} cfg={cfg_name} h0={with_h0}", flush=True)
+    W, R, bw, br, x, h0, qp = _case(T, B, I, H, cfg_name, 4, with_h0)
+    exp_f = GO.forward_quant(W, R, bw, br, x, qp, h0=h0, training=True)
+    fwd = _gpu_forward(cuda, W, R, bw, br, x, h0, qp, True)
+    g = np.random.default_rng(5)
+    dh_new = np.zeros((T + 1, B, H), f32)
+    dh_new[1:] = (g.standard_normal((T, B, H)) * 1e-3).astype(f32)
+    dh_new[-1] += (g.standard_normal((B, H)) * 1e-3).astype(f32)
+    exp = GO.backward_quant(exp_f, dh_new, qp)
+    got = _gpu_backward(cuda, fwd, dh_new, qp, T, B, I, H)
+    for name, a in zip(("dx", "dW", "dR", "dbw", "dbr", "dh0"), got):
+        e = exp[name]
+        scale = max(float(np.abs(e).max()), 1e-30)
+        np.testing.assert_allclose(a, e, rtol=1e-4, atol=1e-5 * scale, err_msg=name)
+
+
+def test_backward_without_masks_and_nan_propagation(cuda):
+    T, B, I, H = 3, 16, 5, 32
+    W, R, bw, br, x, h0, qp = _case(T, B, I, H, "8b-asym", 6, False)
+    fwd = _gpu_forward(cuda, W, R, bw, br, x, None, qp, True)
+    dh_new = np.zeros((T + 1, B, H), f32)
+    dh_new[1:] = 1e-3
+    dh_new[2, 3, 7] = np.nan
+    got = _gpu_backward(cuda, fwd, dh_new, qp, T, B, I, H)
+    assert np.isnan(got[5][3]).any(), "NaN upstream gradient must reach dh0 of its sequence"
+    assert np.isfinite(np.delete(got[5], 3, axis=0)).all(), "NaN leaked into other sequences"
