@@ -6,6 +6,7 @@
  * QAT path uses:
  *   calculate_gru_quantitative_parameters -> rxmet_gru_make_params
  *   forward_calibrate (MINMAX)            -> rxmet_gru_forward_calibrate
+ *   forward_fp (inference)                -> rxmet_gru_forward_fp
  *   forward_quant_float_storage           -> rxmet_gru_forward_quant
  *   backward_quant_float_storage          -> rxmet_gru_backward_quant
  *   (LUT regeneration in GRUQuantParamsPy::to_cpp) -> rxmet_gru_make_luts
@@ -200,6 +201,17 @@ int rxmet_gru_forward_calibrate(int32_t T, int32_t B, int32_t I, int32_t H, cons
                                 const float *R, const float *bw, const float *br,
                                 const float *x, const float *h0, float *h, float *v,
                                 float *stats, void *workspace, void *stream);
+
+/*
+ * Float GRU forward without quantisation: forward_fp
+ * (pytorch/lib/gru_interface_binding.cc:656-697, hasteGRUForward).  Same kernel and
+ * summation order as rxmet_gru_forward_calibrate, no statistics.  Writes h [T+1,B,H]
+ * and, when is_training is non-zero, v [T,B,4H] (z, r, n, hh_n); v may be null
+ * otherwise.  h0 may be null (zeros).  Needs no workspace.
+ */
+int rxmet_gru_forward_fp(int32_t is_training, int32_t T, int32_t B, int32_t I, int32_t H,
+                         const float *W, const float *R, const float *bw, const float *br,
+                         const float *x, const float *h0, float *h, float *v, void *stream);
 
 #ifdef __cplusplus
 }

@@ -12,7 +12,8 @@
 //      rint(b_q * ratio) the pointwise step needs (they do not change over time);
 //   2. quant_input   : x and h0 quantisation (codes + masks), h[0] dequantised;
 //   3. code_gemm     : the time-parallel input projection W_q x_q summed exactly in
-//      int32 and rounded once to fp32;
+//      int32 (int64 when 16-bit codes and long rows could reach 2^31) and rounded once
+//      to fp32;
 //   4. recurrence    : one persistent workgroup per 16 sequences runs all T steps.  The
 //      recurrent weights R_q live in VGPRs as int8 MFMA fragments for the whole kernel;
 //      h_t lives in LDS as int8 planes (16-bit codes are split into a high and a
@@ -121,6 +122,7 @@ __global__ __launch_bounds__(256) void quant_input(int64_t nx, int64_t nh, const
 // ---------------------------------------------------------------------------------
 // 3. exact code GEMM  C[M][N] = A[M][K] * B[K][N]  (integer codes stored as fp32)
 // ---------------------------------------------------------------------------------
+template <typename Acc>
 __global__ __launch_bounds__(256) void code_gemm(int M, int N, int K, const float *__restrict__ A,
                                                  const float *__restrict__ Bm,
                                                  float *__restrict__ Cm) {
@@ -128,7 +130,7 @@ __global__ __launch_bounds__(256) void code_gemm(int M, int N, int K, const floa
   __shared__ int Bs[16][64];
   const int tm = blockIdx.y * 64, tn = blockIdx.x * 64;
   const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
-  int acc[4][4] = {};
+  Acc acc[4][4] = {};
   for (int k0 = 0; k0 < K; k0 += 16) {
     for (int q = 0; q < 4; ++q) {
       const int e = threadIdx.x + 256 * q;
@@ -150,7 +152,7 @@ __global__ __launch_bounds__(256) void code_gemm(int M, int N, int K, const floa
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] += av[i] * bv[j];
+        for (int j = 0; j < 4; ++j) acc[i][j] += static_cast<Acc>(av[i]) * bv[j];
     }
     __syncthreads();
   }
@@ -282,7 +284,6 @@ __global__ __launch_bounds__(512) void recurrence(RecArgs a, StepParams p) {
   __syncthreads();
 
   const float plane_off = 128.0f + a.h_offset;  // added back with the column sums (NPL == 2)
-  const size_t TBH = static_cast<size_t>(B) * H;
   const int nrow0 = 4 * (l / 16);                // first of the 4 batch rows owned
 
   for (int t = 0; t < a.T; ++t) {
@@ -478,12 +479,11 @@ int rxmet_gru_forward_quant(int32_t is_training, int32_t T, int32_t B, int32_t I
                         gate_in_mask && gate_out_mask && h_mask && (h0 == nullptr || h0_mask),
                     "training needs v and every mask output");
   }
-  {
-    // exact-int32 bound of the input projection
-    const double xmax = std::ldexp(1.0, params->g[RXMET_GRU_X].bits);
-    const double wmax = std::ldexp(1.0, params->chan_bits[RXMET_GRU_W] - 1);
-    RXMET_CHECK_ARG(xmax * wmax * I < 2147483647.0, "input projection would overflow int32");
-  }
+  // the input projection accumulates in int32 when |x_q| |W_q| I cannot reach 2^31,
+  // otherwise in int64 (codes are at most 16 bits, I < 2^31: always exact)
+  const bool wide_gemm = std::ldexp(1.0, params->g[RXMET_GRU_X].bits) *
+                             std::ldexp(1.0, params->chan_bits[RXMET_GRU_W] - 1) * I >=
+                         2147483647.0;
   RXMET_CHECK_ARG(static_cast<double>(T + 1) * B * 4 * H < 4294967295.0,
                   "T*B*H too large for the recurrence's 32-bit element offsets");
   hipStream_t stream = static_cast<hipStream_t>(stream_);
@@ -544,8 +544,12 @@ int rxmet_gru_forward_quant(int32_t is_training, int32_t T, int32_t B, int32_t I
   RXMET_CHECK_LAUNCH();
 
   const int M = T * B;
-  hipLaunchKernelGGL(code_gemm, dim3((C + 63) / 64, (M + 63) / 64), dim3(256), 0, stream, M, C, I,
-                     x_q, W_q, gih);
+  if (wide_gemm)
+    hipLaunchKernelGGL(code_gemm<long long>, dim3((C + 63) / 64, (M + 63) / 64), dim3(256), 0,
+                       stream, M, C, I, x_q, W_q, gih);
+  else
+    hipLaunchKernelGGL(code_gemm<int>, dim3((C + 63) / 64, (M + 63) / 64), dim3(256), 0, stream,
+                       M, C, I, x_q, W_q, gih);
   RXMET_CHECK_LAUNCH();
 
   RecArgs ra;

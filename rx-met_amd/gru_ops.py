@@ -187,14 +187,44 @@ def forward_calibrate(is_training, time_steps, batch_size, input_size, hidden_si
     dev = x.device
     T, B, I, H = time_steps, batch_size, input_size, hidden_size
     h = torch.empty((T + 1, B, H), dtype=torch.float32, device=dev)
-    v = torch.empty((T, B, 4 * H), dtype=torch.float32, device=dev)
+    # gate values are only materialised when asked for (is_training); the ranges never need them
+    v = torch.empty((T, B, 4 * H) if is_training else (0,), dtype=torch.float32, device=dev)
+    if quant_ranges is None:
+        raise RuntimeError("forward_calibrate needs quant_ranges (MinMax statistics)")
+    if quant_ranges.hidden_ != H:
+        raise RuntimeError("quant_ranges hidden size does not match hidden_size")
+    if tuple(x.shape) != (T, B, I) or tuple(W.shape) != (I, 3 * H) or tuple(R.shape) != (H, 3 * H):
+        raise RuntimeError("x/W/R shapes do not match (time_steps, batch_size, input_size, "
+                           "hidden_size)")
     if quant_ranges.stats.device != dev:
         quant_ranges.stats = quant_ranges.stats.to(dev)
     h0p = h0.data_ptr() if (h0 is not None and h0.numel() > 0) else None
     ws = _ws(_rx.load().rxmet_gru_calibrate_workspace_bytes(T, B, I, H), dev)
     _rx.call("rxmet_gru_forward_calibrate", T, B, I, H, W.data_ptr(), R.data_ptr(), bw.data_ptr(),
-             br.data_ptr(), x.data_ptr(), h0p, h.data_ptr(), v.data_ptr(),
+             br.data_ptr(), x.data_ptr(), h0p, h.data_ptr(), v.data_ptr() if is_training else None,
              quant_ranges.stats.data_ptr(), ws.data_ptr(), _stream(dev))
+    return h, v
+
+
+def forward_fp(is_training, time_steps, batch_size, input_size, hidden_size, W, R, bw, br, x,
+               h0=None):
+    """Float GRU forward (forward_fp_wrapper, gru_interface_binding.cc:656-697).
+    Returns (h [T+1,B,H], v [T,B,4H]); v is empty when is_training is False."""
+    for n, t in (("W", W), ("R", R), ("bw", bw), ("br", br), ("x", x)):
+        _check_f32_cuda(n, t)
+    T, B, I, H = time_steps, batch_size, input_size, hidden_size
+    dev = x.device
+    has_h0 = h0 is not None and h0.numel() > 0
+    if has_h0:
+        _check_f32_cuda("h0", h0)
+        if tuple(h0.shape) != (B, H):
+            raise RuntimeError("h0 must have shape [batch_size, hidden_size]")
+    h = torch.empty((T + 1, B, H), dtype=torch.float32, device=dev)
+    v = torch.empty((T, B, 4 * H) if is_training else (0,), dtype=torch.float32, device=dev)
+    _rx.call("rxmet_gru_forward_fp", int(bool(is_training)), T, B, I, H, W.data_ptr(),
+             R.data_ptr(), bw.data_ptr(), br.data_ptr(), x.data_ptr(),
+             h0.data_ptr() if has_h0 else None, h.data_ptr(),
+             v.data_ptr() if is_training else None, _stream(dev))
     return h, v
 
 

@@ -1,0 +1,610 @@
+"""QuantGRU for MI355X: an ``nn.GRU``-compatible module whose QAT forward/backward and
+MinMax calibration run in librxmet.so.
+
+Mirrors the public surface of the reference module
+(``operators/quant-gru/pytorch/quant_gru.py``): ``QuantGRU`` (:1120-2306), ``GRUFunction``
+(:807-1102), the weight-format helpers (:664-806) and the operator map (:181-262), with
+the reference's names, argument meanings and error behaviour, so a user can swap the
+import.  Every numerical step goes through ``gru_ops`` (the replacement of the
+reference's pybind module), which calls the HIP kernels; nothing here computes on the CPU.
+
+Not provided (raise ``NotImplementedError`` with the reason): ``num_layers > 1`` and
+dropout (as in the reference), histogram calibration ('sqnr', 'percentile'), the int32
+quantised-value storage and the backward of the float (``use_quantization=False``) path;
+its forward runs on the GPU.
+"""
+from __future__ import annotations
+
+from contextlib import contextmanager
+from typing import Optional, Tuple
+
+import torch
+import torch.nn as nn
+
+import gru_ops
+
+# ------------------------------------------------------------------------------------
+# Operator map (quant_gru.py:181-262): public operator name -> config attribute names.
+# ------------------------------------------------------------------------------------
+
+
+def _op_info(base: str, per_channel: bool = False, default_unsigned: bool = False) -> dict:
+    return {"bw_attr": base, "sym_attr": f"{base}symmetric_", "unsigned_attr": f"{base}unsigned_",
+            "scale_attr": f"scale_{base}", "zp_attr": None if per_channel else f"zp_{base}",
+            "is_per_channel": per_channel, "default_unsigned": default_unsigned}
+
+
+_OPERATOR_MAP = {
+    "input": _op_info("x_"),
+    "output": _op_info("h_"),
+    "weight_ih": _op_info("W_", per_channel=True),
+    "weight_hh": _op_info("R_", per_channel=True),
+    "bias_ih": _op_info("bw_", per_channel=True),
+    "bias_hh": _op_info("br_", per_channel=True),
+    "weight_ih_linear": _op_info("weight_ih_linear_"),
+    "weight_hh_linear": _op_info("weight_hh_linear_"),
+    "update_gate_input": _op_info("update_gate_input_"),
+    "update_gate_output": _op_info("update_gate_output_", default_unsigned=True),
+    "reset_gate_input": _op_info("reset_gate_input_"),
+    "reset_gate_output": _op_info("reset_gate_output_", default_unsigned=True),
+    "new_gate_input": _op_info("new_gate_input_"),
+    "new_gate_output": _op_info("new_gate_output_"),
+    "mul_reset_hidden": _op_info("mul_reset_hidden_"),
+    "mul_old_contribution": _op_info("mul_old_contribution_"),
+    "mul_new_contribution": _op_info("mul_new_contribution_"),
+}
+_VALID_BITWIDTH_ATTRS = {i["bw_attr"] for i in _OPERATOR_MAP.values()}
+_VALID_SYMMETRIC_ATTRS = {i["sym_attr"] for i in _OPERATOR_MAP.values()}
+_VALID_UNSIGNED_ATTRS = {i["unsigned_attr"] for i in _OPERATOR_MAP.values()}
+_WEIGHT_SYMMETRIC_ATTRS = {"W_symmetric_", "R_symmetric_", "bw_symmetric_", "br_symmetric_"}
+_ACTIVATION_SYMMETRIC_ATTRS = _VALID_SYMMETRIC_ATTRS - _WEIGHT_SYMMETRIC_ATTRS
+
+
+def _validate_operator_map() -> None:
+    """Import-time check that every mapped attribute exists on the config object
+    (quant_gru.py:264-296)."""
+    cfg = gru_ops.OperatorQuantConfig()
+    missing = [f"{op} -> {a}" for op, info in _OPERATOR_MAP.items()
+               for a in (info["bw_attr"], info["sym_attr"]) if not hasattr(cfg, a)]
+    if missing:
+        raise RuntimeError(f"_OPERATOR_MAP does not match OperatorQuantConfig: {missing}")
+
+
+_validate_operator_map()
+
+# ------------------------------------------------------------------------------------
+# Weight-format helpers (quant_gru.py:664-759).  PyTorch stores gates as (r, z, n) rows;
+# the kernels take (z, r, n) columns, i.e. W [I, 3H] and R [H, 3H].
+# ------------------------------------------------------------------------------------
+
+_GATE_PERM = {}
+
+
+def _gate_perm(n3: int, device) -> torch.Tensor:
+    key = (n3, str(device))
+    perm = _GATE_PERM.get(key)
+    if perm is None:
+        h = n3 // 3
+        perm = torch.cat([torch.arange(h, 2 * h), torch.arange(0, h),
+                          torch.arange(2 * h, 3 * h)]).to(device)
+        _GATE_PERM[key] = perm
+    return perm
+
+
+def reorder_weights_pytorch_to_haste(w: torch.Tensor) -> torch.Tensor:
+    """(r, z, n) -> (z, r, n) along dim 0 (quant_gru.py:664-686); an involution."""
+    w = w.contiguous()
+    return w.index_select(0, _gate_perm(w.shape[0], w.device)).contiguous()
+
+
+def reorder_weights_haste_to_pytorch(w: torch.Tensor) -> torch.Tensor:
+    """(z, r, n) -> (r, z, n) along dim 0 (quant_gru.py:689-702)."""
+    return reorder_weights_pytorch_to_haste(w)
+
+
+def ensure_cuda_float32(tensor: torch.Tensor, device: torch.device) -> torch.Tensor:
+    """quant_gru.py:705-711."""
+    if tensor.device != device:
+        tensor = tensor.to(device)
+    if tensor.dtype != torch.float32:
+        tensor = tensor.float()
+    return tensor
+
+
+def convert_weights_to_haste_format(weight_ih, weight_hh, bias_ih, bias_hh, hidden_size: int,
+                                    device) -> Tuple[torch.Tensor, ...]:
+    """(W [I,3H], R [H,3H], bw [3H], br [3H]) in kernel layout (quant_gru.py:714-759).
+    Missing biases become zeros."""
+    W = reorder_weights_pytorch_to_haste(ensure_cuda_float32(weight_ih, device)).t().contiguous()
+    R = reorder_weights_pytorch_to_haste(ensure_cuda_float32(weight_hh, device)).t().contiguous()
+    if bias_ih is not None and bias_hh is not None:
+        bw = reorder_weights_pytorch_to_haste(ensure_cuda_float32(bias_ih, device))
+        br = reorder_weights_pytorch_to_haste(ensure_cuda_float32(bias_hh, device))
+    else:
+        bw = torch.zeros(3 * hidden_size, device=device, dtype=torch.float32)
+        br = torch.zeros(3 * hidden_size, device=device, dtype=torch.float32)
+    return W, R, bw, br
+
+
+def get_quant_range(bitwidth: int, is_unsigned: bool = False) -> Tuple[int, int]:
+    """Integer grid of a bit width (quant_gru.py:766-797)."""
+    if not 1 <= bitwidth <= 32:
+        raise ValueError(f"bitwidth must be in range [1, 32], got {bitwidth}")
+    if is_unsigned:
+        return 0, (1 << bitwidth) - 1
+    return -(1 << (bitwidth - 1)), (1 << (bitwidth - 1)) - 1
+
+
+def _require_device(t: torch.Tensor) -> torch.device:
+    if not t.is_cuda:
+        raise RuntimeError("QuantGRU runs on the GPU: move the module and its inputs to a "
+                           "CUDA (ROCm) device")
+    return t.device
+
+
+# ------------------------------------------------------------------------------------
+# GRUFunction (quant_gru.py:807-1102)
+# ------------------------------------------------------------------------------------
+
+
+class GRUFunction(torch.autograd.Function):
+    """One direction of a quantised GRU.  forward: weight reorder -> forward_quant_float_storage;
+    backward: dh_new [T+1,B,H] (dh_new[0]=0, dh_new[1:]=grad_output, grad_h_n added to the last
+    step) -> backward_quant_float_storage -> gradients reordered back to (r, z, n)."""
+
+    @staticmethod
+    def forward(ctx, input, weight_ih, weight_hh, bias_ih, bias_hh, h0, is_training,
+                use_quantization=False, quant_params=None, quant_storage_dtype="float32"):
+        T, B, I = input.shape
+        H = weight_hh.shape[1]
+        ctx.dims = (T, B, I, H)
+        ctx.use_quantization = bool(use_quantization)
+        if not use_quantization:
+            device = _require_device(input)
+            W, R, bw, br = convert_weights_to_haste_format(weight_ih, weight_hh, bias_ih, bias_hh,
+                                                           H, device)
+            h0_t = ensure_cuda_float32(h0, device).contiguous() if h0 is not None else None
+            h_full, _ = gru_ops.forward_fp(False, T, B, I, H, W, R, bw, br,
+                                           ensure_cuda_float32(input, device).contiguous(), h0_t)
+            return h_full[1:], h_full[-1:]
+        if quant_params is None:
+            raise RuntimeError("quant_params is required when use_quantization=True")
+        if quant_storage_dtype != "float32":
+            raise NotImplementedError("only quant_storage_dtype='float32' is provided")
+        device = _require_device(input)
+        input = ensure_cuda_float32(input, device).contiguous()
+        W, R, bw, br = convert_weights_to_haste_format(weight_ih, weight_hh, bias_ih, bias_hh, H,
+                                                       device)
+        h0_t = (ensure_cuda_float32(h0, device).contiguous() if h0 is not None
+                else torch.empty(0, device=device, dtype=torch.float32))
+        outs = gru_ops.forward_quant_float_storage(
+            is_training=is_training, time_steps=T, batch_size=B, input_size=I, hidden_size=H,
+            W=W, R=R, bw=bw, br=br, x=input, h0=h0_t, quant_params=quant_params)
+        h_full = outs[0]
+        ctx.bias_none = (bias_ih is None, bias_hh is None)
+        ctx.h0_is_none = h0 is None
+        ctx.quant_params = quant_params
+        ctx.saved_state = bool(is_training)
+        if is_training:
+            # (W_q, R_q, bw_q, br_q, x_q, h, v, 11 masks) as the backward consumes them
+            ctx.save_for_backward(outs[2], outs[3], outs[4], outs[5], outs[6], h_full, outs[1],
+                                  *outs[7:])
+        return h_full[1:], h_full[-1:]
+
+    @staticmethod
+    def backward(ctx, grad_output, grad_h_n):
+        if not ctx.use_quantization:
+            raise NotImplementedError("the float GRU backward (use_quantization=False training) "
+                                      "is not provided by the MI355X build")
+        if not ctx.saved_state:
+            raise RuntimeError("QuantGRU forward ran without saving backward state (no_grad "
+                               "eval); rerun it with gradients enabled")
+        T, B, I, H = ctx.dims
+        saved = ctx.saved_tensors
+        W_q, R_q, bw_q, br_q, x_q, h, v = saved[:7]
+        masks = saved[7:]
+        dh_new = torch.zeros((T + 1, B, H), device=h.device, dtype=torch.float32)
+        if grad_output is not None:
+            dh_new[1:] = grad_output
+        if grad_h_n is not None and grad_h_n.numel() > 0:
+            dh_new[-1] += grad_h_n[0]
+        dx, dW, dR, dbw, dbr, dh = gru_ops.backward_quant_float_storage(
+            time_steps=T, batch_size=B, input_size=I, hidden_size=H, W_q=W_q, R_q=R_q,
+            bw_q=bw_q, br_q=br_q, x_q=x_q, dh_new=dh_new, h=h, v=v,
+            quant_params=ctx.quant_params, **dict(zip(gru_ops.MASK_NAMES, masks)))
+        dW_pt = reorder_weights_haste_to_pytorch(dW.t())
+        dR_pt = reorder_weights_haste_to_pytorch(dR.t())
+        dbw_pt = None if ctx.bias_none[0] else reorder_weights_haste_to_pytorch(dbw)
+        dbr_pt = None if ctx.bias_none[1] else reorder_weights_haste_to_pytorch(dbr)
+        dh0 = None if ctx.h0_is_none else dh
+        return dx, dW_pt, dR_pt, dbw_pt, dbr_pt, dh0, None, None, None, None
+
+
+# ------------------------------------------------------------------------------------
+# QuantGRU (quant_gru.py:1120-2306)
+# ------------------------------------------------------------------------------------
+
+
+class QuantGRU(nn.Module):
+    """nn.GRU-compatible quantisation-aware GRU (single layer, optional bidirectional).
+
+    Workflow as in the reference: ``calibrating=True`` + forward collects MinMax ranges
+    (on the GPU), ``use_quantization=True`` turns on fake-quantised execution; grids are
+    derived lazily (dirty flag) on the next quantised forward or by ``finalize_calibration``.
+    """
+
+    owns_quantization = True
+
+    def __init__(self, input_size: int, hidden_size: int, num_layers: int = 1, bias: bool = True,
+                 batch_first: bool = False, dropout: float = 0.0, bidirectional: bool = False,
+                 use_quantization: bool = False, use_po2_scale: Optional[bool] = None,
+                 quant_storage_dtype: str = "float32", *, use_pot2_scale: Optional[bool] = None):
+        super().__init__()
+        if num_layers != 1:
+            raise NotImplementedError("only num_layers=1 is supported")
+        if dropout > 0:
+            raise NotImplementedError("dropout is not supported")
+        if quant_storage_dtype not in ("float32", "int32"):
+            raise ValueError("quant_storage_dtype must be 'float32' or 'int32', got "
+                             f"{quant_storage_dtype}")
+        if (use_po2_scale is not None and use_pot2_scale is not None
+                and bool(use_po2_scale) != bool(use_pot2_scale)):
+            raise ValueError("use_po2_scale and use_pot2_scale conflict")
+        self.input_size = input_size
+        self.hidden_size = hidden_size
+        self.num_layers = num_layers
+        self.bias = bias
+        self.batch_first = batch_first
+        self.dropout = dropout
+        self.bidirectional = bidirectional
+        self.use_quantization = use_quantization
+        self.num_directions = 2 if bidirectional else 1
+        self.quant_storage_dtype = quant_storage_dtype
+        self.export_mode = False
+        self._use_pot2_scale = bool(use_po2_scale if use_po2_scale is not None
+                                    else use_pot2_scale)
+
+        g3 = 3 * hidden_size
+        for sfx in ("", "_reverse") if bidirectional else ("",):
+            setattr(self, "weight_ih_l0" + sfx, nn.Parameter(torch.empty(g3, input_size)))
+            setattr(self, "weight_hh_l0" + sfx, nn.Parameter(torch.empty(g3, hidden_size)))
+            if bias:
+                setattr(self, "bias_ih_l0" + sfx, nn.Parameter(torch.empty(g3)))
+                setattr(self, "bias_hh_l0" + sfx, nn.Parameter(torch.empty(g3)))
+            else:
+                self.register_parameter("bias_ih_l0" + sfx, None)
+                self.register_parameter("bias_hh_l0" + sfx, None)
+        self.reset_parameters()
+
+        self.quant_ranges = None
+        self.quant_params = None
+        if bidirectional:
+            self.quant_ranges_reverse = None
+            self.quant_params_reverse = None
+        self._quant_params_dirty = False
+        self._quant_params_locked = False
+        self._bitwidth_config = gru_ops.OperatorQuantConfig()
+        self._bitwidth_config.usePOT2_ = self._use_pot2_scale
+        self._module_name = None
+        self.calibration_method = "minmax"
+        self.percentile_value = 100.0
+        self.hist_collectors = None
+        if bidirectional:
+            self.hist_collectors_reverse = None
+        self.calibrating = False
+
+    # -- pickling (quant_gru.py:1277-1350): bit-width config kept, calibration dropped ----
+
+    def __getstate__(self):
+        state = self.__dict__.copy()
+        cfg = {}
+        for info in _OPERATOR_MAP.values():
+            for a in (info["bw_attr"], info["sym_attr"], info["unsigned_attr"]):
+                cfg[a] = getattr(self._bitwidth_config, a)
+        for a in ("W_granularity_", "R_granularity_", "bw_granularity_", "br_granularity_",
+                  "usePOT2_", "pot_scale_method_", "pot_scale_tolerance_"):
+            cfg[a] = getattr(self._bitwidth_config, a)
+        state["_bitwidth_config"] = cfg
+        for k in ("quant_ranges", "quant_params", "hist_collectors"):
+            state[k] = None
+            if self.bidirectional:
+                state[k + "_reverse"] = None
+        state["_quant_params_dirty"] = False
+        return state
+
+    def __setstate__(self, state):
+        cfg = state.get("_bitwidth_config")
+        obj = gru_ops.OperatorQuantConfig()
+        if isinstance(cfg, dict):
+            for a, v in cfg.items():
+                setattr(obj, a, v)
+        state["_bitwidth_config"] = obj
+        state.setdefault("_quant_params_locked", False)
+        state.setdefault("quant_storage_dtype", "float32")
+        self.__dict__.update(state)
+        self._use_pot2_scale = bool(obj.usePOT2_)
+
+    def reset_parameters(self):
+        """U(-1/sqrt(H), 1/sqrt(H)) for every parameter, as nn.GRU (quant_gru.py:1352-1356)."""
+        stdv = 1.0 / (self.hidden_size ** 0.5)
+        for p in self.parameters():
+            nn.init.uniform_(p, -stdv, stdv)
+
+    # -- configuration ---------------------------------------------------------------
+
+    def set_all_bitwidth(self, bitwidth: int = 8, is_symmetric: bool = True,
+                         verbose: bool = False):
+        """One bit width for every operator; weights/biases stay symmetric, activations
+        follow ``is_symmetric`` (quant_gru.py:1628-1658)."""
+        if not 1 <= bitwidth <= 32:
+            raise ValueError(f"bitwidth must be in range [1, 32], got {bitwidth}")
+        for a in _VALID_BITWIDTH_ATTRS:
+            setattr(self._bitwidth_config, a, bitwidth)
+        for a in _WEIGHT_SYMMETRIC_ATTRS:
+            setattr(self._bitwidth_config, a, True)
+        for a in _ACTIVATION_SYMMETRIC_ATTRS:
+            setattr(self._bitwidth_config, a, is_symmetric)
+        self._quant_params_dirty = True
+        if verbose:
+            print(f"[QuantGRU] all operators {bitwidth}-bit, activations "
+                  f"{'symmetric' if is_symmetric else 'asymmetric'}, weights symmetric")
+
+    def _get_config_attr(self, op_name: str, suffix: str, valid: set, default):
+        attr = f"{op_name}{suffix}"
+        if attr not in valid:
+            import warnings
+            warnings.warn(f"unknown config attribute '{attr}', returning {default}", UserWarning)
+            return default
+        return getattr(self._bitwidth_config, attr, default)
+
+    def _get_bitwidth(self, op_name: str) -> int:
+        return self._get_config_attr(op_name, "_", _VALID_BITWIDTH_ATTRS, 8)
+
+    def _get_symmetric(self, op_name: str) -> bool:
+        return self._get_config_attr(op_name, "_symmetric_", _VALID_SYMMETRIC_ATTRS, True)
+
+    def _get_unsigned(self, op_name: str) -> bool:
+        return self._get_config_attr(op_name, "_unsigned_", _VALID_UNSIGNED_ATTRS, False)
+
+    @property
+    def use_po2_scale(self) -> bool:
+        return bool(self._bitwidth_config.usePOT2_)
+
+    @use_po2_scale.setter
+    def use_po2_scale(self, value: bool):
+        self._use_pot2_scale = bool(value)
+        self._bitwidth_config.usePOT2_ = self._use_pot2_scale
+        if self.quant_params is not None:
+            self.quant_params.bitwidth_config_ = self._bitwidth_config
+        self._quant_params_dirty = True
+
+    use_pot2_scale = use_po2_scale
+
+    def enable_po2(self, method="cover_range", tolerance=0.02):
+        """quant_gru.py:1679-1685."""
+        if self.use_po2_scale:
+            return
+        if self._quant_params_locked:
+            raise RuntimeError("QuantGRU encodings are locked; cannot change scale mode")
+        self.use_po2_scale = True
+
+    def enable_pot2(self, method="cover_range", tolerance=0.02):
+        return self.enable_po2(method=method, tolerance=tolerance)
+
+    def set_module_name(self, module_name: str) -> None:
+        self._module_name = module_name
+
+    # -- calibration state -------------------------------------------------------------
+
+    def is_calibrated(self) -> bool:
+        if self.bidirectional:
+            return self.quant_params is not None and self.quant_params_reverse is not None
+        return self.quant_params is not None
+
+    def _use_histogram_collection(self) -> bool:
+        return self.calibration_method in ("sqnr", "percentile")
+
+    def _check_calibration_method(self):
+        if self.calibration_method not in ("minmax", "sqnr", "percentile"):
+            raise ValueError(f"unknown calibration_method {self.calibration_method!r}")
+        if self._use_histogram_collection():
+            raise NotImplementedError("histogram calibration ('sqnr', 'percentile') is not "
+                                      "provided by the MI355X build; use 'minmax'")
+
+    def _ensure_quant_params_fresh(self):
+        """Resolve a pending dirty flag before locking (quant_gru.py:4436-4472)."""
+        if not self._quant_params_dirty:
+            return
+        if self._quant_params_locked and self.quant_params is not None:
+            self._quant_params_dirty = False
+            return
+        if self.quant_ranges is None:
+            raise RuntimeError("quantisation parameters are stale and the calibration data is "
+                               "gone: recalibrate or call finalize_calibration() first")
+        self.finalize_calibration()
+
+    def set_quant_params_locked(self, locked: bool) -> None:
+        """quant_gru.py:1709-1721."""
+        if locked and not self._quant_params_locked:
+            self._ensure_quant_params_fresh()
+        self._quant_params_locked = bool(locked)
+
+    @contextmanager
+    def calibration_context(self):
+        """One PTQ pass: reset, collect, finalize, restore flags (quant_gru.py:1662-1677)."""
+        if self._quant_params_locked or self.calibrating:
+            yield
+            return
+        previous = self.calibrating
+        self.reset_calibration()
+        self.calibrating = True
+        try:
+            yield
+            if self.quant_ranges is not None:
+                self.finalize_calibration(verbose=False)
+        finally:
+            self.calibrating = previous
+
+    def finalize_calibration(self, verbose: bool = False):
+        """Ranges -> grids for each direction (quant_gru.py:1724-1800)."""
+        if self._quant_params_locked and self.is_calibrated():
+            self._quant_params_dirty = False
+            return
+        self._check_calibration_method()
+        if self.quant_ranges is None:
+            raise RuntimeError("no calibration data: set calibrating=True and call forward() first")
+        cfg = self._bitwidth_config
+        self.quant_params = gru_ops.calculate_gru_quantitative_parameters(
+            quant_ranges=self.quant_ranges, bitwidth_config=cfg)
+        if self.bidirectional:
+            if self.quant_ranges_reverse is None:
+                raise RuntimeError("bidirectional GRU: reverse-direction calibration data missing")
+            self.quant_params_reverse = gru_ops.calculate_gru_quantitative_parameters(
+                quant_ranges=self.quant_ranges_reverse, bitwidth_config=cfg)
+        self._quant_params_dirty = False
+        if verbose:
+            print(f"[QuantGRU] MINMAX grids: x scale {self.quant_params.scale('x'):.6g}, "
+                  f"h scale {self.quant_params.scale('h'):.6g}")
+
+    def reset_calibration(self):
+        """quant_gru.py:1802-1813."""
+        self.quant_ranges = None
+        self.quant_params = None
+        self.hist_collectors = None
+        self._quant_params_dirty = False
+        if self.bidirectional:
+            self.quant_ranges_reverse = None
+            self.quant_params_reverse = None
+            self.hist_collectors_reverse = None
+
+    # -- forward -------------------------------------------------------------------------
+
+    def _direction_weights(self, reverse: bool, device):
+        sfx = "_reverse" if reverse else ""
+        return convert_weights_to_haste_format(
+            getattr(self, "weight_ih_l0" + sfx), getattr(self, "weight_hh_l0" + sfx),
+            getattr(self, "bias_ih_l0" + sfx) if self.bias else None,
+            getattr(self, "bias_hh_l0" + sfx) if self.bias else None, self.hidden_size, device)
+
+    def _parse_initial_state(self, hx, batch_size: int):
+        """hx [D, B, H] -> (h0_forward, h0_reverse) (quant_gru.py:1372-1400)."""
+        if hx is None:
+            return None, None
+        expected = (self.num_layers * self.num_directions, batch_size, self.hidden_size)
+        if tuple(hx.shape) != expected:
+            raise ValueError(f"hx must have shape {expected}, got {tuple(hx.shape)}")
+        return hx[0], (hx[1] if self.bidirectional else None)
+
+    def _combine_bidirectional_outputs(self, out_f, hn_f, out_r=None, hn_r=None):
+        """quant_gru.py:1402-1432."""
+        if self.bidirectional and out_r is not None:
+            return torch.cat([out_f, out_r], dim=-1), torch.cat([hn_f, hn_r], dim=0)
+        return out_f, hn_f
+
+    def _forward_with_calibration(self, input, hx=None):
+        """Float GRU on the GPU + MinMax ranges merged per direction
+        (quant_gru.py:2054-2149)."""
+        self._check_calibration_method()
+        T, B, I = input.shape
+        H = self.hidden_size
+        device = _require_device(input)
+        input = ensure_cuda_float32(input, device).contiguous()
+        h0f, h0r = self._parse_initial_state(hx, B)
+        empty = torch.empty(0, device=device)
+        if self.quant_ranges is None:
+            self.quant_ranges = gru_ops.GRUQuantizationRanges(H, device=device)
+        W, R, bw, br = self._direction_weights(False, device)
+        with torch.no_grad():
+            h, _ = gru_ops.forward_calibrate(
+                is_training=True, time_steps=T, batch_size=B, input_size=I, hidden_size=H,
+                W=W, R=R, bw=bw, br=br, x=input,
+                h0=ensure_cuda_float32(h0f, device).contiguous() if h0f is not None else empty,
+                calib_method=self.calibration_method, bitwidth_config=self._bitwidth_config,
+                quant_ranges=self.quant_ranges)
+        out_f, hn_f = h[1:], h[-1:]
+        out_r = hn_r = None
+        if self.bidirectional:
+            if self.quant_ranges_reverse is None:
+                self.quant_ranges_reverse = gru_ops.GRUQuantizationRanges(H, device=device)
+            W, R, bw, br = self._direction_weights(True, device)
+            with torch.no_grad():
+                h_r, _ = gru_ops.forward_calibrate(
+                    is_training=True, time_steps=T, batch_size=B, input_size=I, hidden_size=H,
+                    W=W, R=R, bw=bw, br=br, x=input.flip(0).contiguous(),
+                    h0=ensure_cuda_float32(h0r, device).contiguous() if h0r is not None else empty,
+                    calib_method=self.calibration_method, bitwidth_config=self._bitwidth_config,
+                    quant_ranges=self.quant_ranges_reverse)
+            out_r, hn_r = h_r[1:].flip(0), h_r[-1:]
+        if (not self._quant_params_locked) or self.quant_params is None:
+            self._quant_params_dirty = True
+        return self._combine_bidirectional_outputs(out_f, hn_f, out_r, hn_r)
+
+    def _resolve_quant_params(self):
+        """Dirty / lock handling before a quantised forward (quant_gru.py:2218-2242)."""
+        if self._quant_params_locked and not self.is_calibrated():
+            raise RuntimeError("quant_params are locked but incomplete: calibrate or load them "
+                               "before locking, or call set_quant_params_locked(False)")
+        if self._quant_params_dirty:
+            if self._quant_params_locked and self.quant_params is not None:
+                self._quant_params_dirty = False
+            else:
+                self.finalize_calibration()
+        elif not self.is_calibrated():
+            if self.quant_ranges is not None or self.hist_collectors is not None:
+                self.finalize_calibration()
+            else:
+                raise RuntimeError(
+                    "quantisation is enabled but the module is not calibrated:\n"
+                    "  1. gru.calibrating = True\n  2. gru(calibration_data)\n"
+                    "  3. gru.calibrating = False\n"
+                    "(calibration data does not survive pickle/deepcopy)")
+
+    def _forward_cuda(self, input, hx=None):
+        """Quantised forward through GRUFunction per direction (quant_gru.py:2207-2288)."""
+        if self.use_quantization:
+            self._resolve_quant_params()
+        T, B, I = input.shape
+        device = _require_device(input)
+        input = ensure_cuda_float32(input, device)
+        h0f, h0r = self._parse_initial_state(hx, B)
+        # gate values and masks are kept whenever a backward may follow (quant_gru.py:2258-2263)
+        save_state = self.training or (torch.is_grad_enabled() and (
+            input.requires_grad or (hx is not None and hx.requires_grad)
+            or any(p.requires_grad for p in self.parameters())))
+        b = self.bias
+        out_f, hn_f = GRUFunction.apply(
+            input, self.weight_ih_l0, self.weight_hh_l0, self.bias_ih_l0 if b else None,
+            self.bias_hh_l0 if b else None, h0f, save_state, self.use_quantization,
+            self.quant_params, self.quant_storage_dtype)
+        out_r = hn_r = None
+        if self.bidirectional:
+            out_r, hn_r = GRUFunction.apply(
+                input.flip(0), self.weight_ih_l0_reverse, self.weight_hh_l0_reverse,
+                self.bias_ih_l0_reverse if b else None, self.bias_hh_l0_reverse if b else None,
+                h0r, save_state, self.use_quantization, self.quant_params_reverse,
+                self.quant_storage_dtype)
+            out_r = out_r.flip(0)
+        return self._combine_bidirectional_outputs(out_f, hn_f, out_r, hn_r)
+
+    def forward(self, input: torch.Tensor, hx: Optional[torch.Tensor] = None
+                ) -> Tuple[torch.Tensor, torch.Tensor]:
+        """input [T,B,I] or [B,T,I] (batch_first); hx [D,B,H].  Returns (output [.., D*H],
+        h_n [D,B,H]) (quant_gru.py:2151-2205)."""
+        if self.export_mode:
+            raise NotImplementedError("ONNX export mode is not provided by the MI355X build")
+        if self.batch_first:
+            input = input.transpose(0, 1).contiguous()
+        if self.calibrating:
+            output, h_n = self._forward_with_calibration(input, hx)
+        else:
+            output, h_n = self._forward_cuda(input, hx)
+        if self.batch_first:
+            output = output.transpose(0, 1).contiguous()
+        return output, h_n
+
+
+def set_quant_gru_module_names(model: nn.Module, prefix: str = "") -> None:
+    """Give every QuantGRU in ``model`` its dotted module path (quant_gru.py:4875-4893)."""
+    for name, mod in model.named_modules(prefix=prefix):
+        if isinstance(mod, QuantGRU):
+            mod.set_module_name(name)

@@ -75,6 +75,7 @@ _SIGS = {
     "rxmet_gru_backward_quant": (ctypes.c_int, [_i32, _i32, _i32, _i32] + [_p] * 8 +
                                  [ctypes.POINTER(GruQParams)] + [_p] * 11 + [_p] * 6 + [_p, _p]),
     "rxmet_gru_forward_calibrate": (ctypes.c_int, [_i32, _i32, _i32, _i32] + [_p] * 9 + [_p, _p]),
+    "rxmet_gru_forward_fp": (ctypes.c_int, [_i32] * 5 + [_p] * 8 + [_p]),
 }
 for _name, (_res, _args) in _SIGS.items():
     _rx.register(_name, _res, _args)

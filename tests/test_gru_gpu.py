@@ -64,6 +64,10 @@ def _config(name):
         c.op[A.GRID["h"]].is_unsigned = 1
         c.op[A.GRID["h"]].bits = 12
         return c
+    if name == "16b-r8":  # 16-bit x and W: the input projection needs int64 accumulation
+        c = A.set_all_bitwidth(A.default_config(), 16, False)
+        c.chan[1].bits = 8
+        return c
     raise KeyError(name)
 
 
@@ -93,7 +97,8 @@ NAMES = ("h", "v", "W_q", "R_q", "bw_q", "br_q", "x_q") + GO.MASKS
 
 @pytest.mark.parametrize("shape", [(5, 20, 7, 32), (4, 16, 80, 256), (3, 33, 40, 64),
                                    (2, 5, 3, 16), (6, 48, 9, 48)])
-@pytest.mark.parametrize("cfg_name", ["8b-sym", "8b-asym", "c3", "16b-act-pot2", "h-unsigned"])
+@pytest.mark.parametrize("cfg_name", ["8b-sym", "8b-asym", "c3", "16b-act-pot2", "h-unsigned",
+                                      "16b-r8"])
 @pytest.mark.parametrize("with_h0", [False, True])
 def test_forward_bit_exact(cuda, shape, cfg_name, with_h0):
     T, B, I, H = shape

@@ -1,0 +1,167 @@
+"""Host-side behaviour of the QuantGRU mirror (no GPU): operator map, weight-format
+helpers, configuration state, lock/dirty rules and error paths, following the reference's
+quant_gru.py and its tests (tests/recurrent/test_gru_storage.py, test_gru_autograd.py)."""
+import pickle
+
+import pytest
+import torch
+
+import quant_gru as Q
+
+
+def test_operator_map_matches_config_attributes():
+    cfg = Q.gru_ops.OperatorQuantConfig()
+    for op, info in Q._OPERATOR_MAP.items():
+        assert hasattr(cfg, info["bw_attr"]), op
+        assert hasattr(cfg, info["sym_attr"]), op
+        assert hasattr(cfg, info["unsigned_attr"]), op
+    assert len(Q._OPERATOR_MAP) == 17
+    # sigmoid outputs default to unsigned grids (quant_gru.py:244-247)
+    assert cfg.update_gate_output_unsigned_ and cfg.reset_gate_output_unsigned_
+    assert not cfg.new_gate_output_unsigned_
+
+
+def test_gate_reorder_is_an_involution_and_swaps_r_z():
+    H, I = 4, 3
+    w = torch.arange(3 * H * I, dtype=torch.float32).reshape(3 * H, I)
+    r, z, n = w.chunk(3, 0)
+    out = Q.reorder_weights_pytorch_to_haste(w)
+    assert torch.equal(out, torch.cat([z, r, n], 0))
+    assert torch.equal(Q.reorder_weights_haste_to_pytorch(out), w)
+
+
+def test_convert_weights_layout_and_missing_bias():
+    H, I = 5, 2
+    wi, wh = torch.randn(3 * H, I), torch.randn(3 * H, H)
+    W, R, bw, br = Q.convert_weights_to_haste_format(wi, wh, None, None, H, torch.device("cpu"))
+    assert W.shape == (I, 3 * H) and R.shape == (H, 3 * H)
+    assert torch.equal(W[:, :H], wi[H:2 * H].t()) and torch.equal(R[:, 2 * H:], wh[2 * H:].t())
+    assert torch.count_nonzero(bw) == 0 and torch.count_nonzero(br) == 0
+
+
+def test_get_quant_range():
+    assert Q.get_quant_range(8) == (-128, 127)
+    assert Q.get_quant_range(8, True) == (0, 255)
+    assert Q.get_quant_range(4) == (-8, 7)
+    assert Q.get_quant_range(16, True) == (0, 65535)
+    with pytest.raises(ValueError):
+        Q.get_quant_range(0)
+
+
+def test_constructor_limits():
+    with pytest.raises(NotImplementedError):
+        Q.QuantGRU(4, 8, num_layers=2)
+    with pytest.raises(NotImplementedError):
+        Q.QuantGRU(4, 8, dropout=0.1)
+    with pytest.raises(ValueError):
+        Q.QuantGRU(4, 8, quant_storage_dtype="int8")
+    with pytest.raises(ValueError):
+        Q.QuantGRU(4, 8, use_po2_scale=True, use_pot2_scale=False)
+
+
+def test_parameters_like_nn_gru():
+    m = Q.QuantGRU(6, 8, bidirectional=True)
+    ref = torch.nn.GRU(6, 8, bidirectional=True)
+    assert {n: p.shape for n, p in m.named_parameters()} == \
+        {n: p.shape for n, p in ref.named_parameters()}
+    bound = 1 / 8 ** 0.5
+    assert all(float(p.detach().abs().max()) <= bound for p in m.parameters())
+    m2 = Q.QuantGRU(6, 8, bias=False)
+    assert m2.bias_ih_l0 is None and len(list(m2.parameters())) == 2
+
+
+def test_set_all_bitwidth_keeps_weights_symmetric():
+    m = Q.QuantGRU(4, 16)
+    m.set_all_bitwidth(6, is_symmetric=False)
+    cfg = m._bitwidth_config
+    for a in Q._VALID_BITWIDTH_ATTRS:
+        assert getattr(cfg, a) == 6, a
+    for a in Q._WEIGHT_SYMMETRIC_ATTRS:
+        assert getattr(cfg, a) is True, a
+    for a in Q._ACTIVATION_SYMMETRIC_ATTRS:
+        assert getattr(cfg, a) is False, a
+    assert m._quant_params_dirty
+    with pytest.raises(ValueError):
+        m.set_all_bitwidth(33)
+    assert m._get_bitwidth("x") == 6 and m._get_symmetric("h") is False
+    with pytest.warns(UserWarning):
+        assert m._get_bitwidth("nope") == 8
+
+
+def test_po2_switch_marks_dirty_and_respects_lock():
+    m = Q.QuantGRU(4, 16, use_pot2_scale=True)
+    assert m.use_po2_scale and m._bitwidth_config.usePOT2_
+    m = Q.QuantGRU(4, 16)
+    m.enable_po2()
+    assert m.use_po2_scale and m._quant_params_dirty
+    m = Q.QuantGRU(4, 16)
+    m._quant_params_locked = True
+    with pytest.raises(RuntimeError, match="locked"):
+        m.enable_pot2()
+
+
+def test_pickle_keeps_bitwidths_drops_calibration():
+    m = Q.QuantGRU(4, 16, bidirectional=True)
+    m.set_all_bitwidth(5, False)
+    m.use_po2_scale = True
+    m.quant_ranges = object()
+    m2 = pickle.loads(pickle.dumps(m))
+    assert m2._bitwidth_config.x_ == 5 and m2._bitwidth_config.usePOT2_
+    assert m2._bitwidth_config.x_symmetric_ is False
+    assert m2.quant_ranges is None and m2.quant_params_reverse is None
+    assert not m2._quant_params_dirty
+    for (n, a), (_, b) in zip(m.named_parameters(), m2.named_parameters()):
+        assert torch.equal(a, b), n
+
+
+def test_quantised_forward_requires_calibration():
+    m = Q.QuantGRU(4, 16, use_quantization=True)
+    with pytest.raises(RuntimeError, match="not calibrated"):
+        m(torch.randn(3, 2, 4))
+
+
+def test_locked_but_uncalibrated_is_an_error():
+    m = Q.QuantGRU(4, 16, use_quantization=True)
+    m.set_quant_params_locked(True)
+    with pytest.raises(RuntimeError, match="locked"):
+        m(torch.randn(3, 2, 4))
+
+
+def test_cpu_input_is_rejected_loudly():
+    m = Q.QuantGRU(4, 16)
+    m.calibrating = True
+    with pytest.raises(RuntimeError, match="GPU"):
+        m(torch.randn(3, 2, 4))
+
+
+def test_histogram_calibration_not_provided():
+    m = Q.QuantGRU(4, 16)
+    m.calibrating = True
+    m.calibration_method = "sqnr"
+    with pytest.raises(NotImplementedError):
+        m(torch.randn(3, 2, 4))
+
+
+def test_calibration_context_restores_flag_when_nothing_collected():
+    m = Q.QuantGRU(4, 16)
+    with m.calibration_context():
+        assert m.calibrating
+    assert not m.calibrating and m.quant_params is None
+
+
+def test_finalize_without_data_raises():
+    m = Q.QuantGRU(4, 16)
+    with pytest.raises(RuntimeError, match="no calibration data"):
+        m.finalize_calibration()
+
+
+def test_hx_shape_checked():
+    m = Q.QuantGRU(4, 16, bidirectional=True)
+    with pytest.raises(ValueError):
+        m._parse_initial_state(torch.zeros(1, 2, 16), 2)
+
+
+def test_module_names():
+    net = torch.nn.Sequential(torch.nn.Linear(2, 4), Q.QuantGRU(4, 16))
+    Q.set_quant_gru_module_names(net)
+    assert net[1]._module_name == "1"
