@@ -1,15 +1,16 @@
 """Benchmark of the MI355X quantization hot path (one GPU).
 
 Prints ONE JSON line.  Legs:
-* gru  — QuantGRU bidirectional QAT forward+backward at BASELINE config c3
-         (B=256, T=200, I=80, H=256): seq/s (the headline ``value`` once built);
+* gru  — QuantGRU bidirectional QAT forward+backward at config c3
+         (B=256, T=200, I=80, H=256): seq/s, the headline ``value``;
 * qdq  — AIMET QuantizeDequantize forward+backward at config c2 ([8192, 8192] fp32,
          learnable min/max encodings, 8-bit asymmetric per-tensor and 4-bit symmetric
          per-channel): algorithmic HBM GB/s.
 
 The roofline object describes the dominant kernel of the headline leg, timed with
-events on the stream the kernel is launched on.  The CPU baseline times the CPU oracle
-on a bounded sample of the same workload.
+hipEvents that the library records around its own launches on the stream they run on
+(rxmet_prof_*), over the timed region.  The CPU baseline times the CPU oracle on a
+bounded sample of the same workload (``qdq_*`` keys: the same for the QDQ leg).
 """
 from __future__ import annotations
 
@@ -126,6 +127,133 @@ def _qdq_leg(torch, steps: int, warmup: int):
     return results, roof
 
 
+# Algorithmic work per launch of the instrumented GRU kernels (one direction, c3 shapes):
+# GEMM FLOPs 2*M*N*K as counted for the metric; the int8 MFMA / fp32 peaks are MI355X's
+# published dense figures in TFLOP/s (int8: TOP/s).
+INT8_MFMA_PEAK = 5000.0
+FP32_MFMA_PEAK = 157.3
+
+
+def _gru_kernel_work(B, T, I, H):
+    C = 3 * H
+    M = T * B
+    return {
+        "gru_fwd_recurrence": (2.0 * M * H * C, INT8_MFMA_PEAK,
+                               "recurrent GEMM R_q.h_q over T steps (int8 MFMA, 16-bit h as two "
+                               "byte planes)"),
+        "gru_bwd_recurrence": (2.0 * M * H * C, INT8_MFMA_PEAK,
+                               "dh GEMM R_q^T.dq over T steps (int8 MFMA, 3 planes of 22-bit "
+                               "block fixed point)"),
+        "gru_bwd_weight_gemms": (2.0 * M * C * (2 * I + H), FP32_MFMA_PEAK,
+                                 "dx, dW, dR fp32 GEMMs (rocBLAS)"),
+        "gru_fwd_input_gemm": (2.0 * M * C * I, FP32_MFMA_PEAK,
+                               "input projection W_q.x_q exact integer GEMM"),
+    }
+
+
+def _gru_leg(torch, steps: int, warmup: int):
+    """c3: QuantGRU bidirectional QAT fwd+bwd, B=256, T=200, I=80, H=256."""
+    import quant_gru as QG
+    import rxmet_lib
+
+    dev = torch.device("cuda:0")
+    B, T, I, H = 256, 200, 80, 256
+    torch.manual_seed(6)
+    x = torch.randn(B, T, I)
+    m = QG.QuantGRU(I, H, batch_first=True, bidirectional=True)  # U(+-1/16) like nn.GRU
+    m.set_all_bitwidth(8, is_symmetric=False)  # weights stay symmetric, per-channel
+    m._bitwidth_config.h_ = 16
+    m = m.to(dev)
+    x = x.to(dev)
+    with m.calibration_context():
+        m(x)
+    m.use_quantization = True
+    m.train()
+
+    def step():
+        m.zero_grad(set_to_none=True)
+        out, _ = m(x)
+        out.mean().backward()
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    rxmet_lib.prof_reset()
+    rxmet_lib.prof_enable(True)
+    t0 = time.perf_counter()
+    evs[0].record(stream)
+    for i in range(steps):
+        step()
+        evs[i + 1].record(stream)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    rxmet_lib.prof_enable(False)
+    per = sorted(evs[i].elapsed_time(evs[i + 1]) for i in range(steps))
+    p50 = per[len(per) // 2]
+    p95 = per[min(len(per) - 1, int(0.95 * len(per)))]
+    work = _gru_kernel_work(B, T, I, H)
+    kernels = {}
+    for name in rxmet_lib.prof_names():
+        ms, n = rxmet_lib.prof_query(name)
+        kernels[name] = {"ms_per_step": ms / steps, "launches_per_step": n / steps,
+                         "us_per_launch": ms / max(n, 1) * 1e3}
+    total = sum(k["ms_per_step"] for k in kernels.values())
+    dom = max((k for k in kernels if k in work), key=lambda k: kernels[k]["ms_per_step"])
+    flops, peak, what = work[dom]
+    t_launch = kernels[dom]["us_per_launch"] * 1e-6
+    achieved = flops / t_launch / 1e12
+    roof = {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 3), "peak": peak,
+            "unit": "TFLOP/s", "frac": round(achieved / peak, 6), "traffic": None,
+            "algorithmic_flops_per_launch": flops, "work": what,
+            "us_per_launch": round(kernels[dom]["us_per_launch"], 2)}
+    _log(f"gru c3: {dt*1e3:.2f} ms/step wall, P50 {p50:.2f} ms P95 {p95:.2f} ms, "
+         f"{B/dt:.1f} seq/s; instrumented kernels {total:.2f} ms/step")
+    for k, v in sorted(kernels.items(), key=lambda kv: -kv[1]["ms_per_step"]):
+        _log(f"  {k}: {v['ms_per_step']:.3f} ms/step, {v['us_per_launch']:.1f} us/launch")
+    res = {"ms_per_step": dt * 1e3, "p50_ms": p50, "p95_ms": p95, "seq_per_s": B / dt,
+           "seq_per_s_p50": B / (p50 * 1e-3),
+           "kernels_ms_per_step": {k: round(v["ms_per_step"], 4) for k, v in kernels.items()}}
+    return res, roof, m, x
+
+
+def _gru_cpu_baseline(m, x, rows: int = 32):
+    """CPU oracle (C, one thread) on the first `rows` sequences of c3: the same QAT
+    forward+backward of both directions with the module's own grids."""
+    import numpy as np
+
+    import gru_oracle as GO
+
+    xs = x[:rows].detach().transpose(0, 1).contiguous().cpu().numpy()  # [T, rows, I]
+    T, Bs, I = xs.shape
+    H = m.hidden_size
+    dirs = []
+    for d, qp in enumerate((m.quant_params, m.quant_params_reverse)):
+        sfx = "_reverse" if d else ""
+        p = lambda n: getattr(m, n + sfx).detach().cpu().numpy()
+
+        def swap(t):
+            r, z, n = np.split(t, 3, axis=0)
+            return np.concatenate([z, r, n], 0)
+
+        W = np.ascontiguousarray(swap(p("weight_ih_l0")).T)
+        R = np.ascontiguousarray(swap(p("weight_hh_l0")).T)
+        dirs.append((W, R, swap(p("bias_ih_l0")), swap(p("bias_hh_l0")), qp.struct,
+                     np.ascontiguousarray(xs[::-1]) if d else xs))
+    gscale = np.float32(1.0 / (x.shape[0] * T * 2 * H))
+    dh = np.zeros((T + 1, Bs, H), np.float32)
+    dh[1:] = gscale
+    t0 = time.perf_counter()
+    for W, R, bw, br, qp, xd in dirs:
+        fwd = GO.forward_quant(W, R, bw, br, xd, qp, training=True)
+        GO.backward_quant(fwd, dh, qp)
+    dt = time.perf_counter() - t0
+    return {"value": round(Bs / dt, 3), "unit": "seq/s", "cores": 1, "kind": "port",
+            "sample": f"c3 QAT fwd+bwd of both directions on {Bs} of the 256 sequences "
+                      f"(T={T}, I={I}, H={H}), C oracle, one thread, {dt:.1f} s"}
+
+
 def _qdq_cpu_baseline():
     """Oracle (numpy, one thread) on a 1024-row sample of c2, fwd+bwd, GB/s formula of c2."""
     import numpy as np
@@ -168,27 +296,38 @@ def main() -> int:
     torch.backends.cuda.matmul.allow_tf32 = False
     torch.backends.cudnn.allow_tf32 = False
     _log(f"device: {torch.cuda.get_device_name(0)}")
-    qdq, roof = _qdq_leg(torch, args.steps, args.warmup)
-    cpu = None if args.no_cpu_baseline else _qdq_cpu_baseline()
-    per_tensor = qdq["per_tensor_8b_asym"]
+    gru, roof, m, x = _gru_leg(torch, args.steps, args.warmup)
+    qdq, qdq_roof = _qdq_leg(torch, args.steps, args.warmup)
+    cpu = cpu_qdq = None
+    if not args.no_cpu_baseline:
+        cpu = _gru_cpu_baseline(m, x)
+        _log(f"cpu baseline: {cpu}")
+        cpu_qdq = _qdq_cpu_baseline()
     line = {
         "metric": METRIC,
-        "value": round(per_tensor["GB_s"], 1),
-        "unit": "GB/s",
+        "value": round(gru["seq_per_s"], 2),
+        "unit": "seq/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(per_tensor["ms_per_step"], 4),
+        "ms_per_step": round(gru["ms_per_step"], 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": "c2: QuantizeDequantize fwd+bwd, fp32 [8192, 8192], learnable "
-                               "min/max encodings, 8-bit asymmetric per-tensor"},
+        "config": {"workload": "c3: QuantGRU bidirectional QAT forward+backward, B=256, T=200, "
+                               "I=80, H=256, batch_first, 8-bit per-channel symmetric weights, "
+                               "8-bit asymmetric activations, 16-bit h, MinMax calibration, "
+                               "loss = mean(output)",
+                   "batch": 256, "seq_len": 200, "input_size": 80, "hidden_size": 256,
+                   "carrier": "fp32 codes; recurrent GEMMs on int8 MFMA"},
+        "gru": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in gru.items()},
         "qdq": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in qdq.items()},
         "roofline": roof,
+        "qdq_roofline": qdq_roof,
         "cpu_baseline": cpu,
+        "qdq_cpu_baseline": cpu_qdq,
     }
     print(json.dumps(line), flush=True)
     return 0

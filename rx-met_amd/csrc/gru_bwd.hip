@@ -22,7 +22,8 @@
 //                    fp64 and rescaled (error <= 2^-22 of the row maximum per term, below
 //                    an fp32 SGEMM's rounding);
 //   3. bias fold   : per-workgroup fp64 partials summed in a fixed order (deterministic);
-//   4. dx, dW, dR  : rocBLAS SGEMMs on the dp/dq buffers, then one mask pass.
+//   4. dx, dW, dR  : rocBLAS SGEMMs on the dp/dq buffers (dW and dR split over the long
+//                    T*B reduction and summed in a fixed order), then one mask pass.
 #include <rocblas/rocblas.h>
 
 #include <mutex>
@@ -345,8 +346,16 @@ size_t bwd_lds_bytes(int KS2) {
          static_cast<size_t>(kPlanes) * kBTile * ROW;
 }
 
+// Split-K factor of the two weight-gradient GEMMs (K = T*B is long, the outputs small).
+static int splitk_chunks(int64_t M) {
+  int64_t s = M / 1024;
+  if (s < 1) s = 1;
+  if (s > 64) s = 64;
+  return static_cast<int>(s);
+}
+
 struct BwdWorkspace {
-  size_t dp, dq, xd, wd, rfrag, rowsum, effr, effw, bias, total;
+  size_t dp, dq, xd, wd, rfrag, rowsum, effr, effw, bias, part, total;
   BwdWorkspace(int T, int B, int I, int H) {
     const size_t C = 3 * static_cast<size_t>(H);
     const size_t KS2 = (C + 63) / 64;
@@ -362,6 +371,8 @@ struct BwdWorkspace {
     effr = o; o += al(sizeof(float) * C);
     effw = o; o += al(sizeof(float) * C);
     bias = o; o += al(sizeof(double) * 2 * C * nwg);
+    const size_t S = static_cast<size_t>(splitk_chunks(static_cast<int64_t>(T) * B));
+    part = o; o += al(sizeof(float) * S * C * (static_cast<size_t>(I) > H ? I : H));
     total = o;
   }
 };
@@ -384,6 +395,45 @@ static rocblas_status gemm_rm(rocblas_handle h, bool ta, bool tb, int M, int N, 
   return rocblas_sgemm(h, tb ? rocblas_operation_transpose : rocblas_operation_none,
                        ta ? rocblas_operation_transpose : rocblas_operation_none, N, M, K, &one, Bm,
                        ldb, A, lda, &zero, Cm, ldc);
+}
+
+// Sum of S partial [rows][C] products in a fixed order.
+__global__ __launch_bounds__(256) void sum_partials(int64_t n, int S, const float *__restrict__ part,
+                                                    float *__restrict__ out) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float acc = part[i];
+  for (int s = 1; s < S; ++s) acc += part[static_cast<size_t>(s) * n + i];
+  out[i] = acc;
+}
+
+// Row-major out[Mo][N] = A[K][Mo]^T B[K][N] with K split into S chunks: one strided-
+// batched SGEMM into `part` (S x Mo x N), the K remainder added to chunk 0, then a
+// fixed-order sum.  Keeps the long-K weight-gradient GEMMs from running on a handful of
+// output tiles.
+static int gemm_tn_splitk(rocblas_handle h, int Mo, int N, int64_t K, const float *A, int lda,
+                          const float *Bm, int ldb, float *out, float *part, int S,
+                          hipStream_t stream) {
+  const int Kc = static_cast<int>(K / S);
+  const float one = 1.0f, zero = 0.0f;
+  rocblas_status st = rocblas_sgemm_strided_batched(
+      h, rocblas_operation_none, rocblas_operation_transpose, N, Mo, Kc, &one, Bm, ldb,
+      static_cast<rocblas_stride>(Kc) * ldb, A, lda, static_cast<rocblas_stride>(Kc) * lda, &zero,
+      part, N, static_cast<rocblas_stride>(Mo) * N, S);
+  RXMET_CHECK_ARG(st == rocblas_status_success, "rocBLAS strided-batched sgemm failed");
+  const int64_t rem = K - static_cast<int64_t>(Kc) * S;
+  if (rem > 0) {
+    const size_t off = static_cast<size_t>(Kc) * S;
+    st = rocblas_sgemm(h, rocblas_operation_none, rocblas_operation_transpose, N, Mo,
+                       static_cast<int>(rem), &one, Bm + off * ldb, ldb, A + off * lda, lda, &one,
+                       part, N);
+    RXMET_CHECK_ARG(st == rocblas_status_success, "rocBLAS sgemm (split-K tail) failed");
+  }
+  const int64_t n = static_cast<int64_t>(Mo) * N;
+  hipLaunchKernelGGL(sum_partials, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
+                     stream, n, S, part, out);
+  RXMET_CHECK_LAUNCH();
+  return 0;
 }
 
 }  // namespace gru
@@ -439,6 +489,7 @@ int rxmet_gru_backward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const f
   float *effr = reinterpret_cast<float *>(wsb + ws.effr);
   float *effw = reinterpret_cast<float *>(wsb + ws.effw);
   double *bias = reinterpret_cast<double *>(wsb + ws.bias);
+  float *part = reinterpret_cast<float *>(wsb + ws.part);
 
   std::vector<float> host(8 * static_cast<size_t>(C));
   try {
@@ -458,8 +509,11 @@ int rxmet_gru_backward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const f
   const int64_t nx = static_cast<int64_t>(T) * B * I, nw = static_cast<int64_t>(I) * C;
   int64_t blocks = (nx + nw + 255) / 256;
   if (blocks > 8192) blocks = 8192;
-  hipLaunchKernelGGL(dequant_inputs, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, nx,
-                     nw, C, x_q, eff_x, zp_x, W_q, effw, xd, wd);
+  {
+    rxmet::prof::Scope ps__("gru_bwd_dequant_inputs", stream);
+    hipLaunchKernelGGL(dequant_inputs, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, nx,
+                       nw, C, x_q, eff_x, zp_x, W_q, effw, xd, wd);
+  }
   RXMET_CHECK_LAUNCH();
   hipLaunchKernelGGL(pack_rt_frags, dim3((H / 16) * KS2), dim3(64), 0, stream, H, KS2, R_q, rfrag,
                      rowsum);
@@ -477,7 +531,10 @@ int rxmet_gru_backward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const f
   RXMET_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&bwd_recurrence),
                                       hipFuncAttributeMaxDynamicSharedMemorySize,
                                       static_cast<int>(lds)));
-  hipLaunchKernelGGL(bwd_recurrence, dim3(nwg), dim3(64 * ((H + 31) / 32)), lds, stream, ba);
+  {
+    rxmet::prof::Scope ps__("gru_bwd_recurrence", stream);
+    hipLaunchKernelGGL(bwd_recurrence, dim3(nwg), dim3(64 * ((H + 31) / 32)), lds, stream, ba);
+  }
   RXMET_CHECK_LAUNCH();
   hipLaunchKernelGGL(fold_bias, dim3((C + 255) / 256), dim3(256), 0, stream, nwg, C, bias, dbw, dbr);
   RXMET_CHECK_LAUNCH();
@@ -488,20 +545,24 @@ int rxmet_gru_backward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const f
   RXMET_CHECK_ARG(bh != nullptr, "rocBLAS handle creation failed");
   rocblas_set_stream(bh, stream);
   const int M = T * B;
-  // dx[M][I] = dp[M][C] * W_deq^T
-  RXMET_CHECK_ARG(gemm_rm(bh, false, true, M, I, C, dp, C, wd, C, dx, I) == rocblas_status_success,
-                  "rocBLAS sgemm (dx) failed");
-  // dW[I][C] = x_deq^T * dp
-  RXMET_CHECK_ARG(gemm_rm(bh, true, false, I, C, M, xd, I, dp, C, dW, C) == rocblas_status_success,
-                  "rocBLAS sgemm (dW) failed");
-  // dR[H][C] = h_prev^T * dq   (h rows 0..T-1)
-  RXMET_CHECK_ARG(gemm_rm(bh, true, false, H, C, M, h, H, dq, C, dR, C) == rocblas_status_success,
-                  "rocBLAS sgemm (dR) failed");
+  {
+    rxmet::prof::Scope ps__("gru_bwd_weight_gemms", stream);
+    // dx[M][I] = dp[M][C] * W_deq^T
+    RXMET_CHECK_ARG(gemm_rm(bh, false, true, M, I, C, dp, C, wd, C, dx, I) == rocblas_status_success,
+                    "rocBLAS sgemm (dx) failed");
+    // dW[I][C] = x_deq^T * dp and dR[H][C] = h_prev^T * dq (h rows 0..T-1), split over K
+    const int S = splitk_chunks(M);
+    if (int rc = gemm_tn_splitk(bh, I, C, M, xd, I, dp, C, dW, part, S, stream)) return rc;
+    if (int rc = gemm_tn_splitk(bh, H, C, M, h, H, dq, C, dR, part, S, stream)) return rc;
+  }
   const int64_t n0 = nx, n1 = nw, n2 = static_cast<int64_t>(H) * C;
   blocks = (n0 + n1 + n2 + 255) / 256;
   if (blocks > 8192) blocks = 8192;
-  hipLaunchKernelGGL(apply_masks, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, n0, n1,
-                     n2, dx, x_mask, dW, W_mask, dR, R_mask);
+  {
+    rxmet::prof::Scope ps__("gru_bwd_apply_masks", stream);
+    hipLaunchKernelGGL(apply_masks, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, n0, n1,
+                       n2, dx, x_mask, dW, W_mask, dR, R_mask);
+  }
   RXMET_CHECK_LAUNCH();
   return 0;
 }

@@ -215,8 +215,11 @@ int rxmet_gru_forward_calibrate(int32_t T, int32_t B, int32_t I, int32_t H, cons
     RXMET_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&calib_forward<true>),
                                         hipFuncAttributeMaxDynamicSharedMemorySize,
                                         static_cast<int>(lds)));
-  hipLaunchKernelGGL(calib_forward<true>, dim3(B), dim3(kCalThreads), lds, stream, T, B, I, H, W, R, bw,
-                     br, x, h0, h, v, ord);
+  {
+    rxmet::prof::Scope ps__("gru_calibrate_forward", stream);
+    hipLaunchKernelGGL(calib_forward<true>, dim3(B), dim3(kCalThreads), lds, stream, T, B, I, H, W, R, bw,
+                       br, x, h0, h, v, ord);
+  }
   RXMET_CHECK_LAUNCH();
   hipLaunchKernelGGL(stats_merge, dim3(1), dim3(64), 0, stream, ord, stats);
   RXMET_CHECK_LAUNCH();

@@ -532,24 +532,33 @@ int rxmet_gru_forward_quant(int32_t is_training, int32_t T, int32_t B, int32_t I
   wa.bwm = training ? bw_mask : nullptr;
   wa.brm = training ? br_mask : nullptr;
   wa.chan = chan;
-  hipLaunchKernelGGL(quant_weights, dim3((C + 255) / 256), dim3(256), 0, stream, I, H, wa);
+  {
+    rxmet::prof::Scope ps__("gru_fwd_quant_weights", stream);
+    hipLaunchKernelGGL(quant_weights, dim3((C + 255) / 256), dim3(256), 0, stream, I, H, wa);
+  }
   RXMET_CHECK_LAUNCH();
 
   const int64_t nx = static_cast<int64_t>(T) * B * I, nh = static_cast<int64_t>(B) * H;
   int64_t blocks = (nx + nh + 255) / 256;
   if (blocks > 8192) blocks = 8192;
-  hipLaunchKernelGGL(quant_input, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, nx, nh,
-                     x, h0, sp.eff_x, sp.zp_x, sp.x, sp.eff_h, sp.zp_h, sp.h, x_q,
-                     training ? x_mask : nullptr, h0codes, training ? h0_mask : nullptr, h);
+  {
+    rxmet::prof::Scope ps__("gru_fwd_quant_input", stream);
+    hipLaunchKernelGGL(quant_input, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, nx,
+                       nh, x, h0, sp.eff_x, sp.zp_x, sp.x, sp.eff_h, sp.zp_h, sp.h, x_q,
+                       training ? x_mask : nullptr, h0codes, training ? h0_mask : nullptr, h);
+  }
   RXMET_CHECK_LAUNCH();
 
   const int M = T * B;
-  if (wide_gemm)
-    hipLaunchKernelGGL(code_gemm<long long>, dim3((C + 63) / 64, (M + 63) / 64), dim3(256), 0,
-                       stream, M, C, I, x_q, W_q, gih);
-  else
-    hipLaunchKernelGGL(code_gemm<int>, dim3((C + 63) / 64, (M + 63) / 64), dim3(256), 0, stream,
-                       M, C, I, x_q, W_q, gih);
+  {
+    rxmet::prof::Scope ps__("gru_fwd_input_gemm", stream);
+    if (wide_gemm)
+      hipLaunchKernelGGL(code_gemm<long long>, dim3((C + 63) / 64, (M + 63) / 64), dim3(256), 0,
+                         stream, M, C, I, x_q, W_q, gih);
+    else
+      hipLaunchKernelGGL(code_gemm<int>, dim3((C + 63) / 64, (M + 63) / 64), dim3(256), 0, stream,
+                         M, C, I, x_q, W_q, gih);
+  }
   RXMET_CHECK_LAUNCH();
 
   RecArgs ra;
@@ -572,12 +581,18 @@ int rxmet_gru_forward_quant(int32_t is_training, int32_t T, int32_t B, int32_t I
     RXMET_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&recurrence<1>),
                                         hipFuncAttributeMaxDynamicSharedMemorySize,
                                         static_cast<int>(lds)));
-    hipLaunchKernelGGL(recurrence<1>, grid, block, lds, stream, ra, sp);
+    {
+      rxmet::prof::Scope ps__("gru_fwd_recurrence", stream);
+      hipLaunchKernelGGL(recurrence<1>, grid, block, lds, stream, ra, sp);
+    }
   } else {
     RXMET_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&recurrence<2>),
                                         hipFuncAttributeMaxDynamicSharedMemorySize,
                                         static_cast<int>(lds)));
-    hipLaunchKernelGGL(recurrence<2>, grid, block, lds, stream, ra, sp);
+    {
+      rxmet::prof::Scope ps__("gru_fwd_recurrence", stream);
+      hipLaunchKernelGGL(recurrence<2>, grid, block, lds, stream, ra, sp);
+    }
   }
   RXMET_CHECK_LAUNCH();
   return 0;

@@ -445,6 +445,7 @@ static int launch_forward(const float *x, float *y, int64_t outer, int64_t C, in
   const Plan p = make_plan(outer, C, inner);
   const int64_t n = p.outer * p.C * p.inner;
   if (n == 0) return 0;
+  rxmet::prof::Scope ps__("qdq_forward_stream", stream);
   if (!p.cols) {
     const int vec4 = (p.inner % 4 == 0) && aligned16(x) && aligned16(y);
     hipLaunchKernelGGL(fwd_runs<OP>, dim3(static_cast<unsigned>(p.runs * p.splits)),
@@ -465,18 +466,22 @@ static int launch_backward_impl(const Plan &p, const float *x, const float *g, f
                                 float *dscale, float *doffset, const float *scale,
                                 const float *offset, float qmin, float qmax, double2 *ws,
                                 hipStream_t stream) {
-  if (!p.cols) {
-    const int vec4 = (p.inner % 4 == 0) && aligned16(x) && aligned16(g) && aligned16(dx);
-    hipLaunchKernelGGL((bwd_runs<OP, ENC>), dim3(static_cast<unsigned>(p.runs * p.splits)),
-                       dim3(kThreads), 0, stream, x, g, dx, p.inner, p.C, p.splits, scale,
-                       offset, qmin, qmax, vec4, ws);
-  } else {
-    hipLaunchKernelGGL((bwd_cols<OP, ENC>), dim3(static_cast<unsigned>(p.col_tiles * p.chunks)),
-                       dim3(kThreads), 0, stream, x, g, dx, p.M, p.K, p.inner, p.col_tiles,
-                       p.rows_per_chunk, scale, offset, qmin, qmax, ws);
+  {
+    rxmet::prof::Scope ps__("qdq_backward_stream", stream);
+    if (!p.cols) {
+      const int vec4 = (p.inner % 4 == 0) && aligned16(x) && aligned16(g) && aligned16(dx);
+      hipLaunchKernelGGL((bwd_runs<OP, ENC>), dim3(static_cast<unsigned>(p.runs * p.splits)),
+                         dim3(kThreads), 0, stream, x, g, dx, p.inner, p.C, p.splits, scale,
+                         offset, qmin, qmax, vec4, ws);
+    } else {
+      hipLaunchKernelGGL((bwd_cols<OP, ENC>), dim3(static_cast<unsigned>(p.col_tiles * p.chunks)),
+                         dim3(kThreads), 0, stream, x, g, dx, p.M, p.K, p.inner, p.col_tiles,
+                         p.rows_per_chunk, scale, offset, qmin, qmax, ws);
+    }
   }
   RXMET_CHECK_LAUNCH();
   if constexpr (ENC) {
+    rxmet::prof::Scope ps__("qdq_backward_fold", stream);
     hipLaunchKernelGGL(fold_sum, dim3(static_cast<unsigned>(p.C)), dim3(kWave), 0, stream, ws,
                        p.fold, dscale, doffset);
     RXMET_CHECK_LAUNCH();
@@ -539,6 +544,7 @@ int rxmet_qdq_minmax(const float *x, int64_t outer, int64_t C, int64_t inner, fl
   RXMET_CHECK_ARG(workspace != nullptr, "min/max needs a workspace");
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   float2 *ws = static_cast<float2 *>(workspace);
+  rxmet::prof::Scope ps__("qdq_minmax", stream);
   if (!p.cols) {
     const int vec4 = (p.inner % 4 == 0) && aligned16(x);
     hipLaunchKernelGGL(minmax_runs, dim3(static_cast<unsigned>(p.runs * p.splits)), dim3(kThreads),

@@ -20,6 +20,24 @@ struct Status {
   int code = 0;
 };
 
+namespace prof {
+// Brackets the launches made during its lifetime with a pair of hipEvents on `stream`
+// when event timing is enabled (rxmet_prof_enable); `name` must be a string literal.
+bool enabled();
+class Scope {
+ public:
+  Scope(const char *name, hipStream_t stream);
+  ~Scope();
+  Scope(const Scope &) = delete;
+  Scope &operator=(const Scope &) = delete;
+
+ private:
+  const char *name_;
+  hipStream_t stream_;
+  hipEvent_t start_ = nullptr;
+};
+}  // namespace prof
+
 }  // namespace rxmet
 
 #define RXMET_CHECK_ARG(cond, msg)          \

@@ -40,6 +40,11 @@ _SIGNATURES = {
     "rxmet_dequantize_backward": (c_int, [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64,
                                           c_ptr, c_ptr, c_ptr, c_ptr]),
     "rxmet_selftest_mfma": (c_int, [c_int, c_ptr, c_ptr, c_ptr, c_ptr]),
+    "rxmet_prof_enable": (c_int, [ctypes.c_int32]),
+    "rxmet_prof_reset": (c_int, []),
+    "rxmet_prof_query": (c_int, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double),
+                                 ctypes.POINTER(c_i64)]),
+    "rxmet_prof_names": (c_i64, [ctypes.c_char_p, c_i64]),
 }
 
 
@@ -103,3 +108,28 @@ def stream_of(device) -> int:
     import torch
 
     return torch.cuda.current_stream(device).cuda_stream
+
+
+def prof_enable(on: bool = True) -> None:
+    """Turn the library's per-launch event timing on or off (include/rxmet_prof.h)."""
+    load().rxmet_prof_enable(1 if on else 0)
+
+
+def prof_reset() -> None:
+    load().rxmet_prof_reset()
+
+
+def prof_query(name: str) -> tuple:
+    """(total milliseconds, launches) recorded for an instrumented kernel name."""
+    ms = ctypes.c_double(0.0)
+    n = ctypes.c_int64(0)
+    load().rxmet_prof_query(name.encode(), ctypes.byref(ms), ctypes.byref(n))
+    return ms.value, n.value
+
+
+def prof_names() -> list:
+    lib = load()
+    need = lib.rxmet_prof_names(None, 0)
+    buf = ctypes.create_string_buffer(int(need) + 1)
+    lib.rxmet_prof_names(buf, need + 1)
+    return [n for n in buf.value.decode().split(",") if n]
