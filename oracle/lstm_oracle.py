@@ -1,0 +1,264 @@
+"""ctypes wrapper of the QuantLSTM CPU oracle (liblstm_oracle.so) and of the reference
+checker (_ref/liblstm_ref.so, the reference's own CPU code).  TEST INFRASTRUCTURE: imported
+only by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg."""
+from __future__ import annotations
+
+import ctypes
+import subprocess
+import sys
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+sys.path.insert(0, str(HERE.parent / "rx-met_amd"))
+import rxmet_lstm_abi as L  # noqa: E402  (struct layouts of include/rxmet_lstm.h)
+
+f32 = np.float32
+_P = ctypes.c_void_p
+_i = ctypes.c_int
+ACT_LIBM, ACT_CR = 0, 1
+
+
+def _lib(path: Path):
+    if not path.exists():
+        subprocess.run(["make", "-C", str(HERE), "all"], check=True, stdout=subprocess.DEVNULL)
+    return ctypes.CDLL(str(path))
+
+
+_o = _lib(HERE / "liblstm_oracle.so")
+_PP = ctypes.POINTER(L.Params)
+_o.olstm_stats_size.restype = ctypes.c_int64
+_o.olstm_finalize_params.argtypes = [_P, ctypes.POINTER(L.Config), _i, _i, _PP]
+_o.olstm_derive_exec.argtypes = [_PP, _i, _P, _P, _P, _P, _P]
+_o.olstm_real_activation.argtypes = [ctypes.c_float, ctypes.c_float, ctypes.c_int32,
+                                     ctypes.c_float, ctypes.c_int32, ctypes.POINTER(L.OpConfig),
+                                     _i, _i, _P, _P]
+_o.olstm_forward_quant.argtypes = [_i] * 4 + [_P] * 7 + [_PP, _i] + [_P] * 3 + \
+    [ctypes.POINTER(L.Saved)] + [_P] * 3
+_o.olstm_forward_float.argtypes = [_i] * 4 + [_P] * 7 + [_i] + [_P] * 4
+_o.olstm_backward_quant.argtypes = [_i] * 4 + [_PP, ctypes.POINTER(L.Saved)] + [_P] * 3 + [_P] * 7
+
+_o.olstm_prim_rne.restype = ctypes.c_double
+_o.olstm_prim_rne.argtypes = [ctypes.c_double]
+_o.olstm_prim_range.argtypes = [ctypes.POINTER(L.OpConfig), _P, _P]
+_o.olstm_prim_quantize.restype = ctypes.c_float
+_o.olstm_prim_quantize.argtypes = [ctypes.c_float, ctypes.c_float, ctypes.c_int32,
+                                   ctypes.POINTER(L.OpConfig)]
+_o.olstm_prim_dequantize.restype = ctypes.c_float
+_o.olstm_prim_dequantize.argtypes = [ctypes.c_float, ctypes.c_float, ctypes.c_int32]
+_o.olstm_prim_mshift.argtypes = [ctypes.c_double, ctypes.POINTER(L.Rescale)]
+_o.olstm_prim_apply.restype = ctypes.c_float
+_o.olstm_prim_apply.argtypes = [ctypes.c_float, ctypes.POINTER(L.Rescale)]
+_o.olstm_prim_calibrate.argtypes = [ctypes.c_float, ctypes.c_float, ctypes.POINTER(L.OpConfig),
+                                    _i, _i, _P, _P]
+prim = _o  # primitive entry points: olstm_prim_*
+
+_REF_PATH = HERE / "_ref" / "liblstm_ref.so"
+_ref = ctypes.CDLL(str(_REF_PATH)) if _REF_PATH.exists() else None
+if _ref is not None:
+    _ref.ref_lstm_error.restype = ctypes.c_char_p
+    _ref.ref_lstm_finalize.argtypes = [_P, ctypes.POINTER(L.Config), _i, _i, _PP]
+    _ref.ref_lstm_exec.argtypes = [_PP, _i, _P, _P, _P, _P, _P]
+    _ref.ref_lstm_forward_fp.argtypes = [_i] * 4 + [_P] * 7 + [_PP] + [_P] * 9
+    _ref.ref_lstm_forward_float.argtypes = [_i] * 4 + [_P] * 10
+    _ref.ref_lstm_calibrate.argtypes = [_i] * 4 + [_P] * 8
+    _ref.ref_lstm_backward_float.argtypes = [_i] * 4 + [_P] * 19
+
+
+def has_ref() -> bool:
+    return _ref is not None
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _c(a, dt=f32):
+    return None if a is None else np.ascontiguousarray(a, dtype=dt)
+
+
+def _check(rc, what, ref=False):
+    if rc != 0:
+        msg = _ref.ref_lstm_error().decode() if ref else ""
+        raise RuntimeError(f"{what} failed ({rc}) {msg}")
+
+
+def finalize(stats, cfg, hidden, bias=True, ref=False):
+    p = L.new_params(hidden)
+    s = _c(stats)
+    fn = _ref.ref_lstm_finalize if ref else _o.olstm_finalize_params
+    _check(fn(_p(s), ctypes.byref(cfg), hidden, int(bias), ctypes.byref(p)), "finalize", ref)
+    if not ref:
+        p.config = cfg
+    return p
+
+
+def derive_exec(params, input_size, ref=False):
+    C = 4 * params.hidden
+    acc = (L.Rescale * (2 * C))()
+    bias = (L.Rescale * (2 * C))()
+    gate = (L.Rescale * 8)()
+    cell = (L.Q31 * 2)()
+    hid = (L.Rescale * 1)()
+    fn = _ref.ref_lstm_exec if ref else _o.olstm_derive_exec
+    _check(fn(ctypes.byref(params), input_size, acc, bias, gate, cell, hid), "derive_exec", ref)
+
+    def rs(arr):
+        return [(r.is_mshift, r.multiplier, r.shift) for r in arr]
+
+    return {"acc_to_linear": rs(acc), "bias_to_acc": rs(bias) if params.bias_enabled else None,
+            "linear_to_gate": rs(gate),
+            "cell": [(q.multiplier, q.mantissa, q.exponent, q.uses_fp) for q in cell],
+            "hidden": rs(hid)}
+
+
+def real_activation(q, s_in, zp_in, s_out, zp_out, out_cfg, is_tanh, mode=ACT_LIBM):
+    out = np.zeros(1, f32)
+    m = np.zeros(1, np.uint8)
+    _o.olstm_real_activation(float(q), float(s_in), int(zp_in), float(s_out), int(zp_out),
+                             ctypes.byref(out_cfg), int(is_tanh), int(mode), _p(out), _p(m))
+    return float(out[0]), bool(m[0])
+
+
+SAVED_SHAPES = None
+
+
+def _saved_arrays(T, B, I, H, bias):
+    C = 4 * H
+    sh = {"x_q": (T, B, I), "w_ih_q": (C, I), "w_hh_q": (C, H), "b_ih_q": (C,), "b_hh_q": (C,),
+          "h0_q": (B, H), "c0_q": (B, H), "gate_out": (T, B, C), "cell": (T, B, H),
+          "cell_tanh": (T, B, H), "hidden": (T, B, H)}
+    msh = {"x_m": (T, B, I), "w_ih_m": (C, I), "w_hh_m": (C, H), "b_ih_m": (C,), "b_hh_m": (C,),
+           "h0_m": (B, H), "c0_m": (B, H), "ih_linear_m": (T, B, C), "hh_linear_m": (T, B, C),
+           "gate_in_m": (T, B, C), "gate_out_m": (T, B, C), "cell_m": (T, B, H),
+           "cell_tanh_m": (T, B, H), "hidden_m": (T, B, H)}
+    arrs = {k: np.zeros(v, f32) for k, v in sh.items()}
+    arrs.update({k: np.zeros(v, np.uint8) for k, v in msh.items()})
+    if not bias:
+        for k in ("b_ih_q", "b_hh_q", "b_ih_m", "b_hh_m"):
+            arrs[k] = None
+    return arrs
+
+
+def saved_struct(arrs):
+    s = L.Saved()
+    for k in L.SAVED_FIELDS:
+        a = arrs.get(k)
+        setattr(s, k, None if a is None else a.ctypes.data)
+    return s
+
+
+def forward_quant(W_ih, W_hh, b_ih, b_hh, x, params, h0=None, c0=None, mode=ACT_CR, traces=False):
+    """Returns dict: output, h_n, c_n (dequantised) + saved masters/checkpoints/masks
+    (+ ih_linear, hh_linear, gate_in code traces when traces=True)."""
+    T, B, I = x.shape
+    H = W_hh.shape[1]
+    C = 4 * H
+    W_ih, W_hh, b_ih, b_hh, x, h0, c0 = (_c(a) for a in (W_ih, W_hh, b_ih, b_hh, x, h0, c0))
+    bias = b_ih is not None
+    arrs = _saved_arrays(T, B, I, H, bias)
+    out = {"output": np.zeros((T, B, H), f32), "h_n": np.zeros((B, H), f32),
+           "c_n": np.zeros((B, H), f32)}
+    tr = {k: np.zeros((T, B, C), f32) for k in ("ih_linear", "hh_linear", "gate_in")} if traces else {}
+    sv = saved_struct(arrs)
+    rc = _o.olstm_forward_quant(T, B, I, H, _p(W_ih), _p(W_hh), _p(b_ih), _p(b_hh), _p(x),
+                                _p(h0), _p(c0), ctypes.byref(params), int(mode),
+                                _p(out["output"]), _p(out["h_n"]), _p(out["c_n"]),
+                                ctypes.byref(sv), _p(tr.get("ih_linear")),
+                                _p(tr.get("hh_linear")), _p(tr.get("gate_in")))
+    _check(rc, "forward_quant")
+    out.update(arrs)
+    out.update(tr)
+    return out
+
+
+def ref_forward_fp(W_ih, W_hh, b_ih, b_hh, x, params, h0=None, c0=None):
+    """Reference CPU q-carrier forward (codes): output, h_n, c_n codes and traces."""
+    T, B, I = x.shape
+    H = W_hh.shape[1]
+    C = 4 * H
+    W_ih, W_hh, b_ih, b_hh, x, h0, c0 = (_c(a) for a in (W_ih, W_hh, b_ih, b_hh, x, h0, c0))
+    o = {"output": np.zeros((T, B, H), f32), "h_n": np.zeros((B, H), f32),
+         "c_n": np.zeros((B, H), f32), "ih_linear": np.zeros((T, B, C), f32),
+         "hh_linear": np.zeros((T, B, C), f32), "gate_in": np.zeros((T, B, C), f32),
+         "gate_out": np.zeros((T, B, C), f32), "cell": np.zeros((T, B, H), f32),
+         "cell_tanh": np.zeros((T, B, H), f32)}
+    rc = _ref.ref_lstm_forward_fp(T, B, I, H, _p(W_ih), _p(W_hh), _p(b_ih), _p(b_hh), _p(x),
+                                  _p(h0), _p(c0), ctypes.byref(params),
+                                  *(_p(o[k]) for k in ("output", "h_n", "c_n", "ih_linear",
+                                                       "hh_linear", "gate_in", "gate_out", "cell",
+                                                       "cell_tanh")))
+    _check(rc, "ref forward_fp", True)
+    return o
+
+
+def forward_float(W_ih, W_hh, b_ih, b_hh, x, h0=None, c0=None, mode=ACT_LIBM, stats=None,
+                  ref=False):
+    T, B, I = x.shape
+    H = W_hh.shape[1]
+    W_ih, W_hh, b_ih, b_hh, x, h0, c0 = (_c(a) for a in (W_ih, W_hh, b_ih, b_hh, x, h0, c0))
+    out = np.zeros((T, B, H), f32)
+    hn = np.zeros((B, H), f32)
+    cn = np.zeros((B, H), f32)
+    if ref:
+        _check(_ref.ref_lstm_forward_float(T, B, I, H, _p(W_ih), _p(W_hh), _p(b_ih), _p(b_hh),
+                                           _p(x), _p(h0), _p(c0), _p(out), _p(hn), _p(cn)),
+               "ref forward_float", True)
+        return out, hn, cn
+    _check(_o.olstm_forward_float(T, B, I, H, _p(W_ih), _p(W_hh), _p(b_ih), _p(b_hh), _p(x),
+                                  _p(h0), _p(c0), int(mode), _p(out), _p(hn), _p(cn),
+                                  _p(stats)), "forward_float")
+    return out, hn, cn
+
+
+def calibrate(W_ih, W_hh, b_ih, b_hh, x, h0=None, c0=None, stats=None, mode=ACT_LIBM, ref=False):
+    """One calibration batch merged into `stats` (rxmet layout); returns stats."""
+    H = W_hh.shape[1]
+    s = L.empty_stats(H) if stats is None else stats
+    if ref:
+        T, B, I = x.shape
+        args = (_c(a) for a in (W_ih, W_hh, b_ih, b_hh, x, h0, c0))
+        a = list(args)
+        _check(_ref.ref_lstm_calibrate(T, B, I, H, *(_p(v) for v in a), _p(s)), "ref calibrate",
+               True)
+        return s
+    forward_float(W_ih, W_hh, b_ih, b_hh, x, h0, c0, mode=mode, stats=s)
+    return s
+
+
+def backward_quant(fwd, params, grad_output, grad_h_n=None, grad_c_n=None):
+    T, B, I = fwd["x_q"].shape
+    H = fwd["h0_q"].shape[1]
+    C = 4 * H
+    sv = saved_struct(fwd)
+    g = {"dx": np.zeros((T, B, I), f32), "dW_ih": np.zeros((C, I), f32),
+         "dW_hh": np.zeros((C, H), f32), "db_ih": np.zeros(C, f32), "db_hh": np.zeros(C, f32),
+         "dh0": np.zeros((B, H), f32), "dc0": np.zeros((B, H), f32)}
+    bias = fwd.get("b_ih_q") is not None
+    go, gh, gc = _c(grad_output), _c(grad_h_n), _c(grad_c_n)
+    _check(_o.olstm_backward_quant(T, B, I, H, ctypes.byref(params), ctypes.byref(sv), _p(go),
+                                   _p(gh), _p(gc), _p(g["dx"]), _p(g["dW_ih"]), _p(g["dW_hh"]),
+                                   _p(g["db_ih"]) if bias else None,
+                                   _p(g["db_hh"]) if bias else None, _p(g["dh0"]), _p(g["dc0"])),
+           "backward_quant")
+    if not bias:
+        g["db_ih"] = g["db_hh"] = None
+    return g
+
+
+def ref_backward_float(W_ih, W_hh, x, h0, c0, gate_out, cell, cell_tanh, hidden, grad_out,
+                       grad_hn, grad_cn):
+    T, B, I = x.shape
+    H = W_hh.shape[1]
+    C = 4 * H
+    a = [_c(v) for v in (W_ih, W_hh, x, h0, c0, gate_out, cell, cell_tanh, hidden, grad_out,
+                         grad_hn, grad_cn)]
+    g = {"dx": np.zeros((T, B, I), f32), "dW_ih": np.zeros((C, I), f32),
+         "dW_hh": np.zeros((C, H), f32), "db_ih": np.zeros(C, f32), "db_hh": np.zeros(C, f32),
+         "dh0": np.zeros((B, H), f32), "dc0": np.zeros((B, H), f32)}
+    _check(_ref.ref_lstm_backward_float(T, B, I, H, *(_p(v) for v in a),
+                                        *(_p(g[k]) for k in ("dx", "dW_ih", "dW_hh", "db_ih",
+                                                             "db_hh", "dh0", "dc0"))),
+           "ref backward_float", True)
+    return g
