@@ -24,11 +24,9 @@
 //   3. bias fold   : per-workgroup fp64 partials summed in a fixed order (deterministic);
 //   4. dx, dW, dR  : rocBLAS SGEMMs on the dp/dq buffers (dW and dR split over the long
 //                    T*B reduction and summed in a fixed order), then one mask pass.
-#include <rocblas/rocblas.h>
-
-#include <mutex>
 #include <vector>
 
+#include "blas_util.h"
 #include "gru_internal.h"
 #include "mfma_frag.h"
 #include "rxmet_common.h"
@@ -346,14 +344,6 @@ size_t bwd_lds_bytes(int KS2) {
          static_cast<size_t>(kPlanes) * kBTile * ROW;
 }
 
-// Split-K factor of the two weight-gradient GEMMs (K = T*B is long, the outputs small).
-static int splitk_chunks(int64_t M) {
-  int64_t s = M / 1024;
-  if (s < 1) s = 1;
-  if (s > 64) s = 64;
-  return static_cast<int>(s);
-}
-
 struct BwdWorkspace {
   size_t dp, dq, xd, wd, rfrag, rowsum, effr, effw, bias, part, total;
   BwdWorkspace(int T, int B, int I, int H) {
@@ -371,76 +361,18 @@ struct BwdWorkspace {
     effr = o; o += al(sizeof(float) * C);
     effw = o; o += al(sizeof(float) * C);
     bias = o; o += al(sizeof(double) * 2 * C * nwg);
-    const size_t S = static_cast<size_t>(splitk_chunks(static_cast<int64_t>(T) * B));
+    const size_t S = static_cast<size_t>(blas::splitk_chunks(static_cast<int64_t>(T) * B));
     part = o; o += al(sizeof(float) * S * C * (static_cast<size_t>(I) > H ? I : H));
     total = o;
   }
 };
-
-// rocBLAS handle per device, created once.
-static rocblas_handle blas_handle(int device) {
-  static std::mutex mu;
-  static std::vector<rocblas_handle> handles;
-  std::lock_guard<std::mutex> g(mu);
-  if (static_cast<int>(handles.size()) <= device) handles.resize(device + 1, nullptr);
-  if (!handles[device]) rocblas_create_handle(&handles[device]);
-  return handles[device];
-}
-
-// Row-major C[M][N] = op(A) op(B) with rocBLAS (column-major) arguments swapped.
-static rocblas_status gemm_rm(rocblas_handle h, bool ta, bool tb, int M, int N, int K,
-                              const float *A, int lda, const float *Bm, int ldb, float *Cm,
-                              int ldc) {
-  const float one = 1.0f, zero = 0.0f;
-  return rocblas_sgemm(h, tb ? rocblas_operation_transpose : rocblas_operation_none,
-                       ta ? rocblas_operation_transpose : rocblas_operation_none, N, M, K, &one, Bm,
-                       ldb, A, lda, &zero, Cm, ldc);
-}
-
-// Sum of S partial [rows][C] products in a fixed order.
-__global__ __launch_bounds__(256) void sum_partials(int64_t n, int S, const float *__restrict__ part,
-                                                    float *__restrict__ out) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= n) return;
-  float acc = part[i];
-  for (int s = 1; s < S; ++s) acc += part[static_cast<size_t>(s) * n + i];
-  out[i] = acc;
-}
-
-// Row-major out[Mo][N] = A[K][Mo]^T B[K][N] with K split into S chunks: one strided-
-// batched SGEMM into `part` (S x Mo x N), the K remainder added to chunk 0, then a
-// fixed-order sum.  Keeps the long-K weight-gradient GEMMs from running on a handful of
-// output tiles.
-static int gemm_tn_splitk(rocblas_handle h, int Mo, int N, int64_t K, const float *A, int lda,
-                          const float *Bm, int ldb, float *out, float *part, int S,
-                          hipStream_t stream) {
-  const int Kc = static_cast<int>(K / S);
-  const float one = 1.0f, zero = 0.0f;
-  rocblas_status st = rocblas_sgemm_strided_batched(
-      h, rocblas_operation_none, rocblas_operation_transpose, N, Mo, Kc, &one, Bm, ldb,
-      static_cast<rocblas_stride>(Kc) * ldb, A, lda, static_cast<rocblas_stride>(Kc) * lda, &zero,
-      part, N, static_cast<rocblas_stride>(Mo) * N, S);
-  RXMET_CHECK_ARG(st == rocblas_status_success, "rocBLAS strided-batched sgemm failed");
-  const int64_t rem = K - static_cast<int64_t>(Kc) * S;
-  if (rem > 0) {
-    const size_t off = static_cast<size_t>(Kc) * S;
-    st = rocblas_sgemm(h, rocblas_operation_none, rocblas_operation_transpose, N, Mo,
-                       static_cast<int>(rem), &one, Bm + off * ldb, ldb, A + off * lda, lda, &one,
-                       part, N);
-    RXMET_CHECK_ARG(st == rocblas_status_success, "rocBLAS sgemm (split-K tail) failed");
-  }
-  const int64_t n = static_cast<int64_t>(Mo) * N;
-  hipLaunchKernelGGL(sum_partials, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
-                     stream, n, S, part, out);
-  RXMET_CHECK_LAUNCH();
-  return 0;
-}
 
 }  // namespace gru
 }  // namespace rxmet
 
 using namespace rxmet;
 using namespace rxmet::gru;
+using namespace rxmet::blas;
 
 extern "C" {
 
@@ -541,7 +473,7 @@ int rxmet_gru_backward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const f
 
   int device = 0;
   RXMET_CHECK_HIP(hipGetDevice(&device));
-  rocblas_handle bh = blas_handle(device);
+  rocblas_handle bh = handle(device);
   RXMET_CHECK_ARG(bh != nullptr, "rocBLAS handle creation failed");
   rocblas_set_stream(bh, stream);
   const int M = T * B;

@@ -1,0 +1,488 @@
+// lstm_bwd.hip — MI355X QuantLSTM STE backward, behind rxmet_lstm_backward_quant.
+//
+// Reference path: lstm_backward_qat (pytorch/lib/lstm_interface_binding.cc:437-480)
+// dequantises the saved masters and checkpoints (dequantizeQCarrierKernel, double) and runs
+// lstmBackwardFloatCuda (src/lstm/backward_float_cuda.cu:189-330): per step t = T-1..0 the
+// pointwise backward with the clamp masks (:50-104) and an SGEMM dh = dgates_hh W_hh, then
+// the dx / dW_ih / dW_hh SGEMMs, a bias column reduction and seven mask passes.
+//
+// Here:
+//   1. prep      : dequantised x and W_ih for the GEMMs, previous hidden states [T,B,H] (h0
+//                  first), each with a trailing column of ones so that the weight-gradient
+//                  GEMMs also produce the bias gradients; W_hh codes packed as int8 MFMA
+//                  fragments of the transposed product, their column sums;
+//   2. recurrence: one persistent workgroup per 16 sequences walks t = T-1..0.  A lane owns
+//                  one hidden unit for four sequences (four unit tiles per wave); dh stays
+//                  in registers, dc in LDS.  Per step: the pointwise backward with every
+//                  mask family in the reference's operation order, both gate-gradient
+//                  tensors written for the GEMMs, then dh = W_hh_deq^T dgates_hh on int8
+//                  MFMA: dgates_hh * scale_W is written per sequence as 22-bit block fixed
+//                  point (exponent from the row maximum) in three int8 planes, multiplied
+//                  exactly against the W_hh codes and recombined in double;
+//   3. rocBLAS   : dx, and split-K dW_ih | db_ih and dW_hh | db_hh; one pass applies the
+//                  master masks and splits off the bias columns.
+#include <cmath>
+#include <vector>
+
+#include "blas_util.h"
+#include "lstm_internal.h"
+#include "mfma_frag.h"
+#include "rxmet_common.h"
+#include "rxmet_lstm.h"
+
+namespace rxmet {
+namespace lstm {
+
+constexpr int kBB = 16;          // sequences per workgroup
+constexpr int kTPW = 4;          // unit tiles per wave
+constexpr int kPlanes = 3;
+constexpr int kMaxHB = 512;
+
+__device__ __forceinline__ float deq(float q, double s, double zp) {
+  return static_cast<float>((static_cast<double>(q) - zp) * s);
+}
+__device__ __forceinline__ float keepf(const uint8_t *m, uint32_t i) {
+  return m[i] == 0 ? 1.0f : 0.0f;
+}
+
+// ---------------------------------------------------------------------------------
+// 1. prep
+// ---------------------------------------------------------------------------------
+struct PrepArgs {
+  int T, B, I, H;
+  const float *x_q, *w_ih_q, *h0_q, *hidden;
+  const float *s_wih;     // [4H]
+  double s_x, zp_x, s_h, zp_h;
+  float *xd;              // [T*B, I+1]
+  float *wid;             // [4H, I]
+  float *hprev;           // [T*B, H+1]
+};
+
+__global__ __launch_bounds__(256) void lstm_bwd_prep(PrepArgs a) {
+  const int64_t M = static_cast<int64_t>(a.T) * a.B, C = 4 * static_cast<int64_t>(a.H);
+  const int64_t n0 = M * (a.I + 1), n1 = C * a.I, n2 = M * (a.H + 1);
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n0 + n1 + n2;
+       i += stride) {
+    if (i < n0) {
+      const int64_t m = i / (a.I + 1), k = i % (a.I + 1);
+      a.xd[i] = k == a.I ? 1.0f : deq(a.x_q[m * a.I + k], a.s_x, a.zp_x);
+    } else if (i < n0 + n1) {
+      const int64_t e = i - n0, c = e / a.I;
+      a.wid[e] = deq(a.w_ih_q[e], static_cast<double>(a.s_wih[c]), 0.0);
+    } else {
+      const int64_t e = i - n0 - n1, m = e / (a.H + 1), k = e % (a.H + 1);
+      float v = 1.0f;
+      if (k < a.H) {
+        const float q = m < a.B ? a.h0_q[m * a.H + k] : a.hidden[(m - a.B) * a.H + k];
+        v = deq(q, a.s_h, a.zp_h);
+      }
+      a.hprev[e] = v;
+    }
+  }
+}
+
+// W_hh codes [4H][H] -> B fragments of D[b][j] = sum_c A[b][c] W[c][j]:
+// frag[(jt * KS2 + s) * 64 + lane] = W[64 s + 16 (lane / 16) + 0..15][16 jt + lane % 16];
+// colsum[j] = sum_c W[c][j].
+__global__ __launch_bounds__(64) void lstm_pack_whh_t(int H, int KS2, const float *__restrict__ wq,
+                                                      v4i *__restrict__ frag,
+                                                      float *__restrict__ colsum) {
+  const int lane = threadIdx.x, idx = blockIdx.x;
+  const int s = idx % KS2, jt = idx / KS2;
+  const int C = 4 * H, j = 16 * jt + lane % 16;
+  int wd[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    int by[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int c = 64 * s + 16 * (lane / 16) + 4 * q + e;
+      by[e] = c < C ? static_cast<int>(wq[static_cast<size_t>(c) * H + j]) : 0;
+    }
+    wd[q] = pack4_i8(by[0], by[1], by[2], by[3]);
+  }
+  frag[static_cast<size_t>(idx) * 64 + lane] = v4i{wd[0], wd[1], wd[2], wd[3]};
+  if (s == 0 && lane < 16) {
+    int sum = 0;
+    for (int c = 0; c < C; ++c) sum += static_cast<int>(wq[static_cast<size_t>(c) * H + j]);
+    colsum[j] = static_cast<float>(sum);
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// 2. recurrence
+// ---------------------------------------------------------------------------------
+struct BwdArgs {
+  int T, B, H, KS2, UT;
+  const float *grad_out, *grad_hn, *grad_cn;   // grad_hn / grad_cn may be null
+  const float *gate_out, *cell, *cell_tanh, *c0_q;
+  const uint8_t *ih_m, *hh_m, *gin_m, *gout_m, *cell_m, *tanh_m, *hid_m, *h0_m, *c0_m;
+  const v4i *frag;
+  const float *colsum;   // [H]
+  const float *s_whh;    // [4H]
+  double s_gout[4], zp_gout[4], s_c, zp_c, s_t, zp_t;
+  float *dli, *dlh;      // [T, B, 4H]
+  float *dh0, *dc0;      // [B, H]
+};
+
+__global__ __launch_bounds__(512) void lstm_bwd_recurrence(BwdArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int H = a.H, C = 4 * H, B = a.B;
+  const int ROW = a.KS2 * 64 + 16;
+  float *dcs = reinterpret_cast<float *>(smem);                              // [16][H]
+  unsigned *rowmax = reinterpret_cast<unsigned *>(dcs + kBB * H);            // [16]
+  int *rowexp = reinterpret_cast<int *>(rowmax + kBB);                       // [16]
+  int8_t *plane = reinterpret_cast<int8_t *>(rowexp + kBB);                  // [3][16][ROW]
+  const int tid = threadIdx.x, w = tid / 64, l = tid % 64;
+  const int b0 = blockIdx.x * kBB, nrow0 = 4 * (l / 16);
+  for (int i = tid; i < kBB * H; i += blockDim.x) {
+    const int n = i / H, j = i % H, b = b0 + n;
+    dcs[i] = (a.grad_cn && b < B) ? a.grad_cn[static_cast<size_t>(b) * H + j] : 0.0f;
+  }
+  for (int i = tid; i < kPlanes * kBB * ROW / 4; i += blockDim.x) reinterpret_cast<int *>(plane)[i] = 0;
+  if (tid < kBB) rowmax[tid] = 0u;
+  float dh[kTPW][4];
+#pragma unroll
+  for (int u = 0; u < kTPW; ++u)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int ut = kTPW * w + u, j = 16 * ut + l % 16, b = b0 + nrow0 + r;
+      dh[u][r] = (a.grad_hn && ut < a.UT && b < B) ? a.grad_hn[static_cast<size_t>(b) * H + j] : 0.0f;
+    }
+  __syncthreads();
+  const uint32_t BH = static_cast<uint32_t>(B) * H, BC = static_cast<uint32_t>(B) * C;
+
+  for (int t = a.T - 1; t >= 0; --t) {
+    // ---- pointwise backward; dgates_hh * scale_W kept in registers for the dh GEMM ----
+    float sv[kTPW][4][4];
+#pragma unroll
+    for (int u = 0; u < kTPW; ++u) {
+      const int ut = kTPW * w + u;
+      const int j = 16 * ut + l % 16;
+      const bool tile = ut < a.UT;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int nr = nrow0 + r, b = b0 + nr;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) sv[u][r][g] = 0.0f;
+        if (!tile || b >= B) continue;
+        const uint32_t e = static_cast<uint32_t>(t) * BH + static_cast<uint32_t>(b) * H + j;
+        const uint32_t gb = static_cast<uint32_t>(t) * BC + static_cast<uint32_t>(b) * C + j;
+        const float ig = deq(a.gate_out[gb], a.s_gout[0], a.zp_gout[0]);
+        const float fg = deq(a.gate_out[gb + H], a.s_gout[1], a.zp_gout[1]);
+        const float gg = deq(a.gate_out[gb + 2 * H], a.s_gout[2], a.zp_gout[2]);
+        const float og = deq(a.gate_out[gb + 3 * H], a.s_gout[3], a.zp_gout[3]);
+        const float ct = deq(a.cell_tanh[e], a.s_t, a.zp_t);
+        const float pc = t == 0 ? deq(a.c0_q[static_cast<uint32_t>(b) * H + j], a.s_c, a.zp_c)
+                                : deq(a.cell[e - BH], a.s_c, a.zp_c);
+        float &dcr = dcs[nr * H + j];
+        const float dht = (dh[u][r] + a.grad_out[e]) * keepf(a.hid_m, e);
+        const float d_o = dht * ct;
+        const float dct = dht * og * keepf(a.tanh_m, e);
+        const float dc = dcr + dct * (1.0f - ct * ct);
+        const float mdc = dc * keepf(a.cell_m, e);
+        const float dfg = mdc * pc;
+        const float dig = mdc * gg, dgg = mdc * ig;
+        const float go0 = dig * keepf(a.gout_m, gb), go1 = dfg * keepf(a.gout_m, gb + H);
+        const float go2 = dgg * keepf(a.gout_m, gb + 2 * H), go3 = d_o * keepf(a.gout_m, gb + 3 * H);
+        const float gi[4] = {go0 * ig * (1.0f - ig), go1 * fg * (1.0f - fg), go2 * (1.0f - gg * gg),
+                             go3 * og * (1.0f - og)};
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const uint32_t gi_ = gb + g * H;
+          const float grad = gi[g] * keepf(a.gin_m, gi_);
+          const float li = grad * keepf(a.ih_m, gi_);
+          const float lh = grad * keepf(a.hh_m, gi_);
+          a.dli[gi_] = li;
+          a.dlh[gi_] = lh;
+          sv[u][r][g] = lh * a.s_whh[g * H + j];
+        }
+        dcr = mdc * fg;
+      }
+    }
+    // row maxima (NaN and inf rows propagate as NaN)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float mx = 0.0f;
+#pragma unroll
+      for (int u = 0; u < kTPW; ++u)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const float as = fabsf(sv[u][r][g]);
+          mx = (as > mx || as != as) ? as : mx;
+        }
+      if (!(mx <= 3.0e38f)) mx = INFINITY;
+      atomicMax(&rowmax[nrow0 + r], __float_as_uint(mx));
+    }
+    __syncthreads();
+    if (tid < kBB) {
+      const float m = __uint_as_float(rowmax[tid]);
+      int ex = 0;
+      if (m > 0.0f && m <= 3.0e38f) frexpf(m, &ex);
+      rowexp[tid] = (m > 0.0f && m <= 3.0e38f) ? 22 - ex : (m == 0.0f ? 0 : 1000);
+    }
+    __syncthreads();
+    // ---- quantise the lane's own values into the three planes ----
+#pragma unroll
+    for (int u = 0; u < kTPW; ++u) {
+      const int ut = kTPW * w + u;
+      if (ut >= a.UT) continue;
+      const int j = 16 * ut + l % 16;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int nr = nrow0 + r, ex = rowexp[nr];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          int q = 0;
+          if (ex != 1000) q = static_cast<int>(rintf(ldexpf(sv[u][r][g], ex)));
+          const int uq = q + (1 << 23);
+          const int c = g * H + j;
+          plane[(0 * kBB + nr) * ROW + c] = static_cast<int8_t>((uq & 255) - 128);
+          plane[(1 * kBB + nr) * ROW + c] = static_cast<int8_t>(((uq >> 8) & 255) - 128);
+          plane[(2 * kBB + nr) * ROW + c] = static_cast<int8_t>((uq >> 16) - 128);
+        }
+      }
+    }
+    __syncthreads();
+    if (tid < kBB) rowmax[tid] = 0u;
+    // ---- dh = W_hh_deq^T dgates_hh on MFMA ----
+#pragma unroll
+    for (int u = 0; u < kTPW; ++u) {
+      const int ut = kTPW * w + u;
+      if (ut >= a.UT) continue;
+      v4i acc[kPlanes];
+#pragma unroll
+      for (int q = 0; q < kPlanes; ++q) acc[q] = v4i{0, 0, 0, 0};
+      for (int s = 0; s < a.KS2; ++s) {
+        const v4i bf = a.frag[(static_cast<uint32_t>(ut) * a.KS2 + s) * 64 + l];
+#pragma unroll
+        for (int q = 0; q < kPlanes; ++q) {
+          const v4i afr = *reinterpret_cast<const v4i *>(plane + (q * kBB + l % 16) * ROW + 64 * s +
+                                                         16 * (l / 16));
+          acc[q] = mfma_i8(afr, bf, acc[q]);
+        }
+      }
+      const double cs = static_cast<double>(a.colsum[16 * ut + l % 16]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int ex = rowexp[nrow0 + r];
+        const double comb = 65536.0 * acc[2][r] + 256.0 * acc[1][r] + static_cast<double>(acc[0][r]) +
+                            32896.0 * cs;
+        dh[u][r] = ex == 1000 ? NAN : static_cast<float>(ldexp(comb, -ex));
+      }
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int u = 0; u < kTPW; ++u) {
+    const int ut = kTPW * w + u;
+    if (ut >= a.UT) continue;
+    const int j = 16 * ut + l % 16;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int nr = nrow0 + r, b = b0 + nr;
+      if (b >= B) continue;
+      const uint32_t o = static_cast<uint32_t>(b) * H + j;
+      a.dh0[o] = dh[u][r] * keepf(a.h0_m, o);
+      a.dc0[o] = dcs[nr * H + j] * keepf(a.c0_m, o);
+    }
+  }
+}
+
+size_t bwd_lds(int H, int KS2) {
+  return sizeof(float) * kBB * static_cast<size_t>(H) + 2 * sizeof(int) * kBB +
+         static_cast<size_t>(kPlanes) * kBB * (KS2 * 64 + 16);
+}
+
+// dx *= keep(x_m); dW = aug[:, :K] * keep(W_m); db = aug[:, K] * keep(b_m) (when bias).
+__global__ __launch_bounds__(256) void lstm_bwd_finish(int64_t nx, float *dx, const uint8_t *xm,
+                                                       int C, int I, int H, const float *aug_ih,
+                                                       const float *aug_hh, float *dwi, float *dwh,
+                                                       float *dbi, float *dbh, const uint8_t *wim,
+                                                       const uint8_t *whm, const uint8_t *bim,
+                                                       const uint8_t *bhm) {
+  const int64_t n1 = static_cast<int64_t>(C) * I, n2 = static_cast<int64_t>(C) * H;
+  const int64_t total = nx + n1 + n2 + C;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+       i += stride) {
+    if (i < nx) {
+      if (xm[i]) dx[i] = 0.0f;
+    } else if (i < nx + n1) {
+      const int64_t e = i - nx, c = e / I, k = e % I;
+      dwi[e] = wim[e] ? 0.0f : aug_ih[c * (I + 1) + k];
+    } else if (i < nx + n1 + n2) {
+      const int64_t e = i - nx - n1, c = e / H, k = e % H;
+      dwh[e] = whm[e] ? 0.0f : aug_hh[c * (H + 1) + k];
+    } else {
+      const int64_t c = i - nx - n1 - n2;
+      if (dbi) dbi[c] = bim[c] ? 0.0f : aug_ih[c * (I + 1) + I];
+      if (dbh) dbh[c] = bhm[c] ? 0.0f : aug_hh[c * (H + 1) + H];
+    }
+  }
+}
+
+struct BwdWorkspace {
+  size_t dli, dlh, xd, wid, hprev, frag, colsum, swih, swhh, aug_ih, aug_hh, part, total;
+  BwdWorkspace(int T, int B, int I, int H) {
+    const size_t C = 4 * static_cast<size_t>(H), M = static_cast<size_t>(T) * B;
+    const size_t KS2 = (C + 63) / 64;
+    auto al = [](size_t x) { return (x + 255) & ~static_cast<size_t>(255); };
+    size_t o = 0;
+    dli = o; o += al(sizeof(float) * M * C);
+    dlh = o; o += al(sizeof(float) * M * C);
+    xd = o; o += al(sizeof(float) * M * (I + 1));
+    wid = o; o += al(sizeof(float) * C * I);
+    hprev = o; o += al(sizeof(float) * M * (H + 1));
+    frag = o; o += al(sizeof(v4i) * 64 * (H / 16 + 1) * KS2);
+    colsum = o; o += al(sizeof(float) * H);
+    swih = o; o += al(sizeof(float) * C);
+    swhh = o; o += al(sizeof(float) * C);
+    aug_ih = o; o += al(sizeof(float) * C * (I + 1));
+    aug_hh = o; o += al(sizeof(float) * C * (H + 1));
+    const size_t S = static_cast<size_t>(blas::splitk_chunks(static_cast<int64_t>(M)));
+    part = o; o += al(sizeof(float) * S * C * (static_cast<size_t>(I) > H ? I + 1 : H + 1));
+    total = o;
+  }
+};
+
+}  // namespace lstm
+}  // namespace rxmet
+
+using namespace rxmet;
+using namespace rxmet::lstm;
+
+extern "C" {
+
+int64_t rxmet_lstm_backward_workspace_bytes(int32_t T, int32_t B, int32_t I, int32_t H) {
+  if (T < 1 || B < 1 || I < 1 || H < 1) return 0;
+  return static_cast<int64_t>(BwdWorkspace(T, B, I, H).total);
+}
+
+int rxmet_lstm_backward_quant(int32_t T, int32_t B, int32_t I, int32_t H,
+                              const rxmet_lstm_params *params, const rxmet_lstm_saved *saved,
+                              const float *grad_output, const float *grad_h_n,
+                              const float *grad_c_n, float *dx, float *dW_ih, float *dW_hh,
+                              float *db_ih, float *db_hh, float *dh0, float *dc0,
+                              void *workspace, void *stream_) {
+  clear_error();
+  RXMET_CHECK_ARG(T >= 1 && B >= 1 && I >= 1 && H >= 1, "dimensions must be positive");
+  RXMET_CHECK_ARG(H % 16 == 0 && H <= kMaxHB,
+                  "hidden_size must be a multiple of 16 and at most 512 for the MFMA backward");
+  RXMET_CHECK_ARG(params && saved && grad_output && dx && dW_ih && dW_hh && dh0 && dc0 && workspace,
+                  "required pointer is null");
+  RXMET_CHECK_ARG(params->hidden == H, "params hidden size does not match");
+  const bool bias = params->bias_enabled != 0;
+  RXMET_CHECK_ARG(!bias || (db_ih && db_hh), "bias gradients requested but pointers are null");
+  const rxmet_lstm_saved &sv = *saved;
+  RXMET_CHECK_ARG(sv.x_q && sv.w_ih_q && sv.w_hh_q && sv.h0_q && sv.c0_q && sv.x_m && sv.w_ih_m &&
+                      sv.w_hh_m && sv.h0_m && sv.c0_m && sv.gate_out && sv.cell && sv.cell_tanh &&
+                      sv.hidden && sv.ih_linear_m && sv.hh_linear_m && sv.gate_in_m &&
+                      sv.gate_out_m && sv.cell_m && sv.cell_tanh_m && sv.hidden_m,
+                  "backward needs every saved tensor");
+  RXMET_CHECK_ARG(!bias || (sv.b_ih_m && sv.b_hh_m), "backward with bias needs the bias masks");
+  RXMET_CHECK_ARG(params->config.op[RXMET_LSTM_W_HH].bits <= 8,
+                  "W_hh wider than 8 bits is not supported by the MFMA backward");
+  RXMET_CHECK_ARG(static_cast<double>(T) * B * 4 * H < 4294967295.0,
+                  "T*B*4H too large for 32-bit element offsets");
+  StepParams sp;
+  ChannelParams cp;
+  if (int rc = derive(*params, &sp, &cp)) return rc;
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  const int C = 4 * H, KS2 = (C + 63) / 64, UT = H / 16, M = T * B;
+  const BwdWorkspace ws(T, B, I, H);
+  char *wsb = static_cast<char *>(workspace);
+  float *dli = reinterpret_cast<float *>(wsb + ws.dli);
+  float *dlh = reinterpret_cast<float *>(wsb + ws.dlh);
+  float *xd = reinterpret_cast<float *>(wsb + ws.xd);
+  float *wid = reinterpret_cast<float *>(wsb + ws.wid);
+  float *hprev = reinterpret_cast<float *>(wsb + ws.hprev);
+  v4i *frag = reinterpret_cast<v4i *>(wsb + ws.frag);
+  float *colsum = reinterpret_cast<float *>(wsb + ws.colsum);
+  float *swih = reinterpret_cast<float *>(wsb + ws.swih);
+  float *swhh = reinterpret_cast<float *>(wsb + ws.swhh);
+  float *aug_ih = reinterpret_cast<float *>(wsb + ws.aug_ih);
+  float *aug_hh = reinterpret_cast<float *>(wsb + ws.aug_hh);
+  float *part = reinterpret_cast<float *>(wsb + ws.part);
+  std::vector<float> host(2 * C);
+  for (int c = 0; c < C; ++c) {
+    host[c] = cp.w_ih_scale[c];
+    host[C + c] = cp.w_hh_scale[c];
+  }
+  RXMET_CHECK_HIP(hipMemcpyAsync(swih, host.data(), sizeof(float) * 2 * C, hipMemcpyHostToDevice,
+                                 stream));
+
+  PrepArgs pa;
+  pa.T = T; pa.B = B; pa.I = I; pa.H = H;
+  pa.x_q = sv.x_q; pa.w_ih_q = sv.w_ih_q; pa.h0_q = sv.h0_q; pa.hidden = sv.hidden;
+  pa.s_wih = swih; pa.s_x = sp.x.dscale; pa.zp_x = sp.x.dzp; pa.s_h = sp.h.dscale; pa.zp_h = sp.h.dzp;
+  pa.xd = xd; pa.wid = wid; pa.hprev = hprev;
+  {
+    const int64_t n = static_cast<int64_t>(M) * (I + 1) + static_cast<int64_t>(C) * I +
+                      static_cast<int64_t>(M) * (H + 1);
+    int64_t blocks = (n + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    hipLaunchKernelGGL(lstm_bwd_prep, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, pa);
+    RXMET_CHECK_LAUNCH();
+  }
+  hipLaunchKernelGGL(lstm_pack_whh_t, dim3(UT * KS2), dim3(64), 0, stream, H, KS2, sv.w_hh_q, frag,
+                     colsum);
+  RXMET_CHECK_LAUNCH();
+
+  BwdArgs ba;
+  ba.T = T; ba.B = B; ba.H = H; ba.KS2 = KS2; ba.UT = UT;
+  ba.grad_out = grad_output; ba.grad_hn = grad_h_n; ba.grad_cn = grad_c_n;
+  ba.gate_out = sv.gate_out; ba.cell = sv.cell; ba.cell_tanh = sv.cell_tanh; ba.c0_q = sv.c0_q;
+  ba.ih_m = sv.ih_linear_m; ba.hh_m = sv.hh_linear_m; ba.gin_m = sv.gate_in_m;
+  ba.gout_m = sv.gate_out_m; ba.cell_m = sv.cell_m; ba.tanh_m = sv.cell_tanh_m;
+  ba.hid_m = sv.hidden_m; ba.h0_m = sv.h0_m; ba.c0_m = sv.c0_m;
+  ba.frag = frag; ba.colsum = colsum; ba.s_whh = swhh;
+  for (int g = 0; g < 4; ++g) {
+    ba.s_gout[g] = sp.gout[g].dscale;
+    ba.zp_gout[g] = sp.gout[g].dzp;
+  }
+  ba.s_c = sp.c.dscale; ba.zp_c = sp.c.dzp; ba.s_t = sp.tanh_c.dscale; ba.zp_t = sp.tanh_c.dzp;
+  ba.dli = dli; ba.dlh = dlh; ba.dh0 = dh0; ba.dc0 = dc0;
+  const size_t lds = bwd_lds(H, KS2);
+  {
+    rxmet::prof::Scope ps__("lstm_bwd_recurrence", stream);
+    RXMET_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&lstm_bwd_recurrence),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        static_cast<int>(lds)));
+    hipLaunchKernelGGL(lstm_bwd_recurrence, dim3((B + kBB - 1) / kBB),
+                       dim3(64 * ((UT + kTPW - 1) / kTPW)), lds, stream, ba);
+  }
+  RXMET_CHECK_LAUNCH();
+
+  int device = 0;
+  RXMET_CHECK_HIP(hipGetDevice(&device));
+  rocblas_handle bh = blas::handle(device);
+  RXMET_CHECK_ARG(bh != nullptr, "rocBLAS handle creation failed");
+  rocblas_set_stream(bh, stream);
+  {
+    rxmet::prof::Scope ps__("lstm_bwd_weight_gemms", stream);
+    // dx[M][I] = dli[M][C] * W_ih_deq[C][I]
+    RXMET_CHECK_ARG(blas::gemm_rm(bh, false, false, M, I, C, dli, C, wid, I, dx, I) ==
+                        rocblas_status_success,
+                    "rocBLAS sgemm (dx) failed");
+    const int S = blas::splitk_chunks(M);
+    if (int rc = blas::gemm_tn_splitk(bh, C, I + 1, M, dli, C, xd, I + 1, aug_ih, part, S, stream))
+      return rc;
+    if (int rc = blas::gemm_tn_splitk(bh, C, H + 1, M, dlh, C, hprev, H + 1, aug_hh, part, S, stream))
+      return rc;
+  }
+  {
+    const int64_t nx = static_cast<int64_t>(M) * I;
+    const int64_t n = nx + static_cast<int64_t>(C) * (I + H + 1);
+    int64_t blocks = (n + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    hipLaunchKernelGGL(lstm_bwd_finish, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
+                       nx, dx, sv.x_m, C, I, H, aug_ih, aug_hh, dW_ih, dW_hh, bias ? db_ih : nullptr,
+                       bias ? db_hh : nullptr, sv.w_ih_m, sv.w_hh_m, sv.b_ih_m, sv.b_hh_m);
+    RXMET_CHECK_LAUNCH();
+  }
+  return 0;
+}
+
+}  // extern "C"

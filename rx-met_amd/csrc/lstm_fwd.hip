@@ -1,0 +1,620 @@
+// lstm_fwd.hip — MI355X QuantLSTM FP32 q-carrier forward, behind rxmet_lstm_forward_quant.
+//
+// Reference path: lstm_forward_quantized (pytorch/lib/lstm_interface_binding.cc:643-806) ->
+// lstmForwardQuantizedFpCuda (src/lstm/forward_quantized_fp_cuda.cu): boundary quantisation
+// kernels (:580-660), one SGEMM for the input linear of all steps, then per step an SGEMM for
+// the recurrent linear and fusedLstmPointwiseKernel (:690-880).  Numerics follow the CPU
+// q-carrier reference that specifies that path (src/lstm/forward_quantized_fp_cpu.cc:20-197).
+//
+// Here:
+//   1. lstm_quant_weights : one wave per gate channel quantises its W_ih / W_hh rows and
+//      biases (codes + clamp masks), sums the W_hh codes and rescales the bias codes to the
+//      accumulator grids;
+//   2. lstm_quant_inputs  : x, h0, c0 codes and masks;
+//   3. lstm_pack_whh      : W_hh codes -> int8 MFMA B fragments;
+//   4. lstm_input_gemm    : the input linear of all T steps as an exact integer GEMM with
+//      the whole input branch fused in its epilogue (bias, rescale, clamp + mask, and the
+//      rescale to each gate-input grid), so the recurrence only adds the recurrent branch;
+//   5. lstm_recurrence    : one persistent workgroup per 16 sequences walks the T steps.  h
+//      codes live in LDS as int8 planes, the recurrent linear is v_mfma_i32_16x16x64_i8 on
+//      W_hh fragments streamed from L2, and the four gates, real sigmoid/tanh, cell and
+//      hidden fusion, every clamp mask and the checkpoints are computed in registers; the
+//      cell state stays in LDS, each entry owned by one lane.
+//
+// Activations: sigmoid keeps the reference's float op order around exp, with exp and tanh
+// evaluated in double and rounded once to float.
+#include <cmath>
+#include <vector>
+
+#include "lstm_internal.h"
+#include "mfma_frag.h"
+#include "rxmet_common.h"
+#include "rxmet_lstm.h"
+
+namespace rxmet {
+namespace lstm {
+
+constexpr int kBT = 16;       // sequences per recurrent workgroup (MFMA N)
+constexpr int kMaxH = 512;    // 8 waves x 4 unit tiles x 16 units
+constexpr int kTilesPerWave = 4;
+
+// Per-channel constants uploaded from the host.
+struct ChanHost {
+  float w_ih_s, w_hh_s, b_ih_s, b_hh_s;
+  float ih_mult, hh_mult, ih_bmult, hh_bmult;
+  int32_t ih_shift, hh_shift, ih_bshift, hh_bshift;
+};
+
+// Per-channel constants produced on the device for the two linears.
+struct ChanRun {
+  float ih_bacc;   // rescaled centred bias of the input linear (0 without bias)
+  float hh_bacc;
+  int32_t hh_k;    // integer correction of the recurrent MFMA sum (zero points, plane offsets)
+  int32_t pad;
+};
+
+__device__ __forceinline__ float rescale(float v, float mult, int shift) {
+  return rintf(ldexpf(v * mult, -shift));
+}
+
+__device__ __forceinline__ float clamp_grid(double v, const Grid &g, uint8_t &clamped) {
+  clamped = (v < g.dlo || v > g.dhi) ? 1 : 0;
+  return v <= g.dflo ? g.flo : (v >= g.dfhi ? g.fhi : static_cast<float>(v));
+}
+
+__device__ __forceinline__ float quantize(float v, float s, int32_t zp, const Grid &g,
+                                          uint8_t &clamped) {
+  const double r = rint(static_cast<double>(v) / static_cast<double>(s)) + static_cast<double>(zp);
+  return clamp_grid(r, g, clamped);
+}
+
+__device__ __forceinline__ float dequant(float q, float s, int32_t zp) {
+  return static_cast<float>((static_cast<double>(q) - zp) * static_cast<double>(s));
+}
+
+__device__ __forceinline__ float center(float v, int32_t zp) {
+  return static_cast<float>(static_cast<double>(v) - zp);
+}
+
+__device__ __forceinline__ float act_sigmoid(float x) {
+  if (x >= 0.0f) {
+    const float e = static_cast<float>(exp(-static_cast<double>(x)));
+    return 1.0f / (1.0f + e);
+  }
+  const float e = static_cast<float>(exp(static_cast<double>(x)));
+  return e / (1.0f + e);
+}
+
+__device__ __forceinline__ float act_tanh(float x) {
+  return static_cast<float>(tanh(static_cast<double>(x)));
+}
+
+// Real activation boundary: dequantise, activate in fp32, quantise to the output grid.
+__device__ __forceinline__ float real_act(float q, const Grid &in, const Grid &out, bool is_tanh,
+                                          uint8_t &clamped) {
+  const float x = static_cast<float>((static_cast<double>(q) - in.dzp) * in.dscale);
+  const float a = is_tanh ? act_tanh(x) : act_sigmoid(x);
+  const double t = rint(static_cast<double>(a) / out.dscale) + out.dzp;
+  return clamp_grid(t, out, clamped);
+}
+
+// Element r of an MFMA accumulator without dynamic register indexing.
+__device__ __forceinline__ int pick(const v4i &v, int r) {
+  return r == 0 ? v[0] : (r == 1 ? v[1] : (r == 2 ? v[2] : v[3]));
+}
+
+__device__ __forceinline__ float cell_scale(float p, const StepParams &sp, int k) {
+  return sp.cell_fp[k]
+             ? static_cast<float>(ldexp(static_cast<double>(p) * sp.cell_mant[k], sp.cell_exp[k]))
+             : p * sp.cell_ratio[k];
+}
+
+// ---------------------------------------------------------------------------------
+// 1-3. quantisation prologue
+// ---------------------------------------------------------------------------------
+struct WeightArgs {
+  int I, H, bias, npl;
+  const float *W_ih, *W_hh, *b_ih, *b_hh;
+  const ChanHost *ch;
+  float *wq_ih, *wq_hh, *bq_ih, *bq_hh;
+  uint8_t *wm_ih, *wm_hh, *bm_ih, *bm_hh;
+  ChanRun *run;
+  int32_t hh_k_factor;  // h_offset - zp_h (+128 with two planes)
+};
+
+__device__ __forceinline__ int wave_sum_int(int v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+__global__ __launch_bounds__(64) void lstm_quant_weights(WeightArgs a, Grid gw_ih, Grid gw_hh,
+                                                         Grid gb_ih, Grid gb_hh) {
+  const int c = blockIdx.x, l = threadIdx.x;
+  const ChanHost ch = a.ch[c];
+  uint8_t m;
+  for (int k = l; k < a.I; k += 64) {
+    const size_t i = static_cast<size_t>(c) * a.I + k;
+    const float q = quantize(a.W_ih[i], ch.w_ih_s, 0, gw_ih, m);
+    a.wq_ih[i] = q;
+    if (a.wm_ih) a.wm_ih[i] = m;
+  }
+  int s = 0;
+  for (int k = l; k < a.H; k += 64) {
+    const size_t i = static_cast<size_t>(c) * a.H + k;
+    const float q = quantize(a.W_hh[i], ch.w_hh_s, 0, gw_hh, m);
+    a.wq_hh[i] = q;
+    if (a.wm_hh) a.wm_hh[i] = m;
+    s += static_cast<int>(q);
+  }
+  s = wave_sum_int(s);
+  if (l == 0) {
+    ChanRun r;
+    r.ih_bacc = 0.0f;
+    r.hh_bacc = 0.0f;
+    if (a.bias) {
+      const float qi = quantize(a.b_ih[c], ch.b_ih_s, 0, gb_ih, m);
+      a.bq_ih[c] = qi;
+      if (a.bm_ih) a.bm_ih[c] = m;
+      const float qh = quantize(a.b_hh[c], ch.b_hh_s, 0, gb_hh, m);
+      a.bq_hh[c] = qh;
+      if (a.bm_hh) a.bm_hh[c] = m;
+      r.ih_bacc = rescale(center(qi, 0), ch.ih_bmult, ch.ih_bshift);
+      r.hh_bacc = rescale(center(qh, 0), ch.hh_bmult, ch.hh_bshift);
+    }
+    r.hh_k = s * a.hh_k_factor;
+    r.pad = 0;
+    a.run[c] = r;
+  }
+}
+
+__global__ __launch_bounds__(256) void lstm_quant_inputs(int64_t nx, int64_t nh, const float *x,
+                                                         const float *h0, const float *c0,
+                                                         StepParams sp, float *xq, uint8_t *xm,
+                                                         float *hq, uint8_t *hm, float *cq,
+                                                         uint8_t *cm) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < nx + nh;
+       i += stride) {
+    uint8_t m = 0;
+    if (i < nx) {
+      xq[i] = quantize(x[i], sp.x.scale, sp.x.zp, sp.x, m);
+      if (xm) xm[i] = m;
+    } else {
+      const int64_t j = i - nx;
+      uint8_t m2 = 0;
+      hq[j] = quantize(h0 ? h0[j] : 0.0f, sp.h.scale, sp.h.zp, sp.h, m);
+      cq[j] = quantize(c0 ? c0[j] : 0.0f, sp.c.scale, sp.c.zp, sp.c, m2);
+      if (hm) hm[j] = h0 ? m : 0;
+      if (cm) cm[j] = c0 ? m2 : 0;
+    }
+  }
+}
+
+// W_hh codes [4H][H] -> B fragments of D[b][c] = sum_k h[b][k] W[c][k]:
+// frag[(ct * KS + s) * 64 + lane] = W[16 ct + lane % 16][64 s + 16 (lane / 16) + 0..15].
+__global__ __launch_bounds__(64) void lstm_pack_whh(int H, int KS, const float *__restrict__ wq,
+                                                    v4i *__restrict__ frag) {
+  const int lane = threadIdx.x, idx = blockIdx.x;
+  const int s = idx % KS, ct = idx / KS;
+  const int c = 16 * ct + lane % 16;
+  int wd[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    int by[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int k = 64 * s + 16 * (lane / 16) + 4 * q + e;
+      by[e] = k < H ? static_cast<int>(wq[static_cast<size_t>(c) * H + k]) : 0;
+    }
+    wd[q] = pack4_i8(by[0], by[1], by[2], by[3]);
+  }
+  frag[static_cast<size_t>(idx) * 64 + lane] = v4i{wd[0], wd[1], wd[2], wd[3]};
+}
+
+// ---------------------------------------------------------------------------------
+// 4. input linear of all steps, exact, with the input branch fused in the epilogue
+// ---------------------------------------------------------------------------------
+template <typename Acc>
+__global__ __launch_bounds__(256) void lstm_input_gemm(int M, int C, int K, int H,
+                                                       const float *__restrict__ xq,
+                                                       const float *__restrict__ wq,
+                                                       const ChanHost *__restrict__ ch,
+                                                       const ChanRun *__restrict__ run,
+                                                       StepParams sp, float *__restrict__ lhs,
+                                                       uint8_t *__restrict__ lin_mask) {
+  __shared__ int As[16][64 + 1];
+  __shared__ int Bs[16][64 + 1];
+  const int tm = blockIdx.y * 64, tn = blockIdx.x * 64;
+  const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
+  const int zx = sp.x.zp;
+  Acc acc[4][4] = {};
+  for (int k0 = 0; k0 < K; k0 += 16) {
+    for (int q = 0; q < 4; ++q) {
+      const int e = threadIdx.x + 256 * q;
+      const int row = e / 16, kk = e % 16;
+      const int gm = tm + row, gk = k0 + kk, gn = tn + row;
+      As[kk][row] = (gm < M && gk < K) ? static_cast<int>(xq[static_cast<size_t>(gm) * K + gk]) - zx : 0;
+      Bs[kk][row] = (gn < C && gk < K) ? static_cast<int>(wq[static_cast<size_t>(gn) * K + gk]) : 0;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < 16; ++kk) {
+      int av[4], bv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) av[i] = As[kk][ty * 4 + i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bv[j] = Bs[kk][tx * 4 + j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] += static_cast<Acc>(av[i]) * bv[j];
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int c = tn + tx * 4 + j;
+    if (c >= C) continue;
+    const int g = c / H;
+    const float bacc = run[c].ih_bacc;
+    const float mult = ch[c].ih_mult;
+    const int shift = ch[c].ih_shift;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = tm + ty * 4 + i;
+      if (m >= M) continue;
+      const float accf = static_cast<float>(acc[i][j]) + bacc;
+      uint8_t clamped;
+      const float lin = clamp_grid(static_cast<double>(rescale(accf, mult, shift)) + sp.ih_lin.dzp,
+                                   sp.ih_lin, clamped);
+      const size_t o = static_cast<size_t>(m) * C + c;
+      lhs[o] = rescale(center(lin, sp.ih_lin.zp), sp.ih_to_gate[g].mult, sp.ih_to_gate[g].shift);
+      if (lin_mask) lin_mask[o] = clamped;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// 5. recurrence
+// ---------------------------------------------------------------------------------
+struct RecArgs {
+  int T, B, H, KS, UT;
+  float h_offset;          // 2^(bits-1) for an unsigned h grid (codes centred into int8/int16)
+  const float *lhs;        // [T, B, 4H] input branch on the gate-input grids
+  const v4i *frag;         // W_hh fragments
+  const ChanHost *ch;
+  const ChanRun *run;
+  const float *h0q, *c0q;  // [B, H]
+  float *output;           // [T, B, H] dequantised
+  float *h_n, *c_n;        // [B, H] dequantised
+  // checkpoints (null in inference)
+  float *gate_out, *cell, *cell_tanh, *hidden;
+  uint8_t *hh_lin_m, *gate_in_m, *gate_out_m, *cell_m, *cell_tanh_m, *hidden_m;
+};
+
+template <int NPL>
+__global__ __launch_bounds__(512) void lstm_recurrence(RecArgs a, StepParams sp) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int H = a.H, C = 4 * H, B = a.B, KS = a.KS;
+  const int ROW = KS * 64 + 16;  // plane row stride in bytes
+  float4 *chan = reinterpret_cast<float4 *>(smem);                       // [4H]: mult, bacc, k, shift
+  float *cstate = reinterpret_cast<float *>(chan + C);                   // [16][H] cell codes
+  int8_t *plane = reinterpret_cast<int8_t *>(cstate + kBT * H);          // [2][NPL][16][ROW]
+  const int tid = threadIdx.x, w = tid / 64, l = tid % 64;
+  const int b0 = blockIdx.x * kBT;
+  for (int c = tid; c < C; c += blockDim.x) {
+    const ChanRun r = a.run[c];
+    const ChanHost h = a.ch[c];
+    chan[c] = make_float4(h.hh_mult, r.hh_bacc, __int_as_float(r.hh_k), __int_as_float(h.hh_shift));
+  }
+  for (int i = tid; i < 2 * NPL * kBT * ROW / 4; i += blockDim.x)
+    reinterpret_cast<int *>(plane)[i] = 0;
+  __syncthreads();
+  // initial h planes
+  for (int i = tid; i < kBT * H; i += blockDim.x) {
+    const int n = i / H, j = i % H, b = b0 + n;
+    const float q = b < B ? a.h0q[static_cast<size_t>(b) * H + j] : static_cast<float>(sp.h.zp);
+    const int hc = static_cast<int>(q - a.h_offset);
+    if (NPL == 1) {
+      plane[n * ROW + j] = static_cast<int8_t>(hc);
+    } else {
+      plane[n * ROW + j] = static_cast<int8_t>((hc & 255) - 128);
+      plane[(kBT + n) * ROW + j] = static_cast<int8_t>(hc >> 8);
+    }
+  }
+  // each (row, unit) cell code is read and written by one lane only
+  for (int i = tid; i < kBT * H; i += blockDim.x) {
+    const int n = i / H, j = i % H, b = b0 + n;
+    cstate[i] = b < B ? a.c0q[static_cast<size_t>(b) * H + j] : static_cast<float>(sp.c.zp);
+  }
+  const int nrow0 = 4 * (l / 16);
+  __syncthreads();
+  const bool train = a.hidden != nullptr;
+
+  for (int t = 0; t < a.T; ++t) {
+    const int cur = t & 1, nxt = cur ^ 1;
+    const int8_t *pc = plane + cur * NPL * kBT * ROW;
+    int8_t *pn = plane + nxt * NPL * kBT * ROW;
+#pragma unroll 1
+    for (int u = 0; u < kTilesPerWave; ++u) {
+      const int ut = kTilesPerWave * w + u;
+      if (ut >= a.UT) continue;
+      const int j = 16 * ut + l % 16;
+      __builtin_amdgcn_sched_barrier(0);
+      v4i acc[4][NPL];
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int q = 0; q < NPL; ++q) acc[g][q] = v4i{0, 0, 0, 0};
+      for (int s = 0; s < KS; ++s) {
+        v4i hfr[NPL];
+#pragma unroll
+        for (int q = 0; q < NPL; ++q)
+          hfr[q] = *reinterpret_cast<const v4i *>(pc + (q * kBT + l % 16) * ROW + 64 * s + 16 * (l / 16));
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const v4i bf = a.frag[(static_cast<uint32_t>(g * a.UT + ut) * KS + s) * 64 + l];
+#pragma unroll
+          for (int q = 0; q < NPL; ++q) acc[g][q] = mfma_i8(hfr[q], bf, acc[g][q]);
+        }
+      }
+      float4 cc[4];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) cc[g] = chan[g * H + j];
+#pragma unroll 1
+      for (int r = 0; r < 4; ++r) {
+        const int nr = nrow0 + r, b = b0 + nr;
+        const bool valid = b < B;
+        const uint32_t row = static_cast<uint32_t>(t) * B + b;  // (t, b)
+        float gout[4];
+        uint8_t m_hl[4], m_gi[4], m_go[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          int v = pick(acc[g][0], r);
+          if (NPL == 2) v += 256 * pick(acc[g][1], r);
+          v += __float_as_int(cc[g].z);
+          const float accf = static_cast<float>(v) + cc[g].y;
+          const float lin = clamp_grid(
+              static_cast<double>(rescale(accf, cc[g].x, __float_as_int(cc[g].w))) + sp.hh_lin.dzp,
+              sp.hh_lin, m_hl[g]);
+          const float rhs = rescale(center(lin, sp.hh_lin.zp), sp.hh_to_gate[g].mult,
+                                    sp.hh_to_gate[g].shift);
+          const float lh = valid ? a.lhs[static_cast<size_t>(row) * C + g * H + j] : 0.0f;
+          const float gi = clamp_grid(static_cast<double>(lh + rhs) + sp.gin[g].dzp, sp.gin[g], m_gi[g]);
+          gout[g] = real_act(gi, sp.gin[g], sp.gout[g], g == 2, m_go[g]);
+        }
+        // cell: two contributions fused, one rounding
+        float &cref = cstate[nr * H + j];
+        const float pf = center(gout[1], sp.gout[1].zp) * center(cref, sp.c.zp);
+        const float pi = center(gout[0], sp.gout[0].zp) * center(gout[2], sp.gout[2].zp);
+        const float sum = cell_scale(pf, sp, 0) + cell_scale(pi, sp, 1);
+        uint8_t m_c, m_t, m_h;
+        const float cn = clamp_grid(static_cast<double>(rintf(sum)) + sp.c.dzp, sp.c, m_c);
+        cref = cn;
+        const float ct = real_act(cn, sp.c, sp.tanh_c, true, m_t);
+        const float raw = center(gout[3], sp.gout[3].zp) * center(ct, sp.tanh_c.zp);
+        const float hv = clamp_grid(static_cast<double>(rescale(raw, sp.hidden.mult, sp.hidden.shift)) +
+                                        sp.h.dzp, sp.h, m_h);
+        if (valid) {
+          const uint32_t oh = row * static_cast<uint32_t>(H) + j;
+          a.output[oh] = dequant(hv, sp.h.scale, sp.h.zp);
+          if (train) {
+            a.cell[oh] = cn;
+            a.cell_tanh[oh] = ct;
+            a.hidden[oh] = hv;
+            a.cell_m[oh] = m_c;
+            a.cell_tanh_m[oh] = m_t;
+            a.hidden_m[oh] = m_h;
+            const uint32_t oc = row * static_cast<uint32_t>(C) + j;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+              a.gate_out[oc + g * H] = gout[g];
+              a.hh_lin_m[oc + g * H] = m_hl[g];
+              a.gate_in_m[oc + g * H] = m_gi[g];
+              a.gate_out_m[oc + g * H] = m_go[g];
+            }
+          }
+          if (t == a.T - 1) {
+            const uint32_t os = static_cast<uint32_t>(b) * H + j;
+            a.h_n[os] = dequant(hv, sp.h.scale, sp.h.zp);
+            a.c_n[os] = dequant(cn, sp.c.scale, sp.c.zp);
+          }
+        }
+        const int hc = static_cast<int>(hv - a.h_offset);
+        if (NPL == 1) {
+          pn[nr * ROW + j] = static_cast<int8_t>(hc);
+        } else {
+          pn[nr * ROW + j] = static_cast<int8_t>((hc & 255) - 128);
+          pn[(kBT + nr) * ROW + j] = static_cast<int8_t>(hc >> 8);
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+size_t recurrence_lds(int H, int KS, int npl) {
+  return sizeof(float4) * 4 * static_cast<size_t>(H) + sizeof(float) * kBT * static_cast<size_t>(H) +
+         static_cast<size_t>(2) * npl * kBT * (KS * 64 + 16);
+}
+
+struct FwdWorkspace {
+  size_t chost, run, frag, lhs, xq, wih, whh, bih, bhh, h0q, c0q, total;
+  FwdWorkspace(int T, int B, int I, int H) {
+    const size_t C = 4 * static_cast<size_t>(H), KS = (H + 63) / 64;
+    auto al = [](size_t x) { return (x + 255) & ~static_cast<size_t>(255); };
+    size_t o = 0;
+    chost = o; o += al(sizeof(ChanHost) * C);
+    run = o; o += al(sizeof(ChanRun) * C);
+    frag = o; o += al(sizeof(v4i) * 64 * (C / 16) * KS);
+    lhs = o; o += al(sizeof(float) * static_cast<size_t>(T) * B * C);
+    // codes used internally when the caller keeps no checkpoints
+    xq = o; o += al(sizeof(float) * static_cast<size_t>(T) * B * I);
+    wih = o; o += al(sizeof(float) * C * I);
+    whh = o; o += al(sizeof(float) * C * H);
+    bih = o; o += al(sizeof(float) * C);
+    bhh = o; o += al(sizeof(float) * C);
+    h0q = o; o += al(sizeof(float) * static_cast<size_t>(B) * H);
+    c0q = o; o += al(sizeof(float) * static_cast<size_t>(B) * H);
+    total = o;
+  }
+};
+
+}  // namespace lstm
+}  // namespace rxmet
+
+using namespace rxmet;
+using namespace rxmet::lstm;
+
+extern "C" {
+
+int64_t rxmet_lstm_forward_workspace_bytes(int32_t T, int32_t B, int32_t I, int32_t H) {
+  if (T < 1 || B < 1 || I < 1 || H < 1) return 0;
+  return static_cast<int64_t>(FwdWorkspace(T, B, I, H).total);
+}
+
+int rxmet_lstm_forward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const float *W_ih,
+                             const float *W_hh, const float *b_ih, const float *b_hh,
+                             const float *x, const float *h0, const float *c0,
+                             const rxmet_lstm_params *params, float *output, float *h_n,
+                             float *c_n, const rxmet_lstm_saved *saved, void *workspace,
+                             void *stream_) {
+  clear_error();
+  RXMET_CHECK_ARG(T >= 1 && B >= 1 && I >= 1 && H >= 1, "dimensions must be positive");
+  RXMET_CHECK_ARG(H % 16 == 0 && H <= kMaxH,
+                  "hidden_size must be a multiple of 16 and at most 512 for the MFMA recurrence");
+  RXMET_CHECK_ARG(W_ih && W_hh && x && params && output && h_n && c_n && workspace,
+                  "required pointer is null");
+  RXMET_CHECK_ARG((h0 == nullptr) == (c0 == nullptr), "h0 and c0 must be given together");
+  RXMET_CHECK_ARG(params->hidden == H, "params hidden size does not match");
+  const bool bias = params->bias_enabled != 0;
+  RXMET_CHECK_ARG(!bias || (b_ih && b_hh), "bias enabled but bias pointers are null");
+  const rxmet_lstm_op_config &whh_t = params->config.op[RXMET_LSTM_W_HH];
+  RXMET_CHECK_ARG(whh_t.bits <= 8, "W_hh wider than 8 bits is not supported by the MFMA recurrence");
+  const rxmet_lstm_op_config &h_t = params->config.op[RXMET_LSTM_OUTPUT];
+  RXMET_CHECK_ARG(h_t.bits <= 16, "output (h) wider than 16 bits is not supported");
+  RXMET_CHECK_ARG(static_cast<double>(T) * B * 4 * H < 4294967295.0,
+                  "T*B*4H too large for 32-bit element offsets");
+  if (saved) {
+    RXMET_CHECK_ARG(saved->x_q && saved->w_ih_q && saved->w_hh_q && saved->h0_q && saved->c0_q &&
+                        saved->x_m && saved->w_ih_m && saved->w_hh_m && saved->h0_m &&
+                        saved->c0_m && saved->gate_out && saved->cell && saved->cell_tanh &&
+                        saved->hidden && saved->ih_linear_m && saved->hh_linear_m &&
+                        saved->gate_in_m && saved->gate_out_m && saved->cell_m &&
+                        saved->cell_tanh_m && saved->hidden_m,
+                    "training forward needs every saved tensor");
+    RXMET_CHECK_ARG(!bias || (saved->b_ih_q && saved->b_hh_q && saved->b_ih_m && saved->b_hh_m),
+                    "training forward with bias needs the saved bias codes and masks");
+  }
+  StepParams sp;
+  ChannelParams cp;
+  if (int rc = derive(*params, &sp, &cp)) return rc;
+  const int C = 4 * H, KS = (H + 63) / 64, UT = H / 16;
+  // exact int32 bound of the input branch and of the recurrent MFMA sum
+  const double xmax = std::ldexp(1.0, params->config.op[RXMET_LSTM_INPUT].bits);
+  const double wmax = std::ldexp(1.0, params->config.op[RXMET_LSTM_W_IH].bits - 1);
+  const bool wide = xmax * wmax * I >= 2147483647.0;
+  RXMET_CHECK_ARG(std::ldexp(1.0, h_t.bits) * 128.0 * H < 2147483647.0,
+                  "recurrent accumulator would overflow int32");
+
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  const FwdWorkspace ws(T, B, I, H);
+  char *wsb = static_cast<char *>(workspace);
+  std::vector<ChanHost> hostc(C);
+  for (int c = 0; c < C; ++c) {
+    ChanHost &h = hostc[c];
+    h.w_ih_s = cp.w_ih_scale[c];
+    h.w_hh_s = cp.w_hh_scale[c];
+    h.b_ih_s = bias ? cp.b_ih_scale[c] : 1.0f;
+    h.b_hh_s = bias ? cp.b_hh_scale[c] : 1.0f;
+    h.ih_mult = cp.ih_acc_to_lin[c].mult;
+    h.ih_shift = cp.ih_acc_to_lin[c].shift;
+    h.hh_mult = cp.hh_acc_to_lin[c].mult;
+    h.hh_shift = cp.hh_acc_to_lin[c].shift;
+    h.ih_bmult = cp.ih_bias_to_acc[c].mult;
+    h.ih_bshift = cp.ih_bias_to_acc[c].shift;
+    h.hh_bmult = cp.hh_bias_to_acc[c].mult;
+    h.hh_bshift = cp.hh_bias_to_acc[c].shift;
+  }
+  ChanHost *chost = reinterpret_cast<ChanHost *>(wsb + ws.chost);
+  ChanRun *run = reinterpret_cast<ChanRun *>(wsb + ws.run);
+  v4i *frag = reinterpret_cast<v4i *>(wsb + ws.frag);
+  float *lhs = reinterpret_cast<float *>(wsb + ws.lhs);
+  RXMET_CHECK_HIP(hipMemcpyAsync(chost, hostc.data(), sizeof(ChanHost) * C, hipMemcpyHostToDevice,
+                                 stream));
+  const rxmet_lstm_saved sv = saved ? *saved : rxmet_lstm_saved{};
+  float *xq = saved ? sv.x_q : reinterpret_cast<float *>(wsb + ws.xq);
+  float *wih = saved ? sv.w_ih_q : reinterpret_cast<float *>(wsb + ws.wih);
+  float *whh = saved ? sv.w_hh_q : reinterpret_cast<float *>(wsb + ws.whh);
+  float *bih = (saved && bias) ? sv.b_ih_q : reinterpret_cast<float *>(wsb + ws.bih);
+  float *bhh = (saved && bias) ? sv.b_hh_q : reinterpret_cast<float *>(wsb + ws.bhh);
+  float *h0q = saved ? sv.h0_q : reinterpret_cast<float *>(wsb + ws.h0q);
+  float *c0q = saved ? sv.c0_q : reinterpret_cast<float *>(wsb + ws.c0q);
+
+  const int npl = h_t.bits <= 8 ? 1 : 2;
+  const float h_offset = (h_t.is_unsigned && h_t.bits < 32) ? std::ldexp(1.0f, h_t.bits - 1) : 0.0f;
+  WeightArgs wa;
+  wa.I = I; wa.H = H; wa.bias = bias ? 1 : 0; wa.npl = npl;
+  wa.W_ih = W_ih; wa.W_hh = W_hh; wa.b_ih = b_ih; wa.b_hh = b_hh; wa.ch = chost;
+  wa.wq_ih = wih; wa.wq_hh = whh; wa.bq_ih = bih; wa.bq_hh = bhh;
+  wa.wm_ih = sv.w_ih_m; wa.wm_hh = sv.w_hh_m; wa.bm_ih = sv.b_ih_m; wa.bm_hh = sv.b_hh_m;
+  wa.run = run;
+  wa.hh_k_factor = static_cast<int32_t>(h_offset) - sp.h.zp + (npl == 2 ? 128 : 0);
+  const rxmet_lstm_op_config *oc = params->config.op;
+  const Grid gwi = grid_of(oc[RXMET_LSTM_W_IH], 1.0f, 0), gwh = grid_of(oc[RXMET_LSTM_W_HH], 1.0f, 0);
+  const Grid gbi = grid_of(oc[RXMET_LSTM_B_IH], 1.0f, 0), gbh = grid_of(oc[RXMET_LSTM_B_HH], 1.0f, 0);
+  {
+    rxmet::prof::Scope ps__("lstm_fwd_quant_weights", stream);
+    hipLaunchKernelGGL(lstm_quant_weights, dim3(C), dim3(64), 0, stream, wa, gwi, gwh, gbi, gbh);
+  }
+  RXMET_CHECK_LAUNCH();
+  const int64_t nx = static_cast<int64_t>(T) * B * I, nh = static_cast<int64_t>(B) * H;
+  int64_t blocks = (nx + nh + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  hipLaunchKernelGGL(lstm_quant_inputs, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
+                     nx, nh, x, h0, c0, sp, xq, sv.x_m, h0q, sv.h0_m, c0q, sv.c0_m);
+  RXMET_CHECK_LAUNCH();
+  hipLaunchKernelGGL(lstm_pack_whh, dim3((C / 16) * KS), dim3(64), 0, stream, H, KS, whh, frag);
+  RXMET_CHECK_LAUNCH();
+  const int M = T * B;
+  {
+    rxmet::prof::Scope ps__("lstm_fwd_input_gemm", stream);
+    const dim3 grid((C + 63) / 64, (M + 63) / 64);
+    if (wide)
+      hipLaunchKernelGGL(lstm_input_gemm<long long>, grid, dim3(256), 0, stream, M, C, I, H, xq,
+                         wih, chost, run, sp, lhs, sv.ih_linear_m);
+    else
+      hipLaunchKernelGGL(lstm_input_gemm<int>, grid, dim3(256), 0, stream, M, C, I, H, xq, wih,
+                         chost, run, sp, lhs, sv.ih_linear_m);
+  }
+  RXMET_CHECK_LAUNCH();
+
+  RecArgs ra;
+  ra.T = T; ra.B = B; ra.H = H; ra.KS = KS; ra.UT = UT; ra.h_offset = h_offset;
+  ra.lhs = lhs; ra.frag = frag; ra.ch = chost; ra.run = run; ra.h0q = h0q; ra.c0q = c0q;
+  ra.output = output; ra.h_n = h_n; ra.c_n = c_n;
+  ra.gate_out = sv.gate_out; ra.cell = sv.cell; ra.cell_tanh = sv.cell_tanh; ra.hidden = sv.hidden;
+  ra.hh_lin_m = sv.hh_linear_m; ra.gate_in_m = sv.gate_in_m; ra.gate_out_m = sv.gate_out_m;
+  ra.cell_m = sv.cell_m; ra.cell_tanh_m = sv.cell_tanh_m; ra.hidden_m = sv.hidden_m;
+  const size_t lds = recurrence_lds(H, KS, npl);
+  const dim3 grid((B + kBT - 1) / kBT), block(64 * ((UT + kTilesPerWave - 1) / kTilesPerWave));
+  {
+    rxmet::prof::Scope ps__("lstm_fwd_recurrence", stream);
+    if (npl == 1) {
+      RXMET_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&lstm_recurrence<1>),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize,
+                                          static_cast<int>(lds)));
+      hipLaunchKernelGGL(lstm_recurrence<1>, grid, block, lds, stream, ra, sp);
+    } else {
+      RXMET_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&lstm_recurrence<2>),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize,
+                                          static_cast<int>(lds)));
+      hipLaunchKernelGGL(lstm_recurrence<2>, grid, block, lds, stream, ra, sp);
+    }
+  }
+  RXMET_CHECK_LAUNCH();
+  return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,239 @@
+"""MI355X replacement of the reference's QuantLSTM native module ``_quant_lstm``
+(``operators/quant-lstm/pytorch/lib/lstm_interface_binding.cc:917-975``) on the QAT path:
+MinMax calibration, parameter finalisation, the quantised forward with its saved state and
+the STE backward.  Every call goes to librxmet.so (``include/rxmet_lstm.h``) on PyTorch's
+current stream; tensors are time-major ``[T, B, *]`` with PyTorch weight layouts and gate
+order (i, f, g, o).
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional
+
+import numpy as np
+import torch
+
+import rxmet_lstm_abi as L
+import rxmet_lib as _rx
+
+_F32 = torch.float32
+
+
+def _dev_f32(name: str, t: torch.Tensor) -> torch.Tensor:
+    if not (t.is_cuda and t.dtype == _F32):
+        raise RuntimeError(f"{name} must be a CUDA float32 tensor")
+    return t.contiguous()
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else t.data_ptr()
+
+
+def _stream(dev) -> int:
+    return _rx.stream_of(dev)
+
+
+def _ws(nbytes: int, dev) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=dev)
+
+
+class LstmQuantParams:
+    """Finalised standard scales / zero points of one direction (LstmQuantParams,
+    include/lstm/quant_params.h), wrapping the C struct with owned channel arrays."""
+
+    def __init__(self, hidden: int):
+        self.hidden = int(hidden)
+        self._p = L.new_params(self.hidden)
+
+    @property
+    def struct(self) -> L.Params:
+        return self._p
+
+    @property
+    def bias_enabled(self) -> bool:
+        return bool(self._p.bias_enabled)
+
+    def scale(self, name: str) -> float:
+        return float(self._p.scale[L.OP[name]])
+
+    def zero_point(self, name: str) -> int:
+        return int(self._p.zero_point[L.OP[name]])
+
+    def channel_scales(self, name: str) -> np.ndarray:
+        return L.chan_scales(self._p, L.PARAM_OPS.index(name)).copy()
+
+    def to_dict(self) -> dict:
+        d = {"hidden": self.hidden, "bias_enabled": self.bias_enabled,
+             "scale_mode": int(self._p.config.scale_mode), "operators": {}}
+        for i, n in enumerate(L.OP_NAMES):
+            t = self._p.config.op[i]
+            e = {"bits": int(t.bits), "is_unsigned": bool(t.is_unsigned),
+                 "is_symmetric": bool(t.is_symmetric), "granularity": int(t.granularity)}
+            if n in L.PARAM_OPS:
+                e["scale"] = [float(v) for v in self.channel_scales(n)]
+                e["zero_point"] = 0
+            else:
+                e["scale"] = self.scale(n)
+                e["zero_point"] = self.zero_point(n)
+            d["operators"][n] = e
+        return d
+
+    @classmethod
+    def from_dict(cls, d: dict) -> "LstmQuantParams":
+        p = cls(int(d["hidden"]))
+        s = p._p
+        s.bias_enabled = int(bool(d["bias_enabled"]))
+        s.config.scale_mode = int(d["scale_mode"])
+        for i, n in enumerate(L.OP_NAMES):
+            e = d["operators"][n]
+            s.config.op[i] = L.OpConfig(int(e["bits"]), int(e["is_unsigned"]),
+                                        int(e["is_symmetric"]), int(e["granularity"]))
+            if n in L.PARAM_OPS:
+                L.chan_scales(s, L.PARAM_OPS.index(n))[:] = np.asarray(e["scale"], np.float32)
+            else:
+                s.scale[i] = float(e["scale"])
+                s.zero_point[i] = int(e["zero_point"])
+        return p
+
+
+def new_stats(hidden: int, device) -> torch.Tensor:
+    """Empty MinMax statistics (layout of rxmet_lstm_stats_size) on ``device``."""
+    return torch.from_numpy(L.empty_stats(hidden)).to(device)
+
+
+def forward_calibrate(x, W_ih, W_hh, b_ih, b_hh, h0, c0, stats: torch.Tensor):
+    """Float forward + MinMax statistics merged into ``stats`` (CalibrationSession.collect).
+    Returns (output [T,B,H], h_n [B,H], c_n [B,H])."""
+    T, B, I = x.shape
+    H = W_hh.shape[1]
+    x, W_ih, W_hh = (_dev_f32(n, t) for n, t in (("x", x), ("weight_ih", W_ih), ("weight_hh", W_hh)))
+    b_ih = _dev_f32("bias_ih", b_ih) if b_ih is not None else None
+    b_hh = _dev_f32("bias_hh", b_hh) if b_hh is not None else None
+    h0 = _dev_f32("h0", h0) if h0 is not None else None
+    c0 = _dev_f32("c0", c0) if c0 is not None else None
+    dev = x.device
+    out = torch.empty((T, B, H), dtype=_F32, device=dev)
+    hn = torch.empty((B, H), dtype=_F32, device=dev)
+    cn = torch.empty((B, H), dtype=_F32, device=dev)
+    ws = _ws(_rx.load().rxmet_lstm_calibrate_workspace_bytes(T, B, I, H), dev)
+    _rx.call("rxmet_lstm_forward_calibrate", T, B, I, H, _ptr(W_ih), _ptr(W_hh), _ptr(b_ih),
+             _ptr(b_hh), _ptr(x), _ptr(h0), _ptr(c0), _ptr(out), _ptr(hn), _ptr(cn),
+             _ptr(stats), _ptr(ws), _stream(dev))
+    return out, hn, cn
+
+
+def finalize_params(stats: torch.Tensor, config: L.Config, hidden: int,
+                    bias: bool) -> LstmQuantParams:
+    """MinMax finalisation (LstmCalibrationSession::finalize, src/lstm/calibration.cc:374-427)."""
+    host = stats.detach().cpu().numpy().astype(np.float32)
+    p = LstmQuantParams(hidden)
+    _rx.call("rxmet_lstm_finalize_params", host.ctypes.data_as(ctypes.c_void_p),
+             ctypes.byref(config), hidden, int(bool(bias)), ctypes.byref(p.struct))
+    return p
+
+
+def forward_float(x, W_ih, W_hh, b_ih, b_hh, h0, c0):
+    """Float forward (lstm_forward).  Returns (output, h_n, c_n)."""
+    T, B, I = x.shape
+    H = W_hh.shape[1]
+    x, W_ih, W_hh = (_dev_f32(n, t) for n, t in (("x", x), ("weight_ih", W_ih), ("weight_hh", W_hh)))
+    b_ih = _dev_f32("bias_ih", b_ih) if b_ih is not None else None
+    b_hh = _dev_f32("bias_hh", b_hh) if b_hh is not None else None
+    h0 = _dev_f32("h0", h0) if h0 is not None else None
+    c0 = _dev_f32("c0", c0) if c0 is not None else None
+    dev = x.device
+    out = torch.empty((T, B, H), dtype=_F32, device=dev)
+    hn = torch.empty((B, H), dtype=_F32, device=dev)
+    cn = torch.empty((B, H), dtype=_F32, device=dev)
+    _rx.call("rxmet_lstm_forward_float", T, B, I, H, _ptr(W_ih), _ptr(W_hh), _ptr(b_ih),
+             _ptr(b_hh), _ptr(x), _ptr(h0), _ptr(c0), _ptr(out), _ptr(hn), _ptr(cn), _stream(dev))
+    return out, hn, cn
+
+
+def _saved_tensors(T, B, I, H, bias, dev) -> dict:
+    C = 4 * H
+    f = dict(dtype=_F32, device=dev)
+    u = dict(dtype=torch.uint8, device=dev)
+    s = {"x_q": torch.empty((T, B, I), **f), "w_ih_q": torch.empty((C, I), **f),
+         "w_hh_q": torch.empty((C, H), **f), "h0_q": torch.empty((B, H), **f),
+         "c0_q": torch.empty((B, H), **f), "x_m": torch.empty((T, B, I), **u),
+         "w_ih_m": torch.empty((C, I), **u), "w_hh_m": torch.empty((C, H), **u),
+         "h0_m": torch.empty((B, H), **u), "c0_m": torch.empty((B, H), **u),
+         "gate_out": torch.empty((T, B, C), **f), "cell": torch.empty((T, B, H), **f),
+         "cell_tanh": torch.empty((T, B, H), **f), "hidden": torch.empty((T, B, H), **f)}
+    for k in ("ih_linear_m", "hh_linear_m", "gate_in_m", "gate_out_m"):
+        s[k] = torch.empty((T, B, C), **u)
+    for k in ("cell_m", "cell_tanh_m", "hidden_m"):
+        s[k] = torch.empty((T, B, H), **u)
+    if bias:
+        s["b_ih_q"] = torch.empty((C,), **f)
+        s["b_hh_q"] = torch.empty((C,), **f)
+        s["b_ih_m"] = torch.empty((C,), **u)
+        s["b_hh_m"] = torch.empty((C,), **u)
+    return s
+
+
+def _saved_struct(saved: dict) -> L.Saved:
+    s = L.Saved()
+    for k in L.SAVED_FIELDS:
+        t = saved.get(k)
+        setattr(s, k, None if t is None else t.data_ptr())
+    return s
+
+
+def forward_quant(x, W_ih, W_hh, b_ih, b_hh, h0, c0, params: LstmQuantParams,
+                  save_checkpoints: bool):
+    """Quantised FP32-carrier forward (lstm_forward_quantized).  Returns (output, h_n, c_n,
+    saved) where ``saved`` holds the masters, checkpoints and clamp masks (1 = clamped) when
+    ``save_checkpoints`` is set, else None."""
+    T, B, I = x.shape
+    H = W_hh.shape[1]
+    x, W_ih, W_hh = (_dev_f32(n, t) for n, t in (("x", x), ("weight_ih", W_ih), ("weight_hh", W_hh)))
+    bias = params.bias_enabled
+    if bias and (b_ih is None or b_hh is None):
+        raise RuntimeError("quant params enable bias but the module has no bias")
+    b_ih = _dev_f32("bias_ih", b_ih) if bias else None
+    b_hh = _dev_f32("bias_hh", b_hh) if bias else None
+    h0 = _dev_f32("h0", h0) if h0 is not None else None
+    c0 = _dev_f32("c0", c0) if c0 is not None else None
+    dev = x.device
+    out = torch.empty((T, B, H), dtype=_F32, device=dev)
+    hn = torch.empty((B, H), dtype=_F32, device=dev)
+    cn = torch.empty((B, H), dtype=_F32, device=dev)
+    saved = _saved_tensors(T, B, I, H, bias, dev) if save_checkpoints else None
+    sv = _saved_struct(saved) if saved is not None else None
+    ws = _ws(_rx.load().rxmet_lstm_forward_workspace_bytes(T, B, I, H), dev)
+    _rx.call("rxmet_lstm_forward_quant", T, B, I, H, _ptr(W_ih), _ptr(W_hh), _ptr(b_ih),
+             _ptr(b_hh), _ptr(x), _ptr(h0), _ptr(c0), ctypes.byref(params.struct), _ptr(out),
+             _ptr(hn), _ptr(cn), ctypes.byref(sv) if sv is not None else None, _ptr(ws),
+             _stream(dev))
+    return out, hn, cn, saved
+
+
+def backward_quant(saved: dict, params: LstmQuantParams, grad_output, grad_h_n=None,
+                   grad_c_n=None):
+    """STE backward (lstm_backward_qat).  grad_output [T,B,H] time-major.  Returns
+    (dx, dW_ih, dW_hh, db_ih, db_hh, dh0, dc0); bias grads are None without bias."""
+    T, B, I = saved["x_q"].shape
+    H = saved["h0_q"].shape[1]
+    C = 4 * H
+    dev = saved["x_q"].device
+    grad_output = _dev_f32("grad_output", grad_output)
+    grad_h_n = _dev_f32("grad_h_n", grad_h_n) if grad_h_n is not None else None
+    grad_c_n = _dev_f32("grad_c_n", grad_c_n) if grad_c_n is not None else None
+    f = dict(dtype=_F32, device=dev)
+    dx = torch.empty((T, B, I), **f)
+    dwi = torch.empty((C, I), **f)
+    dwh = torch.empty((C, H), **f)
+    bias = params.bias_enabled
+    dbi = torch.empty((C,), **f) if bias else None
+    dbh = torch.empty((C,), **f) if bias else None
+    dh0 = torch.empty((B, H), **f)
+    dc0 = torch.empty((B, H), **f)
+    sv = _saved_struct(saved)
+    ws = _ws(_rx.load().rxmet_lstm_backward_workspace_bytes(T, B, I, H), dev)
+    _rx.call("rxmet_lstm_backward_quant", T, B, I, H, ctypes.byref(params.struct),
+             ctypes.byref(sv), _ptr(grad_output), _ptr(grad_h_n), _ptr(grad_c_n), _ptr(dx),
+             _ptr(dwi), _ptr(dwh), _ptr(dbi), _ptr(dbh), _ptr(dh0), _ptr(dc0), _ptr(ws),
+             _stream(dev))
+    return dx, dwi, dwh, dbi, dbh, dh0, dc0
