@@ -3,6 +3,8 @@
 Prints ONE JSON line.  Legs:
 * gru  — QuantGRU bidirectional QAT forward+backward at config c3
          (B=256, T=200, I=80, H=256): seq/s, the headline ``value``;
+* lstm — QuantLSTM unidirectional QAT forward+backward at config c4 (B=512, T=100, I=64,
+         H=512, 8-bit per-channel weights, 8-bit gates, 16-bit cell, 8-bit h): seq/s;
 * qdq  — AIMET QuantizeDequantize forward+backward at config c2 ([8192, 8192] fp32,
          learnable min/max encodings, 8-bit asymmetric per-tensor and 4-bit symmetric
          per-channel): algorithmic HBM GB/s.
@@ -218,6 +220,126 @@ def _gru_leg(torch, steps: int, warmup: int):
     return res, roof, m, x
 
 
+def _lstm_kernel_work(B, T, I, H):
+    C = 4 * H
+    M = T * B
+    return {
+        "lstm_fwd_recurrence": (2.0 * M * H * C, INT8_MFMA_PEAK,
+                                "recurrent GEMM W_hh_q.h_q over T steps (int8 MFMA) with the "
+                                "fused gate / cell / hidden fake-quant"),
+        "lstm_bwd_recurrence": (2.0 * M * H * C, INT8_MFMA_PEAK,
+                                "dh GEMM W_hh_q^T.dgates over T steps (int8 MFMA, 3 planes of "
+                                "22-bit block fixed point) with the fused STE pointwise"),
+        "lstm_bwd_weight_gemms": (2.0 * M * C * (2 * I + H), FP32_MFMA_PEAK,
+                                  "dx, dW_ih, dW_hh fp32 GEMMs (rocBLAS)"),
+        "lstm_fwd_input_gemm": (2.0 * M * C * I, FP32_MFMA_PEAK,
+                                "input linear W_ih_q.x_q exact integer GEMM"),
+    }
+
+
+def _timed_steps(torch, step, steps, warmup, work):
+    """Run warmup + timed steps; per-step events, per-kernel library timings, roofline of the
+    dominant instrumented kernel."""
+    import rxmet_lib
+
+    dev = torch.device("cuda:0")
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    rxmet_lib.prof_reset()
+    rxmet_lib.prof_enable(True)
+    t0 = time.perf_counter()
+    evs[0].record(stream)
+    for i in range(steps):
+        step()
+        evs[i + 1].record(stream)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    rxmet_lib.prof_enable(False)
+    per = sorted(evs[i].elapsed_time(evs[i + 1]) for i in range(steps))
+    p50 = per[len(per) // 2]
+    p95 = per[min(len(per) - 1, int(0.95 * len(per)))]
+    kernels = {}
+    for name in rxmet_lib.prof_names():
+        ms, n = rxmet_lib.prof_query(name)
+        if n == 0:
+            continue
+        kernels[name] = {"ms_per_step": ms / steps, "launches_per_step": n / steps,
+                         "us_per_launch": ms / max(n, 1) * 1e3}
+    dom = max((k for k in kernels if k in work), key=lambda k: kernels[k]["ms_per_step"])
+    flops, peak, what = work[dom]
+    achieved = flops / (kernels[dom]["us_per_launch"] * 1e-6) / 1e12
+    roof = {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 3), "peak": peak,
+            "unit": "TFLOP/s", "frac": round(achieved / peak, 6), "traffic": None,
+            "algorithmic_flops_per_launch": flops, "work": what,
+            "us_per_launch": round(kernels[dom]["us_per_launch"], 2)}
+    return dt, p50, p95, kernels, roof
+
+
+def _lstm_leg(torch, steps: int, warmup: int):
+    """c4: QuantLSTM unidirectional QAT fwd+bwd, B=512, T=100, I=64, H=512."""
+    import quant_lstm as QL
+
+    dev = torch.device("cuda:0")
+    B, T, I, H = 512, 100, 64, 512
+    torch.manual_seed(7)
+    x = torch.rand(T, B, I) * 2 - 1
+    torch.manual_seed(8)
+    g = torch.randn(T, B, H) * 0.1
+    m = QL.QuantLSTM(I, H, quant_config={"schema_version": 1,
+                                         "operators": {"cell_state": {"bitwidth": 16}}})
+    m = m.to(dev)
+    x, g = x.to(dev), g.to(dev)
+    m.calibrating = True
+    with torch.no_grad():
+        m(x)
+    m.calibrating = False
+    m.finalize_calibration()
+    m.use_quantization = True
+    m.train()
+
+    def step():
+        m.zero_grad(set_to_none=True)
+        out, _ = m(x)
+        out.backward(g)
+
+    dt, p50, p95, kernels, roof = _timed_steps(torch, step, steps, warmup,
+                                               _lstm_kernel_work(B, T, I, H))
+    total = sum(k["ms_per_step"] for k in kernels.values())
+    _log(f"lstm c4: {dt*1e3:.2f} ms/step wall, P50 {p50:.2f} ms P95 {p95:.2f} ms, "
+         f"{B/dt:.1f} seq/s; instrumented kernels {total:.2f} ms/step")
+    for k, v in sorted(kernels.items(), key=lambda kv: -kv[1]["ms_per_step"]):
+        _log(f"  {k}: {v['ms_per_step']:.3f} ms/step, {v['us_per_launch']:.1f} us/launch")
+    res = {"ms_per_step": dt * 1e3, "p50_ms": p50, "p95_ms": p95, "seq_per_s": B / dt,
+           "seq_per_s_p50": B / (p50 * 1e-3),
+           "kernels_ms_per_step": {k: round(v["ms_per_step"], 4) for k, v in kernels.items()}}
+    return res, roof, m, x, g
+
+
+def _lstm_cpu_baseline(m, x, g, rows: int = 8):
+    """CPU oracle (C, one thread) on the first `rows` sequences of c4: the q-carrier forward
+    in the reference CPU path's activation semantics (glibc expf/tanhf) plus the STE
+    backward, with the module's own grids."""
+    import lstm_oracle as LO
+
+    xs = x[:, :rows].detach().contiguous().cpu().numpy()
+    gs = g[:, :rows].detach().contiguous().cpu().numpy()
+    Wi, Wh, bi, bh = (p.detach().cpu().numpy() for p in m._direction_params(False))
+    p = m._params[0].struct
+    t0 = time.perf_counter()
+    fwd = LO.forward_quant(Wi, Wh, bi, bh, xs, p, mode=LO.ACT_LIBM)
+    t1 = time.perf_counter()
+    LO.backward_quant(fwd, p, gs)
+    dt = time.perf_counter() - t0
+    T, Bs, I = xs.shape
+    return {"value": round(Bs / dt, 3), "unit": "seq/s", "cores": 1, "kind": "port",
+            "sample": f"c4 QAT fwd+bwd on {Bs} of the 512 sequences (T={T}, I={I}, "
+                      f"H={m.hidden_size}), C oracle, one thread, {dt:.1f} s "
+                      f"(forward {t1 - t0:.1f} s)"}
+
+
 def _gru_cpu_baseline(m, x, rows: int = 32):
     """CPU oracle (C, one thread) on the first `rows` sequences of c3: the same QAT
     forward+backward of both directions with the module's own grids."""
@@ -297,11 +419,14 @@ def main() -> int:
     torch.backends.cudnn.allow_tf32 = False
     _log(f"device: {torch.cuda.get_device_name(0)}")
     gru, roof, m, x = _gru_leg(torch, args.steps, args.warmup)
+    lstm, lstm_roof, lm, lx, lg = _lstm_leg(torch, args.steps, args.warmup)
     qdq, qdq_roof = _qdq_leg(torch, args.steps, args.warmup)
-    cpu = cpu_qdq = None
+    cpu = cpu_qdq = cpu_lstm = None
     if not args.no_cpu_baseline:
         cpu = _gru_cpu_baseline(m, x)
         _log(f"cpu baseline: {cpu}")
+        cpu_lstm = _lstm_cpu_baseline(lm, lx, lg)
+        _log(f"lstm cpu baseline: {cpu_lstm}")
         cpu_qdq = _qdq_cpu_baseline()
     line = {
         "metric": METRIC,
@@ -323,10 +448,13 @@ def main() -> int:
                    "batch": 256, "seq_len": 200, "input_size": 80, "hidden_size": 256,
                    "carrier": "fp32 codes; recurrent GEMMs on int8 MFMA"},
         "gru": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in gru.items()},
+        "lstm": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in lstm.items()},
         "qdq": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in qdq.items()},
         "roofline": roof,
+        "lstm_roofline": lstm_roof,
         "qdq_roofline": qdq_roof,
         "cpu_baseline": cpu,
+        "lstm_cpu_baseline": cpu_lstm,
         "qdq_cpu_baseline": cpu_qdq,
     }
     print(json.dumps(line), flush=True)

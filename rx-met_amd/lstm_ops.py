@@ -132,6 +132,20 @@ def finalize_params(stats: torch.Tensor, config: L.Config, hidden: int,
     return p
 
 
+def check_params(params: LstmQuantParams, input_size: int) -> None:
+    """Validate ``params`` by deriving its integer execution encodings on the host
+    (rxmet_lstm_derive_exec); raises RxmetError for an inconsistent set."""
+    C = 4 * params.hidden
+    acc = (L.Rescale * (2 * C))()
+    bias = (L.Rescale * (2 * C))()
+    gate = (L.Rescale * 8)()
+    cell = (L.Q31 * 2)()
+    hid = (L.Rescale * 1)()
+    _rx.call("rxmet_lstm_derive_exec", ctypes.byref(params.struct), int(input_size),
+             ctypes.addressof(acc), ctypes.addressof(bias), ctypes.addressof(gate),
+             ctypes.addressof(cell), ctypes.addressof(hid))
+
+
 def forward_float(x, W_ih, W_hh, b_ih, b_hh, h0, c0):
     """Float forward (lstm_forward).  Returns (output, h_n, c_n)."""
     T, B, I = x.shape
