@@ -27,7 +27,11 @@
  * the reference's float op order (the reference CPU semantics, pinned against the
  * reference compiled into oracle/_ref); ACT_CR evaluates exp and tanh in double and rounds
  * once to float (correctly rounded apart from double-rounding ties), keeping the same float
- * op order around them.  The GPU kernels implement ACT_CR.
+ * op order around them, and sums each linear's centred integer products exactly (one
+ * rounding to float at the end) instead of accumulating them in float in index order.  The
+ * two sums agree while every partial sum stays below 2^24 (all 8-bit h configurations); past
+ * that the reference's own result depends on its GEMM's summation order.  The GPU kernels
+ * implement ACT_CR.
  *
  * Pinning (tests/test_lstm_oracle.py): the reference's golden vectors
  * (the JSON files in tests/golden/lstm, copied data from the reference tests/golden/spec) for
@@ -76,6 +80,20 @@ static float clamp_carrier(double v, int32_t lo, int32_t hi) {
   return v <= (double)l ? l : (v >= (double)h ? h : (float)v);
 }
 static float center(float v, int32_t zp) { return (float)((double)v - zp); }
+
+/* Sum of w[k] * (x[k] - zx) over k: in float in index order, as linearValue
+ * (forward_quantized_fp_cpu.cc:20-45) does, for ACT_LIBM; exactly in 64-bit integers and
+ * rounded once to float for ACT_CR (the codes are integers, so every product is exact). */
+static float linear_sum(const float *w, const float *x, int32_t zx, int K, int mode) {
+  if (mode == ACT_CR) {
+    int64_t s = 0;
+    for (int k = 0; k < K; ++k) s += (int64_t)w[k] * ((int64_t)x[k] - zx);
+    return (float)s;
+  }
+  float acc = 0.0f;
+  for (int k = 0; k < K; ++k) acc += center(w[k], 0) * center(x[k], zx);
+  return acc;
+}
 
 /* ------------------------------------------------------------------------------ */
 /* Calibration (scale_encoding.cc, quant_params.cc)                                */
@@ -457,14 +475,12 @@ int olstm_forward_quant(int T, int B, int I, int H, const float *W_ih, const flo
       for (int c = 0; c < C; ++c) {
         const int g = c / H;
         /* linearValue (forward_quantized_fp_cpu.cc:20-45) */
-        float acc = 0.0f;
-        for (int k = 0; k < I; ++k) acc += center(wiq[(size_t)c * I + k], 0) * center(xr[k], zx);
+        float acc = linear_sum(wiq + (size_t)c * I, xr, zx, I, mode);
         if (p->bias_enabled) acc += apply_rescale(center(biq[c], 0), &bias_to_acc[c]);
         uint8_t m_il, m_hl, m_gi, m_go;
         const float lin_ih =
             clamp_point((double)apply_rescale(acc, &acc_to_lin[c]) + zil, &cfg[RXMET_LSTM_IH_LINEAR], &m_il);
-        acc = 0.0f;
-        for (int k = 0; k < H; ++k) acc += center(whq[(size_t)c * H + k], 0) * center(hr[k], zh);
+        acc = linear_sum(whq + (size_t)c * H, hr, zh, H, mode);
         if (p->bias_enabled) acc += apply_rescale(center(bhq[c], 0), &bias_to_acc[C + c]);
         const float lin_hh = clamp_point((double)apply_rescale(acc, &acc_to_lin[C + c]) + zhl,
                                          &cfg[RXMET_LSTM_HH_LINEAR], &m_hl);

@@ -1,0 +1,98 @@
+// cluster.h — workgroup clusters inside one cooperative launch.
+//
+// A persistent recurrence splits one batch tile's hidden units over G workgroups (a cluster).
+// Each step the members exchange the new hidden codes through global memory and meet at a
+// counter in global memory.  The launch is cooperative, so every workgroup is resident; the
+// wait is still bounded: after kSpinLimit polls a member gives up, raises the timeout flag
+// and stops stepping, so every wave of the grid reaches the end of the kernel.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+namespace rxmet {
+namespace cluster {
+
+constexpr unsigned kSpinLimit = 1u << 20;  // about a second of polling
+
+struct Place {
+  int cluster, member;
+};
+
+// Block index -> (cluster, member).  The dispatcher deals workgroups round-robin over the
+// eight XCDs, so members that share blockIdx % 8 share an L2; the mapping keeps a cluster on
+// one XCD when the cluster count is a multiple of 8.  Correctness does not depend on it.
+__device__ __forceinline__ Place place(int G, int nclusters) {
+  const int b = blockIdx.x;
+  if (nclusters % 8 == 0) {
+    const int xcd = b % 8, slot = b / 8;
+    return {xcd + 8 * (slot / G), slot % G};
+  }
+  return {b / G, b % G};
+}
+
+// Cluster barrier.  Every thread of the workgroup calls it after its stores of exchanged data;
+// the counter counts arrivals monotonically, so `arrivals` is G times the barrier's ordinal.
+// Returns false when the wait timed out (the caller then stops stepping).
+//
+// Exchanged data must be written with store_coherent and read with load_coherent (agent-scope
+// atomic accesses, which bypass the non-coherent caches).  Arrival waits for the wave's own
+// stores to complete before the workgroup barrier, so every exchanged store of the workgroup
+// is complete before thread 0 increments the counter; a member that has seen the count reach
+// `arrivals` then reads the new values from the coherence point.  No L2 writeback or
+// invalidation is needed, because nothing exchanged lives in a non-coherent cache line.
+__device__ __forceinline__ bool sync(unsigned *counter, unsigned arrivals, int *timeout) {
+  __shared__ int ok;
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    int good = 1;
+    unsigned spins = 0;
+    while (__hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < arrivals) {
+      __builtin_amdgcn_s_sleep(1);
+      if (++spins > kSpinLimit) {
+        good = 0;
+        __hip_atomic_store(timeout, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+    }
+    ok = good;
+  }
+  __syncthreads();
+  return ok != 0;
+}
+
+__device__ __forceinline__ void store_coherent(unsigned *p, unsigned v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// 16 bytes at a 16-byte aligned address, as two coherent 8-byte loads.
+__device__ __forceinline__ int4 load_coherent16(const void *p) {
+  const unsigned long long *q = static_cast<const unsigned long long *>(p);
+  const unsigned long long a = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const unsigned long long b = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return make_int4(static_cast<int>(a), static_cast<int>(a >> 32), static_cast<int>(b),
+                   static_cast<int>(b >> 32));
+}
+
+// Store one byte per lane as packed 32-bit words: lanes 4k..4k+3 (which hold consecutive
+// bytes of the destination) combine into lane 4k, which writes the word at `dst4` (the
+// address of lane 4k's byte; lanes 4k+1..3 pass an ignored pointer).
+__device__ __forceinline__ void store_bytes_coherent(unsigned char *dst4, int byte) {
+  const int lane = threadIdx.x % 64;
+  byte &= 255;
+  const int b1 = __shfl_down(byte, 1, 64), b2 = __shfl_down(byte, 2, 64),
+            b3 = __shfl_down(byte, 3, 64);
+  if ((lane & 3) == 0)
+    store_coherent(reinterpret_cast<unsigned *>(dst4),
+                   static_cast<unsigned>(byte | (b1 << 8) | (b2 << 16) | (b3 << 24)));
+}
+
+// Zero `n` words (counters and flags) on the stream; used instead of a memset node so the
+// sequence stays capturable.
+static __global__ void zero_words(unsigned *p, int n) {
+  for (int i = threadIdx.x; i < n; i += blockDim.x) p[i] = 0u;
+}
+
+}  // namespace cluster
+}  // namespace rxmet

@@ -15,17 +15,24 @@
 //   4. lstm_input_gemm    : the input linear of all T steps as an exact integer GEMM with
 //      the whole input branch fused in its epilogue (bias, rescale, clamp + mask, and the
 //      rescale to each gate-input grid), so the recurrence only adds the recurrent branch;
-//   5. lstm_recurrence    : one persistent workgroup per 16 sequences walks the T steps.  h
-//      codes live in LDS as int8 planes, the recurrent linear is v_mfma_i32_16x16x64_i8 on
-//      W_hh fragments streamed from L2, and the four gates, real sigmoid/tanh, cell and
-//      hidden fusion, every clamp mask and the checkpoints are computed in registers; the
-//      cell state stays in LDS, each entry owned by one lane.
+//   5. lstm_recurrence_cl : (H a multiple of 64) a cluster of H/64 workgroups per 16-sequence
+//      batch tile in one cooperative launch.  Each member keeps the W_hh fragments of its 64
+//      units resident in LDS, computes the recurrent linear on v_mfma_i32_16x16x64_i8, the
+//      gates through precomputed activation tables (exact: the activation is a function of
+//      the integer gate-input code), the cell and hidden update, every clamp mask and the
+//      checkpoints; the new h codes are exchanged through global memory and the members meet
+//      at a counter barrier once per step (cluster.h);
+//   5'. lstm_recurrence   : otherwise, one persistent workgroup per 16 sequences walks the T
+//      steps with h in LDS and W_hh fragments streamed from L2.
 //
 // Activations: sigmoid keeps the reference's float op order around exp, with exp and tanh
 // evaluated in double and rounded once to float.
 #include <cmath>
+#include <cstdlib>
+#include <type_traits>
 #include <vector>
 
+#include "cluster.h"
 #include "lstm_internal.h"
 #include "mfma_frag.h"
 #include "rxmet_common.h"
@@ -434,13 +441,300 @@ __global__ __launch_bounds__(512) void lstm_recurrence(RecArgs a, StepParams sp)
   }
 }
 
+// ---------------------------------------------------------------------------------
+// 5b. clustered recurrence: a batch tile's units split over G = H / 64 workgroups
+// ---------------------------------------------------------------------------------
+// Member m of a cluster owns units [64 m, 64 m + 64) for all four gates and keeps their W_hh
+// fragments (256 channels x H int8) resident in LDS for the whole launch.  Wave w computes
+// unit tile w % 4 for the gate pair w / 4 (i, f or g, o) over the full K; the gate outputs
+// meet in LDS and each wave then finishes the cell and hidden update of two of the lane's
+// four rows.  The new h codes go to a global exchange buffer, double-buffered by step
+// parity, and the members meet at a cluster barrier once per step.
+constexpr int kClUnits = 64;
+constexpr int kLutMaxEntries = 4096;  // activation tables kept in LDS up to 16 KB each
+
+// The real activation of a gate is a function of the gate-input code alone, and the cell's
+// tanh a function of the cell code: on grids of at most kLutMaxEntries codes the clustered
+// recurrence reads precomputed results (same device function, evaluated once per code).
+// Entry = (output code - output grid lo) << 1 | clamp mask.
+struct ActLut {
+  const uint32_t *table;  // gate tables [off[g] .. off[g] + n[g]), then the tanh table
+  int off[4], n[4];       // n = 0: no gate tables (computed in place)
+  int tanh_off, tanh_n;   // tanh_n = 0: computed in place
+  int total;
+};
+
+__global__ __launch_bounds__(256) void lstm_build_act_lut(StepParams sp, ActLut lut,
+                                                          uint32_t *table) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= lut.total) return;
+  uint8_t m;
+  float v;
+  int lo;
+  if (lut.tanh_n > 0 && i >= lut.tanh_off) {
+    v = real_act(static_cast<float>(sp.c.lo + (i - lut.tanh_off)), sp.c, sp.tanh_c, true, m);
+    lo = sp.tanh_c.lo;
+  } else {
+    int g = 0;
+    while (g < 3 && i >= lut.off[g + 1]) ++g;
+    v = real_act(static_cast<float>(sp.gin[g].lo + (i - lut.off[g])), sp.gin[g], sp.gout[g],
+                 g == 2, m);
+    lo = sp.gout[g].lo;
+  }
+  table[i] = (static_cast<uint32_t>(static_cast<int>(v) - lo) << 1) | m;
+}
+
+// Float-domain forms of clamp_grid / center / dequant for grids whose codes lie within
+// +-2^24 (at most 24 bits): every in-range sum or difference of integer-valued floats is then
+// exact in float, a rounded out-of-range sum stays beyond the same endpoint, and the product
+// of a code difference and a float scale is exact in double, so its float rounding equals the
+// fp32 product.  The results equal the double-domain forms bit for bit.
+__device__ __forceinline__ float clamp_grid_f(float v, const Grid &g, uint8_t &clamped) {
+  const float s = v + static_cast<float>(g.zp);
+  clamped = (s < g.flo || s > g.fhi) ? 1 : 0;
+  return s <= g.flo ? g.flo : (s >= g.fhi ? g.fhi : s);
+}
+
+__device__ __forceinline__ float center_f(float v, int32_t zp) { return v - static_cast<float>(zp); }
+
+__device__ __forceinline__ float dequant_f(float q, float s, int32_t zp) {
+  return (q - static_cast<float>(zp)) * s;
+}
+
+inline bool fits_f32(const Grid &g) { return g.lo > -(1 << 24) && g.hi < (1 << 24); }
+
+__device__ __forceinline__ float lut_code(const uint32_t *t, int idx, int out_lo, uint8_t &m) {
+  const uint32_t e = t[idx];
+  m = static_cast<uint8_t>(e & 1u);
+  return static_cast<float>(static_cast<int>(e >> 1) + out_lo);
+}
+
+struct ClusterArgs {
+  int ncl, G, ntiles, Bpad;
+  int8_t *hx;          // [2][NPL][Bpad][H] centred h codes as int8 planes
+  unsigned *counters;  // [ncl] barrier arrivals
+  int *timeout;        // set by a member whose barrier wait gave up
+  ActLut lut;
+};
+
+template <int NPL>
+__global__ __launch_bounds__(512) void lstm_recurrence_cl(RecArgs a, StepParams sp,
+                                                          ClusterArgs cl) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int H = a.H, C = 4 * H, B = a.B, KS = a.KS;
+  v4i *wl = reinterpret_cast<v4i *>(smem);                  // [4 gates][4 tiles][KS][64]
+  float *xg = reinterpret_cast<float *>(wl + 16 * KS * 64);  // [4 tiles][4 gates][16][16]
+  uint32_t *lut = reinterpret_cast<uint32_t *>(xg + 4 * 4 * 16 * 16);  // [cl.lut.total]
+  for (int i = threadIdx.x; i < cl.lut.total; i += blockDim.x) lut[i] = cl.lut.table[i];
+  const bool gate_lut = cl.lut.n[0] > 0, tanh_lut = cl.lut.tanh_n > 0;
+  const int tid = threadIdx.x, w = tid / 64, l = tid % 64;
+  const int ut = w & 3, gp = w >> 2;
+  const cluster::Place pl = cluster::place(cl.G, cl.ncl);
+  const int u0 = pl.member * kClUnits;
+  const int j = u0 + 16 * ut + l % 16;
+  const int nrow0 = 4 * (l / 16);
+  for (int i = tid; i < 16 * KS * 64; i += blockDim.x) {
+    const int lane = i % 64, rest = i / 64, s = rest % KS, gt = rest / KS;
+    const int ct = (gt / 4) * a.UT + u0 / 16 + gt % 4;
+    wl[i] = a.frag[(static_cast<size_t>(ct) * KS + s) * 64 + lane];
+  }
+  float4 cc[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int c = (2 * gp + q) * H + j;
+    const ChanRun r = a.run[c];
+    const ChanHost h = a.ch[c];
+    cc[q] = make_float4(h.hh_mult, r.hh_bacc, __int_as_float(r.hh_k), __int_as_float(h.hh_shift));
+  }
+  unsigned *counter = cl.counters + pl.cluster;
+  unsigned epoch = 0;
+  bool alive = true;
+  const bool train = a.hidden != nullptr;
+  const size_t plane_stride = static_cast<size_t>(cl.Bpad) * H;
+
+  for (int tile = pl.cluster; tile < cl.ntiles && alive; tile += cl.ncl) {
+    const int b0 = tile * 16;
+    float cst[2];
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) {
+      const int b = b0 + nrow0 + 2 * gp + rr;
+      const float q = b < B ? a.h0q[static_cast<size_t>(b) * H + j] : static_cast<float>(sp.h.zp);
+      const int hc = static_cast<int>(q - a.h_offset);
+      unsigned char *dst = reinterpret_cast<unsigned char *>(cl.hx) + static_cast<size_t>(b) * H + j;
+#pragma unroll
+      for (int p = 0; p < NPL; ++p)
+        cluster::store_bytes_coherent(dst + p * plane_stride,
+                                      NPL == 1 ? hc : (p == 0 ? (hc & 255) - 128 : hc >> 8));
+      cst[rr] = b < B ? a.c0q[static_cast<size_t>(b) * H + j] : static_cast<float>(sp.c.zp);
+    }
+    // input branch of my two gates for my four rows, loaded one step ahead
+    float lh[2][4];
+    auto load_lhs = [&](int t) {
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int b = b0 + nrow0 + r;
+          lh[q][r] = b < B ? a.lhs[(static_cast<size_t>(t) * B + b) * C + (2 * gp + q) * H + j]
+                           : 0.0f;
+        }
+    };
+    load_lhs(0);
+    alive = cluster::sync(counter, ++epoch * cl.G, cl.timeout);
+
+    for (int t = 0; t < a.T && alive; ++t) {
+      const int par = t & 1;
+      const int8_t *hin = cl.hx + static_cast<size_t>(par) * NPL * plane_stride;
+      int8_t *hout = cl.hx + static_cast<size_t>(par ^ 1) * NPL * plane_stride;
+      v4i acc[2][NPL];
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+#pragma unroll
+        for (int p = 0; p < NPL; ++p) acc[q][p] = v4i{0, 0, 0, 0};
+      const int8_t *hrow = hin + static_cast<size_t>(b0 + l % 16) * H + 16 * (l / 16);
+      {
+        // all of the step's h fragments in flight at once (KS <= 8)
+        v4i hfr[8][NPL];
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+#pragma unroll
+          for (int p = 0; p < NPL; ++p)
+            if (s < KS) {
+              const int4 v = cluster::load_coherent16(hrow + p * plane_stride + 64 * s);
+              hfr[s][p] = v4i{v.x, v.y, v.z, v.w};
+            }
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+          if (s < KS) {
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+              const v4i bf = wl[(((2 * gp + q) * 4 + ut) * KS + s) * 64 + l];
+#pragma unroll
+              for (int p = 0; p < NPL; ++p) acc[q][p] = mfma_i8(hfr[s][p], bf, acc[q][p]);
+            }
+          }
+        }
+      }
+      // gate phase: two gates x four rows; the gate pair is a compile-time constant so the
+      // per-gate parameters are static kernel-argument reads
+      auto gate_phase = [&](auto gpc) {
+        constexpr int GP = decltype(gpc)::value;
+#pragma unroll 1
+        for (int r = 0; r < 4; ++r) {
+          const int nr = nrow0 + r, b = b0 + nr;
+          const bool valid = b < B;
+          const uint32_t oc = (static_cast<uint32_t>(t) * B + b) * static_cast<uint32_t>(C) + j;
+#pragma unroll
+          for (int q = 0; q < 2; ++q) {
+            constexpr int g0 = 2 * GP;
+            const int g = g0 + q;
+            const Grid &gin = q == 0 ? sp.gin[g0] : sp.gin[g0 + 1];
+            const Grid &gout = q == 0 ? sp.gout[g0] : sp.gout[g0 + 1];
+            const Rescale &h2g = q == 0 ? sp.hh_to_gate[g0] : sp.hh_to_gate[g0 + 1];
+            int v = pick(acc[q][0], r);
+            if constexpr (NPL == 2) v += 256 * pick(acc[q][NPL - 1], r);
+            v += __float_as_int(cc[q].z);
+            const float accf = static_cast<float>(v) + cc[q].y;
+            uint8_t m_hl, m_gi, m_go;
+            const float lin = clamp_grid_f(rescale(accf, cc[q].x, __float_as_int(cc[q].w)),
+                                           sp.hh_lin, m_hl);
+            const float rhs = rescale(center_f(lin, sp.hh_lin.zp), h2g.mult, h2g.shift);
+            const float gi = clamp_grid_f(lh[q][r] + rhs, gin, m_gi);
+            const float go =
+                gate_lut ? lut_code(lut + (q == 0 ? cl.lut.off[g0] : cl.lut.off[g0 + 1]),
+                                    static_cast<int>(gi) - gin.lo, gout.lo, m_go)
+                         : real_act(gi, gin, gout, g == 2, m_go);
+            xg[((ut * 4 + g) * 16 + nr) * 16 + l % 16] = go;
+            if (train && valid) {
+              a.gate_out[oc + g * H] = go;
+              a.hh_lin_m[oc + g * H] = m_hl;
+              a.gate_in_m[oc + g * H] = m_gi;
+              a.gate_out_m[oc + g * H] = m_go;
+            }
+          }
+        }
+      };
+      if (gp == 0)
+        gate_phase(std::integral_constant<int, 0>{});
+      else
+        gate_phase(std::integral_constant<int, 1>{});
+      if (t + 1 < a.T) load_lhs(t + 1);
+      __syncthreads();
+      // cell phase: rows 2 gp, 2 gp + 1 of the lane's four
+#pragma unroll
+      for (int rr = 0; rr < 2; ++rr) {
+        const int nr = nrow0 + 2 * gp + rr, b = b0 + nr;
+        float gout[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) gout[g] = xg[((ut * 4 + g) * 16 + nr) * 16 + l % 16];
+        const float pf = center_f(gout[1], sp.gout[1].zp) * center_f(cst[rr], sp.c.zp);
+        const float pi = center_f(gout[0], sp.gout[0].zp) * center_f(gout[2], sp.gout[2].zp);
+        const float sum = cell_scale(pf, sp, 0) + cell_scale(pi, sp, 1);
+        uint8_t m_c, m_t, m_h;
+        const float cn = clamp_grid_f(rintf(sum), sp.c, m_c);
+        cst[rr] = cn;
+        const float ct =
+            tanh_lut ? lut_code(lut + cl.lut.tanh_off, static_cast<int>(cn) - sp.c.lo,
+                                sp.tanh_c.lo, m_t)
+                     : real_act(cn, sp.c, sp.tanh_c, true, m_t);
+        const float raw = center_f(gout[3], sp.gout[3].zp) * center_f(ct, sp.tanh_c.zp);
+        const float hv = clamp_grid_f(rescale(raw, sp.hidden.mult, sp.hidden.shift), sp.h, m_h);
+        if (b < B) {
+          const uint32_t oh = (static_cast<uint32_t>(t) * B + b) * static_cast<uint32_t>(H) + j;
+          a.output[oh] = dequant_f(hv, sp.h.scale, sp.h.zp);
+          if (train) {
+            a.cell[oh] = cn;
+            a.cell_tanh[oh] = ct;
+            a.hidden[oh] = hv;
+            a.cell_m[oh] = m_c;
+            a.cell_tanh_m[oh] = m_t;
+            a.hidden_m[oh] = m_h;
+          }
+          if (t == a.T - 1) {
+            const uint32_t os = static_cast<uint32_t>(b) * H + j;
+            a.h_n[os] = dequant_f(hv, sp.h.scale, sp.h.zp);
+            a.c_n[os] = dequant_f(cn, sp.c.scale, sp.c.zp);
+          }
+        }
+        const int hc = static_cast<int>(hv - a.h_offset);
+        unsigned char *dst = reinterpret_cast<unsigned char *>(hout) + static_cast<size_t>(b) * H + j;
+#pragma unroll
+        for (int p = 0; p < NPL; ++p)
+          cluster::store_bytes_coherent(dst + p * plane_stride,
+                                        NPL == 1 ? hc : (p == 0 ? (hc & 255) - 128 : hc >> 8));
+      }
+      alive = cluster::sync(counter, ++epoch * cl.G, cl.timeout);
+    }
+  }
+}
+
+size_t recurrence_cl_lds(int KS, int lut_entries) {
+  return sizeof(v4i) * 16 * static_cast<size_t>(KS) * 64 + sizeof(float) * 4 * 4 * 16 * 16 +
+         sizeof(uint32_t) * static_cast<size_t>(lut_entries);
+}
+
+// Outputs of a launch whose cluster wait timed out are not trustworthy: overwrite them with NaN.
+__global__ __launch_bounds__(256) void lstm_poison_on_timeout(const int *timeout, int64_t n_out,
+                                                              float *output, int64_t n_state,
+                                                              float *h_n, float *c_n) {
+  if (*timeout == 0) return;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n_out; i += stride)
+    output[i] = NAN;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n_state;
+       i += stride) {
+    h_n[i] = NAN;
+    c_n[i] = NAN;
+  }
+}
+
 size_t recurrence_lds(int H, int KS, int npl) {
   return sizeof(float4) * 4 * static_cast<size_t>(H) + sizeof(float) * kBT * static_cast<size_t>(H) +
          static_cast<size_t>(2) * npl * kBT * (KS * 64 + 16);
 }
 
 struct FwdWorkspace {
-  size_t chost, run, frag, lhs, xq, wih, whh, bih, bhh, h0q, c0q, total;
+  size_t chost, run, frag, lhs, xq, wih, whh, bih, bhh, h0q, c0q, hx, sync, lut, total;
   FwdWorkspace(int T, int B, int I, int H) {
     const size_t C = 4 * static_cast<size_t>(H), KS = (H + 63) / 64;
     auto al = [](size_t x) { return (x + 255) & ~static_cast<size_t>(255); };
@@ -457,6 +751,11 @@ struct FwdWorkspace {
     bhh = o; o += al(sizeof(float) * C);
     h0q = o; o += al(sizeof(float) * static_cast<size_t>(B) * H);
     c0q = o; o += al(sizeof(float) * static_cast<size_t>(B) * H);
+    // clustered recurrence: h exchange planes (two parities, up to two planes) and counters
+    const size_t Bpad = (static_cast<size_t>(B) + 15) / 16 * 16;
+    hx = o; o += al(2 * 2 * Bpad * H);
+    sync = o; o += al(sizeof(unsigned) * (Bpad / 16 + 1));
+    lut = o; o += al(sizeof(uint32_t) * 2 * kLutMaxEntries);
     total = o;
   }
 };
@@ -597,6 +896,82 @@ int rxmet_lstm_forward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const f
   ra.gate_out = sv.gate_out; ra.cell = sv.cell; ra.cell_tanh = sv.cell_tanh; ra.hidden = sv.hidden;
   ra.hh_lin_m = sv.hh_linear_m; ra.gate_in_m = sv.gate_in_m; ra.gate_out_m = sv.gate_out_m;
   ra.cell_m = sv.cell_m; ra.cell_tanh_m = sv.cell_tanh_m; ra.hidden_m = sv.hidden_m;
+  bool f32_grids = fits_f32(sp.hh_lin) && fits_f32(sp.c) && fits_f32(sp.tanh_c) && fits_f32(sp.h);
+  for (int g = 0; g < 4; ++g) f32_grids = f32_grids && fits_f32(sp.gin[g]) && fits_f32(sp.gout[g]);
+  if (H % kClUnits == 0 && f32_grids) {
+    // clustered path when the whole grid can be resident at once
+    const void *fn = npl == 1 ? reinterpret_cast<const void *>(&lstm_recurrence_cl<1>)
+                              : reinterpret_cast<const void *>(&lstm_recurrence_cl<2>);
+    ActLut lut{};
+    uint32_t *lut_table = reinterpret_cast<uint32_t *>(wsb + ws.lut);
+    {
+      int dev_lds = 0, dev = 0;
+      RXMET_CHECK_HIP(hipGetDevice(&dev));
+      RXMET_CHECK_HIP(hipDeviceGetAttribute(&dev_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev));
+      // table entries that fit beside the resident weights and the gate exchange
+      const int64_t room = (static_cast<int64_t>(dev_lds) -
+                            static_cast<int64_t>(recurrence_cl_lds(KS, 0))) / 4;
+      int64_t n[4], tot = 0;
+      for (int g = 0; g < 4; ++g) {
+        n[g] = static_cast<int64_t>(sp.gin[g].hi) - sp.gin[g].lo + 1;
+        tot += n[g];
+      }
+      if (tot <= kLutMaxEntries && tot <= room) {
+        for (int g = 0, o = 0; g < 4; ++g) {
+          lut.off[g] = o;
+          lut.n[g] = static_cast<int>(n[g]);
+          o += lut.n[g];
+        }
+        lut.total = static_cast<int>(tot);
+      }
+      const int64_t nc = static_cast<int64_t>(sp.c.hi) - sp.c.lo + 1;
+      if (nc <= kLutMaxEntries && lut.total + nc <= room) {
+        lut.tanh_off = lut.total;
+        lut.tanh_n = static_cast<int>(nc);
+        lut.total += lut.tanh_n;
+      }
+      lut.table = lut_table;
+    }
+    const size_t lds_cl = recurrence_cl_lds(KS, lut.total);
+    int device = 0, ncu = 0, per_cu = 0;
+    RXMET_CHECK_HIP(hipGetDevice(&device));
+    RXMET_CHECK_HIP(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, device));
+    RXMET_CHECK_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        static_cast<int>(lds_cl)));
+    RXMET_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 512, lds_cl));
+    ClusterArgs cl;
+    cl.G = H / kClUnits;
+    cl.ntiles = (B + kBT - 1) / kBT;
+    cl.Bpad = cl.ntiles * kBT;
+    int ncl = per_cu * ncu / cl.G;
+    if (ncl > cl.ntiles) ncl = cl.ntiles;
+    if (ncl >= 8) ncl -= ncl % 8;
+    if (ncl >= 1 && std::getenv("RXMET_NO_CLUSTER") == nullptr) {
+      cl.ncl = ncl;
+      cl.hx = reinterpret_cast<int8_t *>(wsb + ws.hx);
+      cl.counters = reinterpret_cast<unsigned *>(wsb + ws.sync);
+      cl.timeout = reinterpret_cast<int *>(cl.counters + ncl);
+      cl.lut = lut;
+      hipLaunchKernelGGL(cluster::zero_words, dim3(1), dim3(256), 0, stream, cl.counters, ncl + 1);
+      RXMET_CHECK_LAUNCH();
+      if (lut.total > 0) {
+        hipLaunchKernelGGL(lstm_build_act_lut, dim3((lut.total + 255) / 256), dim3(256), 0, stream,
+                           sp, lut, lut_table);
+        RXMET_CHECK_LAUNCH();
+      }
+      void *args[] = {&ra, &sp, &cl};
+      {
+        rxmet::prof::Scope ps__("lstm_fwd_recurrence", stream);
+        RXMET_CHECK_HIP(hipLaunchCooperativeKernel(fn, dim3(ncl * cl.G), dim3(512), args,
+                                                   static_cast<unsigned>(lds_cl), stream));
+      }
+      const int64_t n_out = static_cast<int64_t>(T) * B * H, n_state = static_cast<int64_t>(B) * H;
+      hipLaunchKernelGGL(lstm_poison_on_timeout, dim3(64), dim3(256), 0, stream, cl.timeout, n_out,
+                         output, n_state, h_n, c_n);
+      RXMET_CHECK_LAUNCH();
+      return 0;
+    }
+  }
   const size_t lds = recurrence_lds(H, KS, npl);
   const dim3 grid((B + kBT - 1) / kBT), block(64 * ((UT + kTilesPerWave - 1) / kTilesPerWave));
   {

@@ -303,3 +303,23 @@ def test_unsupported_shapes_raise(cuda):
     p16 = O.finalize(stats, c, 16, True)
     with pytest.raises(rxmet_lib.RxmetError, match="8 bits"):
         _gpu_forward(cuda, args, p16, False)
+
+
+@pytest.mark.parametrize("shape,cfg_name", [((3, 2560, 16, 128), "c4"), ((2, 100, 24, 256), "c4"),
+                                            ((2, 48, 8, 64), "c4"), ((3, 40, 8, 128), "16b-act")])
+def test_clustered_recurrence_matches_oracle_and_single_tile_path(cuda, shape, cfg_name,
+                                                                   monkeypatch):
+    """H a multiple of 64 takes the clustered recurrence (H / 64 workgroups per batch tile,
+    several batch tiles per cluster when B is large); it must equal the oracle and the
+    one-workgroup-per-tile recurrence bit for bit."""
+    T, B, I, H = shape
+    args, _, p = _case(T, B, I, H, cfg_name, 41, True, True)
+    Wi, Wh, bi, bh, x, h0, c0 = args
+    out, hn, cn, saved = _gpu_forward(cuda, args, p, True)
+    o = O.forward_quant(Wi, Wh, bi, bh, x, p, h0, c0, mode=O.ACT_CR)
+    _compare_forward(o, out, hn, cn, saved, True)
+    monkeypatch.setenv("RXMET_NO_CLUSTER", "1")
+    out2, hn2, cn2, saved2 = _gpu_forward(cuda, args, p, True)
+    assert torch.equal(out, out2) and torch.equal(hn, hn2) and torch.equal(cn, cn2)
+    for k in saved:
+        assert torch.equal(saved[k], saved2[k]), k

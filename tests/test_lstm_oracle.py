@@ -473,3 +473,24 @@ def test_backward_matches_autograd_surrogate(cfg_name, seed):
             e = e * (1 - f["b_ih_m" if k == "db_ih" else "b_hh_m"])
         scale = max(float(np.abs(e).max()), 1e-30)
         np.testing.assert_allclose(ours[k], e, rtol=1e-4, atol=1e-5 * scale, err_msg=k)
+
+
+def test_cr_mode_sums_are_order_free():
+    """ACT_CR sums each linear exactly, so relabelling the hidden units (a permutation of the
+    recurrent sum's order) only permutes the outputs, even where float partial sums would
+    pass 2^24 (16-bit h and weights)."""
+    T, B, I, H = 4, 3, 5, 32
+    (Wi, Wh, bi, bh, x, h0, c0), _, _, p = _calibrated(T, B, I, H, "16b-tensor", 51, True, True)
+    perm = np.random.default_rng(52).permutation(H)
+    rows = np.concatenate([g * H + perm for g in range(4)])
+    o = O.forward_quant(Wi, Wh, bi, bh, x, p, h0, c0, mode=O.ACT_CR)
+    q = O.forward_quant(Wi[rows], Wh[rows][:, perm], bi[rows], bh[rows], x, p, h0[:, perm],
+                        c0[:, perm], mode=O.ACT_CR)
+    assert np.array_equal(q["output"], o["output"][..., perm])
+    assert np.array_equal(q["c_n"], o["c_n"][:, perm])
+    assert np.array_equal(q["gate_out"], o["gate_out"][..., rows])
+    # the float-order (reference CPU) sum really does pass 2^24 here
+    hc = o["hidden"] - p.zero_point[L.OP["output"]]
+    wq = o["w_hh_q"]
+    assert np.abs(hc[0] @ wq.T.astype(np.float64)).max() > 2 ** 24 or \
+        np.abs(np.cumsum(hc[0][:, None, :] * wq[None], axis=-1)).max() > 2 ** 24
