@@ -21,8 +21,11 @@
 //      exact in int32, followed by the fused pointwise update in registers (bias
 //      rescale, gate inputs, PWL sigmoid/tanh, hidden update, clamps and masks) and the
 //      dequantised outputs.  No host round trip and no grid barrier per step.
+#include <cmath>
+#include <cstdlib>
 #include <vector>
 
+#include "cluster.h"
 #include "gru_internal.h"
 #include "mfma_frag.h"
 #include "rxmet_common.h"
@@ -410,6 +413,229 @@ __global__ __launch_bounds__(512) void recurrence(RecArgs a, StepParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------------
+// 4b. clustered recurrence: a batch tile's units split over G workgroups
+// ---------------------------------------------------------------------------------
+// Member m of a cluster owns UT unit tiles (16 units each) of one 16-sequence batch tile.
+// Four waves per unit tile split the recurrent sum over the K-steps (wave q takes steps
+// q, q+4, ...) with R_q fragments resident in VGPRs, add their partial sums through LDS, and
+// then each finishes one of the four batch rows a lane's MFMA output holds.  The new h codes
+// are exchanged through global memory (coherent accesses, double-buffered by step parity) and
+// the members meet at a counter barrier once per step (cluster.h).
+constexpr int kClMaxKPerWave = 4;  // K-steps per wave: H <= 1024
+
+struct ClArgs {
+  int ncl, G, UT, ntiles, Bpad;
+  int8_t *hx;          // [2][NPL][Bpad][H] centred h codes as int8 planes
+  unsigned *counters;  // [ncl]
+  int *timeout;
+};
+
+template <int NPL>
+__global__ __launch_bounds__(512) void recurrence_cl(RecArgs a, StepParams p, ClArgs cl) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int H = a.H, C = 3 * H, B = a.B, KS = a.KS;
+  float *lut_f = reinterpret_cast<float *>(smem);               // 3 * 16 * 3 (thr, qb, c)
+  int *lut_n = reinterpret_cast<int *>(lut_f + 3 * 16 * 3);     // 3 * 16
+  v4i *red = reinterpret_cast<v4i *>(smem + 1024);              // [UT][4][3][NPL][64]
+  const int tid = threadIdx.x, w = tid / 64, l = tid % 64;
+  const int utl = w / 4, kq = w % 4;
+  const cluster::Place pl = cluster::place(cl.G, cl.ncl);
+  const int ut = pl.member * cl.UT + utl;
+  const int j = 16 * ut + l % 16;
+  const int nr = 4 * (l / 16) + kq;  // batch row finished by this lane
+
+  for (int i = tid; i < 3 * 16; i += blockDim.x) {
+    const int g = i / 16, s = i % 16;
+    lut_f[g * 48 + s] = p.lut[g].thr[s];
+    lut_f[g * 48 + 16 + s] = p.lut[g].qb[s];
+    lut_f[g * 48 + 32 + s] = p.lut[g].c[s];
+    lut_n[g * 16 + s] = p.lut[g].n[s];
+  }
+  v4i rfr[kClMaxKPerWave][3];
+#pragma unroll
+  for (int i = 0; i < kClMaxKPerWave; ++i) {
+    const int s = kq + 4 * i;
+#pragma unroll
+    for (int g = 0; g < 3; ++g)
+      rfr[i][g] = s < KS ? a.rfrag[((ut * 3 + g) * KS + s) * 64 + l] : v4i{0, 0, 0, 0};
+  }
+  float cst[3][kChanParams];
+#pragma unroll
+  for (int g = 0; g < 3; ++g)
+#pragma unroll
+    for (int q = 0; q < kChanParams; ++q) cst[g][q] = a.chan[q * C + g * H + j];
+  __syncthreads();
+
+  const float plane_off = 128.0f + a.h_offset;
+  const size_t plane_stride = static_cast<size_t>(cl.Bpad) * H;
+  unsigned *counter = cl.counters + pl.cluster;
+  unsigned epoch = 0;
+  bool alive = true;
+  v4i *myred = red + (static_cast<size_t>(utl) * 4 + kq) * 3 * NPL * 64;
+
+  for (int tile = pl.cluster; tile < cl.ntiles && alive; tile += cl.ncl) {
+    const int b0 = tile * kTileB, b = b0 + nr;
+    const bool valid = b < B;
+    float hold = valid ? a.h0codes[static_cast<size_t>(b) * H + j] : p.zp_h;
+    {
+      const int hcv = static_cast<int>(hold - a.h_offset);
+      unsigned char *dst = reinterpret_cast<unsigned char *>(cl.hx) + static_cast<size_t>(b) * H + j;
+#pragma unroll
+      for (int q = 0; q < NPL; ++q)
+        cluster::store_bytes_coherent(dst + q * plane_stride,
+                                      NPL == 1 ? hcv : (q == 0 ? (hcv & 255) - 128 : hcv >> 8));
+    }
+    float gi_next[3];
+    auto load_gih = [&](int t) {
+#pragma unroll
+      for (int g = 0; g < 3; ++g)
+        gi_next[g] = valid ? a.gih[(static_cast<size_t>(t) * B + b) * C + g * H + j] : 0.0f;
+    };
+    load_gih(0);
+    alive = cluster::sync(counter, ++epoch * cl.G, cl.timeout);
+
+    for (int t = 0; t < a.T && alive; ++t) {
+      const int par = t & 1;
+      const int8_t *hin = cl.hx + static_cast<size_t>(par) * NPL * plane_stride;
+      int8_t *hout = cl.hx + static_cast<size_t>(par ^ 1) * NPL * plane_stride;
+      float gih[3] = {gi_next[0], gi_next[1], gi_next[2]};
+      // partial recurrent sums over this wave's K-steps
+      v4i acc[3][NPL];
+#pragma unroll
+      for (int g = 0; g < 3; ++g)
+#pragma unroll
+        for (int q = 0; q < NPL; ++q) acc[g][q] = v4i{0, 0, 0, 0};
+      {
+        const int8_t *hrow = hin + static_cast<size_t>(b0 + l % 16) * H + 16 * (l / 16);
+        v4i hfr[kClMaxKPerWave][NPL];
+#pragma unroll
+        for (int i = 0; i < kClMaxKPerWave; ++i)
+#pragma unroll
+          for (int q = 0; q < NPL; ++q)
+            if (kq + 4 * i < KS) {
+              const int4 v = cluster::load_coherent16(hrow + q * plane_stride + 64 * (kq + 4 * i));
+              hfr[i][q] = v4i{v.x, v.y, v.z, v.w};
+            }
+#pragma unroll
+        for (int i = 0; i < kClMaxKPerWave; ++i)
+          if (kq + 4 * i < KS) {
+#pragma unroll
+            for (int g = 0; g < 3; ++g)
+#pragma unroll
+              for (int q = 0; q < NPL; ++q) acc[g][q] = mfma_i8(hfr[i][q], rfr[i][g], acc[g][q]);
+          }
+      }
+#pragma unroll
+      for (int g = 0; g < 3; ++g)
+#pragma unroll
+        for (int q = 0; q < NPL; ++q) myred[(g * NPL + q) * 64 + l] = acc[g][q];
+      __syncthreads();
+      int sum[3][NPL];
+#pragma unroll
+      for (int g = 0; g < 3; ++g)
+#pragma unroll
+        for (int q = 0; q < NPL; ++q) {
+          int v = 0;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const int *src = reinterpret_cast<const int *>(
+                red + ((static_cast<size_t>(utl) * 4 + k) * 3 * NPL + g * NPL + q) * 64 + l);
+            v += src[kq];
+          }
+          sum[g][q] = v;
+        }
+      // pointwise update of (row b, unit j)
+      const uint32_t oH = static_cast<uint32_t>(b) * H + j;
+      const uint32_t oC = 3u * static_cast<uint32_t>(b) * H + j;
+      const uint32_t o4 = 4u * static_cast<uint32_t>(b) * H + j;
+      const uint32_t stepC = static_cast<uint32_t>(t) * B * C;
+      uint8_t k_ih[3], k_hh[3], k_gi[3], k_go[3], k_h;
+      float wx[3], rh[3];
+#pragma unroll
+      for (int g = 0; g < 3; ++g) {
+        const uint32_t col = static_cast<uint32_t>(static_cast<int>(cst[g][6]));
+        uint32_t v_u;
+        if (NPL == 2)
+          v_u = 256u * static_cast<uint32_t>(sum[g][NPL - 1]) + static_cast<uint32_t>(sum[g][0]) +
+                static_cast<uint32_t>(static_cast<int>(plane_off)) * col;
+        else
+          v_u = static_cast<uint32_t>(sum[g][0]) +
+                static_cast<uint32_t>(static_cast<int>(a.h_offset)) * col;
+        const float ghh = static_cast<float>(static_cast<int>(v_u));
+        float val = gih[g] - cst[g][2];
+        wx[g] = clamp_keep(rintf((val + cst[g][4]) * cst[g][0]) + p.zp_wx, p.wx, k_ih[g]);
+        val = ghh - cst[g][3];
+        rh[g] = clamp_keep(rintf((val + cst[g][5]) * cst[g][1]) + p.zp_rh, p.rh, k_hh[g]);
+      }
+      float in = rintf((wx[0] - p.zp_wx) * p.ih_to_zin) + rintf((rh[0] - p.zp_rh) * p.hh_to_zin);
+      in += p.zp_zin;
+      in = clamp_keep(in, p.zin, k_gi[0]);
+      const float z = pwl_eval(in, lut_f, lut_f + 16, lut_n, lut_f + 32, p.lut[0].zp_x, p.zout,
+                               k_go[0]);
+      in = rintf((wx[1] - p.zp_wx) * p.ih_to_rin) + rintf((rh[1] - p.zp_rh) * p.hh_to_rin);
+      in += p.zp_rin;
+      in = clamp_keep(in, p.rin, k_gi[1]);
+      const float rr = pwl_eval(in, lut_f + 48, lut_f + 64, lut_n + 16, lut_f + 80, p.lut[1].zp_x,
+                                p.rout, k_go[1]);
+      const float rmul = (rr - p.zp_rout) * (rh[2] - p.zp_rh);
+      in = rintf((wx[2] - p.zp_wx) * p.ih_to_nin) + rintf(rmul * p.rmul_to_nin);
+      in += p.zp_nin;
+      in = clamp_keep(in, p.nin, k_gi[2]);
+      const float nn = pwl_eval(in, lut_f + 96, lut_f + 112, lut_n + 32, lut_f + 128,
+                                p.lut[2].zp_x, p.nout, k_go[2]);
+      const float n_h = rintf((nn - p.zp_nout) * p.nout_to_h) + p.zp_h;
+      const float oldc = (z - p.zp_zout) * (hold - p.zp_h);
+      const float newc = (p.quant_one - z) * (n_h - p.zp_h);
+      float h2 = rintf((oldc + newc) * p.old_to_h) + p.zp_h;
+      h2 = clamp_keep(h2, p.h, k_h);
+      hold = h2;
+      {
+        const int hcv = static_cast<int>(h2 - a.h_offset);
+        unsigned char *dst = reinterpret_cast<unsigned char *>(hout) + static_cast<size_t>(b) * H + j;
+#pragma unroll
+        for (int q = 0; q < NPL; ++q)
+          cluster::store_bytes_coherent(dst + q * plane_stride,
+                                        NPL == 1 ? hcv : (q == 0 ? (hcv & 255) - 128 : hcv >> 8));
+      }
+      if (valid) {
+        const uint32_t stepH = static_cast<uint32_t>(t) * B * H;
+        a.hout[stepH + static_cast<uint32_t>(B) * H + oH] = (h2 - p.zp_h) * p.eff_h;
+        if (a.training) {
+          const uint32_t v0 = 4u * stepH + o4;
+          a.v[v0] = (z - p.zp_zout) * p.eff_zout;
+          a.v[v0 + H] = (rr - p.zp_rout) * p.eff_rout;
+          a.v[v0 + 2 * H] = (nn - p.zp_nout) * p.eff_nout;
+          a.v[v0 + 3 * H] = (rh[2] - p.zp_rh) * p.eff_rh;
+          const uint32_t m = stepC + oC;
+#pragma unroll
+          for (int g = 0; g < 3; ++g) {
+            a.ih_m[m + g * H] = k_ih[g];
+            a.hh_m[m + g * H] = k_hh[g];
+            a.gin_m[m + g * H] = k_gi[g];
+            a.gout_m[m + g * H] = k_go[g];
+          }
+          a.h_m[stepH + oH] = k_h;
+        }
+      }
+      if (t + 1 < a.T) load_gih(t + 1);
+      alive = cluster::sync(counter, ++epoch * cl.G, cl.timeout);
+    }
+  }
+}
+
+size_t recurrence_cl_lds_bytes(int UT, int npl) {
+  return 1024 + sizeof(v4i) * static_cast<size_t>(UT) * 4 * 3 * npl * 64;
+}
+
+// A launch whose cluster wait timed out leaves untrustworthy outputs: overwrite them with NaN.
+__global__ __launch_bounds__(256) void poison_on_timeout(const int *timeout, int64_t n, float *h) {
+  if (*timeout == 0) return;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
+    h[i] = NAN;
+}
+
 size_t recurrence_lds_bytes(int H, int KS, int npl) {
   const int ROW = KS * 64 + 16;
   return sizeof(float) * (2 * kTileB * H + 3 * 16 * 3) + sizeof(int) * 3 * 16 +
@@ -418,7 +644,7 @@ size_t recurrence_lds_bytes(int H, int KS, int npl) {
 
 // Workspace layout of the forward (bytes, 256-aligned pieces).
 struct FwdWorkspace {
-  size_t gih, chan, h0codes, hostblk, rfrag, total;
+  size_t gih, chan, h0codes, hostblk, rfrag, hx, sync, total;
   FwdWorkspace(int T, int B, int I, int H) {
     (void)I;
     const size_t C = 3 * static_cast<size_t>(H);
@@ -429,6 +655,9 @@ struct FwdWorkspace {
     h0codes = o; o += al(sizeof(float) * static_cast<size_t>(B) * H);
     hostblk = o; o += al(sizeof(float) * 8 * C);  // eff[4C], ibx, ibh, igx, igh
     rfrag = o; o += al(sizeof(v4i) * 64 * static_cast<size_t>(H / 16) * 3 * ((H + 63) / 64));
+    const size_t Bpad = (static_cast<size_t>(B) + kTileB - 1) / kTileB * kTileB;
+    hx = o; o += al(2 * 2 * Bpad * H);
+    sync = o; o += al(sizeof(unsigned) * (Bpad / kTileB + 1));
     total = o;
   }
 };
@@ -575,6 +804,55 @@ int rxmet_gru_forward_quant(int32_t is_training, int32_t T, int32_t B, int32_t I
   ra.gih = gih; ra.rfrag = rfrag; ra.chan = chan; ra.h0codes = h0codes; ra.hout = h; ra.v = v;
   ra.ih_m = ih_mask; ra.hh_m = hh_mask; ra.gin_m = gate_in_mask; ra.gout_m = gate_out_mask;
   ra.h_m = h_mask;
+  if (ra.KS <= 4 * kClMaxKPerWave && std::getenv("RXMET_NO_CLUSTER") == nullptr) {
+    // clustered path: the smallest unit slice per workgroup whose grid is resident at once
+    const void *fn = npl == 1 ? reinterpret_cast<const void *>(&recurrence_cl<1>)
+                              : reinterpret_cast<const void *>(&recurrence_cl<2>);
+    int device = 0, ncu = 0;
+    RXMET_CHECK_HIP(hipGetDevice(&device));
+    RXMET_CHECK_HIP(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, device));
+    ClArgs cl;
+    cl.ntiles = (B + kTileB - 1) / kTileB;
+    cl.Bpad = cl.ntiles * kTileB;
+    int chosen = 0, ncl = 0;
+    size_t lds_cl = 0;
+    for (int UT = 1; UT <= 2 && !chosen; ++UT) {
+      if ((H / 16) % UT) continue;
+      lds_cl = recurrence_cl_lds_bytes(UT, npl);
+      RXMET_CHECK_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                          static_cast<int>(lds_cl)));
+      int per_cu = 0;
+      RXMET_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256 * UT, lds_cl));
+      const int G = H / (16 * UT);
+      ncl = per_cu * ncu / G;
+      if (ncl < 1) continue;
+      if (ncl >= cl.ntiles || UT == 2) {
+        chosen = UT;
+        cl.G = G;
+      }
+    }
+    if (chosen && ncl >= 1) {
+      if (ncl > cl.ntiles) ncl = cl.ntiles;
+      if (ncl >= 8) ncl -= ncl % 8;
+      cl.UT = chosen;
+      cl.ncl = ncl;
+      cl.hx = reinterpret_cast<int8_t *>(wsb + ws.hx);
+      cl.counters = reinterpret_cast<unsigned *>(wsb + ws.sync);
+      cl.timeout = reinterpret_cast<int *>(cl.counters + ncl);
+      hipLaunchKernelGGL(cluster::zero_words, dim3(1), dim3(256), 0, stream, cl.counters, ncl + 1);
+      RXMET_CHECK_LAUNCH();
+      void *args[] = {&ra, &sp, &cl};
+      {
+        rxmet::prof::Scope ps__("gru_fwd_recurrence", stream);
+        RXMET_CHECK_HIP(hipLaunchCooperativeKernel(fn, dim3(ncl * cl.G), dim3(256 * cl.UT), args,
+                                                   static_cast<unsigned>(lds_cl), stream));
+      }
+      const int64_t n_h = static_cast<int64_t>(T + 1) * B * H;
+      hipLaunchKernelGGL(poison_on_timeout, dim3(64), dim3(256), 0, stream, cl.timeout, n_h, h);
+      RXMET_CHECK_LAUNCH();
+      return 0;
+    }
+  }
   const size_t lds = recurrence_lds_bytes(H, ra.KS, npl);
   const dim3 grid((B + kTileB - 1) / kTileB), block(64 * ((H + 31) / 32));
   if (npl == 1) {

@@ -114,6 +114,26 @@ def test_forward_bit_exact(cuda, shape, cfg_name, with_h0):
         np.testing.assert_array_equal(tensor.cpu().numpy(), e, err_msg=name)
 
 
+@pytest.mark.parametrize("shape,cfg_name", [((2, 4800, 8, 256), "c3"), ((3, 200, 16, 128), "c3"),
+                                            ((3, 40, 8, 96), "16b-act-pot2")])
+def test_clustered_forward_matches_oracle_and_single_tile_path(cuda, shape, cfg_name,
+                                                               monkeypatch):
+    """The clustered recurrence (units of a batch tile split over several workgroups, several
+    batch tiles per cluster when B is large) equals the oracle and the one-workgroup-per-tile
+    recurrence bit for bit."""
+    T, B, I, H = shape
+    print(f"[gru fwd cluster] shape={shape} cfg={cfg_name}", flush=True)
+    W, R, bw, br, x, h0, qp = _case(T, B, I, H, cfg_name, 4, True)
+    exp = GO.forward_quant(W, R, bw, br, x, qp, h0=h0, training=True)
+    got = _gpu_forward(cuda, W, R, bw, br, x, h0, qp, True)
+    for name, tensor in zip(NAMES, got):
+        np.testing.assert_array_equal(tensor.cpu().numpy(), exp[name], err_msg=name)
+    monkeypatch.setenv("RXMET_NO_CLUSTER", "1")
+    ref = _gpu_forward(cuda, W, R, bw, br, x, h0, qp, True)
+    for name, a, b in zip(NAMES, got, ref):
+        assert torch.equal(a, b), name
+
+
 def test_forward_eval_matches_training_h(cuda):
     W, R, bw, br, x, h0, qp = _case(4, 16, 8, 32, "c3", 2, True)
     tr = _gpu_forward(cuda, W, R, bw, br, x, h0, qp, True)
