@@ -24,9 +24,12 @@
 //   3. bias fold   : per-workgroup fp64 partials summed in a fixed order (deterministic);
 //   4. dx, dW, dR  : rocBLAS SGEMMs on the dp/dq buffers (dW and dR split over the long
 //                    T*B reduction and summed in a fixed order), then one mask pass.
+#include <cmath>
+#include <cstdlib>
 #include <vector>
 
 #include "blas_util.h"
+#include "cluster.h"
 #include "gru_internal.h"
 #include "mfma_frag.h"
 #include "rxmet_common.h"
@@ -309,6 +312,201 @@ __global__ __launch_bounds__(512) void bwd_recurrence(BwdArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------------
+// 2b. clustered backward recurrence
+// ---------------------------------------------------------------------------------
+// Member m of a cluster owns UT unit tiles (16 units) of one 16-sequence batch tile.  Per step
+// each lane finishes the STE pointwise of one (sequence, unit), writes dq * scale_R of its
+// three channels to a global exchange buffer (coherent stores), and after the cluster barrier
+// the four waves of a unit tile compute dh += R_deq dq for that tile on fp32 MFMA
+// (v_mfma_f32_16x16x4_f32), each over a quarter of the 3H channels with its R_q values
+// resident in VGPRs, and add their partial sums through LDS in a fixed order.
+constexpr int kBwMaxKS2 = 12;  // 3H <= 768
+
+struct BwdClArgs {
+  int ncl, G, UT, ntiles, Bpad, KP;  // KP = 3H padded to a multiple of 64
+  float *xch;                        // [2][Bpad][KP] exchanged dq * scale_R
+  const float *rt;                   // packed R_q values, see pack_rt_f32
+  unsigned *counters;
+  int *timeout;
+};
+
+// R_q [H][3H] -> per (unit tile ut, wave q, MFMA i, lane l) the B value R_q[j][k] with
+// j = 16 ut + l % 16 and k = 16 (q KS2 + i / 4) + 4 (l / 16) + i % 4 (0 beyond 3H).
+__global__ __launch_bounds__(64) void pack_rt_f32(int H, int KS2, const float *__restrict__ Rq,
+                                                  float *__restrict__ rt) {
+  const int l = threadIdx.x, idx = blockIdx.x;  // idx = (ut * 4 + q) * 4 KS2 + i
+  const int n = 4 * KS2;
+  const int i = idx % n, q = (idx / n) % 4, ut = idx / (4 * n);
+  const int j = 16 * ut + l % 16;
+  const int k = 16 * (q * KS2 + i / 4) + 4 * (l / 16) + i % 4;
+  rt[static_cast<size_t>(idx) * 64 + l] = k < 3 * H ? Rq[static_cast<size_t>(j) * 3 * H + k] : 0.0f;
+}
+
+__global__ __launch_bounds__(512) void bwd_recurrence_cl(BwdArgs a, BwdClArgs cl) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int H = a.H, C = 3 * H, B = a.B, KS2 = a.KS2, KP = cl.KP;
+  v4f *red = reinterpret_cast<v4f *>(smem);                          // [UT][4][64]
+  double *bred = reinterpret_cast<double *>(smem + 16 * 1024);       // [UT][4][16][6]
+  const int tid = threadIdx.x, w = tid / 64, l = tid % 64;
+  const int utl = w / 4, kq = w % 4;
+  const cluster::Place pl = cluster::place(cl.G, cl.ncl);
+  const int ut = pl.member * cl.UT + utl;
+  const int j = 16 * ut + l % 16;
+  const int nr = 4 * (l / 16) + kq;
+  float rtv[4 * kBwMaxKS2];
+#pragma unroll
+  for (int i = 0; i < 4 * kBwMaxKS2; ++i)
+    rtv[i] = i < 4 * KS2 ? cl.rt[((static_cast<size_t>(ut) * 4 + kq) * 4 * KS2 + i) * 64 + l] : 0.0f;
+  float effr[3];
+  float mbw[3], mbr[3];
+#pragma unroll
+  for (int g = 0; g < 3; ++g) {
+    effr[g] = a.eff_r[g * H + j];
+    mbw[g] = a.bw_m ? static_cast<float>(a.bw_m[g * H + j]) : 1.0f;
+    mbr[g] = a.br_m ? static_cast<float>(a.br_m[g * H + j]) : 1.0f;
+  }
+  double sbw[3] = {0.0, 0.0, 0.0}, sbr[3] = {0.0, 0.0, 0.0};
+  unsigned *counter = cl.counters + pl.cluster;
+  unsigned epoch = 0;
+  bool alive = true;
+  const uint32_t BH = static_cast<uint32_t>(B) * H;
+  v4f *myred = red + (static_cast<size_t>(utl) * 4 + kq) * 64;
+
+  for (int tile = pl.cluster; tile < cl.ntiles && alive; tile += cl.ncl) {
+    const int b0 = tile * kBTile, b = b0 + nr;
+    const bool valid = b < B;
+    float dhc = 0.0f;
+    for (int t = a.T - 1; t >= 0 && alive; --t) {
+      const int par = t & 1;
+      float dqv[3] = {0.f, 0.f, 0.f};
+      float dhl = 0.0f;
+      if (valid) {
+        const uint32_t oH = static_cast<uint32_t>(b) * H + j;
+        const uint32_t oC = 3u * static_cast<uint32_t>(b) * H + j;
+        const uint32_t tH = static_cast<uint32_t>(t) * BH;
+        const uint32_t tC = 3u * tH, v0 = 4u * tH + 4u * static_cast<uint32_t>(b) * H + j;
+        float dht = a.dh_new[tH + BH + oH] + dhc;
+        if (a.h_m) dht *= static_cast<float>(a.h_m[tH + oH]);
+        const float z = a.v[v0], rr = a.v[v0 + H], g = a.v[v0 + 2 * H], qg = a.v[v0 + 3 * H];
+        dhl = z * dht;
+        const float dg = (1.0f - z) * dht;
+        const float dz = (a.h[tH + oH] - g) * dht;
+        const uint32_t m = tC + oC;
+        float dpg = (1.0f - g * g) * dg;
+        if (a.gout_m) dpg *= static_cast<float>(a.gout_m[m + 2 * H]);
+        if (a.gin_m) dpg *= static_cast<float>(a.gin_m[m + 2 * H]);
+        float dqg = dpg * rr;
+        const float dr = dpg * qg;
+        float dpr = rr * (1.0f - rr) * dr, dqr = dpr;
+        float dpz = z * (1.0f - z) * dz, dqz = dpz;
+        if (a.gout_m) {
+          const float mz = static_cast<float>(a.gout_m[m]), mr = static_cast<float>(a.gout_m[m + H]);
+          dpz *= mz; dqz *= mz; dpr *= mr; dqr *= mr;
+        }
+        if (a.gin_m) {
+          const float mz = static_cast<float>(a.gin_m[m]), mr = static_cast<float>(a.gin_m[m + H]);
+          dpz *= mz; dqz *= mz; dpr *= mr; dqr *= mr;
+        }
+        if (a.hh_m) {
+          dqz *= static_cast<float>(a.hh_m[m]);
+          dqr *= static_cast<float>(a.hh_m[m + H]);
+          dqg *= static_cast<float>(a.hh_m[m + 2 * H]);
+        }
+        if (a.ih_m) {
+          dpz *= static_cast<float>(a.ih_m[m]);
+          dpr *= static_cast<float>(a.ih_m[m + H]);
+          dpg *= static_cast<float>(a.ih_m[m + 2 * H]);
+        }
+        const float dpv[3] = {dpz, dpr, dpg};
+        dqv[0] = dqz; dqv[1] = dqr; dqv[2] = dqg;
+#pragma unroll
+        for (int gg = 0; gg < 3; ++gg) {
+          a.dp[m + gg * H] = dpv[gg];
+          a.dq[m + gg * H] = dqv[gg];
+          sbw[gg] += static_cast<double>(dpv[gg] * mbw[gg]);
+          sbr[gg] += static_cast<double>(dqv[gg] * mbr[gg]);
+        }
+      }
+      float *xrow = cl.xch + (static_cast<size_t>(par) * cl.Bpad + b) * KP;
+#pragma unroll
+      for (int gg = 0; gg < 3; ++gg)
+        cluster::store_coherent(reinterpret_cast<unsigned *>(xrow + gg * H + j),
+                                __float_as_uint(dqv[gg] * effr[gg]));
+      alive = cluster::sync(counter, ++epoch * cl.G, cl.timeout);
+      if (!alive) break;
+      // dh += R_deq dq over this wave's quarter of the channels
+      v4f acc = {0.f, 0.f, 0.f, 0.f};
+      {
+        const float *arow = cl.xch + (static_cast<size_t>(par) * cl.Bpad + b0 + l % 16) * KP +
+                            16 * (kq * KS2) + 4 * (l / 16);
+        int4 av[kBwMaxKS2];
+#pragma unroll
+        for (int qg = 0; qg < kBwMaxKS2; ++qg)
+          if (qg < KS2) av[qg] = cluster::load_coherent16(arow + 16 * qg);
+#pragma unroll
+        for (int qg = 0; qg < kBwMaxKS2; ++qg)
+          if (qg < KS2) {
+            acc = mfma_f32(__int_as_float(av[qg].x), rtv[4 * qg + 0], acc);
+            acc = mfma_f32(__int_as_float(av[qg].y), rtv[4 * qg + 1], acc);
+            acc = mfma_f32(__int_as_float(av[qg].z), rtv[4 * qg + 2], acc);
+            acc = mfma_f32(__int_as_float(av[qg].w), rtv[4 * qg + 3], acc);
+          }
+      }
+      myred[l] = acc;
+      __syncthreads();
+      float gsum = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        gsum += reinterpret_cast<const float *>(red + (static_cast<size_t>(utl) * 4 + k) * 64 + l)[kq];
+      dhc = dhl + gsum;
+    }
+    if (valid && alive) {
+      const uint32_t o = static_cast<uint32_t>(b) * H + j;
+      a.dh0[o] = a.h0_m ? dhc * static_cast<float>(a.h0_m[o]) : dhc;
+    }
+  }
+  // bias partials of this member's units: rows summed in a fixed order
+#pragma unroll
+  for (int gg = 0; gg < 3; ++gg) {
+    sbw[gg] += __shfl_xor(sbw[gg], 16, 64);
+    sbw[gg] += __shfl_xor(sbw[gg], 32, 64);
+    sbr[gg] += __shfl_xor(sbr[gg], 16, 64);
+    sbr[gg] += __shfl_xor(sbr[gg], 32, 64);
+  }
+  __syncthreads();
+  if (l < 16) {
+    double *d = bred + ((static_cast<size_t>(utl) * 4 + kq) * 16 + l) * 6;
+#pragma unroll
+    for (int gg = 0; gg < 3; ++gg) {
+      d[gg] = sbw[gg];
+      d[3 + gg] = sbr[gg];
+    }
+  }
+  __syncthreads();
+  if (kq == 0 && l < 16) {
+    double x[6] = {0, 0, 0, 0, 0, 0};
+    for (int k = 0; k < 4; ++k) {
+      const double *d = bred + ((static_cast<size_t>(utl) * 4 + k) * 16 + l) * 6;
+#pragma unroll
+      for (int e = 0; e < 6; ++e) x[e] += d[e];
+    }
+    double *p = a.bias_partial + static_cast<size_t>(pl.cluster) * 2 * C;
+#pragma unroll
+    for (int gg = 0; gg < 3; ++gg) {
+      p[gg * H + j] = x[gg];
+      p[C + gg * H + j] = x[3 + gg];
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void zero_floats(int64_t n, float *p) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
+    p[i] = 0.0f;
+}
+
+
 __global__ __launch_bounds__(256) void fold_bias(int nwg, int C, const double *__restrict__ part,
                                                  float *__restrict__ dbw, float *__restrict__ dbr) {
   const int c = blockIdx.x * blockDim.x + threadIdx.x;
@@ -345,7 +543,7 @@ size_t bwd_lds_bytes(int KS2) {
 }
 
 struct BwdWorkspace {
-  size_t dp, dq, xd, wd, rfrag, rowsum, effr, effw, bias, part, total;
+  size_t dp, dq, xd, wd, rfrag, rowsum, effr, effw, bias, part, xch, rt, sync, total;
   BwdWorkspace(int T, int B, int I, int H) {
     const size_t C = 3 * static_cast<size_t>(H);
     const size_t KS2 = (C + 63) / 64;
@@ -363,6 +561,11 @@ struct BwdWorkspace {
     bias = o; o += al(sizeof(double) * 2 * C * nwg);
     const size_t S = static_cast<size_t>(blas::splitk_chunks(static_cast<int64_t>(T) * B));
     part = o; o += al(sizeof(float) * S * C * (static_cast<size_t>(I) > H ? I : H));
+    // clustered recurrence: dq exchange, packed R_q values, counters
+    const size_t Bpad = nwg * kBTile;
+    xch = o; o += al(sizeof(float) * 2 * Bpad * KS2 * 64);
+    rt = o; o += al(sizeof(float) * ((H + 15) / 16) * 4 * 4 * KS2 * 64);
+    sync = o; o += al(sizeof(unsigned) * (nwg + 1));
     total = o;
   }
 };
@@ -459,6 +662,68 @@ int rxmet_gru_backward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const f
   ba.rfrag = rfrag; ba.rowsum = rowsum; ba.eff_r = effr;
   ba.dp = dp; ba.dq = dq; ba.bias_partial = bias; ba.dh0 = dh0;
   const int nwg = (B + kBTile - 1) / kBTile;
+  if (KS2 <= kBwMaxKS2 && std::getenv("RXMET_NO_CLUSTER") == nullptr) {
+    const void *fn = reinterpret_cast<const void *>(&bwd_recurrence_cl);
+    const size_t lds_cl = 16 * 1024 + sizeof(double) * 2 * 4 * 16 * 6;
+    int device = 0, ncu = 0;
+    RXMET_CHECK_HIP(hipGetDevice(&device));
+    RXMET_CHECK_HIP(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, device));
+    RXMET_CHECK_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        static_cast<int>(lds_cl)));
+    BwdClArgs cl;
+    cl.ntiles = nwg;
+    cl.Bpad = nwg * kBTile;
+    cl.KP = KS2 * 64;
+    int chosen = 0, ncl = 0;
+    for (int UT = 1; UT <= 2 && !chosen; ++UT) {
+      if ((H / 16) % UT) continue;
+      int per_cu = 0;
+      RXMET_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256 * UT, lds_cl));
+      const int G = H / (16 * UT);
+      ncl = per_cu * ncu / G;
+      if (ncl < 1) continue;
+      if (ncl >= cl.ntiles || UT == 2) {
+        chosen = UT;
+        cl.G = G;
+      }
+    }
+    if (chosen && ncl >= 1) {
+      if (ncl > cl.ntiles) ncl = cl.ntiles;
+      if (ncl >= 8) ncl -= ncl % 8;
+      cl.UT = chosen;
+      cl.ncl = ncl;
+      cl.xch = reinterpret_cast<float *>(wsb + ws.xch);
+      float *rt = reinterpret_cast<float *>(wsb + ws.rt);
+      cl.rt = rt;
+      cl.counters = reinterpret_cast<unsigned *>(wsb + ws.sync);
+      cl.timeout = reinterpret_cast<int *>(cl.counters + ncl);
+      hipLaunchKernelGGL(pack_rt_f32, dim3((H / 16) * 4 * 4 * KS2), dim3(64), 0, stream, H, KS2,
+                         R_q, rt);
+      RXMET_CHECK_LAUNCH();
+      // padding channels of the exchange rows stay zero
+      hipLaunchKernelGGL(cluster::zero_words, dim3(1), dim3(256), 0, stream, cl.counters, ncl + 1);
+      RXMET_CHECK_LAUNCH();
+      {
+        const int64_t nx = static_cast<int64_t>(2) * cl.Bpad * cl.KP;
+        hipLaunchKernelGGL(zero_floats, dim3(256), dim3(256), 0, stream, nx, cl.xch);
+        RXMET_CHECK_LAUNCH();
+      }
+      void *args[] = {&ba, &cl};
+      {
+        rxmet::prof::Scope ps__("gru_bwd_recurrence", stream);
+        RXMET_CHECK_HIP(hipLaunchCooperativeKernel(fn, dim3(ncl * cl.G), dim3(256 * cl.UT), args,
+                                                   static_cast<unsigned>(lds_cl), stream));
+      }
+      hipLaunchKernelGGL(cluster::poison_nan, dim3(64), dim3(256), 0, stream, cl.timeout,
+                         static_cast<int64_t>(B) * H, dh0);
+      RXMET_CHECK_LAUNCH();
+      hipLaunchKernelGGL(fold_bias, dim3((C + 255) / 256), dim3(256), 0, stream, ncl, C, bias, dbw,
+                         dbr);
+      RXMET_CHECK_LAUNCH();
+      goto weight_gemms;
+    }
+  }
+  {
   const size_t lds = bwd_lds_bytes(KS2);
   RXMET_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&bwd_recurrence),
                                       hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -470,7 +735,9 @@ int rxmet_gru_backward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const f
   RXMET_CHECK_LAUNCH();
   hipLaunchKernelGGL(fold_bias, dim3((C + 255) / 256), dim3(256), 0, stream, nwg, C, bias, dbw, dbr);
   RXMET_CHECK_LAUNCH();
+  }
 
+weight_gemms:
   int device = 0;
   RXMET_CHECK_HIP(hipGetDevice(&device));
   rocblas_handle bh = handle(device);

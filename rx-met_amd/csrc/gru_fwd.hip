@@ -628,13 +628,6 @@ size_t recurrence_cl_lds_bytes(int UT, int npl) {
   return 1024 + sizeof(v4i) * static_cast<size_t>(UT) * 4 * 3 * npl * 64;
 }
 
-// A launch whose cluster wait timed out leaves untrustworthy outputs: overwrite them with NaN.
-__global__ __launch_bounds__(256) void poison_on_timeout(const int *timeout, int64_t n, float *h) {
-  if (*timeout == 0) return;
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
-    h[i] = NAN;
-}
 
 size_t recurrence_lds_bytes(int H, int KS, int npl) {
   const int ROW = KS * 64 + 16;
@@ -848,7 +841,7 @@ int rxmet_gru_forward_quant(int32_t is_training, int32_t T, int32_t B, int32_t I
                                                    static_cast<unsigned>(lds_cl), stream));
       }
       const int64_t n_h = static_cast<int64_t>(T + 1) * B * H;
-      hipLaunchKernelGGL(poison_on_timeout, dim3(64), dim3(256), 0, stream, cl.timeout, n_h, h);
+      hipLaunchKernelGGL(cluster::poison_nan, dim3(64), dim3(256), 0, stream, cl.timeout, n_h, h);
       RXMET_CHECK_LAUNCH();
       return 0;
     }

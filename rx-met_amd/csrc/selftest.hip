@@ -34,6 +34,13 @@ __global__ __launch_bounds__(64) void mfma_bf16_probe(const float *A, const floa
   for (int r = 0; r < 4; ++r) D[(4 * (l / 16) + r) * 16 + l % 16] = acc[r];
 }
 
+__global__ __launch_bounds__(64) void mfma_f32_probe(const float *A, const float *B, float *D) {
+  const int l = threadIdx.x;
+  v4f acc = {0.f, 0.f, 0.f, 0.f};
+  acc = mfma_f32(A[(l % 16) * 4 + l / 16], B[(l / 16) * 16 + l % 16], acc);
+  for (int r = 0; r < 4; ++r) D[(4 * (l / 16) + r) * 16 + l % 16] = acc[r];
+}
+
 }  // namespace
 }  // namespace rxmet
 
@@ -49,8 +56,12 @@ extern "C" int rxmet_selftest_mfma(int which, const void *A, const void *B, void
     hipLaunchKernelGGL(rxmet::mfma_bf16_probe, dim3(1), dim3(64), 0, s,
                        static_cast<const float *>(A), static_cast<const float *>(B),
                        static_cast<float *>(D));
+  } else if (which == 2) {
+    hipLaunchKernelGGL(rxmet::mfma_f32_probe, dim3(1), dim3(64), 0, s,
+                       static_cast<const float *>(A), static_cast<const float *>(B),
+                       static_cast<float *>(D));
   } else {
-    rxmet::set_error("which must be 0 (int8) or 1 (bf16)");
+    rxmet::set_error("which must be 0 (int8), 1 (bf16) or 2 (fp32)");
     return -22;
   }
   RXMET_CHECK_LAUNCH();

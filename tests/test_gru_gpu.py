@@ -33,6 +33,13 @@ def test_mfma_layout_selftest(cuda):
     rxmet_lib.call("rxmet_selftest_mfma", 1, at.data_ptr(), bt.data_ptr(), d.data_ptr(),
                    torch.cuda.current_stream().cuda_stream)
     np.testing.assert_array_equal(d.cpu().numpy(), (a.astype(np.float64) @ b).astype(f32))
+    a = g.integers(-100, 100, (16, 4)).astype(f32)
+    b = (g.integers(-100, 100, (4, 16)) / 64.0).astype(f32)
+    d = torch.zeros((16, 16), dtype=torch.float32, device=cuda)
+    at, bt = torch.from_numpy(a).to(cuda), torch.from_numpy(b).to(cuda)
+    rxmet_lib.call("rxmet_selftest_mfma", 2, at.data_ptr(), bt.data_ptr(), d.data_ptr(),
+                   torch.cuda.current_stream().cuda_stream)
+    np.testing.assert_array_equal(d.cpu().numpy(), (a.astype(np.float64) @ b).astype(f32))
 
 
 def _weights(I, H, seed, amp=None):
@@ -177,6 +184,33 @@ def test_backward_matches_oracle(cuda, shape, cfg_name, with_h0):
         e = exp[name]
         scale = max(float(np.abs(e).max()), 1e-30)
         np.testing.assert_allclose(a, e, rtol=1e-4, atol=1e-5 * scale, err_msg=name)
+
+
+@pytest.mark.parametrize("shape,cfg_name", [((2, 4800, 8, 256), "c3"), ((3, 200, 16, 128), "c3"),
+                                            ((4, 40, 8, 96), "16b-act-pot2"), ((3, 20, 5, 16), "8b-sym")])
+def test_clustered_backward_matches_oracle_and_single_tile_path(cuda, shape, cfg_name,
+                                                                monkeypatch):
+    """The clustered backward (fp32 MFMA dh, dq exchanged between the workgroups of a batch
+    tile) against the oracle, and against the one-workgroup-per-tile path within 1e-4."""
+    T, B, I, H = shape
+    print(f"[gru bwd cluster] shape={shape} cfg={cfg_name}", flush=True)
+    W, R, bw, br, x, h0, qp = _case(T, B, I, H, cfg_name, 5, True)
+    exp_f = GO.forward_quant(W, R, bw, br, x, qp, h0=h0, training=True)
+    fwd = _gpu_forward(cuda, W, R, bw, br, x, h0, qp, True)
+    g = np.random.default_rng(6)
+    dh_new = (g.standard_normal((T + 1, B, H)) * 1e-2).astype(f32)
+    exp = GO.backward_quant(exp_f, dh_new, qp)
+    got = _gpu_backward(cuda, fwd, dh_new, qp, T, B, I, H)
+    names = ("dx", "dW", "dR", "dbw", "dbr", "dh0")
+    for name, a in zip(names, got):
+        e = exp[name]
+        scale = max(float(np.abs(e).max()), 1e-30)
+        np.testing.assert_allclose(a, e, rtol=1e-4, atol=1e-5 * scale, err_msg=name)
+    monkeypatch.setenv("RXMET_NO_CLUSTER", "1")
+    ref = _gpu_backward(cuda, fwd, dh_new, qp, T, B, I, H)
+    for name, a, b in zip(names, got, ref):
+        scale = max(float(np.abs(b).max()), 1e-30)
+        np.testing.assert_allclose(a, b, rtol=1e-4, atol=1e-5 * scale, err_msg=name)
 
 
 def test_backward_without_masks_and_nan_propagation(cuda):
