@@ -22,9 +22,11 @@
 //   3. rocBLAS   : dx, and split-K dW_ih | db_ih and dW_hh | db_hh; one pass applies the
 //                  master masks and splits off the bias columns.
 #include <cmath>
+#include <cstdlib>
 #include <vector>
 
 #include "blas_util.h"
+#include "cluster.h"
 #include "lstm_internal.h"
 #include "mfma_frag.h"
 #include "rxmet_common.h"
@@ -290,6 +292,256 @@ __global__ __launch_bounds__(512) void lstm_bwd_recurrence(BwdArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------------
+// 2b. clustered backward recurrence
+// ---------------------------------------------------------------------------------
+// Member m of a cluster owns 64 units (four 16-unit tiles) of one 16-sequence batch tile for
+// all four gates: 256 channels.  Per step each lane finishes the STE pointwise of two
+// (sequence, unit) pairs, the member writes dgates_hh * scale_W of its channels as 22-bit
+// block fixed point with one exponent per sequence (three int8 planes) to a global exchange
+// buffer, and after the cluster barrier dh = W_hh_deq^T dgates_hh of its units is summed on
+// v_mfma_i32_16x16x64_i8: the contraction runs member by member (each member's 256 channels
+// are four K-steps with one exponent), every member's exact plane sums are recombined in
+// double and scaled by that member's exponent, and the two K-halves (waves 0-3 and 4-7) are
+// added in a fixed order.  W_hh codes of the member's units stay resident in LDS.
+constexpr int kBcUnits = 64;
+
+struct BwdClArgs {
+  int ncl, G, ntiles, Bpad;
+  int8_t *xp;          // [2][3][Bpad][4H] planes of the exchanged dgates, K member-major
+  int *xe;             // [2][Bpad][G] exponents
+  const v4i *wfrag;    // W_hh^T fragments in member-major K order, see lstm_pack_whh_t_cl
+  const float *csum;   // [G][H] column sums of W_hh codes over each member's channels
+  unsigned *counters;
+  int *timeout;
+};
+
+// A position k of the member-major contraction order -> channel c.
+__device__ __forceinline__ int cl_channel(int k, int H) {
+  const int m = k / 256, g = (k / 64) % 4, u = k % 64;
+  return g * H + 64 * m + u;
+}
+
+// frag[(jt * KS2 + s) * 64 + lane] = W[cl_channel(64 s + 16 (lane / 16) + e)][16 jt + lane % 16];
+// csum[m][j] = sum over member m's channels c of W[c][j].
+__global__ __launch_bounds__(64) void lstm_pack_whh_t_cl(int H, int KS2, const float *__restrict__ wq,
+                                                         v4i *__restrict__ frag,
+                                                         float *__restrict__ csum) {
+  const int lane = threadIdx.x, idx = blockIdx.x;
+  const int s = idx % KS2, jt = idx / KS2;
+  const int j = 16 * jt + lane % 16;
+  int wd[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    int by[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int c = cl_channel(64 * s + 16 * (lane / 16) + 4 * q + e, H);
+      by[e] = static_cast<int>(wq[static_cast<size_t>(c) * H + j]);
+    }
+    wd[q] = pack4_i8(by[0], by[1], by[2], by[3]);
+  }
+  frag[static_cast<size_t>(idx) * 64 + lane] = v4i{wd[0], wd[1], wd[2], wd[3]};
+  if (s % 4 == 0 && lane < 16) {
+    int sum = 0;
+    for (int k = 64 * s; k < 64 * s + 256; ++k)
+      sum += static_cast<int>(wq[static_cast<size_t>(cl_channel(k, H)) * H + j]);
+    csum[static_cast<size_t>(s / 4) * H + j] = static_cast<float>(sum);
+  }
+}
+
+__global__ __launch_bounds__(512) void lstm_bwd_recurrence_cl(BwdArgs a, BwdClArgs cl) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int H = a.H, C = 4 * H, B = a.B, KS2 = a.KS2, G = cl.G;
+  v4i *wl = reinterpret_cast<v4i *>(smem);                              // [4][KS2][64]
+  double *dred = reinterpret_cast<double *>(wl + 4 * KS2 * 64);         // [8][64][4]
+  unsigned *rowmax = reinterpret_cast<unsigned *>(dred + 8 * 64 * 4);   // [16]
+  int *rowexp = reinterpret_cast<int *>(rowmax + kBB);                  // [16]
+  const int tid = threadIdx.x, w = tid / 64, l = tid % 64;
+  const int utl = w & 3, kh = w >> 2;
+  const cluster::Place pl = cluster::place(G, cl.ncl);
+  const int m0 = pl.member;
+  const int jt = m0 * 4 + utl;  // global unit tile
+  const int j = 16 * jt + l % 16;
+  const int nrow0 = 4 * (l / 16);
+  for (int i = tid; i < 4 * KS2 * 64; i += blockDim.x) {
+    const int lane = i % 64, s = (i / 64) % KS2, u = i / (64 * KS2);
+    wl[i] = cl.wfrag[((static_cast<size_t>(m0) * 4 + u) * KS2 + s) * 64 + lane];
+  }
+  if (tid < kBB) rowmax[tid] = 0u;
+  float sw[4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) sw[g] = a.s_whh[g * H + j];
+  // K-halves: members [0, mh) for waves 0-3, [mh, G) for waves 4-7
+  const int mh = (G + 1) / 2;
+  const int mlo = kh == 0 ? 0 : mh, mhi = kh == 0 ? mh : G;
+  unsigned *counter = cl.counters + pl.cluster;
+  unsigned epoch = 0;
+  bool alive = true;
+  const uint32_t BH = static_cast<uint32_t>(B) * H, BC = static_cast<uint32_t>(B) * C;
+  const size_t pstride = static_cast<size_t>(cl.Bpad) * C;
+  __syncthreads();
+
+  for (int tile = pl.cluster; tile < cl.ntiles && alive; tile += cl.ncl) {
+    const int b0 = tile * kBB;
+    float dh[2], dc[2];
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) {
+      const int b = b0 + nrow0 + 2 * kh + rr;
+      dh[rr] = (a.grad_hn && b < B) ? a.grad_hn[static_cast<size_t>(b) * H + j] : 0.0f;
+      dc[rr] = (a.grad_cn && b < B) ? a.grad_cn[static_cast<size_t>(b) * H + j] : 0.0f;
+    }
+    for (int t = a.T - 1; t >= 0 && alive; --t) {
+      const int par = t & 1;
+      float sv[2][4];
+#pragma unroll
+      for (int rr = 0; rr < 2; ++rr) {
+        const int nr = nrow0 + 2 * kh + rr, b = b0 + nr;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) sv[rr][g] = 0.0f;
+        if (b >= B) continue;
+        const uint32_t e = static_cast<uint32_t>(t) * BH + static_cast<uint32_t>(b) * H + j;
+        const uint32_t gb = static_cast<uint32_t>(t) * BC + static_cast<uint32_t>(b) * C + j;
+        const float ig = deq(a.gate_out[gb], a.s_gout[0], a.zp_gout[0]);
+        const float fg = deq(a.gate_out[gb + H], a.s_gout[1], a.zp_gout[1]);
+        const float gg = deq(a.gate_out[gb + 2 * H], a.s_gout[2], a.zp_gout[2]);
+        const float og = deq(a.gate_out[gb + 3 * H], a.s_gout[3], a.zp_gout[3]);
+        const float ct = deq(a.cell_tanh[e], a.s_t, a.zp_t);
+        const float pc = t == 0 ? deq(a.c0_q[static_cast<uint32_t>(b) * H + j], a.s_c, a.zp_c)
+                                : deq(a.cell[e - BH], a.s_c, a.zp_c);
+        const float dht = (dh[rr] + a.grad_out[e]) * keepf(a.hid_m, e);
+        const float d_o = dht * ct;
+        const float dct = dht * og * keepf(a.tanh_m, e);
+        const float dcv = dc[rr] + dct * (1.0f - ct * ct);
+        const float mdc = dcv * keepf(a.cell_m, e);
+        const float dfg = mdc * pc;
+        const float dig = mdc * gg, dgg = mdc * ig;
+        const float go0 = dig * keepf(a.gout_m, gb), go1 = dfg * keepf(a.gout_m, gb + H);
+        const float go2 = dgg * keepf(a.gout_m, gb + 2 * H), go3 = d_o * keepf(a.gout_m, gb + 3 * H);
+        const float gi[4] = {go0 * ig * (1.0f - ig), go1 * fg * (1.0f - fg), go2 * (1.0f - gg * gg),
+                             go3 * og * (1.0f - og)};
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const uint32_t gi_ = gb + g * H;
+          const float grad = gi[g] * keepf(a.gin_m, gi_);
+          const float li = grad * keepf(a.ih_m, gi_);
+          const float lh = grad * keepf(a.hh_m, gi_);
+          a.dli[gi_] = li;
+          a.dlh[gi_] = lh;
+          sv[rr][g] = lh * sw[g];
+        }
+        dc[rr] = mdc * fg;
+      }
+      // per-sequence exponent of this member's channels (NaN and inf rows propagate as NaN)
+#pragma unroll
+      for (int rr = 0; rr < 2; ++rr) {
+        float mx = 0.0f;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const float as = fabsf(sv[rr][g]);
+          mx = (as > mx || as != as) ? as : mx;
+        }
+        if (!(mx <= 3.0e38f)) mx = INFINITY;
+        atomicMax(&rowmax[nrow0 + 2 * kh + rr], __float_as_uint(mx));
+      }
+      __syncthreads();
+      if (tid < kBB) {
+        const float mv = __uint_as_float(rowmax[tid]);
+        int ex = 0;
+        if (mv > 0.0f && mv <= 3.0e38f) frexpf(mv, &ex);
+        const int re = (mv > 0.0f && mv <= 3.0e38f) ? 22 - ex : (mv == 0.0f ? 0 : 1000);
+        rowexp[tid] = re;
+        rowmax[tid] = 0u;
+        cluster::store_coherent(
+            reinterpret_cast<unsigned *>(cl.xe + (static_cast<size_t>(par) * cl.Bpad + b0 + tid) * G + m0),
+            static_cast<unsigned>(re));
+      }
+      __syncthreads();
+#pragma unroll
+      for (int rr = 0; rr < 2; ++rr) {
+        const int nr = nrow0 + 2 * kh + rr, b = b0 + nr;
+        const int ex = rowexp[nr];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          int q = 0;
+          if (ex != 1000) q = static_cast<int>(rintf(ldexpf(sv[rr][g], ex)));
+          const int uq = q + (1 << 23);
+          unsigned char *dst = reinterpret_cast<unsigned char *>(cl.xp) +
+                               (static_cast<size_t>(par) * 3 * cl.Bpad + b) * C + 256 * m0 + 64 * g +
+                               16 * utl + l % 16;
+          cluster::store_bytes_coherent(dst, (uq & 255) - 128);
+          cluster::store_bytes_coherent(dst + pstride, ((uq >> 8) & 255) - 128);
+          cluster::store_bytes_coherent(dst + 2 * pstride, (uq >> 16) - 128);
+        }
+      }
+      alive = cluster::sync(counter, ++epoch * G, cl.timeout);
+      if (!alive) break;
+      // dh of the tile's rows, this wave's K-half, member by member
+      double dsum[4] = {0.0, 0.0, 0.0, 0.0};
+      const int8_t *arow = cl.xp + (static_cast<size_t>(par) * 3 * cl.Bpad + b0 + l % 16) * C +
+                           16 * (l / 16);
+      for (int m = mlo; m < mhi; ++m) {
+        v4i afr[4][3];
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4)
+#pragma unroll
+          for (int p = 0; p < 3; ++p) {
+            const int4 v = cluster::load_coherent16(arow + p * pstride + 64 * (4 * m + s4));
+            afr[s4][p] = v4i{v.x, v.y, v.z, v.w};
+          }
+        int exr[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          exr[r] = static_cast<int>(__hip_atomic_load(
+              reinterpret_cast<const unsigned *>(cl.xe + (static_cast<size_t>(par) * cl.Bpad + b0 +
+                                                           nrow0 + r) * G + m),
+              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        v4i acc[3];
+#pragma unroll
+        for (int p = 0; p < 3; ++p) acc[p] = v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) {
+          const v4i bf = wl[(utl * KS2 + 4 * m + s4) * 64 + l];
+#pragma unroll
+          for (int p = 0; p < 3; ++p) acc[p] = mfma_i8(afr[s4][p], bf, acc[p]);
+        }
+        const double cs = static_cast<double>(cl.csum[static_cast<size_t>(m) * H + j]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const double comb = 65536.0 * acc[2][r] + 256.0 * acc[1][r] + static_cast<double>(acc[0][r]) +
+                              32896.0 * cs;
+          dsum[r] += exr[r] == 1000 ? static_cast<double>(NAN) : ldexp(comb, -exr[r]);
+        }
+      }
+      double *dr = dred + (static_cast<size_t>(w) * 64 + l) * 4;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dr[r] = dsum[r];
+      __syncthreads();
+#pragma unroll
+      for (int rr = 0; rr < 2; ++rr) {
+        const int r = 2 * kh + rr;
+        const double lo = dred[(static_cast<size_t>(utl) * 64 + l) * 4 + r];
+        const double hi = dred[(static_cast<size_t>(utl + 4) * 64 + l) * 4 + r];
+        dh[rr] = static_cast<float>(lo + hi);
+      }
+    }
+    if (!alive) break;
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) {
+      const int b = b0 + nrow0 + 2 * kh + rr;
+      if (b >= B) continue;
+      const uint32_t o = static_cast<uint32_t>(b) * H + j;
+      a.dh0[o] = dh[rr] * keepf(a.h0_m, o);
+      a.dc0[o] = dc[rr] * keepf(a.c0_m, o);
+    }
+  }
+}
+
+size_t bwd_cl_lds(int KS2) {
+  return sizeof(v4i) * 4 * static_cast<size_t>(KS2) * 64 + sizeof(double) * 8 * 64 * 4 +
+         2 * sizeof(int) * kBB;
+}
+
 size_t bwd_lds(int H, int KS2) {
   return sizeof(float) * kBB * static_cast<size_t>(H) + 2 * sizeof(int) * kBB +
          static_cast<size_t>(kPlanes) * kBB * (KS2 * 64 + 16);
@@ -324,7 +576,8 @@ __global__ __launch_bounds__(256) void lstm_bwd_finish(int64_t nx, float *dx, co
 }
 
 struct BwdWorkspace {
-  size_t dli, dlh, xd, wid, hprev, frag, colsum, swih, swhh, aug_ih, aug_hh, part, total;
+  size_t dli, dlh, xd, wid, hprev, frag, colsum, swih, swhh, aug_ih, aug_hh, part, wfrag_cl, csum,
+      xp, xe, sync, total;
   BwdWorkspace(int T, int B, int I, int H) {
     const size_t C = 4 * static_cast<size_t>(H), M = static_cast<size_t>(T) * B;
     const size_t KS2 = (C + 63) / 64;
@@ -343,6 +596,13 @@ struct BwdWorkspace {
     aug_hh = o; o += al(sizeof(float) * C * (H + 1));
     const size_t S = static_cast<size_t>(blas::splitk_chunks(static_cast<int64_t>(M)));
     part = o; o += al(sizeof(float) * S * C * (static_cast<size_t>(I) > H ? I + 1 : H + 1));
+    // clustered recurrence (H a multiple of 64)
+    const size_t Bpad = (static_cast<size_t>(B) + kBB - 1) / kBB * kBB, G = H / kBcUnits + 1;
+    wfrag_cl = o; o += al(sizeof(v4i) * 64 * (H / 16) * KS2);
+    csum = o; o += al(sizeof(float) * G * H);
+    xp = o; o += al(2 * 3 * Bpad * C);
+    xe = o; o += al(sizeof(int) * 2 * Bpad * G);
+    sync = o; o += al(sizeof(unsigned) * (Bpad / kBB + 1));
     total = o;
   }
 };
@@ -444,16 +704,64 @@ int rxmet_lstm_backward_quant(int32_t T, int32_t B, int32_t I, int32_t H,
   }
   ba.s_c = sp.c.dscale; ba.zp_c = sp.c.dzp; ba.s_t = sp.tanh_c.dscale; ba.zp_t = sp.tanh_c.dzp;
   ba.dli = dli; ba.dlh = dlh; ba.dh0 = dh0; ba.dc0 = dc0;
-  const size_t lds = bwd_lds(H, KS2);
-  {
+  bool clustered = false;
+  if (H % kBcUnits == 0 && std::getenv("RXMET_NO_CLUSTER") == nullptr) {
+    const void *fn = reinterpret_cast<const void *>(&lstm_bwd_recurrence_cl);
+    const size_t lds_cl = bwd_cl_lds(KS2);
+    int device = 0, ncu = 0, per_cu = 0;
+    RXMET_CHECK_HIP(hipGetDevice(&device));
+    RXMET_CHECK_HIP(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, device));
+    RXMET_CHECK_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        static_cast<int>(lds_cl)));
+    RXMET_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 512, lds_cl));
+    BwdClArgs cl;
+    cl.G = H / kBcUnits;
+    cl.ntiles = (B + kBB - 1) / kBB;
+    cl.Bpad = cl.ntiles * kBB;
+    int ncl = per_cu * ncu / cl.G;
+    if (ncl > cl.ntiles) ncl = cl.ntiles;
+    if (ncl >= 8) ncl -= ncl % 8;
+    if (ncl >= 1) {
+      cl.ncl = ncl;
+      v4i *wf = reinterpret_cast<v4i *>(wsb + ws.wfrag_cl);
+      float *cs = reinterpret_cast<float *>(wsb + ws.csum);
+      cl.wfrag = wf;
+      cl.csum = cs;
+      cl.xp = reinterpret_cast<int8_t *>(wsb + ws.xp);
+      cl.xe = reinterpret_cast<int *>(wsb + ws.xe);
+      cl.counters = reinterpret_cast<unsigned *>(wsb + ws.sync);
+      cl.timeout = reinterpret_cast<int *>(cl.counters + ncl);
+      hipLaunchKernelGGL(lstm_pack_whh_t_cl, dim3((H / 16) * KS2), dim3(64), 0, stream, H, KS2,
+                         sv.w_hh_q, wf, cs);
+      RXMET_CHECK_LAUNCH();
+      hipLaunchKernelGGL(cluster::zero_words, dim3(1), dim3(256), 0, stream, cl.counters, ncl + 1);
+      RXMET_CHECK_LAUNCH();
+      void *args[] = {&ba, &cl};
+      {
+        rxmet::prof::Scope ps__("lstm_bwd_recurrence", stream);
+        RXMET_CHECK_HIP(hipLaunchCooperativeKernel(fn, dim3(ncl * cl.G), dim3(512), args,
+                                                   static_cast<unsigned>(lds_cl), stream));
+      }
+      const int64_t n_state = static_cast<int64_t>(B) * H;
+      hipLaunchKernelGGL(cluster::poison_nan, dim3(64), dim3(256), 0, stream, cl.timeout, n_state,
+                         dh0);
+      RXMET_CHECK_LAUNCH();
+      hipLaunchKernelGGL(cluster::poison_nan, dim3(64), dim3(256), 0, stream, cl.timeout, n_state,
+                         dc0);
+      RXMET_CHECK_LAUNCH();
+      clustered = true;
+    }
+  }
+  if (!clustered) {
+    const size_t lds = bwd_lds(H, KS2);
     rxmet::prof::Scope ps__("lstm_bwd_recurrence", stream);
     RXMET_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&lstm_bwd_recurrence),
                                         hipFuncAttributeMaxDynamicSharedMemorySize,
                                         static_cast<int>(lds)));
     hipLaunchKernelGGL(lstm_bwd_recurrence, dim3((B + kBB - 1) / kBB),
                        dim3(64 * ((UT + kTPW - 1) / kTPW)), lds, stream, ba);
+    RXMET_CHECK_LAUNCH();
   }
-  RXMET_CHECK_LAUNCH();
 
   int device = 0;
   RXMET_CHECK_HIP(hipGetDevice(&device));

@@ -323,3 +323,37 @@ def test_clustered_recurrence_matches_oracle_and_single_tile_path(cuda, shape, c
     assert torch.equal(out, out2) and torch.equal(hn, hn2) and torch.equal(cn, cn2)
     for k in saved:
         assert torch.equal(saved[k], saved2[k]), k
+
+
+@pytest.mark.parametrize("shape,cfg_name", [((3, 2560, 16, 128), "c4"), ((2, 100, 24, 256), "c4"),
+                                            ((3, 40, 8, 128), "16b-act"),
+                                            ((3, 20, 64, 512), "pot2-gate")])
+def test_clustered_backward_matches_oracle_and_single_tile_path(cuda, shape, cfg_name,
+                                                                monkeypatch):
+    """H a multiple of 64 takes the clustered backward (members exchange block-fixed-point
+    gate gradients, one exponent per sequence and member); it must match the oracle within
+    1e-4 and the one-workgroup-per-tile backward."""
+    T, B, I, H = shape
+    args, _, p = _case(T, B, I, H, cfg_name, 43, True, True)
+    Wi, Wh, bi, bh, x, h0, c0 = args
+    o = O.forward_quant(Wi, Wh, bi, bh, x, p, h0, c0, mode=O.ACT_CR)
+    _, _, _, saved = _gpu_forward(cuda, args, p, True)
+    go, gh, gc = _grads(T, B, H, 44)
+    exp = O.backward_quant(o, p, go, gh, gc)
+    got = _gpu_backward(cuda, saved, p, go, gh, gc)
+    _assert_grads(got, exp)
+    monkeypatch.setenv("RXMET_NO_CLUSTER", "1")
+    ref = _gpu_backward(cuda, saved, p, go, gh, gc)
+    _assert_grads(got, ref)
+
+
+def test_clustered_backward_nan_stays_in_its_sequence(cuda):
+    T, B, I, H = 3, 32, 5, 128
+    args, _, p = _case(T, B, I, H, "default", 45, True, False)
+    _, _, _, saved = _gpu_forward(cuda, args, p, True)
+    go = np.full((T, B, H), 1e-2, f32)
+    go[2, 3, 7] = np.nan
+    got = _gpu_backward(cuda, saved, p, go, None, None)
+    assert np.isnan(got["dh0"][3]).any() or np.isnan(got["dc0"][3]).any()
+    assert np.isfinite(np.delete(got["dh0"], 3, axis=0)).all()
+    assert np.isfinite(np.delete(got["dc0"], 3, axis=0)).all()
