@@ -167,6 +167,28 @@ int rxmet_gru_forward_quant(int32_t is_training, int32_t T, int32_t B, int32_t I
                             uint8_t *h_mask, void *workspace, void *stream);
 
 /*
+ * Both directions of a bidirectional layer in one call.  No counterpart in the reference,
+ * which calls forward_quant_float_storage once per direction; it is for QuantGRU's
+ * bidirectional forward: the per-direction prologues run first, then one clustered
+ * recurrence launch covers both directions so their sequential steps overlap.  dirs[k]
+ * holds exactly the arguments of one rxmet_gru_forward_quant call (its own workspace of
+ * rxmet_gru_forward_workspace_bytes(T, B, I, H) bytes); the results equal ndir separate
+ * calls.  ndir is 1 or 2.
+ */
+typedef struct rxmet_gru_fwd_dir {
+  const float *W, *R, *bw, *br, *x, *h0;
+  const rxmet_gru_qparams *params;
+  float *h, *v, *W_q, *R_q, *bw_q, *br_q, *x_q;
+  uint8_t *x_mask, *h0_mask, *W_mask, *R_mask, *bw_mask, *br_mask, *ih_mask, *hh_mask,
+      *gate_in_mask, *gate_out_mask, *h_mask;
+  void *workspace;
+} rxmet_gru_fwd_dir;
+
+int rxmet_gru_forward_quant_dirs(int32_t ndir, int32_t is_training, int32_t T, int32_t B,
+                                 int32_t I, int32_t H, const rxmet_gru_fwd_dir *dirs,
+                                 void *stream);
+
+/*
  * Quantised backward: backward_quant_float_storage_wrapper
  * (gru_interface_binding.cc:789-920) + quantGRUBackward / BackwardPassQuant::Run
  * (src/gru_backward_gpu_quant.cu:379-493).  Inputs are the forward's outputs; unlike
@@ -186,6 +208,25 @@ int rxmet_gru_backward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const f
                              const uint8_t *gate_in_mask, const uint8_t *gate_out_mask,
                              const uint8_t *h_mask, float *dx, float *dW, float *dR, float *dbw,
                              float *dbr, float *dh0, void *workspace, void *stream);
+
+/*
+ * Both directions' backward in one call (no counterpart in the reference, which calls
+ * backward_quant_float_storage once per direction): one clustered recurrence launch covers
+ * both directions, then each direction's bias fold, weight-gradient GEMMs and masks.
+ * dirs[k] holds exactly the arguments of one rxmet_gru_backward_quant call; the results
+ * equal ndir separate calls.  ndir is 1 or 2.
+ */
+typedef struct rxmet_gru_bwd_dir {
+  const float *W_q, *R_q, *bw_q, *br_q, *x_q, *dh_new, *h, *v;
+  const rxmet_gru_qparams *params;
+  const uint8_t *x_mask, *h0_mask, *W_mask, *R_mask, *bw_mask, *br_mask, *ih_mask, *hh_mask,
+      *gate_in_mask, *gate_out_mask, *h_mask;
+  float *dx, *dW, *dR, *dbw, *dbr, *dh0;
+  void *workspace;
+} rxmet_gru_bwd_dir;
+
+int rxmet_gru_backward_quant_dirs(int32_t ndir, int32_t T, int32_t B, int32_t I, int32_t H,
+                                  const rxmet_gru_bwd_dir *dirs, void *stream);
 
 /*
  * Float GRU forward with MinMax calibration statistics: forwardWithCalibrationGPU

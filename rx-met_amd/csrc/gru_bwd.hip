@@ -107,6 +107,8 @@ struct BwdArgs {
   float *dp, *dq;            // [T, B, 3H]
   double *bias_partial;      // [numWG][2][3H]
   float *dh0;                // [B, H]
+  float *xch;                // clustered path: [2][Bpad][KP] exchanged dq * scale_R
+  const float *rt;           // clustered path: packed R_q values, see pack_rt_f32
 };
 
 constexpr int kPlanes = 3;
@@ -324,9 +326,7 @@ __global__ __launch_bounds__(512) void bwd_recurrence(BwdArgs a) {
 constexpr int kBwMaxKS2 = 12;  // 3H <= 768
 
 struct BwdClArgs {
-  int ncl, G, UT, ntiles, Bpad, KP;  // KP = 3H padded to a multiple of 64
-  float *xch;                        // [2][Bpad][KP] exchanged dq * scale_R
-  const float *rt;                   // packed R_q values, see pack_rt_f32
+  int ncl, G, UT, ntiles, Bpad, KP, ndir;  // KP = 3H padded to a multiple of 64
   unsigned *counters;
   int *timeout;
 };
@@ -343,21 +343,23 @@ __global__ __launch_bounds__(64) void pack_rt_f32(int H, int KS2, const float *_
   rt[static_cast<size_t>(idx) * 64 + l] = k < 3 * H ? Rq[static_cast<size_t>(j) * 3 * H + k] : 0.0f;
 }
 
-__global__ __launch_bounds__(512) void bwd_recurrence_cl(BwdArgs a, BwdClArgs cl) {
+// One (direction, batch tile) pair, run by one member; writes the pair's bias partials.
+__device__ __forceinline__ void bwd_cl_pair(const BwdArgs &a, const BwdClArgs &cl, int tile,
+                                            int member, unsigned *counter, unsigned &epoch,
+                                            bool &alive) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int H = a.H, C = 3 * H, B = a.B, KS2 = a.KS2, KP = cl.KP;
   v4f *red = reinterpret_cast<v4f *>(smem);                          // [UT][4][64]
   double *bred = reinterpret_cast<double *>(smem + 16 * 1024);       // [UT][4][16][6]
   const int tid = threadIdx.x, w = tid / 64, l = tid % 64;
   const int utl = w / 4, kq = w % 4;
-  const cluster::Place pl = cluster::place(cl.G, cl.ncl);
-  const int ut = pl.member * cl.UT + utl;
+  const int ut = member * cl.UT + utl;
   const int j = 16 * ut + l % 16;
   const int nr = 4 * (l / 16) + kq;
   float rtv[4 * kBwMaxKS2];
 #pragma unroll
   for (int i = 0; i < 4 * kBwMaxKS2; ++i)
-    rtv[i] = i < 4 * KS2 ? cl.rt[((static_cast<size_t>(ut) * 4 + kq) * 4 * KS2 + i) * 64 + l] : 0.0f;
+    rtv[i] = i < 4 * KS2 ? a.rt[((static_cast<size_t>(ut) * 4 + kq) * 4 * KS2 + i) * 64 + l] : 0.0f;
   float effr[3];
   float mbw[3], mbr[3];
 #pragma unroll
@@ -367,13 +369,10 @@ __global__ __launch_bounds__(512) void bwd_recurrence_cl(BwdArgs a, BwdClArgs cl
     mbr[g] = a.br_m ? static_cast<float>(a.br_m[g * H + j]) : 1.0f;
   }
   double sbw[3] = {0.0, 0.0, 0.0}, sbr[3] = {0.0, 0.0, 0.0};
-  unsigned *counter = cl.counters + pl.cluster;
-  unsigned epoch = 0;
-  bool alive = true;
   const uint32_t BH = static_cast<uint32_t>(B) * H;
   v4f *myred = red + (static_cast<size_t>(utl) * 4 + kq) * 64;
 
-  for (int tile = pl.cluster; tile < cl.ntiles && alive; tile += cl.ncl) {
+  {
     const int b0 = tile * kBTile, b = b0 + nr;
     const bool valid = b < B;
     float dhc = 0.0f;
@@ -428,7 +427,7 @@ __global__ __launch_bounds__(512) void bwd_recurrence_cl(BwdArgs a, BwdClArgs cl
           sbr[gg] += static_cast<double>(dqv[gg] * mbr[gg]);
         }
       }
-      float *xrow = cl.xch + (static_cast<size_t>(par) * cl.Bpad + b) * KP;
+      float *xrow = a.xch + (static_cast<size_t>(par) * cl.Bpad + b) * KP;
 #pragma unroll
       for (int gg = 0; gg < 3; ++gg)
         cluster::store_coherent(reinterpret_cast<unsigned *>(xrow + gg * H + j),
@@ -438,7 +437,7 @@ __global__ __launch_bounds__(512) void bwd_recurrence_cl(BwdArgs a, BwdClArgs cl
       // dh += R_deq dq over this wave's quarter of the channels
       v4f acc = {0.f, 0.f, 0.f, 0.f};
       {
-        const float *arow = cl.xch + (static_cast<size_t>(par) * cl.Bpad + b0 + l % 16) * KP +
+        const float *arow = a.xch + (static_cast<size_t>(par) * cl.Bpad + b0 + l % 16) * KP +
                             16 * (kq * KS2) + 4 * (l / 16);
         int4 av[kBwMaxKS2];
 #pragma unroll
@@ -491,12 +490,25 @@ __global__ __launch_bounds__(512) void bwd_recurrence_cl(BwdArgs a, BwdClArgs cl
 #pragma unroll
       for (int e = 0; e < 6; ++e) x[e] += d[e];
     }
-    double *p = a.bias_partial + static_cast<size_t>(pl.cluster) * 2 * C;
+    double *p = a.bias_partial + static_cast<size_t>(tile) * 2 * C;
 #pragma unroll
     for (int gg = 0; gg < 3; ++gg) {
       p[gg * H + j] = x[gg];
       p[C + gg * H + j] = x[3 + gg];
     }
+  }
+}
+
+__global__ __launch_bounds__(512) void bwd_recurrence_cl(BwdArgs a0, BwdArgs a1, BwdClArgs cl) {
+  const cluster::Place pl = cluster::place(cl.G, cl.ncl);
+  unsigned *counter = cl.counters + pl.cluster;
+  unsigned epoch = 0;
+  bool alive = true;
+  for (int pair = pl.cluster; pair < cl.ndir * cl.ntiles && alive; pair += cl.ncl) {
+    const int d = pair / cl.ntiles, tile = pair % cl.ntiles;
+    __syncthreads();
+    // one copy of the step code for both directions (d is uniform across the workgroup)
+    bwd_cl_pair(d == 0 ? a0 : a1, cl, tile, pl.member, counter, epoch, alive);
   }
 }
 
@@ -565,17 +577,232 @@ struct BwdWorkspace {
     const size_t Bpad = nwg * kBTile;
     xch = o; o += al(sizeof(float) * 2 * Bpad * KS2 * 64);
     rt = o; o += al(sizeof(float) * ((H + 15) / 16) * 4 * 4 * KS2 * 64);
-    sync = o; o += al(sizeof(unsigned) * (nwg + 1));
+    sync = o; o += al(sizeof(unsigned) * (2 * nwg + 2));  // clusters of both directions
     total = o;
   }
 };
+
+// One direction's backward state between the phases.
+struct BwdPlan {
+  BwdArgs ba;
+  const rxmet_gru_bwd_dir *d;
+  char *wsb;
+  float *xd, *wd;
+};
+
+static int backward_prologue(int T, int B, int I, int H, const rxmet_gru_bwd_dir &d,
+                             hipStream_t stream, BwdPlan *plan) {
+  const rxmet_gru_qparams *params = d.params;
+  RXMET_CHECK_ARG(params != nullptr, "params must be non-null");
+  RXMET_CHECK_ARG(params->hidden == H, "params.hidden != hidden_size");
+  RXMET_CHECK_ARG(d.W_q && d.R_q && d.x_q && d.dh_new && d.h && d.v && d.dx && d.dW && d.dR &&
+                      d.dbw && d.dbr && d.dh0 && d.workspace,
+                  "required pointer is null");
+  RXMET_CHECK_ARG(params->chan_bits[RXMET_GRU_R] <= 8 && !params->chan_unsigned[RXMET_GRU_R],
+                  "recurrent weights wider than signed 8 bits are not supported");
+  const int C = 3 * H;
+  const int KS2 = (C + 63) / 64;
+  const BwdWorkspace ws(T, B, I, H);
+  char *wsb = static_cast<char *>(d.workspace);
+  float *effr = reinterpret_cast<float *>(wsb + ws.effr);
+  float *effw = reinterpret_cast<float *>(wsb + ws.effw);
+  plan->xd = reinterpret_cast<float *>(wsb + ws.xd);
+  plan->wd = reinterpret_cast<float *>(wsb + ws.wd);
+  std::vector<float> host(8 * static_cast<size_t>(C));
+  try {
+    make_channel_factors(*params, H, host.data() + 4 * C, host.data() + 5 * C, host.data() + 6 * C,
+                         host.data() + 7 * C, host.data(), host.data() + C, host.data() + 2 * C,
+                         host.data() + 3 * C);
+  } catch (const std::exception &e) {
+    set_error(e.what());
+    return -22;
+  }
+  RXMET_CHECK_HIP(hipMemcpyAsync(effw, host.data(), sizeof(float) * C, hipMemcpyHostToDevice, stream));
+  RXMET_CHECK_HIP(hipMemcpyAsync(effr, host.data() + C, sizeof(float) * C, hipMemcpyHostToDevice,
+                                 stream));
+  const float eff_x = effective_scale(params->g[RXMET_GRU_X].scale, params->use_pot2 != 0);
+  const float zp_x = static_cast<float>(params->g[RXMET_GRU_X].zero_point);
+  const int64_t nx = static_cast<int64_t>(T) * B * I, nw = static_cast<int64_t>(I) * C;
+  int64_t blocks = (nx + nw + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  {
+    rxmet::prof::Scope ps__("gru_bwd_dequant_inputs", stream);
+    hipLaunchKernelGGL(dequant_inputs, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, nx,
+                       nw, C, d.x_q, eff_x, zp_x, d.W_q, effw, plan->xd, plan->wd);
+  }
+  RXMET_CHECK_LAUNCH();
+  BwdArgs &ba = plan->ba;
+  ba.T = T; ba.B = B; ba.H = H; ba.KS2 = KS2;
+  ba.dh_new = d.dh_new; ba.h = d.h; ba.v = d.v;
+  ba.ih_m = d.ih_mask; ba.hh_m = d.hh_mask; ba.gin_m = d.gate_in_mask; ba.gout_m = d.gate_out_mask;
+  ba.h_m = d.h_mask; ba.bw_m = d.bw_mask; ba.br_m = d.br_mask; ba.h0_m = d.h0_mask;
+  ba.rfrag = reinterpret_cast<v4i *>(wsb + ws.rfrag);
+  ba.rowsum = reinterpret_cast<float *>(wsb + ws.rowsum);
+  ba.eff_r = effr;
+  ba.dp = reinterpret_cast<float *>(wsb + ws.dp);
+  ba.dq = reinterpret_cast<float *>(wsb + ws.dq);
+  ba.bias_partial = reinterpret_cast<double *>(wsb + ws.bias);
+  ba.dh0 = d.dh0;
+  ba.xch = reinterpret_cast<float *>(wsb + ws.xch);
+  ba.rt = reinterpret_cast<float *>(wsb + ws.rt);
+  plan->d = &d;
+  plan->wsb = wsb;
+  return 0;
+}
+
+// Clustered recurrence over every direction; 1 when launched, 0 when the caller must use the
+// per-tile recurrence.
+static int backward_recurrence_clustered(BwdPlan *plans, int ndir, int T, int B, int I, int H,
+                                         hipStream_t stream) {
+  const int C = 3 * H, KS2 = (C + 63) / 64;
+  if (KS2 > kBwMaxKS2 || std::getenv("RXMET_NO_CLUSTER") != nullptr) return 0;
+  const void *fn = reinterpret_cast<const void *>(&bwd_recurrence_cl);
+  const size_t lds_cl = 16 * 1024 + sizeof(double) * 2 * 4 * 16 * 6;
+  int device = 0, ncu = 0;
+  RXMET_CHECK_HIP(hipGetDevice(&device));
+  RXMET_CHECK_HIP(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, device));
+  RXMET_CHECK_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      static_cast<int>(lds_cl)));
+  BwdClArgs cl;
+  cl.ndir = ndir;
+  cl.ntiles = (B + kBTile - 1) / kBTile;
+  cl.Bpad = cl.ntiles * kBTile;
+  cl.KP = KS2 * 64;
+  const int pairs = ndir * cl.ntiles;
+  // the smallest unit slice per workgroup whose grid fits one workgroup per CU, else the
+  // largest slice
+  int chosen = 0, ncl = 0;
+  for (int UT = 1; UT <= 2 && !chosen; ++UT) {
+    if ((H / 16) % UT) continue;
+    const int G = H / (16 * UT);
+    if (static_cast<int64_t>(pairs) * G <= ncu || UT == 2) {
+      chosen = UT;
+      cl.G = G;
+    }
+  }
+  if (!chosen) return 0;
+  int per_cu = 0;
+  RXMET_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256 * chosen, lds_cl));
+  ncl = per_cu * ncu / cl.G;
+  if (ncl < 1) return 0;
+  if (ncl > pairs) ncl = pairs;
+  if (ncl >= 8) ncl -= ncl % 8;
+  cl.UT = chosen;
+  cl.ncl = ncl;
+  const BwdWorkspace ws(T, B, I, H);
+  cl.counters = reinterpret_cast<unsigned *>(plans[0].wsb + ws.sync);
+  cl.timeout = reinterpret_cast<int *>(cl.counters + ncl);
+  for (int k = 0; k < ndir; ++k) {
+    hipLaunchKernelGGL(pack_rt_f32, dim3((H / 16) * 4 * 4 * KS2), dim3(64), 0, stream, H, KS2,
+                       plans[k].d->R_q, const_cast<float *>(plans[k].ba.rt));
+    RXMET_CHECK_LAUNCH();
+    // padding channels of the exchange rows stay zero
+    const int64_t nx = static_cast<int64_t>(2) * cl.Bpad * cl.KP;
+    hipLaunchKernelGGL(zero_floats, dim3(256), dim3(256), 0, stream, nx, plans[k].ba.xch);
+    RXMET_CHECK_LAUNCH();
+  }
+  hipLaunchKernelGGL(cluster::zero_words, dim3(1), dim3(256), 0, stream, cl.counters, ncl + 1);
+  RXMET_CHECK_LAUNCH();
+  BwdArgs &a1 = plans[ndir > 1 ? 1 : 0].ba;
+  void *args[] = {&plans[0].ba, &a1, &cl};
+  {
+    rxmet::prof::Scope ps__("gru_bwd_recurrence", stream);
+    RXMET_CHECK_HIP(hipLaunchCooperativeKernel(fn, dim3(ncl * cl.G), dim3(256 * cl.UT), args,
+                                               static_cast<unsigned>(lds_cl), stream));
+  }
+  for (int k = 0; k < ndir; ++k) {
+    hipLaunchKernelGGL(cluster::poison_nan, dim3(64), dim3(256), 0, stream, cl.timeout,
+                       static_cast<int64_t>(B) * H, plans[k].ba.dh0);
+    RXMET_CHECK_LAUNCH();
+  }
+  return 1;
+}
+
+static int backward_recurrence_tiles(BwdPlan &plan, int B, int H, hipStream_t stream) {
+  const int C = 3 * H, KS2 = (C + 63) / 64;
+  hipLaunchKernelGGL(pack_rt_frags, dim3((H / 16) * KS2), dim3(64), 0, stream, H, KS2,
+                     plan.d->R_q, const_cast<v4i *>(plan.ba.rfrag),
+                     const_cast<float *>(plan.ba.rowsum));
+  RXMET_CHECK_LAUNCH();
+  const int nwg = (B + kBTile - 1) / kBTile;
+  const size_t lds = bwd_lds_bytes(KS2);
+  RXMET_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&bwd_recurrence),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      static_cast<int>(lds)));
+  rxmet::prof::Scope ps__("gru_bwd_recurrence", stream);
+  hipLaunchKernelGGL(bwd_recurrence, dim3(nwg), dim3(64 * ((H + 31) / 32)), lds, stream, plan.ba);
+  RXMET_CHECK_LAUNCH();
+  return 0;
+}
+
+static int backward_epilogue(int T, int B, int I, int H, BwdPlan &plan, hipStream_t stream) {
+  const rxmet_gru_bwd_dir &d = *plan.d;
+  const int C = 3 * H;
+  const BwdWorkspace ws(T, B, I, H);
+  const int nwg = (B + kBTile - 1) / kBTile;
+  hipLaunchKernelGGL(fold_bias, dim3((C + 255) / 256), dim3(256), 0, stream, nwg, C,
+                     plan.ba.bias_partial, d.dbw, d.dbr);
+  RXMET_CHECK_LAUNCH();
+  int device = 0;
+  RXMET_CHECK_HIP(hipGetDevice(&device));
+  rocblas_handle bh = blas::handle(device);
+  RXMET_CHECK_ARG(bh != nullptr, "rocBLAS handle creation failed");
+  rocblas_set_stream(bh, stream);
+  const int M = T * B;
+  float *part = reinterpret_cast<float *>(plan.wsb + ws.part);
+  {
+    rxmet::prof::Scope ps__("gru_bwd_weight_gemms", stream);
+    // dx[M][I] = dp[M][C] * W_deq^T
+    RXMET_CHECK_ARG(blas::gemm_rm(bh, false, true, M, I, C, plan.ba.dp, C, plan.wd, C, d.dx, I) ==
+                        rocblas_status_success,
+                    "rocBLAS sgemm (dx) failed");
+    // dW[I][C] = x_deq^T * dp and dR[H][C] = h_prev^T * dq (h rows 0..T-1), split over K
+    const int S = blas::splitk_chunks(M);
+    if (int rc = blas::gemm_tn_splitk(bh, I, C, M, plan.xd, I, plan.ba.dp, C, d.dW, part, S, stream))
+      return rc;
+    if (int rc = blas::gemm_tn_splitk(bh, H, C, M, d.h, H, plan.ba.dq, C, d.dR, part, S, stream))
+      return rc;
+  }
+  const int64_t n0 = static_cast<int64_t>(T) * B * I, n1 = static_cast<int64_t>(I) * C,
+                n2 = static_cast<int64_t>(H) * C;
+  int64_t blocks = (n0 + n1 + n2 + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  {
+    rxmet::prof::Scope ps__("gru_bwd_apply_masks", stream);
+    hipLaunchKernelGGL(apply_masks, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, n0, n1,
+                       n2, d.dx, d.x_mask, d.dW, d.W_mask, d.dR, d.R_mask);
+  }
+  RXMET_CHECK_LAUNCH();
+  return 0;
+}
+
+static int backward_dirs(int ndir, int T, int B, int I, int H, const rxmet_gru_bwd_dir *dirs,
+                         hipStream_t stream) {
+  RXMET_CHECK_ARG(ndir == 1 || ndir == 2, "ndir must be 1 or 2");
+  RXMET_CHECK_ARG(dirs != nullptr, "dirs must be non-null");
+  RXMET_CHECK_ARG(T >= 1 && B >= 1 && I >= 1 && H >= 1, "dimensions must be positive");
+  RXMET_CHECK_ARG(H % 16 == 0 && H <= 256,
+                  "hidden_size must be a multiple of 16 and at most 256 for the MFMA recurrence");
+  RXMET_CHECK_ARG(static_cast<double>(T + 1) * B * 4 * H < 4294967295.0,
+                  "T*B*H too large for the recurrence's 32-bit element offsets");
+  BwdPlan plans[2];
+  for (int k = 0; k < ndir; ++k)
+    if (int rc = backward_prologue(T, B, I, H, dirs[k], stream, &plans[k])) return rc;
+  const int rc = backward_recurrence_clustered(plans, ndir, T, B, I, H, stream);
+  if (rc < 0) return rc;
+  if (rc == 0)
+    for (int k = 0; k < ndir; ++k)
+      if (int r = backward_recurrence_tiles(plans[k], B, H, stream)) return r;
+  for (int k = 0; k < ndir; ++k)
+    if (int r = backward_epilogue(T, B, I, H, plans[k], stream)) return r;
+  return 0;
+}
 
 }  // namespace gru
 }  // namespace rxmet
 
 using namespace rxmet;
 using namespace rxmet::gru;
-using namespace rxmet::blas;
 
 extern "C" {
 
@@ -595,175 +822,17 @@ int rxmet_gru_backward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const f
                              const uint8_t *gate_in_mask, const uint8_t *gate_out_mask,
                              const uint8_t *h_mask, float *dx, float *dW, float *dR, float *dbw,
                              float *dbr, float *dh0, void *workspace, void *stream_) {
-  (void)bw_q;
-  (void)br_q;
   clear_error();
-  RXMET_CHECK_ARG(params != nullptr, "params must be non-null");
-  RXMET_CHECK_ARG(T >= 1 && B >= 1 && I >= 1 && H >= 1, "dimensions must be positive");
-  RXMET_CHECK_ARG(params->hidden == H, "params.hidden != hidden_size");
-  RXMET_CHECK_ARG(H % 16 == 0 && H <= 256,
-                  "hidden_size must be a multiple of 16 and at most 256 for the MFMA recurrence");
-  RXMET_CHECK_ARG(W_q && R_q && x_q && dh_new && h && v && dx && dW && dR && dbw && dbr && dh0 &&
-                      workspace,
-                  "required pointer is null");
-  RXMET_CHECK_ARG(params->chan_bits[RXMET_GRU_R] <= 8 && !params->chan_unsigned[RXMET_GRU_R],
-                  "recurrent weights wider than signed 8 bits are not supported");
-  RXMET_CHECK_ARG(static_cast<double>(T + 1) * B * 4 * H < 4294967295.0,
-                  "T*B*H too large for the recurrence's 32-bit element offsets");
-  hipStream_t stream = static_cast<hipStream_t>(stream_);
-  const int C = 3 * H;
-  const int KS2 = (C + 63) / 64;
-  const BwdWorkspace ws(T, B, I, H);
-  char *wsb = static_cast<char *>(workspace);
-  float *dp = reinterpret_cast<float *>(wsb + ws.dp);
-  float *dq = reinterpret_cast<float *>(wsb + ws.dq);
-  float *xd = reinterpret_cast<float *>(wsb + ws.xd);
-  float *wd = reinterpret_cast<float *>(wsb + ws.wd);
-  v4i *rfrag = reinterpret_cast<v4i *>(wsb + ws.rfrag);
-  float *rowsum = reinterpret_cast<float *>(wsb + ws.rowsum);
-  float *effr = reinterpret_cast<float *>(wsb + ws.effr);
-  float *effw = reinterpret_cast<float *>(wsb + ws.effw);
-  double *bias = reinterpret_cast<double *>(wsb + ws.bias);
-  float *part = reinterpret_cast<float *>(wsb + ws.part);
+  const rxmet_gru_bwd_dir d = {W_q, R_q, bw_q, br_q, x_q, dh_new, h, v, params, x_mask, h0_mask,
+                               W_mask, R_mask, bw_mask, br_mask, ih_mask, hh_mask, gate_in_mask,
+                               gate_out_mask, h_mask, dx, dW, dR, dbw, dbr, dh0, workspace};
+  return backward_dirs(1, T, B, I, H, &d, static_cast<hipStream_t>(stream_));
+}
 
-  std::vector<float> host(8 * static_cast<size_t>(C));
-  try {
-    make_channel_factors(*params, H, host.data() + 4 * C, host.data() + 5 * C, host.data() + 6 * C,
-                         host.data() + 7 * C, host.data(), host.data() + C, host.data() + 2 * C,
-                         host.data() + 3 * C);
-  } catch (const std::exception &e) {
-    set_error(e.what());
-    return -22;
-  }
-  RXMET_CHECK_HIP(hipMemcpyAsync(effw, host.data(), sizeof(float) * C, hipMemcpyHostToDevice, stream));
-  RXMET_CHECK_HIP(hipMemcpyAsync(effr, host.data() + C, sizeof(float) * C, hipMemcpyHostToDevice,
-                                 stream));
-  const float eff_x = effective_scale(params->g[RXMET_GRU_X].scale, params->use_pot2 != 0);
-  const float zp_x = static_cast<float>(params->g[RXMET_GRU_X].zero_point);
-
-  const int64_t nx = static_cast<int64_t>(T) * B * I, nw = static_cast<int64_t>(I) * C;
-  int64_t blocks = (nx + nw + 255) / 256;
-  if (blocks > 8192) blocks = 8192;
-  {
-    rxmet::prof::Scope ps__("gru_bwd_dequant_inputs", stream);
-    hipLaunchKernelGGL(dequant_inputs, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, nx,
-                       nw, C, x_q, eff_x, zp_x, W_q, effw, xd, wd);
-  }
-  RXMET_CHECK_LAUNCH();
-  hipLaunchKernelGGL(pack_rt_frags, dim3((H / 16) * KS2), dim3(64), 0, stream, H, KS2, R_q, rfrag,
-                     rowsum);
-  RXMET_CHECK_LAUNCH();
-
-  BwdArgs ba;
-  ba.T = T; ba.B = B; ba.H = H; ba.KS2 = KS2;
-  ba.dh_new = dh_new; ba.h = h; ba.v = v;
-  ba.ih_m = ih_mask; ba.hh_m = hh_mask; ba.gin_m = gate_in_mask; ba.gout_m = gate_out_mask;
-  ba.h_m = h_mask; ba.bw_m = bw_mask; ba.br_m = br_mask; ba.h0_m = h0_mask;
-  ba.rfrag = rfrag; ba.rowsum = rowsum; ba.eff_r = effr;
-  ba.dp = dp; ba.dq = dq; ba.bias_partial = bias; ba.dh0 = dh0;
-  const int nwg = (B + kBTile - 1) / kBTile;
-  if (KS2 <= kBwMaxKS2 && std::getenv("RXMET_NO_CLUSTER") == nullptr) {
-    const void *fn = reinterpret_cast<const void *>(&bwd_recurrence_cl);
-    const size_t lds_cl = 16 * 1024 + sizeof(double) * 2 * 4 * 16 * 6;
-    int device = 0, ncu = 0;
-    RXMET_CHECK_HIP(hipGetDevice(&device));
-    RXMET_CHECK_HIP(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, device));
-    RXMET_CHECK_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                        static_cast<int>(lds_cl)));
-    BwdClArgs cl;
-    cl.ntiles = nwg;
-    cl.Bpad = nwg * kBTile;
-    cl.KP = KS2 * 64;
-    int chosen = 0, ncl = 0;
-    for (int UT = 1; UT <= 2 && !chosen; ++UT) {
-      if ((H / 16) % UT) continue;
-      int per_cu = 0;
-      RXMET_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256 * UT, lds_cl));
-      const int G = H / (16 * UT);
-      ncl = per_cu * ncu / G;
-      if (ncl < 1) continue;
-      if (ncl >= cl.ntiles || UT == 2) {
-        chosen = UT;
-        cl.G = G;
-      }
-    }
-    if (chosen && ncl >= 1) {
-      if (ncl > cl.ntiles) ncl = cl.ntiles;
-      if (ncl >= 8) ncl -= ncl % 8;
-      cl.UT = chosen;
-      cl.ncl = ncl;
-      cl.xch = reinterpret_cast<float *>(wsb + ws.xch);
-      float *rt = reinterpret_cast<float *>(wsb + ws.rt);
-      cl.rt = rt;
-      cl.counters = reinterpret_cast<unsigned *>(wsb + ws.sync);
-      cl.timeout = reinterpret_cast<int *>(cl.counters + ncl);
-      hipLaunchKernelGGL(pack_rt_f32, dim3((H / 16) * 4 * 4 * KS2), dim3(64), 0, stream, H, KS2,
-                         R_q, rt);
-      RXMET_CHECK_LAUNCH();
-      // padding channels of the exchange rows stay zero
-      hipLaunchKernelGGL(cluster::zero_words, dim3(1), dim3(256), 0, stream, cl.counters, ncl + 1);
-      RXMET_CHECK_LAUNCH();
-      {
-        const int64_t nx = static_cast<int64_t>(2) * cl.Bpad * cl.KP;
-        hipLaunchKernelGGL(zero_floats, dim3(256), dim3(256), 0, stream, nx, cl.xch);
-        RXMET_CHECK_LAUNCH();
-      }
-      void *args[] = {&ba, &cl};
-      {
-        rxmet::prof::Scope ps__("gru_bwd_recurrence", stream);
-        RXMET_CHECK_HIP(hipLaunchCooperativeKernel(fn, dim3(ncl * cl.G), dim3(256 * cl.UT), args,
-                                                   static_cast<unsigned>(lds_cl), stream));
-      }
-      hipLaunchKernelGGL(cluster::poison_nan, dim3(64), dim3(256), 0, stream, cl.timeout,
-                         static_cast<int64_t>(B) * H, dh0);
-      RXMET_CHECK_LAUNCH();
-      hipLaunchKernelGGL(fold_bias, dim3((C + 255) / 256), dim3(256), 0, stream, ncl, C, bias, dbw,
-                         dbr);
-      RXMET_CHECK_LAUNCH();
-      goto weight_gemms;
-    }
-  }
-  {
-  const size_t lds = bwd_lds_bytes(KS2);
-  RXMET_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&bwd_recurrence),
-                                      hipFuncAttributeMaxDynamicSharedMemorySize,
-                                      static_cast<int>(lds)));
-  {
-    rxmet::prof::Scope ps__("gru_bwd_recurrence", stream);
-    hipLaunchKernelGGL(bwd_recurrence, dim3(nwg), dim3(64 * ((H + 31) / 32)), lds, stream, ba);
-  }
-  RXMET_CHECK_LAUNCH();
-  hipLaunchKernelGGL(fold_bias, dim3((C + 255) / 256), dim3(256), 0, stream, nwg, C, bias, dbw, dbr);
-  RXMET_CHECK_LAUNCH();
-  }
-
-weight_gemms:
-  int device = 0;
-  RXMET_CHECK_HIP(hipGetDevice(&device));
-  rocblas_handle bh = handle(device);
-  RXMET_CHECK_ARG(bh != nullptr, "rocBLAS handle creation failed");
-  rocblas_set_stream(bh, stream);
-  const int M = T * B;
-  {
-    rxmet::prof::Scope ps__("gru_bwd_weight_gemms", stream);
-    // dx[M][I] = dp[M][C] * W_deq^T
-    RXMET_CHECK_ARG(gemm_rm(bh, false, true, M, I, C, dp, C, wd, C, dx, I) == rocblas_status_success,
-                    "rocBLAS sgemm (dx) failed");
-    // dW[I][C] = x_deq^T * dp and dR[H][C] = h_prev^T * dq (h rows 0..T-1), split over K
-    const int S = splitk_chunks(M);
-    if (int rc = gemm_tn_splitk(bh, I, C, M, xd, I, dp, C, dW, part, S, stream)) return rc;
-    if (int rc = gemm_tn_splitk(bh, H, C, M, h, H, dq, C, dR, part, S, stream)) return rc;
-  }
-  const int64_t n0 = nx, n1 = nw, n2 = static_cast<int64_t>(H) * C;
-  blocks = (n0 + n1 + n2 + 255) / 256;
-  if (blocks > 8192) blocks = 8192;
-  {
-    rxmet::prof::Scope ps__("gru_bwd_apply_masks", stream);
-    hipLaunchKernelGGL(apply_masks, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, n0, n1,
-                       n2, dx, x_mask, dW, W_mask, dR, R_mask);
-  }
-  RXMET_CHECK_LAUNCH();
-  return 0;
+int rxmet_gru_backward_quant_dirs(int32_t ndir, int32_t T, int32_t B, int32_t I, int32_t H,
+                                  const rxmet_gru_bwd_dir *dirs, void *stream_) {
+  clear_error();
+  return backward_dirs(ndir, T, B, I, H, dirs, static_cast<hipStream_t>(stream_));
 }
 
 }  // extern "C"

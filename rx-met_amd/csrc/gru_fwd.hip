@@ -185,6 +185,7 @@ struct RecArgs {
   float *hout;              // [T+1, B, H] dequantised (row 0 written by quant_input)
   float *v;                 // [T, B, 4H] dequantised
   uint8_t *ih_m, *hh_m, *gin_m, *gout_m, *h_m;
+  int8_t *hx;               // clustered path: [2][NPL][Bpad][H] exchanged h codes
 };
 
 // R_q [H][3H] (fp32 codes) -> int8 B fragments of v_mfma_i32_16x16x64_i8:
@@ -425,14 +426,17 @@ __global__ __launch_bounds__(512) void recurrence(RecArgs a, StepParams p) {
 constexpr int kClMaxKPerWave = 4;  // K-steps per wave: H <= 1024
 
 struct ClArgs {
-  int ncl, G, UT, ntiles, Bpad;
-  int8_t *hx;          // [2][NPL][Bpad][H] centred h codes as int8 planes
-  unsigned *counters;  // [ncl]
+  int ncl, G, UT, ntiles, Bpad, ndir;  // clusters walk (direction, batch tile) pairs
+  unsigned *counters;                  // [ncl]
   int *timeout;
 };
 
+// One (direction, batch tile) pair of the clustered recurrence, run by one member.
 template <int NPL>
-__global__ __launch_bounds__(512) void recurrence_cl(RecArgs a, StepParams p, ClArgs cl) {
+__device__ __forceinline__ void recurrence_cl_pair(const RecArgs &a, const StepParams &p,
+                                                   const ClArgs &cl, int tile, int member,
+                                                   unsigned *counter, unsigned &epoch,
+                                                   bool &alive) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int H = a.H, C = 3 * H, B = a.B, KS = a.KS;
   float *lut_f = reinterpret_cast<float *>(smem);               // 3 * 16 * 3 (thr, qb, c)
@@ -440,8 +444,7 @@ __global__ __launch_bounds__(512) void recurrence_cl(RecArgs a, StepParams p, Cl
   v4i *red = reinterpret_cast<v4i *>(smem + 1024);              // [UT][4][3][NPL][64]
   const int tid = threadIdx.x, w = tid / 64, l = tid % 64;
   const int utl = w / 4, kq = w % 4;
-  const cluster::Place pl = cluster::place(cl.G, cl.ncl);
-  const int ut = pl.member * cl.UT + utl;
+  const int ut = member * cl.UT + utl;
   const int j = 16 * ut + l % 16;
   const int nr = 4 * (l / 16) + kq;  // batch row finished by this lane
 
@@ -465,22 +468,18 @@ __global__ __launch_bounds__(512) void recurrence_cl(RecArgs a, StepParams p, Cl
   for (int g = 0; g < 3; ++g)
 #pragma unroll
     for (int q = 0; q < kChanParams; ++q) cst[g][q] = a.chan[q * C + g * H + j];
-  __syncthreads();
 
   const float plane_off = 128.0f + a.h_offset;
   const size_t plane_stride = static_cast<size_t>(cl.Bpad) * H;
-  unsigned *counter = cl.counters + pl.cluster;
-  unsigned epoch = 0;
-  bool alive = true;
   v4i *myred = red + (static_cast<size_t>(utl) * 4 + kq) * 3 * NPL * 64;
 
-  for (int tile = pl.cluster; tile < cl.ntiles && alive; tile += cl.ncl) {
+  {
     const int b0 = tile * kTileB, b = b0 + nr;
     const bool valid = b < B;
     float hold = valid ? a.h0codes[static_cast<size_t>(b) * H + j] : p.zp_h;
     {
       const int hcv = static_cast<int>(hold - a.h_offset);
-      unsigned char *dst = reinterpret_cast<unsigned char *>(cl.hx) + static_cast<size_t>(b) * H + j;
+      unsigned char *dst = reinterpret_cast<unsigned char *>(a.hx) + static_cast<size_t>(b) * H + j;
 #pragma unroll
       for (int q = 0; q < NPL; ++q)
         cluster::store_bytes_coherent(dst + q * plane_stride,
@@ -497,8 +496,8 @@ __global__ __launch_bounds__(512) void recurrence_cl(RecArgs a, StepParams p, Cl
 
     for (int t = 0; t < a.T && alive; ++t) {
       const int par = t & 1;
-      const int8_t *hin = cl.hx + static_cast<size_t>(par) * NPL * plane_stride;
-      int8_t *hout = cl.hx + static_cast<size_t>(par ^ 1) * NPL * plane_stride;
+      const int8_t *hin = a.hx + static_cast<size_t>(par) * NPL * plane_stride;
+      int8_t *hout = a.hx + static_cast<size_t>(par ^ 1) * NPL * plane_stride;
       float gih[3] = {gi_next[0], gi_next[1], gi_next[2]};
       // partial recurrent sums over this wave's K-steps
       v4i acc[3][NPL];
@@ -624,6 +623,23 @@ __global__ __launch_bounds__(512) void recurrence_cl(RecArgs a, StepParams p, Cl
   }
 }
 
+template <int NPL>
+__global__ __launch_bounds__(512) void recurrence_cl(RecArgs a0, RecArgs a1,
+                                                     const StepParams *__restrict__ ps,
+                                                     ClArgs cl) {
+  const cluster::Place pl = cluster::place(cl.G, cl.ncl);
+  unsigned *counter = cl.counters + pl.cluster;
+  unsigned epoch = 0;
+  bool alive = true;
+  for (int pair = pl.cluster; pair < cl.ndir * cl.ntiles && alive; pair += cl.ncl) {
+    const int d = pair / cl.ntiles, tile = pair % cl.ntiles;
+    // the previous pair's readers of the LUT and the partial-sum buffer are done
+    __syncthreads();
+    // one copy of the step code for both directions (d is uniform across the workgroup)
+    recurrence_cl_pair<NPL>(d == 0 ? a0 : a1, ps[d], cl, tile, pl.member, counter, epoch, alive);
+  }
+}
+
 size_t recurrence_cl_lds_bytes(int UT, int npl) {
   return 1024 + sizeof(v4i) * static_cast<size_t>(UT) * 4 * 3 * npl * 64;
 }
@@ -637,7 +653,7 @@ size_t recurrence_lds_bytes(int H, int KS, int npl) {
 
 // Workspace layout of the forward (bytes, 256-aligned pieces).
 struct FwdWorkspace {
-  size_t gih, chan, h0codes, hostblk, rfrag, hx, sync, total;
+  size_t gih, chan, h0codes, hostblk, rfrag, hx, sync, sparams, total;
   FwdWorkspace(int T, int B, int I, int H) {
     (void)I;
     const size_t C = 3 * static_cast<size_t>(H);
@@ -650,7 +666,8 @@ struct FwdWorkspace {
     rfrag = o; o += al(sizeof(v4i) * 64 * static_cast<size_t>(H / 16) * 3 * ((H + 63) / 64));
     const size_t Bpad = (static_cast<size_t>(B) + kTileB - 1) / kTileB * kTileB;
     hx = o; o += al(2 * 2 * Bpad * H);
-    sync = o; o += al(sizeof(unsigned) * (Bpad / kTileB + 1));
+    sync = o; o += al(sizeof(unsigned) * (2 * (Bpad / kTileB) + 2));  // clusters of both directions
+    sparams = o; o += al(2 * sizeof(StepParams));
     total = o;
   }
 };
@@ -662,6 +679,238 @@ static int host_bits_check(const rxmet_gru_qparams &p) {
   RXMET_CHECK_ARG(p.g[RXMET_GRU_H].bits <= 16, "hidden-state grids wider than 16 bits are not supported");
   RXMET_CHECK_ARG(p.g[RXMET_GRU_X].bits <= 16 && p.chan_bits[RXMET_GRU_W] <= 16,
                   "input or input-weight grids wider than 16 bits are not supported");
+  return 0;
+}
+
+}  // namespace gru
+}  // namespace rxmet
+
+namespace rxmet {
+namespace gru {
+
+// One direction's prologue (quantisation, input projection, R_q fragments) and the
+// recurrence arguments it leaves for the launch.
+struct FwdPlan {
+  RecArgs ra;
+  StepParams sp;
+  int npl;
+  char *wsb;
+};
+
+static int forward_prologue(bool training, int T, int B, int I, int H, const rxmet_gru_fwd_dir &d,
+                            hipStream_t stream, FwdPlan *plan) {
+  const rxmet_gru_qparams *params = d.params;
+  RXMET_CHECK_ARG(params != nullptr, "params must be non-null");
+  RXMET_CHECK_ARG(params->hidden == H, "params.hidden != hidden_size");
+  RXMET_CHECK_ARG(d.W && d.R && d.bw && d.br && d.x && d.h && d.W_q && d.R_q && d.bw_q && d.br_q &&
+                      d.x_q && d.workspace,
+                  "required pointer is null");
+  if (int rc = host_bits_check(*params)) return rc;
+  if (training) {
+    RXMET_CHECK_ARG(d.v && d.x_mask && d.W_mask && d.R_mask && d.bw_mask && d.br_mask &&
+                        d.ih_mask && d.hh_mask && d.gate_in_mask && d.gate_out_mask && d.h_mask &&
+                        (d.h0 == nullptr || d.h0_mask),
+                    "training needs v and every mask output");
+  }
+  // the input projection accumulates in int32 when |x_q| |W_q| I cannot reach 2^31,
+  // otherwise in int64 (codes are at most 16 bits, I < 2^31: always exact)
+  const bool wide_gemm = std::ldexp(1.0, params->g[RXMET_GRU_X].bits) *
+                             std::ldexp(1.0, params->chan_bits[RXMET_GRU_W] - 1) * I >=
+                         2147483647.0;
+  const int C = 3 * H;
+  const FwdWorkspace ws(T, B, I, H);
+  char *wsb = static_cast<char *>(d.workspace);
+  float *gih = reinterpret_cast<float *>(wsb + ws.gih);
+  float *chan = reinterpret_cast<float *>(wsb + ws.chan);
+  float *h0codes = reinterpret_cast<float *>(wsb + ws.h0codes);
+  float *hostblk = reinterpret_cast<float *>(wsb + ws.hostblk);
+
+  StepParams &sp = plan->sp;
+  std::vector<float> host(8 * static_cast<size_t>(C));
+  try {
+    make_step_params(*params, H, &sp);
+    // host block: eff[4C] | ibx | ibh | igx | igh
+    make_channel_factors(*params, H, host.data() + 6 * C, host.data() + 4 * C, host.data() + 7 * C,
+                         host.data() + 5 * C, host.data(), host.data() + C, host.data() + 2 * C,
+                         host.data() + 3 * C);
+  } catch (const std::exception &e) {
+    set_error(e.what());
+    return -22;
+  }
+  RXMET_CHECK_HIP(hipMemcpyAsync(hostblk, host.data(), sizeof(float) * host.size(),
+                                 hipMemcpyHostToDevice, stream));
+  // igx/igh go straight into the per-channel block
+  RXMET_CHECK_HIP(hipMemcpyAsync(chan, host.data() + 6 * C, sizeof(float) * C,
+                                 hipMemcpyHostToDevice, stream));
+  RXMET_CHECK_HIP(hipMemcpyAsync(chan + C, host.data() + 7 * C, sizeof(float) * C,
+                                 hipMemcpyHostToDevice, stream));
+  const rxmet_grid *g = params->g;
+  WeightArgs wa;
+  wa.W = d.W; wa.R = d.R; wa.bw = d.bw; wa.br = d.br;
+  wa.eff = hostblk;
+  wa.ibx = hostblk + 4 * C;
+  wa.ibh = hostblk + 5 * C;
+  wa.bW = bounds_of(params->chan_bits[RXMET_GRU_W], params->chan_unsigned[RXMET_GRU_W]);
+  wa.bR = bounds_of(params->chan_bits[RXMET_GRU_R], params->chan_unsigned[RXMET_GRU_R]);
+  wa.bbw = bounds_of(params->chan_bits[RXMET_GRU_BW], params->chan_unsigned[RXMET_GRU_BW]);
+  wa.bbr = bounds_of(params->chan_bits[RXMET_GRU_BR], params->chan_unsigned[RXMET_GRU_BR]);
+  wa.zp_x = static_cast<float>(g[RXMET_GRU_X].zero_point);
+  wa.zp_h = static_cast<float>(g[RXMET_GRU_H].zero_point);
+  wa.Wq = d.W_q; wa.Rq = d.R_q; wa.bwq = d.bw_q; wa.brq = d.br_q;
+  wa.Wm = training ? d.W_mask : nullptr;
+  wa.Rm = training ? d.R_mask : nullptr;
+  wa.bwm = training ? d.bw_mask : nullptr;
+  wa.brm = training ? d.br_mask : nullptr;
+  wa.chan = chan;
+  {
+    rxmet::prof::Scope ps__("gru_fwd_quant_weights", stream);
+    hipLaunchKernelGGL(quant_weights, dim3((C + 255) / 256), dim3(256), 0, stream, I, H, wa);
+  }
+  RXMET_CHECK_LAUNCH();
+
+  const int64_t nx = static_cast<int64_t>(T) * B * I, nh = static_cast<int64_t>(B) * H;
+  int64_t blocks = (nx + nh + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  {
+    rxmet::prof::Scope ps__("gru_fwd_quant_input", stream);
+    hipLaunchKernelGGL(quant_input, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, nx,
+                       nh, d.x, d.h0, sp.eff_x, sp.zp_x, sp.x, sp.eff_h, sp.zp_h, sp.h, d.x_q,
+                       training ? d.x_mask : nullptr, h0codes, training ? d.h0_mask : nullptr,
+                       d.h);
+  }
+  RXMET_CHECK_LAUNCH();
+
+  const int M = T * B;
+  {
+    rxmet::prof::Scope ps__("gru_fwd_input_gemm", stream);
+    if (wide_gemm)
+      hipLaunchKernelGGL(code_gemm<long long>, dim3((C + 63) / 64, (M + 63) / 64), dim3(256), 0,
+                         stream, M, C, I, d.x_q, d.W_q, gih);
+    else
+      hipLaunchKernelGGL(code_gemm<int>, dim3((C + 63) / 64, (M + 63) / 64), dim3(256), 0, stream,
+                         M, C, I, d.x_q, d.W_q, gih);
+  }
+  RXMET_CHECK_LAUNCH();
+
+  RecArgs &ra = plan->ra;
+  ra.T = T; ra.B = B; ra.H = H; ra.KS = (H + 63) / 64;
+  v4i *rfrag = reinterpret_cast<v4i *>(wsb + ws.rfrag);
+  hipLaunchKernelGGL(pack_r_frags, dim3((H / 16) * 3 * ra.KS), dim3(64), 0, stream, H, ra.KS,
+                     d.R_q, rfrag);
+  RXMET_CHECK_LAUNCH();
+  ra.training = training ? 1 : 0;
+  const rxmet_grid &gh = g[RXMET_GRU_H];
+  const bool h_uns = gh.bits < 32 && gh.is_unsigned;
+  ra.h_offset = h_uns ? std::ldexp(1.0f, gh.bits - 1) : 0.0f;
+  plan->npl = (gh.bits <= 8) ? 1 : 2;
+  ra.gih = gih; ra.rfrag = rfrag; ra.chan = chan; ra.h0codes = h0codes; ra.hout = d.h; ra.v = d.v;
+  ra.ih_m = d.ih_mask; ra.hh_m = d.hh_mask; ra.gin_m = d.gate_in_mask;
+  ra.gout_m = d.gate_out_mask; ra.h_m = d.h_mask;
+  ra.hx = reinterpret_cast<int8_t *>(wsb + ws.hx);
+  plan->wsb = wsb;
+  return 0;
+}
+
+// Clustered launch over every direction when the grid can be resident at once; returns 1
+// when launched, 0 when the caller must use the per-tile recurrence.
+static int forward_recurrence_clustered(FwdPlan *plans, int ndir, int T, int B, int I, int H,
+                                        hipStream_t stream) {
+  const int npl = plans[0].npl, KS = plans[0].ra.KS;
+  for (int k = 1; k < ndir; ++k)
+    if (plans[k].npl != npl) return 0;
+  if (KS > 4 * kClMaxKPerWave || std::getenv("RXMET_NO_CLUSTER") != nullptr) return 0;
+  const void *fn = npl == 1 ? reinterpret_cast<const void *>(&recurrence_cl<1>)
+                            : reinterpret_cast<const void *>(&recurrence_cl<2>);
+  int device = 0, ncu = 0;
+  RXMET_CHECK_HIP(hipGetDevice(&device));
+  RXMET_CHECK_HIP(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, device));
+  ClArgs cl;
+  cl.ndir = ndir;
+  cl.ntiles = (B + kTileB - 1) / kTileB;
+  cl.Bpad = cl.ntiles * kTileB;
+  const int pairs = ndir * cl.ntiles;
+  // the smallest unit slice per workgroup whose grid fits one workgroup per CU (two
+  // workgroups sharing a CU step no faster than one doing both), else the largest slice
+  int chosen = 0, ncl = 0;
+  for (int UT = 1; UT <= 2 && !chosen; ++UT) {
+    if ((H / 16) % UT) continue;
+    const int G = H / (16 * UT);
+    if (static_cast<int64_t>(pairs) * G <= ncu || UT == 2) {
+      chosen = UT;
+      cl.G = G;
+    }
+  }
+  if (!chosen) return 0;
+  const size_t lds_cl = recurrence_cl_lds_bytes(chosen, npl);
+  RXMET_CHECK_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      static_cast<int>(lds_cl)));
+  int per_cu = 0;
+  RXMET_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256 * chosen, lds_cl));
+  ncl = per_cu * ncu / cl.G;
+  if (ncl < 1) return 0;
+  if (ncl > pairs) ncl = pairs;
+  if (ncl >= 8) ncl -= ncl % 8;
+  cl.UT = chosen;
+  cl.ncl = ncl;
+  const FwdWorkspace ws(T, B, I, H);
+  cl.counters = reinterpret_cast<unsigned *>(plans[0].wsb + ws.sync);
+  cl.timeout = reinterpret_cast<int *>(cl.counters + ncl);
+  hipLaunchKernelGGL(cluster::zero_words, dim3(1), dim3(256), 0, stream, cl.counters, ncl + 1);
+  RXMET_CHECK_LAUNCH();
+  RecArgs &a1 = plans[ndir > 1 ? 1 : 0].ra;
+  // both directions' step parameters in device memory (read with scalar loads)
+  StepParams host_ps[2] = {plans[0].sp, plans[ndir > 1 ? 1 : 0].sp};
+  StepParams *ps = reinterpret_cast<StepParams *>(plans[0].wsb + ws.sparams);
+  RXMET_CHECK_HIP(hipMemcpyAsync(ps, host_ps, sizeof(host_ps), hipMemcpyHostToDevice, stream));
+  void *args[] = {&plans[0].ra, &a1, &ps, &cl};
+  {
+    rxmet::prof::Scope ps__("gru_fwd_recurrence", stream);
+    RXMET_CHECK_HIP(hipLaunchCooperativeKernel(fn, dim3(ncl * cl.G), dim3(256 * cl.UT), args,
+                                               static_cast<unsigned>(lds_cl), stream));
+  }
+  const int64_t n_h = static_cast<int64_t>(T + 1) * B * H;
+  for (int k = 0; k < ndir; ++k) {
+    hipLaunchKernelGGL(cluster::poison_nan, dim3(64), dim3(256), 0, stream, cl.timeout, n_h,
+                       plans[k].ra.hout);
+    RXMET_CHECK_LAUNCH();
+  }
+  return 1;
+}
+
+static int forward_recurrence_tiles(FwdPlan &plan, int B, int H, hipStream_t stream) {
+  RecArgs &ra = plan.ra;
+  const size_t lds = recurrence_lds_bytes(H, ra.KS, plan.npl);
+  const dim3 grid((B + kTileB - 1) / kTileB), block(64 * ((H + 31) / 32));
+  const void *fn = plan.npl == 1 ? reinterpret_cast<const void *>(&recurrence<1>)
+                                 : reinterpret_cast<const void *>(&recurrence<2>);
+  RXMET_CHECK_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      static_cast<int>(lds)));
+  rxmet::prof::Scope ps__("gru_fwd_recurrence", stream);
+  if (plan.npl == 1)
+    hipLaunchKernelGGL(recurrence<1>, grid, block, lds, stream, ra, plan.sp);
+  else
+    hipLaunchKernelGGL(recurrence<2>, grid, block, lds, stream, ra, plan.sp);
+  RXMET_CHECK_LAUNCH();
+  return 0;
+}
+
+static int forward_dirs(int ndir, bool training, int T, int B, int I, int H,
+                        const rxmet_gru_fwd_dir *dirs, hipStream_t stream) {
+  RXMET_CHECK_ARG(ndir == 1 || ndir == 2, "ndir must be 1 or 2");
+  RXMET_CHECK_ARG(dirs != nullptr, "dirs must be non-null");
+  RXMET_CHECK_ARG(T >= 1 && B >= 1 && I >= 1 && H >= 1, "dimensions must be positive");
+  RXMET_CHECK_ARG(H % 16 == 0 && H <= kMaxH,
+                  "hidden_size must be a multiple of 16 and at most 256 for the MFMA recurrence");
+  RXMET_CHECK_ARG(static_cast<double>(T + 1) * B * 4 * H < 4294967295.0,
+                  "T*B*H too large for the recurrence's 32-bit element offsets");
+  FwdPlan plans[2];
+  for (int k = 0; k < ndir; ++k)
+    if (int rc = forward_prologue(training, T, B, I, H, dirs[k], stream, &plans[k])) return rc;
+  const int rc = forward_recurrence_clustered(plans, ndir, T, B, I, H, stream);
+  if (rc < 0) return rc;
+  if (rc == 1) return 0;
+  for (int k = 0; k < ndir; ++k)
+    if (int r = forward_recurrence_tiles(plans[k], B, H, stream)) return r;
   return 0;
 }
 
@@ -687,186 +936,17 @@ int rxmet_gru_forward_quant(int32_t is_training, int32_t T, int32_t B, int32_t I
                             uint8_t *hh_mask, uint8_t *gate_in_mask, uint8_t *gate_out_mask,
                             uint8_t *h_mask, void *workspace, void *stream_) {
   clear_error();
-  RXMET_CHECK_ARG(params != nullptr, "params must be non-null");
-  RXMET_CHECK_ARG(T >= 1 && B >= 1 && I >= 1 && H >= 1, "dimensions must be positive");
-  RXMET_CHECK_ARG(params->hidden == H, "params.hidden != hidden_size");
-  RXMET_CHECK_ARG(H % 16 == 0 && H <= kMaxH,
-                  "hidden_size must be a multiple of 16 and at most 256 for the MFMA recurrence");
-  RXMET_CHECK_ARG(W && R && bw && br && x && h && W_q && R_q && bw_q && br_q && x_q && workspace,
-                  "required pointer is null");
-  if (int rc = host_bits_check(*params)) return rc;
-  const bool training = is_training != 0;
-  if (training) {
-    RXMET_CHECK_ARG(v && x_mask && W_mask && R_mask && bw_mask && br_mask && ih_mask && hh_mask &&
-                        gate_in_mask && gate_out_mask && h_mask && (h0 == nullptr || h0_mask),
-                    "training needs v and every mask output");
-  }
-  // the input projection accumulates in int32 when |x_q| |W_q| I cannot reach 2^31,
-  // otherwise in int64 (codes are at most 16 bits, I < 2^31: always exact)
-  const bool wide_gemm = std::ldexp(1.0, params->g[RXMET_GRU_X].bits) *
-                             std::ldexp(1.0, params->chan_bits[RXMET_GRU_W] - 1) * I >=
-                         2147483647.0;
-  RXMET_CHECK_ARG(static_cast<double>(T + 1) * B * 4 * H < 4294967295.0,
-                  "T*B*H too large for the recurrence's 32-bit element offsets");
-  hipStream_t stream = static_cast<hipStream_t>(stream_);
-  const int C = 3 * H;
-  const FwdWorkspace ws(T, B, I, H);
-  char *wsb = static_cast<char *>(workspace);
-  float *gih = reinterpret_cast<float *>(wsb + ws.gih);
-  float *chan = reinterpret_cast<float *>(wsb + ws.chan);
-  float *h0codes = reinterpret_cast<float *>(wsb + ws.h0codes);
-  float *hostblk = reinterpret_cast<float *>(wsb + ws.hostblk);
+  const rxmet_gru_fwd_dir d = {W, R, bw, br, x, h0, params, h, v, W_q, R_q, bw_q, br_q, x_q,
+                               x_mask, h0_mask, W_mask, R_mask, bw_mask, br_mask, ih_mask,
+                               hh_mask, gate_in_mask, gate_out_mask, h_mask, workspace};
+  return forward_dirs(1, is_training != 0, T, B, I, H, &d, static_cast<hipStream_t>(stream_));
+}
 
-  StepParams sp;
-  std::vector<float> host(8 * static_cast<size_t>(C));
-  try {
-    make_step_params(*params, H, &sp);
-    // host block: eff[4C] | ibx | ibh | igx | igh
-    make_channel_factors(*params, H, host.data() + 6 * C, host.data() + 4 * C, host.data() + 7 * C,
-                         host.data() + 5 * C, host.data(), host.data() + C, host.data() + 2 * C,
-                         host.data() + 3 * C);
-  } catch (const std::exception &e) {
-    set_error(e.what());
-    return -22;
-  }
-  RXMET_CHECK_HIP(hipMemcpyAsync(hostblk, host.data(), sizeof(float) * host.size(),
-                                 hipMemcpyHostToDevice, stream));
-  // igx/igh go straight into the per-channel block
-  RXMET_CHECK_HIP(hipMemcpyAsync(chan, host.data() + 6 * C, sizeof(float) * C,
-                                 hipMemcpyHostToDevice, stream));
-  RXMET_CHECK_HIP(hipMemcpyAsync(chan + C, host.data() + 7 * C, sizeof(float) * C,
-                                 hipMemcpyHostToDevice, stream));
-  const rxmet_grid *g = params->g;
-  WeightArgs wa;
-  wa.W = W; wa.R = R; wa.bw = bw; wa.br = br;
-  wa.eff = hostblk;
-  wa.ibx = hostblk + 4 * C;
-  wa.ibh = hostblk + 5 * C;
-  wa.bW = bounds_of(params->chan_bits[RXMET_GRU_W], params->chan_unsigned[RXMET_GRU_W]);
-  wa.bR = bounds_of(params->chan_bits[RXMET_GRU_R], params->chan_unsigned[RXMET_GRU_R]);
-  wa.bbw = bounds_of(params->chan_bits[RXMET_GRU_BW], params->chan_unsigned[RXMET_GRU_BW]);
-  wa.bbr = bounds_of(params->chan_bits[RXMET_GRU_BR], params->chan_unsigned[RXMET_GRU_BR]);
-  wa.zp_x = static_cast<float>(g[RXMET_GRU_X].zero_point);
-  wa.zp_h = static_cast<float>(g[RXMET_GRU_H].zero_point);
-  wa.Wq = W_q; wa.Rq = R_q; wa.bwq = bw_q; wa.brq = br_q;
-  wa.Wm = training ? W_mask : nullptr;
-  wa.Rm = training ? R_mask : nullptr;
-  wa.bwm = training ? bw_mask : nullptr;
-  wa.brm = training ? br_mask : nullptr;
-  wa.chan = chan;
-  {
-    rxmet::prof::Scope ps__("gru_fwd_quant_weights", stream);
-    hipLaunchKernelGGL(quant_weights, dim3((C + 255) / 256), dim3(256), 0, stream, I, H, wa);
-  }
-  RXMET_CHECK_LAUNCH();
-
-  const int64_t nx = static_cast<int64_t>(T) * B * I, nh = static_cast<int64_t>(B) * H;
-  int64_t blocks = (nx + nh + 255) / 256;
-  if (blocks > 8192) blocks = 8192;
-  {
-    rxmet::prof::Scope ps__("gru_fwd_quant_input", stream);
-    hipLaunchKernelGGL(quant_input, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, nx,
-                       nh, x, h0, sp.eff_x, sp.zp_x, sp.x, sp.eff_h, sp.zp_h, sp.h, x_q,
-                       training ? x_mask : nullptr, h0codes, training ? h0_mask : nullptr, h);
-  }
-  RXMET_CHECK_LAUNCH();
-
-  const int M = T * B;
-  {
-    rxmet::prof::Scope ps__("gru_fwd_input_gemm", stream);
-    if (wide_gemm)
-      hipLaunchKernelGGL(code_gemm<long long>, dim3((C + 63) / 64, (M + 63) / 64), dim3(256), 0,
-                         stream, M, C, I, x_q, W_q, gih);
-    else
-      hipLaunchKernelGGL(code_gemm<int>, dim3((C + 63) / 64, (M + 63) / 64), dim3(256), 0, stream,
-                         M, C, I, x_q, W_q, gih);
-  }
-  RXMET_CHECK_LAUNCH();
-
-  RecArgs ra;
-  ra.T = T; ra.B = B; ra.H = H; ra.KS = (H + 63) / 64;
-  v4i *rfrag = reinterpret_cast<v4i *>(wsb + ws.rfrag);
-  hipLaunchKernelGGL(pack_r_frags, dim3((H / 16) * 3 * ra.KS), dim3(64), 0, stream, H, ra.KS, R_q,
-                     rfrag);
-  RXMET_CHECK_LAUNCH();
-  ra.training = training ? 1 : 0;
-  const rxmet_grid &gh = g[RXMET_GRU_H];
-  const bool h_uns = gh.bits < 32 && gh.is_unsigned;
-  ra.h_offset = h_uns ? std::ldexp(1.0f, gh.bits - 1) : 0.0f;
-  const int npl = (gh.bits <= 8) ? 1 : 2;
-  ra.gih = gih; ra.rfrag = rfrag; ra.chan = chan; ra.h0codes = h0codes; ra.hout = h; ra.v = v;
-  ra.ih_m = ih_mask; ra.hh_m = hh_mask; ra.gin_m = gate_in_mask; ra.gout_m = gate_out_mask;
-  ra.h_m = h_mask;
-  if (ra.KS <= 4 * kClMaxKPerWave && std::getenv("RXMET_NO_CLUSTER") == nullptr) {
-    // clustered path: the smallest unit slice per workgroup whose grid is resident at once
-    const void *fn = npl == 1 ? reinterpret_cast<const void *>(&recurrence_cl<1>)
-                              : reinterpret_cast<const void *>(&recurrence_cl<2>);
-    int device = 0, ncu = 0;
-    RXMET_CHECK_HIP(hipGetDevice(&device));
-    RXMET_CHECK_HIP(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, device));
-    ClArgs cl;
-    cl.ntiles = (B + kTileB - 1) / kTileB;
-    cl.Bpad = cl.ntiles * kTileB;
-    int chosen = 0, ncl = 0;
-    size_t lds_cl = 0;
-    for (int UT = 1; UT <= 2 && !chosen; ++UT) {
-      if ((H / 16) % UT) continue;
-      lds_cl = recurrence_cl_lds_bytes(UT, npl);
-      RXMET_CHECK_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                          static_cast<int>(lds_cl)));
-      int per_cu = 0;
-      RXMET_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256 * UT, lds_cl));
-      const int G = H / (16 * UT);
-      ncl = per_cu * ncu / G;
-      if (ncl < 1) continue;
-      if (ncl >= cl.ntiles || UT == 2) {
-        chosen = UT;
-        cl.G = G;
-      }
-    }
-    if (chosen && ncl >= 1) {
-      if (ncl > cl.ntiles) ncl = cl.ntiles;
-      if (ncl >= 8) ncl -= ncl % 8;
-      cl.UT = chosen;
-      cl.ncl = ncl;
-      cl.hx = reinterpret_cast<int8_t *>(wsb + ws.hx);
-      cl.counters = reinterpret_cast<unsigned *>(wsb + ws.sync);
-      cl.timeout = reinterpret_cast<int *>(cl.counters + ncl);
-      hipLaunchKernelGGL(cluster::zero_words, dim3(1), dim3(256), 0, stream, cl.counters, ncl + 1);
-      RXMET_CHECK_LAUNCH();
-      void *args[] = {&ra, &sp, &cl};
-      {
-        rxmet::prof::Scope ps__("gru_fwd_recurrence", stream);
-        RXMET_CHECK_HIP(hipLaunchCooperativeKernel(fn, dim3(ncl * cl.G), dim3(256 * cl.UT), args,
-                                                   static_cast<unsigned>(lds_cl), stream));
-      }
-      const int64_t n_h = static_cast<int64_t>(T + 1) * B * H;
-      hipLaunchKernelGGL(cluster::poison_nan, dim3(64), dim3(256), 0, stream, cl.timeout, n_h, h);
-      RXMET_CHECK_LAUNCH();
-      return 0;
-    }
-  }
-  const size_t lds = recurrence_lds_bytes(H, ra.KS, npl);
-  const dim3 grid((B + kTileB - 1) / kTileB), block(64 * ((H + 31) / 32));
-  if (npl == 1) {
-    RXMET_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&recurrence<1>),
-                                        hipFuncAttributeMaxDynamicSharedMemorySize,
-                                        static_cast<int>(lds)));
-    {
-      rxmet::prof::Scope ps__("gru_fwd_recurrence", stream);
-      hipLaunchKernelGGL(recurrence<1>, grid, block, lds, stream, ra, sp);
-    }
-  } else {
-    RXMET_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&recurrence<2>),
-                                        hipFuncAttributeMaxDynamicSharedMemorySize,
-                                        static_cast<int>(lds)));
-    {
-      rxmet::prof::Scope ps__("gru_fwd_recurrence", stream);
-      hipLaunchKernelGGL(recurrence<2>, grid, block, lds, stream, ra, sp);
-    }
-  }
-  RXMET_CHECK_LAUNCH();
-  return 0;
+int rxmet_gru_forward_quant_dirs(int32_t ndir, int32_t is_training, int32_t T, int32_t B,
+                                 int32_t I, int32_t H, const rxmet_gru_fwd_dir *dirs,
+                                 void *stream_) {
+  clear_error();
+  return forward_dirs(ndir, is_training != 0, T, B, I, H, dirs, static_cast<hipStream_t>(stream_));
 }
 
 }  // extern "C"

@@ -233,16 +233,10 @@ MASK_NAMES = ("x_mask", "h0_mask", "W_mask", "R_mask", "bw_mask", "br_mask",
               "gate_output_mask", "h_mask")
 
 
-def forward_quant_float_storage(is_training, time_steps, batch_size, input_size, hidden_size, W, R,
-                                bw, br, x, h0, quant_params: GRUQuantParams):
-    """forward_quant_float_storage_wrapper (gru_interface_binding.cc:306-448).
-
-    Returns (h, v, W_q, R_q, bw_q, br_q, x_q, x_mask, h0_mask, W_mask, R_mask, bw_mask,
-    br_mask, weight_ih_linear_mask, weight_hh_linear_mask, gate_input_mask,
-    gate_output_mask, h_mask); masks are empty tensors when is_training is False."""
+def _forward_dir(is_training, T, B, I, H, W, R, bw, br, x, h0, quant_params):
+    """Check one direction's inputs and allocate its outputs; returns (outputs, FwdDir)."""
     for n, t in (("W", W), ("R", R), ("bw", bw), ("br", br), ("x", x)):
         _check_f32_cuda(n, t)
-    T, B, I, H = time_steps, batch_size, input_size, hidden_size
     has_h0 = h0 is not None and h0.numel() > 0
     if has_h0:
         _check_f32_cuda("h0", h0)
@@ -269,21 +263,45 @@ def forward_quant_float_storage(is_training, time_steps, batch_size, input_size,
         masks = [torch.empty((0,), **u8) for _ in range(11)]
     ws = _ws(_rx.load().rxmet_gru_forward_workspace_bytes(T, B, I, H), dev)
     mp = [m.data_ptr() if m.numel() > 0 else None for m in masks]
-    _rx.call("rxmet_gru_forward_quant", int(bool(is_training)), T, B, I, H, W.data_ptr(),
-             R.data_ptr(), bw.data_ptr(), br.data_ptr(), x.data_ptr(),
-             h0.data_ptr() if has_h0 else None, ctypes.byref(quant_params.struct), h.data_ptr(),
-             v.data_ptr() if is_training else None, W_q.data_ptr(), R_q.data_ptr(), bw_q.data_ptr(),
-             br_q.data_ptr(), x_q.data_ptr(), *mp, ws.data_ptr(), _stream(dev))
-    return (h, v, W_q, R_q, bw_q, br_q, x_q, *masks)
+    d = A.FwdDir(W.data_ptr(), R.data_ptr(), bw.data_ptr(), br.data_ptr(), x.data_ptr(),
+                 h0.data_ptr() if has_h0 else None, ctypes.addressof(quant_params.struct),
+                 h.data_ptr(), v.data_ptr() if is_training else None, W_q.data_ptr(),
+                 R_q.data_ptr(), bw_q.data_ptr(), br_q.data_ptr(), x_q.data_ptr(), *mp,
+                 ws.data_ptr())
+    outs = (h, v, W_q, R_q, bw_q, br_q, x_q, *masks)
+    return outs, d, ws
 
 
-def backward_quant_float_storage(time_steps, batch_size, input_size, hidden_size, W_q, R_q, bw_q,
-                                 br_q, x_q, dh_new, h, v, quant_params: GRUQuantParams, x_mask,
-                                 h0_mask, W_mask, R_mask, bw_mask, br_mask, weight_ih_linear_mask,
-                                 weight_hh_linear_mask, gate_input_mask, gate_output_mask, h_mask):
-    """backward_quant_float_storage_wrapper (gru_interface_binding.cc:789-920).
-    Returns (dx, dW, dR, dbw, dbr, dh).  The saved codes are not modified."""
+def forward_quant_float_storage(is_training, time_steps, batch_size, input_size, hidden_size, W, R,
+                                bw, br, x, h0, quant_params: GRUQuantParams):
+    """forward_quant_float_storage_wrapper (gru_interface_binding.cc:306-448).
+
+    Returns (h, v, W_q, R_q, bw_q, br_q, x_q, x_mask, h0_mask, W_mask, R_mask, bw_mask,
+    br_mask, weight_ih_linear_mask, weight_hh_linear_mask, gate_input_mask,
+    gate_output_mask, h_mask); masks are empty tensors when is_training is False."""
     T, B, I, H = time_steps, batch_size, input_size, hidden_size
+    outs, d, ws = _forward_dir(is_training, T, B, I, H, W, R, bw, br, x, h0, quant_params)
+    _rx.call("rxmet_gru_forward_quant", int(bool(is_training)), T, B, I, H, d.W, d.R, d.bw, d.br,
+             d.x, d.h0, ctypes.byref(quant_params.struct), d.h, d.v, d.W_q, d.R_q, d.bw_q, d.br_q,
+             d.x_q, d.x_mask, d.h0_mask, d.W_mask, d.R_mask, d.bw_mask, d.br_mask, d.ih_mask,
+             d.hh_mask, d.gate_in_mask, d.gate_out_mask, d.h_mask, d.workspace, _stream(x.device))
+    return outs
+
+
+def forward_quant_float_storage_dirs(is_training, time_steps, batch_size, input_size, hidden_size,
+                                     dirs):
+    """Both directions of a bidirectional layer in one call (rxmet_gru_forward_quant_dirs):
+    ``dirs`` is a list of (W, R, bw, br, x, h0, quant_params) per direction; returns one
+    forward_quant_float_storage result tuple per direction."""
+    T, B, I, H = time_steps, batch_size, input_size, hidden_size
+    made = [_forward_dir(is_training, T, B, I, H, *d) for d in dirs]
+    arr = (A.FwdDir * len(made))(*[m[1] for m in made])
+    _rx.call("rxmet_gru_forward_quant_dirs", len(made), int(bool(is_training)), T, B, I, H, arr,
+             _stream(dirs[0][4].device))
+    return [m[0] for m in made]
+
+
+def _backward_dir(T, B, I, H, W_q, R_q, bw_q, br_q, x_q, dh_new, h, v, quant_params, masks):
     C = 3 * H
     dev = x_q.device
     for n, t, shp in (("W_q", W_q, (I, C)), ("R_q", R_q, (H, C)), ("bw_q", bw_q, (C,)),
@@ -294,20 +312,44 @@ def backward_quant_float_storage(time_steps, batch_size, input_size, hidden_size
         if tuple(t.shape) != shp:
             raise RuntimeError(f"{n} must have shape {list(shp)}")
     f32 = dict(dtype=torch.float32, device=dev)
-    dx = torch.empty((T, B, I), **f32)
-    dW = torch.empty((I, C), **f32)
-    dR = torch.empty((H, C), **f32)
-    dbw = torch.empty((C,), **f32)
-    dbr = torch.empty((C,), **f32)
-    dh = torch.empty((B, H), **f32)
-    masks = (x_mask, h0_mask, W_mask, R_mask, bw_mask, br_mask, weight_ih_linear_mask,
-             weight_hh_linear_mask, gate_input_mask, gate_output_mask, h_mask)
+    outs = (torch.empty((T, B, I), **f32), torch.empty((I, C), **f32), torch.empty((H, C), **f32),
+            torch.empty((C,), **f32), torch.empty((C,), **f32), torch.empty((B, H), **f32))
     mp = [m.data_ptr() if (m is not None and m.numel() > 0) else None for m in masks]
     dh_new = dh_new.contiguous()
     ws = _ws(_rx.load().rxmet_gru_backward_workspace_bytes(T, B, I, H), dev)
-    _rx.call("rxmet_gru_backward_quant", T, B, I, H, W_q.data_ptr(), R_q.data_ptr(),
-             bw_q.data_ptr(), br_q.data_ptr(), x_q.data_ptr(), dh_new.data_ptr(), h.data_ptr(),
-             v.data_ptr(), ctypes.byref(quant_params.struct), *mp, dx.data_ptr(), dW.data_ptr(),
-             dR.data_ptr(), dbw.data_ptr(), dbr.data_ptr(), dh.data_ptr(), ws.data_ptr(),
-             _stream(dev))
-    return dx, dW, dR, dbw, dbr, dh
+    d = A.BwdDir(W_q.data_ptr(), R_q.data_ptr(), bw_q.data_ptr(), br_q.data_ptr(), x_q.data_ptr(),
+                 dh_new.data_ptr(), h.data_ptr(), v.data_ptr(),
+                 ctypes.addressof(quant_params.struct), *mp, *[o.data_ptr() for o in outs],
+                 ws.data_ptr())
+    return outs, d, (ws, dh_new)
+
+
+def backward_quant_float_storage(time_steps, batch_size, input_size, hidden_size, W_q, R_q, bw_q,
+                                 br_q, x_q, dh_new, h, v, quant_params: GRUQuantParams, x_mask,
+                                 h0_mask, W_mask, R_mask, bw_mask, br_mask, weight_ih_linear_mask,
+                                 weight_hh_linear_mask, gate_input_mask, gate_output_mask, h_mask):
+    """backward_quant_float_storage_wrapper (gru_interface_binding.cc:789-920).
+    Returns (dx, dW, dR, dbw, dbr, dh).  The saved codes are not modified."""
+    T, B, I, H = time_steps, batch_size, input_size, hidden_size
+    masks = (x_mask, h0_mask, W_mask, R_mask, bw_mask, br_mask, weight_ih_linear_mask,
+             weight_hh_linear_mask, gate_input_mask, gate_output_mask, h_mask)
+    outs, d, keep = _backward_dir(T, B, I, H, W_q, R_q, bw_q, br_q, x_q, dh_new, h, v,
+                                  quant_params, masks)
+    _rx.call("rxmet_gru_backward_quant", T, B, I, H, d.W_q, d.R_q, d.bw_q, d.br_q, d.x_q,
+             d.dh_new, d.h, d.v, ctypes.byref(quant_params.struct), d.x_mask, d.h0_mask, d.W_mask,
+             d.R_mask, d.bw_mask, d.br_mask, d.ih_mask, d.hh_mask, d.gate_in_mask,
+             d.gate_out_mask, d.h_mask, d.dx, d.dW, d.dR, d.dbw, d.dbr, d.dh0, d.workspace,
+             _stream(x_q.device))
+    return outs
+
+
+def backward_quant_float_storage_dirs(time_steps, batch_size, input_size, hidden_size, dirs):
+    """Both directions' backward in one call (rxmet_gru_backward_quant_dirs): ``dirs`` is a
+    list of (W_q, R_q, bw_q, br_q, x_q, dh_new, h, v, quant_params, masks) per direction;
+    returns one (dx, dW, dR, dbw, dbr, dh) tuple per direction."""
+    T, B, I, H = time_steps, batch_size, input_size, hidden_size
+    made = [_backward_dir(T, B, I, H, *d) for d in dirs]
+    arr = (A.BwdDir * len(made))(*[m[1] for m in made])
+    _rx.call("rxmet_gru_backward_quant_dirs", len(made), T, B, I, H, arr,
+             _stream(dirs[0][4].device))
+    return [m[0] for m in made]

@@ -220,6 +220,71 @@ class GRUFunction(torch.autograd.Function):
         return dx, dW_pt, dR_pt, dbw_pt, dbr_pt, dh0, None, None, None, None
 
 
+class GRUBidirectionalFunction(torch.autograd.Function):
+    """Both directions of a quantised bidirectional GRU, equal to two GRUFunction applications
+    on (input, input.flip(0)) (quant_gru.py:2270-2288), with each direction pair of
+    recurrences launched together (forward_quant_float_storage_dirs /
+    backward_quant_float_storage_dirs) so the two directions' sequential steps overlap."""
+
+    @staticmethod
+    def forward(ctx, input, wi_f, wh_f, bi_f, bh_f, h0_f, wi_r, wh_r, bi_r, bh_r, h0_r, is_training,
+                qp_f, qp_r):
+        T, B, I = input.shape
+        H = wh_f.shape[1]
+        ctx.dims = (T, B, I, H)
+        device = _require_device(input)
+        x_f = ensure_cuda_float32(input, device).contiguous()
+        x_r = x_f.flip(0).contiguous()
+        dirs = []
+        for (wi, wh, bi, bh, h0, qp, x) in ((wi_f, wh_f, bi_f, bh_f, h0_f, qp_f, x_f),
+                                           (wi_r, wh_r, bi_r, bh_r, h0_r, qp_r, x_r)):
+            W, R, bw, br = convert_weights_to_haste_format(wi, wh, bi, bh, H, device)
+            h0_t = (ensure_cuda_float32(h0, device).contiguous() if h0 is not None
+                    else torch.empty(0, device=device, dtype=torch.float32))
+            dirs.append((W, R, bw, br, x, h0_t, qp))
+        outs = gru_ops.forward_quant_float_storage_dirs(is_training, T, B, I, H, dirs)
+        ctx.bias_none = (bi_f is None, bh_f is None)
+        ctx.h0_none = (h0_f is None, h0_r is None)
+        ctx.quant_params = (qp_f, qp_r)
+        ctx.saved_state = bool(is_training)
+        if is_training:
+            saved = []
+            for o in outs:
+                saved += [o[2], o[3], o[4], o[5], o[6], o[0], o[1], *o[7:]]
+            ctx.save_for_backward(*saved)
+        (h_f, h_r) = (outs[0][0], outs[1][0])
+        return h_f[1:], h_f[-1:], h_r[1:], h_r[-1:]
+
+    @staticmethod
+    def backward(ctx, g_out_f, g_hn_f, g_out_r, g_hn_r):
+        if not ctx.saved_state:
+            raise RuntimeError("QuantGRU forward ran without saving backward state (no_grad "
+                               "eval); rerun it with gradients enabled")
+        T, B, I, H = ctx.dims
+        saved = ctx.saved_tensors
+        n = len(saved) // 2
+        dirs = []
+        for k, (g_out, g_hn) in enumerate(((g_out_f, g_hn_f), (g_out_r, g_hn_r))):
+            W_q, R_q, bw_q, br_q, x_q, h, v = saved[k * n:k * n + 7]
+            masks = saved[k * n + 7:(k + 1) * n]
+            dh_new = torch.zeros((T + 1, B, H), device=h.device, dtype=torch.float32)
+            if g_out is not None:
+                dh_new[1:] = g_out
+            if g_hn is not None and g_hn.numel() > 0:
+                dh_new[-1] += g_hn[0]
+            dirs.append((W_q, R_q, bw_q, br_q, x_q, dh_new, h, v, ctx.quant_params[k], masks))
+        res = gru_ops.backward_quant_float_storage_dirs(T, B, I, H, dirs)
+        grads = []
+        for k, (dx, dW, dR, dbw, dbr, dh) in enumerate(res):
+            grads.append((reorder_weights_haste_to_pytorch(dW.t()),
+                          reorder_weights_haste_to_pytorch(dR.t()),
+                          None if ctx.bias_none[0] else reorder_weights_haste_to_pytorch(dbw),
+                          None if ctx.bias_none[1] else reorder_weights_haste_to_pytorch(dbr),
+                          None if ctx.h0_none[k] else dh))
+        dx = res[0][0] + res[1][0].flip(0)
+        return (dx, *grads[0], *grads[1], None, None, None)
+
+
 # ------------------------------------------------------------------------------------
 # QuantGRU (quant_gru.py:1120-2306)
 # ------------------------------------------------------------------------------------
@@ -572,6 +637,14 @@ class QuantGRU(nn.Module):
             input.requires_grad or (hx is not None and hx.requires_grad)
             or any(p.requires_grad for p in self.parameters())))
         b = self.bias
+        if self.bidirectional and self.use_quantization and self.quant_storage_dtype == "float32":
+            out_f, hn_f, out_r, hn_r = GRUBidirectionalFunction.apply(
+                input, self.weight_ih_l0, self.weight_hh_l0, self.bias_ih_l0 if b else None,
+                self.bias_hh_l0 if b else None, h0f, self.weight_ih_l0_reverse,
+                self.weight_hh_l0_reverse, self.bias_ih_l0_reverse if b else None,
+                self.bias_hh_l0_reverse if b else None, h0r, save_state, self.quant_params,
+                self.quant_params_reverse)
+            return self._combine_bidirectional_outputs(out_f, hn_f, out_r.flip(0), hn_r)
         out_f, hn_f = GRUFunction.apply(
             input, self.weight_ih_l0, self.weight_hh_l0, self.bias_ih_l0 if b else None,
             self.bias_hh_l0 if b else None, h0f, save_state, self.use_quantization,

@@ -62,6 +62,26 @@ class PwlLut(ctypes.Structure):
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32
+
+FWD_DIR_FIELDS = ("W", "R", "bw", "br", "x", "h0", "params", "h", "v", "W_q", "R_q", "bw_q",
+                  "br_q", "x_q", "x_mask", "h0_mask", "W_mask", "R_mask", "bw_mask", "br_mask",
+                  "ih_mask", "hh_mask", "gate_in_mask", "gate_out_mask", "h_mask", "workspace")
+BWD_DIR_FIELDS = ("W_q", "R_q", "bw_q", "br_q", "x_q", "dh_new", "h", "v", "params", "x_mask",
+                  "h0_mask", "W_mask", "R_mask", "bw_mask", "br_mask", "ih_mask", "hh_mask",
+                  "gate_in_mask", "gate_out_mask", "h_mask", "dx", "dW", "dR", "dbw", "dbr", "dh0",
+                  "workspace")
+
+
+class FwdDir(ctypes.Structure):
+    """rxmet_gru_fwd_dir: the arguments of one rxmet_gru_forward_quant call."""
+    _fields_ = [(n, _p) for n in FWD_DIR_FIELDS]
+
+
+class BwdDir(ctypes.Structure):
+    """rxmet_gru_bwd_dir: the arguments of one rxmet_gru_backward_quant call."""
+    _fields_ = [(n, _p) for n in BWD_DIR_FIELDS]
+
+
 _SIGS = {
     "rxmet_gru_make_params": (ctypes.c_int, [ctypes.POINTER(GruRanges), ctypes.POINTER(GruConfig),
                                              ctypes.POINTER(GruQParams)]),
@@ -74,6 +94,8 @@ _SIGS = {
                                 [ctypes.POINTER(GruQParams)] + [_p] * 18 + [_p, _p]),
     "rxmet_gru_backward_quant": (ctypes.c_int, [_i32, _i32, _i32, _i32] + [_p] * 8 +
                                  [ctypes.POINTER(GruQParams)] + [_p] * 11 + [_p] * 6 + [_p, _p]),
+    "rxmet_gru_forward_quant_dirs": (ctypes.c_int, [_i32] * 6 + [ctypes.POINTER(FwdDir), _p]),
+    "rxmet_gru_backward_quant_dirs": (ctypes.c_int, [_i32] * 5 + [ctypes.POINTER(BwdDir), _p]),
     "rxmet_gru_forward_calibrate": (ctypes.c_int, [_i32, _i32, _i32, _i32] + [_p] * 9 + [_p, _p]),
     "rxmet_gru_forward_fp": (ctypes.c_int, [_i32] * 5 + [_p] * 8 + [_p]),
 }

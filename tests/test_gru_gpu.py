@@ -223,3 +223,40 @@ def test_backward_without_masks_and_nan_propagation(cuda):
     got = _gpu_backward(cuda, fwd, dh_new, qp, T, B, I, H)
     assert np.isnan(got[5][3]).any(), "NaN upstream gradient must reach dh0 of its sequence"
     assert np.isfinite(np.delete(got[5], 3, axis=0)).all(), "NaN leaked into other sequences"
+
+
+@pytest.mark.parametrize("shape", [(4, 48, 9, 64), (3, 300, 16, 256)])
+def test_two_direction_entry_points_equal_single_calls(cuda, shape):
+    """rxmet_gru_forward_quant_dirs / backward_quant_dirs (both directions, one clustered
+    launch each way) equal one call per direction: forward bit for bit, backward within the
+    GEMM summation-order tolerance."""
+    T, B, I, H = shape
+    args = []
+    for d in range(2):
+        W, R, bw, br, x, h0, qp = _case(T, B, I, H, "c3", 7 + d, True)
+        t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(cuda)
+        args.append((t(W), t(R), t(bw), t(br), t(x), t(h0), gru_ops.GRUQuantParams.from_struct(qp)))
+    both = gru_ops.forward_quant_float_storage_dirs(True, T, B, I, H, args)
+    torch.cuda.synchronize()
+    single = [gru_ops.forward_quant_float_storage(True, T, B, I, H, *a) for a in args]
+    torch.cuda.synchronize()
+    for d in range(2):
+        for name, a, b in zip(NAMES, both[d], single[d]):
+            assert torch.equal(a, b), (d, name)
+    g = np.random.default_rng(9)
+    bargs = []
+    for d in range(2):
+        (h, v, W_q, R_q, bw_q, br_q, x_q, *masks) = both[d]
+        dh = torch.from_numpy((g.standard_normal((T + 1, B, H)) * 1e-2).astype(f32)).to(cuda)
+        bargs.append((W_q, R_q, bw_q, br_q, x_q, dh, h, v, args[d][6], masks))
+    gb = gru_ops.backward_quant_float_storage_dirs(T, B, I, H, bargs)
+    torch.cuda.synchronize()
+    for d in range(2):
+        W_q, R_q, bw_q, br_q, x_q, dh, h, v, qp, masks = bargs[d]
+        gs = gru_ops.backward_quant_float_storage(T, B, I, H, W_q, R_q, bw_q, br_q, x_q, dh, h, v,
+                                                  qp, *masks)
+        torch.cuda.synchronize()
+        for name, a, b in zip(("dx", "dW", "dR", "dbw", "dbr", "dh0"), gb[d], gs):
+            a, b = a.cpu().numpy(), b.cpu().numpy()
+            scale = max(float(np.abs(b).max()), 1e-30)
+            np.testing.assert_allclose(a, b, rtol=1e-5, atol=1e-6 * scale, err_msg=f"{d} {name}")
