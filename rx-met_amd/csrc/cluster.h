@@ -62,6 +62,35 @@ __device__ __forceinline__ bool sync(unsigned *counter, unsigned arrivals, int *
   return ok != 0;
 }
 
+// The barrier in two halves, so that stores the other members do not read (outputs,
+// checkpoints) can be issued between them and drain while the workgroup waits.
+// arrive: every thread calls it after its exchanged stores; wait: every thread calls it once,
+// after arrive, and gets false when the wait timed out.
+__device__ __forceinline__ void arrive(unsigned *counter) {
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ bool wait(unsigned *counter, unsigned arrivals, int *timeout) {
+  __shared__ int ok;
+  if (threadIdx.x == 0) {
+    int good = 1;
+    unsigned spins = 0;
+    while (__hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < arrivals) {
+      __builtin_amdgcn_s_sleep(1);
+      if (++spins > kSpinLimit) {
+        good = 0;
+        __hip_atomic_store(timeout, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+    }
+    ok = good;
+  }
+  __syncthreads();
+  return ok != 0;
+}
+
 __device__ __forceinline__ void store_coherent(unsigned *p, unsigned v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

@@ -378,7 +378,8 @@ __device__ __forceinline__ void bwd_cl_pair(const BwdArgs &a, const BwdClArgs &c
     float dhc = 0.0f;
     for (int t = a.T - 1; t >= 0 && alive; --t) {
       const int par = t & 1;
-      float dqv[3] = {0.f, 0.f, 0.f};
+      float dqv[3] = {0.f, 0.f, 0.f}, dpv[3] = {0.f, 0.f, 0.f};
+      uint32_t m = 0;
       float dhl = 0.0f;
       if (valid) {
         const uint32_t oH = static_cast<uint32_t>(b) * H + j;
@@ -391,7 +392,7 @@ __device__ __forceinline__ void bwd_cl_pair(const BwdArgs &a, const BwdClArgs &c
         dhl = z * dht;
         const float dg = (1.0f - z) * dht;
         const float dz = (a.h[tH + oH] - g) * dht;
-        const uint32_t m = tC + oC;
+        m = tC + oC;
         float dpg = (1.0f - g * g) * dg;
         if (a.gout_m) dpg *= static_cast<float>(a.gout_m[m + 2 * H]);
         if (a.gin_m) dpg *= static_cast<float>(a.gin_m[m + 2 * H]);
@@ -417,12 +418,10 @@ __device__ __forceinline__ void bwd_cl_pair(const BwdArgs &a, const BwdClArgs &c
           dpr *= static_cast<float>(a.ih_m[m + H]);
           dpg *= static_cast<float>(a.ih_m[m + 2 * H]);
         }
-        const float dpv[3] = {dpz, dpr, dpg};
+        dpv[0] = dpz; dpv[1] = dpr; dpv[2] = dpg;
         dqv[0] = dqz; dqv[1] = dqr; dqv[2] = dqg;
 #pragma unroll
         for (int gg = 0; gg < 3; ++gg) {
-          a.dp[m + gg * H] = dpv[gg];
-          a.dq[m + gg * H] = dqv[gg];
           sbw[gg] += static_cast<double>(dpv[gg] * mbw[gg]);
           sbr[gg] += static_cast<double>(dqv[gg] * mbr[gg]);
         }
@@ -432,7 +431,17 @@ __device__ __forceinline__ void bwd_cl_pair(const BwdArgs &a, const BwdClArgs &c
       for (int gg = 0; gg < 3; ++gg)
         cluster::store_coherent(reinterpret_cast<unsigned *>(xrow + gg * H + j),
                                 __float_as_uint(dqv[gg] * effr[gg]));
-      alive = cluster::sync(counter, ++epoch * cl.G, cl.timeout);
+      // the other members only read the exchange: arrive, then store dp / dq while waiting
+      cluster::arrive(counter);
+      ++epoch;
+      if (valid) {
+#pragma unroll
+        for (int gg = 0; gg < 3; ++gg) {
+          a.dp[m + gg * H] = dpv[gg];
+          a.dq[m + gg * H] = dqv[gg];
+        }
+      }
+      alive = cluster::wait(counter, epoch * cl.G, cl.timeout);
       if (!alive) break;
       // dh += R_deq dq over this wave's quarter of the channels
       v4f acc = {0.f, 0.f, 0.f, 0.f};

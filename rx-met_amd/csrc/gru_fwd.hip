@@ -597,6 +597,9 @@ __device__ __forceinline__ void recurrence_cl_pair(const RecArgs &a, const StepP
           cluster::store_bytes_coherent(dst + q * plane_stride,
                                         NPL == 1 ? hcv : (q == 0 ? (hcv & 255) - 128 : hcv >> 8));
       }
+      // the other members only read the h codes: arrive now, store the outputs while waiting
+      cluster::arrive(counter);
+      ++epoch;
       if (valid) {
         const uint32_t stepH = static_cast<uint32_t>(t) * B * H;
         a.hout[stepH + static_cast<uint32_t>(B) * H + oH] = (h2 - p.zp_h) * p.eff_h;
@@ -618,7 +621,7 @@ __device__ __forceinline__ void recurrence_cl_pair(const RecArgs &a, const StepP
         }
       }
       if (t + 1 < a.T) load_gih(t + 1);
-      alive = cluster::sync(counter, ++epoch * cl.G, cl.timeout);
+      alive = cluster::wait(counter, epoch * cl.G, cl.timeout);
     }
   }
 }

@@ -393,12 +393,12 @@ __global__ __launch_bounds__(512) void lstm_bwd_recurrence_cl(BwdArgs a, BwdClAr
     }
     for (int t = a.T - 1; t >= 0 && alive; --t) {
       const int par = t & 1;
-      float sv[2][4];
+      float sv[2][4], lis[2][4], lhs[2][4];
 #pragma unroll
       for (int rr = 0; rr < 2; ++rr) {
         const int nr = nrow0 + 2 * kh + rr, b = b0 + nr;
 #pragma unroll
-        for (int g = 0; g < 4; ++g) sv[rr][g] = 0.0f;
+        for (int g = 0; g < 4; ++g) sv[rr][g] = lis[rr][g] = lhs[rr][g] = 0.0f;
         if (b >= B) continue;
         const uint32_t e = static_cast<uint32_t>(t) * BH + static_cast<uint32_t>(b) * H + j;
         const uint32_t gb = static_cast<uint32_t>(t) * BC + static_cast<uint32_t>(b) * C + j;
@@ -424,11 +424,9 @@ __global__ __launch_bounds__(512) void lstm_bwd_recurrence_cl(BwdArgs a, BwdClAr
         for (int g = 0; g < 4; ++g) {
           const uint32_t gi_ = gb + g * H;
           const float grad = gi[g] * keepf(a.gin_m, gi_);
-          const float li = grad * keepf(a.ih_m, gi_);
-          const float lh = grad * keepf(a.hh_m, gi_);
-          a.dli[gi_] = li;
-          a.dlh[gi_] = lh;
-          sv[rr][g] = lh * sw[g];
+          lis[rr][g] = grad * keepf(a.ih_m, gi_);
+          lhs[rr][g] = grad * keepf(a.hh_m, gi_);
+          sv[rr][g] = lhs[rr][g] * sw[g];
         }
         dc[rr] = mdc * fg;
       }
@@ -474,7 +472,22 @@ __global__ __launch_bounds__(512) void lstm_bwd_recurrence_cl(BwdArgs a, BwdClAr
           cluster::store_bytes_coherent(dst + 2 * pstride, (uq >> 16) - 128);
         }
       }
-      alive = cluster::sync(counter, ++epoch * G, cl.timeout);
+      // the other members only read the planes and exponents: arrive, then store the gate
+      // gradients for the weight GEMMs while waiting
+      cluster::arrive(counter);
+      ++epoch;
+#pragma unroll
+      for (int rr = 0; rr < 2; ++rr) {
+        const int b = b0 + nrow0 + 2 * kh + rr;
+        if (b >= B) continue;
+        const uint32_t gb = static_cast<uint32_t>(t) * BC + static_cast<uint32_t>(b) * C + j;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          a.dli[gb + g * H] = lis[rr][g];
+          a.dlh[gb + g * H] = lhs[rr][g];
+        }
+      }
+      alive = cluster::wait(counter, epoch * G, cl.timeout);
       if (!alive) break;
       // dh of the tile's rows, this wave's K-half, member by member
       double dsum[4] = {0.0, 0.0, 0.0, 0.0};

@@ -661,6 +661,8 @@ __global__ __launch_bounds__(512) void lstm_recurrence_cl(RecArgs a, StepParams 
       if (t + 1 < a.T) load_lhs(t + 1);
       __syncthreads();
       // cell phase: rows 2 gp, 2 gp + 1 of the lane's four
+      float hvs[2], cts[2];
+      uint8_t mcs[2], mts[2], mhs[2];
 #pragma unroll
       for (int rr = 0; rr < 2; ++rr) {
         const int nr = nrow0 + 2 * gp + rr, b = b0 + nr;
@@ -670,40 +672,46 @@ __global__ __launch_bounds__(512) void lstm_recurrence_cl(RecArgs a, StepParams 
         const float pf = center_f(gout[1], sp.gout[1].zp) * center_f(cst[rr], sp.c.zp);
         const float pi = center_f(gout[0], sp.gout[0].zp) * center_f(gout[2], sp.gout[2].zp);
         const float sum = cell_scale(pf, sp, 0) + cell_scale(pi, sp, 1);
-        uint8_t m_c, m_t, m_h;
-        const float cn = clamp_grid_f(rintf(sum), sp.c, m_c);
+        const float cn = clamp_grid_f(rintf(sum), sp.c, mcs[rr]);
         cst[rr] = cn;
-        const float ct =
+        cts[rr] =
             tanh_lut ? lut_code(lut + cl.lut.tanh_off, static_cast<int>(cn) - sp.c.lo,
-                                sp.tanh_c.lo, m_t)
-                     : real_act(cn, sp.c, sp.tanh_c, true, m_t);
-        const float raw = center_f(gout[3], sp.gout[3].zp) * center_f(ct, sp.tanh_c.zp);
-        const float hv = clamp_grid_f(rescale(raw, sp.hidden.mult, sp.hidden.shift), sp.h, m_h);
-        if (b < B) {
-          const uint32_t oh = (static_cast<uint32_t>(t) * B + b) * static_cast<uint32_t>(H) + j;
-          a.output[oh] = dequant_f(hv, sp.h.scale, sp.h.zp);
-          if (train) {
-            a.cell[oh] = cn;
-            a.cell_tanh[oh] = ct;
-            a.hidden[oh] = hv;
-            a.cell_m[oh] = m_c;
-            a.cell_tanh_m[oh] = m_t;
-            a.hidden_m[oh] = m_h;
-          }
-          if (t == a.T - 1) {
-            const uint32_t os = static_cast<uint32_t>(b) * H + j;
-            a.h_n[os] = dequant_f(hv, sp.h.scale, sp.h.zp);
-            a.c_n[os] = dequant_f(cn, sp.c.scale, sp.c.zp);
-          }
-        }
-        const int hc = static_cast<int>(hv - a.h_offset);
+                                sp.tanh_c.lo, mts[rr])
+                     : real_act(cn, sp.c, sp.tanh_c, true, mts[rr]);
+        const float raw = center_f(gout[3], sp.gout[3].zp) * center_f(cts[rr], sp.tanh_c.zp);
+        hvs[rr] = clamp_grid_f(rescale(raw, sp.hidden.mult, sp.hidden.shift), sp.h, mhs[rr]);
+        const int hc = static_cast<int>(hvs[rr] - a.h_offset);
         unsigned char *dst = reinterpret_cast<unsigned char *>(hout) + static_cast<size_t>(b) * H + j;
 #pragma unroll
         for (int p = 0; p < NPL; ++p)
           cluster::store_bytes_coherent(dst + p * plane_stride,
                                         NPL == 1 ? hc : (p == 0 ? (hc & 255) - 128 : hc >> 8));
       }
-      alive = cluster::sync(counter, ++epoch * cl.G, cl.timeout);
+      // the other members only read the h codes: arrive, then store outputs while waiting
+      cluster::arrive(counter);
+      ++epoch;
+#pragma unroll
+      for (int rr = 0; rr < 2; ++rr) {
+        const int b = b0 + nrow0 + 2 * gp + rr;
+        if (b >= B) continue;
+        const float hv = hvs[rr], cn = cst[rr];
+        const uint32_t oh = (static_cast<uint32_t>(t) * B + b) * static_cast<uint32_t>(H) + j;
+        a.output[oh] = dequant_f(hv, sp.h.scale, sp.h.zp);
+        if (train) {
+          a.cell[oh] = cn;
+          a.cell_tanh[oh] = cts[rr];
+          a.hidden[oh] = hv;
+          a.cell_m[oh] = mcs[rr];
+          a.cell_tanh_m[oh] = mts[rr];
+          a.hidden_m[oh] = mhs[rr];
+        }
+        if (t == a.T - 1) {
+          const uint32_t os = static_cast<uint32_t>(b) * H + j;
+          a.h_n[os] = dequant_f(hv, sp.h.scale, sp.h.zp);
+          a.c_n[os] = dequant_f(cn, sp.c.scale, sp.c.zp);
+        }
+      }
+      alive = cluster::wait(counter, epoch * cl.G, cl.timeout);
     }
   }
 }
