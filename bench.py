@@ -136,19 +136,21 @@ INT8_MFMA_PEAK = 5000.0
 FP32_MFMA_PEAK = 157.3
 
 
-def _gru_kernel_work(B, T, I, H):
+def _gru_kernel_work(B, T, I, H, D=2):
+    """Algorithmic FLOPs per step of the instrumented c3 kernels (D directions): GEMM FLOPs
+    2*M*N*K as counted for the metric; peaks are MI355X's dense figures in TFLOP/s."""
     C = 3 * H
     M = T * B
     return {
-        "gru_fwd_recurrence": (2.0 * M * H * C, INT8_MFMA_PEAK,
-                               "recurrent GEMM R_q.h_q over T steps (int8 MFMA, 16-bit h as two "
-                               "byte planes)"),
-        "gru_bwd_recurrence": (2.0 * M * H * C, INT8_MFMA_PEAK,
-                               "dh GEMM R_q^T.dq over T steps (int8 MFMA, 3 planes of 22-bit "
-                               "block fixed point)"),
-        "gru_bwd_weight_gemms": (2.0 * M * C * (2 * I + H), FP32_MFMA_PEAK,
+        "gru_fwd_recurrence": (D * 2.0 * M * H * C, INT8_MFMA_PEAK,
+                               "recurrent GEMM R_q.h_q over T steps, both directions in one "
+                               "clustered launch (int8 MFMA, 16-bit h as two byte planes)"),
+        "gru_bwd_recurrence": (D * 2.0 * M * H * C, FP32_MFMA_PEAK,
+                               "dh GEMM R_deq.dq over T steps, both directions in one clustered "
+                               "launch (fp32 MFMA)"),
+        "gru_bwd_weight_gemms": (D * 2.0 * M * C * (2 * I + H), FP32_MFMA_PEAK,
                                  "dx, dW, dR fp32 GEMMs (rocBLAS)"),
-        "gru_fwd_input_gemm": (2.0 * M * C * I, FP32_MFMA_PEAK,
+        "gru_fwd_input_gemm": (D * 2.0 * M * C * I, FP32_MFMA_PEAK,
                                "input projection W_q.x_q exact integer GEMM"),
     }
 
@@ -177,39 +179,9 @@ def _gru_leg(torch, steps: int, warmup: int):
         out, _ = m(x)
         out.mean().backward()
 
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream(dev)
-    evs = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
-    rxmet_lib.prof_reset()
-    rxmet_lib.prof_enable(True)
-    t0 = time.perf_counter()
-    evs[0].record(stream)
-    for i in range(steps):
-        step()
-        evs[i + 1].record(stream)
-    torch.cuda.synchronize()
-    dt = (time.perf_counter() - t0) / steps
-    rxmet_lib.prof_enable(False)
-    per = sorted(evs[i].elapsed_time(evs[i + 1]) for i in range(steps))
-    p50 = per[len(per) // 2]
-    p95 = per[min(len(per) - 1, int(0.95 * len(per)))]
-    work = _gru_kernel_work(B, T, I, H)
-    kernels = {}
-    for name in rxmet_lib.prof_names():
-        ms, n = rxmet_lib.prof_query(name)
-        kernels[name] = {"ms_per_step": ms / steps, "launches_per_step": n / steps,
-                         "us_per_launch": ms / max(n, 1) * 1e3}
+    dt, p50, p95, kernels, roof = _timed_steps(torch, step, steps, warmup,
+                                               _gru_kernel_work(B, T, I, H))
     total = sum(k["ms_per_step"] for k in kernels.values())
-    dom = max((k for k in kernels if k in work), key=lambda k: kernels[k]["ms_per_step"])
-    flops, peak, what = work[dom]
-    t_launch = kernels[dom]["us_per_launch"] * 1e-6
-    achieved = flops / t_launch / 1e12
-    roof = {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 3), "peak": peak,
-            "unit": "TFLOP/s", "frac": round(achieved / peak, 6), "traffic": None,
-            "algorithmic_flops_per_launch": flops, "work": what,
-            "us_per_launch": round(kernels[dom]["us_per_launch"], 2)}
     _log(f"gru c3: {dt*1e3:.2f} ms/step wall, P50 {p50:.2f} ms P95 {p95:.2f} ms, "
          f"{B/dt:.1f} seq/s; instrumented kernels {total:.2f} ms/step")
     for k, v in sorted(kernels.items(), key=lambda kv: -kv[1]["ms_per_step"]):
@@ -221,6 +193,7 @@ def _gru_leg(torch, steps: int, warmup: int):
 
 
 def _lstm_kernel_work(B, T, I, H):
+    """Algorithmic FLOPs per step of the instrumented c4 kernels (one direction)."""
     C = 4 * H
     M = T * B
     return {
@@ -269,7 +242,8 @@ def _timed_steps(torch, step, steps, warmup, work):
         kernels[name] = {"ms_per_step": ms / steps, "launches_per_step": n / steps,
                          "us_per_launch": ms / max(n, 1) * 1e3}
     dom = max((k for k in kernels if k in work), key=lambda k: kernels[k]["ms_per_step"])
-    flops, peak, what = work[dom]
+    flops_step, peak, what = work[dom]
+    flops = flops_step / kernels[dom]["launches_per_step"]
     achieved = flops / (kernels[dom]["us_per_launch"] * 1e-6) / 1e12
     roof = {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 3), "peak": peak,
             "unit": "TFLOP/s", "frac": round(achieved / peak, 6), "traffic": None,
@@ -408,7 +382,11 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--legs", default="gru,lstm,qdq",
+                    help="comma-separated subset of gru,lstm,qdq (profiling runs); the default "
+                         "record runs all three")
     args = ap.parse_args()
+    legs = set(args.legs.split(","))
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the path is data-parallel by batch; "
               "multi-GPU runs are not part of it)", file=sys.stderr)
@@ -418,24 +396,33 @@ def main() -> int:
     torch.backends.cuda.matmul.allow_tf32 = False
     torch.backends.cudnn.allow_tf32 = False
     _log(f"device: {torch.cuda.get_device_name(0)}")
-    gru, roof, m, x = _gru_leg(torch, args.steps, args.warmup)
-    lstm, lstm_roof, lm, lx, lg = _lstm_leg(torch, args.steps, args.warmup)
-    qdq, qdq_roof = _qdq_leg(torch, args.steps, args.warmup)
+    gru = roof = lstm = lstm_roof = qdq = qdq_roof = None
+    if "gru" in legs:
+        gru, roof, m, x = _gru_leg(torch, args.steps, args.warmup)
+    if "lstm" in legs:
+        lstm, lstm_roof, lm, lx, lg = _lstm_leg(torch, args.steps, args.warmup)
+    if "qdq" in legs:
+        qdq, qdq_roof = _qdq_leg(torch, args.steps, args.warmup)
     cpu = cpu_qdq = cpu_lstm = None
     if not args.no_cpu_baseline:
-        cpu = _gru_cpu_baseline(m, x)
-        _log(f"cpu baseline: {cpu}")
-        cpu_lstm = _lstm_cpu_baseline(lm, lx, lg)
-        _log(f"lstm cpu baseline: {cpu_lstm}")
-        cpu_qdq = _qdq_cpu_baseline()
+        if gru is not None:
+            cpu = _gru_cpu_baseline(m, x)
+            _log(f"cpu baseline: {cpu}")
+        if lstm is not None:
+            cpu_lstm = _lstm_cpu_baseline(lm, lx, lg)
+            _log(f"lstm cpu baseline: {cpu_lstm}")
+        if qdq is not None:
+            cpu_qdq = _qdq_cpu_baseline()
+    rnd = lambda d: None if d is None else {k: (round(v, 4) if isinstance(v, float) else v)
+                                            for k, v in d.items()}
     line = {
         "metric": METRIC,
-        "value": round(gru["seq_per_s"], 2),
+        "value": round(gru["seq_per_s"], 2) if gru else None,
         "unit": "seq/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(gru["ms_per_step"], 4),
+        "ms_per_step": round(gru["ms_per_step"], 4) if gru else None,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -447,9 +434,10 @@ def main() -> int:
                                "loss = mean(output)",
                    "batch": 256, "seq_len": 200, "input_size": 80, "hidden_size": 256,
                    "carrier": "fp32 codes; recurrent GEMMs on int8 MFMA"},
-        "gru": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in gru.items()},
-        "lstm": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in lstm.items()},
-        "qdq": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in qdq.items()},
+        "gru": rnd(gru),
+        "lstm": rnd(lstm),
+        "qdq": None if qdq is None else {k: {kk: round(vv, 3) for kk, vv in v.items()}
+                                         for k, v in qdq.items()},
         "roofline": roof,
         "lstm_roofline": lstm_roof,
         "qdq_roofline": qdq_roof,

@@ -7,6 +7,8 @@
 // and stops stepping, so every wave of the grid reaches the end of the kernel.
 #pragma once
 
+#include <cstdlib>
+
 #include <hip/hip_runtime.h>
 
 namespace rxmet {
@@ -130,6 +132,18 @@ static __global__ void poison_nan(const int *timeout, int64_t n, float *p) {
   const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
     p[i] = NAN;
+}
+
+// Launch a clustered recurrence.  The launch is cooperative, which guarantees that every
+// workgroup of the grid is resident at once.  With RXMET_PLAIN_LAUNCH set it is an ordinary
+// launch of the same grid (for profilers that cannot trace cooperative launches): residency
+// then holds only while nothing else occupies the GPU, and a wait that times out poisons the
+// outputs with NaN instead of hanging.
+inline hipError_t launch(const void *fn, dim3 grid, dim3 block, void **args, unsigned lds,
+                         hipStream_t stream) {
+  if (std::getenv("RXMET_PLAIN_LAUNCH") != nullptr)
+    return hipLaunchKernel(fn, grid, block, args, lds, stream);
+  return hipLaunchCooperativeKernel(fn, grid, block, args, lds, stream);
 }
 
 }  // namespace cluster

@@ -1,0 +1,162 @@
+// exact_gemm.h — exact integer GEMM of fp32-stored quantisation codes on int8 MFMA.
+//
+//   S[m][n] = sum_k (A[m][k] - base) * B(k, n)
+//
+// for integer-valued codes.  A is shifted by `off` (from the bottom of its grid) into the
+// signed range of PA byte planes: one plane holds [-128, 127], two planes (v = 256 hi + lo,
+// both in [-128, 127]) hold [-32896, 32639].  B is used as is: one signed byte plane for codes
+// in [-128, 127], or two planes for 16-bit codes, B = 256 bh + bl + 128 with bh = B >> 8 and
+// bl = (B & 255) - 128.  Every plane pair accumulates exactly in int32 on
+// v_mfma_i32_16x16x64_i8 (|sum| <= K * 2^14 < 2^31 for K < 2^17); the row sums of A and the
+// column sums of B come from the same MFMA against an all-ones fragment; everything is
+// combined in int64:
+//   sum_k (A - off) B  = sum_pa sum_pb 256^pa w_pb acc[pa][pb]  (+ 128 rowsum(A - off) if PB=2)
+//   S                  = sum_k (A - off) B + (off - base) colsum(B).
+//
+// Workgroup: 256 threads, a 64 x 64 block of outputs; wave w owns rows 32 (w / 2) .. +31 and
+// columns 32 (w % 2) .. +31 as 2 x 2 tiles of 16 x 16.  K advances in chunks of 64 staged in
+// LDS as byte planes ([row][k] for A, [column][k] for B).
+#pragma once
+
+#include <cstdint>
+
+#include "mfma_frag.h"
+
+namespace rxmet {
+namespace xgemm {
+
+constexpr int kTile = 64;
+constexpr int kRowBytes = 64 + 16;  // LDS row stride (conflict-free 16-byte reads)
+
+struct Operands {
+  int M, N, K;
+  const float *A;  // A[m * lda + k]
+  int lda;
+  float off;       // shift of A (integer valued)
+  long long corr;  // off - base
+  const float *B;  // B(k, n) = B[k * sbk + n * sbn]
+  int sbk, sbn;
+};
+
+// Computes the 64 x 64 block at (tm, tn) and calls epi(m, n, S) for every in-range output.
+template <int PA, int PB, typename Epi>
+__device__ __forceinline__ void block(const Operands &o, int tm, int tn, Epi epi) {
+  __shared__ __align__(16) int8_t As[PA][kTile][kRowBytes];
+  __shared__ __align__(16) int8_t Bs[PB][kTile][kRowBytes];
+  const int tid = threadIdx.x, w = tid / 64, l = tid % 64;
+  const int wm = 32 * (w / 2), wn = 32 * (w % 2);
+  v4i acc[PA][PB][2][2];
+  v4i csum[PB][2], rsum[PA][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int pa = 0; pa < PA; ++pa)
+#pragma unroll
+        for (int pb = 0; pb < PB; ++pb) acc[pa][pb][i][j] = v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int pb = 0; pb < PB; ++pb) csum[pb][i] = v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int pa = 0; pa < PA; ++pa) rsum[pa][i] = v4i{0, 0, 0, 0};
+  }
+  const int one = 0x01010101;
+  const v4i ones = {one, one, one, one};
+  const bool b_nmajor = o.sbn == 1;  // B stored [K][N]: coalesce along n
+  int kp = 0;                        // k positions processed (padding included)
+  for (int k0 = 0; k0 < o.K; k0 += kTile, kp += kTile) {
+    for (int e = tid; e < kTile * kTile; e += 256) {
+      const int r = e / kTile, kk = e % kTile;
+      const int gm = tm + r, gk = k0 + kk;
+      int v = 0;
+      if (gm < o.M && gk < o.K)
+        v = static_cast<int>(o.A[static_cast<size_t>(gm) * o.lda + gk] - o.off);
+      if (PA == 1) {
+        As[0][r][kk] = static_cast<int8_t>(v);
+      } else {
+        const int lo = ((v + 128) & 255) - 128;
+        As[0][r][kk] = static_cast<int8_t>(lo);
+        As[PA - 1][r][kk] = static_cast<int8_t>((v - lo) >> 8);
+      }
+    }
+    for (int e = tid; e < kTile * kTile; e += 256) {
+      const int n = b_nmajor ? e % kTile : e / kTile, kk = b_nmajor ? e / kTile : e % kTile;
+      const int gn = tn + n, gk = k0 + kk;
+      int v = 0;
+      if (gn < o.N && gk < o.K)
+        v = static_cast<int>(o.B[static_cast<size_t>(gk) * o.sbk + static_cast<size_t>(gn) * o.sbn]);
+      if (PB == 1) {
+        Bs[0][n][kk] = static_cast<int8_t>(v);
+      } else {
+        Bs[0][n][kk] = static_cast<int8_t>((v & 255) - 128);
+        Bs[PB - 1][n][kk] = static_cast<int8_t>(v >> 8);
+      }
+    }
+    __syncthreads();
+    v4i af[PA][2], bf[PB][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+      for (int pa = 0; pa < PA; ++pa)
+        af[pa][i] = *reinterpret_cast<const v4i *>(&As[pa][wm + 16 * i + l % 16][16 * (l / 16)]);
+#pragma unroll
+      for (int pb = 0; pb < PB; ++pb)
+        bf[pb][i] = *reinterpret_cast<const v4i *>(&Bs[pb][wn + 16 * i + l % 16][16 * (l / 16)]);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int pa = 0; pa < PA; ++pa)
+#pragma unroll
+          for (int pb = 0; pb < PB; ++pb)
+            acc[pa][pb][i][j] = mfma_i8(af[pa][i], bf[pb][j], acc[pa][pb][i][j]);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int pb = 0; pb < PB; ++pb) csum[pb][j] = mfma_i8(ones, bf[pb][j], csum[pb][j]);
+    if (PB == 2) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int pa = 0; pa < PA; ++pa) rsum[pa][i] = mfma_i8(af[pa][i], ones, rsum[pa][i]);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int n = tn + wn + 16 * j + l % 16;
+    long long cs = csum[0][j][0];
+    if (PB == 2) cs = 256LL * csum[PB - 1][j][0] + cs + 128LL * kp;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = tm + wm + 16 * i + 4 * (l / 16) + r;
+        if (m >= o.M || n >= o.N) continue;
+        long long s = o.corr * cs;
+#pragma unroll
+        for (int pa = 0; pa < PA; ++pa) {
+#pragma unroll
+          for (int pb = 0; pb < PB; ++pb)
+            s += static_cast<long long>(acc[pa][pb][i][j][r]) << (8 * (pa + pb));
+          if (PB == 2) s += (static_cast<long long>(rsum[pa][i][r]) << (8 * pa)) * 128;
+        }
+        epi(m, n, s);
+      }
+  }
+}
+
+// Planes and shift for A codes in [lo, hi]; planes of B for codes in [lo, hi].
+inline int a_planes(double lo, double hi) { return hi - lo <= 255.0 ? 1 : 2; }
+inline float a_shift(double lo, double hi) {
+  return static_cast<float>(hi - lo <= 255.0 ? lo + 128.0 : lo + 32896.0);
+}
+inline int b_planes(double lo, double hi) { return (lo >= -128.0 && hi <= 127.0) ? 1 : 2; }
+// Ranges the planes can carry: A spans at most 2^16 codes, B is within signed 16 bits.
+inline bool a_fits(double lo, double hi) { return hi - lo <= 65535.0; }
+inline bool b_fits(double lo, double hi) { return lo >= -32768.0 && hi <= 32767.0; }
+
+}  // namespace xgemm
+}  // namespace rxmet

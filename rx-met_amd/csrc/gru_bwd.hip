@@ -716,7 +716,7 @@ static int backward_recurrence_clustered(BwdPlan *plans, int ndir, int T, int B,
   void *args[] = {&plans[0].ba, &a1, &cl};
   {
     rxmet::prof::Scope ps__("gru_bwd_recurrence", stream);
-    RXMET_CHECK_HIP(hipLaunchCooperativeKernel(fn, dim3(ncl * cl.G), dim3(256 * cl.UT), args,
+    RXMET_CHECK_HIP(cluster::launch(fn, dim3(ncl * cl.G), dim3(256 * cl.UT), args,
                                                static_cast<unsigned>(lds_cl), stream));
   }
   for (int k = 0; k < ndir; ++k) {

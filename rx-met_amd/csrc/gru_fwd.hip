@@ -26,6 +26,7 @@
 #include <vector>
 
 #include "cluster.h"
+#include "exact_gemm.h"
 #include "gru_internal.h"
 #include "mfma_frag.h"
 #include "rxmet_common.h"
@@ -125,50 +126,22 @@ __global__ __launch_bounds__(256) void quant_input(int64_t nx, int64_t nh, const
 // ---------------------------------------------------------------------------------
 // 3. exact code GEMM  C[M][N] = A[M][K] * B[K][N]  (integer codes stored as fp32)
 // ---------------------------------------------------------------------------------
-template <typename Acc>
-__global__ __launch_bounds__(256) void code_gemm(int M, int N, int K, const float *__restrict__ A,
-                                                 const float *__restrict__ Bm,
-                                                 float *__restrict__ Cm) {
-  __shared__ int As[16][64 + 1];
-  __shared__ int Bs[16][64];
-  const int tm = blockIdx.y * 64, tn = blockIdx.x * 64;
-  const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
-  Acc acc[4][4] = {};
-  for (int k0 = 0; k0 < K; k0 += 16) {
-    for (int q = 0; q < 4; ++q) {
-      const int e = threadIdx.x + 256 * q;
-      const int row = e / 16, kk = e % 16;
-      const int gm = tm + row, gk = k0 + kk;
-      As[kk][row] = (gm < M && gk < K) ? static_cast<int>(A[static_cast<size_t>(gm) * K + gk]) : 0;
-      const int kb = e / 64, col = e % 64;
-      const int gkb = k0 + kb, gn = tn + col;
-      Bs[kb][col] = (gkb < K && gn < N) ? static_cast<int>(Bm[static_cast<size_t>(gkb) * N + gn]) : 0;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int kk = 0; kk < 16; ++kk) {
-      int av[4], bv[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) av[i] = As[kk][ty * 4 + i];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) bv[j] = Bs[kk][tx * 4 + j];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] += static_cast<Acc>(av[i]) * bv[j];
-    }
-    __syncthreads();
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int gm = tm + ty * 4 + i;
-    if (gm >= M) continue;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int gn = tn + tx * 4 + j;
-      if (gn < N) Cm[static_cast<size_t>(gm) * N + gn] = static_cast<float>(acc[i][j]);
-    }
-  }
+// On int8 MFMA with byte planes (exact_gemm.h); the exact integer is rounded once to fp32.
+template <int PA, int PB>
+__global__ __launch_bounds__(256) void code_gemm(xgemm::Operands o, float *__restrict__ Cm) {
+  xgemm::block<PA, PB>(o, blockIdx.y * xgemm::kTile, blockIdx.x * xgemm::kTile,
+                       [&](int m, int n, long long s) {
+                         Cm[static_cast<size_t>(m) * o.N + n] = static_cast<float>(s);
+                       });
+}
+
+template <int PA>
+static void launch_code_gemm(int pb, dim3 grid, hipStream_t stream, const xgemm::Operands &o,
+                             float *C) {
+  if (pb == 1)
+    hipLaunchKernelGGL((code_gemm<PA, 1>), grid, dim3(256), 0, stream, o, C);
+  else
+    hipLaunchKernelGGL((code_gemm<PA, 2>), grid, dim3(256), 0, stream, o, C);
 }
 
 // ---------------------------------------------------------------------------------
@@ -715,11 +688,13 @@ static int forward_prologue(bool training, int T, int B, int I, int H, const rxm
                         (d.h0 == nullptr || d.h0_mask),
                     "training needs v and every mask output");
   }
-  // the input projection accumulates in int32 when |x_q| |W_q| I cannot reach 2^31,
-  // otherwise in int64 (codes are at most 16 bits, I < 2^31: always exact)
-  const bool wide_gemm = std::ldexp(1.0, params->g[RXMET_GRU_X].bits) *
-                             std::ldexp(1.0, params->chan_bits[RXMET_GRU_W] - 1) * I >=
-                         2147483647.0;
+  RXMET_CHECK_ARG(I < (1 << 17), "input_size must be below 131072 for the exact input GEMM");
+  {
+    const Bounds bx = bounds_of(params->g[RXMET_GRU_X].bits, params->g[RXMET_GRU_X].is_unsigned);
+    const Bounds bw = bounds_of(params->chan_bits[RXMET_GRU_W], params->chan_unsigned[RXMET_GRU_W]);
+    RXMET_CHECK_ARG(xgemm::a_fits(bx.lo, bx.hi) && xgemm::b_fits(bw.lo, bw.hi),
+                    "x and W codes must fit 16 bits (signed W) for the exact input GEMM");
+  }
   const int C = 3 * H;
   const FwdWorkspace ws(T, B, I, H);
   char *wsb = static_cast<char *>(d.workspace);
@@ -785,13 +760,22 @@ static int forward_prologue(bool training, int T, int B, int I, int H, const rxm
 
   const int M = T * B;
   {
+    // x codes lie on the x grid, W codes on the (symmetric or not) W grid
+    xgemm::Operands o;
+    o.M = M; o.N = C; o.K = I;
+    o.A = d.x_q; o.lda = I;
+    const Bounds bx = bounds_of(g[RXMET_GRU_X].bits, g[RXMET_GRU_X].is_unsigned);
+    const double xlo = bx.lo, xhi = bx.hi;
+    o.off = xgemm::a_shift(xlo, xhi);
+    o.corr = static_cast<long long>(o.off);
+    o.B = d.W_q; o.sbk = C; o.sbn = 1;
+    const int pa = xgemm::a_planes(xlo, xhi), pb = xgemm::b_planes(wa.bW.lo, wa.bW.hi);
+    const dim3 grid((C + 63) / 64, (M + 63) / 64);
     rxmet::prof::Scope ps__("gru_fwd_input_gemm", stream);
-    if (wide_gemm)
-      hipLaunchKernelGGL(code_gemm<long long>, dim3((C + 63) / 64, (M + 63) / 64), dim3(256), 0,
-                         stream, M, C, I, d.x_q, d.W_q, gih);
+    if (pa == 1)
+      launch_code_gemm<1>(pb, grid, stream, o, gih);
     else
-      hipLaunchKernelGGL(code_gemm<int>, dim3((C + 63) / 64, (M + 63) / 64), dim3(256), 0, stream,
-                         M, C, I, d.x_q, d.W_q, gih);
+      launch_code_gemm<2>(pb, grid, stream, o, gih);
   }
   RXMET_CHECK_LAUNCH();
 
@@ -868,7 +852,7 @@ static int forward_recurrence_clustered(FwdPlan *plans, int ndir, int T, int B, 
   void *args[] = {&plans[0].ra, &a1, &ps, &cl};
   {
     rxmet::prof::Scope ps__("gru_fwd_recurrence", stream);
-    RXMET_CHECK_HIP(hipLaunchCooperativeKernel(fn, dim3(ncl * cl.G), dim3(256 * cl.UT), args,
+    RXMET_CHECK_HIP(cluster::launch(fn, dim3(ncl * cl.G), dim3(256 * cl.UT), args,
                                                static_cast<unsigned>(lds_cl), stream));
   }
   const int64_t n_h = static_cast<int64_t>(T + 1) * B * H;

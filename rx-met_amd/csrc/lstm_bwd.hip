@@ -699,9 +699,6 @@ int rxmet_lstm_backward_quant(int32_t T, int32_t B, int32_t I, int32_t H,
     hipLaunchKernelGGL(lstm_bwd_prep, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, pa);
     RXMET_CHECK_LAUNCH();
   }
-  hipLaunchKernelGGL(lstm_pack_whh_t, dim3(UT * KS2), dim3(64), 0, stream, H, KS2, sv.w_hh_q, frag,
-                     colsum);
-  RXMET_CHECK_LAUNCH();
 
   BwdArgs ba;
   ba.T = T; ba.B = B; ba.H = H; ba.KS2 = KS2; ba.UT = UT;
@@ -752,7 +749,7 @@ int rxmet_lstm_backward_quant(int32_t T, int32_t B, int32_t I, int32_t H,
       void *args[] = {&ba, &cl};
       {
         rxmet::prof::Scope ps__("lstm_bwd_recurrence", stream);
-        RXMET_CHECK_HIP(hipLaunchCooperativeKernel(fn, dim3(ncl * cl.G), dim3(512), args,
+        RXMET_CHECK_HIP(cluster::launch(fn, dim3(ncl * cl.G), dim3(512), args,
                                                    static_cast<unsigned>(lds_cl), stream));
       }
       const int64_t n_state = static_cast<int64_t>(B) * H;
@@ -766,6 +763,9 @@ int rxmet_lstm_backward_quant(int32_t T, int32_t B, int32_t I, int32_t H,
     }
   }
   if (!clustered) {
+    hipLaunchKernelGGL(lstm_pack_whh_t, dim3(UT * KS2), dim3(64), 0, stream, H, KS2, sv.w_hh_q, frag,
+                       colsum);
+    RXMET_CHECK_LAUNCH();
     const size_t lds = bwd_lds(H, KS2);
     rxmet::prof::Scope ps__("lstm_bwd_recurrence", stream);
     RXMET_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&lstm_bwd_recurrence),

@@ -33,6 +33,7 @@
 #include <vector>
 
 #include "cluster.h"
+#include "exact_gemm.h"
 #include "lstm_internal.h"
 #include "mfma_frag.h"
 #include "rxmet_common.h"
@@ -222,64 +223,27 @@ __global__ __launch_bounds__(64) void lstm_pack_whh(int H, int KS, const float *
 // ---------------------------------------------------------------------------------
 // 4. input linear of all steps, exact, with the input branch fused in the epilogue
 // ---------------------------------------------------------------------------------
-template <typename Acc>
-__global__ __launch_bounds__(256) void lstm_input_gemm(int M, int C, int K, int H,
-                                                       const float *__restrict__ xq,
-                                                       const float *__restrict__ wq,
+template <int PA, int PB>
+__global__ __launch_bounds__(256) void lstm_input_gemm(xgemm::Operands o, int H,
                                                        const ChanHost *__restrict__ ch,
                                                        const ChanRun *__restrict__ run,
                                                        StepParams sp, float *__restrict__ lhs,
                                                        uint8_t *__restrict__ lin_mask) {
-  __shared__ int As[16][64 + 1];
-  __shared__ int Bs[16][64 + 1];
-  const int tm = blockIdx.y * 64, tn = blockIdx.x * 64;
-  const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
-  const int zx = sp.x.zp;
-  Acc acc[4][4] = {};
-  for (int k0 = 0; k0 < K; k0 += 16) {
-    for (int q = 0; q < 4; ++q) {
-      const int e = threadIdx.x + 256 * q;
-      const int row = e / 16, kk = e % 16;
-      const int gm = tm + row, gk = k0 + kk, gn = tn + row;
-      As[kk][row] = (gm < M && gk < K) ? static_cast<int>(xq[static_cast<size_t>(gm) * K + gk]) - zx : 0;
-      Bs[kk][row] = (gn < C && gk < K) ? static_cast<int>(wq[static_cast<size_t>(gn) * K + gk]) : 0;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int kk = 0; kk < 16; ++kk) {
-      int av[4], bv[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) av[i] = As[kk][ty * 4 + i];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) bv[j] = Bs[kk][tx * 4 + j];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] += static_cast<Acc>(av[i]) * bv[j];
-    }
-    __syncthreads();
-  }
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int c = tn + tx * 4 + j;
-    if (c >= C) continue;
-    const int g = c / H;
-    const float bacc = run[c].ih_bacc;
-    const float mult = ch[c].ih_mult;
-    const int shift = ch[c].ih_shift;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int m = tm + ty * 4 + i;
-      if (m >= M) continue;
-      const float accf = static_cast<float>(acc[i][j]) + bacc;
-      uint8_t clamped;
-      const float lin = clamp_grid(static_cast<double>(rescale(accf, mult, shift)) + sp.ih_lin.dzp,
-                                   sp.ih_lin, clamped);
-      const size_t o = static_cast<size_t>(m) * C + c;
-      lhs[o] = rescale(center(lin, sp.ih_lin.zp), sp.ih_to_gate[g].mult, sp.ih_to_gate[g].shift);
-      if (lin_mask) lin_mask[o] = clamped;
-    }
-  }
+  const int C = o.N;
+  xgemm::block<PA, PB>(o, blockIdx.y * xgemm::kTile, blockIdx.x * xgemm::kTile,
+                       [&](int m, int c, long long s) {
+                         const int g = c / H;
+                         const float accf = static_cast<float>(s) + run[c].ih_bacc;
+                         uint8_t clamped;
+                         const float lin = clamp_grid(
+                             static_cast<double>(rescale(accf, ch[c].ih_mult, ch[c].ih_shift)) +
+                                 sp.ih_lin.dzp,
+                             sp.ih_lin, clamped);
+                         const size_t oi = static_cast<size_t>(m) * C + c;
+                         lhs[oi] = rescale(center(lin, sp.ih_lin.zp), sp.ih_to_gate[g].mult,
+                                           sp.ih_to_gate[g].shift);
+                         if (lin_mask) lin_mask[oi] = clamped;
+                       });
 }
 
 // ---------------------------------------------------------------------------------
@@ -818,10 +782,9 @@ int rxmet_lstm_forward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const f
   ChannelParams cp;
   if (int rc = derive(*params, &sp, &cp)) return rc;
   const int C = 4 * H, KS = (H + 63) / 64, UT = H / 16;
-  // exact int32 bound of the input branch and of the recurrent MFMA sum
-  const double xmax = std::ldexp(1.0, params->config.op[RXMET_LSTM_INPUT].bits);
-  const double wmax = std::ldexp(1.0, params->config.op[RXMET_LSTM_W_IH].bits - 1);
-  const bool wide = xmax * wmax * I >= 2147483647.0;
+  // the input branch is an exact byte-plane GEMM; the recurrent MFMA sum must fit int32
+  RXMET_CHECK_ARG(I < (1 << 17), "input_size must be below 131072 for the exact input GEMM");
+  RXMET_CHECK_ARG(xgemm::a_fits(sp.x.lo, sp.x.hi), "input codes must span at most 16 bits");
   RXMET_CHECK_ARG(std::ldexp(1.0, h_t.bits) * 128.0 * H < 2147483647.0,
                   "recurrent accumulator would overflow int32");
 
@@ -886,14 +849,28 @@ int rxmet_lstm_forward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const f
   RXMET_CHECK_LAUNCH();
   const int M = T * B;
   {
-    rxmet::prof::Scope ps__("lstm_fwd_input_gemm", stream);
+    RXMET_CHECK_ARG(xgemm::b_fits(gwi.lo, gwi.hi), "W_ih codes must be signed 16-bit at most");
+    xgemm::Operands o;
+    o.M = M; o.N = C; o.K = I;
+    o.A = xq; o.lda = I;
+    o.off = xgemm::a_shift(sp.x.lo, sp.x.hi);
+    o.corr = static_cast<long long>(o.off) - sp.x.zp;
+    o.B = wih; o.sbk = 1; o.sbn = I;  // W_ih codes [4H][I]
+    const int pa = xgemm::a_planes(sp.x.lo, sp.x.hi), pb = xgemm::b_planes(gwi.lo, gwi.hi);
     const dim3 grid((C + 63) / 64, (M + 63) / 64);
-    if (wide)
-      hipLaunchKernelGGL(lstm_input_gemm<long long>, grid, dim3(256), 0, stream, M, C, I, H, xq,
-                         wih, chost, run, sp, lhs, sv.ih_linear_m);
+    rxmet::prof::Scope ps__("lstm_fwd_input_gemm", stream);
+    if (pa == 1 && pb == 1)
+      hipLaunchKernelGGL((lstm_input_gemm<1, 1>), grid, dim3(256), 0, stream, o, H, chost, run, sp,
+                         lhs, sv.ih_linear_m);
+    else if (pa == 1)
+      hipLaunchKernelGGL((lstm_input_gemm<1, 2>), grid, dim3(256), 0, stream, o, H, chost, run, sp,
+                         lhs, sv.ih_linear_m);
+    else if (pb == 1)
+      hipLaunchKernelGGL((lstm_input_gemm<2, 1>), grid, dim3(256), 0, stream, o, H, chost, run, sp,
+                         lhs, sv.ih_linear_m);
     else
-      hipLaunchKernelGGL(lstm_input_gemm<int>, grid, dim3(256), 0, stream, M, C, I, H, xq, wih,
-                         chost, run, sp, lhs, sv.ih_linear_m);
+      hipLaunchKernelGGL((lstm_input_gemm<2, 2>), grid, dim3(256), 0, stream, o, H, chost, run, sp,
+                         lhs, sv.ih_linear_m);
   }
   RXMET_CHECK_LAUNCH();
 
@@ -970,7 +947,7 @@ int rxmet_lstm_forward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const f
       void *args[] = {&ra, &sp, &cl};
       {
         rxmet::prof::Scope ps__("lstm_fwd_recurrence", stream);
-        RXMET_CHECK_HIP(hipLaunchCooperativeKernel(fn, dim3(ncl * cl.G), dim3(512), args,
+        RXMET_CHECK_HIP(cluster::launch(fn, dim3(ncl * cl.G), dim3(512), args,
                                                    static_cast<unsigned>(lds_cl), stream));
       }
       const int64_t n_out = static_cast<int64_t>(T) * B * H, n_state = static_cast<int64_t>(B) * H;
