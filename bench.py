@@ -36,6 +36,32 @@ def _log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic.json"
+
+
+def _traffic(kernel: str):
+    """HBM bytes per launch of an instrumented kernel, from the committed counter summary
+    (rocprofv3 FETCH_SIZE and WRITE_SIZE passes, each scaled by what the counter reads for a
+    plain copy of known size), or None when the kernel was not measured."""
+    try:
+        rec = json.loads(TRAFFIC_FILE.read_text())["kernels"].get(kernel)
+    except (OSError, ValueError, KeyError):
+        return None
+    return None if rec is None else int(rec["fetch_bytes"] + rec["write_bytes"])
+
+
+def _copy_probe(torch, mib: int) -> None:
+    """One elementwise pass (read N bytes, write N bytes) over a buffer of `mib` MiB: the
+    reference kernel that scales the HBM byte counters of a profiling run."""
+    n = mib * (1 << 20) // 4
+    a = torch.ones(n, device="cuda:0")
+    b = torch.empty_like(a)
+    for _ in range(3):
+        torch.neg(a, out=b)
+    torch.cuda.synchronize()
+    _log(f"copy probe: 3 x neg over {mib} MiB")
+
+
 def _qdq_leg(torch, steps: int, warmup: int):
     """c2: learnable-encoding QDQ fwd+bwd on [8192, 8192] (both encodings of c2)."""
     import numpy as np
@@ -124,7 +150,8 @@ def _qdq_leg(torch, steps: int, warmup: int):
          f"bwd {t_b*1e6:.1f} us ({12*n/t_b/1e9:.0f} GB/s)")
     roof = {"kernel": "qdq bwd_runs<LEARNABLE> (fused STE + encoding grads)", "bound": "hbm",
             "achieved": round(12 * n / t_b / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(12 * n / t_b / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
+            "frac": round(12 * n / t_b / 1e9 / HBM_PEAK_GBS, 4),
+            "traffic": _traffic("qdq_bwd_learnable"),
             "algorithmic_bytes_per_launch": 12 * n}
     return results, roof
 
@@ -188,7 +215,8 @@ def _gru_leg(torch, steps: int, warmup: int):
         _log(f"  {k}: {v['ms_per_step']:.3f} ms/step, {v['us_per_launch']:.1f} us/launch")
     res = {"ms_per_step": dt * 1e3, "p50_ms": p50, "p95_ms": p95, "seq_per_s": B / dt,
            "seq_per_s_p50": B / (p50 * 1e-3),
-           "kernels_ms_per_step": {k: round(v["ms_per_step"], 4) for k, v in kernels.items()}}
+           "kernels_ms_per_step": {k: round(v["ms_per_step"], 4) for k, v in kernels.items()},
+           "kernels_us_per_launch": {k: round(v["us_per_launch"], 2) for k, v in kernels.items()}}
     return res, roof, m, x
 
 
@@ -246,7 +274,7 @@ def _timed_steps(torch, step, steps, warmup, work):
     flops = flops_step / kernels[dom]["launches_per_step"]
     achieved = flops / (kernels[dom]["us_per_launch"] * 1e-6) / 1e12
     roof = {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 3), "peak": peak,
-            "unit": "TFLOP/s", "frac": round(achieved / peak, 6), "traffic": None,
+            "unit": "TFLOP/s", "frac": round(achieved / peak, 6), "traffic": _traffic(dom),
             "algorithmic_flops_per_launch": flops, "work": what,
             "us_per_launch": round(kernels[dom]["us_per_launch"], 2)}
     return dt, p50, p95, kernels, roof
@@ -288,7 +316,8 @@ def _lstm_leg(torch, steps: int, warmup: int):
         _log(f"  {k}: {v['ms_per_step']:.3f} ms/step, {v['us_per_launch']:.1f} us/launch")
     res = {"ms_per_step": dt * 1e3, "p50_ms": p50, "p95_ms": p95, "seq_per_s": B / dt,
            "seq_per_s_p50": B / (p50 * 1e-3),
-           "kernels_ms_per_step": {k: round(v["ms_per_step"], 4) for k, v in kernels.items()}}
+           "kernels_ms_per_step": {k: round(v["ms_per_step"], 4) for k, v in kernels.items()},
+           "kernels_us_per_launch": {k: round(v["us_per_launch"], 2) for k, v in kernels.items()}}
     return res, roof, m, x, g
 
 
@@ -385,6 +414,9 @@ def main() -> int:
     ap.add_argument("--legs", default="gru,lstm,qdq",
                     help="comma-separated subset of gru,lstm,qdq (profiling runs); the default "
                          "record runs all three")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="first run a plain elementwise copy over MIB MiB (scales HBM byte "
+                         "counters in profiling runs)")
     args = ap.parse_args()
     legs = set(args.legs.split(","))
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -396,6 +428,8 @@ def main() -> int:
     torch.backends.cuda.matmul.allow_tf32 = False
     torch.backends.cudnn.allow_tf32 = False
     _log(f"device: {torch.cuda.get_device_name(0)}")
+    if args.copy_probe:
+        _copy_probe(torch, args.copy_probe)
     gru = roof = lstm = lstm_roof = qdq = qdq_roof = None
     if "gru" in legs:
         gru, roof, m, x = _gru_leg(torch, args.steps, args.warmup)
