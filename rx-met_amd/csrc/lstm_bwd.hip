@@ -303,8 +303,12 @@ __global__ __launch_bounds__(512) void lstm_bwd_recurrence(BwdArgs a) {
 // v_mfma_i32_16x16x64_i8: the contraction runs member by member (each member's 256 channels
 // are four K-steps with one exponent), every member's exact plane sums are recombined in
 // double and scaled by that member's exponent, and the two K-halves (waves 0-3 and 4-7) are
-// added in a fixed order.  W_hh codes of the member's units stay resident in LDS.
+// added in a fixed order.  Each wave keeps the W_hh codes of its unit tile and K-half in VGPRs;
+// the exchanged planes are read from global memory once per workgroup and step into LDS, where
+// the four waves of a K-half share them.
 constexpr int kBcUnits = 64;
+constexpr int kBcHalf = 4;  // members per K-half at most (H <= 512)
+constexpr int kStageQ = 2048 / 16 / 32;  // 16-byte chunks per thread and plane at C = 2048
 
 struct BwdClArgs {
   int ncl, G, ntiles, Bpad;
@@ -316,9 +320,11 @@ struct BwdClArgs {
   int *timeout;
 };
 
-// A position k of the member-major contraction order -> channel c.
+// A position k of the member-major contraction order -> channel c: member m's 256 channels,
+// unit-major with the four gates of a unit adjacent (so a lane packs its four gate bytes into
+// one word of each plane).
 __device__ __forceinline__ int cl_channel(int k, int H) {
-  const int m = k / 256, g = (k / 64) % 4, u = k % 64;
+  const int m = k / 256, u = (k % 256) / 4, g = k % 4;
   return g * H + 64 * m + u;
 }
 
@@ -353,9 +359,12 @@ __global__ __launch_bounds__(64) void lstm_pack_whh_t_cl(int H, int KS2, const f
 __global__ __launch_bounds__(512) void lstm_bwd_recurrence_cl(BwdArgs a, BwdClArgs cl) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int H = a.H, C = 4 * H, B = a.B, KS2 = a.KS2, G = cl.G;
-  v4i *wl = reinterpret_cast<v4i *>(smem);                              // [4][KS2][64]
-  double *dred = reinterpret_cast<double *>(wl + 4 * KS2 * 64);         // [8][64][4]
-  unsigned *rowmax = reinterpret_cast<unsigned *>(dred + 8 * 64 * 4);   // [16]
+  const int prow = C + 16;                                              // LDS plane row
+  int8_t *pl_s = reinterpret_cast<int8_t *>(smem);                      // [3][16][prow]
+  double *dred = reinterpret_cast<double *>(pl_s + 3 * kBB * prow);     // [8][64][4]
+  double *csl = dred + 8 * 64 * 4;                                      // [G][64]
+  int *exs = reinterpret_cast<int *>(csl + 64 * G);                     // [16][G]
+  unsigned *rowmax = reinterpret_cast<unsigned *>(exs + kBB * G);       // [16]
   int *rowexp = reinterpret_cast<int *>(rowmax + kBB);                  // [16]
   const int tid = threadIdx.x, w = tid / 64, l = tid % 64;
   const int utl = w & 3, kh = w >> 2;
@@ -364,17 +373,25 @@ __global__ __launch_bounds__(512) void lstm_bwd_recurrence_cl(BwdArgs a, BwdClAr
   const int jt = m0 * 4 + utl;  // global unit tile
   const int j = 16 * jt + l % 16;
   const int nrow0 = 4 * (l / 16);
-  for (int i = tid; i < 4 * KS2 * 64; i += blockDim.x) {
-    const int lane = i % 64, s = (i / 64) % KS2, u = i / (64 * KS2);
-    wl[i] = cl.wfrag[((static_cast<size_t>(m0) * 4 + u) * KS2 + s) * 64 + lane];
-  }
   if (tid < kBB) rowmax[tid] = 0u;
+  // zero-point term of every member's plane sums: 32896 * (column sum of its W_hh codes)
+  for (int i = tid; i < 64 * G; i += blockDim.x)
+    csl[i] = 32896.0 * static_cast<double>(cl.csum[static_cast<size_t>(i / 64) * H + 64 * m0 + i % 64]);
   float sw[4];
 #pragma unroll
   for (int g = 0; g < 4; ++g) sw[g] = a.s_whh[g * H + j];
-  // K-halves: members [0, mh) for waves 0-3, [mh, G) for waves 4-7
+  // K-halves: members [0, mh) for waves 0-3, [mh, G) for waves 4-7 (at most kBcHalf each)
   const int mh = (G + 1) / 2;
   const int mlo = kh == 0 ? 0 : mh, mhi = kh == 0 ? mh : G;
+  // the wave's W_hh^T operands (its unit tile, its K-half) stay in VGPRs
+  v4i wr[kBcHalf][4];
+#pragma unroll
+  for (int i = 0; i < kBcHalf; ++i)
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4)
+      wr[i][s4] = mlo + i < mhi
+                      ? cl.wfrag[((static_cast<size_t>(jt)) * KS2 + 4 * (mlo + i) + s4) * 64 + l]
+                      : v4i{0, 0, 0, 0};
   unsigned *counter = cl.counters + pl.cluster;
   unsigned epoch = 0;
   bool alive = true;
@@ -396,36 +413,52 @@ __global__ __launch_bounds__(512) void lstm_bwd_recurrence_cl(BwdArgs a, BwdClAr
       float sv[2][4], lis[2][4], lhs[2][4];
 #pragma unroll
       for (int rr = 0; rr < 2; ++rr) {
-        const int nr = nrow0 + 2 * kh + rr, b = b0 + nr;
+        const int b = b0 + nrow0 + 2 * kh + rr;
 #pragma unroll
         for (int g = 0; g < 4; ++g) sv[rr][g] = lis[rr][g] = lhs[rr][g] = 0.0f;
         if (b >= B) continue;
+        // every checkpoint value and mask of the row is loaded before any is used
+        float r_go[4], r_ct, r_pc, r_gd;
+        uint8_t r_hid, r_tanh, r_cell, r_gm[4], r_gin[4], r_ih[4], r_hh[4];
         const uint32_t e = static_cast<uint32_t>(t) * BH + static_cast<uint32_t>(b) * H + j;
         const uint32_t gb = static_cast<uint32_t>(t) * BC + static_cast<uint32_t>(b) * C + j;
-        const float ig = deq(a.gate_out[gb], a.s_gout[0], a.zp_gout[0]);
-        const float fg = deq(a.gate_out[gb + H], a.s_gout[1], a.zp_gout[1]);
-        const float gg = deq(a.gate_out[gb + 2 * H], a.s_gout[2], a.zp_gout[2]);
-        const float og = deq(a.gate_out[gb + 3 * H], a.s_gout[3], a.zp_gout[3]);
-        const float ct = deq(a.cell_tanh[e], a.s_t, a.zp_t);
-        const float pc = t == 0 ? deq(a.c0_q[static_cast<uint32_t>(b) * H + j], a.s_c, a.zp_c)
-                                : deq(a.cell[e - BH], a.s_c, a.zp_c);
-        const float dht = (dh[rr] + a.grad_out[e]) * keepf(a.hid_m, e);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          r_go[g] = a.gate_out[gb + g * H];
+          r_gm[g] = a.gout_m[gb + g * H];
+          r_gin[g] = a.gin_m[gb + g * H];
+          r_ih[g] = a.ih_m[gb + g * H];
+          r_hh[g] = a.hh_m[gb + g * H];
+        }
+        r_ct = a.cell_tanh[e];
+        r_pc = t == 0 ? a.c0_q[static_cast<uint32_t>(b) * H + j] : a.cell[e - BH];
+        r_gd = a.grad_out[e];
+        r_hid = a.hid_m[e];
+        r_tanh = a.tanh_m[e];
+        r_cell = a.cell_m[e];
+        const auto kp = [](uint8_t m) { return m == 0 ? 1.0f : 0.0f; };
+        const float ig = deq(r_go[0], a.s_gout[0], a.zp_gout[0]);
+        const float fg = deq(r_go[1], a.s_gout[1], a.zp_gout[1]);
+        const float gg = deq(r_go[2], a.s_gout[2], a.zp_gout[2]);
+        const float og = deq(r_go[3], a.s_gout[3], a.zp_gout[3]);
+        const float ct = deq(r_ct, a.s_t, a.zp_t);
+        const float pc = deq(r_pc, a.s_c, a.zp_c);
+        const float dht = (dh[rr] + r_gd) * kp(r_hid);
         const float d_o = dht * ct;
-        const float dct = dht * og * keepf(a.tanh_m, e);
+        const float dct = dht * og * kp(r_tanh);
         const float dcv = dc[rr] + dct * (1.0f - ct * ct);
-        const float mdc = dcv * keepf(a.cell_m, e);
+        const float mdc = dcv * kp(r_cell);
         const float dfg = mdc * pc;
         const float dig = mdc * gg, dgg = mdc * ig;
-        const float go0 = dig * keepf(a.gout_m, gb), go1 = dfg * keepf(a.gout_m, gb + H);
-        const float go2 = dgg * keepf(a.gout_m, gb + 2 * H), go3 = d_o * keepf(a.gout_m, gb + 3 * H);
+        const float go0 = dig * kp(r_gm[0]), go1 = dfg * kp(r_gm[1]);
+        const float go2 = dgg * kp(r_gm[2]), go3 = d_o * kp(r_gm[3]);
         const float gi[4] = {go0 * ig * (1.0f - ig), go1 * fg * (1.0f - fg), go2 * (1.0f - gg * gg),
                              go3 * og * (1.0f - og)};
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const uint32_t gi_ = gb + g * H;
-          const float grad = gi[g] * keepf(a.gin_m, gi_);
-          lis[rr][g] = grad * keepf(a.ih_m, gi_);
-          lhs[rr][g] = grad * keepf(a.hh_m, gi_);
+          const float grad = gi[g] * kp(r_gin[g]);
+          lis[rr][g] = grad * kp(r_ih[g]);
+          lhs[rr][g] = grad * kp(r_hh[g]);
           sv[rr][g] = lhs[rr][g] * sw[g];
         }
         dc[rr] = mdc * fg;
@@ -459,18 +492,22 @@ __global__ __launch_bounds__(512) void lstm_bwd_recurrence_cl(BwdArgs a, BwdClAr
       for (int rr = 0; rr < 2; ++rr) {
         const int nr = nrow0 + 2 * kh + rr, b = b0 + nr;
         const int ex = rowexp[nr];
+        unsigned wd[3] = {0u, 0u, 0u};
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           int q = 0;
           if (ex != 1000) q = static_cast<int>(rintf(ldexpf(sv[rr][g], ex)));
           const int uq = q + (1 << 23);
-          unsigned char *dst = reinterpret_cast<unsigned char *>(cl.xp) +
-                               (static_cast<size_t>(par) * 3 * cl.Bpad + b) * C + 256 * m0 + 64 * g +
-                               16 * utl + l % 16;
-          cluster::store_bytes_coherent(dst, (uq & 255) - 128);
-          cluster::store_bytes_coherent(dst + pstride, ((uq >> 8) & 255) - 128);
-          cluster::store_bytes_coherent(dst + 2 * pstride, (uq >> 16) - 128);
+          wd[0] |= static_cast<unsigned>(((uq & 255) - 128) & 255) << (8 * g);
+          wd[1] |= static_cast<unsigned>((((uq >> 8) & 255) - 128) & 255) << (8 * g);
+          wd[2] |= static_cast<unsigned>(((uq >> 16) - 128) & 255) << (8 * g);
         }
+        unsigned char *dst = reinterpret_cast<unsigned char *>(cl.xp) +
+                             (static_cast<size_t>(par) * 3 * cl.Bpad + b) * C + 256 * m0 +
+                             4 * (16 * utl + l % 16);
+#pragma unroll
+        for (int p = 0; p < 3; ++p)
+          cluster::store_coherent(reinterpret_cast<unsigned *>(dst + p * pstride), wd[p]);
       }
       // the other members only read the planes and exponents: arrive, then store the gate
       // gradients for the weight GEMMs while waiting
@@ -489,41 +526,56 @@ __global__ __launch_bounds__(512) void lstm_bwd_recurrence_cl(BwdArgs a, BwdClAr
       }
       alive = cluster::wait(counter, epoch * G, cl.timeout);
       if (!alive) break;
-      // dh of the tile's rows, this wave's K-half, member by member
-      double dsum[4] = {0.0, 0.0, 0.0, 0.0};
-      const int8_t *arow = cl.xp + (static_cast<size_t>(par) * 3 * cl.Bpad + b0 + l % 16) * C +
-                           16 * (l / 16);
-      for (int m = mlo; m < mhi; ++m) {
-        v4i afr[4][3];
+      // stage the tile's exchanged planes (all members) and exponents in LDS, once per workgroup
+      {
+        // 3 planes x 16 rows x C bytes: thread -> row tid / 32, 16-byte chunks tid % 32 + 32 q
+        // (C a multiple of 512 and at most 2048: q < C / 512 <= 4, uniform).  All loads are
+        // issued before any is stored; a q past the row re-reads chunk q = 0 and is not stored.
+        const int r = tid / 32, c0 = tid % 32, qn = C / 512;
+        const int8_t *src = cl.xp + (static_cast<size_t>(par) * 3 * cl.Bpad + b0 + r) * C + 16 * c0;
+        int8_t *dst = pl_s + r * prow + 16 * c0;
+        int4 v[3][kStageQ];
 #pragma unroll
-        for (int s4 = 0; s4 < 4; ++s4)
+        for (int p = 0; p < 3; ++p)
 #pragma unroll
-          for (int p = 0; p < 3; ++p) {
-            const int4 v = cluster::load_coherent16(arow + p * pstride + 64 * (4 * m + s4));
-            afr[s4][p] = v4i{v.x, v.y, v.z, v.w};
-          }
-        int exr[4];
+          for (int q = 0; q < kStageQ; ++q)
+            v[p][q] = cluster::load_coherent16(src + p * pstride + 512 * (q < qn ? q : 0));
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          exr[r] = static_cast<int>(__hip_atomic_load(
-              reinterpret_cast<const unsigned *>(cl.xe + (static_cast<size_t>(par) * cl.Bpad + b0 +
-                                                           nrow0 + r) * G + m),
+        for (int p = 0; p < 3; ++p)
+#pragma unroll
+          for (int q = 0; q < kStageQ; ++q)
+            if (q < qn) *reinterpret_cast<int4 *>(dst + p * kBB * prow + 512 * q) = v[p][q];
+        for (int i = tid; i < kBB * G; i += blockDim.x)
+          exs[i] = static_cast<int>(__hip_atomic_load(
+              reinterpret_cast<const unsigned *>(cl.xe) + (static_cast<size_t>(par) * cl.Bpad + b0) * G + i,
               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-        v4i acc[3];
+      }
+      __syncthreads();
+      // dh of the tile's rows, this wave's K-half, member by member (in order)
+      double dsum[4] = {0.0, 0.0, 0.0, 0.0};
+      const int8_t *arow = pl_s + (l % 16) * prow + 16 * (l / 16);
 #pragma unroll
-        for (int p = 0; p < 3; ++p) acc[p] = v4i{0, 0, 0, 0};
+      for (int i = 0; i < kBcHalf; ++i) {
+        const int mm = mlo + i;
+        if (mm < mhi) {
+          v4i acc[3];
 #pragma unroll
-        for (int s4 = 0; s4 < 4; ++s4) {
-          const v4i bf = wl[(utl * KS2 + 4 * m + s4) * 64 + l];
+          for (int p = 0; p < 3; ++p) acc[p] = v4i{0, 0, 0, 0};
 #pragma unroll
-          for (int p = 0; p < 3; ++p) acc[p] = mfma_i8(afr[s4][p], bf, acc[p]);
-        }
-        const double cs = static_cast<double>(cl.csum[static_cast<size_t>(m) * H + j]);
+          for (int s4 = 0; s4 < 4; ++s4)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const double comb = 65536.0 * acc[2][r] + 256.0 * acc[1][r] + static_cast<double>(acc[0][r]) +
-                              32896.0 * cs;
-          dsum[r] += exr[r] == 1000 ? static_cast<double>(NAN) : ldexp(comb, -exr[r]);
+            for (int p = 0; p < 3; ++p) {
+              const v4i afr = *reinterpret_cast<const v4i *>(arow + p * kBB * prow + 64 * (4 * mm + s4));
+              acc[p] = mfma_i8(afr, wr[i][s4], acc[p]);
+            }
+          const double zc = csl[mm * 64 + 16 * utl + l % 16];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int ex = exs[(nrow0 + r) * G + mm];
+            const double comb =
+                65536.0 * acc[2][r] + 256.0 * acc[1][r] + static_cast<double>(acc[0][r]) + zc;
+            dsum[r] += ex == 1000 ? static_cast<double>(NAN) : ldexp(comb, -ex);
+          }
         }
       }
       double *dr = dred + (static_cast<size_t>(w) * 64 + l) * 4;
@@ -550,9 +602,9 @@ __global__ __launch_bounds__(512) void lstm_bwd_recurrence_cl(BwdArgs a, BwdClAr
   }
 }
 
-size_t bwd_cl_lds(int KS2) {
-  return sizeof(v4i) * 4 * static_cast<size_t>(KS2) * 64 + sizeof(double) * 8 * 64 * 4 +
-         2 * sizeof(int) * kBB;
+size_t bwd_cl_lds(int C, int G) {
+  return 3 * kBB * static_cast<size_t>(C + 16) + sizeof(double) * (8 * 64 * 4 + 64 * G) +
+         sizeof(int) * kBB * G + 2 * sizeof(int) * kBB;
 }
 
 size_t bwd_lds(int H, int KS2) {
@@ -715,9 +767,10 @@ int rxmet_lstm_backward_quant(int32_t T, int32_t B, int32_t I, int32_t H,
   ba.s_c = sp.c.dscale; ba.zp_c = sp.c.dzp; ba.s_t = sp.tanh_c.dscale; ba.zp_t = sp.tanh_c.dzp;
   ba.dli = dli; ba.dlh = dlh; ba.dh0 = dh0; ba.dc0 = dc0;
   bool clustered = false;
-  if (H % kBcUnits == 0 && std::getenv("RXMET_NO_CLUSTER") == nullptr) {
+  if (H % (2 * kBcUnits) == 0 && H / kBcUnits <= 2 * kBcHalf &&
+      std::getenv("RXMET_NO_CLUSTER") == nullptr) {
     const void *fn = reinterpret_cast<const void *>(&lstm_bwd_recurrence_cl);
-    const size_t lds_cl = bwd_cl_lds(KS2);
+    const size_t lds_cl = bwd_cl_lds(C, H / kBcUnits);
     int device = 0, ncu = 0, per_cu = 0;
     RXMET_CHECK_HIP(hipGetDevice(&device));
     RXMET_CHECK_HIP(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, device));

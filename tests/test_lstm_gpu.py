@@ -330,7 +330,7 @@ def test_clustered_recurrence_matches_oracle_and_single_tile_path(cuda, shape, c
                                             ((3, 20, 64, 512), "pot2-gate")])
 def test_clustered_backward_matches_oracle_and_single_tile_path(cuda, shape, cfg_name,
                                                                 monkeypatch):
-    """H a multiple of 64 takes the clustered backward (members exchange block-fixed-point
+    """H a multiple of 128 takes the clustered backward (members exchange block-fixed-point
     gate gradients, one exponent per sequence and member); it must match the oracle within
     1e-4 and the one-workgroup-per-tile backward."""
     T, B, I, H = shape
