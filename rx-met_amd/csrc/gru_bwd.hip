@@ -343,17 +343,46 @@ __global__ __launch_bounds__(64) void pack_rt_f32(int H, int KS2, const float *_
   rt[static_cast<size_t>(idx) * 64 + l] = k < 3 * H ? Rq[static_cast<size_t>(j) * 3 * H + k] : 0.0f;
 }
 
-// One (direction, batch tile) pair, run by one member; writes the pair's bias partials.
+// A mask that may be absent.  The load is unconditional (an absent mask reads the same index
+// of `fallback`, a buffer at least as large as any mask: the saved activations v, [T, B, 4H]
+// floats) and the value is replaced by 1 afterwards, so the step's loads need no branch;
+// multiplying by 1.0f leaves every value, NaN and -0 included, as it was.
+struct MaskRef {
+  const uint8_t *p;
+  bool on;
+  __device__ __forceinline__ float at(uint32_t i) const {
+    const float v = static_cast<float>(p[i]);
+    return on ? v : 1.0f;
+  }
+};
+__device__ __forceinline__ MaskRef mask_ref(const uint8_t *p, const void *fallback) {
+  return p ? MaskRef{p, true} : MaskRef{static_cast<const uint8_t *>(fallback), false};
+}
+
+// LDS of the clustered backward: partial sums, bias partials, the staged exchange rows.
+constexpr size_t kBwRedBytes = 16 * 1024, kBwBredBytes = sizeof(double) * 2 * 4 * 16 * 6;
+__host__ __device__ constexpr size_t bwd_cl_lds(int KP) {
+  return kBwRedBytes + kBwBredBytes + sizeof(float) * kBTile * static_cast<size_t>(KP + 4);
+}
+
+// One (direction, batch tile) pair, run by one member of UT unit tiles; writes the pair's
+// bias partials.
+template <int UT>
 __device__ __forceinline__ void bwd_cl_pair(const BwdArgs &a, const BwdClArgs &cl, int tile,
                                             int member, unsigned *counter, unsigned &epoch,
                                             bool &alive) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int H = a.H, C = 3 * H, B = a.B, KS2 = a.KS2, KP = cl.KP;
   v4f *red = reinterpret_cast<v4f *>(smem);                          // [UT][4][64]
-  double *bred = reinterpret_cast<double *>(smem + 16 * 1024);       // [UT][4][16][6]
+  double *bred = reinterpret_cast<double *>(smem + kBwRedBytes);     // [UT][4][16][6]
+  float *xs = reinterpret_cast<float *>(smem + kBwRedBytes + kBwBredBytes);  // [16][KP + 4]
   const int tid = threadIdx.x, w = tid / 64, l = tid % 64;
   const int utl = w / 4, kq = w % 4;
-  const int ut = member * cl.UT + utl;
+  const int ut = member * UT + utl;
+  // staging of the exchange rows: thread -> row tid / (16 UT), 16-byte chunks
+  // tid % (16 UT) + 16 UT q for q < ceil(KS2 / UT)
+  constexpr int kQ = (kBwMaxKS2 + UT - 1) / UT;
+  const int srow = tid / (16 * UT), sc0 = tid % (16 * UT), sqn = (KS2 + UT - 1) / UT;
   const int j = 16 * ut + l % 16;
   const int nr = 4 * (l / 16) + kq;
   float rtv[4 * kBwMaxKS2];
@@ -371,6 +400,9 @@ __device__ __forceinline__ void bwd_cl_pair(const BwdArgs &a, const BwdClArgs &c
   double sbw[3] = {0.0, 0.0, 0.0}, sbr[3] = {0.0, 0.0, 0.0};
   const uint32_t BH = static_cast<uint32_t>(B) * H;
   v4f *myred = red + (static_cast<size_t>(utl) * 4 + kq) * 64;
+  const MaskRef mk_h = mask_ref(a.h_m, a.v), mk_go = mask_ref(a.gout_m, a.v),
+                mk_gi = mask_ref(a.gin_m, a.v), mk_hh = mask_ref(a.hh_m, a.v),
+                mk_ih = mask_ref(a.ih_m, a.v);
 
   {
     const int b0 = tile * kBTile, b = b0 + nr;
@@ -386,38 +418,34 @@ __device__ __forceinline__ void bwd_cl_pair(const BwdArgs &a, const BwdClArgs &c
         const uint32_t oC = 3u * static_cast<uint32_t>(b) * H + j;
         const uint32_t tH = static_cast<uint32_t>(t) * BH;
         const uint32_t tC = 3u * tH, v0 = 4u * tH + 4u * static_cast<uint32_t>(b) * H + j;
-        float dht = a.dh_new[tH + BH + oH] + dhc;
-        if (a.h_m) dht *= static_cast<float>(a.h_m[tH + oH]);
+        m = tC + oC;
+        // every input of the step is loaded before any is used (absent masks read a 1)
+        const float r_dhn = a.dh_new[tH + BH + oH], r_h = a.h[tH + oH];
         const float z = a.v[v0], rr = a.v[v0 + H], g = a.v[v0 + 2 * H], qg = a.v[v0 + 3 * H];
+        const float hm = mk_h.at(tH + oH);
+        float mgo[3], mgi[3], mhh[3], mih[3];
+#pragma unroll
+        for (int gg = 0; gg < 3; ++gg) {
+          mgo[gg] = mk_go.at(m + gg * H);
+          mgi[gg] = mk_gi.at(m + gg * H);
+          mhh[gg] = mk_hh.at(m + gg * H);
+          mih[gg] = mk_ih.at(m + gg * H);
+        }
+        const float dht = (r_dhn + dhc) * hm;
         dhl = z * dht;
         const float dg = (1.0f - z) * dht;
-        const float dz = (a.h[tH + oH] - g) * dht;
-        m = tC + oC;
+        const float dz = (r_h - g) * dht;
         float dpg = (1.0f - g * g) * dg;
-        if (a.gout_m) dpg *= static_cast<float>(a.gout_m[m + 2 * H]);
-        if (a.gin_m) dpg *= static_cast<float>(a.gin_m[m + 2 * H]);
+        dpg *= mgo[2];
+        dpg *= mgi[2];
         float dqg = dpg * rr;
         const float dr = dpg * qg;
         float dpr = rr * (1.0f - rr) * dr, dqr = dpr;
         float dpz = z * (1.0f - z) * dz, dqz = dpz;
-        if (a.gout_m) {
-          const float mz = static_cast<float>(a.gout_m[m]), mr = static_cast<float>(a.gout_m[m + H]);
-          dpz *= mz; dqz *= mz; dpr *= mr; dqr *= mr;
-        }
-        if (a.gin_m) {
-          const float mz = static_cast<float>(a.gin_m[m]), mr = static_cast<float>(a.gin_m[m + H]);
-          dpz *= mz; dqz *= mz; dpr *= mr; dqr *= mr;
-        }
-        if (a.hh_m) {
-          dqz *= static_cast<float>(a.hh_m[m]);
-          dqr *= static_cast<float>(a.hh_m[m + H]);
-          dqg *= static_cast<float>(a.hh_m[m + 2 * H]);
-        }
-        if (a.ih_m) {
-          dpz *= static_cast<float>(a.ih_m[m]);
-          dpr *= static_cast<float>(a.ih_m[m + H]);
-          dpg *= static_cast<float>(a.ih_m[m + 2 * H]);
-        }
+        dpz *= mgo[0]; dqz *= mgo[0]; dpr *= mgo[1]; dqr *= mgo[1];
+        dpz *= mgi[0]; dqz *= mgi[0]; dpr *= mgi[1]; dqr *= mgi[1];
+        dqz *= mhh[0]; dqr *= mhh[1]; dqg *= mhh[2];
+        dpz *= mih[0]; dpr *= mih[1]; dpg *= mih[2];
         dpv[0] = dpz; dpv[1] = dpr; dpv[2] = dpg;
         dqv[0] = dqz; dqv[1] = dqr; dqv[2] = dqg;
 #pragma unroll
@@ -443,22 +471,34 @@ __device__ __forceinline__ void bwd_cl_pair(const BwdArgs &a, const BwdClArgs &c
       }
       alive = cluster::wait(counter, epoch * cl.G, cl.timeout);
       if (!alive) break;
-      // dh += R_deq dq over this wave's quarter of the channels
+      // stage the tile's exchange rows in LDS (all loads in flight; a q past the row re-reads
+      // q = 0 and is not stored), then dh += R_deq dq over this wave's quarter of the channels
+      {
+        const float *src = a.xch + (static_cast<size_t>(par) * cl.Bpad + b0 + srow) * KP + 4 * sc0;
+        float *dst = xs + srow * (KP + 4) + 4 * sc0;
+        int4 sv[kQ];
+#pragma unroll
+        for (int q = 0; q < kQ; ++q) {
+          const int qq = (q < sqn && 16 * UT * q + sc0 < 16 * KS2) ? q : 0;
+          sv[q] = cluster::load_coherent16(src + 64 * UT * qq);
+        }
+#pragma unroll
+        for (int q = 0; q < kQ; ++q)
+          if (q < sqn && 16 * UT * q + sc0 < 16 * KS2)
+            *reinterpret_cast<int4 *>(dst + 64 * UT * q) = sv[q];
+      }
+      __syncthreads();
       v4f acc = {0.f, 0.f, 0.f, 0.f};
       {
-        const float *arow = a.xch + (static_cast<size_t>(par) * cl.Bpad + b0 + l % 16) * KP +
-                            16 * (kq * KS2) + 4 * (l / 16);
-        int4 av[kBwMaxKS2];
-#pragma unroll
-        for (int qg = 0; qg < kBwMaxKS2; ++qg)
-          if (qg < KS2) av[qg] = cluster::load_coherent16(arow + 16 * qg);
+        const float *arow = xs + (l % 16) * (KP + 4) + 16 * (kq * KS2) + 4 * (l / 16);
 #pragma unroll
         for (int qg = 0; qg < kBwMaxKS2; ++qg)
           if (qg < KS2) {
-            acc = mfma_f32(__int_as_float(av[qg].x), rtv[4 * qg + 0], acc);
-            acc = mfma_f32(__int_as_float(av[qg].y), rtv[4 * qg + 1], acc);
-            acc = mfma_f32(__int_as_float(av[qg].z), rtv[4 * qg + 2], acc);
-            acc = mfma_f32(__int_as_float(av[qg].w), rtv[4 * qg + 3], acc);
+            const v4f av = *reinterpret_cast<const v4f *>(arow + 16 * qg);
+            acc = mfma_f32(av[0], rtv[4 * qg + 0], acc);
+            acc = mfma_f32(av[1], rtv[4 * qg + 1], acc);
+            acc = mfma_f32(av[2], rtv[4 * qg + 2], acc);
+            acc = mfma_f32(av[3], rtv[4 * qg + 3], acc);
           }
       }
       myred[l] = acc;
@@ -508,7 +548,8 @@ __device__ __forceinline__ void bwd_cl_pair(const BwdArgs &a, const BwdClArgs &c
   }
 }
 
-__global__ __launch_bounds__(512) void bwd_recurrence_cl(BwdArgs a0, BwdArgs a1, BwdClArgs cl) {
+template <int UT>
+__global__ __launch_bounds__(256 * UT) void bwd_recurrence_cl(BwdArgs a0, BwdArgs a1, BwdClArgs cl) {
   const cluster::Place pl = cluster::place(cl.G, cl.ncl);
   unsigned *counter = cl.counters + pl.cluster;
   unsigned epoch = 0;
@@ -517,7 +558,7 @@ __global__ __launch_bounds__(512) void bwd_recurrence_cl(BwdArgs a0, BwdArgs a1,
     const int d = pair / cl.ntiles, tile = pair % cl.ntiles;
     __syncthreads();
     // one copy of the step code for both directions (d is uniform across the workgroup)
-    bwd_cl_pair(d == 0 ? a0 : a1, cl, tile, pl.member, counter, epoch, alive);
+    bwd_cl_pair<UT>(d == 0 ? a0 : a1, cl, tile, pl.member, counter, epoch, alive);
   }
 }
 
@@ -665,13 +706,10 @@ static int backward_recurrence_clustered(BwdPlan *plans, int ndir, int T, int B,
                                          hipStream_t stream) {
   const int C = 3 * H, KS2 = (C + 63) / 64;
   if (KS2 > kBwMaxKS2 || std::getenv("RXMET_NO_CLUSTER") != nullptr) return 0;
-  const void *fn = reinterpret_cast<const void *>(&bwd_recurrence_cl);
-  const size_t lds_cl = 16 * 1024 + sizeof(double) * 2 * 4 * 16 * 6;
+  const size_t lds_cl = bwd_cl_lds(KS2 * 64);
   int device = 0, ncu = 0;
   RXMET_CHECK_HIP(hipGetDevice(&device));
   RXMET_CHECK_HIP(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, device));
-  RXMET_CHECK_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                      static_cast<int>(lds_cl)));
   BwdClArgs cl;
   cl.ndir = ndir;
   cl.ntiles = (B + kBTile - 1) / kBTile;
@@ -690,6 +728,10 @@ static int backward_recurrence_clustered(BwdPlan *plans, int ndir, int T, int B,
     }
   }
   if (!chosen) return 0;
+  const void *fn = chosen == 1 ? reinterpret_cast<const void *>(&bwd_recurrence_cl<1>)
+                               : reinterpret_cast<const void *>(&bwd_recurrence_cl<2>);
+  RXMET_CHECK_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      static_cast<int>(lds_cl)));
   int per_cu = 0;
   RXMET_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256 * chosen, lds_cl));
   ncl = per_cu * ncu / cl.G;
