@@ -21,16 +21,17 @@
 //                  exactly against the W_hh codes and recombined in double;
 //   3. rocBLAS   : dx, and split-K dW_ih | db_ih and dW_hh | db_hh; one pass applies the
 //                  master masks and splits off the bias columns.
+#include <algorithm>
 #include <cmath>
 #include <cstdlib>
 #include <vector>
 
-#include "blas_util.h"
 #include "cluster.h"
 #include "lstm_internal.h"
 #include "mfma_frag.h"
 #include "rxmet_common.h"
 #include "rxmet_lstm.h"
+#include "wgrad_gemm.h"
 
 namespace rxmet {
 namespace lstm {
@@ -50,40 +51,6 @@ __device__ __forceinline__ float keepf(const uint8_t *m, uint32_t i) {
 // ---------------------------------------------------------------------------------
 // 1. prep
 // ---------------------------------------------------------------------------------
-struct PrepArgs {
-  int T, B, I, H;
-  const float *x_q, *w_ih_q, *h0_q, *hidden;
-  const float *s_wih;     // [4H]
-  double s_x, zp_x, s_h, zp_h;
-  float *xd;              // [T*B, I+1]
-  float *wid;             // [4H, I]
-  float *hprev;           // [T*B, H+1]
-};
-
-__global__ __launch_bounds__(256) void lstm_bwd_prep(PrepArgs a) {
-  const int64_t M = static_cast<int64_t>(a.T) * a.B, C = 4 * static_cast<int64_t>(a.H);
-  const int64_t n0 = M * (a.I + 1), n1 = C * a.I, n2 = M * (a.H + 1);
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n0 + n1 + n2;
-       i += stride) {
-    if (i < n0) {
-      const int64_t m = i / (a.I + 1), k = i % (a.I + 1);
-      a.xd[i] = k == a.I ? 1.0f : deq(a.x_q[m * a.I + k], a.s_x, a.zp_x);
-    } else if (i < n0 + n1) {
-      const int64_t e = i - n0, c = e / a.I;
-      a.wid[e] = deq(a.w_ih_q[e], static_cast<double>(a.s_wih[c]), 0.0);
-    } else {
-      const int64_t e = i - n0 - n1, m = e / (a.H + 1), k = e % (a.H + 1);
-      float v = 1.0f;
-      if (k < a.H) {
-        const float q = m < a.B ? a.h0_q[m * a.H + k] : a.hidden[(m - a.B) * a.H + k];
-        v = deq(q, a.s_h, a.zp_h);
-      }
-      a.hprev[e] = v;
-    }
-  }
-}
-
 // W_hh codes [4H][H] -> B fragments of D[b][j] = sum_c A[b][c] W[c][j]:
 // frag[(jt * KS2 + s) * 64 + lane] = W[64 s + 16 (lane / 16) + 0..15][16 jt + lane % 16];
 // colsum[j] = sum_c W[c][j].
@@ -641,8 +608,9 @@ __global__ __launch_bounds__(256) void lstm_bwd_finish(int64_t nx, float *dx, co
 }
 
 struct BwdWorkspace {
-  size_t dli, dlh, xd, wid, hprev, frag, colsum, swih, swhh, aug_ih, aug_hh, part, wfrag_cl, csum,
-      xp, xe, sync, total;
+  size_t dli, dlh, xt, wt, ht, qsc, frag, colsum, swih, swhh, aug_ih, aug_hh, part, gsum, wfrag_cl,
+      csum, xp, xe, sync, total;
+  int Mp, S_ih, kper_ih, S_hh, kper_hh;
   BwdWorkspace(int T, int B, int I, int H) {
     const size_t C = 4 * static_cast<size_t>(H), M = static_cast<size_t>(T) * B;
     const size_t KS2 = (C + 63) / 64;
@@ -650,17 +618,23 @@ struct BwdWorkspace {
     size_t o = 0;
     dli = o; o += al(sizeof(float) * M * C);
     dlh = o; o += al(sizeof(float) * M * C);
-    xd = o; o += al(sizeof(float) * M * (I + 1));
-    wid = o; o += al(sizeof(float) * C * I);
-    hprev = o; o += al(sizeof(float) * M * (H + 1));
+    // weight-gradient GEMM operands: codes as bf16 planes, transposed, rows padded to Mp
+    Mp = static_cast<int>((M + 31) / 32 * 32);
+    xt = o; o += al(sizeof(__bf16) * 2 * I * static_cast<size_t>(Mp));
+    wt = o; o += al(sizeof(__bf16) * 2 * I * C);
+    ht = o; o += al(sizeof(__bf16) * 2 * H * static_cast<size_t>(Mp));
+    qsc = o; o += al(sizeof(float) * (I + H));
     frag = o; o += al(sizeof(v4i) * 64 * (H / 16 + 1) * KS2);
     colsum = o; o += al(sizeof(float) * H);
     swih = o; o += al(sizeof(float) * C);
     swhh = o; o += al(sizeof(float) * C);
     aug_ih = o; o += al(sizeof(float) * C * (I + 1));
     aug_hh = o; o += al(sizeof(float) * C * (H + 1));
-    const size_t S = static_cast<size_t>(blas::splitk_chunks(static_cast<int64_t>(M)));
-    part = o; o += al(sizeof(float) * S * C * (static_cast<size_t>(I) > H ? I + 1 : H + 1));
+    wgrad::tn_plan(static_cast<int>(M), static_cast<int>(C), I, &S_ih, &kper_ih);
+    wgrad::tn_plan(static_cast<int>(M), static_cast<int>(C), H, &S_hh, &kper_hh);
+    const size_t np = std::max(static_cast<size_t>(S_ih) * C * I, static_cast<size_t>(S_hh) * C * H);
+    part = o; o += al(sizeof(float) * np);
+    gsum = o; o += al(sizeof(float) * 2 * C * static_cast<size_t>(std::max(S_ih, S_hh)));
     // clustered recurrence (H a multiple of 64)
     const size_t Bpad = (static_cast<size_t>(B) + kBB - 1) / kBB * kBB, G = H / kBcUnits + 1;
     wfrag_cl = o; o += al(sizeof(v4i) * 64 * (H / 16) * KS2);
@@ -720,9 +694,11 @@ int rxmet_lstm_backward_quant(int32_t T, int32_t B, int32_t I, int32_t H,
   char *wsb = static_cast<char *>(workspace);
   float *dli = reinterpret_cast<float *>(wsb + ws.dli);
   float *dlh = reinterpret_cast<float *>(wsb + ws.dlh);
-  float *xd = reinterpret_cast<float *>(wsb + ws.xd);
-  float *wid = reinterpret_cast<float *>(wsb + ws.wid);
-  float *hprev = reinterpret_cast<float *>(wsb + ws.hprev);
+  __bf16 *xt = reinterpret_cast<__bf16 *>(wsb + ws.xt);
+  __bf16 *wt = reinterpret_cast<__bf16 *>(wsb + ws.wt);
+  __bf16 *ht = reinterpret_cast<__bf16 *>(wsb + ws.ht);
+  float *qsc = reinterpret_cast<float *>(wsb + ws.qsc);
+  float *gsum = reinterpret_cast<float *>(wsb + ws.gsum);
   v4i *frag = reinterpret_cast<v4i *>(wsb + ws.frag);
   float *colsum = reinterpret_cast<float *>(wsb + ws.colsum);
   float *swih = reinterpret_cast<float *>(wsb + ws.swih);
@@ -738,18 +714,27 @@ int rxmet_lstm_backward_quant(int32_t T, int32_t B, int32_t I, int32_t H,
   RXMET_CHECK_HIP(hipMemcpyAsync(swih, host.data(), sizeof(float) * 2 * C, hipMemcpyHostToDevice,
                                  stream));
 
-  PrepArgs pa;
-  pa.T = T; pa.B = B; pa.I = I; pa.H = H;
-  pa.x_q = sv.x_q; pa.w_ih_q = sv.w_ih_q; pa.h0_q = sv.h0_q; pa.hidden = sv.hidden;
-  pa.s_wih = swih; pa.s_x = sp.x.dscale; pa.zp_x = sp.x.dzp; pa.s_h = sp.h.dscale; pa.zp_h = sp.h.dzp;
-  pa.xd = xd; pa.wid = wid; pa.hprev = hprev;
+  // weight-gradient operands: x, h_prev and W_ih codes as bf16 planes, transposed
+  const Grid gwi = grid_of(params->config.op[RXMET_LSTM_W_IH], 1.0f, 0);
+  const int npx = wgrad::planes_for(sp.x.lo, sp.x.hi, sp.x.zp);
+  const int nph = wgrad::planes_for(sp.h.lo, sp.h.hi, sp.h.zp);
+  const int npw = wgrad::planes_for(gwi.lo, gwi.hi, 0.0);
+  const int64_t Mp = ws.Mp;
+  if (int rc = wgrad::codes_t(sv.x_q, M, nullptr, M, I, static_cast<float>(sp.x.zp), npx, xt, Mp,
+                              static_cast<int64_t>(I) * Mp, stream))
+    return rc;
+  if (int rc = wgrad::codes_t(sv.h0_q, B, sv.hidden, M, H, static_cast<float>(sp.h.zp), nph, ht, Mp,
+                              static_cast<int64_t>(H) * Mp, stream))
+    return rc;
+  if (int rc = wgrad::codes_t(sv.w_ih_q, C, nullptr, C, I, 0.0f, npw, wt, C,
+                              static_cast<int64_t>(I) * C, stream))
+    return rc;
   {
-    const int64_t n = static_cast<int64_t>(M) * (I + 1) + static_cast<int64_t>(C) * I +
-                      static_cast<int64_t>(M) * (H + 1);
-    int64_t blocks = (n + 255) / 256;
-    if (blocks > 8192) blocks = 8192;
-    hipLaunchKernelGGL(lstm_bwd_prep, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, pa);
-    RXMET_CHECK_LAUNCH();
+    std::vector<float> qs(I + H);
+    for (int k = 0; k < I; ++k) qs[k] = static_cast<float>(sp.x.dscale);
+    for (int k = 0; k < H; ++k) qs[I + k] = static_cast<float>(sp.h.dscale);
+    RXMET_CHECK_HIP(hipMemcpyAsync(qsc, qs.data(), sizeof(float) * (I + H), hipMemcpyHostToDevice,
+                                   stream));
   }
 
   BwdArgs ba;
@@ -829,21 +814,29 @@ int rxmet_lstm_backward_quant(int32_t T, int32_t B, int32_t I, int32_t H,
     RXMET_CHECK_LAUNCH();
   }
 
-  int device = 0;
-  RXMET_CHECK_HIP(hipGetDevice(&device));
-  rocblas_handle bh = blas::handle(device);
-  RXMET_CHECK_ARG(bh != nullptr, "rocBLAS handle creation failed");
-  rocblas_set_stream(bh, stream);
   {
     rxmet::prof::Scope ps__("lstm_bwd_weight_gemms", stream);
-    // dx[M][I] = dli[M][C] * W_ih_deq[C][I]
-    RXMET_CHECK_ARG(blas::gemm_rm(bh, false, false, M, I, C, dli, C, wid, I, dx, I) ==
-                        rocblas_status_success,
-                    "rocBLAS sgemm (dx) failed");
-    const int S = blas::splitk_chunks(M);
-    if (int rc = blas::gemm_tn_splitk(bh, C, I + 1, M, dli, C, xd, I + 1, aug_ih, part, S, stream))
+    // dx[M][I] = sum_c (dli[m][c] s_wih[c]) W_ih_q[c][i]
+    wgrad::NtArgs na;
+    na.A = dli; na.lda = C; na.kscale = swih;
+    na.Bt = wt; na.ldb = C; na.bplane = static_cast<int64_t>(I) * C;
+    na.M = M; na.N = I; na.K = C; na.out = dx; na.ldo = I;
+    if (int rc = wgrad::nt(na, npw, stream)) return rc;
+    // aug_ih[c][i] = s_x sum_m dli[m][c] (x_q - zp_x)[m][i], aug_ih[c][I] = sum_m dli[m][c]
+    wgrad::TnArgs ta;
+    ta.A = dli; ta.lda = C; ta.Bt = xt; ta.ldb = Mp; ta.bplane = static_cast<int64_t>(I) * Mp;
+    ta.K = M; ta.P = C; ta.Q = I; ta.S = ws.S_ih; ta.kper = ws.kper_ih; ta.part = part;
+    ta.colsum = gsum;
+    if (int rc = wgrad::tn(ta, npx, stream)) return rc;
+    if (int rc = wgrad::tn_finish(part, ws.S_ih, C, I, qsc, aug_ih, I + 1, false, gsum, aug_ih + I,
+                                  stream))
       return rc;
-    if (int rc = blas::gemm_tn_splitk(bh, C, H + 1, M, dlh, C, hprev, H + 1, aug_hh, part, S, stream))
+    // aug_hh[c][j] = s_h sum_m dlh[m][c] (h_prev - zp_h)[m][j], aug_hh[c][H] = sum_m dlh[m][c]
+    ta.A = dlh; ta.Bt = ht; ta.bplane = static_cast<int64_t>(H) * Mp;
+    ta.Q = H; ta.S = ws.S_hh; ta.kper = ws.kper_hh;
+    if (int rc = wgrad::tn(ta, nph, stream)) return rc;
+    if (int rc = wgrad::tn_finish(part, ws.S_hh, C, H, qsc + I, aug_hh, H + 1, false, gsum,
+                                  aug_hh + H, stream))
       return rc;
   }
   {

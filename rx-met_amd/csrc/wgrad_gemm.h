@@ -1,0 +1,70 @@
+// wgrad_gemm.h — weight-gradient GEMMs of the QAT backward on bf16 MFMA.
+//
+// Every product here pairs a float gradient with integer quantisation codes.  The codes are
+// exact in bf16 (one plane for |code| <= 256; two planes 256 hi + lo for 16-bit codes), and the
+// gradient is split exactly into three bf16 terms g = g_hi + g_mid + g_lo (each the RNE bf16 of
+// what the previous terms leave).  Every bf16 x bf16 product is exact in fp32 and the MFMA
+// accumulates in fp32, so the result has the accuracy of an fp32 GEMM (a different summation
+// order), at 3 (or 6) v_mfma_f32_16x16x32_bf16 per 32 K instead of 8 v_mfma_f32_16x16x4_f32.
+#pragma once
+
+#include <cstdint>
+
+#include <hip/hip_runtime.h>
+
+namespace rxmet {
+namespace wgrad {
+
+// part[s][p][q] = sum over k in split s of A[k * lda + p] * sum_pl Bt[pl * bplane + q * ldb + k]
+// (A: gradient rows k; Bt: codes transposed, k contiguous, zero beyond K up to a multiple of 32).
+// colsum (optional, [S][2][P]): partial sums of A over the split's k, written by the first
+// q-tile.  S splits of kper rows (kper a multiple of 32).
+struct TnArgs {
+  const float *A;
+  int64_t lda;
+  const __bf16 *Bt;
+  int64_t ldb, bplane;
+  int K, P, Q, S, kper;
+  float *part;
+  float *colsum;
+};
+
+// out[m * ldo + n] = sum_k (A[m * lda + k] * kscale[k]) * sum_pl Bt[pl * bplane + n * ldb + k]
+// (A: gradient rows m, k contiguous; Bt: codes, k contiguous, zero beyond K up to a multiple
+// of 32).
+struct NtArgs {
+  const float *A;
+  int64_t lda;
+  const float *kscale;
+  const __bf16 *Bt;
+  int64_t ldb, bplane;
+  int M, N, K;
+  float *out;
+  int64_t ldo;
+};
+
+// Number of K splits for a TN product (about 1024 workgroups) and rows per split.
+void tn_plan(int K, int P, int Q, int *S, int *kper);
+// Launches; nplanes is 1 or 2.
+int tn(const TnArgs &a, int nplanes, hipStream_t stream);
+int nt(const NtArgs &a, int nplanes, hipStream_t stream);
+// out[p * ldo + q] = qscale[q] * sum_s part[s][p][q] (fixed order; out[q * ldo + p] when
+// transpose); qscale may be null (1).  bias (optional): bias[p * ldo] = the sum of colsum over
+// splits and halves.
+int tn_finish(const float *part, int S, int P, int Q, const float *qscale, float *out, int64_t ldo,
+              bool transpose, const float *colsum, float *bias, hipStream_t stream);
+
+// Codes as bf16 operand planes, transposed: for r < rows and c < cols, v = code(r, c) - zp with
+// code(r, c) = r < rows0 ? src0[r * cols + c] : src1[(r - rows0) * cols + c]; with one plane
+// dst[c * ldd + r] = v (|v| <= 256), with two planes dst[c * ldd + r] = 256 (v >> 8) and
+// dst[plane + c * ldd + r] = v & 255.  Rows rows..ldd-1 are written as zeros.
+int codes_t(const float *src0, int64_t rows0, const float *src1, int64_t rows, int cols, float zp,
+            int nplanes, __bf16 *dst, int64_t ldd, int64_t plane, hipStream_t stream);
+// Planes needed for integer codes in [lo, hi] centred on zp.
+inline int planes_for(double lo, double hi, double zp) {
+  const double a = lo - zp < 0 ? zp - lo : lo - zp, b = hi - zp < 0 ? zp - hi : hi - zp;
+  return (a > b ? a : b) <= 256.0 ? 1 : 2;
+}
+
+}  // namespace wgrad
+}  // namespace rxmet
