@@ -634,7 +634,7 @@ struct BwdWorkspace {
     wgrad::tn_plan(static_cast<int>(M), static_cast<int>(C), H, &S_hh, &kper_hh);
     const size_t np = std::max(static_cast<size_t>(S_ih) * C * I, static_cast<size_t>(S_hh) * C * H);
     part = o; o += al(sizeof(float) * np);
-    gsum = o; o += al(sizeof(float) * 2 * C * static_cast<size_t>(std::max(S_ih, S_hh)));
+    gsum = o; o += al(sizeof(float) * 4 * C * static_cast<size_t>(std::max(S_ih, S_hh)));
     // clustered recurrence (H a multiple of 64)
     const size_t Bpad = (static_cast<size_t>(B) + kBB - 1) / kBB * kBB, G = H / kBcUnits + 1;
     wfrag_cl = o; o += al(sizeof(v4i) * 64 * (H / 16) * KS2);

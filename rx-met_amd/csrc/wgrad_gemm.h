@@ -17,8 +17,8 @@ namespace wgrad {
 
 // part[s][p][q] = sum over k in split s of A[k * lda + p] * sum_pl Bt[pl * bplane + q * ldb + k]
 // (A: gradient rows k; Bt: codes transposed, k contiguous, zero beyond K up to a multiple of 32).
-// colsum (optional, [S][2][P]): partial sums of A over the split's k, written by the first
-// q-tile.  S splits of kper rows (kper a multiple of 32).
+// colsum (optional, [S][4][P] at most): partial sums of A over the split's k, written by the
+// first q-tile.  S splits of kper rows (kper a multiple of 32).
 struct TnArgs {
   const float *A;
   int64_t lda;

@@ -21,66 +21,74 @@ __device__ __forceinline__ void split3(float a, __bf16 &hi, __bf16 &mid, __bf16 
 }
 
 // ---------------------------------------------------------------------------------
-// TN: part[s][p][q] = sum_k A[k][p] Bt[q][k]; 128 x 128 tile, 256 threads (2 x 2 waves of
-// 64 x 64), K in chunks of 32 staged in LDS (A split into three bf16 planes on the way), the
-// next chunk's global loads issued before the current chunk's MFMAs.
+// TN: part[s][p][q] = sum_k A[k][p] Bt[q][k].  256 threads as 2 x 2 waves, each wave a
+// (16 WI) x (16 WJ) tile, so the block tile is BP = 32 WI by BQ = 32 WJ.  K runs in chunks of
+// 32 staged in LDS (A split into three bf16 planes on the way); the next chunk's global loads
+// are issued before the current chunk's MFMAs.
 // ---------------------------------------------------------------------------------
-template <int NPL>
+template <int NPL, int WI, int WJ>
 __global__ __launch_bounds__(256) void tn_kernel(TnArgs a, int ntp, int ntq, int ngroups) {
-  __shared__ __align__(16) __bf16 As[3][128][kRow];
-  __shared__ __align__(16) __bf16 Bs[NPL][128][kRow];
+  constexpr int BP = 32 * WI, BQ = 32 * WJ;
+  constexpr int ATH = 256 / BP;     // threads per A column (k groups of 8 dealt round robin)
+  constexpr int AG = 4 / ATH;       // k groups of 8 per thread
+  constexpr int BCH = BQ / 64;      // B rows per thread (4 chunks of 16 bytes per row)
+  __shared__ __align__(16) __bf16 As[3][BP][kRow];
+  __shared__ __align__(16) __bf16 Bs[NPL][BQ][kRow];
   // blocks 8 r + x run on XCD x; the ntq q-tiles of one (p-tile, split) group are consecutive
   // blocks of one XCD, so they share the group's A rows in that XCD's L2
   const int xcd = blockIdx.x % 8, r8 = blockIdx.x / 8;
   const int qt = r8 % ntq, grp = (r8 / ntq) * 8 + xcd;
   if (grp >= ngroups) return;
   const int pt = grp % ntp, s = grp / ntp;
-  const int p0 = 128 * pt, q0 = 128 * qt;
+  const int p0 = BP * pt, q0 = BQ * qt;
   const int kbeg = s * a.kper;
   const int kend = min(a.K, kbeg + a.kper);
   const int tid = threadIdx.x, w = tid / 64, l = tid % 64;
   const int wm = w / 2, wn = w % 2;
 
-  // staging roles: A column sp, k groups sg and sg + 2 (8 k each); B rows bq, bq + 64, chunk bc
-  const int sp = tid % 128, sg = tid / 128;
+  // staging roles: A column sp with k groups sg + ATH g; B rows bq + 64 h, 16-byte chunk bc
+  const int sp = tid % BP, sg = tid / BP;
   const bool pin = p0 + sp < a.P;
   const float *ap = a.A + (p0 + sp);
   const int bq = tid / 4, bc = tid % 4;
-  const bool qin0 = q0 + bq < a.Q, qin1 = q0 + bq + 64 < a.Q;
-  // rows past Q read row 0 and are replaced by zeros (value select, not pointer select)
-  const __bf16 *bp0 = a.Bt + static_cast<int64_t>(qin0 ? q0 + bq : 0) * a.ldb + 8 * bc;
-  const __bf16 *bp1 = a.Bt + static_cast<int64_t>(qin1 ? q0 + bq + 64 : 0) * a.ldb + 8 * bc;
+  bool qin[BCH];
+  const __bf16 *bp[BCH];
+#pragma unroll
+  for (int h = 0; h < BCH; ++h) {
+    qin[h] = q0 + bq + 64 * h < a.Q;
+    // rows past Q read row 0 and are replaced by zeros (value select, not pointer select)
+    bp[h] = a.Bt + static_cast<int64_t>(qin[h] ? q0 + bq + 64 * h : 0) * a.ldb + 8 * bc;
+  }
   const bool want_sum = a.colsum != nullptr && qt == 0;
 
-  float av[2][8];
-  int4 bv[NPL][2];
+  float av[AG][8];
+  int4 bv[NPL][BCH];
 #define RXMET_TN_LOAD(K0)                                                                     \
   {                                                                                           \
-    _Pragma("unroll") for (int gi = 0; gi < 2; ++gi)                                          \
+    _Pragma("unroll") for (int gi = 0; gi < AG; ++gi)                                         \
     _Pragma("unroll") for (int j = 0; j < 8; ++j) {                                           \
-      const int k = (K0) + 8 * (sg + 2 * gi) + j;                                             \
+      const int k = (K0) + 8 * (sg + ATH * gi) + j;                                           \
       av[gi][j] = (pin && k < kend) ? ap[static_cast<int64_t>(k) * a.lda] : 0.0f;             \
     }                                                                                         \
-    _Pragma("unroll") for (int pl = 0; pl < NPL; ++pl) {                                      \
-      const int4 t0 = *reinterpret_cast<const int4 *>(bp0 + pl * a.bplane + (K0));            \
-      const int4 t1 = *reinterpret_cast<const int4 *>(bp1 + pl * a.bplane + (K0));            \
-      bv[pl][0] = qin0 ? t0 : make_int4(0, 0, 0, 0);                                          \
-      bv[pl][1] = qin1 ? t1 : make_int4(0, 0, 0, 0);                                          \
+    _Pragma("unroll") for (int pl = 0; pl < NPL; ++pl)                                        \
+    _Pragma("unroll") for (int h = 0; h < BCH; ++h) {                                         \
+      const int4 t = *reinterpret_cast<const int4 *>(bp[h] + pl * a.bplane + (K0));           \
+      bv[pl][h] = qin[h] ? t : make_int4(0, 0, 0, 0);                                         \
     }                                                                                         \
   }
 
-  v4f acc[4][4];
+  v4f acc[WI][WJ];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < WI; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < WJ; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
   float csum = 0.0f;
 
   if (kbeg < kend) RXMET_TN_LOAD(kbeg);
   for (int k0 = kbeg; k0 < kend; k0 += kKC) {
     __syncthreads();  // the previous chunk's fragments are read
 #pragma unroll
-    for (int gi = 0; gi < 2; ++gi) {
+    for (int gi = 0; gi < AG; ++gi) {
       v8bf h, m, lo;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
@@ -89,47 +97,52 @@ __global__ __launch_bounds__(256) void tn_kernel(TnArgs a, int ntp, int ntq, int
         h[j] = x; m[j] = y; lo[j] = z;
         if (want_sum) csum += av[gi][j];
       }
-      const int kk = 8 * (sg + 2 * gi);
+      const int kk = 8 * (sg + ATH * gi);
       *reinterpret_cast<v8bf *>(&As[0][sp][kk]) = h;
       *reinterpret_cast<v8bf *>(&As[1][sp][kk]) = m;
       *reinterpret_cast<v8bf *>(&As[2][sp][kk]) = lo;
     }
 #pragma unroll
-    for (int pl = 0; pl < NPL; ++pl) {
-      *reinterpret_cast<int4 *>(&Bs[pl][bq][8 * bc]) = bv[pl][0];
-      *reinterpret_cast<int4 *>(&Bs[pl][bq + 64][8 * bc]) = bv[pl][1];
-    }
+    for (int pl = 0; pl < NPL; ++pl)
+#pragma unroll
+      for (int h = 0; h < BCH; ++h)
+        *reinterpret_cast<int4 *>(&Bs[pl][bq + 64 * h][8 * bc]) = bv[pl][h];
     __syncthreads();
     if (k0 + kKC < kend) RXMET_TN_LOAD(k0 + kKC);
+    v8bf bf[NPL][WJ];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int pl = 0; pl < NPL; ++pl)
+#pragma unroll
+      for (int j = 0; j < WJ; ++j)
+        bf[pl][j] = *reinterpret_cast<const v8bf *>(&Bs[pl][16 * (WJ * wn + j) + l % 16][8 * (l / 16)]);
+#pragma unroll
+    for (int i = 0; i < WI; ++i) {
       v8bf af[3];
 #pragma unroll
       for (int c = 0; c < 3; ++c)
-        af[c] = *reinterpret_cast<const v8bf *>(&As[c][64 * wm + 16 * i + l % 16][8 * (l / 16)]);
+        af[c] = *reinterpret_cast<const v8bf *>(&As[c][16 * (WI * wm + i) + l % 16][8 * (l / 16)]);
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < WJ; ++j)
 #pragma unroll
         for (int pl = 0; pl < NPL; ++pl) {
-          const v8bf bf = *reinterpret_cast<const v8bf *>(&Bs[pl][64 * wn + 16 * j + l % 16][8 * (l / 16)]);
           // small terms first
-          acc[i][j] = mfma_bf16(af[2], bf, acc[i][j]);
-          acc[i][j] = mfma_bf16(af[1], bf, acc[i][j]);
-          acc[i][j] = mfma_bf16(af[0], bf, acc[i][j]);
+          acc[i][j] = mfma_bf16(af[2], bf[pl][j], acc[i][j]);
+          acc[i][j] = mfma_bf16(af[1], bf[pl][j], acc[i][j]);
+          acc[i][j] = mfma_bf16(af[0], bf[pl][j], acc[i][j]);
         }
     }
   }
 #undef RXMET_TN_LOAD
-  if (want_sum && pin) a.colsum[(static_cast<int64_t>(s) * 2 + sg) * a.P + p0 + sp] = csum;
+  if (want_sum && pin) a.colsum[(static_cast<int64_t>(s) * ATH + sg) * a.P + p0 + sp] = csum;
   float *part = a.part + static_cast<int64_t>(s) * a.P * a.Q;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < WI; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int q = q0 + 64 * wn + 16 * j + l % 16;
+    for (int j = 0; j < WJ; ++j) {
+      const int q = q0 + 16 * (WJ * wn + j) + l % 16;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int p = p0 + 64 * wm + 16 * i + 4 * (l / 16) + r;
+        const int p = p0 + 16 * (WI * wm + i) + 4 * (l / 16) + r;
         if (p < a.P && q < a.Q) part[static_cast<int64_t>(p) * a.Q + q] = acc[i][j][r];
       }
     }
@@ -232,7 +245,7 @@ __global__ __launch_bounds__(256) void nt_kernel(NtArgs a) {
 __global__ __launch_bounds__(256) void tn_finish_kernel(const float *__restrict__ part, int S, int P,
                                                         int Q, const float *__restrict__ qscale,
                                                         float *__restrict__ out, int64_t ldo,
-                                                        bool transpose,
+                                                        bool transpose, int ath,
                                                         const float *__restrict__ colsum,
                                                         float *__restrict__ bias) {
   const int64_t n = static_cast<int64_t>(P) * Q;
@@ -250,7 +263,7 @@ __global__ __launch_bounds__(256) void tn_finish_kernel(const float *__restrict_
     } else if (colsum && bias) {
       const int p = static_cast<int>(i - n);
       float acc = 0.0f;
-      for (int s = 0; s < 2 * S; ++s) acc += colsum[static_cast<int64_t>(s) * P + p];
+      for (int s = 0; s < S * ath; ++s) acc += colsum[static_cast<int64_t>(s) * P + p];
       bias[p * ldo] = acc;
     }
   }
@@ -305,8 +318,22 @@ int codes_t(const float *src0, int64_t rows0, const float *src1, int64_t rows, i
   return 0;
 }
 
+// Block tile of a TN product: wave tiles WI x WJ (of 16 x 16) chosen by the width Q.
+struct TnTile {
+  int wi, wj;
+  int bp() const { return 32 * wi; }
+  int bq() const { return 32 * wj; }
+  int ath() const { return 256 / bp(); }
+};
+static TnTile tn_tile(int Q) {
+  if (Q >= 256) return {4, 8};
+  if (Q <= 64) return {4, 2};
+  return {4, 4};
+}
+
 void tn_plan(int K, int P, int Q, int *S, int *kper) {
-  const int tiles = ((P + 127) / 128) * ((Q + 127) / 128);
+  const TnTile t = tn_tile(Q);
+  const int tiles = ((P + t.bp() - 1) / t.bp()) * ((Q + t.bq() - 1) / t.bq());
   const int chunks = (K + kKC - 1) / kKC;
   int s = (1024 + tiles - 1) / tiles;  // about 1024 workgroups
   if (s > chunks) s = chunks;
@@ -316,16 +343,27 @@ void tn_plan(int K, int P, int Q, int *S, int *kper) {
   *S = (K + *kper - 1) / *kper;
 }
 
-int tn(const TnArgs &a, int nplanes, hipStream_t stream) {
-  RXMET_CHECK_ARG(nplanes == 1 || nplanes == 2, "nplanes must be 1 or 2");
-  RXMET_CHECK_ARG(a.kper % kKC == 0 && a.ldb % 8 == 0, "bad TN layout");
-  const int ntp = (a.P + 127) / 128, ntq = (a.Q + 127) / 128;
+template <int WI, int WJ>
+static void tn_launch(const TnArgs &a, int nplanes, hipStream_t stream) {
+  const int ntp = (a.P + 32 * WI - 1) / (32 * WI), ntq = (a.Q + 32 * WJ - 1) / (32 * WJ);
   const int ngroups = ntp * a.S, padded = (ngroups + 7) / 8 * 8;
   const dim3 grid(static_cast<unsigned>(padded * ntq));
   if (nplanes == 1)
-    hipLaunchKernelGGL(tn_kernel<1>, grid, dim3(256), 0, stream, a, ntp, ntq, ngroups);
+    hipLaunchKernelGGL((tn_kernel<1, WI, WJ>), grid, dim3(256), 0, stream, a, ntp, ntq, ngroups);
   else
-    hipLaunchKernelGGL(tn_kernel<2>, grid, dim3(256), 0, stream, a, ntp, ntq, ngroups);
+    hipLaunchKernelGGL((tn_kernel<2, WI, WJ>), grid, dim3(256), 0, stream, a, ntp, ntq, ngroups);
+}
+
+int tn(const TnArgs &a, int nplanes, hipStream_t stream) {
+  RXMET_CHECK_ARG(nplanes == 1 || nplanes == 2, "nplanes must be 1 or 2");
+  RXMET_CHECK_ARG(a.kper % kKC == 0 && a.ldb % 8 == 0, "bad TN layout");
+  const TnTile t = tn_tile(a.Q);
+  if (t.wj == 8)
+    tn_launch<4, 8>(a, nplanes, stream);
+  else if (t.wj == 2)
+    tn_launch<4, 2>(a, nplanes, stream);
+  else
+    tn_launch<4, 4>(a, nplanes, stream);
   RXMET_CHECK_LAUNCH();
   return 0;
 }
@@ -348,7 +386,7 @@ int tn_finish(const float *part, int S, int P, int Q, const float *qscale, float
   int64_t blocks = (n + 255) / 256;
   if (blocks > 4096) blocks = 4096;
   hipLaunchKernelGGL(tn_finish_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
-                     part, S, P, Q, qscale, out, ldo, transpose, colsum, bias);
+                     part, S, P, Q, qscale, out, ldo, transpose, tn_tile(Q).ath(), colsum, bias);
   RXMET_CHECK_LAUNCH();
   return 0;
 }
