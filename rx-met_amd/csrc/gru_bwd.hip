@@ -8,32 +8,29 @@
 // SGEMMs (dx, dR, dW) and four mask passes.
 //
 // Here:
-//   1. prologue    : dequantised W and x for the weight-gradient GEMMs, R_q packed as
-//                    int8 MFMA fragments of the transposed product, row sums of R_q;
-//   2. recurrence  : one persistent workgroup per 16 sequences walks t = T-1..0.  Each
-//                    lane owns one hidden unit for four sequences (same layout as the
-//                    forward), so dh stays in registers between steps.  Per step: the
-//                    fused STE pointwise (all mask families), dp/dq written for the GEMMs,
-//                    bias gradients accumulated in fp64 registers; then
-//                    dh += R_deq dq on MFMA: dq * scale_R is written per sequence as a
-//                    22-bit block-fixed-point integer (exponent from the row maximum)
-//                    split into three int8 planes, so v_mfma_i32_16x16x64_i8 accumulates
-//                    exactly against the resident int8 R_q; the planes are recombined in
-//                    fp64 and rescaled (error <= 2^-22 of the row maximum per term, below
-//                    an fp32 SGEMM's rounding);
+//   1. prologue    : x, h_prev and W codes as bf16 operand planes for the weight-gradient
+//                    GEMMs (h codes recovered exactly from the dequantised h);
+//   2. recurrence  : both directions walk t = T-1..0 in one clustered launch
+//                    (bwd_recurrence_cl: a batch tile's hidden units split over a cluster of
+//                    workgroups, dq * scale_R exchanged through global memory each step and
+//                    dh += R_deq dq summed on fp32 MFMA with the R values resident in VGPRs);
+//                    the per-tile fallback (bwd_recurrence) keeps one workgroup per 16
+//                    sequences, each lane owning one hidden unit for four sequences, with
+//                    dh += R_deq dq on int8 MFMA over 22-bit block-fixed-point dq (three int8
+//                    planes against the resident int8 R_q, recombined in fp64; error <= 2^-22
+//                    of the row maximum per term).  Both fuse the STE pointwise (all mask
+//                    families), write dp/dq for the GEMMs and keep fp64 bias partials;
 //   3. bias fold   : per-workgroup fp64 partials summed in a fixed order (deterministic);
-//   4. dx, dW, dR  : rocBLAS SGEMMs on the dp/dq buffers (dW and dR split over the long
-//                    T*B reduction and summed in a fixed order), then one mask pass.
-#include <cmath>
-#include <cstdlib>
-#include <vector>
+//   4. dx, dW, dR  : bf16-MFMA GEMMs with the gradients split exactly into three bf16 terms
+//                    (wgrad_gemm.h; dW and dR split over the long T*B reduction and summed in
+//                    a fixed order), then one mask pass.
 
-#include "blas_util.h"
 #include "cluster.h"
 #include "gru_internal.h"
 #include "mfma_frag.h"
 #include "rxmet_common.h"
 #include "rxmet_gru.h"
+#include "wgrad_gemm.h"
 
 namespace rxmet {
 namespace gru {
@@ -43,23 +40,6 @@ constexpr int kBTile = 16;
 // ---------------------------------------------------------------------------------
 // 1. prologue
 // ---------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void dequant_inputs(int64_t nx, int64_t nw, int C,
-                                                      const float *__restrict__ xq, float eff_x,
-                                                      float zp_x, const float *__restrict__ Wq,
-                                                      const float *__restrict__ eff_w,
-                                                      float *__restrict__ xd,
-                                                      float *__restrict__ Wd) {
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < nx + nw;
-       i += stride) {
-    if (i < nx) {
-      xd[i] = (xq[i] - zp_x) * eff_x;
-    } else {
-      const int64_t k = i - nx;
-      Wd[k] = (Wq[k] - 0.0f) * eff_w[k % C];
-    }
-  }
-}
 
 // R_q [H][3H] -> B fragments of D[b][k] = sum_c A[b][c] R[k][c]:
 // frag[((ut * KS2) + s) * 64 + lane] holds R_q[k][c] for k = 16*ut + lane % 16,
@@ -605,7 +585,8 @@ size_t bwd_lds_bytes(int KS2) {
 }
 
 struct BwdWorkspace {
-  size_t dp, dq, xd, wd, rfrag, rowsum, effr, effw, bias, part, xch, rt, sync, total;
+  size_t dp, dq, xt, ht, wb, qsc, rfrag, rowsum, effr, effw, bias, part, xch, rt, sync, total;
+  int Mp, S_w, kper_w, S_r, kper_r;
   BwdWorkspace(int T, int B, int I, int H) {
     const size_t C = 3 * static_cast<size_t>(H);
     const size_t KS2 = (C + 63) / 64;
@@ -614,15 +595,24 @@ struct BwdWorkspace {
     size_t o = 0;
     dp = o; o += al(sizeof(float) * static_cast<size_t>(T) * B * C);
     dq = o; o += al(sizeof(float) * static_cast<size_t>(T) * B * C);
-    xd = o; o += al(sizeof(float) * static_cast<size_t>(T) * B * I);
-    wd = o; o += al(sizeof(float) * static_cast<size_t>(I) * C);
+    // weight-gradient GEMM operands: x and h codes (transposed, rows padded to Mp) and W codes
+    // as bf16 planes; the per-column scales of dW and dR
+    const size_t M = static_cast<size_t>(T) * B;
+    Mp = static_cast<int>((M + 31) / 32 * 32);
+    xt = o; o += al(sizeof(__bf16) * 2 * I * static_cast<size_t>(Mp));
+    ht = o; o += al(sizeof(__bf16) * 2 * H * static_cast<size_t>(Mp));
+    wb = o; o += al(sizeof(__bf16) * 2 * I * C);
+    qsc = o; o += al(sizeof(float) * (I + H));
     rfrag = o; o += al(sizeof(v4i) * 64 * ((H + 15) / 16) * KS2);
     rowsum = o; o += al(sizeof(float) * H);
     effr = o; o += al(sizeof(float) * C);
     effw = o; o += al(sizeof(float) * C);
     bias = o; o += al(sizeof(double) * 2 * C * nwg);
-    const size_t S = static_cast<size_t>(blas::splitk_chunks(static_cast<int64_t>(T) * B));
-    part = o; o += al(sizeof(float) * S * C * (static_cast<size_t>(I) > H ? I : H));
+    wgrad::tn_plan(static_cast<int>(M), static_cast<int>(C), I, &S_w, &kper_w);
+    wgrad::tn_plan(static_cast<int>(M), static_cast<int>(C), H, &S_r, &kper_r);
+    part = o;
+    o += al(sizeof(float) * C *
+            std::max(static_cast<size_t>(S_w) * I, static_cast<size_t>(S_r) * H));
     // clustered recurrence: dq exchange, packed R_q values, counters
     const size_t Bpad = nwg * kBTile;
     xch = o; o += al(sizeof(float) * 2 * Bpad * KS2 * 64);
@@ -637,7 +627,7 @@ struct BwdPlan {
   BwdArgs ba;
   const rxmet_gru_bwd_dir *d;
   char *wsb;
-  float *xd, *wd;
+  int npx, nph, npw;  // bf16 planes of the x, h and W codes
 };
 
 static int backward_prologue(int T, int B, int I, int H, const rxmet_gru_bwd_dir &d,
@@ -656,8 +646,6 @@ static int backward_prologue(int T, int B, int I, int H, const rxmet_gru_bwd_dir
   char *wsb = static_cast<char *>(d.workspace);
   float *effr = reinterpret_cast<float *>(wsb + ws.effr);
   float *effw = reinterpret_cast<float *>(wsb + ws.effw);
-  plan->xd = reinterpret_cast<float *>(wsb + ws.xd);
-  plan->wd = reinterpret_cast<float *>(wsb + ws.wd);
   std::vector<float> host(8 * static_cast<size_t>(C));
   try {
     make_channel_factors(*params, H, host.data() + 4 * C, host.data() + 5 * C, host.data() + 6 * C,
@@ -670,17 +658,42 @@ static int backward_prologue(int T, int B, int I, int H, const rxmet_gru_bwd_dir
   RXMET_CHECK_HIP(hipMemcpyAsync(effw, host.data(), sizeof(float) * C, hipMemcpyHostToDevice, stream));
   RXMET_CHECK_HIP(hipMemcpyAsync(effr, host.data() + C, sizeof(float) * C, hipMemcpyHostToDevice,
                                  stream));
+  // weight-gradient operands: x codes, h codes (recovered from the dequantised h) and W codes
   const float eff_x = effective_scale(params->g[RXMET_GRU_X].scale, params->use_pot2 != 0);
   const float zp_x = static_cast<float>(params->g[RXMET_GRU_X].zero_point);
-  const int64_t nx = static_cast<int64_t>(T) * B * I, nw = static_cast<int64_t>(I) * C;
-  int64_t blocks = (nx + nw + 255) / 256;
-  if (blocks > 8192) blocks = 8192;
+  const float eff_h = effective_scale(params->g[RXMET_GRU_H].scale, params->use_pot2 != 0);
+  const float zp_h = static_cast<float>(params->g[RXMET_GRU_H].zero_point);
+  const Bounds bx = bounds_of(params->g[RXMET_GRU_X].bits, params->g[RXMET_GRU_X].is_unsigned);
+  const Bounds bh = bounds_of(params->g[RXMET_GRU_H].bits, params->g[RXMET_GRU_H].is_unsigned);
+  const Bounds bw = bounds_of(params->chan_bits[RXMET_GRU_W], params->chan_unsigned[RXMET_GRU_W]);
+  plan->npx = wgrad::planes_for(bx.lo, bx.hi, zp_x);
+  plan->nph = wgrad::planes_for(bh.lo, bh.hi, zp_h);
+  plan->npw = wgrad::planes_for(bw.lo, bw.hi, 0.0);
+  const int64_t M = static_cast<int64_t>(T) * B, Mp = ws.Mp;
   {
-    rxmet::prof::Scope ps__("gru_bwd_dequant_inputs", stream);
-    hipLaunchKernelGGL(dequant_inputs, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, nx,
-                       nw, C, d.x_q, eff_x, zp_x, d.W_q, effw, plan->xd, plan->wd);
+    rxmet::prof::Scope ps__("gru_bwd_codes", stream);
+    if (int rc = wgrad::codes_t(d.x_q, M, nullptr, M, I, I, 1, zp_x, 1.0f, plan->npx,
+                                reinterpret_cast<__bf16 *>(wsb + ws.xt), Mp,
+                                static_cast<int64_t>(I) * Mp, stream))
+      return rc;
+    // h rows 0..T-1 are h_prev; each is (q - zp_h) eff_h
+    if (int rc = wgrad::codes_t(d.h, M, nullptr, M, H, H, 1, 0.0f, eff_h, plan->nph,
+                                reinterpret_cast<__bf16 *>(wsb + ws.ht), Mp,
+                                static_cast<int64_t>(H) * Mp, stream))
+      return rc;
+    // W_q [I][C] kept as is: rows are the channels c (K), columns the inputs i
+    if (int rc = wgrad::codes_t(d.W_q, C, nullptr, C, I, 1, C, 0.0f, 1.0f, plan->npw,
+                                reinterpret_cast<__bf16 *>(wsb + ws.wb), C,
+                                static_cast<int64_t>(I) * C, stream))
+      return rc;
   }
-  RXMET_CHECK_LAUNCH();
+  {
+    std::vector<float> qs(I + H);
+    for (int k = 0; k < I; ++k) qs[k] = eff_x;
+    for (int k = 0; k < H; ++k) qs[I + k] = eff_h;
+    RXMET_CHECK_HIP(hipMemcpyAsync(wsb + ws.qsc, qs.data(), sizeof(float) * (I + H),
+                                   hipMemcpyHostToDevice, stream));
+  }
   BwdArgs &ba = plan->ba;
   ba.T = T; ba.B = B; ba.H = H; ba.KS2 = KS2;
   ba.dh_new = d.dh_new; ba.h = d.h; ba.v = d.v;
@@ -794,24 +807,37 @@ static int backward_epilogue(int T, int B, int I, int H, BwdPlan &plan, hipStrea
   hipLaunchKernelGGL(fold_bias, dim3((C + 255) / 256), dim3(256), 0, stream, nwg, C,
                      plan.ba.bias_partial, d.dbw, d.dbr);
   RXMET_CHECK_LAUNCH();
-  int device = 0;
-  RXMET_CHECK_HIP(hipGetDevice(&device));
-  rocblas_handle bh = blas::handle(device);
-  RXMET_CHECK_ARG(bh != nullptr, "rocBLAS handle creation failed");
-  rocblas_set_stream(bh, stream);
   const int M = T * B;
   float *part = reinterpret_cast<float *>(plan.wsb + ws.part);
+  const float *qsc = reinterpret_cast<const float *>(plan.wsb + ws.qsc);
   {
     rxmet::prof::Scope ps__("gru_bwd_weight_gemms", stream);
-    // dx[M][I] = dp[M][C] * W_deq^T
-    RXMET_CHECK_ARG(blas::gemm_rm(bh, false, true, M, I, C, plan.ba.dp, C, plan.wd, C, d.dx, I) ==
-                        rocblas_status_success,
-                    "rocBLAS sgemm (dx) failed");
-    // dW[I][C] = x_deq^T * dp and dR[H][C] = h_prev^T * dq (h rows 0..T-1), split over K
-    const int S = blas::splitk_chunks(M);
-    if (int rc = blas::gemm_tn_splitk(bh, I, C, M, plan.xd, I, plan.ba.dp, C, d.dW, part, S, stream))
+    // dx[m][i] = sum_c (dp[m][c] eff_w[c]) W_q[i][c]
+    wgrad::NtArgs na;
+    na.A = plan.ba.dp; na.lda = C;
+    na.kscale = reinterpret_cast<const float *>(plan.wsb + ws.effw);
+    na.Bt = reinterpret_cast<const __bf16 *>(plan.wsb + ws.wb); na.ldb = C;
+    na.bplane = static_cast<int64_t>(I) * C;
+    na.M = M; na.N = I; na.K = C; na.out = d.dx; na.ldo = I;
+    if (int rc = wgrad::nt(na, plan.npw, stream)) return rc;
+    // dW[i][c] = eff_x sum_m (x_q - zp_x)[m][i] dp[m][c]
+    wgrad::TnArgs ta;
+    ta.A = plan.ba.dp; ta.lda = C;
+    ta.Bt = reinterpret_cast<const __bf16 *>(plan.wsb + ws.xt); ta.ldb = ws.Mp;
+    ta.bplane = static_cast<int64_t>(I) * ws.Mp;
+    ta.K = M; ta.P = C; ta.Q = I; ta.S = ws.S_w; ta.kper = ws.kper_w; ta.part = part;
+    ta.colsum = nullptr;
+    if (int rc = wgrad::tn(ta, plan.npx, stream)) return rc;
+    if (int rc = wgrad::tn_finish(part, ws.S_w, C, I, qsc, d.dW, C, true, nullptr, nullptr, stream))
       return rc;
-    if (int rc = blas::gemm_tn_splitk(bh, H, C, M, d.h, H, plan.ba.dq, C, d.dR, part, S, stream))
+    // dR[j][c] = eff_h sum_m (h_prev codes)[m][j] dq[m][c]
+    ta.A = plan.ba.dq;
+    ta.Bt = reinterpret_cast<const __bf16 *>(plan.wsb + ws.ht);
+    ta.bplane = static_cast<int64_t>(H) * ws.Mp;
+    ta.Q = H; ta.S = ws.S_r; ta.kper = ws.kper_r;
+    if (int rc = wgrad::tn(ta, plan.nph, stream)) return rc;
+    if (int rc = wgrad::tn_finish(part, ws.S_r, C, H, qsc + I, d.dR, C, true, nullptr, nullptr,
+                                  stream))
       return rc;
   }
   const int64_t n0 = static_cast<int64_t>(T) * B * I, n1 = static_cast<int64_t>(I) * C,

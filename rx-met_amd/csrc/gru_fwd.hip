@@ -58,30 +58,49 @@ struct WeightArgs {
   float *chan;  // kChanParams x C, fills wsum, rsum, btx, bth, rcol
 };
 
-__global__ __launch_bounds__(256) void quant_weights(int I, int H, WeightArgs a) {
+// One thread per gate column; rows are processed in blocks of kQwRows whose loads are all
+// issued before any code is stored (the sums stay sequential in k, as the reference's).
+constexpr int kQwRows = 32;
+__global__ __launch_bounds__(64) void quant_weights(int I, int H, WeightArgs a) {
   const int C = 3 * H;
   const int c = blockIdx.x * blockDim.x + threadIdx.x;
   if (c >= C) return;
   uint8_t keep;
   const float ew = a.eff[c], er = a.eff[C + c], ebw = a.eff[2 * C + c], ebr = a.eff[3 * C + c];
   float s = 0.0f;
-  for (int k = 0; k < I; ++k) {
-    const size_t i = static_cast<size_t>(k) * C + c;
-    const float q = clamp_keep(rintf(a.W[i] / ew) + 0.0f, a.bW, keep);
-    a.Wq[i] = q;
-    if (a.Wm) a.Wm[i] = keep;
-    s += q;
+  for (int k0 = 0; k0 < I; k0 += kQwRows) {
+    float v[kQwRows];
+#pragma unroll
+    for (int r = 0; r < kQwRows; ++r)
+      v[r] = k0 + r < I ? a.W[static_cast<size_t>(k0 + r) * C + c] : 0.0f;
+#pragma unroll
+    for (int r = 0; r < kQwRows; ++r) {
+      if (k0 + r >= I) break;
+      const size_t i = static_cast<size_t>(k0 + r) * C + c;
+      const float q = clamp_keep(rintf(v[r] / ew) + 0.0f, a.bW, keep);
+      a.Wq[i] = q;
+      if (a.Wm) a.Wm[i] = keep;
+      s += q;
+    }
   }
   a.chan[2 * C + c] = a.zp_x != 0.0f ? s * a.zp_x : 0.0f;  // wsum
   s = 0.0f;
   int exact = 0;
-  for (int k = 0; k < H; ++k) {
-    const size_t i = static_cast<size_t>(k) * C + c;
-    const float q = clamp_keep(rintf(a.R[i] / er) + 0.0f, a.bR, keep);
-    a.Rq[i] = q;
-    if (a.Rm) a.Rm[i] = keep;
-    s += q;
-    exact += static_cast<int>(q);
+  for (int k0 = 0; k0 < H; k0 += kQwRows) {
+    float v[kQwRows];
+#pragma unroll
+    for (int r = 0; r < kQwRows; ++r)
+      v[r] = k0 + r < H ? a.R[static_cast<size_t>(k0 + r) * C + c] : 0.0f;
+#pragma unroll
+    for (int r = 0; r < kQwRows; ++r) {
+      if (k0 + r >= H) break;
+      const size_t i = static_cast<size_t>(k0 + r) * C + c;
+      const float q = clamp_keep(rintf(v[r] / er) + 0.0f, a.bR, keep);
+      a.Rq[i] = q;
+      if (a.Rm) a.Rm[i] = keep;
+      s += q;
+      exact += static_cast<int>(q);
+    }
   }
   a.chan[3 * C + c] = a.zp_h != 0.0f ? s * a.zp_h : 0.0f;  // rsum
   a.chan[6 * C + c] = static_cast<float>(exact);            // rcol (exact)
@@ -742,7 +761,7 @@ static int forward_prologue(bool training, int T, int B, int I, int H, const rxm
   wa.chan = chan;
   {
     rxmet::prof::Scope ps__("gru_fwd_quant_weights", stream);
-    hipLaunchKernelGGL(quant_weights, dim3((C + 255) / 256), dim3(256), 0, stream, I, H, wa);
+    hipLaunchKernelGGL(quant_weights, dim3((C + 63) / 64), dim3(64), 0, stream, I, H, wa);
   }
   RXMET_CHECK_LAUNCH();
 

@@ -720,13 +720,13 @@ int rxmet_lstm_backward_quant(int32_t T, int32_t B, int32_t I, int32_t H,
   const int nph = wgrad::planes_for(sp.h.lo, sp.h.hi, sp.h.zp);
   const int npw = wgrad::planes_for(gwi.lo, gwi.hi, 0.0);
   const int64_t Mp = ws.Mp;
-  if (int rc = wgrad::codes_t(sv.x_q, M, nullptr, M, I, static_cast<float>(sp.x.zp), npx, xt, Mp,
+  if (int rc = wgrad::codes_t(sv.x_q, M, nullptr, M, I, I, 1, static_cast<float>(sp.x.zp), 1.0f, npx, xt, Mp,
                               static_cast<int64_t>(I) * Mp, stream))
     return rc;
-  if (int rc = wgrad::codes_t(sv.h0_q, B, sv.hidden, M, H, static_cast<float>(sp.h.zp), nph, ht, Mp,
+  if (int rc = wgrad::codes_t(sv.h0_q, B, sv.hidden, M, H, H, 1, static_cast<float>(sp.h.zp), 1.0f, nph, ht, Mp,
                               static_cast<int64_t>(H) * Mp, stream))
     return rc;
-  if (int rc = wgrad::codes_t(sv.w_ih_q, C, nullptr, C, I, 0.0f, npw, wt, C,
+  if (int rc = wgrad::codes_t(sv.w_ih_q, C, nullptr, C, I, I, 1, 0.0f, 1.0f, npw, wt, C,
                               static_cast<int64_t>(I) * C, stream))
     return rc;
   {

@@ -43,7 +43,7 @@ struct NtArgs {
   int64_t ldo;
 };
 
-// Number of K splits for a TN product (about 1024 workgroups) and rows per split.
+// Number of K splits for a TN product (about 512 workgroups) and rows per split.
 void tn_plan(int K, int P, int Q, int *S, int *kper);
 // Launches; nplanes is 1 or 2.
 int tn(const TnArgs &a, int nplanes, hipStream_t stream);
@@ -54,12 +54,15 @@ int nt(const NtArgs &a, int nplanes, hipStream_t stream);
 int tn_finish(const float *part, int S, int P, int Q, const float *qscale, float *out, int64_t ldo,
               bool transpose, const float *colsum, float *bias, hipStream_t stream);
 
-// Codes as bf16 operand planes, transposed: for r < rows and c < cols, v = code(r, c) - zp with
-// code(r, c) = r < rows0 ? src0[r * cols + c] : src1[(r - rows0) * cols + c]; with one plane
-// dst[c * ldd + r] = v (|v| <= 256), with two planes dst[c * ldd + r] = 256 (v >> 8) and
-// dst[plane + c * ldd + r] = v & 255.  Rows rows..ldd-1 are written as zeros.
-int codes_t(const float *src0, int64_t rows0, const float *src1, int64_t rows, int cols, float zp,
-            int nplanes, __bf16 *dst, int64_t ldd, int64_t plane, hipStream_t stream);
+// Codes as bf16 operand planes, transposed: for r < rows and c < cols,
+//   v = rint((x(r, c) - zp) / div),  x(r, c) = r < rows0 ? src0[r rs + c cs] : src1[(r - rows0) rs + c cs]
+// (div = 1 for stored codes; div = the scale for dequantised values (q - zp) s, which it
+// inverts exactly for |q - zp| < 2^16); with one plane dst[c * ldd + r] = v (|v| <= 256), with
+// two planes dst[c * ldd + r] = 256 (v >> 8) and dst[plane + c * ldd + r] = v & 255.  Rows
+// rows..ldd-1 are written as zeros.
+int codes_t(const float *src0, int64_t rows0, const float *src1, int64_t rows, int cols, int64_t rs,
+            int64_t cs, float zp, float div, int nplanes, __bf16 *dst, int64_t ldd, int64_t plane,
+            hipStream_t stream);
 // Planes needed for integer codes in [lo, hi] centred on zp.
 inline int planes_for(double lo, double hi, double zp) {
   const double a = lo - zp < 0 ? zp - lo : lo - zp, b = hi - zp < 0 ? zp - hi : hi - zp;

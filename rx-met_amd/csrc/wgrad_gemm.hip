@@ -149,27 +149,35 @@ __global__ __launch_bounds__(256) void tn_kernel(TnArgs a, int ntp, int ntq, int
 }
 
 // ---------------------------------------------------------------------------------
-// NT: out[m][n] = sum_k (A[m][k] kscale[k]) Bt[n][k]; 128 x 64 tile, 256 threads (2 x 2 waves
-// of 64 x 32), K in chunks of 32.
+// NT: out[m][n] = sum_k (A[m][k] kscale[k]) Bt[n][k]; 128 x (32 WJ) tile, 256 threads (2 x 2
+// waves of 64 x 16 WJ), K in chunks of 32.
 // ---------------------------------------------------------------------------------
-template <int NPL>
+template <int NPL, int WJ>
 __global__ __launch_bounds__(256) void nt_kernel(NtArgs a) {
+  constexpr int BN = 32 * WJ, BCH = (4 * BN + 255) / 256;  // B 16-byte chunks per thread
   __shared__ __align__(16) __bf16 As[3][128][kRow];
-  __shared__ __align__(16) __bf16 Bs[NPL][64][kRow];
-  const int m0 = 128 * blockIdx.x, n0 = 64 * blockIdx.y;
+  __shared__ __align__(16) __bf16 Bs[NPL][BN][kRow];
+  const int m0 = 128 * blockIdx.x, n0 = BN * blockIdx.y;
   const int tid = threadIdx.x, w = tid / 64, l = tid % 64;
   const int wm = w / 2, wn = w % 2;
   // staging roles: A row sm, 16 k at 16 sh; B row bn, chunk bc
   const int sm = tid / 2, sh = tid % 2;
   const bool min_ = m0 + sm < a.M;
   const float *ap = a.A + static_cast<int64_t>(m0 + sm) * a.lda + 16 * sh;
-  const int bn = tid / 4, bc = tid % 4;
-  const bool nin = n0 + bn < a.N;
-  const __bf16 *bp = a.Bt + static_cast<int64_t>(n0 + bn) * a.ldb + 8 * bc;
+  // B chunk e = tid + 256 h: row e / 4, 16-byte chunk e % 4 (rows past N read row 0, zeroed)
+  bool bok[BCH], nin[BCH];
+  const __bf16 *bp[BCH];
+#pragma unroll
+  for (int h = 0; h < BCH; ++h) {
+    const int e = tid + 256 * h, bn = e / 4, bc = e % 4;
+    bok[h] = e < 4 * BN;
+    nin[h] = bok[h] && n0 + bn < a.N;
+    bp[h] = a.Bt + static_cast<int64_t>(nin[h] ? n0 + bn : 0) * a.ldb + 8 * bc;
+  }
 
   float4 av[4];
   float4 sv[4];
-  int4 bv[NPL];
+  int4 bv[NPL][BCH];
   auto load = [&](int k0) {
     const bool kin = k0 + 16 * sh < a.K;  // K is a multiple of 16
 #pragma unroll
@@ -179,14 +187,18 @@ __global__ __launch_bounds__(256) void nt_kernel(NtArgs a) {
     }
 #pragma unroll
     for (int pl = 0; pl < NPL; ++pl)
-      bv[pl] = nin ? *reinterpret_cast<const int4 *>(bp + pl * a.bplane + k0) : make_int4(0, 0, 0, 0);
+#pragma unroll
+      for (int h = 0; h < BCH; ++h) {
+        const int4 t = *reinterpret_cast<const int4 *>(bp[h] + pl * a.bplane + k0);
+        bv[pl][h] = nin[h] ? t : make_int4(0, 0, 0, 0);
+      }
   };
 
-  v4f acc[4][2];
+  v4f acc[4][WJ];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < WJ; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
   load(0);
   for (int k0 = 0; k0 < a.K; k0 += kKC) {
@@ -209,7 +221,12 @@ __global__ __launch_bounds__(256) void nt_kernel(NtArgs a) {
       *reinterpret_cast<v8bf *>(&As[2][sm][kk]) = lo;
     }
 #pragma unroll
-    for (int pl = 0; pl < NPL; ++pl) *reinterpret_cast<int4 *>(&Bs[pl][bn][8 * bc]) = bv[pl];
+    for (int pl = 0; pl < NPL; ++pl)
+#pragma unroll
+      for (int h = 0; h < BCH; ++h) {
+        const int e = tid + 256 * h;
+        if (bok[h]) *reinterpret_cast<int4 *>(&Bs[pl][e / 4][8 * (e % 4)]) = bv[pl][h];
+      }
     __syncthreads();
     if (k0 + kKC < a.K) load(k0 + kKC);
 #pragma unroll
@@ -219,10 +236,10 @@ __global__ __launch_bounds__(256) void nt_kernel(NtArgs a) {
       for (int c = 0; c < 3; ++c)
         af[c] = *reinterpret_cast<const v8bf *>(&As[c][64 * wm + 16 * i + l % 16][8 * (l / 16)]);
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+      for (int j = 0; j < WJ; ++j)
 #pragma unroll
         for (int pl = 0; pl < NPL; ++pl) {
-          const v8bf bf = *reinterpret_cast<const v8bf *>(&Bs[pl][32 * wn + 16 * j + l % 16][8 * (l / 16)]);
+          const v8bf bf = *reinterpret_cast<const v8bf *>(&Bs[pl][16 * (WJ * wn + j) + l % 16][8 * (l / 16)]);
           acc[i][j] = mfma_bf16(af[2], bf, acc[i][j]);
           acc[i][j] = mfma_bf16(af[1], bf, acc[i][j]);
           acc[i][j] = mfma_bf16(af[0], bf, acc[i][j]);
@@ -232,8 +249,8 @@ __global__ __launch_bounds__(256) void nt_kernel(NtArgs a) {
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int n = n0 + 32 * wn + 16 * j + l % 16;
+    for (int j = 0; j < WJ; ++j) {
+      const int n = n0 + 16 * (WJ * wn + j) + l % 16;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int m = m0 + 64 * wm + 16 * i + 4 * (l / 16) + r;
@@ -272,7 +289,8 @@ __global__ __launch_bounds__(256) void tn_finish_kernel(const float *__restrict_
 // Codes -> bf16 planes, transposed through a 64 x 64 LDS tile.
 __global__ __launch_bounds__(256) void codes_t_kernel(const float *__restrict__ src0, int64_t rows0,
                                                       const float *__restrict__ src1, int64_t rows,
-                                                      int cols, float zp, int nplanes,
+                                                      int cols, int64_t rs, int64_t cs, float zp,
+                                                      float div, int nplanes,
                                                       __bf16 *__restrict__ dst, int64_t ldd,
                                                       int64_t plane) {
   __shared__ int tile[64][65];
@@ -284,8 +302,8 @@ __global__ __launch_bounds__(256) void codes_t_kernel(const float *__restrict__ 
     const int c = c0 + cc;
     int v = 0;
     if (r < rows && c < cols) {
-      const float code = r < rows0 ? src0[r * cols + c] : src1[(r - rows0) * cols + c];
-      v = static_cast<int>(code - zp);
+      const float x = r < rows0 ? src0[r * rs + c * cs] : src1[(r - rows0) * rs + c * cs];
+      v = static_cast<int>(rintf((x - zp) / div));
     }
     tile[cc][rr] = v;
   }
@@ -307,13 +325,14 @@ __global__ __launch_bounds__(256) void codes_t_kernel(const float *__restrict__ 
   }
 }
 
-int codes_t(const float *src0, int64_t rows0, const float *src1, int64_t rows, int cols, float zp,
-            int nplanes, __bf16 *dst, int64_t ldd, int64_t plane, hipStream_t stream) {
+int codes_t(const float *src0, int64_t rows0, const float *src1, int64_t rows, int cols, int64_t rs,
+            int64_t cs, float zp, float div, int nplanes, __bf16 *dst, int64_t ldd, int64_t plane,
+            hipStream_t stream) {
   RXMET_CHECK_ARG(nplanes == 1 || nplanes == 2, "nplanes must be 1 or 2");
   RXMET_CHECK_ARG(ldd >= rows && (rows0 >= rows || src1 != nullptr), "bad codes_t layout");
   const dim3 grid(static_cast<unsigned>((ldd + 63) / 64), static_cast<unsigned>((cols + 63) / 64));
-  hipLaunchKernelGGL(codes_t_kernel, grid, dim3(256), 0, stream, src0, rows0, src1, rows, cols, zp,
-                     nplanes, dst, ldd, plane);
+  hipLaunchKernelGGL(codes_t_kernel, grid, dim3(256), 0, stream, src0, rows0, src1, rows, cols, rs,
+                     cs, zp, div, nplanes, dst, ldd, plane);
   RXMET_CHECK_LAUNCH();
   return 0;
 }
@@ -335,8 +354,9 @@ void tn_plan(int K, int P, int Q, int *S, int *kper) {
   const TnTile t = tn_tile(Q);
   const int tiles = ((P + t.bp() - 1) / t.bp()) * ((Q + t.bq() - 1) / t.bq());
   const int chunks = (K + kKC - 1) / kKC;
-  int s = (1024 + tiles - 1) / tiles;  // about 1024 workgroups
-  if (s > chunks) s = chunks;
+  // about 512 workgroups, each at least 32 chunks (fewer, larger partials)
+  int s = (512 + tiles - 1) / tiles;
+  if (s > chunks / 32) s = chunks / 32;
   if (s < 1) s = 1;
   const int per = (chunks + s - 1) / s;
   *kper = per * kKC;
@@ -371,11 +391,14 @@ int tn(const TnArgs &a, int nplanes, hipStream_t stream) {
 int nt(const NtArgs &a, int nplanes, hipStream_t stream) {
   RXMET_CHECK_ARG(nplanes == 1 || nplanes == 2, "nplanes must be 1 or 2");
   RXMET_CHECK_ARG(a.K % 16 == 0 && a.lda % 4 == 0 && a.ldb % 8 == 0, "bad NT layout");
-  const dim3 grid((a.M + 127) / 128, (a.N + 63) / 64);
+  // one column tile when N <= 128 (64, 96 or 128 wide), else tiles of 128
+  const int wj = a.N <= 64 ? 2 : a.N <= 96 ? 3 : 4;
+  const dim3 grid((a.M + 127) / 128, (a.N + 32 * wj - 1) / (32 * wj));
+  auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, dim3(256), 0, stream, a); };
   if (nplanes == 1)
-    hipLaunchKernelGGL(nt_kernel<1>, grid, dim3(256), 0, stream, a);
+    wj == 2 ? go(nt_kernel<1, 2>) : wj == 3 ? go(nt_kernel<1, 3>) : go(nt_kernel<1, 4>);
   else
-    hipLaunchKernelGGL(nt_kernel<2>, grid, dim3(256), 0, stream, a);
+    wj == 2 ? go(nt_kernel<2, 2>) : wj == 3 ? go(nt_kernel<2, 3>) : go(nt_kernel<2, 4>);
   RXMET_CHECK_LAUNCH();
   return 0;
 }
