@@ -586,7 +586,7 @@ size_t bwd_lds_bytes(int KS2) {
 
 struct BwdWorkspace {
   size_t dp, dq, xt, ht, wb, qsc, rfrag, rowsum, effr, effw, bias, part, xch, rt, sync, total;
-  int Mp, S_w, kper_w, S_r, kper_r;
+  int Mp, S_w[2], kper_w[2], S_r[2], kper_r[2];  // K splits by number of B planes
   BwdWorkspace(int T, int B, int I, int H) {
     const size_t C = 3 * static_cast<size_t>(H);
     const size_t KS2 = (C + 63) / 64;
@@ -608,11 +608,14 @@ struct BwdWorkspace {
     effr = o; o += al(sizeof(float) * C);
     effw = o; o += al(sizeof(float) * C);
     bias = o; o += al(sizeof(double) * 2 * C * nwg);
-    wgrad::tn_plan(static_cast<int>(M), static_cast<int>(C), I, &S_w, &kper_w);
-    wgrad::tn_plan(static_cast<int>(M), static_cast<int>(C), H, &S_r, &kper_r);
+    for (int np = 0; np < 2; ++np)
+      wgrad::tn_plan(static_cast<int>(M), static_cast<int>(C), I, np + 1, &S_w[np], &kper_w[np]);
+    for (int np = 0; np < 2; ++np)
+      wgrad::tn_plan(static_cast<int>(M), static_cast<int>(C), H, np + 1, &S_r[np], &kper_r[np]);
     part = o;
     o += al(sizeof(float) * C *
-            std::max(static_cast<size_t>(S_w) * I, static_cast<size_t>(S_r) * H));
+            std::max(static_cast<size_t>(std::max(S_w[0], S_w[1])) * I,
+                     static_cast<size_t>(std::max(S_r[0], S_r[1])) * H));
     // clustered recurrence: dq exchange, packed R_q values, counters
     const size_t Bpad = nwg * kBTile;
     xch = o; o += al(sizeof(float) * 2 * Bpad * KS2 * 64);
@@ -825,18 +828,20 @@ static int backward_epilogue(int T, int B, int I, int H, BwdPlan &plan, hipStrea
     ta.A = plan.ba.dp; ta.lda = C;
     ta.Bt = reinterpret_cast<const __bf16 *>(plan.wsb + ws.xt); ta.ldb = ws.Mp;
     ta.bplane = static_cast<int64_t>(I) * ws.Mp;
-    ta.K = M; ta.P = C; ta.Q = I; ta.S = ws.S_w; ta.kper = ws.kper_w; ta.part = part;
+    ta.K = M; ta.P = C; ta.Q = I; ta.S = ws.S_w[plan.npx - 1]; ta.kper = ws.kper_w[plan.npx - 1];
+    ta.part = part;
     ta.colsum = nullptr;
     if (int rc = wgrad::tn(ta, plan.npx, stream)) return rc;
-    if (int rc = wgrad::tn_finish(part, ws.S_w, C, I, qsc, d.dW, C, true, nullptr, nullptr, stream))
+    if (int rc = wgrad::tn_finish(part, ta.S, C, I, plan.npx, qsc, d.dW, C, true, nullptr, nullptr,
+                                  stream))
       return rc;
     // dR[j][c] = eff_h sum_m (h_prev codes)[m][j] dq[m][c]
     ta.A = plan.ba.dq;
     ta.Bt = reinterpret_cast<const __bf16 *>(plan.wsb + ws.ht);
     ta.bplane = static_cast<int64_t>(H) * ws.Mp;
-    ta.Q = H; ta.S = ws.S_r; ta.kper = ws.kper_r;
+    ta.Q = H; ta.S = ws.S_r[plan.nph - 1]; ta.kper = ws.kper_r[plan.nph - 1];
     if (int rc = wgrad::tn(ta, plan.nph, stream)) return rc;
-    if (int rc = wgrad::tn_finish(part, ws.S_r, C, H, qsc + I, d.dR, C, true, nullptr, nullptr,
+    if (int rc = wgrad::tn_finish(part, ta.S, C, H, plan.nph, qsc + I, d.dR, C, true, nullptr, nullptr,
                                   stream))
       return rc;
   }

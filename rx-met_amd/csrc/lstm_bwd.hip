@@ -610,7 +610,7 @@ __global__ __launch_bounds__(256) void lstm_bwd_finish(int64_t nx, float *dx, co
 struct BwdWorkspace {
   size_t dli, dlh, xt, wt, ht, qsc, frag, colsum, swih, swhh, aug_ih, aug_hh, part, gsum, wfrag_cl,
       csum, xp, xe, sync, total;
-  int Mp, S_ih, kper_ih, S_hh, kper_hh;
+  int Mp, S_ih[2], kper_ih[2], S_hh[2], kper_hh[2];  // K splits by number of B planes
   BwdWorkspace(int T, int B, int I, int H) {
     const size_t C = 4 * static_cast<size_t>(H), M = static_cast<size_t>(T) * B;
     const size_t KS2 = (C + 63) / 64;
@@ -630,11 +630,14 @@ struct BwdWorkspace {
     swhh = o; o += al(sizeof(float) * C);
     aug_ih = o; o += al(sizeof(float) * C * (I + 1));
     aug_hh = o; o += al(sizeof(float) * C * (H + 1));
-    wgrad::tn_plan(static_cast<int>(M), static_cast<int>(C), I, &S_ih, &kper_ih);
-    wgrad::tn_plan(static_cast<int>(M), static_cast<int>(C), H, &S_hh, &kper_hh);
-    const size_t np = std::max(static_cast<size_t>(S_ih) * C * I, static_cast<size_t>(S_hh) * C * H);
+    for (int np = 0; np < 2; ++np)
+      wgrad::tn_plan(static_cast<int>(M), static_cast<int>(C), I, np + 1, &S_ih[np], &kper_ih[np]);
+    for (int np = 0; np < 2; ++np)
+      wgrad::tn_plan(static_cast<int>(M), static_cast<int>(C), H, np + 1, &S_hh[np], &kper_hh[np]);
+    const size_t sih = std::max(S_ih[0], S_ih[1]), shh = std::max(S_hh[0], S_hh[1]);
+    const size_t np = std::max(sih * C * I, shh * C * H);
     part = o; o += al(sizeof(float) * np);
-    gsum = o; o += al(sizeof(float) * 4 * C * static_cast<size_t>(std::max(S_ih, S_hh)));
+    gsum = o; o += al(sizeof(float) * 4 * C * std::max(sih, shh));
     // clustered recurrence (H a multiple of 64)
     const size_t Bpad = (static_cast<size_t>(B) + kBB - 1) / kBB * kBB, G = H / kBcUnits + 1;
     wfrag_cl = o; o += al(sizeof(v4i) * 64 * (H / 16) * KS2);
@@ -825,17 +828,18 @@ int rxmet_lstm_backward_quant(int32_t T, int32_t B, int32_t I, int32_t H,
     // aug_ih[c][i] = s_x sum_m dli[m][c] (x_q - zp_x)[m][i], aug_ih[c][I] = sum_m dli[m][c]
     wgrad::TnArgs ta;
     ta.A = dli; ta.lda = C; ta.Bt = xt; ta.ldb = Mp; ta.bplane = static_cast<int64_t>(I) * Mp;
-    ta.K = M; ta.P = C; ta.Q = I; ta.S = ws.S_ih; ta.kper = ws.kper_ih; ta.part = part;
+    ta.K = M; ta.P = C; ta.Q = I; ta.S = ws.S_ih[npx - 1]; ta.kper = ws.kper_ih[npx - 1];
+    ta.part = part;
     ta.colsum = gsum;
     if (int rc = wgrad::tn(ta, npx, stream)) return rc;
-    if (int rc = wgrad::tn_finish(part, ws.S_ih, C, I, qsc, aug_ih, I + 1, false, gsum, aug_ih + I,
+    if (int rc = wgrad::tn_finish(part, ta.S, C, I, npx, qsc, aug_ih, I + 1, false, gsum, aug_ih + I,
                                   stream))
       return rc;
     // aug_hh[c][j] = s_h sum_m dlh[m][c] (h_prev - zp_h)[m][j], aug_hh[c][H] = sum_m dlh[m][c]
     ta.A = dlh; ta.Bt = ht; ta.bplane = static_cast<int64_t>(H) * Mp;
-    ta.Q = H; ta.S = ws.S_hh; ta.kper = ws.kper_hh;
+    ta.Q = H; ta.S = ws.S_hh[nph - 1]; ta.kper = ws.kper_hh[nph - 1];
     if (int rc = wgrad::tn(ta, nph, stream)) return rc;
-    if (int rc = wgrad::tn_finish(part, ws.S_hh, C, H, qsc + I, aug_hh, H + 1, false, gsum,
+    if (int rc = wgrad::tn_finish(part, ta.S, C, H, nph, qsc + I, aug_hh, H + 1, false, gsum,
                                   aug_hh + H, stream))
       return rc;
   }

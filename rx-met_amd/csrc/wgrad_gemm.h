@@ -44,15 +44,15 @@ struct NtArgs {
 };
 
 // Number of K splits for a TN product (about 512 workgroups) and rows per split.
-void tn_plan(int K, int P, int Q, int *S, int *kper);
+void tn_plan(int K, int P, int Q, int nplanes, int *S, int *kper);
 // Launches; nplanes is 1 or 2.
 int tn(const TnArgs &a, int nplanes, hipStream_t stream);
 int nt(const NtArgs &a, int nplanes, hipStream_t stream);
 // out[p * ldo + q] = qscale[q] * sum_s part[s][p][q] (fixed order; out[q * ldo + p] when
 // transpose); qscale may be null (1).  bias (optional): bias[p * ldo] = the sum of colsum over
 // splits and halves.
-int tn_finish(const float *part, int S, int P, int Q, const float *qscale, float *out, int64_t ldo,
-              bool transpose, const float *colsum, float *bias, hipStream_t stream);
+int tn_finish(const float *part, int S, int P, int Q, int nplanes, const float *qscale, float *out,
+              int64_t ldo, bool transpose, const float *colsum, float *bias, hipStream_t stream);
 
 // Codes as bf16 operand planes, transposed: for r < rows and c < cols,
 //   v = rint((x(r, c) - zp) / div),  x(r, c) = r < rows0 ? src0[r rs + c cs] : src1[(r - rows0) rs + c cs]

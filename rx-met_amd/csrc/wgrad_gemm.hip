@@ -344,14 +344,15 @@ struct TnTile {
   int bq() const { return 32 * wj; }
   int ath() const { return 256 / bp(); }
 };
-static TnTile tn_tile(int Q) {
-  if (Q >= 256) return {4, 8};
+static TnTile tn_tile(int Q, int nplanes) {
+  // two B planes: 128 x 128 at most, so that two waves fit each SIMD
+  if (Q >= 256 && nplanes == 1) return {4, 8};
   if (Q <= 64) return {4, 2};
   return {4, 4};
 }
 
-void tn_plan(int K, int P, int Q, int *S, int *kper) {
-  const TnTile t = tn_tile(Q);
+void tn_plan(int K, int P, int Q, int nplanes, int *S, int *kper) {
+  const TnTile t = tn_tile(Q, nplanes);
   const int tiles = ((P + t.bp() - 1) / t.bp()) * ((Q + t.bq() - 1) / t.bq());
   const int chunks = (K + kKC - 1) / kKC;
   // about 512 workgroups, each at least 32 chunks (fewer, larger partials)
@@ -377,7 +378,7 @@ static void tn_launch(const TnArgs &a, int nplanes, hipStream_t stream) {
 int tn(const TnArgs &a, int nplanes, hipStream_t stream) {
   RXMET_CHECK_ARG(nplanes == 1 || nplanes == 2, "nplanes must be 1 or 2");
   RXMET_CHECK_ARG(a.kper % kKC == 0 && a.ldb % 8 == 0, "bad TN layout");
-  const TnTile t = tn_tile(a.Q);
+  const TnTile t = tn_tile(a.Q, nplanes);
   if (t.wj == 8)
     tn_launch<4, 8>(a, nplanes, stream);
   else if (t.wj == 2)
@@ -403,13 +404,14 @@ int nt(const NtArgs &a, int nplanes, hipStream_t stream) {
   return 0;
 }
 
-int tn_finish(const float *part, int S, int P, int Q, const float *qscale, float *out, int64_t ldo,
-              bool transpose, const float *colsum, float *bias, hipStream_t stream) {
+int tn_finish(const float *part, int S, int P, int Q, int nplanes, const float *qscale, float *out,
+              int64_t ldo, bool transpose, const float *colsum, float *bias, hipStream_t stream) {
   const int64_t n = static_cast<int64_t>(P) * Q + P;
   int64_t blocks = (n + 255) / 256;
   if (blocks > 4096) blocks = 4096;
   hipLaunchKernelGGL(tn_finish_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
-                     part, S, P, Q, qscale, out, ldo, transpose, tn_tile(Q).ath(), colsum, bias);
+                     part, S, P, Q, qscale, out, ldo, transpose, tn_tile(Q, nplanes).ath(), colsum,
+                     bias);
   RXMET_CHECK_LAUNCH();
   return 0;
 }
