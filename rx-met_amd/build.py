@@ -74,7 +74,7 @@ def build(verbose: bool = True) -> Path:
         objs = list(ex.map(_compile, sources))
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs),
-           "-lrocblas", "-Wl,--no-undefined"]
+           "-Wl,--no-undefined"]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{proc.stdout}\n{proc.stderr}")

@@ -121,13 +121,13 @@ __device__ __forceinline__ void store_bytes_coherent(unsigned char *dst4, int by
 
 // Zero `n` words (counters and flags) on the stream; used instead of a memset node so the
 // sequence stays capturable.
-static __global__ void zero_words(unsigned *p, int n) {
+[[maybe_unused]] static __global__ void zero_words(unsigned *p, int n) {
   for (int i = threadIdx.x; i < n; i += blockDim.x) p[i] = 0u;
 }
 
 // A launch whose cluster wait timed out leaves untrustworthy outputs: overwrite `n` floats
 // with NaN when the timeout flag is set (a no-op otherwise).
-static __global__ void poison_nan(const int *timeout, int64_t n, float *p) {
+[[maybe_unused]] static __global__ void poison_nan(const int *timeout, int64_t n, float *p) {
   if (*timeout == 0) return;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)

@@ -20,6 +20,8 @@
 
 #include <cstdint>
 
+#include <hip/hip_runtime.h>
+
 #include "mfma_frag.h"
 
 namespace rxmet {
@@ -157,6 +159,105 @@ inline int b_planes(double lo, double hi) { return (lo >= -128.0 && hi <= 127.0)
 // Ranges the planes can carry: A spans at most 2^16 codes, B is within signed 16 bits.
 inline bool a_fits(double lo, double hi) { return hi - lo <= 65535.0; }
 inline bool b_fits(double lo, double hi) { return lo >= -32768.0 && hi <= 32767.0; }
+
+// ---------------------------------------------------------------------------------
+// Pre-packed variant: both operands prepared once per call (pack_a, pack_b below), so the
+// GEMM streams 16-byte MFMA fragments straight from L2 with no staging.
+//   A planes   : int8 [PA][M][Kp] of v = A - off (low byte first; Kp = K rounded up to 64,
+//                zero beyond K),
+//   B fragments: v4i [PB][N / 16][Kp / 64][64]; lane l of fragment (nt, s) holds
+//                B(64 s + 16 (l / 16) + j, 16 nt + l % 16), j = 0..15 (plane as above),
+//   colsum     : int64 [N], sum over k < K of B(k, n).
+// S(m, n) = sum_k (A - base) B = sum_k (A - off) B + (off - base) colsum(n).
+// ---------------------------------------------------------------------------------
+struct Packed {
+  const int8_t *A;
+  int64_t aplane;   // bytes between A planes (M Kp)
+  int Kp;
+  const v4i *B;
+  int64_t bplane;   // fragments between B planes
+  const long long *colsum;
+  long long corr;   // off - base
+  int M, N;
+};
+
+// Rows m0..m0+15 of one wave against every 16-column tile nt0, nt0 + step, ...; epi(m, n, S)
+// for in-range outputs.
+template <int PA, int PB, typename Epi>
+__device__ __forceinline__ void rows16(const Packed &p, int m0, int nt0, int step, Epi epi) {
+  const int l = threadIdx.x % 64, KS = p.Kp / 64;
+  const int ntiles = (p.N + 15) / 16;
+  const int mrow = m0 + l % 16;
+  const bool rin = mrow < p.M;
+  const int8_t *arow = p.A + static_cast<int64_t>(rin ? mrow : 0) * p.Kp + 16 * (l / 16);
+  constexpr int kMaxKS = 4;  // K <= 256
+  v4i af[PA][kMaxKS];
+#pragma unroll
+  for (int pa = 0; pa < PA; ++pa)
+#pragma unroll
+    for (int s = 0; s < kMaxKS; ++s) {
+      const v4i v = *reinterpret_cast<const v4i *>(arow + pa * p.aplane + 64 * (s < KS ? s : 0));
+      af[pa][s] = (rin && s < KS) ? v : v4i{0, 0, 0, 0};
+    }
+  long long rs[PA][4];
+  if (PB == 2) {
+    const int one = 0x01010101;
+    const v4i ones = {one, one, one, one};
+#pragma unroll
+    for (int pa = 0; pa < PA; ++pa) {
+      v4i acc = {0, 0, 0, 0};
+#pragma unroll
+      for (int s = 0; s < kMaxKS; ++s)
+        if (s < KS) acc = mfma_i8(af[pa][s], ones, acc);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) rs[pa][r] = acc[r];
+    }
+  }
+  for (int nt = nt0; nt < ntiles; nt += step) {
+    v4i acc[PA][PB];
+#pragma unroll
+    for (int pa = 0; pa < PA; ++pa)
+#pragma unroll
+      for (int pb = 0; pb < PB; ++pb) acc[pa][pb] = v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int s = 0; s < kMaxKS; ++s) {
+      if (s >= KS) break;
+      v4i bf[PB];
+#pragma unroll
+      for (int pb = 0; pb < PB; ++pb)
+        bf[pb] = p.B[pb * p.bplane + (static_cast<int64_t>(nt) * KS + s) * 64 + l];
+#pragma unroll
+      for (int pa = 0; pa < PA; ++pa)
+#pragma unroll
+        for (int pb = 0; pb < PB; ++pb) acc[pa][pb] = mfma_i8(af[pa][s], bf[pb], acc[pa][pb]);
+    }
+    const int n = 16 * nt + l % 16;
+    if (n >= p.N) continue;
+    const long long cs = p.corr * p.colsum[n];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = m0 + 4 * (l / 16) + r;
+      if (m >= p.M) continue;
+      long long sum = cs;
+#pragma unroll
+      for (int pa = 0; pa < PA; ++pa) {
+#pragma unroll
+        for (int pb = 0; pb < PB; ++pb)
+          sum += static_cast<long long>(acc[pa][pb][r]) << (8 * (pa + pb));
+        if (PB == 2) sum += (rs[pa][r] << (8 * pa)) * 128;
+      }
+      epi(m, n, sum);
+    }
+  }
+}
+
+// Host launchers (exact_gemm.hip).
+int pack_a(const float *A, int64_t lda, int M, int K, float off, int PA, int8_t *out, int Kp,
+           hipStream_t stream);
+// B(k, n) = B[k sbk + n sbn] (integer codes), PB planes.
+int pack_b(const float *B, int64_t sbk, int64_t sbn, int K, int N, int PB, int Kp, v4i *frag,
+           long long *colsum, hipStream_t stream);
+inline int pad_k(int K) { return (K + 63) / 64 * 64; }
 
 }  // namespace xgemm
 }  // namespace rxmet

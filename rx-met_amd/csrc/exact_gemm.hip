@@ -1,0 +1,97 @@
+// exact_gemm.hip — operand packing for the pre-packed exact GEMM (exact_gemm.h).
+#include "exact_gemm.h"
+
+#include "rxmet_common.h"
+
+namespace rxmet {
+namespace xgemm {
+
+// A planes: four k per thread, written as one 32-bit word per plane.
+__global__ __launch_bounds__(256) void pack_a_kernel(const float *__restrict__ A, int64_t lda, int M,
+                                                     int K, float off, int PA, int8_t *__restrict__ out,
+                                                     int Kp) {
+  const int64_t words = static_cast<int64_t>(M) * (Kp / 4), plane = static_cast<int64_t>(M) * Kp;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t w = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; w < words; w += stride) {
+    const int64_t m = w / (Kp / 4);
+    const int k0 = static_cast<int>(w % (Kp / 4)) * 4;
+    unsigned lo = 0, hi = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int k = k0 + e;
+      const int v = k < K ? static_cast<int>(A[m * lda + k] - off) : 0;
+      if (PA == 1) {
+        lo |= static_cast<unsigned>(v & 255) << (8 * e);
+      } else {
+        const int l8 = ((v + 128) & 255) - 128;
+        lo |= static_cast<unsigned>(l8 & 255) << (8 * e);
+        hi |= static_cast<unsigned>(((v - l8) >> 8) & 255) << (8 * e);
+      }
+    }
+    reinterpret_cast<unsigned *>(out)[w] = lo;
+    if (PA == 2) reinterpret_cast<unsigned *>(out + plane)[w] = hi;
+  }
+}
+
+// B fragments: block (nt, s), lane l packs 16 k of column 16 nt + l % 16; the s == 0 blocks
+// also sum each column exactly.
+__global__ __launch_bounds__(64) void pack_b_kernel(const float *__restrict__ B, int64_t sbk,
+                                                    int64_t sbn, int K, int N, int PB, int Kp,
+                                                    v4i *__restrict__ frag,
+                                                    long long *__restrict__ colsum) {
+  const int l = threadIdx.x, KS = Kp / 64;
+  const int nt = blockIdx.x / KS, s = blockIdx.x % KS;
+  const int n = 16 * nt + l % 16;
+  const int64_t fplane = static_cast<int64_t>((N + 15) / 16) * KS * 64;
+  int w0[4], w1[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    int b0 = 0, b1 = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int k = 64 * s + 16 * (l / 16) + 4 * q + e;
+      const int v = (k < K && n < N) ? static_cast<int>(B[k * sbk + n * sbn]) : 0;
+      if (PB == 1) {
+        b0 |= (v & 255) << (8 * e);
+      } else {
+        b0 |= (((v & 255) - 128) & 255) << (8 * e);
+        b1 |= ((v >> 8) & 255) << (8 * e);
+      }
+    }
+    w0[q] = b0;
+    w1[q] = b1;
+  }
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 64 + l;
+  frag[idx] = v4i{w0[0], w0[1], w0[2], w0[3]};
+  if (PB == 2) frag[fplane + idx] = v4i{w1[0], w1[1], w1[2], w1[3]};
+  if (s == 0 && l < 16 && n < N) {
+    long long sum = 0;
+    for (int k = 0; k < K; ++k) sum += static_cast<long long>(B[k * sbk + n * sbn]);
+    colsum[n] = sum;
+  }
+}
+
+int pack_a(const float *A, int64_t lda, int M, int K, float off, int PA, int8_t *out, int Kp,
+           hipStream_t stream) {
+  RXMET_CHECK_ARG((PA == 1 || PA == 2) && Kp % 64 == 0 && Kp >= K, "bad A packing");
+  const int64_t words = static_cast<int64_t>(M) * (Kp / 4);
+  int64_t blocks = (words + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  hipLaunchKernelGGL(pack_a_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, A,
+                     lda, M, K, off, PA, out, Kp);
+  RXMET_CHECK_LAUNCH();
+  return 0;
+}
+
+int pack_b(const float *B, int64_t sbk, int64_t sbn, int K, int N, int PB, int Kp, v4i *frag,
+           long long *colsum, hipStream_t stream) {
+  RXMET_CHECK_ARG((PB == 1 || PB == 2) && Kp % 64 == 0 && Kp >= K, "bad B packing");
+  const int blocks = ((N + 15) / 16) * (Kp / 64);
+  hipLaunchKernelGGL(pack_b_kernel, dim3(blocks), dim3(64), 0, stream, B, sbk, sbn, K, N, PB, Kp,
+                     frag, colsum);
+  RXMET_CHECK_LAUNCH();
+  return 0;
+}
+
+}  // namespace xgemm
+}  // namespace rxmet

@@ -154,6 +154,16 @@ __global__ __launch_bounds__(256) void code_gemm(xgemm::Operands o, float *__res
                        });
 }
 
+// Pre-packed variant (I <= kPackedMaxK): one wave per 16 rows and every fourth column tile.
+constexpr int kPackedMaxK = 256;
+template <int PA, int PB>
+__global__ __launch_bounds__(256) void code_gemm_packed(xgemm::Packed p, float *__restrict__ Cm) {
+  xgemm::rows16<PA, PB>(p, 16 * blockIdx.x, threadIdx.x / 64, 4,
+                        [&](int m, int n, long long s) {
+                          Cm[static_cast<size_t>(m) * p.N + n] = static_cast<float>(s);
+                        });
+}
+
 template <int PA>
 static void launch_code_gemm(int pb, dim3 grid, hipStream_t stream, const xgemm::Operands &o,
                              float *C) {
@@ -648,10 +658,10 @@ size_t recurrence_lds_bytes(int H, int KS, int npl) {
 
 // Workspace layout of the forward (bytes, 256-aligned pieces).
 struct FwdWorkspace {
-  size_t gih, chan, h0codes, hostblk, rfrag, hx, sync, sparams, total;
+  size_t gih, chan, h0codes, hostblk, rfrag, hx, sync, sparams, xa, bfrag, colsum, total;
   FwdWorkspace(int T, int B, int I, int H) {
-    (void)I;
     const size_t C = 3 * static_cast<size_t>(H);
+    const size_t Kp = static_cast<size_t>(xgemm::pad_k(I));
     auto al = [](size_t x) { return (x + 255) & ~static_cast<size_t>(255); };
     size_t o = 0;
     gih = o; o += al(sizeof(float) * static_cast<size_t>(T) * B * C);
@@ -663,6 +673,11 @@ struct FwdWorkspace {
     hx = o; o += al(2 * 2 * Bpad * H);
     sync = o; o += al(sizeof(unsigned) * (2 * (Bpad / kTileB) + 2));  // clusters of both directions
     sparams = o; o += al(2 * sizeof(StepParams));
+    // packed operands of the input projection (I <= 256): x planes, W fragments, W column sums
+    const size_t ip = static_cast<size_t>(I) <= kPackedMaxK ? 1 : 0;
+    xa = o; o += al(ip * 2 * static_cast<size_t>(T) * B * Kp);
+    bfrag = o; o += al(ip * 2 * C * Kp);
+    colsum = o; o += al(ip * sizeof(long long) * C);
     total = o;
   }
 };
@@ -780,21 +795,41 @@ static int forward_prologue(bool training, int T, int B, int I, int H, const rxm
   const int M = T * B;
   {
     // x codes lie on the x grid, W codes on the (symmetric or not) W grid
-    xgemm::Operands o;
-    o.M = M; o.N = C; o.K = I;
-    o.A = d.x_q; o.lda = I;
     const Bounds bx = bounds_of(g[RXMET_GRU_X].bits, g[RXMET_GRU_X].is_unsigned);
     const double xlo = bx.lo, xhi = bx.hi;
-    o.off = xgemm::a_shift(xlo, xhi);
-    o.corr = static_cast<long long>(o.off);
-    o.B = d.W_q; o.sbk = C; o.sbn = 1;
+    const float off = xgemm::a_shift(xlo, xhi);
     const int pa = xgemm::a_planes(xlo, xhi), pb = xgemm::b_planes(wa.bW.lo, wa.bW.hi);
-    const dim3 grid((C + 63) / 64, (M + 63) / 64);
     rxmet::prof::Scope ps__("gru_fwd_input_gemm", stream);
-    if (pa == 1)
-      launch_code_gemm<1>(pb, grid, stream, o, gih);
-    else
-      launch_code_gemm<2>(pb, grid, stream, o, gih);
+    if (I <= kPackedMaxK) {
+      const int Kp = xgemm::pad_k(I);
+      int8_t *xa = reinterpret_cast<int8_t *>(wsb + ws.xa);
+      v4i *bf = reinterpret_cast<v4i *>(wsb + ws.bfrag);
+      long long *cs = reinterpret_cast<long long *>(wsb + ws.colsum);
+      if (int rc = xgemm::pack_a(d.x_q, I, M, I, off, pa, xa, Kp, stream)) return rc;
+      if (int rc = xgemm::pack_b(d.W_q, C, 1, I, C, pb, Kp, bf, cs, stream)) return rc;
+      xgemm::Packed p;
+      p.A = xa; p.aplane = static_cast<int64_t>(M) * Kp; p.Kp = Kp;
+      p.B = bf; p.bplane = static_cast<int64_t>((C + 15) / 16) * (Kp / 64) * 64;
+      p.colsum = cs; p.corr = static_cast<long long>(off); p.M = M; p.N = C;
+      const dim3 grid((M + 15) / 16);
+      auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, dim3(256), 0, stream, p, gih); };
+      if (pa == 1)
+        pb == 1 ? go(code_gemm_packed<1, 1>) : go(code_gemm_packed<1, 2>);
+      else
+        pb == 1 ? go(code_gemm_packed<2, 1>) : go(code_gemm_packed<2, 2>);
+    } else {
+      xgemm::Operands o;
+      o.M = M; o.N = C; o.K = I;
+      o.A = d.x_q; o.lda = I;
+      o.off = off;
+      o.corr = static_cast<long long>(o.off);
+      o.B = d.W_q; o.sbk = C; o.sbn = 1;
+      const dim3 grid((C + 63) / 64, (M + 63) / 64);
+      if (pa == 1)
+        launch_code_gemm<1>(pb, grid, stream, o, gih);
+      else
+        launch_code_gemm<2>(pb, grid, stream, o, gih);
+    }
   }
   RXMET_CHECK_LAUNCH();
 

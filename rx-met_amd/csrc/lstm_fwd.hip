@@ -246,6 +246,33 @@ __global__ __launch_bounds__(256) void lstm_input_gemm(xgemm::Operands o, int H,
                        });
 }
 
+// Pre-packed variant (I <= kPackedMaxK): one wave per 16 rows and every fourth channel tile,
+// the same input-branch epilogue.
+constexpr int kPackedMaxK = 256;
+template <int PA, int PB>
+__global__ __launch_bounds__(256) void lstm_input_gemm_packed(xgemm::Packed p, int H,
+                                                              const ChanHost *__restrict__ ch,
+                                                              const ChanRun *__restrict__ run,
+                                                              StepParams sp, float *__restrict__ lhs,
+                                                              uint8_t *__restrict__ lin_mask) {
+  const int C = p.N;
+  xgemm::rows16<PA, PB>(p, 16 * blockIdx.x, threadIdx.x / 64, 4, [&](int m, int c, long long s) {
+    const int g = c / H;
+    const float accf = static_cast<float>(s) + run[c].ih_bacc;
+    uint8_t clamped;
+    const float lin = clamp_grid(
+        static_cast<double>(rescale(accf, ch[c].ih_mult, ch[c].ih_shift)) + sp.ih_lin.dzp,
+        sp.ih_lin, clamped);
+    const size_t oi = static_cast<size_t>(m) * C + c;
+    const Rescale tg = g == 0 ? sp.ih_to_gate[0]
+                       : g == 1 ? sp.ih_to_gate[1]
+                       : g == 2 ? sp.ih_to_gate[2]
+                                : sp.ih_to_gate[3];
+    lhs[oi] = rescale(center(lin, sp.ih_lin.zp), tg.mult, tg.shift);
+    if (lin_mask) lin_mask[oi] = clamped;
+  });
+}
+
 // ---------------------------------------------------------------------------------
 // 5. recurrence
 // ---------------------------------------------------------------------------------
@@ -706,7 +733,8 @@ size_t recurrence_lds(int H, int KS, int npl) {
 }
 
 struct FwdWorkspace {
-  size_t chost, run, frag, lhs, xq, wih, whh, bih, bhh, h0q, c0q, hx, sync, lut, total;
+  size_t chost, run, frag, lhs, xq, wih, whh, bih, bhh, h0q, c0q, hx, sync, lut, xa, bfrag, colsum,
+      total;
   FwdWorkspace(int T, int B, int I, int H) {
     const size_t C = 4 * static_cast<size_t>(H), KS = (H + 63) / 64;
     auto al = [](size_t x) { return (x + 255) & ~static_cast<size_t>(255); };
@@ -728,6 +756,12 @@ struct FwdWorkspace {
     hx = o; o += al(2 * 2 * Bpad * H);
     sync = o; o += al(sizeof(unsigned) * (Bpad / 16 + 1));
     lut = o; o += al(sizeof(uint32_t) * 2 * kLutMaxEntries);
+    // packed operands of the input linear (I <= 256): x planes, W_ih fragments, column sums
+    const size_t Kp = static_cast<size_t>(xgemm::pad_k(I));
+    const size_t ip = static_cast<size_t>(I) <= kPackedMaxK ? 1 : 0;
+    xa = o; o += al(ip * 2 * static_cast<size_t>(T) * B * Kp);
+    bfrag = o; o += al(ip * 2 * C * Kp);
+    colsum = o; o += al(ip * sizeof(long long) * C);
     total = o;
   }
 };
@@ -850,27 +884,50 @@ int rxmet_lstm_forward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const f
   const int M = T * B;
   {
     RXMET_CHECK_ARG(xgemm::b_fits(gwi.lo, gwi.hi), "W_ih codes must be signed 16-bit at most");
-    xgemm::Operands o;
-    o.M = M; o.N = C; o.K = I;
-    o.A = xq; o.lda = I;
-    o.off = xgemm::a_shift(sp.x.lo, sp.x.hi);
-    o.corr = static_cast<long long>(o.off) - sp.x.zp;
-    o.B = wih; o.sbk = 1; o.sbn = I;  // W_ih codes [4H][I]
+    const float off = xgemm::a_shift(sp.x.lo, sp.x.hi);
     const int pa = xgemm::a_planes(sp.x.lo, sp.x.hi), pb = xgemm::b_planes(gwi.lo, gwi.hi);
-    const dim3 grid((C + 63) / 64, (M + 63) / 64);
     rxmet::prof::Scope ps__("lstm_fwd_input_gemm", stream);
-    if (pa == 1 && pb == 1)
-      hipLaunchKernelGGL((lstm_input_gemm<1, 1>), grid, dim3(256), 0, stream, o, H, chost, run, sp,
-                         lhs, sv.ih_linear_m);
-    else if (pa == 1)
-      hipLaunchKernelGGL((lstm_input_gemm<1, 2>), grid, dim3(256), 0, stream, o, H, chost, run, sp,
-                         lhs, sv.ih_linear_m);
-    else if (pb == 1)
-      hipLaunchKernelGGL((lstm_input_gemm<2, 1>), grid, dim3(256), 0, stream, o, H, chost, run, sp,
-                         lhs, sv.ih_linear_m);
-    else
-      hipLaunchKernelGGL((lstm_input_gemm<2, 2>), grid, dim3(256), 0, stream, o, H, chost, run, sp,
-                         lhs, sv.ih_linear_m);
+    if (I <= kPackedMaxK) {
+      const int Kp = xgemm::pad_k(I);
+      int8_t *xa = reinterpret_cast<int8_t *>(wsb + ws.xa);
+      v4i *bf = reinterpret_cast<v4i *>(wsb + ws.bfrag);
+      long long *cs = reinterpret_cast<long long *>(wsb + ws.colsum);
+      if (int rc = xgemm::pack_a(xq, I, M, I, off, pa, xa, Kp, stream)) return rc;
+      if (int rc = xgemm::pack_b(wih, 1, I, I, C, pb, Kp, bf, cs, stream)) return rc;
+      xgemm::Packed p;
+      p.A = xa; p.aplane = static_cast<int64_t>(M) * Kp; p.Kp = Kp;
+      p.B = bf; p.bplane = static_cast<int64_t>((C + 15) / 16) * (Kp / 64) * 64;
+      p.colsum = cs; p.corr = static_cast<long long>(off) - sp.x.zp; p.M = M; p.N = C;
+      const dim3 grid((M + 15) / 16);
+      auto go = [&](auto kern) {
+        hipLaunchKernelGGL(kern, grid, dim3(256), 0, stream, p, H, chost, run, sp, lhs,
+                           sv.ih_linear_m);
+      };
+      if (pa == 1)
+        pb == 1 ? go(lstm_input_gemm_packed<1, 1>) : go(lstm_input_gemm_packed<1, 2>);
+      else
+        pb == 1 ? go(lstm_input_gemm_packed<2, 1>) : go(lstm_input_gemm_packed<2, 2>);
+    } else {
+      xgemm::Operands o;
+      o.M = M; o.N = C; o.K = I;
+      o.A = xq; o.lda = I;
+      o.off = off;
+      o.corr = static_cast<long long>(o.off) - sp.x.zp;
+      o.B = wih; o.sbk = 1; o.sbn = I;  // W_ih codes [4H][I]
+      const dim3 grid((C + 63) / 64, (M + 63) / 64);
+      if (pa == 1 && pb == 1)
+        hipLaunchKernelGGL((lstm_input_gemm<1, 1>), grid, dim3(256), 0, stream, o, H, chost, run, sp,
+                           lhs, sv.ih_linear_m);
+      else if (pa == 1)
+        hipLaunchKernelGGL((lstm_input_gemm<1, 2>), grid, dim3(256), 0, stream, o, H, chost, run, sp,
+                           lhs, sv.ih_linear_m);
+      else if (pb == 1)
+        hipLaunchKernelGGL((lstm_input_gemm<2, 1>), grid, dim3(256), 0, stream, o, H, chost, run, sp,
+                           lhs, sv.ih_linear_m);
+      else
+        hipLaunchKernelGGL((lstm_input_gemm<2, 2>), grid, dim3(256), 0, stream, o, H, chost, run, sp,
+                           lhs, sv.ih_linear_m);
+    }
   }
   RXMET_CHECK_LAUNCH();
 
