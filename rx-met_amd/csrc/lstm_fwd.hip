@@ -84,6 +84,25 @@ __device__ __forceinline__ float center(float v, int32_t zp) {
   return static_cast<float>(static_cast<double>(v) - zp);
 }
 
+// Float-domain forms of clamp_grid / center / dequant for grids whose codes lie within
+// +-2^24 (at most 24 bits): every in-range sum or difference of integer-valued floats is then
+// exact in float, a rounded out-of-range sum stays beyond the same endpoint, and the product
+// of a code difference and a float scale is exact in double, so its float rounding equals the
+// fp32 product.  The results equal the double-domain forms bit for bit.
+__device__ __forceinline__ float clamp_grid_f(float v, const Grid &g, uint8_t &clamped) {
+  const float s = v + static_cast<float>(g.zp);
+  clamped = (s < g.flo || s > g.fhi) ? 1 : 0;
+  return s <= g.flo ? g.flo : (s >= g.fhi ? g.fhi : s);
+}
+
+__device__ __forceinline__ float center_f(float v, int32_t zp) { return v - static_cast<float>(zp); }
+
+__device__ __forceinline__ float dequant_f(float q, float s, int32_t zp) {
+  return (q - static_cast<float>(zp)) * s;
+}
+
+inline bool fits_f32(const Grid &g) { return g.lo > -(1 << 24) && g.hi < (1 << 24); }
+
 __device__ __forceinline__ float act_sigmoid(float x) {
   if (x >= 0.0f) {
     const float e = static_cast<float>(exp(-static_cast<double>(x)));
@@ -247,9 +266,10 @@ __global__ __launch_bounds__(256) void lstm_input_gemm(xgemm::Operands o, int H,
 }
 
 // Pre-packed variant (I <= kPackedMaxK): one wave per 16 rows and every fourth channel tile,
-// the same input-branch epilogue.
+// the same input-branch epilogue (in float when the linear grid fits 24 bits, where the float
+// clamp and centring are exact).
 constexpr int kPackedMaxK = 256;
-template <int PA, int PB>
+template <int PA, int PB, bool F32>
 __global__ __launch_bounds__(256) void lstm_input_gemm_packed(xgemm::Packed p, int H,
                                                               const ChanHost *__restrict__ ch,
                                                               const ChanRun *__restrict__ run,
@@ -260,15 +280,16 @@ __global__ __launch_bounds__(256) void lstm_input_gemm_packed(xgemm::Packed p, i
     const int g = c / H;
     const float accf = static_cast<float>(s) + run[c].ih_bacc;
     uint8_t clamped;
-    const float lin = clamp_grid(
-        static_cast<double>(rescale(accf, ch[c].ih_mult, ch[c].ih_shift)) + sp.ih_lin.dzp,
-        sp.ih_lin, clamped);
+    const float r = rescale(accf, ch[c].ih_mult, ch[c].ih_shift);
+    const float lin = F32 ? clamp_grid_f(r, sp.ih_lin, clamped)
+                          : clamp_grid(static_cast<double>(r) + sp.ih_lin.dzp, sp.ih_lin, clamped);
     const size_t oi = static_cast<size_t>(m) * C + c;
     const Rescale tg = g == 0 ? sp.ih_to_gate[0]
                        : g == 1 ? sp.ih_to_gate[1]
                        : g == 2 ? sp.ih_to_gate[2]
                                 : sp.ih_to_gate[3];
-    lhs[oi] = rescale(center(lin, sp.ih_lin.zp), tg.mult, tg.shift);
+    const float cl = F32 ? center_f(lin, sp.ih_lin.zp) : center(lin, sp.ih_lin.zp);
+    lhs[oi] = rescale(cl, tg.mult, tg.shift);
     if (lin_mask) lin_mask[oi] = clamped;
   });
 }
@@ -475,24 +496,6 @@ __global__ __launch_bounds__(256) void lstm_build_act_lut(StepParams sp, ActLut 
   table[i] = (static_cast<uint32_t>(static_cast<int>(v) - lo) << 1) | m;
 }
 
-// Float-domain forms of clamp_grid / center / dequant for grids whose codes lie within
-// +-2^24 (at most 24 bits): every in-range sum or difference of integer-valued floats is then
-// exact in float, a rounded out-of-range sum stays beyond the same endpoint, and the product
-// of a code difference and a float scale is exact in double, so its float rounding equals the
-// fp32 product.  The results equal the double-domain forms bit for bit.
-__device__ __forceinline__ float clamp_grid_f(float v, const Grid &g, uint8_t &clamped) {
-  const float s = v + static_cast<float>(g.zp);
-  clamped = (s < g.flo || s > g.fhi) ? 1 : 0;
-  return s <= g.flo ? g.flo : (s >= g.fhi ? g.fhi : s);
-}
-
-__device__ __forceinline__ float center_f(float v, int32_t zp) { return v - static_cast<float>(zp); }
-
-__device__ __forceinline__ float dequant_f(float q, float s, int32_t zp) {
-  return (q - static_cast<float>(zp)) * s;
-}
-
-inline bool fits_f32(const Grid &g) { return g.lo > -(1 << 24) && g.hi < (1 << 24); }
 
 __device__ __forceinline__ float lut_code(const uint32_t *t, int idx, int out_lo, uint8_t &m) {
   const uint32_t e = t[idx];
@@ -903,10 +906,15 @@ int rxmet_lstm_forward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const f
         hipLaunchKernelGGL(kern, grid, dim3(256), 0, stream, p, H, chost, run, sp, lhs,
                            sv.ih_linear_m);
       };
-      if (pa == 1)
-        pb == 1 ? go(lstm_input_gemm_packed<1, 1>) : go(lstm_input_gemm_packed<1, 2>);
+      const bool f32 = fits_f32(sp.ih_lin);
+      if (pa == 1 && pb == 1)
+        f32 ? go(lstm_input_gemm_packed<1, 1, true>) : go(lstm_input_gemm_packed<1, 1, false>);
+      else if (pa == 1)
+        f32 ? go(lstm_input_gemm_packed<1, 2, true>) : go(lstm_input_gemm_packed<1, 2, false>);
+      else if (pb == 1)
+        f32 ? go(lstm_input_gemm_packed<2, 1, true>) : go(lstm_input_gemm_packed<2, 1, false>);
       else
-        pb == 1 ? go(lstm_input_gemm_packed<2, 1>) : go(lstm_input_gemm_packed<2, 2>);
+        f32 ? go(lstm_input_gemm_packed<2, 2, true>) : go(lstm_input_gemm_packed<2, 2, false>);
     } else {
       xgemm::Operands o;
       o.M = M; o.N = C; o.K = I;
