@@ -181,8 +181,9 @@ struct Packed {
   int M, N;
 };
 
-// Rows m0..m0+15 of one wave against every 16-column tile nt0, nt0 + step, ...; epi(m, n, S)
-// for in-range outputs.
+// Rows m0..m0+15 of one wave against every 16-column tile nt0, nt0 + step, ...; per tile each
+// lane calls epi(m, n, S, rows) with the S of rows m, m + 1, .., m + rows - 1 of its column n
+// (rows <= 4: the in-range ones).
 template <int PA, int PB, typename Epi>
 __device__ __forceinline__ void rows16(const Packed &p, int m0, int nt0, int step, Epi epi) {
   const int l = threadIdx.x % 64, KS = p.Kp / 64;
@@ -234,20 +235,21 @@ __device__ __forceinline__ void rows16(const Packed &p, int m0, int nt0, int ste
     const int n = 16 * nt + l % 16;
     if (n >= p.N) continue;
     const long long cs = p.corr * p.colsum[n];
+    long long sum[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int m = m0 + 4 * (l / 16) + r;
-      if (m >= p.M) continue;
-      long long sum = cs;
+      sum[r] = cs;
 #pragma unroll
       for (int pa = 0; pa < PA; ++pa) {
 #pragma unroll
         for (int pb = 0; pb < PB; ++pb)
-          sum += static_cast<long long>(acc[pa][pb][r]) << (8 * (pa + pb));
-        if (PB == 2) sum += (rs[pa][r] << (8 * pa)) * 128;
+          sum[r] += static_cast<long long>(acc[pa][pb][r]) << (8 * (pa + pb));
+        if (PB == 2) sum[r] += (rs[pa][r] << (8 * pa)) * 128;
       }
-      epi(m, n, sum);
     }
+    const int mfirst = m0 + 4 * (l / 16);
+    const int rows = p.M - mfirst >= 4 ? 4 : p.M - mfirst;
+    if (rows > 0) epi(mfirst, n, sum, rows);
   }
 }
 

@@ -159,8 +159,11 @@ constexpr int kPackedMaxK = 256;
 template <int PA, int PB>
 __global__ __launch_bounds__(256) void code_gemm_packed(xgemm::Packed p, float *__restrict__ Cm) {
   xgemm::rows16<PA, PB>(p, 16 * blockIdx.x, threadIdx.x / 64, 4,
-                        [&](int m, int n, long long s) {
-                          Cm[static_cast<size_t>(m) * p.N + n] = static_cast<float>(s);
+                        [&](int m, int n, const long long *s, int rows) {
+#pragma unroll
+                          for (int r = 0; r < 4; ++r)
+                            if (r < rows)
+                              Cm[static_cast<size_t>(m + r) * p.N + n] = static_cast<float>(s[r]);
                         });
 }
 

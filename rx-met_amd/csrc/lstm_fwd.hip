@@ -276,22 +276,30 @@ __global__ __launch_bounds__(256) void lstm_input_gemm_packed(xgemm::Packed p, i
                                                               StepParams sp, float *__restrict__ lhs,
                                                               uint8_t *__restrict__ lin_mask) {
   const int C = p.N;
-  xgemm::rows16<PA, PB>(p, 16 * blockIdx.x, threadIdx.x / 64, 4, [&](int m, int c, long long s) {
-    const int g = c / H;
-    const float accf = static_cast<float>(s) + run[c].ih_bacc;
-    uint8_t clamped;
-    const float r = rescale(accf, ch[c].ih_mult, ch[c].ih_shift);
-    const float lin = F32 ? clamp_grid_f(r, sp.ih_lin, clamped)
-                          : clamp_grid(static_cast<double>(r) + sp.ih_lin.dzp, sp.ih_lin, clamped);
-    const size_t oi = static_cast<size_t>(m) * C + c;
-    const Rescale tg = g == 0 ? sp.ih_to_gate[0]
-                       : g == 1 ? sp.ih_to_gate[1]
-                       : g == 2 ? sp.ih_to_gate[2]
-                                : sp.ih_to_gate[3];
-    const float cl = F32 ? center_f(lin, sp.ih_lin.zp) : center(lin, sp.ih_lin.zp);
-    lhs[oi] = rescale(cl, tg.mult, tg.shift);
-    if (lin_mask) lin_mask[oi] = clamped;
-  });
+  xgemm::rows16<PA, PB>(
+      p, 16 * blockIdx.x, threadIdx.x / 64, 4, [&](int m, int c, const long long *s, int rows) {
+        // the channel's constants once for its (up to) four rows
+        const int g = c / H;
+        const float bacc = run[c].ih_bacc, mult = ch[c].ih_mult;
+        const int32_t shift = ch[c].ih_shift;
+        const Rescale tg = g == 0 ? sp.ih_to_gate[0]
+                           : g == 1 ? sp.ih_to_gate[1]
+                           : g == 2 ? sp.ih_to_gate[2]
+                                    : sp.ih_to_gate[3];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          if (r >= rows) break;
+          const float accf = static_cast<float>(s[r]) + bacc;
+          uint8_t clamped;
+          const float x = rescale(accf, mult, shift);
+          const float lin = F32 ? clamp_grid_f(x, sp.ih_lin, clamped)
+                                : clamp_grid(static_cast<double>(x) + sp.ih_lin.dzp, sp.ih_lin, clamped);
+          const size_t oi = static_cast<size_t>(m + r) * C + c;
+          const float cl = F32 ? center_f(lin, sp.ih_lin.zp) : center(lin, sp.ih_lin.zp);
+          lhs[oi] = rescale(cl, tg.mult, tg.shift);
+          if (lin_mask) lin_mask[oi] = clamped;
+        }
+      });
 }
 
 // ---------------------------------------------------------------------------------
