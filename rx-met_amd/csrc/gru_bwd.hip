@@ -339,6 +339,34 @@ __device__ __forceinline__ MaskRef mask_ref(const uint8_t *p, const void *fallba
   return p ? MaskRef{p, true} : MaskRef{static_cast<const uint8_t *>(fallback), false};
 }
 
+// The step inputs of one lane (sequence b, unit j) at time t: dh_new, h, the four saved gate
+// values and the 13 mask values (absent masks read 1).
+constexpr int kBwRaw = 19;
+struct BwdMasks {
+  MaskRef h, go, gi, hh, ih;
+};
+__device__ __forceinline__ void bwd_load_step(const BwdArgs &a, const BwdMasks &mk, int t, int b,
+                                              int j, float (&r)[kBwRaw]) {
+  const int H = a.H;
+  const uint32_t BH = static_cast<uint32_t>(a.B) * H;
+  const uint32_t oH = static_cast<uint32_t>(b) * H + j;
+  const uint32_t tH = static_cast<uint32_t>(t) * BH;
+  const uint32_t m = 3u * tH + 3u * static_cast<uint32_t>(b) * H + j;
+  const uint32_t v0 = 4u * tH + 4u * static_cast<uint32_t>(b) * H + j;
+  r[0] = a.dh_new[tH + BH + oH];
+  r[1] = a.h[tH + oH];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) r[2 + q] = a.v[v0 + q * H];
+  r[6] = mk.h.at(tH + oH);
+#pragma unroll
+  for (int gg = 0; gg < 3; ++gg) {
+    r[7 + gg] = mk.go.at(m + gg * H);
+    r[10 + gg] = mk.gi.at(m + gg * H);
+    r[13 + gg] = mk.hh.at(m + gg * H);
+    r[16 + gg] = mk.ih.at(m + gg * H);
+  }
+}
+
 // LDS of the clustered backward: partial sums, bias partials, the staged exchange rows.
 constexpr size_t kBwRedBytes = 16 * 1024, kBwBredBytes = sizeof(double) * 2 * 4 * 16 * 6;
 __host__ __device__ constexpr size_t bwd_cl_lds(int KP) {
@@ -380,52 +408,40 @@ __device__ __forceinline__ void bwd_cl_pair(const BwdArgs &a, const BwdClArgs &c
   double sbw[3] = {0.0, 0.0, 0.0}, sbr[3] = {0.0, 0.0, 0.0};
   const uint32_t BH = static_cast<uint32_t>(B) * H;
   v4f *myred = red + (static_cast<size_t>(utl) * 4 + kq) * 64;
-  const MaskRef mk_h = mask_ref(a.h_m, a.v), mk_go = mask_ref(a.gout_m, a.v),
-                mk_gi = mask_ref(a.gin_m, a.v), mk_hh = mask_ref(a.hh_m, a.v),
-                mk_ih = mask_ref(a.ih_m, a.v);
+  const BwdMasks mk = {mask_ref(a.h_m, a.v), mask_ref(a.gout_m, a.v), mask_ref(a.gin_m, a.v),
+                       mask_ref(a.hh_m, a.v), mask_ref(a.ih_m, a.v)};
 
   {
     const int b0 = tile * kBTile, b = b0 + nr;
     const bool valid = b < B;
     float dhc = 0.0f;
+    // step inputs are loaded one step ahead: the next step's loads are in flight during the
+    // cluster wait
+    float cur[kBwRaw];
+    if (valid) bwd_load_step(a, mk, a.T - 1, b, j, cur);
     for (int t = a.T - 1; t >= 0 && alive; --t) {
       const int par = t & 1;
       float dqv[3] = {0.f, 0.f, 0.f}, dpv[3] = {0.f, 0.f, 0.f};
       uint32_t m = 0;
       float dhl = 0.0f;
       if (valid) {
-        const uint32_t oH = static_cast<uint32_t>(b) * H + j;
-        const uint32_t oC = 3u * static_cast<uint32_t>(b) * H + j;
-        const uint32_t tH = static_cast<uint32_t>(t) * BH;
-        const uint32_t tC = 3u * tH, v0 = 4u * tH + 4u * static_cast<uint32_t>(b) * H + j;
-        m = tC + oC;
-        // every input of the step is loaded before any is used (absent masks read a 1)
-        const float r_dhn = a.dh_new[tH + BH + oH], r_h = a.h[tH + oH];
-        const float z = a.v[v0], rr = a.v[v0 + H], g = a.v[v0 + 2 * H], qg = a.v[v0 + 3 * H];
-        const float hm = mk_h.at(tH + oH);
-        float mgo[3], mgi[3], mhh[3], mih[3];
-#pragma unroll
-        for (int gg = 0; gg < 3; ++gg) {
-          mgo[gg] = mk_go.at(m + gg * H);
-          mgi[gg] = mk_gi.at(m + gg * H);
-          mhh[gg] = mk_hh.at(m + gg * H);
-          mih[gg] = mk_ih.at(m + gg * H);
-        }
-        const float dht = (r_dhn + dhc) * hm;
+        m = 3u * static_cast<uint32_t>(t) * BH + 3u * static_cast<uint32_t>(b) * H + j;
+        const float z = cur[2], rr = cur[3], g = cur[4], qg = cur[5];
+        const float dht = (cur[0] + dhc) * cur[6];
         dhl = z * dht;
         const float dg = (1.0f - z) * dht;
-        const float dz = (r_h - g) * dht;
+        const float dz = (cur[1] - g) * dht;
         float dpg = (1.0f - g * g) * dg;
-        dpg *= mgo[2];
-        dpg *= mgi[2];
+        dpg *= cur[7 + 2];
+        dpg *= cur[10 + 2];
         float dqg = dpg * rr;
         const float dr = dpg * qg;
         float dpr = rr * (1.0f - rr) * dr, dqr = dpr;
         float dpz = z * (1.0f - z) * dz, dqz = dpz;
-        dpz *= mgo[0]; dqz *= mgo[0]; dpr *= mgo[1]; dqr *= mgo[1];
-        dpz *= mgi[0]; dqz *= mgi[0]; dpr *= mgi[1]; dqr *= mgi[1];
-        dqz *= mhh[0]; dqr *= mhh[1]; dqg *= mhh[2];
-        dpz *= mih[0]; dpr *= mih[1]; dpg *= mih[2];
+        dpz *= cur[7]; dqz *= cur[7]; dpr *= cur[8]; dqr *= cur[8];
+        dpz *= cur[10]; dqz *= cur[10]; dpr *= cur[11]; dqr *= cur[11];
+        dqz *= cur[13]; dqr *= cur[14]; dqg *= cur[15];
+        dpz *= cur[16]; dpr *= cur[17]; dpg *= cur[18];
         dpv[0] = dpz; dpv[1] = dpr; dpv[2] = dpg;
         dqv[0] = dqz; dqv[1] = dqr; dqv[2] = dqg;
 #pragma unroll
@@ -449,6 +465,7 @@ __device__ __forceinline__ void bwd_cl_pair(const BwdArgs &a, const BwdClArgs &c
           a.dq[m + gg * H] = dqv[gg];
         }
       }
+      if (valid && t > 0) bwd_load_step(a, mk, t - 1, b, j, cur);
       alive = cluster::wait(counter, epoch * cl.G, cl.timeout);
       if (!alive) break;
       // stage the tile's exchange rows in LDS (all loads in flight; a q past the row re-reads
