@@ -191,6 +191,8 @@ struct RecArgs {
   float *v;                 // [T, B, 4H] dequantised
   uint8_t *ih_m, *hh_m, *gin_m, *gout_m, *h_m;
   int8_t *hx;               // clustered path: [2][NPL][Bpad][H] exchanged h codes
+  int wide_out;             // clustered path: outputs 16-byte aligned (H % 16 == 0), stored
+                            // through the LDS staging area as 16-byte rows
 };
 
 // R_q [H][3H] (fp32 codes) -> int8 B fragments of v_mfma_i32_16x16x64_i8:
@@ -436,6 +438,20 @@ struct ClArgs {
   int *timeout;
 };
 
+// Staged mask bytes of fields f0..f0+ng-1 ([16 rows][13][UW] in LDS) to a mask array
+// [T][B][ng][H] as 16-byte rows; c0 is this thread's first chunk.
+__device__ __forceinline__ void flush_masks(uint8_t *arr, int f0, int ng, const uint8_t *sb, int UW,
+                                            int bq, int b0, int B, int H, int member, size_t stepH,
+                                            int c0, int nthr) {
+  for (int c = c0; c < 16 * ng * bq; c += nthr) {
+    const int row = c / (ng * bq), g = (c / bq) % ng, q = c % bq, bb = b0 + row;
+    if (bb < B)
+      *reinterpret_cast<uint4 *>(arr + ng * (stepH + static_cast<size_t>(bb) * H) + g * H +
+                                 member * UW + 16 * q) =
+          *reinterpret_cast<const uint4 *>(sb + (row * 13 + f0 + g) * UW + 16 * q);
+  }
+}
+
 // One (direction, batch tile) pair of the clustered recurrence, run by one member.
 template <int NPL>
 __device__ __forceinline__ void recurrence_cl_pair(const RecArgs &a, const StepParams &p,
@@ -447,10 +463,16 @@ __device__ __forceinline__ void recurrence_cl_pair(const RecArgs &a, const StepP
   float *lut_f = reinterpret_cast<float *>(smem);               // 3 * 16 * 3 (thr, qb, c)
   int *lut_n = reinterpret_cast<int *>(lut_f + 3 * 16 * 3);     // 3 * 16
   v4i *red = reinterpret_cast<v4i *>(smem + 1024);              // [UT][4][3][NPL][64]
+  // output staging of one step: [16 rows][5][UW] floats (h, the four v fields) and
+  // [16 rows][13][UW] mask bytes (ih, hh, gate in, gate out per gate; h)
+  const int UW = 16 * cl.UT;
+  float *sf = reinterpret_cast<float *>(red + static_cast<size_t>(cl.UT) * 4 * 3 * NPL * 64);
+  uint8_t *sb = reinterpret_cast<uint8_t *>(sf + 16 * 5 * UW);
   const int tid = threadIdx.x, w = tid / 64, l = tid % 64;
   const int utl = w / 4, kq = w % 4;
   const int ut = member * cl.UT + utl;
   const int j = 16 * ut + l % 16;
+  const int jj = 16 * utl + l % 16;  // unit within the member's slice of UW units
   const int nr = 4 * (l / 16) + kq;  // batch row finished by this lane
 
   for (int i = tid; i < 3 * 16; i += blockDim.x) {
@@ -602,10 +624,57 @@ __device__ __forceinline__ void recurrence_cl_pair(const RecArgs &a, const StepP
           cluster::store_bytes_coherent(dst + q * plane_stride,
                                         NPL == 1 ? hcv : (q == 0 ? (hcv & 255) - 128 : hcv >> 8));
       }
+      if (a.wide_out) {
+        float *f = sf + nr * 5 * UW + jj;
+        f[0] = (h2 - p.zp_h) * p.eff_h;
+        if (a.training) {
+          f[UW] = (z - p.zp_zout) * p.eff_zout;
+          f[2 * UW] = (rr - p.zp_rout) * p.eff_rout;
+          f[3 * UW] = (nn - p.zp_nout) * p.eff_nout;
+          f[4 * UW] = (rh[2] - p.zp_rh) * p.eff_rh;
+          uint8_t *m8 = sb + nr * 13 * UW + jj;
+#pragma unroll
+          for (int g = 0; g < 3; ++g) {
+            m8[g * UW] = k_ih[g];
+            m8[(3 + g) * UW] = k_hh[g];
+            m8[(6 + g) * UW] = k_gi[g];
+            m8[(9 + g) * UW] = k_go[g];
+          }
+          m8[12 * UW] = k_h;
+        }
+      }
       // the other members only read the h codes: arrive now, store the outputs while waiting
+      // (the arrival's workgroup barrier also publishes the staged outputs)
       cluster::arrive(counter);
       ++epoch;
-      if (valid) {
+      if (a.wide_out) {
+        // 16-byte rows of the staged outputs, spread over the whole workgroup (each array
+        // in a loop of its own: a pointer chosen per lane would put the arguments in scratch)
+        const size_t stepH = static_cast<size_t>(t) * B * H;
+        const int nthr = blockDim.x, fq = UW / 4;
+        for (int c = tid; c < 16 * fq; c += nthr) {
+          const int row = c / fq, q = c % fq, bb = b0 + row;
+          if (bb < B)
+            *reinterpret_cast<float4 *>(a.hout + stepH + static_cast<size_t>(B + bb) * H +
+                                        member * UW + 4 * q) =
+                *reinterpret_cast<const float4 *>(sf + row * 5 * UW + 4 * q);
+        }
+        if (a.training) {
+          for (int c = (tid + nthr - (16 * fq) % nthr) % nthr; c < 64 * fq; c += nthr) {
+            const int row = c / (4 * fq), fld = (c / fq) % 4, q = c % fq, bb = b0 + row;
+            if (bb < B)
+              *reinterpret_cast<float4 *>(a.v + 4 * (stepH + static_cast<size_t>(bb) * H) +
+                                          fld * H + member * UW + 4 * q) =
+                  *reinterpret_cast<const float4 *>(sf + (row * 5 + 1 + fld) * UW + 4 * q);
+          }
+          const int bq = UW / 16;
+          flush_masks(a.ih_m, 0, 3, sb, UW, bq, b0, B, H, member, stepH, (tid + 0 * 48 * bq) % nthr, nthr);
+          flush_masks(a.hh_m, 3, 3, sb, UW, bq, b0, B, H, member, stepH, (tid + nthr - (48 * bq) % nthr) % nthr, nthr);
+          flush_masks(a.gin_m, 6, 3, sb, UW, bq, b0, B, H, member, stepH, (tid + nthr - (96 * bq) % nthr) % nthr, nthr);
+          flush_masks(a.gout_m, 9, 3, sb, UW, bq, b0, B, H, member, stepH, (tid + nthr - (144 * bq) % nthr) % nthr, nthr);
+          flush_masks(a.h_m, 12, 1, sb, UW, bq, b0, B, H, member, stepH, (tid + nthr - (192 * bq) % nthr) % nthr, nthr);
+        }
+      } else if (valid) {
         const uint32_t stepH = static_cast<uint32_t>(t) * B * H;
         a.hout[stepH + static_cast<uint32_t>(B) * H + oH] = (h2 - p.zp_h) * p.eff_h;
         if (a.training) {
@@ -649,7 +718,8 @@ __global__ __launch_bounds__(512) void recurrence_cl(RecArgs a0, RecArgs a1,
 }
 
 size_t recurrence_cl_lds_bytes(int UT, int npl) {
-  return 1024 + sizeof(v4i) * static_cast<size_t>(UT) * 4 * 3 * npl * 64;
+  return 1024 + sizeof(v4i) * static_cast<size_t>(UT) * 4 * 3 * npl * 64 +
+         static_cast<size_t>(16) * 16 * UT * (5 * sizeof(float) + 13);
 }
 
 
@@ -851,6 +921,14 @@ static int forward_prologue(bool training, int T, int B, int I, int H, const rxm
   ra.ih_m = d.ih_mask; ra.hh_m = d.hh_mask; ra.gin_m = d.gate_in_mask;
   ra.gout_m = d.gate_out_mask; ra.h_m = d.h_mask;
   ra.hx = reinterpret_cast<int8_t *>(wsb + ws.hx);
+  {
+    auto a16 = [](const void *q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; };
+    bool wide = H % 16 == 0 && a16(ra.hout);
+    if (training)
+      wide = wide && a16(ra.v) && a16(ra.ih_m) && a16(ra.hh_m) && a16(ra.gin_m) &&
+             a16(ra.gout_m) && a16(ra.h_m);
+    ra.wide_out = wide ? 1 : 0;
+  }
   plan->wsb = wsb;
   return 0;
 }
