@@ -318,6 +318,7 @@ struct RecArgs {
   // checkpoints (null in inference)
   float *gate_out, *cell, *cell_tanh, *hidden;
   uint8_t *hh_lin_m, *gate_in_m, *gate_out_m, *cell_m, *cell_tanh_m, *hidden_m;
+  int wide_out;  // clustered path: outputs 16-byte aligned, stored as 16-byte rows through LDS
 };
 
 template <int NPL>
@@ -519,6 +520,85 @@ struct ClusterArgs {
   ActLut lut;
 };
 
+// Bits k of sixteen packed mask bytes as sixteen 0/1 bytes.
+__device__ __forceinline__ uint4 mask_bits(const uint4 v, int k) {
+  return make_uint4((v.x >> k) & 0x01010101u, (v.y >> k) & 0x01010101u, (v.z >> k) & 0x01010101u,
+                    (v.w >> k) & 0x01010101u);
+}
+
+// One float array [T, B, H] of the member's 64 units for the tile's 16 rows from the staging
+// rows src ([16][64] in LDS), as 16-byte stores (deq: dequantise h codes on the way).
+__device__ __forceinline__ void flush_rows(float *dst, const float *src, int t, int b0, int B, int H,
+                                           int u0, int c0, int nthr, bool deq, float scale, int32_t zp) {
+  for (int c = c0; c < 16 * 16; c += nthr) {
+    const int row = c / 16, q = c % 16, b = b0 + row;
+    if (b >= B) continue;
+    float4 v = *reinterpret_cast<const float4 *>(src + row * kClUnits + 4 * q);
+    if (deq) {
+      v.x = dequant_f(v.x, scale, zp);
+      v.y = dequant_f(v.y, scale, zp);
+      v.z = dequant_f(v.z, scale, zp);
+      v.w = dequant_f(v.w, scale, zp);
+    }
+    *reinterpret_cast<float4 *>(dst + (static_cast<size_t>(t) * B + b) * H + u0 + 4 * q) = v;
+  }
+}
+
+// Stores of one step's outputs and checkpoints for the member's units, after the arrival:
+// the gate outputs straight from the gate exchange xg, the mask bytes from their packed bits,
+// and the cell-phase values staged through xg once every wave has finished reading it.
+// Every thread of the workgroup calls it; (srow, su) is the lane's first staging row and unit.
+__device__ __forceinline__ void flush_step(const RecArgs &a, const StepParams &sp, int t, int b0,
+                                           int u0, bool train, float *xg, const uint8_t *gm,
+                                           const uint8_t *cm, const float (&hvs)[2],
+                                           const float (&cst)[2], const float (&cts)[2], int srow,
+                                           int su) {
+  const int H = a.H, C = 4 * H, B = a.B, tid = threadIdx.x, nthr = blockDim.x;
+  if (train) {
+    for (int c = tid; c < 4 * 16 * 16; c += nthr) {
+      const int k = c % 4, ut = (c / 4) % 4, row = (c / 16) % 16, g = c / 256, b = b0 + row;
+      if (b >= B) continue;
+      *reinterpret_cast<float4 *>(a.gate_out + (static_cast<size_t>(t) * B + b) * C + g * H + u0 +
+                                  16 * ut + 4 * k) =
+          *reinterpret_cast<const float4 *>(xg + ((ut * 4 + g) * 16 + row) * 16 + 4 * k);
+    }
+    for (int c = (tid + nthr - 256 % nthr) % nthr; c < 4 * 16 * 4; c += nthr) {
+      const int q = c % 4, row = (c / 4) % 16, g = c / 64, b = b0 + row;
+      if (b >= B) continue;
+      const uint4 v = *reinterpret_cast<const uint4 *>(gm + (g * 16 + row) * kClUnits + 16 * q);
+      const size_t o = (static_cast<size_t>(t) * B + b) * C + g * H + u0 + 16 * q;
+      *reinterpret_cast<uint4 *>(a.hh_lin_m + o) = mask_bits(v, 0);
+      *reinterpret_cast<uint4 *>(a.gate_in_m + o) = mask_bits(v, 1);
+      *reinterpret_cast<uint4 *>(a.gate_out_m + o) = mask_bits(v, 2);
+    }
+  }
+  __syncthreads();  // every read of xg is done
+#pragma unroll
+  for (int rr = 0; rr < 2; ++rr) {
+    float *d = xg + (srow + rr) * kClUnits + su;
+    d[0] = hvs[rr];
+    d[16 * kClUnits] = cst[rr];
+    d[32 * kClUnits] = cts[rr];
+  }
+  __syncthreads();
+  flush_rows(a.output, xg, t, b0, B, H, u0, tid, nthr, true, sp.h.scale, sp.h.zp);
+  if (train) {
+    flush_rows(a.hidden, xg, t, b0, B, H, u0, (tid + nthr - 256 % nthr) % nthr, nthr, false, 0.f, 0);
+    flush_rows(a.cell, xg + 16 * kClUnits, t, b0, B, H, u0, tid, nthr, false, 0.f, 0);
+    flush_rows(a.cell_tanh, xg + 32 * kClUnits, t, b0, B, H, u0, (tid + nthr - 256 % nthr) % nthr,
+               nthr, false, 0.f, 0);
+    for (int c = tid; c < 16 * 4; c += nthr) {
+      const int q = c % 4, row = c / 4, b = b0 + row;
+      if (b >= B) continue;
+      const uint4 v = *reinterpret_cast<const uint4 *>(cm + row * kClUnits + 16 * q);
+      const size_t o = (static_cast<size_t>(t) * B + b) * H + u0 + 16 * q;
+      *reinterpret_cast<uint4 *>(a.cell_m + o) = mask_bits(v, 0);
+      *reinterpret_cast<uint4 *>(a.cell_tanh_m + o) = mask_bits(v, 1);
+      *reinterpret_cast<uint4 *>(a.hidden_m + o) = mask_bits(v, 2);
+    }
+  }
+}
+
 template <int NPL>
 __global__ __launch_bounds__(512) void lstm_recurrence_cl(RecArgs a, StepParams sp,
                                                           ClusterArgs cl) {
@@ -526,7 +606,11 @@ __global__ __launch_bounds__(512) void lstm_recurrence_cl(RecArgs a, StepParams 
   const int H = a.H, C = 4 * H, B = a.B, KS = a.KS;
   v4i *wl = reinterpret_cast<v4i *>(smem);                  // [4 gates][4 tiles][KS][64]
   float *xg = reinterpret_cast<float *>(wl + 16 * KS * 64);  // [4 tiles][4 gates][16][16]
-  uint32_t *lut = reinterpret_cast<uint32_t *>(xg + 4 * 4 * 16 * 16);  // [cl.lut.total]
+  // mask bits of a step (bit 0..2): gate phase [4 gates][16][64] (hh linear, gate in, gate out),
+  // cell phase [16][64] (cell, cell tanh, hidden)
+  uint8_t *gm = reinterpret_cast<uint8_t *>(xg + 4 * 4 * 16 * 16);
+  uint8_t *cm = gm + 4 * 16 * kClUnits;
+  uint32_t *lut = reinterpret_cast<uint32_t *>(cm + 16 * kClUnits);  // [cl.lut.total]
   for (int i = threadIdx.x; i < cl.lut.total; i += blockDim.x) lut[i] = cl.lut.table[i];
   const bool gate_lut = cl.lut.n[0] > 0, tanh_lut = cl.lut.tanh_n > 0;
   const int tid = threadIdx.x, w = tid / 64, l = tid % 64;
@@ -647,7 +731,11 @@ __global__ __launch_bounds__(512) void lstm_recurrence_cl(RecArgs a, StepParams 
                                     static_cast<int>(gi) - gin.lo, gout.lo, m_go)
                          : real_act(gi, gin, gout, g == 2, m_go);
             xg[((ut * 4 + g) * 16 + nr) * 16 + l % 16] = go;
-            if (train && valid) {
+            if (a.wide_out) {
+              if (train)
+                gm[(g * 16 + nr) * kClUnits + 16 * ut + l % 16] =
+                    static_cast<uint8_t>(m_hl | (m_gi << 1) | (m_go << 2));
+            } else if (train && valid) {
               a.gate_out[oc + g * H] = go;
               a.hh_lin_m[oc + g * H] = m_hl;
               a.gate_in_m[oc + g * H] = m_gi;
@@ -682,6 +770,9 @@ __global__ __launch_bounds__(512) void lstm_recurrence_cl(RecArgs a, StepParams 
                      : real_act(cn, sp.c, sp.tanh_c, true, mts[rr]);
         const float raw = center_f(gout[3], sp.gout[3].zp) * center_f(cts[rr], sp.tanh_c.zp);
         hvs[rr] = clamp_grid_f(rescale(raw, sp.hidden.mult, sp.hidden.shift), sp.h, mhs[rr]);
+        if (a.wide_out && train)
+          cm[nr * kClUnits + 16 * ut + l % 16] =
+              static_cast<uint8_t>(mcs[rr] | (mts[rr] << 1) | (mhs[rr] << 2));
         const int hc = static_cast<int>(hvs[rr] - a.h_offset);
         unsigned char *dst = reinterpret_cast<unsigned char *>(hout) + static_cast<size_t>(b) * H + j;
 #pragma unroll
@@ -692,6 +783,19 @@ __global__ __launch_bounds__(512) void lstm_recurrence_cl(RecArgs a, StepParams 
       // the other members only read the h codes: arrive, then store outputs while waiting
       cluster::arrive(counter);
       ++epoch;
+      if (a.wide_out) {
+        flush_step(a, sp, t, b0, u0, train, xg, gm, cm, hvs, cst, cts, nrow0 + 2 * gp, 16 * ut + l % 16);
+        if (t == a.T - 1) {
+#pragma unroll
+          for (int rr = 0; rr < 2; ++rr) {
+            const int b = b0 + nrow0 + 2 * gp + rr;
+            if (b >= B) continue;
+            const uint32_t os = static_cast<uint32_t>(b) * H + j;
+            a.h_n[os] = dequant_f(hvs[rr], sp.h.scale, sp.h.zp);
+            a.c_n[os] = dequant_f(cst[rr], sp.c.scale, sp.c.zp);
+          }
+        }
+      } else {
 #pragma unroll
       for (int rr = 0; rr < 2; ++rr) {
         const int b = b0 + nrow0 + 2 * gp + rr;
@@ -713,6 +817,7 @@ __global__ __launch_bounds__(512) void lstm_recurrence_cl(RecArgs a, StepParams 
           a.c_n[os] = dequant_f(cn, sp.c.scale, sp.c.zp);
         }
       }
+      }
       alive = cluster::wait(counter, epoch * cl.G, cl.timeout);
     }
   }
@@ -720,7 +825,7 @@ __global__ __launch_bounds__(512) void lstm_recurrence_cl(RecArgs a, StepParams 
 
 size_t recurrence_cl_lds(int KS, int lut_entries) {
   return sizeof(v4i) * 16 * static_cast<size_t>(KS) * 64 + sizeof(float) * 4 * 4 * 16 * 16 +
-         sizeof(uint32_t) * static_cast<size_t>(lut_entries);
+         5 * 16 * kClUnits + sizeof(uint32_t) * static_cast<size_t>(lut_entries);
 }
 
 // Outputs of a launch whose cluster wait timed out are not trustworthy: overwrite them with NaN.
@@ -954,6 +1059,15 @@ int rxmet_lstm_forward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const f
   ra.gate_out = sv.gate_out; ra.cell = sv.cell; ra.cell_tanh = sv.cell_tanh; ra.hidden = sv.hidden;
   ra.hh_lin_m = sv.hh_linear_m; ra.gate_in_m = sv.gate_in_m; ra.gate_out_m = sv.gate_out_m;
   ra.cell_m = sv.cell_m; ra.cell_tanh_m = sv.cell_tanh_m; ra.hidden_m = sv.hidden_m;
+  {
+    auto a16 = [](const void *q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; };
+    bool wide = H % 16 == 0 && a16(ra.output);
+    if (ra.hidden != nullptr)
+      wide = wide && a16(ra.gate_out) && a16(ra.cell) && a16(ra.cell_tanh) && a16(ra.hidden) &&
+             a16(ra.hh_lin_m) && a16(ra.gate_in_m) && a16(ra.gate_out_m) && a16(ra.cell_m) &&
+             a16(ra.cell_tanh_m) && a16(ra.hidden_m);
+    ra.wide_out = wide ? 1 : 0;
+  }
   bool f32_grids = fits_f32(sp.hh_lin) && fits_f32(sp.c) && fits_f32(sp.tanh_c) && fits_f32(sp.h);
   for (int g = 0; g < 4; ++g) f32_grids = f32_grids && fits_f32(sp.gin[g]) && fits_f32(sp.gout[g]);
   if (H % kClUnits == 0 && f32_grids) {
