@@ -176,7 +176,8 @@ def _gru_kernel_work(B, T, I, H, D=2):
                                "dh GEMM R_deq.dq over T steps, both directions in one clustered "
                                "launch (fp32 MFMA)"),
         "gru_bwd_weight_gemms": (D * 2.0 * M * C * (2 * I + H), FP32_MFMA_PEAK,
-                                 "dx, dW, dR fp32 GEMMs (rocBLAS)"),
+                                 "dx, dW, dR GEMMs (float gradient split into three bf16 "
+                                 "terms against exact bf16 code planes, MFMA)"),
         "gru_fwd_input_gemm": (D * 2.0 * M * C * I, FP32_MFMA_PEAK,
                                "input projection W_q.x_q exact integer GEMM"),
     }
@@ -220,6 +221,42 @@ def _gru_leg(torch, steps: int, warmup: int):
     return res, roof, m, x
 
 
+def _gru_c5_leg(torch, steps: int, warmup: int):
+    """c5 (a parity configuration, timed on request): QuantGRU unidirectional QAT fwd+bwd,
+    B=1024, T=50, I=256, H=1024, 4-bit symmetric per-channel W_ih/W_hh, 16-bit activations
+    and hidden state, power-of-2 scales."""
+    import quant_gru as QG
+
+    dev = torch.device("cuda:0")
+    B, T, I, H = 1024, 50, 256, 1024
+    torch.manual_seed(9)
+    x = torch.randn(T, B, I)
+    m = QG.QuantGRU(I, H)
+    m.set_all_bitwidth(16, is_symmetric=False)
+    m._bitwidth_config.W_ = 4
+    m._bitwidth_config.R_ = 4
+    m.use_po2_scale = True
+    m = m.to(dev)
+    x = x.to(dev)
+    with m.calibration_context():
+        m(x)
+    m.use_quantization = True
+    m.train()
+
+    def step():
+        m.zero_grad(set_to_none=True)
+        out, _ = m(x)
+        out.mean().backward()
+
+    dt, p50, p95, kernels, _ = _timed_steps(torch, step, steps, warmup,
+                                            _gru_kernel_work(B, T, I, H, D=1))
+    _log(f"gru c5: {dt*1e3:.2f} ms/step wall, P50 {p50:.2f} ms, {B/dt:.1f} seq/s")
+    for k, v in sorted(kernels.items(), key=lambda kv: -kv[1]["ms_per_step"]):
+        _log(f"  {k}: {v['ms_per_step']:.3f} ms/step, {v['us_per_launch']:.1f} us/launch")
+    return {"ms_per_step": dt * 1e3, "p50_ms": p50, "seq_per_s": B / dt,
+            "kernels_ms_per_step": {k: round(v["ms_per_step"], 4) for k, v in kernels.items()}}
+
+
 def _lstm_kernel_work(B, T, I, H):
     """Algorithmic FLOPs per step of the instrumented c4 kernels (one direction)."""
     C = 4 * H
@@ -232,7 +269,8 @@ def _lstm_kernel_work(B, T, I, H):
                                 "dh GEMM W_hh_q^T.dgates over T steps (int8 MFMA, 3 planes of "
                                 "22-bit block fixed point) with the fused STE pointwise"),
         "lstm_bwd_weight_gemms": (2.0 * M * C * (2 * I + H), FP32_MFMA_PEAK,
-                                  "dx, dW_ih, dW_hh fp32 GEMMs (rocBLAS)"),
+                                  "dx, dW_ih, dW_hh GEMMs (float gradient split into three "
+                                  "bf16 terms against exact bf16 code planes, MFMA)"),
         "lstm_fwd_input_gemm": (2.0 * M * C * I, FP32_MFMA_PEAK,
                                 "input linear W_ih_q.x_q exact integer GEMM"),
     }
@@ -412,8 +450,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--legs", default="gru,lstm,qdq",
-                    help="comma-separated subset of gru,lstm,qdq (profiling runs); the default "
-                         "record runs all three")
+                    help="comma-separated subset of gru,lstm,qdq,c5 (profiling runs); the "
+                         "default record runs gru, lstm and qdq")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run a plain elementwise copy over MIB MiB (scales HBM byte "
                          "counters in profiling runs)")
@@ -430,13 +468,15 @@ def main() -> int:
     _log(f"device: {torch.cuda.get_device_name(0)}")
     if args.copy_probe:
         _copy_probe(torch, args.copy_probe)
-    gru = roof = lstm = lstm_roof = qdq = qdq_roof = None
+    gru = roof = lstm = lstm_roof = qdq = qdq_roof = c5 = None
     if "gru" in legs:
         gru, roof, m, x = _gru_leg(torch, args.steps, args.warmup)
     if "lstm" in legs:
         lstm, lstm_roof, lm, lx, lg = _lstm_leg(torch, args.steps, args.warmup)
     if "qdq" in legs:
         qdq, qdq_roof = _qdq_leg(torch, args.steps, args.warmup)
+    if "c5" in legs:
+        c5 = _gru_c5_leg(torch, args.steps, args.warmup)
     cpu = cpu_qdq = cpu_lstm = None
     if not args.no_cpu_baseline:
         if gru is not None:
@@ -470,6 +510,7 @@ def main() -> int:
                    "carrier": "fp32 codes; recurrent GEMMs on int8 MFMA"},
         "gru": rnd(gru),
         "lstm": rnd(lstm),
+        **({"gru_c5": rnd(c5)} if c5 is not None else {}),
         "qdq": None if qdq is None else {k: {kk: round(vv, 3) for kk, vv in v.items()}
                                          for k, v in qdq.items()},
         "roofline": roof,

@@ -304,6 +304,7 @@ __global__ __launch_bounds__(512) void bwd_recurrence(BwdArgs a) {
 // (v_mfma_f32_16x16x4_f32), each over a quarter of the 3H channels with its R_q values
 // resident in VGPRs, and add their partial sums through LDS in a fixed order.
 constexpr int kBwMaxKS2 = 12;  // 3H <= 768
+constexpr int kMaxHStepped = 1024;
 
 struct BwdClArgs {
   int ncl, G, UT, ntiles, Bpad, KP, ndir;  // KP = 3H padded to a multiple of 64
@@ -367,6 +368,31 @@ __device__ __forceinline__ void bwd_load_step(const BwdArgs &a, const BwdMasks &
   }
 }
 
+// STE pointwise of one (sequence, unit) at one step: from the step inputs and the carried
+// gradient dhc, the pre-activation gradients dp (input branch) and dq (recurrent branch) of
+// the three gates; returns the part of dh_{t-1} that does not pass through R (z dh_t).
+__device__ __forceinline__ float bwd_point(const float (&cur)[kBwRaw], float dhc, float (&dpv)[3],
+                                           float (&dqv)[3]) {
+  const float z = cur[2], rr = cur[3], g = cur[4], qg = cur[5];
+  const float dht = (cur[0] + dhc) * cur[6];
+  const float dg = (1.0f - z) * dht;
+  const float dz = (cur[1] - g) * dht;
+  float dpg = (1.0f - g * g) * dg;
+  dpg *= cur[7 + 2];
+  dpg *= cur[10 + 2];
+  float dqg = dpg * rr;
+  const float dr = dpg * qg;
+  float dpr = rr * (1.0f - rr) * dr, dqr = dpr;
+  float dpz = z * (1.0f - z) * dz, dqz = dpz;
+  dpz *= cur[7]; dqz *= cur[7]; dpr *= cur[8]; dqr *= cur[8];
+  dpz *= cur[10]; dqz *= cur[10]; dpr *= cur[11]; dqr *= cur[11];
+  dqz *= cur[13]; dqr *= cur[14]; dqg *= cur[15];
+  dpz *= cur[16]; dpr *= cur[17]; dpg *= cur[18];
+  dpv[0] = dpz; dpv[1] = dpr; dpv[2] = dpg;
+  dqv[0] = dqz; dqv[1] = dqr; dqv[2] = dqg;
+  return z * dht;
+}
+
 // LDS of the clustered backward: partial sums, bias partials, the staged exchange rows.
 constexpr size_t kBwRedBytes = 16 * 1024, kBwBredBytes = sizeof(double) * 2 * 4 * 16 * 6;
 __host__ __device__ constexpr size_t bwd_cl_lds(int KP) {
@@ -426,24 +452,7 @@ __device__ __forceinline__ void bwd_cl_pair(const BwdArgs &a, const BwdClArgs &c
       float dhl = 0.0f;
       if (valid) {
         m = 3u * static_cast<uint32_t>(t) * BH + 3u * static_cast<uint32_t>(b) * H + j;
-        const float z = cur[2], rr = cur[3], g = cur[4], qg = cur[5];
-        const float dht = (cur[0] + dhc) * cur[6];
-        dhl = z * dht;
-        const float dg = (1.0f - z) * dht;
-        const float dz = (cur[1] - g) * dht;
-        float dpg = (1.0f - g * g) * dg;
-        dpg *= cur[7 + 2];
-        dpg *= cur[10 + 2];
-        float dqg = dpg * rr;
-        const float dr = dpg * qg;
-        float dpr = rr * (1.0f - rr) * dr, dqr = dpr;
-        float dpz = z * (1.0f - z) * dz, dqz = dpz;
-        dpz *= cur[7]; dqz *= cur[7]; dpr *= cur[8]; dqr *= cur[8];
-        dpz *= cur[10]; dqz *= cur[10]; dpr *= cur[11]; dqr *= cur[11];
-        dqz *= cur[13]; dqr *= cur[14]; dqg *= cur[15];
-        dpz *= cur[16]; dpr *= cur[17]; dpg *= cur[18];
-        dpv[0] = dpz; dpv[1] = dpr; dpv[2] = dpg;
-        dqv[0] = dqz; dqv[1] = dqr; dqv[2] = dqg;
+        dhl = bwd_point(cur, dhc, dpv, dqv);
 #pragma unroll
         for (int gg = 0; gg < 3; ++gg) {
           sbw[gg] += static_cast<double>(dpv[gg] * mbw[gg]);
@@ -559,6 +568,66 @@ __global__ __launch_bounds__(256 * UT) void bwd_recurrence_cl(BwdArgs a0, BwdArg
   }
 }
 
+// ---------------------------------------------------------------------------------
+// stepped backward (H > 256): per step one pointwise launch and one dh GEMM launch
+// ---------------------------------------------------------------------------------
+// Step t: every (sequence, unit) takes dh_c = dhl + gsum of step t + 1 (zero at t = T - 1),
+// stores dp, dq and dhl = z dh_t, and adds its bias terms to the partial sums of its 16-row
+// chunk (bias_partial[chunk][2][3H], each slot owned by one thread, steps in order); the dh
+// GEMM gsum = (dq_t scale_R) R_q^T then runs on the split-bf16 MFMA product (wgrad::nt).
+__global__ __launch_bounds__(256) void bwd_step_point(BwdArgs a, int t, const float *__restrict__ gsum,
+                                                      float *__restrict__ dhl) {
+  const int H = a.H, C = 3 * H, B = a.B;
+  const int j = blockIdx.x * blockDim.x + threadIdx.x, chunk = blockIdx.y;
+  if (j >= H) return;
+  const BwdMasks mk = {mask_ref(a.h_m, a.v), mask_ref(a.gout_m, a.v), mask_ref(a.gin_m, a.v),
+                       mask_ref(a.hh_m, a.v), mask_ref(a.ih_m, a.v)};
+  float mbw[3], mbr[3];
+#pragma unroll
+  for (int g = 0; g < 3; ++g) {
+    mbw[g] = a.bw_m ? static_cast<float>(a.bw_m[g * H + j]) : 1.0f;
+    mbr[g] = a.br_m ? static_cast<float>(a.br_m[g * H + j]) : 1.0f;
+  }
+  double sbw[3] = {0.0, 0.0, 0.0}, sbr[3] = {0.0, 0.0, 0.0};
+  const uint32_t BH = static_cast<uint32_t>(B) * H;
+  for (int r = 0; r < kBTile; ++r) {
+    const int b = chunk * kBTile + r;
+    if (b >= B) break;
+    const uint32_t o = static_cast<uint32_t>(b) * H + j;
+    const float dhc = t == a.T - 1 ? 0.0f : dhl[o] + gsum[o];
+    float cur[kBwRaw];
+    bwd_load_step(a, mk, t, b, j, cur);
+    float dpv[3], dqv[3];
+    dhl[o] = bwd_point(cur, dhc, dpv, dqv);
+    const uint32_t m = 3u * static_cast<uint32_t>(t) * BH + 3u * static_cast<uint32_t>(b) * H + j;
+#pragma unroll
+    for (int g = 0; g < 3; ++g) {
+      a.dp[m + g * H] = dpv[g];
+      a.dq[m + g * H] = dqv[g];
+      sbw[g] += static_cast<double>(dpv[g] * mbw[g]);
+      sbr[g] += static_cast<double>(dqv[g] * mbr[g]);
+    }
+  }
+  double *p = a.bias_partial + static_cast<size_t>(chunk) * 2 * C;
+  const bool first = t == a.T - 1;
+#pragma unroll
+  for (int g = 0; g < 3; ++g) {
+    p[g * H + j] = (first ? 0.0 : p[g * H + j]) + sbw[g];
+    p[C + g * H + j] = (first ? 0.0 : p[C + g * H + j]) + sbr[g];
+  }
+}
+
+// dh0 = (dhl + gsum of step 0) * h0 mask.
+__global__ __launch_bounds__(256) void bwd_step_dh0(int64_t n, const float *__restrict__ dhl,
+                                                    const float *__restrict__ gsum,
+                                                    const uint8_t *__restrict__ h0_m,
+                                                    float *__restrict__ dh0) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float v = dhl[i] + gsum[i];
+  dh0[i] = h0_m ? v * static_cast<float>(h0_m[i]) : v;
+}
+
 __global__ __launch_bounds__(256) void zero_floats(int64_t n, float *p) {
   const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
@@ -602,8 +671,10 @@ size_t bwd_lds_bytes(int KS2) {
 }
 
 struct BwdWorkspace {
-  size_t dp, dq, xt, ht, wb, qsc, rfrag, rowsum, effr, effw, bias, part, xch, rt, sync, total;
+  size_t dp, dq, xt, ht, wb, qsc, rfrag, rowsum, effr, effw, bias, part, xch, rt, sync, rb, gsum,
+      dhl, total;
   int Mp, S_w[2], kper_w[2], S_r[2], kper_r[2];  // K splits by number of B planes
+  int Cp;                                         // 3H rounded up to a multiple of 32
   BwdWorkspace(int T, int B, int I, int H) {
     const size_t C = 3 * static_cast<size_t>(H);
     const size_t KS2 = (C + 63) / 64;
@@ -638,6 +709,11 @@ struct BwdWorkspace {
     xch = o; o += al(sizeof(float) * 2 * Bpad * KS2 * 64);
     rt = o; o += al(sizeof(float) * ((H + 15) / 16) * 4 * 4 * KS2 * 64);
     sync = o; o += al(sizeof(unsigned) * (2 * nwg + 2));  // clusters of both directions
+    // stepped recurrence: R codes as bf16 planes [H][Cp], the dh GEMM output, dhl
+    Cp = static_cast<int>((C + 31) / 32 * 32);
+    rb = o; o += al(sizeof(__bf16) * 2 * H * static_cast<size_t>(Cp));
+    gsum = o; o += al(sizeof(float) * static_cast<size_t>(B) * H);
+    dhl = o; o += al(sizeof(float) * static_cast<size_t>(B) * H);
     total = o;
   }
 };
@@ -802,6 +878,41 @@ static int backward_recurrence_clustered(BwdPlan *plans, int ndir, int T, int B,
   return 1;
 }
 
+// The stepped recurrence of one direction (any H): 2 T launches.
+static int backward_recurrence_stepped(BwdPlan &plan, int T, int B, int I, int H,
+                                       hipStream_t stream) {
+  const int C = 3 * H;
+  const BwdWorkspace ws(T, B, I, H);
+  const rxmet_gru_bwd_dir &d = *plan.d;
+  const Bounds br = bounds_of(d.params->chan_bits[RXMET_GRU_R], d.params->chan_unsigned[RXMET_GRU_R]);
+  const int npr = wgrad::planes_for(br.lo, br.hi, 0.0);
+  __bf16 *rb = reinterpret_cast<__bf16 *>(plan.wsb + ws.rb);
+  float *gsum = reinterpret_cast<float *>(plan.wsb + ws.gsum);
+  float *dhl = reinterpret_cast<float *>(plan.wsb + ws.dhl);
+  // R_q [H][3H] as is: rows are the units (N), the channels c are K
+  if (int rc = wgrad::codes_t(d.R_q, C, nullptr, C, H, 1, C, 0.0f, 1.0f, npr, rb, ws.Cp,
+                              static_cast<int64_t>(H) * ws.Cp, stream))
+    return rc;
+  rxmet::prof::Scope ps__("gru_bwd_recurrence", stream);
+  const dim3 grid((H + 255) / 256, (B + kBTile - 1) / kBTile);
+  wgrad::NtArgs na;
+  na.lda = C;
+  na.kscale = plan.ba.eff_r;
+  na.Bt = rb; na.ldb = ws.Cp; na.bplane = static_cast<int64_t>(H) * ws.Cp;
+  na.M = B; na.N = H; na.K = C; na.out = gsum; na.ldo = H;
+  for (int t = T - 1; t >= 0; --t) {
+    hipLaunchKernelGGL(bwd_step_point, grid, dim3(256), 0, stream, plan.ba, t, gsum, dhl);
+    RXMET_CHECK_LAUNCH();
+    na.A = plan.ba.dq + static_cast<size_t>(t) * B * C;
+    if (int rc = wgrad::nt(na, npr, stream)) return rc;
+  }
+  const int64_t n = static_cast<int64_t>(B) * H;
+  hipLaunchKernelGGL(bwd_step_dh0, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, stream,
+                     n, dhl, gsum, plan.ba.h0_m, plan.ba.dh0);
+  RXMET_CHECK_LAUNCH();
+  return 0;
+}
+
 static int backward_recurrence_tiles(BwdPlan &plan, int B, int H, hipStream_t stream) {
   const int C = 3 * H, KS2 = (C + 63) / 64;
   hipLaunchKernelGGL(pack_rt_frags, dim3((H / 16) * KS2), dim3(64), 0, stream, H, KS2,
@@ -880,18 +991,23 @@ static int backward_dirs(int ndir, int T, int B, int I, int H, const rxmet_gru_b
   RXMET_CHECK_ARG(ndir == 1 || ndir == 2, "ndir must be 1 or 2");
   RXMET_CHECK_ARG(dirs != nullptr, "dirs must be non-null");
   RXMET_CHECK_ARG(T >= 1 && B >= 1 && I >= 1 && H >= 1, "dimensions must be positive");
-  RXMET_CHECK_ARG(H % 16 == 0 && H <= 256,
-                  "hidden_size must be a multiple of 16 and at most 256 for the MFMA recurrence");
+  RXMET_CHECK_ARG(H % 16 == 0 && H <= kMaxHStepped,
+                  "hidden_size must be a multiple of 16 and at most 1024");
   RXMET_CHECK_ARG(static_cast<double>(T + 1) * B * 4 * H < 4294967295.0,
                   "T*B*H too large for the recurrence's 32-bit element offsets");
   BwdPlan plans[2];
   for (int k = 0; k < ndir; ++k)
     if (int rc = backward_prologue(T, B, I, H, dirs[k], stream, &plans[k])) return rc;
-  const int rc = backward_recurrence_clustered(plans, ndir, T, B, I, H, stream);
+  // H > 256 (more R values than the clustered and per-tile kernels keep in registers), or
+  // RXMET_BWD_STEPPED set: one pointwise and one GEMM launch per step
+  const bool stepped = H > 256 || std::getenv("RXMET_BWD_STEPPED") != nullptr;
+  const int rc = stepped ? 0 : backward_recurrence_clustered(plans, ndir, T, B, I, H, stream);
   if (rc < 0) return rc;
   if (rc == 0)
     for (int k = 0; k < ndir; ++k)
-      if (int r = backward_recurrence_tiles(plans[k], B, H, stream)) return r;
+      if (int r = stepped ? backward_recurrence_stepped(plans[k], T, B, I, H, stream)
+                          : backward_recurrence_tiles(plans[k], B, H, stream))
+        return r;
   for (int k = 0; k < ndir; ++k)
     if (int r = backward_epilogue(T, B, I, H, plans[k], stream)) return r;
   return 0;

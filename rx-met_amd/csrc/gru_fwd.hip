@@ -1021,8 +1021,8 @@ static int forward_dirs(int ndir, bool training, int T, int B, int I, int H,
   RXMET_CHECK_ARG(ndir == 1 || ndir == 2, "ndir must be 1 or 2");
   RXMET_CHECK_ARG(dirs != nullptr, "dirs must be non-null");
   RXMET_CHECK_ARG(T >= 1 && B >= 1 && I >= 1 && H >= 1, "dimensions must be positive");
-  RXMET_CHECK_ARG(H % 16 == 0 && H <= kMaxH,
-                  "hidden_size must be a multiple of 16 and at most 256 for the MFMA recurrence");
+  RXMET_CHECK_ARG(H % 16 == 0 && H <= 64 * 4 * kClMaxKPerWave,
+                  "hidden_size must be a multiple of 16 and at most 1024");
   RXMET_CHECK_ARG(static_cast<double>(T + 1) * B * 4 * H < 4294967295.0,
                   "T*B*H too large for the recurrence's 32-bit element offsets");
   FwdPlan plans[2];
@@ -1031,6 +1031,8 @@ static int forward_dirs(int ndir, bool training, int T, int B, int I, int H,
   const int rc = forward_recurrence_clustered(plans, ndir, T, B, I, H, stream);
   if (rc < 0) return rc;
   if (rc == 1) return 0;
+  RXMET_CHECK_ARG(H <= kMaxH,
+                  "hidden_size above 256 needs the clustered recurrence (cooperative launch)");
   for (int k = 0; k < ndir; ++k)
     if (int r = forward_recurrence_tiles(plans[k], B, H, stream)) return r;
   return 0;

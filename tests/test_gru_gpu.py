@@ -71,6 +71,11 @@ def _config(name):
         c.op[A.GRID["h"]].is_unsigned = 1
         c.op[A.GRID["h"]].bits = 12
         return c
+    if name == "c5":  # 4-bit symmetric per-channel W and R, 16-bit activations and h, pot2 scales
+        c = A.set_all_bitwidth(A.default_config(), 16, False)
+        c.chan[0].bits = c.chan[1].bits = 4
+        c.use_pot2 = 1
+        return c
     if name == "16b-r8":  # 16-bit x and W: the input projection needs int64 accumulation
         c = A.set_all_bitwidth(A.default_config(), 16, False)
         c.chan[1].bits = 8
@@ -260,3 +265,85 @@ def test_two_direction_entry_points_equal_single_calls(cuda, shape):
             a, b = a.cpu().numpy(), b.cpu().numpy()
             scale = max(float(np.abs(b).max()), 1e-30)
             np.testing.assert_allclose(a, b, rtol=1e-5, atol=1e-6 * scale, err_msg=f"{d} {name}")
+
+
+@pytest.mark.parametrize("shape", [(3, 20, 24, 1024), (4, 35, 16, 512), (2, 18, 8, 272)])
+def test_large_hidden_forward_backward_match_oracle(cuda, shape):
+    """H above 256 (the c5 hidden size 1024 with its quantisation): the clustered forward
+    (K split over four waves, several batch tiles per cluster) bit for bit, and the stepped
+    backward (pointwise + dh GEMM per step) within 1e-4 of the oracle."""
+    T, B, I, H = shape
+    print(f"[gru large H] shape={shape}", flush=True)
+    W, R, bw, br, x, h0, qp = _case(T, B, I, H, "c5", 11, True)
+    exp_f = GO.forward_quant(W, R, bw, br, x, qp, h0=h0, training=True)
+    fwd = _gpu_forward(cuda, W, R, bw, br, x, h0, qp, True)
+    for name, tensor in zip(NAMES, fwd):
+        np.testing.assert_array_equal(tensor.cpu().numpy(), exp_f[name], err_msg=name)
+    g = np.random.default_rng(12)
+    dh_new = (g.standard_normal((T + 1, B, H)) * 1e-2).astype(f32)
+    exp = GO.backward_quant(exp_f, dh_new, qp)
+    got = _gpu_backward(cuda, fwd, dh_new, qp, T, B, I, H)
+    for name, a in zip(("dx", "dW", "dR", "dbw", "dbr", "dh0"), got):
+        e = exp[name]
+        scale = max(float(np.abs(e).max()), 1e-30)
+        np.testing.assert_allclose(a, e, rtol=1e-4, atol=1e-5 * scale, err_msg=name)
+
+
+@pytest.mark.parametrize("shape,cfg_name", [((3, 40, 8, 96), "c3"), ((4, 33, 5, 48), "16b-act-pot2")])
+def test_stepped_backward_matches_clustered(cuda, shape, cfg_name, monkeypatch):
+    """The stepped backward (forced with RXMET_BWD_STEPPED) against the oracle and the
+    clustered backward within 1e-4, masks and h0 included."""
+    T, B, I, H = shape
+    print(f"[gru bwd stepped] shape={shape} cfg={cfg_name}", flush=True)
+    W, R, bw, br, x, h0, qp = _case(T, B, I, H, cfg_name, 13, True)
+    exp_f = GO.forward_quant(W, R, bw, br, x, qp, h0=h0, training=True)
+    fwd = _gpu_forward(cuda, W, R, bw, br, x, h0, qp, True)
+    g = np.random.default_rng(14)
+    dh_new = (g.standard_normal((T + 1, B, H)) * 1e-2).astype(f32)
+    exp = GO.backward_quant(exp_f, dh_new, qp)
+    clustered = _gpu_backward(cuda, fwd, dh_new, qp, T, B, I, H)
+    monkeypatch.setenv("RXMET_BWD_STEPPED", "1")
+    got = _gpu_backward(cuda, fwd, dh_new, qp, T, B, I, H)
+    for name, a, c in zip(("dx", "dW", "dR", "dbw", "dbr", "dh0"), got, clustered):
+        e = exp[name]
+        scale = max(float(np.abs(e).max()), 1e-30)
+        np.testing.assert_allclose(a, e, rtol=1e-4, atol=1e-5 * scale, err_msg=name)
+        np.testing.assert_allclose(a, c, rtol=1e-4, atol=1e-5 * scale, err_msg=name)
+
+
+def test_c5_full_size_rows_match_oracle(cuda):
+    """c5 at its full size (T=50, B=1024, I=256, H=1024, 4-bit W and R, 16-bit activations and
+    h, pot2): sequences are independent, so the GPU's rows of a sample of sequences equal the
+    oracle run on those sequences alone — forward outputs and masks bit for bit, dx and dh0
+    within 1e-4."""
+    T, B, I, H = 50, 1024, 256, 1024
+    rows = [0, 1, 517, 1023]
+    print(f"[gru c5 full] T={T} B={B} I={I} H={H} rows={rows}", flush=True)
+    W, R, bw, br = _weights(I, H, 21)
+    g = np.random.default_rng(22)
+    x = g.standard_normal((T, B, I)).astype(f32)
+    h0 = (g.standard_normal((B, H)) * 0.4).astype(f32)
+    _, _, stats = GO.forward_calibrate(W, R, bw, br, x[:, rows], h0[rows])
+    qp, _ = GO.make_params(A.make_ranges(stats, H), _config("c5"))
+    fwd = _gpu_forward(cuda, W, R, bw, br, x, h0, qp, True)
+    exp_f = GO.forward_quant(W, R, bw, br, np.ascontiguousarray(x[:, rows]), qp,
+                             h0=np.ascontiguousarray(h0[rows]), training=True)
+    per_seq = {"h": 1, "v": 1, "x_q": 1, "x_mask": 1, "h0_mask": 0}
+    for name, tensor in zip(NAMES, fwd):
+        e = exp_f[name]
+        if e is None:
+            continue
+        axis = per_seq.get(name, 1 if tensor.dim() >= 3 else None)
+        if name in ("W_q", "R_q", "bw_q", "br_q", "W_mask", "R_mask", "bw_mask", "br_mask"):
+            np.testing.assert_array_equal(tensor.cpu().numpy(), e, err_msg=name)
+            continue
+        idx = torch.tensor(rows, device=tensor.device)
+        np.testing.assert_array_equal(tensor.index_select(axis, idx).cpu().numpy(), e, err_msg=name)
+    dh_new = (g.standard_normal((T + 1, B, H)) * 1e-2).astype(f32)
+    got = _gpu_backward(cuda, fwd, dh_new, qp, T, B, I, H)
+    exp = GO.backward_quant(exp_f, np.ascontiguousarray(dh_new[:, rows]), qp)
+    for name, a, axis in (("dx", got[0], 1), ("dh0", got[5], 0)):
+        e = exp[name]
+        scale = max(float(np.abs(e).max()), 1e-30)
+        np.testing.assert_allclose(a.take(rows, axis=axis), e, rtol=1e-4, atol=1e-5 * scale,
+                                   err_msg=name)
