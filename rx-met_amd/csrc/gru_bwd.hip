@@ -305,6 +305,7 @@ __global__ __launch_bounds__(512) void bwd_recurrence(BwdArgs a) {
 // resident in VGPRs, and add their partial sums through LDS in a fixed order.
 constexpr int kBwMaxKS2 = 12;  // 3H <= 768
 constexpr int kMaxHStepped = 1024;
+constexpr int kStepMaxSplit = 8;  // K splits of the stepped dh GEMM
 
 struct BwdClArgs {
   int ncl, G, UT, ntiles, Bpad, KP, ndir;  // KP = 3H padded to a multiple of 64
@@ -575,56 +576,76 @@ __global__ __launch_bounds__(256 * UT) void bwd_recurrence_cl(BwdArgs a0, BwdArg
 // stores dp, dq and dhl = z dh_t, and adds its bias terms to the partial sums of its 16-row
 // chunk (bias_partial[chunk][2][3H], each slot owned by one thread, steps in order); the dh
 // GEMM gsum = (dq_t scale_R) R_q^T then runs on the split-bf16 MFMA product (wgrad::nt).
-__global__ __launch_bounds__(256) void bwd_step_point(BwdArgs a, int t, const float *__restrict__ gsum,
+__global__ __launch_bounds__(256) void bwd_step_point(BwdArgs a, int t, int S,
+                                                      const float *__restrict__ gsum,
                                                       float *__restrict__ dhl) {
+  // block: 64 units x 4 row groups; a 16-row chunk per block (row group y takes rows y + 4 i)
+  __shared__ double red[3][6][64];
   const int H = a.H, C = 3 * H, B = a.B;
-  const int j = blockIdx.x * blockDim.x + threadIdx.x, chunk = blockIdx.y;
-  if (j >= H) return;
+  const int tx = threadIdx.x % 64, ty = threadIdx.x / 64;
+  const int j = blockIdx.x * 64 + tx, chunk = blockIdx.y;
+  const bool on = j < H;
+  const int jj = on ? j : 0;
   const BwdMasks mk = {mask_ref(a.h_m, a.v), mask_ref(a.gout_m, a.v), mask_ref(a.gin_m, a.v),
                        mask_ref(a.hh_m, a.v), mask_ref(a.ih_m, a.v)};
-  float mbw[3], mbr[3];
-#pragma unroll
-  for (int g = 0; g < 3; ++g) {
-    mbw[g] = a.bw_m ? static_cast<float>(a.bw_m[g * H + j]) : 1.0f;
-    mbr[g] = a.br_m ? static_cast<float>(a.br_m[g * H + j]) : 1.0f;
-  }
-  double sbw[3] = {0.0, 0.0, 0.0}, sbr[3] = {0.0, 0.0, 0.0};
+  double sb[6] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
   const uint32_t BH = static_cast<uint32_t>(B) * H;
-  for (int r = 0; r < kBTile; ++r) {
-    const int b = chunk * kBTile + r;
-    if (b >= B) break;
-    const uint32_t o = static_cast<uint32_t>(b) * H + j;
-    const float dhc = t == a.T - 1 ? 0.0f : dhl[o] + gsum[o];
+  const size_t split = static_cast<size_t>(B) * H;
+#pragma unroll
+  for (int i = 0; i < kBTile / 4; ++i) {
+    const int b = chunk * kBTile + ty + 4 * i;
+    if (!on || b >= B) continue;
+    const uint32_t o = static_cast<uint32_t>(b) * H + jj;
+    float dhc = 0.0f;
+    if (t != a.T - 1) {
+      float gs = gsum[o];
+      for (int z = 1; z < S; ++z) gs += gsum[z * split + o];
+      dhc = dhl[o] + gs;
+    }
     float cur[kBwRaw];
-    bwd_load_step(a, mk, t, b, j, cur);
+    bwd_load_step(a, mk, t, b, jj, cur);
     float dpv[3], dqv[3];
     dhl[o] = bwd_point(cur, dhc, dpv, dqv);
-    const uint32_t m = 3u * static_cast<uint32_t>(t) * BH + 3u * static_cast<uint32_t>(b) * H + j;
+    const uint32_t m = 3u * static_cast<uint32_t>(t) * BH + 3u * static_cast<uint32_t>(b) * H + jj;
 #pragma unroll
     for (int g = 0; g < 3; ++g) {
       a.dp[m + g * H] = dpv[g];
       a.dq[m + g * H] = dqv[g];
-      sbw[g] += static_cast<double>(dpv[g] * mbw[g]);
-      sbr[g] += static_cast<double>(dqv[g] * mbr[g]);
+      sb[g] += static_cast<double>(dpv[g]);
+      sb[3 + g] += static_cast<double>(dqv[g]);
     }
   }
-  double *p = a.bias_partial + static_cast<size_t>(chunk) * 2 * C;
-  const bool first = t == a.T - 1;
+  if (ty > 0)
 #pragma unroll
-  for (int g = 0; g < 3; ++g) {
-    p[g * H + j] = (first ? 0.0 : p[g * H + j]) + sbw[g];
-    p[C + g * H + j] = (first ? 0.0 : p[C + g * H + j]) + sbr[g];
+    for (int e = 0; e < 6; ++e) red[ty - 1][e][tx] = sb[e];
+  __syncthreads();
+  if (ty == 0 && on) {
+#pragma unroll
+    for (int k = 0; k < 3; ++k)
+#pragma unroll
+      for (int e = 0; e < 6; ++e) sb[e] += red[k][e][tx];
+    double *p = a.bias_partial + static_cast<size_t>(chunk) * 2 * C;
+    const bool first = t == a.T - 1;
+#pragma unroll
+    for (int g = 0; g < 3; ++g) {
+      const double mw = a.bw_m ? static_cast<double>(a.bw_m[g * H + j]) : 1.0;
+      const double mr = a.br_m ? static_cast<double>(a.br_m[g * H + j]) : 1.0;
+      p[g * H + j] = (first ? 0.0 : p[g * H + j]) + sb[g] * mw;
+      p[C + g * H + j] = (first ? 0.0 : p[C + g * H + j]) + sb[3 + g] * mr;
+    }
   }
 }
 
-// dh0 = (dhl + gsum of step 0) * h0 mask.
-__global__ __launch_bounds__(256) void bwd_step_dh0(int64_t n, const float *__restrict__ dhl,
+// dh0 = (dhl + gsum of step 0) * h0 mask (gsum: S K-split parts summed in order).
+__global__ __launch_bounds__(256) void bwd_step_dh0(int64_t n, int S, const float *__restrict__ dhl,
                                                     const float *__restrict__ gsum,
                                                     const uint8_t *__restrict__ h0_m,
                                                     float *__restrict__ dh0) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= n) return;
-  const float v = dhl[i] + gsum[i];
+  float gs = gsum[i];
+  for (int z = 1; z < S; ++z) gs += gsum[z * n + i];
+  const float v = dhl[i] + gs;
   dh0[i] = h0_m ? v * static_cast<float>(h0_m[i]) : v;
 }
 
@@ -712,7 +733,7 @@ struct BwdWorkspace {
     // stepped recurrence: R codes as bf16 planes [H][Cp], the dh GEMM output, dhl
     Cp = static_cast<int>((C + 31) / 32 * 32);
     rb = o; o += al(sizeof(__bf16) * 2 * H * static_cast<size_t>(Cp));
-    gsum = o; o += al(sizeof(float) * static_cast<size_t>(B) * H);
+    gsum = o; o += al(sizeof(float) * kStepMaxSplit * static_cast<size_t>(B) * H);
     dhl = o; o += al(sizeof(float) * static_cast<size_t>(B) * H);
     total = o;
   }
@@ -894,21 +915,35 @@ static int backward_recurrence_stepped(BwdPlan &plan, int T, int B, int I, int H
                               static_cast<int64_t>(H) * ws.Cp, stream))
     return rc;
   rxmet::prof::Scope ps__("gru_bwd_recurrence", stream);
-  const dim3 grid((H + 255) / 256, (B + kBTile - 1) / kBTile);
+  const dim3 grid((H + 63) / 64, (B + kBTile - 1) / kBTile);
   wgrad::NtArgs na;
   na.lda = C;
   na.kscale = plan.ba.eff_r;
   na.Bt = rb; na.ldb = ws.Cp; na.bplane = static_cast<int64_t>(H) * ws.Cp;
   na.M = B; na.N = H; na.K = C; na.out = gsum; na.ldo = H;
+  // K splits so that the dh GEMM has about 256 workgroups (the parts are summed in order by
+  // the next step's pointwise)
+  {
+    const int wj = H <= 64 ? 2 : H <= 96 ? 3 : 4;
+    const int wgs = ((B + 127) / 128) * ((H + 32 * wj - 1) / (32 * wj));
+    int S = 256 / wgs;
+    S = S < 1 ? 1 : (S > kStepMaxSplit ? kStepMaxSplit : S);
+    int kper = ((C + S - 1) / S + 31) / 32 * 32;
+    while (S > 1 && kper * (S - 1) >= C) --S;
+    na.ksplit = S;
+    na.kper = S > 1 ? kper : C;
+    na.out_split = static_cast<int64_t>(B) * H;
+  }
+  const int S = na.ksplit;
   for (int t = T - 1; t >= 0; --t) {
-    hipLaunchKernelGGL(bwd_step_point, grid, dim3(256), 0, stream, plan.ba, t, gsum, dhl);
+    hipLaunchKernelGGL(bwd_step_point, grid, dim3(256), 0, stream, plan.ba, t, S, gsum, dhl);
     RXMET_CHECK_LAUNCH();
     na.A = plan.ba.dq + static_cast<size_t>(t) * B * C;
     if (int rc = wgrad::nt(na, npr, stream)) return rc;
   }
   const int64_t n = static_cast<int64_t>(B) * H;
   hipLaunchKernelGGL(bwd_step_dh0, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, stream,
-                     n, dhl, gsum, plan.ba.h0_m, plan.ba.dh0);
+                     n, S, dhl, gsum, plan.ba.h0_m, plan.ba.dh0);
   RXMET_CHECK_LAUNCH();
   return 0;
 }

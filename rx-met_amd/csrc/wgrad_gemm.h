@@ -41,6 +41,9 @@ struct NtArgs {
   int M, N, K;
   float *out;
   int64_t ldo;
+  // optional K split: split z sums k in [z kper, min((z + 1) kper, K)) into out + z out_split
+  int ksplit = 1, kper = 0;
+  int64_t out_split = 0;
 };
 
 // Number of K splits for a TN product (about 512 workgroups) and rows per split.

@@ -158,12 +158,16 @@ __global__ __launch_bounds__(256) void nt_kernel(NtArgs a) {
   __shared__ __align__(16) __bf16 As[3][128][kRow];
   __shared__ __align__(16) __bf16 Bs[NPL][BN][kRow];
   const int m0 = 128 * blockIdx.x, n0 = BN * blockIdx.y;
+  // K split blockIdx.z: k in [kz, kz + K), written to out + blockIdx.z * out_split
+  const int kz = blockIdx.z * a.kper, K = min(a.kper, a.K - kz);
+  const float *ks = a.kscale + kz;
+  float *out = a.out + blockIdx.z * a.out_split;
   const int tid = threadIdx.x, w = tid / 64, l = tid % 64;
   const int wm = w / 2, wn = w % 2;
   // staging roles: A row sm, 16 k at 16 sh; B row bn, chunk bc
   const int sm = tid / 2, sh = tid % 2;
   const bool min_ = m0 + sm < a.M;
-  const float *ap = a.A + static_cast<int64_t>(m0 + sm) * a.lda + 16 * sh;
+  const float *ap = a.A + static_cast<int64_t>(m0 + sm) * a.lda + kz + 16 * sh;
   // B chunk e = tid + 256 h: row e / 4, 16-byte chunk e % 4 (rows past N read row 0, zeroed)
   bool bok[BCH], nin[BCH];
   const __bf16 *bp[BCH];
@@ -172,18 +176,18 @@ __global__ __launch_bounds__(256) void nt_kernel(NtArgs a) {
     const int e = tid + 256 * h, bn = e / 4, bc = e % 4;
     bok[h] = e < 4 * BN;
     nin[h] = bok[h] && n0 + bn < a.N;
-    bp[h] = a.Bt + static_cast<int64_t>(nin[h] ? n0 + bn : 0) * a.ldb + 8 * bc;
+    bp[h] = a.Bt + static_cast<int64_t>(nin[h] ? n0 + bn : 0) * a.ldb + kz + 8 * bc;
   }
 
   float4 av[4];
   float4 sv[4];
   int4 bv[NPL][BCH];
   auto load = [&](int k0) {
-    const bool kin = k0 + 16 * sh < a.K;  // K is a multiple of 16
+    const bool kin = k0 + 16 * sh < K;  // K is a multiple of 16
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       av[c] = (min_ && kin) ? *reinterpret_cast<const float4 *>(ap + k0 + 4 * c) : make_float4(0, 0, 0, 0);
-      sv[c] = kin ? *reinterpret_cast<const float4 *>(a.kscale + k0 + 16 * sh + 4 * c) : make_float4(0, 0, 0, 0);
+      sv[c] = kin ? *reinterpret_cast<const float4 *>(ks + k0 + 16 * sh + 4 * c) : make_float4(0, 0, 0, 0);
     }
 #pragma unroll
     for (int pl = 0; pl < NPL; ++pl)
@@ -201,7 +205,7 @@ __global__ __launch_bounds__(256) void nt_kernel(NtArgs a) {
     for (int j = 0; j < WJ; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
   load(0);
-  for (int k0 = 0; k0 < a.K; k0 += kKC) {
+  for (int k0 = 0; k0 < K; k0 += kKC) {
     __syncthreads();
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
@@ -228,7 +232,7 @@ __global__ __launch_bounds__(256) void nt_kernel(NtArgs a) {
         if (bok[h]) *reinterpret_cast<int4 *>(&Bs[pl][e / 4][8 * (e % 4)]) = bv[pl][h];
       }
     __syncthreads();
-    if (k0 + kKC < a.K) load(k0 + kKC);
+    if (k0 + kKC < K) load(k0 + kKC);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       v8bf af[3];
@@ -254,7 +258,7 @@ __global__ __launch_bounds__(256) void nt_kernel(NtArgs a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int m = m0 + 64 * wm + 16 * i + 4 * (l / 16) + r;
-        if (m < a.M && n < a.N) a.out[static_cast<int64_t>(m) * a.ldo + n] = acc[i][j][r];
+        if (m < a.M && n < a.N) out[static_cast<int64_t>(m) * a.ldo + n] = acc[i][j][r];
       }
     }
 }
@@ -392,10 +396,14 @@ int tn(const TnArgs &a, int nplanes, hipStream_t stream) {
 int nt(const NtArgs &a, int nplanes, hipStream_t stream) {
   RXMET_CHECK_ARG(nplanes == 1 || nplanes == 2, "nplanes must be 1 or 2");
   RXMET_CHECK_ARG(a.K % 16 == 0 && a.lda % 4 == 0 && a.ldb % 8 == 0, "bad NT layout");
+  RXMET_CHECK_ARG(a.ksplit >= 1 && (a.ksplit == 1 || (a.kper % 32 == 0 && a.kper * (a.ksplit - 1) < a.K)),
+                  "bad NT K split");
   // one column tile when N <= 128 (64, 96 or 128 wide), else tiles of 128
   const int wj = a.N <= 64 ? 2 : a.N <= 96 ? 3 : 4;
-  const dim3 grid((a.M + 127) / 128, (a.N + 32 * wj - 1) / (32 * wj));
-  auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, dim3(256), 0, stream, a); };
+  const dim3 grid((a.M + 127) / 128, (a.N + 32 * wj - 1) / (32 * wj), a.ksplit);
+  NtArgs b = a;
+  if (b.ksplit == 1) b.kper = b.K;
+  auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, dim3(256), 0, stream, b); };
   if (nplanes == 1)
     wj == 2 ? go(nt_kernel<1, 2>) : wj == 3 ? go(nt_kernel<1, 3>) : go(nt_kernel<1, 4>);
   else
