@@ -189,6 +189,49 @@ int rxmet_gru_forward_quant_dirs(int32_t ndir, int32_t is_training, int32_t T, i
                                  void *stream);
 
 /*
+ * rxmet_gru_forward_quant_dirs with each direction's x read in place from the caller's input.
+ * No counterpart in the reference, whose QuantGRU transposes batch-first input and flips it
+ * for the reverse direction with tensor copies (quant_gru.py:2151-2205, 2270-2288).
+ * x_layout[3 k .. 3 k + 2] = {t stride, b stride, reversed} of direction k in elements (the
+ * feature stride is 1): element (t, b, i) of the direction is x[t' st + b sb + i] with
+ * t' = reversed ? T-1-t : t.  x_q, x_mask and everything else come out as in
+ * rxmet_gru_forward_quant_dirs, in the direction's own [T, B, .] order.  T*B*I < 2^32.
+ */
+int rxmet_gru_forward_quant_dirs_x(int32_t ndir, int32_t is_training, int32_t T, int32_t B,
+                                   int32_t I, int32_t H, const rxmet_gru_fwd_dir *dirs,
+                                   const int64_t *x_layout, void *stream);
+
+/*
+ * Output assembly of a bidirectional layer in one pass; replaces the reference's
+ * torch.cat([out_f, out_r.flip(0)], -1) / torch.cat([hn_f, hn_r]) (quant_gru.py:1402-1432)
+ * and the batch-first transpose after it.  h_f, h_r: [T+1, B, H] of each direction (row 0 = h0);
+ * out element (t, b, k < 2H) at out[t out_st + b out_sb + k] = k < H ? h_f[t+1][b][k] :
+ * h_r[T-t][b][k-H]; h_n [2, B, H] (may be null) = {h_f[T], h_r[T]}.  H, out_st and out_sb
+ * multiples of 4, pointers 16-byte aligned.
+ */
+int rxmet_gru_bidir_assemble(int32_t T, int32_t B, int32_t H, const float *h_f, const float *h_r,
+                             float *out, int64_t out_st, int64_t out_sb, float *h_n, void *stream);
+
+/*
+ * The backward of rxmet_gru_bidir_assemble: writes each direction's dh_new [T+1, B, H]
+ * (row 0 zero) from the output gradient g (element (t, b, k) at g[t g_st + b g_sb + k g_sk],
+ * strides may be zero, g may be null) and the h_n gradient g_hn ([2, B, H] contiguous, may be
+ * null): dh_f[t+1][b][j] = g(t, b, j), dh_r[s+1][b][j] = g(T-1-s, b, H+j), plus g_hn at the last
+ * row.  Replaces the reference's zero-fill and slice copies of the upstream gradient.
+ */
+int rxmet_gru_bidir_split_grad(int32_t T, int32_t B, int32_t H, const float *g, int64_t g_st,
+                               int64_t g_sb, int64_t g_sk, const float *g_hn, float *dh_f,
+                               float *dh_r, void *stream);
+
+/*
+ * Input gradient of a bidirectional layer in the caller's layout: dx[t dx_st + b dx_sb + i] =
+ * dx_f[t][b][i] + dx_r[T-1-t][b][i] (dx_f, dx_r [T, B, I] from the two directions' backward).
+ * Replaces the reference's dx_f + dx_r.flip(0) and the batch-first transpose.
+ */
+int rxmet_gru_bidir_dx(int32_t T, int32_t B, int32_t I, const float *dx_f, const float *dx_r,
+                       float *dx, int64_t dx_st, int64_t dx_sb, void *stream);
+
+/*
  * Quantised backward: backward_quant_float_storage_wrapper
  * (gru_interface_binding.cc:789-920) + quantGRUBackward / BackwardPassQuant::Run
  * (src/gru_backward_gpu_quant.cu:379-493).  Inputs are the forward's outputs; unlike

@@ -117,7 +117,15 @@ __global__ __launch_bounds__(64) void quant_weights(int I, int H, WeightArgs a) 
 // ---------------------------------------------------------------------------------
 // 2. inputs
 // ---------------------------------------------------------------------------------
+// Where x element (t, b, k) of the direction lies in the caller's input: t stride, b stride
+// (elements, k stride 1) and whether the direction reads time reversed.
+struct XLayout {
+  int64_t st, sb;
+  int rev;
+};
+
 __global__ __launch_bounds__(256) void quant_input(int64_t nx, int64_t nh, const float *x,
+                                                   XLayout xl, int T, uint32_t BI, uint32_t I,
                                                    const float *h0, float eff_x, float zp_x,
                                                    Bounds bx, float eff_h, float zp_h, Bounds bh,
                                                    float *xq, uint8_t *xm, float *h0codes,
@@ -127,7 +135,14 @@ __global__ __launch_bounds__(256) void quant_input(int64_t nx, int64_t nh, const
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < nx + nh;
        i += stride) {
     if (i < nx) {
-      xq[i] = clamp_keep(rintf(x[i] / eff_x) + zp_x, bx, keep);
+      // canonical [T, B, I] order of the direction; the source follows the caller's layout
+      int64_t src = i;
+      if (xl.rev || xl.st != static_cast<int64_t>(BI) || xl.sb != static_cast<int64_t>(I)) {
+        const uint32_t ii = static_cast<uint32_t>(i), t = ii / BI, r = ii - t * BI, b = r / I;
+        src = (xl.rev ? T - 1 - static_cast<int>(t) : static_cast<int>(t)) * xl.st + b * xl.sb +
+              (r - b * I);
+      }
+      xq[i] = clamp_keep(rintf(x[src] / eff_x) + zp_x, bx, keep);
       if (xm) xm[i] = keep;
     } else {
       const int64_t j = i - nx;
@@ -781,6 +796,7 @@ struct FwdPlan {
 };
 
 static int forward_prologue(bool training, int T, int B, int I, int H, const rxmet_gru_fwd_dir &d,
+                            const XLayout &xl,
                             hipStream_t stream, FwdPlan *plan) {
   const rxmet_gru_qparams *params = d.params;
   RXMET_CHECK_ARG(params != nullptr, "params must be non-null");
@@ -859,7 +875,9 @@ static int forward_prologue(bool training, int T, int B, int I, int H, const rxm
   {
     rxmet::prof::Scope ps__("gru_fwd_quant_input", stream);
     hipLaunchKernelGGL(quant_input, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, nx,
-                       nh, d.x, d.h0, sp.eff_x, sp.zp_x, sp.x, sp.eff_h, sp.zp_h, sp.h, d.x_q,
+                       nh, d.x, xl, T, static_cast<uint32_t>(static_cast<int64_t>(B) * I),
+                       static_cast<uint32_t>(I), d.h0, sp.eff_x, sp.zp_x, sp.x, sp.eff_h, sp.zp_h,
+                       sp.h, d.x_q,
                        training ? d.x_mask : nullptr, h0codes, training ? d.h0_mask : nullptr,
                        d.h);
   }
@@ -1017,7 +1035,8 @@ static int forward_recurrence_tiles(FwdPlan &plan, int B, int H, hipStream_t str
 }
 
 static int forward_dirs(int ndir, bool training, int T, int B, int I, int H,
-                        const rxmet_gru_fwd_dir *dirs, hipStream_t stream) {
+                        const rxmet_gru_fwd_dir *dirs, const int64_t *x_layout,
+                        hipStream_t stream) {
   RXMET_CHECK_ARG(ndir == 1 || ndir == 2, "ndir must be 1 or 2");
   RXMET_CHECK_ARG(dirs != nullptr, "dirs must be non-null");
   RXMET_CHECK_ARG(T >= 1 && B >= 1 && I >= 1 && H >= 1, "dimensions must be positive");
@@ -1026,8 +1045,15 @@ static int forward_dirs(int ndir, bool training, int T, int B, int I, int H,
   RXMET_CHECK_ARG(static_cast<double>(T + 1) * B * 4 * H < 4294967295.0,
                   "T*B*H too large for the recurrence's 32-bit element offsets");
   FwdPlan plans[2];
-  for (int k = 0; k < ndir; ++k)
-    if (int rc = forward_prologue(training, T, B, I, H, dirs[k], stream, &plans[k])) return rc;
+  for (int k = 0; k < ndir; ++k) {
+    XLayout xl{static_cast<int64_t>(B) * I, I, 0};
+    if (x_layout) {
+      xl = XLayout{x_layout[3 * k], x_layout[3 * k + 1], x_layout[3 * k + 2] != 0 ? 1 : 0};
+      RXMET_CHECK_ARG(static_cast<double>(T) * B * I < 4294967295.0 && xl.st >= 0 && xl.sb >= 0,
+                      "strided x: T*B*I must be below 2^32 and the strides non-negative");
+    }
+    if (int rc = forward_prologue(training, T, B, I, H, dirs[k], xl, stream, &plans[k])) return rc;
+  }
   const int rc = forward_recurrence_clustered(plans, ndir, T, B, I, H, stream);
   if (rc < 0) return rc;
   if (rc == 1) return 0;
@@ -1063,14 +1089,24 @@ int rxmet_gru_forward_quant(int32_t is_training, int32_t T, int32_t B, int32_t I
   const rxmet_gru_fwd_dir d = {W, R, bw, br, x, h0, params, h, v, W_q, R_q, bw_q, br_q, x_q,
                                x_mask, h0_mask, W_mask, R_mask, bw_mask, br_mask, ih_mask,
                                hh_mask, gate_in_mask, gate_out_mask, h_mask, workspace};
-  return forward_dirs(1, is_training != 0, T, B, I, H, &d, static_cast<hipStream_t>(stream_));
+  return forward_dirs(1, is_training != 0, T, B, I, H, &d, nullptr, static_cast<hipStream_t>(stream_));
 }
 
 int rxmet_gru_forward_quant_dirs(int32_t ndir, int32_t is_training, int32_t T, int32_t B,
                                  int32_t I, int32_t H, const rxmet_gru_fwd_dir *dirs,
                                  void *stream_) {
   clear_error();
-  return forward_dirs(ndir, is_training != 0, T, B, I, H, dirs, static_cast<hipStream_t>(stream_));
+  return forward_dirs(ndir, is_training != 0, T, B, I, H, dirs, nullptr,
+                      static_cast<hipStream_t>(stream_));
+}
+
+int rxmet_gru_forward_quant_dirs_x(int32_t ndir, int32_t is_training, int32_t T, int32_t B,
+                                   int32_t I, int32_t H, const rxmet_gru_fwd_dir *dirs,
+                                   const int64_t *x_layout, void *stream_) {
+  clear_error();
+  RXMET_CHECK_ARG(x_layout != nullptr, "x_layout must be non-null");
+  return forward_dirs(ndir, is_training != 0, T, B, I, H, dirs, x_layout,
+                      static_cast<hipStream_t>(stream_));
 }
 
 }  // extern "C"

@@ -301,6 +301,70 @@ def forward_quant_float_storage_dirs(is_training, time_steps, batch_size, input_
     return [m[0] for m in made]
 
 
+def forward_quant_float_storage_dirs_x(is_training, time_steps, batch_size, input_size,
+                                       hidden_size, dirs, x_layouts):
+    """forward_quant_float_storage_dirs with each direction's x read in place
+    (rxmet_gru_forward_quant_dirs_x): ``x_layouts[k]`` = (t stride, b stride, reversed) of
+    direction k's x in elements (feature stride 1)."""
+    T, B, I, H = time_steps, batch_size, input_size, hidden_size
+    for k, d in enumerate(dirs):
+        if d[4].dim() != 3 or d[4].stride(2) != 1:
+            raise RuntimeError(f"x of direction {k} needs a unit feature stride")
+    made = [_forward_dir(is_training, T, B, I, H, *d) for d in dirs]
+    arr = (A.FwdDir * len(made))(*[m[1] for m in made])
+    lay = (ctypes.c_int64 * (3 * len(made)))(*[int(v) for xl in x_layouts for v in xl])
+    _rx.call("rxmet_gru_forward_quant_dirs_x", len(made), int(bool(is_training)), T, B, I, H, arr,
+             lay, _stream(dirs[0][4].device))
+    return [m[0] for m in made]
+
+
+def bidir_assemble(h_f, h_r, batch_first: bool):
+    """(output, h_n) of a bidirectional layer from both directions' h [T+1, B, H]
+    (rxmet_gru_bidir_assemble): output [T, B, 2H], or [B, T, 2H] when batch_first."""
+    T1, B, H = h_f.shape
+    T = T1 - 1
+    shape = (B, T, 2 * H) if batch_first else (T, B, 2 * H)
+    out = torch.empty(shape, dtype=torch.float32, device=h_f.device)
+    h_n = torch.empty((2, B, H), dtype=torch.float32, device=h_f.device)
+    st, sb = (out.stride(1), out.stride(0)) if batch_first else (out.stride(0), out.stride(1))
+    _rx.call("rxmet_gru_bidir_assemble", T, B, H, h_f.data_ptr(), h_r.data_ptr(), out.data_ptr(),
+             st, sb, h_n.data_ptr(), _stream(h_f.device))
+    return out, h_n
+
+
+def bidir_split_grad(g_out, g_hn, T, B, H, batch_first: bool, device):
+    """Each direction's dh_new [T+1, B, H] from the output gradient (any strides, or None)
+    and the h_n gradient (rxmet_gru_bidir_split_grad)."""
+    f32 = dict(dtype=torch.float32, device=device)
+    dh_f, dh_r = torch.empty((T + 1, B, H), **f32), torch.empty((T + 1, B, H), **f32)
+    gp, st, sb, sk = None, 0, 0, 0
+    if g_out is not None:
+        _check_f32_cuda("grad_output", g_out)
+        gp = g_out.data_ptr()
+        st, sb = (g_out.stride(1), g_out.stride(0)) if batch_first else (g_out.stride(0),
+                                                                          g_out.stride(1))
+        sk = g_out.stride(2)
+    hp = None
+    if g_hn is not None and g_hn.numel() > 0:
+        _check_f32_cuda("grad_h_n", g_hn)
+        g_hn = g_hn.contiguous()
+        hp = g_hn.data_ptr()
+    _rx.call("rxmet_gru_bidir_split_grad", T, B, H, gp, st, sb, sk, hp, dh_f.data_ptr(),
+             dh_r.data_ptr(), _stream(device))
+    return dh_f, dh_r, g_hn
+
+
+def bidir_dx(dx_f, dx_r, batch_first: bool):
+    """Input gradient of a bidirectional layer in the caller's layout (rxmet_gru_bidir_dx)."""
+    T, B, I = dx_f.shape
+    shape = (B, T, I) if batch_first else (T, B, I)
+    dx = torch.empty(shape, dtype=torch.float32, device=dx_f.device)
+    st, sb = (dx.stride(1), dx.stride(0)) if batch_first else (dx.stride(0), dx.stride(1))
+    _rx.call("rxmet_gru_bidir_dx", T, B, I, dx_f.data_ptr(), dx_r.data_ptr(), dx.data_ptr(), st, sb,
+             _stream(dx_f.device))
+    return dx
+
+
 def _backward_dir(T, B, I, H, W_q, R_q, bw_q, br_q, x_q, dh_new, h, v, quant_params, masks):
     C = 3 * H
     dev = x_q.device

@@ -222,27 +222,40 @@ class GRUFunction(torch.autograd.Function):
 
 class GRUBidirectionalFunction(torch.autograd.Function):
     """Both directions of a quantised bidirectional GRU, equal to two GRUFunction applications
-    on (input, input.flip(0)) (quant_gru.py:2270-2288), with each direction pair of
-    recurrences launched together (forward_quant_float_storage_dirs /
-    backward_quant_float_storage_dirs) so the two directions' sequential steps overlap."""
+    on (input, input.flip(0)) followed by the output concatenation (quant_gru.py:2270-2288,
+    1402-1432), with the layout work done by the library instead of tensor copies: each
+    direction reads its x in place from the caller's input (batch-first or not, the reverse
+    direction time-reversed), one kernel assembles output and h_n in the caller's layout, and
+    the backward splits the output gradient and assembles dx the same way.  Each direction
+    pair of recurrences is one launch (forward_quant_float_storage_dirs_x /
+    backward_quant_float_storage_dirs), so the two directions' sequential steps overlap.
+    Returns (output, h_n)."""
 
     @staticmethod
     def forward(ctx, input, wi_f, wh_f, bi_f, bh_f, h0_f, wi_r, wh_r, bi_r, bh_r, h0_r, is_training,
-                qp_f, qp_r):
-        T, B, I = input.shape
+                qp_f, qp_r, batch_first):
+        device = _require_device(input)
+        x = ensure_cuda_float32(input, device)
+        if x.stride(2) != 1:
+            x = x.contiguous()
+        if batch_first:
+            B, T, I = x.shape
+            st, sb = x.stride(1), x.stride(0)
+        else:
+            T, B, I = x.shape
+            st, sb = x.stride(0), x.stride(1)
         H = wh_f.shape[1]
         ctx.dims = (T, B, I, H)
-        device = _require_device(input)
-        x_f = ensure_cuda_float32(input, device).contiguous()
-        x_r = x_f.flip(0).contiguous()
+        ctx.batch_first = bool(batch_first)
         dirs = []
-        for (wi, wh, bi, bh, h0, qp, x) in ((wi_f, wh_f, bi_f, bh_f, h0_f, qp_f, x_f),
-                                           (wi_r, wh_r, bi_r, bh_r, h0_r, qp_r, x_r)):
+        for (wi, wh, bi, bh, h0, qp) in ((wi_f, wh_f, bi_f, bh_f, h0_f, qp_f),
+                                         (wi_r, wh_r, bi_r, bh_r, h0_r, qp_r)):
             W, R, bw, br = convert_weights_to_haste_format(wi, wh, bi, bh, H, device)
             h0_t = (ensure_cuda_float32(h0, device).contiguous() if h0 is not None
                     else torch.empty(0, device=device, dtype=torch.float32))
             dirs.append((W, R, bw, br, x, h0_t, qp))
-        outs = gru_ops.forward_quant_float_storage_dirs(is_training, T, B, I, H, dirs)
+        outs = gru_ops.forward_quant_float_storage_dirs_x(is_training, T, B, I, H, dirs,
+                                                          [(st, sb, 0), (st, sb, 1)])
         ctx.bias_none = (bi_f is None, bh_f is None)
         ctx.h0_none = (h0_f is None, h0_r is None)
         ctx.quant_params = (qp_f, qp_r)
@@ -252,26 +265,22 @@ class GRUBidirectionalFunction(torch.autograd.Function):
             for o in outs:
                 saved += [o[2], o[3], o[4], o[5], o[6], o[0], o[1], *o[7:]]
             ctx.save_for_backward(*saved)
-        (h_f, h_r) = (outs[0][0], outs[1][0])
-        return h_f[1:], h_f[-1:], h_r[1:], h_r[-1:]
+        return gru_ops.bidir_assemble(outs[0][0], outs[1][0], ctx.batch_first)
 
     @staticmethod
-    def backward(ctx, g_out_f, g_hn_f, g_out_r, g_hn_r):
+    def backward(ctx, g_out, g_hn):
         if not ctx.saved_state:
             raise RuntimeError("QuantGRU forward ran without saving backward state (no_grad "
                                "eval); rerun it with gradients enabled")
         T, B, I, H = ctx.dims
         saved = ctx.saved_tensors
         n = len(saved) // 2
+        dh_f, dh_r, _ = gru_ops.bidir_split_grad(g_out, g_hn, T, B, H, ctx.batch_first,
+                                                 saved[5].device)
         dirs = []
-        for k, (g_out, g_hn) in enumerate(((g_out_f, g_hn_f), (g_out_r, g_hn_r))):
+        for k, dh_new in enumerate((dh_f, dh_r)):
             W_q, R_q, bw_q, br_q, x_q, h, v = saved[k * n:k * n + 7]
             masks = saved[k * n + 7:(k + 1) * n]
-            dh_new = torch.zeros((T + 1, B, H), device=h.device, dtype=torch.float32)
-            if g_out is not None:
-                dh_new[1:] = g_out
-            if g_hn is not None and g_hn.numel() > 0:
-                dh_new[-1] += g_hn[0]
             dirs.append((W_q, R_q, bw_q, br_q, x_q, dh_new, h, v, ctx.quant_params[k], masks))
         res = gru_ops.backward_quant_float_storage_dirs(T, B, I, H, dirs)
         grads = []
@@ -281,8 +290,8 @@ class GRUBidirectionalFunction(torch.autograd.Function):
                           None if ctx.bias_none[0] else reorder_weights_haste_to_pytorch(dbw),
                           None if ctx.bias_none[1] else reorder_weights_haste_to_pytorch(dbr),
                           None if ctx.h0_none[k] else dh))
-        dx = res[0][0] + res[1][0].flip(0)
-        return (dx, *grads[0], *grads[1], None, None, None)
+        dx = gru_ops.bidir_dx(res[0][0], res[1][0], ctx.batch_first)
+        return (dx, *grads[0], *grads[1], None, None, None, None)
 
 
 # ------------------------------------------------------------------------------------
@@ -632,19 +641,8 @@ class QuantGRU(nn.Module):
         device = _require_device(input)
         input = ensure_cuda_float32(input, device)
         h0f, h0r = self._parse_initial_state(hx, B)
-        # gate values and masks are kept whenever a backward may follow (quant_gru.py:2258-2263)
-        save_state = self.training or (torch.is_grad_enabled() and (
-            input.requires_grad or (hx is not None and hx.requires_grad)
-            or any(p.requires_grad for p in self.parameters())))
+        save_state = self._save_state(input, hx)
         b = self.bias
-        if self.bidirectional and self.use_quantization and self.quant_storage_dtype == "float32":
-            out_f, hn_f, out_r, hn_r = GRUBidirectionalFunction.apply(
-                input, self.weight_ih_l0, self.weight_hh_l0, self.bias_ih_l0 if b else None,
-                self.bias_hh_l0 if b else None, h0f, self.weight_ih_l0_reverse,
-                self.weight_hh_l0_reverse, self.bias_ih_l0_reverse if b else None,
-                self.bias_hh_l0_reverse if b else None, h0r, save_state, self.quant_params,
-                self.quant_params_reverse)
-            return self._combine_bidirectional_outputs(out_f, hn_f, out_r.flip(0), hn_r)
         out_f, hn_f = GRUFunction.apply(
             input, self.weight_ih_l0, self.weight_hh_l0, self.bias_ih_l0 if b else None,
             self.bias_hh_l0 if b else None, h0f, save_state, self.use_quantization,
@@ -659,12 +657,38 @@ class QuantGRU(nn.Module):
             out_r = out_r.flip(0)
         return self._combine_bidirectional_outputs(out_f, hn_f, out_r, hn_r)
 
+    def _save_state(self, input, hx) -> bool:
+        """Gate values and masks are kept whenever a backward may follow
+        (quant_gru.py:2258-2263)."""
+        return self.training or (torch.is_grad_enabled() and (
+            input.requires_grad or (hx is not None and hx.requires_grad)
+            or any(p.requires_grad for p in self.parameters())))
+
+    def _forward_bidirectional(self, input, hx=None):
+        """Quantised bidirectional forward on the caller's layout (GRUBidirectionalFunction):
+        no transposes, flips or concatenations outside the library."""
+        self._resolve_quant_params()
+        device = _require_device(input)
+        B = input.shape[0] if self.batch_first else input.shape[1]
+        h0f, h0r = self._parse_initial_state(hx, B)
+        b = self.bias
+        return GRUBidirectionalFunction.apply(
+            ensure_cuda_float32(input, device), self.weight_ih_l0, self.weight_hh_l0,
+            self.bias_ih_l0 if b else None, self.bias_hh_l0 if b else None, h0f,
+            self.weight_ih_l0_reverse, self.weight_hh_l0_reverse,
+            self.bias_ih_l0_reverse if b else None, self.bias_hh_l0_reverse if b else None, h0r,
+            self._save_state(input, hx), self.quant_params, self.quant_params_reverse,
+            self.batch_first)
+
     def forward(self, input: torch.Tensor, hx: Optional[torch.Tensor] = None
                 ) -> Tuple[torch.Tensor, torch.Tensor]:
         """input [T,B,I] or [B,T,I] (batch_first); hx [D,B,H].  Returns (output [.., D*H],
         h_n [D,B,H]) (quant_gru.py:2151-2205)."""
         if self.export_mode:
             raise NotImplementedError("ONNX export mode is not provided by the MI355X build")
+        if (not self.calibrating and self.bidirectional and self.use_quantization
+                and self.quant_storage_dtype == "float32"):
+            return self._forward_bidirectional(input, hx)
         if self.batch_first:
             input = input.transpose(0, 1).contiguous()
         if self.calibrating:

@@ -62,6 +62,7 @@ class PwlLut(ctypes.Structure):
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32
+_i64 = ctypes.c_int64
 
 FWD_DIR_FIELDS = ("W", "R", "bw", "br", "x", "h0", "params", "h", "v", "W_q", "R_q", "bw_q",
                   "br_q", "x_q", "x_mask", "h0_mask", "W_mask", "R_mask", "bw_mask", "br_mask",
@@ -98,6 +99,10 @@ _SIGS = {
     "rxmet_gru_backward_quant_dirs": (ctypes.c_int, [_i32] * 5 + [ctypes.POINTER(BwdDir), _p]),
     "rxmet_gru_forward_calibrate": (ctypes.c_int, [_i32, _i32, _i32, _i32] + [_p] * 9 + [_p, _p]),
     "rxmet_gru_forward_fp": (ctypes.c_int, [_i32] * 5 + [_p] * 8 + [_p]),
+    "rxmet_gru_forward_quant_dirs_x": (ctypes.c_int, [_i32] * 6 + [ctypes.POINTER(FwdDir), _p, _p]),
+    "rxmet_gru_bidir_assemble": (ctypes.c_int, [_i32] * 3 + [_p] * 3 + [_i64, _i64, _p, _p]),
+    "rxmet_gru_bidir_split_grad": (ctypes.c_int, [_i32] * 3 + [_p, _i64, _i64, _i64] + [_p] * 4),
+    "rxmet_gru_bidir_dx": (ctypes.c_int, [_i32] * 3 + [_p] * 3 + [_i64, _i64, _p]),
 }
 for _name, (_res, _args) in _SIGS.items():
     _rx.register(_name, _res, _args)

@@ -267,3 +267,46 @@ def test_float_forward_matches_nn_gru_and_refuses_backward(cuda):
     y, _ = m(x.to(cuda))
     with pytest.raises(NotImplementedError, match="float GRU backward"):
         y.sum().backward()
+
+
+@pytest.mark.parametrize("batch_first", [False, True])
+def test_bidirectional_layout_in_library_equals_per_direction_path(cuda, batch_first):
+    """The bidirectional QAT path (each direction reads x in place, output / h_n assembled,
+    the output gradient split and dx assembled by the library) equals the per-direction
+    GRUFunction path with PyTorch's flips, concatenations and transposes: outputs and h_n bit
+    for bit, gradients within 1e-5.  The input is a view with padded rows and the loss a mean
+    (a stride-0 output gradient) plus a term on h_n."""
+    T, B, I, H = 7, 20, 12, 48
+    m, x_tbi, hx = _module_case(True, batch_first, True, "c3", 31, shape=(T, B, I, H))
+    m = m.to(cuda)
+    x_in = (x_tbi.transpose(0, 1).contiguous() if batch_first else x_tbi).to(cuda)
+    hx = hx.to(cuda)
+    with m.calibration_context():
+        m(x_in, hx)
+    m.use_quantization = True
+    m.train()
+    wide = torch.zeros(*x_in.shape[:2], I + 5, device=cuda)
+    wide[..., :I] = x_in
+    results = []
+    for fused in (True, False):
+        m.zero_grad(set_to_none=True)
+        leaf = wide.clone().requires_grad_(True)
+        hxl = hx.clone().requires_grad_(True)
+        xv = leaf[..., :I]
+        if fused:
+            out, hn = m(xv, hxl)
+        else:
+            x_tb = xv.transpose(0, 1) if batch_first else xv
+            out, hn = m._forward_cuda(x_tb.contiguous(), hxl)
+            if batch_first:
+                out = out.transpose(0, 1).contiguous()
+        (out.mean() + 0.5 * hn.sum()).backward()
+        torch.cuda.synchronize()
+        grads = [leaf.grad, hxl.grad] + [p.grad for p in m.parameters()]
+        results.append((out.detach(), hn.detach(), [g.clone() for g in grads]))
+    (o1, h1, g1), (o2, h2, g2) = results
+    assert torch.equal(o1, o2) and torch.equal(h1, h2)
+    for k, (a, b) in enumerate(zip(g1, g2)):
+        a, b = a.cpu().numpy(), b.cpu().numpy()
+        scale = max(float(np.abs(b).max()), 1e-30)
+        np.testing.assert_allclose(a, b, rtol=1e-5, atol=1e-6 * scale, err_msg=f"grad {k}")
