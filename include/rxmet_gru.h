@@ -189,13 +189,16 @@ int rxmet_gru_forward_quant_dirs(int32_t ndir, int32_t is_training, int32_t T, i
                                  void *stream);
 
 /*
- * rxmet_gru_forward_quant_dirs with each direction's x read in place from the caller's input.
- * No counterpart in the reference, whose QuantGRU transposes batch-first input and flips it
- * for the reverse direction with tensor copies (quant_gru.py:2151-2205, 2270-2288).
- * x_layout[3 k .. 3 k + 2] = {t stride, b stride, reversed} of direction k in elements (the
- * feature stride is 1): element (t, b, i) of the direction is x[t' st + b sb + i] with
- * t' = reversed ? T-1-t : t.  x_q, x_mask and everything else come out as in
- * rxmet_gru_forward_quant_dirs, in the direction's own [T, B, .] order.  T*B*I < 2^32.
+ * rxmet_gru_forward_quant_dirs with each direction's x read in place from the caller's input
+ * and, optionally, the weights read in PyTorch's layout.  No counterpart in the reference, whose
+ * QuantGRU transposes batch-first input, flips it for the reverse direction and reorders the
+ * weights with tensor copies (quant_gru.py:714-759, 2151-2205, 2270-2288).
+ * x_layout[4 k .. 4 k + 3] = {t stride, b stride, reversed, flags} of direction k in elements
+ * (the feature stride is 1): element (t, b, i) of the direction is x[t' st + b sb + i] with
+ * t' = reversed ? T-1-t : t.  flags bit 0: W, R, bw, br are PyTorch's weight_ih [3H, I],
+ * weight_hh [3H, H], bias_ih, bias_hh in (r, z, n) gate order instead of [I, 3H], [H, 3H] in
+ * (z, r, n).  x_q, x_mask, W_q and everything else come out as in rxmet_gru_forward_quant_dirs,
+ * in the direction's own [T, B, .] order and the (z, r, n) layouts.  T*B*I < 2^32.
  */
 int rxmet_gru_forward_quant_dirs_x(int32_t ndir, int32_t is_training, int32_t T, int32_t B,
                                    int32_t I, int32_t H, const rxmet_gru_fwd_dir *dirs,
@@ -270,6 +273,15 @@ typedef struct rxmet_gru_bwd_dir {
 
 int rxmet_gru_backward_quant_dirs(int32_t ndir, int32_t T, int32_t B, int32_t I, int32_t H,
                                   const rxmet_gru_bwd_dir *dirs, void *stream);
+
+/*
+ * rxmet_gru_backward_quant_dirs with, for flags bit 0, the weight gradients written in
+ * PyTorch's layout: dW [3H, I], dR [3H, H], dbw, dbr [3H] in (r, z, n) gate order (W and R
+ * masks applied as before).  No counterpart in the reference, which reorders the gradients
+ * with tensor copies (quant_gru.py:689-702).
+ */
+int rxmet_gru_backward_quant_dirs_x(int32_t ndir, int32_t T, int32_t B, int32_t I, int32_t H,
+                                    const rxmet_gru_bwd_dir *dirs, int32_t flags, void *stream);
 
 /*
  * Float GRU forward with MinMax calibration statistics: forwardWithCalibrationGPU

@@ -656,17 +656,20 @@ __global__ __launch_bounds__(256) void zero_floats(int64_t n, float *p) {
 }
 
 
+// swap_h > 0: written in the (r, z, n) gate order (the first two blocks of swap_h swapped).
 __global__ __launch_bounds__(256) void fold_bias(int nwg, int C, const double *__restrict__ part,
-                                                 float *__restrict__ dbw, float *__restrict__ dbr) {
+                                                 float *__restrict__ dbw, float *__restrict__ dbr,
+                                                 int swap_h) {
   const int c = blockIdx.x * blockDim.x + threadIdx.x;
   if (c >= C) return;
+  const int co = swap_h > 0 ? (c < swap_h ? c + swap_h : (c < 2 * swap_h ? c - swap_h : c)) : c;
   double x = 0.0, y = 0.0;
   for (int k = 0; k < nwg; ++k) {
     x += part[static_cast<size_t>(k) * 2 * C + c];
     y += part[static_cast<size_t>(k) * 2 * C + C + c];
   }
-  dbw[c] = static_cast<float>(x);
-  dbr[c] = static_cast<float>(y);
+  dbw[co] = static_cast<float>(x);
+  dbr[co] = static_cast<float>(y);
 }
 
 __global__ __launch_bounds__(256) void apply_masks(int64_t n0, int64_t n1, int64_t n2, float *d0,
@@ -745,6 +748,7 @@ struct BwdPlan {
   const rxmet_gru_bwd_dir *d;
   char *wsb;
   int npx, nph, npw;  // bf16 planes of the x, h and W codes
+  bool torch_layout;  // dW, dR, dbw, dbr in PyTorch's layout and (r, z, n) gate order
 };
 
 static int backward_prologue(int T, int B, int I, int H, const rxmet_gru_bwd_dir &d,
@@ -970,8 +974,9 @@ static int backward_epilogue(int T, int B, int I, int H, BwdPlan &plan, hipStrea
   const int C = 3 * H;
   const BwdWorkspace ws(T, B, I, H);
   const int nwg = (B + kBTile - 1) / kBTile;
+  const int swap_h = plan.torch_layout ? H : 0;
   hipLaunchKernelGGL(fold_bias, dim3((C + 255) / 256), dim3(256), 0, stream, nwg, C,
-                     plan.ba.bias_partial, d.dbw, d.dbr);
+                     plan.ba.bias_partial, d.dbw, d.dbr, swap_h);
   RXMET_CHECK_LAUNCH();
   const int M = T * B;
   float *part = reinterpret_cast<float *>(plan.wsb + ws.part);
@@ -995,8 +1000,12 @@ static int backward_epilogue(int T, int B, int I, int H, BwdPlan &plan, hipStrea
     ta.part = part;
     ta.colsum = nullptr;
     if (int rc = wgrad::tn(ta, plan.npx, stream)) return rc;
-    if (int rc = wgrad::tn_finish(part, ta.S, C, I, plan.npx, qsc, d.dW, C, true, nullptr, nullptr,
-                                  stream))
+    // haste layout dW [I][3H] (masked below), or PyTorch's [3H][I] with the W mask applied here
+    if (int rc = plan.torch_layout
+                     ? wgrad::tn_finish(part, ta.S, C, I, plan.npx, qsc, d.dW, I, false, nullptr,
+                                        nullptr, stream, d.W_mask, H)
+                     : wgrad::tn_finish(part, ta.S, C, I, plan.npx, qsc, d.dW, C, true, nullptr,
+                                        nullptr, stream))
       return rc;
     // dR[j][c] = eff_h sum_m (h_prev codes)[m][j] dq[m][c]
     ta.A = plan.ba.dq;
@@ -1004,12 +1013,16 @@ static int backward_epilogue(int T, int B, int I, int H, BwdPlan &plan, hipStrea
     ta.bplane = static_cast<int64_t>(H) * ws.Mp;
     ta.Q = H; ta.S = ws.S_r[plan.nph - 1]; ta.kper = ws.kper_r[plan.nph - 1];
     if (int rc = wgrad::tn(ta, plan.nph, stream)) return rc;
-    if (int rc = wgrad::tn_finish(part, ta.S, C, H, plan.nph, qsc + I, d.dR, C, true, nullptr, nullptr,
-                                  stream))
+    if (int rc = plan.torch_layout
+                     ? wgrad::tn_finish(part, ta.S, C, H, plan.nph, qsc + I, d.dR, H, false, nullptr,
+                                        nullptr, stream, d.R_mask, H)
+                     : wgrad::tn_finish(part, ta.S, C, H, plan.nph, qsc + I, d.dR, C, true, nullptr,
+                                        nullptr, stream))
       return rc;
   }
-  const int64_t n0 = static_cast<int64_t>(T) * B * I, n1 = static_cast<int64_t>(I) * C,
-                n2 = static_cast<int64_t>(H) * C;
+  const int64_t n0 = static_cast<int64_t>(T) * B * I,
+                n1 = plan.torch_layout ? 0 : static_cast<int64_t>(I) * C,
+                n2 = plan.torch_layout ? 0 : static_cast<int64_t>(H) * C;
   int64_t blocks = (n0 + n1 + n2 + 255) / 256;
   if (blocks > 8192) blocks = 8192;
   {
@@ -1022,7 +1035,7 @@ static int backward_epilogue(int T, int B, int I, int H, BwdPlan &plan, hipStrea
 }
 
 static int backward_dirs(int ndir, int T, int B, int I, int H, const rxmet_gru_bwd_dir *dirs,
-                         hipStream_t stream) {
+                         bool torch_layout, hipStream_t stream) {
   RXMET_CHECK_ARG(ndir == 1 || ndir == 2, "ndir must be 1 or 2");
   RXMET_CHECK_ARG(dirs != nullptr, "dirs must be non-null");
   RXMET_CHECK_ARG(T >= 1 && B >= 1 && I >= 1 && H >= 1, "dimensions must be positive");
@@ -1033,6 +1046,7 @@ static int backward_dirs(int ndir, int T, int B, int I, int H, const rxmet_gru_b
   BwdPlan plans[2];
   for (int k = 0; k < ndir; ++k)
     if (int rc = backward_prologue(T, B, I, H, dirs[k], stream, &plans[k])) return rc;
+  for (int k = 0; k < ndir; ++k) plans[k].torch_layout = torch_layout;
   // H > 256 (more R values than the clustered and per-tile kernels keep in registers), or
   // RXMET_BWD_STEPPED set: one pointwise and one GEMM launch per step
   const bool stepped = H > 256 || std::getenv("RXMET_BWD_STEPPED") != nullptr;
@@ -1076,13 +1090,20 @@ int rxmet_gru_backward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const f
   const rxmet_gru_bwd_dir d = {W_q, R_q, bw_q, br_q, x_q, dh_new, h, v, params, x_mask, h0_mask,
                                W_mask, R_mask, bw_mask, br_mask, ih_mask, hh_mask, gate_in_mask,
                                gate_out_mask, h_mask, dx, dW, dR, dbw, dbr, dh0, workspace};
-  return backward_dirs(1, T, B, I, H, &d, static_cast<hipStream_t>(stream_));
+  return backward_dirs(1, T, B, I, H, &d, false, static_cast<hipStream_t>(stream_));
 }
 
 int rxmet_gru_backward_quant_dirs(int32_t ndir, int32_t T, int32_t B, int32_t I, int32_t H,
                                   const rxmet_gru_bwd_dir *dirs, void *stream_) {
   clear_error();
-  return backward_dirs(ndir, T, B, I, H, dirs, static_cast<hipStream_t>(stream_));
+  return backward_dirs(ndir, T, B, I, H, dirs, false, static_cast<hipStream_t>(stream_));
+}
+
+int rxmet_gru_backward_quant_dirs_x(int32_t ndir, int32_t T, int32_t B, int32_t I, int32_t H,
+                                    const rxmet_gru_bwd_dir *dirs, int32_t flags, void *stream_) {
+  clear_error();
+  return backward_dirs(ndir, T, B, I, H, dirs, (flags & 1) != 0,
+                       static_cast<hipStream_t>(stream_));
 }
 
 }  // extern "C"

@@ -49,6 +49,10 @@ __device__ __forceinline__ float clamp_keep(float v, Bounds b, uint8_t &keep) {
 // ---------------------------------------------------------------------------------
 struct WeightArgs {
   const float *W, *R, *bw, *br;
+  // element (k, c) of W / R at W[k w_sk + c' w_sc]; c' = c, or with swap set the column of
+  // the (r, z, n) gate order (PyTorch's weight_ih [3H, I] / weight_hh [3H, H]); biases at [c']
+  int64_t w_sk, w_sc, r_sk, r_sc;
+  int swap;
   const float *eff;  // 4 x C: W, R, bw, br effective scales
   const float *ibx, *ibh;
   Bounds bW, bR, bbw, bbr;
@@ -67,12 +71,13 @@ __global__ __launch_bounds__(64) void quant_weights(int I, int H, WeightArgs a) 
   if (c >= C) return;
   uint8_t keep;
   const float ew = a.eff[c], er = a.eff[C + c], ebw = a.eff[2 * C + c], ebr = a.eff[3 * C + c];
+  const int cs = a.swap ? (c < H ? c + H : (c < 2 * H ? c - H : c)) : c;
   float s = 0.0f;
   for (int k0 = 0; k0 < I; k0 += kQwRows) {
     float v[kQwRows];
 #pragma unroll
     for (int r = 0; r < kQwRows; ++r)
-      v[r] = k0 + r < I ? a.W[static_cast<size_t>(k0 + r) * C + c] : 0.0f;
+      v[r] = k0 + r < I ? a.W[(k0 + r) * a.w_sk + cs * a.w_sc] : 0.0f;
 #pragma unroll
     for (int r = 0; r < kQwRows; ++r) {
       if (k0 + r >= I) break;
@@ -90,7 +95,7 @@ __global__ __launch_bounds__(64) void quant_weights(int I, int H, WeightArgs a) 
     float v[kQwRows];
 #pragma unroll
     for (int r = 0; r < kQwRows; ++r)
-      v[r] = k0 + r < H ? a.R[static_cast<size_t>(k0 + r) * C + c] : 0.0f;
+      v[r] = k0 + r < H ? a.R[(k0 + r) * a.r_sk + cs * a.r_sc] : 0.0f;
 #pragma unroll
     for (int r = 0; r < kQwRows; ++r) {
       if (k0 + r >= H) break;
@@ -104,10 +109,10 @@ __global__ __launch_bounds__(64) void quant_weights(int I, int H, WeightArgs a) 
   }
   a.chan[3 * C + c] = a.zp_h != 0.0f ? s * a.zp_h : 0.0f;  // rsum
   a.chan[6 * C + c] = static_cast<float>(exact);            // rcol (exact)
-  const float qbw = clamp_keep(rintf(a.bw[c] / ebw) + 0.0f, a.bbw, keep);
+  const float qbw = clamp_keep(rintf(a.bw[cs] / ebw) + 0.0f, a.bbw, keep);
   a.bwq[c] = qbw;
   if (a.bwm) a.bwm[c] = keep;
-  const float qbr = clamp_keep(rintf(a.br[c] / ebr) + 0.0f, a.bbr, keep);
+  const float qbr = clamp_keep(rintf(a.br[cs] / ebr) + 0.0f, a.bbr, keep);
   a.brq[c] = qbr;
   if (a.brm) a.brm[c] = keep;
   a.chan[4 * C + c] = rintf(qbw * a.ibx[c]);  // btx
@@ -122,6 +127,7 @@ __global__ __launch_bounds__(64) void quant_weights(int I, int H, WeightArgs a) 
 struct XLayout {
   int64_t st, sb;
   int rev;
+  int torch_w;  // W, R, bw, br in PyTorch's layout and (r, z, n) gate order
 };
 
 __global__ __launch_bounds__(256) void quant_input(int64_t nx, int64_t nh, const float *x,
@@ -848,6 +854,9 @@ static int forward_prologue(bool training, int T, int B, int I, int H, const rxm
   const rxmet_grid *g = params->g;
   WeightArgs wa;
   wa.W = d.W; wa.R = d.R; wa.bw = d.bw; wa.br = d.br;
+  wa.swap = xl.torch_w;
+  wa.w_sk = xl.torch_w ? 1 : C; wa.w_sc = xl.torch_w ? I : 1;
+  wa.r_sk = xl.torch_w ? 1 : C; wa.r_sc = xl.torch_w ? H : 1;
   wa.eff = hostblk;
   wa.ibx = hostblk + 4 * C;
   wa.ibh = hostblk + 5 * C;
@@ -1046,9 +1055,10 @@ static int forward_dirs(int ndir, bool training, int T, int B, int I, int H,
                   "T*B*H too large for the recurrence's 32-bit element offsets");
   FwdPlan plans[2];
   for (int k = 0; k < ndir; ++k) {
-    XLayout xl{static_cast<int64_t>(B) * I, I, 0};
+    XLayout xl{static_cast<int64_t>(B) * I, I, 0, 0};
     if (x_layout) {
-      xl = XLayout{x_layout[3 * k], x_layout[3 * k + 1], x_layout[3 * k + 2] != 0 ? 1 : 0};
+      xl = XLayout{x_layout[4 * k], x_layout[4 * k + 1], x_layout[4 * k + 2] != 0 ? 1 : 0,
+                   (x_layout[4 * k + 3] & 1) != 0 ? 1 : 0};
       RXMET_CHECK_ARG(static_cast<double>(T) * B * I < 4294967295.0 && xl.st >= 0 && xl.sb >= 0,
                       "strided x: T*B*I must be below 2^32 and the strides non-negative");
     }

@@ -54,8 +54,12 @@ int nt(const NtArgs &a, int nplanes, hipStream_t stream);
 // out[p * ldo + q] = qscale[q] * sum_s part[s][p][q] (fixed order; out[q * ldo + p] when
 // transpose); qscale may be null (1).  bias (optional): bias[p * ldo] = the sum of colsum over
 // splits and halves.
+// mask (optional): out is multiplied by mask[q * P + p]; swap_h > 0: row (or column, when
+// transpose) p is written at the index with the first two blocks of swap_h swapped (the
+// (z, r, n) <-> (r, z, n) gate order of the GRU).
 int tn_finish(const float *part, int S, int P, int Q, int nplanes, const float *qscale, float *out,
-              int64_t ldo, bool transpose, const float *colsum, float *bias, hipStream_t stream);
+              int64_t ldo, bool transpose, const float *colsum, float *bias, hipStream_t stream,
+              const uint8_t *mask = nullptr, int swap_h = 0);
 
 // Codes as bf16 operand planes, transposed: for r < rows and c < cols,
 //   v = rint((x(r, c) - zp) / div),  x(r, c) = r < rows0 ? src0[r rs + c cs] : src1[(r - rows0) rs + c cs]

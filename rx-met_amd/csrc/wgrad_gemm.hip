@@ -268,7 +268,9 @@ __global__ __launch_bounds__(256) void tn_finish_kernel(const float *__restrict_
                                                         float *__restrict__ out, int64_t ldo,
                                                         bool transpose, int ath,
                                                         const float *__restrict__ colsum,
-                                                        float *__restrict__ bias) {
+                                                        float *__restrict__ bias,
+                                                        const uint8_t *__restrict__ mask,
+                                                        int swap_h) {
   const int64_t n = static_cast<int64_t>(P) * Q;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n + P; i += stride) {
@@ -276,11 +278,14 @@ __global__ __launch_bounds__(256) void tn_finish_kernel(const float *__restrict_
       float acc = part[i];
       for (int s = 1; s < S; ++s) acc += part[static_cast<int64_t>(s) * n + i];
       const int p = static_cast<int>(i / Q), q = static_cast<int>(i % Q);
-      const float v = qscale ? acc * qscale[q] : acc;
+      float v = qscale ? acc * qscale[q] : acc;
+      if (mask) v *= static_cast<float>(mask[static_cast<int64_t>(q) * P + p]);
+      int po = p;
+      if (swap_h > 0) po = p < swap_h ? p + swap_h : (p < 2 * swap_h ? p - swap_h : p);
       if (transpose)
-        out[q * ldo + p] = v;
+        out[q * ldo + po] = v;
       else
-        out[p * ldo + q] = v;
+        out[po * ldo + q] = v;
     } else if (colsum && bias) {
       const int p = static_cast<int>(i - n);
       float acc = 0.0f;
@@ -413,13 +418,14 @@ int nt(const NtArgs &a, int nplanes, hipStream_t stream) {
 }
 
 int tn_finish(const float *part, int S, int P, int Q, int nplanes, const float *qscale, float *out,
-              int64_t ldo, bool transpose, const float *colsum, float *bias, hipStream_t stream) {
+              int64_t ldo, bool transpose, const float *colsum, float *bias, hipStream_t stream,
+              const uint8_t *mask, int swap_h) {
   const int64_t n = static_cast<int64_t>(P) * Q + P;
   int64_t blocks = (n + 255) / 256;
   if (blocks > 4096) blocks = 4096;
   hipLaunchKernelGGL(tn_finish_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
                      part, S, P, Q, qscale, out, ldo, transpose, tn_tile(Q, nplanes).ath(), colsum,
-                     bias);
+                     bias, mask, swap_h);
   RXMET_CHECK_LAUNCH();
   return 0;
 }

@@ -304,15 +304,16 @@ def forward_quant_float_storage_dirs(is_training, time_steps, batch_size, input_
 def forward_quant_float_storage_dirs_x(is_training, time_steps, batch_size, input_size,
                                        hidden_size, dirs, x_layouts):
     """forward_quant_float_storage_dirs with each direction's x read in place
-    (rxmet_gru_forward_quant_dirs_x): ``x_layouts[k]`` = (t stride, b stride, reversed) of
-    direction k's x in elements (feature stride 1)."""
+    (rxmet_gru_forward_quant_dirs_x): ``x_layouts[k]`` = (t stride, b stride, reversed, flags)
+    of direction k's x in elements (feature stride 1); flags bit 0: W, R, bw, br given in
+    PyTorch's layout (weight_ih [3H, I], weight_hh [3H, H], (r, z, n) gate order)."""
     T, B, I, H = time_steps, batch_size, input_size, hidden_size
     for k, d in enumerate(dirs):
         if d[4].dim() != 3 or d[4].stride(2) != 1:
             raise RuntimeError(f"x of direction {k} needs a unit feature stride")
     made = [_forward_dir(is_training, T, B, I, H, *d) for d in dirs]
     arr = (A.FwdDir * len(made))(*[m[1] for m in made])
-    lay = (ctypes.c_int64 * (3 * len(made)))(*[int(v) for xl in x_layouts for v in xl])
+    lay = (ctypes.c_int64 * (4 * len(made)))(*[int(v) for xl in x_layouts for v in xl])
     _rx.call("rxmet_gru_forward_quant_dirs_x", len(made), int(bool(is_training)), T, B, I, H, arr,
              lay, _stream(dirs[0][4].device))
     return [m[0] for m in made]
@@ -365,7 +366,8 @@ def bidir_dx(dx_f, dx_r, batch_first: bool):
     return dx
 
 
-def _backward_dir(T, B, I, H, W_q, R_q, bw_q, br_q, x_q, dh_new, h, v, quant_params, masks):
+def _backward_dir(T, B, I, H, W_q, R_q, bw_q, br_q, x_q, dh_new, h, v, quant_params, masks,
+                  torch_layout=False):
     C = 3 * H
     dev = x_q.device
     for n, t, shp in (("W_q", W_q, (I, C)), ("R_q", R_q, (H, C)), ("bw_q", bw_q, (C,)),
@@ -376,7 +378,9 @@ def _backward_dir(T, B, I, H, W_q, R_q, bw_q, br_q, x_q, dh_new, h, v, quant_par
         if tuple(t.shape) != shp:
             raise RuntimeError(f"{n} must have shape {list(shp)}")
     f32 = dict(dtype=torch.float32, device=dev)
-    outs = (torch.empty((T, B, I), **f32), torch.empty((I, C), **f32), torch.empty((H, C), **f32),
+    outs = (torch.empty((T, B, I), **f32),
+            torch.empty((C, I) if torch_layout else (I, C), **f32),
+            torch.empty((C, H) if torch_layout else (H, C), **f32),
             torch.empty((C,), **f32), torch.empty((C,), **f32), torch.empty((B, H), **f32))
     mp = [m.data_ptr() if (m is not None and m.numel() > 0) else None for m in masks]
     dh_new = dh_new.contiguous()
@@ -415,5 +419,17 @@ def backward_quant_float_storage_dirs(time_steps, batch_size, input_size, hidden
     made = [_backward_dir(T, B, I, H, *d) for d in dirs]
     arr = (A.BwdDir * len(made))(*[m[1] for m in made])
     _rx.call("rxmet_gru_backward_quant_dirs", len(made), T, B, I, H, arr,
+             _stream(dirs[0][4].device))
+    return [m[0] for m in made]
+
+
+def backward_quant_float_storage_dirs_x(time_steps, batch_size, input_size, hidden_size, dirs):
+    """backward_quant_float_storage_dirs with the weight gradients in PyTorch's layout
+    (rxmet_gru_backward_quant_dirs_x): per direction (dx, dW [3H, I], dR [3H, H], dbw [3H],
+    dbr [3H], dh) in (r, z, n) gate order."""
+    T, B, I, H = time_steps, batch_size, input_size, hidden_size
+    made = [_backward_dir(T, B, I, H, *d, torch_layout=True) for d in dirs]
+    arr = (A.BwdDir * len(made))(*[m[1] for m in made])
+    _rx.call("rxmet_gru_backward_quant_dirs_x", len(made), T, B, I, H, arr, 1,
              _stream(dirs[0][4].device))
     return [m[0] for m in made]

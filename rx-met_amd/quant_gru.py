@@ -102,6 +102,18 @@ def reorder_weights_haste_to_pytorch(w: torch.Tensor) -> torch.Tensor:
     return reorder_weights_pytorch_to_haste(w)
 
 
+_ZEROS = {}
+
+
+def _zeros(n: int, device) -> torch.Tensor:
+    """A cached read-only zero vector (the bias of a layer without biases)."""
+    key = (n, str(device))
+    z = _ZEROS.get(key)
+    if z is None:
+        z = _ZEROS[key] = torch.zeros(n, device=device, dtype=torch.float32)
+    return z
+
+
 def ensure_cuda_float32(tensor: torch.Tensor, device: torch.device) -> torch.Tensor:
     """quant_gru.py:705-711."""
     if tensor.device != device:
@@ -250,12 +262,19 @@ class GRUBidirectionalFunction(torch.autograd.Function):
         dirs = []
         for (wi, wh, bi, bh, h0, qp) in ((wi_f, wh_f, bi_f, bh_f, h0_f, qp_f),
                                          (wi_r, wh_r, bi_r, bh_r, h0_r, qp_r)):
-            W, R, bw, br = convert_weights_to_haste_format(wi, wh, bi, bh, H, device)
+            # weights in PyTorch's layout and gate order: the library reads them as they are
+            W = ensure_cuda_float32(wi, device).contiguous()
+            R = ensure_cuda_float32(wh, device).contiguous()
+            if bi is not None and bh is not None:
+                bw = ensure_cuda_float32(bi, device).contiguous()
+                br = ensure_cuda_float32(bh, device).contiguous()
+            else:
+                bw = br = _zeros(3 * H, device)
             h0_t = (ensure_cuda_float32(h0, device).contiguous() if h0 is not None
                     else torch.empty(0, device=device, dtype=torch.float32))
             dirs.append((W, R, bw, br, x, h0_t, qp))
         outs = gru_ops.forward_quant_float_storage_dirs_x(is_training, T, B, I, H, dirs,
-                                                          [(st, sb, 0), (st, sb, 1)])
+                                                          [(st, sb, 0, 1), (st, sb, 1, 1)])
         ctx.bias_none = (bi_f is None, bh_f is None)
         ctx.h0_none = (h0_f is None, h0_r is None)
         ctx.quant_params = (qp_f, qp_r)
@@ -282,14 +301,12 @@ class GRUBidirectionalFunction(torch.autograd.Function):
             W_q, R_q, bw_q, br_q, x_q, h, v = saved[k * n:k * n + 7]
             masks = saved[k * n + 7:(k + 1) * n]
             dirs.append((W_q, R_q, bw_q, br_q, x_q, dh_new, h, v, ctx.quant_params[k], masks))
-        res = gru_ops.backward_quant_float_storage_dirs(T, B, I, H, dirs)
+        # weight gradients come back in PyTorch's layout and gate order
+        res = gru_ops.backward_quant_float_storage_dirs_x(T, B, I, H, dirs)
         grads = []
         for k, (dx, dW, dR, dbw, dbr, dh) in enumerate(res):
-            grads.append((reorder_weights_haste_to_pytorch(dW.t()),
-                          reorder_weights_haste_to_pytorch(dR.t()),
-                          None if ctx.bias_none[0] else reorder_weights_haste_to_pytorch(dbw),
-                          None if ctx.bias_none[1] else reorder_weights_haste_to_pytorch(dbr),
-                          None if ctx.h0_none[k] else dh))
+            grads.append((dW, dR, None if ctx.bias_none[0] else dbw,
+                          None if ctx.bias_none[1] else dbr, None if ctx.h0_none[k] else dh))
         dx = gru_ops.bidir_dx(res[0][0], res[1][0], ctx.batch_first)
         return (dx, *grads[0], *grads[1], None, None, None, None)
 

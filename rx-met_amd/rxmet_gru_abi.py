@@ -100,6 +100,7 @@ _SIGS = {
     "rxmet_gru_forward_calibrate": (ctypes.c_int, [_i32, _i32, _i32, _i32] + [_p] * 9 + [_p, _p]),
     "rxmet_gru_forward_fp": (ctypes.c_int, [_i32] * 5 + [_p] * 8 + [_p]),
     "rxmet_gru_forward_quant_dirs_x": (ctypes.c_int, [_i32] * 6 + [ctypes.POINTER(FwdDir), _p, _p]),
+    "rxmet_gru_backward_quant_dirs_x": (ctypes.c_int, [_i32] * 5 + [ctypes.POINTER(BwdDir), _i32, _p]),
     "rxmet_gru_bidir_assemble": (ctypes.c_int, [_i32] * 3 + [_p] * 3 + [_i64, _i64, _p, _p]),
     "rxmet_gru_bidir_split_grad": (ctypes.c_int, [_i32] * 3 + [_p, _i64, _i64, _i64] + [_p] * 4),
     "rxmet_gru_bidir_dx": (ctypes.c_int, [_i32] * 3 + [_p] * 3 + [_i64, _i64, _p]),
