@@ -119,6 +119,88 @@ __global__ __launch_bounds__(64) void quant_weights(int I, int H, WeightArgs a) 
   a.chan[5 * C + c] = rintf(qbr * a.ibh[c]);  // bth
 }
 
+// The same with the rows of each column split over kQsGroups threads, for grids where every
+// partial sum of codes stays below 2^24: the float sums are then exact, so the split order gives
+// the sequential sums bit for bit.  32 columns x 8 row groups per 256-thread block.
+constexpr int kQsCols = 32, kQsGroups = 8;
+__global__ __launch_bounds__(256) void quant_weights_split(int I, int H, WeightArgs a) {
+  __shared__ float red[2][kQsGroups][kQsCols];
+  __shared__ int redi[kQsGroups][kQsCols];
+  const int C = 3 * H;
+  const int cx = threadIdx.x % kQsCols, rg = threadIdx.x / kQsCols;
+  const int c = blockIdx.x * kQsCols + cx;
+  const bool on = c < C;
+  const int cc = on ? c : 0;
+  const int cs = a.swap ? (cc < H ? cc + H : (cc < 2 * H ? cc - H : cc)) : cc;
+  uint8_t keep;
+  float sw = 0.0f, sr = 0.0f;
+  int exact = 0;
+  if (on) {
+    const float ew = a.eff[c], er = a.eff[C + c];
+    // rows in batches of kQsBatch whose loads are all issued before any code is stored
+    constexpr int kQsBatch = 16;
+    for (int k0 = rg; k0 < I; k0 += kQsGroups * kQsBatch) {
+      float v[kQsBatch];
+#pragma unroll
+      for (int r = 0; r < kQsBatch; ++r) {
+        const int k = k0 + kQsGroups * r;
+        v[r] = k < I ? a.W[k * a.w_sk + cs * a.w_sc] : 0.0f;
+      }
+#pragma unroll
+      for (int r = 0; r < kQsBatch; ++r) {
+        const int k = k0 + kQsGroups * r;
+        if (k >= I) break;
+        const size_t i = static_cast<size_t>(k) * C + c;
+        const float q = clamp_keep(rintf(v[r] / ew) + 0.0f, a.bW, keep);
+        a.Wq[i] = q;
+        if (a.Wm) a.Wm[i] = keep;
+        sw += q;
+      }
+    }
+    for (int k0 = rg; k0 < H; k0 += kQsGroups * kQsBatch) {
+      float v[kQsBatch];
+#pragma unroll
+      for (int r = 0; r < kQsBatch; ++r) {
+        const int k = k0 + kQsGroups * r;
+        v[r] = k < H ? a.R[k * a.r_sk + cs * a.r_sc] : 0.0f;
+      }
+#pragma unroll
+      for (int r = 0; r < kQsBatch; ++r) {
+        const int k = k0 + kQsGroups * r;
+        if (k >= H) break;
+        const size_t i = static_cast<size_t>(k) * C + c;
+        const float q = clamp_keep(rintf(v[r] / er) + 0.0f, a.bR, keep);
+        a.Rq[i] = q;
+        if (a.Rm) a.Rm[i] = keep;
+        sr += q;
+        exact += static_cast<int>(q);
+      }
+    }
+  }
+  red[0][rg][cx] = sw;
+  red[1][rg][cx] = sr;
+  redi[rg][cx] = exact;
+  __syncthreads();
+  if (rg != 0 || !on) return;
+  for (int g = 1; g < kQsGroups; ++g) {
+    sw += red[0][g][cx];
+    sr += red[1][g][cx];
+    exact += redi[g][cx];
+  }
+  a.chan[2 * C + c] = a.zp_x != 0.0f ? sw * a.zp_x : 0.0f;  // wsum
+  a.chan[3 * C + c] = a.zp_h != 0.0f ? sr * a.zp_h : 0.0f;  // rsum
+  a.chan[6 * C + c] = static_cast<float>(exact);             // rcol (exact)
+  const float ebw = a.eff[2 * C + c], ebr = a.eff[3 * C + c];
+  const float qbw = clamp_keep(rintf(a.bw[cs] / ebw) + 0.0f, a.bbw, keep);
+  a.bwq[c] = qbw;
+  if (a.bwm) a.bwm[c] = keep;
+  const float qbr = clamp_keep(rintf(a.br[cs] / ebr) + 0.0f, a.bbr, keep);
+  a.brq[c] = qbr;
+  if (a.brm) a.brm[c] = keep;
+  a.chan[4 * C + c] = rintf(qbw * a.ibx[c]);  // btx
+  a.chan[5 * C + c] = rintf(qbr * a.ibh[c]);  // bth
+}
+
 // ---------------------------------------------------------------------------------
 // 2. inputs
 // ---------------------------------------------------------------------------------
@@ -874,7 +956,14 @@ static int forward_prologue(bool training, int T, int B, int I, int H, const rxm
   wa.chan = chan;
   {
     rxmet::prof::Scope ps__("gru_fwd_quant_weights", stream);
-    hipLaunchKernelGGL(quant_weights, dim3((C + 63) / 64), dim3(64), 0, stream, I, H, wa);
+    // partial sums of codes exact in float (below 2^24): rows split over 8 threads
+    const double wmax = std::max(std::fabs(static_cast<double>(wa.bW.lo)), std::fabs(static_cast<double>(wa.bW.hi)));
+    const double rmax = std::max(std::fabs(static_cast<double>(wa.bR.lo)), std::fabs(static_cast<double>(wa.bR.hi)));
+    if (wmax * I < 16777216.0 && rmax * H < 16777216.0)
+      hipLaunchKernelGGL(quant_weights_split, dim3((C + kQsCols - 1) / kQsCols), dim3(256), 0, stream,
+                         I, H, wa);
+    else
+      hipLaunchKernelGGL(quant_weights, dim3((C + 63) / 64), dim3(64), 0, stream, I, H, wa);
   }
   RXMET_CHECK_LAUNCH();
 
