@@ -15,13 +15,18 @@ its forward runs on the GPU.
 """
 from __future__ import annotations
 
+import json
+import math
 from contextlib import contextmanager
 from typing import Optional, Tuple
+
+import numpy as np
 
 import torch
 import torch.nn as nn
 
 import gru_ops
+import rxmet_gru_abi as A
 
 # ------------------------------------------------------------------------------------
 # Operator map (quant_gru.py:181-262): public operator name -> config attribute names.
@@ -152,6 +157,105 @@ def _require_device(t: torch.Tensor) -> torch.device:
         raise RuntimeError("QuantGRU runs on the GPU: move the module and its inputs to a "
                            "CUDA (ROCm) device")
     return t.device
+
+
+# ------------------------------------------------------------------------------------
+# Quant-params JSON document (quant_gru.py:2548-2592, 3961-4230, 4353-4526): per operator
+# dtype, symmetric, scale, zero_point, enc_type, real_min, real_max; per-tensor operators
+# first, the per-channel weights last; "operators_reverse" for a bidirectional layer.
+# ------------------------------------------------------------------------------------
+
+# JSON operator name -> grid of the rxmet_gru_qparams struct
+_JSON_GRID = {"input": "x", "output": "h", "weight_ih_linear": "weight_ih_linear",
+              "weight_hh_linear": "weight_hh_linear", "update_gate_input": "update_gate_input",
+              "update_gate_output": "update_gate_output", "reset_gate_input": "reset_gate_input",
+              "reset_gate_output": "reset_gate_output", "new_gate_input": "new_gate_input",
+              "new_gate_output": "new_gate_output", "mul_reset_hidden": "mul_reset_hidden",
+              "mul_old_contribution": "mul_old_contribution",
+              "mul_new_contribution": "mul_new_contribution"}
+_JSON_CHAN = {"weight_ih": "W", "weight_hh": "R", "bias_ih": "bw", "bias_hh": "br"}
+_ENC_TYPES = ("PER_TENSOR", "PER_GATE", "PER_CHANNEL")
+
+
+def _one_or_list(values):
+    """quant_gru.py:4032-4036: one value as a scalar, several as a list."""
+    return values[0] if len(values) == 1 else values
+
+
+def _operators_to_json(cfg, qp: "gru_ops.GRUQuantParams") -> dict:
+    """One direction's operators dict (quant_gru.py:4111-4198)."""
+    per_tensor, per_channel = {}, {}
+    for name, info in _OPERATOR_MAP.items():
+        bits = int(getattr(cfg, info["bw_attr"]))
+        unsigned = bool(getattr(cfg, info["unsigned_attr"]))
+        qmin, qmax = get_quant_range(bits, unsigned)
+        if name in _JSON_CHAN:
+            scales = [float(v) for v in qp.channel_scales(_JSON_CHAN[name])]
+            enc = _ENC_TYPES[int(getattr(cfg, info["bw_attr"] + "granularity_"))]
+            zps = [0] * len(scales)
+        else:
+            scales = [float(qp.scale(_JSON_GRID[name]))]
+            enc = "PER_TENSOR"
+            zps = [int(qp.zero_point(_JSON_GRID[name]))]
+        op = {"dtype": f"{'UINT' if unsigned else 'INT'}{bits}",
+              "symmetric": bool(getattr(cfg, info["sym_attr"])),
+              "scale": _one_or_list(scales), "zero_point": _one_or_list(zps), "enc_type": enc,
+              "real_min": _one_or_list([sc * (qmin - z) for sc, z in zip(scales, zps)]),
+              "real_max": _one_or_list([sc * (qmax - z) for sc, z in zip(scales, zps)])}
+        (per_channel if enc != "PER_TENSOR" or name in _JSON_CHAN else per_tensor)[name] = op
+    per_tensor.update(per_channel)
+    return per_tensor
+
+
+def _operators_from_json(ops: dict, cfg, hidden: int) -> "gru_ops.GRUQuantParams":
+    """Parse one direction's operators dict into cfg and new grids (quant_gru.py:4230-4434).
+    Per-channel scales may be given per channel (3H values), per gate (3) or per tensor (1)."""
+    qp = gru_ops.GRUQuantParams(hidden)
+    C = 3 * hidden
+    for name, op in ops.items():
+        if name not in _OPERATOR_MAP:
+            raise ValueError(f"unknown operator {name!r} in the quant params document")
+        info = _OPERATOR_MAP[name]
+        if "dtype" in op:
+            dtype = str(op["dtype"]).upper()
+            digits = "".join(ch for ch in dtype if ch.isdigit())
+            setattr(cfg, info["bw_attr"], int(digits) if digits else 8)
+            setattr(cfg, info["unsigned_attr"], dtype.startswith("UINT"))
+        if "symmetric" in op:
+            setattr(cfg, info["sym_attr"], bool(op["symmetric"]))
+        if "scale" not in op:
+            raise ValueError(f"operator {name!r} has no scale")
+        scales = op["scale"] if isinstance(op["scale"], list) else [op["scale"]]
+        scales = [float(v) for v in scales]
+        if not scales or any(not (v > 0.0) or not math.isfinite(v) for v in scales):
+            raise ValueError(f"operator {name!r}: scales must be positive and finite")
+        bits = int(getattr(cfg, info["bw_attr"]))
+        unsigned = bool(getattr(cfg, info["unsigned_attr"]))
+        if name in _JSON_CHAN:
+            enc = op.get("enc_type", "PER_CHANNEL")
+            if enc not in _ENC_TYPES:
+                raise ValueError(f"operator {name!r}: unknown enc_type {enc!r}")
+            setattr(cfg, info["bw_attr"] + "granularity_", _ENC_TYPES.index(enc))
+            if len(scales) == 1:
+                full = scales * C
+            elif len(scales) == 3:
+                full = [scales[c // hidden] for c in range(C)]
+            elif len(scales) == C:
+                full = scales
+            else:
+                raise ValueError(f"operator {name!r}: {len(scales)} scales for {C} channels")
+            k = A.CHAN[_JSON_CHAN[name]]
+            qp.struct.chan_bits[k] = bits
+            qp.struct.chan_unsigned[k] = int(unsigned)
+            A.qparams_chan(qp.struct, k)[:] = np.asarray(full, dtype=np.float32)
+        else:
+            zp = op.get("zero_point", 0)
+            zp = zp[0] if isinstance(zp, list) else zp
+            g = qp.struct.g[A.GRID[_JSON_GRID[name]]]
+            g.scale, g.zero_point, g.bits, g.is_unsigned = scales[0], int(zp), bits, int(unsigned)
+    qp.struct.use_pot2 = int(bool(cfg.usePOT2_))
+    qp.bitwidth_config_ = cfg
+    return qp
 
 
 # ------------------------------------------------------------------------------------
@@ -484,6 +588,81 @@ class QuantGRU(nn.Module):
 
     def set_module_name(self, module_name: str) -> None:
         self._module_name = module_name
+
+    # -- quant-params document (quant_gru.py:2548-2592, 4475-4526, 4581-4680) ----------
+
+    def export_quant_params(self, export_path: str, include_weights: bool = False,
+                            verbose: bool = False) -> None:
+        """Write the grids of each direction as the reference's JSON document."""
+        if not self.is_calibrated() and not (self._quant_params_dirty and
+                                             self.quant_ranges is not None):
+            raise RuntimeError("calibrate first: gru.calibrating = True; gru(data); "
+                               "gru.calibrating = False; gru.finalize_calibration()")
+        self._ensure_quant_params_fresh()
+        doc = {"model_info": {"input_size": self.input_size, "hidden_size": self.hidden_size,
+                              "bias": self.bias, "batch_first": self.batch_first,
+                              "bidirectional": self.bidirectional,
+                              "use_pot2_scale": bool(self.use_po2_scale)},
+               "operators": _operators_to_json(self._bitwidth_config, self.quant_params)}
+        if self.bidirectional and self.quant_params_reverse is not None:
+            doc["operators_reverse"] = _operators_to_json(self._bitwidth_config,
+                                                          self.quant_params_reverse)
+        if include_weights:
+            doc["quantized_weights"] = self._quantized_weights_json()
+        with open(export_path, "w", encoding="utf-8") as f:
+            json.dump(doc, f, indent=2, ensure_ascii=False)
+        if verbose:
+            print(f"[QuantGRU] quant params written to {export_path}")
+
+    def _quantized_weights_json(self) -> dict:
+        """Integer weight codes in kernel layout (quant_gru.py:4527-4580)."""
+        qp = self.quant_params
+        W, R, bw, br = convert_weights_to_haste_format(
+            self.weight_ih_l0, self.weight_hh_l0, self.bias_ih_l0 if self.bias else None,
+            self.bias_hh_l0 if self.bias else None, self.hidden_size, self.weight_ih_l0.device)
+        cfg = self._bitwidth_config
+
+        def codes(t, name, bits):
+            s = torch.from_numpy(np.array(qp.channel_scales(name), dtype=np.float32)).to(t.device)
+            lo, hi = get_quant_range(bits)
+            return torch.clamp(torch.round(t.detach() / s), lo, hi).to(torch.int32).tolist()
+
+        out = {"W": codes(W, "W", cfg.W_), "R": codes(R, "R", cfg.R_)}
+        if self.bias:
+            out["bw"] = codes(bw, "bw", cfg.bw_)
+            out["br"] = codes(br, "br", cfg.br_)
+        return out
+
+    def load_quant_params(self, import_path: str, verbose: bool = False) -> None:
+        """Read a quant-params document; the module is calibrated afterwards."""
+        with open(import_path, "r", encoding="utf-8") as f:
+            doc = json.load(f)
+        info = doc.get("model_info", {})
+        for key, mine in (("input_size", self.input_size), ("hidden_size", self.hidden_size),
+                          ("bidirectional", self.bidirectional)):
+            if info.get(key, False if key == "bidirectional" else None) != mine:
+                raise ValueError(f"{key} mismatch: document has {info.get(key)}, module has {mine}")
+        if "operators" not in doc:
+            raise ValueError(f"not a quant params document (no 'operators'; keys {list(doc)})")
+        if self.bidirectional and "operators_reverse" not in doc:
+            raise ValueError("bidirectional=True needs 'operators_reverse' in the document")
+        cfg = gru_ops.OperatorQuantConfig()
+        cfg.usePOT2_ = bool(info.get("use_pot2_scale", False))
+        qp = _operators_from_json(doc["operators"], cfg, self.hidden_size)
+        qpr = None
+        if self.bidirectional:
+            qpr = _operators_from_json(doc["operators_reverse"], cfg, self.hidden_size)
+            fin, rin = doc["operators"].get("input", {}), doc["operators_reverse"].get("input", {})
+            if fin.get("zero_point") != rin.get("zero_point"):
+                raise ValueError("operators.input and operators_reverse.input disagree")
+        self._bitwidth_config = cfg
+        self._use_pot2_scale = bool(cfg.usePOT2_)
+        self.quant_params = qp
+        if self.bidirectional:
+            self.quant_params_reverse = qpr
+        self._quant_params_dirty = False
+        if verbose:
+            print(f"[QuantGRU] quant params loaded from {import_path}")
 
     # -- calibration state -------------------------------------------------------------
 

@@ -165,3 +165,84 @@ def test_module_names():
     net = torch.nn.Sequential(torch.nn.Linear(2, 4), Q.QuantGRU(4, 16))
     Q.set_quant_gru_module_names(net)
     assert net[1]._module_name == "1"
+
+
+def _calibrated_on_host(m, seed):
+    """Grids from synthetic MinMax ranges through the host parameter derivation (no GPU)."""
+    import numpy as np
+    import gru_ops
+    H = m.hidden_size
+    g = np.random.default_rng(seed)
+    params = []
+    for _ in range(2 if m.bidirectional else 1):
+        r = gru_ops.GRUQuantizationRanges(H)
+        st = r.stats.numpy()
+        # 13 operator minima, 13 maxima, then per-channel min / max blocks of 3H for W, R, bw, br
+        mins = -np.abs(g.standard_normal(13)).astype(np.float32) - 0.1
+        mins[0] = -1.7  # both directions read the same x: one x grid
+        st[:13], st[13:26] = mins, -mins * 1.3
+        for k in range(4):
+            base = 26 + 2 * k * 3 * H
+            cm = -np.abs(g.standard_normal(3 * H)).astype(np.float32) * 0.2 - 0.01
+            st[base:base + 3 * H], st[base + 3 * H:base + 6 * H] = cm, -cm * 1.1
+        params.append(gru_ops.calculate_gru_quantitative_parameters(r, m._bitwidth_config))
+    m.quant_params = params[0]
+    if m.bidirectional:
+        m.quant_params_reverse = params[1]
+    m._quant_params_dirty = False
+
+
+@pytest.mark.parametrize("bidirectional", [False, True])
+@pytest.mark.parametrize("pot2", [False, True])
+def test_quant_params_json_round_trip(tmp_path, bidirectional, pot2):
+    """export_quant_params -> load_quant_params into a fresh module gives the same grids,
+    per-channel scales, bit widths and flags (quant_gru.py:2548-2592)."""
+    import json
+    import numpy as np
+    import rxmet_gru_abi as A
+    m = Q.QuantGRU(6, 16, bidirectional=bidirectional)
+    m.set_all_bitwidth(8, is_symmetric=False)
+    m._bitwidth_config.h_ = 16
+    m._bitwidth_config.W_granularity_ = A.PER_GATE
+    m.use_po2_scale = pot2
+    _calibrated_on_host(m, 3)
+    path = tmp_path / "qp.json"
+    m.export_quant_params(str(path), include_weights=True)
+    doc = json.loads(path.read_text())
+    assert list(doc["operators"])[-4:] == ["weight_ih", "weight_hh", "bias_ih", "bias_hh"]
+    op = doc["operators"]["output"]
+    assert op["dtype"] == "INT16" and op["symmetric"] is False
+    assert op["real_min"] == pytest.approx(op["scale"] * (-32768 - op["zero_point"]))
+    assert doc["operators"]["weight_ih"]["enc_type"] == "PER_GATE"
+    assert doc["operators"]["update_gate_output"]["dtype"] == "UINT8"
+    assert ("operators_reverse" in doc) == bidirectional
+    assert len(doc["quantized_weights"]["W"]) == 6 and len(doc["quantized_weights"]["W"][0]) == 48
+    n = Q.QuantGRU(6, 16, bidirectional=bidirectional)
+    n.load_quant_params(str(path))
+    assert n.is_calibrated() and n.use_po2_scale == pot2
+    for a, b in ((m.quant_params, n.quant_params),) + (
+            ((m.quant_params_reverse, n.quant_params_reverse),) if bidirectional else ()):
+        for name in A.GRID_NAMES:
+            assert a.scale(name) == b.scale(name), name
+            assert a.zero_point(name) == b.zero_point(name), name
+            ga, gb = a.struct.g[A.GRID[name]], b.struct.g[A.GRID[name]]
+            assert (ga.bits, bool(ga.is_unsigned)) == (gb.bits, bool(gb.is_unsigned)), name
+        for k, name in enumerate(A.CHAN_NAMES):
+            np.testing.assert_array_equal(a.channel_scales(name), b.channel_scales(name))
+            assert a.struct.chan_bits[k] == b.struct.chan_bits[k]
+        assert a.struct.use_pot2 == b.struct.use_pot2
+    for attr in ("x_", "h_", "W_", "R_", "h_symmetric_", "update_gate_output_unsigned_",
+                 "W_granularity_", "usePOT2_"):
+        assert getattr(m._bitwidth_config, attr) == getattr(n._bitwidth_config, attr), attr
+
+
+def test_quant_params_json_checks(tmp_path):
+    m = Q.QuantGRU(6, 16)
+    with pytest.raises(RuntimeError, match="calibrate"):
+        m.export_quant_params(str(tmp_path / "x.json"))
+    _calibrated_on_host(m, 4)
+    m.export_quant_params(str(tmp_path / "a.json"))
+    with pytest.raises(ValueError, match="hidden_size"):
+        Q.QuantGRU(6, 32).load_quant_params(str(tmp_path / "a.json"))
+    with pytest.raises(ValueError, match="bidirectional"):
+        Q.QuantGRU(6, 16, bidirectional=True).load_quant_params(str(tmp_path / "a.json"))

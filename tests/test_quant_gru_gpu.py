@@ -310,3 +310,26 @@ def test_bidirectional_layout_in_library_equals_per_direction_path(cuda, batch_f
         a, b = a.cpu().numpy(), b.cpu().numpy()
         scale = max(float(np.abs(b).max()), 1e-30)
         np.testing.assert_allclose(a, b, rtol=1e-5, atol=1e-6 * scale, err_msg=f"grad {k}")
+
+
+@pytest.mark.parametrize("bidirectional", [False, True])
+def test_quant_params_document_reproduces_qat_forward(cuda, tmp_path, bidirectional):
+    """Grids calibrated on the GPU, written with export_quant_params and read into a fresh
+    module with the same weights: the quantised forward is bit for bit the same."""
+    T, B, I, H = 5, 24, 10, 32
+    m, x_tbi, hx = _module_case(bidirectional, False, True, "po2-16b", 41, shape=(T, B, I, H))
+    m = m.to(cuda)
+    x, hx = x_tbi.to(cuda), hx.to(cuda)
+    with m.calibration_context():
+        m(x, hx)
+    m.use_quantization = True
+    path = tmp_path / "gru_qp.json"
+    m.export_quant_params(str(path))
+    n = Q.QuantGRU(I, H, bidirectional=bidirectional).to(cuda)
+    n.load_state_dict(m.state_dict())
+    n.load_quant_params(str(path))
+    n.use_quantization = True
+    with torch.no_grad():
+        o1, h1 = m(x, hx)
+        o2, h2 = n(x, hx)
+    assert torch.equal(o1, o2) and torch.equal(h1, h2)
