@@ -149,12 +149,13 @@ __global__ __launch_bounds__(256) void quant_weights_split(int I, int H, WeightA
 #pragma unroll
       for (int r = 0; r < kQsBatch; ++r) {
         const int k = k0 + kQsGroups * r;
-        if (k >= I) break;
-        const size_t i = static_cast<size_t>(k) * C + c;
-        const float q = clamp_keep(rintf(v[r] / ew) + 0.0f, a.bW, keep);
-        a.Wq[i] = q;
-        if (a.Wm) a.Wm[i] = keep;
-        sw += q;
+        if (k < I) {
+          const size_t i = static_cast<size_t>(k) * C + c;
+          const float q = clamp_keep(rintf(v[r] / ew) + 0.0f, a.bW, keep);
+          a.Wq[i] = q;
+          if (a.Wm) a.Wm[i] = keep;
+          sw += q;
+        }
       }
     }
     for (int k0 = rg; k0 < H; k0 += kQsGroups * kQsBatch) {
@@ -167,13 +168,14 @@ __global__ __launch_bounds__(256) void quant_weights_split(int I, int H, WeightA
 #pragma unroll
       for (int r = 0; r < kQsBatch; ++r) {
         const int k = k0 + kQsGroups * r;
-        if (k >= H) break;
-        const size_t i = static_cast<size_t>(k) * C + c;
-        const float q = clamp_keep(rintf(v[r] / er) + 0.0f, a.bR, keep);
-        a.Rq[i] = q;
-        if (a.Rm) a.Rm[i] = keep;
-        sr += q;
-        exact += static_cast<int>(q);
+        if (k < H) {
+          const size_t i = static_cast<size_t>(k) * C + c;
+          const float q = clamp_keep(rintf(v[r] / er) + 0.0f, a.bR, keep);
+          a.Rq[i] = q;
+          if (a.Rm) a.Rm[i] = keep;
+          sr += q;
+          exact += static_cast<int>(q);
+        }
       }
     }
   }
