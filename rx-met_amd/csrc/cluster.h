@@ -134,6 +134,16 @@ __device__ __forceinline__ void store_bytes_coherent(unsigned char *dst4, int by
     p[i] = NAN;
 }
 
+// The same for two outputs of n floats each (q may be null).
+[[maybe_unused]] static __global__ void poison_nan2(const int *timeout, int64_t n, float *p, float *q) {
+  if (*timeout == 0) return;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
+    p[i] = NAN;
+    if (q) q[i] = NAN;
+  }
+}
+
 // Launch a clustered recurrence.  The launch is cooperative, which guarantees that every
 // workgroup of the grid is resident at once.  With RXMET_PLAIN_LAUNCH set it is an ordinary
 // launch of the same grid (for profilers that cannot trace cooperative launches): residency

@@ -714,11 +714,13 @@ struct BwdWorkspace {
     xt = o; o += al(sizeof(__bf16) * 2 * I * static_cast<size_t>(Mp));
     ht = o; o += al(sizeof(__bf16) * 2 * H * static_cast<size_t>(Mp));
     wb = o; o += al(sizeof(__bf16) * 2 * I * C);
-    qsc = o; o += al(sizeof(float) * (I + H));
+    // one host upload: eff_w [C] | eff_r [C] | GEMM column scales [I + H]
+    effw = o;
+    effr = effw + sizeof(float) * C;
+    qsc = effr + sizeof(float) * C;
+    o += al(sizeof(float) * (2 * C + I + H));
     rfrag = o; o += al(sizeof(v4i) * 64 * ((H + 15) / 16) * KS2);
     rowsum = o; o += al(sizeof(float) * H);
-    effr = o; o += al(sizeof(float) * C);
-    effw = o; o += al(sizeof(float) * C);
     bias = o; o += al(sizeof(double) * 2 * C * nwg);
     for (int np = 0; np < 2; ++np)
       wgrad::tn_plan(static_cast<int>(M), static_cast<int>(C), I, np + 1, &S_w[np], &kper_w[np]);
@@ -766,7 +768,6 @@ static int backward_prologue(int T, int B, int I, int H, const rxmet_gru_bwd_dir
   const BwdWorkspace ws(T, B, I, H);
   char *wsb = static_cast<char *>(d.workspace);
   float *effr = reinterpret_cast<float *>(wsb + ws.effr);
-  float *effw = reinterpret_cast<float *>(wsb + ws.effw);
   std::vector<float> host(8 * static_cast<size_t>(C));
   try {
     make_channel_factors(*params, H, host.data() + 4 * C, host.data() + 5 * C, host.data() + 6 * C,
@@ -776,9 +777,7 @@ static int backward_prologue(int T, int B, int I, int H, const rxmet_gru_bwd_dir
     set_error(e.what());
     return -22;
   }
-  RXMET_CHECK_HIP(hipMemcpyAsync(effw, host.data(), sizeof(float) * C, hipMemcpyHostToDevice, stream));
-  RXMET_CHECK_HIP(hipMemcpyAsync(effr, host.data() + C, sizeof(float) * C, hipMemcpyHostToDevice,
-                                 stream));
+
   // weight-gradient operands: x codes, h codes (recovered from the dequantised h) and W codes
   const float eff_x = effective_scale(params->g[RXMET_GRU_X].scale, params->use_pot2 != 0);
   const float zp_x = static_cast<float>(params->g[RXMET_GRU_X].zero_point);
@@ -809,10 +808,11 @@ static int backward_prologue(int T, int B, int I, int H, const rxmet_gru_bwd_dir
       return rc;
   }
   {
-    std::vector<float> qs(I + H);
-    for (int k = 0; k < I; ++k) qs[k] = eff_x;
-    for (int k = 0; k < H; ++k) qs[I + k] = eff_h;
-    RXMET_CHECK_HIP(hipMemcpyAsync(wsb + ws.qsc, qs.data(), sizeof(float) * (I + H),
+    // host holds eff_w, eff_r in its first 2C floats; the column scales follow
+    host.resize(2 * static_cast<size_t>(C) + I + H);
+    for (int k = 0; k < I; ++k) host[2 * static_cast<size_t>(C) + k] = eff_x;
+    for (int k = 0; k < H; ++k) host[2 * static_cast<size_t>(C) + I + k] = eff_h;
+    RXMET_CHECK_HIP(hipMemcpyAsync(wsb + ws.effw, host.data(), sizeof(float) * host.size(),
                                    hipMemcpyHostToDevice, stream));
   }
   BwdArgs &ba = plan->ba;
@@ -895,11 +895,10 @@ static int backward_recurrence_clustered(BwdPlan *plans, int ndir, int T, int B,
     RXMET_CHECK_HIP(cluster::launch(fn, dim3(ncl * cl.G), dim3(256 * cl.UT), args,
                                                static_cast<unsigned>(lds_cl), stream));
   }
-  for (int k = 0; k < ndir; ++k) {
-    hipLaunchKernelGGL(cluster::poison_nan, dim3(64), dim3(256), 0, stream, cl.timeout,
-                       static_cast<int64_t>(B) * H, plans[k].ba.dh0);
-    RXMET_CHECK_LAUNCH();
-  }
+  hipLaunchKernelGGL(cluster::poison_nan2, dim3(64), dim3(256), 0, stream, cl.timeout,
+                     static_cast<int64_t>(B) * H, plans[0].ba.dh0,
+                     ndir > 1 ? plans[1].ba.dh0 : nullptr);
+  RXMET_CHECK_LAUNCH();
   return 1;
 }
 

@@ -53,7 +53,7 @@ struct WeightArgs {
   // the (r, z, n) gate order (PyTorch's weight_ih [3H, I] / weight_hh [3H, H]); biases at [c']
   int64_t w_sk, w_sc, r_sk, r_sc;
   int swap;
-  const float *eff;  // 4 x C: W, R, bw, br effective scales
+  const float *eff;  // 8 x C host block: W, R, bw, br effective scales, ibx, ibh, igx, igh
   const float *ibx, *ibh;
   Bounds bW, bR, bbw, bbr;
   float zp_x, zp_h;
@@ -88,6 +88,8 @@ __global__ __launch_bounds__(64) void quant_weights(int I, int H, WeightArgs a) 
       s += q;
     }
   }
+  a.chan[c] = a.eff[6 * C + c];      // igx
+  a.chan[C + c] = a.eff[7 * C + c];  // igh
   a.chan[2 * C + c] = a.zp_x != 0.0f ? s * a.zp_x : 0.0f;  // wsum
   s = 0.0f;
   int exact = 0;
@@ -189,6 +191,8 @@ __global__ __launch_bounds__(256) void quant_weights_split(int I, int H, WeightA
     sr += red[1][g][cx];
     exact += redi[g][cx];
   }
+  a.chan[c] = a.eff[6 * C + c];      // igx
+  a.chan[C + c] = a.eff[7 * C + c];  // igh
   a.chan[2 * C + c] = a.zp_x != 0.0f ? sw * a.zp_x : 0.0f;  // wsum
   a.chan[3 * C + c] = a.zp_h != 0.0f ? sr * a.zp_h : 0.0f;  // rsum
   a.chan[6 * C + c] = static_cast<float>(exact);             // rcol (exact)
@@ -928,12 +932,8 @@ static int forward_prologue(bool training, int T, int B, int I, int H, const rxm
     set_error(e.what());
     return -22;
   }
+  // one upload; quant_weights copies igx / igh into the per-channel block
   RXMET_CHECK_HIP(hipMemcpyAsync(hostblk, host.data(), sizeof(float) * host.size(),
-                                 hipMemcpyHostToDevice, stream));
-  // igx/igh go straight into the per-channel block
-  RXMET_CHECK_HIP(hipMemcpyAsync(chan, host.data() + 6 * C, sizeof(float) * C,
-                                 hipMemcpyHostToDevice, stream));
-  RXMET_CHECK_HIP(hipMemcpyAsync(chan + C, host.data() + 7 * C, sizeof(float) * C,
                                  hipMemcpyHostToDevice, stream));
   const rxmet_grid *g = params->g;
   WeightArgs wa;
@@ -1109,11 +1109,9 @@ static int forward_recurrence_clustered(FwdPlan *plans, int ndir, int T, int B, 
                                                static_cast<unsigned>(lds_cl), stream));
   }
   const int64_t n_h = static_cast<int64_t>(T + 1) * B * H;
-  for (int k = 0; k < ndir; ++k) {
-    hipLaunchKernelGGL(cluster::poison_nan, dim3(64), dim3(256), 0, stream, cl.timeout, n_h,
-                       plans[k].ra.hout);
-    RXMET_CHECK_LAUNCH();
-  }
+  hipLaunchKernelGGL(cluster::poison_nan2, dim3(64), dim3(256), 0, stream, cl.timeout, n_h,
+                     plans[0].ra.hout, ndir > 1 ? plans[1].ra.hout : nullptr);
+  RXMET_CHECK_LAUNCH();
   return 1;
 }
 
