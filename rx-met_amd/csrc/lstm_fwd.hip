@@ -678,7 +678,44 @@ __global__ __launch_bounds__(512) void lstm_recurrence_cl(RecArgs a, StepParams 
 #pragma unroll
         for (int p = 0; p < NPL; ++p) acc[q][p] = v4i{0, 0, 0, 0};
       const int8_t *hrow = hin + static_cast<size_t>(b0 + l % 16) * H + 16 * (l / 16);
-      {
+      if (NPL == 1 && kBT * (H + 16) <= static_cast<int>(sizeof(float)) * 4 * 4 * 16 * 16) {
+        // The tile's h codes are read from the exchange buffer once per workgroup (one 16-byte
+        // coherent load per thread and plane-chunk) into the gate exchange area, which is free
+        // until the gate phase; the waves then take their A fragments from LDS.
+        int8_t *hs = reinterpret_cast<int8_t *>(xg);
+        const int rs = H + 16, cpr = H / 16, n = NPL * kBT * cpr;
+        int4 hv[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int e0 = tid + 512 * i, e = e0 < n ? e0 : 0;
+          const int p = e / (kBT * cpr), r = (e / cpr) % kBT, c = e % cpr;
+          hv[i] = cluster::load_coherent16(hin + p * plane_stride + static_cast<size_t>(b0 + r) * H + 16 * c);
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int e = tid + 512 * i;
+          if (e < n) {
+            const int p = e / (kBT * cpr), r = (e / cpr) % kBT, c = e % cpr;
+            *reinterpret_cast<int4 *>(hs + (p * kBT + r) * rs + 16 * c) = hv[i];
+          }
+        }
+        __syncthreads();
+        const int8_t *arow = hs + (l % 16) * rs + 16 * (l / 16);
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+          if (s < KS) {
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+              const v4i bf = wl[(((2 * gp + q) * 4 + ut) * KS + s) * 64 + l];
+#pragma unroll
+              for (int p = 0; p < NPL; ++p)
+                acc[q][p] = mfma_i8(*reinterpret_cast<const v4i *>(arow + p * kBT * rs + 64 * s), bf,
+                                    acc[q][p]);
+            }
+          }
+        }
+        __syncthreads();  // the gate phase rewrites the area
+      } else {
         // all of the step's h fragments in flight at once (KS <= 8)
         v4i hfr[8][NPL];
 #pragma unroll
