@@ -540,9 +540,12 @@ __global__ __launch_bounds__(512) void recurrence(RecArgs a, StepParams p) {
 // are exchanged through global memory (coherent accesses, double-buffered by step parity) and
 // the members meet at a counter barrier once per step (cluster.h).
 constexpr int kClMaxKPerWave = 4;  // K-steps per wave: H <= 1024
+constexpr int kHsMax = 4;          // 16-byte h chunks staged per thread and step
+constexpr int kStageMinH = 512;    // H from which the h tile is staged in LDS
 
 struct ClArgs {
   int ncl, G, UT, ntiles, Bpad, ndir;  // clusters walk (direction, batch tile) pairs
+  int stage_h;                         // h tile staged in LDS once per workgroup (large H)
   unsigned *counters;                  // [ncl]
   int *timeout;
 };
@@ -562,7 +565,7 @@ __device__ __forceinline__ void flush_masks(uint8_t *arr, int f0, int ng, const 
 }
 
 // One (direction, batch tile) pair of the clustered recurrence, run by one member.
-template <int NPL>
+template <int NPL, bool STAGE>
 __device__ __forceinline__ void recurrence_cl_pair(const RecArgs &a, const StepParams &p,
                                                    const ClArgs &cl, int tile, int member,
                                                    unsigned *counter, unsigned &epoch,
@@ -577,6 +580,8 @@ __device__ __forceinline__ void recurrence_cl_pair(const RecArgs &a, const StepP
   const int UW = 16 * cl.UT;
   float *sf = reinterpret_cast<float *>(red + static_cast<size_t>(cl.UT) * 4 * 3 * NPL * 64);
   uint8_t *sb = reinterpret_cast<uint8_t *>(sf + 16 * 5 * UW);
+  // the tile's h codes of the step, [NPL][16][H + 16] bytes
+  int8_t *hs = reinterpret_cast<int8_t *>(sb + 16 * 13 * UW);
   const int tid = threadIdx.x, w = tid / 64, l = tid % 64;
   const int utl = w / 4, kq = w % 4;
   const int ut = member * cl.UT + utl;
@@ -641,7 +646,44 @@ __device__ __forceinline__ void recurrence_cl_pair(const RecArgs &a, const StepP
       for (int g = 0; g < 3; ++g)
 #pragma unroll
         for (int q = 0; q < NPL; ++q) acc[g][q] = v4i{0, 0, 0, 0};
-      {
+      if constexpr (STAGE) {
+        // the tile's h codes are read from the exchange buffer once per workgroup (16-byte
+        // coherent loads, all issued before any is stored) into LDS, where the unit tiles
+        // share them (at H >= 512; at smaller H the extra barrier costs more than it saves)
+        const int rs = H + 16, cpr = H / 16, n = NPL * kTileB * cpr, nt = blockDim.x;
+        int4 hv[kHsMax];
+#pragma unroll
+        for (int i = 0; i < kHsMax; ++i) {
+          const int e0 = tid + nt * i, e = e0 < n ? e0 : 0;
+          const int p = e / (kTileB * cpr), r = (e / cpr) % kTileB, c = e % cpr;
+          hv[i] = cluster::load_coherent16(hin + p * plane_stride + static_cast<size_t>(b0 + r) * H + 16 * c);
+        }
+#pragma unroll
+        for (int i = 0; i < kHsMax; ++i) {
+          const int e = tid + nt * i;
+          if (e < n) {
+            const int p = e / (kTileB * cpr), r = (e / cpr) % kTileB, c = e % cpr;
+            *reinterpret_cast<int4 *>(hs + (p * kTileB + r) * rs + 16 * c) = hv[i];
+          }
+        }
+        __syncthreads();
+        const int8_t *hrow = hs + (l % 16) * rs + 16 * (l / 16);
+        v4i hfr[kClMaxKPerWave][NPL];
+#pragma unroll
+        for (int i = 0; i < kClMaxKPerWave; ++i)
+#pragma unroll
+          for (int q = 0; q < NPL; ++q)
+            if (kq + 4 * i < KS)
+              hfr[i][q] = *reinterpret_cast<const v4i *>(hrow + q * kTileB * rs + 64 * (kq + 4 * i));
+#pragma unroll
+        for (int i = 0; i < kClMaxKPerWave; ++i)
+          if (kq + 4 * i < KS) {
+#pragma unroll
+            for (int g = 0; g < 3; ++g)
+#pragma unroll
+              for (int q = 0; q < NPL; ++q) acc[g][q] = mfma_i8(hfr[i][q], rfr[i][g], acc[g][q]);
+          }
+      } else {
         const int8_t *hrow = hin + static_cast<size_t>(b0 + l % 16) * H + 16 * (l / 16);
         v4i hfr[kClMaxKPerWave][NPL];
 #pragma unroll
@@ -809,7 +851,7 @@ __device__ __forceinline__ void recurrence_cl_pair(const RecArgs &a, const StepP
   }
 }
 
-template <int NPL>
+template <int NPL, bool STAGE>
 __global__ __launch_bounds__(512) void recurrence_cl(RecArgs a0, RecArgs a1,
                                                      const StepParams *__restrict__ ps,
                                                      ClArgs cl) {
@@ -822,13 +864,15 @@ __global__ __launch_bounds__(512) void recurrence_cl(RecArgs a0, RecArgs a1,
     // the previous pair's readers of the LUT and the partial-sum buffer are done
     __syncthreads();
     // one copy of the step code for both directions (d is uniform across the workgroup)
-    recurrence_cl_pair<NPL>(d == 0 ? a0 : a1, ps[d], cl, tile, pl.member, counter, epoch, alive);
+    recurrence_cl_pair<NPL, STAGE>(d == 0 ? a0 : a1, ps[d], cl, tile, pl.member, counter, epoch,
+                                   alive);
   }
 }
 
-size_t recurrence_cl_lds_bytes(int UT, int npl) {
+size_t recurrence_cl_lds_bytes(int UT, int npl, int H) {
   return 1024 + sizeof(v4i) * static_cast<size_t>(UT) * 4 * 3 * npl * 64 +
-         static_cast<size_t>(16) * 16 * UT * (5 * sizeof(float) + 13);
+         static_cast<size_t>(16) * 16 * UT * (5 * sizeof(float) + 13) +
+         static_cast<size_t>(npl) * kTileB * (H + 16);
 }
 
 
@@ -1059,8 +1103,11 @@ static int forward_recurrence_clustered(FwdPlan *plans, int ndir, int T, int B, 
   for (int k = 1; k < ndir; ++k)
     if (plans[k].npl != npl) return 0;
   if (KS > 4 * kClMaxKPerWave || std::getenv("RXMET_NO_CLUSTER") != nullptr) return 0;
-  const void *fn = npl == 1 ? reinterpret_cast<const void *>(&recurrence_cl<1>)
-                            : reinterpret_cast<const void *>(&recurrence_cl<2>);
+  const bool stage = H >= kStageMinH;
+  const void *fn = npl == 1 ? (stage ? reinterpret_cast<const void *>(&recurrence_cl<1, true>)
+                                     : reinterpret_cast<const void *>(&recurrence_cl<1, false>))
+                            : (stage ? reinterpret_cast<const void *>(&recurrence_cl<2, true>)
+                                     : reinterpret_cast<const void *>(&recurrence_cl<2, false>));
   int device = 0, ncu = 0;
   RXMET_CHECK_HIP(hipGetDevice(&device));
   RXMET_CHECK_HIP(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, device));
@@ -1074,6 +1121,8 @@ static int forward_recurrence_clustered(FwdPlan *plans, int ndir, int T, int B, 
   int chosen = 0, ncl = 0;
   for (int UT = 1; UT <= 2 && !chosen; ++UT) {
     if ((H / 16) % UT) continue;
+    // the staged h tile takes at most kHsMax chunks per thread
+    if (H >= kStageMinH && npl * H > kHsMax * 256 * UT) continue;
     const int G = H / (16 * UT);
     if (static_cast<int64_t>(pairs) * G <= ncu || UT == 2) {
       chosen = UT;
@@ -1081,7 +1130,7 @@ static int forward_recurrence_clustered(FwdPlan *plans, int ndir, int T, int B, 
     }
   }
   if (!chosen) return 0;
-  const size_t lds_cl = recurrence_cl_lds_bytes(chosen, npl);
+  const size_t lds_cl = recurrence_cl_lds_bytes(chosen, npl, H);
   RXMET_CHECK_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                       static_cast<int>(lds_cl)));
   int per_cu = 0;
@@ -1091,6 +1140,7 @@ static int forward_recurrence_clustered(FwdPlan *plans, int ndir, int T, int B, 
   if (ncl > pairs) ncl = pairs;
   if (ncl >= 8) ncl -= ncl % 8;
   cl.UT = chosen;
+  cl.stage_h = stage ? 1 : 0;
   cl.ncl = ncl;
   const FwdWorkspace ws(T, B, I, H);
   cl.counters = reinterpret_cast<unsigned *>(plans[0].wsb + ws.sync);
