@@ -333,6 +333,8 @@ __global__ __launch_bounds__(512) void lstm_bwd_recurrence_cl(BwdArgs a, BwdClAr
   int *exs = reinterpret_cast<int *>(csl + 64 * G);                     // [16][G]
   unsigned *rowmax = reinterpret_cast<unsigned *>(exs + kBB * G);       // [16]
   int *rowexp = reinterpret_cast<int *>(rowmax + kBB);                  // [16]
+  // the step's gate gradients of the member's units, [16 rows][8][64]: dli gates 0-3, dlh 4-7
+  float *sdl = reinterpret_cast<float *>(rowexp + kBB);
   const int tid = threadIdx.x, w = tid / 64, l = tid % 64;
   const int utl = w & 3, kh = w >> 2;
   const cluster::Place pl = cluster::place(G, cl.ncl);
@@ -430,6 +432,16 @@ __global__ __launch_bounds__(512) void lstm_bwd_recurrence_cl(BwdArgs a, BwdClAr
         }
         dc[rr] = mdc * fg;
       }
+      // stage the gate gradients for the stores after the arrival
+#pragma unroll
+      for (int rr = 0; rr < 2; ++rr) {
+        float *d = sdl + (nrow0 + 2 * kh + rr) * 8 * kBcUnits + 16 * utl + l % 16;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          d[g * kBcUnits] = lis[rr][g];
+          d[(4 + g) * kBcUnits] = lhs[rr][g];
+        }
+      }
       // per-sequence exponent of this member's channels (NaN and inf rows propagate as NaN)
 #pragma unroll
       for (int rr = 0; rr < 2; ++rr) {
@@ -476,19 +488,25 @@ __global__ __launch_bounds__(512) void lstm_bwd_recurrence_cl(BwdArgs a, BwdClAr
         for (int p = 0; p < 3; ++p)
           cluster::store_coherent(reinterpret_cast<unsigned *>(dst + p * pstride), wd[p]);
       }
-      // the other members only read the planes and exponents: arrive, then store the gate
-      // gradients for the weight GEMMs while waiting
+      // the other members only read the planes and exponents: arrive (which also publishes the
+      // staged gate gradients), then store them for the weight GEMMs as 16-byte rows while
+      // waiting
       cluster::arrive(counter);
       ++epoch;
-#pragma unroll
-      for (int rr = 0; rr < 2; ++rr) {
-        const int b = b0 + nrow0 + 2 * kh + rr;
-        if (b >= B) continue;
-        const uint32_t gb = static_cast<uint32_t>(t) * BC + static_cast<uint32_t>(b) * C + j;
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          a.dli[gb + g * H] = lis[rr][g];
-          a.dlh[gb + g * H] = lhs[rr][g];
+      {
+        const size_t tb = static_cast<size_t>(t) * BC;
+        const int u0 = kBcUnits * m0;
+        for (int c = tid; c < kBB * 4 * 16; c += blockDim.x) {
+          const int row = c / 64, g = (c / 16) % 4, q = c % 16, b = b0 + row;
+          if (b < B)
+            *reinterpret_cast<float4 *>(a.dli + tb + static_cast<size_t>(b) * C + g * H + u0 + 4 * q) =
+                *reinterpret_cast<const float4 *>(sdl + (row * 8 + g) * kBcUnits + 4 * q);
+        }
+        for (int c = tid; c < kBB * 4 * 16; c += blockDim.x) {
+          const int row = c / 64, g = (c / 16) % 4, q = c % 16, b = b0 + row;
+          if (b < B)
+            *reinterpret_cast<float4 *>(a.dlh + tb + static_cast<size_t>(b) * C + g * H + u0 + 4 * q) =
+                *reinterpret_cast<const float4 *>(sdl + (row * 8 + 4 + g) * kBcUnits + 4 * q);
         }
       }
       alive = cluster::wait(counter, epoch * G, cl.timeout);
@@ -571,7 +589,7 @@ __global__ __launch_bounds__(512) void lstm_bwd_recurrence_cl(BwdArgs a, BwdClAr
 
 size_t bwd_cl_lds(int C, int G) {
   return 3 * kBB * static_cast<size_t>(C + 16) + sizeof(double) * (8 * 64 * 4 + 64 * G) +
-         sizeof(int) * kBB * G + 2 * sizeof(int) * kBB;
+         sizeof(int) * kBB * G + 2 * sizeof(int) * kBB + sizeof(float) * kBB * 8 * kBcUnits;
 }
 
 size_t bwd_lds(int H, int KS2) {
