@@ -20,6 +20,8 @@
 //                    planes against the resident int8 R_q, recombined in fp64; error <= 2^-22
 //                    of the row maximum per term).  Both fuse the STE pointwise (all mask
 //                    families), write dp/dq for the GEMMs and keep fp64 bias partials;
+//                    For H > 256 the stepped path (bwd_step_point + a K-split dh GEMM per
+//                    step) replaces both;
 //   3. bias fold   : per-workgroup fp64 partials summed in a fixed order (deterministic);
 //   4. dx, dW, dR  : bf16-MFMA GEMMs with the gradients split exactly into three bf16 terms
 //                    (wgrad_gemm.h; dW and dR split over the long T*B reduction and summed in

@@ -7,20 +7,22 @@
 // 604-801), and two in-place dequantisation passes over h and v.
 //
 // Here:
-//   1. quant_weights : one thread per channel column quantises W/R/bw/br, writes masks,
-//      the fp32 column sums of codes times the input zero points, and the bias terms
-//      rint(b_q * ratio) the pointwise step needs (they do not change over time);
-//   2. quant_input   : x and h0 quantisation (codes + masks), h[0] dequantised;
-//   3. code_gemm     : the time-parallel input projection W_q x_q summed exactly in
-//      int32 (int64 when 16-bit codes and long rows could reach 2^31) and rounded once
-//      to fp32;
-//   4. recurrence    : one persistent workgroup per 16 sequences runs all T steps.  The
-//      recurrent weights R_q live in VGPRs as int8 MFMA fragments for the whole kernel;
-//      h_t lives in LDS as int8 planes (16-bit codes are split into a high and a
-//      low byte plane); each step is 3 x (H/64) x planes v_mfma_i32_16x16x64_i8 per wave,
-//      exact in int32, followed by the fused pointwise update in registers (bias
-//      rescale, gate inputs, PWL sigmoid/tanh, hidden update, clamps and masks) and the
-//      dequantised outputs.  No host round trip and no grid barrier per step.
+//   1. quant_weights : W/R/bw/br quantisation (codes, masks), read in the kernel layout or in
+//      PyTorch's layout and gate order; the fp32 column sums of codes times the input zero
+//      points and the bias terms rint(b_q * ratio) the pointwise step needs (rows split over
+//      eight threads per column where the float sums are exact);
+//   2. quant_input   : x (read in place from the caller's layout, time-reversed for a reverse
+//      direction) and h0 quantisation (codes + masks), h[0] dequantised;
+//   3. code_gemm     : the time-parallel input projection W_q x_q summed exactly on int8 MFMA
+//      over pre-packed byte planes and rounded once to fp32 (exact_gemm.h);
+//   4. recurrence    : both directions' T steps in one clustered cooperative launch
+//      (recurrence_cl; cluster.h): a batch tile's hidden units split over a cluster of
+//      workgroups, the new h codes exchanged through global memory each step.  R_q lives in
+//      VGPRs as int8 MFMA fragments for the whole kernel; h_t arrives as int8 planes (16-bit
+//      codes as a high and a low byte plane); the pointwise update (bias rescale, gate
+//      inputs, PWL sigmoid/tanh, hidden update, clamps and masks) is fused in registers, and
+//      the step's outputs leave as 16-byte rows staged in LDS while the members wait.  The
+//      per-tile fallback (recurrence) keeps one workgroup per 16 sequences.
 #include <cmath>
 #include <cstdlib>
 #include <vector>

@@ -7,20 +7,21 @@
 // the dx / dW_ih / dW_hh SGEMMs, a bias column reduction and seven mask passes.
 //
 // Here:
-//   1. prep      : dequantised x and W_ih for the GEMMs, previous hidden states [T,B,H] (h0
-//                  first), each with a trailing column of ones so that the weight-gradient
-//                  GEMMs also produce the bias gradients; W_hh codes packed as int8 MFMA
-//                  fragments of the transposed product, their column sums;
-//   2. recurrence: one persistent workgroup per 16 sequences walks t = T-1..0.  A lane owns
-//                  one hidden unit for four sequences (four unit tiles per wave); dh stays
-//                  in registers, dc in LDS.  Per step: the pointwise backward with every
-//                  mask family in the reference's operation order, both gate-gradient
-//                  tensors written for the GEMMs, then dh = W_hh_deq^T dgates_hh on int8
-//                  MFMA: dgates_hh * scale_W is written per sequence as 22-bit block fixed
-//                  point (exponent from the row maximum) in three int8 planes, multiplied
-//                  exactly against the W_hh codes and recombined in double;
-//   3. rocBLAS   : dx, and split-K dW_ih | db_ih and dW_hh | db_hh; one pass applies the
-//                  master masks and splits off the bias columns.
+//   1. prologue  : x and h_prev codes and the W_ih codes as bf16 operand planes for the
+//                  weight-gradient GEMMs; W_hh codes packed as int8 MFMA fragments of the
+//                  transposed product, with their column sums;
+//   2. recurrence: both K-halves of a batch tile's dh product over a cluster of workgroups
+//                  (lstm_bwd_recurrence_cl; the per-tile fallback lstm_bwd_recurrence keeps
+//                  one workgroup per 16 sequences).  Per step: the pointwise backward with
+//                  every mask family in the reference's operation order; dgates_hh * scale_W
+//                  published as 22-bit block fixed point (a per-sequence exponent from the
+//                  row maximum) in three int8 planes; after the cluster barrier,
+//                  dh = W_hh_deq^T dgates_hh on int8 MFMA against the resident W_hh codes,
+//                  recombined exactly in double; the gate gradients for the GEMMs go out as
+//                  16-byte rows staged in LDS while the members wait;
+//   3. GEMMs     : dx, dW_ih | db_ih and dW_hh | db_hh on bf16 MFMA with the gradients split
+//                  exactly into three bf16 terms (wgrad_gemm.h), the bias columns from fused
+//                  column sums; one pass applies the master masks.
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
