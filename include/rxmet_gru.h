@@ -220,7 +220,8 @@ int rxmet_gru_bidir_assemble(int32_t T, int32_t B, int32_t H, const float *h_f, 
  * (row 0 zero) from the output gradient g (element (t, b, k) at g[t g_st + b g_sb + k g_sk],
  * strides may be zero, g may be null) and the h_n gradient g_hn ([2, B, H] contiguous, may be
  * null): dh_f[t+1][b][j] = g(t, b, j), dh_r[s+1][b][j] = g(T-1-s, b, H+j), plus g_hn at the last
- * row.  Replaces the reference's zero-fill and slice copies of the upstream gradient.
+ * row.  H a multiple of 4, dh_f and dh_r 16-byte aligned.  Replaces the reference's zero-fill
+ * and slice copies of the upstream gradient.
  */
 int rxmet_gru_bidir_split_grad(int32_t T, int32_t B, int32_t H, const float *g, int64_t g_st,
                                int64_t g_sb, int64_t g_sk, const float *g_hn, float *dh_f,

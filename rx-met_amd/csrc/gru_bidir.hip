@@ -50,28 +50,40 @@ __global__ __launch_bounds__(256) void bidir_assemble(int T, int B, int H, const
 
 // dh_f[s + 1][b][j] = g[s][b][j] (+ g_hn[0][b][j] at s = T-1), dh_r[s + 1][b][j] =
 // g[T-1-s][b][H + j] (+ g_hn[1][b][j] at s = T-1); row 0 of both is zero.  g element (t, b, k)
-// at g[t gt + b gb + k gk] (strides may be zero); g or g_hn may be absent (zero).
+// at g[t gt + b gb + k gk] (strides may be zero); g or g_hn may be absent (zero).  One thread
+// per four consecutive units, written as one 16-byte store (H is a multiple of 4).
 __global__ __launch_bounds__(256) void bidir_split_grad(int T, int B, int H, const float *__restrict__ g,
                                                         int64_t gt, int64_t gb, int64_t gk,
                                                         const float *__restrict__ g_hn,
                                                         float *__restrict__ dh_f,
                                                         float *__restrict__ dh_r) {
-  const size_t BH = static_cast<size_t>(B) * H;
-  const int64_t n = 2 * static_cast<int64_t>(T + 1) * BH;  // both directions
+  const int h4 = H / 4;
+  const int64_t rows = static_cast<int64_t>(T + 1) * B;  // rows of one direction
+  const int64_t n = 2 * rows * h4;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  const size_t BH = static_cast<size_t>(B) * H;
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
-    const int dir = i >= static_cast<int64_t>((T + 1) * BH) ? 1 : 0;
-    const int64_t e = i - dir * static_cast<int64_t>((T + 1) * BH);
-    const int s1 = static_cast<int>(e / BH);  // row s + 1 of dh_new
-    const int64_t rem = e - s1 * static_cast<int64_t>(BH);
-    const int b = static_cast<int>(rem / H), j = static_cast<int>(rem % H);
-    float v = 0.0f;
+    const int64_t row2 = i / h4;
+    const int j = 4 * static_cast<int>(i - row2 * h4);
+    const int dir = row2 >= rows ? 1 : 0;
+    const int64_t row = row2 - dir * rows;
+    const int s1 = static_cast<int>(row / B), b = static_cast<int>(row - static_cast<int64_t>(s1) * B);
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
     if (s1 > 0) {
       const int t = dir == 0 ? s1 - 1 : T - s1;
-      if (g) v = g[t * gt + b * gb + (dir * H + j) * gk];
-      if (g_hn && s1 == T) v += g_hn[dir * BH + rem];
+      if (g) {
+        const float *src = g + t * gt + b * gb + (static_cast<int64_t>(dir) * H + j) * gk;
+        v = make_float4(src[0], src[gk], src[2 * gk], src[3 * gk]);
+      }
+      if (g_hn && s1 == T) {
+        const float *h = g_hn + dir * BH + static_cast<size_t>(b) * H + j;
+        v.x += h[0];
+        v.y += h[1];
+        v.z += h[2];
+        v.w += h[3];
+      }
     }
-    (dir == 0 ? dh_f : dh_r)[e] = v;
+    *reinterpret_cast<float4 *>((dir == 0 ? dh_f : dh_r) + row * H + j) = v;
   }
 }
 
@@ -124,9 +136,12 @@ int rxmet_gru_bidir_split_grad(int32_t T, int32_t B, int32_t H, const float *g, 
                                int64_t g_sb, int64_t g_sk, const float *g_hn, float *dh_f,
                                float *dh_r, void *stream) {
   clear_error();
-  RXMET_CHECK_ARG(T >= 1 && B >= 1 && H >= 1, "bad dimensions");
+  RXMET_CHECK_ARG(T >= 1 && B >= 1 && H >= 1 && H % 4 == 0, "bad dimensions (H a multiple of 4)");
   RXMET_CHECK_ARG(dh_f && dh_r, "required pointer is null");
-  const int64_t n = 2 * static_cast<int64_t>(T + 1) * B * H;
+  RXMET_CHECK_ARG((reinterpret_cast<uintptr_t>(dh_f) & 15u) == 0 &&
+                      (reinterpret_cast<uintptr_t>(dh_r) & 15u) == 0,
+                  "dh_new buffers must be 16-byte aligned");
+  const int64_t n = 2 * static_cast<int64_t>(T + 1) * B * (H / 4);
   hipLaunchKernelGGL(bidir_split_grad, dim3(grid_for(n)), dim3(256), 0, static_cast<hipStream_t>(stream),
                      T, B, H, g, g_st, g_sb, g_sk, g_hn, dh_f, dh_r);
   RXMET_CHECK_LAUNCH();
