@@ -19,6 +19,10 @@ extern "C" {
 
 /* Turn event timing on (non-zero) or off. Returns 0. */
 int rxmet_prof_enable(int32_t on);
+/* Time only the launches whose name is in the comma-separated list `names` (null or empty:
+ * every instrumented launch).  Each timed launch adds two event records to its stream, so a
+ * benchmark can keep the perturbation of its timed region to the kernels it reports. */
+int rxmet_prof_filter(const char *names);
 /* Drop every accumulated figure and pending event pair. Returns 0. */
 int rxmet_prof_reset(void);
 /* Total milliseconds and launch count recorded for `name` since the last reset

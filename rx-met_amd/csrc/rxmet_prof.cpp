@@ -26,6 +26,8 @@ std::mutex g_mu;
 bool g_on = false;
 std::map<std::string, Entry> g_entries;
 std::vector<hipEvent_t> g_pool;
+constexpr size_t kPrewarm = 4096;  // events kept ready while timing is on
+std::vector<std::string> g_filter;  // names timed; empty: all
 
 hipEvent_t take_event() {
   if (!g_pool.empty()) {
@@ -59,6 +61,11 @@ bool enabled() { return g_on; }
 Scope::Scope(const char *name, hipStream_t stream) : name_(name), stream_(stream) {
   if (!g_on) return;
   std::lock_guard<std::mutex> lk(g_mu);
+  if (!g_filter.empty()) {
+    bool hit = false;
+    for (const std::string &f : g_filter) hit = hit || f == name_;
+    if (!hit) return;
+  }
   start_ = take_event();
   if (start_ && hipEventRecord(start_, stream_) != hipSuccess) {
     g_pool.push_back(start_);
@@ -88,6 +95,30 @@ extern "C" {
 int rxmet_prof_enable(int32_t on) {
   std::lock_guard<std::mutex> lk(g_mu);
   g_on = on != 0;
+  // events are created up front, so that timed launches only take them from the pool
+  // (creating one per launch costs host time inside the timed region)
+  for (size_t i = g_pool.size(); g_on && i < kPrewarm; ++i) {
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) break;
+    g_pool.push_back(e);
+  }
+  return 0;
+}
+
+int rxmet_prof_filter(const char *names) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  g_filter.clear();
+  if (names == nullptr) return 0;
+  std::string cur;
+  for (const char *c = names;; ++c) {
+    if (*c == ',' || *c == '\0') {
+      if (!cur.empty()) g_filter.push_back(cur);
+      cur.clear();
+      if (*c == '\0') break;
+    } else {
+      cur += *c;
+    }
+  }
   return 0;
 }
 

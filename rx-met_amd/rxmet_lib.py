@@ -41,6 +41,7 @@ _SIGNATURES = {
                                           c_ptr, c_ptr, c_ptr, c_ptr]),
     "rxmet_selftest_mfma": (c_int, [c_int, c_ptr, c_ptr, c_ptr, c_ptr]),
     "rxmet_prof_enable": (c_int, [ctypes.c_int32]),
+    "rxmet_prof_filter": (c_int, [ctypes.c_char_p]),
     "rxmet_prof_reset": (c_int, []),
     "rxmet_prof_query": (c_int, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double),
                                  ctypes.POINTER(c_i64)]),
@@ -113,6 +114,11 @@ def stream_of(device) -> int:
 def prof_enable(on: bool = True) -> None:
     """Turn the library's per-launch event timing on or off (include/rxmet_prof.h)."""
     load().rxmet_prof_enable(1 if on else 0)
+
+
+def prof_filter(names=None) -> None:
+    """Time only the named launches (an iterable of names; None: all)."""
+    load().rxmet_prof_filter(None if names is None else ",".join(names).encode())
 
 
 def prof_reset() -> None:
