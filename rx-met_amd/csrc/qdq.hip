@@ -347,19 +347,35 @@ __device__ __forceinline__ int64_t fold_index(const FoldMap &f, int64_t c, int64
   return a * f.a_stride + c * f.c_stride + bb * f.b_stride;
 }
 
-__global__ __launch_bounds__(kWave) void fold_sum(const double2 *__restrict__ partial, FoldMap f,
-                                                  float *__restrict__ dscale,
-                                                  float *__restrict__ doffset) {
+// NT threads per encoding (one wave, or four waves for encodings with many partials); the
+// waves' sums are added in a fixed order.
+template <int NT>
+__global__ __launch_bounds__(NT) void fold_sum(const double2 *__restrict__ partial, FoldMap f,
+                                               float *__restrict__ dscale,
+                                               float *__restrict__ doffset) {
+  __shared__ double red[2][NT / kWave];
   const int64_t c = blockIdx.x;
   const int64_t n = f.a_count * f.b_count;
   double a = 0.0, b = 0.0;
-  for (int64_t p = threadIdx.x; p < n; p += kWave) {
+  for (int64_t p = threadIdx.x; p < n; p += NT) {
     const double2 v = partial[fold_index(f, c, p)];
     a += v.x;
     b += v.y;
   }
   a = wave_sum(a);
   b = wave_sum(b);
+  if (NT > kWave) {
+    if (threadIdx.x % kWave == 0) {
+      red[0][threadIdx.x / kWave] = a;
+      red[1][threadIdx.x / kWave] = b;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0)
+      for (int w = 1; w < NT / kWave; ++w) {
+        a += red[0][w];
+        b += red[1][w];
+      }
+  }
   if (threadIdx.x == 0) {
     if (dscale) dscale[c] = static_cast<float>(a);
     if (doffset) doffset[c] = static_cast<float>(b);
@@ -482,8 +498,12 @@ static int launch_backward_impl(const Plan &p, const float *x, const float *g, f
   RXMET_CHECK_LAUNCH();
   if constexpr (ENC) {
     rxmet::prof::Scope ps__("qdq_backward_fold", stream);
-    hipLaunchKernelGGL(fold_sum, dim3(static_cast<unsigned>(p.C)), dim3(kWave), 0, stream, ws,
-                       p.fold, dscale, doffset);
+    if (p.fold.a_count * p.fold.b_count >= 1024)
+      hipLaunchKernelGGL(fold_sum<4 * kWave>, dim3(static_cast<unsigned>(p.C)), dim3(4 * kWave), 0,
+                         stream, ws, p.fold, dscale, doffset);
+    else
+      hipLaunchKernelGGL(fold_sum<kWave>, dim3(static_cast<unsigned>(p.C)), dim3(kWave), 0, stream,
+                         ws, p.fold, dscale, doffset);
     RXMET_CHECK_LAUNCH();
   }
   return 0;
