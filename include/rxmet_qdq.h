@@ -116,6 +116,30 @@ int rxmet_dequantize_backward(const float *q, const float *g, float *dq, float *
                               const float *scale, const float *offset, void *workspace,
                               void *stream);
 
+/*
+ * Encodings of learnable min/max (QuantizeDequantize.get_scale / _get_offset,
+ * quantizer.py:345-464), n encodings in one launch instead of the reference's chain of
+ * one-element tensor operations:
+ *   scale  = max(|(max - min) * fl(1 / (qmax - qmin))|, min_scale),
+ *   offset = symmetric ? sym_offset : clamp(round_half_even(min / scale) - qmin, -qmax, -qmin),
+ * the float operations PyTorch performs for the reference's tensor expressions on the GPU (a
+ * tensor divided by a scalar is a product with the scalar's rounded reciprocal there).
+ */
+int rxmet_qdq_encoding_forward(const float *mn, const float *mx, int64_t n, int64_t qmin,
+                               int64_t qmax, int32_t symmetric, float sym_offset,
+                               float min_scale, float *scale, float *offset, void *stream);
+
+/*
+ * Gradients of the above with respect to min and max, given those of scale (g_scale) and of
+ * offset (g_offset, ignored when symmetric; either may be null = zero), with the
+ * reference's autograd rules: straight-through rounding, clamp and clamp_min pass the
+ * gradient inside their range (bounds included), |x|' = sign(x).
+ */
+int rxmet_qdq_encoding_backward(const float *mn, const float *mx, const float *g_scale,
+                                const float *g_offset, int64_t n, int64_t qmin, int64_t qmax,
+                                int32_t symmetric, float min_scale, float *d_min, float *d_max,
+                                void *stream);
+
 #ifdef __cplusplus
 }
 #endif

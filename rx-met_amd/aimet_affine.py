@@ -415,7 +415,16 @@ class QuantizeDequantize(nn.Module):
             raise RuntimeError(
                 "Failed to run QuantizeDequantize since quantization parameters are not initialized."
                 " Please initialize the quantization parameters using `compute_encodings()`.")
-        scale, offset = self.get_encodings()
+        mn, mx = self.min, self.max
+        if (mn.is_cuda and mn.dtype == torch.float32 and mx.dtype == torch.float32
+                and mn.is_contiguous() and mx.is_contiguous()):
+            # get_encodings() in two launches instead of a chain of one-element tensor ops
+            scale, offset = mi355x_qdq.minmax_encodings(
+                mn, mx, self.qmin, self.qmax, self.symmetric,
+                _get_minimum_scale(self.qmax - self.qmin),
+                float(symmetric_offset(self.qmin, self.qmax)))
+        else:
+            scale, offset = self.get_encodings()
         return quantize_dequantize(input, scale, offset, self.qmin, self.qmax,
                                    block_size=self.block_size,
                                    zero_point_shift=self.zero_point_shift)

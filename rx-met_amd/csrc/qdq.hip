@@ -540,6 +540,55 @@ static int check_grid(int64_t qmin, int64_t qmax) {
   return 0;
 }
 
+// Encodings of learnable min / max, one thread per encoding (see rxmet_qdq_encoding_forward).
+__global__ __launch_bounds__(256) void encoding_fwd(int64_t n, const float *__restrict__ mn,
+                                                    const float *__restrict__ mx, float inv_steps,
+                                                    float qmin, float qmax, int symmetric,
+                                                    float sym_offset, float min_scale,
+                                                    float *__restrict__ scale,
+                                                    float *__restrict__ offset) {
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (c >= n) return;
+  // a tensor divided by a scalar is evaluated on the GPU as a product with the rounded
+  // reciprocal of the scalar
+  float s = fabsf((mx[c] - mn[c]) * inv_steps);
+  s = s < min_scale ? min_scale : s;  // clamp_min keeps NaN
+  scale[c] = s;
+  if (symmetric) {
+    offset[c] = sym_offset;
+  } else {
+    float o = rintf(mn[c] / s) - qmin;
+    o = o < -qmax ? -qmax : o;
+    o = o > -qmin ? -qmin : o;
+    offset[c] = o;
+  }
+}
+
+__global__ __launch_bounds__(256) void encoding_bwd(int64_t n, const float *__restrict__ mn,
+                                                    const float *__restrict__ mx,
+                                                    const float *__restrict__ g_scale,
+                                                    const float *__restrict__ g_offset, float inv_steps,
+                                                    float qmin, float qmax, int symmetric,
+                                                    float min_scale, float *__restrict__ d_min,
+                                                    float *__restrict__ d_max) {
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (c >= n) return;
+  const float raw = (mx[c] - mn[c]) * inv_steps, a = fabsf(raw);
+  const float s = a < min_scale ? min_scale : a;
+  float gs = g_scale ? g_scale[c] : 0.0f, gmin = 0.0f;
+  if (!symmetric && g_offset) {
+    const float o = rintf(mn[c] / s) - qmin;
+    const float gr = (o >= -qmax && o <= -qmin) ? g_offset[c] : 0.0f;  // clamp, then STE round
+    gmin += gr / s;                                                   // d(min / s) / d min
+    gs += -gr * ((mn[c] / s) / s);                                    // d(min / s) / d s
+  }
+  const float ga = a >= min_scale ? gs : 0.0f;  // clamp_min
+  const float sg = raw > 0.0f ? 1.0f : (raw < 0.0f ? -1.0f : 0.0f);
+  const float gr2 = (ga * sg) * inv_steps;      // d|raw| and d((max - min) / steps)
+  d_max[c] = gr2;
+  d_min[c] = gmin - gr2;
+}
+
 }  // namespace qdq
 }  // namespace rxmet
 
@@ -662,6 +711,36 @@ int rxmet_dequantize_backward(const float *q, const float *g, float *dq, float *
   RXMET_CHECK_ARG(scale != nullptr, "scale must be non-null");
   return launch_backward<OP_DQ>(q, g, dq, dscale, doffset, outer, C, inner, scale, offset, 0.f,
                                 0.f, workspace, static_cast<hipStream_t>(stream));
+}
+
+int rxmet_qdq_encoding_forward(const float *mn, const float *mx, int64_t n, int64_t qmin,
+                               int64_t qmax, int32_t symmetric, float sym_offset,
+                               float min_scale, float *scale, float *offset, void *stream) {
+  clear_error();
+  RXMET_CHECK_ARG(n >= 1 && mn && mx && scale && offset, "bad encoding arguments");
+  if (int rc = check_grid(qmin, qmax)) return rc;
+  hipLaunchKernelGGL(encoding_fwd, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), n, mn, mx,
+                     1.0f / static_cast<float>(qmax - qmin), static_cast<float>(qmin),
+                     static_cast<float>(qmax), symmetric, sym_offset,
+                     min_scale, scale, offset);
+  RXMET_CHECK_LAUNCH();
+  return 0;
+}
+
+int rxmet_qdq_encoding_backward(const float *mn, const float *mx, const float *g_scale,
+                                const float *g_offset, int64_t n, int64_t qmin, int64_t qmax,
+                                int32_t symmetric, float min_scale, float *d_min, float *d_max,
+                                void *stream) {
+  clear_error();
+  RXMET_CHECK_ARG(n >= 1 && mn && mx && d_min && d_max, "bad encoding arguments");
+  if (int rc = check_grid(qmin, qmax)) return rc;
+  hipLaunchKernelGGL(encoding_bwd, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), n, mn, mx, g_scale, g_offset,
+                     1.0f / static_cast<float>(qmax - qmin), static_cast<float>(qmin),
+                     static_cast<float>(qmax), symmetric, min_scale, d_min, d_max);
+  RXMET_CHECK_LAUNCH();
+  return 0;
 }
 
 }  // extern "C"

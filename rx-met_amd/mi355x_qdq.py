@@ -401,3 +401,42 @@ def minmax(tensor: torch.Tensor, enc_shape) -> Tuple[torch.Tensor, torch.Tensor]
     _rx.call("rxmet_qdq_minmax", _rx.ptr(x), outer, C, inner, _rx.ptr(mn), _rx.ptr(mx), _rx.ptr(ws),
              _rx.stream_of(x.device))
     return mn.view(tuple(enc_shape)), mx.view(tuple(enc_shape))
+
+
+class _MinMaxEncodings(torch.autograd.Function):
+    """(scale, offset) of learnable min/max in one launch each way
+    (rxmet_qdq_encoding_forward / _backward): the values of QuantizeDequantize.get_scale and
+    _get_offset (quantizer.py:345-464) bit for bit, and their gradients by the same autograd
+    rules, without the chain of one-element tensor operations."""
+
+    @staticmethod
+    def forward(ctx, mn, mx, qmin: int, qmax: int, symmetric: bool, min_scale: float,
+                sym_offset: float):
+        scale = torch.empty_like(mn)
+        offset = torch.empty_like(mn)
+        _rx.call("rxmet_qdq_encoding_forward", _rx.ptr(mn), _rx.ptr(mx), mn.numel(), int(qmin),
+                 int(qmax), int(bool(symmetric)), float(sym_offset), float(min_scale),
+                 _rx.ptr(scale), _rx.ptr(offset), _rx.stream_of(mn.device))
+        ctx.save_for_backward(mn, mx)
+        ctx.args = (int(qmin), int(qmax), bool(symmetric), float(min_scale))
+        if symmetric:
+            ctx.mark_non_differentiable(offset)
+        return scale, offset
+
+    @staticmethod
+    def backward(ctx, g_scale, g_offset):
+        mn, mx = ctx.saved_tensors
+        qmin, qmax, symmetric, min_scale = ctx.args
+        gs = g_scale.contiguous() if g_scale is not None else None
+        go = g_offset.contiguous() if (g_offset is not None and not symmetric) else None
+        d_min, d_max = torch.empty_like(mn), torch.empty_like(mx)
+        _rx.call("rxmet_qdq_encoding_backward", _rx.ptr(mn), _rx.ptr(mx), _rx.ptr(gs), _rx.ptr(go),
+                 mn.numel(), qmin, qmax, int(symmetric), min_scale, _rx.ptr(d_min), _rx.ptr(d_max),
+                 _rx.stream_of(mn.device))
+        return d_min, d_max, None, None, None, None, None
+
+
+def minmax_encodings(mn: torch.Tensor, mx: torch.Tensor, qmin: int, qmax: int, symmetric: bool,
+                     min_scale: float, sym_offset: float):
+    """Fused (scale, offset) of contiguous CUDA float32 min/max tensors."""
+    return _MinMaxEncodings.apply(mn, mx, qmin, qmax, symmetric, min_scale, sym_offset)

@@ -40,6 +40,10 @@ _SIGNATURES = {
     "rxmet_dequantize_backward": (c_int, [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64,
                                           c_ptr, c_ptr, c_ptr, c_ptr]),
     "rxmet_selftest_mfma": (c_int, [c_int, c_ptr, c_ptr, c_ptr, c_ptr]),
+    "rxmet_qdq_encoding_forward": (c_int, [c_ptr, c_ptr, c_i64, c_i64, c_i64, ctypes.c_int32,
+                                           ctypes.c_float, ctypes.c_float, c_ptr, c_ptr, c_ptr]),
+    "rxmet_qdq_encoding_backward": (c_int, [c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64,
+                                            ctypes.c_int32, ctypes.c_float, c_ptr, c_ptr, c_ptr]),
     "rxmet_prof_enable": (c_int, [ctypes.c_int32]),
     "rxmet_prof_filter": (c_int, [ctypes.c_char_p]),
     "rxmet_prof_reset": (c_int, []),
