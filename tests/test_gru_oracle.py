@@ -314,3 +314,33 @@ def test_backward_matches_autograd_surrogate(bits, h_bits, seed):
         e = exp[k].numpy()
         np.testing.assert_allclose(got[k], e, rtol=1e-5, atol=1e-6 * max(1.0, np.abs(e).max()),
                                    err_msg=k)
+
+
+@needs_ref
+@pytest.mark.parametrize("seed", [5, 9])
+def test_reference_int_carrier_agrees_with_fp_carrier(seed):
+    """Pins the compiled reference CPU int carrier (``quantGRUForwardCPU``,
+    gru_host.cc:161-252 / gru_forward_cpu_quant.cc:109-343), the checker for an int-IO forward.
+    Both carriers share the grids and LUTs and differ only in how the rescales round, so
+    at 8-bit grids they give the same h codes, and at 16-bit grids they stay within a few steps
+    of the h grid.  Both track the float GRU."""
+    T, B, I, H = 6, 4, 5, 8
+    w = _gru_weights(I, H, seed)
+    W, R, bw, br = to_haste(*w)
+    x = np.random.default_rng(seed + 1).standard_normal((T, B, I)).astype(f32)
+    ref = torch.nn.GRU(I, H)
+    with torch.no_grad():
+        ref.weight_ih_l0.copy_(w[0]); ref.weight_hh_l0.copy_(w[1])
+        ref.bias_ih_l0.copy_(w[2]); ref.bias_hh_l0.copy_(w[3])
+        y, _ = ref(torch.from_numpy(x))
+    for bits in (8, 16):
+        cfg = A.set_all_bitwidth(A.default_config(), bits, False)
+        qp, ranges = calibrated_params(W, R, bw, br, x, cfg)
+        fp = GO.forward_quant(W, R, bw, br, x, qp)["h"]
+        h, _ = GO.ref_forward_ptq(W, R, bw, br, x, ranges, cfg)
+        steps = np.abs(h - fp) / qp.g[A.GRID["h"]].scale
+        if bits == 8:
+            np.testing.assert_array_equal(h, fp)
+        else:
+            assert steps.max() <= 3.0 and steps.mean() <= 0.5, (steps.max(), steps.mean())
+        assert np.abs(h[1:] - y.numpy()).max() < 3e-2
