@@ -1,18 +1,25 @@
 """Benchmark of the MI355X quantization hot path (one GPU).
 
-Prints ONE JSON line.  Legs:
+Prints ONE JSON line.  Legs (all run by default):
 * gru  — QuantGRU bidirectional QAT forward+backward at config c3
          (B=256, T=200, I=80, H=256): seq/s, the headline ``value``;
 * lstm — QuantLSTM unidirectional QAT forward+backward at config c4 (B=512, T=100, I=64,
          H=512, 8-bit per-channel weights, 8-bit gates, 16-bit cell, 8-bit h): seq/s;
 * qdq  — AIMET QuantizeDequantize forward+backward at config c2 ([8192, 8192] fp32,
          learnable min/max encodings, 8-bit asymmetric per-tensor and 4-bit symmetric
-         per-channel): algorithmic HBM GB/s.
+         per-channel): algorithmic HBM GB/s;
+* c1   — the QuantGRU PTQ calibration pass (B=32, T=98, I=40, H=64): calibration forward,
+         parameter derivation and PTQ forward, seq/s;
+* c5   — QuantGRU unidirectional QAT forward+backward at B=1024, T=50, I=256, H=1024 (4-bit
+         weights, 16-bit activations and h, power-of-2 scales): seq/s.
 
 The roofline object describes the dominant kernel of the headline leg, timed with
 hipEvents that the library records around its own launches on the stream they run on
-(rxmet_prof_*), over the timed region.  The CPU baseline times the CPU oracle on a
-bounded sample of the same workload (``qdq_*`` keys: the same for the QDQ leg).
+(rxmet_prof_*), over the timed region.  After each leg the benchmarked outputs are checked:
+every output and gradient finite, and sampled sequences equal to the CPU oracle (forward
+bit-exact, dx within 1e-4); a failed check ends the run with exit status 3 and no JSON line.
+The CPU baselines time the reference's own CPU code (compiled from its sources into
+oracle/_ref) on a bounded sample of the same workload, with the host's CPU model stated.
 """
 from __future__ import annotations
 
@@ -62,7 +69,7 @@ def _copy_probe(torch, mib: int) -> None:
     _log(f"copy probe: 3 x neg over {mib} MiB")
 
 
-def _qdq_leg(torch, steps: int, warmup: int):
+def _qdq_leg(torch, steps: int, warmup: int, validate: bool = True):
     """c2: learnable-encoding QDQ fwd+bwd on [8192, 8192] (both encodings of c2)."""
     import numpy as np
 
@@ -148,12 +155,32 @@ def _qdq_leg(torch, steps: int, warmup: int):
     results["kernel_bwd"] = {"us": t_b * 1e6, "GB_s": 12 * n / t_b / 1e9}
     _log(f"qdq kernels: fwd {t_f*1e6:.1f} us ({8*n/t_f/1e9:.0f} GB/s), "
          f"bwd {t_b*1e6:.1f} us ({12*n/t_b/1e9:.0f} GB/s)")
+    check = None
+    if validate:
+        # the timed kernels' outputs on 64 rows against the oracle: y and dx bit-exact, the
+        # per-row encoding gradients within summation-order noise
+        import qdq_oracle as O
+
+        torch.cuda.synchronize()
+        rows = 64
+        xs, gs = x[:rows].cpu().numpy(), g[:rows].cpu().numpy()
+        sv, ov = s_vec[:rows].cpu().numpy(), o_vec[:rows].cpu().numpy()
+        lay = (1, rows, Cc)
+        ey, _ = O.qdq_learnable(xs, sv, ov, -8, 7, lay)
+        edx, eds, edo = O.qdq_learnable_backward(xs, gs, sv, ov, -8, 7, lay)
+        _check_equal("qdq forward", y[:rows].cpu().numpy(), ey)
+        _check_equal("qdq dx", dx[:rows].cpu().numpy(), edx)
+        e1 = _check_close("qdq dscale", ds[:rows].cpu().numpy(), eds, rtol=1e-5)
+        e2 = _check_close("qdq doffset", do[:rows].cpu().numpy(), edo, rtol=1e-5)
+        check = {"rows": rows, "forward": "bit-exact", "dx": "bit-exact",
+                 "encoding_grad_max_abs_err_rel": max(e1, e2)}
+        _log(f"c2 validation: {check}")
     roof = {"kernel": "qdq bwd_runs<LEARNABLE> (fused STE + encoding grads)", "bound": "hbm",
             "achieved": round(12 * n / t_b / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(12 * n / t_b / 1e9 / HBM_PEAK_GBS, 4),
             "traffic": _traffic("qdq_bwd_learnable"),
             "algorithmic_bytes_per_launch": 12 * n}
-    return results, roof
+    return results, roof, check
 
 
 # Algorithmic work per launch of the instrumented GRU kernels (one direction, c3 shapes):
@@ -181,6 +208,115 @@ def _gru_kernel_work(B, T, I, H, D=2):
         "gru_fwd_input_gemm": (D * 2.0 * M * C * I, FP32_MFMA_PEAK,
                                "input projection W_q.x_q exact integer GEMM"),
     }
+
+
+class ValidationError(RuntimeError):
+    """The benchmarked path produced outputs that are non-finite or differ from the oracle."""
+
+
+def _host_info():
+    """Host CPU of the box the baselines ran on."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = None
+    return {"cpu_model": model, "nproc": os.cpu_count(), "usable_cpus": usable}
+
+
+def _check_close(name, got, exp, rtol=1e-4):
+    import numpy as np
+
+    if not np.isfinite(got).all():
+        raise ValidationError(f"{name}: non-finite values")
+    scale = max(float(np.abs(exp).max()), 1e-30)
+    err = float((np.abs(got - exp) / (rtol * np.abs(exp) + 1e-5 * scale)).max())
+    if err > 1.0:
+        raise ValidationError(f"{name}: differs from the oracle (error {err:.3g} of the bar)")
+    return float(np.abs(got - exp).max() / scale)
+
+
+def _check_equal(name, got, exp):
+    import numpy as np
+
+    if not np.array_equal(got, exp):
+        raise ValidationError(f"{name}: not bit-exact against the oracle "
+                              f"({int((got != exp).sum())} elements differ)")
+
+
+def _swap_gates(t):
+    import numpy as np
+
+    r, z, n = np.split(t, 3, axis=0)
+    return np.concatenate([z, r, n], 0)
+
+
+def _gru_dirs_haste(m):
+    """Per direction: (W [I,3H], R [H,3H], bw, br, qparams struct, ranges, config) of a
+    QuantGRU, in the kernel-side (z, r, n) layout the oracle takes."""
+    import numpy as np
+
+    out = []
+    for d in range(m.num_directions):
+        sfx = "_reverse" if d else ""
+        p = lambda n: getattr(m, n + sfx).detach().cpu().numpy()
+        qp = m.quant_params_reverse if d else m.quant_params
+        rg = m.quant_ranges_reverse if d else m.quant_ranges
+        out.append((np.ascontiguousarray(_swap_gates(p("weight_ih_l0")).T),
+                    np.ascontiguousarray(_swap_gates(p("weight_hh_l0")).T),
+                    _swap_gates(p("bias_ih_l0")), _swap_gates(p("bias_hh_l0")), qp.struct,
+                    rg.to_struct(), m._bitwidth_config.to_struct()))
+    return out
+
+
+def _validate_gru(torch, m, x, rows, batch_first):
+    """One more step of the benchmarked module (loss = mean of the output): outputs and every
+    gradient finite, the sampled sequences' output (bit-exact) and dx (1e-4) equal to the
+    oracle run on those sequences alone."""
+    import numpy as np
+
+    import gru_oracle as GO
+
+    m.zero_grad(set_to_none=True)
+    xl = x.detach().clone().requires_grad_(True)
+    out, _ = m(xl)
+    out.mean().backward()
+    torch.cuda.synchronize()
+    if not bool(torch.isfinite(out).all()) or not bool(torch.isfinite(xl.grad).all()):
+        raise ValidationError("gru: non-finite output or input gradient")
+    for name, p in m.named_parameters():
+        if not bool(torch.isfinite(p.grad).all()):
+            raise ValidationError(f"gru: non-finite gradient of {name}")
+    H = m.hidden_size
+    xt = x.detach().transpose(0, 1) if batch_first else x.detach()
+    xs = xt[:, rows].contiguous().cpu().numpy()
+    ot = out.detach().transpose(0, 1) if batch_first else out.detach()
+    got = ot[:, rows].cpu().numpy()
+    gx = xl.grad.transpose(0, 1) if batch_first else xl.grad
+    gx = gx[:, rows].cpu().numpy()
+    T = xs.shape[0]
+    gval = np.float32(1.0 / out.numel())
+    dx = np.zeros(xs.shape, np.float64)
+    for d, (W, R, bw, br, qp, _, _) in enumerate(_gru_dirs_haste(m)):
+        xd = np.ascontiguousarray(xs[::-1]) if d else xs
+        fwd = GO.forward_quant(W, R, bw, br, xd, qp, training=True)
+        o = fwd["h"][1:][::-1] if d else fwd["h"][1:]
+        _check_equal(f"gru output dir{d}", got[..., d * H:(d + 1) * H], o)
+        dh = np.zeros((T + 1, len(rows), H), np.float32)
+        dh[1:] = gval
+        bwd = GO.backward_quant(fwd, dh, qp)
+        dx += bwd["dx"][::-1] if d else bwd["dx"]
+    err = _check_close("gru dx", gx, dx)
+    return {"sequences": list(rows), "forward": "bit-exact", "dx_max_abs_err_rel": err,
+            "grads_finite": True}
 
 
 def _gru_leg(torch, steps: int, warmup: int):
@@ -222,7 +358,7 @@ def _gru_leg(torch, steps: int, warmup: int):
 
 
 def _gru_c5_leg(torch, steps: int, warmup: int):
-    """c5 (a parity configuration, timed on request): QuantGRU unidirectional QAT fwd+bwd,
+    """c5: QuantGRU unidirectional QAT fwd+bwd,
     B=1024, T=50, I=256, H=1024, 4-bit symmetric per-channel W_ih/W_hh, 16-bit activations
     and hidden state, power-of-2 scales."""
     import quant_gru as QG
@@ -248,13 +384,14 @@ def _gru_c5_leg(torch, steps: int, warmup: int):
         out, _ = m(x)
         out.mean().backward()
 
-    dt, p50, p95, kernels, _ = _timed_steps(torch, step, steps, warmup,
-                                            _gru_kernel_work(B, T, I, H, D=1))
+    dt, p50, p95, kernels, roof = _timed_steps(torch, step, steps, warmup,
+                                               _gru_kernel_work(B, T, I, H, D=1))
     _log(f"gru c5: {dt*1e3:.2f} ms/step wall, P50 {p50:.2f} ms, {B/dt:.1f} seq/s")
     for k, v in sorted(kernels.items(), key=lambda kv: -kv[1]["ms_per_step"]):
         _log(f"  {k}: {v['ms_per_step']:.3f} ms/step, {v['us_per_launch']:.1f} us/launch")
-    return {"ms_per_step": dt * 1e3, "p50_ms": p50, "seq_per_s": B / dt,
-            "kernels_ms_per_step": {k: round(v["ms_per_step"], 4) for k, v in kernels.items()}}
+    return {"ms_per_step": dt * 1e3, "p50_ms": p50, "p95_ms": p95, "seq_per_s": B / dt,
+            "kernels_ms_per_step": {k: round(v["ms_per_step"], 4) for k, v in kernels.items()},
+            "roofline": roof}, m, x
 
 
 def _lstm_kernel_work(B, T, I, H):
@@ -381,88 +518,239 @@ def _lstm_leg(torch, steps: int, warmup: int):
     return res, roof, m, x, g
 
 
-def _lstm_cpu_baseline(m, x, g, rows: int = 8):
-    """CPU oracle (C, one thread) on the first `rows` sequences of c4: the q-carrier forward
-    in the reference CPU path's activation semantics (glibc expf/tanhf) plus the STE
-    backward, with the module's own grids."""
+def _validate_lstm(torch, m, x, g, rows):
+    """One more step of the benchmarked module: outputs and every gradient finite, the sampled
+    sequences' output (bit-exact) and dx (1e-4) equal to the oracle's."""
+    import numpy as np
+
     import lstm_oracle as LO
 
-    xs = x[:, :rows].detach().contiguous().cpu().numpy()
-    gs = g[:, :rows].detach().contiguous().cpu().numpy()
+    m.zero_grad(set_to_none=True)
+    xl = x.detach().clone().requires_grad_(True)
+    out, _ = m(xl)
+    out.backward(g)
+    torch.cuda.synchronize()
+    if not bool(torch.isfinite(out).all()) or not bool(torch.isfinite(xl.grad).all()):
+        raise ValidationError("lstm: non-finite output or input gradient")
+    for name, p in m.named_parameters():
+        if not bool(torch.isfinite(p.grad).all()):
+            raise ValidationError(f"lstm: non-finite gradient of {name}")
     Wi, Wh, bi, bh = (p.detach().cpu().numpy() for p in m._direction_params(False))
-    p = m._params[0].struct
-    t0 = time.perf_counter()
-    fwd = LO.forward_quant(Wi, Wh, bi, bh, xs, p, mode=LO.ACT_LIBM)
-    t1 = time.perf_counter()
-    LO.backward_quant(fwd, p, gs)
-    dt = time.perf_counter() - t0
-    T, Bs, I = xs.shape
-    return {"value": round(Bs / dt, 3), "unit": "seq/s", "cores": 1, "kind": "port",
-            "sample": f"c4 QAT fwd+bwd on {Bs} of the 512 sequences (T={T}, I={I}, "
-                      f"H={m.hidden_size}), C oracle, one thread, {dt:.1f} s "
-                      f"(forward {t1 - t0:.1f} s)"}
+    prm = m._params[0].struct
+    xs = x[:, rows].detach().contiguous().cpu().numpy()
+    o = LO.forward_quant(Wi, Wh, bi, bh, xs, prm, mode=LO.ACT_CR)
+    _check_equal("lstm output", out[:, rows].detach().cpu().numpy(), o["output"])
+    gr = LO.backward_quant(o, prm, g[:, rows].detach().contiguous().cpu().numpy())
+    err = _check_close("lstm dx", xl.grad[:, rows].cpu().numpy(), gr["dx"])
+    return {"sequences": list(rows), "forward": "bit-exact", "dx_max_abs_err_rel": err,
+            "grads_finite": True}
 
 
-def _gru_cpu_baseline(m, x, rows: int = 32):
-    """CPU oracle (C, one thread) on the first `rows` sequences of c3: the same QAT
-    forward+backward of both directions with the module's own grids."""
+def _timed_cpu(fn, budget_s: float):
+    """Run fn until about budget_s seconds have passed (at least once); seconds per call."""
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        reps += 1
+        dt = time.perf_counter() - t0
+        if dt >= budget_s:
+            return dt / reps, reps
+
+
+def _gru_cpu_baseline(m, x, rows: int, batch_first: bool, what: str, budget_s: float = 12.0):
+    """The reference's own CPU PTQ forward (quantGRUForwardCPU, integer carrier; src/
+    gru_host.cc:161-252, gru_forward_cpu_quant.cc), compiled from its sources into
+    oracle/_ref, over every direction of the first `rows` sequences, with the module's
+    calibrated ranges and bit-width configuration.  The reference has no CPU QAT
+    (quant_gru.py:2171-2173), so this is forward only.  Without oracle/_ref: the C oracle's
+    FP-carrier QAT forward+backward (kind "port")."""
     import numpy as np
 
     import gru_oracle as GO
 
-    xs = x[:rows].detach().transpose(0, 1).contiguous().cpu().numpy()  # [T, rows, I]
+    xt = x.detach().transpose(0, 1) if batch_first else x.detach()
+    xs = xt[:, :rows].contiguous().cpu().numpy()
     T, Bs, I = xs.shape
     H = m.hidden_size
-    dirs = []
-    for d, qp in enumerate((m.quant_params, m.quant_params_reverse)):
-        sfx = "_reverse" if d else ""
-        p = lambda n: getattr(m, n + sfx).detach().cpu().numpy()
-
-        def swap(t):
-            r, z, n = np.split(t, 3, axis=0)
-            return np.concatenate([z, r, n], 0)
-
-        W = np.ascontiguousarray(swap(p("weight_ih_l0")).T)
-        R = np.ascontiguousarray(swap(p("weight_hh_l0")).T)
-        dirs.append((W, R, swap(p("bias_ih_l0")), swap(p("bias_hh_l0")), qp.struct,
-                     np.ascontiguousarray(xs[::-1]) if d else xs))
-    gscale = np.float32(1.0 / (x.shape[0] * T * 2 * H))
+    dirs = _gru_dirs_haste(m)
+    if GO.has_ref():
+        def run():
+            for d, (W, R, bw, br, _, rg, cfg) in enumerate(dirs):
+                GO.ref_forward_ptq(W, R, bw, br, np.ascontiguousarray(xs[::-1]) if d else xs, rg,
+                                   cfg)
+        dt, reps = _timed_cpu(run, budget_s)
+        return {"value": round(Bs / dt, 3), "unit": "seq/s", "cores": 1, "kind": "reference",
+                "sample": f"{what}: the reference's quantGRUForwardCPU (integer-carrier PTQ "
+                          f"forward, {len(dirs)} direction(s)) on {Bs} sequences (T={T}, I={I}, "
+                          f"H={H}), one thread, {reps} run(s) of {dt:.2f} s; forward only: "
+                          f"the reference has no CPU QAT",
+                **_host_info()}
     dh = np.zeros((T + 1, Bs, H), np.float32)
-    dh[1:] = gscale
-    t0 = time.perf_counter()
-    for W, R, bw, br, qp, xd in dirs:
-        fwd = GO.forward_quant(W, R, bw, br, xd, qp, training=True)
-        GO.backward_quant(fwd, dh, qp)
-    dt = time.perf_counter() - t0
+    dh[1:] = 1e-6
+
+    def run_port():
+        for d, (W, R, bw, br, qp, _, _) in enumerate(dirs):
+            fwd = GO.forward_quant(W, R, bw, br, np.ascontiguousarray(xs[::-1]) if d else xs, qp,
+                                   training=True)
+            GO.backward_quant(fwd, dh, qp)
+    dt, reps = _timed_cpu(run_port, budget_s)
     return {"value": round(Bs / dt, 3), "unit": "seq/s", "cores": 1, "kind": "port",
-            "sample": f"c3 QAT fwd+bwd of both directions on {Bs} of the 256 sequences "
-                      f"(T={T}, I={I}, H={H}), C oracle, one thread, {dt:.1f} s"}
+            "sample": f"{what}: C oracle QAT forward+backward on {Bs} sequences, one thread",
+            **_host_info()}
 
 
-def _qdq_cpu_baseline():
-    """Oracle (numpy, one thread) on a 1024-row sample of c2, fwd+bwd, GB/s formula of c2."""
+def _lstm_cpu_baseline(m, x, rows: int = 16, budget_s: float = 12.0):
+    """The reference's own CPU q-carrier forward (lstmForwardQuantizedFpCpuReference,
+    src/lstm/forward_quantized_fp_cpu.cc, compiled into oracle/_ref) on the first `rows`
+    sequences of c4 with the module's grids; forward only (no CPU QAT in the reference,
+    quant_lstm.py:751-756).  Without oracle/_ref: the C oracle's forward+backward."""
     import numpy as np
 
+    import lstm_oracle as LO
+
+    xs = x[:, :rows].detach().contiguous().cpu().numpy()
+    Wi, Wh, bi, bh = (p.detach().cpu().numpy() for p in m._direction_params(False))
+    prm = m._params[0].struct
+    T, Bs, I = xs.shape
+    if LO.has_ref():
+        dt, reps = _timed_cpu(lambda: LO.ref_forward_fp(Wi, Wh, bi, bh, xs, prm), budget_s)
+        return {"value": round(Bs / dt, 3), "unit": "seq/s", "cores": 1, "kind": "reference",
+                "sample": f"c4: the reference's lstmForwardQuantizedFpCpuReference (q-carrier "
+                          f"forward) on {Bs} of the 512 sequences (T={T}, I={I}, "
+                          f"H={m.hidden_size}), one thread, {reps} run(s) of {dt:.2f} s; forward "
+                          f"only: the reference has no CPU QAT",
+                **_host_info()}
+    g = np.full((T, Bs, m.hidden_size), 1e-3, np.float32)
+
+    def run_port():
+        LO.backward_quant(LO.forward_quant(Wi, Wh, bi, bh, xs, prm, mode=LO.ACT_LIBM), prm, g)
+    dt, reps = _timed_cpu(run_port, budget_s)
+    return {"value": round(Bs / dt, 3), "unit": "seq/s", "cores": 1, "kind": "port",
+            "sample": f"c4: C oracle QAT forward+backward on {Bs} sequences, one thread",
+            **_host_info()}
+
+
+def _qdq_cpu_baseline(torch, budget_s: float = 8.0):
+    """The reference's QDQ step on the host, as aten on CPU tensors with every intra-op thread:
+    the learnable-encoding QuantDequantFunc forward+backward (torch_builtins.py:640-691)
+    restated as aten operations, on the full c2 tensor [8192, 8192]; the frozen path
+    (fake_quantize_per_tensor_affine forward + its STE backward, :287-361) reported beside it.
+    GB/s on c2's byte formula (20 bytes per element, fwd+bwd)."""
     import qdq_oracle as O
 
-    rows, cols = 1024, 8192
-    rng = np.random.default_rng(2)
-    x = rng.standard_normal((rows, cols)).astype(np.float32)
-    g = rng.standard_normal((rows, cols)).astype(np.float32)
-    s, o = O.scale_offset(np.array([-4.0], np.float32), np.array([4.2], np.float32), -128, 127,
-                          False)
-    layout = (1, 1, rows * cols)
-    t0 = time.perf_counter()
-    reps = 0
-    while time.perf_counter() - t0 < 10.0 or reps < 2:
-        O.qdq_learnable(x, s, o, -128, 127, layout)
-        O.qdq_learnable_backward(x, g, s, o, -128, 127, layout)
-        reps += 1
-    dt = (time.perf_counter() - t0) / reps
-    gbs = 20 * rows * cols / dt / 1e9
-    return {"value": round(gbs, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"c2 per-tensor 8-bit learnable QDQ fwd+bwd on a [{rows}, {cols}] slice, "
-                      f"numpy oracle, {reps} reps"}
+    R = Cc = 8192
+    torch.manual_seed(2)
+    x = torch.randn(R, Cc)
+    torch.manual_seed(5)
+    g = torch.randn(R, Cc)
+    s = torch.tensor(0.05)
+    o = torch.tensor(-3.0)
+    threads = torch.get_num_threads()
+    dt, reps = _timed_cpu(lambda: O.torch_learnable_step(torch, x, g, s, o, -128, 127), budget_s)
+    dtf, repsf = _timed_cpu(lambda: O.torch_frozen_step(torch, x, g, 0.05, 3, -128, 127),
+                            budget_s / 2)
+    n = R * Cc
+    return {"value": round(20 * n / dt / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": f"c2 per-tensor 8-bit learnable QDQ fwd+bwd on the full [{R}, {Cc}] tensor, "
+                      f"aten on CPU ({threads} threads), {reps} run(s) of {dt:.3f} s",
+            "frozen_fake_quantize_GB_s": round(20 * n / dtf / 1e9, 3),
+            "frozen_note": "the reference's own frozen-encoding path (aten "
+                           "fake_quantize_per_tensor_affine), same tensor and threads",
+            **_host_info()}
+
+
+def _c1_leg(torch, steps: int, warmup: int):
+    """c1: the PTQ calibration pass of a unidirectional QuantGRU (B=32, T=98, I=40, H=64):
+    MinMax calibration forward on the GPU, parameter derivation, then the PTQ (quantised,
+    eval) forward.  One step = that whole pass over the batch."""
+    import quant_gru as QG
+    import rxmet_gru_abi as A
+
+    dev = torch.device("cuda:0")
+    B, T, I, H = 32, 98, 40, 64
+    torch.manual_seed(1)
+    x = torch.randn(B, T, I)
+    m = QG.QuantGRU(I, H, batch_first=True)
+    torch.nn.init.xavier_uniform_(m.weight_ih_l0)
+    torch.nn.init.xavier_uniform_(m.weight_hh_l0)
+    m.set_all_bitwidth(8, is_symmetric=False)
+    for k in ("W_granularity_", "R_granularity_", "bw_granularity_", "br_granularity_"):
+        setattr(m._bitwidth_config, k, A.PER_TENSOR)
+    m = m.to(dev).eval()
+    x = x.to(dev)
+    out = {}
+
+    def step():
+        with torch.no_grad():
+            m.use_quantization = False
+            with m.calibration_context():  # reset, MinMax forward, derive the grids
+                m(x)
+            m.use_quantization = True
+            out["y"] = m(x)[0]
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    per = []
+    for _ in range(steps):
+        t0 = time.perf_counter()
+        step()
+        torch.cuda.synchronize()
+        per.append(time.perf_counter() - t0)
+    dt = sum(per) / len(per)
+    per.sort()
+    _log(f"gru c1: {dt*1e3:.3f} ms per calibration + PTQ pass, {B/dt:.1f} seq/s")
+    return {"ms_per_step": dt * 1e3, "p50_ms": per[len(per) // 2] * 1e3, "seq_per_s": B / dt}, \
+        m, x, out["y"]
+
+
+def _validate_c1(m, x, y):
+    """The GPU's PTQ output of every c1 sequence equals the oracle's FP-carrier forward with the
+    module's grids, bit for bit."""
+    import numpy as np
+
+    import gru_oracle as GO
+
+    W, R, bw, br, qp, _, _ = _gru_dirs_haste(m)[0]
+    xs = x.detach().transpose(0, 1).contiguous().cpu().numpy()
+    fwd = GO.forward_quant(W, R, bw, br, xs, qp, training=False)
+    _check_equal("c1 PTQ output", y.transpose(0, 1).cpu().numpy(), fwd["h"][1:])
+    return {"sequences": "all 32", "forward": "bit-exact"}
+
+
+def _c1_cpu_baseline(m, x, budget_s: float = 10.0):
+    """The reference's own CPU PTQ calibration pass on the whole c1 batch: forwardWithCalibrationCPU
+    (src/gru_forward_cpu.cc:58-151), calculateGRUQuantitativeParameters (src/gru_host.cc:13-124)
+    and the PTQ forward quantGRUForwardCPU (:161-252), compiled into oracle/_ref; one thread
+    (the reference has no OpenMP there).  Without oracle/_ref: the C oracle's calibration and
+    FP-carrier forward."""
+    import numpy as np
+
+    import gru_oracle as GO
+    import rxmet_gru_abi as A
+
+    W, R, bw, br, qp, _, cfg = _gru_dirs_haste(m)[0]
+    xs = x.detach().transpose(0, 1).contiguous().cpu().numpy()
+    T, B, I = xs.shape
+    H = m.hidden_size
+    ref = GO.has_ref()
+
+    def run():
+        _, _, stats = GO.forward_calibrate(W, R, bw, br, xs, ref=ref)
+        ranges = A.make_ranges(stats, H)
+        if ref:
+            GO.ref_forward_ptq(W, R, bw, br, xs, ranges, cfg)
+        else:
+            q, _ = GO.make_params(ranges, cfg)
+            GO.forward_quant(W, R, bw, br, xs, q, training=False)
+    dt, reps = _timed_cpu(run, budget_s)
+    return {"value": round(B / dt, 3), "unit": "seq/s", "cores": 1,
+            "kind": "reference" if ref else "port",
+            "sample": f"c1: {'the reference' if ref else 'C oracle'} calibration forward + "
+                      f"parameter derivation + PTQ forward on all {B} sequences (T={T}, I={I}, "
+                      f"H={H}), one thread, {reps} run(s) of {dt:.3f} s",
+            **_host_info()}
 
 
 def main() -> int:
@@ -471,9 +759,10 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--legs", default="gru,lstm,qdq",
-                    help="comma-separated subset of gru,lstm,qdq,c5 (profiling runs); the "
-                         "default record runs gru, lstm and qdq")
+    ap.add_argument("--no-validate", action="store_true",
+                    help="skip the oracle comparison of the benchmarked outputs (profiling runs)")
+    ap.add_argument("--legs", default="gru,lstm,qdq,c1,c5",
+                    help="comma-separated subset of gru,lstm,qdq,c1,c5")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run a plain elementwise copy over MIB MiB (scales HBM byte "
                          "counters in profiling runs)")
@@ -490,25 +779,53 @@ def main() -> int:
     _log(f"device: {torch.cuda.get_device_name(0)}")
     if args.copy_probe:
         _copy_probe(torch, args.copy_probe)
-    gru = roof = lstm = lstm_roof = qdq = qdq_roof = c5 = None
-    if "gru" in legs:
-        gru, roof, m, x = _gru_leg(torch, args.steps, args.warmup)
-    if "lstm" in legs:
-        lstm, lstm_roof, lm, lx, lg = _lstm_leg(torch, args.steps, args.warmup)
-    if "qdq" in legs:
-        qdq, qdq_roof = _qdq_leg(torch, args.steps, args.warmup)
-    if "c5" in legs:
-        c5 = _gru_c5_leg(torch, args.steps, args.warmup)
-    cpu = cpu_qdq = cpu_lstm = None
+    validate = not args.no_validate
+    checks = {}
+    gru = roof = lstm = lstm_roof = qdq = qdq_roof = c5 = c1 = None
+    try:
+        if "gru" in legs:
+            gru, roof, m, x = _gru_leg(torch, args.steps, args.warmup)
+            if validate:
+                checks["c3"] = _validate_gru(torch, m, x, [0, 255], batch_first=True)
+                _log(f"c3 validation: {checks['c3']}")
+        if "lstm" in legs:
+            lstm, lstm_roof, lm, lx, lg = _lstm_leg(torch, args.steps, args.warmup)
+            if validate:
+                checks["c4"] = _validate_lstm(torch, lm, lx, lg, [0, 511])
+                _log(f"c4 validation: {checks['c4']}")
+        if "qdq" in legs:
+            qdq, qdq_roof, qcheck = _qdq_leg(torch, args.steps, args.warmup, validate)
+            if qcheck is not None:
+                checks["c2"] = qcheck
+        if "c1" in legs:
+            c1, c1m, c1x, c1y = _c1_leg(torch, args.steps, args.warmup)
+            if validate:
+                checks["c1"] = _validate_c1(c1m, c1x, c1y)
+        if "c5" in legs:
+            c5, c5m, c5x = _gru_c5_leg(torch, args.steps, args.warmup)
+            if validate:
+                checks["c5"] = _validate_gru(torch, c5m, c5x, [1023], batch_first=False)
+                _log(f"c5 validation: {checks['c5']}")
+    except ValidationError as e:
+        print(f"bench.py: the benchmarked path failed its check: {e}", file=sys.stderr)
+        return 3
+    cpu = cpu_qdq = cpu_lstm = cpu_c1 = cpu_c5 = None
     if not args.no_cpu_baseline:
         if gru is not None:
-            cpu = _gru_cpu_baseline(m, x)
-            _log(f"cpu baseline: {cpu}")
+            cpu = _gru_cpu_baseline(m, x, 32, True, "c3")
+            _log(f"c3 cpu baseline: {cpu}")
         if lstm is not None:
-            cpu_lstm = _lstm_cpu_baseline(lm, lx, lg)
-            _log(f"lstm cpu baseline: {cpu_lstm}")
+            cpu_lstm = _lstm_cpu_baseline(lm, lx)
+            _log(f"c4 cpu baseline: {cpu_lstm}")
         if qdq is not None:
-            cpu_qdq = _qdq_cpu_baseline()
+            cpu_qdq = _qdq_cpu_baseline(torch)
+            _log(f"c2 cpu baseline: {cpu_qdq}")
+        if c1 is not None:
+            cpu_c1 = _c1_cpu_baseline(c1m, c1x)
+            _log(f"c1 cpu baseline: {cpu_c1}")
+        if c5 is not None:
+            cpu_c5 = _gru_cpu_baseline(c5m, c5x, 8, False, "c5", budget_s=8.0)
+            _log(f"c5 cpu baseline: {cpu_c5}")
     rnd = lambda d: None if d is None else {k: (round(v, 4) if isinstance(v, float) else v)
                                             for k, v in d.items()}
     line = {
@@ -532,7 +849,8 @@ def main() -> int:
                    "carrier": "fp32 codes; recurrent GEMMs on int8 MFMA"},
         "gru": rnd(gru),
         "lstm": rnd(lstm),
-        **({"gru_c5": rnd(c5)} if c5 is not None else {}),
+        "gru_c1": rnd(c1),
+        "gru_c5": rnd(c5),
         "qdq": None if qdq is None else {k: {kk: round(vv, 3) for kk, vv in v.items()}
                                          for k, v in qdq.items()},
         "roofline": roof,
@@ -541,6 +859,9 @@ def main() -> int:
         "cpu_baseline": cpu,
         "lstm_cpu_baseline": cpu_lstm,
         "qdq_cpu_baseline": cpu_qdq,
+        "c1_cpu_baseline": cpu_c1,
+        "c5_cpu_baseline": cpu_c5,
+        "validation": checks if validate else None,
     }
     print(json.dumps(line), flush=True)
     return 0

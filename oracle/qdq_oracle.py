@@ -216,3 +216,35 @@ def scale_offset(mn, mx, qmin: int, qmax: int, symmetric: bool, gpu_scalar_div: 
     else:
         o = np.clip(np.rint((mn / s).astype(f32)) - f32(qmin), -qmax, -qmin).astype(f32)
     return s, o
+
+
+# ---------------------------------------------------------------------------------
+# torch-on-CPU forms, for the CPU baseline (all intra-op threads)
+# ---------------------------------------------------------------------------------
+
+
+def torch_learnable_step(torch, x, g, scale, offset, qmin: int, qmax: int):
+    """QuantDequantFunc forward + backward (torch_builtins.py:640-691) as aten operations on
+    CPU tensors, the encoding gradients summed to the scale's shape as autograd does.
+    Returns (y, dx, dscale, doffset).  The same arithmetic as ``qdq_learnable`` and
+    ``qdq_learnable_backward`` (fp32 elementwise); the sums use aten's reduction order."""
+    xs = x / scale
+    rr = torch.round(xs)
+    r = rr - offset
+    mask = (r >= qmin) & (r <= qmax)
+    y = (r.clamp(qmin, qmax) + offset) * scale
+    mf = mask.to(x.dtype)
+    dx = g * mf
+    lo, hi = offset + qmin, offset + qmax
+    ds = (g * (torch.maximum(torch.minimum(rr, hi), lo) - xs * mf)).sum_to_size(scale.shape)
+    do = (g * ((1.0 - mf) * scale)).sum_to_size(offset.shape)
+    return y, dx, ds, do
+
+
+def torch_frozen_step(torch, x, g, scale: float, zero_point: int, qmin: int, qmax: int):
+    """The frozen-encoding path (torch_builtins.py:287-361): aten's
+    fake_quantize_per_tensor_affine forward and its STE backward, on CPU tensors."""
+    xg = x.detach().requires_grad_(True)
+    y = torch.fake_quantize_per_tensor_affine(xg, scale, zero_point, qmin, qmax)
+    y.backward(g)
+    return y.detach(), xg.grad

@@ -1,8 +1,9 @@
 // ref_shim.cpp — C entry points over the reference's own CPU QuantGRU code, compiled
 // from /root/reference/operators/quant-gru/src into oracle/_ref/libgru_ref.so by
-// oracle/Makefile.  TEST INFRASTRUCTURE: used only by tests/ (to pin the oracle's
-// parameter derivation, LUT generation and calibration forward) and by bench.py's
-// cpu_baseline leg.  Nothing here is part of the product.
+// oracle/Makefile.  TEST INFRASTRUCTURE: used by tests/ (to pin the oracle's parameter
+// derivation, LUT generation, calibration forward and the int-carrier agreement) and by
+// bench.py's CPU-baseline legs, which time the reference's calibration and PTQ forwards.
+// Nothing here is part of the product.
 #include <cstring>
 #include <stdexcept>
 

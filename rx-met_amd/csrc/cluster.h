@@ -144,6 +144,28 @@ __device__ __forceinline__ void store_bytes_coherent(unsigned char *dst4, int by
   }
 }
 
+// Every output of a computation whose recurrence timed out: up to 12 float buffers (null
+// entries are skipped), all overwritten with NaN when the flag is set.  Launched after the
+// last kernel that writes any of them, so nothing downstream of a stuck launch (weight and
+// input gradients built from partly written gate gradients included) can look finite.
+struct PoisonList {
+  float *p[12];
+  int64_t n[12];
+  int count;
+};
+
+[[maybe_unused]] static __global__ void poison_list(const int *timeout, PoisonList l) {
+  if (*timeout == 0) return;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int k = 0; k < l.count; ++k) {
+    float *p = l.p[k];
+    if (p == nullptr) continue;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < l.n[k];
+         i += stride)
+      p[i] = NAN;
+  }
+}
+
 // Launch a clustered recurrence.  The launch is cooperative, which guarantees that every
 // workgroup of the grid is resident at once.  With RXMET_PLAIN_LAUNCH set it is an ordinary
 // launch of the same grid (for profilers that cannot trace cooperative launches): residency

@@ -839,7 +839,7 @@ static int backward_prologue(int T, int B, int I, int H, const rxmet_gru_bwd_dir
 // Clustered recurrence over every direction; 1 when launched, 0 when the caller must use the
 // per-tile recurrence.
 static int backward_recurrence_clustered(BwdPlan *plans, int ndir, int T, int B, int I, int H,
-                                         hipStream_t stream) {
+                                         hipStream_t stream, int **timeout_flag) {
   const int C = 3 * H, KS2 = (C + 63) / 64;
   if (KS2 > kBwMaxKS2 || std::getenv("RXMET_NO_CLUSTER") != nullptr) return 0;
   const size_t lds_cl = bwd_cl_lds(KS2 * 64);
@@ -897,10 +897,7 @@ static int backward_recurrence_clustered(BwdPlan *plans, int ndir, int T, int B,
     RXMET_CHECK_HIP(cluster::launch(fn, dim3(ncl * cl.G), dim3(256 * cl.UT), args,
                                                static_cast<unsigned>(lds_cl), stream));
   }
-  hipLaunchKernelGGL(cluster::poison_nan2, dim3(64), dim3(256), 0, stream, cl.timeout,
-                     static_cast<int64_t>(B) * H, plans[0].ba.dh0,
-                     ndir > 1 ? plans[1].ba.dh0 : nullptr);
-  RXMET_CHECK_LAUNCH();
+  *timeout_flag = cl.timeout;
   return 1;
 }
 
@@ -1051,7 +1048,10 @@ static int backward_dirs(int ndir, int T, int B, int I, int H, const rxmet_gru_b
   // H > 256 (more R values than the clustered and per-tile kernels keep in registers), or
   // RXMET_BWD_STEPPED set: one pointwise and one GEMM launch per step
   const bool stepped = H > 256 || std::getenv("RXMET_BWD_STEPPED") != nullptr;
-  const int rc = stepped ? 0 : backward_recurrence_clustered(plans, ndir, T, B, I, H, stream);
+  int *timeout_flag = nullptr;
+  const int rc = stepped ? 0
+                         : backward_recurrence_clustered(plans, ndir, T, B, I, H, stream,
+                                                         &timeout_flag);
   if (rc < 0) return rc;
   if (rc == 0)
     for (int k = 0; k < ndir; ++k)
@@ -1060,6 +1060,23 @@ static int backward_dirs(int ndir, int T, int B, int I, int H, const rxmet_gru_b
         return r;
   for (int k = 0; k < ndir; ++k)
     if (int r = backward_epilogue(T, B, I, H, plans[k], stream)) return r;
+  if (timeout_flag != nullptr) {
+    // a clustered wait that timed out: every gradient of every direction becomes NaN
+    const int C = 3 * H;
+    cluster::PoisonList pl{};
+    for (int k = 0; k < ndir; ++k) {
+      const rxmet_gru_bwd_dir &d = *plans[k].d;
+      float *ps[6] = {d.dx, d.dW, d.dR, d.dbw, d.dbr, d.dh0};
+      const int64_t ns[6] = {static_cast<int64_t>(T) * B * I, static_cast<int64_t>(I) * C,
+                             static_cast<int64_t>(H) * C, C, C, static_cast<int64_t>(B) * H};
+      for (int j = 0; j < 6; ++j) {
+        pl.p[pl.count] = ps[j];
+        pl.n[pl.count++] = ns[j];
+      }
+    }
+    hipLaunchKernelGGL(cluster::poison_list, dim3(256), dim3(256), 0, stream, timeout_flag, pl);
+    RXMET_CHECK_LAUNCH();
+  }
   return 0;
 }
 

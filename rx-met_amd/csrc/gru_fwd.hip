@@ -304,7 +304,27 @@ struct RecArgs {
   int8_t *hx;               // clustered path: [2][NPL][Bpad][H] exchanged h codes
   int wide_out;             // clustered path: outputs 16-byte aligned (H % 16 == 0), stored
                             // through the LDS staging area as 16-byte rows
+  int wide_acc;             // |R_q h| can reach 2^31: recombine the plane sums in int64
 };
+
+// R_q h of one element from its plane sums (exact).  With wide_acc clear the exact value fits
+// in int32 and the modular uint32 combination is exact; otherwise it is combined in int64.
+// Either way it is rounded once to fp32, as the exact sum of the oracle.
+template <int NPL>
+__device__ __forceinline__ float recombine_rh(int wide_acc, int lo, int hi, float plane_off,
+                                              float h_offset, float colsum) {
+  const int col = static_cast<int>(colsum);
+  if (NPL == 2) {
+    if (wide_acc)
+      return static_cast<float>(256LL * hi + lo + static_cast<long long>(static_cast<int>(plane_off)) * col);
+    return static_cast<float>(static_cast<int>(256u * static_cast<uint32_t>(hi) + static_cast<uint32_t>(lo) +
+                                               static_cast<uint32_t>(static_cast<int>(plane_off)) *
+                                                   static_cast<uint32_t>(col)));
+  }
+  return static_cast<float>(static_cast<int>(static_cast<uint32_t>(lo) +
+                                             static_cast<uint32_t>(static_cast<int>(h_offset)) *
+                                                 static_cast<uint32_t>(col)));
+}
 
 // R_q [H][3H] (fp32 codes) -> int8 B fragments of v_mfma_i32_16x16x64_i8:
 // frag[((ut * 3 + g) * KS + s) * 64 + lane] holds R[k][c] for c = g*H + 16*ut + lane % 16,
@@ -453,17 +473,9 @@ __global__ __launch_bounds__(512) void recurrence(RecArgs a, StepParams p) {
         float wx[3], rh[3];
 #pragma unroll
         for (int g = 0; g < 3; ++g) {
-          // R_q h = 256 R hi + R lo' + (128 + offset) colsum(R); the exact result fits in
-          // int32, so the (modular) unsigned combination is exact.
-          const uint32_t col = static_cast<uint32_t>(static_cast<int>(cst[u][g][6]));
-          uint32_t v_u;
-          if (NPL == 2)
-            v_u = 256u * static_cast<uint32_t>(acc[g][1][r]) + static_cast<uint32_t>(acc[g][0][r]) +
-                  static_cast<uint32_t>(static_cast<int>(plane_off)) * col;
-          else
-            v_u = static_cast<uint32_t>(acc[g][0][r]) +
-                  static_cast<uint32_t>(static_cast<int>(a.h_offset)) * col;
-          const float ghh = static_cast<float>(static_cast<int>(v_u));
+          // R_q h = 256 R hi + R lo' + (128 + offset) colsum(R)
+          const float ghh = recombine_rh<NPL>(a.wide_acc, acc[g][0][r], acc[g][NPL - 1][r],
+                                              plane_off, a.h_offset, cst[u][g][6]);
           const float gi = valid ? a.gih[stepC + oC + g * H] : 0.0f;
           float val = gi - cst[u][g][2];
           wx[g] = clamp_keep(rintf((val + cst[u][g][4]) * cst[u][g][0]) + p.zp_wx, p.wx, k_ih[g]);
@@ -733,15 +745,8 @@ __device__ __forceinline__ void recurrence_cl_pair(const RecArgs &a, const StepP
       float wx[3], rh[3];
 #pragma unroll
       for (int g = 0; g < 3; ++g) {
-        const uint32_t col = static_cast<uint32_t>(static_cast<int>(cst[g][6]));
-        uint32_t v_u;
-        if (NPL == 2)
-          v_u = 256u * static_cast<uint32_t>(sum[g][NPL - 1]) + static_cast<uint32_t>(sum[g][0]) +
-                static_cast<uint32_t>(static_cast<int>(plane_off)) * col;
-        else
-          v_u = static_cast<uint32_t>(sum[g][0]) +
-                static_cast<uint32_t>(static_cast<int>(a.h_offset)) * col;
-        const float ghh = static_cast<float>(static_cast<int>(v_u));
+        const float ghh = recombine_rh<NPL>(a.wide_acc, sum[g][0], sum[g][NPL - 1], plane_off,
+                                            a.h_offset, cst[g][6]);
         float val = gih[g] - cst[g][2];
         wx[g] = clamp_keep(rintf((val + cst[g][4]) * cst[g][0]) + p.zp_wx, p.wx, k_ih[g]);
         val = ghh - cst[g][3];
@@ -1081,6 +1086,14 @@ static int forward_prologue(bool training, int T, int B, int I, int H, const rxm
   const bool h_uns = gh.bits < 32 && gh.is_unsigned;
   ra.h_offset = h_uns ? std::ldexp(1.0f, gh.bits - 1) : 0.0f;
   plan->npl = (gh.bits <= 8) ? 1 : 2;
+  {
+    // bound of |R_q h| over the h grid and the R grid
+    const Bounds brq = bounds_of(params->chan_bits[RXMET_GRU_R], params->chan_unsigned[RXMET_GRU_R]);
+    const double rmax = std::max(std::fabs(brq.lo), std::fabs(brq.hi));
+    const Bounds bhq = bounds_of(gh.bits, gh.is_unsigned);
+    const double hmax = std::max(std::fabs(bhq.lo), std::fabs(bhq.hi));
+    ra.wide_acc = hmax * rmax * H >= 2147483648.0 ? 1 : 0;
+  }
   ra.gih = gih; ra.rfrag = rfrag; ra.chan = chan; ra.h0codes = h0codes; ra.hout = d.h; ra.v = d.v;
   ra.ih_m = d.ih_mask; ra.hh_m = d.hh_mask; ra.gin_m = d.gate_in_mask;
   ra.gout_m = d.gate_out_mask; ra.h_m = d.h_mask;
@@ -1160,9 +1173,15 @@ static int forward_recurrence_clustered(FwdPlan *plans, int ndir, int T, int B, 
     RXMET_CHECK_HIP(cluster::launch(fn, dim3(ncl * cl.G), dim3(256 * cl.UT), args,
                                                static_cast<unsigned>(lds_cl), stream));
   }
-  const int64_t n_h = static_cast<int64_t>(T + 1) * B * H;
-  hipLaunchKernelGGL(cluster::poison_nan2, dim3(64), dim3(256), 0, stream, cl.timeout, n_h,
-                     plans[0].ra.hout, ndir > 1 ? plans[1].ra.hout : nullptr);
+  // a wait that timed out: h and v of every direction become NaN
+  cluster::PoisonList pl{};
+  for (int k = 0; k < ndir; ++k) {
+    pl.p[pl.count] = plans[k].ra.hout;
+    pl.n[pl.count++] = static_cast<int64_t>(T + 1) * B * H;
+    pl.p[pl.count] = plans[k].ra.v;
+    pl.n[pl.count++] = static_cast<int64_t>(T) * B * 4 * H;
+  }
+  hipLaunchKernelGGL(cluster::poison_list, dim3(256), dim3(256), 0, stream, cl.timeout, pl);
   RXMET_CHECK_LAUNCH();
   return 1;
 }

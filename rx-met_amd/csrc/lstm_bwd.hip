@@ -774,6 +774,7 @@ int rxmet_lstm_backward_quant(int32_t T, int32_t B, int32_t I, int32_t H,
   ba.s_c = sp.c.dscale; ba.zp_c = sp.c.dzp; ba.s_t = sp.tanh_c.dscale; ba.zp_t = sp.tanh_c.dzp;
   ba.dli = dli; ba.dlh = dlh; ba.dh0 = dh0; ba.dc0 = dc0;
   bool clustered = false;
+  int *timeout_flag = nullptr;
   if (H % (2 * kBcUnits) == 0 && H / kBcUnits <= 2 * kBcHalf &&
       std::getenv("RXMET_NO_CLUSTER") == nullptr) {
     const void *fn = reinterpret_cast<const void *>(&lstm_bwd_recurrence_cl);
@@ -812,13 +813,7 @@ int rxmet_lstm_backward_quant(int32_t T, int32_t B, int32_t I, int32_t H,
         RXMET_CHECK_HIP(cluster::launch(fn, dim3(ncl * cl.G), dim3(512), args,
                                                    static_cast<unsigned>(lds_cl), stream));
       }
-      const int64_t n_state = static_cast<int64_t>(B) * H;
-      hipLaunchKernelGGL(cluster::poison_nan, dim3(64), dim3(256), 0, stream, cl.timeout, n_state,
-                         dh0);
-      RXMET_CHECK_LAUNCH();
-      hipLaunchKernelGGL(cluster::poison_nan, dim3(64), dim3(256), 0, stream, cl.timeout, n_state,
-                         dc0);
-      RXMET_CHECK_LAUNCH();
+      timeout_flag = cl.timeout;
       clustered = true;
     }
   }
@@ -870,6 +865,21 @@ int rxmet_lstm_backward_quant(int32_t T, int32_t B, int32_t I, int32_t H,
     hipLaunchKernelGGL(lstm_bwd_finish, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
                        nx, dx, sv.x_m, C, I, H, aug_ih, aug_hh, dW_ih, dW_hh, bias ? db_ih : nullptr,
                        bias ? db_hh : nullptr, sv.w_ih_m, sv.w_hh_m, sv.b_ih_m, sv.b_hh_m);
+    RXMET_CHECK_LAUNCH();
+  }
+  if (timeout_flag != nullptr) {
+    // a clustered wait that timed out: every gradient becomes NaN
+    const int64_t n_state = static_cast<int64_t>(B) * H;
+    cluster::PoisonList pl{};
+    float *ps[7] = {dx, dW_ih, dW_hh, bias ? db_ih : nullptr, bias ? db_hh : nullptr, dh0, dc0};
+    const int64_t ns[7] = {static_cast<int64_t>(M) * I, static_cast<int64_t>(C) * I,
+                           static_cast<int64_t>(C) * H, C, C, n_state, n_state};
+    for (int j = 0; j < 7; ++j) {
+      pl.p[j] = ps[j];
+      pl.n[j] = ns[j];
+    }
+    pl.count = 7;
+    hipLaunchKernelGGL(cluster::poison_list, dim3(256), dim3(256), 0, stream, timeout_flag, pl);
     RXMET_CHECK_LAUNCH();
   }
   return 0;

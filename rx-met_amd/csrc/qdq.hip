@@ -509,6 +509,13 @@ static int launch_backward_impl(const Plan &p, const float *x, const float *g, f
   return 0;
 }
 
+__global__ __launch_bounds__(256) void zero_enc_grads(int64_t C, float *dscale, float *doffset) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= C) return;
+  if (dscale) dscale[i] = 0.0f;
+  if (doffset) doffset[i] = 0.0f;
+}
+
 template <int OP>
 static int launch_backward(const float *x, const float *g, float *dx, float *dscale,
                            float *doffset, int64_t outer, int64_t C, int64_t inner,
@@ -518,9 +525,11 @@ static int launch_backward(const float *x, const float *g, float *dx, float *dsc
   const int64_t n = p.outer * p.C * p.inner;
   const bool enc = dscale != nullptr || doffset != nullptr;
   if (n == 0) {
-    if (enc) {
-      if (dscale) RXMET_CHECK_HIP(hipMemsetAsync(dscale, 0, sizeof(float) * C, stream));
-      if (doffset) RXMET_CHECK_HIP(hipMemsetAsync(doffset, 0, sizeof(float) * C, stream));
+    // zeroed by a kernel, not a memset node, so a captured training step replays correctly
+    if (enc && C > 0) {
+      hipLaunchKernelGGL(zero_enc_grads, dim3(static_cast<unsigned>((C + 255) / 256)), dim3(256), 0,
+                         stream, C, dscale, doffset);
+      RXMET_CHECK_LAUNCH();
     }
     return 0;
   }

@@ -146,6 +146,35 @@ def test_clustered_forward_matches_oracle_and_single_tile_path(cuda, shape, cfg_
         assert torch.equal(a, b), name
 
 
+@pytest.mark.parametrize("H", [512, 1024])
+def test_forward_recurrent_sums_beyond_int32_are_exact(cuda, H):
+    """A 16-bit unsigned h grid with 8-bit R: all-positive R columns (codes near 127) against
+    h0 saturated at the top code make |R_q h| about 65535 * 120 * H, beyond 2^31.  The
+    recurrent sums must still be the oracle's exact int64 sums rounded once to fp32."""
+    T, B, I = 3, 16, 8
+    print(f"[gru fwd wide sums] H={H}", flush=True)
+    g = np.random.default_rng(31)
+    W = ((g.random((I, 3 * H)) * 2 - 1) * 0.1).astype(f32)
+    R = (0.05 + 0.01 * g.random((H, 3 * H))).astype(f32)
+    bw = ((g.random(3 * H) * 2 - 1) * 0.1).astype(f32)
+    br = ((g.random(3 * H) * 2 - 1) * 0.1).astype(f32)
+    x = g.standard_normal((T, B, I)).astype(f32)
+    h0 = np.full((B, H), 50.0, f32)
+    _, _, stats = GO.forward_calibrate(W, R, bw, br, x, h0)
+    c = A.set_all_bitwidth(A.default_config(), 8, False)
+    c.op[A.GRID["h"]].bits = 16
+    c.op[A.GRID["h"]].is_unsigned = 1
+    qp, _ = GO.make_params(A.make_ranges(stats, H), c)
+    exp = GO.forward_quant(W, R, bw, br, x, qp, h0=h0, training=True)
+    hq = exp["h"][0] / GO.effective_scale(float(qp.g[A.GRID["h"]].scale), False) \
+        + qp.g[A.GRID["h"]].zero_point
+    rmax = np.abs(exp["R_q"]).sum(axis=0).max()
+    assert float(np.abs(hq).max()) * rmax >= 2 ** 31, "case does not exceed int32"
+    got = _gpu_forward(cuda, W, R, bw, br, x, h0, qp, True)
+    for name, tensor in zip(NAMES, got):
+        np.testing.assert_array_equal(tensor.cpu().numpy(), exp[name], err_msg=name)
+
+
 def test_forward_eval_matches_training_h(cuda):
     W, R, bw, br, x, h0, qp = _case(4, 16, 8, 32, "c3", 2, True)
     tr = _gpu_forward(cuda, W, R, bw, br, x, h0, qp, True)

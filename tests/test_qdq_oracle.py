@@ -177,6 +177,61 @@ def test_quantize_dequantize_gradients_match_autograd():
                                       s.reshape(1, 4, 1)).astype(f32).reshape(-1))
 
 
+@pytest.mark.parametrize("qmin,qmax", [(0, 255), (-128, 127), (-8, 7)])
+def test_quantize_gradients_match_autograd_surrogate(qmin, qmax):
+    """QuantizeFunc's backward (torch_builtins.py:554-571) against torch autograd through
+    q = clamp(ste_round(x/s) - o): float64 arithmetic, the forward's fp32 rounding decisions,
+    clamp's inclusive pass-through at the grid ends as the reference's mask."""
+    layout = (1, 4, 500)
+    x = _data(2000, 13)
+    g = np.random.default_rng(14).standard_normal(2000).astype(f32)
+    s = np.array([0.01, 0.02, 0.03, 0.05], f32)
+    o = np.array([-100, -128, -10, -200], f32) if qmin == 0 else np.zeros(4, f32)
+    gq, ds, do = O.quantize_backward(x, g, s, o, qmin, qmax, layout)
+    xt = torch.from_numpy(x.astype(np.float64)).view(1, 4, 500).requires_grad_()
+    st = torch.from_numpy(s.astype(np.float64)).view(1, 4, 1).requires_grad_()
+    ot = torch.from_numpy(o.astype(np.float64)).view(1, 4, 1).requires_grad_()
+    xs32 = (x.reshape(1, 4, 500) / s.reshape(1, 4, 1)).astype(f32)
+    rounded = torch.from_numpy(np.rint(xs32).astype(np.float64))
+    xs = xt / st
+    r = xs + (rounded - xs).detach() - ot
+    q = torch.clamp(r, qmin, qmax)
+    q.backward(torch.from_numpy(g.astype(np.float64)).view(1, 4, 500))
+    assert 0 < (gq == 0).mean() < 1, "case must clamp some elements and keep others"
+    np.testing.assert_allclose(gq, xt.grad.numpy().reshape(-1), rtol=1e-6)
+    sref = (np.abs(g) * np.abs(x)).reshape(1, 4, 500).sum(axis=(0, 2)) / s.astype(np.float64) ** 2
+    np.testing.assert_allclose(ds, st.grad.numpy().reshape(-1), rtol=0, atol=1e-6 * sref.max())
+    np.testing.assert_allclose(do, ot.grad.numpy().reshape(-1), rtol=1e-6, atol=1e-6)
+    np.testing.assert_array_equal(
+        O.quantize(x, s, o, qmin, qmax, layout),
+        np.clip(np.rint(xs32) - o.reshape(1, 4, 1), qmin, qmax).astype(f32).reshape(-1))
+
+
+@pytest.mark.parametrize("shape,bits", [((), 8), ((64, 1), 4)])
+def test_torch_cpu_step_matches_numpy_oracle(shape, bits):
+    """The torch-on-CPU form used as the QDQ CPU baseline computes what the oracle does:
+    y and dx bit for bit, the encoding gradients within summation-order noise."""
+    R, Cc = 64, 1000
+    rng = np.random.default_rng(21)
+    x = rng.standard_normal((R, Cc)).astype(f32)
+    g = rng.standard_normal((R, Cc)).astype(f32)
+    qmin, qmax = (-128, 127) if bits == 8 else (-8, 7)
+    n = 1 if shape == () else R
+    s = (rng.random(n) * 0.05 + 0.01).astype(f32)
+    o = (np.round(rng.random(n) * 10) - 5).astype(f32) if bits == 8 else np.zeros(n, f32)
+    layout = (1, 1, R * Cc) if shape == () else (1, R, Cc)
+    ey, _ = O.qdq_learnable(x, s, o, qmin, qmax, layout)
+    edx, eds, edo = O.qdq_learnable_backward(x, g, s, o, qmin, qmax, layout)
+    st = torch.from_numpy(s).reshape(shape)
+    ot = torch.from_numpy(o).reshape(shape)
+    y, dx, ds, do = O.torch_learnable_step(torch, torch.from_numpy(x), torch.from_numpy(g), st, ot,
+                                           qmin, qmax)
+    np.testing.assert_array_equal(y.numpy(), ey)
+    np.testing.assert_array_equal(dx.numpy(), edx)
+    np.testing.assert_allclose(ds.numpy().reshape(-1), eds, rtol=1e-4, atol=1e-3)
+    np.testing.assert_allclose(do.numpy().reshape(-1), edo, rtol=1e-4, atol=1e-3)
+
+
 def test_minimum_scale_table():
     # quantsim.py:463-470
     assert O.minimum_scale(15) == 2.0 ** -23
