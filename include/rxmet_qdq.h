@@ -84,6 +84,31 @@ int rxmet_qdq_backward(const float *x, const float *g, float *dx, float *dscale,
                        int mode, void *workspace, void *stream);
 
 /*
+ * Size of the device scratch array rxmet_qdq_backward_noalloc works in (4 MiB: the
+ * encoding-gradient partials of tensors up to about 2^31 elements in the per-tensor case).
+ */
+#define RXMET_QDQ_NOALLOC_SCRATCH_BYTES (4LL << 20)
+
+/*
+ * rxmet_qdq_backward without a workspace argument and without any device allocation: the
+ * partial sums of the encoding gradients live in a 4 MiB file-scope device array
+ * (RXMET_QDQ_NOALLOC_SCRATCH_BYTES), one per GPU, held until the process ends.  No
+ * counterpart in the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments, kernels and results as rxmet_qdq_backward (bit for bit).
+ * Limits: a layout whose partials need more than the scratch (rxmet_qdq_workspace_bytes >
+ * RXMET_QDQ_NOALLOC_SCRATCH_BYTES) is rejected with -22 and a message; calls that overlap on
+ * one GPU (different streams, or host threads) share the array and race; the stream must
+ * belong to the current device.  Nothing in the array needs clearing between calls.  (The
+ * library's optional kernel timing, off unless rxmet_prof_enable turns it on, creates hipEvents;
+ * with it off this call makes no allocating call at all.)
+ */
+int rxmet_qdq_backward_noalloc(const float *x, const float *g, float *dx, float *dscale,
+                               float *doffset, int64_t outer, int64_t C, int64_t inner,
+                               const float *scale, const float *offset, int64_t qmin,
+                               int64_t qmax, int mode, void *stream);
+
+/*
  * Quantize forward: q = clamp(rint(x / s) - o, qmin, qmax) (codes as fp32).
  * Replaces QuantizeFunc.forward (torch_builtins.py:527-552).
  */

@@ -17,6 +17,9 @@
 // write one fp64 partial per workgroup (or per column and row-chunk) and a second
 // kernel folds the partials of each encoding in a fixed order, so results are
 // deterministic and need no atomics.
+#include <mutex>
+#include <string>
+
 #include "rxmet_common.h"
 #include "rxmet_qdq.h"
 
@@ -604,6 +607,40 @@ __global__ __launch_bounds__(256) void encoding_bwd(int64_t n, const float *__re
 using namespace rxmet;
 using namespace rxmet::qdq;
 
+namespace rxmet {
+namespace qdq {
+
+// Scratch of rxmet_qdq_backward_noalloc: the per-block partial sums of the encoding
+// gradients, in a file-scope device array instead of a caller workspace.  Each device holds
+// its own copy for the life of the process.  Every slot a call uses is written by its block
+// before the fold reads it, so nothing needs clearing between calls.
+constexpr int64_t kNoAllocScratchBytes = RXMET_QDQ_NOALLOC_SCRATCH_BYTES;
+__device__ __align__(256) double2 scratch[kNoAllocScratchBytes / sizeof(double2)];
+
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mu;
+void *scratch_dev[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device, looked up once per device (the array's
+// host-side name is not a device address).
+static int scratch_address(void **out) {
+  int dev = 0;
+  RXMET_CHECK_HIP(hipGetDevice(&dev));
+  RXMET_CHECK_ARG(dev >= 0 && dev < kMaxDevices, "device ordinal out of range");
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (scratch_dev[dev] == nullptr) {
+    void *p = nullptr;
+    RXMET_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    RXMET_CHECK_ARG(p != nullptr, "hipGetSymbolAddress returned no address for the scratch array");
+    scratch_dev[dev] = p;
+  }
+  *out = scratch_dev[dev];
+  return 0;
+}
+
+}  // namespace qdq
+}  // namespace rxmet
+
 extern "C" {
 
 int64_t rxmet_qdq_workspace_bytes(int64_t outer, int64_t C, int64_t inner) {
@@ -676,6 +713,31 @@ int rxmet_qdq_backward(const float *x, const float *g, float *dx, float *dscale,
   }
   set_error("unknown qdq mode");
   return -22;
+}
+
+int rxmet_qdq_backward_noalloc(const float *x, const float *g, float *dx, float *dscale,
+                               float *doffset, int64_t outer, int64_t C, int64_t inner,
+                               const float *scale, const float *offset, int64_t qmin,
+                               int64_t qmax, int mode, void *stream) {
+  clear_error();
+  if (int rc = check_layout(outer, C, inner)) return rc;
+  if (int rc = check_grid(qmin, qmax)) return rc;
+  RXMET_CHECK_ARG(scale != nullptr, "scale must be non-null");
+  RXMET_CHECK_ARG(mode == RXMET_QDQ_LEARNABLE || mode == RXMET_QDQ_FROZEN, "unknown qdq mode");
+  void *ws = nullptr;
+  if ((dscale != nullptr || doffset != nullptr) && outer * inner > 0) {
+    const int64_t need = rxmet_qdq_workspace_bytes(outer, C, inner);
+    if (need > kNoAllocScratchBytes) {
+      set_error("rxmet_qdq_backward_noalloc: the encoding-gradient partials of this layout need " +
+                std::to_string(need) + " bytes, more than the " +
+                std::to_string(kNoAllocScratchBytes) +
+                "-byte scratch; call rxmet_qdq_backward with a workspace instead");
+      return -22;
+    }
+    if (int rc = scratch_address(&ws)) return rc;
+  }
+  return rxmet_qdq_backward(x, g, dx, dscale, doffset, outer, C, inner, scale, offset, qmin, qmax,
+                            mode, ws, stream);
 }
 
 int rxmet_quantize_forward(const float *x, float *q, int64_t outer, int64_t C, int64_t inner,

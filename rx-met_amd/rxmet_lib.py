@@ -32,6 +32,8 @@ _SIGNATURES = {
                                   c_int, c_ptr]),
     "rxmet_qdq_backward": (c_int, [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_ptr,
                                    c_ptr, c_i64, c_i64, c_int, c_ptr, c_ptr]),
+    "rxmet_qdq_backward_noalloc": (c_int, [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64,
+                                           c_ptr, c_ptr, c_i64, c_i64, c_int, c_ptr]),
     "rxmet_quantize_forward": (c_int, [c_ptr, c_ptr, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_i64,
                                        c_i64, c_ptr]),
     "rxmet_quantize_backward": (c_int, [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64,

@@ -40,3 +40,20 @@ def test_host_only_calls_work_without_gpu():
     # [8192, 8192] per-channel on dim 0: one partial per channel row
     assert lib.rxmet_qdq_workspace_bytes(1, 8192, 8192) == 8192 * 16
     assert lib.rxmet_qdq_workspace_bytes(1, 1, 8192 * 8192) == 8192 * 16
+
+
+def test_noalloc_backward_rejects_layouts_beyond_its_scratch():
+    """The size check of rxmet_qdq_backward_noalloc runs on the host before any device call:
+    a layout whose partials exceed the 4 MiB scratch returns -22 with a message, no GPU needed."""
+    import ctypes
+
+    lib = rxmet_lib.load()
+    buf = (ctypes.c_float * 4)()
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    n = 1 << 33  # per-tensor: 2^33 / 8192 partials of 16 bytes = 16 MiB
+    need = lib.rxmet_qdq_workspace_bytes(1, 1, n)
+    assert need > 4 << 20
+    rc = lib.rxmet_qdq_backward_noalloc(p, p, p, p, p, 1, 1, n, p, p, -128, 127, 0, None)
+    assert rc == -22
+    msg = lib.rxmet_last_error().decode()
+    assert "scratch" in msg and str(need) in msg, msg
