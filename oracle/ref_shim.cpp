@@ -203,7 +203,9 @@ int ref_gru_forward_ptq(int T, int B, int I, int H, const float *W, const float 
       cmax[k]->assign(r->chan_max[k], r->chan_max[k] + C);
     }
     GRUQuantParams p = calculateGRUQuantitativeParameters(rq, config_of(*c));
-    quantGRUForwardCPU(false, T, B, I, H, W, R, bw, br, x, h0, p, h, v);
+    // the reference writes v (gate codes, dequantised) only in training mode, the only
+    // difference training makes to its CPU forward (gru_forward_cpu_quant.cc:199)
+    quantGRUForwardCPU(v != nullptr, T, B, I, H, W, R, bw, br, x, h0, p, h, v);
     return 0;
   } catch (const std::exception &) {
     return -1;

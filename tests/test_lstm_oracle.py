@@ -494,3 +494,165 @@ def test_cr_mode_sums_are_order_free():
     wq = o["w_hh_q"]
     assert np.abs(hc[0] @ wq.T.astype(np.float64)).max() > 2 ** 24 or \
         np.abs(np.cumsum(hc[0][:, None, :] * wq[None], axis=-1)).max() > 2 ** 24
+
+
+# --------------------------------------------------------------------------------------
+# masks: an independent restatement of the q-carrier forward that takes each mask at its
+# own clamp
+# --------------------------------------------------------------------------------------
+
+
+def _np_qcarrier(Wi, Wh, bi, bh, x, h0, c0, p, ex, mode):
+    """The reference's FP32 q-carrier forward restated in numpy from its CPU source:
+    masters (quantizeFp: RNE(double(v) / double(s)) + zp, clamped), linearValue
+    (forward_quantized_fp_cpu.cc:18-44, exact centred sums as the GPU-semantics mode),
+    gate inputs (:116-129), the cell and hidden cores (quantized_cell_fp.h:74-141) and the
+    rescale cores (float_carrier_ops.h:81-90); the activation is the oracle's single-value
+    realActivation (pinned by the reference's golden boundary vectors).  Each mask is taken
+    where its value is clamped: 1 = clamped (the CUDA kernels' convention)."""
+    T, B, I = x.shape
+    H = Wh.shape[1]
+    C = 4 * H
+    cfg = p.config
+    op = lambda n: cfg.op[L.OP[n]]
+
+    def grid(n):
+        o = op(n)
+        if o.is_unsigned:
+            return 0.0, float(2 ** o.bits - 1)
+        return float(-2 ** (o.bits - 1)), float(2 ** (o.bits - 1) - 1)
+
+    def clampm(v, n):
+        lo, hi = grid(n)
+        v = np.asarray(v, np.float64)
+        return np.clip(v, lo, hi).astype(f32), ((v < lo) | (v > hi)).astype(np.uint8)
+
+    S = lambda n: p.scale[L.OP[n]]
+    Z = lambda n: p.zero_point[L.OP[n]]
+
+    def master(v, s, zp, n):
+        return clampm(np.rint(np.asarray(v, np.float64) / np.float64(s)) + zp, n)
+
+    def R(v, enc):
+        is_m, mult, sh = enc
+        v = np.asarray(v, f32)
+        if is_m:
+            v = (v * f32(mult)).astype(f32)
+        return np.rint(np.ldexp(v, -sh).astype(f32)).astype(f32)
+
+    cs = lambda k: L.chan_scales(p, k)
+    xq, xm = master(x, S("input"), Z("input"), "input")
+    wiq, wim = master(Wi, cs(0)[:, None], 0, "weight_ih")
+    whq, whm = master(Wh, cs(1)[:, None], 0, "weight_hh")
+    biq = bim = bhq = bhm = None
+    if bi is not None:
+        biq, bim = master(bi, cs(2), 0, "bias_ih")
+        bhq, bhm = master(bh, cs(3), 0, "bias_hh")
+    hq, h0m = master(np.zeros((B, H), f32) if h0 is None else h0, S("output"), Z("output"), "output")
+    cq, c0m = master(np.zeros((B, H), f32) if c0 is None else c0, S("cell_state"), Z("cell_state"),
+                     "cell_state")
+    acc_enc = [ex["acc_to_linear"][:C], ex["acc_to_linear"][C:]]
+    bias_enc = None if bi is None else [ex["bias_to_acc"][:C], ex["bias_to_acc"][C:]]
+
+    def linear(v, vzp, w, b, l, out):
+        acc = ((v.astype(np.float64) - vzp) @ w.astype(np.float64).T).astype(f32)
+        if b is not None:
+            acc = (acc + np.array([R(b[c], bias_enc[l][c]) for c in range(C)], f32)).astype(f32)
+        r = np.stack([R(acc[:, c], acc_enc[l][c]) for c in range(C)], -1)
+        return clampm(r.astype(np.float64) + Z(out), out)
+
+    act_cache = {}
+
+    def act(q, inp, out, tanh):
+        key = (inp, out)
+        tab = act_cache.setdefault(key, {})
+        vals = np.empty(q.shape, f32)
+        msk = np.empty(q.shape, np.uint8)
+        for i, v in np.ndenumerate(q):
+            if v not in tab:
+                tab[v] = O.real_activation(v, S(inp), Z(inp), S(out), Z(out), op(out), tanh, mode)
+            vals[i], msk[i] = tab[v][0], tab[v][1]
+        return vals, msk
+
+    def q31(v, enc):
+        mult, mant, expo, uses_fp = enc
+        if uses_fp:
+            return np.ldexp(v.astype(np.float64) * mant, expo).astype(f32)
+        return (v * np.ldexp(f32(mult), -31).astype(f32)).astype(f32)
+
+    gates = ("input_gate", "forget_gate", "cell_gate", "output_gate")
+    rec = {k: [] for k in ("ih_linear_m", "hh_linear_m", "gate_in_m", "gate_out_m", "cell_m",
+                           "cell_tanh_m", "hidden_m", "gate_out", "cell", "cell_tanh", "hidden")}
+    for t in range(T):
+        li, mli = linear(xq[t], Z("input"), wiq, biq, 0, "weight_ih_linear")
+        lh, mlh = linear(hq, Z("output"), whq, bhq, 1, "weight_hh_linear")
+        gin, gout, mgi, mgo = [], [], [], []
+        for gi, gname in enumerate(gates):
+            sl = slice(gi * H, (gi + 1) * H)
+            lhs = R(li[:, sl] - f32(Z("weight_ih_linear")), ex["linear_to_gate"][gi])
+            rhs = R(lh[:, sl] - f32(Z("weight_hh_linear")), ex["linear_to_gate"][4 + gi])
+            q, m = clampm((lhs + rhs).astype(f32).astype(np.float64) + Z(gname + "_input"),
+                          gname + "_input")
+            a, am = act(q, gname + "_input", gname + "_output", gi == 2)
+            gin.append(q); mgi.append(m); gout.append(a); mgo.append(am)
+        cen = lambda v, n: (np.asarray(v, np.float64) - Z(n)).astype(f32)
+        pf = (cen(gout[1], "forget_gate_output") * cen(cq, "cell_state")).astype(f32)
+        pi = (cen(gout[0], "input_gate_output") * cen(gout[2], "cell_gate_output")).astype(f32)
+        pre = (q31(pf, ex["cell"][0]) + q31(pi, ex["cell"][1])).astype(f32)
+        cq, mc = clampm(np.rint(pre).astype(np.float64) + Z("cell_state"), "cell_state")
+        tq, mt = act(cq, "cell_state", "cell_tanh_output", True)
+        raw = (cen(gout[3], "output_gate_output") * cen(tq, "cell_tanh_output")).astype(f32)
+        hq, mh = clampm(R(raw, ex["hidden"][0]).astype(np.float64) + Z("output"), "output")
+        for k, v in (("ih_linear_m", mli), ("hh_linear_m", mlh),
+                     ("gate_in_m", np.concatenate(mgi, -1)), ("gate_out_m", np.concatenate(mgo, -1)),
+                     ("cell_m", mc), ("cell_tanh_m", mt), ("hidden_m", mh),
+                     ("gate_out", np.concatenate(gout, -1)), ("cell", cq), ("cell_tanh", tq),
+                     ("hidden", hq)):
+            rec[k].append(v)
+    out = {k: np.stack(v) for k, v in rec.items()}
+    out.update({"x_q": xq, "x_m": xm, "w_ih_q": wiq, "w_ih_m": wim, "w_hh_q": whq, "w_hh_m": whm,
+                "b_ih_q": biq, "b_ih_m": bim, "b_hh_q": bhq, "b_hh_m": bhm, "h0_m": h0m,
+                "c0_m": c0m})
+    return out
+
+
+_LSTM_MASKS = ("x_m", "w_ih_m", "w_hh_m", "b_ih_m", "b_hh_m", "h0_m", "c0_m", "ih_linear_m",
+               "hh_linear_m", "gate_in_m", "gate_out_m", "cell_m", "cell_tanh_m", "hidden_m")
+
+
+def _narrow_lstm(T, B, I, H, cfg_name, seed, shrink, cell_shrink=1.0):
+    (Wi, Wh, bi, bh, x, h0, c0), stats, cfg, _ = _calibrated(T, B, I, H, cfg_name, seed, True, True)
+    n = L.NOPS
+    stats[:n] *= shrink
+    stats[n:2 * n] *= shrink
+    stats[L.OP["cell_state"]] *= cell_shrink
+    stats[n + L.OP["cell_state"]] *= cell_shrink
+    stats[2 * n:2 * n + 8 * 4 * H] *= shrink
+    return (Wi, Wh, bi, bh, x, h0 * 2, c0 * 2), O.finalize(stats, cfg, H, True)
+
+
+@pytest.mark.parametrize("cfg_name", CONFIGS)
+@pytest.mark.parametrize("mode", [O.ACT_LIBM, O.ACT_CR])
+@pytest.mark.parametrize("cell_shrink", [1.0, 0.05])
+def test_masks_equal_independent_restatement(cfg_name, mode, cell_shrink):
+    """The oracle's codes and all fourteen mask families (masters, linear, gate input/output,
+    cell, cell tanh, hidden) equal an independent restatement that takes each mask at its own
+    clamp; ranges are narrowed so that clamps fire."""
+    T, B, I, H = 4, 3, 5, 8
+    (Wi, Wh, bi, bh, x, h0, c0), p = _narrow_lstm(T, B, I, H, cfg_name, 17, 0.6, cell_shrink)
+    exp = O.forward_quant(Wi, Wh, bi, bh, x, p, h0, c0, mode=mode)
+    got = _np_qcarrier(Wi, Wh, bi, bh, x, h0, c0, p, O.derive_exec(p, I), mode)
+    for k in ("gate_out", "cell", "cell_tanh", "hidden", "x_q", "w_ih_q", "w_hh_q", "b_ih_q",
+              "b_hh_q") + _LSTM_MASKS:
+        np.testing.assert_array_equal(got[k], exp[k], err_msg=k)
+
+
+def test_mask_restatement_cases_fire_every_family():
+    fired = set()
+    for cfg_name in CONFIGS:
+        for shrink, cell_shrink in ((0.6, 1.0), (0.3, 1.0), (0.6, 0.05)):
+            (Wi, Wh, bi, bh, x, h0, c0), p = _narrow_lstm(4, 3, 5, 8, cfg_name, 17, shrink,
+                                                          cell_shrink)
+            got = _np_qcarrier(Wi, Wh, bi, bh, x, h0, c0, p, O.derive_exec(p, 5), O.ACT_CR)
+            fired |= {k for k in _LSTM_MASKS if got[k].max() == 1}
+    assert fired == set(_LSTM_MASKS), sorted(set(_LSTM_MASKS) - fired)
