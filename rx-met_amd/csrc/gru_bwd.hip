@@ -763,8 +763,11 @@ static int backward_prologue(int T, int B, int I, int H, const rxmet_gru_bwd_dir
   RXMET_CHECK_ARG(d.W_q && d.R_q && d.x_q && d.dh_new && d.h && d.v && d.dx && d.dW && d.dR &&
                       d.dbw && d.dbr && d.dh0 && d.workspace,
                   "required pointer is null");
-  RXMET_CHECK_ARG(params->chan_bits[RXMET_GRU_R] <= 8 && !params->chan_unsigned[RXMET_GRU_R],
-                  "recurrent weights wider than signed 8 bits are not supported");
+  {
+    const Bounds brq = bounds_of(params->chan_bits[RXMET_GRU_R], params->chan_unsigned[RXMET_GRU_R]);
+    RXMET_CHECK_ARG(brq.lo >= -32768.0f && brq.hi <= 32767.0f,
+                    "recurrent weights must fit signed 16 bits");
+  }
   const int C = 3 * H;
   const int KS2 = (C + 63) / 64;
   const BwdWorkspace ws(T, B, I, H);
@@ -1053,10 +1056,15 @@ static int backward_dirs(int ndir, int T, int B, int I, int H, const rxmet_gru_b
                          : backward_recurrence_clustered(plans, ndir, T, B, I, H, stream,
                                                          &timeout_flag);
   if (rc < 0) return rc;
+  // the per-tile recurrence holds R as int8 fragments: wider recurrent weights step instead
+  bool wide_r = false;
+  for (int k = 0; k < ndir; ++k)
+    wide_r = wide_r || dirs[k].params->chan_bits[RXMET_GRU_R] > 8 ||
+             dirs[k].params->chan_unsigned[RXMET_GRU_R] != 0;
   if (rc == 0)
     for (int k = 0; k < ndir; ++k)
-      if (int r = stepped ? backward_recurrence_stepped(plans[k], T, B, I, H, stream)
-                          : backward_recurrence_tiles(plans[k], B, H, stream))
+      if (int r = (stepped || wide_r) ? backward_recurrence_stepped(plans[k], T, B, I, H, stream)
+                                      : backward_recurrence_tiles(plans[k], B, H, stream))
         return r;
   for (int k = 0; k < ndir; ++k)
     if (int r = backward_epilogue(T, B, I, H, plans[k], stream)) return r;

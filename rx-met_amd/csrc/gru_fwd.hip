@@ -363,6 +363,82 @@ __device__ __forceinline__ float pwl_eval(float q, const float *thr, const float
   return clamp_keep(val, ob, keep);
 }
 
+// One (sequence, unit) step of the FP carrier (gru_forward_gpu_quant_fp.cu:138-393): both
+// linears from their exact sums (zero-point and bias terms, rescale, clamp), the three gates
+// through the PWL LUTs (thresholds, slopes, offsets in lut_f, shifts in lut_n; 48 floats and
+// 16 ints per gate) and the hidden update, with the keep flag of every clamp.
+struct PointOut {
+  float h, z, r, n, rh_n;  // codes: new h, the gate outputs, the new gate's recurrent linear
+  uint8_t k_ih[3], k_hh[3], k_gi[3], k_go[3], k_h;
+};
+
+__device__ __forceinline__ PointOut gru_point(const float gih[3], const float ghh[3],
+                                              const float (&cst)[3][kChanParams],
+                                              const StepParams &p, const float *lut_f,
+                                              const int *lut_n, float hold) {
+  PointOut o;
+  float wx[3], rh[3];
+#pragma unroll
+  for (int g = 0; g < 3; ++g) {
+    float val = gih[g] - cst[g][2];
+    wx[g] = clamp_keep(rintf((val + cst[g][4]) * cst[g][0]) + p.zp_wx, p.wx, o.k_ih[g]);
+    val = ghh[g] - cst[g][3];
+    rh[g] = clamp_keep(rintf((val + cst[g][5]) * cst[g][1]) + p.zp_rh, p.rh, o.k_hh[g]);
+  }
+  // update gate
+  float in = rintf((wx[0] - p.zp_wx) * p.ih_to_zin) + rintf((rh[0] - p.zp_rh) * p.hh_to_zin);
+  in += p.zp_zin;
+  in = clamp_keep(in, p.zin, o.k_gi[0]);
+  o.z = pwl_eval(in, lut_f, lut_f + 16, lut_n, lut_f + 32, p.lut[0].zp_x, p.zout, o.k_go[0]);
+  // reset gate
+  in = rintf((wx[1] - p.zp_wx) * p.ih_to_rin) + rintf((rh[1] - p.zp_rh) * p.hh_to_rin);
+  in += p.zp_rin;
+  in = clamp_keep(in, p.rin, o.k_gi[1]);
+  o.r = pwl_eval(in, lut_f + 48, lut_f + 64, lut_n + 16, lut_f + 80, p.lut[1].zp_x, p.rout,
+                 o.k_go[1]);
+  // new gate
+  const float rmul = (o.r - p.zp_rout) * (rh[2] - p.zp_rh);
+  in = rintf((wx[2] - p.zp_wx) * p.ih_to_nin) + rintf(rmul * p.rmul_to_nin);
+  in += p.zp_nin;
+  in = clamp_keep(in, p.nin, o.k_gi[2]);
+  o.n = pwl_eval(in, lut_f + 96, lut_f + 112, lut_n + 32, lut_f + 128, p.lut[2].zp_x, p.nout,
+                 o.k_go[2]);
+  // hidden update
+  const float n_h = rintf((o.n - p.zp_nout) * p.nout_to_h) + p.zp_h;
+  const float oldc = (o.z - p.zp_zout) * (hold - p.zp_h);
+  const float newc = (p.quant_one - o.z) * (n_h - p.zp_h);
+  const float h2 = rintf((oldc + newc) * p.old_to_h) + p.zp_h;
+  o.h = clamp_keep(h2, p.h, o.k_h);
+  o.rh_n = rh[2];
+  return o;
+}
+
+// The outputs of one (step t, sequence b, unit j): dequantised h at row t + 1, and in
+// training v (z, r, n, hh_n dequantised) and the five mask families, one element at a time.
+__device__ __forceinline__ void store_point(const RecArgs &a, const StepParams &p, int t, int b,
+                                            int j, const PointOut &o) {
+  const uint32_t H = static_cast<uint32_t>(a.H), B = static_cast<uint32_t>(a.B), C = 3u * H;
+  const uint32_t stepH = static_cast<uint32_t>(t) * B * H;
+  const uint32_t oH = static_cast<uint32_t>(b) * H + j;
+  a.hout[stepH + B * H + oH] = (o.h - p.zp_h) * p.eff_h;
+  if (a.training) {
+    const uint32_t v0 = 4u * stepH + 4u * static_cast<uint32_t>(b) * H + j;
+    a.v[v0] = (o.z - p.zp_zout) * p.eff_zout;
+    a.v[v0 + H] = (o.r - p.zp_rout) * p.eff_rout;
+    a.v[v0 + 2 * H] = (o.n - p.zp_nout) * p.eff_nout;
+    a.v[v0 + 3 * H] = (o.rh_n - p.zp_rh) * p.eff_rh;
+    const uint32_t m = static_cast<uint32_t>(t) * B * C + 3u * static_cast<uint32_t>(b) * H + j;
+#pragma unroll
+    for (int g = 0; g < 3; ++g) {
+      a.ih_m[m + g * H] = o.k_ih[g];
+      a.hh_m[m + g * H] = o.k_hh[g];
+      a.gin_m[m + g * H] = o.k_gi[g];
+      a.gout_m[m + g * H] = o.k_go[g];
+    }
+    a.h_m[stepH + oH] = o.k_h;
+  }
+}
+
 // One workgroup = 16 sequences x all H units; wave w owns unit tiles 2w and 2w+1.
 // MFMA orientation: D[b][c] = h[b][:] . R[:, c]  (A = h planes from LDS, B = R_q fragments
 // resident in VGPRs), so lane l owns unit 16u + (l % 16) for batch rows 4 (l / 16) + r.
@@ -465,70 +541,17 @@ __global__ __launch_bounds__(512) void recurrence(RecArgs a, StepParams p) {
         const int b = b0 + nr;
         const bool valid = b < B;
         // 32-bit element offsets from uniform bases keep the per-row addressing cheap
-        const uint32_t oH = static_cast<uint32_t>(b) * H + j;          // [.., B, H]
-        const uint32_t oC = 3u * static_cast<uint32_t>(b) * H + j;     // [.., B, 3H]
-        const uint32_t o4 = 4u * static_cast<uint32_t>(b) * H + j;     // [.., B, 4H]
-        const uint32_t stepC = static_cast<uint32_t>(t) * B * C;
-        uint8_t k_ih[3], k_hh[3], k_gi[3], k_go[3], k_h;
-        float wx[3], rh[3];
+        float gi3[3], gh3[3];
 #pragma unroll
         for (int g = 0; g < 3; ++g) {
           // R_q h = 256 R hi + R lo' + (128 + offset) colsum(R)
-          const float ghh = recombine_rh<NPL>(a.wide_acc, acc[g][0][r], acc[g][NPL - 1][r],
-                                              plane_off, a.h_offset, cst[u][g][6]);
-          const float gi = valid ? a.gih[stepC + oC + g * H] : 0.0f;
-          float val = gi - cst[u][g][2];
-          wx[g] = clamp_keep(rintf((val + cst[u][g][4]) * cst[u][g][0]) + p.zp_wx, p.wx, k_ih[g]);
-          val = ghh - cst[u][g][3];
-          rh[g] = clamp_keep(rintf((val + cst[u][g][5]) * cst[u][g][1]) + p.zp_rh, p.rh, k_hh[g]);
+          gh3[g] = recombine_rh<NPL>(a.wide_acc, acc[g][0][r], acc[g][NPL - 1][r], plane_off,
+                                     a.h_offset, cst[u][g][6]);
+          gi3[g] = valid ? a.gih[(static_cast<size_t>(t) * B + b) * C + g * H + j] : 0.0f;
         }
-        // update gate
-        float in = rintf((wx[0] - p.zp_wx) * p.ih_to_zin) + rintf((rh[0] - p.zp_rh) * p.hh_to_zin);
-        in += p.zp_zin;
-        in = clamp_keep(in, p.zin, k_gi[0]);
-        const float z = pwl_eval(in, lut_f, lut_f + 16, lut_n, lut_f + 32, p.lut[0].zp_x, p.zout,
-                                 k_go[0]);
-        // reset gate
-        in = rintf((wx[1] - p.zp_wx) * p.ih_to_rin) + rintf((rh[1] - p.zp_rh) * p.hh_to_rin);
-        in += p.zp_rin;
-        in = clamp_keep(in, p.rin, k_gi[1]);
-        const float rr = pwl_eval(in, lut_f + 48, lut_f + 64, lut_n + 16, lut_f + 80, p.lut[1].zp_x,
-                                  p.rout, k_go[1]);
-        // new gate
-        const float rmul = (rr - p.zp_rout) * (rh[2] - p.zp_rh);
-        in = rintf((wx[2] - p.zp_wx) * p.ih_to_nin) + rintf(rmul * p.rmul_to_nin);
-        in += p.zp_nin;
-        in = clamp_keep(in, p.nin, k_gi[2]);
-        const float nn = pwl_eval(in, lut_f + 96, lut_f + 112, lut_n + 32, lut_f + 128,
-                                  p.lut[2].zp_x, p.nout, k_go[2]);
-        // hidden update
-        const float hold = hc[nr * H + j];
-        const float n_h = rintf((nn - p.zp_nout) * p.nout_to_h) + p.zp_h;
-        const float oldc = (z - p.zp_zout) * (hold - p.zp_h);
-        const float newc = (p.quant_one - z) * (n_h - p.zp_h);
-        float h2 = rintf((oldc + newc) * p.old_to_h) + p.zp_h;
-        h2 = clamp_keep(h2, p.h, k_h);
-
-        if (valid) {
-          const uint32_t stepH = static_cast<uint32_t>(t) * B * H;
-          a.hout[stepH + static_cast<uint32_t>(B) * H + oH] = (h2 - p.zp_h) * p.eff_h;
-          if (a.training) {
-            const uint32_t v0 = 4u * stepH + o4;
-            a.v[v0] = (z - p.zp_zout) * p.eff_zout;
-            a.v[v0 + H] = (rr - p.zp_rout) * p.eff_rout;
-            a.v[v0 + 2 * H] = (nn - p.zp_nout) * p.eff_nout;
-            a.v[v0 + 3 * H] = (rh[2] - p.zp_rh) * p.eff_rh;
-            const uint32_t m = stepC + oC;
-#pragma unroll
-            for (int g = 0; g < 3; ++g) {
-              a.ih_m[m + g * H] = k_ih[g];
-              a.hh_m[m + g * H] = k_hh[g];
-              a.gin_m[m + g * H] = k_gi[g];
-              a.gout_m[m + g * H] = k_go[g];
-            }
-            a.h_m[stepH + oH] = k_h;
-          }
-        }
+        const PointOut o = gru_point(gi3, gh3, cst[u], p, lut_f, lut_n, hc[nr * H + j]);
+        const float h2 = o.h;
+        if (valid) store_point(a, p, t, b, j, o);
         // next state into LDS
         hn[nr * H + j] = h2;
         const int hcv = static_cast<int>(h2 - a.h_offset);
@@ -542,6 +565,50 @@ __global__ __launch_bounds__(512) void recurrence(RecArgs a, StepParams p) {
     }
     __syncthreads();
   }
+}
+
+// ---------------------------------------------------------------------------------
+// 4a'. stepped recurrence (recurrent weights wider than 8 bits)
+// ---------------------------------------------------------------------------------
+// Per step one exact GEMM ghh = h_q R_q (xgemm::block: byte planes on int8 MFMA, combined in
+// int64, rounded once to fp32, as the oracle's exact sums) and one pointwise launch over all
+// (sequence, unit) pairs; the h codes go through two fp32 [B, H] buffers.
+template <int PA, int PB>
+__global__ __launch_bounds__(256) void step_rh_gemm(xgemm::Operands o, float *ghh) {
+  xgemm::block<PA, PB>(o, blockIdx.x * xgemm::kTile, blockIdx.y * xgemm::kTile,
+                       [&](int m, int n, long long sum) {
+                         ghh[static_cast<size_t>(m) * o.N + n] = static_cast<float>(sum);
+                       });
+}
+
+__global__ __launch_bounds__(256) void step_point(RecArgs a, StepParams p, int t, const float *ghh,
+                                                  const float *hcur, float *hnext) {
+  __shared__ float lut_f[3 * 48];
+  __shared__ int lut_n[3 * 16];
+  for (int i = threadIdx.x; i < 3 * 16; i += blockDim.x) {
+    const int g = i / 16, s = i % 16;
+    lut_f[g * 48 + s] = p.lut[g].thr[s];
+    lut_f[g * 48 + 16 + s] = p.lut[g].qb[s];
+    lut_f[g * 48 + 32 + s] = p.lut[g].c[s];
+    lut_n[g * 16 + s] = p.lut[g].n[s];
+  }
+  __syncthreads();
+  const int H = a.H, C = 3 * H;
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (e >= static_cast<int64_t>(a.B) * H) return;
+  const int b = static_cast<int>(e / H), j = static_cast<int>(e % H);
+  float gi[3], gh[3], cst[3][kChanParams];
+#pragma unroll
+  for (int g = 0; g < 3; ++g) {
+    const int c = g * H + j;
+    gi[g] = a.gih[(static_cast<size_t>(t) * a.B + b) * C + c];
+    gh[g] = ghh[static_cast<size_t>(b) * C + c];
+#pragma unroll
+    for (int q = 0; q < kChanParams; ++q) cst[g][q] = a.chan[q * C + c];
+  }
+  const PointOut o = gru_point(gi, gh, cst, p, lut_f, lut_n, hcur[e]);
+  hnext[e] = o.h;
+  store_point(a, p, t, b, j, o);
 }
 
 // ---------------------------------------------------------------------------------
@@ -737,42 +804,13 @@ __device__ __forceinline__ void recurrence_cl_pair(const RecArgs &a, const StepP
           sum[g][q] = v;
         }
       // pointwise update of (row b, unit j)
-      const uint32_t oH = static_cast<uint32_t>(b) * H + j;
-      const uint32_t oC = 3u * static_cast<uint32_t>(b) * H + j;
-      const uint32_t o4 = 4u * static_cast<uint32_t>(b) * H + j;
-      const uint32_t stepC = static_cast<uint32_t>(t) * B * C;
-      uint8_t k_ih[3], k_hh[3], k_gi[3], k_go[3], k_h;
-      float wx[3], rh[3];
+      float gh3[3];
 #pragma unroll
-      for (int g = 0; g < 3; ++g) {
-        const float ghh = recombine_rh<NPL>(a.wide_acc, sum[g][0], sum[g][NPL - 1], plane_off,
-                                            a.h_offset, cst[g][6]);
-        float val = gih[g] - cst[g][2];
-        wx[g] = clamp_keep(rintf((val + cst[g][4]) * cst[g][0]) + p.zp_wx, p.wx, k_ih[g]);
-        val = ghh - cst[g][3];
-        rh[g] = clamp_keep(rintf((val + cst[g][5]) * cst[g][1]) + p.zp_rh, p.rh, k_hh[g]);
-      }
-      float in = rintf((wx[0] - p.zp_wx) * p.ih_to_zin) + rintf((rh[0] - p.zp_rh) * p.hh_to_zin);
-      in += p.zp_zin;
-      in = clamp_keep(in, p.zin, k_gi[0]);
-      const float z = pwl_eval(in, lut_f, lut_f + 16, lut_n, lut_f + 32, p.lut[0].zp_x, p.zout,
-                               k_go[0]);
-      in = rintf((wx[1] - p.zp_wx) * p.ih_to_rin) + rintf((rh[1] - p.zp_rh) * p.hh_to_rin);
-      in += p.zp_rin;
-      in = clamp_keep(in, p.rin, k_gi[1]);
-      const float rr = pwl_eval(in, lut_f + 48, lut_f + 64, lut_n + 16, lut_f + 80, p.lut[1].zp_x,
-                                p.rout, k_go[1]);
-      const float rmul = (rr - p.zp_rout) * (rh[2] - p.zp_rh);
-      in = rintf((wx[2] - p.zp_wx) * p.ih_to_nin) + rintf(rmul * p.rmul_to_nin);
-      in += p.zp_nin;
-      in = clamp_keep(in, p.nin, k_gi[2]);
-      const float nn = pwl_eval(in, lut_f + 96, lut_f + 112, lut_n + 32, lut_f + 128,
-                                p.lut[2].zp_x, p.nout, k_go[2]);
-      const float n_h = rintf((nn - p.zp_nout) * p.nout_to_h) + p.zp_h;
-      const float oldc = (z - p.zp_zout) * (hold - p.zp_h);
-      const float newc = (p.quant_one - z) * (n_h - p.zp_h);
-      float h2 = rintf((oldc + newc) * p.old_to_h) + p.zp_h;
-      h2 = clamp_keep(h2, p.h, k_h);
+      for (int g = 0; g < 3; ++g)
+        gh3[g] = recombine_rh<NPL>(a.wide_acc, sum[g][0], sum[g][NPL - 1], plane_off, a.h_offset,
+                                   cst[g][6]);
+      const PointOut o = gru_point(gih, gh3, cst, p, lut_f, lut_n, hold);
+      const float h2 = o.h;
       hold = h2;
       {
         const int hcv = static_cast<int>(h2 - a.h_offset);
@@ -786,19 +824,19 @@ __device__ __forceinline__ void recurrence_cl_pair(const RecArgs &a, const StepP
         float *f = sf + nr * 5 * UW + jj;
         f[0] = (h2 - p.zp_h) * p.eff_h;
         if (a.training) {
-          f[UW] = (z - p.zp_zout) * p.eff_zout;
-          f[2 * UW] = (rr - p.zp_rout) * p.eff_rout;
-          f[3 * UW] = (nn - p.zp_nout) * p.eff_nout;
-          f[4 * UW] = (rh[2] - p.zp_rh) * p.eff_rh;
+          f[UW] = (o.z - p.zp_zout) * p.eff_zout;
+          f[2 * UW] = (o.r - p.zp_rout) * p.eff_rout;
+          f[3 * UW] = (o.n - p.zp_nout) * p.eff_nout;
+          f[4 * UW] = (o.rh_n - p.zp_rh) * p.eff_rh;
           uint8_t *m8 = sb + nr * 13 * UW + jj;
 #pragma unroll
           for (int g = 0; g < 3; ++g) {
-            m8[g * UW] = k_ih[g];
-            m8[(3 + g) * UW] = k_hh[g];
-            m8[(6 + g) * UW] = k_gi[g];
-            m8[(9 + g) * UW] = k_go[g];
+            m8[g * UW] = o.k_ih[g];
+            m8[(3 + g) * UW] = o.k_hh[g];
+            m8[(6 + g) * UW] = o.k_gi[g];
+            m8[(9 + g) * UW] = o.k_go[g];
           }
-          m8[12 * UW] = k_h;
+          m8[12 * UW] = o.k_h;
         }
       }
       // the other members only read the h codes: arrive now, store the outputs while waiting
@@ -833,24 +871,7 @@ __device__ __forceinline__ void recurrence_cl_pair(const RecArgs &a, const StepP
           flush_masks(a.h_m, 12, 1, sb, UW, bq, b0, B, H, member, stepH, (tid + nthr - (192 * bq) % nthr) % nthr, nthr);
         }
       } else if (valid) {
-        const uint32_t stepH = static_cast<uint32_t>(t) * B * H;
-        a.hout[stepH + static_cast<uint32_t>(B) * H + oH] = (h2 - p.zp_h) * p.eff_h;
-        if (a.training) {
-          const uint32_t v0 = 4u * stepH + o4;
-          a.v[v0] = (z - p.zp_zout) * p.eff_zout;
-          a.v[v0 + H] = (rr - p.zp_rout) * p.eff_rout;
-          a.v[v0 + 2 * H] = (nn - p.zp_nout) * p.eff_nout;
-          a.v[v0 + 3 * H] = (rh[2] - p.zp_rh) * p.eff_rh;
-          const uint32_t m = stepC + oC;
-#pragma unroll
-          for (int g = 0; g < 3; ++g) {
-            a.ih_m[m + g * H] = k_ih[g];
-            a.hh_m[m + g * H] = k_hh[g];
-            a.gin_m[m + g * H] = k_gi[g];
-            a.gout_m[m + g * H] = k_go[g];
-          }
-          a.h_m[stepH + oH] = k_h;
-        }
+        store_point(a, p, t, b, j, o);
       }
       if (t + 1 < a.T) load_gih(t + 1);
       alive = cluster::wait(counter, epoch * cl.G, cl.timeout);
@@ -891,7 +912,7 @@ size_t recurrence_lds_bytes(int H, int KS, int npl) {
 
 // Workspace layout of the forward (bytes, 256-aligned pieces).
 struct FwdWorkspace {
-  size_t gih, chan, h0codes, hostblk, rfrag, hx, sync, sparams, xa, bfrag, colsum, total;
+  size_t gih, chan, h0codes, hostblk, rfrag, hx, sync, sparams, xa, bfrag, colsum, sh, sg, total;
   FwdWorkspace(int T, int B, int I, int H) {
     const size_t C = 3 * static_cast<size_t>(H);
     const size_t Kp = static_cast<size_t>(xgemm::pad_k(I));
@@ -911,14 +932,22 @@ struct FwdWorkspace {
     xa = o; o += al(ip * 2 * static_cast<size_t>(T) * B * Kp);
     bfrag = o; o += al(ip * 2 * C * Kp);
     colsum = o; o += al(ip * sizeof(long long) * C);
+    // stepped recurrence: two h code buffers [B, H] and the recurrent sums [B, 3H]
+    sh = o; o += al(sizeof(float) * 2 * static_cast<size_t>(B) * H);
+    sg = o; o += al(sizeof(float) * static_cast<size_t>(B) * C);
     total = o;
   }
 };
 
+// Recurrent weights wider than signed 8 bits run on the stepped recurrence (two byte planes).
+static bool needs_stepped(const rxmet_gru_qparams &p) {
+  return p.chan_bits[RXMET_GRU_R] > 8 || p.chan_unsigned[RXMET_GRU_R] != 0;
+}
+
 static int host_bits_check(const rxmet_gru_qparams &p) {
-  RXMET_CHECK_ARG(p.chan_bits[RXMET_GRU_R] <= 8 && !p.chan_unsigned[RXMET_GRU_R],
-                  "recurrent weights wider than signed 8 bits are not supported by the MFMA "
-                  "recurrence");
+  const Bounds br = bounds_of(p.chan_bits[RXMET_GRU_R], p.chan_unsigned[RXMET_GRU_R]);
+  RXMET_CHECK_ARG(xgemm::b_fits(br.lo, br.hi),
+                  "recurrent weights must fit signed 16 bits");
   RXMET_CHECK_ARG(p.g[RXMET_GRU_H].bits <= 16, "hidden-state grids wider than 16 bits are not supported");
   RXMET_CHECK_ARG(p.g[RXMET_GRU_X].bits <= 16 && p.chan_bits[RXMET_GRU_W] <= 16,
                   "input or input-weight grids wider than 16 bits are not supported");
@@ -937,6 +966,8 @@ struct FwdPlan {
   RecArgs ra;
   StepParams sp;
   int npl;
+  bool stepped;  // recurrent weights wider than 8 bits: forward_recurrence_stepped
+  const float *rq;  // R_q codes [H, 3H]
   char *wsb;
 };
 
@@ -1078,9 +1109,12 @@ static int forward_prologue(bool training, int T, int B, int I, int H, const rxm
   RecArgs &ra = plan->ra;
   ra.T = T; ra.B = B; ra.H = H; ra.KS = (H + 63) / 64;
   v4i *rfrag = reinterpret_cast<v4i *>(wsb + ws.rfrag);
-  hipLaunchKernelGGL(pack_r_frags, dim3((H / 16) * 3 * ra.KS), dim3(64), 0, stream, H, ra.KS,
-                     d.R_q, rfrag);
-  RXMET_CHECK_LAUNCH();
+  plan->stepped = needs_stepped(*params) || std::getenv("RXMET_FWD_STEPPED") != nullptr;
+  if (!plan->stepped) {
+    hipLaunchKernelGGL(pack_r_frags, dim3((H / 16) * 3 * ra.KS), dim3(64), 0, stream, H, ra.KS,
+                       d.R_q, rfrag);
+    RXMET_CHECK_LAUNCH();
+  }
   ra.training = training ? 1 : 0;
   const rxmet_grid &gh = g[RXMET_GRU_H];
   const bool h_uns = gh.bits < 32 && gh.is_unsigned;
@@ -1106,6 +1140,7 @@ static int forward_prologue(bool training, int T, int B, int I, int H, const rxm
              a16(ra.gout_m) && a16(ra.h_m);
     ra.wide_out = wide ? 1 : 0;
   }
+  plan->rq = d.R_q;
   plan->wsb = wsb;
   return 0;
 }
@@ -1186,6 +1221,49 @@ static int forward_recurrence_clustered(FwdPlan *plans, int ndir, int T, int B, 
   return 1;
 }
 
+// The stepped recurrence of one direction: 2 T launches.
+static int forward_recurrence_stepped(FwdPlan &plan, const rxmet_gru_qparams &params, int T, int B,
+                                      int I, int H, hipStream_t stream) {
+  const int C = 3 * H;
+  const FwdWorkspace ws(T, B, I, H);
+  float *hb = reinterpret_cast<float *>(plan.wsb + ws.sh);
+  float *ghh = reinterpret_cast<float *>(plan.wsb + ws.sg);
+  const Bounds bh = bounds_of(params.g[RXMET_GRU_H].bits, params.g[RXMET_GRU_H].is_unsigned);
+  const Bounds br = bounds_of(params.chan_bits[RXMET_GRU_R], params.chan_unsigned[RXMET_GRU_R]);
+  RXMET_CHECK_ARG(xgemm::a_fits(bh.lo, bh.hi), "h codes must span at most 16 bits");
+  const int pa = xgemm::a_planes(bh.lo, bh.hi), pb = xgemm::b_planes(br.lo, br.hi);
+  xgemm::Operands o{};
+  o.M = B; o.N = C; o.K = H;
+  o.lda = H;
+  o.off = xgemm::a_shift(bh.lo, bh.hi);
+  o.corr = static_cast<long long>(o.off);  // raw codes: base 0
+  o.sbk = C; o.sbn = 1;
+  const dim3 ggrid((B + xgemm::kTile - 1) / xgemm::kTile, (C + xgemm::kTile - 1) / xgemm::kTile);
+  const int64_t n = static_cast<int64_t>(B) * H;
+  const dim3 pgrid(static_cast<unsigned>((n + 255) / 256));
+  rxmet::prof::Scope ps__("gru_fwd_recurrence", stream);
+  const float *hcur = plan.ra.h0codes;
+  for (int t = 0; t < T; ++t) {
+    float *hnext = hb + static_cast<size_t>(t & 1) * n;
+    o.A = hcur;
+    o.B = plan.rq;
+    if (pa == 1 && pb == 1)
+      hipLaunchKernelGGL((step_rh_gemm<1, 1>), ggrid, dim3(256), 0, stream, o, ghh);
+    else if (pa == 1)
+      hipLaunchKernelGGL((step_rh_gemm<1, 2>), ggrid, dim3(256), 0, stream, o, ghh);
+    else if (pb == 1)
+      hipLaunchKernelGGL((step_rh_gemm<2, 1>), ggrid, dim3(256), 0, stream, o, ghh);
+    else
+      hipLaunchKernelGGL((step_rh_gemm<2, 2>), ggrid, dim3(256), 0, stream, o, ghh);
+    RXMET_CHECK_LAUNCH();
+    hipLaunchKernelGGL(step_point, pgrid, dim3(256), 0, stream, plan.ra, plan.sp, t, ghh, hcur,
+                       hnext);
+    RXMET_CHECK_LAUNCH();
+    hcur = hnext;
+  }
+  return 0;
+}
+
 static int forward_recurrence_tiles(FwdPlan &plan, int B, int H, hipStream_t stream) {
   RecArgs &ra = plan.ra;
   const size_t lds = recurrence_lds_bytes(H, ra.KS, plan.npl);
@@ -1223,6 +1301,13 @@ static int forward_dirs(int ndir, bool training, int T, int B, int I, int H,
                       "strided x: T*B*I must be below 2^32 and the strides non-negative");
     }
     if (int rc = forward_prologue(training, T, B, I, H, dirs[k], xl, stream, &plans[k])) return rc;
+  }
+  bool stepped = false;
+  for (int k = 0; k < ndir; ++k) stepped = stepped || plans[k].stepped;
+  if (stepped) {
+    for (int k = 0; k < ndir; ++k)
+      if (int r = forward_recurrence_stepped(plans[k], *dirs[k].params, T, B, I, H, stream)) return r;
+    return 0;
   }
   const int rc = forward_recurrence_clustered(plans, ndir, T, B, I, H, stream);
   if (rc < 0) return rc;

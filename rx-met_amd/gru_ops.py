@@ -45,7 +45,7 @@ class OperatorQuantConfig:
 
     def __getattr__(self, name):
         c = object.__getattribute__(self, "_c")
-        if name == "usePOT2_":
+        if name in ("usePOT2_", "usePO2_"):
             return bool(c.use_pot2)
         if name == "pot_scale_method_":
             return int(c.pot_method)
@@ -65,7 +65,7 @@ class OperatorQuantConfig:
 
     def __setattr__(self, name, value):
         c = self._c
-        if name == "usePOT2_":
+        if name in ("usePOT2_", "usePO2_"):
             c.use_pot2 = int(bool(value))
             return
         if name == "pot_scale_method_":
@@ -95,34 +95,92 @@ class OperatorQuantConfig:
     def to_struct(self) -> A.GruConfig:
         return self._c
 
+    def copy(self) -> "OperatorQuantConfig":
+        out = OperatorQuantConfig()
+        ctypes.pointer(out._c)[0] = self._c
+        return out
+
+
+# Reference attribute stems of the 13 activation grids (gru_interface_binding.cc:1365-1410
+# names the two linear grids Wx / Rh in GRUQuantizationRanges).
+_RANGE_GRID = {n: n for n in A.GRID_NAMES}
+_RANGE_GRID.update(Wx="weight_ih_linear", Rh="weight_hh_linear")
+del _RANGE_GRID["weight_ih_linear"], _RANGE_GRID["weight_hh_linear"]
+
 
 class GRUQuantizationRanges:
-    """MinMax statistics of one direction: flat vector in the layout of
-    rxmet_gru_forward_calibrate, kept on the device between calibration batches."""
+    """MinMax statistics of one direction (GRUQuantizationRanges, gru_interface_binding.cc:
+    1365-1410): a flat vector in the layout of rxmet_gru_forward_calibrate, kept on the device
+    between calibration batches.  The reference's attributes read and write it: ``hidden_``,
+    ``min_<op>_`` / ``max_<op>_`` for the 13 grids (``Wx``, ``Rh`` for the two linears) and
+    per-channel lists ``min_W_``, ``max_W_``, ``min_R_``, .., ``max_br_`` of length 3H."""
 
-    def __init__(self, hidden_size: int, device=None):
-        self.hidden_ = int(hidden_size)
-        self.stats = torch.from_numpy(A.empty_stats(self.hidden_))
+    def __init__(self, hidden_size: int = 0, device=None):
+        object.__setattr__(self, "hidden_", int(hidden_size))
+        object.__setattr__(self, "stats", torch.from_numpy(A.empty_stats(self.hidden_)))
         if device is not None:
             self.stats = self.stats.to(device)
 
     def reset(self, hidden: int = -1):
         if hidden > 0:
-            self.hidden_ = hidden
+            object.__setattr__(self, "hidden_", int(hidden))
         self.stats = torch.from_numpy(A.empty_stats(self.hidden_)).to(self.stats.device)
 
     def to_struct(self):
         return A.make_ranges(self.stats.detach().cpu().numpy(), self.hidden_)
 
+    def _slot(self, name):
+        for side, off in (("min_", 0), ("max_", A.NGRIDS)):
+            if name.startswith(side) and name.endswith("_"):
+                stem = name[len(side):-1]
+                if stem in _RANGE_GRID:
+                    return ("grid", off + A.GRID[_RANGE_GRID[stem]])
+                if stem in A.CHAN:
+                    C = 3 * self.hidden_
+                    base = 2 * A.NGRIDS + 2 * A.CHAN[stem] * C + (C if side == "max_" else 0)
+                    return ("chan", base)
+        return None
+
+    def __getattr__(self, name):
+        slot = GRUQuantizationRanges._slot(self, name) if not name.startswith("__") else None
+        if slot is None:
+            raise AttributeError(name)
+        kind, i = slot
+        st = self.stats.detach().cpu()
+        if kind == "grid":
+            return float(st[i])
+        return [float(v) for v in st[i:i + 3 * self.hidden_]]
+
+    def __setattr__(self, name, value):
+        slot = self._slot(name)
+        if slot is None:
+            if name == "hidden_":
+                self.reset(int(value))
+                return
+            object.__setattr__(self, name, value)
+            return
+        kind, i = slot
+        if kind == "grid":
+            self.stats[i] = float(value)
+        else:
+            vals = torch.as_tensor(np.asarray(value, np.float32))
+            if vals.numel() != 3 * self.hidden_:
+                raise ValueError(f"{name} needs {3 * self.hidden_} values")
+            self.stats[i:i + 3 * self.hidden_] = vals.to(self.stats.device)
+
 
 class GRUQuantParams:
-    """Quantisation grids of one direction (quantize_param_types.h:88-118)."""
+    """Quantisation grids of one direction (GRUQuantParams, quantize_param_types.h:88-118;
+    binding attributes gru_interface_binding.cc:1480-1522): ``hidden_``, ``scale_<op>_`` /
+    ``zp_<op>_`` for the 13 activation grids, per-channel lists ``scale_W_``, ``scale_R_``,
+    ``scale_bw_``, ``scale_br_`` (3H values, zero points 0) and ``bitwidth_config_``, whose
+    bit widths, signedness and power-of-two flag the grids take (as the reference's to_cpp)."""
 
     def __init__(self, hidden: int = 0):
-        self.hidden_ = int(hidden)
-        self._qp = A.new_qparams(max(self.hidden_, 1))
-        self.bitwidth_config_ = None
-        self._device_cache = {}
+        object.__setattr__(self, "_qp", A.new_qparams(max(int(hidden), 1)))
+        self._qp.hidden = int(hidden)
+        object.__setattr__(self, "_cfg", None)
+        object.__setattr__(self, "_device_cache", {})
 
     @classmethod
     def from_struct(cls, qp) -> "GRUQuantParams":
@@ -137,9 +195,54 @@ class GRUQuantParams:
             A.qparams_chan(out._qp, k)[:] = A.qparams_chan(qp, k)
         return out
 
+    def _sync_config(self):
+        cfg = self._cfg
+        if cfg is None:
+            return
+        c = cfg.to_struct()
+        for i in range(A.NGRIDS):
+            self._qp.g[i].bits = c.op[i].bits
+            self._qp.g[i].is_unsigned = c.op[i].is_unsigned
+        for k in range(A.NCHAN):
+            self._qp.chan_bits[k] = c.chan[k].bits
+            self._qp.chan_unsigned[k] = c.chan[k].is_unsigned
+        self._qp.use_pot2 = c.use_pot2
+
     @property
     def struct(self):
+        self._sync_config()
         return self._qp
+
+    @property
+    def hidden_(self) -> int:
+        return int(self._qp.hidden)
+
+    @hidden_.setter
+    def hidden_(self, value: int):
+        value = int(value)
+        if value == self._qp.hidden:
+            return
+        old = self._qp
+        qp = A.new_qparams(max(value, 1))
+        qp.hidden = value
+        qp.use_pot2 = old.use_pot2
+        for i in range(A.NGRIDS):
+            qp.g[i] = old.g[i]
+        for k in range(A.NCHAN):
+            qp.chan_bits[k] = old.chan_bits[k]
+            qp.chan_unsigned[k] = old.chan_unsigned[k]
+        object.__setattr__(self, "_qp", qp)
+
+    @property
+    def bitwidth_config_(self):
+        return self._cfg
+
+    @bitwidth_config_.setter
+    def bitwidth_config_(self, cfg):
+        # stored by value, as the reference's C++ member: later changes to the caller's object
+        # do not reach these grids; changes made through this attribute's value do
+        object.__setattr__(self, "_cfg", None if cfg is None else cfg.copy())
+        self._sync_config()
 
     def scale(self, name: str) -> float:
         return float(self._qp.g[A.GRID[name]].scale)
@@ -149,6 +252,64 @@ class GRUQuantParams:
 
     def channel_scales(self, name: str) -> np.ndarray:
         return A.qparams_chan(self._qp, A.CHAN[name])
+
+    @staticmethod
+    def _attr(name):
+        for pre, kind in (("scale_", "scale"), ("zp_", "zp")):
+            if name.startswith(pre) and name.endswith("_"):
+                stem = name[len(pre):-1]
+                if stem in A.GRID:
+                    return kind, "grid", stem
+                if stem in A.CHAN:
+                    return kind, "chan", stem
+        return None
+
+    def __getattr__(self, name):
+        a = GRUQuantParams._attr(name) if not name.startswith("_") else None
+        if a is None:
+            raise AttributeError(name)
+        kind, where, stem = a
+        if where == "grid":
+            g = self._qp.g[A.GRID[stem]]
+            return float(g.scale) if kind == "scale" else int(g.zero_point)
+        if kind == "zp":  # weights and biases are symmetric: zero points are 0 per channel
+            return [0] * (3 * self.hidden_)
+        return [float(v) for v in A.qparams_chan(self._qp, A.CHAN[stem])[:3 * self.hidden_]]
+
+    def __setattr__(self, name, value):
+        a = self._attr(name)
+        if a is None:
+            object.__setattr__(self, name, value)
+            return
+        kind, where, stem = a
+        if where == "grid":
+            g = self._qp.g[A.GRID[stem]]
+            if kind == "scale":
+                g.scale = float(value)
+            else:
+                g.zero_point = int(value)
+            return
+        if kind == "zp":
+            if any(int(v) != 0 for v in np.atleast_1d(value)):
+                raise ValueError(f"{name}: per-channel weight grids are symmetric (zero point 0)")
+            return
+        vals = np.asarray(value, np.float32).reshape(-1)
+        if vals.size != 3 * self.hidden_:
+            raise ValueError(f"{name} needs {3 * self.hidden_} values (3 * hidden_)")
+        A.qparams_chan(self._qp, A.CHAN[stem])[:vals.size] = vals
+
+
+def decode_effective_scale(scale: float, usePOT2: bool) -> float:
+    """The scale the kernels quantise and dequantise with: the 16-bit-mantissa M·2^-shift
+    encoding of ``scale`` decoded, or its power of two with usePOT2
+    (decode_effective_scale_wrapper, gru_interface_binding.cc:1349)."""
+    return float(_rx.load().rxmet_gru_effective_scale(float(scale), int(bool(usePOT2))))
+
+
+def init_gru_cublas():
+    """The reference creates its cuBLAS handle here (gru_interface_binding.cc:1357); the
+    MI355X build has no library handle to create, so this only checks the library loads."""
+    _rx.load()
 
 
 def calculate_gru_quantitative_parameters(quant_ranges: GRUQuantizationRanges,
@@ -228,6 +389,91 @@ def forward_fp(is_training, time_steps, batch_size, input_size, hidden_size, W, 
     return h, v
 
 
+# ---------------------------------------------------------------------------------------
+# Hidden sizes that are not a multiple of 16.  The library's recurrences work on tiles of 16
+# hidden units; any other H runs as Hp = H rounded up to 16 with inert padded units: their
+# weight columns, recurrent rows and biases are zero, so they never feed a real unit, and
+# their outputs (and gradients) are dropped.  Channel c = g H + j of a gate-major [.., 3H]
+# axis becomes g Hp + j.
+# ---------------------------------------------------------------------------------------
+
+_UNIT_TILE = 16
+
+
+def _padded_hidden(H: int) -> int:
+    return (H + _UNIT_TILE - 1) // _UNIT_TILE * _UNIT_TILE
+
+
+def pad_blocks(t: torch.Tensor, H: int, Hp: int, axis: int, groups: int, fill=0) -> torch.Tensor:
+    """``groups`` consecutive blocks of H along ``axis``, each widened to Hp with ``fill``."""
+    if t is None or t.numel() == 0:
+        return t
+    shape = list(t.shape)
+    shape[axis] = groups * Hp
+    out = torch.full(shape, fill, dtype=t.dtype, device=t.device)
+    for g in range(groups):
+        out.narrow(axis, g * Hp, H).copy_(t.narrow(axis, g * H, H))
+    return out
+
+
+def unpad_blocks(t: torch.Tensor, H: int, Hp: int, axis: int, groups: int) -> torch.Tensor:
+    """Inverse of pad_blocks: the first H of each of ``groups`` blocks of Hp along ``axis``."""
+    if t is None or t.numel() == 0:
+        return t
+    return torch.cat([t.narrow(axis, g * Hp, H) for g in range(groups)], dim=axis).contiguous()
+
+
+def _padded_params(qp: "GRUQuantParams", H: int, Hp: int) -> "GRUQuantParams":
+    """The same grids for Hp units: real channels keep their scales, padded ones get 1.0."""
+    out = GRUQuantParams(Hp)
+    src = qp.struct
+    out._qp.use_pot2 = src.use_pot2
+    for i in range(A.NGRIDS):
+        out._qp.g[i] = src.g[i]
+    for k in range(A.NCHAN):
+        out._qp.chan_bits[k] = src.chan_bits[k]
+        out._qp.chan_unsigned[k] = src.chan_unsigned[k]
+        dst = A.qparams_chan(out._qp, k)
+        dst[:] = 1.0
+        s = A.qparams_chan(src, k)
+        for g in range(3):
+            dst[g * Hp:g * Hp + H] = s[g * H:(g + 1) * H]
+    out.bitwidth_config_ = qp.bitwidth_config_
+    return out
+
+
+def _forward_padded(is_training, T, B, I, H, W, R, bw, br, x, h0, quant_params):
+    Hp = _padded_hidden(H)
+    Wp = pad_blocks(W, H, Hp, 1, 3)
+    Rp = pad_blocks(pad_blocks(R, H, Hp, 1, 3), H, Hp, 0, 1)
+    bwp, brp = pad_blocks(bw, H, Hp, 0, 3), pad_blocks(br, H, Hp, 0, 3)
+    h0p = h0 if (h0 is None or h0.numel() == 0) else pad_blocks(h0, H, Hp, 1, 1)
+    outs = forward_quant_float_storage(is_training, T, B, I, Hp, Wp, Rp, bwp, brp, x, h0p,
+                                       _padded_params(quant_params, H, Hp))
+    (h, v, W_q, R_q, bw_q, br_q, x_q, x_m, h0_m, W_m, R_m, bw_m, br_m, ih_m, hh_m, gi_m, go_m,
+     h_m) = outs
+    un = lambda t, axis, groups: unpad_blocks(t, H, Hp, axis, groups)
+    return (un(h, 2, 1), un(v, 2, 4), un(W_q, 1, 3), un(un(R_q, 1, 3), 0, 1), un(bw_q, 0, 3),
+            un(br_q, 0, 3), x_q, x_m, un(h0_m, 1, 1), un(W_m, 1, 3), un(un(R_m, 1, 3), 0, 1),
+            un(bw_m, 0, 3), un(br_m, 0, 3), un(ih_m, 2, 3), un(hh_m, 2, 3), un(gi_m, 2, 3),
+            un(go_m, 2, 3), un(h_m, 2, 1))
+
+
+def _backward_padded(T, B, I, H, W_q, R_q, bw_q, br_q, x_q, dh_new, h, v, quant_params, masks):
+    Hp = _padded_hidden(H)
+    pb = lambda t, axis, groups: pad_blocks(t, H, Hp, axis, groups)
+    x_m, h0_m, W_m, R_m, bw_m, br_m, ih_m, hh_m, gi_m, go_m, h_m = masks
+    pmasks = (x_m, pb(h0_m, 1, 1), pb(W_m, 1, 3), pb(pb(R_m, 1, 3), 0, 1), pb(bw_m, 0, 3),
+              pb(br_m, 0, 3), pb(ih_m, 2, 3), pb(hh_m, 2, 3), pb(gi_m, 2, 3), pb(go_m, 2, 3),
+              pb(h_m, 2, 1))
+    dx, dW, dR, dbw, dbr, dh0 = backward_quant_float_storage(
+        T, B, I, Hp, pb(W_q, 1, 3), pb(pb(R_q, 1, 3), 0, 1), pb(bw_q, 0, 3), pb(br_q, 0, 3), x_q,
+        pb(dh_new.contiguous(), 2, 1), pb(h, 2, 1), pb(v, 2, 4),
+        _padded_params(quant_params, H, Hp), *pmasks)
+    un = lambda t, axis, groups: unpad_blocks(t, H, Hp, axis, groups)
+    return dx, un(dW, 1, 3), un(un(dR, 1, 3), 0, 1), un(dbw, 0, 3), un(dbr, 0, 3), un(dh0, 1, 1)
+
+
 MASK_NAMES = ("x_mask", "h0_mask", "W_mask", "R_mask", "bw_mask", "br_mask",
               "weight_ih_linear_mask", "weight_hh_linear_mask", "gate_input_mask",
               "gate_output_mask", "h_mask")
@@ -280,6 +526,8 @@ def forward_quant_float_storage(is_training, time_steps, batch_size, input_size,
     br_mask, weight_ih_linear_mask, weight_hh_linear_mask, gate_input_mask,
     gate_output_mask, h_mask); masks are empty tensors when is_training is False."""
     T, B, I, H = time_steps, batch_size, input_size, hidden_size
+    if H % _UNIT_TILE:
+        return _forward_padded(is_training, T, B, I, H, W, R, bw, br, x, h0, quant_params)
     outs, d, ws = _forward_dir(is_training, T, B, I, H, W, R, bw, br, x, h0, quant_params)
     _rx.call("rxmet_gru_forward_quant", int(bool(is_training)), T, B, I, H, d.W, d.R, d.bw, d.br,
              d.x, d.h0, ctypes.byref(quant_params.struct), d.h, d.v, d.W_q, d.R_q, d.bw_q, d.br_q,
@@ -294,6 +542,9 @@ def forward_quant_float_storage_dirs(is_training, time_steps, batch_size, input_
     ``dirs`` is a list of (W, R, bw, br, x, h0, quant_params) per direction; returns one
     forward_quant_float_storage result tuple per direction."""
     T, B, I, H = time_steps, batch_size, input_size, hidden_size
+    if H % _UNIT_TILE:
+        raise RuntimeError("the two-direction entry points need hidden_size % 16 == 0; call "
+                           "the per-direction functions, which take any hidden size")
     made = [_forward_dir(is_training, T, B, I, H, *d) for d in dirs]
     arr = (A.FwdDir * len(made))(*[m[1] for m in made])
     _rx.call("rxmet_gru_forward_quant_dirs", len(made), int(bool(is_training)), T, B, I, H, arr,
@@ -308,6 +559,9 @@ def forward_quant_float_storage_dirs_x(is_training, time_steps, batch_size, inpu
     of direction k's x in elements (feature stride 1); flags bit 0: W, R, bw, br given in
     PyTorch's layout (weight_ih [3H, I], weight_hh [3H, H], (r, z, n) gate order)."""
     T, B, I, H = time_steps, batch_size, input_size, hidden_size
+    if H % _UNIT_TILE:
+        raise RuntimeError("the two-direction entry points need hidden_size % 16 == 0; call "
+                           "the per-direction functions, which take any hidden size")
     for k, d in enumerate(dirs):
         if d[4].dim() != 3 or d[4].stride(2) != 1:
             raise RuntimeError(f"x of direction {k} needs a unit feature stride")
@@ -401,6 +655,9 @@ def backward_quant_float_storage(time_steps, batch_size, input_size, hidden_size
     T, B, I, H = time_steps, batch_size, input_size, hidden_size
     masks = (x_mask, h0_mask, W_mask, R_mask, bw_mask, br_mask, weight_ih_linear_mask,
              weight_hh_linear_mask, gate_input_mask, gate_output_mask, h_mask)
+    if H % _UNIT_TILE:
+        return _backward_padded(T, B, I, H, W_q, R_q, bw_q, br_q, x_q, dh_new, h, v, quant_params,
+                                masks)
     outs, d, keep = _backward_dir(T, B, I, H, W_q, R_q, bw_q, br_q, x_q, dh_new, h, v,
                                   quant_params, masks)
     _rx.call("rxmet_gru_backward_quant", T, B, I, H, d.W_q, d.R_q, d.bw_q, d.br_q, d.x_q,
@@ -416,6 +673,9 @@ def backward_quant_float_storage_dirs(time_steps, batch_size, input_size, hidden
     list of (W_q, R_q, bw_q, br_q, x_q, dh_new, h, v, quant_params, masks) per direction;
     returns one (dx, dW, dR, dbw, dbr, dh) tuple per direction."""
     T, B, I, H = time_steps, batch_size, input_size, hidden_size
+    if H % _UNIT_TILE:
+        raise RuntimeError("the two-direction entry points need hidden_size % 16 == 0; call "
+                           "the per-direction functions, which take any hidden size")
     made = [_backward_dir(T, B, I, H, *d) for d in dirs]
     arr = (A.BwdDir * len(made))(*[m[1] for m in made])
     _rx.call("rxmet_gru_backward_quant_dirs", len(made), T, B, I, H, arr,
@@ -428,6 +688,9 @@ def backward_quant_float_storage_dirs_x(time_steps, batch_size, input_size, hidd
     (rxmet_gru_backward_quant_dirs_x): per direction (dx, dW [3H, I], dR [3H, H], dbw [3H],
     dbr [3H], dh) in (r, z, n) gate order."""
     T, B, I, H = time_steps, batch_size, input_size, hidden_size
+    if H % _UNIT_TILE:
+        raise RuntimeError("the two-direction entry points need hidden_size % 16 == 0; call "
+                           "the per-direction functions, which take any hidden size")
     made = [_backward_dir(T, B, I, H, *d, torch_layout=True) for d in dirs]
     arr = (A.BwdDir * len(made))(*[m[1] for m in made])
     _rx.call("rxmet_gru_backward_quant_dirs_x", len(made), T, B, I, H, arr, 1,

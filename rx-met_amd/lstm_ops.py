@@ -195,6 +195,100 @@ def _saved_struct(saved: dict) -> L.Saved:
     return s
 
 
+# ---------------------------------------------------------------------------------------
+# Hidden sizes that are not a multiple of 16.  The recurrences work on tiles of 16 hidden
+# units; any other H runs as Hp = H rounded up to 16 with inert padded units: their rows of
+# W_ih / W_hh, their columns of W_hh and their biases are zero, so they never feed a real
+# unit, and their outputs and gradients are dropped.  Channel c = g H + j of a gate-major
+# [4H] axis becomes g Hp + j.
+# ---------------------------------------------------------------------------------------
+
+_UNIT_TILE = 16
+
+
+def _padded_hidden(H: int) -> int:
+    return (H + _UNIT_TILE - 1) // _UNIT_TILE * _UNIT_TILE
+
+
+def _pad(t, H, Hp, axis, groups, fill=0):
+    if t is None or t.numel() == 0:
+        return t
+    shape = list(t.shape)
+    shape[axis] = groups * Hp
+    out = torch.full(shape, fill, dtype=t.dtype, device=t.device)
+    for g in range(groups):
+        out.narrow(axis, g * Hp, H).copy_(t.narrow(axis, g * H, H))
+    return out
+
+
+def _unpad(t, H, Hp, axis, groups):
+    if t is None or t.numel() == 0:
+        return t
+    return torch.cat([t.narrow(axis, g * Hp, H) for g in range(groups)], dim=axis).contiguous()
+
+
+# (axis, gate groups) of each saved tensor's hidden axes, in the order they are padded
+_SAVED_HIDDEN_AXES = {
+    "w_ih_q": ((0, 4),), "w_hh_q": ((0, 4), (1, 1)), "b_ih_q": ((0, 4),), "b_hh_q": ((0, 4),),
+    "h0_q": ((1, 1),), "c0_q": ((1, 1),), "w_ih_m": ((0, 4),), "w_hh_m": ((0, 4), (1, 1)),
+    "b_ih_m": ((0, 4),), "b_hh_m": ((0, 4),), "h0_m": ((1, 1),), "c0_m": ((1, 1),),
+    "gate_out": ((2, 4),), "cell": ((2, 1),), "cell_tanh": ((2, 1),), "hidden": ((2, 1),),
+    "ih_linear_m": ((2, 4),), "hh_linear_m": ((2, 4),), "gate_in_m": ((2, 4),),
+    "gate_out_m": ((2, 4),), "cell_m": ((2, 1),), "cell_tanh_m": ((2, 1),), "hidden_m": ((2, 1),)}
+
+
+def _padded_params(params: LstmQuantParams, H: int, Hp: int) -> LstmQuantParams:
+    """The same grids for Hp units: real channels keep their scales, padded ones get 1.0."""
+    out = LstmQuantParams(Hp)
+    src, dst = params.struct, out.struct
+    dst.bias_enabled = src.bias_enabled
+    dst.config = src.config
+    for i in range(L.NOPS):
+        dst.scale[i] = src.scale[i]
+        dst.zero_point[i] = src.zero_point[i]
+    for k in range(4):
+        d = L.chan_scales(dst, k)
+        d[:] = 1.0
+        sk = L.chan_scales(src, k)
+        for g in range(4):
+            d[g * Hp:g * Hp + H] = sk[g * H:(g + 1) * H]
+    return out
+
+
+def _forward_padded(x, W_ih, W_hh, b_ih, b_hh, h0, c0, params, save_checkpoints):
+    H = W_hh.shape[1]
+    Hp = _padded_hidden(H)
+    pw = _pad(_pad(W_hh, H, Hp, 0, 4), H, Hp, 1, 1)
+    out, hn, cn, saved = forward_quant(
+        x, _pad(W_ih, H, Hp, 0, 4), pw, _pad(b_ih, H, Hp, 0, 4), _pad(b_hh, H, Hp, 0, 4),
+        _pad(h0, H, Hp, 1, 1), _pad(c0, H, Hp, 1, 1), _padded_params(params, H, Hp),
+        save_checkpoints)
+    if saved is not None:
+        for k, axes in _SAVED_HIDDEN_AXES.items():
+            if k in saved:
+                for axis, groups in axes:
+                    saved[k] = _unpad(saved[k], H, Hp, axis, groups)
+    return (_unpad(out, H, Hp, 2, 1), _unpad(hn, H, Hp, 1, 1), _unpad(cn, H, Hp, 1, 1), saved)
+
+
+def _backward_padded(saved, params, grad_output, grad_h_n, grad_c_n):
+    H = saved["h0_q"].shape[1]
+    Hp = _padded_hidden(H)
+    padded = dict(saved)
+    for k, axes in _SAVED_HIDDEN_AXES.items():
+        if k in padded:
+            # padded masks read "clamped" (1), so no gradient passes through a padded unit
+            fill = 1 if padded[k].dtype == torch.uint8 else 0
+            for axis, groups in axes:
+                padded[k] = _pad(padded[k], H, Hp, axis, groups, fill)
+    dx, dwi, dwh, dbi, dbh, dh0, dc0 = backward_quant(
+        padded, _padded_params(params, H, Hp), _pad(grad_output.contiguous(), H, Hp, 2, 1),
+        _pad(grad_h_n, H, Hp, 1, 1), _pad(grad_c_n, H, Hp, 1, 1))
+    un = lambda t, axis, groups: _unpad(t, H, Hp, axis, groups)
+    return (dx, un(dwi, 0, 4), un(un(dwh, 0, 4), 1, 1), un(dbi, 0, 4), un(dbh, 0, 4),
+            un(dh0, 1, 1), un(dc0, 1, 1))
+
+
 def forward_quant(x, W_ih, W_hh, b_ih, b_hh, h0, c0, params: LstmQuantParams,
                   save_checkpoints: bool):
     """Quantised FP32-carrier forward (lstm_forward_quantized).  Returns (output, h_n, c_n,
@@ -202,6 +296,8 @@ def forward_quant(x, W_ih, W_hh, b_ih, b_hh, h0, c0, params: LstmQuantParams,
     ``save_checkpoints`` is set, else None."""
     T, B, I = x.shape
     H = W_hh.shape[1]
+    if H % _UNIT_TILE:
+        return _forward_padded(x, W_ih, W_hh, b_ih, b_hh, h0, c0, params, save_checkpoints)
     x, W_ih, W_hh = (_dev_f32(n, t) for n, t in (("x", x), ("weight_ih", W_ih), ("weight_hh", W_hh)))
     bias = params.bias_enabled
     if bias and (b_ih is None or b_hh is None):
@@ -230,6 +326,8 @@ def backward_quant(saved: dict, params: LstmQuantParams, grad_output, grad_h_n=N
     (dx, dW_ih, dW_hh, db_ih, db_hh, dh0, dc0); bias grads are None without bias."""
     T, B, I = saved["x_q"].shape
     H = saved["h0_q"].shape[1]
+    if H % _UNIT_TILE:
+        return _backward_padded(saved, params, grad_output, grad_h_n, grad_c_n)
     C = 4 * H
     dev = saved["x_q"].device
     grad_output = _dev_f32("grad_output", grad_output)

@@ -883,7 +883,7 @@ class QuantGRU(nn.Module):
         if self.export_mode:
             raise NotImplementedError("ONNX export mode is not provided by the MI355X build")
         if (not self.calibrating and self.bidirectional and self.use_quantization
-                and self.quant_storage_dtype == "float32"):
+                and self.quant_storage_dtype == "float32" and self.hidden_size % 16 == 0):
             return self._forward_bidirectional(input, hx)
         if self.batch_first:
             input = input.transpose(0, 1).contiguous()

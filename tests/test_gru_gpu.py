@@ -76,6 +76,14 @@ def _config(name):
         c.chan[0].bits = c.chan[1].bits = 4
         c.use_pot2 = 1
         return c
+    if name == "16b-all":  # every grid 16-bit, recurrent weights included (stepped recurrence)
+        return A.set_all_bitwidth(A.default_config(), 16, False)
+    if name == "r12-pot2":  # 12-bit recurrent weights, 16-bit activations, power-of-two scales
+        c = A.set_all_bitwidth(A.default_config(), 16, False)
+        c.chan[0].bits = 8
+        c.chan[1].bits = 12
+        c.use_pot2 = 1
+        return c
     if name == "16b-r8":  # 16-bit x and W: the input projection needs int64 accumulation
         c = A.set_all_bitwidth(A.default_config(), 16, False)
         c.chan[1].bits = 8
@@ -183,10 +191,36 @@ def test_forward_eval_matches_training_h(cuda):
     assert all(m.numel() == 0 for m in ev[7:])
 
 
-def test_forward_rejects_unsupported(cuda):
-    W, R, bw, br, x, h0, qp = _case(2, 4, 3, 20, "8b-sym", 3, False)  # H % 16 != 0
-    with pytest.raises(rxmet_lib.RxmetError, match="multiple of 16"):
-        _gpu_forward(cuda, W, R, bw, br, x, h0, qp, True)
+@pytest.mark.parametrize("H", [1, 2, 5, 20, 33])
+@pytest.mark.parametrize("cfg_name", ["c3", "16b-act-pot2"])
+def test_any_hidden_size_forward_backward_match_oracle(cuda, H, cfg_name):
+    """Hidden sizes that are not a multiple of 16 (the reference's own fixtures use 1 and 2)
+    run with inert padded units inside the boundary: every forward output bit-exact, every
+    gradient within 1e-4 of the oracle at the real size."""
+    T, B, I = 4, 6, 3
+    print(f"[gru any H] H={H} cfg={cfg_name}", flush=True)
+    W, R, bw, br, x, h0, qp = _case(T, B, I, H, cfg_name, 17, True)
+    exp_f = GO.forward_quant(W, R, bw, br, x, qp, h0=h0, training=True)
+    fwd = _gpu_forward(cuda, W, R, bw, br, x, h0, qp, True)
+    for name, tensor in zip(NAMES, fwd):
+        np.testing.assert_array_equal(tensor.cpu().numpy(), exp_f[name], err_msg=name)
+    g = np.random.default_rng(18)
+    dh_new = (g.standard_normal((T + 1, B, H)) * 1e-2).astype(f32)
+    exp = GO.backward_quant(exp_f, dh_new, qp)
+    got = _gpu_backward(cuda, fwd, dh_new, qp, T, B, I, H)
+    for name, a in zip(("dx", "dW", "dR", "dbw", "dbr", "dh0"), got):
+        e = exp[name]
+        scale = max(float(np.abs(e).max()), 1e-30)
+        np.testing.assert_allclose(a, e, rtol=1e-4, atol=1e-5 * scale, err_msg=name)
+
+
+def test_two_direction_entry_points_refuse_unaligned_hidden_size(cuda):
+    W, R, bw, br, x, h0, qp = _case(2, 4, 3, 20, "8b-sym", 3, False)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(cuda)
+    d = (t(W), t(R), t(bw), t(br), t(x), torch.empty(0, device=cuda),
+         gru_ops.GRUQuantParams.from_struct(qp))
+    with pytest.raises(RuntimeError, match="hidden_size % 16"):
+        gru_ops.forward_quant_float_storage_dirs(True, 2, 4, 3, 20, [d, d])
 
 
 def _gpu_backward(dev, fwd, dh_new, qp, T, B, I, H):
@@ -376,3 +410,41 @@ def test_c5_full_size_rows_match_oracle(cuda):
         scale = max(float(np.abs(e).max()), 1e-30)
         np.testing.assert_allclose(a.take(rows, axis=axis), e, rtol=1e-4, atol=1e-5 * scale,
                                    err_msg=name)
+
+
+@pytest.mark.parametrize("shape", [(4, 20, 7, 32), (3, 33, 40, 64), (2, 5, 3, 256), (3, 40, 8, 512),
+                                   (3, 6, 2, 1), (3, 6, 2, 33)])
+@pytest.mark.parametrize("cfg_name", ["16b-all", "r12-pot2"])
+def test_wide_recurrent_weights_forward_backward_match_oracle(cuda, shape, cfg_name):
+    """Recurrent weights of 16 bits (the reference's set_all_bitwidth(16)): the stepped
+    recurrence (an exact two-plane GEMM and a pointwise launch per step) bit-exact in every
+    forward output, and the backward within 1e-4 of the oracle."""
+    T, B, I, H = shape
+    print(f"[gru wide R] shape={shape} cfg={cfg_name}", flush=True)
+    W, R, bw, br, x, h0, qp = _case(T, B, I, H, cfg_name, 23, True)
+    exp_f = GO.forward_quant(W, R, bw, br, x, qp, h0=h0, training=True)
+    fwd = _gpu_forward(cuda, W, R, bw, br, x, h0, qp, True)
+    for name, tensor in zip(NAMES, fwd):
+        np.testing.assert_array_equal(tensor.cpu().numpy(), exp_f[name], err_msg=name)
+    g = np.random.default_rng(24)
+    dh_new = (g.standard_normal((T + 1, B, H)) * 1e-2).astype(f32)
+    exp = GO.backward_quant(exp_f, dh_new, qp)
+    got = _gpu_backward(cuda, fwd, dh_new, qp, T, B, I, H)
+    for name, a in zip(("dx", "dW", "dR", "dbw", "dbr", "dh0"), got):
+        e = exp[name]
+        scale = max(float(np.abs(e).max()), 1e-30)
+        np.testing.assert_allclose(a, e, rtol=1e-4, atol=1e-5 * scale, err_msg=name)
+
+
+@pytest.mark.parametrize("shape,cfg_name", [((4, 40, 9, 64), "c3"), ((3, 20, 5, 256), "8b-asym")])
+def test_stepped_forward_equals_clustered(cuda, shape, cfg_name, monkeypatch):
+    """The stepped recurrence forced on 8-bit recurrent weights equals the clustered one bit
+    for bit."""
+    T, B, I, H = shape
+    print(f"[gru fwd stepped] shape={shape} cfg={cfg_name}", flush=True)
+    W, R, bw, br, x, h0, qp = _case(T, B, I, H, cfg_name, 25, True)
+    ref = _gpu_forward(cuda, W, R, bw, br, x, h0, qp, True)
+    monkeypatch.setenv("RXMET_FWD_STEPPED", "1")
+    got = _gpu_forward(cuda, W, R, bw, br, x, h0, qp, True)
+    for name, a, b in zip(NAMES, got, ref):
+        assert torch.equal(a, b), name

@@ -124,10 +124,12 @@ def _oracle_direction(m, reverse, x_tbi, h0, qp_struct, gout_tbh, ghn_bh):
 @pytest.mark.parametrize("batch_first", [False, True])
 @pytest.mark.parametrize("with_hx", [False, True])
 @pytest.mark.parametrize("cfg", ["c3", "po2-16b"])
-def test_module_calibrate_qat_matches_oracle(cuda, bidirectional, batch_first, with_hx, cfg):
-    print(f"[quantgru module] bi={bidirectional} bf={batch_first} hx={with_hx} cfg={cfg}",
-          flush=True)
-    m, x_tbi, hx = _module_case(bidirectional, batch_first, with_hx, cfg, 21)
+@pytest.mark.parametrize("shape", [(6, 24, 10, 32), (5, 12, 6, 33)])
+def test_module_calibrate_qat_matches_oracle(cuda, bidirectional, batch_first, with_hx, cfg,
+                                             shape):
+    print(f"[quantgru module] bi={bidirectional} bf={batch_first} hx={with_hx} cfg={cfg} "
+          f"shape={shape}", flush=True)
+    m, x_tbi, hx = _module_case(bidirectional, batch_first, with_hx, cfg, 21, shape=shape)
     m = m.to(cuda)
     T, B, I = x_tbi.shape
     H = m.hidden_size
@@ -198,7 +200,6 @@ def test_module_tracks_nn_gru_at_16_bits(cuda):
     m = Q.QuantGRU(I, H, bidirectional=True, batch_first=True)
     m.load_state_dict(ref.state_dict())
     m.set_all_bitwidth(16, is_symmetric=False)
-    m._bitwidth_config.R_ = 8  # the MFMA recurrence takes recurrent weights of up to 8 bits
     m = m.to(cuda)
     x = torch.randn(B, T, I)
     with m.calibration_context():
@@ -333,3 +334,37 @@ def test_quant_params_document_reproduces_qat_forward(cuda, tmp_path, bidirectio
         o1, h1 = m(x, hx)
         o2, h2 = n(x, hx)
     assert torch.equal(o1, o2) and torch.equal(h1, h2)
+
+
+@pytest.mark.parametrize("bits,mse,mae,cos", [(8, 1e-3, 0.05, 0.999), (16, 1e-4, 0.015, 0.999)])
+def test_quantized_module_tracks_nn_gru_with_reference_thresholds(cuda, bits, mse, mae, cos):
+    """operators/quant-gru/tests/test_quant_gru.py:400-526: QuantGRU with nn.GRU's weights,
+    set_all_bitwidth(bits), calibrated on one U(-0.7, 0.8) batch (I=128, H=256, B=64, T=50),
+    then evaluated on a fresh batch; MSE, MAE and cosine similarity against nn.GRU within the
+    reference's thresholds.  At 16 bits every grid is 16-bit, the recurrent weights included."""
+    I, H, B, T = 128, 256, 64, 50
+    print(f"[quantgru vs nn.GRU] bits={bits}", flush=True)
+    torch.manual_seed(0)
+    ref = torch.nn.GRU(I, H).to(cuda)
+    m = Q.QuantGRU(I, H).to(cuda)
+    m.load_state_dict(ref.state_dict())
+    m.set_all_bitwidth(bits)
+    calib = torch.rand(T, B, I, device=cuda) * 1.5 - 0.7
+    m.calibrating = True
+    with torch.no_grad():
+        m(calib)
+    m.calibrating = False
+    m.finalize_calibration()
+    m.use_quantization = True
+    x = torch.rand(T, B, I, device=cuda) * 1.5 - 0.7
+    ref.eval()
+    m.eval()
+    with torch.no_grad():
+        y_ref, _ = ref(x)
+        y, _ = m(x)
+    d = (y - y_ref).double()
+    got_mse = float((d ** 2).mean())
+    got_mae = float(d.abs().mean())
+    got_cos = float(torch.nn.functional.cosine_similarity(y.double().flatten(),
+                                                          y_ref.double().flatten(), dim=0))
+    assert got_mse < mse and got_mae < mae and got_cos > cos, (got_mse, got_mae, got_cos)

@@ -41,8 +41,11 @@ def _np(t):
 @pytest.mark.parametrize("batch_first", [False, True])
 @pytest.mark.parametrize("with_state", [False, True])
 @pytest.mark.parametrize("cfg", [None, C4])
-def test_module_qat_matches_oracle(cuda, bidirectional, batch_first, with_state, cfg):
-    T, B, I, H = 5, 18, 7, 32
+@pytest.mark.parametrize("H", [32, 33])
+def test_module_qat_matches_oracle(cuda, bidirectional, batch_first, with_state, cfg, H):
+    T, B, I = 5, 18, 7
+    print(f"[quantlstm module] bi={bidirectional} bf={batch_first} state={with_state} "
+          f"cfg={cfg is not None} H={H}", flush=True)
     D = 2 if bidirectional else 1
     m = _module(cuda, I, H, bidirectional, batch_first, cfg=cfg)
     g = torch.Generator().manual_seed(3)
