@@ -96,6 +96,50 @@ struct BwdArgs {
   float *dh0, *dc0;      // [B, H]
 };
 
+// The STE backward of one (step t, sequence b, unit j) given dh and dc arriving from step t + 1
+// (lstm_backward_oracle / backward_float_cpu order: output mask, tanh, cell mask, the four
+// gate-output masks and activation derivatives, then the gate-input and linear masks): the
+// gate-input gradients of both linears and the cell gradient passed to step t - 1.
+struct LstmBwdPoint {
+  float li[4], lh[4], dc_prev;
+};
+
+__device__ __forceinline__ LstmBwdPoint lstm_bwd_point(const BwdArgs &a, int t, int b, int j,
+                                                       float dh_in, float dc_in) {
+  const uint32_t H = static_cast<uint32_t>(a.H), C = 4u * H, B = static_cast<uint32_t>(a.B);
+  const uint32_t BH = B * H, BC = B * C;
+  const uint32_t e = static_cast<uint32_t>(t) * BH + static_cast<uint32_t>(b) * H + j;
+  const uint32_t gb = static_cast<uint32_t>(t) * BC + static_cast<uint32_t>(b) * C + j;
+  const float ig = deq(a.gate_out[gb], a.s_gout[0], a.zp_gout[0]);
+  const float fg = deq(a.gate_out[gb + H], a.s_gout[1], a.zp_gout[1]);
+  const float gg = deq(a.gate_out[gb + 2 * H], a.s_gout[2], a.zp_gout[2]);
+  const float og = deq(a.gate_out[gb + 3 * H], a.s_gout[3], a.zp_gout[3]);
+  const float ct = deq(a.cell_tanh[e], a.s_t, a.zp_t);
+  const float pc = t == 0 ? deq(a.c0_q[static_cast<uint32_t>(b) * H + j], a.s_c, a.zp_c)
+                          : deq(a.cell[e - BH], a.s_c, a.zp_c);
+  const float dht = (dh_in + a.grad_out[e]) * keepf(a.hid_m, e);
+  const float d_o = dht * ct;
+  const float dct = dht * og * keepf(a.tanh_m, e);
+  const float dc = dc_in + dct * (1.0f - ct * ct);
+  const float mdc = dc * keepf(a.cell_m, e);
+  const float dfg = mdc * pc;
+  const float dig = mdc * gg, dgg = mdc * ig;
+  const float go0 = dig * keepf(a.gout_m, gb), go1 = dfg * keepf(a.gout_m, gb + H);
+  const float go2 = dgg * keepf(a.gout_m, gb + 2 * H), go3 = d_o * keepf(a.gout_m, gb + 3 * H);
+  const float gi[4] = {go0 * ig * (1.0f - ig), go1 * fg * (1.0f - fg), go2 * (1.0f - gg * gg),
+                       go3 * og * (1.0f - og)};
+  LstmBwdPoint o;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const uint32_t gi_ = gb + g * H;
+    const float grad = gi[g] * keepf(a.gin_m, gi_);
+    o.li[g] = grad * keepf(a.ih_m, gi_);
+    o.lh[g] = grad * keepf(a.hh_m, gi_);
+  }
+  o.dc_prev = mdc * fg;
+  return o;
+}
+
 __global__ __launch_bounds__(512) void lstm_bwd_recurrence(BwdArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int H = a.H, C = 4 * H, B = a.B;
@@ -121,7 +165,7 @@ __global__ __launch_bounds__(512) void lstm_bwd_recurrence(BwdArgs a) {
       dh[u][r] = (a.grad_hn && ut < a.UT && b < B) ? a.grad_hn[static_cast<size_t>(b) * H + j] : 0.0f;
     }
   __syncthreads();
-  const uint32_t BH = static_cast<uint32_t>(B) * H, BC = static_cast<uint32_t>(B) * C;
+  const uint32_t BC = static_cast<uint32_t>(B) * C;
 
   for (int t = a.T - 1; t >= 0; --t) {
     // ---- pointwise backward; dgates_hh * scale_W kept in registers for the dh GEMM ----
@@ -137,38 +181,16 @@ __global__ __launch_bounds__(512) void lstm_bwd_recurrence(BwdArgs a) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) sv[u][r][g] = 0.0f;
         if (!tile || b >= B) continue;
-        const uint32_t e = static_cast<uint32_t>(t) * BH + static_cast<uint32_t>(b) * H + j;
         const uint32_t gb = static_cast<uint32_t>(t) * BC + static_cast<uint32_t>(b) * C + j;
-        const float ig = deq(a.gate_out[gb], a.s_gout[0], a.zp_gout[0]);
-        const float fg = deq(a.gate_out[gb + H], a.s_gout[1], a.zp_gout[1]);
-        const float gg = deq(a.gate_out[gb + 2 * H], a.s_gout[2], a.zp_gout[2]);
-        const float og = deq(a.gate_out[gb + 3 * H], a.s_gout[3], a.zp_gout[3]);
-        const float ct = deq(a.cell_tanh[e], a.s_t, a.zp_t);
-        const float pc = t == 0 ? deq(a.c0_q[static_cast<uint32_t>(b) * H + j], a.s_c, a.zp_c)
-                                : deq(a.cell[e - BH], a.s_c, a.zp_c);
         float &dcr = dcs[nr * H + j];
-        const float dht = (dh[u][r] + a.grad_out[e]) * keepf(a.hid_m, e);
-        const float d_o = dht * ct;
-        const float dct = dht * og * keepf(a.tanh_m, e);
-        const float dc = dcr + dct * (1.0f - ct * ct);
-        const float mdc = dc * keepf(a.cell_m, e);
-        const float dfg = mdc * pc;
-        const float dig = mdc * gg, dgg = mdc * ig;
-        const float go0 = dig * keepf(a.gout_m, gb), go1 = dfg * keepf(a.gout_m, gb + H);
-        const float go2 = dgg * keepf(a.gout_m, gb + 2 * H), go3 = d_o * keepf(a.gout_m, gb + 3 * H);
-        const float gi[4] = {go0 * ig * (1.0f - ig), go1 * fg * (1.0f - fg), go2 * (1.0f - gg * gg),
-                             go3 * og * (1.0f - og)};
+        const LstmBwdPoint o = lstm_bwd_point(a, t, b, j, dh[u][r], dcr);
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const uint32_t gi_ = gb + g * H;
-          const float grad = gi[g] * keepf(a.gin_m, gi_);
-          const float li = grad * keepf(a.ih_m, gi_);
-          const float lh = grad * keepf(a.hh_m, gi_);
-          a.dli[gi_] = li;
-          a.dlh[gi_] = lh;
-          sv[u][r][g] = lh * a.s_whh[g * H + j];
+          a.dli[gb + g * H] = o.li[g];
+          a.dlh[gb + g * H] = o.lh[g];
+          sv[u][r][g] = o.lh[g] * a.s_whh[g * H + j];
         }
-        dcr = mdc * fg;
+        dcr = o.dc_prev;
       }
     }
     // row maxima (NaN and inf rows propagate as NaN)
@@ -258,6 +280,52 @@ __global__ __launch_bounds__(512) void lstm_bwd_recurrence(BwdArgs a) {
       a.dc0[o] = dcs[nr * H + j] * keepf(a.c0_m, o);
     }
   }
+}
+
+// ---------------------------------------------------------------------------------
+// 2'. stepped backward recurrence (W_hh wider than 8 bits or H above 512)
+// ---------------------------------------------------------------------------------
+// Per step t = T-1..0 one pointwise launch over all (sequence, unit) pairs, then the dh GEMM
+// dh = (dgates_hh * scale_W) W_hh codes on bf16 MFMA (wgrad::nt: the gradient split exactly into
+// three bf16 terms against exact bf16 code planes, fp32 accumulation) with a K split whose S
+// parts the next pointwise adds in a fixed order.
+constexpr int kBStepMaxSplit = 16;
+
+__global__ __launch_bounds__(256) void lstm_bstep_point(BwdArgs a, int t, int S, const float *dhr,
+                                                        float *dcs) {
+  const int H = a.H, C = 4 * H;
+  const int64_t n = static_cast<int64_t>(a.B) * H;
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (e >= n) return;
+  const int b = static_cast<int>(e / H), j = static_cast<int>(e % H);
+  float dh = 0.0f, dc = 0.0f;
+  if (t == a.T - 1) {
+    dh = a.grad_hn ? a.grad_hn[e] : 0.0f;
+    dc = a.grad_cn ? a.grad_cn[e] : 0.0f;
+  } else {
+    for (int z = 0; z < S; ++z) dh += dhr[z * n + e];
+    dc = dcs[e];
+  }
+  const LstmBwdPoint o = lstm_bwd_point(a, t, b, j, dh, dc);
+  const size_t gb = (static_cast<size_t>(t) * a.B + b) * C + j;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    a.dli[gb + g * H] = o.li[g];
+    a.dlh[gb + g * H] = o.lh[g];
+  }
+  dcs[e] = o.dc_prev;
+}
+
+// dh0 / dc0 after the last step, with the h0 / c0 master masks.
+__global__ __launch_bounds__(256) void lstm_bstep_finish(BwdArgs a, int S, const float *dhr,
+                                                         const float *dcs) {
+  const int64_t n = static_cast<int64_t>(a.B) * a.H;
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (e >= n) return;
+  float dh = 0.0f;
+  for (int z = 0; z < S; ++z) dh += dhr[z * n + e];
+  a.dh0[e] = dh * keepf(a.h0_m, static_cast<uint32_t>(e));
+  a.dc0[e] = dcs[e] * keepf(a.c0_m, static_cast<uint32_t>(e));
 }
 
 // ---------------------------------------------------------------------------------
@@ -628,7 +696,7 @@ __global__ __launch_bounds__(256) void lstm_bwd_finish(int64_t nx, float *dx, co
 
 struct BwdWorkspace {
   size_t dli, dlh, xt, wt, ht, qsc, frag, colsum, swih, swhh, aug_ih, aug_hh, part, gsum, wfrag_cl,
-      csum, xp, xe, sync, total;
+      csum, xp, xe, sync, dhr, dcs, whht, total;
   int Mp, S_ih[2], kper_ih[2], S_hh[2], kper_hh[2];  // K splits by number of B planes
   BwdWorkspace(int T, int B, int I, int H) {
     const size_t C = 4 * static_cast<size_t>(H), M = static_cast<size_t>(T) * B;
@@ -664,6 +732,10 @@ struct BwdWorkspace {
     xp = o; o += al(2 * 3 * Bpad * C);
     xe = o; o += al(sizeof(int) * 2 * Bpad * G);
     sync = o; o += al(sizeof(unsigned) * (Bpad / kBB + 1));
+    // stepped recurrence: K-split parts of dh, the cell gradient, W_hh codes as bf16 planes
+    dhr = o; o += al(sizeof(float) * kBStepMaxSplit * static_cast<size_t>(B) * H);
+    dcs = o; o += al(sizeof(float) * static_cast<size_t>(B) * H);
+    whht = o; o += al(sizeof(__bf16) * 2 * static_cast<size_t>(H) * C);
     total = o;
   }
 };
@@ -689,8 +761,7 @@ int rxmet_lstm_backward_quant(int32_t T, int32_t B, int32_t I, int32_t H,
                               void *workspace, void *stream_) {
   clear_error();
   RXMET_CHECK_ARG(T >= 1 && B >= 1 && I >= 1 && H >= 1, "dimensions must be positive");
-  RXMET_CHECK_ARG(H % 16 == 0 && H <= kMaxHB,
-                  "hidden_size must be a multiple of 16 and at most 512 for the MFMA backward");
+  RXMET_CHECK_ARG(H % 16 == 0, "hidden_size must be a multiple of 16");
   RXMET_CHECK_ARG(params && saved && grad_output && dx && dW_ih && dW_hh && dh0 && dc0 && workspace,
                   "required pointer is null");
   RXMET_CHECK_ARG(params->hidden == H, "params hidden size does not match");
@@ -703,8 +774,11 @@ int rxmet_lstm_backward_quant(int32_t T, int32_t B, int32_t I, int32_t H,
                       sv.gate_out_m && sv.cell_m && sv.cell_tanh_m && sv.hidden_m,
                   "backward needs every saved tensor");
   RXMET_CHECK_ARG(!bias || (sv.b_ih_m && sv.b_hh_m), "backward with bias needs the bias masks");
-  RXMET_CHECK_ARG(params->config.op[RXMET_LSTM_W_HH].bits <= 8,
-                  "W_hh wider than 8 bits is not supported by the MFMA backward");
+  const Grid gwh_b = grid_of(params->config.op[RXMET_LSTM_W_HH], 1.0f, 0);
+  RXMET_CHECK_ARG(gwh_b.lo >= -32768 && gwh_b.hi <= 32767, "W_hh codes must fit signed 16 bits");
+  // the MFMA recurrences hold W_hh as int8 fragments for at most 512 units: anything else steps
+  const bool stepped = gwh_b.lo < -128 || gwh_b.hi > 127 || H > kMaxHB ||
+                       std::getenv("RXMET_LSTM_STEPPED") != nullptr;
   RXMET_CHECK_ARG(static_cast<double>(T) * B * 4 * H < 4294967295.0,
                   "T*B*4H too large for 32-bit element offsets");
   StepParams sp;
@@ -773,9 +847,51 @@ int rxmet_lstm_backward_quant(int32_t T, int32_t B, int32_t I, int32_t H,
   }
   ba.s_c = sp.c.dscale; ba.zp_c = sp.c.dzp; ba.s_t = sp.tanh_c.dscale; ba.zp_t = sp.tanh_c.dzp;
   ba.dli = dli; ba.dlh = dlh; ba.dh0 = dh0; ba.dc0 = dc0;
-  bool clustered = false;
+  bool recurrence_done = false;  // set by the stepped or the clustered recurrence
   int *timeout_flag = nullptr;
-  if (H % (2 * kBcUnits) == 0 && H / kBcUnits <= 2 * kBcHalf &&
+  if (stepped) {
+    const int npwh = wgrad::planes_for(gwh_b.lo, gwh_b.hi, 0.0);
+    __bf16 *whht = reinterpret_cast<__bf16 *>(wsb + ws.whht);
+    float *dhr = reinterpret_cast<float *>(wsb + ws.dhr);
+    float *dcs = reinterpret_cast<float *>(wsb + ws.dcs);
+    // W_hh codes [4H][H] transposed: row j (unit) holds the 4H channels
+    if (int rc = wgrad::codes_t(sv.w_hh_q, C, nullptr, C, H, H, 1, 0.0f, 1.0f, npwh, whht, C,
+                                static_cast<int64_t>(H) * C, stream))
+      return rc;
+    wgrad::NtArgs na;
+    na.lda = C;
+    na.kscale = swhh;
+    na.Bt = whht; na.ldb = C; na.bplane = static_cast<int64_t>(H) * C;
+    na.M = B; na.N = H; na.K = C; na.out = dhr; na.ldo = H;
+    {
+      // a K split that fills about 256 workgroups
+      const int wj = H <= 64 ? 2 : H <= 96 ? 3 : 4;
+      const int wgs = ((B + 127) / 128) * ((H + 32 * wj - 1) / (32 * wj));
+      int S = 256 / wgs;
+      S = S < 1 ? 1 : (S > kBStepMaxSplit ? kBStepMaxSplit : S);
+      int kper = ((C + S - 1) / S + 31) / 32 * 32;
+      while (S > 1 && kper * (S - 1) >= C) --S;
+      na.ksplit = S;
+      na.kper = S > 1 ? kper : C;
+      na.out_split = static_cast<int64_t>(B) * H;
+    }
+    const int64_t n = static_cast<int64_t>(B) * H;
+    const dim3 pgrid(static_cast<unsigned>((n + 255) / 256));
+    {
+      rxmet::prof::Scope ps__("lstm_bwd_recurrence", stream);
+      for (int t = T - 1; t >= 0; --t) {
+        hipLaunchKernelGGL(lstm_bstep_point, pgrid, dim3(256), 0, stream, ba, t, na.ksplit, dhr,
+                           dcs);
+        RXMET_CHECK_LAUNCH();
+        na.A = dlh + static_cast<size_t>(t) * B * C;
+        if (int rc = wgrad::nt(na, npwh, stream)) return rc;
+      }
+      hipLaunchKernelGGL(lstm_bstep_finish, pgrid, dim3(256), 0, stream, ba, na.ksplit, dhr, dcs);
+      RXMET_CHECK_LAUNCH();
+    }
+    recurrence_done = true;
+  }
+  if (!stepped && H % (2 * kBcUnits) == 0 && H / kBcUnits <= 2 * kBcHalf &&
       std::getenv("RXMET_NO_CLUSTER") == nullptr) {
     const void *fn = reinterpret_cast<const void *>(&lstm_bwd_recurrence_cl);
     const size_t lds_cl = bwd_cl_lds(C, H / kBcUnits);
@@ -814,10 +930,10 @@ int rxmet_lstm_backward_quant(int32_t T, int32_t B, int32_t I, int32_t H,
                                                    static_cast<unsigned>(lds_cl), stream));
       }
       timeout_flag = cl.timeout;
-      clustered = true;
+      recurrence_done = true;
     }
   }
-  if (!clustered) {
+  if (!recurrence_done) {
     hipLaunchKernelGGL(lstm_pack_whh_t, dim3(UT * KS2), dim3(64), 0, stream, H, KS2, sv.w_hh_q, frag,
                        colsum);
     RXMET_CHECK_LAUNCH();

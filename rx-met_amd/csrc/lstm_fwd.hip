@@ -321,6 +321,73 @@ struct RecArgs {
   int wide_out;  // clustered path: outputs 16-byte aligned, stored as 16-byte rows through LDS
 };
 
+// One (sequence, unit) step of the q-carrier (forward_quantized_fp_cpu.cc:18-44, 116-190): per
+// gate the recurrent linear from its exact centred sum plus the rescaled bias (accf), its
+// rescale and clamp, the gate input with the input branch (lhs), the real activation; then the
+// cell (two contributions, one rounding) and the hidden update, with every clamp mask
+// (1 = clamped).
+struct LstmPoint {
+  float gout[4], cn, ct, hv;
+  uint8_t m_hl[4], m_gi[4], m_go[4], m_c, m_t, m_h;
+};
+
+__device__ __forceinline__ LstmPoint lstm_point(const float accf[4], const float mult[4],
+                                                const int shift[4], const float lhs[4],
+                                                float c_old, const StepParams &sp) {
+  LstmPoint o;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const float lin = clamp_grid(static_cast<double>(rescale(accf[g], mult[g], shift[g])) +
+                                     sp.hh_lin.dzp,
+                                 sp.hh_lin, o.m_hl[g]);
+    const float rhs = rescale(center(lin, sp.hh_lin.zp), sp.hh_to_gate[g].mult,
+                              sp.hh_to_gate[g].shift);
+    const float gi = clamp_grid(static_cast<double>(lhs[g] + rhs) + sp.gin[g].dzp, sp.gin[g],
+                                o.m_gi[g]);
+    o.gout[g] = real_act(gi, sp.gin[g], sp.gout[g], g == 2, o.m_go[g]);
+  }
+  const float pf = center(o.gout[1], sp.gout[1].zp) * center(c_old, sp.c.zp);
+  const float pi = center(o.gout[0], sp.gout[0].zp) * center(o.gout[2], sp.gout[2].zp);
+  const float sum = cell_scale(pf, sp, 0) + cell_scale(pi, sp, 1);
+  o.cn = clamp_grid(static_cast<double>(rintf(sum)) + sp.c.dzp, sp.c, o.m_c);
+  o.ct = real_act(o.cn, sp.c, sp.tanh_c, true, o.m_t);
+  const float raw = center(o.gout[3], sp.gout[3].zp) * center(o.ct, sp.tanh_c.zp);
+  o.hv = clamp_grid(static_cast<double>(rescale(raw, sp.hidden.mult, sp.hidden.shift)) + sp.h.dzp,
+                    sp.h, o.m_h);
+  return o;
+}
+
+// The outputs of one (step t, sequence b, unit j): dequantised output, the checkpoints and
+// masks in training, h_n / c_n at the last step.
+__device__ __forceinline__ void lstm_store(const RecArgs &a, const StepParams &sp, int t, int b,
+                                           int j, const LstmPoint &o) {
+  const uint32_t H = static_cast<uint32_t>(a.H), C = 4u * H;
+  const uint32_t row = static_cast<uint32_t>(t) * a.B + b;
+  const uint32_t oh = row * H + j;
+  a.output[oh] = dequant(o.hv, sp.h.scale, sp.h.zp);
+  if (a.hidden != nullptr) {
+    a.cell[oh] = o.cn;
+    a.cell_tanh[oh] = o.ct;
+    a.hidden[oh] = o.hv;
+    a.cell_m[oh] = o.m_c;
+    a.cell_tanh_m[oh] = o.m_t;
+    a.hidden_m[oh] = o.m_h;
+    const uint32_t oc = row * C + j;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      a.gate_out[oc + g * H] = o.gout[g];
+      a.hh_lin_m[oc + g * H] = o.m_hl[g];
+      a.gate_in_m[oc + g * H] = o.m_gi[g];
+      a.gate_out_m[oc + g * H] = o.m_go[g];
+    }
+  }
+  if (t == a.T - 1) {
+    const uint32_t os = static_cast<uint32_t>(b) * H + j;
+    a.h_n[os] = dequant(o.hv, sp.h.scale, sp.h.zp);
+    a.c_n[os] = dequant(o.cn, sp.c.scale, sp.c.zp);
+  }
+}
+
 template <int NPL>
 __global__ __launch_bounds__(512) void lstm_recurrence(RecArgs a, StepParams sp) {
   extern __shared__ __align__(16) unsigned char smem[];
@@ -358,7 +425,6 @@ __global__ __launch_bounds__(512) void lstm_recurrence(RecArgs a, StepParams sp)
   }
   const int nrow0 = 4 * (l / 16);
   __syncthreads();
-  const bool train = a.hidden != nullptr;
 
   for (int t = 0; t < a.T; ++t) {
     const int cur = t & 1, nxt = cur ^ 1;
@@ -395,60 +461,23 @@ __global__ __launch_bounds__(512) void lstm_recurrence(RecArgs a, StepParams sp)
         const int nr = nrow0 + r, b = b0 + nr;
         const bool valid = b < B;
         const uint32_t row = static_cast<uint32_t>(t) * B + b;  // (t, b)
-        float gout[4];
-        uint8_t m_hl[4], m_gi[4], m_go[4];
+        float accf[4], mult[4], lhs[4];
+        int shift[4];
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           int v = pick(acc[g][0], r);
           if (NPL == 2) v += 256 * pick(acc[g][1], r);
           v += __float_as_int(cc[g].z);
-          const float accf = static_cast<float>(v) + cc[g].y;
-          const float lin = clamp_grid(
-              static_cast<double>(rescale(accf, cc[g].x, __float_as_int(cc[g].w))) + sp.hh_lin.dzp,
-              sp.hh_lin, m_hl[g]);
-          const float rhs = rescale(center(lin, sp.hh_lin.zp), sp.hh_to_gate[g].mult,
-                                    sp.hh_to_gate[g].shift);
-          const float lh = valid ? a.lhs[static_cast<size_t>(row) * C + g * H + j] : 0.0f;
-          const float gi = clamp_grid(static_cast<double>(lh + rhs) + sp.gin[g].dzp, sp.gin[g], m_gi[g]);
-          gout[g] = real_act(gi, sp.gin[g], sp.gout[g], g == 2, m_go[g]);
+          accf[g] = static_cast<float>(v) + cc[g].y;
+          mult[g] = cc[g].x;
+          shift[g] = __float_as_int(cc[g].w);
+          lhs[g] = valid ? a.lhs[static_cast<size_t>(row) * C + g * H + j] : 0.0f;
         }
-        // cell: two contributions fused, one rounding
         float &cref = cstate[nr * H + j];
-        const float pf = center(gout[1], sp.gout[1].zp) * center(cref, sp.c.zp);
-        const float pi = center(gout[0], sp.gout[0].zp) * center(gout[2], sp.gout[2].zp);
-        const float sum = cell_scale(pf, sp, 0) + cell_scale(pi, sp, 1);
-        uint8_t m_c, m_t, m_h;
-        const float cn = clamp_grid(static_cast<double>(rintf(sum)) + sp.c.dzp, sp.c, m_c);
-        cref = cn;
-        const float ct = real_act(cn, sp.c, sp.tanh_c, true, m_t);
-        const float raw = center(gout[3], sp.gout[3].zp) * center(ct, sp.tanh_c.zp);
-        const float hv = clamp_grid(static_cast<double>(rescale(raw, sp.hidden.mult, sp.hidden.shift)) +
-                                        sp.h.dzp, sp.h, m_h);
-        if (valid) {
-          const uint32_t oh = row * static_cast<uint32_t>(H) + j;
-          a.output[oh] = dequant(hv, sp.h.scale, sp.h.zp);
-          if (train) {
-            a.cell[oh] = cn;
-            a.cell_tanh[oh] = ct;
-            a.hidden[oh] = hv;
-            a.cell_m[oh] = m_c;
-            a.cell_tanh_m[oh] = m_t;
-            a.hidden_m[oh] = m_h;
-            const uint32_t oc = row * static_cast<uint32_t>(C) + j;
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-              a.gate_out[oc + g * H] = gout[g];
-              a.hh_lin_m[oc + g * H] = m_hl[g];
-              a.gate_in_m[oc + g * H] = m_gi[g];
-              a.gate_out_m[oc + g * H] = m_go[g];
-            }
-          }
-          if (t == a.T - 1) {
-            const uint32_t os = static_cast<uint32_t>(b) * H + j;
-            a.h_n[os] = dequant(hv, sp.h.scale, sp.h.zp);
-            a.c_n[os] = dequant(cn, sp.c.scale, sp.c.zp);
-          }
-        }
+        const LstmPoint o = lstm_point(accf, mult, shift, lhs, cref, sp);
+        cref = o.cn;
+        const float hv = o.hv;
+        if (valid) lstm_store(a, sp, t, b, j, o);
         const int hc = static_cast<int>(hv - a.h_offset);
         if (NPL == 1) {
           pn[nr * ROW + j] = static_cast<int8_t>(hc);
@@ -460,6 +489,43 @@ __global__ __launch_bounds__(512) void lstm_recurrence(RecArgs a, StepParams sp)
     }
     __syncthreads();
   }
+}
+
+// ---------------------------------------------------------------------------------
+// 5'. stepped recurrence (W_hh wider than 8 bits, H above 512, or recurrent sums beyond int32)
+// ---------------------------------------------------------------------------------
+// Per step one exact GEMM of the centred h codes against the W_hh codes (xgemm::block: byte
+// planes on int8 MFMA, combined in int64, rounded once to fp32) and one pointwise launch over
+// all (sequence, unit) pairs; h codes in two fp32 [B, H] buffers, the cell codes in one.
+template <int PA, int PB>
+__global__ __launch_bounds__(256) void lstm_step_gemm(xgemm::Operands o, float *ghh) {
+  xgemm::block<PA, PB>(o, blockIdx.x * xgemm::kTile, blockIdx.y * xgemm::kTile,
+                       [&](int m, int n, long long sum) {
+                         ghh[static_cast<size_t>(m) * o.N + n] = static_cast<float>(sum);
+                       });
+}
+
+__global__ __launch_bounds__(256) void lstm_step_point(RecArgs a, StepParams sp, int t,
+                                                       const float *ghh, const float *cin,
+                                                       float *cout, float *hnext) {
+  const int H = a.H, C = 4 * H;
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (e >= static_cast<int64_t>(a.B) * H) return;
+  const int b = static_cast<int>(e / H), j = static_cast<int>(e % H);
+  float accf[4], mult[4], lhs[4];
+  int shift[4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int c = g * H + j;
+    accf[g] = ghh[static_cast<size_t>(b) * C + c] + a.run[c].hh_bacc;
+    mult[g] = a.ch[c].hh_mult;
+    shift[g] = a.ch[c].hh_shift;
+    lhs[g] = a.lhs[(static_cast<size_t>(t) * a.B + b) * C + c];
+  }
+  const LstmPoint o = lstm_point(accf, mult, shift, lhs, cin[e], sp);
+  cout[e] = o.cn;
+  hnext[e] = o.hv;
+  lstm_store(a, sp, t, b, j, o);
 }
 
 // ---------------------------------------------------------------------------------
@@ -887,7 +953,7 @@ size_t recurrence_lds(int H, int KS, int npl) {
 
 struct FwdWorkspace {
   size_t chost, run, frag, lhs, xq, wih, whh, bih, bhh, h0q, c0q, hx, sync, lut, xa, bfrag, colsum,
-      total;
+      sh, sc, sg, total;
   FwdWorkspace(int T, int B, int I, int H) {
     const size_t C = 4 * static_cast<size_t>(H), KS = (H + 63) / 64;
     auto al = [](size_t x) { return (x + 255) & ~static_cast<size_t>(255); };
@@ -915,6 +981,10 @@ struct FwdWorkspace {
     xa = o; o += al(ip * 2 * static_cast<size_t>(T) * B * Kp);
     bfrag = o; o += al(ip * 2 * C * Kp);
     colsum = o; o += al(ip * sizeof(long long) * C);
+    // stepped recurrence: two h code buffers, the cell codes [B, H] and the sums [B, 4H]
+    sh = o; o += al(sizeof(float) * 2 * static_cast<size_t>(B) * H);
+    sc = o; o += al(sizeof(float) * static_cast<size_t>(B) * H);
+    sg = o; o += al(sizeof(float) * static_cast<size_t>(B) * C);
     total = o;
   }
 };
@@ -940,16 +1010,13 @@ int rxmet_lstm_forward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const f
                              void *stream_) {
   clear_error();
   RXMET_CHECK_ARG(T >= 1 && B >= 1 && I >= 1 && H >= 1, "dimensions must be positive");
-  RXMET_CHECK_ARG(H % 16 == 0 && H <= kMaxH,
-                  "hidden_size must be a multiple of 16 and at most 512 for the MFMA recurrence");
+  RXMET_CHECK_ARG(H % 16 == 0, "hidden_size must be a multiple of 16");
   RXMET_CHECK_ARG(W_ih && W_hh && x && params && output && h_n && c_n && workspace,
                   "required pointer is null");
   RXMET_CHECK_ARG((h0 == nullptr) == (c0 == nullptr), "h0 and c0 must be given together");
   RXMET_CHECK_ARG(params->hidden == H, "params hidden size does not match");
   const bool bias = params->bias_enabled != 0;
   RXMET_CHECK_ARG(!bias || (b_ih && b_hh), "bias enabled but bias pointers are null");
-  const rxmet_lstm_op_config &whh_t = params->config.op[RXMET_LSTM_W_HH];
-  RXMET_CHECK_ARG(whh_t.bits <= 8, "W_hh wider than 8 bits is not supported by the MFMA recurrence");
   const rxmet_lstm_op_config &h_t = params->config.op[RXMET_LSTM_OUTPUT];
   RXMET_CHECK_ARG(h_t.bits <= 16, "output (h) wider than 16 bits is not supported");
   RXMET_CHECK_ARG(static_cast<double>(T) * B * 4 * H < 4294967295.0,
@@ -972,8 +1039,14 @@ int rxmet_lstm_forward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const f
   // the input branch is an exact byte-plane GEMM; the recurrent MFMA sum must fit int32
   RXMET_CHECK_ARG(I < (1 << 17), "input_size must be below 131072 for the exact input GEMM");
   RXMET_CHECK_ARG(xgemm::a_fits(sp.x.lo, sp.x.hi), "input codes must span at most 16 bits");
-  RXMET_CHECK_ARG(std::ldexp(1.0, h_t.bits) * 128.0 * H < 2147483647.0,
-                  "recurrent accumulator would overflow int32");
+  const Grid gwh_t = grid_of(params->config.op[RXMET_LSTM_W_HH], 1.0f, 0);
+  RXMET_CHECK_ARG(xgemm::b_fits(gwh_t.lo, gwh_t.hi), "W_hh codes must fit signed 16 bits");
+  RXMET_CHECK_ARG(xgemm::a_fits(sp.h.lo, sp.h.hi), "h codes must span at most 16 bits");
+  // the MFMA recurrences hold W_hh as int8 fragments, keep at most 512 units per batch tile and
+  // sum in int32; anything else steps
+  const bool stepped = xgemm::b_planes(gwh_t.lo, gwh_t.hi) > 1 || H > kMaxH ||
+                       !(std::ldexp(1.0, h_t.bits) * 128.0 * H < 2147483647.0) ||
+                       std::getenv("RXMET_LSTM_STEPPED") != nullptr;
 
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   const FwdWorkspace ws(T, B, I, H);
@@ -1032,8 +1105,10 @@ int rxmet_lstm_forward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const f
   hipLaunchKernelGGL(lstm_quant_inputs, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
                      nx, nh, x, h0, c0, sp, xq, sv.x_m, h0q, sv.h0_m, c0q, sv.c0_m);
   RXMET_CHECK_LAUNCH();
-  hipLaunchKernelGGL(lstm_pack_whh, dim3((C / 16) * KS), dim3(64), 0, stream, H, KS, whh, frag);
-  RXMET_CHECK_LAUNCH();
+  if (!stepped) {
+    hipLaunchKernelGGL(lstm_pack_whh, dim3((C / 16) * KS), dim3(64), 0, stream, H, KS, whh, frag);
+    RXMET_CHECK_LAUNCH();
+  }
   const int M = T * B;
   {
     RXMET_CHECK_ARG(xgemm::b_fits(gwi.lo, gwi.hi), "W_ih codes must be signed 16-bit at most");
@@ -1104,6 +1179,42 @@ int rxmet_lstm_forward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const f
              a16(ra.hh_lin_m) && a16(ra.gate_in_m) && a16(ra.gate_out_m) && a16(ra.cell_m) &&
              a16(ra.cell_tanh_m) && a16(ra.hidden_m);
     ra.wide_out = wide ? 1 : 0;
+  }
+  if (stepped) {
+    float *hb = reinterpret_cast<float *>(wsb + ws.sh);
+    float *cs = reinterpret_cast<float *>(wsb + ws.sc);
+    float *ghh = reinterpret_cast<float *>(wsb + ws.sg);
+    const int pa = xgemm::a_planes(sp.h.lo, sp.h.hi), pb = xgemm::b_planes(gwh_t.lo, gwh_t.hi);
+    xgemm::Operands o{};
+    o.M = B; o.N = C; o.K = H;
+    o.lda = H;
+    o.off = xgemm::a_shift(sp.h.lo, sp.h.hi);
+    o.corr = static_cast<long long>(o.off) - sp.h.zp;  // sums of (h - zp_h) W_hh
+    o.B = whh; o.sbk = 1; o.sbn = H;                    // W_hh codes [4H][H]
+    const dim3 ggrid((B + xgemm::kTile - 1) / xgemm::kTile, (C + xgemm::kTile - 1) / xgemm::kTile);
+    const int64_t n = static_cast<int64_t>(B) * H;
+    const dim3 pgrid(static_cast<unsigned>((n + 255) / 256));
+    rxmet::prof::Scope ps__("lstm_fwd_recurrence", stream);
+    const float *hcur = h0q, *cin = c0q;
+    for (int t = 0; t < T; ++t) {
+      float *hnext = hb + static_cast<size_t>(t & 1) * n;
+      o.A = hcur;
+      if (pa == 1 && pb == 1)
+        hipLaunchKernelGGL((lstm_step_gemm<1, 1>), ggrid, dim3(256), 0, stream, o, ghh);
+      else if (pa == 1)
+        hipLaunchKernelGGL((lstm_step_gemm<1, 2>), ggrid, dim3(256), 0, stream, o, ghh);
+      else if (pb == 1)
+        hipLaunchKernelGGL((lstm_step_gemm<2, 1>), ggrid, dim3(256), 0, stream, o, ghh);
+      else
+        hipLaunchKernelGGL((lstm_step_gemm<2, 2>), ggrid, dim3(256), 0, stream, o, ghh);
+      RXMET_CHECK_LAUNCH();
+      hipLaunchKernelGGL(lstm_step_point, pgrid, dim3(256), 0, stream, ra, sp, t, ghh, cin, cs,
+                         hnext);
+      RXMET_CHECK_LAUNCH();
+      hcur = hnext;
+      cin = cs;
+    }
+    return 0;
   }
   bool f32_grids = fits_f32(sp.hh_lin) && fits_f32(sp.c) && fits_f32(sp.tanh_c) && fits_f32(sp.h);
   for (int g = 0; g < 4; ++g) f32_grids = f32_grids && fits_f32(sp.gin[g]) && fits_f32(sp.gout[g]);

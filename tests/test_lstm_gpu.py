@@ -42,6 +42,16 @@ def _config(name):
             c.op[L.OP[n]].granularity = L.PER_GATE
         c.op[L.OP["output"]].is_symmetric = 0
         return c
+    if name == "16b-whh":  # every operator 16-bit, W_hh included
+        for k in range(L.NOPS):
+            c.op[k].bits = 16
+        return c
+    if name == "mixed-8-16":  # the strict matrix's mixed profile: 16-bit W_ih, input branch
+        for n in ("output", "weight_ih", "bias_ih", "weight_ih_linear", "input_gate_input",
+                  "cell_gate_input", "input_gate_output", "cell_gate_output", "cell_tanh_output",
+                  "weight_hh"):
+            c.op[L.OP[n]].bits = 16
+        return c
     if name == "16b-act":  # 16-bit activations and state, 8-bit per-tensor parameters
         for k in range(L.NOPS):
             if L.OP_NAMES[k] in L.PARAM_OPS:
@@ -314,11 +324,49 @@ def test_any_hidden_size_forward_backward_match_oracle(cuda, H, cfg_name):
 
 def test_unsupported_shapes_raise(cuda):
     c = _config("default")
-    c.op[L.OP["weight_hh"]].bits = 16
+    c.op[L.OP["weight_hh"]].bits = 24
     args, stats, _ = _case(2, 4, 3, 16, "default", 34)
-    p16 = O.finalize(stats, c, 16, True)
-    with pytest.raises(rxmet_lib.RxmetError, match="8 bits"):
-        _gpu_forward(cuda, args, p16, False)
+    p24 = O.finalize(stats, c, 16, True)
+    with pytest.raises(rxmet_lib.RxmetError, match="16 bits"):
+        _gpu_forward(cuda, args, p24, False)
+
+
+@pytest.mark.parametrize("shape", [(4, 20, 7, 32), (3, 33, 40, 64), (3, 6, 2, 33), (2, 40, 8, 640)])
+@pytest.mark.parametrize("cfg_name", ["16b-whh", "mixed-8-16"])
+def test_wide_recurrent_weights_forward_backward_match_oracle(cuda, shape, cfg_name):
+    """W_hh of 16 bits (the reference's int16 and mixed profiles) and H above 512 run on the
+    stepped recurrence (an exact two-plane GEMM and a pointwise launch per step; a bf16-plane
+    dh GEMM per step backward): forward and saved tensors bit-exact, gradients within 1e-4."""
+    T, B, I, H = shape
+    print(f"[lstm wide W_hh] shape={shape} cfg={cfg_name}", flush=True)
+    args, _, p = _case(T, B, I, H, cfg_name, 51, True, True)
+    Wi, Wh, bi, bh, x, h0, c0 = args
+    o = O.forward_quant(Wi, Wh, bi, bh, x, p, h0, c0, mode=O.ACT_CR)
+    out, hn, cn, saved = _gpu_forward(cuda, args, p, True)
+    _compare_forward(o, out, hn, cn, saved, True)
+    go, gh, gc = _grads(T, B, H, 52)
+    exp = O.backward_quant(o, p, go, gh, gc)
+    got = _gpu_backward(cuda, saved, p, go, gh, gc)
+    _assert_grads(got, exp)
+
+
+@pytest.mark.parametrize("shape,cfg_name", [((3, 40, 8, 128), "c4"), ((4, 20, 5, 64), "16b-act"),
+                                            ((3, 17, 6, 1024), "c4")])
+def test_hidden_above_512_and_forced_stepped_match_oracle(cuda, shape, cfg_name, monkeypatch):
+    """H above 512 steps by itself; below it the stepped path forced with RXMET_LSTM_STEPPED
+    gives the same results as the MFMA recurrences (forward bit for bit, gradients within 1e-4
+    of the oracle)."""
+    T, B, I, H = shape
+    print(f"[lstm stepped] shape={shape} cfg={cfg_name}", flush=True)
+    args, _, p = _case(T, B, I, H, cfg_name, 53, True, True)
+    Wi, Wh, bi, bh, x, h0, c0 = args
+    o = O.forward_quant(Wi, Wh, bi, bh, x, p, h0, c0, mode=O.ACT_CR)
+    go, gh, gc = _grads(T, B, H, 54)
+    exp = O.backward_quant(o, p, go, gh, gc)
+    monkeypatch.setenv("RXMET_LSTM_STEPPED", "1")
+    out, hn, cn, saved = _gpu_forward(cuda, args, p, True)
+    _compare_forward(o, out, hn, cn, saved, True)
+    _assert_grads(_gpu_backward(cuda, saved, p, go, gh, gc), exp)
 
 
 @pytest.mark.parametrize("shape,cfg_name", [((3, 2560, 16, 128), "c4"), ((2, 100, 24, 256), "c4"),
