@@ -9,6 +9,10 @@
  *   forward_fp (inference)                -> rxmet_gru_forward_fp
  *   forward_quant_float_storage           -> rxmet_gru_forward_quant
  *   backward_quant_float_storage          -> rxmet_gru_backward_quant
+ *   forward_quant_int_storage             -> rxmet_gru_forward_quant_int
+ *   backward_quant_int_storage            -> rxmet_gru_backward_quant on the int32 codes
+ *                                            converted to fp32 (as the binding does)
+ *   forward_quantized_int_io              -> rxmet_gru_forward_int_io
  *   (LUT regeneration in GRUQuantParamsPy::to_cpp) -> rxmet_gru_make_luts
  *
  * Conventions (all as in the reference):
@@ -283,6 +287,47 @@ int rxmet_gru_backward_quant_dirs(int32_t ndir, int32_t T, int32_t B, int32_t I,
  */
 int rxmet_gru_backward_quant_dirs_x(int32_t ndir, int32_t T, int32_t B, int32_t I, int32_t H,
                                     const rxmet_gru_bwd_dir *dirs, int32_t flags, void *stream);
+
+/*
+ * Quantised forward, int32 carrier: quantGRUForwardInt (src/gru_interface.cc:443-559) behind
+ * forward_quant_int_storage_wrapper (gru_interface_binding.cc:451-586), i.e. ForwardPassQuant
+ * (src/gru_forward_gpu_quant.cu) and the reference's CPU carrier (src/gru_forward_cpu_quant.cc:
+ * 109-343).  Every value between the boundaries is an integer code: GEMM sums exact in int64
+ * with the bias rescaled into the accumulator scale, rescales rshift_round(x M, shift) (16-bit
+ * mantissa M, or shifts only in power-of-two mode), integer PWL gates.  Arguments and outputs as
+ * rxmet_gru_forward_quant, except that W_q [I,3H], R_q [H,3H], bw_q, br_q [3H] and x_q [T,B,I]
+ * are int32 codes; h [T+1,B,H] and v [T,B,4H] are dequantised with the effective scales.
+ * x, h0 (both may carry any values), W and R in the kernel layout; x and h grids of at most
+ * 16 bits, W and R codes within signed 16 bits.  Any hidden size.  Workspace:
+ * rxmet_gru_forward_int_workspace_bytes.
+ */
+int64_t rxmet_gru_forward_int_workspace_bytes(int32_t T, int32_t B, int32_t I, int32_t H);
+int rxmet_gru_forward_quant_int(int32_t is_training, int32_t T, int32_t B, int32_t I, int32_t H,
+                                const float *W, const float *R, const float *bw, const float *br,
+                                const float *x, const float *h0, const rxmet_gru_qparams *params,
+                                float *h, float *v, int32_t *W_q, int32_t *R_q, int32_t *bw_q,
+                                int32_t *br_q, int32_t *x_q, uint8_t *x_mask, uint8_t *h0_mask,
+                                uint8_t *W_mask, uint8_t *R_mask, uint8_t *bw_mask,
+                                uint8_t *br_mask, uint8_t *ih_mask, uint8_t *hh_mask,
+                                uint8_t *gate_in_mask, uint8_t *gate_out_mask, uint8_t *h_mask,
+                                void *workspace, void *stream);
+
+/*
+ * Integer-in, integer-out inference: quantGRUForwardIntIO (src/gru_interface.cc:561-627) behind
+ * forward_quantized_int_io_wrapper (gru_interface_binding.cc:588-646).  x_q [T,B,I] and h0_q
+ * [B,H] (may be null: the zero point of h) are int32 codes on the x and h grids, used as they
+ * are; only the weights are quantised (W_q, R_q, bw_q, br_q written as in
+ * rxmet_gru_forward_quant_int).  Writes the int32 h codes h_q [T+1,B,H] (row 0 = h0_q); the
+ * reference's output_q and h_n_q are rows 1..T and row T.  Codes outside the x / h grids are
+ * rejected (-22); that check synchronises the stream once.  Workspace:
+ * rxmet_gru_forward_int_workspace_bytes.
+ */
+int rxmet_gru_forward_int_io(int32_t T, int32_t B, int32_t I, int32_t H, const float *W,
+                             const float *R, const float *bw, const float *br,
+                             const int32_t *x_q, const int32_t *h0_q,
+                             const rxmet_gru_qparams *params, int32_t *h_q, int32_t *W_q,
+                             int32_t *R_q, int32_t *bw_q, int32_t *br_q, void *workspace,
+                             void *stream);
 
 /*
  * Float GRU forward with MinMax calibration statistics: forwardWithCalibrationGPU

@@ -816,3 +816,252 @@ int oracle_gru_backward_quant(int T, int B, int I, int H, const float *W_q, cons
   free(Wd); free(Rd); free(dp); free(dq); free(dh); free(sbw); free(sbr);
   return 0;
 }
+
+/* ------------------------------------------------------------------------------ */
+/* Quantised forward, int32 carrier                                                */
+/* ------------------------------------------------------------------------------ */
+/*
+ * quantGRUForwardInt / quantGRUForwardIntIO (src/gru_interface.cc:384-627) over
+ * ForwardPassQuant (src/gru_forward_gpu_quant.cu:112-176, 230-373, 526-847), whose
+ * arithmetic the reference's CPU carrier repeats (src/gru_forward_cpu_quant.cc:109-343):
+ *   - boundary quantisation with the effective scale, the code kept in double before the
+ *     saturation (quantize<Training>, quantize_ops_helper.h:356-364,472-476);
+ *   - GEMMs of codes summed exactly in int64 with the zero point of the right operand
+ *     removed, the bias rescaled into the accumulator scale, then one rescale to the linear
+ *     grid (quantizedGemmBiasFused);
+ *   - the integer gate templates computeUpdateGate/ResetGate/NewGate/HiddenState
+ *     (quantize_ops_helper.h:683-1023) with the 16-segment PWL (:503-549);
+ *   - rescales rshift_round(x * M, shift) (M16) or rshift_round(x, shift) (POT2)
+ *     (quantize_ops_helper.h:201-247) derived by makeRescale / makeRescaleProduct /
+ *     makeRescaleToProduct (scale_encoding.h:133-188).
+ * Outputs are int32 codes; h_q [T+1,B,H] holds the initial state in row 0.
+ */
+
+typedef struct { int64_t m; int32_t shift; } int_rescale;
+
+/* rshift_round (quantize_ops_helper.h:201-224): round(x / 2^n), half to even, on |x|. */
+static int64_t rshift_round64(int64_t x, int n) {
+  if (n <= 0) return (int64_t)((uint64_t)x << (-n));
+  const int neg = x < 0;
+  const uint64_t ax = neg ? (uint64_t)0 - (uint64_t)x : (uint64_t)x;
+  const uint64_t half = (uint64_t)1 << (n - 1);
+  const uint64_t q = ax >> n, r = ax & (((uint64_t)1 << n) - 1);
+  const uint64_t res = r > half ? q + 1 : (r < half ? q : q + (q & 1));
+  return neg ? -(int64_t)res : (int64_t)res;
+}
+static int64_t apply_rescale(int64_t x, int_rescale r) { return rshift_round64(x * r.m, r.shift); }
+
+static int_rescale rescale_of_ratio(float ratio, int pot, int8_t pot_shift) {
+  int_rescale r;
+  if (pot) {
+    r.m = 1;
+    r.shift = pot_shift;
+  } else {
+    const fixed_scale f = encode_mshift(ratio);
+    r.m = f.m;
+    r.shift = f.shift;
+  }
+  return r;
+}
+/* src -> dst */
+static int_rescale rs_single(float src, float dst, int pot) {
+  return rescale_of_ratio(src / dst, pot, (int8_t)(pot2_shift(src) - pot2_shift(dst)));
+}
+/* a*b -> dst */
+static int_rescale rs_product(float a, float b, float dst, int pot) {
+  return rescale_of_ratio((a * b) / dst, pot,
+                          (int8_t)(pot2_shift(a) + pot2_shift(b) - pot2_shift(dst)));
+}
+/* src -> a*b */
+static int_rescale rs_to_product(float src, float a, float b, int pot) {
+  return rescale_of_ratio(src / (a * b), pot,
+                          (int8_t)(pot2_shift(src) - (pot2_shift(a) + pot2_shift(b))));
+}
+
+/* clamp_by_bitwidth<Training> on int32 (quantize_ops_helper.h:267-279) */
+static int32_t clampi(int32_t v, int32_t bits, int32_t uns, uint8_t *keep) {
+  uns = eff_uns(bits, uns);
+  const int32_t lo = g_qmin(bits, uns), hi = g_qmax(bits, uns);
+  if (keep) *keep = (v < lo || v > hi) ? 0 : 1;
+  return v < lo ? lo : (v > hi ? hi : v);
+}
+
+/* quantize(float, FixedPointScale, zp, bw): rint in float, zero point added in double,
+ * saturated in double before the integer conversion. */
+static int32_t quant_int(float v, float eff, int32_t zp, int32_t bits, int32_t uns,
+                         uint8_t *keep) {
+  uns = eff_uns(bits, uns);
+  const double code = (double)rintf(v / eff) + (double)zp;
+  const int32_t lo = g_qmin(bits, uns), hi = g_qmax(bits, uns);
+  if (keep) *keep = (code < lo || code > hi) ? 0 : 1;
+  return code < lo ? lo : (code > hi ? hi : (int32_t)code);
+}
+
+/* piecewise_linear_raw (quantize_ops_helper.h:519-535) */
+static int32_t pwl_int(int32_t q, const rxmet_pwl_lut *lut) {
+  int s = 15;
+  for (int i = 0; i < 16; ++i)
+    if (q < lut->seg[i].threshold) { s = i; break; }
+  const int32_t off = (int32_t)((uint32_t)q - (uint32_t)lut->zp_x);
+  const int64_t bx = (int64_t)lut->seg[s].q_b * (int64_t)off;
+  const int n = lut->seg[s].n;
+  const int32_t term = n >= 0 ? (int32_t)rshift_round64(bx, n)
+                              : (int32_t)(int64_t)((uint64_t)bx << (-n));
+  return (int32_t)((uint32_t)term + (uint32_t)lut->seg[s].c);
+}
+
+static int32_t add32(int32_t a, int32_t b) { return (int32_t)((uint32_t)a + (uint32_t)b); }
+
+/*
+ * x_q_in / h0_q_in non-null: the int-IO form (quantGRUForwardIntIO): codes taken as given,
+ * x / h0 ignored.  Otherwise x (and h0 when non-null) are quantised into x_q / h_q[0].
+ * v_q [T,B,4H] (z, r, n, weight_hh_linear of n) may be null; masks are written when
+ * is_training is set and the pointer is non-null.
+ */
+int oracle_gru_forward_int(int is_training, int T, int B, int I, int H, const float *W,
+                           const float *R, const float *bw, const float *br, const float *x,
+                           const int32_t *x_q_in, const float *h0, const int32_t *h0_q_in,
+                           const rxmet_gru_qparams *p, int32_t *h_q, int32_t *v_q,
+                           int32_t *W_q, int32_t *R_q, int32_t *bw_q, int32_t *br_q,
+                           int32_t *x_q, uint8_t *x_mask, uint8_t *h0_mask, uint8_t *W_mask,
+                           uint8_t *R_mask, uint8_t *bw_mask, uint8_t *br_mask,
+                           uint8_t *ih_mask, uint8_t *hh_mask, uint8_t *gin_mask,
+                           uint8_t *gout_mask, uint8_t *h_mask) {
+  const int C = 3 * H;
+  const size_t NH = (size_t)B * H;
+  const int pot = p->use_pot2;
+  const rxmet_grid *q = p->g;
+  uint8_t k;
+#define KEEP(ptr, idx) (is_training && (ptr) ? &(ptr)[idx] : &k)
+  /* boundary quantisation: per-channel weights and biases */
+  const float *wsrc[4] = {W, R, bw, br};
+  int32_t *wdst[4] = {W_q, R_q, bw_q, br_q};
+  uint8_t *wmask[4] = {W_mask, R_mask, bw_mask, br_mask};
+  const int wrows[4] = {I, H, 1, 1};
+  for (int kk = 0; kk < 4; ++kk)
+    for (int r = 0; r < wrows[kk]; ++r)
+      for (int c = 0; c < C; ++c) {
+        const size_t idx = (size_t)r * C + c;
+        const float eff = oracle_effective_scale(p->chan_scale[kk][c], pot);
+        wdst[kk][idx] = quant_int(wsrc[kk][idx], eff, 0, p->chan_bits[kk], p->chan_unsigned[kk],
+                                  KEEP(wmask[kk], idx));
+      }
+  const rxmet_grid *gx = &q[RXMET_GRU_X], *gh = &q[RXMET_GRU_H];
+  const float eff_x = oracle_effective_scale(gx->scale, pot);
+  const float eff_h = oracle_effective_scale(gh->scale, pot);
+  const size_t nx = (size_t)T * B * I;
+  const int32_t *xq = x_q_in;
+  if (!xq) {
+    for (size_t i = 0; i < nx; ++i)
+      x_q[i] = quant_int(x[i], eff_x, gx->zero_point, gx->bits, gx->is_unsigned, KEEP(x_mask, i));
+    xq = x_q;
+  }
+  for (size_t i = 0; i < NH; ++i) {
+    if (h0_q_in)
+      h_q[i] = h0_q_in[i];
+    else if (h0)
+      h_q[i] = quant_int(h0[i], eff_h, gh->zero_point, gh->bits, gh->is_unsigned,
+                         KEEP(h0_mask, i));
+    else
+      h_q[i] = gh->zero_point;
+  }
+  /* rescale parameters (setRescaleParam: fillLinearParams / fillGateParams) */
+  int_rescale *rgx = malloc(sizeof(int_rescale) * C), *rbw = malloc(sizeof(int_rescale) * C);
+  int_rescale *rgh = malloc(sizeof(int_rescale) * C), *rbr = malloc(sizeof(int_rescale) * C);
+  const float sx = gx->scale, sh = gh->scale;
+  const float swx = q[RXMET_GRU_WX].scale, srh = q[RXMET_GRU_RH].scale;
+  for (int c = 0; c < C; ++c) {
+    const float sW = p->chan_scale[RXMET_GRU_W][c], sR = p->chan_scale[RXMET_GRU_R][c];
+    rgx[c] = rs_product(sW, sx, swx, pot);
+    rbw[c] = rs_to_product(p->chan_scale[RXMET_GRU_BW][c], sW, sx, pot);
+    rgh[c] = rs_product(sR, sh, srh, pot);
+    rbr[c] = rs_to_product(p->chan_scale[RXMET_GRU_BR][c], sR, sh, pot);
+  }
+  const int32_t zp_x = gx->zero_point, zp_h = gh->zero_point;
+  const int32_t zp_wx = q[RXMET_GRU_WX].zero_point, zp_rh = q[RXMET_GRU_RH].zero_point;
+  const int32_t zp_zin = q[RXMET_GRU_Z_IN].zero_point, zp_zout = q[RXMET_GRU_Z_OUT].zero_point;
+  const int32_t zp_rin = q[RXMET_GRU_R_IN].zero_point, zp_rout = q[RXMET_GRU_R_OUT].zero_point;
+  const int32_t zp_nin = q[RXMET_GRU_N_IN].zero_point, zp_nout = q[RXMET_GRU_N_OUT].zero_point;
+  const float szin = q[RXMET_GRU_Z_IN].scale, szout = q[RXMET_GRU_Z_OUT].scale;
+  const float srin = q[RXMET_GRU_R_IN].scale, srout = q[RXMET_GRU_R_OUT].scale;
+  const float snin = q[RXMET_GRU_N_IN].scale, snout = q[RXMET_GRU_N_OUT].scale;
+  const int_rescale ih_zin = rs_single(swx, szin, pot), hh_zin = rs_single(srh, szin, pot);
+  const int_rescale ih_rin = rs_single(swx, srin, pot), hh_rin = rs_single(srh, srin, pot);
+  const int_rescale ih_nin = rs_single(swx, snin, pot);
+  const int_rescale rmul_nin = rs_product(srout, srh, snin, pot);
+  const int_rescale nout_h = rs_single(snout, sh, pot);
+  const int_rescale old_h = rs_product(szout, sh, sh, pot);
+  const int32_t quant_one = add32((int32_t)rintf(1.0f / szout), zp_zout);
+  rxmet_pwl_lut lut[3];
+  oracle_gru_make_luts(p, lut);
+#define GB(id) q[id].bits, q[id].is_unsigned
+  /* input projection: W_q (x_q - zp_x) + rescaled bw -> weight_ih_linear */
+  int32_t *wx = malloc(sizeof(int32_t) * (size_t)T * B * C);
+  for (size_t n = 0; n < (size_t)T * B; ++n)
+    for (int c = 0; c < C; ++c) {
+      int64_t acc = 0;
+      for (int r = 0; r < I; ++r)
+        acc += (int64_t)W_q[(size_t)r * C + c] * ((int64_t)xq[n * I + r] - zp_x);
+      const int64_t b = apply_rescale((int64_t)bw_q[c], rbw[c]);
+      const int32_t res = add32((int32_t)apply_rescale(acc + b, rgx[c]), zp_wx);
+      wx[n * C + c] = clampi(res, GB(RXMET_GRU_WX), KEEP(ih_mask, n * C + c));
+    }
+  int32_t *rh = malloc(sizeof(int32_t) * C);
+  for (int t = 0; t < T; ++t)
+    for (int b = 0; b < B; ++b) {
+      const int32_t *hp = h_q + (size_t)t * NH + (size_t)b * H;
+      const size_t n = (size_t)t * B + b;
+      /* recurrent projection: R_q (h - zp_h) + rescaled br -> weight_hh_linear */
+      for (int c = 0; c < C; ++c) {
+        int64_t acc = 0;
+        for (int r = 0; r < H; ++r)
+          acc += (int64_t)R_q[(size_t)r * C + c] * ((int64_t)hp[r] - zp_h);
+        const int64_t bb = apply_rescale((int64_t)br_q[c], rbr[c]);
+        const int32_t res = add32((int32_t)apply_rescale(acc + bb, rgh[c]), zp_rh);
+        rh[c] = clampi(res, GB(RXMET_GRU_RH), KEEP(hh_mask, n * C + c));
+      }
+      const int32_t *wxn = wx + n * C;
+      for (int j = 0; j < H; ++j) {
+        const size_t mi = n * C + j;
+        /* update gate */
+        int32_t in = add32(add32((int32_t)apply_rescale((int64_t)wxn[j] - zp_wx, ih_zin),
+                                 (int32_t)apply_rescale((int64_t)rh[j] - zp_rh, hh_zin)),
+                           zp_zin);
+        in = clampi(in, GB(RXMET_GRU_Z_IN), KEEP(gin_mask, mi));
+        const int32_t z = clampi(pwl_int(in, &lut[0]), GB(RXMET_GRU_Z_OUT), KEEP(gout_mask, mi));
+        /* reset gate */
+        in = add32(add32((int32_t)apply_rescale((int64_t)wxn[H + j] - zp_wx, ih_rin),
+                         (int32_t)apply_rescale((int64_t)rh[H + j] - zp_rh, hh_rin)),
+                   zp_rin);
+        in = clampi(in, GB(RXMET_GRU_R_IN), KEEP(gin_mask, mi + H));
+        const int32_t r = clampi(pwl_int(in, &lut[1]), GB(RXMET_GRU_R_OUT),
+                                 KEEP(gout_mask, mi + H));
+        /* new gate: r (weight_hh_linear of n) aligned to new_gate_input in one rescale */
+        const int64_t rmul = ((int64_t)r - zp_rout) * ((int64_t)rh[2 * H + j] - zp_rh);
+        in = add32(add32((int32_t)apply_rescale((int64_t)wxn[2 * H + j] - zp_wx, ih_nin),
+                         (int32_t)apply_rescale(rmul, rmul_nin)),
+                   zp_nin);
+        in = clampi(in, GB(RXMET_GRU_N_IN), KEEP(gin_mask, mi + 2 * H));
+        const int32_t nn = clampi(pwl_int(in, &lut[2]), GB(RXMET_GRU_N_OUT),
+                                  KEEP(gout_mask, mi + 2 * H));
+        /* hidden update: u h_old + (1 - u) n on the scale S_zout S_h, one rescale to h */
+        const int32_t n_h = add32((int32_t)apply_rescale((int64_t)nn - zp_nout, nout_h), zp_h);
+        const int64_t oldc = ((int64_t)z - zp_zout) * ((int64_t)hp[j] - zp_h);
+        const int64_t newc = ((int64_t)quant_one - z) * ((int64_t)n_h - zp_h);
+        const int32_t hn = add32((int32_t)apply_rescale(oldc + newc, old_h), zp_h);
+        const size_t hi = (size_t)t * NH + (size_t)b * H + j;
+        h_q[hi + NH] = clampi(hn, GB(RXMET_GRU_H), KEEP(h_mask, hi));
+        if (v_q) {
+          const size_t vb = n * 4 * H + j;
+          v_q[vb] = z;
+          v_q[vb + H] = r;
+          v_q[vb + 2 * H] = nn;
+          v_q[vb + 3 * H] = rh[2 * H + j];
+        }
+      }
+    }
+#undef GB
+#undef KEEP
+  free(rgx); free(rbw); free(rgh); free(rbr); free(wx); free(rh);
+  return 0;
+}

@@ -39,6 +39,8 @@ _o.oracle_gru_forward_calibrate.argtypes = [_i] * 4 + [_P] * 9
 _o.oracle_gru_forward_quant.argtypes = [_i] * 5 + [_P] * 6 + [ctypes.POINTER(A.GruQParams)] + [_P] * 18
 _o.oracle_gru_backward_quant.argtypes = [_i] * 4 + [_P] * 8 + [ctypes.POINTER(A.GruQParams)] + \
     [_P] * 11 + [_P] * 6
+_o.oracle_gru_forward_int.argtypes = [_i] * 5 + [_P] * 8 + [ctypes.POINTER(A.GruQParams)] + \
+    [_P] * 7 + [_P] * 11
 
 _REF_PATH = HERE / "_ref" / "libgru_ref.so"
 _ref = ctypes.CDLL(str(_REF_PATH)) if _REF_PATH.exists() else None
@@ -48,6 +50,8 @@ if _ref is not None:
     _ref.ref_gru_forward_calibrate.argtypes = [_i] * 4 + [_P] * 9
     _ref.ref_gru_forward_ptq.argtypes = [_i] * 4 + [_P] * 6 + [ctypes.POINTER(A.GruRanges),
                                                                 ctypes.POINTER(A.GruConfig), _P, _P]
+    _ref.ref_gru_forward_int_codes.argtypes = [_i] * 4 + [_P] * 8 + \
+        [ctypes.POINTER(A.GruQParams)] + [_P] * 7
 
 
 def has_ref() -> bool:
@@ -174,3 +178,75 @@ def ref_forward_ptq(W, R, bw, br, x, ranges, cfg, h0=None):
     if rc != 0:
         raise RuntimeError("ref forward_ptq failed")
     return h, v
+
+
+I32 = np.int32
+
+
+def _ci(a):
+    return None if a is None else np.ascontiguousarray(a, dtype=I32)
+
+
+def forward_int(W, R, bw, br, x, qp, h0=None, training=True, x_q=None, h0_q=None):
+    """int32 carrier (forward_quant_int_storage / forward_quantized_int_io semantics).
+
+    With x_q (int32 [T,B,I]) given, x is ignored and the codes are used as they are, and
+    h0_q (int32 [B,H]) likewise replaces h0.  Returns int32 codes h_q [T+1,B,H],
+    v_q [T,B,4H], W_q, R_q, bw_q, br_q, x_q and, in training, the eleven uint8 masks."""
+    T, B, I = (x_q if x_q is not None else x).shape
+    H = R.shape[0]
+    C = 3 * H
+    W, R, bw, br, x, h0 = (_c(a) for a in (W, R, bw, br, x, h0))
+    x_q, h0_q = _ci(x_q), _ci(h0_q)
+    o = {
+        "h_q": np.zeros((T + 1, B, H), I32), "v_q": np.zeros((T, B, 4 * H), I32),
+        "W_q": np.zeros((I, C), I32), "R_q": np.zeros((H, C), I32), "bw_q": np.zeros(C, I32),
+        "br_q": np.zeros(C, I32),
+        "x_q": x_q.copy() if x_q is not None else np.zeros((T, B, I), I32),
+    }
+    mk = {
+        "x_mask": (T, B, I), "h0_mask": (B, H), "W_mask": (I, C), "R_mask": (H, C), "bw_mask": (C,),
+        "br_mask": (C,), "ih_mask": (T, B, C), "hh_mask": (T, B, C), "gate_in_mask": (T, B, C),
+        "gate_out_mask": (T, B, C), "h_mask": (T, B, H),
+    }
+    skip = set()
+    if x_q is not None:
+        skip.add("x_mask")
+    if h0 is None or h0_q is not None:
+        skip.add("h0_mask")
+    for k, shp in mk.items():
+        o[k] = np.zeros(shp, np.uint8) if (training and k not in skip) else None
+    rc = _o.oracle_gru_forward_int(
+        int(training), T, B, I, H, _p(W), _p(R), _p(bw), _p(br), _p(x), _p(x_q), _p(h0),
+        _p(h0_q), ctypes.byref(qp),
+        *(_p(o[k]) for k in ("h_q", "v_q", "W_q", "R_q", "bw_q", "br_q")),
+        None if x_q is not None else _p(o["x_q"]), *(_p(o[k]) for k in mk))
+    if rc != 0:
+        raise RuntimeError("forward_int failed")
+    return o
+
+
+def dequant_int(codes, grid, use_pot2: bool):
+    """dequantize(q, FixedPointScale, zp): (q - zp) in int32, converted, times the effective
+    scale (quantize_ops_helper.h:450-454)."""
+    d = (np.asarray(codes, I32) - I32(grid.zero_point)).astype(f32)
+    return d * f32(effective_scale(grid.scale, use_pot2))
+
+
+def ref_forward_int_codes(W, R, bw, br, x, qp, h0=None, x_q=None, h0_q=None, with_v=True):
+    """The reference's CPU int32 carrier on codes (oracle/_ref ref_gru_forward_int_codes)."""
+    T, B, I = (x_q if x_q is not None else x).shape
+    H = R.shape[0]
+    C = 3 * H
+    W, R, bw, br, x, h0 = (_c(a) for a in (W, R, bw, br, x, h0))
+    x_q, h0_q = _ci(x_q), _ci(h0_q)
+    o = {"h_q": np.zeros((T + 1, B, H), I32),
+         "v_q": np.zeros((T, B, 4 * H), I32) if with_v else None,
+         "W_q": np.zeros((I, C), I32), "R_q": np.zeros((H, C), I32), "bw_q": np.zeros(C, I32),
+         "br_q": np.zeros(C, I32), "x_q": np.zeros((T, B, I), I32)}
+    rc = _ref.ref_gru_forward_int_codes(
+        T, B, I, H, _p(W), _p(R), _p(bw), _p(br), _p(x), _p(x_q), _p(h0), _p(h0_q),
+        ctypes.byref(qp), *(_p(o[k]) for k in ("h_q", "v_q", "W_q", "R_q", "bw_q", "br_q", "x_q")))
+    if rc != 0:
+        raise RuntimeError("ref forward_int_codes failed")
+    return o

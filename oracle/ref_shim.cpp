@@ -2,12 +2,14 @@
 // from /root/reference/operators/quant-gru/src into oracle/_ref/libgru_ref.so by
 // oracle/Makefile.  TEST INFRASTRUCTURE: used by tests/ (to pin the oracle's parameter
 // derivation, LUT generation, calibration forward and the int-carrier agreement) and by
-// bench.py's CPU-baseline legs, which time the reference's calibration and PTQ forwards.
+// bench.py's CPU-baseline legs, which time the reference's calibration and PTQ forwards;
+// ref_gru_forward_int_codes pins the oracle's int32-carrier forward.
 // Nothing here is part of the product.
 #include <cstring>
 #include <stdexcept>
 
 #include "gru_host.h"
+#include "gru_quant_cpu.h"
 #include "quantize_ops_helper.h"
 #include "rxmet_gru.h"
 
@@ -64,6 +66,41 @@ void lut_out(const SigmoidLUT &l, rxmet_pwl_lut *o) {
     o->seg[i].threshold = l.segments[i].threshold;
   }
   o->zp_x = l.zp_x;
+}
+
+// GRUQuantParams straight from a parameter block (scales, zero points, bit widths; weights
+// per channel), with the LUTs the reference generates from them.
+GRUQuantParams params_of(const rxmet_gru_qparams &qp) {
+  GRUQuantParams p;
+  const int H = qp.hidden, C = 3 * H;
+  OperatorQuantConfig &o = p.bitwidth_config_;
+  QuantBitWidth *ops[RXMET_GRU_NGRIDS] = {
+      &o.x_, &o.h_, &o.weight_ih_linear_, &o.weight_hh_linear_, &o.update_gate_input_,
+      &o.reset_gate_input_, &o.new_gate_input_, &o.update_gate_output_, &o.reset_gate_output_,
+      &o.new_gate_output_, &o.mul_reset_hidden_, &o.mul_new_contribution_,
+      &o.mul_old_contribution_};
+  QuantParam *g[RXMET_GRU_NGRIDS] = {
+      &p.x_, &p.h_, &p.weight_ih_linear_, &p.weight_hh_linear_, &p.update_gate_input_,
+      &p.reset_gate_input_, &p.new_gate_input_, &p.update_gate_output_,
+      &p.reset_gate_output_, &p.new_gate_output_, &p.mul_reset_hidden_,
+      &p.mul_new_contribution_, &p.mul_old_contribution_};
+  for (int i = 0; i < RXMET_GRU_NGRIDS; ++i) {
+    *ops[i] = QuantBitWidth(static_cast<int8_t>(qp.g[i].bits), qp.g[i].is_unsigned != 0);
+    g[i]->scale = qp.g[i].scale;
+    g[i]->zero_point = qp.g[i].zero_point;
+  }
+  QuantBitWidth *ch[4] = {&o.W_, &o.R_, &o.bw_, &o.br_};
+  ChannelQuantParam *cp[4] = {&p.W_, &p.R_, &p.bw_, &p.br_};
+  for (int k = 0; k < 4; ++k) {
+    *ch[k] = QuantBitWidth(static_cast<int8_t>(qp.chan_bits[k]), qp.chan_unsigned[k] != 0);
+    cp[k]->hidden = H;
+    cp[k]->resize(C);
+    for (int c = 0; c < C; ++c) cp[k]->channel(c).scale = qp.chan_scale[k][c];
+  }
+  o.usePOT2_ = qp.use_pot2 != 0;
+  p.hidden_ = H;
+  generate_piecewise_linear_lut_to_params(p);
+  return p;
 }
 
 }  // namespace
@@ -206,6 +243,54 @@ int ref_gru_forward_ptq(int T, int B, int I, int H, const float *W, const float 
     // the reference writes v (gate codes, dequantised) only in training mode, the only
     // difference training makes to its CPU forward (gru_forward_cpu_quant.cc:199)
     quantGRUForwardCPU(v != nullptr, T, B, I, H, W, R, bw, br, x, h0, p, h, v);
+    return 0;
+  } catch (const std::exception &) {
+    return -1;
+  }
+}
+
+// The reference's CPU int32 carrier on codes: quantitativeWeightCPU, the boundary
+// quantisation of quantGRUForwardCPU (src/gru_host.cc:161-216) unless x_q / h0_q are given
+// (then as quantGRUForwardIntIO, src/gru_interface.cc:561-627, on the CPU carrier), and
+// ForwardPassQuantCPU::Run.  Writes the int32 h codes [T+1, B, H], the v codes [T, B, 4H]
+// (when v_q is non-null; training mode) and, when non-null, the weight and input codes.
+int ref_gru_forward_int_codes(int T, int B, int I, int H, const float *W, const float *R,
+                              const float *bw, const float *br, const float *x,
+                              const int32_t *x_q_in, const float *h0, const int32_t *h0_q_in,
+                              const rxmet_gru_qparams *qp, int32_t *h_q, int32_t *v_q,
+                              int32_t *W_q, int32_t *R_q, int32_t *bw_q, int32_t *br_q,
+                              int32_t *x_q) {
+  try {
+    const int C = 3 * H;
+    const GRUQuantParams p = params_of(*qp);
+    std::vector<int32_t> wq(static_cast<size_t>(I) * C), rq(static_cast<size_t>(H) * C), bwq(C),
+        brq(C);
+    quantitativeWeightCPU(I, H, W, R, bw, br, p, wq.data(), rq.data(), bwq.data(), brq.data());
+    const bool pot = p.bitwidth_config_.usePOT2_;
+    const size_t nx = static_cast<size_t>(T) * B * I, nh = static_cast<size_t>(B) * H;
+    std::vector<int32_t> xq(nx);
+    if (x_q_in) {
+      std::memcpy(xq.data(), x_q_in, sizeof(int32_t) * nx);
+    } else {
+      for (size_t i = 0; i < nx; ++i)
+        xq[i] = quantize(x[i], toFixedScale(p.x_, pot), p.x_.zero_point, p.bitwidth_config_.x_);
+    }
+    for (size_t i = 0; i < nh; ++i) {
+      if (h0_q_in)
+        h_q[i] = h0_q_in[i];
+      else if (h0)
+        h_q[i] = quantize(h0[i], toFixedScale(p.h_, pot), p.h_.zero_point, p.bitwidth_config_.h_);
+      else
+        h_q[i] = p.h_.zero_point;
+    }
+    cpu::ForwardPassQuantCPU fwd(v_q != nullptr, B, I, H);
+    fwd.setRescaleParam(p);
+    fwd.Run(T, wq.data(), rq.data(), bwq.data(), brq.data(), xq.data(), h_q, v_q, 0.0f, nullptr);
+    if (W_q) std::memcpy(W_q, wq.data(), sizeof(int32_t) * wq.size());
+    if (R_q) std::memcpy(R_q, rq.data(), sizeof(int32_t) * rq.size());
+    if (bw_q) std::memcpy(bw_q, bwq.data(), sizeof(int32_t) * C);
+    if (br_q) std::memcpy(br_q, brq.data(), sizeof(int32_t) * C);
+    if (x_q) std::memcpy(x_q, xq.data(), sizeof(int32_t) * nx);
     return 0;
   } catch (const std::exception &) {
     return -1;

@@ -30,19 +30,22 @@ namespace xgemm {
 constexpr int kTile = 64;
 constexpr int kRowBytes = 64 + 16;  // LDS row stride (conflict-free 16-byte reads)
 
-struct Operands {
+// Codes stored as fp32 (integer valued) or as int32.
+template <typename EA, typename EB>
+struct OperandsT {
   int M, N, K;
-  const float *A;  // A[m * lda + k]
+  const EA *A;     // A[m * lda + k]
   int lda;
   float off;       // shift of A (integer valued)
   long long corr;  // off - base
-  const float *B;  // B(k, n) = B[k * sbk + n * sbn]
+  const EB *B;     // B(k, n) = B[k * sbk + n * sbn]
   int sbk, sbn;
 };
+using Operands = OperandsT<float, float>;
 
 // Computes the 64 x 64 block at (tm, tn) and calls epi(m, n, S) for every in-range output.
-template <int PA, int PB, typename Epi>
-__device__ __forceinline__ void block(const Operands &o, int tm, int tn, Epi epi) {
+template <int PA, int PB, typename EA, typename EB, typename Epi>
+__device__ __forceinline__ void block(const OperandsT<EA, EB> &o, int tm, int tn, Epi epi) {
   __shared__ __align__(16) int8_t As[PA][kTile][kRowBytes];
   __shared__ __align__(16) int8_t Bs[PB][kTile][kRowBytes];
   const int tid = threadIdx.x, w = tid / 64, l = tid % 64;
@@ -72,7 +75,7 @@ __device__ __forceinline__ void block(const Operands &o, int tm, int tn, Epi epi
       const int gm = tm + r, gk = k0 + kk;
       int v = 0;
       if (gm < o.M && gk < o.K)
-        v = static_cast<int>(o.A[static_cast<size_t>(gm) * o.lda + gk] - o.off);
+        v = static_cast<int>(o.A[static_cast<size_t>(gm) * o.lda + gk]) - static_cast<int>(o.off);
       if (PA == 1) {
         As[0][r][kk] = static_cast<int8_t>(v);
       } else {
@@ -253,11 +256,15 @@ __device__ __forceinline__ void rows16(const Packed &p, int m0, int nt0, int ste
   }
 }
 
-// Host launchers (exact_gemm.hip).
+// Host launchers (exact_gemm.hip), for codes stored as fp32 or int32.
 int pack_a(const float *A, int64_t lda, int M, int K, float off, int PA, int8_t *out, int Kp,
+           hipStream_t stream);
+int pack_a(const int32_t *A, int64_t lda, int M, int K, float off, int PA, int8_t *out, int Kp,
            hipStream_t stream);
 // B(k, n) = B[k sbk + n sbn] (integer codes), PB planes.
 int pack_b(const float *B, int64_t sbk, int64_t sbn, int K, int N, int PB, int Kp, v4i *frag,
+           long long *colsum, hipStream_t stream);
+int pack_b(const int32_t *B, int64_t sbk, int64_t sbn, int K, int N, int PB, int Kp, v4i *frag,
            long long *colsum, hipStream_t stream);
 inline int pad_k(int K) { return (K + 63) / 64 * 64; }
 

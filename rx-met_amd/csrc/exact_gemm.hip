@@ -1,4 +1,5 @@
-// exact_gemm.hip — operand packing for the pre-packed exact GEMM (exact_gemm.h).
+// exact_gemm.hip — operand packing for the pre-packed exact GEMM (exact_gemm.h), for codes
+// stored as fp32 or int32.
 #include "exact_gemm.h"
 
 #include "rxmet_common.h"
@@ -7,7 +8,8 @@ namespace rxmet {
 namespace xgemm {
 
 // A planes: four k per thread, written as one 32-bit word per plane.
-__global__ __launch_bounds__(256) void pack_a_kernel(const float *__restrict__ A, int64_t lda, int M,
+template <typename E>
+__global__ __launch_bounds__(256) void pack_a_kernel(const E *__restrict__ A, int64_t lda, int M,
                                                      int K, float off, int PA, int8_t *__restrict__ out,
                                                      int Kp) {
   const int64_t words = static_cast<int64_t>(M) * (Kp / 4), plane = static_cast<int64_t>(M) * Kp;
@@ -19,7 +21,7 @@ __global__ __launch_bounds__(256) void pack_a_kernel(const float *__restrict__ A
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int k = k0 + e;
-      const int v = k < K ? static_cast<int>(A[m * lda + k] - off) : 0;
+      const int v = k < K ? static_cast<int>(A[m * lda + k]) - static_cast<int>(off) : 0;
       if (PA == 1) {
         lo |= static_cast<unsigned>(v & 255) << (8 * e);
       } else {
@@ -35,7 +37,8 @@ __global__ __launch_bounds__(256) void pack_a_kernel(const float *__restrict__ A
 
 // B fragments: block (nt, s), lane l packs 16 k of column 16 nt + l % 16; the s == 0 blocks
 // also sum each column exactly.
-__global__ __launch_bounds__(64) void pack_b_kernel(const float *__restrict__ B, int64_t sbk,
+template <typename E>
+__global__ __launch_bounds__(64) void pack_b_kernel(const E *__restrict__ B, int64_t sbk,
                                                     int64_t sbn, int K, int N, int PB, int Kp,
                                                     v4i *__restrict__ frag,
                                                     long long *__restrict__ colsum) {
@@ -71,26 +74,45 @@ __global__ __launch_bounds__(64) void pack_b_kernel(const float *__restrict__ B,
   }
 }
 
-int pack_a(const float *A, int64_t lda, int M, int K, float off, int PA, int8_t *out, int Kp,
-           hipStream_t stream) {
+template <typename E>
+static int pack_a_t(const E *A, int64_t lda, int M, int K, float off, int PA, int8_t *out, int Kp,
+                    hipStream_t stream) {
   RXMET_CHECK_ARG((PA == 1 || PA == 2) && Kp % 64 == 0 && Kp >= K, "bad A packing");
   const int64_t words = static_cast<int64_t>(M) * (Kp / 4);
   int64_t blocks = (words + 255) / 256;
   if (blocks > 8192) blocks = 8192;
-  hipLaunchKernelGGL(pack_a_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, A,
-                     lda, M, K, off, PA, out, Kp);
+  hipLaunchKernelGGL(pack_a_kernel<E>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
+                     A, lda, M, K, off, PA, out, Kp);
   RXMET_CHECK_LAUNCH();
   return 0;
 }
 
-int pack_b(const float *B, int64_t sbk, int64_t sbn, int K, int N, int PB, int Kp, v4i *frag,
-           long long *colsum, hipStream_t stream) {
+template <typename E>
+static int pack_b_t(const E *B, int64_t sbk, int64_t sbn, int K, int N, int PB, int Kp, v4i *frag,
+                    long long *colsum, hipStream_t stream) {
   RXMET_CHECK_ARG((PB == 1 || PB == 2) && Kp % 64 == 0 && Kp >= K, "bad B packing");
   const int blocks = ((N + 15) / 16) * (Kp / 64);
-  hipLaunchKernelGGL(pack_b_kernel, dim3(blocks), dim3(64), 0, stream, B, sbk, sbn, K, N, PB, Kp,
-                     frag, colsum);
+  hipLaunchKernelGGL(pack_b_kernel<E>, dim3(blocks), dim3(64), 0, stream, B, sbk, sbn, K, N, PB,
+                     Kp, frag, colsum);
   RXMET_CHECK_LAUNCH();
   return 0;
+}
+
+int pack_a(const float *A, int64_t lda, int M, int K, float off, int PA, int8_t *out, int Kp,
+           hipStream_t stream) {
+  return pack_a_t(A, lda, M, K, off, PA, out, Kp, stream);
+}
+int pack_a(const int32_t *A, int64_t lda, int M, int K, float off, int PA, int8_t *out, int Kp,
+           hipStream_t stream) {
+  return pack_a_t(A, lda, M, K, off, PA, out, Kp, stream);
+}
+int pack_b(const float *B, int64_t sbk, int64_t sbn, int K, int N, int PB, int Kp, v4i *frag,
+           long long *colsum, hipStream_t stream) {
+  return pack_b_t(B, sbk, sbn, K, N, PB, Kp, frag, colsum, stream);
+}
+int pack_b(const int32_t *B, int64_t sbk, int64_t sbn, int K, int N, int PB, int Kp, v4i *frag,
+           long long *colsum, hipStream_t stream) {
+  return pack_b_t(B, sbk, sbn, K, N, PB, Kp, frag, colsum, stream);
 }
 
 }  // namespace xgemm

@@ -930,7 +930,7 @@ struct FwdWorkspace {
     // packed operands of the input projection (I <= 256): x planes, W fragments, W column sums
     const size_t ip = static_cast<size_t>(I) <= kPackedMaxK ? 1 : 0;
     xa = o; o += al(ip * 2 * static_cast<size_t>(T) * B * Kp);
-    bfrag = o; o += al(ip * 2 * C * Kp);
+    bfrag = o; o += al(ip * 2 * ((C + 15) / 16 * 16) * Kp);  // fragments of 16-column tiles
     colsum = o; o += al(ip * sizeof(long long) * C);
     // stepped recurrence: two h code buffers [B, H] and the recurrent sums [B, 3H]
     sh = o; o += al(sizeof(float) * 2 * static_cast<size_t>(B) * H);

@@ -1,0 +1,575 @@
+// gru_int.hip — MI355X QuantGRU forward on the int32 carrier, behind
+// rxmet_gru_forward_quant_int (forward_quant_int_storage) and rxmet_gru_forward_int_io
+// (forward_quantized_int_io).
+//
+// Reference path: quantGRUForwardInt / quantGRUForwardIntIO (operators/quant-gru/src/
+// gru_interface.cc:384-627) over ForwardPassQuant (src/gru_forward_gpu_quant.cu): per-channel
+// weight quantisation, x/h0 quantisation, one tiled int64 GEMM+bias kernel for the input
+// projection, then a host loop of T steps each launching a tiled GEMM+bias kernel for R h and
+// the integer pointwise kernel, and dequantisation passes over h and v.  Every value between
+// the boundaries is an integer code; rescales are rshift_round(x M, shift) with a 16-bit
+// mantissa M (or a pure shift in power-of-two mode) and activations are 16-segment PWL tables on
+// codes.
+//
+// Here:
+//   1. iq_weights : W/R/bw/br -> int32 codes + masks in one pass, plus the two bias terms
+//      rescaled into each GEMM's accumulator scale;
+//   2. iq_input   : x -> int32 codes + mask, h0 -> codes of row 0 (+ mask, + dequantised h[0]);
+//   3. wx_gemm    : the time-parallel input projection summed exactly on int8 MFMA over
+//      byte planes (exact_gemm.h, int32 operands), with the GEMM+bias rescale, clamp and mask
+//      fused into the epilogue;
+//   4. per step, rh_gemm (the same for R_q (h - zp_h)) and int_point: the integer update,
+//      reset and new gates, the hidden update, clamps and masks, the dequantised h and v.
+#include <cmath>
+#include <vector>
+
+#include "cluster.h"
+#include "exact_gemm.h"
+#include "gru_internal.h"
+#include "rxmet_common.h"
+#include "rxmet_gru.h"
+
+namespace rxmet {
+namespace gru {
+namespace {
+
+// rshift_round (include/quantize_ops_helper.h:201-224): round(x / 2^n), ties to even, on |x|;
+// a left shift for n <= 0.  Shifts lie in [-32, 62] (checked on the host).
+__device__ __forceinline__ long long rshift_round(long long x, int n) {
+  if (n <= 0) return static_cast<long long>(static_cast<unsigned long long>(x) << (-n));
+  const bool neg = x < 0;
+  const unsigned long long ax =
+      neg ? 0ull - static_cast<unsigned long long>(x) : static_cast<unsigned long long>(x);
+  const unsigned long long q = ax >> n, r = ax & ((1ull << n) - 1ull), half = 1ull << (n - 1);
+  const unsigned long long res = r > half ? q + 1ull : (r < half ? q : q + (q & 1ull));
+  return neg ? -static_cast<long long>(res) : static_cast<long long>(res);
+}
+
+__device__ __forceinline__ long long rescale(long long x, IRescale r) {
+  return rshift_round(x * static_cast<long long>(r.mult), r.shift);
+}
+
+// int32 addition with two's-complement wrap (the reference adds int32 values).
+__device__ __forceinline__ int32_t add32(int32_t a, int32_t b) {
+  return static_cast<int32_t>(static_cast<uint32_t>(a) + static_cast<uint32_t>(b));
+}
+
+__device__ __forceinline__ int32_t clampi(int32_t v, IGrid g, uint8_t &keep) {
+  keep = (v < g.lo || v > g.hi) ? 0 : 1;
+  return v < g.lo ? g.lo : (v > g.hi ? g.hi : v);
+}
+
+// quantize(float, FixedPointScale, zp, bw) (quantize_ops_helper.h:356-364, 472-476): rint of
+// the quotient in fp32, the zero point added in double, saturated before the conversion.
+__device__ __forceinline__ int32_t quant_i(float v, float eff, int32_t zp, IGrid g,
+                                           uint8_t &keep) {
+  const double code = static_cast<double>(rintf(v / eff)) + static_cast<double>(zp);
+  keep = (code < g.lo || code > g.hi) ? 0 : 1;
+  return code < g.lo ? g.lo : (code > g.hi ? g.hi : static_cast<int32_t>(code));
+}
+
+// piecewise_linear_raw (quantize_ops_helper.h:503-535) over a table in LDS.
+__device__ __forceinline__ int32_t pwl_i(int32_t q, const ILut &l) {
+  int s = kSegments - 1;
+#pragma unroll
+  for (int i = kSegments - 1; i >= 0; --i)
+    if (q < l.thr[i]) s = i;
+  const long long bx = static_cast<long long>(l.qb[s]) *
+                       static_cast<long long>(static_cast<int32_t>(static_cast<uint32_t>(q) -
+                                                                   static_cast<uint32_t>(l.zp_x)));
+  const int n = l.n[s];
+  const int32_t term =
+      n >= 0 ? static_cast<int32_t>(rshift_round(bx, n))
+             : static_cast<int32_t>(static_cast<long long>(static_cast<unsigned long long>(bx) << (-n)));
+  return add32(term, l.c[s]);
+}
+
+// ---------------------------------------------------------------------------------
+// 1. weights
+// ---------------------------------------------------------------------------------
+struct IWeightArgs {
+  const float *W, *R, *bw, *br;  // [I, 3H], [H, 3H], [3H], [3H]
+  const float *eff;              // [4][3H] effective scales of W, R, bw, br
+  const IRescale *rs;            // [4][3H] channel rescales (gemm_x, bw, gemm_h, br)
+  IGrid gW, gR, gbw, gbr;
+  int32_t *Wq, *Rq, *bwq, *brq;
+  uint8_t *Wm, *Rm, *bwm, *brm;
+  long long *bias;  // [2][3H]: bw and br in their GEMM's accumulator scale
+};
+
+__global__ __launch_bounds__(256) void iq_weights(int I, int H, IWeightArgs a) {
+  const int C = 3 * H;
+  const int64_t nW = static_cast<int64_t>(I) * C, nR = static_cast<int64_t>(H) * C;
+  const int64_t total = nW + nR + C;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+       i += stride) {
+    uint8_t keep;
+    if (i < nW) {
+      const int c = static_cast<int>(i % C);
+      a.Wq[i] = quant_i(a.W[i], a.eff[c], 0, a.gW, keep);
+      if (a.Wm) a.Wm[i] = keep;
+    } else if (i < nW + nR) {
+      const int64_t j = i - nW;
+      const int c = static_cast<int>(j % C);
+      a.Rq[j] = quant_i(a.R[j], a.eff[C + c], 0, a.gR, keep);
+      if (a.Rm) a.Rm[j] = keep;
+    } else {
+      const int c = static_cast<int>(i - nW - nR);
+      const int32_t qb = quant_i(a.bw[c], a.eff[2 * C + c], 0, a.gbw, keep);
+      a.bwq[c] = qb;
+      if (a.bwm) a.bwm[c] = keep;
+      const int32_t qr = quant_i(a.br[c], a.eff[3 * C + c], 0, a.gbr, keep);
+      a.brq[c] = qr;
+      if (a.brm) a.brm[c] = keep;
+      a.bias[c] = rescale(qb, a.rs[C + c]);
+      a.bias[C + c] = rescale(qr, a.rs[3 * C + c]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// 2. inputs
+// ---------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void iq_input(int64_t nx, int64_t nh, const float *x,
+                                                const float *h0, const int32_t *h0q,
+                                                IntStepParams p, int32_t *xq, uint8_t *xm,
+                                                int32_t *hq0, uint8_t *h0m, float *hout0) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < nx + nh;
+       i += stride) {
+    uint8_t keep;
+    if (i < nx) {
+      xq[i] = quant_i(x[i], p.eff_x, p.zp_x, p.x, keep);
+      if (xm) xm[i] = keep;
+    } else {
+      const int64_t j = i - nx;
+      int32_t q = p.zp_h;
+      if (h0q) {
+        q = h0q[j];
+      } else if (h0) {
+        q = quant_i(h0[j], p.eff_h, p.zp_h, p.h, keep);
+        if (h0m) h0m[j] = keep;
+      }
+      hq0[j] = q;
+      if (hout0)
+        hout0[j] = static_cast<float>(static_cast<int32_t>(static_cast<uint32_t>(q) -
+                                                           static_cast<uint32_t>(p.zp_h))) *
+                   p.eff_h;
+    }
+  }
+}
+
+// Codes outside [lo, hi] set *flag (int-IO inputs must lie on their grids).
+__global__ __launch_bounds__(256) void check_codes(const int32_t *a, int64_t n, int32_t lo,
+                                                   int32_t hi, int *flag) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  bool bad = false;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
+    bad = bad || a[i] < lo || a[i] > hi;
+  if (bad) atomicOr(flag, 1);
+}
+
+// ---------------------------------------------------------------------------------
+// 3./4a. GEMM + bias + rescale + clamp (quantizedGemmBiasFused,
+//        src/gru_forward_gpu_quant.cu:112-176) on exact int8-MFMA sums
+// ---------------------------------------------------------------------------------
+// S(m, c) = sum_k (A(m, k) - zp) B(k, c) exactly; out(m, c) = clamp(int32(rescale(S + bias[c],
+// rs[c])) + zp_out), mask (1 = kept) when non-null.
+struct LinearOut {
+  const long long *bias;
+  const IRescale *rs;
+  int32_t zp_out;
+  IGrid g;
+  int32_t *out;
+  uint8_t *mask;
+  int ld;  // row stride of out and mask
+};
+
+__device__ __forceinline__ void linear_store(const LinearOut &e, int m, int c, long long s) {
+  uint8_t keep;
+  const int32_t v = clampi(add32(static_cast<int32_t>(rescale(s + e.bias[c], e.rs[c])), e.zp_out),
+                           e.g, keep);
+  const size_t i = static_cast<size_t>(m) * e.ld + c;
+  e.out[i] = v;
+  if (e.mask) e.mask[i] = keep;
+}
+
+template <int PA, int PB>
+__global__ __launch_bounds__(256) void linear_gemm(xgemm::OperandsT<int32_t, int32_t> o,
+                                                   LinearOut e) {
+  xgemm::block<PA, PB>(o, blockIdx.y * xgemm::kTile, blockIdx.x * xgemm::kTile,
+                       [&](int m, int n, long long s) { linear_store(e, m, n, s); });
+}
+
+constexpr int kPackedMaxK = 256;
+template <int PA, int PB>
+__global__ __launch_bounds__(256) void linear_gemm_packed(xgemm::Packed p, LinearOut e) {
+  xgemm::rows16<PA, PB>(p, 16 * blockIdx.x, threadIdx.x / 64, 4,
+                        [&](int m, int n, const long long *s, int rows) {
+#pragma unroll
+                          for (int r = 0; r < 4; ++r)
+                            if (r < rows) linear_store(e, m + r, n, s[r]);
+                        });
+}
+
+// ---------------------------------------------------------------------------------
+// 4b. pointwise step (PointwiseOperationsQuant, src/gru_forward_gpu_quant.cu:230-373, with
+//     computeUpdateGate / ResetGate / NewGate / HiddenState, quantize_ops_helper.h:683-1023)
+// ---------------------------------------------------------------------------------
+struct IPointArgs {
+  int T, B, H;
+  const int32_t *wx;  // [T, B, 3H] weight_ih_linear codes
+  const int32_t *rh;  // [B, 3H] weight_hh_linear codes of the step
+  float *hout;        // [T+1, B, H] dequantised h, or null
+  float *v;           // [T, B, 4H] dequantised (z, r, n, weight_hh_linear n), or null
+  uint8_t *gin_m, *gout_m, *h_m;  // training masks, or null
+};
+
+__device__ __forceinline__ float dq(int32_t q, int32_t zp, float eff) {
+  return static_cast<float>(add32(q, -zp)) * eff;
+}
+
+__global__ __launch_bounds__(256) void int_point(IPointArgs a, IntStepParams p, int t,
+                                                 const int32_t *hq, int32_t *hq_next) {
+  __shared__ ILut lut[3];
+  for (int i = threadIdx.x; i < 3 * static_cast<int>(sizeof(ILut) / 4); i += blockDim.x)
+    reinterpret_cast<int32_t *>(lut)[i] = reinterpret_cast<const int32_t *>(p.lut)[i];
+  __syncthreads();
+  const int H = a.H, C = 3 * H;
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (e >= static_cast<int64_t>(a.B) * H) return;
+  const int b = static_cast<int>(e / H), j = static_cast<int>(e % H);
+  const size_t n = static_cast<size_t>(t) * a.B + b;
+  const int32_t *wx = a.wx + n * C;
+  const int32_t *rh = a.rh + static_cast<size_t>(b) * C;
+  const int32_t wz = wx[j], wr = wx[H + j], wn = wx[2 * H + j];
+  const int32_t hz = rh[j], hr = rh[H + j], hn = rh[2 * H + j];
+  uint8_t k_zi, k_zo, k_ri, k_ro, k_ni, k_no, k_h;
+  // update gate
+  int32_t in = add32(add32(static_cast<int32_t>(rescale(static_cast<long long>(wz) - p.zp_wx, p.ih_zin)),
+                           static_cast<int32_t>(rescale(static_cast<long long>(hz) - p.zp_rh, p.hh_zin))),
+                     p.zp_zin);
+  in = clampi(in, p.zin, k_zi);
+  const int32_t z = clampi(pwl_i(in, lut[0]), p.zout, k_zo);
+  // reset gate
+  in = add32(add32(static_cast<int32_t>(rescale(static_cast<long long>(wr) - p.zp_wx, p.ih_rin)),
+                   static_cast<int32_t>(rescale(static_cast<long long>(hr) - p.zp_rh, p.hh_rin))),
+             p.zp_rin);
+  in = clampi(in, p.rin, k_ri);
+  const int32_t r = clampi(pwl_i(in, lut[1]), p.rout, k_ro);
+  // new gate: r times the weight_hh_linear code of n, aligned to new_gate_input in one rescale
+  const long long rmul = (static_cast<long long>(r) - p.zp_rout) * (static_cast<long long>(hn) - p.zp_rh);
+  in = add32(add32(static_cast<int32_t>(rescale(static_cast<long long>(wn) - p.zp_wx, p.ih_nin)),
+                   static_cast<int32_t>(rescale(rmul, p.rmul_nin))),
+             p.zp_nin);
+  in = clampi(in, p.nin, k_ni);
+  const int32_t nn = clampi(pwl_i(in, lut[2]), p.nout, k_no);
+  // hidden update: u h_old + (1 - u) n on the scale S_zout S_h, one rescale to h
+  const int32_t hold = hq[e];
+  const int32_t n_h = add32(static_cast<int32_t>(rescale(static_cast<long long>(nn) - p.zp_nout, p.nout_h)), p.zp_h);
+  const long long oldc = (static_cast<long long>(z) - p.zp_zout) * (static_cast<long long>(hold) - p.zp_h);
+  const long long newc = (static_cast<long long>(p.quant_one) - z) * (static_cast<long long>(n_h) - p.zp_h);
+  const int32_t hnew = clampi(add32(static_cast<int32_t>(rescale(oldc + newc, p.old_h)), p.zp_h), p.h, k_h);
+  hq_next[e] = hnew;
+  const size_t NH = static_cast<size_t>(a.B) * H;
+  if (a.hout) a.hout[(static_cast<size_t>(t) + 1) * NH + e] = dq(hnew, p.zp_h, p.eff_h);
+  if (a.v) {
+    float *vp = a.v + n * 4 * H + j;
+    vp[0] = dq(z, p.zp_zout, p.eff_zout);
+    vp[H] = dq(r, p.zp_rout, p.eff_rout);
+    vp[2 * H] = dq(nn, p.zp_nout, p.eff_nout);
+    vp[3 * H] = dq(hn, p.zp_rh, p.eff_rh);
+  }
+  if (a.gin_m) {
+    const size_t mi = n * C + j;
+    a.gin_m[mi] = k_zi;
+    a.gin_m[mi + H] = k_ri;
+    a.gin_m[mi + 2 * H] = k_ni;
+    a.gout_m[mi] = k_zo;
+    a.gout_m[mi + H] = k_ro;
+    a.gout_m[mi + 2 * H] = k_no;
+    a.h_m[static_cast<size_t>(t) * NH + e] = k_h;
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// host
+// ---------------------------------------------------------------------------------
+struct IntWorkspace {
+  size_t hostblk, bias, wx, rh, hq, xa, bfrag, colsum, flag, total;
+  IntWorkspace(int T, int B, int I, int H) {
+    const size_t C = 3 * static_cast<size_t>(H);
+    const size_t Kp = static_cast<size_t>(xgemm::pad_k(I));
+    auto al = [](size_t x) { return (x + 255) & ~static_cast<size_t>(255); };
+    size_t o = 0;
+    hostblk = o; o += al(4 * C * (sizeof(float) + sizeof(IRescale)));
+    bias = o; o += al(2 * C * sizeof(long long));
+    wx = o; o += al(sizeof(int32_t) * static_cast<size_t>(T) * B * C);
+    rh = o; o += al(sizeof(int32_t) * static_cast<size_t>(B) * C);
+    hq = o; o += al(sizeof(int32_t) * 2 * static_cast<size_t>(B) * H);
+    const size_t ip = static_cast<size_t>(I) <= kPackedMaxK ? 1 : 0;
+    xa = o; o += al(ip * 2 * static_cast<size_t>(T) * B * Kp);
+    bfrag = o; o += al(ip * 2 * ((C + 15) / 16 * 16) * Kp);  // fragments of 16-column tiles
+    colsum = o; o += al(ip * sizeof(long long) * C);
+    flag = o; o += al(sizeof(int));
+    total = o;
+  }
+};
+
+// A(m, k) codes with base zp (A spans at most 16 bits), B(k, c) signed 16-bit codes.
+static int launch_linear(const int32_t *A, int lda, int M, int K, float off, long long corr,
+                         int pa, const int32_t *Bm, int sbk, int N, int pb, const LinearOut &e,
+                         char *packed_ws, const IntWorkspace &ws, hipStream_t stream) {
+  if (packed_ws != nullptr && K <= kPackedMaxK) {
+    const int Kp = xgemm::pad_k(K);
+    int8_t *xa = reinterpret_cast<int8_t *>(packed_ws + ws.xa);
+    v4i *bf = reinterpret_cast<v4i *>(packed_ws + ws.bfrag);
+    long long *cs = reinterpret_cast<long long *>(packed_ws + ws.colsum);
+    if (int rc = xgemm::pack_a(A, lda, M, K, off, pa, xa, Kp, stream)) return rc;
+    if (int rc = xgemm::pack_b(Bm, sbk, 1, K, N, pb, Kp, bf, cs, stream)) return rc;
+    xgemm::Packed p;
+    p.A = xa; p.aplane = static_cast<int64_t>(M) * Kp; p.Kp = Kp;
+    p.B = bf; p.bplane = static_cast<int64_t>((N + 15) / 16) * (Kp / 64) * 64;
+    p.colsum = cs; p.corr = corr; p.M = M; p.N = N;
+    const dim3 grid((M + 15) / 16);
+    auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, dim3(256), 0, stream, p, e); };
+    if (pa == 1)
+      pb == 1 ? go(linear_gemm_packed<1, 1>) : go(linear_gemm_packed<1, 2>);
+    else
+      pb == 1 ? go(linear_gemm_packed<2, 1>) : go(linear_gemm_packed<2, 2>);
+  } else {
+    xgemm::OperandsT<int32_t, int32_t> o;
+    o.M = M; o.N = N; o.K = K;
+    o.A = A; o.lda = lda;
+    o.off = off; o.corr = corr;
+    o.B = Bm; o.sbk = sbk; o.sbn = 1;
+    const dim3 grid((N + xgemm::kTile - 1) / xgemm::kTile, (M + xgemm::kTile - 1) / xgemm::kTile);
+    auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, dim3(256), 0, stream, o, e); };
+    if (pa == 1)
+      pb == 1 ? go(linear_gemm<1, 1>) : go(linear_gemm<1, 2>);
+    else
+      pb == 1 ? go(linear_gemm<2, 1>) : go(linear_gemm<2, 2>);
+  }
+  RXMET_CHECK_LAUNCH();
+  return 0;
+}
+
+struct IntCall {
+  bool training;
+  int T, B, I, H;
+  const float *W, *R, *bw, *br, *x, *h0;
+  const int32_t *xq_in, *h0q_in;  // int-IO inputs (x, h0 unused then)
+  const rxmet_gru_qparams *params;
+  float *h, *v;                                   // dequantised outputs, or null
+  int32_t *hq_out;                                // int-IO: h codes [T+1, B, H], or null
+  int32_t *Wq, *Rq, *bwq, *brq, *xq;              // codes (xq null for int-IO)
+  uint8_t *x_m, *h0_m, *W_m, *R_m, *bw_m, *br_m, *ih_m, *hh_m, *gin_m, *gout_m, *h_m;
+  void *workspace;
+};
+
+static int forward_int(const IntCall &k, hipStream_t stream) {
+  const int T = k.T, B = k.B, I = k.I, H = k.H;
+  RXMET_CHECK_ARG(k.params != nullptr && k.workspace != nullptr, "params and workspace must be non-null");
+  RXMET_CHECK_ARG(T >= 1 && B >= 1 && I >= 1 && H >= 1, "dimensions must be positive");
+  RXMET_CHECK_ARG(k.params->hidden == H, "params.hidden != hidden_size");
+  RXMET_CHECK_ARG(k.W && k.R && k.bw && k.br && k.Wq && k.Rq && k.bwq && k.brq,
+                  "required pointer is null");
+  RXMET_CHECK_ARG(I < (1 << 17) && H < (1 << 17), "input_size and hidden_size must be below 131072");
+  RXMET_CHECK_ARG(static_cast<double>(T) * B * 3 * H < 9.0e18, "tensor too large");
+  const rxmet_gru_qparams &P = *k.params;
+  const rxmet_grid *g = P.g;
+  {
+    const IGrid gx = igrid_of(g[RXMET_GRU_X].bits, g[RXMET_GRU_X].is_unsigned);
+    const IGrid gh = igrid_of(g[RXMET_GRU_H].bits, g[RXMET_GRU_H].is_unsigned);
+    const IGrid gw = igrid_of(P.chan_bits[RXMET_GRU_W], P.chan_unsigned[RXMET_GRU_W]);
+    const IGrid gr = igrid_of(P.chan_bits[RXMET_GRU_R], P.chan_unsigned[RXMET_GRU_R]);
+    RXMET_CHECK_ARG(xgemm::a_fits(gx.lo, gx.hi) && xgemm::a_fits(gh.lo, gh.hi),
+                    "x and h grids must span at most 16 bits");
+    RXMET_CHECK_ARG(xgemm::b_fits(gw.lo, gw.hi) && xgemm::b_fits(gr.lo, gr.hi),
+                    "W and R codes must fit signed 16 bits");
+  }
+  const int C = 3 * H;
+  const IntWorkspace ws(T, B, I, H);
+  char *wsb = static_cast<char *>(k.workspace);
+  float *eff = reinterpret_cast<float *>(wsb + ws.hostblk);
+  IRescale *rs = reinterpret_cast<IRescale *>(wsb + ws.hostblk + 4 * static_cast<size_t>(C) * sizeof(float));
+  long long *bias = reinterpret_cast<long long *>(wsb + ws.bias);
+  int32_t *wx = reinterpret_cast<int32_t *>(wsb + ws.wx);
+  int32_t *rh = reinterpret_cast<int32_t *>(wsb + ws.rh);
+  int32_t *hqb = reinterpret_cast<int32_t *>(wsb + ws.hq);
+
+  IntStepParams sp;
+  std::vector<char> host(4 * static_cast<size_t>(C) * (sizeof(float) + sizeof(IRescale)));
+  try {
+    make_int_step_params(P, H, &sp);
+    float *he = reinterpret_cast<float *>(host.data());
+    for (int kk = 0; kk < 4; ++kk)
+      for (int c = 0; c < C; ++c) he[kk * C + c] = effective_scale(P.chan_scale[kk][c], P.use_pot2 != 0);
+    make_int_channel_rescales(P, H, reinterpret_cast<IRescale *>(host.data() + 4 * static_cast<size_t>(C) * sizeof(float)));
+  } catch (const std::exception &ex) {
+    set_error(ex.what());
+    return -22;
+  }
+
+  // int-IO inputs must lie on the x / h grids: checked once, with one stream synchronisation
+  if (k.xq_in != nullptr) {
+    int *flag = reinterpret_cast<int *>(wsb + ws.flag);
+    hipLaunchKernelGGL(cluster::zero_words, dim3(1), dim3(64), 0, stream,
+                       reinterpret_cast<unsigned *>(flag), 1);
+    RXMET_CHECK_LAUNCH();
+    const int64_t nx = static_cast<int64_t>(T) * B * I;
+    hipLaunchKernelGGL(check_codes, dim3(static_cast<unsigned>(std::min<int64_t>((nx + 255) / 256, 4096))),
+                       dim3(256), 0, stream, k.xq_in, nx, sp.x.lo, sp.x.hi, flag);
+    RXMET_CHECK_LAUNCH();
+    if (k.h0q_in) {
+      const int64_t nh = static_cast<int64_t>(B) * H;
+      hipLaunchKernelGGL(check_codes, dim3(static_cast<unsigned>(std::min<int64_t>((nh + 255) / 256, 4096))),
+                         dim3(256), 0, stream, k.h0q_in, nh, sp.h.lo, sp.h.hi, flag);
+      RXMET_CHECK_LAUNCH();
+    }
+    int bad = 0;
+    RXMET_CHECK_HIP(hipMemcpyAsync(&bad, flag, sizeof(int), hipMemcpyDeviceToHost, stream));
+    RXMET_CHECK_HIP(hipStreamSynchronize(stream));
+    RXMET_CHECK_ARG(bad == 0, "x_q / h0_q hold codes outside the x / h grids");
+  }
+
+  RXMET_CHECK_HIP(hipMemcpyAsync(wsb + ws.hostblk, host.data(), host.size(), hipMemcpyHostToDevice, stream));
+  IWeightArgs wa;
+  wa.W = k.W; wa.R = k.R; wa.bw = k.bw; wa.br = k.br;
+  wa.eff = eff; wa.rs = rs;
+  wa.gW = igrid_of(P.chan_bits[RXMET_GRU_W], P.chan_unsigned[RXMET_GRU_W]);
+  wa.gR = igrid_of(P.chan_bits[RXMET_GRU_R], P.chan_unsigned[RXMET_GRU_R]);
+  wa.gbw = igrid_of(P.chan_bits[RXMET_GRU_BW], P.chan_unsigned[RXMET_GRU_BW]);
+  wa.gbr = igrid_of(P.chan_bits[RXMET_GRU_BR], P.chan_unsigned[RXMET_GRU_BR]);
+  wa.Wq = k.Wq; wa.Rq = k.Rq; wa.bwq = k.bwq; wa.brq = k.brq;
+  wa.Wm = k.training ? k.W_m : nullptr;
+  wa.Rm = k.training ? k.R_m : nullptr;
+  wa.bwm = k.training ? k.bw_m : nullptr;
+  wa.brm = k.training ? k.br_m : nullptr;
+  wa.bias = bias;
+  {
+    rxmet::prof::Scope ps__("gru_int_quant_weights", stream);
+    const int64_t total = static_cast<int64_t>(I + H + 1) * C;
+    hipLaunchKernelGGL(iq_weights, dim3(static_cast<unsigned>(std::min<int64_t>((total + 255) / 256, 8192))),
+                       dim3(256), 0, stream, I, H, wa);
+  }
+  RXMET_CHECK_LAUNCH();
+
+  const int64_t nx = k.xq_in ? 0 : static_cast<int64_t>(T) * B * I, nh = static_cast<int64_t>(B) * H;
+  int32_t *hq0 = k.hq_out ? k.hq_out : hqb;
+  {
+    rxmet::prof::Scope ps__("gru_int_quant_input", stream);
+    const int64_t blocks = std::min<int64_t>((nx + nh + 255) / 256, 8192);
+    hipLaunchKernelGGL(iq_input, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, nx, nh,
+                       k.x, k.h0, k.h0q_in, sp, k.xq, k.training ? k.x_m : nullptr, hq0,
+                       k.training ? k.h0_m : nullptr, k.h);
+  }
+  RXMET_CHECK_LAUNCH();
+
+  // input projection: weight_ih_linear codes of every step
+  const int32_t *xq = k.xq_in ? k.xq_in : k.xq;
+  {
+    const double xlo = sp.x.lo, xhi = sp.x.hi;
+    const float off = xgemm::a_shift(xlo, xhi);
+    const int pa = xgemm::a_planes(xlo, xhi), pb = xgemm::b_planes(wa.gW.lo, wa.gW.hi);
+    LinearOut e{bias, rs, sp.zp_wx, sp.wx, wx, k.training ? k.ih_m : nullptr, C};
+    rxmet::prof::Scope ps__("gru_int_input_gemm", stream);
+    if (int rc = launch_linear(xq, I, T * B, I, off, static_cast<long long>(off) - sp.zp_x, pa,
+                               k.Wq, C, C, pb, e, wsb, ws, stream))
+      return rc;
+  }
+
+  // recurrence: per step R_q (h - zp_h) + br -> weight_hh_linear codes, then the gates
+  const double hlo = sp.h.lo, hhi = sp.h.hi;
+  const float hoff = xgemm::a_shift(hlo, hhi);
+  const int hpa = xgemm::a_planes(hlo, hhi), rpb = xgemm::b_planes(wa.gR.lo, wa.gR.hi);
+  IPointArgs pa;
+  pa.T = T; pa.B = B; pa.H = H;
+  pa.wx = wx; pa.rh = rh; pa.hout = k.h; pa.v = k.v;
+  pa.gin_m = k.training ? k.gin_m : nullptr;
+  pa.gout_m = k.training ? k.gout_m : nullptr;
+  pa.h_m = k.training ? k.h_m : nullptr;
+  if (pa.gin_m && !(pa.gout_m && pa.h_m)) pa.gin_m = nullptr;
+  const dim3 pgrid(static_cast<unsigned>((nh + 255) / 256));
+  rxmet::prof::Scope ps__("gru_int_recurrence", stream);
+  const int32_t *hcur = hq0;
+  for (int t = 0; t < T; ++t) {
+    int32_t *hnext = k.hq_out ? k.hq_out + (static_cast<size_t>(t) + 1) * nh
+                              : hqb + static_cast<size_t>((t + 1) & 1) * nh;
+    LinearOut e{bias + C, rs + 2 * C, sp.zp_rh, sp.rh, rh,
+                k.training && k.hh_m ? k.hh_m + static_cast<size_t>(t) * B * C : nullptr, C};
+    if (int rc = launch_linear(hcur, H, B, H, hoff, static_cast<long long>(hoff) - sp.zp_h, hpa,
+                               k.Rq, C, C, rpb, e, nullptr, ws, stream))
+      return rc;
+    hipLaunchKernelGGL(int_point, pgrid, dim3(256), 0, stream, pa, sp, t, hcur, hnext);
+    RXMET_CHECK_LAUNCH();
+    hcur = hnext;
+  }
+  return 0;
+}
+
+}  // namespace
+}  // namespace gru
+}  // namespace rxmet
+
+using namespace rxmet;
+using namespace rxmet::gru;
+
+extern "C" {
+
+int64_t rxmet_gru_forward_int_workspace_bytes(int32_t T, int32_t B, int32_t I, int32_t H) {
+  if (T < 1 || B < 1 || I < 1 || H < 1) return -22;
+  return static_cast<int64_t>(IntWorkspace(T, B, I, H).total);
+}
+
+int rxmet_gru_forward_quant_int(int32_t is_training, int32_t T, int32_t B, int32_t I, int32_t H,
+                                const float *W, const float *R, const float *bw, const float *br,
+                                const float *x, const float *h0, const rxmet_gru_qparams *params,
+                                float *h, float *v, int32_t *W_q, int32_t *R_q, int32_t *bw_q,
+                                int32_t *br_q, int32_t *x_q, uint8_t *x_mask, uint8_t *h0_mask,
+                                uint8_t *W_mask, uint8_t *R_mask, uint8_t *bw_mask,
+                                uint8_t *br_mask, uint8_t *ih_mask, uint8_t *hh_mask,
+                                uint8_t *gate_in_mask, uint8_t *gate_out_mask, uint8_t *h_mask,
+                                void *workspace, void *stream) {
+  clear_error();
+  RXMET_CHECK_ARG(x && h && x_q, "x, h and x_q must be non-null");
+  if (is_training)
+    RXMET_CHECK_ARG(v && x_mask && W_mask && R_mask && bw_mask && br_mask && ih_mask && hh_mask &&
+                        gate_in_mask && gate_out_mask && h_mask && (h0 == nullptr || h0_mask),
+                    "training needs v and every mask output");
+  IntCall k{};
+  k.training = is_training != 0;
+  k.T = T; k.B = B; k.I = I; k.H = H;
+  k.W = W; k.R = R; k.bw = bw; k.br = br; k.x = x; k.h0 = h0;
+  k.params = params;
+  k.h = h; k.v = v;
+  k.Wq = W_q; k.Rq = R_q; k.bwq = bw_q; k.brq = br_q; k.xq = x_q;
+  k.x_m = x_mask; k.h0_m = h0_mask; k.W_m = W_mask; k.R_m = R_mask; k.bw_m = bw_mask;
+  k.br_m = br_mask; k.ih_m = ih_mask; k.hh_m = hh_mask; k.gin_m = gate_in_mask;
+  k.gout_m = gate_out_mask; k.h_m = h_mask;
+  k.workspace = workspace;
+  return forward_int(k, static_cast<hipStream_t>(stream));
+}
+
+int rxmet_gru_forward_int_io(int32_t T, int32_t B, int32_t I, int32_t H, const float *W,
+                             const float *R, const float *bw, const float *br,
+                             const int32_t *x_q, const int32_t *h0_q,
+                             const rxmet_gru_qparams *params, int32_t *h_q, int32_t *W_q,
+                             int32_t *R_q, int32_t *bw_q, int32_t *br_q, void *workspace,
+                             void *stream) {
+  clear_error();
+  RXMET_CHECK_ARG(x_q && h_q, "x_q and h_q must be non-null");
+  IntCall k{};
+  k.training = false;
+  k.T = T; k.B = B; k.I = I; k.H = H;
+  k.W = W; k.R = R; k.bw = bw; k.br = br;
+  k.xq_in = x_q; k.h0q_in = h0_q;
+  k.params = params;
+  k.hq_out = h_q;
+  k.Wq = W_q; k.Rq = R_q; k.bwq = bw_q; k.brq = br_q;
+  k.workspace = workspace;
+  return forward_int(k, static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

@@ -11,7 +11,9 @@
 //   (src/quantize_lut.cc:53-365), rebuilt from the stored scales as the reference binding
 //   does on every call (pytorch/lib/gru_interface_binding.cc:1313).
 // * make_step_params / make_channel_factors: the kernels' parameter block, i.e. the
-//   reference's setRescaleParam (src/gru_forward_gpu_quant_fp.cu:454-645).
+//   reference's setRescaleParam (src/gru_forward_gpu_quant_fp.cu:454-645);
+//   make_int_step_params / make_int_channel_rescales: the int32 carrier's
+//   (src/gru_forward_gpu_quant.cu:662-752, fillLinearParams / fillGateParams).
 //
 // All arithmetic is fp32 in the reference's evaluation order (the library is built with
 // -ffp-contract=off); libm calls are the same glibc functions the reference uses.
@@ -345,6 +347,107 @@ void make_step_params(const rxmet_gru_qparams &p, int H, StepParams *s) {
   s->eff_rout = effective_scale(sc(RXMET_GRU_R_OUT), pot);
   s->eff_nout = effective_scale(sc(RXMET_GRU_N_OUT), pot);
   s->eff_rh = effective_scale(sc(RXMET_GRU_RH), pot);
+}
+
+// ---- int32 carrier ----
+// makeRescale / makeRescaleProduct / makeRescaleToProduct (include/scale_encoding.h:133-188):
+// power-of-two mode takes differences of the grids' shifts, affine mode encodes the fp32 ratio
+// of the stored scales as a 16-bit mantissa and a shift.
+static IRescale checked(IRescale r) {
+  if (r.shift < -32 || r.shift > 62) throw std::runtime_error("integer rescale shift out of range");
+  return r;
+}
+static IRescale rescale_of(bool pot, float ratio, int pot_shift) {
+  if (pot) return checked(IRescale{1, static_cast<int8_t>(pot_shift)});
+  const MShift m = MShift::encode(ratio);
+  return checked(IRescale{static_cast<int32_t>(m.m), m.shift});
+}
+static IRescale rs_single(bool pot, float src, float dst) {
+  return rescale_of(pot, src / dst, pow2_exponent(src) - pow2_exponent(dst));
+}
+static IRescale rs_product(bool pot, float a, float b, float dst) {
+  return rescale_of(pot, (a * b) / dst, pow2_exponent(a) + pow2_exponent(b) - pow2_exponent(dst));
+}
+static IRescale rs_to_product(bool pot, float src, float a, float b) {
+  return rescale_of(pot, src / (a * b), pow2_exponent(src) - (pow2_exponent(a) + pow2_exponent(b)));
+}
+
+IGrid igrid_of(int32_t bits, int32_t is_unsigned) {
+  const Grid g(bits, is_unsigned);
+  return IGrid{g.qmin(), g.qmax()};
+}
+
+void make_int_step_params(const rxmet_gru_qparams &p, int H, IntStepParams *s) {
+  const rxmet_grid *g = p.g;
+  const bool pot = p.use_pot2 != 0;
+  auto sc = [&](int i) { return g[i].scale; };
+  s->H = H;
+  s->zp_x = g[RXMET_GRU_X].zero_point;
+  s->zp_h = g[RXMET_GRU_H].zero_point;
+  s->zp_wx = g[RXMET_GRU_WX].zero_point;
+  s->zp_rh = g[RXMET_GRU_RH].zero_point;
+  s->zp_zin = g[RXMET_GRU_Z_IN].zero_point;
+  s->zp_zout = g[RXMET_GRU_Z_OUT].zero_point;
+  s->zp_rin = g[RXMET_GRU_R_IN].zero_point;
+  s->zp_rout = g[RXMET_GRU_R_OUT].zero_point;
+  s->zp_nin = g[RXMET_GRU_N_IN].zero_point;
+  s->zp_nout = g[RXMET_GRU_N_OUT].zero_point;
+  s->ih_zin = rs_single(pot, sc(RXMET_GRU_WX), sc(RXMET_GRU_Z_IN));
+  s->hh_zin = rs_single(pot, sc(RXMET_GRU_RH), sc(RXMET_GRU_Z_IN));
+  s->ih_rin = rs_single(pot, sc(RXMET_GRU_WX), sc(RXMET_GRU_R_IN));
+  s->hh_rin = rs_single(pot, sc(RXMET_GRU_RH), sc(RXMET_GRU_R_IN));
+  s->ih_nin = rs_single(pot, sc(RXMET_GRU_WX), sc(RXMET_GRU_N_IN));
+  s->rmul_nin = rs_product(pot, sc(RXMET_GRU_R_OUT), sc(RXMET_GRU_RH), sc(RXMET_GRU_N_IN));
+  s->nout_h = rs_single(pot, sc(RXMET_GRU_N_OUT), sc(RXMET_GRU_H));
+  s->old_h = rs_product(pot, sc(RXMET_GRU_Z_OUT), sc(RXMET_GRU_H), sc(RXMET_GRU_H));
+  // the constant 1 on the update-gate output grid: round_to_int(1 / S) + zp
+  s->quant_one = static_cast<int32_t>(static_cast<uint32_t>(static_cast<int32_t>(
+                                          std::rint(1.0f / sc(RXMET_GRU_Z_OUT)))) +
+                                      static_cast<uint32_t>(s->zp_zout));
+  auto ig = [&](int i) { return igrid_of(g[i].bits, g[i].is_unsigned); };
+  s->x = ig(RXMET_GRU_X);
+  s->h = ig(RXMET_GRU_H);
+  s->wx = ig(RXMET_GRU_WX);
+  s->rh = ig(RXMET_GRU_RH);
+  s->zin = ig(RXMET_GRU_Z_IN);
+  s->zout = ig(RXMET_GRU_Z_OUT);
+  s->rin = ig(RXMET_GRU_R_IN);
+  s->rout = ig(RXMET_GRU_R_OUT);
+  s->nin = ig(RXMET_GRU_N_IN);
+  s->nout = ig(RXMET_GRU_N_OUT);
+  rxmet_pwl_lut luts[3];
+  build_lut(false, g[RXMET_GRU_Z_IN], g[RXMET_GRU_Z_OUT], &luts[0]);
+  build_lut(false, g[RXMET_GRU_R_IN], g[RXMET_GRU_R_OUT], &luts[1]);
+  build_lut(true, g[RXMET_GRU_N_IN], g[RXMET_GRU_N_OUT], &luts[2]);
+  for (int i = 0; i < 3; ++i) {
+    for (int k = 0; k < kSegments; ++k) {
+      s->lut[i].thr[k] = luts[i].seg[k].threshold;
+      s->lut[i].qb[k] = luts[i].seg[k].q_b;
+      s->lut[i].n[k] = luts[i].seg[k].n;
+      s->lut[i].c[k] = luts[i].seg[k].c;
+    }
+    s->lut[i].zp_x = luts[i].zp_x;
+  }
+  s->eff_x = effective_scale(sc(RXMET_GRU_X), pot);
+  s->eff_h = effective_scale(sc(RXMET_GRU_H), pot);
+  s->eff_zout = effective_scale(sc(RXMET_GRU_Z_OUT), pot);
+  s->eff_rout = effective_scale(sc(RXMET_GRU_R_OUT), pot);
+  s->eff_nout = effective_scale(sc(RXMET_GRU_N_OUT), pot);
+  s->eff_rh = effective_scale(sc(RXMET_GRU_RH), pot);
+}
+
+void make_int_channel_rescales(const rxmet_gru_qparams &p, int H, IRescale *rs) {
+  const bool pot = p.use_pot2 != 0;
+  const int C = 3 * H;
+  const float sx = p.g[RXMET_GRU_X].scale, sh = p.g[RXMET_GRU_H].scale;
+  const float swx = p.g[RXMET_GRU_WX].scale, srh = p.g[RXMET_GRU_RH].scale;
+  for (int c = 0; c < C; ++c) {
+    const float sW = p.chan_scale[RXMET_GRU_W][c], sR = p.chan_scale[RXMET_GRU_R][c];
+    rs[c] = rs_product(pot, sW, sx, swx);
+    rs[C + c] = rs_to_product(pot, p.chan_scale[RXMET_GRU_BW][c], sW, sx);
+    rs[2 * C + c] = rs_product(pot, sR, sh, srh);
+    rs[3 * C + c] = rs_to_product(pot, p.chan_scale[RXMET_GRU_BR][c], sR, sh);
+  }
 }
 
 void make_channel_factors(const rxmet_gru_qparams &p, int H, float *igx, float *ibx, float *igh,

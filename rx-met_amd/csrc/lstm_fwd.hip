@@ -979,7 +979,7 @@ struct FwdWorkspace {
     const size_t Kp = static_cast<size_t>(xgemm::pad_k(I));
     const size_t ip = static_cast<size_t>(I) <= kPackedMaxK ? 1 : 0;
     xa = o; o += al(ip * 2 * static_cast<size_t>(T) * B * Kp);
-    bfrag = o; o += al(ip * 2 * C * Kp);
+    bfrag = o; o += al(ip * 2 * ((C + 15) / 16 * 16) * Kp);  // fragments of 16-column tiles
     colsum = o; o += al(ip * sizeof(long long) * C);
     // stepped recurrence: two h code buffers, the cell codes [B, H] and the sums [B, 4H]
     sh = o; o += al(sizeof(float) * 2 * static_cast<size_t>(B) * H);

@@ -696,3 +696,104 @@ def backward_quant_float_storage_dirs_x(time_steps, batch_size, input_size, hidd
     _rx.call("rxmet_gru_backward_quant_dirs_x", len(made), T, B, I, H, arr, 1,
              _stream(dirs[0][4].device))
     return [m[0] for m in made]
+
+
+# ---------------------------------------------------------------------------------------
+# int32 carrier
+# ---------------------------------------------------------------------------------------
+
+def _check_i32_cuda(name, t):
+    if not (t.is_cuda and t.dtype == torch.int32):
+        raise RuntimeError(f"{name} must be CUDA int32 tensor")
+
+
+def forward_quant_int_storage(is_training, time_steps, batch_size, input_size, hidden_size, W, R,
+                              bw, br, x, h0, quant_params: GRUQuantParams):
+    """forward_quant_int_storage_wrapper (gru_interface_binding.cc:451-586): the int32 carrier
+    (quantGRUForwardInt), rxmet_gru_forward_quant_int.
+
+    Returns the 18 tensors of forward_quant_float_storage with W_q, R_q, bw_q, br_q and x_q as
+    int32 codes; h and v are dequantised float32; masks are empty when is_training is False."""
+    T, B, I, H = time_steps, batch_size, input_size, hidden_size
+    for n, t in (("W", W), ("R", R), ("bw", bw), ("br", br), ("x", x)):
+        _check_f32_cuda(n, t)
+    has_h0 = h0 is not None and h0.numel() > 0
+    if has_h0:
+        _check_f32_cuda("h0", h0)
+        if tuple(h0.shape) != (B, H):
+            raise RuntimeError("h0 must have shape [batch_size, hidden_size]")
+    if tuple(x.shape) != (T, B, I) or tuple(W.shape) != (I, 3 * H) or tuple(R.shape) != (H, 3 * H):
+        raise RuntimeError("x/W/R shapes do not match (time_steps, batch_size, input_size, "
+                           "hidden_size)")
+    dev = x.device
+    C = 3 * H
+    f32 = dict(dtype=torch.float32, device=dev)
+    i32 = dict(dtype=torch.int32, device=dev)
+    u8 = dict(dtype=torch.uint8, device=dev)
+    h = torch.empty((T + 1, B, H), **f32)
+    v = torch.empty((T, B, 4 * H), **f32)
+    W_q, R_q = torch.empty((I, C), **i32), torch.empty((H, C), **i32)
+    bw_q, br_q = torch.empty((C,), **i32), torch.empty((C,), **i32)
+    x_q = torch.empty((T, B, I), **i32)
+    if is_training:
+        masks = [torch.empty((T, B, I), **u8),
+                 torch.empty((B, H), **u8) if has_h0 else torch.empty((0,), **u8),
+                 torch.empty((I, C), **u8), torch.empty((H, C), **u8), torch.empty((C,), **u8),
+                 torch.empty((C,), **u8)] + [torch.empty((T, B, C), **u8) for _ in range(4)] + \
+                [torch.empty((T, B, H), **u8)]
+    else:
+        masks = [torch.empty((0,), **u8) for _ in range(11)]
+    ws = _ws(_rx.load().rxmet_gru_forward_int_workspace_bytes(T, B, I, H), dev)
+    mp = [m.data_ptr() if m.numel() > 0 else None for m in masks]
+    _rx.call("rxmet_gru_forward_quant_int", int(bool(is_training)), T, B, I, H, W.data_ptr(),
+             R.data_ptr(), bw.data_ptr(), br.data_ptr(), x.data_ptr(),
+             h0.data_ptr() if has_h0 else None, ctypes.byref(quant_params.struct), h.data_ptr(),
+             v.data_ptr(), W_q.data_ptr(), R_q.data_ptr(), bw_q.data_ptr(), br_q.data_ptr(),
+             x_q.data_ptr(), *mp, ws.data_ptr(), _stream(dev))
+    return (h, v, W_q, R_q, bw_q, br_q, x_q, *masks)
+
+
+def backward_quant_int_storage(time_steps, batch_size, input_size, hidden_size, W_q, R_q, bw_q,
+                               br_q, x_q, dh_new, h, v, quant_params: GRUQuantParams, x_mask,
+                               h0_mask, W_mask, R_mask, bw_mask, br_mask, weight_ih_linear_mask,
+                               weight_hh_linear_mask, gate_input_mask, gate_output_mask, h_mask):
+    """backward_quant_int_storage_wrapper (gru_interface_binding.cc:923-963): the int32 codes the
+    forward saved, converted to float32 codes, through backward_quant_float_storage."""
+    for n, t in (("W_q", W_q), ("R_q", R_q), ("bw_q", bw_q), ("br_q", br_q), ("x_q", x_q)):
+        _check_i32_cuda(n, t)
+    return backward_quant_float_storage(
+        time_steps, batch_size, input_size, hidden_size, W_q.float(), R_q.float(), bw_q.float(),
+        br_q.float(), x_q.float(), dh_new, h, v, quant_params, x_mask, h0_mask, W_mask, R_mask,
+        bw_mask, br_mask, weight_ih_linear_mask, weight_hh_linear_mask, gate_input_mask,
+        gate_output_mask, h_mask)
+
+
+def forward_quantized_int_io(time_steps, batch_size, input_size, hidden_size, W, R, bw, br, x_q,
+                             h0_q, quant_params: GRUQuantParams):
+    """forward_quantized_int_io_wrapper (gru_interface_binding.cc:588-646): int32 codes in and
+    out (quantGRUForwardIntIO), rxmet_gru_forward_int_io.  x_q [T,B,I] and h0_q [B,H] (may be
+    empty) lie on the x and h grids.  Returns (output_q [T,B,H], h_n_q [1,B,H]) int32."""
+    T, B, I, H = time_steps, batch_size, input_size, hidden_size
+    for n, t in (("W", W), ("R", R), ("bw", bw), ("br", br)):
+        _check_f32_cuda(n, t)
+    _check_i32_cuda("x_q", x_q)
+    if tuple(x_q.shape) != (T, B, I):
+        raise RuntimeError("x_q must have shape [time_steps, batch_size, input_size]")
+    has_h0 = h0_q is not None and h0_q.numel() > 0
+    if has_h0:
+        _check_i32_cuda("h0_q", h0_q)
+        if tuple(h0_q.shape) != (B, H):
+            raise RuntimeError("h0_q must have shape [batch_size, hidden_size]")
+    dev = x_q.device
+    C = 3 * H
+    i32 = dict(dtype=torch.int32, device=dev)
+    h_q = torch.empty((T + 1, B, H), **i32)
+    codes = [torch.empty(s, **i32) for s in ((I, C), (H, C), (C,), (C,))]
+    ws = _ws(_rx.load().rxmet_gru_forward_int_workspace_bytes(T, B, I, H), dev)
+    x_q = x_q.contiguous()
+    h0c = h0_q.contiguous() if has_h0 else None
+    _rx.call("rxmet_gru_forward_int_io", T, B, I, H, W.data_ptr(), R.data_ptr(), bw.data_ptr(),
+             br.data_ptr(), x_q.data_ptr(), h0c.data_ptr() if has_h0 else None,
+             ctypes.byref(quant_params.struct), h_q.data_ptr(), *[c.data_ptr() for c in codes],
+             ws.data_ptr(), _stream(dev))
+    return h_q[1:].contiguous(), h_q[T:T + 1].contiguous()

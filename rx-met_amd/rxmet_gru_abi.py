@@ -104,6 +104,11 @@ _SIGS = {
     "rxmet_gru_bidir_assemble": (ctypes.c_int, [_i32] * 3 + [_p] * 3 + [_i64, _i64, _p, _p]),
     "rxmet_gru_bidir_split_grad": (ctypes.c_int, [_i32] * 3 + [_p, _i64, _i64, _i64] + [_p] * 4),
     "rxmet_gru_bidir_dx": (ctypes.c_int, [_i32] * 3 + [_p] * 3 + [_i64, _i64, _p]),
+    "rxmet_gru_forward_int_workspace_bytes": (ctypes.c_int64, [_i32, _i32, _i32, _i32]),
+    "rxmet_gru_forward_quant_int": (ctypes.c_int, [_i32, _i32, _i32, _i32, _i32] + [_p] * 6 +
+                                    [ctypes.POINTER(GruQParams)] + [_p] * 18 + [_p, _p]),
+    "rxmet_gru_forward_int_io": (ctypes.c_int, [_i32] * 4 + [_p] * 6 +
+                                 [ctypes.POINTER(GruQParams)] + [_p] * 5 + [_p, _p]),
 }
 for _name, (_res, _args) in _SIGS.items():
     _rx.register(_name, _res, _args)
