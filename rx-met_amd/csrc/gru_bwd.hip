@@ -715,7 +715,7 @@ struct BwdWorkspace {
     Mp = static_cast<int>((M + 31) / 32 * 32);
     xt = o; o += al(sizeof(__bf16) * 2 * I * static_cast<size_t>(Mp));
     ht = o; o += al(sizeof(__bf16) * 2 * H * static_cast<size_t>(Mp));
-    wb = o; o += al(sizeof(__bf16) * 2 * I * C);
+    wb = o; o += al(sizeof(__bf16) * 2 * I * ((C + 31) / 32 * 32));  // rows of Cp, zero past C
     // one host upload: eff_w [C] | eff_r [C] | GEMM column scales [I + H]
     effw = o;
     effr = effw + sizeof(float) * C;
@@ -808,8 +808,8 @@ static int backward_prologue(int T, int B, int I, int H, const rxmet_gru_bwd_dir
       return rc;
     // W_q [I][C] kept as is: rows are the channels c (K), columns the inputs i
     if (int rc = wgrad::codes_t(d.W_q, C, nullptr, C, I, 1, C, 0.0f, 1.0f, plan->npw,
-                                reinterpret_cast<__bf16 *>(wsb + ws.wb), C,
-                                static_cast<int64_t>(I) * C, stream))
+                                reinterpret_cast<__bf16 *>(wsb + ws.wb), ws.Cp,
+                                static_cast<int64_t>(I) * ws.Cp, stream))
       return rc;
   }
   {
@@ -988,8 +988,8 @@ static int backward_epilogue(int T, int B, int I, int H, BwdPlan &plan, hipStrea
     wgrad::NtArgs na;
     na.A = plan.ba.dp; na.lda = C;
     na.kscale = reinterpret_cast<const float *>(plan.wsb + ws.effw);
-    na.Bt = reinterpret_cast<const __bf16 *>(plan.wsb + ws.wb); na.ldb = C;
-    na.bplane = static_cast<int64_t>(I) * C;
+    na.Bt = reinterpret_cast<const __bf16 *>(plan.wsb + ws.wb); na.ldb = ws.Cp;
+    na.bplane = static_cast<int64_t>(I) * ws.Cp;
     na.M = M; na.N = I; na.K = C; na.out = d.dx; na.ldo = I;
     if (int rc = wgrad::nt(na, plan.npw, stream)) return rc;
     // dW[i][c] = eff_x sum_m (x_q - zp_x)[m][i] dp[m][c]

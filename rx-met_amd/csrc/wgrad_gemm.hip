@@ -401,6 +401,8 @@ int tn(const TnArgs &a, int nplanes, hipStream_t stream) {
 int nt(const NtArgs &a, int nplanes, hipStream_t stream) {
   RXMET_CHECK_ARG(nplanes == 1 || nplanes == 2, "nplanes must be 1 or 2");
   RXMET_CHECK_ARG(a.K % 16 == 0 && a.lda % 4 == 0 && a.ldb % 8 == 0, "bad NT layout");
+  // B is read in whole 32-wide K chunks: its rows must hold zeros up to a multiple of 32
+  RXMET_CHECK_ARG(a.ldb >= (a.K + 31) / 32 * 32, "NT B rows must be padded to a multiple of 32");
   RXMET_CHECK_ARG(a.ksplit >= 1 && (a.ksplit == 1 || (a.kper % 32 == 0 && a.kper * (a.ksplit - 1) < a.K)),
                   "bad NT K split");
   // one column tile when N <= 128 (64, 96 or 128 wide), else tiles of 128

@@ -264,9 +264,11 @@ def _operators_from_json(ops: dict, cfg, hidden: int) -> "gru_ops.GRUQuantParams
 
 
 class GRUFunction(torch.autograd.Function):
-    """One direction of a quantised GRU.  forward: weight reorder -> forward_quant_float_storage;
-    backward: dh_new [T+1,B,H] (dh_new[0]=0, dh_new[1:]=grad_output, grad_h_n added to the last
-    step) -> backward_quant_float_storage -> gradients reordered back to (r, z, n)."""
+    """One direction of a quantised GRU.  forward: weight reorder -> forward_quant_float_storage
+    (or forward_quant_int_storage for quant_storage_dtype='int32'); backward: dh_new [T+1,B,H]
+    (dh_new[0]=0, dh_new[1:]=grad_output, grad_h_n added to the last step) ->
+    backward_quant_float_storage (backward_quant_int_storage) -> gradients reordered back to
+    (r, z, n)."""
 
     @staticmethod
     def forward(ctx, input, weight_ih, weight_hh, bias_ih, bias_hh, h0, is_training,
@@ -285,18 +287,23 @@ class GRUFunction(torch.autograd.Function):
             return h_full[1:], h_full[-1:]
         if quant_params is None:
             raise RuntimeError("quant_params is required when use_quantization=True")
-        if quant_storage_dtype != "float32":
-            raise NotImplementedError("only quant_storage_dtype='float32' is provided")
+        if quant_storage_dtype not in ("float32", "int32"):
+            raise ValueError(f"quant_storage_dtype must be 'float32' or 'int32', got "
+                             f"{quant_storage_dtype}")
         device = _require_device(input)
         input = ensure_cuda_float32(input, device).contiguous()
         W, R, bw, br = convert_weights_to_haste_format(weight_ih, weight_hh, bias_ih, bias_hh, H,
                                                        device)
         h0_t = (ensure_cuda_float32(h0, device).contiguous() if h0 is not None
                 else torch.empty(0, device=device, dtype=torch.float32))
-        outs = gru_ops.forward_quant_float_storage(
+        # float32: codes stored as fp32 (FP32 carrier); int32: the int32 carrier
+        forward_fn = (gru_ops.forward_quant_int_storage if quant_storage_dtype == "int32"
+                      else gru_ops.forward_quant_float_storage)
+        outs = forward_fn(
             is_training=is_training, time_steps=T, batch_size=B, input_size=I, hidden_size=H,
             W=W, R=R, bw=bw, br=br, x=input, h0=h0_t, quant_params=quant_params)
         h_full = outs[0]
+        ctx.quant_storage_dtype = quant_storage_dtype
         ctx.bias_none = (bias_ih is None, bias_hh is None)
         ctx.h0_is_none = h0 is None
         ctx.quant_params = quant_params
@@ -324,7 +331,9 @@ class GRUFunction(torch.autograd.Function):
             dh_new[1:] = grad_output
         if grad_h_n is not None and grad_h_n.numel() > 0:
             dh_new[-1] += grad_h_n[0]
-        dx, dW, dR, dbw, dbr, dh = gru_ops.backward_quant_float_storage(
+        backward_fn = (gru_ops.backward_quant_int_storage if ctx.quant_storage_dtype == "int32"
+                       else gru_ops.backward_quant_float_storage)
+        dx, dW, dR, dbw, dbr, dh = backward_fn(
             time_steps=T, batch_size=B, input_size=I, hidden_size=H, W_q=W_q, R_q=R_q,
             bw_q=bw_q, br_q=br_q, x_q=x_q, dh_new=dh_new, h=h, v=v,
             quant_params=ctx.quant_params, **dict(zip(gru_ops.MASK_NAMES, masks)))
@@ -894,6 +903,107 @@ class QuantGRU(nn.Module):
         if self.batch_first:
             output = output.transpose(0, 1).contiguous()
         return output, h_n
+
+
+    # -- AIMET fixed-point contract (quant_gru.py:2290-2537) -------------------------------
+
+    _AIMET_SUPPORTED_MODES = ("fp32", "fp32_qdq", "fp16_qdq", "int16_fixed_eval",
+                              "int16_fixed_qat_sim", "calibrating")
+
+    def aimet_capabilities(self) -> dict:
+        """The adapter capability report (quant_gru.py:2336-2353)."""
+        return {
+            "adapter_version": "1.1",
+            "supported_modes": list(self._AIMET_SUPPORTED_MODES),
+            "forward_io_dtype": "float32",
+            "forward_io_device": "cuda",
+            "requires_calibration_for": ["int16_fixed_eval", "int16_fixed_qat_sim"],
+            "supports_forward_quantized": True,
+            "forward_quantized_input_dtypes": ["int32"],
+        }
+
+    def aimet_configure(self, mode: str) -> None:
+        """Map an AIMET execution mode onto the module flags (quant_gru.py:2355-2378)."""
+        normalized = str(mode).lower()
+        if normalized not in self._AIMET_SUPPORTED_MODES:
+            raise ValueError(f"Unsupported aimet_configure mode: {mode!r}. "
+                             f"Expected one of: {', '.join(self._AIMET_SUPPORTED_MODES)}.")
+        self.export_mode = False
+        if normalized == "calibrating":
+            self.calibrating = True
+            self.use_quantization = False
+            return
+        self.calibrating = False
+        self.use_quantization = normalized in ("int16_fixed_eval", "int16_fixed_qat_sim")
+
+    def get_io_quant_meta(self) -> dict:
+        """Grids of the input, output and hidden state as forward_quantized reads and writes
+        them (quant_gru.py:2380-2429): the effective (encoded) scale, zero point, bit width and
+        signedness of the x and h operators."""
+        if not self.is_calibrated() or self.quant_params is None:
+            raise RuntimeError("QuantGRU not calibrated")
+        qp = self.quant_params
+        cfg = self._bitwidth_config
+        use_pot2 = bool(self.use_pot2_scale)
+
+        def entry(prefix: str) -> dict:
+            scale = float(gru_ops.decode_effective_scale(float(getattr(qp, f"scale_{prefix}")),
+                                                         use_pot2))
+            is_symmetric = bool(getattr(cfg, f"{prefix}symmetric_"))
+            is_unsigned = bool(getattr(cfg, f"{prefix}unsigned_", False))
+            if is_unsigned and is_symmetric:
+                is_symmetric = False
+            return {"scale": scale, "zp": int(getattr(qp, f"zp_{prefix}")),
+                    "bitwidth": int(getattr(cfg, prefix)), "is_symmetric": is_symmetric,
+                    "is_unsigned": is_unsigned}
+
+        return {"input": entry("x_"), "output": entry("h_"), "hidden": entry("h_")}
+
+    def _forward_quantized_dir(self, x_q, h0_q, reverse: bool, device):
+        T, B, I = x_q.shape
+        W, R, bw, br = self._direction_weights(reverse, device)
+        qp = self.quant_params_reverse if reverse else self.quant_params
+        h0 = h0_q if h0_q is not None else torch.empty(0, dtype=torch.int32, device=device)
+        return gru_ops.forward_quantized_int_io(T, B, I, self.hidden_size, W, R, bw, br, x_q, h0,
+                                                qp)
+
+    def forward_quantized(self, input: torch.Tensor, hx: Optional[torch.Tensor] = None
+                          ) -> Tuple[torch.Tensor, torch.Tensor]:
+        """Integer-in, integer-out inference (quant_gru.py:2482-2537): input holds int32 codes
+        on the x grid ([T,B,I], or [B,T,I] with batch_first), hx int32 codes on the h grid (or
+        None); only the weights are quantised.  Returns int32 (output_q, h_n_q) shaped like
+        forward's outputs, with (output_q - zp) * scale equal to the quantised forward's
+        output (scale and zp from get_io_quant_meta)."""
+        if not self.is_calibrated() or self.quant_params is None:
+            raise RuntimeError("QuantGRU not calibrated")
+        if self.export_mode:
+            raise RuntimeError("forward_quantized does not support export_mode")
+        if input.is_floating_point():
+            raise TypeError("forward_quantized takes integer codes on the input grid (int in, "
+                            f"int out); got dtype={input.dtype}")
+        if self.batch_first:
+            input = input.transpose(0, 1)
+        T, B, I = input.shape
+        device = _require_device(input)
+        input = input.to(device=device, dtype=torch.int32).contiguous()
+        h0f = h0r = None
+        if hx is not None:
+            expected = (self.num_layers * self.num_directions, B, self.hidden_size)
+            if tuple(hx.shape) != expected:
+                raise ValueError(f"hx must have shape {expected}, got {tuple(hx.shape)}")
+            hx = hx.to(device=device, dtype=torch.int32)
+            h0f = hx[0].contiguous()
+            h0r = hx[1].contiguous() if self.bidirectional else None
+        out_f, hn_f = self._forward_quantized_dir(input, h0f, False, device)
+        out_r = hn_r = None
+        if self.bidirectional:
+            out_r, hn_r = self._forward_quantized_dir(input.flip(0).contiguous(), h0r, True,
+                                                      device)
+            out_r = out_r.flip(0)
+        output_q, h_n_q = self._combine_bidirectional_outputs(out_f, hn_f, out_r, hn_r)
+        if self.batch_first:
+            output_q = output_q.transpose(0, 1).contiguous()
+        return output_q, h_n_q
 
 
 def set_quant_gru_module_names(model: nn.Module, prefix: str = "") -> None:

@@ -448,3 +448,39 @@ def test_stepped_forward_equals_clustered(cuda, shape, cfg_name, monkeypatch):
     got = _gpu_forward(cuda, W, R, bw, br, x, h0, qp, True)
     for name, a, b in zip(NAMES, got, ref):
         assert torch.equal(a, b), name
+
+
+@pytest.mark.parametrize("cfg_name", ["c3", "16b-all"])
+@pytest.mark.parametrize("H", [48, 33])
+def test_workspace_contents_never_leak_into_results(cuda, monkeypatch, cfg_name, H):
+    """Forward and backward (FP32 and int32 carriers) read no workspace byte they did not write:
+    with every workspace filled with NaN bytes first the results equal those of zero-filled
+    workspaces.  3H = 144 / 99 is not a multiple of 32, where the GEMMs' last K chunk and the
+    packed operand tiles run past the data."""
+    T, B, I = 4, 10, 6
+    print(f"[gru workspace] H={H} cfg={cfg_name}", flush=True)
+    W, R, bw, br, x, h0, qp = _case(T, B, I, H, cfg_name, 9, True)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(cuda)
+    g = np.random.default_rng(10)
+    dh_new = g.standard_normal((T + 1, B, H)).astype(f32)
+
+    def run(fill):
+        monkeypatch.setattr(gru_ops, "_ws", lambda n, dev: torch.full(
+            (max(int(n), 256),), fill, dtype=torch.uint8, device=dev))
+        P = gru_ops.GRUQuantParams.from_struct(qp)
+        res = []
+        for fwd_fn, bwd_fn in ((gru_ops.forward_quant_float_storage,
+                                gru_ops.backward_quant_float_storage),
+                               (gru_ops.forward_quant_int_storage,
+                                gru_ops.backward_quant_int_storage)):
+            outs = fwd_fn(True, T, B, I, H, t(W), t(R), t(bw), t(br), t(x), t(h0), P)
+            grads = bwd_fn(T, B, I, H, outs[2], outs[3], outs[4], outs[5], outs[6], t(dh_new),
+                           outs[0], outs[1], P, *outs[7:])
+            res += [o.cpu().numpy() for o in (*outs, *grads) if o.numel()]
+        torch.cuda.synchronize()
+        return res
+
+    clean, dirty = run(0), run(255)
+    for k, (a, b) in enumerate(zip(clean, dirty)):
+        assert np.isfinite(b).all() if b.dtype.kind == "f" else True, k
+        np.testing.assert_array_equal(a, b, err_msg=f"output {k}")

@@ -246,3 +246,31 @@ def test_quant_params_json_checks(tmp_path):
         Q.QuantGRU(6, 32).load_quant_params(str(tmp_path / "a.json"))
     with pytest.raises(ValueError, match="bidirectional"):
         Q.QuantGRU(6, 16, bidirectional=True).load_quant_params(str(tmp_path / "a.json"))
+
+
+def test_aimet_capabilities_and_configure():
+    """The AIMET adapter contract (quant_gru.py:2290-2378): capability report and the
+    mode -> flag mapping."""
+    m = Q.QuantGRU(3, 4)
+    caps = m.aimet_capabilities()
+    assert caps["supports_forward_quantized"] and caps["forward_quantized_input_dtypes"] == ["int32"]
+    assert set(caps["supported_modes"]) == set(Q.QuantGRU._AIMET_SUPPORTED_MODES)
+    m.aimet_configure("calibrating")
+    assert m.calibrating and not m.use_quantization
+    m.aimet_configure("INT16_FIXED_EVAL")
+    assert not m.calibrating and m.use_quantization
+    m.aimet_configure("fp32_qdq")
+    assert not m.use_quantization
+    with pytest.raises(ValueError, match="Unsupported aimet_configure mode"):
+        m.aimet_configure("int4")
+
+
+def test_int_io_entry_points_check_their_arguments():
+    m = Q.QuantGRU(3, 4, quant_storage_dtype="int32")
+    assert m.quant_storage_dtype == "int32"
+    with pytest.raises(RuntimeError, match="not calibrated"):
+        m.get_io_quant_meta()
+    with pytest.raises(RuntimeError, match="not calibrated"):
+        m.forward_quantized(torch.zeros(2, 1, 3, dtype=torch.int32))
+    with pytest.raises(ValueError, match="quant_storage_dtype"):
+        Q.QuantGRU(3, 4, quant_storage_dtype="int16")
