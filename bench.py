@@ -11,7 +11,9 @@ Prints ONE JSON line.  Legs (all run by default):
 * c1   — the QuantGRU PTQ calibration pass (B=32, T=98, I=40, H=64): calibration forward,
          parameter derivation and PTQ forward, seq/s;
 * c5   — QuantGRU unidirectional QAT forward+backward at B=1024, T=50, I=256, H=1024 (4-bit
-         weights, 16-bit activations and h, power-of-2 scales): seq/s.
+         weights, 16-bit activations and h, power-of-2 scales): seq/s;
+* gint — the c3 model on the int32 carrier, PTQ inference of both directions (the work the
+         reference's CPU int carrier does, timed by the c3 CPU baseline), float and int-IO: seq/s.
 
 The roofline object describes the dominant kernel of the headline leg, timed with
 hipEvents that the library records around its own launches on the stream they run on
@@ -355,6 +357,92 @@ def _gru_leg(torch, steps: int, warmup: int):
            "kernels_ms_per_step": {k: round(v["ms_per_step"], 4) for k, v in kernels.items()},
            "kernels_us_per_launch": {k: round(v["us_per_launch"], 2) for k, v in kernels.items()}}
     return res, roof, m, x
+
+
+def _gru_int_leg(torch, steps: int, warmup: int):
+    """gint: the c3 model on the int32 carrier, PTQ inference (eval, no autograd) of both
+    directions -- the work of the reference's quantGRUForwardCPU, which the c3 CPU baseline
+    times -- with float input and output (quant_storage_dtype='int32'), and the same forward
+    with int32 codes in and out (forward_quantized)."""
+    import quant_gru as QG
+
+    dev = torch.device("cuda:0")
+    B, T, I, H = 256, 200, 80, 256
+    torch.manual_seed(6)
+    x = torch.randn(B, T, I)
+    m = QG.QuantGRU(I, H, batch_first=True, bidirectional=True)
+    m.set_all_bitwidth(8, is_symmetric=False)
+    m._bitwidth_config.h_ = 16
+    m = m.to(dev).eval()
+    x = x.to(dev)
+    with m.calibration_context():
+        m(x)
+    m.use_quantization = True
+    m.quant_storage_dtype = "int32"
+    out = {}
+
+    def step():
+        with torch.no_grad():
+            out["y"] = m(x)[0]
+
+    C, M = 3 * H, T * B
+    work = {"gru_int_recurrence": (2.0 * M * H * C, INT8_MFMA_PEAK,
+                                   "recurrent GEMM R_q (h_q - zp_h) of one direction over T steps "
+                                   "(one exact byte-plane int8-MFMA GEMM launch and one integer "
+                                   "pointwise launch per step)"),
+            "gru_int_input_gemm": (2.0 * M * C * I, INT8_MFMA_PEAK,
+                                   "input projection W_q (x_q - zp_x) of one direction")}
+    dt, p50, p95, kernels, roof = _timed_steps(torch, step, steps, warmup, work)
+    meta = m.get_io_quant_meta()
+    xin = meta["input"]
+    lo = 0 if xin["is_unsigned"] else -(1 << (xin["bitwidth"] - 1))
+    hi = (1 << xin["bitwidth"]) - 1 if xin["is_unsigned"] else (1 << (xin["bitwidth"] - 1)) - 1
+    xq = (torch.round(x / torch.tensor(xin["scale"], device=dev)) + xin["zp"]).clamp(lo, hi)
+    xq = xq.to(torch.int32)
+
+    def step_io():
+        out["q"] = m.forward_quantized(xq)[0]
+
+    for _ in range(warmup):
+        step_io()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step_io()
+    torch.cuda.synchronize()
+    dt_io = (time.perf_counter() - t0) / steps
+    _log(f"gru int32 carrier (c3 shape, PTQ inference): {dt*1e3:.2f} ms/step, {B/dt:.1f} seq/s; "
+         f"int codes in/out {dt_io*1e3:.2f} ms/step, {B/dt_io:.1f} seq/s")
+    for k, v in sorted(kernels.items(), key=lambda kv: -kv[1]["ms_per_step"]):
+        _log(f"  {k}: {v['ms_per_step']:.3f} ms/step, {v['us_per_launch']:.1f} us/launch")
+    res = {"ms_per_step": dt * 1e3, "p50_ms": p50, "p95_ms": p95, "seq_per_s": B / dt,
+           "int_io_ms_per_step": dt_io * 1e3, "int_io_seq_per_s": B / dt_io,
+           "kernels_ms_per_step": {k: round(v["ms_per_step"], 4) for k, v in kernels.items()}}
+    return res, roof, m, x, out
+
+
+def _validate_gru_int(m, x, y, yq, rows):
+    """The int32-carrier outputs of the sampled sequences equal the oracle's int32 carrier
+    (which equals the reference's CPU carrier code for code), bit for bit; the int-IO output
+    codes are the same h codes."""
+    import numpy as np
+
+    import gru_oracle as GO
+    import rxmet_gru_abi as A
+
+    H = m.hidden_size
+    xs = x.detach().transpose(0, 1)[:, rows].contiguous().cpu().numpy()
+    got = y.detach().transpose(0, 1)[:, rows].cpu().numpy()
+    gq = yq.detach().transpose(0, 1)[:, rows].cpu().numpy()
+    for d, (W, R, bw, br, qp, _, _) in enumerate(_gru_dirs_haste(m)):
+        xd = np.ascontiguousarray(xs[::-1]) if d else xs
+        f = GO.forward_int(W, R, bw, br, xd, qp, training=False)
+        hq = f["h_q"][1:][::-1] if d else f["h_q"][1:]
+        h = GO.dequant_int(hq, qp.g[A.GRID["h"]], bool(qp.use_pot2))
+        _check_equal(f"gru int32 output dir{d}", got[..., d * H:(d + 1) * H], h)
+        if d == 0:
+            _check_equal("gru int-IO codes dir0", gq[..., :H], hq)
+    return {"sequences": list(rows), "forward": "bit-exact (int32 carrier and int-IO codes)"}
 
 
 def _gru_c5_leg(torch, steps: int, warmup: int):
@@ -761,8 +849,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-validate", action="store_true",
                     help="skip the oracle comparison of the benchmarked outputs (profiling runs)")
-    ap.add_argument("--legs", default="gru,lstm,qdq,c1,c5",
-                    help="comma-separated subset of gru,lstm,qdq,c1,c5")
+    ap.add_argument("--legs", default="gru,lstm,qdq,c1,c5,gint",
+                    help="comma-separated subset of gru,lstm,qdq,c1,c5,gint")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run a plain elementwise copy over MIB MiB (scales HBM byte "
                          "counters in profiling runs)")
@@ -781,7 +869,7 @@ def main() -> int:
         _copy_probe(torch, args.copy_probe)
     validate = not args.no_validate
     checks = {}
-    gru = roof = lstm = lstm_roof = qdq = qdq_roof = c5 = c1 = None
+    gru = roof = lstm = lstm_roof = qdq = qdq_roof = c5 = c1 = gint = gint_roof = None
     try:
         if "gru" in legs:
             gru, roof, m, x = _gru_leg(torch, args.steps, args.warmup)
@@ -801,6 +889,11 @@ def main() -> int:
             c1, c1m, c1x, c1y = _c1_leg(torch, args.steps, args.warmup)
             if validate:
                 checks["c1"] = _validate_c1(c1m, c1x, c1y)
+        if "gint" in legs:
+            gint, gint_roof, gm, gx, gout = _gru_int_leg(torch, args.steps, args.warmup)
+            if validate:
+                checks["gint"] = _validate_gru_int(gm, gx, gout["y"], gout["q"], [0, 255])
+                _log(f"gint validation: {checks['gint']}")
         if "c5" in legs:
             c5, c5m, c5x = _gru_c5_leg(torch, args.steps, args.warmup)
             if validate:
@@ -826,6 +919,8 @@ def main() -> int:
         if c5 is not None:
             cpu_c5 = _gru_cpu_baseline(c5m, c5x, 8, False, "c5", budget_s=8.0)
             _log(f"c5 cpu baseline: {cpu_c5}")
+        if gint is not None and cpu is None:
+            cpu = _gru_cpu_baseline(gm, gx, 32, True, "c3")
     rnd = lambda d: None if d is None else {k: (round(v, 4) if isinstance(v, float) else v)
                                             for k, v in d.items()}
     line = {
@@ -851,6 +946,8 @@ def main() -> int:
         "lstm": rnd(lstm),
         "gru_c1": rnd(c1),
         "gru_c5": rnd(c5),
+        "gru_int32_c3": rnd(gint),
+        "gru_int32_roofline": gint_roof,
         "qdq": None if qdq is None else {k: {kk: round(vv, 3) for kk, vv in v.items()}
                                          for k, v in qdq.items()},
         "roofline": roof,

@@ -9,7 +9,8 @@ is checked against the oracle as well.
   weights, 8-bit asymmetric activations, 16-bit h; calibrated on the GPU over the whole batch.
 - c4: QuantLSTM QAT, B=512, T=100, I=64, H=512, 8-bit weights and gates, 16-bit cell state.
 - c1: QuantGRU PTQ calibration pass, B=32, T=98, I=40, H=64, per-tensor symmetric 8-bit
-  weights, asymmetric 8-bit activations; every sequence checked.
+  weights, asymmetric 8-bit activations, then the PTQ forward on the FP32 carrier and on the
+  int32 carrier (and int codes in and out); every sequence checked.
 
 Bars: forward outputs bit-exact; gradients within 1e-4 relative of the oracle; calibration
 ranges within the device-tanhf tolerance of the calibration tests.
@@ -220,3 +221,26 @@ def test_c1_full_size_calibration_and_ptq_forward_match_oracle(cuda):
     fwd = GO.forward_quant(W, R, bw, br, xs, qp, training=False)
     np.testing.assert_array_equal(y.transpose(0, 1).cpu().numpy(), fwd["h"][1:], err_msg="PTQ h")
     np.testing.assert_array_equal(hn[0].cpu().numpy(), fwd["h"][-1], err_msg="PTQ h_n")
+    # the same PTQ forward on the int32 carrier: every code equals the oracle's int32 carrier
+    # (pinned code for code against the reference's compiled CPU carrier) and, where oracle/_ref
+    # is present, the reference's own quantGRUForwardCPU run on the GPU's grids
+    m.quant_storage_dtype = "int32"
+    with torch.no_grad():
+        yi, hni = m(xd)
+    torch.cuda.synchronize()
+    fi = GO.forward_int(W, R, bw, br, xs, qp, training=False)
+    hi = GO.dequant_int(fi["h_q"], qp.g[A.GRID["h"]], False)
+    np.testing.assert_array_equal(yi.transpose(0, 1).cpu().numpy(), hi[1:], err_msg="int32 h")
+    np.testing.assert_array_equal(hni[0].cpu().numpy(), hi[-1], err_msg="int32 h_n")
+    if GO.has_ref():
+        ref = GO.ref_forward_int_codes(W, R, bw, br, xs, qp, with_v=False)
+        np.testing.assert_array_equal(fi["h_q"], ref["h_q"], err_msg="oracle vs reference codes")
+    # int codes in and out: forward_quantized on the input codes gives the same h codes
+    meta = m.get_io_quant_meta()
+    out_q, hn_q = m.forward_quantized(torch.from_numpy(fi["x_q"]).transpose(0, 1).to(cuda))
+    np.testing.assert_array_equal(out_q.transpose(0, 1).cpu().numpy(), fi["h_q"][1:])
+    np.testing.assert_array_equal(hn_q[0].cpu().numpy(), fi["h_q"][-1])
+    assert meta["input"]["zp"] == qp.g[A.GRID["x"]].zero_point
+    # the two carriers round their rescales differently; they stay within a few h steps
+    steps = np.abs(yi.cpu().numpy() - y.cpu().numpy()) / meta["output"]["scale"]
+    assert steps.max() <= 8, steps.max()
