@@ -140,8 +140,10 @@ int64_t rxmet_lstm_forward_workspace_bytes(int32_t T, int32_t B, int32_t I, int3
 
 /* Quantised FP32-carrier forward.  x [T,B,I] time-major; h0/c0 [B,H] both or neither.
  * Writes output [T,B,H], h_n, c_n [B,H] dequantised.  With saved != null (training) every
- * pointer in it must be set (bias ones only with bias).  Requires W_hh of at most 8 bits
- * (int8 MFMA recurrence). */
+ * pointer in it must be set (bias ones only with bias).  W_hh within signed 16 bits and H a
+ * multiple of 16: W_hh of at most 8 bits and H up to 512 run on the int8-MFMA clustered
+ * recurrence, wider W_hh or larger H on the stepped recurrence (exact GEMM + pointwise per
+ * step). */
 int rxmet_lstm_forward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const float *W_ih,
                              const float *W_hh, const float *b_ih, const float *b_hh,
                              const float *x, const float *h0, const float *c0,
