@@ -165,6 +165,101 @@ int rxmet_qdq_encoding_backward(const float *mn, const float *mx, const float *g
                                 int32_t symmetric, float min_scale, float *d_min, float *d_max,
                                 void *stream);
 
+/* ---------------------------------------------------------------------------------------
+ * General entry points: fp16 / bf16 tensors, the reference's internal arithmetic type,
+ * zero_point_shift, and encodings over two separated groups of axes.
+ * ------------------------------------------------------------------------------------- */
+
+/* Element types (tensors: F32, F16, BF16; internal arithmetic: also F64). */
+enum {
+  RXMET_QDQ_F32 = 0,
+  RXMET_QDQ_F16 = 1,
+  RXMET_QDQ_BF16 = 2,
+  RXMET_QDQ_F64 = 3,
+};
+
+/*
+ * Tensor layout [outer, C0, mid, C1, inner] (row-major): element (o, c0, m, c1, k) uses
+ * encoding c0 * C1 + c1, so scale/offset hold C0 * C1 values.  The three-argument layout
+ * [outer, C, inner] above is {1, 1, outer, C, inner}.  Two separated encoding groups cover
+ * per-channel encodings on two non-adjacent axes and two-dimensional block quantization
+ * (torch_builtins.py:694-754 reshapes a [R, Cc] tensor with block sizes (br, bc) to
+ * [R/br, br, Cc/bc, bc] with encodings [R/br, 1, Cc/bc, 1]: {1, R/br, br, Cc/bc, bc}).
+ */
+typedef struct rxmet_qdq_layout {
+  int64_t outer, C0, mid, C1, inner;
+} rxmet_qdq_layout;
+
+/*
+ * Arithmetic of one call, as the reference's backend evaluates it:
+ *   io_dtype        element type of x, y, g and dx (F32, F16 or BF16);
+ *   internal_dtype  type QuantizeFunc / QuantDequantFunc compute in (io_dtype, F32 or F64:
+ *                   torch_builtins.py:171-174, 255-262 widen it while the grid is not
+ *                   numerically stable in the narrower type); every operation's result is
+ *                   rounded to it, and the result to io_dtype.  Dequantize computes in
+ *                   io_dtype (internal_dtype must equal it); the frozen mode computes as
+ *                   torch.fake_quantize does, in fp32, whatever the io type.
+ *   zero_point_shift  quantize_dequantize only (learnable mode): y = qdq(x - shift * s) +
+ *                   shift * s (torch_builtins.py:276-284); 0 for none.
+ *   scalar_scale    the reference's scale is a 0-dim tensor.  PyTorch then evaluates binary
+ *                   operations between the input tensor and the scale in the input's type
+ *                   (the scale rounded to it first): the shift's subtraction and
+ *                   QuantizeFunc.backward's tensor / scale.  Only matters when
+ *                   internal_dtype is wider than io_dtype.
+ * scale and offset always arrive as fp32 arrays holding the internal-type values
+ * (scale.to(internal) of the reference; with an F64 internal type the values must be exact
+ * in fp32, which fp32/fp16/bf16 parameters are).
+ */
+typedef struct rxmet_qdq_numerics {
+  int32_t io_dtype;
+  int32_t internal_dtype;
+  double zero_point_shift;
+  int32_t scalar_scale;
+  int32_t reserved; /* 0 */
+} rxmet_qdq_numerics;
+
+/* Workspace bytes of the _ex reductions for this layout and io type. */
+int64_t rxmet_qdq_workspace_bytes_ex(const rxmet_qdq_layout *layout, int32_t io_dtype);
+
+/* rxmet_qdq_minmax for any io type and layout; out_min/out_max: [C0 * C1] fp32 (exact). */
+int rxmet_qdq_minmax_ex(const void *x, int32_t io_dtype, const rxmet_qdq_layout *layout,
+                        float *out_min, float *out_max, void *workspace, void *stream);
+
+/*
+ * quantize_dequantize forward / backward (torch_builtins.py:199-284 with QuantDequantFunc
+ * :618-691, or the frozen fast path :221-249 + :287-361).  Gradients of the shift's own
+ * terms are included: dscale[c] gains shift * sum g * (1 - mask).  dscale / doffset come back
+ * rounded to the internal type (stored as fp32).
+ */
+int rxmet_qdq_forward_ex(const void *x, void *y, const rxmet_qdq_layout *layout,
+                         const rxmet_qdq_numerics *numerics, const float *scale,
+                         const float *offset, int64_t qmin, int64_t qmax, int mode,
+                         void *stream);
+int rxmet_qdq_backward_ex(const void *x, const void *g, void *dx, float *dscale, float *doffset,
+                          const rxmet_qdq_layout *layout, const rxmet_qdq_numerics *numerics,
+                          const float *scale, const float *offset, int64_t qmin, int64_t qmax,
+                          int mode, void *workspace, void *stream);
+
+/* quantize forward / backward (torch_builtins.py:151-194 with QuantizeFunc :505-571); q in
+ * io_dtype (the grid must be exact in it). */
+int rxmet_quantize_forward_ex(const void *x, void *q, const rxmet_qdq_layout *layout,
+                              const rxmet_qdq_numerics *numerics, const float *scale,
+                              const float *offset, int64_t qmin, int64_t qmax, void *stream);
+int rxmet_quantize_backward_ex(const void *x, const void *g, void *dx, float *dscale,
+                               float *doffset, const rxmet_qdq_layout *layout,
+                               const rxmet_qdq_numerics *numerics, const float *scale,
+                               const float *offset, int64_t qmin, int64_t qmax,
+                               void *workspace, void *stream);
+
+/* dequantize forward / backward (torch_builtins.py:459-488 with DequantizeFunc :574-615). */
+int rxmet_dequantize_forward_ex(const void *q, void *y, const rxmet_qdq_layout *layout,
+                                const rxmet_qdq_numerics *numerics, const float *scale,
+                                const float *offset, void *stream);
+int rxmet_dequantize_backward_ex(const void *q, const void *g, void *dq, float *dscale,
+                                 float *doffset, const rxmet_qdq_layout *layout,
+                                 const rxmet_qdq_numerics *numerics, const float *scale,
+                                 const float *offset, void *workspace, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -248,3 +248,234 @@ def torch_frozen_step(torch, x, g, scale: float, zero_point: int, qmin: int, qma
     y = torch.fake_quantize_per_tensor_affine(xg, scale, zero_point, qmin, qmax)
     y.backward(g)
     return y.detach(), xg.grad
+
+
+# ---------------------------------------------------------------------------------
+# General numerics: fp16 / bf16 tensors, the reference's internal arithmetic type, the
+# zero-point shift, and encodings of any broadcastable shape.
+#
+# torch_builtins.quantize_dequantize (:199-284) computes in an internal type R (the tensor's
+# type, widened to fp32 or fp64 while the grid is not numerically stable in it, :255-262)
+# and returns the result in the tensor's type T.  PyTorch evaluates each elementwise
+# operation on 16-bit tensors in fp32 and rounds the result to the storage type; these
+# functions do the same with numpy: every operation in fp32 (fp64 when R is fp64), its
+# result rounded to R.  Shapes follow torch broadcasting: x of any shape, scale/offset
+# broadcastable to it, encoding gradients summed back to the broadcast encoding shape in
+# fp64 (the reference sums in R; the sums here are then rounded to R).
+#
+# On the GPU a 0-dim scale tensor next to a T tensor makes PyTorch evaluate the operation
+# in T with the scale rounded to T (``scalar_scale``): the shift's subtraction (:277) and
+# QuantizeFunc.backward's tensor / scale (:567).  The CPU tensor iterator instead reads a
+# 0-dim operand at its original precision, so the CPU cannot stand in for this case; the
+# GPU tests check it against torch on the GPU.
+# ---------------------------------------------------------------------------------
+
+f64 = np.float64
+TYPES = ("f32", "f16", "bf16", "f64")
+
+
+def round_to(v, dt: str):
+    """Values rounded to type ``dt``, returned as float32 (float64 for "f64")."""
+    if dt == "f64":
+        return np.asarray(v, dtype=f64)
+    v = np.asarray(v, dtype=f32)
+    if dt == "f32":
+        return v
+    if dt == "f16":
+        return v.astype(np.float16).astype(f32)
+    if dt == "bf16":
+        u = v.view(np.uint32).astype(np.uint64)
+        r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+        out = r.astype(np.uint32).view(f32)
+        return np.where(np.isnan(v), f32(np.nan), out).astype(f32)
+    raise ValueError(dt)
+
+
+def to_io(v, io: str):
+    """The final ``.to(T)``: fp64 results pass through fp32 on their way to 16-bit types,
+    as PyTorch's conversions do."""
+    v = np.asarray(v)
+    if v.dtype == f64:
+        v = v.astype(f32)
+    return round_to(v, io)
+
+
+def _ctype(internal: str):
+    return f64 if internal == "f64" else f32
+
+
+def _sum_to(el, shape):
+    """Sum fp64 terms over the axes broadcast from ``shape`` (torch's sum_to_size)."""
+    el = np.asarray(el, dtype=f64)
+    nd = el.ndim
+    shape = (1,) * (nd - len(shape)) + tuple(shape)
+    axes = tuple(a for a in range(nd) if shape[a] == 1 and el.shape[a] != 1)
+    return el.sum(axis=axes, keepdims=True).reshape(shape)
+
+
+def _check_shift(shift):
+    # x - shift * s and y + shift * s are evaluated as fused multiply-adds on the GPU; a
+    # power-of-two shift (the quantizers allow 0.5) makes the product exact, so one rounding
+    # of the sum is the result either way
+    if shift != 0.0:
+        m, _ = math.frexp(abs(shift))
+        assert m == 0.5, "power-of-two zero_point_shift only"
+
+
+def _shifted(x, s, shift, io, internal, scalar_scale):
+    A = _ctype(internal)
+    if shift == 0.0:
+        return np.asarray(x, dtype=A)
+    if scalar_scale:
+        s_io = round_to(np.asarray(s, dtype=f32), io)
+        return round_to((np.asarray(x, f32) - (f32(shift) * s_io).astype(f32)).astype(f32),
+                        io).astype(A)
+    return round_to((np.asarray(x, A) - (A(shift) * np.asarray(s, A)).astype(A)).astype(A),
+                    internal)
+
+
+def qdq_general(x, scale, offset, qmin, qmax, io="f32", internal="f32", shift=0.0,
+                scalar_scale=False):
+    """quantize_dequantize forward, learnable path (QuantDequantFunc :640-672, with the
+    shift of :276-284).  ``x`` holds values of type ``io``; scale/offset hold the values of
+    scale.to(R) / offset.to(R).  Returns (y as ``io`` values, mask)."""
+    _check_shift(shift)
+    A = _ctype(internal)
+
+    def r(v):
+        return round_to(np.asarray(v, A), internal)
+
+    s, o = np.asarray(scale, A), np.asarray(offset, A)
+    with np.errstate(invalid="ignore", over="ignore", divide="ignore"):
+        v = _shifted(x, scale, shift, io, internal, scalar_scale)
+        t = r(v / s)
+        q = r(np.rint(t) - o)
+        mask = (q >= qmin) & (q <= qmax)
+        c = np.where(q < qmin, A(qmin), np.where(q > qmax, A(qmax), q)).astype(A)
+        y = r(r(c + o) * s)
+        if shift != 0.0:
+            y = r(y + (A(shift) * s).astype(A))
+    return to_io(y, io), mask
+
+
+def qdq_general_backward(x, g, scale, offset, qmin, qmax, io="f32", internal="f32", shift=0.0,
+                         scalar_scale=False):
+    """QuantDequantFunc.backward (:675-691) plus the shift's scale terms; returns
+    (dx as ``io`` values, dscale, doffset) with the encoding gradients in the broadcast
+    encoding shape, summed in fp64 and rounded to R."""
+    _check_shift(shift)
+    A = _ctype(internal)
+
+    def r(v):
+        return round_to(np.asarray(v, A), internal)
+
+    s, o = np.asarray(scale, A), np.asarray(offset, A)
+    enc_shape = np.broadcast_shapes(np.shape(scale), np.shape(offset))
+    ga = np.asarray(g, A)
+    with np.errstate(invalid="ignore", over="ignore", divide="ignore"):
+        v = _shifted(x, scale, shift, io, internal, scalar_scale)
+        t = r(v / s)
+        rr = np.rint(t)
+        q = r(rr - o)
+        m = ((q >= qmin) & (q <= qmax)).astype(A)
+        lo, hi = r(o + A(qmin)), r(o + A(qmax))
+        cl = np.where(rr < lo, lo, np.where(rr > hi, hi, rr)).astype(A)
+        ds_el = r(ga * r(cl - (t * m).astype(A))).astype(f64)
+        if shift != 0.0:
+            ds_el = ds_el + f64(shift) * (ga * (A(1) - m)).astype(f64)
+        do_el = r(ga * r((A(1) - m) * s)).astype(f64)
+        dx = (ga * m).astype(A)
+    ds = round_to(_sum_to(ds_el, enc_shape).astype(f32), internal)
+    do = round_to(_sum_to(do_el, enc_shape).astype(f32), internal)
+    return to_io(dx, io), np.asarray(ds, f32), np.asarray(do, f32)
+
+
+def qdq_frozen_general(x, scale, offset, qmin, qmax, io="f32"):
+    """The fast path for any io type: torch.fake_quantize computes in fp32 and stores the
+    result in the tensor's type (torch_builtins.py:287-361)."""
+    xs = np.asarray(x, f32)
+    s = np.asarray(scale, f32)
+    inv_s = (f32(1.0) / s).astype(f32)
+    zp = -np.trunc(np.asarray(offset, f32)).astype(f32)
+    with np.errstate(invalid="ignore", over="ignore"):
+        q = (np.rint((xs * inv_s).astype(f32)) + zp).astype(f32)
+        mask = (q >= qmin) & (q <= qmax)
+        c = np.where(q < qmin, f32(qmin), np.where(q > qmax, f32(qmax), q)).astype(f32)
+        y = ((c - zp).astype(f32) * s).astype(f32)
+    return round_to(y, io), mask
+
+
+def quantize_general(x, scale, offset, qmin, qmax, io="f32", internal="f32"):
+    """QuantizeFunc.forward (:527-552) in R, stored in T."""
+    A = _ctype(internal)
+
+    def r(v):
+        return round_to(np.asarray(v, A), internal)
+
+    s, o = np.asarray(scale, A), np.asarray(offset, A)
+    with np.errstate(invalid="ignore", over="ignore", divide="ignore"):
+        q = r(np.rint(r(np.asarray(x, A) / s)) - o)
+        c = np.where(q < qmin, A(qmin), np.where(q > qmax, A(qmax), q)).astype(A)
+    return to_io(c, io)
+
+
+def quantize_general_backward(x, g, scale, offset, qmin, qmax, io="f32", internal="f32",
+                              scalar_scale=False):
+    """QuantizeFunc.backward (:555-571): dx = fl(g*mask/s), dscale = sum -(g*mask/s)*(x/s),
+    doffset = sum -g*mask, each operation rounded to R (x/s in T when the scale is 0-dim)."""
+    A = _ctype(internal)
+
+    def r(v):
+        return round_to(np.asarray(v, A), internal)
+
+    s, o = np.asarray(scale, A), np.asarray(offset, A)
+    enc_shape = np.broadcast_shapes(np.shape(scale), np.shape(offset))
+    ga = np.asarray(g, A)
+    with np.errstate(invalid="ignore", over="ignore", divide="ignore"):
+        t = r(np.asarray(x, A) / s)
+        q = r(np.rint(t) - o)
+        m = ((q >= qmin) & (q <= qmax)).astype(A)
+        mg = (ga * m).astype(A)
+        gs = r(mg / s)
+        if scalar_scale:
+            s_io = round_to(np.asarray(scale, f32), io)
+            xs = round_to((np.asarray(x, f32) / s_io).astype(f32), io).astype(A)
+        else:
+            xs = t
+        ds_el = r(-gs * xs).astype(f64)
+        do_el = (-mg).astype(f64)
+    ds = round_to(_sum_to(ds_el, enc_shape).astype(f32), internal)
+    do = round_to(_sum_to(do_el, enc_shape).astype(f32), internal)
+    return to_io(gs, io), np.asarray(ds, f32), np.asarray(do, f32)
+
+
+def dequantize_general(q, scale, offset, io="f32"):
+    """DequantizeFunc.forward (:589-603) in the tensor's type."""
+    def r(v):
+        return round_to(np.asarray(v, f32), io)
+
+    return r(r(np.asarray(q, f32) + np.asarray(offset, f32)) * np.asarray(scale, f32))
+
+
+def dequantize_general_backward(q, g, scale, offset, io="f32"):
+    """DequantizeFunc.backward (:607-615) in the tensor's type."""
+    def r(v):
+        return round_to(np.asarray(v, f32), io)
+
+    s, o = np.asarray(scale, f32), np.asarray(offset, f32)
+    enc_shape = np.broadcast_shapes(np.shape(scale), np.shape(offset))
+    ga = np.asarray(g, f32)
+    gs = r(ga * s)
+    ds = round_to(_sum_to(r(ga * r(np.asarray(q, f32) + o)), enc_shape).astype(f32), io)
+    do = round_to(_sum_to(gs, enc_shape).astype(f32), io)
+    return gs, np.asarray(ds, f32), np.asarray(do, f32)
+
+
+def minmax_general(x, enc_shape):
+    """Min / max of x reduced to ``enc_shape`` (NaN propagates)."""
+    x = np.asarray(x, f32)
+    nd = x.ndim
+    shape = (1,) * (nd - len(enc_shape)) + tuple(enc_shape)
+    axes = tuple(a for a in range(nd) if shape[a] == 1)
+    return (x.min(axis=axes, keepdims=True).reshape(tuple(enc_shape)),
+            x.max(axis=axes, keepdims=True).reshape(tuple(enc_shape)))

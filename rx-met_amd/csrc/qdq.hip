@@ -1,369 +1,55 @@
-// qdq.hip — MI355X (gfx950) streaming fake-quantization kernels behind rxmet_qdq.h.
+// qdq.hip — C ABI of the MI355X (gfx950) fake-quantization kernels (rxmet_qdq.h).
 //
 // The AIMET reference runs QuantizeDequantize as a chain of PyTorch elementwise ops
 // (src/aimet_torch/v2/quantization/affine/backends/torch_builtins.py:618-691): about seven
 // full HBM passes forward and ten backward plus broadcast reductions.  Here each
 // direction is one pass:
-//   forward  : read x, write y                                   (8 B/element)
-//   backward : read x and g, write dx, reduce encoding gradients (12 B/element)
-//   min/max  : read x                                            (4 B/element)
-//
-// Work decomposition.  The tensor is [outer, C, inner]; a "run" is one contiguous
-// stretch of `inner` elements sharing one encoding.  When runs are long (or the
-// encoding is per-tensor) every workgroup streams one CHUNK of one run with f4
-// accesses and wave-uniform (scalar) encoding loads.  When runs are short (per-channel
-// on a trailing axis) a "column" decomposition is used instead: threads own columns of
-// the [outer, C*inner] matrix and walk rows, so accesses stay coalesced.  Reductions
-// write one fp64 partial per workgroup (or per column and row-chunk) and a second
-// kernel folds the partials of each encoding in a fixed order, so results are
-// deterministic and need no atomics.
+//   forward  : read x, write y                                   (2 * sizeof(T) B/element)
+//   backward : read x and g, write dx, reduce encoding gradients (3 * sizeof(T) B/element)
+//   min/max  : read x                                            (sizeof(T) B/element)
+// The kernels and their work decompositions are in qdq_kernels.h, instantiated per
+// tensor type in qdq_f32.hip / qdq_f16.hip / qdq_bf16.hip.  This file plans a call
+// (layout normalization, decomposition, partial-sum layout), checks its arguments, and
+// folds the per-block partial sums of the encoding gradients and min/max.
 #include <mutex>
 #include <string>
 
-#include "rxmet_common.h"
-#include "rxmet_qdq.h"
+#include "qdq_kernels.h"
 
 namespace rxmet {
 namespace qdq {
 
-enum Op { OP_QDQ_LEARN = 0, OP_QDQ_FROZEN = 1, OP_Q = 2, OP_DQ = 3 };
-
-constexpr int kThreads = 256;
-constexpr int kVecPerThread = 8;                            // f4 per thread per chunk
-constexpr int64_t kChunk = kThreads * kVecPerThread * 4;    // 8192 elements
-constexpr int64_t kMinRun = 1024;                           // shorter runs use columns
-constexpr int kColTargetBlocks = 2048;
-
-struct Enc {
-  float s, o, inv_s, zp, qmin, qmax;
-};
-
-__device__ __forceinline__ Enc load_enc(const float *scale, const float *offset, int64_t c,
-                                        float qmin, float qmax) {
-  Enc e;
-  e.s = scale[c];
-  e.o = offset ? offset[c] : 0.0f;
-  e.inv_s = 1.0f / e.s;  // torch's fake_quantize kernels multiply by fp32 1/scale
-  e.zp = -truncf(e.o);   // zero point = -offset.to(int32)
-  e.qmin = qmin;
-  e.qmax = qmax;
-  return e;
-}
-
-template <int OP>
-__device__ __forceinline__ float fwd_elem(float x, const Enc &e) {
-  if constexpr (OP == OP_QDQ_LEARN) {
-    const float r = rintf(x / e.s) - e.o;
-    return (clamp_keep_nan(r, e.qmin, e.qmax) + e.o) * e.s;
-  } else if constexpr (OP == OP_QDQ_FROZEN) {
-    const float r = rintf(x * e.inv_s) + e.zp;
-    return (clamp_keep_nan(r, e.qmin, e.qmax) - e.zp) * e.s;
-  } else if constexpr (OP == OP_Q) {
-    const float r = rintf(x / e.s) - e.o;
-    return clamp_keep_nan(r, e.qmin, e.qmax);
-  } else {
-    return (x + e.o) * e.s;
-  }
-}
-
-// One element of the backward: returns dx and adds this element's encoding-gradient
-// terms to (ds, dof).
-template <int OP>
-__device__ __forceinline__ float bwd_elem(float x, float g, const Enc &e, double &ds,
-                                          double &dof) {
-  if constexpr (OP == OP_QDQ_LEARN) {
-    const float xs = x / e.s;
-    const float rr = rintf(xs);
-    const float r = rr - e.o;
-    const float m = (r >= e.qmin && r <= e.qmax) ? 1.0f : 0.0f;
-    const float lo = e.o + e.qmin, hi = e.o + e.qmax;
-    ds += static_cast<double>(g * (clamp_keep_nan(rr, lo, hi) - xs * m));
-    dof += static_cast<double>(g * ((1.0f - m) * e.s));
-    return g * m;
-  } else if constexpr (OP == OP_QDQ_FROZEN) {
-    const float r = rintf(x * e.inv_s) + e.zp;
-    const float m = (r >= e.qmin && r <= e.qmax) ? 1.0f : 0.0f;
-    return g * m;
-  } else if constexpr (OP == OP_Q) {
-    const float r = rintf(x / e.s) - e.o;
-    const float m = (r >= e.qmin && r <= e.qmax) ? 1.0f : 0.0f;
-    const float mg = g * m;
-    const float gs = mg / e.s;
-    ds += static_cast<double>(-gs * (x / e.s));
-    dof += static_cast<double>(-mg);
-    return gs;
-  } else {
-    const float gs = g * e.s;
-    ds += static_cast<double>(g * (x + e.o));
-    dof += static_cast<double>(gs);
-    return gs;
-  }
-}
-
 // ---------------------------------------------------------------------------------
-// Block-wide reductions (256 threads = 4 waves).
+// Partial folding: one workgroup per encoding; the partials of encoding c are
+// fold_index(c, p) for p < n0 * n1 * n2.  Each thread folds a fixed, strided subset; the
+// lanes are then combined by a fixed butterfly and the waves in a fixed order.
 // ---------------------------------------------------------------------------------
-__device__ __forceinline__ void block_sum2(double &a, double &b) {
-  __shared__ double sa[kThreads / kWave], sb[kThreads / kWave];
-  a = wave_sum(a);
-  b = wave_sum(b);
-  const int lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
-  if (lane == 0) {
-    sa[w] = a;
-    sb[w] = b;
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    a = sa[0];
-    b = sb[0];
-#pragma unroll
-    for (int i = 1; i < kThreads / kWave; ++i) {
-      a += sa[i];
-      b += sb[i];
-    }
-  }
-}
-
-__device__ __forceinline__ void block_minmax(float &mn, float &mx) {
-  __shared__ float smn[kThreads / kWave], smx[kThreads / kWave];
-  mn = wave_min(mn);
-  mx = wave_max(mx);
-  const int lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
-  if (lane == 0) {
-    smn[w] = mn;
-    smx[w] = mx;
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    mn = smn[0];
-    mx = smx[0];
-#pragma unroll
-    for (int i = 1; i < kThreads / kWave; ++i) {
-      mn = nan_min(mn, smn[i]);
-      mx = nan_max(mx, smx[i]);
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------------
-// Run decomposition: block b handles chunk (b % splits) of run (b / splits).
-// ---------------------------------------------------------------------------------
-template <int OP>
-__global__ __launch_bounds__(kThreads) void fwd_runs(const float *__restrict__ x,
-                                                     float *__restrict__ y, int64_t inner,
-                                                     int64_t C, int64_t splits,
-                                                     const float *__restrict__ scale,
-                                                     const float *__restrict__ offset,
-                                                     float qmin, float qmax, int vec4) {
-  const int64_t b = blockIdx.x;
-  const int64_t run = b / splits, sp = b % splits;
-  const Enc e = load_enc(scale, offset, run % C, qmin, qmax);
-  const int64_t beg = sp * kChunk;
-  const int64_t end = min(inner, beg + kChunk);
-  const int64_t base = run * inner + beg;
-  if (vec4) {
-    const f4 *xv = reinterpret_cast<const f4 *>(x + base);
-    f4 *yv = reinterpret_cast<f4 *>(y + base);
-    const int nv = static_cast<int>((end - beg) >> 2);
-    f4 v[kVecPerThread];
-#pragma unroll
-    for (int k = 0; k < kVecPerThread; ++k) {
-      const int i = k * kThreads + threadIdx.x;
-      if (i < nv) v[k] = __builtin_nontemporal_load(xv + i);
-    }
-#pragma unroll
-    for (int k = 0; k < kVecPerThread; ++k) {
-      const int i = k * kThreads + threadIdx.x;
-      if (i < nv) {
-        f4 o;
-        o.x = fwd_elem<OP>(v[k].x, e);
-        o.y = fwd_elem<OP>(v[k].y, e);
-        o.z = fwd_elem<OP>(v[k].z, e);
-        o.w = fwd_elem<OP>(v[k].w, e);
-        __builtin_nontemporal_store(o, yv + i);
-      }
-    }
-  } else {
-    const int n = static_cast<int>(end - beg);
-    for (int i = threadIdx.x; i < n; i += kThreads) y[base + i] = fwd_elem<OP>(x[base + i], e);
-  }
-}
-
-template <int OP, bool ENC>
-__global__ __launch_bounds__(kThreads) void bwd_runs(
-    const float *__restrict__ x, const float *__restrict__ g, float *__restrict__ dx,
-    int64_t inner, int64_t C, int64_t splits, const float *__restrict__ scale,
-    const float *__restrict__ offset, float qmin, float qmax, int vec4,
-    double2 *__restrict__ partial) {
-  const int64_t b = blockIdx.x;
-  const int64_t run = b / splits, sp = b % splits;
-  const Enc e = load_enc(scale, offset, run % C, qmin, qmax);
-  const int64_t beg = sp * kChunk;
-  const int64_t end = min(inner, beg + kChunk);
-  const int64_t base = run * inner + beg;
-  double ds = 0.0, dof = 0.0;
-  if (vec4) {
-    const f4 *xv = reinterpret_cast<const f4 *>(x + base);
-    const f4 *gv = reinterpret_cast<const f4 *>(g + base);
-    f4 *dv = reinterpret_cast<f4 *>(dx + base);
-    const int nv = static_cast<int>((end - beg) >> 2);
-    f4 xr[kVecPerThread], gr[kVecPerThread];
-#pragma unroll
-    for (int k = 0; k < kVecPerThread; ++k) {
-      const int i = k * kThreads + threadIdx.x;
-      if (i < nv) {
-        xr[k] = __builtin_nontemporal_load(xv + i);
-        gr[k] = __builtin_nontemporal_load(gv + i);
-      }
-    }
-#pragma unroll
-    for (int k = 0; k < kVecPerThread; ++k) {
-      const int i = k * kThreads + threadIdx.x;
-      if (i < nv) {
-        f4 o;
-        o.x = bwd_elem<OP>(xr[k].x, gr[k].x, e, ds, dof);
-        o.y = bwd_elem<OP>(xr[k].y, gr[k].y, e, ds, dof);
-        o.z = bwd_elem<OP>(xr[k].z, gr[k].z, e, ds, dof);
-        o.w = bwd_elem<OP>(xr[k].w, gr[k].w, e, ds, dof);
-        __builtin_nontemporal_store(o, dv + i);
-      }
-    }
-  } else {
-    const int n = static_cast<int>(end - beg);
-    for (int i = threadIdx.x; i < n; i += kThreads)
-      dx[base + i] = bwd_elem<OP>(x[base + i], g[base + i], e, ds, dof);
-  }
-  if constexpr (ENC) {
-    block_sum2(ds, dof);
-    if (threadIdx.x == 0) partial[b] = make_double2(ds, dof);
-  }
-}
-
-__global__ __launch_bounds__(kThreads) void minmax_runs(const float *__restrict__ x,
-                                                        int64_t inner, int64_t splits,
-                                                        int vec4, float2 *__restrict__ partial) {
-  const int64_t b = blockIdx.x;
-  const int64_t run = b / splits, sp = b % splits;
-  const int64_t beg = sp * kChunk;
-  const int64_t end = min(inner, beg + kChunk);
-  const int64_t base = run * inner + beg;
-  float mn = INFINITY, mx = -INFINITY;
-  if (vec4) {
-    const f4 *xv = reinterpret_cast<const f4 *>(x + base);
-    const int nv = static_cast<int>((end - beg) >> 2);
-    f4 v[kVecPerThread];
-#pragma unroll
-    for (int k = 0; k < kVecPerThread; ++k) {
-      const int i = k * kThreads + threadIdx.x;
-      if (i < nv) v[k] = __builtin_nontemporal_load(xv + i);
-    }
-#pragma unroll
-    for (int k = 0; k < kVecPerThread; ++k) {
-      const int i = k * kThreads + threadIdx.x;
-      if (i < nv) {
-        mn = nan_min(nan_min(mn, v[k].x), nan_min(v[k].y, nan_min(v[k].z, v[k].w)));
-        mx = nan_max(nan_max(mx, v[k].x), nan_max(v[k].y, nan_max(v[k].z, v[k].w)));
-      }
-    }
-  } else {
-    const int n = static_cast<int>(end - beg);
-    for (int i = threadIdx.x; i < n; i += kThreads) {
-      mn = nan_min(mn, x[base + i]);
-      mx = nan_max(mx, x[base + i]);
-    }
-  }
-  block_minmax(mn, mx);
-  if (threadIdx.x == 0) partial[b] = make_float2(mn, mx);
-}
-
-// ---------------------------------------------------------------------------------
-// Column decomposition for short runs: matrix [M = outer, K = C * inner]; block b owns
-// columns [tile * 256, +256) of rows [chunk * rows_per_chunk, +rows_per_chunk).
-// ---------------------------------------------------------------------------------
-template <int OP>
-__global__ __launch_bounds__(kThreads) void fwd_elementwise(const float *__restrict__ x,
-                                                            float *__restrict__ y, int64_t n,
-                                                            int64_t C, int64_t inner,
-                                                            const float *__restrict__ scale,
-                                                            const float *__restrict__ offset,
-                                                            float qmin, float qmax) {
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n;
-       i += stride) {
-    const Enc e = load_enc(scale, offset, (i / inner) % C, qmin, qmax);
-    y[i] = fwd_elem<OP>(x[i], e);
-  }
-}
-
-template <int OP, bool ENC>
-__global__ __launch_bounds__(kThreads) void bwd_cols(
-    const float *__restrict__ x, const float *__restrict__ g, float *__restrict__ dx,
-    int64_t M, int64_t K, int64_t inner, int64_t col_tiles, int64_t rows_per_chunk,
-    const float *__restrict__ scale, const float *__restrict__ offset, float qmin,
-    float qmax, double2 *__restrict__ partial) {
-  const int64_t tile = blockIdx.x % col_tiles, chunk = blockIdx.x / col_tiles;
-  const int64_t j = tile * kThreads + threadIdx.x;
-  if (j >= K) return;
-  const Enc e = load_enc(scale, offset, j / inner, qmin, qmax);
-  const int64_t r0 = chunk * rows_per_chunk;
-  const int64_t r1 = min(M, r0 + rows_per_chunk);
-  double ds = 0.0, dof = 0.0;
-  for (int64_t r = r0; r < r1; ++r) {
-    const int64_t i = r * K + j;
-    dx[i] = bwd_elem<OP>(x[i], g[i], e, ds, dof);
-  }
-  if constexpr (ENC) partial[chunk * K + j] = make_double2(ds, dof);
-}
-
-__global__ __launch_bounds__(kThreads) void minmax_cols(const float *__restrict__ x, int64_t M,
-                                                        int64_t K, int64_t col_tiles,
-                                                        int64_t rows_per_chunk,
-                                                        float2 *__restrict__ partial) {
-  const int64_t tile = blockIdx.x % col_tiles, chunk = blockIdx.x / col_tiles;
-  const int64_t j = tile * kThreads + threadIdx.x;
-  if (j >= K) return;
-  const int64_t r0 = chunk * rows_per_chunk;
-  const int64_t r1 = min(M, r0 + rows_per_chunk);
-  float mn = INFINITY, mx = -INFINITY;
-  for (int64_t r = r0; r < r1; ++r) {
-    const float v = x[r * K + j];
-    mn = nan_min(mn, v);
-    mx = nan_max(mx, v);
-  }
-  partial[chunk * K + j] = make_float2(mn, mx);
-}
-
-// ---------------------------------------------------------------------------------
-// Partial folding: one wavefront per encoding c.  Partial p of encoding c lives at
-//   runs:    ((o * C + c) * splits + s)    for o < outer, s < splits
-//   columns: (h * K + c * inner + k)       for h < chunks, k < inner
-// Each lane folds a fixed, strided subset; lanes are then combined by a fixed butterfly.
-// ---------------------------------------------------------------------------------
-struct FoldMap {
-  int64_t a_count, a_stride;  // outer loop (o or h)
-  int64_t b_count, b_stride;  // inner loop (s or k)
-  int64_t c_stride;           // encoding stride
-};
-
 __device__ __forceinline__ int64_t fold_index(const FoldMap &f, int64_t c, int64_t p) {
-  const int64_t a = p / f.b_count, bb = p % f.b_count;
-  return a * f.a_stride + c * f.c_stride + bb * f.b_stride;
+  const int64_t l2 = p % f.n2, t = p / f.n2;
+  const int64_t l1 = t % f.n1, l0 = t / f.n1;
+  return l0 * f.s0 + l1 * f.s1 + l2 * f.s2 + (c / f.C1) * f.sc0 + (c % f.C1) * f.sc1;
 }
 
-// NT threads per encoding (one wave, or four waves for encodings with many partials); the
-// waves' sums are added in a fixed order.
+// Rounding of a folded encoding gradient to the internal type (0: fp32, 1: fp16, 2: bf16),
+// as the reference's gradient tensors carry it.
+__device__ __forceinline__ float round_internal(float v, int round16) {
+  if (round16 == 1) return Io<half_t>::round(v);
+  if (round16 == 2) return Io<bf16_t>::round(v);
+  return v;
+}
+
 template <int NT>
-__global__ __launch_bounds__(NT) void fold_sum(const double2 *__restrict__ partial, FoldMap f,
+__global__ __launch_bounds__(NT) void fold_sum(const Sum2 *__restrict__ partial, FoldMap f,
                                                float *__restrict__ dscale,
-                                               float *__restrict__ doffset) {
+                                               float *__restrict__ doffset, int round16) {
   __shared__ double red[2][NT / kWave];
   const int64_t c = blockIdx.x;
-  const int64_t n = f.a_count * f.b_count;
+  const int64_t n = f.n0 * f.n1 * f.n2;
   double a = 0.0, b = 0.0;
   for (int64_t p = threadIdx.x; p < n; p += NT) {
-    const double2 v = partial[fold_index(f, c, p)];
-    a += v.x;
-    b += v.y;
+    const Sum2 v = partial[fold_index(f, c, p)];
+    a += v.a;
+    b += v.b;
   }
   a = wave_sum(a);
   b = wave_sum(b);
@@ -380,21 +66,21 @@ __global__ __launch_bounds__(NT) void fold_sum(const double2 *__restrict__ parti
       }
   }
   if (threadIdx.x == 0) {
-    if (dscale) dscale[c] = static_cast<float>(a);
-    if (doffset) doffset[c] = static_cast<float>(b);
+    if (dscale) dscale[c] = round_internal(static_cast<float>(a), round16);
+    if (doffset) doffset[c] = round_internal(static_cast<float>(b), round16);
   }
 }
 
-__global__ __launch_bounds__(kWave) void fold_minmax(const float2 *__restrict__ partial, FoldMap f,
-                                                     float *__restrict__ out_min,
+__global__ __launch_bounds__(kWave) void fold_minmax(const MinMax *__restrict__ partial,
+                                                     FoldMap f, float *__restrict__ out_min,
                                                      float *__restrict__ out_max) {
   const int64_t c = blockIdx.x;
-  const int64_t n = f.a_count * f.b_count;
+  const int64_t n = f.n0 * f.n1 * f.n2;
   float mn = INFINITY, mx = -INFINITY;
   for (int64_t p = threadIdx.x; p < n; p += kWave) {
-    const float2 v = partial[fold_index(f, c, p)];
-    mn = nan_min(mn, v.x);
-    mx = nan_max(mx, v.y);
+    const MinMax v = partial[fold_index(f, c, p)];
+    mn = nan_min(mn, v.mn);
+    mx = nan_max(mx, v.mx);
   }
   mn = wave_min(mn);
   mx = wave_max(mx);
@@ -404,114 +90,6 @@ __global__ __launch_bounds__(kWave) void fold_minmax(const float2 *__restrict__ 
   }
 }
 
-// ---------------------------------------------------------------------------------
-// Host-side planning.
-// ---------------------------------------------------------------------------------
-struct Plan {
-  bool cols = false;
-  int64_t outer = 0, C = 0, inner = 0;
-  // runs
-  int64_t runs = 0, splits = 0;
-  // columns
-  int64_t M = 0, K = 0, col_tiles = 0, rows_per_chunk = 0, chunks = 0;
-  int64_t partial_slots = 0;
-  FoldMap fold{};
-};
-
-static Plan make_plan(int64_t outer, int64_t C, int64_t inner) {
-  Plan p;
-  if (C == 1) {  // every element shares the encoding: one long run
-    inner = outer * inner;
-    outer = 1;
-  }
-  p.outer = outer;
-  p.C = C;
-  p.inner = inner;
-  if (C == 1 || inner >= kMinRun) {
-    p.cols = false;
-    p.runs = outer * C;
-    p.splits = (inner + kChunk - 1) / kChunk;
-    p.partial_slots = p.runs * p.splits;
-    p.fold = FoldMap{outer, C * p.splits, p.splits, 1, p.splits};
-  } else {
-    p.cols = true;
-    p.M = outer;
-    p.K = C * inner;
-    p.col_tiles = (p.K + kThreads - 1) / kThreads;
-    int64_t chunks = kColTargetBlocks / p.col_tiles;
-    chunks = chunks < 1 ? 1 : (chunks > p.M ? p.M : chunks);
-    p.rows_per_chunk = (p.M + chunks - 1) / chunks;
-    p.chunks = (p.M + p.rows_per_chunk - 1) / p.rows_per_chunk;
-    p.partial_slots = p.chunks * p.K;
-    p.fold = FoldMap{p.chunks, p.K, inner, 1, inner};
-  }
-  return p;
-}
-
-static bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
-
-static int check_layout(int64_t outer, int64_t C, int64_t inner) {
-  RXMET_CHECK_ARG(outer >= 0 && C >= 1 && inner >= 0, "invalid layout: need outer>=0, C>=1, inner>=0");
-  RXMET_CHECK_ARG(outer <= (int64_t(1) << 40) / (C * (inner > 0 ? inner : 1)),
-                  "tensor too large");
-  return 0;
-}
-
-template <int OP>
-static int launch_forward(const float *x, float *y, int64_t outer, int64_t C, int64_t inner,
-                          const float *scale, const float *offset, float qmin, float qmax,
-                          hipStream_t stream) {
-  const Plan p = make_plan(outer, C, inner);
-  const int64_t n = p.outer * p.C * p.inner;
-  if (n == 0) return 0;
-  rxmet::prof::Scope ps__("qdq_forward_stream", stream);
-  if (!p.cols) {
-    const int vec4 = (p.inner % 4 == 0) && aligned16(x) && aligned16(y);
-    hipLaunchKernelGGL(fwd_runs<OP>, dim3(static_cast<unsigned>(p.runs * p.splits)),
-                       dim3(kThreads), 0, stream, x, y, p.inner, p.C, p.splits, scale, offset,
-                       qmin, qmax, vec4);
-  } else {
-    int64_t blocks = (n + kThreads - 1) / kThreads;
-    if (blocks > 65536) blocks = 65536;
-    hipLaunchKernelGGL(fwd_elementwise<OP>, dim3(static_cast<unsigned>(blocks)), dim3(kThreads),
-                       0, stream, x, y, n, p.C, p.inner, scale, offset, qmin, qmax);
-  }
-  RXMET_CHECK_LAUNCH();
-  return 0;
-}
-
-template <int OP, bool ENC>
-static int launch_backward_impl(const Plan &p, const float *x, const float *g, float *dx,
-                                float *dscale, float *doffset, const float *scale,
-                                const float *offset, float qmin, float qmax, double2 *ws,
-                                hipStream_t stream) {
-  {
-    rxmet::prof::Scope ps__("qdq_backward_stream", stream);
-    if (!p.cols) {
-      const int vec4 = (p.inner % 4 == 0) && aligned16(x) && aligned16(g) && aligned16(dx);
-      hipLaunchKernelGGL((bwd_runs<OP, ENC>), dim3(static_cast<unsigned>(p.runs * p.splits)),
-                         dim3(kThreads), 0, stream, x, g, dx, p.inner, p.C, p.splits, scale,
-                         offset, qmin, qmax, vec4, ws);
-    } else {
-      hipLaunchKernelGGL((bwd_cols<OP, ENC>), dim3(static_cast<unsigned>(p.col_tiles * p.chunks)),
-                         dim3(kThreads), 0, stream, x, g, dx, p.M, p.K, p.inner, p.col_tiles,
-                         p.rows_per_chunk, scale, offset, qmin, qmax, ws);
-    }
-  }
-  RXMET_CHECK_LAUNCH();
-  if constexpr (ENC) {
-    rxmet::prof::Scope ps__("qdq_backward_fold", stream);
-    if (p.fold.a_count * p.fold.b_count >= 1024)
-      hipLaunchKernelGGL(fold_sum<4 * kWave>, dim3(static_cast<unsigned>(p.C)), dim3(4 * kWave), 0,
-                         stream, ws, p.fold, dscale, doffset);
-    else
-      hipLaunchKernelGGL(fold_sum<kWave>, dim3(static_cast<unsigned>(p.C)), dim3(kWave), 0, stream,
-                         ws, p.fold, dscale, doffset);
-    RXMET_CHECK_LAUNCH();
-  }
-  return 0;
-}
-
 __global__ __launch_bounds__(256) void zero_enc_grads(int64_t C, float *dscale, float *doffset) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= C) return;
@@ -519,37 +97,253 @@ __global__ __launch_bounds__(256) void zero_enc_grads(int64_t C, float *dscale, 
   if (doffset) doffset[i] = 0.0f;
 }
 
-template <int OP>
-static int launch_backward(const float *x, const float *g, float *dx, float *dscale,
-                           float *doffset, int64_t outer, int64_t C, int64_t inner,
-                           const float *scale, const float *offset, float qmin, float qmax,
-                           void *workspace, hipStream_t stream) {
-  const Plan p = make_plan(outer, C, inner);
-  const int64_t n = p.outer * p.C * p.inner;
+// ---------------------------------------------------------------------------------
+// Planning.
+// ---------------------------------------------------------------------------------
+
+// Normalize a [outer, C0, mid, C1, inner] layout (one encoding group -> C0 = outer = 1;
+// one encoding -> a single run) and choose the decomposition.
+static Plan make_plan(int64_t outer, int64_t C0, int64_t mid, int64_t C1, int64_t inner,
+                      int esize) {
+  Plan p;
+  p.esize = esize;
+  if (C0 == 1) {
+    mid *= outer;
+    outer = 1;
+  } else if (mid == 1) {  // adjacent groups
+    mid = outer;
+    outer = 1;
+    C1 *= C0;
+    C0 = 1;
+  } else if (C1 == 1) {
+    inner *= mid;
+    mid = outer;
+    outer = 1;
+    C1 = C0;
+    C0 = 1;
+  }
+  if (C0 == 1 && C1 == 1) {  // one encoding: one run
+    inner *= mid;
+    mid = 1;
+  }
+  p.outer = outer;
+  p.C0 = C0;
+  p.mid = mid;
+  p.C1 = C1;
+  p.inner = inner;
+  p.n = outer * C0 * mid * C1 * inner;
+  p.runs = outer * C0 * mid * C1;
+  p.geo = Geo{inner, C1, mid * C1, C0};
+  const int64_t chunk = int64_t(kThreads) * kVecPerThread * (16 / esize);
+  if ((C0 == 1 && C1 == 1) || inner >= kMinRun) {
+    p.kind = KIND_RUNS;
+    p.splits = inner > 0 ? (inner + chunk - 1) / chunk : 1;
+    p.partial_slots = p.runs * p.splits;
+    p.fold = FoldMap{outer, mid, p.splits, C0 * mid * C1 * p.splits, C1 * p.splits, 1,
+                     C1, mid * C1 * p.splits, p.splits};
+  } else if (inner >= kMinSeg) {
+    p.kind = KIND_SEGS;
+    p.splits = 1;
+    p.partial_slots = p.runs;
+    p.fold = FoldMap{outer, mid, 1, C0 * mid * C1, C1, 0, C1, mid * C1, 1};
+  } else {
+    p.kind = KIND_COLS;
+    const int64_t K = C1 * inner;
+    int kt_shift = 0;
+    while (kt_shift < 8 && (int64_t(1) << kt_shift) < K) ++kt_shift;
+    const int64_t kt = int64_t(1) << kt_shift, rows_par = kThreads / kt;
+    const int64_t col_tiles = (K + kt - 1) / kt;
+    const int64_t bands = outer * C0;
+    int64_t chunks = kColTargetBlocks / (bands * col_tiles > 0 ? bands * col_tiles : 1);
+    const int64_t max_chunks = (mid + rows_par - 1) / rows_par;
+    chunks = chunks < 1 ? 1 : (chunks > max_chunks ? max_chunks : chunks);
+    if (chunks < 1) chunks = 1;
+    const int64_t rpc = mid > 0 ? (mid + chunks - 1) / chunks : 1;
+    chunks = mid > 0 ? (mid + rpc - 1) / rpc : 1;
+    p.cg = ColGeo{mid, K, inner, C1, C0, col_tiles, chunks, rpc, kt_shift};
+    p.col_blocks = bands * chunks * col_tiles;
+    p.partial_slots = bands * chunks * K;
+    p.fold = FoldMap{outer, chunks, inner, C0 * chunks * K, K, 1, C1, chunks * K, inner};
+  }
+  return p;
+}
+
+static int check_layout(int64_t outer, int64_t C0, int64_t mid, int64_t C1, int64_t inner) {
+  RXMET_CHECK_ARG(outer >= 0 && mid >= 0 && inner >= 0 && C0 >= 1 && C1 >= 1,
+                  "invalid layout: need outer, mid, inner >= 0 and C0, C1 >= 1");
+  const int64_t lim = int64_t(1) << 40;
+  int64_t n = 1;
+  for (int64_t d : {outer, C0, mid, C1, inner}) {
+    if (d == 0) return 0;
+    RXMET_CHECK_ARG(n <= lim / d, "tensor too large");
+    n *= d;
+  }
+  return 0;
+}
+
+static int esize_of(int32_t io) { return io == RXMET_QDQ_F32 ? 4 : 2; }
+
+static int mantissa_bits(int32_t t) {
+  return t == RXMET_QDQ_F64 ? 53 : t == RXMET_QDQ_F32 ? 24 : t == RXMET_QDQ_F16 ? 11 : 8;
+}
+
+// The grid's end points are exact integers of the type the arithmetic runs in.
+static int check_grid(int64_t qmin, int64_t qmax, int32_t type) {
+  RXMET_CHECK_ARG(qmin <= qmax, "qmin must be <= qmax");
+  const int64_t lim = int64_t(1) << mantissa_bits(type);
+  RXMET_CHECK_ARG(qmin >= -lim && qmax <= lim,
+                  "grid not exactly representable in the arithmetic type (|q| > 2^" +
+                      std::to_string(mantissa_bits(type)) + ")");
+  return 0;
+}
+
+static bool is_io(int32_t t) {
+  return t == RXMET_QDQ_F32 || t == RXMET_QDQ_F16 || t == RXMET_QDQ_BF16;
+}
+
+// Which internal type an op computes in under these numerics.
+static int32_t arithmetic_type(int op, const rxmet_qdq_numerics &nm) {
+  if (op == OP_QDQ_FROZEN) return RXMET_QDQ_F32;
+  if (op == OP_DQ) return nm.io_dtype;
+  return nm.internal_dtype;
+}
+
+static int check_numerics(int op, const rxmet_qdq_numerics &nm) {
+  RXMET_CHECK_ARG(is_io(nm.io_dtype), "io_dtype must be RXMET_QDQ_F32, F16 or BF16");
+  const int32_t r = nm.internal_dtype;
+  RXMET_CHECK_ARG(r == nm.io_dtype || r == RXMET_QDQ_F32 || r == RXMET_QDQ_F64,
+                  "internal_dtype must be io_dtype, RXMET_QDQ_F32 or RXMET_QDQ_F64");
+  RXMET_CHECK_ARG(nm.reserved == 0, "rxmet_qdq_numerics.reserved must be 0");
+  RXMET_CHECK_ARG(nm.zero_point_shift == nm.zero_point_shift &&
+                      nm.zero_point_shift > -1e30 && nm.zero_point_shift < 1e30,
+                  "zero_point_shift must be finite");
+  if (op != OP_QDQ_LEARN)
+    RXMET_CHECK_ARG(nm.zero_point_shift == 0.0,
+                    "zero_point_shift applies to learnable-mode quantize_dequantize only");
+  if (op == OP_DQ)
+    RXMET_CHECK_ARG(r == nm.io_dtype, "dequantize computes in the tensor's own type");
+  return 0;
+}
+
+static Params make_params(int64_t qmin, int64_t qmax, const rxmet_qdq_numerics &nm) {
+  return Params{static_cast<double>(qmin), static_cast<double>(qmax),
+                static_cast<float>(nm.zero_point_shift), nm.scalar_scale ? 1 : 0};
+}
+
+static int dispatch(const Call &c, int32_t io, int what) {
+  int rc = -22;
+  if (io == RXMET_QDQ_F32) rc = run_f32(c, what);
+  else if (io == RXMET_QDQ_F16) rc = run_f16(c, what);
+  else if (io == RXMET_QDQ_BF16) rc = run_bf16(c, what);
+  if (rc != 0) {
+    set_error("qdq: no kernel for this op / io type / internal type combination");
+    return rc;
+  }
+  RXMET_CHECK_LAUNCH();
+  return 0;
+}
+
+static int forward_impl(int op, const void *x, void *y, const rxmet_qdq_layout *l,
+                        const rxmet_qdq_numerics *nm, const float *scale, const float *offset,
+                        int64_t qmin, int64_t qmax, void *stream) {
+  RXMET_CHECK_ARG(l != nullptr && nm != nullptr, "layout and numerics must be non-null");
+  if (int rc = check_layout(l->outer, l->C0, l->mid, l->C1, l->inner)) return rc;
+  if (int rc = check_numerics(op, *nm)) return rc;
+  if (op != OP_DQ)
+    if (int rc = check_grid(qmin, qmax, arithmetic_type(op, *nm))) return rc;
+  RXMET_CHECK_ARG(scale != nullptr, "scale must be non-null");
+  const Plan p = make_plan(l->outer, l->C0, l->mid, l->C1, l->inner, esize_of(nm->io_dtype));
+  if (p.n == 0) return 0;
+  RXMET_CHECK_ARG(x != nullptr && y != nullptr, "input/output must be non-null");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const Call c{&p, op, nm->internal_dtype, x, nullptr, y, scale, offset,
+               make_params(qmin, qmax, *nm), nullptr, s};
+  rxmet::prof::Scope ps__("qdq_forward_stream", s);
+  return dispatch(c, nm->io_dtype, WHAT_FORWARD);
+}
+
+static int backward_impl(int op, const void *x, const void *g, void *dx, float *dscale,
+                         float *doffset, const rxmet_qdq_layout *l, const rxmet_qdq_numerics *nm,
+                         const float *scale, const float *offset, int64_t qmin, int64_t qmax,
+                         void *workspace, void *stream) {
+  RXMET_CHECK_ARG(l != nullptr && nm != nullptr, "layout and numerics must be non-null");
+  if (int rc = check_layout(l->outer, l->C0, l->mid, l->C1, l->inner)) return rc;
+  if (int rc = check_numerics(op, *nm)) return rc;
+  if (op != OP_DQ)
+    if (int rc = check_grid(qmin, qmax, arithmetic_type(op, *nm))) return rc;
+  RXMET_CHECK_ARG(scale != nullptr, "scale must be non-null");
+  if (op == OP_QDQ_FROZEN)
+    RXMET_CHECK_ARG(dscale == nullptr && doffset == nullptr,
+                    "frozen encodings have no encoding gradients");
+  const Plan p = make_plan(l->outer, l->C0, l->mid, l->C1, l->inner, esize_of(nm->io_dtype));
   const bool enc = dscale != nullptr || doffset != nullptr;
-  if (n == 0) {
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t C = l->C0 * l->C1;
+  if (p.n == 0) {
     // zeroed by a kernel, not a memset node, so a captured training step replays correctly
-    if (enc && C > 0) {
-      hipLaunchKernelGGL(zero_enc_grads, dim3(static_cast<unsigned>((C + 255) / 256)), dim3(256), 0,
-                         stream, C, dscale, doffset);
+    if (enc) {
+      hipLaunchKernelGGL(zero_enc_grads, dim3(static_cast<unsigned>((C + 255) / 256)), dim3(256),
+                         0, s, C, dscale, doffset);
       RXMET_CHECK_LAUNCH();
     }
     return 0;
   }
-  if (enc) {
-    RXMET_CHECK_ARG(workspace != nullptr, "encoding gradients need a workspace");
-    return launch_backward_impl<OP, true>(p, x, g, dx, dscale, doffset, scale, offset, qmin,
-                                          qmax, static_cast<double2 *>(workspace), stream);
+  RXMET_CHECK_ARG(x != nullptr && g != nullptr && dx != nullptr, "x, g and dx must be non-null");
+  if (enc) RXMET_CHECK_ARG(workspace != nullptr, "encoding gradients need a workspace");
+  const Call c{&p, op, nm->internal_dtype, x, g, dx, scale, offset,
+               make_params(qmin, qmax, *nm), enc ? workspace : nullptr, s};
+  {
+    rxmet::prof::Scope ps__("qdq_backward_stream", s);
+    if (int rc = dispatch(c, nm->io_dtype, WHAT_BACKWARD)) return rc;
   }
-  return launch_backward_impl<OP, false>(p, x, g, dx, nullptr, nullptr, scale, offset, qmin,
-                                         qmax, nullptr, stream);
+  if (enc) {
+    const int32_t r = arithmetic_type(op, *nm);
+    const int round16 = r == RXMET_QDQ_F16 ? 1 : (r == RXMET_QDQ_BF16 ? 2 : 0);
+    rxmet::prof::Scope ps__("qdq_backward_fold", s);
+    const Sum2 *ws = static_cast<const Sum2 *>(workspace);
+    if (p.fold.n0 * p.fold.n1 * p.fold.n2 >= 1024)
+      hipLaunchKernelGGL(fold_sum<4 * kWave>, dim3(static_cast<unsigned>(C)), dim3(4 * kWave), 0,
+                         s, ws, p.fold, dscale, doffset, round16);
+    else
+      hipLaunchKernelGGL(fold_sum<kWave>, dim3(static_cast<unsigned>(C)), dim3(kWave), 0, s, ws,
+                         p.fold, dscale, doffset, round16);
+    RXMET_CHECK_LAUNCH();
+  }
+  return 0;
 }
 
-static int check_grid(int64_t qmin, int64_t qmax) {
-  RXMET_CHECK_ARG(qmin <= qmax, "qmin must be <= qmax");
-  RXMET_CHECK_ARG(qmin >= -(int64_t(1) << 24) && qmax <= (int64_t(1) << 24),
-                  "grid not exactly representable in fp32 (|q| > 2^24)");
+static int minmax_impl(const void *x, int32_t io, const rxmet_qdq_layout *l, float *out_min,
+                       float *out_max, void *workspace, void *stream) {
+  RXMET_CHECK_ARG(l != nullptr, "layout must be non-null");
+  if (int rc = check_layout(l->outer, l->C0, l->mid, l->C1, l->inner)) return rc;
+  RXMET_CHECK_ARG(is_io(io), "io_dtype must be RXMET_QDQ_F32, F16 or BF16");
+  RXMET_CHECK_ARG(out_min && out_max, "out_min/out_max must be non-null");
+  const Plan p = make_plan(l->outer, l->C0, l->mid, l->C1, l->inner, esize_of(io));
+  RXMET_CHECK_ARG(p.n > 0, "min/max of an empty tensor");
+  RXMET_CHECK_ARG(x != nullptr, "x must be non-null");
+  RXMET_CHECK_ARG(workspace != nullptr, "min/max needs a workspace");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  rxmet::prof::Scope ps__("qdq_minmax", s);
+  rxmet_qdq_numerics nm{io, io, 0.0, 0, 0};
+  const Call c{&p, OP_QDQ_LEARN, nm.internal_dtype, x, nullptr, nullptr, nullptr, nullptr,
+               make_params(0, 0, nm), workspace, s};
+  if (int rc = dispatch(c, io, WHAT_MINMAX)) return rc;
+  hipLaunchKernelGGL(fold_minmax, dim3(static_cast<unsigned>(l->C0 * l->C1)), dim3(kWave), 0, s,
+                     static_cast<const MinMax *>(workspace), p.fold, out_min, out_max);
+  RXMET_CHECK_LAUNCH();
   return 0;
+}
+
+// The three-argument fp32 layout [outer, C, inner] of the original entry points.
+static rxmet_qdq_layout layout3(int64_t outer, int64_t C, int64_t inner) {
+  return rxmet_qdq_layout{1, 1, outer, C, inner};
+}
+static const rxmet_qdq_numerics kF32{RXMET_QDQ_F32, RXMET_QDQ_F32, 0.0, 0, 0};
+
+static int check_layout3(int64_t outer, int64_t C, int64_t inner) {
+  RXMET_CHECK_ARG(outer >= 0 && C >= 1 && inner >= 0,
+                  "invalid layout: need outer>=0, C>=1, inner>=0");
+  return check_layout(1, 1, outer, C, inner);
 }
 
 // Encodings of learnable min / max, one thread per encoding (see rxmet_qdq_encoding_forward).
@@ -601,15 +395,6 @@ __global__ __launch_bounds__(256) void encoding_bwd(int64_t n, const float *__re
   d_min[c] = gmin - gr2;
 }
 
-}  // namespace qdq
-}  // namespace rxmet
-
-using namespace rxmet;
-using namespace rxmet::qdq;
-
-namespace rxmet {
-namespace qdq {
-
 // Scratch of rxmet_qdq_backward_noalloc: the per-block partial sums of the encoding
 // gradients, in a file-scope device array instead of a caller workspace.  Each device holds
 // its own copy for the life of the process.  Every slot a call uses is written by its block
@@ -638,58 +423,63 @@ static int scratch_address(void **out) {
   return 0;
 }
 
+
 }  // namespace qdq
 }  // namespace rxmet
+
+using namespace rxmet;
+using namespace rxmet::qdq;
 
 extern "C" {
 
 int64_t rxmet_qdq_workspace_bytes(int64_t outer, int64_t C, int64_t inner) {
-  if (outer < 0 || C < 1 || inner < 0) return 0;
-  const Plan p = make_plan(outer, C, inner);
-  return p.partial_slots * static_cast<int64_t>(sizeof(double2));
+  const rxmet_qdq_layout l = layout3(outer, C, inner);
+  return rxmet_qdq_workspace_bytes_ex(&l, RXMET_QDQ_F32);
+}
+
+int64_t rxmet_qdq_workspace_bytes_ex(const rxmet_qdq_layout *l, int32_t io_dtype) {
+  if (l == nullptr || !is_io(io_dtype) || l->outer < 0 || l->mid < 0 || l->inner < 0 ||
+      l->C0 < 1 || l->C1 < 1)
+    return 0;
+  const Plan p = make_plan(l->outer, l->C0, l->mid, l->C1, l->inner, esize_of(io_dtype));
+  return p.partial_slots * static_cast<int64_t>(sizeof(Sum2));
 }
 
 int rxmet_qdq_minmax(const float *x, int64_t outer, int64_t C, int64_t inner, float *out_min,
-                     float *out_max, void *workspace, void *stream_) {
+                     float *out_max, void *workspace, void *stream) {
   clear_error();
-  if (int rc = check_layout(outer, C, inner)) return rc;
-  RXMET_CHECK_ARG(out_min && out_max, "out_min/out_max must be non-null");
-  const Plan p = make_plan(outer, C, inner);
-  RXMET_CHECK_ARG(p.outer * p.C * p.inner > 0, "min/max of an empty tensor");
-  RXMET_CHECK_ARG(workspace != nullptr, "min/max needs a workspace");
-  hipStream_t stream = static_cast<hipStream_t>(stream_);
-  float2 *ws = static_cast<float2 *>(workspace);
-  rxmet::prof::Scope ps__("qdq_minmax", stream);
-  if (!p.cols) {
-    const int vec4 = (p.inner % 4 == 0) && aligned16(x);
-    hipLaunchKernelGGL(minmax_runs, dim3(static_cast<unsigned>(p.runs * p.splits)), dim3(kThreads),
-                       0, stream, x, p.inner, p.splits, vec4, ws);
-  } else {
-    hipLaunchKernelGGL(minmax_cols, dim3(static_cast<unsigned>(p.col_tiles * p.chunks)),
-                       dim3(kThreads), 0, stream, x, p.M, p.K, p.col_tiles, p.rows_per_chunk, ws);
-  }
-  RXMET_CHECK_LAUNCH();
-  hipLaunchKernelGGL(fold_minmax, dim3(static_cast<unsigned>(p.C)), dim3(kWave), 0, stream, ws,
-                     p.fold, out_min, out_max);
-  RXMET_CHECK_LAUNCH();
-  return 0;
+  if (int rc = check_layout3(outer, C, inner)) return rc;
+  const rxmet_qdq_layout l = layout3(outer, C, inner);
+  return minmax_impl(x, RXMET_QDQ_F32, &l, out_min, out_max, workspace, stream);
+}
+
+int rxmet_qdq_minmax_ex(const void *x, int32_t io_dtype, const rxmet_qdq_layout *layout,
+                        float *out_min, float *out_max, void *workspace, void *stream) {
+  clear_error();
+  return minmax_impl(x, io_dtype, layout, out_min, out_max, workspace, stream);
+}
+
+static int qdq_op(int mode) {
+  return mode == RXMET_QDQ_LEARNABLE ? OP_QDQ_LEARN : (mode == RXMET_QDQ_FROZEN ? OP_QDQ_FROZEN : -1);
 }
 
 int rxmet_qdq_forward(const float *x, float *y, int64_t outer, int64_t C, int64_t inner,
                       const float *scale, const float *offset, int64_t qmin, int64_t qmax,
                       int mode, void *stream) {
   clear_error();
-  if (int rc = check_layout(outer, C, inner)) return rc;
-  if (int rc = check_grid(qmin, qmax)) return rc;
-  RXMET_CHECK_ARG(scale != nullptr, "scale must be non-null");
-  const float lo = static_cast<float>(qmin), hi = static_cast<float>(qmax);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  if (mode == RXMET_QDQ_LEARNABLE)
-    return launch_forward<OP_QDQ_LEARN>(x, y, outer, C, inner, scale, offset, lo, hi, s);
-  if (mode == RXMET_QDQ_FROZEN)
-    return launch_forward<OP_QDQ_FROZEN>(x, y, outer, C, inner, scale, offset, lo, hi, s);
-  set_error("unknown qdq mode");
-  return -22;
+  if (int rc = check_layout3(outer, C, inner)) return rc;
+  const rxmet_qdq_layout l = layout3(outer, C, inner);
+  return rxmet_qdq_forward_ex(x, y, &l, &kF32, scale, offset, qmin, qmax, mode, stream);
+}
+
+int rxmet_qdq_forward_ex(const void *x, void *y, const rxmet_qdq_layout *layout,
+                         const rxmet_qdq_numerics *numerics, const float *scale,
+                         const float *offset, int64_t qmin, int64_t qmax, int mode,
+                         void *stream) {
+  clear_error();
+  const int op = qdq_op(mode);
+  RXMET_CHECK_ARG(op >= 0, "unknown qdq mode");
+  return forward_impl(op, x, y, layout, numerics, scale, offset, qmin, qmax, stream);
 }
 
 int rxmet_qdq_backward(const float *x, const float *g, float *dx, float *dscale, float *doffset,
@@ -697,22 +487,21 @@ int rxmet_qdq_backward(const float *x, const float *g, float *dx, float *dscale,
                        const float *offset, int64_t qmin, int64_t qmax, int mode,
                        void *workspace, void *stream) {
   clear_error();
-  if (int rc = check_layout(outer, C, inner)) return rc;
-  if (int rc = check_grid(qmin, qmax)) return rc;
-  RXMET_CHECK_ARG(scale != nullptr, "scale must be non-null");
-  const float lo = static_cast<float>(qmin), hi = static_cast<float>(qmax);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  if (mode == RXMET_QDQ_LEARNABLE)
-    return launch_backward<OP_QDQ_LEARN>(x, g, dx, dscale, doffset, outer, C, inner, scale,
-                                         offset, lo, hi, workspace, s);
-  if (mode == RXMET_QDQ_FROZEN) {
-    RXMET_CHECK_ARG(dscale == nullptr && doffset == nullptr,
-                    "frozen encodings have no encoding gradients");
-    return launch_backward<OP_QDQ_FROZEN>(x, g, dx, nullptr, nullptr, outer, C, inner, scale,
-                                          offset, lo, hi, workspace, s);
-  }
-  set_error("unknown qdq mode");
-  return -22;
+  if (int rc = check_layout3(outer, C, inner)) return rc;
+  const rxmet_qdq_layout l = layout3(outer, C, inner);
+  return rxmet_qdq_backward_ex(x, g, dx, dscale, doffset, &l, &kF32, scale, offset, qmin, qmax,
+                               mode, workspace, stream);
+}
+
+int rxmet_qdq_backward_ex(const void *x, const void *g, void *dx, float *dscale, float *doffset,
+                          const rxmet_qdq_layout *layout, const rxmet_qdq_numerics *numerics,
+                          const float *scale, const float *offset, int64_t qmin, int64_t qmax,
+                          int mode, void *workspace, void *stream) {
+  clear_error();
+  const int op = qdq_op(mode);
+  RXMET_CHECK_ARG(op >= 0, "unknown qdq mode");
+  return backward_impl(op, x, g, dx, dscale, doffset, layout, numerics, scale, offset, qmin,
+                       qmax, workspace, stream);
 }
 
 int rxmet_qdq_backward_noalloc(const float *x, const float *g, float *dx, float *dscale,
@@ -720,8 +509,8 @@ int rxmet_qdq_backward_noalloc(const float *x, const float *g, float *dx, float 
                                const float *scale, const float *offset, int64_t qmin,
                                int64_t qmax, int mode, void *stream) {
   clear_error();
-  if (int rc = check_layout(outer, C, inner)) return rc;
-  if (int rc = check_grid(qmin, qmax)) return rc;
+  if (int rc = check_layout3(outer, C, inner)) return rc;
+  if (int rc = check_grid(qmin, qmax, RXMET_QDQ_F32)) return rc;
   RXMET_CHECK_ARG(scale != nullptr, "scale must be non-null");
   RXMET_CHECK_ARG(mode == RXMET_QDQ_LEARNABLE || mode == RXMET_QDQ_FROZEN, "unknown qdq mode");
   void *ws = nullptr;
@@ -744,11 +533,16 @@ int rxmet_quantize_forward(const float *x, float *q, int64_t outer, int64_t C, i
                            const float *scale, const float *offset, int64_t qmin, int64_t qmax,
                            void *stream) {
   clear_error();
-  if (int rc = check_layout(outer, C, inner)) return rc;
-  if (int rc = check_grid(qmin, qmax)) return rc;
-  RXMET_CHECK_ARG(scale != nullptr, "scale must be non-null");
-  return launch_forward<OP_Q>(x, q, outer, C, inner, scale, offset, static_cast<float>(qmin),
-                              static_cast<float>(qmax), static_cast<hipStream_t>(stream));
+  if (int rc = check_layout3(outer, C, inner)) return rc;
+  const rxmet_qdq_layout l = layout3(outer, C, inner);
+  return forward_impl(OP_Q, x, q, &l, &kF32, scale, offset, qmin, qmax, stream);
+}
+
+int rxmet_quantize_forward_ex(const void *x, void *q, const rxmet_qdq_layout *layout,
+                              const rxmet_qdq_numerics *numerics, const float *scale,
+                              const float *offset, int64_t qmin, int64_t qmax, void *stream) {
+  clear_error();
+  return forward_impl(OP_Q, x, q, layout, numerics, scale, offset, qmin, qmax, stream);
 }
 
 int rxmet_quantize_backward(const float *x, const float *g, float *dx, float *dscale,
@@ -756,21 +550,35 @@ int rxmet_quantize_backward(const float *x, const float *g, float *dx, float *ds
                             const float *scale, const float *offset, int64_t qmin, int64_t qmax,
                             void *workspace, void *stream) {
   clear_error();
-  if (int rc = check_layout(outer, C, inner)) return rc;
-  if (int rc = check_grid(qmin, qmax)) return rc;
-  RXMET_CHECK_ARG(scale != nullptr, "scale must be non-null");
-  return launch_backward<OP_Q>(x, g, dx, dscale, doffset, outer, C, inner, scale, offset,
-                               static_cast<float>(qmin), static_cast<float>(qmax), workspace,
-                               static_cast<hipStream_t>(stream));
+  if (int rc = check_layout3(outer, C, inner)) return rc;
+  const rxmet_qdq_layout l = layout3(outer, C, inner);
+  return backward_impl(OP_Q, x, g, dx, dscale, doffset, &l, &kF32, scale, offset, qmin, qmax,
+                       workspace, stream);
+}
+
+int rxmet_quantize_backward_ex(const void *x, const void *g, void *dx, float *dscale,
+                               float *doffset, const rxmet_qdq_layout *layout,
+                               const rxmet_qdq_numerics *numerics, const float *scale,
+                               const float *offset, int64_t qmin, int64_t qmax,
+                               void *workspace, void *stream) {
+  clear_error();
+  return backward_impl(OP_Q, x, g, dx, dscale, doffset, layout, numerics, scale, offset, qmin,
+                       qmax, workspace, stream);
 }
 
 int rxmet_dequantize_forward(const float *q, float *y, int64_t outer, int64_t C, int64_t inner,
                              const float *scale, const float *offset, void *stream) {
   clear_error();
-  if (int rc = check_layout(outer, C, inner)) return rc;
-  RXMET_CHECK_ARG(scale != nullptr, "scale must be non-null");
-  return launch_forward<OP_DQ>(q, y, outer, C, inner, scale, offset, 0.f, 0.f,
-                               static_cast<hipStream_t>(stream));
+  if (int rc = check_layout3(outer, C, inner)) return rc;
+  const rxmet_qdq_layout l = layout3(outer, C, inner);
+  return forward_impl(OP_DQ, q, y, &l, &kF32, scale, offset, 0, 0, stream);
+}
+
+int rxmet_dequantize_forward_ex(const void *q, void *y, const rxmet_qdq_layout *layout,
+                                const rxmet_qdq_numerics *numerics, const float *scale,
+                                const float *offset, void *stream) {
+  clear_error();
+  return forward_impl(OP_DQ, q, y, layout, numerics, scale, offset, 0, 0, stream);
 }
 
 int rxmet_dequantize_backward(const float *q, const float *g, float *dq, float *dscale,
@@ -778,10 +586,19 @@ int rxmet_dequantize_backward(const float *q, const float *g, float *dq, float *
                               const float *scale, const float *offset, void *workspace,
                               void *stream) {
   clear_error();
-  if (int rc = check_layout(outer, C, inner)) return rc;
-  RXMET_CHECK_ARG(scale != nullptr, "scale must be non-null");
-  return launch_backward<OP_DQ>(q, g, dq, dscale, doffset, outer, C, inner, scale, offset, 0.f,
-                                0.f, workspace, static_cast<hipStream_t>(stream));
+  if (int rc = check_layout3(outer, C, inner)) return rc;
+  const rxmet_qdq_layout l = layout3(outer, C, inner);
+  return backward_impl(OP_DQ, q, g, dq, dscale, doffset, &l, &kF32, scale, offset, 0, 0,
+                       workspace, stream);
+}
+
+int rxmet_dequantize_backward_ex(const void *q, const void *g, void *dq, float *dscale,
+                                 float *doffset, const rxmet_qdq_layout *layout,
+                                 const rxmet_qdq_numerics *numerics, const float *scale,
+                                 const float *offset, void *workspace, void *stream) {
+  clear_error();
+  return backward_impl(OP_DQ, q, g, dq, dscale, doffset, layout, numerics, scale, offset, 0, 0,
+                       workspace, stream);
 }
 
 int rxmet_qdq_encoding_forward(const float *mn, const float *mx, int64_t n, int64_t qmin,
@@ -789,7 +606,7 @@ int rxmet_qdq_encoding_forward(const float *mn, const float *mx, int64_t n, int6
                                float min_scale, float *scale, float *offset, void *stream) {
   clear_error();
   RXMET_CHECK_ARG(n >= 1 && mn && mx && scale && offset, "bad encoding arguments");
-  if (int rc = check_grid(qmin, qmax)) return rc;
+  if (int rc = check_grid(qmin, qmax, RXMET_QDQ_F32)) return rc;
   hipLaunchKernelGGL(encoding_fwd, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), n, mn, mx,
                      1.0f / static_cast<float>(qmax - qmin), static_cast<float>(qmin),
@@ -805,7 +622,7 @@ int rxmet_qdq_encoding_backward(const float *mn, const float *mx, const float *g
                                 void *stream) {
   clear_error();
   RXMET_CHECK_ARG(n >= 1 && mn && mx && d_min && d_max, "bad encoding arguments");
-  if (int rc = check_grid(qmin, qmax)) return rc;
+  if (int rc = check_grid(qmin, qmax, RXMET_QDQ_F32)) return rc;
   hipLaunchKernelGGL(encoding_bwd, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), n, mn, mx, g_scale, g_offset,
                      1.0f / static_cast<float>(qmax - qmin), static_cast<float>(qmin),

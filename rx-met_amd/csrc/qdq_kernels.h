@@ -1,0 +1,691 @@
+// qdq_kernels.h — streaming fake-quantization kernels (MI355X, gfx950), shared by the
+// per-element-type translation units qdq_f32.hip / qdq_f16.hip / qdq_bf16.hip.
+//
+// Element types.  Tensors hold fp32, fp16 or bf16 elements ("io" type T).  The arithmetic
+// of the reference runs in an "internal" type R chosen by its numerical-stability rule
+// (torch_builtins.py:85-101, 255-262): R = T for small grids, else fp32, else fp64.  Here
+// every element is widened to fp32 (fp64 when R is fp64), each operation is evaluated
+// there and its result rounded back to R, which is what PyTorch's 16-bit elementwise
+// kernels do (fp32 "opmath", one rounding to the storage type per operation; for +, -, *, /
+// of fp16/bf16 operands the fp32 result rounded once more is the correctly rounded
+// 16-bit result, because fp32 carries more than 2p+2 bits).
+//
+// Work decompositions of a [outer, C0, mid, C1, inner] tensor whose element
+// (o, c0, m, c1, k) uses encoding c0 * C1 + c1 (a "run" is one contiguous stretch of
+// `inner` elements sharing an encoding):
+//   runs : long runs (>= 1024 elements) or one encoding — each workgroup streams one
+//          chunk of one run with 16-byte accesses and one scalar encoding load.
+//   segs : medium runs (16..1023 elements, e.g. block quantization) — a power-of-two
+//          segment of lanes per run, several runs per workgroup, one partial per run
+//          reduced with lane shuffles inside the segment.
+//   cols : short runs (< 16 elements, e.g. per-channel on the last axis) — the tensor is
+//          outer*C0 bands of a [mid, C1*inner] matrix; threads own columns and walk the
+//          rows of one band, several rows in parallel when the matrix is narrow.
+// Reductions write one fp64 (or min/max) partial per workgroup, run or column chunk; a
+// second kernel folds the partials of each encoding in a fixed order, so results are
+// deterministic and need no atomics.
+#pragma once
+
+#include <stdint.h>
+
+#include <type_traits>
+
+#include "rxmet_common.h"
+#include "rxmet_qdq.h"
+
+namespace rxmet {
+namespace qdq {
+
+enum Op { OP_QDQ_LEARN = 0, OP_QDQ_FROZEN = 1, OP_Q = 2, OP_DQ = 3 };
+
+constexpr int kThreads = 256;
+constexpr int kVecPerThread = 8;   // 16-byte vectors per thread per chunk (runs)
+constexpr int64_t kMinRun = 1024;  // runs at least this long use the runs decomposition
+constexpr int64_t kMinSeg = 16;    // shorter runs use the column decomposition
+constexpr int kColTargetBlocks = 2048;
+
+typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------------
+// Element types and rounding.
+// ---------------------------------------------------------------------------------
+struct half_t {
+  uint16_t b;
+};
+struct bf16_t {
+  uint16_t b;
+};
+
+__device__ __forceinline__ float f16_to_f(uint32_t b) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(b)));
+}
+__device__ __forceinline__ uint32_t f_to_f16(float v) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));  // round to nearest even
+}
+__device__ __forceinline__ float bf16_to_f(uint32_t b) {
+  return __builtin_bit_cast(float, (b & 0xFFFFu) << 16);
+}
+// Round to nearest even on the bit pattern; NaN becomes the quiet NaN 0x7FC0, as torch's
+// BFloat16 conversion does.
+__device__ __forceinline__ uint32_t f_to_bf16(float v) {
+  if (v != v) return 0x7FC0u;
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+// Loads, stores and 16-byte (un)packing of the io type, all through fp32 values.
+template <typename T>
+struct Io;
+
+template <>
+struct Io<float> {
+  static constexpr int E = 4;  // elements per 16-byte vector
+  __device__ static float ld(const float *p, int64_t i) { return p[i]; }
+  __device__ static void st(float *p, int64_t i, float v) { p[i] = v; }
+  __device__ static void unpack(const u4 &v, float (&a)[E]) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      // copy the element out first: __builtin_bit_cast of an ext-vector element lvalue
+      // reads element 0
+      const unsigned w = v[k];
+      a[k] = __builtin_bit_cast(float, w);
+    }
+  }
+  __device__ static u4 pack(const float (&a)[E]) {
+    u4 v;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v[k] = __builtin_bit_cast(unsigned, a[k]);
+    return v;
+  }
+  __device__ static float round(float v) { return v; }
+};
+
+// 16-bit io types: BF selects bf16 (else fp16).
+template <typename Tag, bool BF>
+struct Io16 {
+  static constexpr int E = 8;
+  __device__ static float to_f(uint32_t b) { return BF ? bf16_to_f(b) : f16_to_f(b); }
+  __device__ static uint32_t from_f(float v) { return BF ? f_to_bf16(v) : f_to_f16(v); }
+  __device__ static float ld(const Tag *p, int64_t i) { return to_f(p[i].b); }
+  __device__ static void st(Tag *p, int64_t i, float v) {
+    Tag t;
+    t.b = static_cast<uint16_t>(from_f(v));
+    p[i] = t;
+  }
+  __device__ static void unpack(const u4 &v, float (&a)[E]) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      a[2 * k] = to_f(v[k] & 0xFFFFu);
+      a[2 * k + 1] = to_f(v[k] >> 16);
+    }
+  }
+  __device__ static u4 pack(const float (&a)[E]) {
+    u4 v;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v[k] = from_f(a[2 * k]) | (from_f(a[2 * k + 1]) << 16);
+    return v;
+  }
+  __device__ static float round(float v) { return to_f(from_f(v)); }
+};
+
+template <>
+struct Io<half_t> : Io16<half_t, false> {};
+template <>
+struct Io<bf16_t> : Io16<bf16_t, true> {};
+
+// Rounding of an intermediate result to the internal type R, in R's compute type A.
+template <typename R>
+struct Rnd {
+  using A = float;
+  __device__ static float r(float v) { return Io<R>::round(v); }
+};
+template <>
+struct Rnd<double> {
+  using A = double;
+  __device__ static double r(double v) { return v; }
+};
+
+__device__ __forceinline__ float rint_a(float v) { return rintf(v); }
+__device__ __forceinline__ double rint_a(double v) { return rint(v); }
+__device__ __forceinline__ float fma_a(float a, float b, float c) { return fmaf(a, b, c); }
+__device__ __forceinline__ double fma_a(double a, double b, double c) { return fma(a, b, c); }
+template <typename A>
+__device__ __forceinline__ A clamp_a(A v, A lo, A hi) {
+  return v < lo ? lo : (v > hi ? hi : v);  // NaN falls through (torch.clamp)
+}
+
+// Per-launch scalars.
+struct Params {
+  double qmin, qmax;   // grid (exact in R)
+  float alpha;         // zero_point_shift (0: none)
+  int scalar_scale;    // the scale is a 0-dim tensor (see rxmet_qdq_numerics)
+};
+
+// One encoding as the element functions use it.
+template <typename T, typename R>
+struct Elem {
+  using A = typename Rnd<R>::A;
+  struct Enc {
+    A s, o, qmin, qmax, lo, hi;  // internal-type values (lo/hi: o + qmin, o + qmax)
+    float fs, inv_s, zp, s_io;   // fp32 forms (frozen path) and the scale rounded to T
+  };
+
+  __device__ static A r(A v) { return Rnd<R>::r(v); }
+
+  __device__ static Enc enc(const float *scale, const float *offset, int64_t c,
+                            const Params &p) {
+    Enc e;
+    const float s = scale[c];
+    const float o = offset ? offset[c] : 0.0f;
+    e.s = A(s);
+    e.o = A(o);
+    e.qmin = A(p.qmin);
+    e.qmax = A(p.qmax);
+    e.lo = r(e.o + e.qmin);
+    e.hi = r(e.o + e.qmax);
+    e.fs = s;
+    e.inv_s = 1.0f / s;  // torch's fake_quantize kernels multiply by fp32 1/scale
+    e.zp = -truncf(o);   // zero point = -offset.to(int32)
+    e.s_io = Io<T>::round(s);
+    return e;
+  }
+
+  // The tensor QuantDequantFunc receives: x, or torch.sub(x, scale, alpha=shift).  With a
+  // 0-dim scale and R wider than T, type promotion keeps that subtraction in T (the scale
+  // is rounded to T first); otherwise it runs in R.
+  __device__ static A shifted(float x, const Enc &e, const Params &p) {
+    if (p.alpha == 0.0f) return A(x);
+    if (p.scalar_scale) return A(Io<T>::round(fmaf(-p.alpha, e.s_io, x)));
+    return r(fma_a(A(-p.alpha), e.s, A(x)));
+  }
+
+  // QuantDequantFunc.forward: (clamp(rint(v / s) - o) + o) * s, each step rounded to R.
+  __device__ static A qdq(A v, const Enc &e) {
+    const A t = r(v / e.s);
+    const A q = r(rint_a(t) - e.o);
+    return r(r(clamp_a(q, e.qmin, e.qmax) + e.o) * e.s);
+  }
+
+  // torch.add(qdq, scale, alpha=shift) in R.
+  __device__ static A unshift(A y, const Enc &e, const Params &p) {
+    return p.alpha == 0.0f ? y : r(fma_a(A(p.alpha), e.s, y));
+  }
+};
+
+// Forward value of one element (as fp32; the store rounds it to T).
+template <int OP, typename T, typename R>
+__device__ __forceinline__ float fwd_elem(float x, const typename Elem<T, R>::Enc &e,
+                                          const Params &p) {
+  using El = Elem<T, R>;
+  using A = typename El::A;
+  if constexpr (OP == OP_QDQ_LEARN) {
+    return static_cast<float>(El::unshift(El::qdq(El::shifted(x, e, p), e), e, p));
+  } else if constexpr (OP == OP_QDQ_FROZEN) {
+    const float q = rintf(x * e.inv_s) + e.zp;
+    return (clamp_keep_nan(q, static_cast<float>(p.qmin), static_cast<float>(p.qmax)) - e.zp) *
+           e.fs;
+  } else if constexpr (OP == OP_Q) {
+    const A t = El::r(A(x) / e.s);
+    return static_cast<float>(clamp_a(El::r(rint_a(t) - e.o), e.qmin, e.qmax));
+  } else {
+    return static_cast<float>(El::r(El::r(A(x) + e.o) * e.s));
+  }
+}
+
+// One element of the backward: returns dx and adds this element's encoding-gradient terms
+// (as the reference rounds them, in R) to (ds, dof).
+template <int OP, typename T, typename R>
+__device__ __forceinline__ float bwd_elem(float x, float g, const typename Elem<T, R>::Enc &e,
+                                          const Params &p, double &ds, double &dof) {
+  using El = Elem<T, R>;
+  using A = typename El::A;
+  const A ga = A(g);
+  if constexpr (OP == OP_QDQ_LEARN) {
+    const A t = El::r(El::shifted(x, e, p) / e.s);
+    const A rr = rint_a(t);
+    const A q = El::r(rr - e.o);
+    const A m = (q >= e.qmin && q <= e.qmax) ? A(1) : A(0);
+    const A nm = A(1) - m;
+    ds += static_cast<double>(El::r(ga * El::r(clamp_a(rr, e.lo, e.hi) - t * m)));
+    dof += static_cast<double>(El::r(ga * El::r(nm * e.s)));
+    // the shift's own scale terms: +alpha*g from the add, -alpha*g*mask through the sub
+    if (p.alpha != 0.0f) ds += static_cast<double>(p.alpha) * static_cast<double>(ga * nm);
+    return static_cast<float>(ga * m);
+  } else if constexpr (OP == OP_QDQ_FROZEN) {
+    const float q = rintf(x * e.inv_s) + e.zp;
+    const float m = (q >= p.qmin && q <= p.qmax) ? 1.0f : 0.0f;
+    return g * m;
+  } else if constexpr (OP == OP_Q) {
+    const A t = El::r(A(x) / e.s);
+    const A q = El::r(rint_a(t) - e.o);
+    const A m = (q >= e.qmin && q <= e.qmax) ? A(1) : A(0);
+    const A mg = ga * m;
+    const A gs = El::r(mg / e.s);
+    // QuantizeFunc.backward divides the saved input (type T) by the scale: in T when the
+    // scale is 0-dim, in R otherwise
+    const A xs = p.scalar_scale ? A(Io<T>::round(x / e.s_io)) : t;
+    ds += static_cast<double>(El::r(-gs * xs));
+    dof += static_cast<double>(-mg);
+    return static_cast<float>(gs);
+  } else {
+    const A gs = El::r(ga * e.s);
+    ds += static_cast<double>(El::r(ga * El::r(A(x) + e.o)));
+    dof += static_cast<double>(gs);
+    return static_cast<float>(gs);
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// Accumulators.
+// ---------------------------------------------------------------------------------
+struct Sum2 {
+  double a, b;
+};
+struct MinMax {
+  float mn, mx;
+};
+
+__device__ __forceinline__ void acc_add(Sum2 &x, const Sum2 &y) {
+  x.a += y.a;
+  x.b += y.b;
+}
+__device__ __forceinline__ void acc_add(MinMax &x, const MinMax &y) {
+  x.mn = nan_min(x.mn, y.mn);
+  x.mx = nan_max(x.mx, y.mx);
+}
+__device__ __forceinline__ Sum2 acc_shfl(const Sum2 &x, int off) {
+  return Sum2{__shfl_xor(x.a, off, kWave), __shfl_xor(x.b, off, kWave)};
+}
+__device__ __forceinline__ MinMax acc_shfl(const MinMax &x, int off) {
+  return MinMax{__shfl_xor(x.mn, off, kWave), __shfl_xor(x.mx, off, kWave)};
+}
+
+// Whole-block reduction; thread 0 ends with the block's value (fixed order).
+template <typename Acc>
+__device__ __forceinline__ void block_reduce(Acc &a) {
+  __shared__ Acc red[kThreads / kWave];
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) acc_add(a, acc_shfl(a, off));
+  if (threadIdx.x % kWave == 0) red[threadIdx.x / kWave] = a;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    a = red[0];
+#pragma unroll
+    for (int i = 1; i < kThreads / kWave; ++i) acc_add(a, red[i]);
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// Work policies: what one element / one 16-byte vector does.
+// ---------------------------------------------------------------------------------
+template <int OP, typename T, typename R>
+struct FwdW {
+  using El = Elem<T, R>;
+  using Enc = typename El::Enc;
+  using Acc = Sum2;  // unused
+  static constexpr bool kReduce = false;
+  static constexpr int E = Io<T>::E;
+  const T *x;
+  T *y;
+  const float *scale, *offset;
+  Params p;
+
+  __device__ Enc enc(int64_t c) const { return El::enc(scale, offset, c, p); }
+  __device__ static Acc zero() { return Sum2{0.0, 0.0}; }
+  __device__ void elem(const Enc &e, int64_t i, Acc &) const {
+    Io<T>::st(y, i, fwd_elem<OP, T, R>(Io<T>::ld(x, i), e, p));
+  }
+  __device__ void compute(const Enc &e, const u4 &v, int64_t vi) const {
+    float a[E];
+    Io<T>::unpack(v, a);
+#pragma unroll
+    for (int k = 0; k < E; ++k) a[k] = fwd_elem<OP, T, R>(a[k], e, p);
+    __builtin_nontemporal_store(Io<T>::pack(a), reinterpret_cast<u4 *>(y) + vi);
+  }
+  __device__ void vec1(const Enc &e, int64_t vi, Acc &) const {
+    compute(e, __builtin_nontemporal_load(reinterpret_cast<const u4 *>(x) + vi), vi);
+  }
+  // kVecPerThread vectors per thread: all loads issued before any compute
+  __device__ void vec_block(const Enc &e, int64_t vb, int nv, Acc &) const {
+    const u4 *xv = reinterpret_cast<const u4 *>(x) + vb;
+    u4 v[kVecPerThread];
+#pragma unroll
+    for (int k = 0; k < kVecPerThread; ++k) {
+      const int i = k * kThreads + threadIdx.x;
+      if (i < nv) v[k] = __builtin_nontemporal_load(xv + i);
+    }
+#pragma unroll
+    for (int k = 0; k < kVecPerThread; ++k) {
+      const int i = k * kThreads + threadIdx.x;
+      if (i < nv) compute(e, v[k], vb + i);
+    }
+  }
+};
+
+template <int OP, typename T, typename R, bool ENC>
+struct BwdW {
+  using El = Elem<T, R>;
+  using Enc = typename El::Enc;
+  using Acc = Sum2;
+  static constexpr bool kReduce = ENC;
+  static constexpr int E = Io<T>::E;
+  const T *x, *g;
+  T *dx;
+  const float *scale, *offset;
+  Params p;
+
+  __device__ Enc enc(int64_t c) const { return El::enc(scale, offset, c, p); }
+  __device__ static Acc zero() { return Sum2{0.0, 0.0}; }
+  __device__ void elem(const Enc &e, int64_t i, Acc &acc) const {
+    Io<T>::st(dx, i,
+              bwd_elem<OP, T, R>(Io<T>::ld(x, i), Io<T>::ld(g, i), e, p, acc.a, acc.b));
+  }
+  __device__ void compute(const Enc &e, const u4 &xv, const u4 &gv, int64_t vi,
+                          Acc &acc) const {
+    float a[E], b[E];
+    Io<T>::unpack(xv, a);
+    Io<T>::unpack(gv, b);
+#pragma unroll
+    for (int k = 0; k < E; ++k) a[k] = bwd_elem<OP, T, R>(a[k], b[k], e, p, acc.a, acc.b);
+    __builtin_nontemporal_store(Io<T>::pack(a), reinterpret_cast<u4 *>(dx) + vi);
+  }
+  __device__ void vec1(const Enc &e, int64_t vi, Acc &acc) const {
+    const u4 xv = __builtin_nontemporal_load(reinterpret_cast<const u4 *>(x) + vi);
+    const u4 gv = __builtin_nontemporal_load(reinterpret_cast<const u4 *>(g) + vi);
+    compute(e, xv, gv, vi, acc);
+  }
+  __device__ void vec_block(const Enc &e, int64_t vb, int nv, Acc &acc) const {
+    const u4 *xv = reinterpret_cast<const u4 *>(x) + vb;
+    const u4 *gv = reinterpret_cast<const u4 *>(g) + vb;
+    u4 xr[kVecPerThread], gr[kVecPerThread];
+#pragma unroll
+    for (int k = 0; k < kVecPerThread; ++k) {
+      const int i = k * kThreads + threadIdx.x;
+      if (i < nv) {
+        xr[k] = __builtin_nontemporal_load(xv + i);
+        gr[k] = __builtin_nontemporal_load(gv + i);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kVecPerThread; ++k) {
+      const int i = k * kThreads + threadIdx.x;
+      if (i < nv) compute(e, xr[k], gr[k], vb + i, acc);
+    }
+  }
+};
+
+template <typename T>
+struct MinMaxW {
+  struct Enc {};
+  using Acc = MinMax;
+  static constexpr bool kReduce = true;
+  static constexpr int E = Io<T>::E;
+  const T *x;
+
+  __device__ Enc enc(int64_t) const { return Enc{}; }
+  __device__ static Acc zero() { return MinMax{INFINITY, -INFINITY}; }
+  __device__ static void take(Acc &acc, float v) {
+    acc.mn = nan_min(acc.mn, v);
+    acc.mx = nan_max(acc.mx, v);
+  }
+  __device__ void elem(const Enc &, int64_t i, Acc &acc) const { take(acc, Io<T>::ld(x, i)); }
+  __device__ static void take_vec(const u4 &v, Acc &acc) {
+    float a[E];
+    Io<T>::unpack(v, a);
+#pragma unroll
+    for (int k = 0; k < E; ++k) take(acc, a[k]);
+  }
+  __device__ void vec1(const Enc &, int64_t vi, Acc &acc) const {
+    take_vec(__builtin_nontemporal_load(reinterpret_cast<const u4 *>(x) + vi), acc);
+  }
+  __device__ void vec_block(const Enc &, int64_t vb, int nv, Acc &acc) const {
+    const u4 *xv = reinterpret_cast<const u4 *>(x) + vb;
+    u4 v[kVecPerThread];
+#pragma unroll
+    for (int k = 0; k < kVecPerThread; ++k) {
+      const int i = k * kThreads + threadIdx.x;
+      if (i < nv) v[k] = __builtin_nontemporal_load(xv + i);
+    }
+#pragma unroll
+    for (int k = 0; k < kVecPerThread; ++k) {
+      const int i = k * kThreads + threadIdx.x;
+      if (i < nv) take_vec(v[k], acc);
+    }
+  }
+};
+
+// ---------------------------------------------------------------------------------
+// Decompositions.
+// ---------------------------------------------------------------------------------
+struct Geo {
+  int64_t inner, C1, midC1, C0;
+};
+// encoding of run q = ((o * C0 + c0) * mid + m) * C1 + c1
+__device__ __forceinline__ int64_t enc_of_run(const Geo &g, int64_t q) {
+  return ((q / g.midC1) % g.C0) * g.C1 + q % g.C1;
+}
+
+struct ColGeo {
+  int64_t mid, K, inner, C1, C0;  // band rows, band columns (C1 * inner)
+  int64_t col_tiles, chunks, rows_per_chunk;
+  int kt_shift;                    // log2 of the threads per row (the rest walk rows)
+};
+
+// runs: block b handles chunk (b % splits) of run (b / splits); one partial per block.
+template <class W>
+__global__ __launch_bounds__(kThreads) void k_runs(W w, Geo geo, int64_t splits, int vec,
+                                                   typename W::Acc *__restrict__ partial) {
+  constexpr int64_t kChunk = int64_t(kThreads) * kVecPerThread * W::E;
+  const int64_t b = blockIdx.x;
+  const int64_t run = b / splits, sp = b % splits;
+  const auto e = w.enc(enc_of_run(geo, run));
+  const int64_t beg = sp * kChunk;
+  const int64_t end = min(geo.inner, beg + kChunk);
+  const int64_t base = run * geo.inner + beg;
+  typename W::Acc acc = W::zero();
+  if (vec) {
+    w.vec_block(e, base / W::E, static_cast<int>((end - beg) / W::E), acc);
+  } else {
+    const int n = static_cast<int>(end - beg);
+    for (int i = threadIdx.x; i < n; i += kThreads) w.elem(e, base + i, acc);
+  }
+  if constexpr (W::kReduce) {
+    block_reduce(acc);
+    if (threadIdx.x == 0) partial[b] = acc;
+  }
+}
+
+// segs: a segment of 2^tpr_shift lanes per run, kThreads >> tpr_shift runs per pass,
+// `iters` passes per block; one partial per run.
+template <class W>
+__global__ __launch_bounds__(kThreads) void k_segs(W w, Geo geo, int64_t runs, int tpr_shift,
+                                                   int iters, int vec,
+                                                   typename W::Acc *__restrict__ partial) {
+  const int tpr = 1 << tpr_shift;
+  const int seg = threadIdx.x >> tpr_shift, lane = threadIdx.x & (tpr - 1);
+  const int64_t per_pass = kThreads >> tpr_shift;
+  const int64_t n = vec ? geo.inner / W::E : geo.inner;
+  for (int it = 0; it < iters; ++it) {
+    const int64_t q = (static_cast<int64_t>(blockIdx.x) * iters + it) * per_pass + seg;
+    typename W::Acc acc = W::zero();
+    if (q < runs) {
+      const auto e = w.enc(enc_of_run(geo, q));
+      if (vec) {
+        const int64_t vb = q * n;
+        for (int64_t v = lane; v < n; v += tpr) w.vec1(e, vb + v, acc);
+      } else {
+        const int64_t base = q * geo.inner;
+        for (int64_t i = lane; i < n; i += tpr) w.elem(e, base + i, acc);
+      }
+    }
+    if constexpr (W::kReduce) {
+      for (int off = tpr >> 1; off > 0; off >>= 1) acc_add(acc, acc_shfl(acc, off));
+      if (lane == 0 && q < runs) partial[q] = acc;
+    }
+  }
+}
+
+// cols: block b owns columns [tile * Kt, +Kt) of the rows of chunk h of band `band`;
+// kThreads / Kt rows are walked in parallel and combined through LDS.
+template <class W>
+__global__ __launch_bounds__(kThreads) void k_cols(W w, ColGeo cg,
+                                                   typename W::Acc *__restrict__ partial) {
+  const int kt = 1 << cg.kt_shift;
+  const int lane = threadIdx.x & (kt - 1), prow = threadIdx.x >> cg.kt_shift;
+  const int P = kThreads >> cg.kt_shift;
+  const int64_t tile = blockIdx.x % cg.col_tiles, rest = blockIdx.x / cg.col_tiles;
+  const int64_t h = rest % cg.chunks, band = rest / cg.chunks;
+  const int64_t j = tile * kt + lane;
+  typename W::Acc acc = W::zero();
+  if (j < cg.K) {
+    const auto e = w.enc((band % cg.C0) * cg.C1 + j / cg.inner);
+    const int64_t rb = band * cg.mid;
+    const int64_t r1 = rb + min(cg.mid, (h + 1) * cg.rows_per_chunk);
+    for (int64_t r = rb + h * cg.rows_per_chunk + prow; r < r1; r += P)
+      w.elem(e, r * cg.K + j, acc);
+  }
+  if constexpr (W::kReduce) {
+    if (P > 1) {
+      __shared__ typename W::Acc red[kThreads];
+      red[threadIdx.x] = acc;
+      __syncthreads();
+      if (prow == 0)
+        for (int q = 1; q < P; ++q) acc_add(acc, red[q * kt + lane]);
+    }
+    if (prow == 0 && j < cg.K) partial[(band * cg.chunks + h) * cg.K + j] = acc;
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// Host-side plan (shared by the entry points and the per-type launchers).
+// ---------------------------------------------------------------------------------
+enum Kind { KIND_RUNS = 0, KIND_SEGS = 1, KIND_COLS = 2 };
+
+struct FoldMap {
+  int64_t n0, n1, n2;  // loop counts
+  int64_t s0, s1, s2;  // loop strides
+  int64_t C1, sc0, sc1;  // encoding c = c0 * C1 + c1 adds c0 * sc0 + c1 * sc1
+};
+
+struct Plan {
+  int kind = KIND_RUNS;
+  int64_t outer = 0, C0 = 1, mid = 1, C1 = 1, inner = 0;  // normalized layout
+  int64_t n = 0;                                           // elements
+  int64_t runs = 0, splits = 0;                            // runs / segs
+  Geo geo{};
+  ColGeo cg{};
+  int64_t col_blocks = 0;
+  int64_t partial_slots = 0;
+  FoldMap fold{};
+  int esize = 4;
+};
+
+struct Call {
+  const Plan *plan;
+  int op;
+  int internal;            // RXMET_QDQ_F32 / F16 / BF16 / F64
+  const void *x, *g;
+  void *out;               // y / q / dx
+  const float *scale, *offset;
+  Params p;
+  void *partial;           // Sum2 / MinMax partials, or null
+  hipStream_t stream;
+};
+
+template <class W>
+static int launch_decomp(const Plan &pl, const W &w, bool aligned, void *partial,
+                         hipStream_t s) {
+  using Acc = typename W::Acc;
+  Acc *part = static_cast<Acc *>(partial);
+  const bool vec = aligned && pl.inner % W::E == 0;
+  if (pl.kind == KIND_RUNS) {
+    hipLaunchKernelGGL(k_runs<W>, dim3(static_cast<unsigned>(pl.runs * pl.splits)),
+                       dim3(kThreads), 0, s, w, pl.geo, pl.splits, int(vec), part);
+  } else if (pl.kind == KIND_SEGS) {
+    const int64_t nv = vec ? pl.inner / W::E : pl.inner;
+    int shift = 0;
+    while (shift < 6 && (int64_t(1) << shift) < nv) ++shift;
+    const int64_t per_thread = (nv + (int64_t(1) << shift) - 1) >> shift;
+    const int64_t per_pass = kThreads >> shift;
+    int iters = per_thread >= 8 ? 1 : static_cast<int>(8 / per_thread);
+    while (iters > 1 && (pl.runs + per_pass * iters - 1) / (per_pass * iters) < 2048) iters >>= 1;
+    const int64_t blocks = (pl.runs + per_pass * iters - 1) / (per_pass * iters);
+    hipLaunchKernelGGL(k_segs<W>, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, s, w,
+                       pl.geo, pl.runs, shift, iters, int(vec), part);
+  } else {
+    hipLaunchKernelGGL(k_cols<W>, dim3(static_cast<unsigned>(pl.col_blocks)), dim3(kThreads), 0,
+                       s, w, pl.cg, part);
+  }
+  return 0;
+}
+
+static inline bool aligned16(const void *p) {
+  return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
+
+template <int OP, typename T, typename R>
+static int run_forward(const Call &c) {
+  FwdW<OP, T, R> w{static_cast<const T *>(c.x), static_cast<T *>(c.out), c.scale, c.offset, c.p};
+  return launch_decomp(*c.plan, w, aligned16(c.x) && aligned16(c.out), nullptr, c.stream);
+}
+
+template <int OP, typename T, typename R>
+static int run_backward(const Call &c) {
+  const bool al = aligned16(c.x) && aligned16(c.g) && aligned16(c.out);
+  if (c.partial) {
+    BwdW<OP, T, R, true> w{static_cast<const T *>(c.x), static_cast<const T *>(c.g),
+                           static_cast<T *>(c.out), c.scale, c.offset, c.p};
+    return launch_decomp(*c.plan, w, al, c.partial, c.stream);
+  }
+  BwdW<OP, T, R, false> w{static_cast<const T *>(c.x), static_cast<const T *>(c.g),
+                          static_cast<T *>(c.out), c.scale, c.offset, c.p};
+  return launch_decomp(*c.plan, w, al, nullptr, c.stream);
+}
+
+template <typename T>
+static int run_minmax(const Call &c) {
+  MinMaxW<T> w{static_cast<const T *>(c.x)};
+  return launch_decomp(*c.plan, w, aligned16(c.x), c.partial, c.stream);
+}
+
+enum What { WHAT_FORWARD = 0, WHAT_BACKWARD = 1, WHAT_MINMAX = 2 };
+
+// The internal types each io type pairs with: R = T, fp32 or fp64 (fp32 io: fp32, fp64).
+template <typename T>
+static int run_typed(const Call &c, int what) {
+  if (what == WHAT_MINMAX) return run_minmax<T>(c);
+  auto go = [&](auto rtag) -> int {
+    using R = decltype(rtag);
+    auto fw = what == WHAT_FORWARD;
+    switch (c.op) {
+      case OP_QDQ_LEARN:
+        return fw ? run_forward<OP_QDQ_LEARN, T, R>(c) : run_backward<OP_QDQ_LEARN, T, R>(c);
+      case OP_Q:
+        return fw ? run_forward<OP_Q, T, R>(c) : run_backward<OP_Q, T, R>(c);
+      default:
+        return -22;
+    }
+  };
+  if (c.op == OP_QDQ_FROZEN)  // torch's fake_quantize kernels: fp32 math on any io type
+    return what == WHAT_FORWARD ? run_forward<OP_QDQ_FROZEN, T, float>(c)
+                                : run_backward<OP_QDQ_FROZEN, T, float>(c);
+  if (c.op == OP_DQ)  // DequantizeFunc runs in the tensor's own type
+    return what == WHAT_FORWARD ? run_forward<OP_DQ, T, T>(c) : run_backward<OP_DQ, T, T>(c);
+  switch (c.internal) {
+    case RXMET_QDQ_F64:
+      return go(double{});
+    case RXMET_QDQ_F32:
+      return go(float{});
+    default:
+      if constexpr (!std::is_same<T, float>::value) return go(T{});
+      return -22;
+  }
+}
+
+// Per-io-type entry points, one translation unit each.
+int run_f32(const Call &c, int what);
+int run_f16(const Call &c, int what);
+int run_bf16(const Call &c, int what);
+
+}  // namespace qdq
+}  // namespace rxmet

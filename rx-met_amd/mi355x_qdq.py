@@ -123,193 +123,248 @@ def reshape_tensor_for_blocks(tensor, encoding_shape, block_size):
 
 
 # ---------------------------------------------------------------------------------
-# Layout: map (tensor shape, encoding shape) onto the kernels' [outer, C, inner] view.
+# Layout: map (tensor shape, encoding shape) onto the kernels' [outer, C0, mid, C1, inner]
+# view (encoding c0 * C1 + c1 of row-major element (o, c0, m, c1, k)).
 # ---------------------------------------------------------------------------------
 
+_IO_CODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+_INTERNAL_CODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2, torch.float64: 3}
 
-def kernel_layout(tensor_shape, enc_shape) -> Optional[Tuple[int, int, int]]:
-    """Return (outer, C, inner) with encoding index (i // inner) % C for row-major
-    element i, or None when the encoding axes are not one contiguous span."""
+
+def _groups(tensor_shape, enc_shape):
+    """Maximal runs of adjacent axes that all carry encodings ("E") or none ("N"), as
+    (kind, size, axes); axes of size 1 join no group."""
     tensor_shape = tuple(int(d) for d in tensor_shape)
     nd = len(tensor_shape)
     enc = (1,) * (nd - len(enc_shape)) + tuple(int(d) for d in enc_shape)
-    numel = math.prod(tensor_shape)
-    axes = [a for a in range(nd) if enc[a] != 1]
-    if not axes:
-        return 1, 1, numel
-    a0, a1 = axes[0], axes[-1]
-    for a in range(a0, a1 + 1):
-        if enc[a] == 1 and tensor_shape[a] != 1:
-            return None
-        if enc[a] != 1 and enc[a] != tensor_shape[a]:
-            return None
-    outer = math.prod(tensor_shape[:a0])
-    C = math.prod(tensor_shape[a0:a1 + 1])
-    inner = math.prod(tensor_shape[a1 + 1:])
-    return outer, C, inner
+    out = []
+    for a, (t, e) in enumerate(zip(tensor_shape, enc)):
+        if e not in (1, t):
+            raise ValueError(f"encoding shape {tuple(enc_shape)} does not match tensor shape "
+                             f"{tensor_shape}")
+        if t == 1:
+            continue
+        kind = "E" if e != 1 else "N"
+        if out and out[-1][0] == kind:
+            out[-1] = (kind, out[-1][1] * t, out[-1][2] + (a,))
+        else:
+            out.append((kind, t, (a,)))
+    return out
+
+
+def kernel_layout(tensor_shape, enc_shape) -> Optional[Tuple[int, int, int, int, int]]:
+    """(outer, C0, mid, C1, inner) for encodings on at most two separated groups of axes,
+    or None (three or more groups)."""
+    numel = math.prod(int(d) for d in tensor_shape)
+    groups = _groups(tensor_shape, enc_shape)
+    n_enc = sum(1 for g in groups if g[0] == "E")
+    if n_enc == 0:
+        return 1, 1, 1, 1, numel
+    if n_enc > 2:
+        return None
+    sizes = [g[1] for g in groups]
+    outer = 1
+    if groups[0][0] == "N":
+        outer, sizes = sizes[0], sizes[1:]
+    sizes = sizes + [1] * (4 - len(sizes))  # E [N [E [N]]]
+    if n_enc == 1:
+        return 1, 1, outer, sizes[0], sizes[1]
+    return outer, sizes[0], sizes[1], sizes[2], sizes[3]
+
+
+class _Plan:
+    """How a tensor reaches the kernels: its layout, and (for encodings on three or more
+    separated axis groups) the permutation that gathers the encoding axes in front."""
+
+    __slots__ = ("layout", "perm", "inv", "C")
+
+    def __init__(self, tensor_shape, enc_shape):
+        tensor_shape = tuple(int(d) for d in tensor_shape)
+        nd = len(tensor_shape)
+        enc = (1,) * (nd - len(enc_shape)) + tuple(int(d) for d in enc_shape)
+        self.C = math.prod(enc)
+        self.perm = self.inv = None
+        if math.prod(tensor_shape) == 0:
+            self.layout = (1, 1, 0, max(self.C, 1), 1)
+            return
+        lay = kernel_layout(tensor_shape, enc)
+        if lay is None:
+            e_axes = [a for a in range(nd) if enc[a] != 1 and tensor_shape[a] != 1]
+            self.perm = tuple(e_axes + [a for a in range(nd) if a not in e_axes])
+            self.inv = tuple(sorted(range(nd), key=self.perm.__getitem__))
+            lay = (1, 1, 1, self.C, math.prod(tensor_shape) // self.C)
+        self.layout = lay
+
+    def to_kernel(self, t: torch.Tensor) -> torch.Tensor:
+        return (t.permute(self.perm) if self.perm else t).contiguous()
+
+    def from_kernel(self, t: torch.Tensor) -> torch.Tensor:
+        return t.permute(self.inv).contiguous() if self.perm else t
+
+    def cstruct(self):
+        return _rx.QdqLayout(*self.layout)
 
 
 def _require(tensor: torch.Tensor, what: str):
     if not tensor.is_cuda:
         raise RuntimeError(f"mi355x backend: {what} must be a GPU tensor")
-    if tensor.dtype != torch.float32:
+    if tensor.dtype not in _IO_CODE:
         raise NotImplementedError(
-            f"mi355x backend: {what} must be float32 (got {tensor.dtype})")
+            f"mi355x backend: {what} must be float32, float16 or bfloat16 (got {tensor.dtype})")
 
 
-def _enc_vector(t: Optional[torch.Tensor], like: torch.Tensor, C: int) -> Optional[torch.Tensor]:
-    if t is None:
-        return None
-    v = t.detach().to(device=like.device, dtype=torch.float32).reshape(-1)
-    if v.numel() == 1 and C != 1:
-        v = v.expand(C)
-    return v.contiguous()
+def _numerics(io: torch.dtype, internal: torch.dtype, shift: float = 0.0,
+              scalar_scale: bool = False):
+    return _rx.QdqNumerics(_IO_CODE[io], _INTERNAL_CODE[internal], float(shift),
+                           int(bool(scalar_scale)), 0)
 
 
-def _workspace(outer: int, C: int, inner: int, device) -> torch.Tensor:
-    nbytes = int(_rx.load().rxmet_qdq_workspace_bytes(outer, C, inner))
+def _internal_dtype(dtype: torch.dtype, qmin: int, qmax: int) -> torch.dtype:
+    """The reference's widening rule (torch_builtins.py:171-174, 255-262)."""
+    internal = dtype
+    if not _is_numerically_stable(internal, qmin, qmax):
+        internal = torch.float32
+        if not _is_numerically_stable(internal, qmin, qmax):
+            internal = torch.float64
+    return internal
+
+
+def _enc_vectors(scale, offset, internal: torch.dtype, enc_shape):
+    """scale.to(internal) / offset.to(internal) of the reference, broadcast to the encoding
+    shape and flattened in the kernels' encoding order, carried as float32 (exact: the
+    internal type is fp16/bf16/fp32, or fp64 holding fp32/fp16/bf16 values).  Autograd flows
+    through these conversions back to the caller's parameters."""
+    if internal == torch.float64 and torch.float64 in (scale.dtype, offset.dtype):
+        raise NotImplementedError(
+            "mi355x backend: float64 encodings with float64 arithmetic are not supported")
+
+    def vec(t):
+        return t.to(internal).expand(enc_shape).reshape(-1).to(torch.float32).contiguous()
+
+    return vec(scale), vec(offset)
+
+
+def _enc_shape(scale, offset, nd: int):
+    shape = torch.broadcast_shapes(tuple(scale.shape), tuple(offset.shape))
+    return (1,) * (nd - len(shape)) + tuple(shape)
+
+
+def _workspace(plan: _Plan, io: torch.dtype, device) -> torch.Tensor:
+    lay = plan.cstruct()
+    nbytes = int(_rx.load().rxmet_qdq_workspace_bytes_ex(lay, _IO_CODE[io]))
     return torch.empty(max(nbytes, 16), dtype=torch.uint8, device=device)
 
 
-def _plan(tensor: torch.Tensor, scale: torch.Tensor):
-    layout = kernel_layout(tensor.shape, scale.shape)
-    if layout is None:
-        raise NotImplementedError(
-            f"mi355x backend: encodings of shape {tuple(scale.shape)} over a tensor of shape "
-            f"{tuple(tensor.shape)} span non-adjacent axes")
-    return layout
+def _enc_grad(need: bool, C: int, device):
+    return torch.empty(C, dtype=torch.float32, device=device) if need else None
 
 
 # ---------------------------------------------------------------------------------
 # Autograd functions — each direction is one kernel launch (+ a tiny fold kernel).
+# The encoding arguments are the flat float32 vectors of _enc_vectors.
 # ---------------------------------------------------------------------------------
 
 
 class _QuantDequant(torch.autograd.Function):
-    """QuantDequantFunc (torch_builtins.py:618-691) or the fake_quantize fast path."""
+    """QuantDequantFunc (torch_builtins.py:618-691) with the zero_point_shift around it
+    (:276-284), or the fake_quantize fast path (:221-249)."""
 
     @staticmethod
-    def forward(ctx, x, scale, offset, qmin: int, qmax: int, mode: int):
-        _require(x, "tensor")
-        x_c = x.contiguous()
-        outer, C, inner = _plan(x_c, scale)
-        s = _enc_vector(scale, x_c, C)
-        o = _enc_vector(offset, x_c, C)
-        y = torch.empty_like(x_c)
-        _rx.call("rxmet_qdq_forward", _rx.ptr(x_c), _rx.ptr(y), outer, C, inner, _rx.ptr(s),
-                 _rx.ptr(o), int(qmin), int(qmax), int(mode), _rx.stream_of(x_c.device))
-        ctx.layout = (outer, C, inner)
-        ctx.qmin, ctx.qmax, ctx.mode = int(qmin), int(qmax), int(mode)
-        ctx.scale_shape = scale.shape
-        ctx.offset_shape = None if offset is None else offset.shape
-        ctx.save_for_backward(x_c, s, o)
-        return y
+    def forward(ctx, x, s, o, qmin: int, qmax: int, mode: int, plan: _Plan, numerics):
+        xk = plan.to_kernel(x)
+        y = torch.empty_like(xk)
+        if s.numel() > 0:
+            _rx.call("rxmet_qdq_forward_ex", _rx.ptr(xk), _rx.ptr(y), plan.cstruct(), numerics,
+                     _rx.ptr(s), _rx.ptr(o), int(qmin), int(qmax), int(mode),
+                     _rx.stream_of(xk.device))
+        ctx.args = (int(qmin), int(qmax), int(mode), plan, numerics)
+        ctx.save_for_backward(xk, s, o)
+        return plan.from_kernel(y)
 
     @staticmethod
     def backward(ctx, g):
-        x, s, o = ctx.saved_tensors
-        outer, C, inner = ctx.layout
+        xk, s, o = ctx.saved_tensors
+        qmin, qmax, mode, plan, numerics = ctx.args
         need_x, need_s, need_o = ctx.needs_input_grad[:3]
-        g = g.contiguous()
-        dx = torch.empty_like(x)
-        learn = ctx.mode == LEARNABLE
-        ds = torch.empty(C, dtype=torch.float32, device=x.device) if (need_s and learn) else None
-        do = torch.empty(C, dtype=torch.float32, device=x.device) if (need_o and learn) else None
-        ws = _workspace(outer, C, inner, x.device) if (ds is not None or do is not None) else None
-        _rx.call("rxmet_qdq_backward", _rx.ptr(x), _rx.ptr(g), _rx.ptr(dx), _rx.ptr(ds), _rx.ptr(do),
-                 outer, C, inner, _rx.ptr(s), _rx.ptr(o), ctx.qmin, ctx.qmax, ctx.mode,
-                 _rx.ptr(ws), _rx.stream_of(x.device))
-        ds = None if ds is None else ds.view(ctx.scale_shape)
-        do = None if do is None else do.view(ctx.offset_shape)
-        return (dx if need_x else None), ds, do, None, None, None
+        learn = mode == LEARNABLE
+        gk = plan.to_kernel(g.to(xk.dtype))
+        dx = torch.empty_like(xk)
+        ds = _enc_grad(need_s and learn, s.numel(), xk.device)
+        do = _enc_grad(need_o and learn, s.numel(), xk.device)
+        ws = _workspace(plan, xk.dtype, xk.device) if (ds is not None or do is not None) else None
+        if s.numel() > 0:
+            _rx.call("rxmet_qdq_backward_ex", _rx.ptr(xk), _rx.ptr(gk), _rx.ptr(dx), _rx.ptr(ds),
+                     _rx.ptr(do), plan.cstruct(), numerics, _rx.ptr(s), _rx.ptr(o), qmin, qmax,
+                     mode, _rx.ptr(ws), _rx.stream_of(xk.device))
+        return (plan.from_kernel(dx) if need_x else None), ds, do, None, None, None, None, None
 
 
 class _Quantize(torch.autograd.Function):
     """QuantizeFunc (torch_builtins.py:505-571)."""
 
     @staticmethod
-    def forward(ctx, x, scale, offset, qmin: int, qmax: int):
-        _require(x, "tensor")
-        x_c = x.contiguous()
-        outer, C, inner = _plan(x_c, scale)
-        s = _enc_vector(scale, x_c, C)
-        o = _enc_vector(offset, x_c, C)
-        q = torch.empty_like(x_c)
-        _rx.call("rxmet_quantize_forward", _rx.ptr(x_c), _rx.ptr(q), outer, C, inner, _rx.ptr(s),
-                 _rx.ptr(o), int(qmin), int(qmax), _rx.stream_of(x_c.device))
-        ctx.layout = (outer, C, inner)
-        ctx.qmin, ctx.qmax = int(qmin), int(qmax)
-        ctx.scale_shape = scale.shape
-        ctx.offset_shape = None if offset is None else offset.shape
-        ctx.save_for_backward(x_c, s, o)
-        return q
+    def forward(ctx, x, s, o, qmin: int, qmax: int, plan: _Plan, numerics):
+        xk = plan.to_kernel(x)
+        q = torch.empty_like(xk)
+        if s.numel() > 0:
+            _rx.call("rxmet_quantize_forward_ex", _rx.ptr(xk), _rx.ptr(q), plan.cstruct(),
+                     numerics, _rx.ptr(s), _rx.ptr(o), int(qmin), int(qmax),
+                     _rx.stream_of(xk.device))
+        ctx.args = (int(qmin), int(qmax), plan, numerics)
+        ctx.save_for_backward(xk, s, o)
+        return plan.from_kernel(q)
 
     @staticmethod
     def backward(ctx, g):
-        x, s, o = ctx.saved_tensors
-        outer, C, inner = ctx.layout
+        xk, s, o = ctx.saved_tensors
+        qmin, qmax, plan, numerics = ctx.args
         need_x, need_s, need_o = ctx.needs_input_grad[:3]
-        g = g.contiguous()
-        dx = torch.empty_like(x)
-        ds = torch.empty(C, dtype=torch.float32, device=x.device) if need_s else None
-        do = torch.empty(C, dtype=torch.float32, device=x.device) if need_o else None
-        ws = _workspace(outer, C, inner, x.device) if (need_s or need_o) else None
-        _rx.call("rxmet_quantize_backward", _rx.ptr(x), _rx.ptr(g), _rx.ptr(dx), _rx.ptr(ds),
-                 _rx.ptr(do), outer, C, inner, _rx.ptr(s), _rx.ptr(o), ctx.qmin, ctx.qmax,
-                 _rx.ptr(ws), _rx.stream_of(x.device))
-        ds = None if ds is None else ds.view(ctx.scale_shape)
-        do = None if do is None else do.view(ctx.offset_shape)
-        return (dx if need_x else None), ds, do, None, None
+        gk = plan.to_kernel(g.to(xk.dtype))
+        dx = torch.empty_like(xk)
+        ds = _enc_grad(need_s, s.numel(), xk.device)
+        do = _enc_grad(need_o, s.numel(), xk.device)
+        ws = _workspace(plan, xk.dtype, xk.device) if (need_s or need_o) else None
+        if s.numel() > 0:
+            _rx.call("rxmet_quantize_backward_ex", _rx.ptr(xk), _rx.ptr(gk), _rx.ptr(dx),
+                     _rx.ptr(ds), _rx.ptr(do), plan.cstruct(), numerics, _rx.ptr(s),
+                     _rx.ptr(o), qmin, qmax, _rx.ptr(ws), _rx.stream_of(xk.device))
+        return (plan.from_kernel(dx) if need_x else None), ds, do, None, None, None, None
 
 
 class _Dequantize(torch.autograd.Function):
     """DequantizeFunc (torch_builtins.py:574-615)."""
 
     @staticmethod
-    def forward(ctx, q, scale, offset):
-        _require(q, "tensor")
-        q_c = q.contiguous()
-        outer, C, inner = _plan(q_c, scale)
-        s = _enc_vector(scale, q_c, C)
-        o = _enc_vector(offset, q_c, C)
-        y = torch.empty_like(q_c)
-        _rx.call("rxmet_dequantize_forward", _rx.ptr(q_c), _rx.ptr(y), outer, C, inner,
-                 _rx.ptr(s), _rx.ptr(o), _rx.stream_of(q_c.device))
-        ctx.layout = (outer, C, inner)
-        ctx.scale_shape = scale.shape
-        ctx.offset_shape = None if offset is None else offset.shape
-        ctx.save_for_backward(q_c, s, o)
-        return y
+    def forward(ctx, q, s, o, plan: _Plan, numerics):
+        qk = plan.to_kernel(q)
+        y = torch.empty_like(qk)
+        if s.numel() > 0:
+            _rx.call("rxmet_dequantize_forward_ex", _rx.ptr(qk), _rx.ptr(y), plan.cstruct(),
+                     numerics, _rx.ptr(s), _rx.ptr(o), _rx.stream_of(qk.device))
+        ctx.args = (plan, numerics)
+        ctx.save_for_backward(qk, s, o)
+        return plan.from_kernel(y)
 
     @staticmethod
     def backward(ctx, g):
-        q, s, o = ctx.saved_tensors
-        outer, C, inner = ctx.layout
+        qk, s, o = ctx.saved_tensors
+        plan, numerics = ctx.args
         need_q, need_s, need_o = ctx.needs_input_grad[:3]
-        g = g.contiguous()
-        dq = torch.empty_like(q)
-        ds = torch.empty(C, dtype=torch.float32, device=q.device) if need_s else None
-        do = torch.empty(C, dtype=torch.float32, device=q.device) if need_o else None
-        ws = _workspace(outer, C, inner, q.device) if (need_s or need_o) else None
-        _rx.call("rxmet_dequantize_backward", _rx.ptr(q), _rx.ptr(g), _rx.ptr(dq), _rx.ptr(ds),
-                 _rx.ptr(do), outer, C, inner, _rx.ptr(s), _rx.ptr(o), _rx.ptr(ws),
-                 _rx.stream_of(q.device))
-        ds = None if ds is None else ds.view(ctx.scale_shape)
-        do = None if do is None else do.view(ctx.offset_shape)
-        return (dq if need_q else None), ds, do
+        gk = plan.to_kernel(g.to(qk.dtype))
+        dq = torch.empty_like(qk)
+        ds = _enc_grad(need_s, s.numel(), qk.device)
+        do = _enc_grad(need_o, s.numel(), qk.device)
+        ws = _workspace(plan, qk.dtype, qk.device) if (need_s or need_o) else None
+        if s.numel() > 0:
+            _rx.call("rxmet_dequantize_backward_ex", _rx.ptr(qk), _rx.ptr(gk), _rx.ptr(dq),
+                     _rx.ptr(ds), _rx.ptr(do), plan.cstruct(), numerics, _rx.ptr(s),
+                     _rx.ptr(o), _rx.ptr(ws), _rx.stream_of(qk.device))
+        return (plan.from_kernel(dq) if need_q else None), ds, do, None, None
 
 
 # ---------------------------------------------------------------------------------
 # Backend protocol
 # ---------------------------------------------------------------------------------
-
-
-def _check_fp32_grid(dtype, qmin, qmax):
-    if not _is_numerically_stable(dtype, qmin, qmax):
-        raise NotImplementedError(
-            f"mi355x backend: grid [{qmin}, {qmax}] needs float64 internals (fp32 kernels only)")
-    if not _is_grid_representable(dtype, qmin, qmax):
-        raise RuntimeError(f"{dtype} is unable to represent quantized output of range [{qmin}, {qmax}].")
 
 
 def _fast_path_layout(scale, offset, tensor, qmin: int, qmax: int) -> bool:
@@ -332,6 +387,14 @@ def _fast_path_layout(scale, offset, tensor, qmin: int, qmax: int) -> bool:
     return not bool(((zp < qmin) | (zp > qmax)).any())
 
 
+def _blocked(tensor, scale, offset, block_size):
+    """The reference's block reshape (torch_builtins.py:178-181, 266-271)."""
+    t = reshape_tensor_for_blocks(tensor, scale.shape, block_size)
+    s = scale.view(get_encoding_shape_with_blocks(scale.shape, block_size))
+    o = offset.view(get_encoding_shape_with_blocks(offset.shape, block_size))
+    return t, s, o
+
+
 def quantize(tensor: torch.Tensor, scale: torch.Tensor, offset: torch.Tensor, qmin: int, qmax: int,
              block_size: Optional[List] = None) -> torch.Tensor:
     """Differentiable quantization (torch_builtins.quantize, :151-194)."""
@@ -340,12 +403,14 @@ def quantize(tensor: torch.Tensor, scale: torch.Tensor, offset: torch.Tensor, qm
     if not _is_grid_representable(tensor.dtype, qmin, qmax):
         raise RuntimeError(
             f"{tensor.dtype} is unable to represent quantized output of range [{qmin}, {qmax}].")
-    _check_fp32_grid(tensor.dtype, qmin, qmax)
+    internal = _internal_dtype(tensor.dtype, qmin, qmax)
     orig_shape = tensor.shape
-    t = reshape_tensor_for_blocks(tensor, scale.shape, block_size)
-    s = scale.view(get_encoding_shape_with_blocks(scale.shape, block_size))
-    o = offset.view(get_encoding_shape_with_blocks(offset.shape, block_size))
-    return _Quantize.apply(t, s.to(torch.float32), o.to(torch.float32), qmin, qmax).view(orig_shape)
+    t, s, o = _blocked(tensor, scale, offset, block_size)
+    enc_shape = _enc_shape(s, o, t.dim())
+    sv, ov = _enc_vectors(s, o, internal, enc_shape)
+    scalar = s.dim() == 0 and t.dim() > 0 and internal != t.dtype
+    return _Quantize.apply(t, sv, ov, int(qmin), int(qmax), _Plan(t.shape, enc_shape),
+                           _numerics(t.dtype, internal, 0.0, scalar)).view(orig_shape)
 
 
 def dequantize(tensor: torch.Tensor, scale: torch.Tensor, offset: torch.Tensor,
@@ -354,10 +419,11 @@ def dequantize(tensor: torch.Tensor, scale: torch.Tensor, offset: torch.Tensor,
     _validate_arguments(tensor, scale, block_size=block_size)
     _require(tensor, "tensor")
     orig_shape = tensor.shape
-    t = reshape_tensor_for_blocks(tensor, scale.shape, block_size)
-    s = scale.view(get_encoding_shape_with_blocks(scale.shape, block_size))
-    o = offset.view(get_encoding_shape_with_blocks(offset.shape, block_size))
-    return _Dequantize.apply(t, s.to(torch.float32), o.to(torch.float32)).view(orig_shape)
+    t, s, o = _blocked(tensor, scale, offset, block_size)
+    enc_shape = _enc_shape(s, o, t.dim())
+    sv, ov = _enc_vectors(s, o, t.dtype, enc_shape)
+    return _Dequantize.apply(t, sv, ov, _Plan(t.shape, enc_shape),
+                             _numerics(t.dtype, t.dtype)).view(orig_shape)
 
 
 def quantize_dequantize(tensor: torch.Tensor, scale: torch.Tensor, offset: torch.Tensor, qmin: int,
@@ -366,41 +432,52 @@ def quantize_dequantize(tensor: torch.Tensor, scale: torch.Tensor, offset: torch
     """Differentiable fake quantization (torch_builtins.quantize_dequantize, :199-284)."""
     _validate_arguments(tensor, scale, qmin, qmax, block_size)
     _require(tensor, "tensor")
-    if zero_point_shift != 0.0:
-        raise NotImplementedError("mi355x backend: zero_point_shift is not supported yet")
-    fast = block_size is None and not torch.jit.is_tracing()
+    fast = block_size is None and not torch.jit.is_tracing() and zero_point_shift == 0.0
     fast &= ((not scale.requires_grad and not getattr(offset, "requires_grad", False))
              or not torch.is_grad_enabled())
     if fast and _fast_path_layout(scale, offset, tensor, qmin, qmax):
-        if scale.dtype != torch.float32:
-            scale = scale.to(torch.float32)
-        return _QuantDequant.apply(tensor, scale, offset.to(torch.float32), int(qmin), int(qmax),
-                                   FROZEN)
-    _check_fp32_grid(tensor.dtype, qmin, qmax)
+        if max(abs(int(qmin)), abs(int(qmax))) > 1 << 24:
+            raise NotImplementedError(
+                "mi355x backend: frozen fake-quantization of grids beyond 2^24 (fp32 kernels)")
+        enc_shape = _enc_shape(scale, offset, tensor.dim())
+        sv = scale.detach().to(torch.float32).expand(enc_shape).reshape(-1).contiguous()
+        ov = offset.detach().to(torch.float32).expand(enc_shape).reshape(-1).contiguous()
+        return _QuantDequant.apply(tensor, sv, ov, int(qmin), int(qmax), FROZEN,
+                                   _Plan(tensor.shape, enc_shape),
+                                   _numerics(tensor.dtype, torch.float32))
+    internal = _internal_dtype(tensor.dtype, qmin, qmax)
+    if not _is_grid_representable(internal, qmin, qmax):
+        raise RuntimeError(
+            f"{internal} is unable to represent quantized output of range [{qmin}, {qmax}].")
     orig_shape = tensor.shape
-    t = reshape_tensor_for_blocks(tensor, scale.shape, block_size)
-    s = scale.view(get_encoding_shape_with_blocks(scale.shape, block_size)).to(torch.float32)
-    o = offset.view(get_encoding_shape_with_blocks(offset.shape, block_size)).to(torch.float32)
-    return _QuantDequant.apply(t, s, o, int(qmin), int(qmax), LEARNABLE).view(orig_shape)
+    t, s, o = _blocked(tensor, scale, offset, block_size)
+    enc_shape = _enc_shape(s, o, t.dim())
+    sv, ov = _enc_vectors(s, o, internal, enc_shape)
+    scalar = s.dim() == 0 and t.dim() > 0 and internal != t.dtype
+    return _QuantDequant.apply(t, sv, ov, int(qmin), int(qmax), LEARNABLE,
+                               _Plan(t.shape, enc_shape),
+                               _numerics(t.dtype, internal, zero_point_shift, scalar)
+                               ).view(orig_shape)
 
 
 def minmax(tensor: torch.Tensor, enc_shape) -> Tuple[torch.Tensor, torch.Tensor]:
-    """Min and max of ``tensor`` reduced to ``enc_shape`` (NaN propagates).
-
-    Kernel of ``_MinMaxObserver.collect_stats`` (encoding_analyzer.py:101-105)."""
+    """Min and max of ``tensor`` reduced to ``enc_shape`` (NaN propagates), in the tensor's
+    dtype.  Kernel of ``_MinMaxObserver.collect_stats`` (encoding_analyzer.py:101-105)."""
     _require(tensor, "tensor")
-    x = tensor.contiguous()
-    layout = kernel_layout(x.shape, enc_shape)
-    if layout is None:
-        raise NotImplementedError(
-            f"mi355x backend: cannot reduce shape {tuple(x.shape)} to {tuple(enc_shape)}")
-    outer, C, inner = layout
+    nd = tensor.dim()
+    enc = (1,) * (nd - len(enc_shape)) + tuple(int(d) for d in enc_shape)
+    plan = _Plan(tensor.shape, enc)
+    x = plan.to_kernel(tensor)
+    if x.numel() == 0:
+        raise RuntimeError("mi355x backend: min/max of an empty tensor")
+    C = plan.C
     mn = torch.empty(C, dtype=torch.float32, device=x.device)
     mx = torch.empty(C, dtype=torch.float32, device=x.device)
-    ws = _workspace(outer, C, inner, x.device)
-    _rx.call("rxmet_qdq_minmax", _rx.ptr(x), outer, C, inner, _rx.ptr(mn), _rx.ptr(mx), _rx.ptr(ws),
-             _rx.stream_of(x.device))
-    return mn.view(tuple(enc_shape)), mx.view(tuple(enc_shape))
+    ws = _workspace(plan, x.dtype, x.device)
+    _rx.call("rxmet_qdq_minmax_ex", _rx.ptr(x), _IO_CODE[x.dtype], plan.cstruct(), _rx.ptr(mn),
+             _rx.ptr(mx), _rx.ptr(ws), _rx.stream_of(x.device))
+    shape = tuple(enc_shape)
+    return mn.to(x.dtype).view(shape), mx.to(x.dtype).view(shape)
 
 
 class _MinMaxEncodings(torch.autograd.Function):

@@ -22,6 +22,23 @@ c_int = ctypes.c_int
 c_ptr = ctypes.c_void_p
 c_float = ctypes.c_float
 
+
+
+class QdqLayout(ctypes.Structure):
+    """rxmet_qdq_layout: [outer, C0, mid, C1, inner], encoding c0 * C1 + c1."""
+    _fields_ = [("outer", c_i64), ("C0", c_i64), ("mid", c_i64), ("C1", c_i64), ("inner", c_i64)]
+
+
+class QdqNumerics(ctypes.Structure):
+    """rxmet_qdq_numerics: io / internal element types, zero_point_shift, 0-dim scale."""
+    _fields_ = [("io_dtype", ctypes.c_int32), ("internal_dtype", ctypes.c_int32),
+                ("zero_point_shift", ctypes.c_double), ("scalar_scale", ctypes.c_int32),
+                ("reserved", ctypes.c_int32)]
+
+
+_LAY = ctypes.POINTER(QdqLayout)
+_NUM = ctypes.POINTER(QdqNumerics)
+
 # name -> (restype, argtypes); mirrors include/rxmet_qdq.h and include/rxmet_gru.h
 _SIGNATURES = {
     "rxmet_last_error": (ctypes.c_char_p, []),
@@ -41,6 +58,19 @@ _SIGNATURES = {
     "rxmet_dequantize_forward": (c_int, [c_ptr, c_ptr, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_ptr]),
     "rxmet_dequantize_backward": (c_int, [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64,
                                           c_ptr, c_ptr, c_ptr, c_ptr]),
+    "rxmet_qdq_workspace_bytes_ex": (c_i64, [_LAY, ctypes.c_int32]),
+    "rxmet_qdq_minmax_ex": (c_int, [c_ptr, ctypes.c_int32, _LAY, c_ptr, c_ptr, c_ptr, c_ptr]),
+    "rxmet_qdq_forward_ex": (c_int, [c_ptr, c_ptr, _LAY, _NUM, c_ptr, c_ptr, c_i64, c_i64, c_int,
+                                     c_ptr]),
+    "rxmet_qdq_backward_ex": (c_int, [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, _LAY, _NUM, c_ptr, c_ptr,
+                                      c_i64, c_i64, c_int, c_ptr, c_ptr]),
+    "rxmet_quantize_forward_ex": (c_int, [c_ptr, c_ptr, _LAY, _NUM, c_ptr, c_ptr, c_i64, c_i64,
+                                          c_ptr]),
+    "rxmet_quantize_backward_ex": (c_int, [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, _LAY, _NUM, c_ptr,
+                                           c_ptr, c_i64, c_i64, c_ptr, c_ptr]),
+    "rxmet_dequantize_forward_ex": (c_int, [c_ptr, c_ptr, _LAY, _NUM, c_ptr, c_ptr, c_ptr]),
+    "rxmet_dequantize_backward_ex": (c_int, [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, _LAY, _NUM, c_ptr,
+                                             c_ptr, c_ptr, c_ptr]),
     "rxmet_selftest_mfma": (c_int, [c_int, c_ptr, c_ptr, c_ptr, c_ptr]),
     "rxmet_qdq_encoding_forward": (c_int, [c_ptr, c_ptr, c_i64, c_i64, c_i64, ctypes.c_int32,
                                            ctypes.c_float, ctypes.c_float, c_ptr, c_ptr, c_ptr]),

@@ -178,7 +178,9 @@ def _module_case(cuda, shape, enc_shape, bits, symmetric, seed, learn=True):
     xg = xd.clone().requires_grad_()
     y = q(xg)
     y.backward(_t(g, cuda))
-    layout = Q.kernel_layout(shape, enc_shape)
+    lay5 = Q.kernel_layout(shape, enc_shape)
+    assert lay5[0] == lay5[1] == 1  # one encoding group
+    layout = lay5[2:]
     C = layout[1]
     mn, mx = O.minmax(x, layout)
     qmin, qmax = q.qmin, q.qmax

@@ -287,3 +287,202 @@ def test_gpu_scalar_division_is_reciprocal_multiply():
     a = np.array([1.0, 3.0, 0.7, 1e-3], f32)
     np.testing.assert_array_equal(O.sdiv(a, 255, True), (a * f32(f32(1) / f32(255))).astype(f32))
     np.testing.assert_array_equal(O.sdiv(a, 255, False), (a / f32(255)).astype(f32))
+
+
+# ---------------------------------------------------------------------------------
+# General numerics (fp16 / bf16 tensors, internal types, zero_point_shift, any encoding
+# shape).  The reference's operation sequence run by torch on CPU tensors of the real
+# dtypes pins the oracle's per-operation rounding; torch's own casts pin round_to.
+# ---------------------------------------------------------------------------------
+
+TDT = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16, "f64": torch.float64}
+
+
+def _internal(io, qmin, qmax):
+    """torch_builtins' widening rule (:85-101, 255-262) on the io type's eps."""
+    for dt in (io, "f32", "f64"):
+        eps = torch.finfo(TDT[dt]).eps
+        if qmin == qmax or not eps > 1e-1 / (qmax - qmin):
+            return dt
+    return "f64"
+
+
+def _edge_values():
+    v = [0.0, -0.0, 1.0, 1.5, 2.5, -2.5, 65504.0, 65520.0, 65519.99, 1e-8, 6e-8, 2.0 ** -24,
+         2.0 ** -25, 3.0 * 2.0 ** -26, 1 + 2.0 ** -8, 1 + 3 * 2.0 ** -9, 1 + 2.0 ** -9,
+         3.3895314e38, np.inf, -np.inf, np.nan, 1e-40, -1e-40]
+    return np.concatenate([np.array(v, f32), _data(5000, 40) * f32(3.7)])
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+def test_round_to_matches_torch_casts(dt):
+    v = _edge_values()
+    exp = torch.from_numpy(v).to(TDT[dt]).float().numpy()
+    with np.errstate(over="ignore"):
+        got = O.round_to(v, dt)
+    np.testing.assert_array_equal(got, exp)
+    # fp64 values reach 16-bit types through fp32, as torch's .to() does
+    d = np.array([1 + 2.0 ** -11 + 2.0 ** -40, 1 + 2.0 ** -8 + 2.0 ** -30], np.float64)
+    exp = torch.from_numpy(d).to(TDT[dt]).float().numpy()
+    np.testing.assert_array_equal(O.to_io(d, dt), exp)
+
+
+def _torch_qdq(x, scale, offset, qmin, qmax, io, internal, shift):
+    """quantize_dequantize's learnable path (torch_builtins.py:255-284 + :640-672) as torch
+    operations on CPU tensors of the real dtypes (dimensioned encodings)."""
+    R = TDT[internal]
+    xt = torch.from_numpy(x).to(TDT[io])
+    s = torch.from_numpy(scale).to(R)
+    o = torch.from_numpy(offset).to(R)
+    sh = torch.sub(xt, s, alpha=shift) if shift else xt
+    x_round = torch.round(sh.to(R) / s).sub_(o)
+    mask = (qmin <= x_round) & (x_round <= qmax)
+    y = x_round.clamp_(qmin, qmax).add_(o).mul_(s)
+    if shift:
+        y = torch.add(y, s, alpha=shift)
+    return y.to(TDT[io]).float().numpy(), mask.numpy()
+
+
+def _torch_qdq_backward(x, g, scale, offset, qmin, qmax, io, internal, shift):
+    """QuantDequantFunc.backward (:675-691) and the shift's add/sub gradients, elementwise in
+    the real dtypes, summed to the encoding shape in fp64."""
+    R = TDT[internal]
+    xt = torch.from_numpy(x).to(TDT[io])
+    gt = torch.from_numpy(g).to(TDT[io]).to(R)
+    s = torch.from_numpy(scale).to(R)
+    o = torch.from_numpy(offset).to(R)
+    sh = torch.sub(xt, s, alpha=shift) if shift else xt
+    t = sh.to(R) / s
+    x_round = torch.round(t) - o
+    mask = (qmin <= x_round) & (x_round <= qmax)
+    ds = gt * (torch.round(t).clamp(o + qmin, o + qmax) - (t * mask))
+    do = gt * (~mask * s)
+    dx = gt * mask
+    ds64 = ds.double()
+    if shift:
+        ds64 = ds64 + (gt * shift).double() + (-(dx * shift)).double()
+    enc = tuple(np.broadcast_shapes(scale.shape, offset.shape))
+    return (dx.to(TDT[io]).float().numpy(), O._sum_to(ds64.numpy(), enc),
+            O._sum_to(do.double().numpy(), enc))
+
+
+CASES = [  # io, (qmin, qmax)
+    ("f16", (-8, 7)), ("f16", (0, 63)), ("f16", (-128, 127)), ("bf16", (-4, 3)),
+    ("bf16", (0, 255)), ("f32", (-128, 127)), ("f32", (0, (1 << 22) - 1)),
+]
+
+
+@pytest.mark.parametrize("io,grid", CASES, ids=[f"{c[0]}-{c[1][1]}" for c in CASES])
+@pytest.mark.parametrize("shift", [0.0, 0.5])
+@pytest.mark.parametrize("enc", ["per_tensor", "per_channel", "two_axes"])
+def test_general_oracle_matches_torch_on_cpu(io, grid, shift, enc):
+    qmin, qmax = grid
+    internal = _internal(io, qmin, qmax)
+    g = np.random.default_rng(qmax + int(shift * 10))
+    shape = (6, 5, 40)
+    enc_shape = {"per_tensor": (1,), "per_channel": (5, 1), "two_axes": (6, 1, 40)}[enc]
+    x = O.round_to(_data(int(np.prod(shape)), qmax).reshape(shape) * f32(0.8), io)
+    x.reshape(-1)[:6] = [np.nan, np.inf, -np.inf, 0.0, -0.0, 1e-3]
+    gr = O.round_to(g.standard_normal(shape).astype(f32), io)
+    steps = qmax - qmin
+    scale = O.round_to((g.random(enc_shape) * 2 + 0.5).astype(f32) / f32(steps), internal)
+    offset = np.full(enc_shape, f32(-round((qmin + qmax) / 2) if qmin < 0 else -(steps // 3)))
+    scale, offset = scale.astype(f32), offset.astype(f32)
+    y, mask = O.qdq_general(x, scale, offset, qmin, qmax, io, internal, shift)
+    ey, emask = _torch_qdq(x, scale, offset, qmin, qmax, io, internal, shift)
+    np.testing.assert_array_equal(y, ey)
+    np.testing.assert_array_equal(mask, emask)
+    dx, ds, do = O.qdq_general_backward(x, gr, scale, offset, qmin, qmax, io, internal, shift)
+    edx, eds, edo = _torch_qdq_backward(x, gr, scale, offset, qmin, qmax, io, internal, shift)
+    np.testing.assert_array_equal(dx, edx)
+    # the oracle's sums are rounded to the internal type; the reference rounds its sum too
+    ulp = 2.0 ** -10 if internal == "f16" else 2.0 ** -7 if internal == "bf16" else 1e-6
+    for a, e in ((ds, eds), (do, edo)):
+        fin = np.isfinite(e)
+        if fin.any():
+            np.testing.assert_allclose(a[fin], e[fin], rtol=ulp,
+                                       atol=ulp * np.abs(e[fin]).max())
+        assert np.array_equal(np.isnan(a), np.isnan(e))
+
+
+@pytest.mark.parametrize("io", ["f16", "bf16", "f32"])
+def test_shift_grid_invariant(io):
+    """With a power-of-two scale every step is exact: y = (k + offset + shift) * scale for an
+    integer k in [qmin, qmax], inputs beyond the grid land on its ends, and a NaN stays NaN."""
+    qmin, qmax, s, o = -8, 7, 2.0 ** -3, 0.0
+    internal = _internal(io, qmin, qmax)
+    x = O.round_to(np.linspace(-3, 3, 401).astype(f32), io)
+    y, _ = O.qdq_general(x, f32(s), f32(o), qmin, qmax, io, internal, 0.5)
+    k = y / s - 0.5 - o
+    np.testing.assert_array_equal(k, np.rint(k))
+    assert k.min() == qmin and k.max() == qmax
+    # the nearest grid point: |x - y| <= s / 2 inside the grid
+    inside = (x >= (qmin + 0.5) * s) & (x <= (qmax + 0.5) * s)
+    assert np.all(np.abs(x[inside] - y[inside]) <= s / 2)
+    assert np.isnan(O.qdq_general(np.array([np.nan], f32), f32(s), f32(o), qmin, qmax, io,
+                                  internal, 0.5)[0][0])
+
+
+def test_general_oracle_equals_fp32_oracle():
+    """io = internal = fp32 without a shift reduces to the [outer, C, inner] oracle."""
+    x = _data(3 * 7 * 50, 41).reshape(3, 7, 50)
+    g = _data(x.size, 42).reshape(x.shape)
+    s = (np.random.default_rng(43).random(7) * 0.05 + 0.01).astype(f32)
+    o = np.full(7, f32(-3))
+    y, m = O.qdq_general(x, s.reshape(7, 1), o.reshape(7, 1), -8, 7)
+    ey, em = O.qdq_learnable(x, s, o, -8, 7, (3, 7, 50))
+    np.testing.assert_array_equal(y, ey)
+    dx, ds, do = O.qdq_general_backward(x, g, s.reshape(7, 1), o.reshape(7, 1), -8, 7)
+    edx, eds, edo = O.qdq_learnable_backward(x, g, s, o, -8, 7, (3, 7, 50))
+    np.testing.assert_array_equal(dx, edx)
+    np.testing.assert_array_equal(ds.reshape(-1), eds)
+    np.testing.assert_array_equal(do.reshape(-1), edo)
+    q = O.quantize_general(x, s.reshape(7, 1), o.reshape(7, 1), 0, 15)
+    np.testing.assert_array_equal(q, O.quantize(x, s, o, 0, 15, (3, 7, 50)))
+    qd = O.quantize_general_backward(x, g, s.reshape(7, 1), o.reshape(7, 1), 0, 15)
+    eq = O.quantize_backward(x, g, s, o, 0, 15, (3, 7, 50))
+    np.testing.assert_array_equal(qd[0], eq[0])
+    np.testing.assert_array_equal(qd[1].reshape(-1), eq[1])
+    np.testing.assert_array_equal(qd[2].reshape(-1), eq[2])
+    dq = O.dequantize_general(q, s.reshape(7, 1), o.reshape(7, 1))
+    np.testing.assert_array_equal(dq, O.dequantize(q, s, o, (3, 7, 50)))
+
+
+@pytest.mark.parametrize("io,grid", [("f16", (-8, 7)), ("bf16", (0, 255)), ("f16", (0, 255))])
+def test_quantize_and_dequantize_general_match_torch(io, grid):
+    qmin, qmax = grid
+    internal = _internal(io, qmin, qmax)
+    x = O.round_to(_data(4 * 300, 44).reshape(4, 300), io)
+    g = O.round_to(_data(x.size, 45).reshape(x.shape), io)
+    scale = O.round_to(np.array([[0.05], [0.11], [0.013], [0.3]], f32), internal)
+    offset = np.array([[0.0], [-2.0], [3.0], [-1.0]], f32)
+    R, T = TDT[internal], TDT[io]
+    xt, gt = torch.from_numpy(x).to(T), torch.from_numpy(g).to(T)
+    s, o = torch.from_numpy(scale).to(R), torch.from_numpy(offset).to(R)
+    # QuantizeFunc.forward / backward (:527-571) in R, result .to(T)
+    x_round = torch.round(xt.to(R) / s).sub_(o)
+    mask = (x_round >= qmin) * (x_round <= qmax)
+    q_ref = x_round.clamp_(qmin, qmax).to(T).float().numpy()
+    np.testing.assert_array_equal(O.quantize_general(x, scale, offset, qmin, qmax, io, internal),
+                                  q_ref)
+    mg = gt.to(R) * mask
+    dx_ref = (mg / s).to(T).float().numpy()
+    ds_ref = O._sum_to((-(mg / s) * (xt / s)).double().numpy(), scale.shape)
+    dx, ds, do = O.quantize_general_backward(x, g, scale, offset, qmin, qmax, io, internal)
+    np.testing.assert_array_equal(dx, dx_ref)
+    ulp = 2.0 ** -10 if internal == "f16" else 2.0 ** -7 if internal == "bf16" else 1e-6
+    np.testing.assert_allclose(ds, ds_ref, rtol=ulp, atol=ulp * np.abs(ds_ref).max())
+    np.testing.assert_allclose(do, O._sum_to((-mg).double().numpy(), scale.shape), rtol=ulp)
+    # DequantizeFunc (:589-615) in the tensor's type
+    qt = torch.from_numpy(q_ref).to(T)
+    sT, oT = s.to(T), o.to(T)
+    y_ref = (qt + oT).mul_(sT).float().numpy()
+    sv, ov = O.round_to(scale, io), O.round_to(offset, io)
+    np.testing.assert_array_equal(O.dequantize_general(q_ref, sv, ov, io), y_ref)
+    gq, dsq, doq = O.dequantize_general_backward(q_ref, g, sv, ov, io)
+    np.testing.assert_array_equal(gq, (gt * sT).float().numpy())
+    ulp_io = 2.0 ** -10 if io == "f16" else 2.0 ** -7
+    eds = O._sum_to((gt * (qt + oT)).double().numpy(), scale.shape)
+    np.testing.assert_allclose(dsq, eds, rtol=ulp_io, atol=ulp_io * np.abs(eds).max())
+    edo = O._sum_to((gt * sT).double().numpy(), scale.shape)
+    np.testing.assert_allclose(doq, edo, rtol=ulp_io, atol=ulp_io * np.abs(edo).max())
