@@ -15,8 +15,10 @@ its forward runs on the GPU.
 """
 from __future__ import annotations
 
+import copy
 import json
 import math
+import re
 from contextlib import contextmanager
 from typing import Optional, Tuple
 
@@ -202,7 +204,7 @@ def _operators_to_json(cfg, qp: "gru_ops.GRUQuantParams") -> dict:
               "scale": _one_or_list(scales), "zero_point": _one_or_list(zps), "enc_type": enc,
               "real_min": _one_or_list([sc * (qmin - z) for sc, z in zip(scales, zps)]),
               "real_max": _one_or_list([sc * (qmax - z) for sc, z in zip(scales, zps)])}
-        (per_channel if enc != "PER_TENSOR" or name in _JSON_CHAN else per_tensor)[name] = op
+        (per_channel if enc != "PER_TENSOR" else per_tensor)[name] = op
     per_tensor.update(per_channel)
     return per_tensor
 
@@ -256,6 +258,159 @@ def _operators_from_json(ops: dict, cfg, hidden: int) -> "gru_ops.GRUQuantParams
     qp.struct.use_pot2 = int(bool(cfg.usePOT2_))
     qp.bitwidth_config_ = cfg
     return qp
+
+
+# ------------------------------------------------------------------------------------
+# AIMET encodings (quant_gru.py:2593-3592): the operators dict above rewritten into an
+# AIMET encodings dictionary — activation_encodings[module] {input, output, internal_ops
+# (+ internal_ops_reverse)}, param_encodings[module.weight_ih.weight / .weight_hh.weight /
+# .bias] (the reverse direction appended to every list; the bias as [bias_ih, bias_hh] per
+# direction) — and back.
+# ------------------------------------------------------------------------------------
+
+# the 13 internal-op slots of the skeleton, in its key order
+_AIMET_SLOTS = ("add_final_hidden", "mul_new_contribution", "mul_old_contribution",
+                "mul_reset_hidden", "new_gate_input", "new_gate_output", "reset_gate_input",
+                "reset_gate_output", "sub_one_minus_update", "update_gate_input",
+                "update_gate_output", "weight_ih_linear", "weight_hh_linear")
+# the 11 operators stored under their own name, in export order
+_AIMET_OWN = ("weight_ih_linear", "weight_hh_linear", "update_gate_input", "update_gate_output",
+              "reset_gate_input", "reset_gate_output", "new_gate_input", "new_gate_output",
+              "mul_reset_hidden", "mul_old_contribution", "mul_new_contribution")
+# slots that carry another operator's encoding
+_AIMET_ALIAS = {"add_final_hidden": "output", "sub_one_minus_update": "update_gate_output"}
+_AIMET_LIST_FIELDS = ("scale", "zero_point", "real_min", "real_max")
+_AIMET_DROP = ("multiplier", "shift", "scale_encoding", "n", "exp2_inv")
+
+
+def _encoding_n(scale):
+    """round(-log2(scale)) per scale (quant_gru.py:4039-4046)."""
+    if isinstance(scale, list):
+        if not scale:
+            raise ValueError("Encoding scale cannot be empty")
+        return [_encoding_n(v) for v in scale]
+    if isinstance(scale, bool) or not isinstance(scale, (int, float)) or \
+            not math.isfinite(scale) or scale <= 0:
+        raise ValueError("Encoding scale must be positive and finite")
+    return int(round(-math.log2(scale)))
+
+
+def _validate_encoding_n(value) -> None:
+    """Every encoding that states n must state the n of its scale (quant_gru.py:4049-4065)."""
+    if isinstance(value, list):
+        for v in value:
+            _validate_encoding_n(v)
+        return
+    if not isinstance(value, dict):
+        return
+    if "scale" not in value:
+        for v in value.values():
+            _validate_encoding_n(v)
+        return
+    if "n" not in value:
+        return
+
+    def same(a, e):
+        if isinstance(e, list):
+            return isinstance(a, list) and len(a) == len(e) and all(map(same, a, e))
+        return type(a) is int and a == e
+
+    if not same(value["n"], _encoding_n(value["scale"])):
+        raise ValueError("Encoding n does not match scale")
+
+
+def _aimet_zero_points(op: dict) -> dict:
+    """A list of scales gets a zero point per scale (quant_gru.py:2593-2626)."""
+    if not isinstance(op, dict) or not isinstance(op.get("scale"), list):
+        return op
+    n = len(op["scale"])
+    zp = op.get("zero_point", 0)
+    if not isinstance(zp, list):
+        op["zero_point"] = [zp] * n
+    elif len(zp) == 1:
+        op["zero_point"] = zp * n
+    elif not zp:
+        op["zero_point"] = [0] * n
+    elif len(zp) != n:
+        raise ValueError(f"zero_point length mismatch: expected {n}, got {len(zp)}")
+    return op
+
+
+def _aimet_encoding(op: dict) -> dict:
+    """One operator as an AIMET encoding (quant_gru.py:2628-2672): bitwidth from dtype,
+    is_symmetric as "True"/"False", execution fields dropped, n derived from the scale."""
+    if not isinstance(op, dict):
+        return op
+    enc = copy.deepcopy(op)
+    m = re.fullmatch(r"U?INT([1-9][0-9]*)", str(enc.get("dtype", "")))
+    if m:
+        enc["bitwidth"] = int(m.group(1))
+    if "symmetric" in enc:
+        enc["is_symmetric"] = "True" if enc.pop("symmetric") else "False"
+    if isinstance(enc.get("is_symmetric"), bool):
+        enc["is_symmetric"] = "True" if enc["is_symmetric"] else "False"
+    for key in _AIMET_DROP:
+        enc.pop(key, None)
+    if "scale" in enc:
+        enc["n"] = _encoding_n(enc["scale"])
+    return enc
+
+
+def _append_fields(dst: Optional[dict], src: Optional[dict], fields=_AIMET_LIST_FIELDS):
+    """dst's list fields followed by src's (scalars become lists)."""
+    if dst is None:
+        return copy.deepcopy(src)
+    if src is None:
+        return dst
+    for f in fields:
+        if f not in src:
+            continue
+        if f not in dst:
+            dst[f] = copy.deepcopy(src[f])
+            continue
+        a, b = dst[f], src[f]
+        dst[f] = (a if isinstance(a, list) else [a]) + (list(b) if isinstance(b, list) else [b])
+    return dst
+
+
+def _aimet_skeleton() -> dict:
+    return {slot: {"output": []} for slot in _AIMET_SLOTS}
+
+
+def _aimet_fill_internal(slots: dict, ops: dict) -> None:
+    for name in _AIMET_OWN + tuple(_AIMET_ALIAS):
+        src = ops.get(_AIMET_ALIAS.get(name, name))
+        if src is None:
+            continue
+        enc = _aimet_encoding(_aimet_zero_points(copy.deepcopy(src)))
+        if isinstance(slots.get(name), dict) and "output" in slots[name]:
+            slots[name]["output"] = [enc]
+        else:
+            slots[name] = enc
+
+
+def _aimet_first(entry):
+    """An encoding stored as {"0": enc}, [enc, ...], {"output": [enc]} or enc itself."""
+    if isinstance(entry, dict) and "output" in entry:
+        out = entry["output"]
+        return out[0] if isinstance(out, list) and out else (out if isinstance(out, dict) else None)
+    if isinstance(entry, dict) and "0" in entry:
+        return entry["0"]
+    if isinstance(entry, list):
+        return entry[0] if entry else None
+    return entry if isinstance(entry, dict) else None
+
+
+def _aimet_split(op: dict, parts: int) -> list:
+    """Cut every list field of an encoding into `parts` equal pieces (scalars repeated)."""
+    out = [copy.deepcopy(op) for _ in range(parts)]
+    for f in ("scale", "multiplier", "shift", "real_min", "real_max", "zero_point"):
+        v = op.get(f)
+        if isinstance(v, list):
+            n = len(v) // parts
+            for k in range(parts):
+                out[k][f] = v[k * n:(k + 1) * n] if k < parts - 1 else v[k * n:]
+    return out
 
 
 # ------------------------------------------------------------------------------------
@@ -672,6 +827,161 @@ class QuantGRU(nn.Module):
         self._quant_params_dirty = False
         if verbose:
             print(f"[QuantGRU] quant params loaded from {import_path}")
+
+    # -- AIMET encodings (quant_gru.py:2674-3592) --------------------------------------
+
+    def export_quant_params_to_aimet_format(self, encodings_dict: dict, module_name: str = None,
+                                            verbose: bool = False, *,
+                                            for_onnx: bool = True) -> dict:
+        """Merge this layer's grids into an AIMET encodings dictionary and return it.  An
+        uncalibrated layer is skipped (the dictionary comes back unchanged); a
+        "tensor_encodings" entry is removed, as the reference does for older loaders."""
+        if not self.is_calibrated():
+            if verbose:
+                print(f"[QuantGRU] {module_name or 'unknown'} is not calibrated; not exported")
+            return encodings_dict
+        self._ensure_quant_params_fresh()
+        name = module_name or self._module_name or "gru"
+        ops = _operators_to_json(self._bitwidth_config, self.quant_params)
+        rev = None
+        if self.bidirectional and self.quant_params_reverse is not None:
+            rev = _operators_to_json(self._bitwidth_config, self.quant_params_reverse)
+        encodings_dict.setdefault("schema_version", 3)
+        acts = encodings_dict.setdefault("activation_encodings", {})
+        if name not in acts:
+            acts[name] = {"is_GRU": True, "input": {}, "output": {},
+                          "internal_ops": _aimet_skeleton()}
+            if self.bidirectional:
+                acts[name]["internal_ops_reverse"] = _aimet_skeleton()
+        params = encodings_dict.setdefault("param_encodings", {})
+        encodings_dict.setdefault("tensor_encodings", {})
+        layer = acts[name]
+        if self.bidirectional and "internal_ops_reverse" not in layer:
+            layer["internal_ops_reverse"] = _aimet_skeleton()
+
+        def enc(op):
+            return _aimet_encoding(_aimet_zero_points(copy.deepcopy(op)))
+
+        layer["input"] = {"0": enc(ops["input"])}
+        layer["output"] = {"0": enc(ops["output"])}
+        for key, op in (("weight_ih.weight", "weight_ih"), ("weight_hh.weight", "weight_hh")):
+            data = _aimet_zero_points(copy.deepcopy(ops[op]))
+            if rev is not None:
+                data = _append_fields(data, _aimet_zero_points(copy.deepcopy(rev[op])))
+            params[f"{name}.{key}"] = _aimet_encoding(data)
+        for op in ("bias_ih", "bias_hh"):
+            if op not in ops:
+                raise ValueError(f"{name}.bias needs both bias_ih and bias_hh (missing {op})")
+        bias = _aimet_zero_points(copy.deepcopy(ops["bias_ih"]))
+        bias = _append_fields(bias, _aimet_zero_points(copy.deepcopy(ops["bias_hh"])))
+        if rev is not None:
+            for op in ("bias_ih", "bias_hh"):
+                bias = _append_fields(bias, _aimet_zero_points(copy.deepcopy(rev[op])))
+        params[f"{name}.bias"] = _aimet_encoding(bias)
+        _aimet_fill_internal(layer["internal_ops"], ops)
+        if rev is not None and "internal_ops_reverse" in layer:
+            _aimet_fill_internal(layer["internal_ops_reverse"], rev)
+        encodings_dict.pop("tensor_encodings", None)
+        if verbose:
+            print(f"[QuantGRU] {name} exported to AIMET encodings")
+        return encodings_dict
+
+    def load_quant_params_from_aimet_format(self, encodings_dict: dict, module_name: str = None,
+                                            verbose: bool = False) -> bool:
+        """Read this layer's grids from an AIMET encodings dictionary.  Returns False when the
+        layer's entries are missing or do not parse; an n that contradicts its scale raises
+        ValueError.  Scales that are all powers of two select the POT2 execution mode."""
+        name = module_name or self._module_name or "gru"
+        self._module_name = name
+
+        def fail(msg):
+            if verbose:
+                print(f"[QuantGRU] {name}: {msg}")
+            return False
+
+        acts = encodings_dict.get("activation_encodings")
+        if not isinstance(acts, dict):
+            return fail("no activation_encodings")
+        if name not in acts:
+            return fail("no activation_encodings entry for this module")
+        layer = acts[name]
+        _validate_encoding_n(layer)
+        params = encodings_dict.get("param_encodings", {})
+        for suffix in ("weight_ih.weight", "weight_hh.weight", "bias"):
+            _validate_encoding_n(params.get(f"{name}.{suffix}"))
+        if layer.get("is_GRU") is not True and verbose:
+            print(f"[QuantGRU] {name}: is_GRU is not True")
+        bidir = self.bidirectional
+        ops, rev = {}, ({} if bidir else None)
+        for key in ("input", "output"):
+            if key not in layer or _aimet_first(layer[key]) is None:
+                return fail(f"no {key!r} encoding")
+            ops[key] = copy.deepcopy(_aimet_first(layer[key]))
+        if bidir:
+            rev["input"] = copy.deepcopy(ops["input"])  # both directions read one x
+        if "param_encodings" in encodings_dict:
+            for key, op in (("weight_ih.weight", "weight_ih"), ("weight_hh.weight", "weight_hh")):
+                data = params.get(f"{name}.{key}")
+                if data is None:
+                    return fail(f"no param encoding {name}.{key}")
+                if bidir:
+                    ops[op], rev[op] = _aimet_split(data, 2)
+                else:
+                    ops[op] = copy.deepcopy(data)
+            data = params.get(f"{name}.bias")
+            if data is None:
+                return fail(f"no param encoding {name}.bias")
+            if bidir:
+                n = next((len(data[f]) for f in _AIMET_LIST_FIELDS
+                          if isinstance(data.get(f), list)), None)
+                if n is None or n % 4:
+                    return fail("cannot split the bias into two directions")
+                ops["bias_ih"], ops["bias_hh"], rev["bias_ih"], rev["bias_hh"] = \
+                    _aimet_split(data, 4)
+            else:
+                ops["bias_ih"], ops["bias_hh"] = _aimet_split(data, 2)
+        elif verbose:
+            print(f"[QuantGRU] {name}: no param_encodings")
+        for slots_key, dst in (("internal_ops", ops), ("internal_ops_reverse", rev)):
+            slots = layer.get(slots_key)
+            if dst is None or not isinstance(slots, dict):
+                continue
+            for op in _AIMET_OWN:
+                if op in slots and _aimet_first(slots[op]) is not None:
+                    dst[op] = copy.deepcopy(_aimet_first(slots[op]))
+            if dst is rev and "add_final_hidden" in slots:
+                first = _aimet_first(slots["add_final_hidden"])
+                if first is not None:
+                    rev["output"] = copy.deepcopy(first)
+        for d in (ops, rev):
+            for op in (d or {}).values():
+                if isinstance(op, dict) and "is_symmetric" in op:
+                    v = op.pop("is_symmetric")
+                    op["symmetric"] = v.lower() == "true" if isinstance(v, str) else bool(v)
+        try:
+            scales = []
+            for d in (ops, rev):
+                for op in (d or {}).values():
+                    sc = op.get("scale", [])
+                    scales.extend(sc if isinstance(sc, list) else [sc])
+            pot2 = bool(scales) and all(
+                isinstance(v, (int, float)) and v > 0 and math.isfinite(v)
+                and math.frexp(v)[0] == 0.5 for v in scales)
+            cfg = gru_ops.OperatorQuantConfig()
+            cfg.usePOT2_ = pot2
+            qp = _operators_from_json(ops, cfg, self.hidden_size)
+            qpr = _operators_from_json(rev, cfg, self.hidden_size) if bidir and rev else None
+        except (ValueError, KeyError, TypeError) as e:
+            return fail(f"could not load the encodings: {e}")
+        self._bitwidth_config = cfg
+        self._use_pot2_scale = pot2
+        self.quant_params = qp
+        if bidir:
+            self.quant_params_reverse = qpr
+        self._quant_params_dirty = False
+        if verbose:
+            print(f"[QuantGRU] {name} loaded from AIMET encodings")
+        return True
 
     # -- calibration state -------------------------------------------------------------
 

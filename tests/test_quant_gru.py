@@ -274,3 +274,96 @@ def test_int_io_entry_points_check_their_arguments():
         m.forward_quantized(torch.zeros(2, 1, 3, dtype=torch.int32))
     with pytest.raises(ValueError, match="quant_storage_dtype"):
         Q.QuantGRU(3, 4, quant_storage_dtype="int16")
+
+
+def _same_grids(m, n):
+    import numpy as np
+    import rxmet_gru_abi as A
+    pairs = [(m.quant_params, n.quant_params)]
+    if m.bidirectional:
+        pairs.append((m.quant_params_reverse, n.quant_params_reverse))
+    for a, b in pairs:
+        for name in A.GRID_NAMES:
+            assert a.scale(name) == b.scale(name), name
+            assert a.zero_point(name) == b.zero_point(name), name
+            ga, gb = a.struct.g[A.GRID[name]], b.struct.g[A.GRID[name]]
+            assert (ga.bits, bool(ga.is_unsigned)) == (gb.bits, bool(gb.is_unsigned)), name
+        for k, name in enumerate(A.CHAN_NAMES):
+            np.testing.assert_array_equal(a.channel_scales(name), b.channel_scales(name))
+            assert a.struct.chan_bits[k] == b.struct.chan_bits[k]
+        assert a.struct.use_pot2 == b.struct.use_pot2
+
+
+@pytest.mark.parametrize("bidirectional", [False, True])
+@pytest.mark.parametrize("pot2", [False, True])
+def test_aimet_encodings_round_trip(bidirectional, pot2):
+    """export_quant_params_to_aimet_format -> load_quant_params_from_aimet_format into a fresh
+    module gives the same grids (quant_gru.py:2674-3592), through a JSON round trip."""
+    import json
+    import math
+    import numpy as np
+    import rxmet_gru_abi as A
+    H = 16
+    m = Q.QuantGRU(6, H, bidirectional=bidirectional)
+    m.set_all_bitwidth(8, is_symmetric=False)
+    m._bitwidth_config.h_ = 16
+    m._bitwidth_config.W_granularity_ = A.PER_CHANNEL
+    m.use_po2_scale = pot2
+    _calibrated_on_host(m, 5)
+    enc = json.loads(json.dumps(m.export_quant_params_to_aimet_format(
+        {"tensor_encodings": {"old": 1}}, "enc.gru")))
+    assert enc["schema_version"] == 3 and "tensor_encodings" not in enc
+    layer = enc["activation_encodings"]["enc.gru"]
+    assert layer["is_GRU"] is True and set(layer["input"]) == {"0"}
+    assert list(layer["internal_ops"]) == list(Q._AIMET_SLOTS)
+    assert ("internal_ops_reverse" in layer) == bidirectional
+    out = layer["output"]["0"]
+    assert out["bitwidth"] == 16 and out["is_symmetric"] == "False" and "symmetric" not in out
+    assert out["n"] == int(round(-math.log2(out["scale"])))
+    assert layer["internal_ops"]["add_final_hidden"]["output"] == [out]
+    assert layer["internal_ops"]["sub_one_minus_update"]["output"] == \
+        layer["internal_ops"]["update_gate_output"]["output"]
+    dirs = [m.quant_params] + ([m.quant_params_reverse] if bidirectional else [])
+    w = enc["param_encodings"]["enc.gru.weight_ih.weight"]
+    np.testing.assert_array_equal(np.float32(w["scale"]),
+                                  np.concatenate([q.channel_scales("W") for q in dirs]))
+    assert w["zero_point"] == [0] * len(w["scale"]) and w["n"] == Q._encoding_n(w["scale"])
+    b = enc["param_encodings"]["enc.gru.bias"]
+    parts = []
+    for q in dirs:
+        parts += [q.channel_scales("bw"), q.channel_scales("br")]
+    np.testing.assert_array_equal(np.float32(b["scale"]), np.concatenate(parts))
+    n = Q.QuantGRU(6, H, bidirectional=bidirectional)
+    assert n.load_quant_params_from_aimet_format(enc, "enc.gru")
+    assert n.is_calibrated() and n._module_name == "enc.gru"
+    _same_grids(m, n)
+    for attr in ("x_", "h_", "W_", "R_", "h_symmetric_", "update_gate_output_unsigned_",
+                 "W_granularity_"):
+        assert getattr(m._bitwidth_config, attr) == getattr(n._bitwidth_config, attr), attr
+    # the same dictionary comes out again
+    again = n.export_quant_params_to_aimet_format({}, "enc.gru")
+    assert json.loads(json.dumps(again)) == enc
+
+
+def test_aimet_encodings_checks():
+    m = Q.QuantGRU(6, 16)
+    assert m.export_quant_params_to_aimet_format({"a": 1}) == {"a": 1}  # not calibrated
+    _calibrated_on_host(m, 6)
+    enc = m.export_quant_params_to_aimet_format({})
+    assert "gru" in enc["activation_encodings"]  # default module name
+    n = Q.QuantGRU(6, 16)
+    assert n.load_quant_params_from_aimet_format(enc, "other") is False
+    assert n.load_quant_params_from_aimet_format({}, "gru") is False
+    bad = json_copy(enc)
+    bad["activation_encodings"]["gru"]["output"]["0"]["n"] += 1
+    with pytest.raises(ValueError, match="n does not match"):
+        n.load_quant_params_from_aimet_format(bad, "gru")
+    bad = json_copy(enc)
+    del bad["param_encodings"]["gru.bias"]
+    assert n.load_quant_params_from_aimet_format(bad, "gru") is False
+    assert not n.is_calibrated()
+
+
+def json_copy(d):
+    import json
+    return json.loads(json.dumps(d))

@@ -336,6 +336,31 @@ def test_quant_params_document_reproduces_qat_forward(cuda, tmp_path, bidirectio
     assert torch.equal(o1, o2) and torch.equal(h1, h2)
 
 
+@pytest.mark.parametrize("bidirectional", [False, True])
+def test_aimet_encodings_reproduce_qat_forward(cuda, bidirectional):
+    """Grids calibrated on the GPU, exported with export_quant_params_to_aimet_format, passed
+    through JSON and loaded into a fresh module with the same weights
+    (load_quant_params_from_aimet_format): the quantised forward is bit for bit the same."""
+    import json
+    T, B, I, H = 5, 24, 10, 32
+    print(f"[quantgru aimet] bidirectional={bidirectional}", flush=True)
+    m, x_tbi, hx = _module_case(bidirectional, False, True, "c3", 43, shape=(T, B, I, H))
+    m = m.to(cuda)
+    x, hx = x_tbi.to(cuda), hx.to(cuda)
+    with m.calibration_context():
+        m(x, hx)
+    m.use_quantization = True
+    enc = json.loads(json.dumps(m.export_quant_params_to_aimet_format({}, "model.gru")))
+    n = Q.QuantGRU(I, H, bidirectional=bidirectional).to(cuda)
+    n.load_state_dict(m.state_dict())
+    assert n.load_quant_params_from_aimet_format(enc, "model.gru")
+    n.use_quantization = True
+    with torch.no_grad():
+        o1, h1 = m(x, hx)
+        o2, h2 = n(x, hx)
+    assert torch.equal(o1, o2) and torch.equal(h1, h2)
+
+
 @pytest.mark.parametrize("bits,mse,mae,cos", [(8, 1e-3, 0.05, 0.999), (16, 1e-4, 0.015, 0.999)])
 def test_quantized_module_tracks_nn_gru_with_reference_thresholds(cuda, bits, mse, mae, cos):
     """operators/quant-gru/tests/test_quant_gru.py:400-526: QuantGRU with nn.GRU's weights,
