@@ -92,9 +92,16 @@ def _qdq_leg(torch, steps: int, warmup: int, validate: bool = True):
     g = torch.randn(R, Cc)
     x, g = x.to(dev), g.to(dev)
     results = {}
-    for name, enc_shape, bits, sym in (("per_tensor_8b_asym", (), 8, False),
-                                        ("per_channel_4b_sym", (R, 1), 4, True)):
+    # fused: the mirror module's one-launch encodings; reference_path: the reference module's
+    # get_encodings() tensor expressions before the backend call, what aimet_torch's own
+    # QuantizeDequantize runs with this backend registered
+    for name, enc_shape, bits, sym, fused in (
+            ("per_tensor_8b_asym", (), 8, False, True),
+            ("per_channel_4b_sym", (R, 1), 4, True, True),
+            ("per_tensor_8b_asym_reference_path", (), 8, False, False),
+            ("per_channel_4b_sym_reference_path", (R, 1), 4, True, False)):
         q = A.QuantizeDequantize(enc_shape, bits, sym).to(dev)
+        q.fused_encodings = fused
         with q.compute_encodings():
             q(x)
         xg = x.detach().requires_grad_()
@@ -157,6 +164,32 @@ def _qdq_leg(torch, steps: int, warmup: int, validate: bool = True):
     results["kernel_bwd"] = {"us": t_b * 1e6, "GB_s": 12 * n / t_b / 1e9}
     _log(f"qdq kernels: fwd {t_f*1e6:.1f} us ({8*n/t_f/1e9:.0f} GB/s), "
          f"bwd {t_b*1e6:.1f} us ({12*n/t_b/1e9:.0f} GB/s)")
+    # the same launches on a bf16 copy of the tensor (2 bytes per element; the 4-bit grid is
+    # not stable in bf16, so the arithmetic runs in fp32 as the reference's would)
+    xh, gh = x.to(torch.bfloat16), g.to(torch.bfloat16)
+    yh, dxh = torch.empty_like(xh), torch.empty_like(xh)
+    dsh, doh = torch.empty_like(ds), torch.empty_like(do)
+    lay = rxmet_lib.QdqLayout(1, 1, 1, R, Cc)
+    num = rxmet_lib.QdqNumerics(2, 0, 0.0, 0, 0)
+    wsh = torch.empty(rxmet_lib.load().rxmet_qdq_workspace_bytes_ex(lay, 2), dtype=torch.uint8,
+                      device=dev)
+
+    def fwd_bf16():
+        rxmet_lib.call("rxmet_qdq_forward_ex", xh.data_ptr(), yh.data_ptr(), lay, num,
+                       s_vec.data_ptr(), o_vec.data_ptr(), -8, 7, Q.LEARNABLE, sh)
+
+    def bwd_bf16():
+        rxmet_lib.call("rxmet_qdq_backward_ex", xh.data_ptr(), gh.data_ptr(), dxh.data_ptr(),
+                       dsh.data_ptr(), doh.data_ptr(), lay, num, s_vec.data_ptr(),
+                       o_vec.data_ptr(), -8, 7, Q.LEARNABLE, wsh.data_ptr(), sh)
+
+    t_fh = ev_time(fwd_bf16, max(steps, 20))
+    t_bh = ev_time(bwd_bf16, max(steps, 20))
+    results["kernel_fwd_bf16"] = {"us": t_fh * 1e6, "GB_s": 4 * n / t_fh / 1e9}
+    results["kernel_bwd_bf16"] = {"us": t_bh * 1e6, "GB_s": 6 * n / t_bh / 1e9}
+    _log(f"qdq kernels (bf16 tensor): fwd {t_fh*1e6:.1f} us ({4*n/t_fh/1e9:.0f} GB/s), "
+         f"bwd {t_bh*1e6:.1f} us ({6*n/t_bh/1e9:.0f} GB/s)")
+    del xh, gh, yh, dxh, dsh, doh, wsh
     check = None
     if validate:
         # the timed kernels' outputs on 64 rows against the oracle: y and dx bit-exact, the

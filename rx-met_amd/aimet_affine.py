@@ -403,6 +403,11 @@ class QuantizeDequantize(nn.Module):
             enc_min = torch.zeros_like(enc_min)
         self.set_range(enc_min, enc_max)
 
+    # True: (scale, offset) from rxmet_qdq_encoding_forward/_backward (one launch each way).
+    # False: the reference's own get_encodings() tensor expressions, i.e. what aimet_torch's
+    # QuantizeDequantize computes before it calls the backend (quantizer.py:466-483, 1060-1082).
+    fused_encodings = True
+
     def get_encodings(self) -> Optional[Tuple[torch.Tensor, torch.Tensor]]:
         if not self.is_initialized():
             return None
@@ -416,8 +421,8 @@ class QuantizeDequantize(nn.Module):
                 "Failed to run QuantizeDequantize since quantization parameters are not initialized."
                 " Please initialize the quantization parameters using `compute_encodings()`.")
         mn, mx = self.min, self.max
-        if (mn.is_cuda and mn.dtype == torch.float32 and mx.dtype == torch.float32
-                and mn.is_contiguous() and mx.is_contiguous()):
+        if (self.fused_encodings and mn.is_cuda and mn.dtype == torch.float32
+                and mx.dtype == torch.float32 and mn.is_contiguous() and mx.is_contiguous()):
             # get_encodings() in two launches instead of a chain of one-element tensor ops
             scale, offset = mi355x_qdq.minmax_encodings(
                 mn, mx, self.qmin, self.qmax, self.symmetric,
