@@ -42,6 +42,15 @@ __device__ __forceinline__ Place place(int G, int nclusters) {
 // is complete before thread 0 increments the counter; a member that has seen the count reach
 // `arrivals` then reads the new values from the coherence point.  No L2 writeback or
 // invalidation is needed, because nothing exchanged lives in a non-coherent cache line.
+//
+// The ordering rests on the ISA rather than on the language memory model: the exchanged
+// stores and loads are agent-scope atomics (global_store/global_load with sc1), and
+// s_waitcnt vmcnt(0) returns only once a wave's sc1 stores are complete at the coherence
+// point.  The language-level form — a release fetch_add and an acquire fence after the poll
+// — compiles on gfx950 to buffer_wbl2 sc1 before the increment and buffer_inv sc1 after the
+// wait (write back, then invalidate, the whole XCD's L2), issued by every workgroup at every
+// step.  Measured on the c3 GRU step: 6.10 ms against 3.50 ms; c4 LSTM step 4.41 against
+// 3.37 ms.  Nothing here needs that cache maintenance.
 __device__ __forceinline__ bool sync(unsigned *counter, unsigned arrivals, int *timeout) {
   __shared__ int ok;
   __builtin_amdgcn_s_waitcnt(0);
