@@ -421,8 +421,8 @@ def _gru_int_leg(torch, steps: int, warmup: int):
     C, M = 3 * H, T * B
     work = {"gru_int_recurrence": (2.0 * M * H * C, INT8_MFMA_PEAK,
                                    "recurrent GEMM R_q (h_q - zp_h) of one direction over T steps "
-                                   "(one exact byte-plane int8-MFMA GEMM launch and one integer "
-                                   "pointwise launch per step)"),
+                                   "(one clustered launch: int8 MFMA on h byte planes, the "
+                                   "integer gates fused)"),
             "gru_int_input_gemm": (2.0 * M * C * I, INT8_MFMA_PEAK,
                                    "input projection W_q (x_q - zp_x) of one direction")}
     dt, p50, p95, kernels, roof = _timed_steps(torch, step, steps, warmup, work)

@@ -18,14 +18,22 @@
 //   3. wx_gemm    : the time-parallel input projection summed exactly on int8 MFMA over
 //      byte planes (exact_gemm.h, int32 operands), with the GEMM+bias rescale, clamp and mask
 //      fused into the epilogue;
-//   4. per step, rh_gemm (the same for R_q (h - zp_h)) and int_point: the integer update,
+//   4. the recurrence, clustered (int_recurrence_cl; cluster.h) when R_q fits signed 8 bits,
+//      H is a multiple of 16 and H <= 1024: one cooperative launch for all T steps, a batch
+//      tile's hidden units split over a cluster of workgroups, R_q resident in VGPRs as int8
+//      MFMA fragments, the h codes exchanged as byte planes each step, and the recurrent
+//      linear's bias, rescale and clamp plus the integer gates fused in registers.  Otherwise
+//      per step rh_gemm (the same GEMM for R_q (h - zp_h)) and int_point: the integer update,
 //      reset and new gates, the hidden update, clamps and masks, the dequantised h and v.
+#include <climits>
 #include <cmath>
+#include <cstdlib>
 #include <vector>
 
 #include "cluster.h"
 #include "exact_gemm.h"
 #include "gru_internal.h"
+#include "mfma_frag.h"
 #include "rxmet_common.h"
 #include "rxmet_gru.h"
 
@@ -294,10 +302,267 @@ __global__ __launch_bounds__(256) void int_point(IPointArgs a, IntStepParams p, 
 }
 
 // ---------------------------------------------------------------------------------
+// 4c. clustered recurrence: a batch tile's units split over G workgroups
+// ---------------------------------------------------------------------------------
+// Member m of a cluster owns UT unit tiles (16 units each) of one 16-sequence batch tile.
+// Four waves per unit tile split the recurrent sum over the K-steps (wave q takes steps
+// q, q+4, ...) with R_q fragments resident in VGPRs and add their partial sums through LDS;
+// each lane then finishes one (sequence, unit) element: the three weight_hh_linear codes from
+// the exact sums, the gates and the new h code.  The h codes are exchanged through global
+// memory as byte planes (coherent accesses, double-buffered by step parity) and the members
+// meet at a counter barrier once per step.
+constexpr int kITile = 16;
+constexpr int kIMaxKPerWave = 4;  // K-steps per wave: H <= 1024
+
+struct IClArgs {
+  int T, B, H, KS, Bpad;
+  int G, UT, ncl, ntiles;
+  int h_offset;                 // 0 (signed h grid) or 2^(bits-1) (unsigned): centred codes
+  const int32_t *wx;            // [T, B, 3H] weight_ih_linear codes
+  const v4i *rfrag;             // R_q as int8 MFMA B fragments, [H/16][3][KS][64]
+  const int32_t *rcol;          // [3H] column sums of R_q
+  const long long *bias;        // [3H] br in the recurrent accumulator's scale
+  const IRescale *rs;           // [3H] recurrent accumulator -> weight_hh_linear
+  const int32_t *h0q;           // [B, H] h codes of row 0
+  float *hout, *v;              // dequantised h [T+1, B, H] (row 0 written) and v, or null
+  int32_t *hq;                  // h codes [T+1, B, H] (row 0 written), or null
+  uint8_t *hh_m, *gin_m, *gout_m, *h_m;  // training masks, or null
+  int8_t *hx;                   // [2][NPL][Bpad][H] exchanged h codes
+  unsigned *counters;           // [ncl]
+  int *timeout;
+};
+
+// R_q [H][3H] int32 codes -> int8 B fragments of v_mfma_i32_16x16x64_i8:
+// frag[((ut * 3 + g) * KS + s) * 64 + lane] holds R[k][c] for c = g*H + 16*ut + lane % 16,
+// k = 64*s + 16*(lane / 16) + 0..15 (zero beyond H).
+__global__ __launch_bounds__(64) void pack_r_frags_i32(int H, int KS, const int32_t *__restrict__ Rq,
+                                                       v4i *__restrict__ frag) {
+  const int lane = threadIdx.x;
+  const int idx = blockIdx.x;  // (ut * 3 + g) * KS + s
+  const int s = idx % KS, g = (idx / KS) % 3, ut = idx / (3 * KS);
+  const int C = 3 * H;
+  const int c = g * H + 16 * ut + lane % 16;
+  int wd[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    int by[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int k = 64 * s + 16 * (lane / 16) + 4 * q + e;
+      by[e] = k < H ? Rq[static_cast<size_t>(k) * C + c] : 0;
+    }
+    wd[q] = pack4_i8(by[0], by[1], by[2], by[3]);
+  }
+  frag[static_cast<size_t>(idx) * 64 + lane] = v4i{wd[0], wd[1], wd[2], wd[3]};
+}
+
+__global__ __launch_bounds__(256) void r_colsum(int H, const int32_t *__restrict__ Rq,
+                                                int32_t *__restrict__ rcol) {
+  const int C = 3 * H;
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= C) return;
+  int32_t s = 0;
+  for (int k = 0; k < H; ++k) s += Rq[static_cast<size_t>(k) * C + c];
+  rcol[c] = s;
+}
+
+// h codes as exchanged bytes: one plane (the centred code) or two (low byte - 128, high byte)
+template <int NPL>
+__device__ __forceinline__ void publish_h(int8_t *hx, size_t plane_stride, int b, int H, int j,
+                                          int hcv) {
+  unsigned char *dst = reinterpret_cast<unsigned char *>(hx) + static_cast<size_t>(b) * H + j;
+#pragma unroll
+  for (int q = 0; q < NPL; ++q)
+    cluster::store_bytes_coherent(dst + q * plane_stride,
+                                  NPL == 1 ? hcv : (q == 0 ? (hcv & 255) - 128 : hcv >> 8));
+}
+
+template <int NPL>
+__global__ __launch_bounds__(512) void int_recurrence_cl(IClArgs a, IntStepParams p) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  ILut *lut = reinterpret_cast<ILut *>(smem);
+  v4i *red = reinterpret_cast<v4i *>(smem + (3 * sizeof(ILut) + 15) / 16 * 16);  // [UT][4][3][NPL][64]
+  const cluster::Place pl = cluster::place(a.G, a.ncl);
+  unsigned *counter = a.counters + pl.cluster;
+  const int H = a.H, C = 3 * H, B = a.B, KS = a.KS;
+  const int tid = threadIdx.x, w = tid / 64, l = tid % 64;
+  const int utl = w / 4, kq = w % 4;
+  const int ut = pl.member * a.UT + utl;
+  const int j = 16 * ut + l % 16;
+  const int nr = 4 * (l / 16) + kq;  // batch row finished by this lane
+  for (int i = tid; i < 3 * static_cast<int>(sizeof(ILut) / 4); i += blockDim.x)
+    reinterpret_cast<int32_t *>(lut)[i] = reinterpret_cast<const int32_t *>(p.lut)[i];
+  v4i rfr[kIMaxKPerWave][3];
+#pragma unroll
+  for (int i = 0; i < kIMaxKPerWave; ++i) {
+    const int s = kq + 4 * i;
+#pragma unroll
+    for (int g = 0; g < 3; ++g)
+      rfr[i][g] = s < KS ? a.rfrag[((ut * 3 + g) * KS + s) * 64 + l] : v4i{0, 0, 0, 0};
+  }
+  // S = sum_k R (h - zp_h) = (plane sums) + (centring - zp_h) colsum
+  const long long centre = (NPL == 2 ? 128 : 0) + a.h_offset - p.zp_h;
+  long long rc[3], bias[3];
+  IRescale rs[3];
+#pragma unroll
+  for (int g = 0; g < 3; ++g) {
+    const int c = g * H + j;
+    rc[g] = centre * a.rcol[c];
+    bias[g] = a.bias[c];
+    rs[g] = a.rs[c];
+  }
+  const size_t plane_stride = static_cast<size_t>(a.Bpad) * H;
+  const size_t NH = static_cast<size_t>(B) * H;
+  v4i *myred = red + (static_cast<size_t>(utl) * 4 + kq) * 3 * NPL * 64;
+  unsigned epoch = 0;
+  bool alive = true;
+  for (int tile = pl.cluster; tile < a.ntiles && alive; tile += a.ncl) {
+    __syncthreads();  // the previous tile's readers of the partial-sum buffer are done
+    const int b0 = tile * kITile, b = b0 + nr;
+    const bool valid = b < B;
+    int32_t hold = valid ? a.h0q[static_cast<size_t>(b) * H + j] : p.zp_h;
+    publish_h<NPL>(a.hx, plane_stride, b, H, j, hold - a.h_offset);
+    int32_t wn_[3];
+    auto load_wx = [&](int t) {
+#pragma unroll
+      for (int g = 0; g < 3; ++g)
+        wn_[g] = valid ? a.wx[(static_cast<size_t>(t) * B + b) * C + g * H + j] : 0;
+    };
+    load_wx(0);
+    alive = cluster::sync(counter, ++epoch * a.G, a.timeout);
+    for (int t = 0; t < a.T && alive; ++t) {
+      const int par = t & 1;
+      const int8_t *hin = a.hx + static_cast<size_t>(par) * NPL * plane_stride;
+      int8_t *hnext = a.hx + static_cast<size_t>(par ^ 1) * NPL * plane_stride;
+      const int32_t wz = wn_[0], wr = wn_[1], wn = wn_[2];
+      v4i acc[3][NPL];
+#pragma unroll
+      for (int g = 0; g < 3; ++g)
+#pragma unroll
+        for (int q = 0; q < NPL; ++q) acc[g][q] = v4i{0, 0, 0, 0};
+      {
+        const int8_t *hrow = hin + static_cast<size_t>(b0 + l % 16) * H + 16 * (l / 16);
+        v4i hfr[kIMaxKPerWave][NPL];
+#pragma unroll
+        for (int i = 0; i < kIMaxKPerWave; ++i)
+#pragma unroll
+          for (int q = 0; q < NPL; ++q)
+            if (kq + 4 * i < KS) {
+              const int4 v = cluster::load_coherent16(hrow + q * plane_stride + 64 * (kq + 4 * i));
+              hfr[i][q] = v4i{v.x, v.y, v.z, v.w};
+            }
+#pragma unroll
+        for (int i = 0; i < kIMaxKPerWave; ++i)
+          if (kq + 4 * i < KS) {
+#pragma unroll
+            for (int g = 0; g < 3; ++g)
+#pragma unroll
+              for (int q = 0; q < NPL; ++q) acc[g][q] = mfma_i8(hfr[i][q], rfr[i][g], acc[g][q]);
+          }
+      }
+#pragma unroll
+      for (int g = 0; g < 3; ++g)
+#pragma unroll
+        for (int q = 0; q < NPL; ++q) myred[(g * NPL + q) * 64 + l] = acc[g][q];
+      __syncthreads();
+      // the three weight_hh_linear codes of (row b, unit j)
+      int32_t rh[3];
+      uint8_t k_hh[3];
+#pragma unroll
+      for (int g = 0; g < 3; ++g) {
+        long long ps[NPL];
+#pragma unroll
+        for (int q = 0; q < NPL; ++q) {
+          int v = 0;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const int *src = reinterpret_cast<const int *>(
+                red + ((static_cast<size_t>(utl) * 4 + k) * 3 * NPL + g * NPL + q) * 64 + l);
+            v += src[kq];
+          }
+          ps[q] = v;
+        }
+        const long long S = (NPL == 2 ? 256 * ps[NPL - 1] + ps[0] : ps[0]) + rc[g];
+        rh[g] = clampi(add32(static_cast<int32_t>(rescale(S + bias[g], rs[g])), p.zp_rh), p.rh,
+                       k_hh[g]);
+      }
+      // gates and the hidden update (as int_point)
+      uint8_t k_zi, k_zo, k_ri, k_ro, k_ni, k_no, k_h;
+      int32_t in = add32(add32(static_cast<int32_t>(rescale(static_cast<long long>(wz) - p.zp_wx, p.ih_zin)),
+                               static_cast<int32_t>(rescale(static_cast<long long>(rh[0]) - p.zp_rh, p.hh_zin))),
+                         p.zp_zin);
+      in = clampi(in, p.zin, k_zi);
+      const int32_t z = clampi(pwl_i(in, lut[0]), p.zout, k_zo);
+      in = add32(add32(static_cast<int32_t>(rescale(static_cast<long long>(wr) - p.zp_wx, p.ih_rin)),
+                       static_cast<int32_t>(rescale(static_cast<long long>(rh[1]) - p.zp_rh, p.hh_rin))),
+                 p.zp_rin);
+      in = clampi(in, p.rin, k_ri);
+      const int32_t r = clampi(pwl_i(in, lut[1]), p.rout, k_ro);
+      const long long rmul = (static_cast<long long>(r) - p.zp_rout) * (static_cast<long long>(rh[2]) - p.zp_rh);
+      in = add32(add32(static_cast<int32_t>(rescale(static_cast<long long>(wn) - p.zp_wx, p.ih_nin)),
+                       static_cast<int32_t>(rescale(rmul, p.rmul_nin))),
+                 p.zp_nin);
+      in = clampi(in, p.nin, k_ni);
+      const int32_t nn = clampi(pwl_i(in, lut[2]), p.nout, k_no);
+      const int32_t n_h = add32(static_cast<int32_t>(rescale(static_cast<long long>(nn) - p.zp_nout, p.nout_h)), p.zp_h);
+      const long long oldc = (static_cast<long long>(z) - p.zp_zout) * (static_cast<long long>(hold) - p.zp_h);
+      const long long newc = (static_cast<long long>(p.quant_one) - z) * (static_cast<long long>(n_h) - p.zp_h);
+      const int32_t hnew = clampi(add32(static_cast<int32_t>(rescale(oldc + newc, p.old_h)), p.zp_h), p.h, k_h);
+      hold = hnew;
+      publish_h<NPL>(hnext, plane_stride, b, H, j, hnew - a.h_offset);
+      // the other members only read the h codes: arrive now, store the outputs while waiting
+      cluster::arrive(counter);
+      ++epoch;
+      if (valid) {
+        const size_t e = static_cast<size_t>(b) * H + j;
+        const size_t row = (static_cast<size_t>(t) + 1) * NH + e;
+        if (a.hq) a.hq[row] = hnew;
+        if (a.hout) a.hout[row] = dq(hnew, p.zp_h, p.eff_h);
+        const size_t n = static_cast<size_t>(t) * B + b;
+        if (a.v) {
+          float *vp = a.v + n * 4 * H + j;
+          vp[0] = dq(z, p.zp_zout, p.eff_zout);
+          vp[H] = dq(r, p.zp_rout, p.eff_rout);
+          vp[2 * H] = dq(nn, p.zp_nout, p.eff_nout);
+          vp[3 * H] = dq(rh[2], p.zp_rh, p.eff_rh);
+        }
+        if (a.hh_m) {
+          const size_t mi = n * C + j;
+          a.hh_m[mi] = k_hh[0];
+          a.hh_m[mi + H] = k_hh[1];
+          a.hh_m[mi + 2 * H] = k_hh[2];
+        }
+        if (a.gin_m) {
+          const size_t mi = n * C + j;
+          a.gin_m[mi] = k_zi;
+          a.gin_m[mi + H] = k_ri;
+          a.gin_m[mi + 2 * H] = k_ni;
+          a.gout_m[mi] = k_zo;
+          a.gout_m[mi + H] = k_ro;
+          a.gout_m[mi + 2 * H] = k_no;
+          a.h_m[static_cast<size_t>(t) * NH + e] = k_h;
+        }
+      }
+      if (t + 1 < a.T) load_wx(t + 1);
+      alive = cluster::wait(counter, epoch * a.G, a.timeout);
+    }
+  }
+}
+
+// A launch whose cluster wait timed out: the int32 h codes are overwritten with INT32_MIN
+// (outside every grid) so that no caller mistakes them for a result.
+__global__ __launch_bounds__(256) void poison_codes(const int *timeout, int64_t n, int32_t *p) {
+  if (*timeout == 0) return;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
+    p[i] = INT32_MIN;
+}
+
+// ---------------------------------------------------------------------------------
 // host
 // ---------------------------------------------------------------------------------
 struct IntWorkspace {
-  size_t hostblk, bias, wx, rh, hq, xa, bfrag, colsum, flag, total;
+  size_t hostblk, bias, wx, rh, hq, xa, bfrag, colsum, flag, rfrag, rcol, hx, sync, total;
   IntWorkspace(int T, int B, int I, int H) {
     const size_t C = 3 * static_cast<size_t>(H);
     const size_t Kp = static_cast<size_t>(xgemm::pad_k(I));
@@ -313,6 +578,13 @@ struct IntWorkspace {
     bfrag = o; o += al(ip * 2 * ((C + 15) / 16 * 16) * Kp);  // fragments of 16-column tiles
     colsum = o; o += al(ip * sizeof(long long) * C);
     flag = o; o += al(sizeof(int));
+    // clustered recurrence: R_q fragments, R_q column sums, the exchanged h planes, counters
+    const size_t KS = (static_cast<size_t>(H) + 63) / 64;
+    const size_t Bpad = (static_cast<size_t>(B) + kITile - 1) / kITile * kITile;
+    rfrag = o; o += al(sizeof(v4i) * 64 * (static_cast<size_t>(H) / 16) * 3 * KS);
+    rcol = o; o += al(sizeof(int32_t) * C);
+    hx = o; o += al(2 * 2 * Bpad * H);
+    sync = o; o += al(sizeof(unsigned) * (Bpad / kITile + 2));
     total = o;
   }
 };
@@ -367,6 +639,99 @@ struct IntCall {
   uint8_t *x_m, *h0_m, *W_m, *R_m, *bw_m, *br_m, *ih_m, *hh_m, *gin_m, *gout_m, *h_m;
   void *workspace;
 };
+
+// The clustered recurrence when R_q fits signed 8 bits, h spans at most 16 bits, H is a
+// multiple of 16 up to 1024 and the grid can be resident at once; returns 1 when launched,
+// 0 when the caller must step, negative on error.
+static int int_recurrence_clustered(const IntCall &k, const IntStepParams &sp,
+                                    const IWeightArgs &wa, const int32_t *wx, const int32_t *hq0,
+                                    const IntWorkspace &ws, hipStream_t stream) {
+  const int T = k.T, B = k.B, H = k.H, C = 3 * H;
+  if (H % 16 != 0 || H > 1024 || wa.gR.lo < -128 || wa.gR.hi > 127 ||
+      std::getenv("RXMET_NO_CLUSTER") != nullptr)
+    return 0;
+  const rxmet_grid &gh = k.params->g[RXMET_GRU_H];
+  const int npl = gh.bits <= 8 ? 1 : 2;
+  const void *fn = npl == 1 ? reinterpret_cast<const void *>(&int_recurrence_cl<1>)
+                            : reinterpret_cast<const void *>(&int_recurrence_cl<2>);
+  int device = 0, ncu = 0;
+  RXMET_CHECK_HIP(hipGetDevice(&device));
+  RXMET_CHECK_HIP(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, device));
+  IClArgs a{};
+  a.T = T; a.B = B; a.H = H; a.KS = (H + 63) / 64;
+  a.ntiles = (B + kITile - 1) / kITile;
+  a.Bpad = a.ntiles * kITile;
+  // the smallest unit slice per workgroup whose grid fits one workgroup per CU, else two tiles
+  a.UT = (H / 16) % 2 == 0 && static_cast<int64_t>(a.ntiles) * (H / 16) > ncu ? 2 : 1;
+  a.G = H / (16 * a.UT);
+  const size_t lds = (3 * sizeof(ILut) + 15) / 16 * 16 +
+                     sizeof(v4i) * static_cast<size_t>(a.UT) * 4 * 3 * npl * 64;
+  RXMET_CHECK_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      static_cast<int>(lds)));
+  int per_cu = 0;
+  RXMET_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256 * a.UT, lds));
+  int ncl = per_cu * ncu / a.G;
+  if (ncl < 1) return 0;
+  if (ncl > a.ntiles) ncl = a.ntiles;
+  if (ncl >= 8) ncl -= ncl % 8;
+  a.ncl = ncl;
+  a.h_offset = gh.bits < 32 && gh.is_unsigned ? 1 << (gh.bits - 1) : 0;
+  char *wsb = static_cast<char *>(k.workspace);
+  v4i *rfrag = reinterpret_cast<v4i *>(wsb + ws.rfrag);
+  int32_t *rcol = reinterpret_cast<int32_t *>(wsb + ws.rcol);
+  hipLaunchKernelGGL(pack_r_frags_i32, dim3((H / 16) * 3 * a.KS), dim3(64), 0, stream, H, a.KS,
+                     k.Rq, rfrag);
+  RXMET_CHECK_LAUNCH();
+  hipLaunchKernelGGL(r_colsum, dim3((C + 255) / 256), dim3(256), 0, stream, H, k.Rq, rcol);
+  RXMET_CHECK_LAUNCH();
+  a.wx = wx;
+  a.rfrag = rfrag;
+  a.rcol = rcol;
+  a.bias = wa.bias + C;
+  a.rs = wa.rs + 2 * C;
+  a.h0q = hq0;
+  a.hout = k.h;
+  a.v = k.v;
+  a.hq = k.hq_out;
+  a.hh_m = k.training ? k.hh_m : nullptr;
+  a.gin_m = k.training ? k.gin_m : nullptr;
+  a.gout_m = k.training ? k.gout_m : nullptr;
+  a.h_m = k.training ? k.h_m : nullptr;
+  if (a.gin_m && !(a.gout_m && a.h_m)) a.gin_m = nullptr;
+  a.hx = reinterpret_cast<int8_t *>(wsb + ws.hx);
+  a.counters = reinterpret_cast<unsigned *>(wsb + ws.sync);
+  a.timeout = reinterpret_cast<int *>(a.counters + ncl);
+  hipLaunchKernelGGL(cluster::zero_words, dim3(1), dim3(256), 0, stream, a.counters, ncl + 1);
+  RXMET_CHECK_LAUNCH();
+  IntStepParams spc = sp;
+  void *args[] = {&a, &spc};
+  {
+    rxmet::prof::Scope ps__("gru_int_recurrence", stream);
+    RXMET_CHECK_HIP(cluster::launch(fn, dim3(ncl * a.G), dim3(256 * a.UT), args,
+                                    static_cast<unsigned>(lds), stream));
+  }
+  // a wait that timed out: every output after row 0 becomes NaN (codes: INT32_MIN)
+  const size_t NH = static_cast<size_t>(B) * H;
+  cluster::PoisonList pl{};
+  if (k.h) {
+    pl.p[pl.count] = k.h + NH;
+    pl.n[pl.count++] = static_cast<int64_t>(T) * NH;
+  }
+  if (k.v) {
+    pl.p[pl.count] = k.v;
+    pl.n[pl.count++] = static_cast<int64_t>(T) * NH * 4;
+  }
+  if (pl.count) {
+    hipLaunchKernelGGL(cluster::poison_list, dim3(256), dim3(256), 0, stream, a.timeout, pl);
+    RXMET_CHECK_LAUNCH();
+  }
+  if (k.hq_out) {
+    hipLaunchKernelGGL(poison_codes, dim3(256), dim3(256), 0, stream, a.timeout,
+                       static_cast<int64_t>(T) * NH, k.hq_out + NH);
+    RXMET_CHECK_LAUNCH();
+  }
+  return 1;
+}
 
 static int forward_int(const IntCall &k, hipStream_t stream) {
   const int T = k.T, B = k.B, I = k.I, H = k.H;
@@ -480,8 +845,14 @@ static int forward_int(const IntCall &k, hipStream_t stream) {
       return rc;
   }
 
-  // recurrence: per step R_q (h - zp_h) + br -> weight_hh_linear codes, then the gates
+  // recurrence: clustered when it applies, else per step R_q (h - zp_h) + br ->
+  // weight_hh_linear codes, then the gates
   const double hlo = sp.h.lo, hhi = sp.h.hi;
+  {
+    const int rc = int_recurrence_clustered(k, sp, wa, wx, hq0, ws, stream);
+    if (rc < 0) return rc;
+    if (rc == 1) return 0;
+  }
   const float hoff = xgemm::a_shift(hlo, hhi);
   const int hpa = xgemm::a_planes(hlo, hhi), rpb = xgemm::b_planes(wa.gR.lo, wa.gR.hi);
   IPointArgs pa;
