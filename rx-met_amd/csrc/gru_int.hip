@@ -334,15 +334,17 @@ struct IClArgs {
 
 // R_q [H][3H] int32 codes -> int8 B fragments of v_mfma_i32_16x16x64_i8:
 // frag[((ut * 3 + g) * KS + s) * 64 + lane] holds R[k][c] for c = g*H + 16*ut + lane % 16,
-// k = 64*s + 16*(lane / 16) + 0..15 (zero beyond H).
+// k = 64*s + 16*(lane / 16) + 0..15 (zero beyond H).  Each lane also adds its 16 codes to the
+// column sum rcol[c] (zeroed beforehand; integer atomics, so the sum is exact in any order).
 __global__ __launch_bounds__(64) void pack_r_frags_i32(int H, int KS, const int32_t *__restrict__ Rq,
-                                                       v4i *__restrict__ frag) {
+                                                       v4i *__restrict__ frag,
+                                                       int32_t *__restrict__ rcol) {
   const int lane = threadIdx.x;
   const int idx = blockIdx.x;  // (ut * 3 + g) * KS + s
   const int s = idx % KS, g = (idx / KS) % 3, ut = idx / (3 * KS);
   const int C = 3 * H;
   const int c = g * H + 16 * ut + lane % 16;
-  int wd[4];
+  int wd[4], sum = 0;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     int by[4];
@@ -350,20 +352,12 @@ __global__ __launch_bounds__(64) void pack_r_frags_i32(int H, int KS, const int3
     for (int e = 0; e < 4; ++e) {
       const int k = 64 * s + 16 * (lane / 16) + 4 * q + e;
       by[e] = k < H ? Rq[static_cast<size_t>(k) * C + c] : 0;
+      sum += by[e];
     }
     wd[q] = pack4_i8(by[0], by[1], by[2], by[3]);
   }
   frag[static_cast<size_t>(idx) * 64 + lane] = v4i{wd[0], wd[1], wd[2], wd[3]};
-}
-
-__global__ __launch_bounds__(256) void r_colsum(int H, const int32_t *__restrict__ Rq,
-                                                int32_t *__restrict__ rcol) {
-  const int C = 3 * H;
-  const int c = blockIdx.x * blockDim.x + threadIdx.x;
-  if (c >= C) return;
-  int32_t s = 0;
-  for (int k = 0; k < H; ++k) s += Rq[static_cast<size_t>(k) * C + c];
-  rcol[c] = s;
+  atomicAdd(rcol + c, sum);
 }
 
 // h codes as exchanged bytes: one plane (the centred code) or two (low byte - 128, high byte)
@@ -679,10 +673,11 @@ static int int_recurrence_clustered(const IntCall &k, const IntStepParams &sp,
   char *wsb = static_cast<char *>(k.workspace);
   v4i *rfrag = reinterpret_cast<v4i *>(wsb + ws.rfrag);
   int32_t *rcol = reinterpret_cast<int32_t *>(wsb + ws.rcol);
-  hipLaunchKernelGGL(pack_r_frags_i32, dim3((H / 16) * 3 * a.KS), dim3(64), 0, stream, H, a.KS,
-                     k.Rq, rfrag);
+  hipLaunchKernelGGL(cluster::zero_words, dim3(1), dim3(256), 0, stream,
+                     reinterpret_cast<unsigned *>(rcol), C);
   RXMET_CHECK_LAUNCH();
-  hipLaunchKernelGGL(r_colsum, dim3((C + 255) / 256), dim3(256), 0, stream, H, k.Rq, rcol);
+  hipLaunchKernelGGL(pack_r_frags_i32, dim3((H / 16) * 3 * a.KS), dim3(64), 0, stream, H, a.KS,
+                     k.Rq, rfrag, rcol);
   RXMET_CHECK_LAUNCH();
   a.wx = wx;
   a.rfrag = rfrag;
