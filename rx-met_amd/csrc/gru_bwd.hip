@@ -926,19 +926,10 @@ static int backward_recurrence_stepped(BwdPlan &plan, int T, int B, int I, int H
   na.kscale = plan.ba.eff_r;
   na.Bt = rb; na.ldb = ws.Cp; na.bplane = static_cast<int64_t>(H) * ws.Cp;
   na.M = B; na.N = H; na.K = C; na.out = gsum; na.ldo = H;
-  // K splits so that the dh GEMM has about 256 workgroups (the parts are summed in order by
-  // the next step's pointwise)
-  {
-    const int wj = H <= 64 ? 2 : H <= 96 ? 3 : 4;
-    const int wgs = ((B + 127) / 128) * ((H + 32 * wj - 1) / (32 * wj));
-    int S = 256 / wgs;
-    S = S < 1 ? 1 : (S > kStepMaxSplit ? kStepMaxSplit : S);
-    int kper = ((C + S - 1) / S + 31) / 32 * 32;
-    while (S > 1 && kper * (S - 1) >= C) --S;
-    na.ksplit = S;
-    na.kper = S > 1 ? kper : C;
-    na.out_split = static_cast<int64_t>(B) * H;
-  }
+  // K splits so that the dh GEMM fills the GPU (the parts are summed in order by the next
+  // step's pointwise)
+  wgrad::nt_plan(B, H, C, kStepMaxSplit, &na.ksplit, &na.kper);
+  na.out_split = static_cast<int64_t>(B) * H;
   const int S = na.ksplit;
   for (int t = T - 1; t >= 0; --t) {
     hipLaunchKernelGGL(bwd_step_point, grid, dim3(256), 0, stream, plan.ba, t, S, gsum, dhl);

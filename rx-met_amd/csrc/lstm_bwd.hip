@@ -863,18 +863,9 @@ int rxmet_lstm_backward_quant(int32_t T, int32_t B, int32_t I, int32_t H,
     na.kscale = swhh;
     na.Bt = whht; na.ldb = C; na.bplane = static_cast<int64_t>(H) * C;
     na.M = B; na.N = H; na.K = C; na.out = dhr; na.ldo = H;
-    {
-      // a K split that fills about 256 workgroups
-      const int wj = H <= 64 ? 2 : H <= 96 ? 3 : 4;
-      const int wgs = ((B + 127) / 128) * ((H + 32 * wj - 1) / (32 * wj));
-      int S = 256 / wgs;
-      S = S < 1 ? 1 : (S > kBStepMaxSplit ? kBStepMaxSplit : S);
-      int kper = ((C + S - 1) / S + 31) / 32 * 32;
-      while (S > 1 && kper * (S - 1) >= C) --S;
-      na.ksplit = S;
-      na.kper = S > 1 ? kper : C;
-      na.out_split = static_cast<int64_t>(B) * H;
-    }
+    // a K split that fills the GPU (the parts are summed in order by the next step's pointwise)
+    wgrad::nt_plan(B, H, C, kBStepMaxSplit, &na.ksplit, &na.kper);
+    na.out_split = static_cast<int64_t>(B) * H;
     const int64_t n = static_cast<int64_t>(B) * H;
     const dim3 pgrid(static_cast<unsigned>((n + 255) / 256));
     {

@@ -17,8 +17,8 @@ namespace wgrad {
 
 // part[s][p][q] = sum over k in split s of A[k * lda + p] * sum_pl Bt[pl * bplane + q * ldb + k]
 // (A: gradient rows k; Bt: codes transposed, k contiguous, zero beyond K up to a multiple of 32).
-// colsum (optional, [S][4][P] at most): partial sums of A over the split's k, written by the
-// first q-tile.  S splits of kper rows (kper a multiple of 32).
+// colsum (optional, [S][P]): sums of A over each split's k.  S splits of kper rows (kper a
+// multiple of 32).  A must be 16-byte aligned, with lda and P multiples of 4.
 struct TnArgs {
   const float *A;
   int64_t lda;
@@ -31,7 +31,7 @@ struct TnArgs {
 
 // out[m * ldo + n] = sum_k (A[m * lda + k] * kscale[k]) * sum_pl Bt[pl * bplane + n * ldb + k]
 // (A: gradient rows m, k contiguous; Bt: codes, k contiguous, zero beyond K up to a multiple
-// of 32).
+// of 32; A, kscale and Bt 16-byte aligned, lda a multiple of 4, K a multiple of 16).
 struct NtArgs {
   const float *A;
   int64_t lda;
@@ -46,14 +46,18 @@ struct NtArgs {
   int64_t out_split = 0;
 };
 
-// Number of K splits for a TN product (about 512 workgroups) and rows per split.
+// Number of K splits for a TN product and rows per split (a makespan model over the GPU's CUs
+// that also prices the partial sums each split adds).
 void tn_plan(int K, int P, int Q, int nplanes, int *S, int *kper);
+// K split of an NT product for about two waves per SIMD, at most max_split parts (kper = K
+// when S = 1).
+void nt_plan(int M, int N, int K, int max_split, int *S, int *kper);
 // Launches; nplanes is 1 or 2.
 int tn(const TnArgs &a, int nplanes, hipStream_t stream);
 int nt(const NtArgs &a, int nplanes, hipStream_t stream);
 // out[p * ldo + q] = qscale[q] * sum_s part[s][p][q] (fixed order; out[q * ldo + p] when
 // transpose); qscale may be null (1).  bias (optional): bias[p * ldo] = the sum of colsum over
-// splits and halves.
+// the splits.
 // mask (optional): out is multiplied by mask[q * P + p]; swap_h > 0: row (or column, when
 // transpose) p is written at the index with the first two blocks of swap_h swapped (the
 // (z, r, n) <-> (r, z, n) gate order of the GRU).
