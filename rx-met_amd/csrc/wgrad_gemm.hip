@@ -660,11 +660,24 @@ __global__ __launch_bounds__(256) void tn_finish_kernel(const float *__restrict_
                                                         int swap_h) {
   const int64_t n = static_cast<int64_t>(P) * Q;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  // the partials are added in split order, eight loads in flight at a time
+  auto sum_parts = [](const float *__restrict__ src, int64_t step, int count) {
+    float acc = src[0];
+    int s = 1;
+    for (; s + 8 <= count; s += 8) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = src[static_cast<int64_t>(s + u) * step];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc += v[u];
+    }
+    for (; s < count; ++s) acc += src[static_cast<int64_t>(s) * step];
+    return acc;
+  };
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n + P; i += stride) {
     if (i < n) {
-      float acc = part[i];
-      for (int s = 1; s < S; ++s) acc += part[static_cast<int64_t>(s) * n + i];
-      const int p = static_cast<int>(i / Q), q = static_cast<int>(i % Q);
+      const float acc = sum_parts(part + i, n, S);
+      const int p = static_cast<int>(i / Q), q = static_cast<int>(i - static_cast<int64_t>(p) * Q);
       float v = qscale ? acc * qscale[q] : acc;
       if (mask) v *= static_cast<float>(mask[static_cast<int64_t>(q) * P + p]);
       int po = p;
@@ -675,12 +688,12 @@ __global__ __launch_bounds__(256) void tn_finish_kernel(const float *__restrict_
         out[po * ldo + q] = v;
     } else if (colsum && bias) {
       const int p = static_cast<int>(i - n);
-      float acc = 0.0f;
-      for (int s = 0; s < S * ath; ++s) acc += colsum[static_cast<int64_t>(s) * P + p];
-      bias[p * ldo] = acc;
+      bias[p * ldo] = sum_parts(colsum + p, P, S * ath);
     }
   }
 }
+
+static bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // Codes -> bf16 planes, transposed through a 64 x 64 LDS tile.
 __global__ __launch_bounds__(256) void codes_t_kernel(const float *__restrict__ src0, int64_t rows0,
@@ -721,14 +734,87 @@ __global__ __launch_bounds__(256) void codes_t_kernel(const float *__restrict__ 
   }
 }
 
+// The same for a row-major source (cs = 1, rows 16-byte aligned): 16-byte loads of four
+// columns, and 16-byte stores of eight consecutive rows per plane, through the same tile.
+__global__ __launch_bounds__(256) void codes_t_rows_kernel(const float *__restrict__ src0,
+                                                           int64_t rows0,
+                                                           const float *__restrict__ src1,
+                                                           int64_t rows, int cols, int64_t rs,
+                                                           float zp, float div, int nplanes,
+                                                           __bf16 *__restrict__ dst, int64_t ldd,
+                                                           int64_t plane) {
+  __shared__ int tile[64][65];
+  const int64_t r0 = 64 * static_cast<int64_t>(blockIdx.x);
+  const int c0 = 64 * blockIdx.y;
+  const int cg = threadIdx.x % 16;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int rr = threadIdx.x / 16 + 16 * u;
+    const int64_t r = r0 + rr;
+    const int c = c0 + 4 * cg;
+    int v[4] = {0, 0, 0, 0};
+    if (r < rows) {
+      const float *row = r < rows0 ? src0 + r * rs : src1 + (r - rows0) * rs;
+      if (c + 4 <= cols) {
+        const float4 x = *reinterpret_cast<const float4 *>(row + c);
+        v[0] = static_cast<int>(rintf((x.x - zp) / div));
+        v[1] = static_cast<int>(rintf((x.y - zp) / div));
+        v[2] = static_cast<int>(rintf((x.z - zp) / div));
+        v[3] = static_cast<int>(rintf((x.w - zp) / div));
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (c + e < cols) v[e] = static_cast<int>(rintf((row[c + e] - zp) / div));
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) tile[4 * cg + e][rr] = v[e];
+  }
+  __syncthreads();
+  const int g = threadIdx.x % 8;
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int cc = threadIdx.x / 8 + 32 * u;
+    const int c = c0 + cc;
+    const int64_t r = r0 + 8 * g;
+    if (c >= cols || r >= ldd) continue;
+    __bf16 hi[8], lo[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int v = tile[cc][8 * g + e];
+      if (nplanes == 1) {
+        hi[e] = static_cast<__bf16>(static_cast<float>(v));
+      } else {
+        hi[e] = static_cast<__bf16>(static_cast<float>(256 * (v >> 8)));  // v = 256 hi + (v & 255)
+        lo[e] = static_cast<__bf16>(static_cast<float>(v & 255));
+      }
+    }
+    // ldd is a multiple of 8, so the eight rows lie inside the destination row
+    __bf16 *d = dst + static_cast<int64_t>(c) * ldd + r;
+    uint4 w;
+    __builtin_memcpy(&w, hi, sizeof w);
+    *reinterpret_cast<uint4 *>(d) = w;
+    if (nplanes == 2) {
+      __builtin_memcpy(&w, lo, sizeof w);
+      *reinterpret_cast<uint4 *>(d + plane) = w;
+    }
+  }
+}
+
 int codes_t(const float *src0, int64_t rows0, const float *src1, int64_t rows, int cols, int64_t rs,
             int64_t cs, float zp, float div, int nplanes, __bf16 *dst, int64_t ldd, int64_t plane,
             hipStream_t stream) {
   RXMET_CHECK_ARG(nplanes == 1 || nplanes == 2, "nplanes must be 1 or 2");
   RXMET_CHECK_ARG(ldd >= rows && (rows0 >= rows || src1 != nullptr), "bad codes_t layout");
   const dim3 grid(static_cast<unsigned>((ldd + 63) / 64), static_cast<unsigned>((cols + 63) / 64));
-  hipLaunchKernelGGL(codes_t_kernel, grid, dim3(256), 0, stream, src0, rows0, src1, rows, cols, rs,
-                     cs, zp, div, nplanes, dst, ldd, plane);
+  const bool rows_ok = cs == 1 && rs % 4 == 0 && aligned16(src0) && (src1 == nullptr || aligned16(src1)) &&
+                       ldd % 8 == 0 && plane % 8 == 0 && aligned16(dst);
+  if (rows_ok)
+    hipLaunchKernelGGL(codes_t_rows_kernel, grid, dim3(256), 0, stream, src0, rows0, src1, rows, cols,
+                       rs, zp, div, nplanes, dst, ldd, plane);
+  else
+    hipLaunchKernelGGL(codes_t_kernel, grid, dim3(256), 0, stream, src0, rows0, src1, rows, cols, rs,
+                       cs, zp, div, nplanes, dst, ldd, plane);
   RXMET_CHECK_LAUNCH();
   return 0;
 }
@@ -832,8 +918,6 @@ static void tn_dispatch(const TnArgs &a, hipStream_t stream) {
     default: return tn_launch<NPL, 4, 1, 5>(a, stream);
   }
 }
-
-static bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 int tn(const TnArgs &a, int nplanes, hipStream_t stream) {
   RXMET_CHECK_ARG(nplanes == 1 || nplanes == 2, "nplanes must be 1 or 2");
