@@ -1,6 +1,7 @@
 // wgrad_gemm.hip — see wgrad_gemm.h.
 #include "wgrad_gemm.h"
 
+#include <algorithm>
 #include <type_traits>
 
 #include "mfma_frag.h"
@@ -76,18 +77,35 @@ __device__ __forceinline__ float lane4(const float4 &v, int i) {
   return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
 }
 
+// Block -> (p-tile, q-tile, split) of a TN product.  The tiles of one split are dealt in groups
+// of up to gt (a whole number of p-tiles, at most one XCD's worth of resident workgroups) and
+// the groups go round robin over the eight XCDs (block b runs on XCD b % 8): a group's
+// workgroups start together on one XCD and walk the same K rows, so each chunk of A and B is
+// fetched from HBM once and served to the group from that XCD's L2.
+struct TnMap {
+  int ntq, tiles, gt, gps, ngroups;  // q-tiles, tiles per split, group size, groups per split, groups
+};
+
+__device__ __forceinline__ bool tn_place(const TnMap &m, int *pt, int *qt, int *s) {
+  const int xcd = blockIdx.x % 8, i = blockIdx.x / 8;
+  const int g = (i / m.gt) * 8 + xcd;
+  if (g >= m.ngroups) return false;
+  const int t = (g % m.gps) * m.gt + i % m.gt;
+  if (t >= m.tiles) return false;
+  *s = g / m.gps;
+  *pt = t / m.ntq;
+  *qt = t % m.ntq;
+  return true;
+}
+
 // TN: part[s][p][q] = sum_k A[k][p] Bt[q][k].  The A loads are 16 bytes along p, so a lane's
 // four values belong to four sub-tiles: row r of sub-tile i is column p = pw + 4 r + i.
-// Workgroups of WM x WN waves (a BP x BQ tile); block b runs on XCD b % 8, and the q-tiles of
-// one (p-tile, split) group are consecutive blocks of one XCD, sharing its A rows in L2.
+// Workgroups of WM x WN waves (a BP x BQ tile), placed by tn_place.
 template <int NPL, int WM, int WN, int WJ>
-__global__ __launch_bounds__(64 * WM * WN, 2) void tn_wave_kernel(TnArgs a, int ntp, int ntq,
-                                                               int ngroups) {
+__global__ __launch_bounds__(64 * WM * WN, 2) void tn_wave_kernel(TnArgs a, TnMap map) {
   constexpr int BP = 64 * WM, BQ = 16 * WJ * WN;
-  const int xcd = blockIdx.x % 8, r8 = blockIdx.x / 8;
-  const int qt = r8 % ntq, grp = (r8 / ntq) * 8 + xcd;
-  if (grp >= ngroups) return;
-  const int pt = grp % ntp, s = grp / ntp;
+  int pt, qt, s;
+  if (!tn_place(map, &pt, &qt, &s)) return;
   const int kbeg = s * a.kper, kend = min(a.K, kbeg + a.kper);
   const int w = threadIdx.x / 64, l = threadIdx.x % 64, r = l % 16, kb = l / 16;
   const int pw = BP * pt + 64 * (w / WN), qw = BQ * qt + 16 * WJ * (w % WN);
@@ -217,8 +235,7 @@ __device__ __forceinline__ void raw_barrier() {
 }
 
 template <int NPL, int WM, int WN, int WJ>
-__global__ __launch_bounds__(64 * WM * WN, 2) void tn_lds_kernel(TnArgs a, int ntp, int ntq,
-                                                                 int ngroups) {
+__global__ __launch_bounds__(64 * WM * WN, 2) void tn_lds_kernel(TnArgs a, TnMap map) {
   constexpr int NW = WM * WN, BP = 64 * WM, BQ = 16 * WJ * WN;
   constexpr int UPR = BP / 4;            // 16-byte units per A row of the tile
   constexpr int RPI = 64 / UPR;          // A rows per DMA instruction (1 KB)
@@ -231,10 +248,8 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void tn_lds_kernel(TnArgs a, int n
   __shared__ __align__(16) float As0[32 * BP], As1[32 * BP];
   __shared__ __align__(16) unsigned Bs0[NPL * BQ * 16], Bs1[NPL * BQ * 16];
 
-  const int xcd = blockIdx.x % 8, r8 = blockIdx.x / 8;
-  const int qt = r8 % ntq, grp = (r8 / ntq) * 8 + xcd;
-  if (grp >= ngroups) return;  // whole workgroup
-  const int pt = grp % ntp, s = grp / ntp;
+  int pt, qt, s;
+  if (!tn_place(map, &pt, &qt, &s)) return;  // whole workgroup
   const int kbeg = s * a.kper, kend = min(a.K, kbeg + a.kper);
   const int w = threadIdx.x / 64, l = threadIdx.x % 64, r = l % 16, kb = l / 16;
   const int wm = w / WN, wn = w % WN;
@@ -842,13 +857,28 @@ static WaveTile tn_tile(int width, int nplanes) {
   return {2, 2, 4, true};
 }
 
+// Placement of a TN product on bp x bq block tiles in S splits (see tn_place); `blocks` is the
+// grid size.
+constexpr int kXcdSlots = 64;  // resident workgroups per XCD: 32 CUs x 2
+static TnMap tn_map(int P, int Q, int S, int bp, int bq, unsigned *blocks) {
+  TnMap m;
+  const int ntp = (P + bp - 1) / bp;
+  m.ntq = (Q + bq - 1) / bq;
+  m.tiles = ntp * m.ntq;
+  // keep whole p-tiles in a group (their q-tiles share the A rows)
+  m.gt = m.ntq >= kXcdSlots ? m.ntq : std::min(m.tiles, kXcdSlots / m.ntq * m.ntq);
+  m.gps = (m.tiles + m.gt - 1) / m.gt;
+  m.ngroups = m.gps * S;
+  *blocks = static_cast<unsigned>(8 * ((m.ngroups + 7) / 8) * m.gt);
+  return m;
+}
+
 void tn_plan(int K, int P, int Q, int nplanes, int *S, int *kper) {
   const WaveTile t = tn_tile(Q, nplanes);
-  const int tiles = ((P + t.rows() - 1) / t.rows()) * ((Q + t.cols() - 1) / t.cols());
   const int chunks = (K + kKC - 1) / kKC;
-  // Makespan model in chunk times: the workgroups run in rounds of 256 (one per CU, at least
-  // two rounds' worth so that two share each CU), plus the cost of writing and re-reading one
-  // more [P][Q] partial per split (about 6.5 MB per chunk time).
+  // Makespan model in chunk times.  The groups of tn_place go round robin over the eight XCDs,
+  // whose 64 workgroup slots (two per CU) take them in rounds; the busiest XCD sets the time.
+  // Each split also adds one [P][Q] partial to write and re-read (about 6.5 MB per chunk time).
   const double part_cost = 8.0 * P * Q / 6.5e6;
   int best = 1;
   double best_cost = 0.0;
@@ -856,8 +886,10 @@ void tn_plan(int K, int P, int Q, int nplanes, int *S, int *kper) {
   for (int s = 1; s <= smax; ++s) {
     const int per = (chunks + s - 1) / s;
     if ((s - 1) * per >= chunks) continue;  // an empty split
-    int rounds = (tiles * s + 255) / 256;
-    rounds = rounds < 2 ? 2 : rounds;
+    unsigned blocks = 0;
+    const TnMap m = tn_map(P, Q, s, t.rows(), t.cols(), &blocks);
+    const int load = (m.ngroups + 7) / 8 * m.gt;  // workgroups of the busiest XCD
+    const int rounds = (load + kXcdSlots - 1) / kXcdSlots;
     const double cost = static_cast<double>(rounds) * per + part_cost * s;
     if (s == 1 || cost < best_cost) {
       best = s;
@@ -887,20 +919,17 @@ void nt_plan(int M, int N, int K, int max_split, int *S, int *kper) {
 
 template <int NPL, int WM, int WN, int WJ>
 static void tn_launch(const TnArgs &a, hipStream_t stream) {
-  constexpr int BP = 64 * WM, BQ = 16 * WJ * WN;
-  const int ntp = (a.P + BP - 1) / BP, ntq = (a.Q + BQ - 1) / BQ;
-  const int ngroups = ntp * a.S, padded = (ngroups + 7) / 8 * 8;
-  hipLaunchKernelGGL((tn_wave_kernel<NPL, WM, WN, WJ>), dim3(static_cast<unsigned>(padded * ntq)),
-                     dim3(64 * WM * WN), 0, stream, a, ntp, ntq, ngroups);
+  unsigned blocks = 0;
+  const TnMap m = tn_map(a.P, a.Q, a.S, 64 * WM, 16 * WJ * WN, &blocks);
+  hipLaunchKernelGGL((tn_wave_kernel<NPL, WM, WN, WJ>), dim3(blocks), dim3(64 * WM * WN), 0, stream,
+                     a, m);
 }
 
 template <int NPL, int WJ>
 static void tn_lds_launch(const TnArgs &a, hipStream_t stream) {
-  constexpr int BP = 128, BQ = 32 * WJ;
-  const int ntp = (a.P + BP - 1) / BP, ntq = (a.Q + BQ - 1) / BQ;
-  const int ngroups = ntp * a.S, padded = (ngroups + 7) / 8 * 8;
-  hipLaunchKernelGGL((tn_lds_kernel<NPL, 2, 2, WJ>), dim3(static_cast<unsigned>(padded * ntq)),
-                     dim3(256), 0, stream, a, ntp, ntq, ngroups);
+  unsigned blocks = 0;
+  const TnMap m = tn_map(a.P, a.Q, a.S, 128, 32 * WJ, &blocks);
+  hipLaunchKernelGGL((tn_lds_kernel<NPL, 2, 2, WJ>), dim3(blocks), dim3(256), 0, stream, a, m);
 }
 
 template <int NPL>
