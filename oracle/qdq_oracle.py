@@ -18,6 +18,9 @@ IEEE round-half-to-even (``np.rint``) and fp64 accumulation of encoding gradient
 * ``minmax``          — _MinMaxObserver.collect_stats (encoding_analyzer.py:101-105).
 * ``compute_encodings_from_stats`` — MinMaxEncodingAnalyzer (encoding_analyzer.py:217-272).
 * ``scale_offset``    — get_scale / _get_offset (quantizer.py:345-403).
+* ``native_qdq``      — the native libpymo form, DlQuantization::stableQuantizeDequantize
+  (native/common/src/quantize_dequantize.hpp:35-46): clip in value space, multiply by the
+  correctly rounded reciprocal of the scale, round half to even, times the scale.
 
 Pinned by tests/test_qdq_oracle.py against: torch's own fake_quantize kernels (the
 reference's frozen path, third-party, exact); the reference's docstring tables
@@ -98,6 +101,27 @@ def qdq_learnable_backward(x, g, scale, offset, qmin, qmax, layout):
     ds = ds_el.astype(np.float64).sum(axis=(0, 2))
     do = do_el.astype(np.float64).sum(axis=(0, 2))
     return dx.reshape(np.shape(x)), ds.astype(f32), do.astype(f32)
+
+
+def native_qdq(x, minimum, maximum, scale, dtype=np.float32, noise=None):
+    """stableQuantizeDequantize (quantize_dequantize.hpp:35-46) in `dtype` (float or double):
+    NaN is returned as is; the value is clipped to [minimum, maximum]
+    (``fmax(fmin(v, max), min)``), multiplied by ``qdqReciprocal(scale)`` = the correctly
+    rounded 1 / scale (:15-29), rounded half to even (``nearbyint``) — or ``floor(scaled +
+    noise)`` when a stochastic noise array is given — and multiplied by the scale.  minimum,
+    maximum and scale broadcast against x (per-channel encodings)."""
+    dt = np.dtype(dtype)
+    v = np.asarray(x, dtype=dt)
+    lo, hi, sc = (np.asarray(a, dtype=dt) for a in (minimum, maximum, scale))
+    with np.errstate(invalid="ignore", over="ignore", divide="ignore"):
+        clipped = np.fmax(np.fmin(v, hi), lo)  # fmin/fmax return the other operand for NaN
+        scaled = (clipped * (dt.type(1) / sc).astype(dt)).astype(dt)
+        if noise is None:
+            rounded = np.rint(scaled)
+        else:
+            rounded = np.floor((scaled + np.asarray(noise, dtype=dt)).astype(dt))
+        out = (rounded * sc).astype(dt)
+    return np.where(np.isnan(v), v, out).astype(dt)
 
 
 def qdq_frozen_backward(x, g, scale, offset, qmin, qmax, layout):

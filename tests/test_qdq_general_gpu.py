@@ -367,3 +367,53 @@ def test_backend_quantize_dequantize_16bit(cuda):
     assert lo.dtype == torch.bfloat16
     assert torch.equal(lo, x.amin(dim=1, keepdim=True)) and torch.equal(hi, x.amax(dim=1,
                                                                                 keepdim=True))
+
+
+def _tf_grid(bits, scale, offset=None):
+    off = -(1 << (bits - 1)) if offset is None else offset
+    return off * scale, (off + (1 << bits) - 1) * scale
+
+
+def _frozen_qdq(x, scales, bits, offset, cuda):
+    """The backend's frozen-encoding QDQ with the aimet grid of a TfEncoding (symmetric:
+    signed codes and offset 0; otherwise unsigned codes and the given offset)."""
+    shape = (len(scales), 1) if len(scales) > 1 else ()
+    scale = torch.tensor(scales, dtype=torch.float32).reshape(shape).to(cuda)
+    if offset is None:
+        qmin, qmax, off = -(1 << (bits - 1)), (1 << (bits - 1)) - 1, 0.0
+    else:
+        qmin, qmax, off = 0, (1 << bits) - 1, float(offset)
+    offs = torch.full(shape, off, dtype=torch.float32, device=cuda)
+    return Q.quantize_dequantize(torch.from_numpy(x).to(cuda), scale, offs, qmin, qmax).cpu().numpy()
+
+
+def test_native_libpymo_qdq_alignment_on_gpu(cuda):
+    """The cases of the reference's native-vs-Torch alignment test
+    (tests/integration/test_native_qdq_alignment.py:88-137) through this backend's frozen QDQ
+    equal the native form stableQuantizeDequantize (quantize_dequantize.hpp:35-46): exact
+    codes with int32 offsets, per-channel 32-bit grids, ties to even at 8/16/32 bits on
+    symmetric and asymmetric grids, the float32 reciprocal of decimal scales, NaN kept and
+    infinity clipped."""
+    cases = []
+    codes = np.array([-257, -65, -7, -3, -1, 0, 1, 3, 7, 65, 257], dtype=f32)
+    cases.append(((codes * f32(2.0 ** -21)).reshape(1, -1), 32, [2.0 ** -21], None))
+    codes = np.array([-7, -3, -1, 0, 1, 3, 7], dtype=f32)
+    sc = [2.0 ** -21, 2.0 ** -20]
+    cases.append((np.stack([codes * f32(s) for s in sc]), 32, sc, None))
+    codes = np.array([-7.5, -3.5, -2.5, -1.5, -.5, .5, 1.5, 2.5, 3.5, 7.5], dtype=f32)
+    for bits in (8, 16, 32):
+        s = 2.0 ** -7 if bits == 8 else 2.0 ** -15 if bits == 16 else 2.0 ** -21
+        for off in (None, -13):
+            cases.append(((codes * f32(s)).reshape(1, -1), bits, [s], off))
+    for s in (1.0 / 32767, .013007, .027019):
+        cases.append((((np.arange(-63, 64, dtype=f32) + f32(.5)) * f32(s)).reshape(1, -1), 16, [s], None))
+    for bits in (8, 16, 32):
+        s = 2.0 ** -7 if bits == 8 else 2.0 ** -15 if bits == 16 else 2.0 ** -21
+        cases.append((np.array([[np.nan, -np.inf, -s, 0, s, np.inf]], dtype=f32), bits, [s], None))
+    for x, bits, scales, off in cases:
+        print(f"[native alignment] bits={bits} scales={scales} offset={off}", flush=True)
+        s = np.array(scales, dtype=f32).reshape(-1, 1) if len(scales) > 1 else f32(scales[0])
+        lo, hi = _tf_grid(bits, np.asarray(scales, dtype=np.float64).reshape(np.shape(s)), off)
+        expect = O.native_qdq(x, f32(lo) if np.ndim(lo) == 0 else lo.astype(f32),
+                              f32(hi) if np.ndim(hi) == 0 else hi.astype(f32), s)
+        np.testing.assert_array_equal(_frozen_qdq(x, scales, bits, off, cuda), expect)

@@ -119,6 +119,94 @@ def test_nan_kept_and_infinity_saturates():
             assert list(mask) == [False, False, True, True, True, False]
 
 
+def _tf_grid(bits, scale, offset=None):
+    """TfEncoding min / max of test_native_qdq_alignment.py:18-25."""
+    off = -(1 << (bits - 1)) if offset is None else offset
+    return off * scale, (off + (1 << bits) - 1) * scale
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_native_qdq_alignment_tables(dtype):
+    # quantize_dequantize.hpp:35-46 on the cases of test_native_qdq_alignment.py:88-137
+    t = np.dtype(dtype).type
+    # exact integer codes with an int32 offset (:88-90) and per channel (:107-110)
+    codes = np.array([-257, -65, -7, -3, -1, 0, 1, 3, 7, 65, 257], dtype=dtype)
+    s = 2.0 ** -21
+    lo, hi = _tf_grid(32, s)
+    np.testing.assert_array_equal(O.native_qdq(codes * t(s), lo, hi, s, dtype), codes * t(s))
+    codes = np.array([-7, -3, -1, 0, 1, 3, 7], dtype=dtype)
+    scales = np.array([[2.0 ** -21], [2.0 ** -20]])
+    x = np.stack([codes * t(sc) for sc in scales[:, 0]])
+    lo, hi = _tf_grid(32, scales)
+    np.testing.assert_array_equal(O.native_qdq(x, lo, hi, scales, dtype), x)
+    # ties to even (:111-118), also on asymmetric grids (offset -13)
+    codes = np.array([-7.5, -3.5, -2.5, -1.5, -.5, .5, 1.5, 2.5, 3.5, 7.5], dtype=dtype)
+    for bits in (8, 16, 32):
+        s = 2.0 ** -7 if bits == 8 else 2.0 ** -15 if bits == 16 else 2.0 ** -21
+        for off in (None, -13):
+            lo, hi = _tf_grid(bits, s, off)
+            y = O.native_qdq(codes * t(s), lo, hi, s, dtype)
+            np.testing.assert_array_equal(y, np.array([-8, -4, -2, -2, 0, 0, 2, 2, 4, 8]) * t(s))
+    # NaN kept, infinity clipped to the grid ends (:126-137)
+    for bits in (8, 16, 32):
+        s = 2.0 ** -7 if bits == 8 else 2.0 ** -15 if bits == 16 else 2.0 ** -21
+        lo, hi = _tf_grid(bits, s)
+        x = np.array([np.nan, -np.inf, -s, 0, s, np.inf], dtype=dtype)
+        y = O.native_qdq(x, lo, hi, s, dtype)
+        np.testing.assert_array_equal(y, np.array([np.nan, lo, -s, 0, s, hi], dtype=dtype))
+
+
+@pytest.mark.parametrize("scale", [.013007, .027019])
+def test_native_qdq_multiplies_by_the_rounded_reciprocal(scale):
+    # :120-124.  On these half-code values x / s and x * fl(1 / s) round apart: a division
+    # in place of qdqReciprocal would fail here.
+    s = f32(scale)
+    x = ((np.arange(-63, 64, dtype=f32) + f32(.5)) * s).astype(f32)
+    lo, hi = _tf_grid(16, float(s))
+    y = O.native_qdq(x, lo, hi, s)
+    by_rcp = (np.rint((x * (f32(1) / s)).astype(f32)) * s).astype(f32)
+    by_div = (np.rint((x / s).astype(f32)) * s).astype(f32)
+    np.testing.assert_array_equal(y, by_rcp)
+    assert (y != by_div).any()
+    # and it is the value the Torch path gives (the alignment the reference test asserts)
+    ref = torch.fake_quantize_per_tensor_affine(torch.from_numpy(x), float(s), 0, -32768, 32767)
+    np.testing.assert_array_equal(y, ref.numpy())
+
+
+@pytest.mark.parametrize("bits,scale,off", [(8, 2.0 ** -5, None), (8, 0.0173, -40), (16, 0.00031, None),
+                                            (4, 0.25, -3)])
+def test_native_qdq_equals_frozen_qdq_on_random_values(bits, scale, off):
+    # on grid-aligned minimum / maximum the two forms agree value for value
+    g = np.random.default_rng(bits)
+    s = f32(scale)
+    lo, hi = _tf_grid(bits, float(s), off)
+    x = (g.standard_normal(4096) * (hi - lo) / 3).astype(f32)
+    x[:4] = [np.nan, np.inf, -np.inf, 0.0]
+    if off is None:  # symmetric: signed codes, offset 0
+        qmin, qmax, aoff = -(1 << (bits - 1)), (1 << (bits - 1)) - 1, 0.0
+    else:  # asymmetric: unsigned codes shifted by the offset
+        qmin, qmax, aoff = 0, (1 << bits) - 1, float(off)
+    yf, _ = O.qdq_frozen(x, [s], [aoff], qmin, qmax, (1, 1, x.size))
+    yn = O.native_qdq(x, f32(lo), f32(hi), s)
+    np.testing.assert_array_equal(yn, yf)
+
+
+def test_native_qdq_stochastic_rounding():
+    # floor(scaled + noise): noise 0 truncates down, noise just below 1 rounds every
+    # non-integer up, and the mean over uniform noise is the value itself
+    s = 2.0 ** -4
+    lo, hi = _tf_grid(8, s)
+    x = np.array([-1.3, -0.55, 0.2, 0.7, 0.95], dtype=f32) * f32(8 * s)  # no whole codes
+    scaled = x / f32(s)
+    np.testing.assert_array_equal(O.native_qdq(x, lo, hi, s, noise=np.zeros(5)), np.floor(scaled) * f32(s))
+    near1 = np.full(5, np.nextafter(f32(1), f32(0)))
+    np.testing.assert_array_equal(O.native_qdq(x, lo, hi, s, noise=near1), np.ceil(scaled) * f32(s))
+    g = np.random.default_rng(1)
+    noise = g.random((20000, 5)).astype(f32)
+    mean = O.native_qdq(np.broadcast_to(x, noise.shape), lo, hi, s, noise=noise).mean(axis=0)
+    np.testing.assert_allclose(mean, x, atol=4 * float(s) / np.sqrt(20000) * 3)
+
+
 def _surrogate_grads(x, g, s, o, qmin, qmax, layout):
     """Autograd of y = (clamp(ste_round(x/s) - o) + o) * s, fp64 arithmetic with the
     fp32 rounding decisions of the forward; independent of the oracle's formulas."""
