@@ -363,10 +363,22 @@ __device__ __forceinline__ float pwl_eval(float q, const float *thr, const float
   return clamp_keep(val, ob, keep);
 }
 
+// Gate activations by table.  A gate input is an integer code clamped to its grid (clamp_keep
+// drops NaN), so when the grid has at most kGateTabMax codes the clustered recurrence
+// tabulates pwl_eval over it once per launch: entry e of a gate holds code << 1 | keep for the
+// input lo + e, one LDS read in place of the threshold search.
+constexpr int kGateTabMax = 1024;
+__device__ __forceinline__ float gate_tab(float q, const int *tab, float lo, uint8_t &keep) {
+  const int e = tab[static_cast<int>(q - lo)];
+  keep = static_cast<uint8_t>(e & 1);
+  return static_cast<float>(e >> 1);
+}
+
 // One (sequence, unit) step of the FP carrier (gru_forward_gpu_quant_fp.cu:138-393): both
 // linears from their exact sums (zero-point and bias terms, rescale, clamp), the three gates
 // through the PWL LUTs (thresholds, slopes, offsets in lut_f, shifts in lut_n; 48 floats and
-// 16 ints per gate) and the hidden update, with the keep flag of every clamp.
+// 16 ints per gate; or the gate tables `tab`, three of kGateTabMax entries, when not null) and
+// the hidden update, with the keep flag of every clamp.
 struct PointOut {
   float h, z, r, n, rh_n;  // codes: new h, the gate outputs, the new gate's recurrent linear
   uint8_t k_ih[3], k_hh[3], k_gi[3], k_go[3], k_h;
@@ -375,7 +387,8 @@ struct PointOut {
 __device__ __forceinline__ PointOut gru_point(const float gih[3], const float ghh[3],
                                               const float (&cst)[3][kChanParams],
                                               const StepParams &p, const float *lut_f,
-                                              const int *lut_n, float hold) {
+                                              const int *lut_n, float hold,
+                                              const int *tab = nullptr) {
   PointOut o;
   float wx[3], rh[3];
 #pragma unroll
@@ -389,20 +402,23 @@ __device__ __forceinline__ PointOut gru_point(const float gih[3], const float gh
   float in = rintf((wx[0] - p.zp_wx) * p.ih_to_zin) + rintf((rh[0] - p.zp_rh) * p.hh_to_zin);
   in += p.zp_zin;
   in = clamp_keep(in, p.zin, o.k_gi[0]);
-  o.z = pwl_eval(in, lut_f, lut_f + 16, lut_n, lut_f + 32, p.lut[0].zp_x, p.zout, o.k_go[0]);
+  o.z = tab ? gate_tab(in, tab, p.zin.lo, o.k_go[0])
+            : pwl_eval(in, lut_f, lut_f + 16, lut_n, lut_f + 32, p.lut[0].zp_x, p.zout, o.k_go[0]);
   // reset gate
   in = rintf((wx[1] - p.zp_wx) * p.ih_to_rin) + rintf((rh[1] - p.zp_rh) * p.hh_to_rin);
   in += p.zp_rin;
   in = clamp_keep(in, p.rin, o.k_gi[1]);
-  o.r = pwl_eval(in, lut_f + 48, lut_f + 64, lut_n + 16, lut_f + 80, p.lut[1].zp_x, p.rout,
-                 o.k_go[1]);
+  o.r = tab ? gate_tab(in, tab + kGateTabMax, p.rin.lo, o.k_go[1])
+            : pwl_eval(in, lut_f + 48, lut_f + 64, lut_n + 16, lut_f + 80, p.lut[1].zp_x, p.rout,
+                       o.k_go[1]);
   // new gate
   const float rmul = (o.r - p.zp_rout) * (rh[2] - p.zp_rh);
   in = rintf((wx[2] - p.zp_wx) * p.ih_to_nin) + rintf(rmul * p.rmul_to_nin);
   in += p.zp_nin;
   in = clamp_keep(in, p.nin, o.k_gi[2]);
-  o.n = pwl_eval(in, lut_f + 96, lut_f + 112, lut_n + 32, lut_f + 128, p.lut[2].zp_x, p.nout,
-                 o.k_go[2]);
+  o.n = tab ? gate_tab(in, tab + 2 * kGateTabMax, p.nin.lo, o.k_go[2])
+            : pwl_eval(in, lut_f + 96, lut_f + 112, lut_n + 32, lut_f + 128, p.lut[2].zp_x, p.nout,
+                       o.k_go[2]);
   // hidden update
   const float n_h = rintf((o.n - p.zp_nout) * p.nout_to_h) + p.zp_h;
   const float oldc = (o.z - p.zp_zout) * (hold - p.zp_h);
@@ -627,6 +643,7 @@ constexpr int kStageMinH = 512;    // H from which the h tile is staged in LDS
 struct ClArgs {
   int ncl, G, UT, ntiles, Bpad, ndir;  // clusters walk (direction, batch tile) pairs
   int stage_h;                         // h tile staged in LDS once per workgroup (large H)
+  int gate_tab;                        // gate activations by table (every gate grid fits)
   unsigned *counters;                  // [ncl]
   int *timeout;
 };
@@ -663,6 +680,8 @@ __device__ __forceinline__ void recurrence_cl_pair(const RecArgs &a, const StepP
   uint8_t *sb = reinterpret_cast<uint8_t *>(sf + 16 * 5 * UW);
   // the tile's h codes of the step, [NPL][16][H + 16] bytes
   int8_t *hs = reinterpret_cast<int8_t *>(sb + 16 * 13 * UW);
+  // gate tables, [3][kGateTabMax] (16-byte aligned: H is a multiple of 16)
+  int *gtab = reinterpret_cast<int *>(hs + NPL * kTileB * (H + 16));
   const int tid = threadIdx.x, w = tid / 64, l = tid % 64;
   const int utl = w / 4, kq = w % 4;
   const int ut = member * cl.UT + utl;
@@ -676,6 +695,21 @@ __device__ __forceinline__ void recurrence_cl_pair(const RecArgs &a, const StepP
     lut_f[g * 48 + 16 + s] = p.lut[g].qb[s];
     lut_f[g * 48 + 32 + s] = p.lut[g].c[s];
     lut_n[g * 16 + s] = p.lut[g].n[s];
+  }
+  const int *tab = nullptr;
+  if (cl.gate_tab) {
+    __syncthreads();  // the LUT is in LDS
+    const Bounds gin[3] = {p.zin, p.rin, p.nin}, gout[3] = {p.zout, p.rout, p.nout};
+    for (int i = tid; i < 3 * kGateTabMax; i += blockDim.x) {
+      const int g = i / kGateTabMax, e = i % kGateTabMax;
+      if (e <= static_cast<int>(gin[g].hi - gin[g].lo)) {
+        uint8_t k = 0;
+        const float v = pwl_eval(gin[g].lo + static_cast<float>(e), lut_f + 48 * g, lut_f + 48 * g + 16,
+                                 lut_n + 16 * g, lut_f + 48 * g + 32, p.lut[g].zp_x, gout[g], k);
+        gtab[i] = static_cast<int>(v) * 2 | k;
+      }
+    }
+    tab = gtab;  // read after the first cluster barrier (a workgroup barrier as well)
   }
   v4i rfr[kClMaxKPerWave][3];
 #pragma unroll
@@ -809,7 +843,7 @@ __device__ __forceinline__ void recurrence_cl_pair(const RecArgs &a, const StepP
       for (int g = 0; g < 3; ++g)
         gh3[g] = recombine_rh<NPL>(a.wide_acc, sum[g][0], sum[g][NPL - 1], plane_off, a.h_offset,
                                    cst[g][6]);
-      const PointOut o = gru_point(gih, gh3, cst, p, lut_f, lut_n, hold);
+      const PointOut o = gru_point(gih, gh3, cst, p, lut_f, lut_n, hold, tab);
       const float h2 = o.h;
       hold = h2;
       {
@@ -900,7 +934,7 @@ __global__ __launch_bounds__(512) void recurrence_cl(RecArgs a0, RecArgs a1,
 size_t recurrence_cl_lds_bytes(int UT, int npl, int H) {
   return 1024 + sizeof(v4i) * static_cast<size_t>(UT) * 4 * 3 * npl * 64 +
          static_cast<size_t>(16) * 16 * UT * (5 * sizeof(float) + 13) +
-         static_cast<size_t>(npl) * kTileB * (H + 16);
+         static_cast<size_t>(npl) * kTileB * (H + 16) + sizeof(int) * 3 * kGateTabMax;
 }
 
 
@@ -1191,6 +1225,12 @@ static int forward_recurrence_clustered(FwdPlan *plans, int ndir, int T, int B, 
   if (ncl >= 8) ncl -= ncl % 8;
   cl.UT = chosen;
   cl.stage_h = stage ? 1 : 0;
+  cl.gate_tab = 1;
+  for (int k = 0; k < ndir; ++k) {
+    const StepParams &sp = plans[k].sp;
+    for (const Bounds &g : {sp.zin, sp.rin, sp.nin})
+      if (!(g.hi - g.lo < static_cast<float>(kGateTabMax))) cl.gate_tab = 0;
+  }
   cl.ncl = ncl;
   const FwdWorkspace ws(T, B, I, H);
   cl.counters = reinterpret_cast<unsigned *>(plans[0].wsb + ws.sync);
