@@ -330,7 +330,13 @@ struct IClArgs {
   int8_t *hx;                   // [2][NPL][Bpad][H] exchanged h codes
   unsigned *counters;           // [ncl]
   int *timeout;
+  int gate_tab;                 // gate activations by table (every gate grid fits)
 };
+
+// Gate activations by table: a gate input is clamped to its grid, so when the grid has at most
+// kIGateTabMax codes the recurrence tabulates clampi(pwl_i(lo + e), out grid) once per launch
+// (value * 2 | keep of the output clamp per entry): one LDS read per gate and step.
+constexpr int kIGateTabMax = 1024;
 
 // R_q [H][3H] int32 codes -> int8 B fragments of v_mfma_i32_16x16x64_i8:
 // frag[((ut * 3 + g) * KS + s) * 64 + lane] holds R[k][c] for c = g*H + 16*ut + lane % 16,
@@ -376,6 +382,7 @@ __global__ __launch_bounds__(512) void int_recurrence_cl(IClArgs a, IntStepParam
   extern __shared__ __align__(16) unsigned char smem[];
   ILut *lut = reinterpret_cast<ILut *>(smem);
   v4i *red = reinterpret_cast<v4i *>(smem + (3 * sizeof(ILut) + 15) / 16 * 16);  // [UT][4][3][NPL][64]
+  int32_t *gtab = reinterpret_cast<int32_t *>(red + static_cast<size_t>(a.UT) * 4 * 3 * NPL * 64);
   const cluster::Place pl = cluster::place(a.G, a.ncl);
   unsigned *counter = a.counters + pl.cluster;
   const int H = a.H, C = 3 * H, B = a.B, KS = a.KS;
@@ -386,6 +393,27 @@ __global__ __launch_bounds__(512) void int_recurrence_cl(IClArgs a, IntStepParam
   const int nr = 4 * (l / 16) + kq;  // batch row finished by this lane
   for (int i = tid; i < 3 * static_cast<int>(sizeof(ILut) / 4); i += blockDim.x)
     reinterpret_cast<int32_t *>(lut)[i] = reinterpret_cast<const int32_t *>(p.lut)[i];
+  if (a.gate_tab) {
+    __syncthreads();  // the LUT is in LDS; the tables are read after the first cluster barrier
+    const IGrid gin[3] = {p.zin, p.rin, p.nin}, gout[3] = {p.zout, p.rout, p.nout};
+    for (int i = tid; i < 3 * kIGateTabMax; i += blockDim.x) {
+      const int g = i / kIGateTabMax, e = i % kIGateTabMax;
+      if (e <= gin[g].hi - gin[g].lo) {
+        uint8_t k = 0;
+        const int32_t v = clampi(pwl_i(gin[g].lo + e, lut[g]), gout[g], k);
+        gtab[i] = v * 2 | k;
+      }
+    }
+  }
+  // gate g of input code q (clamped to its grid): output code and output-clamp keep flag
+  auto gate = [&](int g, int32_t q, const IGrid &gi, const IGrid &go, uint8_t &keep) -> int32_t {
+    if (a.gate_tab) {
+      const int32_t e = gtab[g * kIGateTabMax + (q - gi.lo)];
+      keep = static_cast<uint8_t>(e & 1);
+      return e >> 1;
+    }
+    return clampi(pwl_i(q, lut[g]), go, keep);
+  };
   v4i rfr[kIMaxKPerWave][3];
 #pragma unroll
   for (int i = 0; i < kIMaxKPerWave; ++i) {
@@ -486,18 +514,18 @@ __global__ __launch_bounds__(512) void int_recurrence_cl(IClArgs a, IntStepParam
                                static_cast<int32_t>(rescale(static_cast<long long>(rh[0]) - p.zp_rh, p.hh_zin))),
                          p.zp_zin);
       in = clampi(in, p.zin, k_zi);
-      const int32_t z = clampi(pwl_i(in, lut[0]), p.zout, k_zo);
+      const int32_t z = gate(0, in, p.zin, p.zout, k_zo);
       in = add32(add32(static_cast<int32_t>(rescale(static_cast<long long>(wr) - p.zp_wx, p.ih_rin)),
                        static_cast<int32_t>(rescale(static_cast<long long>(rh[1]) - p.zp_rh, p.hh_rin))),
                  p.zp_rin);
       in = clampi(in, p.rin, k_ri);
-      const int32_t r = clampi(pwl_i(in, lut[1]), p.rout, k_ro);
+      const int32_t r = gate(1, in, p.rin, p.rout, k_ro);
       const long long rmul = (static_cast<long long>(r) - p.zp_rout) * (static_cast<long long>(rh[2]) - p.zp_rh);
       in = add32(add32(static_cast<int32_t>(rescale(static_cast<long long>(wn) - p.zp_wx, p.ih_nin)),
                        static_cast<int32_t>(rescale(rmul, p.rmul_nin))),
                  p.zp_nin);
       in = clampi(in, p.nin, k_ni);
-      const int32_t nn = clampi(pwl_i(in, lut[2]), p.nout, k_no);
+      const int32_t nn = gate(2, in, p.nin, p.nout, k_no);
       const int32_t n_h = add32(static_cast<int32_t>(rescale(static_cast<long long>(nn) - p.zp_nout, p.nout_h)), p.zp_h);
       const long long oldc = (static_cast<long long>(z) - p.zp_zout) * (static_cast<long long>(hold) - p.zp_h);
       const long long newc = (static_cast<long long>(p.quant_one) - z) * (static_cast<long long>(n_h) - p.zp_h);
@@ -658,8 +686,12 @@ static int int_recurrence_clustered(const IntCall &k, const IntStepParams &sp,
   // the smallest unit slice per workgroup whose grid fits one workgroup per CU, else two tiles
   a.UT = (H / 16) % 2 == 0 && static_cast<int64_t>(a.ntiles) * (H / 16) > ncu ? 2 : 1;
   a.G = H / (16 * a.UT);
+  a.gate_tab = 1;
+  for (const IGrid &g : {sp.zin, sp.rin, sp.nin})
+    if (static_cast<int64_t>(g.hi) - g.lo >= kIGateTabMax) a.gate_tab = 0;
   const size_t lds = (3 * sizeof(ILut) + 15) / 16 * 16 +
-                     sizeof(v4i) * static_cast<size_t>(a.UT) * 4 * 3 * npl * 64;
+                     sizeof(v4i) * static_cast<size_t>(a.UT) * 4 * 3 * npl * 64 +
+                     sizeof(int32_t) * 3 * kIGateTabMax;
   RXMET_CHECK_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                       static_cast<int>(lds)));
   int per_cu = 0;
