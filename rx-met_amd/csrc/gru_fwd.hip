@@ -696,8 +696,10 @@ __device__ __forceinline__ void recurrence_cl_pair(const RecArgs &a, const StepP
     lut_f[g * 48 + 32 + s] = p.lut[g].c[s];
     lut_n[g * 16 + s] = p.lut[g].n[s];
   }
+  // gate activations by table: only in the unstaged kernel (the staged one has no table; a
+  // runtime branch there measured 5% slower on H = 1024 steps that never take it)
   const int *tab = nullptr;
-  if (cl.gate_tab) {
+  if (!STAGE && cl.gate_tab) {
     __syncthreads();  // the LUT is in LDS
     const Bounds gin[3] = {p.zin, p.rin, p.nin}, gout[3] = {p.zout, p.rout, p.nout};
     for (int i = tid; i < 3 * kGateTabMax; i += blockDim.x) {
@@ -931,10 +933,10 @@ __global__ __launch_bounds__(512) void recurrence_cl(RecArgs a0, RecArgs a1,
   }
 }
 
-size_t recurrence_cl_lds_bytes(int UT, int npl, int H) {
+size_t recurrence_cl_lds_bytes(int UT, int npl, int H, bool gate_tab) {
   return 1024 + sizeof(v4i) * static_cast<size_t>(UT) * 4 * 3 * npl * 64 +
          static_cast<size_t>(16) * 16 * UT * (5 * sizeof(float) + 13) +
-         static_cast<size_t>(npl) * kTileB * (H + 16) + sizeof(int) * 3 * kGateTabMax;
+         static_cast<size_t>(npl) * kTileB * (H + 16) + (gate_tab ? sizeof(int) * 3 * kGateTabMax : 0);
 }
 
 
@@ -1188,10 +1190,6 @@ static int forward_recurrence_clustered(FwdPlan *plans, int ndir, int T, int B, 
     if (plans[k].npl != npl) return 0;
   if (KS > 4 * kClMaxKPerWave || std::getenv("RXMET_NO_CLUSTER") != nullptr) return 0;
   const bool stage = H >= kStageMinH;
-  const void *fn = npl == 1 ? (stage ? reinterpret_cast<const void *>(&recurrence_cl<1, true>)
-                                     : reinterpret_cast<const void *>(&recurrence_cl<1, false>))
-                            : (stage ? reinterpret_cast<const void *>(&recurrence_cl<2, true>)
-                                     : reinterpret_cast<const void *>(&recurrence_cl<2, false>));
   int device = 0, ncu = 0;
   RXMET_CHECK_HIP(hipGetDevice(&device));
   RXMET_CHECK_HIP(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, device));
@@ -1214,7 +1212,19 @@ static int forward_recurrence_clustered(FwdPlan *plans, int ndir, int T, int B, 
     }
   }
   if (!chosen) return 0;
-  const size_t lds_cl = recurrence_cl_lds_bytes(chosen, npl, H);
+  // gate tables (unstaged kernel only) when every gate grid has at most kGateTabMax codes
+  cl.gate_tab = stage ? 0 : 1;
+  for (int k = 0; k < ndir; ++k) {
+    const StepParams &sp = plans[k].sp;
+    for (const Bounds &g : {sp.zin, sp.rin, sp.nin})
+      if (!(g.hi - g.lo < static_cast<float>(kGateTabMax))) cl.gate_tab = 0;
+  }
+  const bool tab = cl.gate_tab != 0;
+  const void *fn = npl == 1 ? (stage ? reinterpret_cast<const void *>(&recurrence_cl<1, true>)
+                                     : reinterpret_cast<const void *>(&recurrence_cl<1, false>))
+                            : (stage ? reinterpret_cast<const void *>(&recurrence_cl<2, true>)
+                                     : reinterpret_cast<const void *>(&recurrence_cl<2, false>));
+  const size_t lds_cl = recurrence_cl_lds_bytes(chosen, npl, H, tab);
   RXMET_CHECK_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                       static_cast<int>(lds_cl)));
   int per_cu = 0;
@@ -1225,12 +1235,6 @@ static int forward_recurrence_clustered(FwdPlan *plans, int ndir, int T, int B, 
   if (ncl >= 8) ncl -= ncl % 8;
   cl.UT = chosen;
   cl.stage_h = stage ? 1 : 0;
-  cl.gate_tab = 1;
-  for (int k = 0; k < ndir; ++k) {
-    const StepParams &sp = plans[k].sp;
-    for (const Bounds &g : {sp.zin, sp.rin, sp.nin})
-      if (!(g.hi - g.lo < static_cast<float>(kGateTabMax))) cl.gate_tab = 0;
-  }
   cl.ncl = ncl;
   const FwdWorkspace ws(T, B, I, H);
   cl.counters = reinterpret_cast<unsigned *>(plans[0].wsb + ws.sync);
