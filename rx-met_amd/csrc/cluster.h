@@ -115,6 +115,23 @@ __device__ __forceinline__ int4 load_coherent16(const void *p) {
                    static_cast<int>(b >> 32));
 }
 
+// Buffer resource over `bytes` bytes at `base` (raw addressing, 32-bit offsets).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, static_cast<int>(bytes),
+                                           0x00020000);
+}
+
+// 16 bytes at a 16-byte aligned byte offset of a buffer in one instruction, with the cache policy
+// of an agent-scope atomic load (sc1: served from the coherence point, never from a stale
+// non-coherent line).  The 16 bytes are not one atomic access; the exchange never needs that,
+// since every exchanged store is complete before the barrier that precedes the load.
+__device__ __forceinline__ int4 load_coherent16(__amdgpu_buffer_rsrc_t r, unsigned off) {
+  constexpr int kSc1 = 16;  // cache-policy operand: sc1
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kSc1);
+  return make_int4(static_cast<int>(v[0]), static_cast<int>(v[1]), static_cast<int>(v[2]),
+                   static_cast<int>(v[3]));
+}
+
 // Store one byte per lane as packed 32-bit words: lanes 4k..4k+3 (which hold consecutive
 // bytes of the destination) combine into lane 4k, which writes the word at `dst4` (the
 // address of lane 4k's byte; lanes 4k+1..3 pass an ignored pointer).

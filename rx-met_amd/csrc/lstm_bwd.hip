@@ -336,25 +336,32 @@ __global__ __launch_bounds__(256) void lstm_bstep_finish(BwdArgs a, int S, const
 // (sequence, unit) pairs, the member writes dgates_hh * scale_W of its channels as 22-bit
 // block fixed point with one exponent per sequence (three int8 planes) to a global exchange
 // buffer, and after the cluster barrier dh = W_hh_deq^T dgates_hh of its units is summed on
-// v_mfma_i32_16x16x64_i8: the contraction runs member by member (each member's 256 channels
-// are four K-steps with one exponent), every member's exact plane sums are recombined in
-// double and scaled by that member's exponent, and the two K-halves (waves 0-3 and 4-7) are
-// added in a fixed order.  Each wave keeps the W_hh codes of its unit tile and K-half in VGPRs;
-// the exchanged planes are read from global memory once per workgroup and step into LDS, where
-// the four waves of a K-half share them.
+// v_mfma_i32_16x16x64_i8.  The contraction's K-steps (64 channels each, member-major) are
+// dealt to the eight waves in contiguous runs: each wave loads its own A fragments straight
+// from the exchange buffer into VGPRs (every exchanged byte is read by one wave, with no LDS
+// staging), multiplies them against the W_hh codes of all four unit tiles of the member (held
+// in VGPRs), recombines the exact plane sums of each member segment in double scaled by that
+// member's exponent, and the eight waves' partials are added in wave (K) order through LDS.
 constexpr int kBcUnits = 64;
-constexpr int kBcHalf = 4;  // members per K-half at most (H <= 512)
-constexpr int kStageQ = 2048 / 16 / 32;  // 16-byte chunks per thread and plane at C = 2048
+constexpr int kBcMaxKs = 4;  // K-steps per wave at most: 4H / 64 / 8 with H <= 512
 
 struct BwdClArgs {
   int ncl, G, ntiles, Bpad;
-  int8_t *xp;          // [2][3][Bpad][4H] planes of the exchanged dgates, K member-major
+  int8_t *xp;          // [2][3][ntiles][KS2][16][64] planes of the exchanged dgates, one 1 KB
+                       // block per (parity, plane, batch tile, K-step), see xblock
   int *xe;             // [2][Bpad][G] exponents
   const v4i *wfrag;    // W_hh^T fragments in member-major K order, see lstm_pack_whh_t_cl
-  const float *csum;   // [G][H] column sums of W_hh codes over each member's channels
+  const float *csum;   // [KS2][H] column sums of W_hh codes over each K-step's 64 channels
   unsigned *counters;
   int *timeout;
 };
+
+// Byte offset of the exchange buffer's block for (parity, plane, batch tile, K-step): the tile's
+// 16 rows x 64 channels of the step, row-major.  A wave reads a block as one MFMA A fragment
+// with a contiguous 16-byte load per lane (lane L: row L % 16, channels 16 (L / 16) .. + 15).
+__device__ __forceinline__ unsigned xblock(int par, int p, int tile, int ntiles, int KS2, int ks) {
+  return (static_cast<unsigned>((par * 3 + p) * ntiles + tile) * KS2 + ks) * 1024;
+}
 
 // A position k of the member-major contraction order -> channel c: member m's 256 channels,
 // unit-major with the four gates of a unit adjacent (so a lane packs its four gate bytes into
@@ -365,7 +372,7 @@ __device__ __forceinline__ int cl_channel(int k, int H) {
 }
 
 // frag[(jt * KS2 + s) * 64 + lane] = W[cl_channel(64 s + 16 (lane / 16) + e)][16 jt + lane % 16];
-// csum[m][j] = sum over member m's channels c of W[c][j].
+// csum[s][j] = sum over K-step s's channels c of W[c][j].
 __global__ __launch_bounds__(64) void lstm_pack_whh_t_cl(int H, int KS2, const float *__restrict__ wq,
                                                          v4i *__restrict__ frag,
                                                          float *__restrict__ csum) {
@@ -384,26 +391,74 @@ __global__ __launch_bounds__(64) void lstm_pack_whh_t_cl(int H, int KS2, const f
     wd[q] = pack4_i8(by[0], by[1], by[2], by[3]);
   }
   frag[static_cast<size_t>(idx) * 64 + lane] = v4i{wd[0], wd[1], wd[2], wd[3]};
-  if (s % 4 == 0 && lane < 16) {
+  if (lane < 16) {
     int sum = 0;
-    for (int k = 64 * s; k < 64 * s + 256; ++k)
+    for (int k = 64 * s; k < 64 * s + 64; ++k)
       sum += static_cast<int>(wq[static_cast<size_t>(cl_channel(k, H)) * H + j]);
-    csum[static_cast<size_t>(s / 4) * H + j] = static_cast<float>(sum);
+    csum[static_cast<size_t>(s) * H + j] = static_cast<float>(sum);
+  }
+}
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// The checkpoint block of one step for a member's 64 units of a 16-row batch tile, as copied
+// into LDS (16-byte chunks; rows past B repeat row B - 1 and are not used):
+//   gate_out  floats [16 rows][4 gates][64]      chunks    0..1023
+//   masks     bytes  [4 kinds][16][4 gates][64]  chunks 1024..2047 (gate_out, gate_in, ih, hh)
+//   values    floats [3][16][64]                 chunks 2048..2815 (cell_tanh, c_prev, grad_out)
+//   masks     bytes  [3][16][64]                 chunks 2816..3007 (hidden, cell_tanh, cell)
+constexpr int kCkInst = 47;  // 1 KB copies
+constexpr int kCkBytes = kCkInst * 1024;
+constexpr int kCkMaskOff = 1024 * 16, kCkValOff = 2048 * 16, kCkBitOff = 2816 * 16;
+
+// Start the copies of step t's checkpoint block into ck: one 1 KB LDS-DMA instruction per wave
+// and 64 chunks, dealt to waves 1-7 (wave 0 polls the cluster counter and keeps no loads of its
+// own outstanding).  Each instruction lies in one segment, so every branch is wave-uniform.
+__device__ __forceinline__ void ck_issue(const BwdArgs &a, int t, int b0, int u0, unsigned char *ck,
+                                         int w, int l) {
+  if (w == 0) return;
+  const int H = a.H, C = 4 * H;
+  const uint32_t BH = static_cast<uint32_t>(a.B) * H, BC = static_cast<uint32_t>(a.B) * C;
+  for (int k = w - 1; k < kCkInst; k += 7) {
+    const int q = k * 64 + l;
+    const void *src;
+    if (k < 16) {
+      const int R = q / 64, g = (q / 16) % 4, c = q % 16, b = min(b0 + R, a.B - 1);
+      src = a.gate_out + (static_cast<uint32_t>(t) * BC + static_cast<uint32_t>(b) * C + g * H + u0 + 4 * c);
+    } else if (k < 32) {
+      const int q2 = q - 1024, kind = q2 / 256, R = (q2 / 16) % 16, g = (q2 / 4) % 4, c = q2 % 4;
+      const int b = min(b0 + R, a.B - 1);
+      const uint8_t *m = kind == 0 ? a.gout_m : kind == 1 ? a.gin_m : kind == 2 ? a.ih_m : a.hh_m;
+      src = m + (static_cast<uint32_t>(t) * BC + static_cast<uint32_t>(b) * C + g * H + u0 + 16 * c);
+    } else if (k < 44) {
+      const int q3 = q - 2048, kind = q3 / 256, R = (q3 / 16) % 16, c = q3 % 16;
+      const uint32_t row = static_cast<uint32_t>(min(b0 + R, a.B - 1)) * H + u0 + 4 * c;
+      src = kind == 0 ? a.cell_tanh + (static_cast<uint32_t>(t) * BH + row)
+            : kind == 2 ? a.grad_out + (static_cast<uint32_t>(t) * BH + row)
+            : t == 0 ? a.c0_q + row
+                     : a.cell + (static_cast<uint32_t>(t - 1) * BH + row);
+    } else {
+      const int q4 = q - 2816, kind = q4 / 64, R = (q4 / 4) % 16, c = q4 % 4;
+      const uint32_t row = static_cast<uint32_t>(min(b0 + R, a.B - 1)) * H + u0 + 16 * c;
+      const uint8_t *m = kind == 0 ? a.hid_m : kind == 1 ? a.tanh_m : a.cell_m;
+      src = m + (static_cast<uint32_t>(t) * BH + row);
+    }
+    __builtin_amdgcn_global_load_lds(src, (lds_void *)(ck + 1024 * k), 16, 0, 0);
   }
 }
 
 __global__ __launch_bounds__(512) void lstm_bwd_recurrence_cl(BwdArgs a, BwdClArgs cl) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int H = a.H, C = 4 * H, B = a.B, KS2 = a.KS2, G = cl.G;
-  const int prow = C + 16;                                              // LDS plane row
-  int8_t *pl_s = reinterpret_cast<int8_t *>(smem);                      // [3][16][prow]
-  double *dred = reinterpret_cast<double *>(pl_s + 3 * kBB * prow);     // [8][64][4]
-  double *csl = dred + 8 * 64 * 4;                                      // [G][64]
-  int *exs = reinterpret_cast<int *>(csl + 64 * G);                     // [16][G]
-  unsigned *rowmax = reinterpret_cast<unsigned *>(exs + kBB * G);       // [16]
+  // every wave's partial dh: [8 waves][4 unit tiles][64 lanes][4 rows]
+  double *pd = reinterpret_cast<double *>(smem);
+  unsigned *rowmax = reinterpret_cast<unsigned *>(pd + 8 * 4 * 64 * 4);  // [16]
   int *rowexp = reinterpret_cast<int *>(rowmax + kBB);                  // [16]
   // the step's gate gradients of the member's units, [16 rows][8][64]: dli gates 0-3, dlh 4-7
   float *sdl = reinterpret_cast<float *>(rowexp + kBB);
+  // the step's checkpoint block (ck_issue)
+  unsigned char *ck = reinterpret_cast<unsigned char *>(sdl + kBB * 8 * kBcUnits);
+  const float *ckf = reinterpret_cast<const float *>(ck);
   const int tid = threadIdx.x, w = tid / 64, l = tid % 64;
   const int utl = w & 3, kh = w >> 2;
   const cluster::Place pl = cluster::place(G, cl.ncl);
@@ -412,33 +467,49 @@ __global__ __launch_bounds__(512) void lstm_bwd_recurrence_cl(BwdArgs a, BwdClAr
   const int j = 16 * jt + l % 16;
   const int nrow0 = 4 * (l / 16);
   if (tid < kBB) rowmax[tid] = 0u;
-  // zero-point term of every member's plane sums: 32896 * (column sum of its W_hh codes)
-  for (int i = tid; i < 64 * G; i += blockDim.x)
-    csl[i] = 32896.0 * static_cast<double>(cl.csum[static_cast<size_t>(i / 64) * H + 64 * m0 + i % 64]);
   float sw[4];
 #pragma unroll
   for (int g = 0; g < 4; ++g) sw[g] = a.s_whh[g * H + j];
-  // K-halves: members [0, mh) for waves 0-3, [mh, G) for waves 4-7 (at most kBcHalf each)
-  const int mh = (G + 1) / 2;
-  const int mlo = kh == 0 ? 0 : mh, mhi = kh == 0 ? mh : G;
-  // the wave's W_hh^T operands (its unit tile, its K-half) stay in VGPRs
-  v4i wr[kBcHalf][4];
+  // the wave's K-steps [ks0, ks0 + nks) (KS2 = 4G with G even, so nks = KS2 / 8 is whole); they
+  // belong to member mA, and to mB too when the run crosses a member boundary (G = 6)
+  const int nks = KS2 / 8, ks0 = w * nks;
+  const int mA = ks0 / 4, mB = (ks0 + nks - 1) / 4;
+  // W_hh^T operands of the member's four unit tiles over those K-steps stay in VGPRs
+  v4i wr[4][kBcMaxKs];
 #pragma unroll
-  for (int i = 0; i < kBcHalf; ++i)
+  for (int ut = 0; ut < 4; ++ut)
 #pragma unroll
-    for (int s4 = 0; s4 < 4; ++s4)
-      wr[i][s4] = mlo + i < mhi
-                      ? cl.wfrag[((static_cast<size_t>(jt)) * KS2 + 4 * (mlo + i) + s4) * 64 + l]
-                      : v4i{0, 0, 0, 0};
+    for (int i = 0; i < kBcMaxKs; ++i)
+      wr[ut][i] = i < nks ? cl.wfrag[((static_cast<size_t>(4 * m0 + ut)) * KS2 + ks0 + i) * 64 + l]
+                          : v4i{0, 0, 0, 0};
+  // column sums of the W_hh codes over each member segment's channels (integers, exact in
+  // float); the segment's plane sums carry 32896 times this as their zero-point term
+  float zc[2][4];
+#pragma unroll
+  for (int ut = 0; ut < 4; ++ut) {
+    float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kBcMaxKs; ++i) {
+      if (i >= nks) continue;
+      const float v = cl.csum[static_cast<size_t>(ks0 + i) * H + 64 * m0 + 16 * ut + l % 16];
+      if ((ks0 + i) / 4 == mA) s0 += v;
+      else s1 += v;
+    }
+    zc[0][ut] = s0;
+    zc[1][ut] = s1;
+  }
   unsigned *counter = cl.counters + pl.cluster;
   unsigned epoch = 0;
   bool alive = true;
-  const uint32_t BH = static_cast<uint32_t>(B) * H, BC = static_cast<uint32_t>(B) * C;
-  const size_t pstride = static_cast<size_t>(cl.Bpad) * C;
+  const uint32_t BC = static_cast<uint32_t>(B) * C;
+  const auto xr = cluster::buffer_rsrc(cl.xp, 6u * cl.ntiles * KS2 * 1024);
   __syncthreads();
 
   for (int tile = pl.cluster; tile < cl.ntiles && alive; tile += cl.ncl) {
     const int b0 = tile * kBB;
+    ck_issue(a, a.T - 1, b0, kBcUnits * m0, ck, w, l);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
     float dh[2], dc[2];
 #pragma unroll
     for (int rr = 0; rr < 2; ++rr) {
@@ -455,25 +526,24 @@ __global__ __launch_bounds__(512) void lstm_bwd_recurrence_cl(BwdArgs a, BwdClAr
 #pragma unroll
         for (int g = 0; g < 4; ++g) sv[rr][g] = lis[rr][g] = lhs[rr][g] = 0.0f;
         if (b >= B) continue;
-        // every checkpoint value and mask of the row is loaded before any is used
+        // the row's checkpoint values and masks from the step's block in LDS
+        const int R = nrow0 + 2 * kh + rr, uu = 16 * utl + l % 16;
         float r_go[4], r_ct, r_pc, r_gd;
         uint8_t r_hid, r_tanh, r_cell, r_gm[4], r_gin[4], r_ih[4], r_hh[4];
-        const uint32_t e = static_cast<uint32_t>(t) * BH + static_cast<uint32_t>(b) * H + j;
-        const uint32_t gb = static_cast<uint32_t>(t) * BC + static_cast<uint32_t>(b) * C + j;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          r_go[g] = a.gate_out[gb + g * H];
-          r_gm[g] = a.gout_m[gb + g * H];
-          r_gin[g] = a.gin_m[gb + g * H];
-          r_ih[g] = a.ih_m[gb + g * H];
-          r_hh[g] = a.hh_m[gb + g * H];
+          r_go[g] = ckf[(R * 4 + g) * 64 + uu];
+          r_gm[g] = ck[kCkMaskOff + ((0 * 16 + R) * 4 + g) * 64 + uu];
+          r_gin[g] = ck[kCkMaskOff + ((1 * 16 + R) * 4 + g) * 64 + uu];
+          r_ih[g] = ck[kCkMaskOff + ((2 * 16 + R) * 4 + g) * 64 + uu];
+          r_hh[g] = ck[kCkMaskOff + ((3 * 16 + R) * 4 + g) * 64 + uu];
         }
-        r_ct = a.cell_tanh[e];
-        r_pc = t == 0 ? a.c0_q[static_cast<uint32_t>(b) * H + j] : a.cell[e - BH];
-        r_gd = a.grad_out[e];
-        r_hid = a.hid_m[e];
-        r_tanh = a.tanh_m[e];
-        r_cell = a.cell_m[e];
+        r_ct = ckf[kCkValOff / 4 + (0 * 16 + R) * 64 + uu];
+        r_pc = ckf[kCkValOff / 4 + (1 * 16 + R) * 64 + uu];
+        r_gd = ckf[kCkValOff / 4 + (2 * 16 + R) * 64 + uu];
+        r_hid = ck[kCkBitOff + (0 * 16 + R) * 64 + uu];
+        r_tanh = ck[kCkBitOff + (1 * 16 + R) * 64 + uu];
+        r_cell = ck[kCkBitOff + (2 * 16 + R) * 64 + uu];
         const auto kp = [](uint8_t m) { return m == 0 ? 1.0f : 0.0f; };
         const float ig = deq(r_go[0], a.s_gout[0], a.zp_gout[0]);
         const float fg = deq(r_go[1], a.s_gout[1], a.zp_gout[1]);
@@ -538,7 +608,7 @@ __global__ __launch_bounds__(512) void lstm_bwd_recurrence_cl(BwdArgs a, BwdClAr
       __syncthreads();
 #pragma unroll
       for (int rr = 0; rr < 2; ++rr) {
-        const int nr = nrow0 + 2 * kh + rr, b = b0 + nr;
+        const int nr = nrow0 + 2 * kh + rr;
         const int ex = rowexp[nr];
         unsigned wd[3] = {0u, 0u, 0u};
 #pragma unroll
@@ -550,18 +620,22 @@ __global__ __launch_bounds__(512) void lstm_bwd_recurrence_cl(BwdArgs a, BwdClAr
           wd[1] |= static_cast<unsigned>((((uq >> 8) & 255) - 128) & 255) << (8 * g);
           wd[2] |= static_cast<unsigned>(((uq >> 16) - 128) & 255) << (8 * g);
         }
-        unsigned char *dst = reinterpret_cast<unsigned char *>(cl.xp) +
-                             (static_cast<size_t>(par) * 3 * cl.Bpad + b) * C + 256 * m0 +
-                             4 * (16 * utl + l % 16);
+        // channels 256 m0 + 4 (16 utl + l % 16) + 0..3: K-step 4 m0 + utl, channel 4 (l % 16)
 #pragma unroll
         for (int p = 0; p < 3; ++p)
-          cluster::store_coherent(reinterpret_cast<unsigned *>(dst + p * pstride), wd[p]);
+          cluster::store_coherent(
+              reinterpret_cast<unsigned *>(cl.xp + xblock(par, p, tile, cl.ntiles, KS2, 4 * m0 + utl) +
+                                           64 * nr + 4 * (l % 16)),
+              wd[p]);
       }
       // the other members only read the planes and exponents: arrive (which also publishes the
       // staged gate gradients), then store them for the weight GEMMs as 16-byte rows while
       // waiting
       cluster::arrive(counter);
       ++epoch;
+      // the next step's checkpoint block (the block of this step was read before the exponent
+      // barriers above); complete before the partial-sum barrier below
+      if (t > 0) ck_issue(a, t - 1, b0, kBcUnits * m0, ck, w, l);
       {
         const size_t tb = static_cast<size_t>(t) * BC;
         const int u0 = kBcUnits * m0;
@@ -580,68 +654,67 @@ __global__ __launch_bounds__(512) void lstm_bwd_recurrence_cl(BwdArgs a, BwdClAr
       }
       alive = cluster::wait(counter, epoch * G, cl.timeout);
       if (!alive) break;
-      // stage the tile's exchanged planes (all members) and exponents in LDS, once per workgroup
+      // dh partial of the wave's K-steps for the member's 64 units: A fragments (row l % 16,
+      // channels 64 ks + 16 (l / 16) + 0..15 of each plane) and the rows' exponents loaded
+      // together, then the MFMAs, one member segment at a time
       {
-        // 3 planes x 16 rows x C bytes: thread -> row tid / 32, 16-byte chunks tid % 32 + 32 q
-        // (C a multiple of 512 and at most 2048: q < C / 512 <= 4, uniform).  All loads are
-        // issued before any is stored; a q past the row re-reads chunk q = 0 and is not stored.
-        const int r = tid / 32, c0 = tid % 32, qn = C / 512;
-        const int8_t *src = cl.xp + (static_cast<size_t>(par) * 3 * cl.Bpad + b0 + r) * C + 16 * c0;
-        int8_t *dst = pl_s + r * prow + 16 * c0;
-        int4 v[3][kStageQ];
+        int4 av[kBcMaxKs][3];
 #pragma unroll
-        for (int p = 0; p < 3; ++p)
+        for (int i = 0; i < kBcMaxKs; ++i)
 #pragma unroll
-          for (int q = 0; q < kStageQ; ++q)
-            v[p][q] = cluster::load_coherent16(src + p * pstride + 512 * (q < qn ? q : 0));
+          for (int p = 0; p < 3; ++p)
+            av[i][p] = cluster::load_coherent16(
+                xr, xblock(par, p, tile, cl.ntiles, KS2, ks0 + (i < nks ? i : 0)) + 64 * (l % 16) + 16 * (l / 16));
+        const unsigned *xe =
+            reinterpret_cast<const unsigned *>(cl.xe) + (static_cast<size_t>(par) * cl.Bpad + b0 + nrow0) * G;
+        int exA[4], exB[4];
 #pragma unroll
-        for (int p = 0; p < 3; ++p)
+        for (int r = 0; r < 4; ++r) {
+          exA[r] = static_cast<int>(__hip_atomic_load(xe + r * G + mA, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+          exB[r] = static_cast<int>(__hip_atomic_load(xe + r * G + mB, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        }
+        // one unit tile at a time (its three plane sums in 12 VGPRs), K-steps in order
 #pragma unroll
-          for (int q = 0; q < kStageQ; ++q)
-            if (q < qn) *reinterpret_cast<int4 *>(dst + p * kBB * prow + 512 * q) = v[p][q];
-        for (int i = tid; i < kBB * G; i += blockDim.x)
-          exs[i] = static_cast<int>(__hip_atomic_load(
-              reinterpret_cast<const unsigned *>(cl.xe) + (static_cast<size_t>(par) * cl.Bpad + b0) * G + i,
-              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-      }
-      __syncthreads();
-      // dh of the tile's rows, this wave's K-half, member by member (in order)
-      double dsum[4] = {0.0, 0.0, 0.0, 0.0};
-      const int8_t *arow = pl_s + (l % 16) * prow + 16 * (l / 16);
+        for (int ut = 0; ut < 4; ++ut) {
+          double *d = pd + ((static_cast<size_t>(w) * 4 + ut) * 64 + l) * 4;
+          v4i acc[3] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}};
 #pragma unroll
-      for (int i = 0; i < kBcHalf; ++i) {
-        const int mm = mlo + i;
-        if (mm < mhi) {
-          v4i acc[3];
+          for (int i = 0; i < kBcMaxKs; ++i) {
+            if (i >= nks) continue;
 #pragma unroll
-          for (int p = 0; p < 3; ++p) acc[p] = v4i{0, 0, 0, 0};
+            for (int p = 0; p < 3; ++p)
+              acc[p] = mfma_i8(v4i{av[i][p].x, av[i][p].y, av[i][p].z, av[i][p].w}, wr[ut][i], acc[p]);
+            const int ks = ks0 + i;
+            if (i == nks - 1 || (ks & 3) == 3) {
+              // the end of a member segment: its exact sums scaled by the member's exponent go
+              // to the wave's partial (written by the first segment, the member mA; added to by
+              // the second)
+              const bool sa = ks / 4 == mA;
+              const double z = 32896.0 * static_cast<double>(sa ? zc[0][ut] : zc[1][ut]);
 #pragma unroll
-          for (int s4 = 0; s4 < 4; ++s4)
+              for (int r = 0; r < 4; ++r) {
+                const int ex = sa ? exA[r] : exB[r];
+                const double comb = 65536.0 * acc[2][r] + 256.0 * acc[1][r] +
+                                    static_cast<double>(acc[0][r]) + z;
+                const double v = ex == 1000 ? static_cast<double>(NAN) : ldexp(comb, -ex);
+                d[r] = sa ? v : d[r] + v;
+              }
 #pragma unroll
-            for (int p = 0; p < 3; ++p) {
-              const v4i afr = *reinterpret_cast<const v4i *>(arow + p * kBB * prow + 64 * (4 * mm + s4));
-              acc[p] = mfma_i8(afr, wr[i][s4], acc[p]);
+              for (int p = 0; p < 3; ++p) acc[p] = v4i{0, 0, 0, 0};
             }
-          const double zc = csl[mm * 64 + 16 * utl + l % 16];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int ex = exs[(nrow0 + r) * G + mm];
-            const double comb =
-                65536.0 * acc[2][r] + 256.0 * acc[1][r] + static_cast<double>(acc[0][r]) + zc;
-            dsum[r] += ex == 1000 ? static_cast<double>(NAN) : ldexp(comb, -ex);
           }
         }
       }
-      double *dr = dred + (static_cast<size_t>(w) * 64 + l) * 4;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) dr[r] = dsum[r];
+      __builtin_amdgcn_s_waitcnt(0);  // this wave's checkpoint copies are in LDS
       __syncthreads();
+      // each (unit, row) pair of the lane: the eight partials in wave (K) order
 #pragma unroll
       for (int rr = 0; rr < 2; ++rr) {
         const int r = 2 * kh + rr;
-        const double lo = dred[(static_cast<size_t>(utl) * 64 + l) * 4 + r];
-        const double hi = dred[(static_cast<size_t>(utl + 4) * 64 + l) * 4 + r];
-        dh[rr] = static_cast<float>(lo + hi);
+        double sum = 0.0;
+#pragma unroll
+        for (int w2 = 0; w2 < 8; ++w2) sum += pd[((static_cast<size_t>(w2) * 4 + utl) * 64 + l) * 4 + r];
+        dh[rr] = static_cast<float>(sum);
       }
     }
     if (!alive) break;
@@ -656,9 +729,9 @@ __global__ __launch_bounds__(512) void lstm_bwd_recurrence_cl(BwdArgs a, BwdClAr
   }
 }
 
-size_t bwd_cl_lds(int C, int G) {
-  return 3 * kBB * static_cast<size_t>(C + 16) + sizeof(double) * (8 * 64 * 4 + 64 * G) +
-         sizeof(int) * kBB * G + 2 * sizeof(int) * kBB + sizeof(float) * kBB * 8 * kBcUnits;
+size_t bwd_cl_lds() {
+  return sizeof(double) * 8 * 4 * 64 * 4 + 2 * sizeof(int) * kBB + sizeof(float) * kBB * 8 * kBcUnits +
+         kCkBytes;
 }
 
 size_t bwd_lds(int H, int KS2) {
@@ -728,7 +801,7 @@ struct BwdWorkspace {
     // clustered recurrence (H a multiple of 64)
     const size_t Bpad = (static_cast<size_t>(B) + kBB - 1) / kBB * kBB, G = H / kBcUnits + 1;
     wfrag_cl = o; o += al(sizeof(v4i) * 64 * (H / 16) * KS2);
-    csum = o; o += al(sizeof(float) * G * H);
+    csum = o; o += al(sizeof(float) * KS2 * H);
     xp = o; o += al(2 * 3 * Bpad * C);
     xe = o; o += al(sizeof(int) * 2 * Bpad * G);
     sync = o; o += al(sizeof(unsigned) * (Bpad / kBB + 1));
@@ -882,10 +955,18 @@ int rxmet_lstm_backward_quant(int32_t T, int32_t B, int32_t I, int32_t H,
     }
     recurrence_done = true;
   }
-  if (!stepped && H % (2 * kBcUnits) == 0 && H / kBcUnits <= 2 * kBcHalf &&
+  // (the exchange buffer, 6 Bpad C bytes, is addressed with 32-bit buffer offsets; checkpoint
+  // rows are copied into LDS as 16-byte chunks)
+  const auto a16 = [](const void *p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+  const bool ck_aligned = a16(sv.gate_out) && a16(sv.cell) && a16(sv.cell_tanh) && a16(sv.c0_q) &&
+                          a16(grad_output) && a16(sv.ih_linear_m) && a16(sv.hh_linear_m) &&
+                          a16(sv.gate_in_m) && a16(sv.gate_out_m) && a16(sv.cell_m) &&
+                          a16(sv.cell_tanh_m) && a16(sv.hidden_m);
+  if (!stepped && H % (2 * kBcUnits) == 0 && KS2 <= 8 * kBcMaxKs && ck_aligned &&
+      6.0 * ((B + kBB - 1) / kBB * kBB) * C < 2147483648.0 &&
       std::getenv("RXMET_NO_CLUSTER") == nullptr) {
     const void *fn = reinterpret_cast<const void *>(&lstm_bwd_recurrence_cl);
-    const size_t lds_cl = bwd_cl_lds(C, H / kBcUnits);
+    const size_t lds_cl = bwd_cl_lds();
     int device = 0, ncu = 0, per_cu = 0;
     RXMET_CHECK_HIP(hipGetDevice(&device));
     RXMET_CHECK_HIP(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, device));
