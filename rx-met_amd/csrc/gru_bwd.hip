@@ -27,6 +27,8 @@
 //                    (wgrad_gemm.h; dW and dR split over the long T*B reduction and summed in
 //                    a fixed order), then one mask pass.
 
+#include <algorithm>
+
 #include "cluster.h"
 #include "gru_internal.h"
 #include "mfma_frag.h"
@@ -90,7 +92,7 @@ struct BwdArgs {
   double *bias_partial;      // [numWG][2][3H]
   float *dh0;                // [B, H]
   float *xch;                // clustered path: [2][Bpad][KP] exchanged dq * scale_R
-  const float *rt;           // clustered path: packed R_q values, see pack_rt_f32
+  const uint4 *rt;           // clustered path: packed R_q codes, see pack_rt_bf16
 };
 
 constexpr int kPlanes = 3;
@@ -302,10 +304,13 @@ __global__ __launch_bounds__(512) void bwd_recurrence(BwdArgs a) {
 // Member m of a cluster owns UT unit tiles (16 units) of one 16-sequence batch tile.  Per step
 // each lane finishes the STE pointwise of one (sequence, unit), writes dq * scale_R of its
 // three channels to a global exchange buffer (coherent stores), and after the cluster barrier
-// the four waves of a unit tile compute dh += R_deq dq for that tile on fp32 MFMA
-// (v_mfma_f32_16x16x4_f32), each over a quarter of the 3H channels with its R_q values
-// resident in VGPRs, and add their partial sums through LDS in a fixed order.
+// the four waves of a unit tile compute dh += R_deq dq for that tile on bf16 MFMA
+// (v_mfma_f32_16x16x32_bf16), each over a quarter of the 3H channels: the exchanged values
+// split exactly into three bf16 terms against the R_q codes (resident in VGPRs as one bf16
+// plane, or two for codes beyond +-256: the RNE bf16 of the code and the exact residual), fp32
+// accumulation; the four partial sums are added through LDS in a fixed order.
 constexpr int kBwMaxKS2 = 12;  // 3H <= 768
+constexpr int kBwMaxKB = (kBwMaxKS2 + 1) / 2;  // 32-channel MFMA blocks per wave
 constexpr int kMaxHStepped = 1024;
 constexpr int kStepMaxSplit = 8;  // K splits of the stepped dh GEMM
 
@@ -315,16 +320,31 @@ struct BwdClArgs {
   int *timeout;
 };
 
-// R_q [H][3H] -> per (unit tile ut, wave q, MFMA i, lane l) the B value R_q[j][k] with
-// j = 16 ut + l % 16 and k = 16 (q KS2 + i / 4) + 4 (l / 16) + i % 4 (0 beyond 3H).
-__global__ __launch_bounds__(64) void pack_rt_f32(int H, int KS2, const float *__restrict__ Rq,
-                                                  float *__restrict__ rt) {
-  const int l = threadIdx.x, idx = blockIdx.x;  // idx = (ut * 4 + q) * 4 KS2 + i
-  const int n = 4 * KS2;
-  const int i = idx % n, q = (idx / n) % 4, ut = idx / (4 * n);
+// R_q [H][3H] -> per (unit tile ut, wave q, 32-channel block kb, lane l) the bf16 B fragment
+// R_q[j][k + e], e = 0..7, with j = 16 ut + l % 16 and k = 16 q KS2 + 32 kb + 8 (l / 16): wave q
+// contracts channels [16 q KS2, 16 (q + 1) KS2), zero beyond them and beyond 3H.  Plane 0 holds
+// the RNE bf16 of each code; with two planes plane 1 (at rt + nfrag * 64, nfrag = gridDim.x)
+// holds the residual code - plane 0, exact in bf16 for |code| < 2^16.
+__global__ __launch_bounds__(64) void pack_rt_bf16(int H, int KS2, int nplanes, const float *__restrict__ Rq,
+                                                   uint4 *__restrict__ rt) {
+  const int l = threadIdx.x, idx = blockIdx.x;  // idx = (ut * 4 + q) * nkb + kb
+  const int nkb = (KS2 + 1) / 2;
+  const int kb = idx % nkb, q = (idx / nkb) % 4, ut = idx / (4 * nkb);
   const int j = 16 * ut + l % 16;
-  const int k = 16 * (q * KS2 + i / 4) + 4 * (l / 16) + i % 4;
-  rt[static_cast<size_t>(idx) * 64 + l] = k < 3 * H ? Rq[static_cast<size_t>(j) * 3 * H + k] : 0.0f;
+  const int k0 = 16 * q * KS2 + 32 * kb + 8 * (l / 16), kend = min(16 * (q + 1) * KS2, 3 * H);
+  float v[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = k0 + e < kend ? Rq[static_cast<size_t>(j) * 3 * H + k0 + e] : 0.0f;
+  unsigned w[4], r[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const v2f x = v2f{v[2 * e], v[2 * e + 1]};
+    w[e] = pack_bf16x2(x);
+    r[e] = pack_bf16x2(x - unpack_bf16x2(w[e]));
+  }
+  rt[static_cast<size_t>(idx) * 64 + l] = make_uint4(w[0], w[1], w[2], w[3]);
+  if (nplanes == 2)
+    rt[(static_cast<size_t>(gridDim.x) + idx) * 64 + l] = make_uint4(r[0], r[1], r[2], r[3]);
 }
 
 // A mask that may be absent.  The load is unconditional (an absent mask reads the same index
@@ -404,7 +424,7 @@ __host__ __device__ constexpr size_t bwd_cl_lds(int KP) {
 
 // One (direction, batch tile) pair, run by one member of UT unit tiles; writes the pair's
 // bias partials.
-template <int UT>
+template <int UT, int NPL>
 __device__ __forceinline__ void bwd_cl_pair(const BwdArgs &a, const BwdClArgs &cl, int tile,
                                             int member, unsigned *counter, unsigned &epoch,
                                             bool &alive) {
@@ -422,10 +442,16 @@ __device__ __forceinline__ void bwd_cl_pair(const BwdArgs &a, const BwdClArgs &c
   const int srow = tid / (16 * UT), sc0 = tid % (16 * UT), sqn = (KS2 + UT - 1) / UT;
   const int j = 16 * ut + l % 16;
   const int nr = 4 * (l / 16) + kq;
-  float rtv[4 * kBwMaxKS2];
+  const int nkb = (KS2 + 1) / 2;
+  const size_t nfrag = static_cast<size_t>(H / 16) * 4 * nkb;
+  v8bf rtb[NPL][kBwMaxKB];
 #pragma unroll
-  for (int i = 0; i < 4 * kBwMaxKS2; ++i)
-    rtv[i] = i < 4 * KS2 ? a.rt[((static_cast<size_t>(ut) * 4 + kq) * 4 * KS2 + i) * 64 + l] : 0.0f;
+  for (int pl = 0; pl < NPL; ++pl)
+#pragma unroll
+    for (int i = 0; i < kBwMaxKB; ++i)
+      rtb[pl][i] = __builtin_bit_cast(
+          v8bf, i < nkb ? a.rt[(pl * nfrag + (static_cast<size_t>(ut) * 4 + kq) * nkb + i) * 64 + l]
+                        : make_uint4(0, 0, 0, 0));
   float effr[3];
   float mbw[3], mbr[3];
 #pragma unroll
@@ -437,6 +463,8 @@ __device__ __forceinline__ void bwd_cl_pair(const BwdArgs &a, const BwdClArgs &c
   double sbw[3] = {0.0, 0.0, 0.0}, sbr[3] = {0.0, 0.0, 0.0};
   const uint32_t BH = static_cast<uint32_t>(B) * H;
   v4f *myred = red + (static_cast<size_t>(utl) * 4 + kq) * 64;
+  // the exchange buffer, [2][Bpad][KP] floats (32-bit byte offsets: checked by the launcher)
+  const auto xr = cluster::buffer_rsrc(a.xch, 8u * cl.Bpad * KP);
   const BwdMasks mk = {mask_ref(a.h_m, a.v), mask_ref(a.gout_m, a.v), mask_ref(a.gin_m, a.v),
                        mask_ref(a.hh_m, a.v), mask_ref(a.ih_m, a.v)};
 
@@ -483,13 +511,13 @@ __device__ __forceinline__ void bwd_cl_pair(const BwdArgs &a, const BwdClArgs &c
       // stage the tile's exchange rows in LDS (all loads in flight; a q past the row re-reads
       // q = 0 and is not stored), then dh += R_deq dq over this wave's quarter of the channels
       {
-        const float *src = a.xch + (static_cast<size_t>(par) * cl.Bpad + b0 + srow) * KP + 4 * sc0;
+        const unsigned src = 4u * ((static_cast<unsigned>(par) * cl.Bpad + b0 + srow) * KP + 4 * sc0);
         float *dst = xs + srow * (KP + 4) + 4 * sc0;
         int4 sv[kQ];
 #pragma unroll
         for (int q = 0; q < kQ; ++q) {
           const int qq = (q < sqn && 16 * UT * q + sc0 < 16 * KS2) ? q : 0;
-          sv[q] = cluster::load_coherent16(src + 64 * UT * qq);
+          sv[q] = cluster::load_coherent16(xr, src + 256u * UT * qq);
         }
 #pragma unroll
         for (int q = 0; q < kQ; ++q)
@@ -499,15 +527,26 @@ __device__ __forceinline__ void bwd_cl_pair(const BwdArgs &a, const BwdClArgs &c
       __syncthreads();
       v4f acc = {0.f, 0.f, 0.f, 0.f};
       {
-        const float *arow = xs + (l % 16) * (KP + 4) + 16 * (kq * KS2) + 4 * (l / 16);
+        // A: row l % 16, channels 16 kq KS2 + 32 kb + 8 (l / 16) + 0..7 (zero past the wave's
+        // channels, which another wave contracts), split into three bf16 terms, smallest first
+        const float *arow = xs + (l % 16) * (KP + 4) + 16 * (kq * KS2) + 8 * (l / 16);
 #pragma unroll
-        for (int qg = 0; qg < kBwMaxKS2; ++qg)
-          if (qg < KS2) {
-            const v4f av = *reinterpret_cast<const v4f *>(arow + 16 * qg);
-            acc = mfma_f32(av[0], rtv[4 * qg + 0], acc);
-            acc = mfma_f32(av[1], rtv[4 * qg + 1], acc);
-            acc = mfma_f32(av[2], rtv[4 * qg + 2], acc);
-            acc = mfma_f32(av[3], rtv[4 * qg + 3], acc);
+        for (int kb = 0; kb < kBwMaxKB; ++kb)
+          if (kb < nkb) {
+            const bool in = 32 * kb + 8 * (l / 16) < 16 * KS2;
+            const float *ap = arow + (in ? 32 * kb : 0);  // (a lane past the row reads its start)
+            const v4f a0 = *reinterpret_cast<const v4f *>(ap);
+            const v4f a1 = *reinterpret_cast<const v4f *>(ap + 4);
+            const float v[8] = {in ? a0[0] : 0.f, in ? a0[1] : 0.f, in ? a0[2] : 0.f, in ? a0[3] : 0.f,
+                                in ? a1[0] : 0.f, in ? a1[1] : 0.f, in ? a1[2] : 0.f, in ? a1[3] : 0.f};
+            uint4 h, m, o;
+            split3x8(v, h, m, o);
+#pragma unroll
+            for (int pl = 0; pl < NPL; ++pl) {
+              acc = mfma_bf16(__builtin_bit_cast(v8bf, o), rtb[pl][kb], acc);
+              acc = mfma_bf16(__builtin_bit_cast(v8bf, m), rtb[pl][kb], acc);
+              acc = mfma_bf16(__builtin_bit_cast(v8bf, h), rtb[pl][kb], acc);
+            }
           }
       }
       myred[l] = acc;
@@ -557,7 +596,7 @@ __device__ __forceinline__ void bwd_cl_pair(const BwdArgs &a, const BwdClArgs &c
   }
 }
 
-template <int UT>
+template <int UT, int NPL>
 __global__ __launch_bounds__(256 * UT) void bwd_recurrence_cl(BwdArgs a0, BwdArgs a1, BwdClArgs cl) {
   const cluster::Place pl = cluster::place(cl.G, cl.ncl);
   unsigned *counter = cl.counters + pl.cluster;
@@ -567,7 +606,7 @@ __global__ __launch_bounds__(256 * UT) void bwd_recurrence_cl(BwdArgs a0, BwdArg
     const int d = pair / cl.ntiles, tile = pair % cl.ntiles;
     __syncthreads();
     // one copy of the step code for both directions (d is uniform across the workgroup)
-    bwd_cl_pair<UT>(d == 0 ? a0 : a1, cl, tile, pl.member, counter, epoch, alive);
+    bwd_cl_pair<UT, NPL>(d == 0 ? a0 : a1, cl, tile, pl.member, counter, epoch, alive);
   }
 }
 
@@ -735,7 +774,7 @@ struct BwdWorkspace {
     // clustered recurrence: dq exchange, packed R_q values, counters
     const size_t Bpad = nwg * kBTile;
     xch = o; o += al(sizeof(float) * 2 * Bpad * KS2 * 64);
-    rt = o; o += al(sizeof(float) * ((H + 15) / 16) * 4 * 4 * KS2 * 64);
+    rt = o; o += al(sizeof(uint4) * 2 * ((H + 15) / 16) * 4 * ((KS2 + 1) / 2) * 64);
     sync = o; o += al(sizeof(unsigned) * (2 * nwg + 2));  // clusters of both directions
     // stepped recurrence: R codes as bf16 planes [H][Cp], the dh GEMM output, dhl
     Cp = static_cast<int>((C + 31) / 32 * 32);
@@ -833,7 +872,7 @@ static int backward_prologue(int T, int B, int I, int H, const rxmet_gru_bwd_dir
   ba.bias_partial = reinterpret_cast<double *>(wsb + ws.bias);
   ba.dh0 = d.dh0;
   ba.xch = reinterpret_cast<float *>(wsb + ws.xch);
-  ba.rt = reinterpret_cast<float *>(wsb + ws.rt);
+  ba.rt = reinterpret_cast<uint4 *>(wsb + ws.rt);
   plan->d = &d;
   plan->wsb = wsb;
   return 0;
@@ -845,6 +884,8 @@ static int backward_recurrence_clustered(BwdPlan *plans, int ndir, int T, int B,
                                          hipStream_t stream, int **timeout_flag) {
   const int C = 3 * H, KS2 = (C + 63) / 64;
   if (KS2 > kBwMaxKS2 || std::getenv("RXMET_NO_CLUSTER") != nullptr) return 0;
+  // the exchange buffer (2 Bpad KP floats) is addressed with 32-bit byte offsets
+  if (8.0 * ((B + kBTile - 1) / kBTile * kBTile) * (64.0 * KS2) >= 2147483648.0) return 0;
   const size_t lds_cl = bwd_cl_lds(KS2 * 64);
   int device = 0, ncu = 0;
   RXMET_CHECK_HIP(hipGetDevice(&device));
@@ -867,8 +908,17 @@ static int backward_recurrence_clustered(BwdPlan *plans, int ndir, int T, int B,
     }
   }
   if (!chosen) return 0;
-  const void *fn = chosen == 1 ? reinterpret_cast<const void *>(&bwd_recurrence_cl<1>)
-                               : reinterpret_cast<const void *>(&bwd_recurrence_cl<2>);
+  // bf16 planes of the R codes (one when every direction's codes are within +-256)
+  int npr = 1;
+  for (int k = 0; k < ndir; ++k) {
+    const rxmet_gru_qparams *q = plans[k].d->params;
+    const Bounds br = bounds_of(q->chan_bits[RXMET_GRU_R], q->chan_unsigned[RXMET_GRU_R]);
+    npr = std::max(npr, wgrad::planes_for(br.lo, br.hi, 0.0));
+  }
+  const void *fn = chosen == 1 ? (npr == 1 ? reinterpret_cast<const void *>(&bwd_recurrence_cl<1, 1>)
+                                           : reinterpret_cast<const void *>(&bwd_recurrence_cl<1, 2>))
+                               : (npr == 1 ? reinterpret_cast<const void *>(&bwd_recurrence_cl<2, 1>)
+                                           : reinterpret_cast<const void *>(&bwd_recurrence_cl<2, 2>));
   RXMET_CHECK_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                       static_cast<int>(lds_cl)));
   int per_cu = 0;
@@ -883,8 +933,8 @@ static int backward_recurrence_clustered(BwdPlan *plans, int ndir, int T, int B,
   cl.counters = reinterpret_cast<unsigned *>(plans[0].wsb + ws.sync);
   cl.timeout = reinterpret_cast<int *>(cl.counters + ncl);
   for (int k = 0; k < ndir; ++k) {
-    hipLaunchKernelGGL(pack_rt_f32, dim3((H / 16) * 4 * 4 * KS2), dim3(64), 0, stream, H, KS2,
-                       plans[k].d->R_q, const_cast<float *>(plans[k].ba.rt));
+    hipLaunchKernelGGL(pack_rt_bf16, dim3((H / 16) * 4 * ((KS2 + 1) / 2)), dim3(64), 0, stream, H, KS2,
+                       npr, plans[k].d->R_q, const_cast<uint4 *>(plans[k].ba.rt));
     RXMET_CHECK_LAUNCH();
     // padding channels of the exchange rows stay zero
     const int64_t nx = static_cast<int64_t>(2) * cl.Bpad * cl.KP;

@@ -301,7 +301,8 @@ struct RecArgs {
   float *hout;              // [T+1, B, H] dequantised (row 0 written by quant_input)
   float *v;                 // [T, B, 4H] dequantised
   uint8_t *ih_m, *hh_m, *gin_m, *gout_m, *h_m;
-  int8_t *hx;               // clustered path: [2][NPL][Bpad][H] exchanged h codes
+  int8_t *hx;               // clustered path: [2][NPL][Bpad / 16][KS][16][64] exchanged h codes
+                            // (1 KB blocks of 16 rows x 64 units, see hx_offset)
   int wide_out;             // clustered path: outputs 16-byte aligned (H % 16 == 0), stored
                             // through the LDS staging area as 16-byte rows
   int wide_acc;             // |R_q h| can reach 2^31: recombine the plane sums in int64
@@ -662,6 +663,13 @@ __device__ __forceinline__ void flush_masks(uint8_t *arr, int f0, int ng, const 
   }
 }
 
+// Byte offset of (row b, unit j) in one plane of the exchange buffer: blocks of 16 rows x 64
+// units, row-major inside, one per (batch tile, K-step), so that a wave reads an MFMA A fragment
+// (lane L: row L % 16, units 16 (L / 16) .. + 15 of the step) as 1 KB of contiguous bytes.
+__device__ __forceinline__ unsigned hx_offset(int b, int j, int KS) {
+  return ((static_cast<unsigned>(b / kTileB) * KS + j / 64) * kTileB + b % kTileB) * 64 + j % 64;
+}
+
 // One (direction, batch tile) pair of the clustered recurrence, run by one member.
 template <int NPL, bool STAGE>
 __device__ __forceinline__ void recurrence_cl_pair(const RecArgs &a, const StepParams &p,
@@ -728,7 +736,9 @@ __device__ __forceinline__ void recurrence_cl_pair(const RecArgs &a, const StepP
     for (int q = 0; q < kChanParams; ++q) cst[g][q] = a.chan[q * C + g * H + j];
 
   const float plane_off = 128.0f + a.h_offset;
-  const size_t plane_stride = static_cast<size_t>(cl.Bpad) * H;
+  const unsigned plane_stride = static_cast<unsigned>(cl.Bpad) * KS * 64;
+  // the exchange buffer, 2 NPL planes (32-bit byte offsets: checked by the launcher)
+  const auto xr = cluster::buffer_rsrc(a.hx, 2u * NPL * plane_stride);
   v4i *myred = red + (static_cast<size_t>(utl) * 4 + kq) * 3 * NPL * 64;
 
   {
@@ -737,7 +747,7 @@ __device__ __forceinline__ void recurrence_cl_pair(const RecArgs &a, const StepP
     float hold = valid ? a.h0codes[static_cast<size_t>(b) * H + j] : p.zp_h;
     {
       const int hcv = static_cast<int>(hold - a.h_offset);
-      unsigned char *dst = reinterpret_cast<unsigned char *>(a.hx) + static_cast<size_t>(b) * H + j;
+      unsigned char *dst = reinterpret_cast<unsigned char *>(a.hx) + hx_offset(b, j, KS);
 #pragma unroll
       for (int q = 0; q < NPL; ++q)
         cluster::store_bytes_coherent(dst + q * plane_stride,
@@ -754,8 +764,8 @@ __device__ __forceinline__ void recurrence_cl_pair(const RecArgs &a, const StepP
 
     for (int t = 0; t < a.T && alive; ++t) {
       const int par = t & 1;
-      const int8_t *hin = a.hx + static_cast<size_t>(par) * NPL * plane_stride;
-      int8_t *hout = a.hx + static_cast<size_t>(par ^ 1) * NPL * plane_stride;
+      const unsigned hin = par * NPL * plane_stride;  // byte offset of the step's planes
+      int8_t *hout = a.hx + (par ^ 1) * NPL * plane_stride;
       float gih[3] = {gi_next[0], gi_next[1], gi_next[2]};
       // partial recurrent sums over this wave's K-steps
       v4i acc[3][NPL];
@@ -767,21 +777,23 @@ __device__ __forceinline__ void recurrence_cl_pair(const RecArgs &a, const StepP
         // the tile's h codes are read from the exchange buffer once per workgroup (16-byte
         // coherent loads, all issued before any is stored) into LDS, where the unit tiles
         // share them (at H >= 512; at smaller H the extra barrier costs more than it saves)
-        const int rs = H + 16, cpr = H / 16, n = NPL * kTileB * cpr, nt = blockDim.x;
+        // 16-byte chunk e -> plane p, K-step s, row r, chunk c of the step: the tile's blocks
+        // in order, 1 KB per 64 threads; chunks past H (a partial last step) are not stored
+        const int rs = H + 16, n = NPL * KS * 64, nt = blockDim.x;
+        const unsigned tb = hin + static_cast<unsigned>(tile) * KS * 1024;
         int4 hv[kHsMax];
 #pragma unroll
         for (int i = 0; i < kHsMax; ++i) {
           const int e0 = tid + nt * i, e = e0 < n ? e0 : 0;
-          const int p = e / (kTileB * cpr), r = (e / cpr) % kTileB, c = e % cpr;
-          hv[i] = cluster::load_coherent16(hin + p * plane_stride + static_cast<size_t>(b0 + r) * H + 16 * c);
+          const int p = e / (KS * 64), s = (e / 64) % KS;
+          hv[i] = cluster::load_coherent16(xr, tb + p * plane_stride + s * 1024 + 16 * (e % 64));
         }
 #pragma unroll
         for (int i = 0; i < kHsMax; ++i) {
           const int e = tid + nt * i;
-          if (e < n) {
-            const int p = e / (kTileB * cpr), r = (e / cpr) % kTileB, c = e % cpr;
+          const int p = e / (KS * 64), s = (e / 64) % KS, r = (e / 4) % kTileB, c = 4 * s + e % 4;
+          if (e < n && 16 * c < H)
             *reinterpret_cast<int4 *>(hs + (p * kTileB + r) * rs + 16 * c) = hv[i];
-          }
         }
         __syncthreads();
         const int8_t *hrow = hs + (l % 16) * rs + 16 * (l / 16);
@@ -801,14 +813,15 @@ __device__ __forceinline__ void recurrence_cl_pair(const RecArgs &a, const StepP
               for (int q = 0; q < NPL; ++q) acc[g][q] = mfma_i8(hfr[i][q], rfr[i][g], acc[g][q]);
           }
       } else {
-        const int8_t *hrow = hin + static_cast<size_t>(b0 + l % 16) * H + 16 * (l / 16);
+        // lane l: row l % 16, units 16 (l / 16) .. + 15 of K-step kq + 4 i
+        const unsigned hrow = hin + static_cast<unsigned>(tile) * KS * 1024 + 64 * (l % 16) + 16 * (l / 16);
         v4i hfr[kClMaxKPerWave][NPL];
 #pragma unroll
         for (int i = 0; i < kClMaxKPerWave; ++i)
 #pragma unroll
           for (int q = 0; q < NPL; ++q)
             if (kq + 4 * i < KS) {
-              const int4 v = cluster::load_coherent16(hrow + q * plane_stride + 64 * (kq + 4 * i));
+              const int4 v = cluster::load_coherent16(xr, hrow + q * plane_stride + 1024 * (kq + 4 * i));
               hfr[i][q] = v4i{v.x, v.y, v.z, v.w};
             }
 #pragma unroll
@@ -850,7 +863,7 @@ __device__ __forceinline__ void recurrence_cl_pair(const RecArgs &a, const StepP
       hold = h2;
       {
         const int hcv = static_cast<int>(h2 - a.h_offset);
-        unsigned char *dst = reinterpret_cast<unsigned char *>(hout) + static_cast<size_t>(b) * H + j;
+        unsigned char *dst = reinterpret_cast<unsigned char *>(hout) + hx_offset(b, j, KS);
 #pragma unroll
         for (int q = 0; q < NPL; ++q)
           cluster::store_bytes_coherent(dst + q * plane_stride,
@@ -960,7 +973,7 @@ struct FwdWorkspace {
     hostblk = o; o += al(sizeof(float) * 8 * C);  // eff[4C], ibx, ibh, igx, igh
     rfrag = o; o += al(sizeof(v4i) * 64 * static_cast<size_t>(H / 16) * 3 * ((H + 63) / 64));
     const size_t Bpad = (static_cast<size_t>(B) + kTileB - 1) / kTileB * kTileB;
-    hx = o; o += al(2 * 2 * Bpad * H);
+    hx = o; o += al(2 * 2 * Bpad * ((H + 63) / 64) * 64);
     sync = o; o += al(sizeof(unsigned) * (2 * (Bpad / kTileB) + 2));  // clusters of both directions
     sparams = o; o += al(2 * sizeof(StepParams));
     // packed operands of the input projection (I <= 256): x planes, W fragments, W column sums
@@ -1189,6 +1202,8 @@ static int forward_recurrence_clustered(FwdPlan *plans, int ndir, int T, int B, 
   for (int k = 1; k < ndir; ++k)
     if (plans[k].npl != npl) return 0;
   if (KS > 4 * kClMaxKPerWave || std::getenv("RXMET_NO_CLUSTER") != nullptr) return 0;
+  // the exchange buffer (2 npl planes of Bpad KS 64 bytes) is addressed with 32-bit offsets
+  if (2.0 * npl * ((B + kTileB - 1) / kTileB * kTileB) * KS * 64 >= 2147483648.0) return 0;
   const bool stage = H >= kStageMinH;
   int device = 0, ncu = 0;
   RXMET_CHECK_HIP(hipGetDevice(&device));
@@ -1204,7 +1219,7 @@ static int forward_recurrence_clustered(FwdPlan *plans, int ndir, int T, int B, 
   for (int UT = 1; UT <= 2 && !chosen; ++UT) {
     if ((H / 16) % UT) continue;
     // the staged h tile takes at most kHsMax chunks per thread
-    if (H >= kStageMinH && npl * H > kHsMax * 256 * UT) continue;
+    if (H >= kStageMinH && npl * KS * 64 > kHsMax * 256 * UT) continue;
     const int G = H / (16 * UT);
     if (static_cast<int64_t>(pairs) * G <= ncu || UT == 2) {
       chosen = UT;

@@ -12,39 +12,6 @@ namespace wgrad {
 
 constexpr int kKC = 32;  // K per chunk: one v_mfma_f32_16x16x32_bf16
 
-typedef float v2f __attribute__((ext_vector_type(2)));
-typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
-
-// The two bf16 halves of a packed word as floats (exact).
-__device__ __forceinline__ v2f unpack_bf16x2(unsigned u) {
-  return v2f{__builtin_bit_cast(float, u << 16), __builtin_bit_cast(float, u & 0xffff0000u)};
-}
-
-__device__ __forceinline__ unsigned pack_bf16x2(v2f a) {
-  return __builtin_bit_cast(unsigned, __builtin_convertvector(a, v2bf));
-}
-
-// a = hi + mid + lo exactly, for two values at once (packed bf16 pairs, first value in the
-// low half): each term is the RNE bf16 of what the previous ones leave (the differences are
-// exact in fp32).  Non-finite inputs give non-finite terms.
-__device__ __forceinline__ void split3x2(v2f a, unsigned &hi, unsigned &mid, unsigned &lo) {
-  hi = pack_bf16x2(a);
-  const v2f r1 = a - unpack_bf16x2(hi);
-  mid = pack_bf16x2(r1);
-  const v2f r2 = r1 - unpack_bf16x2(mid);
-  lo = pack_bf16x2(r2);
-}
-
-// Eight k-consecutive values -> three 16-byte bf16 planes (MFMA operand fragments).
-__device__ __forceinline__ void split3x8(const float (&v)[8], uint4 &hi, uint4 &mid, uint4 &lo) {
-  unsigned h[4], m[4], o[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) split3x2(v2f{v[2 * e], v[2 * e + 1]}, h[e], m[e], o[e]);
-  hi = make_uint4(h[0], h[1], h[2], h[3]);
-  mid = make_uint4(m[0], m[1], m[2], m[3]);
-  lo = make_uint4(o[0], o[1], o[2], o[3]);
-}
-
 // ---------------------------------------------------------------------------------
 // Wave-tile kernels (products whose B side is at most 80 wide).  Each wave computes a
 // 64 x 16 WJ output tile with its operands loaded from global memory straight into MFMA
