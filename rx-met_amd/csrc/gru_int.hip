@@ -327,7 +327,7 @@ struct IClArgs {
   float *hout, *v;              // dequantised h [T+1, B, H] (row 0 written) and v, or null
   int32_t *hq;                  // h codes [T+1, B, H] (row 0 written), or null
   uint8_t *hh_m, *gin_m, *gout_m, *h_m;  // training masks, or null
-  int8_t *hx;                   // [2][NPL][Bpad][H] exchanged h codes
+  int8_t *hx;                   // [2][NPL][Bpad / 16][KS][16][64] exchanged h codes (see ihx_offset)
   unsigned *counters;           // [ncl]
   int *timeout;
   int gate_tab;                 // gate activations by table (every gate grid fits)
@@ -367,10 +367,17 @@ __global__ __launch_bounds__(64) void pack_r_frags_i32(int H, int KS, const int3
 }
 
 // h codes as exchanged bytes: one plane (the centred code) or two (low byte - 128, high byte)
+// Byte offset of (row b, unit j) in one plane of the exchange buffer: 1 KB blocks of 16 rows x
+// 64 units, one per (batch tile, K-step), so that a wave reads an MFMA A fragment as contiguous
+// bytes.
+__device__ __forceinline__ unsigned ihx_offset(int b, int j, int KS) {
+  return ((static_cast<unsigned>(b / kITile) * KS + j / 64) * kITile + b % kITile) * 64 + j % 64;
+}
+
 template <int NPL>
-__device__ __forceinline__ void publish_h(int8_t *hx, size_t plane_stride, int b, int H, int j,
+__device__ __forceinline__ void publish_h(int8_t *hx, unsigned plane_stride, int b, int KS, int j,
                                           int hcv) {
-  unsigned char *dst = reinterpret_cast<unsigned char *>(hx) + static_cast<size_t>(b) * H + j;
+  unsigned char *dst = reinterpret_cast<unsigned char *>(hx) + ihx_offset(b, j, KS);
 #pragma unroll
   for (int q = 0; q < NPL; ++q)
     cluster::store_bytes_coherent(dst + q * plane_stride,
@@ -433,7 +440,9 @@ __global__ __launch_bounds__(512) void int_recurrence_cl(IClArgs a, IntStepParam
     bias[g] = a.bias[c];
     rs[g] = a.rs[c];
   }
-  const size_t plane_stride = static_cast<size_t>(a.Bpad) * H;
+  const unsigned plane_stride = static_cast<unsigned>(a.Bpad) * KS * 64;
+  // the exchange buffer, 2 NPL planes (32-bit byte offsets: checked by the launcher)
+  const auto xr = cluster::buffer_rsrc(a.hx, 2u * NPL * plane_stride);
   const size_t NH = static_cast<size_t>(B) * H;
   v4i *myred = red + (static_cast<size_t>(utl) * 4 + kq) * 3 * NPL * 64;
   unsigned epoch = 0;
@@ -443,7 +452,7 @@ __global__ __launch_bounds__(512) void int_recurrence_cl(IClArgs a, IntStepParam
     const int b0 = tile * kITile, b = b0 + nr;
     const bool valid = b < B;
     int32_t hold = valid ? a.h0q[static_cast<size_t>(b) * H + j] : p.zp_h;
-    publish_h<NPL>(a.hx, plane_stride, b, H, j, hold - a.h_offset);
+    publish_h<NPL>(a.hx, plane_stride, b, KS, j, hold - a.h_offset);
     int32_t wn_[3];
     auto load_wx = [&](int t) {
 #pragma unroll
@@ -454,8 +463,8 @@ __global__ __launch_bounds__(512) void int_recurrence_cl(IClArgs a, IntStepParam
     alive = cluster::sync(counter, ++epoch * a.G, a.timeout);
     for (int t = 0; t < a.T && alive; ++t) {
       const int par = t & 1;
-      const int8_t *hin = a.hx + static_cast<size_t>(par) * NPL * plane_stride;
-      int8_t *hnext = a.hx + static_cast<size_t>(par ^ 1) * NPL * plane_stride;
+      const unsigned hin = par * NPL * plane_stride;  // byte offset of the step's planes
+      int8_t *hnext = a.hx + (par ^ 1) * NPL * plane_stride;
       const int32_t wz = wn_[0], wr = wn_[1], wn = wn_[2];
       v4i acc[3][NPL];
 #pragma unroll
@@ -463,14 +472,15 @@ __global__ __launch_bounds__(512) void int_recurrence_cl(IClArgs a, IntStepParam
 #pragma unroll
         for (int q = 0; q < NPL; ++q) acc[g][q] = v4i{0, 0, 0, 0};
       {
-        const int8_t *hrow = hin + static_cast<size_t>(b0 + l % 16) * H + 16 * (l / 16);
+        // lane l: row l % 16, units 16 (l / 16) .. + 15 of K-step kq + 4 i
+        const unsigned hrow = hin + static_cast<unsigned>(tile) * KS * 1024 + 64 * (l % 16) + 16 * (l / 16);
         v4i hfr[kIMaxKPerWave][NPL];
 #pragma unroll
         for (int i = 0; i < kIMaxKPerWave; ++i)
 #pragma unroll
           for (int q = 0; q < NPL; ++q)
             if (kq + 4 * i < KS) {
-              const int4 v = cluster::load_coherent16(hrow + q * plane_stride + 64 * (kq + 4 * i));
+              const int4 v = cluster::load_coherent16(xr, hrow + q * plane_stride + 1024 * (kq + 4 * i));
               hfr[i][q] = v4i{v.x, v.y, v.z, v.w};
             }
 #pragma unroll
@@ -531,7 +541,7 @@ __global__ __launch_bounds__(512) void int_recurrence_cl(IClArgs a, IntStepParam
       const long long newc = (static_cast<long long>(p.quant_one) - z) * (static_cast<long long>(n_h) - p.zp_h);
       const int32_t hnew = clampi(add32(static_cast<int32_t>(rescale(oldc + newc, p.old_h)), p.zp_h), p.h, k_h);
       hold = hnew;
-      publish_h<NPL>(hnext, plane_stride, b, H, j, hnew - a.h_offset);
+      publish_h<NPL>(hnext, plane_stride, b, KS, j, hnew - a.h_offset);
       // the other members only read the h codes: arrive now, store the outputs while waiting
       cluster::arrive(counter);
       ++epoch;
@@ -605,7 +615,7 @@ struct IntWorkspace {
     const size_t Bpad = (static_cast<size_t>(B) + kITile - 1) / kITile * kITile;
     rfrag = o; o += al(sizeof(v4i) * 64 * (static_cast<size_t>(H) / 16) * 3 * KS);
     rcol = o; o += al(sizeof(int32_t) * C);
-    hx = o; o += al(2 * 2 * Bpad * H);
+    hx = o; o += al(2 * 2 * Bpad * KS * 64);
     sync = o; o += al(sizeof(unsigned) * (Bpad / kITile + 2));
     total = o;
   }
@@ -674,6 +684,8 @@ static int int_recurrence_clustered(const IntCall &k, const IntStepParams &sp,
     return 0;
   const rxmet_grid &gh = k.params->g[RXMET_GRU_H];
   const int npl = gh.bits <= 8 ? 1 : 2;
+  // the exchange buffer (2 npl planes of Bpad KS 64 bytes) is addressed with 32-bit offsets
+  if (2.0 * npl * ((B + kITile - 1) / kITile * kITile) * ((H + 63) / 64 * 64) >= 2147483648.0) return 0;
   const void *fn = npl == 1 ? reinterpret_cast<const void *>(&int_recurrence_cl<1>)
                             : reinterpret_cast<const void *>(&int_recurrence_cl<2>);
   int device = 0, ncu = 0;

@@ -702,7 +702,9 @@ __global__ __launch_bounds__(512) void lstm_recurrence_cl(RecArgs a, StepParams 
   unsigned epoch = 0;
   bool alive = true;
   const bool train = a.hidden != nullptr;
-  const size_t plane_stride = static_cast<size_t>(cl.Bpad) * H;
+  const unsigned plane_stride = static_cast<unsigned>(cl.Bpad) * H;
+  // the exchange buffer, 2 NPL planes (32-bit byte offsets: checked by the launcher)
+  const auto xr = cluster::buffer_rsrc(cl.hx, 2u * NPL * plane_stride);
 
   for (int tile = pl.cluster; tile < cl.ntiles && alive; tile += cl.ncl) {
     const int b0 = tile * 16;
@@ -736,14 +738,13 @@ __global__ __launch_bounds__(512) void lstm_recurrence_cl(RecArgs a, StepParams 
 
     for (int t = 0; t < a.T && alive; ++t) {
       const int par = t & 1;
-      const int8_t *hin = cl.hx + static_cast<size_t>(par) * NPL * plane_stride;
+      const unsigned hin_off = par * NPL * plane_stride;  // byte offset of the step's planes
       int8_t *hout = cl.hx + static_cast<size_t>(par ^ 1) * NPL * plane_stride;
       v4i acc[2][NPL];
 #pragma unroll
       for (int q = 0; q < 2; ++q)
 #pragma unroll
         for (int p = 0; p < NPL; ++p) acc[q][p] = v4i{0, 0, 0, 0};
-      const int8_t *hrow = hin + static_cast<size_t>(b0 + l % 16) * H + 16 * (l / 16);
       if (NPL == 1 && kBT * (H + 16) <= static_cast<int>(sizeof(float)) * 4 * 4 * 16 * 16) {
         // The tile's h codes are read from the exchange buffer once per workgroup (one 16-byte
         // coherent load per thread and plane-chunk) into the gate exchange area, which is free
@@ -755,7 +756,7 @@ __global__ __launch_bounds__(512) void lstm_recurrence_cl(RecArgs a, StepParams 
         for (int i = 0; i < 2; ++i) {
           const int e0 = tid + 512 * i, e = e0 < n ? e0 : 0;
           const int p = e / (kBT * cpr), r = (e / cpr) % kBT, c = e % cpr;
-          hv[i] = cluster::load_coherent16(hin + p * plane_stride + static_cast<size_t>(b0 + r) * H + 16 * c);
+          hv[i] = cluster::load_coherent16(xr, hin_off + p * plane_stride + (b0 + r) * H + 16 * c);
         }
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
@@ -789,7 +790,8 @@ __global__ __launch_bounds__(512) void lstm_recurrence_cl(RecArgs a, StepParams 
 #pragma unroll
           for (int p = 0; p < NPL; ++p)
             if (s < KS) {
-              const int4 v = cluster::load_coherent16(hrow + p * plane_stride + 64 * s);
+              const int4 v = cluster::load_coherent16(
+                  xr, hin_off + (b0 + l % 16) * H + 16 * (l / 16) + p * plane_stride + 64 * s);
               hfr[s][p] = v4i{v.x, v.y, v.z, v.w};
             }
 #pragma unroll
@@ -1266,7 +1268,8 @@ int rxmet_lstm_forward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const f
     int ncl = per_cu * ncu / cl.G;
     if (ncl > cl.ntiles) ncl = cl.ntiles;
     if (ncl >= 8) ncl -= ncl % 8;
-    if (ncl >= 1 && std::getenv("RXMET_NO_CLUSTER") == nullptr) {
+    // (the exchange buffer, 2 npl planes of Bpad H bytes, is addressed with 32-bit offsets)
+    if (ncl >= 1 && 4.0 * cl.Bpad * H < 2147483648.0 && std::getenv("RXMET_NO_CLUSTER") == nullptr) {
       cl.ncl = ncl;
       cl.hx = reinterpret_cast<int8_t *>(wsb + ws.hx);
       cl.counters = reinterpret_cast<unsigned *>(wsb + ws.sync);
