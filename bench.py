@@ -219,10 +219,12 @@ def _qdq_leg(torch, steps: int, warmup: int, validate: bool = True):
 
 
 # Algorithmic work per launch of the instrumented GRU kernels (one direction, c3 shapes):
-# GEMM FLOPs 2*M*N*K as counted for the metric; the int8 MFMA / fp32 peaks are MI355X's
-# published dense figures in TFLOP/s (int8: TOP/s).
+# GEMM FLOPs 2*M*N*K as counted for the metric, priced against the MI355X published dense peak
+# of the MFMA type that executes them, in TFLOP/s (int8: TOP/s).  Float products computed as
+# three exact bf16 terms against exact bf16 code planes run on bf16 MFMA: three bf16 products
+# per algorithmic product, so their fraction of the bf16 peak is at most 1/3.
 INT8_MFMA_PEAK = 5000.0
-FP32_MFMA_PEAK = 157.3
+BF16_MFMA_PEAK = 2500.0
 
 
 def _gru_kernel_work(B, T, I, H, D=2):
@@ -234,13 +236,14 @@ def _gru_kernel_work(B, T, I, H, D=2):
         "gru_fwd_recurrence": (D * 2.0 * M * H * C, INT8_MFMA_PEAK,
                                "recurrent GEMM R_q.h_q over T steps, both directions in one "
                                "clustered launch (int8 MFMA, 16-bit h as two byte planes)"),
-        "gru_bwd_recurrence": (D * 2.0 * M * H * C, FP32_MFMA_PEAK,
+        "gru_bwd_recurrence": (D * 2.0 * M * H * C, BF16_MFMA_PEAK,
                                "dh GEMM R_deq.dq over T steps, both directions in one clustered "
-                               "launch (fp32 MFMA)"),
-        "gru_bwd_weight_gemms": (D * 2.0 * M * C * (2 * I + H), FP32_MFMA_PEAK,
+                               "launch (bf16 MFMA: dq split into three bf16 terms against the "
+                               "R codes)"),
+        "gru_bwd_weight_gemms": (D * 2.0 * M * C * (2 * I + H), BF16_MFMA_PEAK,
                                  "dx, dW, dR GEMMs (float gradient split into three bf16 "
                                  "terms against exact bf16 code planes, MFMA)"),
-        "gru_fwd_input_gemm": (D * 2.0 * M * C * I, FP32_MFMA_PEAK,
+        "gru_fwd_input_gemm": (D * 2.0 * M * C * I, INT8_MFMA_PEAK,
                                "input projection W_q.x_q exact integer GEMM"),
     }
 
@@ -526,10 +529,10 @@ def _lstm_kernel_work(B, T, I, H):
         "lstm_bwd_recurrence": (2.0 * M * H * C, INT8_MFMA_PEAK,
                                 "dh GEMM W_hh_q^T.dgates over T steps (int8 MFMA, 3 planes of "
                                 "22-bit block fixed point) with the fused STE pointwise"),
-        "lstm_bwd_weight_gemms": (2.0 * M * C * (2 * I + H), FP32_MFMA_PEAK,
+        "lstm_bwd_weight_gemms": (2.0 * M * C * (2 * I + H), BF16_MFMA_PEAK,
                                   "dx, dW_ih, dW_hh GEMMs (float gradient split into three "
                                   "bf16 terms against exact bf16 code planes, MFMA)"),
-        "lstm_fwd_input_gemm": (2.0 * M * C * I, FP32_MFMA_PEAK,
+        "lstm_fwd_input_gemm": (2.0 * M * C * I, INT8_MFMA_PEAK,
                                 "input linear W_ih_q.x_q exact integer GEMM"),
     }
 

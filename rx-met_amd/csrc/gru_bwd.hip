@@ -13,7 +13,8 @@
 //   2. recurrence  : both directions walk t = T-1..0 in one clustered launch
 //                    (bwd_recurrence_cl: a batch tile's hidden units split over a cluster of
 //                    workgroups, dq * scale_R exchanged through global memory each step and
-//                    dh += R_deq dq summed on fp32 MFMA with the R values resident in VGPRs);
+//                    dh += R_deq dq summed on bf16 MFMA, dq split exactly into three bf16
+//                    terms against the R codes resident in VGPRs);
 //                    the per-tile fallback (bwd_recurrence) keeps one workgroup per 16
 //                    sequences, each lane owning one hidden unit for four sequences, with
 //                    dh += R_deq dq on int8 MFMA over 22-bit block-fixed-point dq (three int8

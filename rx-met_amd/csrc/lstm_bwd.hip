@@ -18,7 +18,8 @@
 //                  row maximum) in three int8 planes; after the cluster barrier,
 //                  dh = W_hh_deq^T dgates_hh on int8 MFMA against the resident W_hh codes,
 //                  recombined exactly in double; the gate gradients for the GEMMs go out as
-//                  16-byte rows staged in LDS while the members wait;
+//                  16-byte rows staged in LDS while the members wait, and the next step's
+//                  checkpoints are copied into LDS meanwhile;
 //   3. GEMMs     : dx, dW_ih | db_ih and dW_hh | db_hh on bf16 MFMA with the gradients split
 //                  exactly into three bf16 terms (wgrad_gemm.h), the bias columns from fused
 //                  column sums; one pass applies the master masks.

@@ -258,7 +258,7 @@ def test_backward_matches_oracle(cuda, shape, cfg_name, with_h0):
                                             ((4, 40, 8, 96), "16b-act-pot2"), ((3, 20, 5, 16), "8b-sym")])
 def test_clustered_backward_matches_oracle_and_single_tile_path(cuda, shape, cfg_name,
                                                                 monkeypatch):
-    """The clustered backward (fp32 MFMA dh, dq exchanged between the workgroups of a batch
+    """The clustered backward (split-bf16 MFMA dh, dq exchanged between the workgroups of a batch
     tile) against the oracle, and against the one-workgroup-per-tile path within 1e-4."""
     T, B, I, H = shape
     print(f"[gru bwd cluster] shape={shape} cfg={cfg_name}", flush=True)
