@@ -10,7 +10,7 @@
 //   1. prologue  : x and h_prev codes and the W_ih codes as bf16 operand planes for the
 //                  weight-gradient GEMMs; W_hh codes packed as int8 MFMA fragments of the
 //                  transposed product, with their column sums;
-//   2. recurrence: both K-halves of a batch tile's dh product over a cluster of workgroups
+//   2. recurrence: a batch tile's dh product over a cluster of workgroups
 //                  (lstm_bwd_recurrence_cl; the per-tile fallback lstm_bwd_recurrence keeps
 //                  one workgroup per 16 sequences).  Per step: the pointwise backward with
 //                  every mask family in the reference's operation order; dgates_hh * scale_W
