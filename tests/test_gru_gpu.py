@@ -330,7 +330,8 @@ def test_two_direction_entry_points_equal_single_calls(cuda, shape):
             np.testing.assert_allclose(a, b, rtol=1e-5, atol=1e-6 * scale, err_msg=f"{d} {name}")
 
 
-@pytest.mark.parametrize("shape", [(3, 20, 24, 1024), (4, 35, 16, 512), (2, 18, 8, 272)])
+@pytest.mark.parametrize("shape", [(3, 20, 24, 1024), (4, 35, 16, 512), (2, 18, 8, 272),
+                                   (2, 18, 8, 544)])
 def test_large_hidden_forward_backward_match_oracle(cuda, shape):
     """H above 256 (the c5 hidden size 1024 with its quantisation): the clustered forward
     (K split over four waves, several batch tiles per cluster) bit for bit, and the stepped

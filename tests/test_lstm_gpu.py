@@ -391,12 +391,14 @@ def test_clustered_recurrence_matches_oracle_and_single_tile_path(cuda, shape, c
 
 @pytest.mark.parametrize("shape,cfg_name", [((3, 2560, 16, 128), "c4"), ((2, 100, 24, 256), "c4"),
                                             ((3, 40, 8, 128), "16b-act"),
-                                            ((3, 20, 64, 512), "pot2-gate")])
+                                            ((3, 20, 64, 512), "pot2-gate"),
+                                            ((3, 40, 8, 384), "c4")])
 def test_clustered_backward_matches_oracle_and_single_tile_path(cuda, shape, cfg_name,
                                                                 monkeypatch):
     """H a multiple of 128 takes the clustered backward (members exchange block-fixed-point
     gate gradients, one exponent per sequence and member); it must match the oracle within
-    1e-4 and the one-workgroup-per-tile backward."""
+    1e-4 and the one-workgroup-per-tile backward.  H = 384 (six members, three K-steps per
+    wave) has waves whose K-steps span two members, each with its own exponent."""
     T, B, I, H = shape
     args, _, p = _case(T, B, I, H, cfg_name, 43, True, True)
     Wi, Wh, bi, bh, x, h0, c0 = args
