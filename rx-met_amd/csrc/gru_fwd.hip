@@ -125,8 +125,8 @@ __global__ __launch_bounds__(64) void quant_weights(int I, int H, WeightArgs a) 
 
 // The same with the rows of each column split over kQsGroups threads, for grids where every
 // partial sum of codes stays below 2^24: the float sums are then exact, so the split order gives
-// the sequential sums bit for bit.  32 columns x 8 row groups per 256-thread block.
-constexpr int kQsCols = 32, kQsGroups = 8;
+// the sequential sums bit for bit.  8 columns x 32 row groups per 256-thread block.
+constexpr int kQsCols = 8, kQsGroups = 32;
 __global__ __launch_bounds__(256) void quant_weights_split(int I, int H, WeightArgs a) {
   __shared__ float red[2][kQsGroups][kQsCols];
   __shared__ int redi[kQsGroups][kQsCols];
@@ -142,7 +142,7 @@ __global__ __launch_bounds__(256) void quant_weights_split(int I, int H, WeightA
   if (on) {
     const float ew = a.eff[c], er = a.eff[C + c];
     // rows in batches of kQsBatch whose loads are all issued before any code is stored
-    constexpr int kQsBatch = 16;
+    constexpr int kQsBatch = 8;
     for (int k0 = rg; k0 < I; k0 += kQsGroups * kQsBatch) {
       float v[kQsBatch];
 #pragma unroll
