@@ -20,18 +20,22 @@ namespace rxmet {
 namespace gru {
 
 // One thread per 4 consecutive values of a row of 2H; h_f, h_r: [T+1, B, H] (row 0 = h0).
+// Ix: the type of the element index and of its divisions (32-bit whenever the count fits: a
+// 64-bit division is a long software sequence on the GPU).
+template <typename Ix>
 __global__ __launch_bounds__(256) void bidir_assemble(int T, int B, int H, const float *__restrict__ h_f,
                                                       const float *__restrict__ h_r,
                                                       float *__restrict__ out, int64_t st, int64_t sb,
                                                       float *__restrict__ h_n) {
-  const int q4 = H / 2;  // float4 per output row
-  const int64_t n = static_cast<int64_t>(T) * B * q4;
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  const Ix q4 = H / 2;  // float4 per output row
+  const Ix n = static_cast<Ix>(T) * B * q4;
+  const Ix stride = static_cast<Ix>(gridDim.x) * blockDim.x;
   const size_t BH = static_cast<size_t>(B) * H;
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
-    const int q = static_cast<int>(i % q4);
-    const int64_t row = i / q4;
-    const int b = static_cast<int>(row % B), t = static_cast<int>(row / B);
+  for (Ix i = static_cast<Ix>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const Ix row = i / q4;
+    const int q = static_cast<int>(i - row * q4);
+    const Ix tq = row / static_cast<Ix>(B);
+    const int b = static_cast<int>(row - tq * B), t = static_cast<int>(tq);
     const int k = 4 * q;
     const float4 v = k < H
         ? *reinterpret_cast<const float4 *>(h_f + (t + 1) * BH + static_cast<size_t>(b) * H + k)
@@ -52,22 +56,24 @@ __global__ __launch_bounds__(256) void bidir_assemble(int T, int B, int H, const
 // g[T-1-s][b][H + j] (+ g_hn[1][b][j] at s = T-1); row 0 of both is zero.  g element (t, b, k)
 // at g[t gt + b gb + k gk] (strides may be zero); g or g_hn may be absent (zero).  One thread
 // per four consecutive units, written as one 16-byte store (H is a multiple of 4).
+template <typename Ix>
 __global__ __launch_bounds__(256) void bidir_split_grad(int T, int B, int H, const float *__restrict__ g,
                                                         int64_t gt, int64_t gb, int64_t gk,
                                                         const float *__restrict__ g_hn,
                                                         float *__restrict__ dh_f,
                                                         float *__restrict__ dh_r) {
-  const int h4 = H / 4;
-  const int64_t rows = static_cast<int64_t>(T + 1) * B;  // rows of one direction
-  const int64_t n = 2 * rows * h4;
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  const Ix h4 = H / 4;
+  const Ix rows = static_cast<Ix>(T + 1) * B;  // rows of one direction
+  const Ix n = 2 * rows * h4;
+  const Ix stride = static_cast<Ix>(gridDim.x) * blockDim.x;
   const size_t BH = static_cast<size_t>(B) * H;
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
-    const int64_t row2 = i / h4;
+  for (Ix i = static_cast<Ix>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const Ix row2 = i / h4;
     const int j = 4 * static_cast<int>(i - row2 * h4);
     const int dir = row2 >= rows ? 1 : 0;
-    const int64_t row = row2 - dir * rows;
-    const int s1 = static_cast<int>(row / B), b = static_cast<int>(row - static_cast<int64_t>(s1) * B);
+    const Ix row = row2 - dir * rows;
+    const Ix sq = row / static_cast<Ix>(B);
+    const int s1 = static_cast<int>(sq), b = static_cast<int>(row - sq * B);
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
     if (s1 > 0) {
       const int t = dir == 0 ? s1 - 1 : T - s1;
@@ -83,24 +89,29 @@ __global__ __launch_bounds__(256) void bidir_split_grad(int T, int B, int H, con
         v.w += h[3];
       }
     }
-    *reinterpret_cast<float4 *>((dir == 0 ? dh_f : dh_r) + row * H + j) = v;
+    *reinterpret_cast<float4 *>((dir == 0 ? dh_f : dh_r) + static_cast<size_t>(row) * H + j) = v;
   }
 }
 
 // dx[t st + b sb + i] = dx_f[t][b][i] + dx_r[T-1-t][b][i].
+template <typename Ix>
 __global__ __launch_bounds__(256) void bidir_dx(int T, int B, int I, const float *__restrict__ dx_f,
                                                 const float *__restrict__ dx_r, float *__restrict__ dx,
                                                 int64_t st, int64_t sb) {
-  const int64_t n = static_cast<int64_t>(T) * B * I;
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-  const int64_t BI = static_cast<int64_t>(B) * I;
-  for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < n; e += stride) {
-    const int t = static_cast<int>(e / BI);
-    const int64_t rem = e - t * BI;
-    const int b = static_cast<int>(rem / I), i = static_cast<int>(rem % I);
-    dx[t * st + b * sb + i] = dx_f[e] + dx_r[(T - 1 - t) * BI + rem];
+  const Ix n = static_cast<Ix>(T) * B * I;
+  const Ix stride = static_cast<Ix>(gridDim.x) * blockDim.x;
+  const Ix BI = static_cast<Ix>(B) * I;
+  for (Ix e = static_cast<Ix>(blockIdx.x) * blockDim.x + threadIdx.x; e < n; e += stride) {
+    const Ix tq = e / BI;
+    const Ix rem = e - tq * BI;
+    const Ix bq = rem / static_cast<Ix>(I);
+    const int t = static_cast<int>(tq), b = static_cast<int>(bq), i = static_cast<int>(rem - bq * I);
+    dx[t * st + b * sb + i] = dx_f[e] + dx_r[static_cast<size_t>(T - 1 - t) * BI + rem];
   }
 }
+
+// Element counts (plus one grid stride) that 32-bit index arithmetic covers.
+static bool fits32(int64_t n) { return n + 8192LL * 256 < (1LL << 32); }
 
 static unsigned grid_for(int64_t n) {
   int64_t blocks = (n + 255) / 256;
@@ -126,7 +137,8 @@ int rxmet_gru_bidir_assemble(int32_t T, int32_t B, int32_t H, const float *h_f, 
                       (reinterpret_cast<uintptr_t>(h_n) & 15u) == 0,
                   "outputs and strides must allow 16-byte rows");
   const int64_t n = static_cast<int64_t>(T) * B * (H / 2);
-  hipLaunchKernelGGL(bidir_assemble, dim3(grid_for(n)), dim3(256), 0, static_cast<hipStream_t>(stream),
+  hipLaunchKernelGGL((fits32(n) ? bidir_assemble<uint32_t> : bidir_assemble<int64_t>), dim3(grid_for(n)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream),
                      T, B, H, h_f, h_r, out, out_st, out_sb, h_n);
   RXMET_CHECK_LAUNCH();
   return 0;
@@ -142,7 +154,8 @@ int rxmet_gru_bidir_split_grad(int32_t T, int32_t B, int32_t H, const float *g, 
                       (reinterpret_cast<uintptr_t>(dh_r) & 15u) == 0,
                   "dh_new buffers must be 16-byte aligned");
   const int64_t n = 2 * static_cast<int64_t>(T + 1) * B * (H / 4);
-  hipLaunchKernelGGL(bidir_split_grad, dim3(grid_for(n)), dim3(256), 0, static_cast<hipStream_t>(stream),
+  hipLaunchKernelGGL((fits32(n) ? bidir_split_grad<uint32_t> : bidir_split_grad<int64_t>), dim3(grid_for(n)), dim3(256),
+                     0, static_cast<hipStream_t>(stream),
                      T, B, H, g, g_st, g_sb, g_sk, g_hn, dh_f, dh_r);
   RXMET_CHECK_LAUNCH();
   return 0;
@@ -154,7 +167,8 @@ int rxmet_gru_bidir_dx(int32_t T, int32_t B, int32_t I, const float *dx_f, const
   RXMET_CHECK_ARG(T >= 1 && B >= 1 && I >= 1, "bad dimensions");
   RXMET_CHECK_ARG(dx_f && dx_r && dx, "required pointer is null");
   const int64_t n = static_cast<int64_t>(T) * B * I;
-  hipLaunchKernelGGL(bidir_dx, dim3(grid_for(n)), dim3(256), 0, static_cast<hipStream_t>(stream), T, B,
+  hipLaunchKernelGGL((fits32(n) ? bidir_dx<uint32_t> : bidir_dx<int64_t>), dim3(grid_for(n)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), T, B,
                      I, dx_f, dx_r, dx, dx_st, dx_sb);
   RXMET_CHECK_LAUNCH();
   return 0;
