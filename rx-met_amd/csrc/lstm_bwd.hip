@@ -592,7 +592,12 @@ __global__ __launch_bounds__(512) void lstm_bwd_recurrence_cl(BwdArgs a, BwdClAr
           mx = (as > mx || as != as) ? as : mx;
         }
         if (!(mx <= 3.0e38f)) mx = INFINITY;
-        atomicMax(&rowmax[nrow0 + 2 * kh + rr], __float_as_uint(mx));
+        // the 16 lanes of a row first (the bits of non-negative floats order as the values),
+        // then one LDS atomic per wave and row
+        unsigned u = __float_as_uint(mx);
+#pragma unroll
+        for (int o = 8; o >= 1; o >>= 1) u = max(u, static_cast<unsigned>(__shfl_xor(static_cast<int>(u), o, 64)));
+        if (l % 16 == 0) atomicMax(&rowmax[nrow0 + 2 * kh + rr], u);
       }
       __syncthreads();
       if (tid < kBB) {
