@@ -810,7 +810,7 @@ __global__ __launch_bounds__(512) void lstm_recurrence_cl(RecArgs a, StepParams 
       // per-gate parameters are static kernel-argument reads
       auto gate_phase = [&](auto gpc) {
         constexpr int GP = decltype(gpc)::value;
-#pragma unroll 1
+#pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int nr = nrow0 + r, b = b0 + nr;
           const bool valid = b < B;
