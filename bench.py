@@ -662,7 +662,7 @@ def _validate_lstm(torch, m, x, g, rows):
     Wi, Wh, bi, bh = (p.detach().cpu().numpy() for p in m._direction_params(False))
     prm = m._params[0].struct
     xs = x[:, rows].detach().contiguous().cpu().numpy()
-    o = LO.forward_quant(Wi, Wh, bi, bh, xs, prm, mode=LO.ACT_CR)
+    o = LO.forward_quant(Wi, Wh, bi, bh, xs, prm, mode=LO.ACT_LIBM_EXACT)
     _check_equal("lstm output", out[:, rows].detach().cpu().numpy(), o["output"])
     gr = LO.backward_quant(o, prm, g[:, rows].detach().contiguous().cpu().numpy())
     err = _check_close("lstm dx", xl.grad[:, rows].cpu().numpy(), gr["dx"])

@@ -124,6 +124,25 @@ int rxmet_lstm_derive_exec(const rxmet_lstm_params *params, int32_t input_size,
                            rxmet_lstm_q31 *cell /* [2]: forget, input */,
                            rxmet_lstm_rescale *hidden_rescale /* [1] */);
 
+/* Host-side activation tables, for tests (no counterpart in the reference's binding: they
+ * expose what rxmet_lstm_forward_quant applies).  The reference's CPU core evaluates its real
+ * activations with the C library's expf / tanhf (realSigmoid / realTanh /
+ * realActivationQuantizedCore, operators/quant-lstm/src/lstm/cuda/quantized_fp_math.cuh:21-63);
+ * the kernels evaluate exp / tanh in double and take the reference's result at the input codes
+ * where the two give different output codes.
+ * rxmet_lstm_activation_table: entries (output code - output lo) << 1 | clamp mask of
+ * activation k (0..3: gates i, f, g, o; 4: tanh of the cell) for every code lo..hi of its
+ * input grid (at most 65536 codes), the reference's arithmetic (reference != 0) or the
+ * kernels' double evaluation; returns the number of codes or a negative error.
+ * rxmet_lstm_activation_exceptions: the exception lists of all five activations (sorted input
+ * codes and the reference's entries, copied up to capacity; off/n [5] per activation; grids
+ * wider than 65536 codes are not listed); returns the total count or a negative error. */
+int32_t rxmet_lstm_activation_table(const rxmet_lstm_params *params, int32_t k, int32_t reference,
+                                    uint32_t *entries, int32_t capacity);
+int32_t rxmet_lstm_activation_exceptions(const rxmet_lstm_params *params, int32_t *keys,
+                                         uint32_t *entries, int32_t capacity,
+                                         int32_t *off /* [5] */, int32_t *n /* [5] */);
+
 /* Tensors kept by a training forward for the STE backward (device pointers).
  * Masters: quantised x, W_ih, W_hh, b_ih, b_hh, h0, c0 (h0/c0 quantised from zeros when
  * absent); checkpoints: gate outputs [T,B,4H], cell states, tanh(cell), hidden [T,B,H]

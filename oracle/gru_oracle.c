@@ -39,6 +39,16 @@
 
 #include "../include/rxmet_gru.h"
 
+/* Summation of the two GEMMs of codes in the FP32-carrier forward.  ORACLE_SUM_EXACT (the
+ * default, what the HIP kernels compute): exact int64 sums rounded once to fp32.
+ * ORACLE_SUM_SEQ_F32: fp32 products added in K order, a model of the reference's cuBLAS
+ * SGEMM (ComputeLinearX / ComputeLinearH, gru_forward_gpu_quant_fp.cu:1111-1155), whose own
+ * summation order is not reproducible here.  The two agree while every partial sum stays
+ * below 2^24; the mode exists to measure how far they drift apart beyond that. */
+enum { ORACLE_SUM_EXACT = 0, ORACLE_SUM_SEQ_F32 = 1 };
+static int g_sum_mode = ORACLE_SUM_EXACT;
+void oracle_gru_set_sum_mode(int mode) { g_sum_mode = mode; }
+
 /* ------------------------------------------------------------------------------ */
 /* Grids                                                                           */
 /* ------------------------------------------------------------------------------ */
@@ -624,11 +634,20 @@ int oracle_gru_forward_quant(int is_training, int T, int B, int I, int H, const 
         const size_t mi = ((size_t)t * B + b) * C + j;  /* mask index of gate 0 */
         for (int gt = 0; gt < 3; ++gt) {
           const int c = gt * H + j;
-          int64_t si = 0, sh = 0;
-          for (int r = 0; r < I; ++r) si += (int64_t)xp[r] * (int64_t)W_q[(size_t)r * C + c];
-          for (int r = 0; r < H; ++r) sh += (int64_t)hp[r] * (int64_t)R_q[(size_t)r * C + c];
-          gih[gt] = (float)si;
-          ghh[gt] = (float)sh;
+          if (g_sum_mode == ORACLE_SUM_SEQ_F32) {
+            /* a plain SGEMM model: products rounded to fp32, added in K order */
+            float fi = 0.0f, fh = 0.0f;
+            for (int r = 0; r < I; ++r) fi += xp[r] * W_q[(size_t)r * C + c];
+            for (int r = 0; r < H; ++r) fh += hp[r] * R_q[(size_t)r * C + c];
+            gih[gt] = fi;
+            ghh[gt] = fh;
+          } else {
+            int64_t si = 0, sh = 0;
+            for (int r = 0; r < I; ++r) si += (int64_t)xp[r] * (int64_t)W_q[(size_t)r * C + c];
+            for (int r = 0; r < H; ++r) sh += (int64_t)hp[r] * (int64_t)R_q[(size_t)r * C + c];
+            gih[gt] = (float)si;
+            ghh[gt] = (float)sh;
+          }
           /* biasRescaleInline */
           float val = gih[gt] - wsum[c];
           float bt = rintf(bw_q[c] * ibx[c]);

@@ -42,6 +42,16 @@ _o.oracle_gru_backward_quant.argtypes = [_i] * 4 + [_P] * 8 + [ctypes.POINTER(A.
 _o.oracle_gru_forward_int.argtypes = [_i] * 5 + [_P] * 8 + [ctypes.POINTER(A.GruQParams)] + \
     [_P] * 7 + [_P] * 11
 
+_o.oracle_gru_set_sum_mode.argtypes = [_i]
+SUM_EXACT, SUM_SEQ_F32 = 0, 1
+
+
+def set_sum_mode(mode: int) -> None:
+    """GEMM-sum model of the FP32-carrier forward: SUM_EXACT (the kernels' exact integer
+    sums, the default) or SUM_SEQ_F32 (fp32 products added in K order, an SGEMM model)."""
+    _o.oracle_gru_set_sum_mode(int(mode))
+
+
 _REF_PATH = HERE / "_ref" / "libgru_ref.so"
 _ref = ctypes.CDLL(str(_REF_PATH)) if _REF_PATH.exists() else None
 if _ref is not None:

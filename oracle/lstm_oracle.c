@@ -23,15 +23,16 @@
  *     src/lstm/backward_float_cuda.cu:50-104 pointwise with masks, :286-327 GEMMs and
  *     masks) with GEMM sums accumulated in double.
  *
- * Activation modes: ACT_LIBM evaluates sigmoid/tanh with the C library's expf/tanhf in
- * the reference's float op order (the reference CPU semantics, pinned against the
- * reference compiled into oracle/_ref); ACT_CR evaluates exp and tanh in double and rounds
- * once to float (correctly rounded apart from double-rounding ties), keeping the same float
- * op order around them, and sums each linear's centred integer products exactly (one
- * rounding to float at the end) instead of accumulating them in float in index order.  The
- * two sums agree while every partial sum stays below 2^24 (all 8-bit h configurations); past
- * that the reference's own result depends on its GEMM's summation order.  The GPU kernels
- * implement ACT_CR.
+ * Modes: ACT_LIBM evaluates sigmoid/tanh with the C library's expf/tanhf in the
+ * reference's float op order and accumulates each linear's centred integer products in
+ * float in index order (the reference CPU semantics, pinned against the reference compiled
+ * into oracle/_ref); ACT_CR evaluates exp and tanh in double and rounds once to float
+ * (correctly rounded apart from double-rounding ties), keeping the same float op order
+ * around them, and sums each linear's products exactly (one rounding to float at the end);
+ * ACT_LIBM_EXACT takes ACT_LIBM's activations with ACT_CR's exact sums, which is what the GPU
+ * kernels compute.  The two sums agree while every partial sum stays below 2^24 (all 8-bit h
+ * configurations); past that the reference's own result depends on its GEMM's summation
+ * order.
  *
  * Pinning (tests/test_lstm_oracle.py): the reference's golden vectors
  * (the JSON files in tests/golden/lstm, copied data from the reference tests/golden/spec) for
@@ -47,7 +48,7 @@
 
 #include "../include/rxmet_lstm.h"
 
-enum { ACT_LIBM = 0, ACT_CR = 1 };
+enum { ACT_LIBM = 0, ACT_CR = 1, ACT_LIBM_EXACT = 2 };
 
 /* ------------------------------------------------------------------------------ */
 /* Grids and rounding                                                              */
@@ -83,9 +84,10 @@ static float center(float v, int32_t zp) { return (float)((double)v - zp); }
 
 /* Sum of w[k] * (x[k] - zx) over k: in float in index order, as linearValue
  * (forward_quantized_fp_cpu.cc:20-45) does, for ACT_LIBM; exactly in 64-bit integers and
- * rounded once to float for ACT_CR (the codes are integers, so every product is exact). */
+ * rounded once to float for ACT_CR and ACT_LIBM_EXACT (the codes are integers, so every
+ * product is exact). */
 static float linear_sum(const float *w, const float *x, int32_t zx, int K, int mode) {
-  if (mode == ACT_CR) {
+  if (mode != ACT_LIBM) {
     int64_t s = 0;
     for (int k = 0; k < K; ++k) s += (int64_t)w[k] * ((int64_t)x[k] - zx);
     return (float)s;
@@ -397,6 +399,16 @@ int olstm_real_activation(float q, float s_in, int32_t zp_in, float s_out, int32
                           const rxmet_lstm_op_config *out_t, int is_tanh, int mode, float *out,
                           uint8_t *clamped) {
   *out = real_activation(q, s_in, zp_in, s_out, zp_out, out_t, is_tanh, mode, clamped);
+  return 0;
+}
+
+/* real_activation of every code lo..hi of an input grid (a whole activation table). */
+int olstm_real_activation_table(float s_in, int32_t zp_in, int32_t lo, int32_t hi, float s_out,
+                                int32_t zp_out, const rxmet_lstm_op_config *out_t, int is_tanh,
+                                int mode, float *out, uint8_t *clamped) {
+  for (int64_t q = lo; q <= hi; ++q)
+    out[q - lo] = real_activation((float)q, s_in, zp_in, s_out, zp_out, out_t, is_tanh, mode,
+                                  &clamped[q - lo]);
   return 0;
 }
 

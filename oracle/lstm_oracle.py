@@ -17,7 +17,10 @@ import rxmet_lstm_abi as L  # noqa: E402  (struct layouts of include/rxmet_lstm.
 f32 = np.float32
 _P = ctypes.c_void_p
 _i = ctypes.c_int
-ACT_LIBM, ACT_CR = 0, 1
+# ACT_LIBM: the reference CPU core (C-library expf/tanhf, linear sums in fp32 in index order);
+# ACT_CR: exp/tanh in double, exact linear sums; ACT_LIBM_EXACT: the C library's activations
+# with exact linear sums, what the GPU kernels compute.
+ACT_LIBM, ACT_CR, ACT_LIBM_EXACT = 0, 1, 2
 
 
 def _lib(path: Path):
@@ -34,6 +37,9 @@ _o.olstm_derive_exec.argtypes = [_PP, _i, _P, _P, _P, _P, _P]
 _o.olstm_real_activation.argtypes = [ctypes.c_float, ctypes.c_float, ctypes.c_int32,
                                      ctypes.c_float, ctypes.c_int32, ctypes.POINTER(L.OpConfig),
                                      _i, _i, _P, _P]
+_o.olstm_real_activation_table.argtypes = [ctypes.c_float, ctypes.c_int32, ctypes.c_int32,
+                                            ctypes.c_int32, ctypes.c_float, ctypes.c_int32,
+                                            ctypes.POINTER(L.OpConfig), _i, _i, _P, _P]
 _o.olstm_forward_quant.argtypes = [_i] * 4 + [_P] * 7 + [_PP, _i] + [_P] * 3 + \
     [ctypes.POINTER(L.Saved)] + [_P] * 3
 _o.olstm_forward_float.argtypes = [_i] * 4 + [_P] * 7 + [_i] + [_P] * 4
@@ -111,6 +117,17 @@ def derive_exec(params, input_size, ref=False):
             "linear_to_gate": rs(gate),
             "cell": [(q.multiplier, q.mantissa, q.exponent, q.uses_fp) for q in cell],
             "hidden": rs(hid)}
+
+
+def real_activation_table(lo, hi, s_in, zp_in, s_out, zp_out, out_cfg, is_tanh, mode=ACT_LIBM):
+    """Output codes and clamp masks of the real activation for every input code lo..hi."""
+    n = int(hi) - int(lo) + 1
+    out = np.zeros(n, f32)
+    m = np.zeros(n, np.uint8)
+    _o.olstm_real_activation_table(float(s_in), int(zp_in), int(lo), int(hi), float(s_out),
+                                   int(zp_out), ctypes.byref(out_cfg), int(is_tanh), int(mode),
+                                   _p(out), _p(m))
+    return out, m
 
 
 def real_activation(q, s_in, zp_in, s_out, zp_out, out_cfg, is_tanh, mode=ACT_LIBM):

@@ -3,7 +3,7 @@
 // A persistent recurrence splits one batch tile's hidden units over G workgroups (a cluster).
 // Each step the members exchange the new hidden codes through global memory and meet at a
 // counter in global memory.  The launch is cooperative, so every workgroup is resident; the
-// wait is still bounded: after kSpinLimit polls a member gives up, raises the timeout flag
+// wait is still bounded: after a limit of polls a member gives up, raises the timeout flag
 // and stops stepping, so every wave of the grid reaches the end of the kernel.
 #pragma once
 
@@ -15,6 +15,15 @@ namespace rxmet {
 namespace cluster {
 
 constexpr unsigned kSpinLimit = 1u << 20;  // about a second of polling
+
+// The poll limit a launch passes to its waits: kSpinLimit, or RXMET_TEST_SPIN_LIMIT from the
+// environment.  Tests of the timeout path set it to 0, so that a wait that has to poll gives
+// up at once: the launch then takes the path of a real timeout (flag raised, members stop
+// stepping, every wave reaches the end of the kernel, outputs poisoned with NaN).
+inline unsigned spin_limit() {
+  const char *s = std::getenv("RXMET_TEST_SPIN_LIMIT");
+  return s != nullptr ? static_cast<unsigned>(std::strtoul(s, nullptr, 10)) : kSpinLimit;
+}
 
 struct Place {
   int cluster, member;
@@ -51,7 +60,8 @@ __device__ __forceinline__ Place place(int G, int nclusters) {
 // wait (write back, then invalidate, the whole XCD's L2), issued by every workgroup at every
 // step.  Measured on the c3 GRU step: 6.10 ms against 3.50 ms; c4 LSTM step 4.41 against
 // 3.37 ms.  Nothing here needs that cache maintenance.
-__device__ __forceinline__ bool sync(unsigned *counter, unsigned arrivals, int *timeout) {
+__device__ __forceinline__ bool sync(unsigned *counter, unsigned arrivals, int *timeout,
+                                     unsigned limit) {
   __shared__ int ok;
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
@@ -61,7 +71,7 @@ __device__ __forceinline__ bool sync(unsigned *counter, unsigned arrivals, int *
     unsigned spins = 0;
     while (__hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < arrivals) {
       __builtin_amdgcn_s_sleep(1);
-      if (++spins > kSpinLimit) {
+      if (++spins > limit) {
         good = 0;
         __hip_atomic_store(timeout, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         break;
@@ -83,14 +93,15 @@ __device__ __forceinline__ void arrive(unsigned *counter) {
   if (threadIdx.x == 0) __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ __forceinline__ bool wait(unsigned *counter, unsigned arrivals, int *timeout) {
+__device__ __forceinline__ bool wait(unsigned *counter, unsigned arrivals, int *timeout,
+                                     unsigned limit) {
   __shared__ int ok;
   if (threadIdx.x == 0) {
     int good = 1;
     unsigned spins = 0;
     while (__hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < arrivals) {
       __builtin_amdgcn_s_sleep(1);
-      if (++spins > kSpinLimit) {
+      if (++spins > limit) {
         good = 0;
         __hip_atomic_store(timeout, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         break;

@@ -319,6 +319,7 @@ struct BwdClArgs {
   int ncl, G, UT, ntiles, Bpad, KP, ndir;  // KP = 3H padded to a multiple of 64
   unsigned *counters;
   int *timeout;
+  unsigned spin_limit;  // polls before a wait gives up (cluster::spin_limit())
 };
 
 // R_q [H][3H] -> per (unit tile ut, wave q, 32-channel block kb, lane l) the bf16 B fragment
@@ -507,7 +508,7 @@ __device__ __forceinline__ void bwd_cl_pair(const BwdArgs &a, const BwdClArgs &c
         }
       }
       if (valid && t > 0) bwd_load_step(a, mk, t - 1, b, j, cur);
-      alive = cluster::wait(counter, epoch * cl.G, cl.timeout);
+      alive = cluster::wait(counter, epoch * cl.G, cl.timeout, cl.spin_limit);
       if (!alive) break;
       // stage the tile's exchange rows in LDS (all loads in flight; a q past the row re-reads
       // q = 0 and is not stored), then dh += R_deq dq over this wave's quarter of the channels
@@ -933,6 +934,7 @@ static int backward_recurrence_clustered(BwdPlan *plans, int ndir, int T, int B,
   const BwdWorkspace ws(T, B, I, H);
   cl.counters = reinterpret_cast<unsigned *>(plans[0].wsb + ws.sync);
   cl.timeout = reinterpret_cast<int *>(cl.counters + ncl);
+  cl.spin_limit = cluster::spin_limit();
   for (int k = 0; k < ndir; ++k) {
     hipLaunchKernelGGL(pack_rt_bf16, dim3((H / 16) * 4 * ((KS2 + 1) / 2)), dim3(64), 0, stream, H, KS2,
                        npr, plans[k].d->R_q, const_cast<uint4 *>(plans[k].ba.rt));

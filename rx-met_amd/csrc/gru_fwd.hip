@@ -647,6 +647,7 @@ struct ClArgs {
   int gate_tab;                        // gate activations by table (every gate grid fits)
   unsigned *counters;                  // [ncl]
   int *timeout;
+  unsigned spin_limit;  // polls before a wait gives up (cluster::spin_limit())
 };
 
 // Staged mask bytes of fields f0..f0+ng-1 ([16 rows][13][UW] in LDS) to a mask array
@@ -760,7 +761,7 @@ __device__ __forceinline__ void recurrence_cl_pair(const RecArgs &a, const StepP
         gi_next[g] = valid ? a.gih[(static_cast<size_t>(t) * B + b) * C + g * H + j] : 0.0f;
     };
     load_gih(0);
-    alive = cluster::sync(counter, ++epoch * cl.G, cl.timeout);
+    alive = cluster::sync(counter, ++epoch * cl.G, cl.timeout, cl.spin_limit);
 
     for (int t = 0; t < a.T && alive; ++t) {
       const int par = t & 1;
@@ -923,7 +924,7 @@ __device__ __forceinline__ void recurrence_cl_pair(const RecArgs &a, const StepP
         store_point(a, p, t, b, j, o);
       }
       if (t + 1 < a.T) load_gih(t + 1);
-      alive = cluster::wait(counter, epoch * cl.G, cl.timeout);
+      alive = cluster::wait(counter, epoch * cl.G, cl.timeout, cl.spin_limit);
     }
   }
 }
@@ -1254,6 +1255,7 @@ static int forward_recurrence_clustered(FwdPlan *plans, int ndir, int T, int B, 
   const FwdWorkspace ws(T, B, I, H);
   cl.counters = reinterpret_cast<unsigned *>(plans[0].wsb + ws.sync);
   cl.timeout = reinterpret_cast<int *>(cl.counters + ncl);
+  cl.spin_limit = cluster::spin_limit();
   hipLaunchKernelGGL(cluster::zero_words, dim3(1), dim3(256), 0, stream, cl.counters, ncl + 1);
   RXMET_CHECK_LAUNCH();
   RecArgs &a1 = plans[ndir > 1 ? 1 : 0].ra;

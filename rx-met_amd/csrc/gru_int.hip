@@ -330,6 +330,7 @@ struct IClArgs {
   int8_t *hx;                   // [2][NPL][Bpad / 16][KS][16][64] exchanged h codes (see ihx_offset)
   unsigned *counters;           // [ncl]
   int *timeout;
+  unsigned spin_limit;  // polls before a wait gives up (cluster::spin_limit())
   int gate_tab;                 // gate activations by table (every gate grid fits)
 };
 
@@ -460,7 +461,7 @@ __global__ __launch_bounds__(512) void int_recurrence_cl(IClArgs a, IntStepParam
         wn_[g] = valid ? a.wx[(static_cast<size_t>(t) * B + b) * C + g * H + j] : 0;
     };
     load_wx(0);
-    alive = cluster::sync(counter, ++epoch * a.G, a.timeout);
+    alive = cluster::sync(counter, ++epoch * a.G, a.timeout, a.spin_limit);
     for (int t = 0; t < a.T && alive; ++t) {
       const int par = t & 1;
       const unsigned hin = par * NPL * plane_stride;  // byte offset of the step's planes
@@ -576,7 +577,7 @@ __global__ __launch_bounds__(512) void int_recurrence_cl(IClArgs a, IntStepParam
         }
       }
       if (t + 1 < a.T) load_wx(t + 1);
-      alive = cluster::wait(counter, epoch * a.G, a.timeout);
+      alive = cluster::wait(counter, epoch * a.G, a.timeout, a.spin_limit);
     }
   }
 }
@@ -740,6 +741,7 @@ static int int_recurrence_clustered(const IntCall &k, const IntStepParams &sp,
   a.hx = reinterpret_cast<int8_t *>(wsb + ws.hx);
   a.counters = reinterpret_cast<unsigned *>(wsb + ws.sync);
   a.timeout = reinterpret_cast<int *>(a.counters + ncl);
+  a.spin_limit = cluster::spin_limit();
   hipLaunchKernelGGL(cluster::zero_words, dim3(1), dim3(256), 0, stream, a.counters, ncl + 1);
   RXMET_CHECK_LAUNCH();
   IntStepParams spc = sp;

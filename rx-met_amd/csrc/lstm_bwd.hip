@@ -355,6 +355,7 @@ struct BwdClArgs {
   const float *csum;   // [KS2][H] column sums of W_hh codes over each K-step's 64 channels
   unsigned *counters;
   int *timeout;
+  unsigned spin_limit;  // polls before a wait gives up (cluster::spin_limit())
 };
 
 // Byte offset of the exchange buffer's block for (parity, plane, batch tile, K-step): the tile's
@@ -658,7 +659,7 @@ __global__ __launch_bounds__(512) void lstm_bwd_recurrence_cl(BwdArgs a, BwdClAr
                 *reinterpret_cast<const float4 *>(sdl + (row * 8 + 4 + g) * kBcUnits + 4 * q);
         }
       }
-      alive = cluster::wait(counter, epoch * G, cl.timeout);
+      alive = cluster::wait(counter, epoch * G, cl.timeout, cl.spin_limit);
       if (!alive) break;
       // dh partial of the wave's K-steps for the member's 64 units: A fragments (row l % 16,
       // channels 64 ks + 16 (l / 16) + 0..15 of each plane) and the rows' exponents loaded
@@ -996,6 +997,7 @@ int rxmet_lstm_backward_quant(int32_t T, int32_t B, int32_t I, int32_t H,
       cl.xe = reinterpret_cast<int *>(wsb + ws.xe);
       cl.counters = reinterpret_cast<unsigned *>(wsb + ws.sync);
       cl.timeout = reinterpret_cast<int *>(cl.counters + ncl);
+      cl.spin_limit = cluster::spin_limit();
       hipLaunchKernelGGL(lstm_pack_whh_t_cl, dim3((H / 16) * KS2), dim3(64), 0, stream, H, KS2,
                          sv.w_hh_q, wf, cs);
       RXMET_CHECK_LAUNCH();

@@ -117,12 +117,36 @@ __device__ __forceinline__ float act_tanh(float x) {
 }
 
 // Real activation boundary: dequantise, activate in fp32, quantise to the output grid.
+// Activation k (gates 0..3, 4 = tanh of the cell) then takes the reference CPU core's result
+// at the few input codes where its C-library expf / tanhf lead to another output code than
+// the double evaluation (sp.exc_*, listed on the host; none on most grids).
+// EXC = false skips the lookup (launches whose parameters have no exception codes).
+template <bool EXC = true>
 __device__ __forceinline__ float real_act(float q, const Grid &in, const Grid &out, bool is_tanh,
-                                          uint8_t &clamped) {
+                                          const StepParams &sp, int k, uint8_t &clamped) {
   const float x = static_cast<float>((static_cast<double>(q) - in.dzp) * in.dscale);
   const float a = is_tanh ? act_tanh(x) : act_sigmoid(x);
   const double t = rint(static_cast<double>(a) / out.dscale) + out.dzp;
-  return clamp_grid(t, out, clamped);
+  float v = clamp_grid(t, out, clamped);
+  const int n = EXC ? sp.exc_n[k] : 0;
+  if (n > 0) {
+    const int32_t key = static_cast<int32_t>(q);
+    const int32_t *ks = sp.exc_key + sp.exc_off[k];
+    int lo = 0, hi = n;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (ks[mid] < key)
+        lo = mid + 1;
+      else
+        hi = mid;
+    }
+    if (lo < n && ks[lo] == key) {
+      const uint32_t e = sp.exc_val[sp.exc_off[k] + lo];
+      clamped = static_cast<uint8_t>(e & 1u);
+      v = static_cast<float>(static_cast<int64_t>(e >> 1) + out.lo);
+    }
+  }
+  return v;
 }
 
 // Element r of an MFMA accumulator without dynamic register indexing.
@@ -344,13 +368,13 @@ __device__ __forceinline__ LstmPoint lstm_point(const float accf[4], const float
                               sp.hh_to_gate[g].shift);
     const float gi = clamp_grid(static_cast<double>(lhs[g] + rhs) + sp.gin[g].dzp, sp.gin[g],
                                 o.m_gi[g]);
-    o.gout[g] = real_act(gi, sp.gin[g], sp.gout[g], g == 2, o.m_go[g]);
+    o.gout[g] = real_act(gi, sp.gin[g], sp.gout[g], g == 2, sp, g, o.m_go[g]);
   }
   const float pf = center(o.gout[1], sp.gout[1].zp) * center(c_old, sp.c.zp);
   const float pi = center(o.gout[0], sp.gout[0].zp) * center(o.gout[2], sp.gout[2].zp);
   const float sum = cell_scale(pf, sp, 0) + cell_scale(pi, sp, 1);
   o.cn = clamp_grid(static_cast<double>(rintf(sum)) + sp.c.dzp, sp.c, o.m_c);
-  o.ct = real_act(o.cn, sp.c, sp.tanh_c, true, o.m_t);
+  o.ct = real_act(o.cn, sp.c, sp.tanh_c, true, sp, 4, o.m_t);
   const float raw = center(o.gout[3], sp.gout[3].zp) * center(o.ct, sp.tanh_c.zp);
   o.hv = clamp_grid(static_cast<double>(rescale(raw, sp.hidden.mult, sp.hidden.shift)) + sp.h.dzp,
                     sp.h, o.m_h);
@@ -559,13 +583,14 @@ __global__ __launch_bounds__(256) void lstm_build_act_lut(StepParams sp, ActLut 
   float v;
   int lo;
   if (lut.tanh_n > 0 && i >= lut.tanh_off) {
-    v = real_act(static_cast<float>(sp.c.lo + (i - lut.tanh_off)), sp.c, sp.tanh_c, true, m);
+    v = real_act(static_cast<float>(sp.c.lo + (i - lut.tanh_off)), sp.c, sp.tanh_c, true, sp, 4,
+                 m);
     lo = sp.tanh_c.lo;
   } else {
     int g = 0;
     while (g < 3 && i >= lut.off[g + 1]) ++g;
     v = real_act(static_cast<float>(sp.gin[g].lo + (i - lut.off[g])), sp.gin[g], sp.gout[g],
-                 g == 2, m);
+                 g == 2, sp, g, m);
     lo = sp.gout[g].lo;
   }
   table[i] = (static_cast<uint32_t>(static_cast<int>(v) - lo) << 1) | m;
@@ -583,6 +608,7 @@ struct ClusterArgs {
   int8_t *hx;          // [2][NPL][Bpad][H] centred h codes as int8 planes
   unsigned *counters;  // [ncl] barrier arrivals
   int *timeout;        // set by a member whose barrier wait gave up
+  unsigned spin_limit; // polls before a wait gives up (cluster::spin_limit())
   ActLut lut;
 };
 
@@ -665,7 +691,7 @@ __device__ __forceinline__ void flush_step(const RecArgs &a, const StepParams &s
   }
 }
 
-template <int NPL>
+template <int NPL, bool EXC>
 __global__ __launch_bounds__(512) void lstm_recurrence_cl(RecArgs a, StepParams sp,
                                                           ClusterArgs cl) {
   extern __shared__ __align__(16) unsigned char smem[];
@@ -734,7 +760,7 @@ __global__ __launch_bounds__(512) void lstm_recurrence_cl(RecArgs a, StepParams 
         }
     };
     load_lhs(0);
-    alive = cluster::sync(counter, ++epoch * cl.G, cl.timeout);
+    alive = cluster::sync(counter, ++epoch * cl.G, cl.timeout, cl.spin_limit);
 
     for (int t = 0; t < a.T && alive; ++t) {
       const int par = t & 1;
@@ -834,7 +860,7 @@ __global__ __launch_bounds__(512) void lstm_recurrence_cl(RecArgs a, StepParams 
             const float go =
                 gate_lut ? lut_code(lut + (q == 0 ? cl.lut.off[g0] : cl.lut.off[g0 + 1]),
                                     static_cast<int>(gi) - gin.lo, gout.lo, m_go)
-                         : real_act(gi, gin, gout, g == 2, m_go);
+                         : real_act<EXC>(gi, gin, gout, g == 2, sp, g, m_go);
             xg[((ut * 4 + g) * 16 + nr) * 16 + l % 16] = go;
             if (a.wide_out) {
               if (train)
@@ -872,7 +898,7 @@ __global__ __launch_bounds__(512) void lstm_recurrence_cl(RecArgs a, StepParams 
         cts[rr] =
             tanh_lut ? lut_code(lut + cl.lut.tanh_off, static_cast<int>(cn) - sp.c.lo,
                                 sp.tanh_c.lo, mts[rr])
-                     : real_act(cn, sp.c, sp.tanh_c, true, mts[rr]);
+                     : real_act<EXC>(cn, sp.c, sp.tanh_c, true, sp, 4, mts[rr]);
         const float raw = center_f(gout[3], sp.gout[3].zp) * center_f(cts[rr], sp.tanh_c.zp);
         hvs[rr] = clamp_grid_f(rescale(raw, sp.hidden.mult, sp.hidden.shift), sp.h, mhs[rr]);
         if (a.wide_out && train)
@@ -923,7 +949,7 @@ __global__ __launch_bounds__(512) void lstm_recurrence_cl(RecArgs a, StepParams 
         }
       }
       }
-      alive = cluster::wait(counter, epoch * cl.G, cl.timeout);
+      alive = cluster::wait(counter, epoch * cl.G, cl.timeout, cl.spin_limit);
     }
   }
 }
@@ -954,8 +980,8 @@ size_t recurrence_lds(int H, int KS, int npl) {
 }
 
 struct FwdWorkspace {
-  size_t chost, run, frag, lhs, xq, wih, whh, bih, bhh, h0q, c0q, hx, sync, lut, xa, bfrag, colsum,
-      sh, sc, sg, total;
+  size_t chost, run, frag, lhs, xq, wih, whh, bih, bhh, h0q, c0q, hx, sync, lut, exc, xa, bfrag,
+      colsum, sh, sc, sg, total;
   FwdWorkspace(int T, int B, int I, int H) {
     const size_t C = 4 * static_cast<size_t>(H), KS = (H + 63) / 64;
     auto al = [](size_t x) { return (x + 255) & ~static_cast<size_t>(255); };
@@ -977,6 +1003,8 @@ struct FwdWorkspace {
     hx = o; o += al(2 * 2 * Bpad * H);
     sync = o; o += al(sizeof(unsigned) * (Bpad / 16 + 1));
     lut = o; o += al(sizeof(uint32_t) * 2 * kLutMaxEntries);
+    // reference activation exceptions: keys, then entries, of at most 5 full 16-bit grids
+    exc = o; o += al(sizeof(int32_t) * 2 * 5 * static_cast<size_t>(kActExcMaxCodes));
     // packed operands of the input linear (I <= 256): x planes, W_ih fragments, column sums
     const size_t Kp = static_cast<size_t>(xgemm::pad_k(I));
     const size_t ip = static_cast<size_t>(I) <= kPackedMaxK ? 1 : 0;
@@ -1053,6 +1081,21 @@ int rxmet_lstm_forward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const f
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   const FwdWorkspace ws(T, B, I, H);
   char *wsb = static_cast<char *>(workspace);
+  const ActExceptions exc = act_exceptions(sp);
+  if (!exc.key.empty()) {
+    int32_t *ek = reinterpret_cast<int32_t *>(wsb + ws.exc);
+    uint32_t *ev = reinterpret_cast<uint32_t *>(ek + 5 * static_cast<size_t>(kActExcMaxCodes));
+    RXMET_CHECK_HIP(hipMemcpyAsync(ek, exc.key.data(), sizeof(int32_t) * exc.key.size(),
+                                   hipMemcpyHostToDevice, stream));
+    RXMET_CHECK_HIP(hipMemcpyAsync(ev, exc.val.data(), sizeof(uint32_t) * exc.val.size(),
+                                   hipMemcpyHostToDevice, stream));
+    sp.exc_key = ek;
+    sp.exc_val = ev;
+    for (int k = 0; k < 5; ++k) {
+      sp.exc_off[k] = exc.off[k];
+      sp.exc_n[k] = exc.n[k];
+    }
+  }
   std::vector<ChanHost> hostc(C);
   for (int c = 0; c < C; ++c) {
     ChanHost &h = hostc[c];
@@ -1222,8 +1265,12 @@ int rxmet_lstm_forward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const f
   for (int g = 0; g < 4; ++g) f32_grids = f32_grids && fits_f32(sp.gin[g]) && fits_f32(sp.gout[g]);
   if (H % kClUnits == 0 && f32_grids) {
     // clustered path when the whole grid can be resident at once
-    const void *fn = npl == 1 ? reinterpret_cast<const void *>(&lstm_recurrence_cl<1>)
-                              : reinterpret_cast<const void *>(&lstm_recurrence_cl<2>);
+    const bool has_exc = !exc.key.empty();
+    const void *fn =
+        npl == 1 ? (has_exc ? reinterpret_cast<const void *>(&lstm_recurrence_cl<1, true>)
+                            : reinterpret_cast<const void *>(&lstm_recurrence_cl<1, false>))
+                 : (has_exc ? reinterpret_cast<const void *>(&lstm_recurrence_cl<2, true>)
+                            : reinterpret_cast<const void *>(&lstm_recurrence_cl<2, false>));
     ActLut lut{};
     uint32_t *lut_table = reinterpret_cast<uint32_t *>(wsb + ws.lut);
     {
@@ -1274,6 +1321,7 @@ int rxmet_lstm_forward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const f
       cl.hx = reinterpret_cast<int8_t *>(wsb + ws.hx);
       cl.counters = reinterpret_cast<unsigned *>(wsb + ws.sync);
       cl.timeout = reinterpret_cast<int *>(cl.counters + ncl);
+      cl.spin_limit = cluster::spin_limit();
       cl.lut = lut;
       hipLaunchKernelGGL(cluster::zero_words, dim3(1), dim3(256), 0, stream, cl.counters, ncl + 1);
       RXMET_CHECK_LAUNCH();

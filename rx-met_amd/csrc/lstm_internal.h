@@ -35,6 +35,25 @@ struct StepParams {
   double cell_mant[2];
   int32_t cell_exp[2];
   int32_t cell_fp[2];
+  // Reference activation exceptions (device copies of ActExceptions below): for activation k
+  // (gates i, f, g, o, then tanh of the cell) the sorted input codes exc_key[exc_off[k] ..
+  // + exc_n[k]) and their entries exc_val[...] = (output code - output lo) << 1 | clamp mask.
+  const int32_t *exc_key;
+  const uint32_t *exc_val;
+  int32_t exc_off[5], exc_n[5];
+};
+
+// The reference's CPU core evaluates the real activations with the C library's expf / tanhf
+// (quantized_fp_math.cuh:21-30, compiled for the host); the kernels evaluate exp / tanh in
+// double and round once.  Both are then quantised to the output grid, so the two differ only
+// at the input codes listed here: every code of each input grid of at most 2^16 codes is
+// evaluated both ways on the host (kActExcMaxCodes), and the codes whose output code or clamp
+// mask differ are kept with the reference's result.  Wider grids are not enumerated (n = 0).
+constexpr int kActExcMaxCodes = 1 << 16;
+struct ActExceptions {
+  std::vector<int32_t> key;
+  std::vector<uint32_t> val;
+  int32_t off[5] = {0, 0, 0, 0, 0}, n[5] = {0, 0, 0, 0, 0};
 };
 
 // Per-channel (4H) parameters, laid out as arrays of length 4H.
@@ -46,6 +65,12 @@ struct ChannelParams {
 Grid grid_of(const rxmet_lstm_op_config &t, float scale, int32_t zp);
 // Derives every encoding; returns 0 or -22 with the error message set.
 int derive(const rxmet_lstm_params &p, StepParams *sp, ChannelParams *cp);
+// Exception lists of the five activations of sp (computed once per set of grids and cached;
+// thread-safe; returned by value).
+ActExceptions act_exceptions(const StepParams &sp);
+// Entry (output code - lo) << 1 | mask of activation k at input code q: the reference CPU
+// core's arithmetic (reference = true) or the kernels' double evaluation.
+uint32_t act_entry(const StepParams &sp, int k, int32_t q, bool reference);
 
 }  // namespace lstm
 }  // namespace rxmet

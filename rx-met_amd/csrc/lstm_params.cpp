@@ -11,6 +11,7 @@
 #include <cfloat>
 #include <cmath>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "lstm_internal.h"
@@ -163,7 +164,96 @@ void cell_ratio(double ratio, float *r, int64_t *q31, double *mant, int32_t *ex,
   *fp = 1;
 }
 
+// The activation's input and output grids: k < 4 gate k, k == 4 tanh of the cell.
+void act_grids(const StepParams &sp, int k, const Grid **in, const Grid **out, bool *is_tanh) {
+  *in = k < 4 ? &sp.gin[k] : &sp.c;
+  *out = k < 4 ? &sp.gout[k] : &sp.tanh_c;
+  *is_tanh = k == 2 || k == 4;
+}
+
+// realSigmoid / realTanh of the reference (quantized_fp_math.cuh:21-30) on the host: the C
+// library's expf and tanhf in fp32.
+float sigmoid_libm(float x) {
+  if (x >= 0.0f) {
+    const float e = ::expf(-x);
+    return 1.0f / (1.0f + e);
+  }
+  const float e = ::expf(x);
+  return e / (1.0f + e);
+}
+
+// The kernels' form: exp and tanh in double, rounded once to fp32, same op order around exp.
+float sigmoid_dbl(float x) {
+  if (x >= 0.0f) {
+    const float e = static_cast<float>(std::exp(-static_cast<double>(x)));
+    return 1.0f / (1.0f + e);
+  }
+  const float e = static_cast<float>(std::exp(static_cast<double>(x)));
+  return e / (1.0f + e);
+}
+
+struct ActCacheEntry {
+  std::vector<double> key;
+  ActExceptions ex;
+};
+
 }  // namespace
+
+uint32_t act_entry(const StepParams &sp, int k, int32_t q, bool reference) {
+  const Grid *in, *out;
+  bool is_tanh;
+  act_grids(sp, k, &in, &out, &is_tanh);
+  // realActivationQuantizedCore (quantized_fp_math.cuh:32-63): dequantise in double,
+  // activate in fp32, RNE of the double quotient plus the zero point, clamp to the grid.
+  const float x = static_cast<float>((static_cast<double>(q) - in->dzp) * in->dscale);
+  const float a = is_tanh ? (reference ? ::tanhf(x) : static_cast<float>(std::tanh(static_cast<double>(x))))
+                          : (reference ? sigmoid_libm(x) : sigmoid_dbl(x));
+  const double t = std::nearbyint(static_cast<double>(a) / out->dscale) + out->dzp;
+  const uint32_t m = (t < out->dlo || t > out->dhi) ? 1u : 0u;
+  const double v = t <= out->dflo ? out->flo : (t >= out->dfhi ? out->fhi : t);
+  return (static_cast<uint32_t>(static_cast<int64_t>(v) - out->lo) << 1) | m;
+}
+
+ActExceptions act_exceptions(const StepParams &sp) {
+  std::vector<double> key;
+  for (int k = 0; k < 5; ++k) {
+    const Grid *in, *out;
+    bool is_tanh;
+    act_grids(sp, k, &in, &out, &is_tanh);
+    for (const Grid *g : {in, out}) {
+      key.push_back(g->lo);
+      key.push_back(g->hi);
+      key.push_back(g->scale);
+      key.push_back(g->zp);
+    }
+  }
+  static std::mutex mu;
+  static std::vector<ActCacheEntry> cache;  // most recent last; a handful of parameter sets
+  std::lock_guard<std::mutex> lock(mu);
+  for (size_t i = 0; i < cache.size(); ++i)
+    if (cache[i].key == key) return cache[i].ex;
+  ActCacheEntry e;
+  e.key = key;
+  for (int k = 0; k < 5; ++k) {
+    const Grid *in, *out;
+    bool is_tanh;
+    act_grids(sp, k, &in, &out, &is_tanh);
+    e.ex.off[k] = static_cast<int32_t>(e.ex.key.size());
+    const int64_t ncodes = static_cast<int64_t>(in->hi) - in->lo + 1;
+    if (ncodes <= kActExcMaxCodes)
+      for (int64_t q = in->lo; q <= in->hi; ++q) {
+        const uint32_t r = act_entry(sp, k, static_cast<int32_t>(q), true);
+        if (r != act_entry(sp, k, static_cast<int32_t>(q), false)) {
+          e.ex.key.push_back(static_cast<int32_t>(q));
+          e.ex.val.push_back(r);
+        }
+      }
+    e.ex.n[k] = static_cast<int32_t>(e.ex.key.size()) - e.ex.off[k];
+  }
+  if (cache.size() >= 8) cache.erase(cache.begin());
+  cache.push_back(std::move(e));
+  return cache.back().ex;
+}
 
 Grid grid_of(const rxmet_lstm_op_config &t, float scale, int32_t zp) {
   Grid g;
@@ -192,6 +282,9 @@ int derive(const rxmet_lstm_params &p, StepParams *sp, ChannelParams *cp) {
       RXMET_CHECK_ARG(std::isfinite(p.scale[i]) && p.scale[i] > 0.0f,
                       "QuantLSTM standard scales must be finite and positive");
   const bool pot2 = p.config.scale_mode == RXMET_LSTM_POT2;
+  sp->exc_key = nullptr;
+  sp->exc_val = nullptr;
+  for (int k = 0; k < 5; ++k) sp->exc_off[k] = sp->exc_n[k] = 0;
   auto G = [&](int i) { return grid_of(op[i], p.scale[i], p.zero_point[i]); };
   sp->x = G(RXMET_LSTM_INPUT);
   sp->h = G(RXMET_LSTM_OUTPUT);
@@ -349,6 +442,43 @@ int rxmet_lstm_derive_exec(const rxmet_lstm_params *p, int32_t input_size,
   }
   if (hidden_rescale) put(sp.hidden, hidden_rescale);
   return 0;
+}
+
+int32_t rxmet_lstm_activation_table(const rxmet_lstm_params *p, int32_t k, int32_t reference,
+                                    uint32_t *entries, int32_t capacity) {
+  clear_error();
+  RXMET_CHECK_ARG(p && entries && k >= 0 && k < 5, "invalid arguments");
+  StepParams sp;
+  if (int rc = derive(*p, &sp, nullptr)) return rc;
+  const Grid &in = k < 4 ? sp.gin[k] : sp.c;
+  const int64_t n = static_cast<int64_t>(in.hi) - in.lo + 1;
+  RXMET_CHECK_ARG(n <= kActExcMaxCodes && n <= capacity,
+                  "input grid wider than 65536 codes or capacity too small");
+  for (int64_t i = 0; i < n; ++i)
+    entries[i] = act_entry(sp, k, static_cast<int32_t>(in.lo + i), reference != 0);
+  return static_cast<int32_t>(n);
+}
+
+int32_t rxmet_lstm_activation_exceptions(const rxmet_lstm_params *p, int32_t *keys,
+                                         uint32_t *entries, int32_t capacity, int32_t *off,
+                                         int32_t *n) {
+  clear_error();
+  RXMET_CHECK_ARG(p && off && n && capacity >= 0 && (capacity == 0 || (keys && entries)),
+                  "invalid arguments");
+  StepParams sp;
+  if (int rc = derive(*p, &sp, nullptr)) return rc;
+  const ActExceptions ex = act_exceptions(sp);
+  for (int k = 0; k < 5; ++k) {
+    off[k] = ex.off[k];
+    n[k] = ex.n[k];
+  }
+  const size_t m = ex.key.size() < static_cast<size_t>(capacity) ? ex.key.size()
+                                                                 : static_cast<size_t>(capacity);
+  for (size_t i = 0; i < m; ++i) {
+    keys[i] = ex.key[i];
+    entries[i] = ex.val[i];
+  }
+  return static_cast<int32_t>(ex.key.size());
 }
 
 }  // extern "C"

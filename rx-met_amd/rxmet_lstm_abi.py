@@ -118,6 +118,8 @@ _SIGS = {
                                   [_p] * 3 + [_p] * 7 + [_p, _p]),
     "rxmet_lstm_forward_calibrate": (ctypes.c_int, [_i32] * 4 + [_p] * 7 + [_p] * 4 + [_p, _p]),
     "rxmet_lstm_forward_float": (ctypes.c_int, [_i32] * 4 + [_p] * 7 + [_p] * 3 + [_p]),
+    "rxmet_lstm_activation_table": (_i32, [ctypes.POINTER(Params), _i32, _i32, _p, _i32]),
+    "rxmet_lstm_activation_exceptions": (_i32, [ctypes.POINTER(Params), _p, _p, _i32, _p, _p]),
 }
 for _name, (_res, _args) in _SIGS.items():
     _rx.register(_name, _res, _args)

@@ -378,8 +378,9 @@ def test_stepped_backward_matches_clustered(cuda, shape, cfg_name, monkeypatch):
 def test_c5_full_size_rows_match_oracle(cuda):
     """c5 at its full size (T=50, B=1024, I=256, H=1024, 4-bit W and R, 16-bit activations and
     h, pot2): sequences are independent, so the GPU's rows of a sample of sequences equal the
-    oracle run on those sequences alone — forward outputs and masks bit for bit, dx and dh0
-    within 1e-4."""
+    oracle run on those sequences alone — forward outputs and masks bit for bit.  The output
+    gradient is set on the sampled sequences only (zero elsewhere), so every weight and bias
+    gradient is a sum over those sequences: dx, dh0, dW, dR, dbw and dbr within 1e-4."""
     T, B, I, H = 50, 1024, 256, 1024
     rows = [0, 1, 517, 1023]
     print(f"[gru c5 full] T={T} B={B} I={I} H={H} rows={rows}", flush=True)
@@ -403,14 +404,17 @@ def test_c5_full_size_rows_match_oracle(cuda):
             continue
         idx = torch.tensor(rows, device=tensor.device)
         np.testing.assert_array_equal(tensor.index_select(axis, idx).cpu().numpy(), e, err_msg=name)
-    dh_new = (g.standard_normal((T + 1, B, H)) * 1e-2).astype(f32)
+    dh_new = np.zeros((T + 1, B, H), f32)
+    dh_new[1:, rows] = (g.standard_normal((T, len(rows), H)) * 1e-2).astype(f32)
     got = _gpu_backward(cuda, fwd, dh_new, qp, T, B, I, H)
     exp = GO.backward_quant(exp_f, np.ascontiguousarray(dh_new[:, rows]), qp)
-    for name, a, axis in (("dx", got[0], 1), ("dh0", got[5], 0)):
+    for name, a, axis in (("dx", got[0], 1), ("dW", got[1], None), ("dR", got[2], None),
+                          ("dbw", got[3], None), ("dbr", got[4], None), ("dh0", got[5], 0)):
         e = exp[name]
         scale = max(float(np.abs(e).max()), 1e-30)
-        np.testing.assert_allclose(a.take(rows, axis=axis), e, rtol=1e-4, atol=1e-5 * scale,
-                                   err_msg=name)
+        assert np.isfinite(a).all(), name
+        np.testing.assert_allclose(a if axis is None else a.take(rows, axis=axis), e, rtol=1e-4,
+                                   atol=1e-5 * scale, err_msg=name)
 
 
 @pytest.mark.parametrize("shape", [(4, 20, 7, 32), (3, 33, 40, 64), (2, 5, 3, 256), (3, 40, 8, 512),

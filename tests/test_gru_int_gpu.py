@@ -79,6 +79,24 @@ def test_int_storage_forward_bit_exact(cuda, shape, cfg_name, with_h0):
     assert all(ev[k].numel() == 0 for k in GO.MASKS)
 
 
+@pytest.mark.parametrize("cfg_name", ["h-unsigned", "c3"])
+def test_int_storage_clusters_walking_several_tiles(cuda, cfg_name):
+    """B = 160 gives 10 batch tiles; the clustered recurrence rounds its cluster count down to
+    a multiple of 8, so 8 clusters walk the 10 tiles (cluster 0 and 1 take a second tile, with
+    h0 published afresh).  One h plane (8-bit unsigned h) and two (16-bit h)."""
+    T, B, I, H = 4, 160, 7, 32
+    print(f"[gru int fwd multi-tile] B={B} cfg={cfg_name}", flush=True)
+    W, R, bw, br, x, h0, qp = _case(T, B, I, H, cfg_name, 8, True)
+    exp = GO.forward_int(W, R, bw, br, x, qp, h0=h0, training=True)
+    got = dict(zip(("h", "v") + CODES + GO.MASKS, _gpu_int(cuda, W, R, bw, br, x, h0, qp, True)))
+    for k in CODES:
+        np.testing.assert_array_equal(got[k].cpu().numpy(), exp[k], err_msg=k)
+    for k in GO.MASKS:
+        np.testing.assert_array_equal(got[k].cpu().numpy(), exp[k], err_msg=k)
+    np.testing.assert_array_equal(got["h"].cpu().numpy(), _dequant(exp["h_q"], qp, "h"))
+    np.testing.assert_array_equal(got["v"].cpu().numpy(), _v_dequant(exp["v_q"], qp, H))
+
+
 @pytest.mark.parametrize("shape", [(5, 20, 7, 32), (3, 33, 300, 64), (4, 7, 5, 33)],
                          ids=str)
 @pytest.mark.parametrize("cfg_name", ["8b-asym", "c3", "16b-all", "c5"])

@@ -1,10 +1,11 @@
 """GPU parity of the QuantLSTM kernels against the pinned oracle (oracle/lstm_oracle.c).
 
 Bar: the quantised forward (dequantised outputs, saved masters, checkpoints and clamp masks)
-is bit-exact with the oracle run in its correctly-rounded activation mode (exp/tanh in double,
-rounded to float: the GPU's activations); backward gradients within 1e-4 relative of the
-oracle's fp64 sums; calibration statistics within float rounding of the oracle's (the float
-forward's summation order differs).
+is bit-exact with the oracle run in its reference activation mode (ACT_LIBM: the C library's
+expf / tanhf, as the reference CPU core compiled into oracle/_ref; the kernels evaluate in double
+and take the reference's result at the few codes where the output code differs); backward
+gradients within 1e-4 relative of the oracle's fp64 sums; calibration statistics (a float
+forward, activations in double on the GPU) within float rounding of the oracle's.
 """
 import numpy as np
 import pytest
@@ -166,7 +167,7 @@ def test_forward_quant_bit_exact(cuda, cfg_name, shape, with_state):
     T, B, I, H = shape
     args, _, p = _case(T, B, I, H, cfg_name, 11, True, with_state)
     Wi, Wh, bi, bh, x, h0, c0 = args
-    o = O.forward_quant(Wi, Wh, bi, bh, x, p, h0, c0, mode=O.ACT_CR)
+    o = O.forward_quant(Wi, Wh, bi, bh, x, p, h0, c0, mode=O.ACT_LIBM_EXACT)
     out, hn, cn, saved = _gpu_forward(cuda, args, p, True)
     _compare_forward(o, out, hn, cn, saved, True)
     # inference (no checkpoints) gives the same outputs
@@ -180,7 +181,7 @@ def test_forward_quant_without_bias(cuda, cfg_name):
     T, B, I, H = 4, 17, 9, 32
     args, _, p = _case(T, B, I, H, cfg_name, 13, False, True)
     Wi, Wh, bi, bh, x, h0, c0 = args
-    o = O.forward_quant(Wi, Wh, bi, bh, x, p, h0, c0, mode=O.ACT_CR)
+    o = O.forward_quant(Wi, Wh, bi, bh, x, p, h0, c0, mode=O.ACT_LIBM_EXACT)
     out, hn, cn, saved = _gpu_forward(cuda, args, p, True)
     _compare_forward(o, out, hn, cn, saved, False)
 
@@ -190,7 +191,7 @@ def test_forward_quant_c4_hidden_512(cuda):
     T, B, I, H = 3, 20, 64, 512
     args, _, p = _case(T, B, I, H, "c4", 17, True, False)
     Wi, Wh, bi, bh, x, h0, c0 = args
-    o = O.forward_quant(Wi, Wh, bi, bh, x, p, h0, c0, mode=O.ACT_CR)
+    o = O.forward_quant(Wi, Wh, bi, bh, x, p, h0, c0, mode=O.ACT_LIBM_EXACT)
     out, hn, cn, saved = _gpu_forward(cuda, args, p, True)
     _compare_forward(o, out, hn, cn, saved, True)
 
@@ -201,7 +202,7 @@ def test_forward_saturating_inputs_set_masks(cuda):
     Wi, Wh, bi, bh, x, h0, c0 = args
     x = (x * 4).astype(f32)  # beyond the calibrated range: input clamps
     h0 = (h0 * 10).astype(f32)
-    o = O.forward_quant(Wi, Wh, bi, bh, x, p, h0, c0, mode=O.ACT_CR)
+    o = O.forward_quant(Wi, Wh, bi, bh, x, p, h0, c0, mode=O.ACT_LIBM_EXACT)
     assert o["x_m"].any() and o["h0_m"].any()
     out, hn, cn, saved = _gpu_forward(cuda, (Wi, Wh, bi, bh, x, h0, c0), p, True)
     _compare_forward(o, out, hn, cn, saved, True)
@@ -239,7 +240,7 @@ def test_backward_matches_oracle(cuda, cfg_name, shape, with_state):
     T, B, I, H = shape
     args, _, p = _case(T, B, I, H, cfg_name, 21, True, with_state)
     Wi, Wh, bi, bh, x, h0, c0 = args
-    o = O.forward_quant(Wi, Wh, bi, bh, x, p, h0, c0, mode=O.ACT_CR)
+    o = O.forward_quant(Wi, Wh, bi, bh, x, p, h0, c0, mode=O.ACT_LIBM_EXACT)
     _, _, _, saved = _gpu_forward(cuda, args, p, True)
     go, gh, gc = _grads(T, B, H, 22)
     exp = O.backward_quant(o, p, go, gh, gc)
@@ -251,7 +252,7 @@ def test_backward_without_bias_and_final_state_grads(cuda):
     T, B, I, H = 4, 18, 10, 32
     args, _, p = _case(T, B, I, H, "c4", 23, False, True)
     Wi, Wh, bi, bh, x, h0, c0 = args
-    o = O.forward_quant(Wi, Wh, bi, bh, x, p, h0, c0, mode=O.ACT_CR)
+    o = O.forward_quant(Wi, Wh, bi, bh, x, p, h0, c0, mode=O.ACT_LIBM_EXACT)
     _, _, _, saved = _gpu_forward(cuda, args, p, True)
     go, _, _ = _grads(T, B, H, 24)
     exp = O.backward_quant(o, p, go)
@@ -263,7 +264,7 @@ def test_backward_c4_hidden_512(cuda):
     T, B, I, H = 3, 20, 64, 512
     args, _, p = _case(T, B, I, H, "c4", 25, True, True)
     Wi, Wh, bi, bh, x, h0, c0 = args
-    o = O.forward_quant(Wi, Wh, bi, bh, x, p, h0, c0, mode=O.ACT_CR)
+    o = O.forward_quant(Wi, Wh, bi, bh, x, p, h0, c0, mode=O.ACT_LIBM_EXACT)
     _, _, _, saved = _gpu_forward(cuda, args, p, True)
     go, gh, gc = _grads(T, B, H, 26)
     exp = O.backward_quant(o, p, go, gh, gc)
@@ -313,7 +314,7 @@ def test_any_hidden_size_forward_backward_match_oracle(cuda, H, cfg_name):
     print(f"[lstm any H] H={H} cfg={cfg_name}", flush=True)
     args, _, p = _case(T, B, I, H, cfg_name, 41, True, True)
     Wi, Wh, bi, bh, x, h0, c0 = args
-    o = O.forward_quant(Wi, Wh, bi, bh, x, p, h0, c0, mode=O.ACT_CR)
+    o = O.forward_quant(Wi, Wh, bi, bh, x, p, h0, c0, mode=O.ACT_LIBM_EXACT)
     out, hn, cn, saved = _gpu_forward(cuda, args, p, True)
     _compare_forward(o, out, hn, cn, saved, True)
     go, gh, gc = _grads(T, B, H, 42)
@@ -341,7 +342,7 @@ def test_wide_recurrent_weights_forward_backward_match_oracle(cuda, shape, cfg_n
     print(f"[lstm wide W_hh] shape={shape} cfg={cfg_name}", flush=True)
     args, _, p = _case(T, B, I, H, cfg_name, 51, True, True)
     Wi, Wh, bi, bh, x, h0, c0 = args
-    o = O.forward_quant(Wi, Wh, bi, bh, x, p, h0, c0, mode=O.ACT_CR)
+    o = O.forward_quant(Wi, Wh, bi, bh, x, p, h0, c0, mode=O.ACT_LIBM_EXACT)
     out, hn, cn, saved = _gpu_forward(cuda, args, p, True)
     _compare_forward(o, out, hn, cn, saved, True)
     go, gh, gc = _grads(T, B, H, 52)
@@ -360,7 +361,7 @@ def test_hidden_above_512_and_forced_stepped_match_oracle(cuda, shape, cfg_name,
     print(f"[lstm stepped] shape={shape} cfg={cfg_name}", flush=True)
     args, _, p = _case(T, B, I, H, cfg_name, 53, True, True)
     Wi, Wh, bi, bh, x, h0, c0 = args
-    o = O.forward_quant(Wi, Wh, bi, bh, x, p, h0, c0, mode=O.ACT_CR)
+    o = O.forward_quant(Wi, Wh, bi, bh, x, p, h0, c0, mode=O.ACT_LIBM_EXACT)
     go, gh, gc = _grads(T, B, H, 54)
     exp = O.backward_quant(o, p, go, gh, gc)
     monkeypatch.setenv("RXMET_LSTM_STEPPED", "1")
@@ -380,7 +381,7 @@ def test_clustered_recurrence_matches_oracle_and_single_tile_path(cuda, shape, c
     args, _, p = _case(T, B, I, H, cfg_name, 41, True, True)
     Wi, Wh, bi, bh, x, h0, c0 = args
     out, hn, cn, saved = _gpu_forward(cuda, args, p, True)
-    o = O.forward_quant(Wi, Wh, bi, bh, x, p, h0, c0, mode=O.ACT_CR)
+    o = O.forward_quant(Wi, Wh, bi, bh, x, p, h0, c0, mode=O.ACT_LIBM_EXACT)
     _compare_forward(o, out, hn, cn, saved, True)
     monkeypatch.setenv("RXMET_NO_CLUSTER", "1")
     out2, hn2, cn2, saved2 = _gpu_forward(cuda, args, p, True)
@@ -402,7 +403,7 @@ def test_clustered_backward_matches_oracle_and_single_tile_path(cuda, shape, cfg
     T, B, I, H = shape
     args, _, p = _case(T, B, I, H, cfg_name, 43, True, True)
     Wi, Wh, bi, bh, x, h0, c0 = args
-    o = O.forward_quant(Wi, Wh, bi, bh, x, p, h0, c0, mode=O.ACT_CR)
+    o = O.forward_quant(Wi, Wh, bi, bh, x, p, h0, c0, mode=O.ACT_LIBM_EXACT)
     _, _, _, saved = _gpu_forward(cuda, args, p, True)
     go, gh, gc = _grads(T, B, H, 44)
     exp = O.backward_quant(o, p, go, gh, gc)

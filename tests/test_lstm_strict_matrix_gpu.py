@@ -6,8 +6,8 @@ GPU: each case's resolved operator config (all-int8, all-int16 and mixed 8/16 pr
 16x128x64x128), bias, layout and initial-state profile; calibrated on the GPU, then one QAT
 forward and backward.
 
-Bars: output, h_n and c_n bit-exact against the oracle (its GPU-semantics activation mode) with
-the module's own grids; every gradient within 1e-4 relative.  The reference gates these cases
+Bars: output, h_n and c_n bit-exact against the oracle in its reference activation mode (the C
+library's expf / tanhf of the reference CPU core) with the module's own grids; every gradient within 1e-4 relative.  The reference gates these cases
 against a float LSTM with MSE / MAE / cosine thresholds; the oracle comparison is stricter."""
 import json
 from pathlib import Path
@@ -75,7 +75,7 @@ def test_strict_matrix_case_matches_oracle(cuda, case):
     p = m._params[0].struct
     h0 = None if st is None else st[0][0].numpy()
     c0 = None if st is None else st[1][0].numpy()
-    o = O.forward_quant(Wi, Wh, bi, bh, xt.numpy(), p, h0, c0, mode=O.ACT_CR)
+    o = O.forward_quant(Wi, Wh, bi, bh, xt.numpy(), p, h0, c0, mode=O.ACT_LIBM_EXACT)
     out_tm = _np(out.transpose(0, 1) if bf else out)
     np.testing.assert_array_equal(out_tm, o["output"], err_msg="output")
     np.testing.assert_array_equal(_np(hn[0]), o["h_n"], err_msg="h_n")

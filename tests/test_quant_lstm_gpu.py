@@ -77,7 +77,7 @@ def test_module_qat_matches_oracle(cuda, bidirectional, batch_first, with_state,
         h0 = _np(hx[0][d]) if hx is not None else None
         c0 = _np(hx[1][d]) if hx is not None else None
         p = m._params[d].struct
-        o = O.forward_quant(Wi, Wh, bi, bh, xd, p, h0, c0, mode=O.ACT_CR)
+        o = O.forward_quant(Wi, Wh, bi, bh, xd, p, h0, c0, mode=O.ACT_LIBM_EXACT)
         od = out_tm[..., d * H:(d + 1) * H]
         np.testing.assert_array_equal(od[::-1] if d == 1 else od, o["output"])
         np.testing.assert_array_equal(_np(hn[d]), o["h_n"])
