@@ -13,7 +13,9 @@ Prints ONE JSON line.  Legs (all run by default):
 * c5   — QuantGRU unidirectional QAT forward+backward at B=1024, T=50, I=256, H=1024 (4-bit
          weights, 16-bit activations and h, power-of-2 scales): seq/s;
 * gint — the c3 model on the int32 carrier, PTQ inference of both directions (the work the
-         reference's CPU int carrier does, timed by the c3 CPU baseline), float and int-IO: seq/s.
+         reference's CPU int carrier does, timed by the c3 CPU baseline), float and int-IO: seq/s;
+* lstmpub — the reference's published QuantLSTM inference profiles ([50, 64, 128, 256] and
+         [16, 128, 64, 128], cuda-performance.md), P50 / P95 over 200 calls, beside its numbers.
 
 The roofline object describes the dominant kernel of the headline leg, timed with
 hipEvents that the library records around its own launches on the stream they run on
@@ -121,7 +123,7 @@ def _qdq_leg(torch, steps: int, warmup: int, validate: bool = True):
         torch.cuda.synchronize()
         dt = (time.perf_counter() - t0) / steps
         gbs = (8 + 12) * n / dt / 1e9
-        results[name] = {"ms_per_step": dt * 1e3, "GB_s": gbs}
+        results[name] = {"ms_per_step": dt * 1e3, "GB_s": gbs, "frac": gbs / HBM_PEAK_GBS}
         _log(f"qdq {name}: {dt*1e3:.3f} ms/step fwd+bwd, {gbs:.0f} GB/s algorithmic")
 
     # Per-kernel timing of the dominant kernel (fused backward, 12 B/element) and the
@@ -160,6 +162,30 @@ def _qdq_leg(torch, steps: int, warmup: int, validate: bool = True):
 
     t_f = ev_time(fwd, max(steps, 20))
     t_b = ev_time(bwd, max(steps, 20))
+    # calibration min / max (the observer's pass, 4 B/element read) per tensor and per channel
+    ws1 = torch.empty(rxmet_lib.load().rxmet_qdq_workspace_bytes(1, 1, n), dtype=torch.uint8,
+                      device=dev)
+    ws2 = torch.empty_like(ws)
+    mn_out, mx_out = torch.empty(R, device=dev), torch.empty(R, device=dev)
+    for nm, C_, inner_, w_ in (("kernel_minmax_per_tensor", 1, n, ws1),
+                               ("kernel_minmax_per_channel", R, Cc, ws2)):
+        t_m = ev_time(lambda: rxmet_lib.call("rxmet_qdq_minmax", x.data_ptr(), 1, C_, inner_,
+                                             mn_out.data_ptr(), mx_out.data_ptr(),
+                                             w_.data_ptr(), sh),
+                      max(steps, 20))
+        results[nm] = {"us": t_m * 1e6, "GB_s": 4 * n / t_m / 1e9,
+                       "frac": 4 * n / t_m / 1e9 / HBM_PEAK_GBS}
+    # the practical ceiling: a plain elementwise pass over the same tensor (read + write)
+    y_copy = torch.empty_like(x)
+    t_c = ev_time(lambda: torch.neg(x, out=y_copy), max(steps, 20))
+    del y_copy, ws1, ws2
+    results["copy_ceiling"] = {"us": t_c * 1e6, "GB_s": 8 * n / t_c / 1e9,
+                               "frac": 8 * n / t_c / 1e9 / HBM_PEAK_GBS,
+                               "what": "torch.neg over the [8192, 8192] fp32 tensor (read x, "
+                                       "write y): the bandwidth a plain streaming pass reaches"}
+    _log(f"qdq min/max: per tensor {results['kernel_minmax_per_tensor']['GB_s']:.0f} GB/s, "
+         f"per channel {results['kernel_minmax_per_channel']['GB_s']:.0f} GB/s; copy ceiling "
+         f"{results['copy_ceiling']['GB_s']:.0f} GB/s")
     results["kernel_fwd"] = {"us": t_f * 1e6, "GB_s": 8 * n / t_f / 1e9}
     results["kernel_bwd"] = {"us": t_b * 1e6, "GB_s": 12 * n / t_b / 1e9}
     _log(f"qdq kernels: fwd {t_f*1e6:.1f} us ({8*n/t_f/1e9:.0f} GB/s), "
@@ -642,6 +668,100 @@ def _lstm_leg(torch, steps: int, warmup: int):
     return res, roof, m, x, g
 
 
+# The reference's only published numbers for this path: QuantLSTM CUDA FP32 q-carrier forward
+# inference, timed from input quantisation to the dequantised final state with the static
+# parameters cached (operators/quant-lstm/docs/cuda-performance.md:45-50; profiles and floors in
+# tests/benchmarks/config/cuda_performance_thresholds_v1.json:24-58), on an NVIDIA RTX 6000D:
+# (case id of the reference's strict matrix, profile, P50 ms, P95 ms, seq/s).
+PUBLISHED_LSTM = [
+    ("stage4_basic_cuda_fp32_pedantic_int8_bias_time", "cuda_gru_basic / pedantic",
+     1.283040, 1.290176, 49882),
+    ("stage4_basic_cuda_fp32_tf32_int16_no_bias_batch", "cuda_gru_basic / tf32",
+     1.036768, 1.039744, 61730),
+    ("stage4_performance_cuda_fp32_large_batch_pedantic", "large_batch / pedantic",
+     0.416640, 0.419936, 307220),
+    ("stage4_performance_cuda_fp32_large_batch_tf32", "large_batch / tf32",
+     0.324608, 0.333952, 394322),
+]
+
+
+def _lstm_published_leg(torch, iters: int = 200, warmup: int = 20):
+    """The reference's published QuantLSTM inference profiles: each case's resolved operator
+    config (tests/golden/lstm/strict_matrix_cuda_cases.json, the reference's strict matrix) on
+    its shape [T, B, I, H], calibrated on synthetic U(-1, 1) input, then the quantised forward
+    (no checkpoints) called through the C ABI on time-major device buffers, as the reference's
+    benchmark calls its C++ core.  Per-call hipEvents on the launch stream, P50 / P95 over
+    ``iters`` calls after ``warmup``; seq/s = B / P50.  The weights are quantised inside every
+    timed call (the reference caches them: its timed region is smaller).  Every case runs the
+    exact arithmetic: its tf32 rows are the reference's faster, approximate math mode."""
+    import ctypes
+
+    import lstm_ops
+    import quant_lstm as QL
+    import rxmet_lib
+
+    dev = torch.device("cuda:0")
+    doc = json.loads((ROOT / "tests" / "golden" / "lstm" / "strict_matrix_cuda_cases.json").read_text())
+    cases = {c["case_id"]: c for c in doc["cases"]}
+    lib = rxmet_lib.load()
+    stream = torch.cuda.current_stream(dev)
+    out = {}
+    for case_id, profile, ref_p50, ref_p95, ref_sps in PUBLISHED_LSTM:
+        c = cases[case_id]
+        T, B, I, H = c["shape"]
+        bias = c["bias_profile"] != "disabled"
+        torch.manual_seed(doc["parameter_seeds"][c["shape_profile"]])
+        m = QL.QuantLSTM(I, H, bias=bias, quant_config=c["resolved_quant_config"]).to(dev)
+        g = torch.Generator().manual_seed(1001)
+        x = (torch.rand((T, B, I), generator=g) * 2 - 1).to(dev)
+        m.calibrating = True
+        with torch.no_grad():
+            m(x)
+        m.calibrating = False
+        m.finalize_calibration()
+        m.use_quantization = True
+        m.eval()
+        Wi, Wh, bi, bh = m._direction_params(False)
+        prm = m._params[0].struct
+        y = torch.empty((T, B, H), device=dev)
+        hn = torch.empty((B, H), device=dev)
+        cn = torch.empty((B, H), device=dev)
+        ws = torch.empty(int(lib.rxmet_lstm_forward_workspace_bytes(T, B, I, H)), dtype=torch.uint8,
+                         device=dev)
+        ptr = lambda t: None if t is None else ctypes.c_void_p(t.data_ptr())
+        args = (T, B, I, H, ptr(Wi), ptr(Wh), ptr(bi), ptr(bh), ptr(x), None, None,
+                ctypes.byref(prm), ptr(y), ptr(hn), ptr(cn), None, ptr(ws),
+                ctypes.c_void_p(stream.cuda_stream))
+
+        def call():
+            rxmet_lib.call("rxmet_lstm_forward_quant", *args)
+
+        with torch.no_grad():
+            ref_out, _ = m(x)
+        for _ in range(warmup):
+            call()
+        torch.cuda.synchronize()
+        if not torch.equal(y, ref_out):
+            raise ValidationError(f"lstm published {case_id}: C-ABI forward differs from the module")
+        evs = [torch.cuda.Event(enable_timing=True) for _ in range(iters + 1)]
+        evs[0].record(stream)
+        for i in range(iters):
+            call()
+            evs[i + 1].record(stream)
+        torch.cuda.synchronize()
+        per = sorted(evs[i].elapsed_time(evs[i + 1]) for i in range(iters))
+        p50, p95 = per[len(per) // 2], per[min(len(per) - 1, int(0.95 * len(per)))]
+        out[case_id] = {"profile": profile, "shape_TBIH": [T, B, I, H],
+                        "bits": c["bitwidth_profile"], "p50_ms": round(p50, 4),
+                        "p95_ms": round(p95, 4), "seq_per_s": round(B / (p50 * 1e-3), 1),
+                        "reference_p50_ms": ref_p50, "reference_p95_ms": ref_p95,
+                        "reference_seq_per_s": ref_sps,
+                        "speedup_p50": round(ref_p50 / p50, 3)}
+        _log(f"lstm published {profile} {c['shape']}: P50 {p50:.4f} ms P95 {p95:.4f} ms "
+             f"{B / (p50 * 1e-3):.0f} seq/s (reference RTX 6000D {ref_sps} seq/s)")
+    return out
+
+
 def _validate_lstm(torch, m, x, g, rows):
     """One more step of the benchmarked module: outputs and every gradient finite, the sampled
     sequences' output (bit-exact) and dx (1e-4) equal to the oracle's."""
@@ -885,8 +1005,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-validate", action="store_true",
                     help="skip the oracle comparison of the benchmarked outputs (profiling runs)")
-    ap.add_argument("--legs", default="gru,lstm,qdq,c1,c5,gint",
-                    help="comma-separated subset of gru,lstm,qdq,c1,c5,gint")
+    ap.add_argument("--legs", default="gru,lstm,qdq,c1,c5,gint,lstmpub",
+                    help="comma-separated subset of gru,lstm,qdq,c1,c5,gint,lstmpub")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run a plain elementwise copy over MIB MiB (scales HBM byte "
                          "counters in profiling runs)")
@@ -906,6 +1026,7 @@ def main() -> int:
     validate = not args.no_validate
     checks = {}
     gru = roof = lstm = lstm_roof = qdq = qdq_roof = c5 = c1 = gint = gint_roof = None
+    lstmpub = None
     try:
         if "gru" in legs:
             gru, roof, m, x = _gru_leg(torch, args.steps, args.warmup)
@@ -930,6 +1051,8 @@ def main() -> int:
             if validate:
                 checks["gint"] = _validate_gru_int(gm, gx, gout["y"], gout["q"], [0, 255])
                 _log(f"gint validation: {checks['gint']}")
+        if "lstmpub" in legs:
+            lstmpub = _lstm_published_leg(torch)
         if "c5" in legs:
             c5, c5m, c5x = _gru_c5_leg(torch, args.steps, args.warmup)
             if validate:
@@ -984,8 +1107,9 @@ def main() -> int:
         "gru_c5": rnd(c5),
         "gru_int32_c3": rnd(gint),
         "gru_int32_roofline": gint_roof,
-        "qdq": None if qdq is None else {k: {kk: round(vv, 3) for kk, vv in v.items()}
-                                         for k, v in qdq.items()},
+        "lstm_published_inference": lstmpub,
+        "qdq": None if qdq is None else {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv)
+                                             for kk, vv in v.items()} for k, v in qdq.items()},
         "roofline": roof,
         "lstm_roofline": lstm_roof,
         "qdq_roofline": qdq_roof,
@@ -997,7 +1121,25 @@ def main() -> int:
         "validation": checks if validate else None,
     }
     print(json.dumps(line), flush=True)
+    _end_children()
     return 0
+
+
+def _end_children() -> None:
+    """End any child process this run left behind (none is started on purpose), so that the
+    benchmark exits with nothing of its own still running."""
+    try:
+        import psutil
+    except ImportError:
+        return
+    kids = psutil.Process().children(recursive=True)
+    for k in kids:
+        k.terminate()
+    _, alive = psutil.wait_procs(kids, timeout=5)
+    for k in alive:
+        k.kill()
+    if kids:
+        _log(f"ended {len(kids)} leftover child process(es): {[k.pid for k in kids]}")
 
 
 if __name__ == "__main__":

@@ -251,6 +251,33 @@ int rxmet_quantize_backward_ex(const void *x, const void *g, void *dx, float *ds
                                const float *offset, int64_t qmin, int64_t qmax,
                                void *workspace, void *stream);
 
+/*
+ * QuantizeDequantize.forward with learnable min / max (quantizer.py:1048-1082: get_encodings()
+ * then the backend's quantize_dequantize, learnable mode) in one launch each way: the kernels
+ * derive every encoding's scale and offset from min and max as rxmet_qdq_encoding_forward does
+ * (then take them to the internal type), so no scale / offset tensors are made; the backward
+ * folds the encoding gradients straight on to min and max (rxmet_qdq_encoding_backward's rules
+ * applied to the folded, internal-type-rounded gradients of scale and offset).  y, dx, d_min
+ * and d_max equal those of rxmet_qdq_encoding_forward + rxmet_qdq_forward_ex and
+ * rxmet_qdq_backward_ex + rxmet_qdq_encoding_backward bit for bit.  min / max: [C0 * C1] fp32;
+ * d_min / d_max: both or neither (then dx only, no workspace needed).
+ */
+typedef struct rxmet_qdq_minmax_enc {
+  const float *min, *max;
+  int32_t symmetric;  /* offset = sym_offset, else derived from min */
+  float sym_offset;
+  float min_scale;    /* lower clamp of the scale (quantsim's minimum scale) */
+  int32_t reserved;   /* 0 */
+} rxmet_qdq_minmax_enc;
+
+int rxmet_qdq_forward_minmax(const void *x, void *y, const rxmet_qdq_layout *layout,
+                             const rxmet_qdq_numerics *numerics, const rxmet_qdq_minmax_enc *enc,
+                             int64_t qmin, int64_t qmax, void *stream);
+int rxmet_qdq_backward_minmax(const void *x, const void *g, void *dx, float *d_min,
+                              float *d_max, const rxmet_qdq_layout *layout,
+                              const rxmet_qdq_numerics *numerics, const rxmet_qdq_minmax_enc *enc,
+                              int64_t qmin, int64_t qmax, void *workspace, void *stream);
+
 /* dequantize forward / backward (torch_builtins.py:459-488 with DequantizeFunc :574-615). */
 int rxmet_dequantize_forward_ex(const void *q, void *y, const rxmet_qdq_layout *layout,
                                 const rxmet_qdq_numerics *numerics, const float *scale,

@@ -403,9 +403,12 @@ class QuantizeDequantize(nn.Module):
             enc_min = torch.zeros_like(enc_min)
         self.set_range(enc_min, enc_max)
 
-    # True: (scale, offset) from rxmet_qdq_encoding_forward/_backward (one launch each way).
-    # False: the reference's own get_encodings() tensor expressions, i.e. what aimet_torch's
-    # QuantizeDequantize computes before it calls the backend (quantizer.py:466-483, 1060-1082).
+    # True: with this build's backend, the encodings are derived from min / max inside the
+    # quantize-dequantize kernels (rxmet_qdq_forward_minmax / _backward_minmax: one launch each
+    # way plus the gradient fold); elsewhere (scale, offset) come from
+    # rxmet_qdq_encoding_forward/_backward.  False: the reference's own get_encodings() tensor
+    # expressions, i.e. what aimet_torch's QuantizeDequantize computes before it calls the
+    # backend (quantizer.py:466-483, 1060-1082).
     fused_encodings = True
 
     def get_encodings(self) -> Optional[Tuple[torch.Tensor, torch.Tensor]]:
@@ -421,6 +424,14 @@ class QuantizeDequantize(nn.Module):
                 "Failed to run QuantizeDequantize since quantization parameters are not initialized."
                 " Please initialize the quantization parameters using `compute_encodings()`.")
         mn, mx = self.min, self.max
+        if self.fused_encodings and get_backend() is mi355x_qdq:
+            y = mi355x_qdq.quantize_dequantize_minmax(
+                input, mn, mx, self.qmin, self.qmax, self.symmetric,
+                _get_minimum_scale(self.qmax - self.qmin),
+                float(symmetric_offset(self.qmin, self.qmax)), self.block_size,
+                self.zero_point_shift)
+            if y is not None:
+                return y
         if (self.fused_encodings and mn.is_cuda and mn.dtype == torch.float32
                 and mx.dtype == torch.float32 and mn.is_contiguous() and mx.is_contiguous()):
             # get_encodings() in two launches instead of a chain of one-element tensor ops

@@ -20,14 +20,49 @@ namespace rxmet {
 namespace qdq {
 
 // ---------------------------------------------------------------------------------
-// Partial folding: one workgroup per encoding; the partials of encoding c are
-// fold_index(c, p) for p < n0 * n1 * n2.  Each thread folds a fixed, strided subset; the
-// lanes are then combined by a fixed butterfly and the waves in a fixed order.
+// Partial folding.  The partials of encoding c are at base(c) + l0 * s0 + l1 * s1 + l2 * s2
+// for p = (l0 * n1 + l1) * n2 + l2 < n0 * n1 * n2.  Each thread folds a fixed, strided
+// subset of p (kFoldUnroll loads in flight), the lanes are combined by a fixed butterfly and
+// the waves in a fixed order, so results do not depend on timing.  Three shapes:
+//   many partials per encoding (>= 8192): one 1024-thread workgroup per encoding;
+//   (1024 .. 8191): one 256-thread workgroup per encoding;
+//   some (64 .. 1023): one wave per encoding;
+//   few (< 64, e.g. per-channel runs with one chunk per channel): one thread per encoding,
+//   the partials in order.
+// A single strided run of partials (n0 = n1 = 1, every runs decomposition with one
+// encoding group) is indexed without divisions.
 // ---------------------------------------------------------------------------------
-__device__ __forceinline__ int64_t fold_index(const FoldMap &f, int64_t c, int64_t p) {
+constexpr int kFoldUnroll = 8;
+
+__device__ __forceinline__ int64_t fold_base(const FoldMap &f, int64_t c) {
+  return (c / f.C1) * f.sc0 + (c % f.C1) * f.sc1;
+}
+
+__device__ __forceinline__ int64_t fold_offset(const FoldMap &f, int64_t p) {
+  if (f.n0 * f.n1 == 1) return p * f.s2;
   const int64_t l2 = p % f.n2, t = p / f.n2;
   const int64_t l1 = t % f.n1, l0 = t / f.n1;
-  return l0 * f.s0 + l1 * f.s1 + l2 * f.s2 + (c / f.C1) * f.sc0 + (c % f.C1) * f.sc1;
+  return l0 * f.s0 + l1 * f.s1 + l2 * f.s2;
+}
+
+// Thread-strided fold of encoding c's partials from position `first` in steps of `step`.
+template <typename Acc, typename Add>
+__device__ __forceinline__ Acc fold_strided(const Acc *__restrict__ partial, const FoldMap &f,
+                                            int64_t c, int64_t first, int64_t step, Acc a,
+                                            Add add) {
+  const int64_t n = f.n0 * f.n1 * f.n2, base = fold_base(f, c);
+  for (int64_t p0 = first; p0 < n; p0 += kFoldUnroll * step) {
+    Acc v[kFoldUnroll];
+#pragma unroll
+    for (int k = 0; k < kFoldUnroll; ++k) {
+      const int64_t p = p0 + k * step;
+      if (p < n) v[k] = partial[base + fold_offset(f, p)];
+    }
+#pragma unroll
+    for (int k = 0; k < kFoldUnroll; ++k)
+      if (p0 + k * step < n) add(a, v[k]);
+  }
+  return a;
 }
 
 // Rounding of a folded encoding gradient to the internal type (0: fp32, 1: fp16, 2: bf16),
@@ -38,56 +73,129 @@ __device__ __forceinline__ float round_internal(float v, int round16) {
   return v;
 }
 
-template <int NT>
-__global__ __launch_bounds__(NT) void fold_sum(const Sum2 *__restrict__ partial, FoldMap f,
-                                               float *__restrict__ dscale,
-                                               float *__restrict__ doffset, int round16) {
-  __shared__ double red[2][NT / kWave];
-  const int64_t c = blockIdx.x;
-  const int64_t n = f.n0 * f.n1 * f.n2;
-  double a = 0.0, b = 0.0;
-  for (int64_t p = threadIdx.x; p < n; p += NT) {
-    const Sum2 v = partial[fold_index(f, c, p)];
-    a += v.a;
-    b += v.b;
+// Folded encoding gradients, written as the gradients of scale and offset.
+struct PutScaleOffset {
+  float *dscale, *doffset;
+  int round16;
+  __device__ void operator()(const Sum2 &v, int64_t c) const {
+    if (dscale) dscale[c] = round_internal(static_cast<float>(v.a), round16);
+    if (doffset) doffset[c] = round_internal(static_cast<float>(v.b), round16);
   }
-  a = wave_sum(a);
-  b = wave_sum(b);
-  if (NT > kWave) {
-    if (threadIdx.x % kWave == 0) {
-      red[0][threadIdx.x / kWave] = a;
-      red[1][threadIdx.x / kWave] = b;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0)
-      for (int w = 1; w < NT / kWave; ++w) {
-        a += red[0][w];
-        b += red[1][w];
-      }
+};
+
+// Folded encoding gradients taken on to the min / max they were derived from.
+struct PutMinMaxGrad {
+  MinMaxSrc mm;
+  float *d_min, *d_max;
+  int round16;
+  __device__ void operator()(const Sum2 &v, int64_t c) const {
+    const float gs = round_internal(static_cast<float>(v.a), round16);
+    const float go = round_internal(static_cast<float>(v.b), round16);
+    float a, b;
+    minmax_encoding_grad(mm, c, gs, &go, a, b);
+    d_min[c] = a;
+    d_max[c] = b;
   }
-  if (threadIdx.x == 0) {
-    if (dscale) dscale[c] = round_internal(static_cast<float>(a), round16);
-    if (doffset) doffset[c] = round_internal(static_cast<float>(b), round16);
-  }
+};
+
+__device__ __forceinline__ void put_minmax(const MinMax &v, int64_t c, float *out_min,
+                                           float *out_max) {
+  out_min[c] = v.mn;
+  out_max[c] = v.mx;
 }
 
-__global__ __launch_bounds__(kWave) void fold_minmax(const MinMax *__restrict__ partial,
-                                                     FoldMap f, float *__restrict__ out_min,
-                                                     float *__restrict__ out_max) {
+struct AddSum {
+  __device__ void operator()(Sum2 &a, const Sum2 &v) const { acc_add(a, v); }
+};
+struct AddMinMax {
+  __device__ void operator()(MinMax &a, const MinMax &v) const { acc_add(a, v); }
+};
+
+// NT threads per encoding (a wave or a workgroup).
+template <int NT, typename Acc, typename Add, typename Put>
+__device__ __forceinline__ void fold_block(const Acc *__restrict__ partial, const FoldMap &f,
+                                           Acc zero, Add add, Put put) {
+  __shared__ Acc red[NT / kWave];
   const int64_t c = blockIdx.x;
+  Acc a = fold_strided(partial, f, c, threadIdx.x, NT, zero, add);
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) add(a, acc_shfl(a, off));
+  if (NT > kWave) {
+    if (threadIdx.x % kWave == 0) red[threadIdx.x / kWave] = a;
+    __syncthreads();
+    if (threadIdx.x == 0)
+      for (int w = 1; w < NT / kWave; ++w) add(a, red[w]);
+  }
+  if (threadIdx.x == 0) put(a, c);
+}
+
+template <int NT, typename Put>
+__global__ __launch_bounds__(NT) void fold_sum(const Sum2 *__restrict__ partial, FoldMap f,
+                                               Put put) {
+  fold_block<NT>(partial, f, Sum2{0.0, 0.0}, AddSum{}, put);
+}
+
+template <int NT>
+__global__ __launch_bounds__(NT) void fold_minmax(const MinMax *__restrict__ partial, FoldMap f,
+                                                  float *__restrict__ out_min,
+                                                  float *__restrict__ out_max) {
+  fold_block<NT>(partial, f, MinMax{INFINITY, -INFINITY}, AddMinMax{},
+                 [&](const MinMax &v, int64_t c) { put_minmax(v, c, out_min, out_max); });
+}
+
+// One thread per encoding, its partials in order.
+template <typename Put>
+__global__ __launch_bounds__(256) void fold_sum_thread(const Sum2 *__restrict__ partial,
+                                                       FoldMap f, int64_t C, Put put) {
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (c >= C) return;
+  put(fold_strided(partial, f, c, 0, 1, Sum2{0.0, 0.0}, AddSum{}), c);
+}
+
+__global__ __launch_bounds__(256) void fold_minmax_thread(const MinMax *__restrict__ partial,
+                                                          FoldMap f, int64_t C,
+                                                          float *__restrict__ out_min,
+                                                          float *__restrict__ out_max) {
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (c >= C) return;
+  put_minmax(fold_strided(partial, f, c, 0, 1, MinMax{INFINITY, -INFINITY}, AddMinMax{}), c,
+             out_min, out_max);
+}
+
+// Launch the fold of C encodings' partials with the shape their count calls for.
+template <typename Put>
+static void launch_fold_sum(const Sum2 *ws, const FoldMap &f, int64_t C, Put put,
+                            hipStream_t s) {
   const int64_t n = f.n0 * f.n1 * f.n2;
-  float mn = INFINITY, mx = -INFINITY;
-  for (int64_t p = threadIdx.x; p < n; p += kWave) {
-    const MinMax v = partial[fold_index(f, c, p)];
-    mn = nan_min(mn, v.mn);
-    mx = nan_max(mx, v.mx);
-  }
-  mn = wave_min(mn);
-  mx = wave_max(mx);
-  if (threadIdx.x == 0) {
-    out_min[c] = mn;
-    out_max[c] = mx;
-  }
+  if (n >= 8192)
+    hipLaunchKernelGGL((fold_sum<16 * kWave, Put>), dim3(static_cast<unsigned>(C)),
+                       dim3(16 * kWave), 0, s, ws, f, put);
+  else if (n >= 1024)
+    hipLaunchKernelGGL((fold_sum<4 * kWave, Put>), dim3(static_cast<unsigned>(C)),
+                       dim3(4 * kWave), 0, s, ws, f, put);
+  else if (n >= 64)
+    hipLaunchKernelGGL((fold_sum<kWave, Put>), dim3(static_cast<unsigned>(C)), dim3(kWave), 0, s,
+                       ws, f, put);
+  else
+    hipLaunchKernelGGL((fold_sum_thread<Put>), dim3(static_cast<unsigned>((C + 255) / 256)),
+                       dim3(256), 0, s, ws, f, C, put);
+}
+
+static void launch_fold_minmax(const MinMax *ws, const FoldMap &f, int64_t C, float *out_min,
+                               float *out_max, hipStream_t s) {
+  const int64_t n = f.n0 * f.n1 * f.n2;
+  if (n >= 8192)
+    hipLaunchKernelGGL(fold_minmax<16 * kWave>, dim3(static_cast<unsigned>(C)), dim3(16 * kWave),
+                       0, s, ws, f, out_min, out_max);
+  else if (n >= 1024)
+    hipLaunchKernelGGL(fold_minmax<4 * kWave>, dim3(static_cast<unsigned>(C)), dim3(4 * kWave), 0,
+                       s, ws, f, out_min, out_max);
+  else if (n >= 64)
+    hipLaunchKernelGGL(fold_minmax<kWave>, dim3(static_cast<unsigned>(C)), dim3(kWave), 0, s, ws,
+                       f, out_min, out_max);
+  else
+    hipLaunchKernelGGL(fold_minmax_thread, dim3(static_cast<unsigned>((C + 255) / 256)), dim3(256),
+                       0, s, ws, f, C, out_min, out_max);
 }
 
 __global__ __launch_bounds__(256) void zero_enc_grads(int64_t C, float *dscale, float *doffset) {
@@ -104,7 +212,7 @@ __global__ __launch_bounds__(256) void zero_enc_grads(int64_t C, float *dscale, 
 // Normalize a [outer, C0, mid, C1, inner] layout (one encoding group -> C0 = outer = 1;
 // one encoding -> a single run) and choose the decomposition.
 static Plan make_plan(int64_t outer, int64_t C0, int64_t mid, int64_t C1, int64_t inner,
-                      int esize) {
+                      int esize, int vec) {
   Plan p;
   p.esize = esize;
   if (C0 == 1) {
@@ -134,7 +242,7 @@ static Plan make_plan(int64_t outer, int64_t C0, int64_t mid, int64_t C1, int64_
   p.n = outer * C0 * mid * C1 * inner;
   p.runs = outer * C0 * mid * C1;
   p.geo = Geo{inner, C1, mid * C1, C0};
-  const int64_t chunk = int64_t(kThreads) * kVecPerThread * (16 / esize);
+  const int64_t chunk = int64_t(kThreads) * vec * (16 / esize);
   if ((C0 == 1 && C1 == 1) || inner >= kMinRun) {
     p.kind = KIND_RUNS;
     p.splits = inner > 0 ? (inner + chunk - 1) / chunk : 1;
@@ -226,8 +334,8 @@ static int check_numerics(int op, const rxmet_qdq_numerics &nm) {
 }
 
 static Params make_params(int64_t qmin, int64_t qmax, const rxmet_qdq_numerics &nm) {
-  return Params{static_cast<double>(qmin), static_cast<double>(qmax),
-                static_cast<float>(nm.zero_point_shift), nm.scalar_scale ? 1 : 0};
+  return Params{static_cast<double>(qmin), static_cast<double>(qmax), nm.zero_point_shift,
+                nm.scalar_scale ? 1 : 0};
 }
 
 static int dispatch(const Call &c, int32_t io, int what) {
@@ -245,45 +353,54 @@ static int dispatch(const Call &c, int32_t io, int what) {
 
 static int forward_impl(int op, const void *x, void *y, const rxmet_qdq_layout *l,
                         const rxmet_qdq_numerics *nm, const float *scale, const float *offset,
-                        int64_t qmin, int64_t qmax, void *stream) {
+                        int64_t qmin, int64_t qmax, void *stream,
+                        const MinMaxSrc *mm = nullptr) {
   RXMET_CHECK_ARG(l != nullptr && nm != nullptr, "layout and numerics must be non-null");
   if (int rc = check_layout(l->outer, l->C0, l->mid, l->C1, l->inner)) return rc;
   if (int rc = check_numerics(op, *nm)) return rc;
   if (op != OP_DQ)
     if (int rc = check_grid(qmin, qmax, arithmetic_type(op, *nm))) return rc;
-  RXMET_CHECK_ARG(scale != nullptr, "scale must be non-null");
-  const Plan p = make_plan(l->outer, l->C0, l->mid, l->C1, l->inner, esize_of(nm->io_dtype));
+  RXMET_CHECK_ARG(scale != nullptr || mm != nullptr, "scale must be non-null");
+  const Plan p =
+      make_plan(l->outer, l->C0, l->mid, l->C1, l->inner, esize_of(nm->io_dtype), kVecQdq);
   if (p.n == 0) return 0;
   RXMET_CHECK_ARG(x != nullptr && y != nullptr, "input/output must be non-null");
   hipStream_t s = static_cast<hipStream_t>(stream);
   const Call c{&p, op, nm->internal_dtype, x, nullptr, y, scale, offset,
-               make_params(qmin, qmax, *nm), nullptr, s};
+               make_params(qmin, qmax, *nm), nullptr, s, mm ? *mm : MinMaxSrc{}};
   rxmet::prof::Scope ps__("qdq_forward_stream", s);
   return dispatch(c, nm->io_dtype, WHAT_FORWARD);
 }
 
+// With mm (encodings derived from min / max in the kernels), d_min / d_max receive the
+// gradients of min and max instead of dscale / doffset receiving those of scale and offset.
 static int backward_impl(int op, const void *x, const void *g, void *dx, float *dscale,
                          float *doffset, const rxmet_qdq_layout *l, const rxmet_qdq_numerics *nm,
                          const float *scale, const float *offset, int64_t qmin, int64_t qmax,
-                         void *workspace, void *stream) {
+                         void *workspace, void *stream, const MinMaxSrc *mm = nullptr,
+                         float *d_min = nullptr, float *d_max = nullptr) {
   RXMET_CHECK_ARG(l != nullptr && nm != nullptr, "layout and numerics must be non-null");
   if (int rc = check_layout(l->outer, l->C0, l->mid, l->C1, l->inner)) return rc;
   if (int rc = check_numerics(op, *nm)) return rc;
   if (op != OP_DQ)
     if (int rc = check_grid(qmin, qmax, arithmetic_type(op, *nm))) return rc;
-  RXMET_CHECK_ARG(scale != nullptr, "scale must be non-null");
+  RXMET_CHECK_ARG(scale != nullptr || mm != nullptr, "scale must be non-null");
   if (op == OP_QDQ_FROZEN)
     RXMET_CHECK_ARG(dscale == nullptr && doffset == nullptr,
                     "frozen encodings have no encoding gradients");
-  const Plan p = make_plan(l->outer, l->C0, l->mid, l->C1, l->inner, esize_of(nm->io_dtype));
-  const bool enc = dscale != nullptr || doffset != nullptr;
+  if (mm != nullptr)
+    RXMET_CHECK_ARG(dscale == nullptr && doffset == nullptr && (d_min == nullptr) == (d_max == nullptr),
+                    "min/max encodings give d_min and d_max together");
+  const Plan p =
+      make_plan(l->outer, l->C0, l->mid, l->C1, l->inner, esize_of(nm->io_dtype), kVecQdq);
+  const bool enc = dscale != nullptr || doffset != nullptr || d_min != nullptr;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t C = l->C0 * l->C1;
   if (p.n == 0) {
     // zeroed by a kernel, not a memset node, so a captured training step replays correctly
     if (enc) {
       hipLaunchKernelGGL(zero_enc_grads, dim3(static_cast<unsigned>((C + 255) / 256)), dim3(256),
-                         0, s, C, dscale, doffset);
+                         0, s, C, d_min ? d_min : dscale, d_min ? d_max : doffset);
       RXMET_CHECK_LAUNCH();
     }
     return 0;
@@ -291,7 +408,8 @@ static int backward_impl(int op, const void *x, const void *g, void *dx, float *
   RXMET_CHECK_ARG(x != nullptr && g != nullptr && dx != nullptr, "x, g and dx must be non-null");
   if (enc) RXMET_CHECK_ARG(workspace != nullptr, "encoding gradients need a workspace");
   const Call c{&p, op, nm->internal_dtype, x, g, dx, scale, offset,
-               make_params(qmin, qmax, *nm), enc ? workspace : nullptr, s};
+               make_params(qmin, qmax, *nm), enc ? workspace : nullptr, s,
+               mm ? *mm : MinMaxSrc{}};
   {
     rxmet::prof::Scope ps__("qdq_backward_stream", s);
     if (int rc = dispatch(c, nm->io_dtype, WHAT_BACKWARD)) return rc;
@@ -301,12 +419,10 @@ static int backward_impl(int op, const void *x, const void *g, void *dx, float *
     const int round16 = r == RXMET_QDQ_F16 ? 1 : (r == RXMET_QDQ_BF16 ? 2 : 0);
     rxmet::prof::Scope ps__("qdq_backward_fold", s);
     const Sum2 *ws = static_cast<const Sum2 *>(workspace);
-    if (p.fold.n0 * p.fold.n1 * p.fold.n2 >= 1024)
-      hipLaunchKernelGGL(fold_sum<4 * kWave>, dim3(static_cast<unsigned>(C)), dim3(4 * kWave), 0,
-                         s, ws, p.fold, dscale, doffset, round16);
+    if (mm != nullptr)
+      launch_fold_sum(ws, p.fold, C, PutMinMaxGrad{*mm, d_min, d_max, round16}, s);
     else
-      hipLaunchKernelGGL(fold_sum<kWave>, dim3(static_cast<unsigned>(C)), dim3(kWave), 0, s, ws,
-                         p.fold, dscale, doffset, round16);
+      launch_fold_sum(ws, p.fold, C, PutScaleOffset{dscale, doffset, round16}, s);
     RXMET_CHECK_LAUNCH();
   }
   return 0;
@@ -318,7 +434,7 @@ static int minmax_impl(const void *x, int32_t io, const rxmet_qdq_layout *l, flo
   if (int rc = check_layout(l->outer, l->C0, l->mid, l->C1, l->inner)) return rc;
   RXMET_CHECK_ARG(is_io(io), "io_dtype must be RXMET_QDQ_F32, F16 or BF16");
   RXMET_CHECK_ARG(out_min && out_max, "out_min/out_max must be non-null");
-  const Plan p = make_plan(l->outer, l->C0, l->mid, l->C1, l->inner, esize_of(io));
+  const Plan p = make_plan(l->outer, l->C0, l->mid, l->C1, l->inner, esize_of(io), kVecMinMax);
   RXMET_CHECK_ARG(p.n > 0, "min/max of an empty tensor");
   RXMET_CHECK_ARG(x != nullptr, "x must be non-null");
   RXMET_CHECK_ARG(workspace != nullptr, "min/max needs a workspace");
@@ -328,8 +444,8 @@ static int minmax_impl(const void *x, int32_t io, const rxmet_qdq_layout *l, flo
   const Call c{&p, OP_QDQ_LEARN, nm.internal_dtype, x, nullptr, nullptr, nullptr, nullptr,
                make_params(0, 0, nm), workspace, s};
   if (int rc = dispatch(c, io, WHAT_MINMAX)) return rc;
-  hipLaunchKernelGGL(fold_minmax, dim3(static_cast<unsigned>(l->C0 * l->C1)), dim3(kWave), 0, s,
-                     static_cast<const MinMax *>(workspace), p.fold, out_min, out_max);
+  launch_fold_minmax(static_cast<const MinMax *>(workspace), p.fold, l->C0 * l->C1, out_min,
+                     out_max, s);
   RXMET_CHECK_LAUNCH();
   return 0;
 }
@@ -347,52 +463,32 @@ static int check_layout3(int64_t outer, int64_t C, int64_t inner) {
 }
 
 // Encodings of learnable min / max, one thread per encoding (see rxmet_qdq_encoding_forward).
-__global__ __launch_bounds__(256) void encoding_fwd(int64_t n, const float *__restrict__ mn,
-                                                    const float *__restrict__ mx, float inv_steps,
-                                                    float qmin, float qmax, int symmetric,
-                                                    float sym_offset, float min_scale,
+__global__ __launch_bounds__(256) void encoding_fwd(int64_t n, MinMaxSrc m,
                                                     float *__restrict__ scale,
                                                     float *__restrict__ offset) {
   const int64_t c = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (c >= n) return;
-  // a tensor divided by a scalar is evaluated on the GPU as a product with the rounded
-  // reciprocal of the scalar
-  float s = fabsf((mx[c] - mn[c]) * inv_steps);
-  s = s < min_scale ? min_scale : s;  // clamp_min keeps NaN
+  float s, o;
+  minmax_scale_offset(m, c, s, o);
   scale[c] = s;
-  if (symmetric) {
-    offset[c] = sym_offset;
-  } else {
-    float o = rintf(mn[c] / s) - qmin;
-    o = o < -qmax ? -qmax : o;
-    o = o > -qmin ? -qmin : o;
-    offset[c] = o;
-  }
+  offset[c] = o;
 }
 
-__global__ __launch_bounds__(256) void encoding_bwd(int64_t n, const float *__restrict__ mn,
-                                                    const float *__restrict__ mx,
+__global__ __launch_bounds__(256) void encoding_bwd(int64_t n, MinMaxSrc m,
                                                     const float *__restrict__ g_scale,
-                                                    const float *__restrict__ g_offset, float inv_steps,
-                                                    float qmin, float qmax, int symmetric,
-                                                    float min_scale, float *__restrict__ d_min,
+                                                    const float *__restrict__ g_offset,
+                                                    float *__restrict__ d_min,
                                                     float *__restrict__ d_max) {
   const int64_t c = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (c >= n) return;
-  const float raw = (mx[c] - mn[c]) * inv_steps, a = fabsf(raw);
-  const float s = a < min_scale ? min_scale : a;
-  float gs = g_scale ? g_scale[c] : 0.0f, gmin = 0.0f;
-  if (!symmetric && g_offset) {
-    const float o = rintf(mn[c] / s) - qmin;
-    const float gr = (o >= -qmax && o <= -qmin) ? g_offset[c] : 0.0f;  // clamp, then STE round
-    gmin += gr / s;                                                   // d(min / s) / d min
-    gs += -gr * ((mn[c] / s) / s);                                    // d(min / s) / d s
-  }
-  const float ga = a >= min_scale ? gs : 0.0f;  // clamp_min
-  const float sg = raw > 0.0f ? 1.0f : (raw < 0.0f ? -1.0f : 0.0f);
-  const float gr2 = (ga * sg) * inv_steps;      // d|raw| and d((max - min) / steps)
-  d_max[c] = gr2;
-  d_min[c] = gmin - gr2;
+  minmax_encoding_grad(m, c, g_scale ? g_scale[c] : 0.0f, g_offset ? g_offset + c : nullptr,
+                       d_min[c], d_max[c]);
+}
+
+static MinMaxSrc minmax_src(const float *mn, const float *mx, int64_t qmin, int64_t qmax,
+                            int32_t symmetric, float sym_offset, float min_scale) {
+  return MinMaxSrc{mn, mx, 1.0f / static_cast<float>(qmax - qmin), static_cast<float>(qmin),
+                   static_cast<float>(qmax), sym_offset, min_scale, symmetric ? 1 : 0};
 }
 
 // Scratch of rxmet_qdq_backward_noalloc: the per-block partial sums of the encoding
@@ -441,7 +537,8 @@ int64_t rxmet_qdq_workspace_bytes_ex(const rxmet_qdq_layout *l, int32_t io_dtype
   if (l == nullptr || !is_io(io_dtype) || l->outer < 0 || l->mid < 0 || l->inner < 0 ||
       l->C0 < 1 || l->C1 < 1)
     return 0;
-  const Plan p = make_plan(l->outer, l->C0, l->mid, l->C1, l->inner, esize_of(io_dtype));
+  // the forward / backward passes' chunks are the smaller ones, so they have the most partials
+  const Plan p = make_plan(l->outer, l->C0, l->mid, l->C1, l->inner, esize_of(io_dtype), kVecQdq);
   return p.partial_slots * static_cast<int64_t>(sizeof(Sum2));
 }
 
@@ -502,6 +599,38 @@ int rxmet_qdq_backward_ex(const void *x, const void *g, void *dx, float *dscale,
   RXMET_CHECK_ARG(op >= 0, "unknown qdq mode");
   return backward_impl(op, x, g, dx, dscale, doffset, layout, numerics, scale, offset, qmin,
                        qmax, workspace, stream);
+}
+
+static int minmax_args(const rxmet_qdq_minmax_enc *enc, int64_t qmin, int64_t qmax, MinMaxSrc *mm) {
+  RXMET_CHECK_ARG(enc != nullptr && enc->min != nullptr && enc->max != nullptr,
+                  "min/max encodings must be non-null");
+  RXMET_CHECK_ARG(enc->reserved == 0, "rxmet_qdq_minmax_enc.reserved must be 0");
+  if (int rc = check_grid(qmin, qmax, RXMET_QDQ_F32)) return rc;
+  RXMET_CHECK_ARG(qmax > qmin, "min/max encodings need qmax > qmin");
+  *mm = minmax_src(enc->min, enc->max, qmin, qmax, enc->symmetric, enc->sym_offset,
+                   enc->min_scale);
+  return 0;
+}
+
+int rxmet_qdq_forward_minmax(const void *x, void *y, const rxmet_qdq_layout *layout,
+                             const rxmet_qdq_numerics *numerics, const rxmet_qdq_minmax_enc *enc,
+                             int64_t qmin, int64_t qmax, void *stream) {
+  clear_error();
+  MinMaxSrc mm;
+  if (int rc = minmax_args(enc, qmin, qmax, &mm)) return rc;
+  return forward_impl(OP_QDQ_LEARN, x, y, layout, numerics, nullptr, nullptr, qmin, qmax, stream,
+                      &mm);
+}
+
+int rxmet_qdq_backward_minmax(const void *x, const void *g, void *dx, float *d_min,
+                              float *d_max, const rxmet_qdq_layout *layout,
+                              const rxmet_qdq_numerics *numerics, const rxmet_qdq_minmax_enc *enc,
+                              int64_t qmin, int64_t qmax, void *workspace, void *stream) {
+  clear_error();
+  MinMaxSrc mm;
+  if (int rc = minmax_args(enc, qmin, qmax, &mm)) return rc;
+  return backward_impl(OP_QDQ_LEARN, x, g, dx, nullptr, nullptr, layout, numerics, nullptr,
+                       nullptr, qmin, qmax, workspace, stream, &mm, d_min, d_max);
 }
 
 int rxmet_qdq_backward_noalloc(const float *x, const float *g, float *dx, float *dscale,
@@ -608,10 +737,9 @@ int rxmet_qdq_encoding_forward(const float *mn, const float *mx, int64_t n, int6
   RXMET_CHECK_ARG(n >= 1 && mn && mx && scale && offset, "bad encoding arguments");
   if (int rc = check_grid(qmin, qmax, RXMET_QDQ_F32)) return rc;
   hipLaunchKernelGGL(encoding_fwd, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), n, mn, mx,
-                     1.0f / static_cast<float>(qmax - qmin), static_cast<float>(qmin),
-                     static_cast<float>(qmax), symmetric, sym_offset,
-                     min_scale, scale, offset);
+                     static_cast<hipStream_t>(stream), n,
+                     minmax_src(mn, mx, qmin, qmax, symmetric, sym_offset, min_scale), scale,
+                     offset);
   RXMET_CHECK_LAUNCH();
   return 0;
 }
@@ -624,9 +752,9 @@ int rxmet_qdq_encoding_backward(const float *mn, const float *mx, const float *g
   RXMET_CHECK_ARG(n >= 1 && mn && mx && d_min && d_max, "bad encoding arguments");
   if (int rc = check_grid(qmin, qmax, RXMET_QDQ_F32)) return rc;
   hipLaunchKernelGGL(encoding_bwd, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), n, mn, mx, g_scale, g_offset,
-                     1.0f / static_cast<float>(qmax - qmin), static_cast<float>(qmin),
-                     static_cast<float>(qmax), symmetric, min_scale, d_min, d_max);
+                     static_cast<hipStream_t>(stream), n,
+                     minmax_src(mn, mx, qmin, qmax, symmetric, 0.0f, min_scale), g_scale,
+                     g_offset, d_min, d_max);
   RXMET_CHECK_LAUNCH();
   return 0;
 }

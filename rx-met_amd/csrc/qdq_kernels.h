@@ -39,7 +39,12 @@ namespace qdq {
 enum Op { OP_QDQ_LEARN = 0, OP_QDQ_FROZEN = 1, OP_Q = 2, OP_DQ = 3 };
 
 constexpr int kThreads = 256;
-constexpr int kVecPerThread = 8;   // 16-byte vectors per thread per chunk (runs)
+// 16-byte vectors per thread per chunk (runs decomposition), per kind of pass.  Measured on
+// c2 ([8192, 8192] fp32) as a forward + backward training step of QuantizeDequantize: 4 for the
+// forward / backward passes (236-240 us) against 8 (241-244 us); 8 for the read-only min / max
+// (45 us against 49 with 4).
+constexpr int kVecQdq = 4;
+constexpr int kVecMinMax = 8;
 constexpr int64_t kMinRun = 1024;  // runs at least this long use the runs decomposition
 constexpr int64_t kMinSeg = 16;    // shorter runs use the column decomposition
 constexpr int kColTargetBlocks = 2048;
@@ -157,9 +162,57 @@ __device__ __forceinline__ A clamp_a(A v, A lo, A hi) {
 // Per-launch scalars.
 struct Params {
   double qmin, qmax;   // grid (exact in R)
-  float alpha;         // zero_point_shift (0: none)
+  double alpha;        // zero_point_shift (0: none); taken to R where it is used
   int scalar_scale;    // the scale is a 0-dim tensor (see rxmet_qdq_numerics)
 };
+
+// Learnable min / max encodings (QuantizeDequantize's parameters) as the source of a launch's
+// scale and offset: each block derives its encodings from min and max itself, as
+// get_scale / _get_offset evaluate them on the GPU (quantizer.py:345-403), instead of reading
+// scale and offset tensors made by separate launches.  mn == null: scale / offset are given.
+struct MinMaxSrc {
+  const float *mn, *mx;
+  float inv_steps;  // fp32 reciprocal of (qmax - qmin): a tensor / scalar on the GPU
+  float qmin, qmax, sym_offset, min_scale;
+  int symmetric;
+};
+
+// scale = clamp_min(|(max - min) / steps|, min_scale); offset = the symmetric offset, or
+// clamp(rint(min / scale) - qmin, -qmax, -qmin); all in fp32 (clamp_min keeps NaN).
+__device__ __forceinline__ void minmax_scale_offset(const MinMaxSrc &m, int64_t c, float &s,
+                                                    float &o) {
+  s = fabsf((m.mx[c] - m.mn[c]) * m.inv_steps);
+  s = s < m.min_scale ? m.min_scale : s;
+  if (m.symmetric) {
+    o = m.sym_offset;
+  } else {
+    o = rintf(m.mn[c] / s) - m.qmin;
+    o = o < -m.qmax ? -m.qmax : o;
+    o = o > -m.qmin ? -m.qmin : o;
+  }
+}
+
+// Gradients of min and max from those of scale (gs) and offset (go; unused when symmetric):
+// the autograd rules of the expressions above (STE through rint).
+__device__ __forceinline__ void minmax_encoding_grad(const MinMaxSrc &m, int64_t c, float gs,
+                                                     const float *go, float &d_min,
+                                                     float &d_max) {
+  const float mn = m.mn[c];
+  const float raw = (m.mx[c] - mn) * m.inv_steps, a = fabsf(raw);
+  const float s = a < m.min_scale ? m.min_scale : a;
+  float gmin = 0.0f;
+  if (!m.symmetric && go) {
+    const float o = rintf(mn / s) - m.qmin;
+    const float gr = (o >= -m.qmax && o <= -m.qmin) ? *go : 0.0f;  // clamp, then STE round
+    gmin += gr / s;                                                // d(min / s) / d min
+    gs += -gr * ((mn / s) / s);                                    // d(min / s) / d s
+  }
+  const float ga = a >= m.min_scale ? gs : 0.0f;  // clamp_min
+  const float sg = raw > 0.0f ? 1.0f : (raw < 0.0f ? -1.0f : 0.0f);
+  const float gr2 = (ga * sg) * m.inv_steps;      // d|raw| and d((max - min) / steps)
+  d_max = gr2;
+  d_min = gmin - gr2;
+}
 
 // One encoding as the element functions use it.
 template <typename T, typename R>
@@ -172,11 +225,21 @@ struct Elem {
 
   __device__ static A r(A v) { return Rnd<R>::r(v); }
 
-  __device__ static Enc enc(const float *scale, const float *offset, int64_t c,
-                            const Params &p) {
+  __device__ static Enc enc(const float *scale, const float *offset, const MinMaxSrc &mm,
+                            int64_t c, const Params &p) {
     Enc e;
-    const float s = scale[c];
-    const float o = offset ? offset[c] : 0.0f;
+    float s, o;
+    if (mm.mn != nullptr) {
+      // scale.to(R), offset.to(R) of the derived fp32 encodings
+      minmax_scale_offset(mm, c, s, o);
+      if constexpr (std::is_same<A, float>::value) {
+        s = Rnd<R>::r(s);
+        o = Rnd<R>::r(o);
+      }
+    } else {
+      s = scale[c];
+      o = offset ? offset[c] : 0.0f;
+    }
     e.s = A(s);
     e.o = A(o);
     e.qmin = A(p.qmin);
@@ -194,8 +257,8 @@ struct Elem {
   // 0-dim scale and R wider than T, type promotion keeps that subtraction in T (the scale
   // is rounded to T first); otherwise it runs in R.
   __device__ static A shifted(float x, const Enc &e, const Params &p) {
-    if (p.alpha == 0.0f) return A(x);
-    if (p.scalar_scale) return A(Io<T>::round(fmaf(-p.alpha, e.s_io, x)));
+    if (p.alpha == 0.0) return A(x);
+    if (p.scalar_scale) return A(Io<T>::round(fmaf(-static_cast<float>(p.alpha), e.s_io, x)));
     return r(fma_a(A(-p.alpha), e.s, A(x)));
   }
 
@@ -208,7 +271,7 @@ struct Elem {
 
   // torch.add(qdq, scale, alpha=shift) in R.
   __device__ static A unshift(A y, const Enc &e, const Params &p) {
-    return p.alpha == 0.0f ? y : r(fma_a(A(p.alpha), e.s, y));
+    return p.alpha == 0.0 ? y : r(fma_a(A(p.alpha), e.s, y));
   }
 };
 
@@ -249,7 +312,7 @@ __device__ __forceinline__ float bwd_elem(float x, float g, const typename Elem<
     ds += static_cast<double>(El::r(ga * El::r(clamp_a(rr, e.lo, e.hi) - t * m)));
     dof += static_cast<double>(El::r(ga * El::r(nm * e.s)));
     // the shift's own scale terms: +alpha*g from the add, -alpha*g*mask through the sub
-    if (p.alpha != 0.0f) ds += static_cast<double>(p.alpha) * static_cast<double>(ga * nm);
+    if (p.alpha != 0.0) ds += static_cast<double>(A(p.alpha)) * static_cast<double>(ga * nm);
     return static_cast<float>(ga * m);
   } else if constexpr (OP == OP_QDQ_FROZEN) {
     const float q = rintf(x * e.inv_s) + e.zp;
@@ -325,16 +388,21 @@ struct FwdW {
   using Acc = Sum2;  // unused
   static constexpr bool kReduce = false;
   static constexpr int E = Io<T>::E;
+  static constexpr int V = kVecQdq;
   const T *x;
   T *y;
   const float *scale, *offset;
   Params p;
+  MinMaxSrc mm;
 
-  __device__ Enc enc(int64_t c) const { return El::enc(scale, offset, c, p); }
+  __device__ Enc enc(int64_t c) const { return El::enc(scale, offset, mm, c, p); }
   __device__ static Acc zero() { return Sum2{0.0, 0.0}; }
   __device__ void elem(const Enc &e, int64_t i, Acc &) const {
     Io<T>::st(y, i, fwd_elem<OP, T, R>(Io<T>::ld(x, i), e, p));
   }
+  // Non-temporal loads and stores.  Ordinary stores time about 6 % faster in a loop of one
+  // pass, but leave the output in the caches to be written back during the next pass: a
+  // forward + backward training step measured 255-263 us with them against 236-240 us.
   __device__ void compute(const Enc &e, const u4 &v, int64_t vi) const {
     float a[E];
     Io<T>::unpack(v, a);
@@ -345,17 +413,17 @@ struct FwdW {
   __device__ void vec1(const Enc &e, int64_t vi, Acc &) const {
     compute(e, __builtin_nontemporal_load(reinterpret_cast<const u4 *>(x) + vi), vi);
   }
-  // kVecPerThread vectors per thread: all loads issued before any compute
+  // V vectors per thread: all loads issued before any compute
   __device__ void vec_block(const Enc &e, int64_t vb, int nv, Acc &) const {
     const u4 *xv = reinterpret_cast<const u4 *>(x) + vb;
-    u4 v[kVecPerThread];
+    u4 v[V];
 #pragma unroll
-    for (int k = 0; k < kVecPerThread; ++k) {
+    for (int k = 0; k < V; ++k) {
       const int i = k * kThreads + threadIdx.x;
       if (i < nv) v[k] = __builtin_nontemporal_load(xv + i);
     }
 #pragma unroll
-    for (int k = 0; k < kVecPerThread; ++k) {
+    for (int k = 0; k < V; ++k) {
       const int i = k * kThreads + threadIdx.x;
       if (i < nv) compute(e, v[k], vb + i);
     }
@@ -369,12 +437,14 @@ struct BwdW {
   using Acc = Sum2;
   static constexpr bool kReduce = ENC;
   static constexpr int E = Io<T>::E;
+  static constexpr int V = kVecQdq;
   const T *x, *g;
   T *dx;
   const float *scale, *offset;
   Params p;
+  MinMaxSrc mm;
 
-  __device__ Enc enc(int64_t c) const { return El::enc(scale, offset, c, p); }
+  __device__ Enc enc(int64_t c) const { return El::enc(scale, offset, mm, c, p); }
   __device__ static Acc zero() { return Sum2{0.0, 0.0}; }
   __device__ void elem(const Enc &e, int64_t i, Acc &acc) const {
     Io<T>::st(dx, i,
@@ -397,9 +467,9 @@ struct BwdW {
   __device__ void vec_block(const Enc &e, int64_t vb, int nv, Acc &acc) const {
     const u4 *xv = reinterpret_cast<const u4 *>(x) + vb;
     const u4 *gv = reinterpret_cast<const u4 *>(g) + vb;
-    u4 xr[kVecPerThread], gr[kVecPerThread];
+    u4 xr[V], gr[V];
 #pragma unroll
-    for (int k = 0; k < kVecPerThread; ++k) {
+    for (int k = 0; k < V; ++k) {
       const int i = k * kThreads + threadIdx.x;
       if (i < nv) {
         xr[k] = __builtin_nontemporal_load(xv + i);
@@ -407,7 +477,7 @@ struct BwdW {
       }
     }
 #pragma unroll
-    for (int k = 0; k < kVecPerThread; ++k) {
+    for (int k = 0; k < V; ++k) {
       const int i = k * kThreads + threadIdx.x;
       if (i < nv) compute(e, xr[k], gr[k], vb + i, acc);
     }
@@ -420,6 +490,7 @@ struct MinMaxW {
   using Acc = MinMax;
   static constexpr bool kReduce = true;
   static constexpr int E = Io<T>::E;
+  static constexpr int V = kVecMinMax;
   const T *x;
 
   __device__ Enc enc(int64_t) const { return Enc{}; }
@@ -440,14 +511,14 @@ struct MinMaxW {
   }
   __device__ void vec_block(const Enc &, int64_t vb, int nv, Acc &acc) const {
     const u4 *xv = reinterpret_cast<const u4 *>(x) + vb;
-    u4 v[kVecPerThread];
+    u4 v[V];
 #pragma unroll
-    for (int k = 0; k < kVecPerThread; ++k) {
+    for (int k = 0; k < V; ++k) {
       const int i = k * kThreads + threadIdx.x;
       if (i < nv) v[k] = __builtin_nontemporal_load(xv + i);
     }
 #pragma unroll
-    for (int k = 0; k < kVecPerThread; ++k) {
+    for (int k = 0; k < V; ++k) {
       const int i = k * kThreads + threadIdx.x;
       if (i < nv) take_vec(v[k], acc);
     }
@@ -475,7 +546,7 @@ struct ColGeo {
 template <class W>
 __global__ __launch_bounds__(kThreads) void k_runs(W w, Geo geo, int64_t splits, int vec,
                                                    typename W::Acc *__restrict__ partial) {
-  constexpr int64_t kChunk = int64_t(kThreads) * kVecPerThread * W::E;
+  constexpr int64_t kChunk = int64_t(kThreads) * W::V * W::E;
   const int64_t b = blockIdx.x;
   const int64_t run = b / splits, sp = b % splits;
   const auto e = w.enc(enc_of_run(geo, run));
@@ -590,6 +661,7 @@ struct Call {
   Params p;
   void *partial;           // Sum2 / MinMax partials, or null
   hipStream_t stream;
+  MinMaxSrc mm;            // mm.mn != null: encodings derived from min / max in the kernels
 };
 
 template <class W>
@@ -625,7 +697,8 @@ static inline bool aligned16(const void *p) {
 
 template <int OP, typename T, typename R>
 static int run_forward(const Call &c) {
-  FwdW<OP, T, R> w{static_cast<const T *>(c.x), static_cast<T *>(c.out), c.scale, c.offset, c.p};
+  FwdW<OP, T, R> w{static_cast<const T *>(c.x), static_cast<T *>(c.out), c.scale, c.offset, c.p,
+                   c.mm};
   return launch_decomp(*c.plan, w, aligned16(c.x) && aligned16(c.out), nullptr, c.stream);
 }
 
@@ -634,11 +707,11 @@ static int run_backward(const Call &c) {
   const bool al = aligned16(c.x) && aligned16(c.g) && aligned16(c.out);
   if (c.partial) {
     BwdW<OP, T, R, true> w{static_cast<const T *>(c.x), static_cast<const T *>(c.g),
-                           static_cast<T *>(c.out), c.scale, c.offset, c.p};
+                           static_cast<T *>(c.out), c.scale, c.offset, c.p, c.mm};
     return launch_decomp(*c.plan, w, al, c.partial, c.stream);
   }
   BwdW<OP, T, R, false> w{static_cast<const T *>(c.x), static_cast<const T *>(c.g),
-                          static_cast<T *>(c.out), c.scale, c.offset, c.p};
+                          static_cast<T *>(c.out), c.scale, c.offset, c.p, c.mm};
   return launch_decomp(*c.plan, w, al, nullptr, c.stream);
 }
 

@@ -180,7 +180,6 @@ class GRUQuantParams:
         object.__setattr__(self, "_qp", A.new_qparams(max(int(hidden), 1)))
         self._qp.hidden = int(hidden)
         object.__setattr__(self, "_cfg", None)
-        object.__setattr__(self, "_device_cache", {})
 
     @classmethod
     def from_struct(cls, qp) -> "GRUQuantParams":

@@ -299,6 +299,53 @@ class _QuantDequant(torch.autograd.Function):
         return (plan.from_kernel(dx) if need_x else None), ds, do, None, None, None, None, None
 
 
+class _QuantDequantMinMax(torch.autograd.Function):
+    """QuantizeDequantize.forward with learnable min / max (quantizer.py:1048-1082): the
+    encodings of get_encodings() (:466-483) and the learnable QuantDequantFunc path in one
+    launch each way (rxmet_qdq_forward_minmax / _backward_minmax).  The kernels derive scale and
+    offset from min and max themselves, and the backward's fold takes the encoding gradients on
+    to min and max; the results equal minmax_encodings() followed by quantize_dequantize() bit
+    for bit."""
+
+    @staticmethod
+    def forward(ctx, x, mn, mx, qmin: int, qmax: int, enc: tuple, plan: _Plan, numerics):
+        xk = plan.to_kernel(x)
+        y = torch.empty_like(xk)
+        mnv, mxv = mn.detach().reshape(-1), mx.detach().reshape(-1)
+        _rx.call("rxmet_qdq_forward_minmax", _rx.ptr(xk), _rx.ptr(y), plan.cstruct(), numerics,
+                 _minmax_struct(mnv, mxv, enc), int(qmin), int(qmax), _rx.stream_of(xk.device))
+        ctx.args = (int(qmin), int(qmax), enc, plan, numerics)
+        ctx.min_shape = mn.shape
+        ctx.save_for_backward(xk, mnv, mxv)
+        return plan.from_kernel(y)
+
+    @staticmethod
+    def backward(ctx, g):
+        xk, mnv, mxv = ctx.saved_tensors
+        qmin, qmax, enc, plan, numerics = ctx.args
+        need_x, need_mn, need_mx = ctx.needs_input_grad[:3]
+        gk = plan.to_kernel(g.to(xk.dtype))
+        dx = torch.empty_like(xk)
+        need_enc = need_mn or need_mx
+        d_min = torch.empty_like(mnv) if need_enc else None
+        d_max = torch.empty_like(mxv) if need_enc else None
+        ws = _workspace(plan, xk.dtype, xk.device) if need_enc else None
+        _rx.call("rxmet_qdq_backward_minmax", _rx.ptr(xk), _rx.ptr(gk), _rx.ptr(dx),
+                 _rx.ptr(d_min), _rx.ptr(d_max), plan.cstruct(), numerics,
+                 _minmax_struct(mnv, mxv, enc), qmin, qmax, _rx.ptr(ws),
+                 _rx.stream_of(xk.device))
+        shape = ctx.min_shape
+        return ((plan.from_kernel(dx) if need_x else None),
+                d_min.view(shape) if need_mn else None, d_max.view(shape) if need_mx else None,
+                None, None, None, None, None)
+
+
+def _minmax_struct(mnv, mxv, enc):
+    symmetric, sym_offset, min_scale = enc
+    return _rx.QdqMinMaxEnc(mnv.data_ptr(), mxv.data_ptr(), int(bool(symmetric)),
+                            float(sym_offset), float(min_scale), 0)
+
+
 class _Quantize(torch.autograd.Function):
     """QuantizeFunc (torch_builtins.py:505-571)."""
 
@@ -458,6 +505,44 @@ def quantize_dequantize(tensor: torch.Tensor, scale: torch.Tensor, offset: torch
                                _Plan(t.shape, enc_shape),
                                _numerics(t.dtype, internal, zero_point_shift, scalar)
                                ).view(orig_shape)
+
+
+def quantize_dequantize_minmax(tensor: torch.Tensor, mn: torch.Tensor, mx: torch.Tensor,
+                               qmin: int, qmax: int, symmetric: bool, min_scale: float,
+                               sym_offset: float, block_size: Optional[List] = None,
+                               zero_point_shift: float = 0.0) -> Optional[torch.Tensor]:
+    """QuantizeDequantize.forward of learnable fp32 min / max parameters (their shape is the
+    encoding shape) through the fused kernels, or None where this form does not apply (the
+    caller then takes get_encodings() and quantize_dequantize): it needs CUDA fp32 contiguous
+    min / max with one value per encoding, and a tensor on the same device.  Encodings without
+    gradient (frozen min / max, or autograd off) take the reference's fake_quantize fast path
+    (torch_builtins.py:221-249), so they are left to quantize_dequantize."""
+    if not (torch.is_grad_enabled() and (mn.requires_grad or mx.requires_grad)):
+        return None
+    if not (mn.is_cuda and mx.is_cuda and tensor.is_cuda and mn.dtype == torch.float32
+            and mx.dtype == torch.float32 and mn.is_contiguous() and mx.is_contiguous()
+            and mn.shape == mx.shape and tensor.dtype in _IO_CODE and qmax > qmin):
+        return None
+    _validate_arguments(tensor, mn, qmin, qmax, block_size)
+    internal = _internal_dtype(tensor.dtype, qmin, qmax)
+    if not _is_grid_representable(internal, qmin, qmax):
+        raise RuntimeError(
+            f"{internal} is unable to represent quantized output of range [{qmin}, {qmax}].")
+    if max(abs(int(qmin)), abs(int(qmax))) > 1 << 24:
+        return None
+    orig_shape = tensor.shape
+    t = reshape_tensor_for_blocks(tensor, mn.shape, block_size)
+    enc_view = get_encoding_shape_with_blocks(mn.shape, block_size)
+    enc_shape = (1,) * (t.dim() - len(enc_view)) + tuple(enc_view)
+    plan = _Plan(t.shape, enc_shape)
+    if plan.C != mn.numel() or t.numel() == 0:
+        return None
+    scalar = mn.dim() == 0 and t.dim() > 0 and internal != t.dtype
+    fn = _QuantDequantMinMax
+    y = fn.apply(t, mn, mx, int(qmin), int(qmax),
+                 (bool(symmetric), float(sym_offset), float(min_scale)), plan,
+                 _numerics(t.dtype, internal, zero_point_shift, scalar))
+    return y.view(orig_shape)
 
 
 def minmax(tensor: torch.Tensor, enc_shape) -> Tuple[torch.Tensor, torch.Tensor]:

@@ -36,7 +36,15 @@ class QdqNumerics(ctypes.Structure):
                 ("reserved", ctypes.c_int32)]
 
 
+class QdqMinMaxEnc(ctypes.Structure):
+    """rxmet_qdq_minmax_enc: learnable min / max encodings derived inside the kernels."""
+    _fields_ = [("min", c_ptr), ("max", c_ptr), ("symmetric", ctypes.c_int32),
+                ("sym_offset", ctypes.c_float), ("min_scale", ctypes.c_float),
+                ("reserved", ctypes.c_int32)]
+
+
 _LAY = ctypes.POINTER(QdqLayout)
+_MME = ctypes.POINTER(QdqMinMaxEnc)
 _NUM = ctypes.POINTER(QdqNumerics)
 
 # name -> (restype, argtypes); mirrors include/rxmet_qdq.h and include/rxmet_gru.h
@@ -64,6 +72,9 @@ _SIGNATURES = {
                                      c_ptr]),
     "rxmet_qdq_backward_ex": (c_int, [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, _LAY, _NUM, c_ptr, c_ptr,
                                       c_i64, c_i64, c_int, c_ptr, c_ptr]),
+    "rxmet_qdq_forward_minmax": (c_int, [c_ptr, c_ptr, _LAY, _NUM, _MME, c_i64, c_i64, c_ptr]),
+    "rxmet_qdq_backward_minmax": (c_int, [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, _LAY, _NUM, _MME,
+                                          c_i64, c_i64, c_ptr, c_ptr]),
     "rxmet_quantize_forward_ex": (c_int, [c_ptr, c_ptr, _LAY, _NUM, c_ptr, c_ptr, c_i64, c_i64,
                                           c_ptr]),
     "rxmet_quantize_backward_ex": (c_int, [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, _LAY, _NUM, c_ptr,

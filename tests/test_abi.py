@@ -37,9 +37,11 @@ def test_python_signatures_cover_headers():
 def test_host_only_calls_work_without_gpu():
     lib = rxmet_lib.load()
     assert lib.rxmet_abi_version() >= 1
-    # [8192, 8192] per-channel on dim 0: one partial per channel row
-    assert lib.rxmet_qdq_workspace_bytes(1, 8192, 8192) == 8192 * 16
-    assert lib.rxmet_qdq_workspace_bytes(1, 1, 8192 * 8192) == 8192 * 16
+    # [8192, 8192] per-channel on dim 0: a 4096-element chunk per block (256 threads x four
+    # 16-byte vectors of fp32), two partials of 16 bytes per channel row; per-tensor the same
+    # 16384 chunks
+    assert lib.rxmet_qdq_workspace_bytes(1, 8192, 8192) == 8192 * 2 * 16
+    assert lib.rxmet_qdq_workspace_bytes(1, 1, 8192 * 8192) == 16384 * 16
 
 
 def test_noalloc_backward_rejects_layouts_beyond_its_scratch():
@@ -50,7 +52,7 @@ def test_noalloc_backward_rejects_layouts_beyond_its_scratch():
     lib = rxmet_lib.load()
     buf = (ctypes.c_float * 4)()
     p = ctypes.cast(buf, ctypes.c_void_p)
-    n = 1 << 33  # per-tensor: 2^33 / 8192 partials of 16 bytes = 16 MiB
+    n = 1 << 33  # per-tensor: 2^33 / 4096 partials of 16 bytes = 32 MiB
     need = lib.rxmet_qdq_workspace_bytes(1, 1, n)
     assert need > 4 << 20
     rc = lib.rxmet_qdq_backward_noalloc(p, p, p, p, p, 1, 1, n, p, p, -128, 127, 0, None)

@@ -293,6 +293,29 @@ def test_backend_matches_torch_reference_on_gpu(cuda, dtype, grid, sshape, shape
                                        err_msg=what)
 
 
+@pytest.mark.parametrize("sshape", [(), (64, 1)])
+def test_shift_not_exact_in_fp32_on_a_double_grid(cuda, sshape):
+    """A grid of more than 838,860 steps computes in fp64 (the reference's stability rule),
+    where torch.sub / torch.add(..., alpha=shift) use the shift at double precision: a shift
+    of 0.1, which fp32 cannot hold, must enter the double arithmetic unrounded."""
+    qmin, qmax = -(1 << 22), (1 << 22) - 1
+    shift = 0.1
+    print(f"[qdq backend] f64 internal shift={shift} scale{sshape}", flush=True)
+    gen = torch.Generator().manual_seed(77)
+    shape = (64, 257)
+    x = (torch.randn(shape, generator=gen) * 1.5).to(cuda)
+    g = torch.randn(shape, generator=gen).to(cuda)
+    scale = ((torch.rand(sshape, generator=gen) + 0.5) * 3.0 / (qmax - qmin)).to(cuda)
+    offset = torch.zeros(sshape).to(cuda)
+    assert Q._internal_dtype(torch.float32, qmin, qmax) == torch.float64
+    (y, dx, ds, do), (ey, edx, eds, edo) = _run_both(x, scale, offset, qmin, qmax, shift, g)
+    assert torch.equal(y, ey)
+    assert torch.equal(dx, edx)
+    for a, e, what in ((ds, eds, "scale"), (do, edo, "offset")):
+        a, e = a.double().cpu().numpy(), e.double().cpu().numpy()
+        np.testing.assert_allclose(a, e, rtol=2e-6, atol=2e-6 * np.abs(e).max(), err_msg=what)
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("block_size,sshape,shape", [
     ((16, 32), (4, 8), (64, 256)),      # two-dimensional blocks: two encoding groups
