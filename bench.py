@@ -745,9 +745,11 @@ def _lstm_published_leg(torch, iters: int = 200, warmup: int = 20):
             raise ValidationError(f"lstm published {case_id}: C-ABI forward differs from the module")
         evs = [torch.cuda.Event(enable_timing=True) for _ in range(iters + 1)]
         evs[0].record(stream)
+        h0 = time.perf_counter()
         for i in range(iters):
             call()
             evs[i + 1].record(stream)
+        host_ms = (time.perf_counter() - h0) / iters * 1e3
         torch.cuda.synchronize()
         per = sorted(evs[i].elapsed_time(evs[i + 1]) for i in range(iters))
         p50, p95 = per[len(per) // 2], per[min(len(per) - 1, int(0.95 * len(per)))]
@@ -756,9 +758,11 @@ def _lstm_published_leg(torch, iters: int = 200, warmup: int = 20):
                         "p95_ms": round(p95, 4), "seq_per_s": round(B / (p50 * 1e-3), 1),
                         "reference_p50_ms": ref_p50, "reference_p95_ms": ref_p95,
                         "reference_seq_per_s": ref_sps,
-                        "speedup_p50": round(ref_p50 / p50, 3)}
+                        "speedup_p50": round(ref_p50 / p50, 3),
+                        "host_ms_per_call": round(host_ms, 4)}
         _log(f"lstm published {profile} {c['shape']}: P50 {p50:.4f} ms P95 {p95:.4f} ms "
-             f"{B / (p50 * 1e-3):.0f} seq/s (reference RTX 6000D {ref_sps} seq/s)")
+             f"{B / (p50 * 1e-3):.0f} seq/s (reference RTX 6000D {ref_sps} seq/s); host "
+             f"{host_ms:.4f} ms per call")
     return out
 
 

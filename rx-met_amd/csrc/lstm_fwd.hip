@@ -58,7 +58,7 @@ struct ChanRun {
   float ih_bacc;   // rescaled centred bias of the input linear (0 without bias)
   float hh_bacc;
   int32_t hh_k;    // integer correction of the recurrent MFMA sum (zero points, plane offsets)
-  int32_t pad;
+  int32_t hh_k_hi; // its upper 32 bits (the correction exceeds int32 only with 16-bit W_hh)
 };
 
 __device__ __forceinline__ float rescale(float v, float mult, int shift) {
@@ -190,7 +190,7 @@ __global__ __launch_bounds__(64) void lstm_quant_weights(WeightArgs a, Grid gw_i
     a.wq_ih[i] = q;
     if (a.wm_ih) a.wm_ih[i] = m;
   }
-  int s = 0;
+  int s = 0;  // |sum| <= 2^15 * H: int32 for H < 2^16
   for (int k = l; k < a.H; k += 64) {
     const size_t i = static_cast<size_t>(c) * a.H + k;
     const float q = quantize(a.W_hh[i], ch.w_hh_s, 0, gw_hh, m);
@@ -213,8 +213,9 @@ __global__ __launch_bounds__(64) void lstm_quant_weights(WeightArgs a, Grid gw_i
       r.ih_bacc = rescale(center(qi, 0), ch.ih_bmult, ch.ih_bshift);
       r.hh_bacc = rescale(center(qh, 0), ch.hh_bmult, ch.hh_bshift);
     }
-    r.hh_k = s * a.hh_k_factor;
-    r.pad = 0;
+    const int64_t k64 = static_cast<int64_t>(s) * a.hh_k_factor;
+    r.hh_k = static_cast<int32_t>(k64);
+    r.hh_k_hi = static_cast<int32_t>(k64 >> 32);
     a.run[c] = r;
   }
 }
@@ -244,23 +245,33 @@ __global__ __launch_bounds__(256) void lstm_quant_inputs(int64_t nx, int64_t nh,
 
 // W_hh codes [4H][H] -> B fragments of D[b][c] = sum_k h[b][k] W[c][k]:
 // frag[(ct * KS + s) * 64 + lane] = W[16 ct + lane % 16][64 s + 16 (lane / 16) + 0..15].
-__global__ __launch_bounds__(64) void lstm_pack_whh(int H, int KS, const float *__restrict__ wq,
+// With pw = 2 planes (W_hh wider than 8 bits, at most 16) W = 256 bh + bl + 128 with bl, bh
+// signed bytes: bl's fragments first, then bh's, plane_stride fragments apart.
+__global__ __launch_bounds__(64) void lstm_pack_whh(int H, int KS, int pw, size_t plane_stride,
+                                                    const float *__restrict__ wq,
                                                     v4i *__restrict__ frag) {
   const int lane = threadIdx.x, idx = blockIdx.x;
   const int s = idx % KS, ct = idx / KS;
   const int c = 16 * ct + lane % 16;
-  int wd[4];
+  for (int p = 0; p < pw; ++p) {
+    int wd[4];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    int by[4];
+    for (int q = 0; q < 4; ++q) {
+      int by[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int k = 64 * s + 16 * (lane / 16) + 4 * q + e;
-      by[e] = k < H ? static_cast<int>(wq[static_cast<size_t>(c) * H + k]) : 0;
+      for (int e = 0; e < 4; ++e) {
+        const int k = 64 * s + 16 * (lane / 16) + 4 * q + e;
+        int w = k < H ? static_cast<int>(wq[static_cast<size_t>(c) * H + k]) : 0;
+        if (pw == 2) {  // (the two-plane recurrence needs H a multiple of 64: no padded k)
+          const int u = w + 32768;
+          w = p == 0 ? (u & 255) - 128 : (u >> 8) - 128;
+        }
+        by[e] = w;
+      }
+      wd[q] = pack4_i8(by[0], by[1], by[2], by[3]);
     }
-    wd[q] = pack4_i8(by[0], by[1], by[2], by[3]);
+    frag[p * plane_stride + static_cast<size_t>(idx) * 64 + lane] = v4i{wd[0], wd[1], wd[2], wd[3]};
   }
-  frag[static_cast<size_t>(idx) * 64 + lane] = v4i{wd[0], wd[1], wd[2], wd[3]};
 }
 
 // ---------------------------------------------------------------------------------
@@ -566,13 +577,21 @@ constexpr int kLutMaxEntries = 4096;  // activation tables kept in LDS up to 16 
 
 // The real activation of a gate is a function of the gate-input code alone, and the cell's
 // tanh a function of the cell code: on grids of at most kLutMaxEntries codes the clustered
-// recurrence reads precomputed results (same device function, evaluated once per code).
-// Entry = (output code - output grid lo) << 1 | clamp mask.
+// recurrence reads precomputed results (same device function, evaluated once per code) from
+// LDS.  Grids of up to kGlobalLutMaxCodes codes that LDS cannot hold have their tables in
+// global memory (L2-resident, 256 KB per 16-bit grid) when that saves work on the step's
+// dependent chain: the four gates (eight evaluations per lane and step, one gather instead),
+// and the cell's tanh when its grid has exception codes (a lookup instead of the evaluation
+// and the search of the exception list).  Entry = (output code - output grid lo) << 1 | mask.
+constexpr int kGlobalLutMaxCodes = 1 << 16;
 struct ActLut {
   const uint32_t *table;  // gate tables [off[g] .. off[g] + n[g]), then the tanh table
   int off[4], n[4];       // n = 0: no gate tables (computed in place)
   int tanh_off, tanh_n;   // tanh_n = 0: computed in place
   int total;
+  // tables read from global memory, laid out the same way
+  const uint32_t *gtable;
+  int goff[4], gn[4], gtanh_off, gtanh_n, gtotal;
 };
 
 __global__ __launch_bounds__(256) void lstm_build_act_lut(StepParams sp, ActLut lut,
@@ -582,18 +601,48 @@ __global__ __launch_bounds__(256) void lstm_build_act_lut(StepParams sp, ActLut 
   uint8_t m;
   float v;
   int lo;
+  // the double evaluation only: lstm_act_lut_exceptions then writes the exception entries.
+  // Every StepParams member is named with a constant index (a run-time index into the
+  // kernel-argument struct would copy the whole struct to scratch memory per thread).
+  auto gate = [&](auto kc) {
+    constexpr int k = decltype(kc)::value;
+    v = real_act<false>(static_cast<float>(sp.gin[k].lo + (i - lut.off[k])), sp.gin[k],
+                        sp.gout[k], k == 2, sp, k, m);
+    lo = sp.gout[k].lo;
+  };
   if (lut.tanh_n > 0 && i >= lut.tanh_off) {
-    v = real_act(static_cast<float>(sp.c.lo + (i - lut.tanh_off)), sp.c, sp.tanh_c, true, sp, 4,
-                 m);
+    v = real_act<false>(static_cast<float>(sp.c.lo + (i - lut.tanh_off)), sp.c, sp.tanh_c, true,
+                        sp, 4, m);
     lo = sp.tanh_c.lo;
+  } else if (i < lut.off[1]) {
+    gate(std::integral_constant<int, 0>{});
+  } else if (i < lut.off[2]) {
+    gate(std::integral_constant<int, 1>{});
+  } else if (i < lut.off[3]) {
+    gate(std::integral_constant<int, 2>{});
   } else {
-    int g = 0;
-    while (g < 3 && i >= lut.off[g + 1]) ++g;
-    v = real_act(static_cast<float>(sp.gin[g].lo + (i - lut.off[g])), sp.gin[g], sp.gout[g],
-                 g == 2, sp, g, m);
-    lo = sp.gout[g].lo;
+    gate(std::integral_constant<int, 3>{});
   }
   table[i] = (static_cast<uint32_t>(static_cast<int>(v) - lo) << 1) | m;
+}
+
+// The reference's entries at the exception codes of the activations a table holds (one thread
+// per listed code; launched after lstm_build_act_lut on the same stream).
+__global__ __launch_bounds__(256) void lstm_act_lut_exceptions(StepParams sp, ActLut lut,
+                                                               uint32_t *table) {
+  int i = blockIdx.x * blockDim.x + threadIdx.x;
+#pragma unroll
+  for (int k = 0; k < 5; ++k) {
+    if (i < sp.exc_n[k]) {
+      const bool have = k < 4 ? lut.n[k] > 0 : lut.tanh_n > 0;
+      if (!have) return;
+      const int lo_in = k < 4 ? sp.gin[k].lo : sp.c.lo;
+      const int base = k < 4 ? lut.off[k] : lut.tanh_off;
+      table[base + (sp.exc_key[sp.exc_off[k] + i] - lo_in)] = sp.exc_val[sp.exc_off[k] + i];
+      return;
+    }
+    i -= sp.exc_n[k];
+  }
 }
 
 
@@ -691,13 +740,16 @@ __device__ __forceinline__ void flush_step(const RecArgs &a, const StepParams &s
   }
 }
 
-template <int NPL, bool EXC>
+// PW = 2: W_hh of up to 16 bits as two int8 planes, W = 256 bh + bl + 128 (lstm_pack_whh), so
+// sum_k W y = 256 sum bh y + sum bl y + 128 sum_k y for each h plane y; the row sums sum_k y come
+// from one more MFMA against a fragment of ones, and the planes are recombined in int64.
+template <int NPL, int PW, bool EXC>
 __global__ __launch_bounds__(512) void lstm_recurrence_cl(RecArgs a, StepParams sp,
                                                           ClusterArgs cl) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int H = a.H, C = 4 * H, B = a.B, KS = a.KS;
-  v4i *wl = reinterpret_cast<v4i *>(smem);                  // [4 gates][4 tiles][KS][64]
-  float *xg = reinterpret_cast<float *>(wl + 16 * KS * 64);  // [4 tiles][4 gates][16][16]
+  v4i *wl = reinterpret_cast<v4i *>(smem);                       // [PW][4 gates][4 tiles][KS][64]
+  float *xg = reinterpret_cast<float *>(wl + PW * 16 * KS * 64);  // [4 tiles][4 gates][16][16]
   // mask bits of a step (bit 0..2): gate phase [4 gates][16][64] (hh linear, gate in, gate out),
   // cell phase [16][64] (cell, cell tanh, hidden)
   uint8_t *gm = reinterpret_cast<uint8_t *>(xg + 4 * 4 * 16 * 16);
@@ -705,25 +757,31 @@ __global__ __launch_bounds__(512) void lstm_recurrence_cl(RecArgs a, StepParams 
   uint32_t *lut = reinterpret_cast<uint32_t *>(cm + 16 * kClUnits);  // [cl.lut.total]
   for (int i = threadIdx.x; i < cl.lut.total; i += blockDim.x) lut[i] = cl.lut.table[i];
   const bool gate_lut = cl.lut.n[0] > 0, tanh_lut = cl.lut.tanh_n > 0;
+  const bool gate_glut = cl.lut.gn[0] > 0, tanh_glut = cl.lut.gtanh_n > 0;
   const int tid = threadIdx.x, w = tid / 64, l = tid % 64;
   const int ut = w & 3, gp = w >> 2;
   const cluster::Place pl = cluster::place(cl.G, cl.ncl);
   const int u0 = pl.member * kClUnits;
   const int j = u0 + 16 * ut + l % 16;
   const int nrow0 = 4 * (l / 16);
-  for (int i = tid; i < 16 * KS * 64; i += blockDim.x) {
-    const int lane = i % 64, rest = i / 64, s = rest % KS, gt = rest / KS;
+  const size_t frag_plane = static_cast<size_t>(C / 16) * KS * 64;
+  for (int i = tid; i < PW * 16 * KS * 64; i += blockDim.x) {
+    const int pw = i / (16 * KS * 64), i1 = i % (16 * KS * 64);
+    const int lane = i1 % 64, rest = i1 / 64, s = rest % KS, gt = rest / KS;
     const int ct = (gt / 4) * a.UT + u0 / 16 + gt % 4;
-    wl[i] = a.frag[(static_cast<size_t>(ct) * KS + s) * 64 + lane];
+    wl[i] = a.frag[pw * frag_plane + (static_cast<size_t>(ct) * KS + s) * 64 + lane];
   }
   float4 cc[2];
+  int64_t hk64[2];
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
     const int c = (2 * gp + q) * H + j;
     const ChanRun r = a.run[c];
     const ChanHost h = a.ch[c];
     cc[q] = make_float4(h.hh_mult, r.hh_bacc, __int_as_float(r.hh_k), __int_as_float(h.hh_shift));
+    hk64[q] = (static_cast<int64_t>(r.hh_k_hi) << 32) | static_cast<uint32_t>(r.hh_k);
   }
+  const v4i ones = v4i{0x01010101, 0x01010101, 0x01010101, 0x01010101};
   unsigned *counter = cl.counters + pl.cluster;
   unsigned epoch = 0;
   bool alive = true;
@@ -766,17 +824,21 @@ __global__ __launch_bounds__(512) void lstm_recurrence_cl(RecArgs a, StepParams 
       const int par = t & 1;
       const unsigned hin_off = par * NPL * plane_stride;  // byte offset of the step's planes
       int8_t *hout = cl.hx + static_cast<size_t>(par ^ 1) * NPL * plane_stride;
-      v4i acc[2][NPL];
+      v4i acc[2][PW][NPL], rs[NPL];
 #pragma unroll
       for (int q = 0; q < 2; ++q)
 #pragma unroll
-        for (int p = 0; p < NPL; ++p) acc[q][p] = v4i{0, 0, 0, 0};
+        for (int pw = 0; pw < PW; ++pw)
+#pragma unroll
+          for (int p = 0; p < NPL; ++p) acc[q][pw][p] = v4i{0, 0, 0, 0};
+#pragma unroll
+      for (int p = 0; p < NPL; ++p) rs[p] = v4i{0, 0, 0, 0};
       if (NPL == 1 && kBT * (H + 16) <= static_cast<int>(sizeof(float)) * 4 * 4 * 16 * 16) {
         // The tile's h codes are read from the exchange buffer once per workgroup (one 16-byte
         // coherent load per thread and plane-chunk) into the gate exchange area, which is free
         // until the gate phase; the waves then take their A fragments from LDS.
         int8_t *hs = reinterpret_cast<int8_t *>(xg);
-        const int rs = H + 16, cpr = H / 16, n = NPL * kBT * cpr;
+        const int rst = H + 16, cpr = H / 16, n = NPL * kBT * cpr;
         int4 hv[2];
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
@@ -789,30 +851,39 @@ __global__ __launch_bounds__(512) void lstm_recurrence_cl(RecArgs a, StepParams 
           const int e = tid + 512 * i;
           if (e < n) {
             const int p = e / (kBT * cpr), r = (e / cpr) % kBT, c = e % cpr;
-            *reinterpret_cast<int4 *>(hs + (p * kBT + r) * rs + 16 * c) = hv[i];
+            *reinterpret_cast<int4 *>(hs + (p * kBT + r) * rst + 16 * c) = hv[i];
           }
         }
         __syncthreads();
-        const int8_t *arow = hs + (l % 16) * rs + 16 * (l / 16);
+        const int8_t *arow = hs + (l % 16) * rst + 16 * (l / 16);
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
           if (s < KS) {
+            v4i af[NPL];
 #pragma unroll
-            for (int q = 0; q < 2; ++q) {
-              const v4i bf = wl[(((2 * gp + q) * 4 + ut) * KS + s) * 64 + l];
+            for (int p = 0; p < NPL; ++p)
+              af[p] = *reinterpret_cast<const v4i *>(arow + p * kBT * rst + 64 * s);
 #pragma unroll
-              for (int p = 0; p < NPL; ++p)
-                acc[q][p] = mfma_i8(*reinterpret_cast<const v4i *>(arow + p * kBT * rs + 64 * s), bf,
-                                    acc[q][p]);
+            for (int q = 0; q < 2; ++q)
+#pragma unroll
+              for (int pw = 0; pw < PW; ++pw) {
+                const v4i bf = wl[((pw * 16 + (2 * gp + q) * 4 + ut) * KS + s) * 64 + l];
+#pragma unroll
+                for (int p = 0; p < NPL; ++p) acc[q][pw][p] = mfma_i8(af[p], bf, acc[q][pw][p]);
+              }
+            if constexpr (PW == 2) {
+#pragma unroll
+              for (int p = 0; p < NPL; ++p) rs[p] = mfma_i8(af[p], ones, rs[p]);
             }
           }
         }
         __syncthreads();  // the gate phase rewrites the area
       } else {
-        // all of the step's h fragments in flight at once (KS <= 8)
-        v4i hfr[8][NPL];
+        // all of the step's h fragments in flight at once (KS <= 8; <= 4 with two W planes)
+        constexpr int kKS = PW == 2 ? 4 : 8;
+        v4i hfr[kKS][NPL];
 #pragma unroll
-        for (int s = 0; s < 8; ++s)
+        for (int s = 0; s < kKS; ++s)
 #pragma unroll
           for (int p = 0; p < NPL; ++p)
             if (s < KS) {
@@ -821,13 +892,20 @@ __global__ __launch_bounds__(512) void lstm_recurrence_cl(RecArgs a, StepParams 
               hfr[s][p] = v4i{v.x, v.y, v.z, v.w};
             }
 #pragma unroll
-        for (int s = 0; s < 8; ++s) {
+        for (int s = 0; s < kKS; ++s) {
           if (s < KS) {
 #pragma unroll
-            for (int q = 0; q < 2; ++q) {
-              const v4i bf = wl[(((2 * gp + q) * 4 + ut) * KS + s) * 64 + l];
+            for (int q = 0; q < 2; ++q)
 #pragma unroll
-              for (int p = 0; p < NPL; ++p) acc[q][p] = mfma_i8(hfr[s][p], bf, acc[q][p]);
+              for (int pw = 0; pw < PW; ++pw) {
+                const v4i bf = wl[((pw * 16 + (2 * gp + q) * 4 + ut) * KS + s) * 64 + l];
+#pragma unroll
+                for (int p = 0; p < NPL; ++p)
+                  acc[q][pw][p] = mfma_i8(hfr[s][p], bf, acc[q][pw][p]);
+              }
+            if constexpr (PW == 2) {
+#pragma unroll
+              for (int p = 0; p < NPL; ++p) rs[p] = mfma_i8(hfr[s][p], ones, rs[p]);
             }
           }
         }
@@ -848,19 +926,35 @@ __global__ __launch_bounds__(512) void lstm_recurrence_cl(RecArgs a, StepParams 
             const Grid &gin = q == 0 ? sp.gin[g0] : sp.gin[g0 + 1];
             const Grid &gout = q == 0 ? sp.gout[g0] : sp.gout[g0 + 1];
             const Rescale &h2g = q == 0 ? sp.hh_to_gate[g0] : sp.hh_to_gate[g0 + 1];
-            int v = pick(acc[q][0], r);
-            if constexpr (NPL == 2) v += 256 * pick(acc[q][NPL - 1], r);
-            v += __float_as_int(cc[q].z);
-            const float accf = static_cast<float>(v) + cc[q].y;
+            float accf;
+            if constexpr (PW == 1) {
+              int v = pick(acc[q][0][0], r);
+              if constexpr (NPL == 2) v += 256 * pick(acc[q][0][NPL - 1], r);
+              v += __float_as_int(cc[q].z);
+              accf = static_cast<float>(v) + cc[q].y;
+            } else {
+              int64_t v = hk64[q];
+#pragma unroll
+              for (int p = 0; p < NPL; ++p) {
+                const int64_t sp_ = 256 * static_cast<int64_t>(pick(acc[q][1][p], r)) +
+                                    pick(acc[q][0][p], r) + 128 * static_cast<int64_t>(pick(rs[p], r));
+                v += p == 0 ? sp_ : 256 * sp_;
+              }
+              accf = static_cast<float>(v) + cc[q].y;
+            }
             uint8_t m_hl, m_gi, m_go;
             const float lin = clamp_grid_f(rescale(accf, cc[q].x, __float_as_int(cc[q].w)),
                                            sp.hh_lin, m_hl);
             const float rhs = rescale(center_f(lin, sp.hh_lin.zp), h2g.mult, h2g.shift);
             const float gi = clamp_grid_f(lh[q][r] + rhs, gin, m_gi);
             const float go =
-                gate_lut ? lut_code(lut + (q == 0 ? cl.lut.off[g0] : cl.lut.off[g0 + 1]),
-                                    static_cast<int>(gi) - gin.lo, gout.lo, m_go)
-                         : real_act<EXC>(gi, gin, gout, g == 2, sp, g, m_go);
+                gate_lut
+                    ? lut_code(lut + (q == 0 ? cl.lut.off[g0] : cl.lut.off[g0 + 1]),
+                               static_cast<int>(gi) - gin.lo, gout.lo, m_go)
+                    : (gate_glut
+                           ? lut_code(cl.lut.gtable + (q == 0 ? cl.lut.goff[g0] : cl.lut.goff[g0 + 1]),
+                                      static_cast<int>(gi) - gin.lo, gout.lo, m_go)
+                           : real_act<EXC>(gi, gin, gout, g == 2, sp, g, m_go));
             xg[((ut * 4 + g) * 16 + nr) * 16 + l % 16] = go;
             if (a.wide_out) {
               if (train)
@@ -898,7 +992,9 @@ __global__ __launch_bounds__(512) void lstm_recurrence_cl(RecArgs a, StepParams 
         cts[rr] =
             tanh_lut ? lut_code(lut + cl.lut.tanh_off, static_cast<int>(cn) - sp.c.lo,
                                 sp.tanh_c.lo, mts[rr])
-                     : real_act<EXC>(cn, sp.c, sp.tanh_c, true, sp, 4, mts[rr]);
+                     : (tanh_glut ? lut_code(cl.lut.gtable + cl.lut.gtanh_off,
+                                             static_cast<int>(cn) - sp.c.lo, sp.tanh_c.lo, mts[rr])
+                                  : real_act<EXC>(cn, sp.c, sp.tanh_c, true, sp, 4, mts[rr]));
         const float raw = center_f(gout[3], sp.gout[3].zp) * center_f(cts[rr], sp.tanh_c.zp);
         hvs[rr] = clamp_grid_f(rescale(raw, sp.hidden.mult, sp.hidden.shift), sp.h, mhs[rr]);
         if (a.wide_out && train)
@@ -954,8 +1050,8 @@ __global__ __launch_bounds__(512) void lstm_recurrence_cl(RecArgs a, StepParams 
   }
 }
 
-size_t recurrence_cl_lds(int KS, int lut_entries) {
-  return sizeof(v4i) * 16 * static_cast<size_t>(KS) * 64 + sizeof(float) * 4 * 4 * 16 * 16 +
+size_t recurrence_cl_lds(int KS, int pw, int lut_entries) {
+  return sizeof(v4i) * pw * 16 * static_cast<size_t>(KS) * 64 + sizeof(float) * 4 * 4 * 16 * 16 +
          5 * 16 * kClUnits + sizeof(uint32_t) * static_cast<size_t>(lut_entries);
 }
 
@@ -980,15 +1076,15 @@ size_t recurrence_lds(int H, int KS, int npl) {
 }
 
 struct FwdWorkspace {
-  size_t chost, run, frag, lhs, xq, wih, whh, bih, bhh, h0q, c0q, hx, sync, lut, exc, xa, bfrag,
-      colsum, sh, sc, sg, total;
+  size_t chost, run, frag, lhs, xq, wih, whh, bih, bhh, h0q, c0q, hx, sync, lut, glut, exc, xa,
+      bfrag, colsum, sh, sc, sg, total;
   FwdWorkspace(int T, int B, int I, int H) {
     const size_t C = 4 * static_cast<size_t>(H), KS = (H + 63) / 64;
     auto al = [](size_t x) { return (x + 255) & ~static_cast<size_t>(255); };
     size_t o = 0;
     chost = o; o += al(sizeof(ChanHost) * C);
     run = o; o += al(sizeof(ChanRun) * C);
-    frag = o; o += al(sizeof(v4i) * 64 * (C / 16) * KS);
+    frag = o; o += al(sizeof(v4i) * 64 * (C / 16) * KS * 2);  // up to two W_hh planes
     lhs = o; o += al(sizeof(float) * static_cast<size_t>(T) * B * C);
     // codes used internally when the caller keeps no checkpoints
     xq = o; o += al(sizeof(float) * static_cast<size_t>(T) * B * I);
@@ -1003,6 +1099,7 @@ struct FwdWorkspace {
     hx = o; o += al(2 * 2 * Bpad * H);
     sync = o; o += al(sizeof(unsigned) * (Bpad / 16 + 1));
     lut = o; o += al(sizeof(uint32_t) * 2 * kLutMaxEntries);
+    glut = o; o += al(sizeof(uint32_t) * 5 * static_cast<size_t>(kGlobalLutMaxCodes));
     // reference activation exceptions: keys, then entries, of at most 5 full 16-bit grids
     exc = o; o += al(sizeof(int32_t) * 2 * 5 * static_cast<size_t>(kActExcMaxCodes));
     // packed operands of the input linear (I <= 256): x planes, W_ih fragments, column sums
@@ -1072,10 +1169,17 @@ int rxmet_lstm_forward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const f
   const Grid gwh_t = grid_of(params->config.op[RXMET_LSTM_W_HH], 1.0f, 0);
   RXMET_CHECK_ARG(xgemm::b_fits(gwh_t.lo, gwh_t.hi), "W_hh codes must fit signed 16 bits");
   RXMET_CHECK_ARG(xgemm::a_fits(sp.h.lo, sp.h.hi), "h codes must span at most 16 bits");
-  // the MFMA recurrences hold W_hh as int8 fragments, keep at most 512 units per batch tile and
-  // sum in int32; anything else steps
-  const bool stepped = xgemm::b_planes(gwh_t.lo, gwh_t.hi) > 1 || H > kMaxH ||
-                       !(std::ldexp(1.0, h_t.bits) * 128.0 * H < 2147483647.0) ||
+  // the MFMA recurrences hold W_hh as int8 fragments and keep at most 512 units per batch tile;
+  // one W_hh plane sums in int32; two planes (W_hh of 9-16 bits) only in the clustered
+  // recurrence, for H a multiple of 64 up to 256 (both planes resident in LDS), summed in int64;
+  // anything else steps
+  const int pw = xgemm::b_planes(gwh_t.lo, gwh_t.hi);
+  bool f32_grids = fits_f32(sp.hh_lin) && fits_f32(sp.c) && fits_f32(sp.tanh_c) && fits_f32(sp.h);
+  for (int g = 0; g < 4; ++g) f32_grids = f32_grids && fits_f32(sp.gin[g]) && fits_f32(sp.gout[g]);
+  const bool may_cluster = H % kClUnits == 0 && f32_grids &&
+                           std::getenv("RXMET_NO_CLUSTER") == nullptr;
+  const bool stepped = (pw > 1 && !(may_cluster && H <= 256)) || H > kMaxH ||
+                       (pw == 1 && !(std::ldexp(1.0, h_t.bits) * 128.0 * H < 2147483647.0)) ||
                        std::getenv("RXMET_LSTM_STEPPED") != nullptr;
 
   hipStream_t stream = static_cast<hipStream_t>(stream_);
@@ -1085,10 +1189,8 @@ int rxmet_lstm_forward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const f
   if (!exc.key.empty()) {
     int32_t *ek = reinterpret_cast<int32_t *>(wsb + ws.exc);
     uint32_t *ev = reinterpret_cast<uint32_t *>(ek + 5 * static_cast<size_t>(kActExcMaxCodes));
-    RXMET_CHECK_HIP(hipMemcpyAsync(ek, exc.key.data(), sizeof(int32_t) * exc.key.size(),
-                                   hipMemcpyHostToDevice, stream));
-    RXMET_CHECK_HIP(hipMemcpyAsync(ev, exc.val.data(), sizeof(uint32_t) * exc.val.size(),
-                                   hipMemcpyHostToDevice, stream));
+    if (int rc = upload(ek, exc.key.data(), sizeof(int32_t) * exc.key.size(), stream)) return rc;
+    if (int rc = upload(ev, exc.val.data(), sizeof(uint32_t) * exc.val.size(), stream)) return rc;
     sp.exc_key = ek;
     sp.exc_val = ev;
     for (int k = 0; k < 5; ++k) {
@@ -1116,8 +1218,7 @@ int rxmet_lstm_forward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const f
   ChanRun *run = reinterpret_cast<ChanRun *>(wsb + ws.run);
   v4i *frag = reinterpret_cast<v4i *>(wsb + ws.frag);
   float *lhs = reinterpret_cast<float *>(wsb + ws.lhs);
-  RXMET_CHECK_HIP(hipMemcpyAsync(chost, hostc.data(), sizeof(ChanHost) * C, hipMemcpyHostToDevice,
-                                 stream));
+  if (int rc = upload(chost, hostc.data(), sizeof(ChanHost) * C, stream)) return rc;
   const rxmet_lstm_saved sv = saved ? *saved : rxmet_lstm_saved{};
   float *xq = saved ? sv.x_q : reinterpret_cast<float *>(wsb + ws.xq);
   float *wih = saved ? sv.w_ih_q : reinterpret_cast<float *>(wsb + ws.wih);
@@ -1151,7 +1252,8 @@ int rxmet_lstm_forward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const f
                      nx, nh, x, h0, c0, sp, xq, sv.x_m, h0q, sv.h0_m, c0q, sv.c0_m);
   RXMET_CHECK_LAUNCH();
   if (!stepped) {
-    hipLaunchKernelGGL(lstm_pack_whh, dim3((C / 16) * KS), dim3(64), 0, stream, H, KS, whh, frag);
+    hipLaunchKernelGGL(lstm_pack_whh, dim3((C / 16) * KS), dim3(64), 0, stream, H, KS, pw,
+                       static_cast<size_t>(C / 16) * KS * 64, whh, frag);
     RXMET_CHECK_LAUNCH();
   }
   const int M = T * B;
@@ -1225,7 +1327,7 @@ int rxmet_lstm_forward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const f
              a16(ra.cell_tanh_m) && a16(ra.hidden_m);
     ra.wide_out = wide ? 1 : 0;
   }
-  if (stepped) {
+  auto run_stepped = [&]() -> int {
     float *hb = reinterpret_cast<float *>(wsb + ws.sh);
     float *cs = reinterpret_cast<float *>(wsb + ws.sc);
     float *ghh = reinterpret_cast<float *>(wsb + ws.sg);
@@ -1260,26 +1362,31 @@ int rxmet_lstm_forward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const f
       cin = cs;
     }
     return 0;
-  }
-  bool f32_grids = fits_f32(sp.hh_lin) && fits_f32(sp.c) && fits_f32(sp.tanh_c) && fits_f32(sp.h);
-  for (int g = 0; g < 4; ++g) f32_grids = f32_grids && fits_f32(sp.gin[g]) && fits_f32(sp.gout[g]);
-  if (H % kClUnits == 0 && f32_grids) {
+  };
+  if (stepped) return run_stepped();
+  if (may_cluster) {
     // clustered path when the whole grid can be resident at once
     const bool has_exc = !exc.key.empty();
-    const void *fn =
-        npl == 1 ? (has_exc ? reinterpret_cast<const void *>(&lstm_recurrence_cl<1, true>)
-                            : reinterpret_cast<const void *>(&lstm_recurrence_cl<1, false>))
-                 : (has_exc ? reinterpret_cast<const void *>(&lstm_recurrence_cl<2, true>)
-                            : reinterpret_cast<const void *>(&lstm_recurrence_cl<2, false>));
+    const void *fns[2][2][2] = {
+        {{reinterpret_cast<const void *>(&lstm_recurrence_cl<1, 1, false>),
+          reinterpret_cast<const void *>(&lstm_recurrence_cl<1, 1, true>)},
+         {reinterpret_cast<const void *>(&lstm_recurrence_cl<1, 2, false>),
+          reinterpret_cast<const void *>(&lstm_recurrence_cl<1, 2, true>)}},
+        {{reinterpret_cast<const void *>(&lstm_recurrence_cl<2, 1, false>),
+          reinterpret_cast<const void *>(&lstm_recurrence_cl<2, 1, true>)},
+         {reinterpret_cast<const void *>(&lstm_recurrence_cl<2, 2, false>),
+          reinterpret_cast<const void *>(&lstm_recurrence_cl<2, 2, true>)}}};
+    const void *fn = fns[npl - 1][pw - 1][has_exc ? 1 : 0];
     ActLut lut{};
     uint32_t *lut_table = reinterpret_cast<uint32_t *>(wsb + ws.lut);
+    int dev_lds = 0;
     {
-      int dev_lds = 0, dev = 0;
+      int dev = 0;
       RXMET_CHECK_HIP(hipGetDevice(&dev));
       RXMET_CHECK_HIP(hipDeviceGetAttribute(&dev_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev));
       // table entries that fit beside the resident weights and the gate exchange
       const int64_t room = (static_cast<int64_t>(dev_lds) -
-                            static_cast<int64_t>(recurrence_cl_lds(KS, 0))) / 4;
+                            static_cast<int64_t>(recurrence_cl_lds(KS, pw, 0))) / 4;
       int64_t n[4], tot = 0;
       for (int g = 0; g < 4; ++g) {
         n[g] = static_cast<int64_t>(sp.gin[g].hi) - sp.gin[g].lo + 1;
@@ -1300,8 +1407,29 @@ int rxmet_lstm_forward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const f
         lut.total += lut.tanh_n;
       }
       lut.table = lut_table;
+      // global tables for what LDS does not hold
+      bool gates_fit = lut.n[0] == 0;
+      for (int g = 0; g < 4; ++g) gates_fit = gates_fit && n[g] <= kGlobalLutMaxCodes;
+      if (gates_fit) {
+        for (int g = 0, o = 0; g < 4; ++g) {
+          lut.goff[g] = o;
+          lut.gn[g] = static_cast<int>(n[g]);
+          o += lut.gn[g];
+        }
+        lut.gtotal = static_cast<int>(tot);
+      }
+      if (lut.tanh_n == 0 && nc <= kGlobalLutMaxCodes && exc.n[4] > 0) {
+        lut.gtanh_off = lut.gtotal;
+        lut.gtanh_n = static_cast<int>(nc);
+        lut.gtotal += lut.gtanh_n;
+      }
+      lut.gtable = reinterpret_cast<uint32_t *>(wsb + ws.glut);
     }
-    const size_t lds_cl = recurrence_cl_lds(KS, lut.total);
+    const size_t lds_cl = recurrence_cl_lds(KS, pw, lut.total);
+    if (static_cast<int64_t>(lds_cl) > dev_lds) {
+      RXMET_CHECK_ARG(pw == 2, "clustered recurrence does not fit in LDS");
+      return run_stepped();  // the two W_hh planes do not fit beside the exchange areas
+    }
     int device = 0, ncu = 0, per_cu = 0;
     RXMET_CHECK_HIP(hipGetDevice(&device));
     RXMET_CHECK_HIP(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, device));
@@ -1325,10 +1453,35 @@ int rxmet_lstm_forward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const f
       cl.lut = lut;
       hipLaunchKernelGGL(cluster::zero_words, dim3(1), dim3(256), 0, stream, cl.counters, ncl + 1);
       RXMET_CHECK_LAUNCH();
+      const int n_exc = static_cast<int>(exc.key.size());
       if (lut.total > 0) {
         hipLaunchKernelGGL(lstm_build_act_lut, dim3((lut.total + 255) / 256), dim3(256), 0, stream,
                            sp, lut, lut_table);
         RXMET_CHECK_LAUNCH();
+        if (n_exc > 0) {
+          hipLaunchKernelGGL(lstm_act_lut_exceptions, dim3((n_exc + 255) / 256), dim3(256), 0,
+                             stream, sp, lut, lut_table);
+          RXMET_CHECK_LAUNCH();
+        }
+      }
+      if (lut.gtotal > 0) {  // the builder on the global tables' layout
+        ActLut gl{};
+        for (int g = 0; g < 4; ++g) {
+          gl.off[g] = lut.goff[g];
+          gl.n[g] = lut.gn[g];
+        }
+        gl.tanh_off = lut.gtanh_off;
+        gl.tanh_n = lut.gtanh_n;
+        gl.total = lut.gtotal;
+        uint32_t *gt = reinterpret_cast<uint32_t *>(wsb + ws.glut);
+        hipLaunchKernelGGL(lstm_build_act_lut, dim3((gl.total + 255) / 256), dim3(256), 0, stream,
+                           sp, gl, gt);
+        RXMET_CHECK_LAUNCH();
+        if (n_exc > 0) {
+          hipLaunchKernelGGL(lstm_act_lut_exceptions, dim3((n_exc + 255) / 256), dim3(256), 0,
+                             stream, sp, gl, gt);
+          RXMET_CHECK_LAUNCH();
+        }
       }
       void *args[] = {&ra, &sp, &cl};
       {
@@ -1343,6 +1496,7 @@ int rxmet_lstm_forward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const f
       return 0;
     }
   }
+  if (pw == 2) return run_stepped();  // the per-tile recurrence holds one W_hh plane
   const size_t lds = recurrence_lds(H, KS, npl);
   const dim3 grid((B + kBT - 1) / kBT), block(64 * ((UT + kTilesPerWave - 1) / kTilesPerWave));
   {

@@ -20,6 +20,10 @@ struct Status {
   int code = 0;
 };
 
+// Asynchronous host -> device copy of a small per-call table (through pinned staging; the
+// source may be reused as soon as the call returns).  0 or a negative error (message set).
+int upload(void *dst, const void *src, size_t bytes, hipStream_t stream);
+
 namespace prof {
 // Brackets the launches made during its lifetime with a pair of hipEvents on `stream`
 // when event timing is enabled (rxmet_prof_enable); `name` must be a string literal.

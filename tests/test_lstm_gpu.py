@@ -53,6 +53,9 @@ def _config(name):
                   "weight_hh"):
             c.op[L.OP[n]].bits = 16
         return c
+    if name == "whh16-h8":  # 16-bit W_hh, everything else 8-bit (one h plane)
+        c.op[L.OP["weight_hh"]].bits = 16
+        return c
     if name == "16b-act":  # 16-bit activations and state, 8-bit per-tensor parameters
         for k in range(L.NOPS):
             if L.OP_NAMES[k] in L.PARAM_OPS:
@@ -384,6 +387,30 @@ def test_clustered_recurrence_matches_oracle_and_single_tile_path(cuda, shape, c
     o = O.forward_quant(Wi, Wh, bi, bh, x, p, h0, c0, mode=O.ACT_LIBM_EXACT)
     _compare_forward(o, out, hn, cn, saved, True)
     monkeypatch.setenv("RXMET_NO_CLUSTER", "1")
+    out2, hn2, cn2, saved2 = _gpu_forward(cuda, args, p, True)
+    assert torch.equal(out, out2) and torch.equal(hn, hn2) and torch.equal(cn, cn2)
+    for k in saved:
+        assert torch.equal(saved[k], saved2[k]), k
+
+
+@pytest.mark.parametrize("shape,cfg_name", [((4, 36, 9, 128), "16b-whh"), ((3, 70, 8, 256), "16b-whh"),
+                                            ((3, 40, 8, 64), "mixed-8-16"),
+                                            ((3, 50, 12, 192), "whh16-h8"),
+                                            ((3, 300, 8, 128), "whh16-h8")])
+def test_clustered_recurrence_with_16bit_recurrent_weights(cuda, shape, cfg_name, monkeypatch):
+    """W_hh of 9-16 bits in the clustered recurrence (two int8 planes resident in LDS, H a
+    multiple of 64 up to 256, sums recombined in int64): forward and saved tensors bit-exact
+    against the oracle and against the stepped recurrence, inference equal to training."""
+    T, B, I, H = shape
+    print(f"[lstm cl 16-bit W_hh] shape={shape} cfg={cfg_name}", flush=True)
+    args, _, p = _case(T, B, I, H, cfg_name, 47, True, True)
+    Wi, Wh, bi, bh, x, h0, c0 = args
+    out, hn, cn, saved = _gpu_forward(cuda, args, p, True)
+    o = O.forward_quant(Wi, Wh, bi, bh, x, p, h0, c0, mode=O.ACT_LIBM_EXACT)
+    _compare_forward(o, out, hn, cn, saved, True)
+    oi, hi, ci, _ = _gpu_forward(cuda, args, p, False)
+    assert torch.equal(out, oi) and torch.equal(hn, hi) and torch.equal(cn, ci)
+    monkeypatch.setenv("RXMET_LSTM_STEPPED", "1")
     out2, hn2, cn2, saved2 = _gpu_forward(cuda, args, p, True)
     assert torch.equal(out, out2) and torch.equal(hn, hn2) and torch.equal(cn, cn2)
     for k in saved:
