@@ -64,6 +64,40 @@ def _compile(src: Path) -> Path:
     return obj
 
 
+# ONNX Runtime headers for the QcQuantizeOp plugin (librxmet_ort_ops.so): $RXMET_ORT_INCLUDE, or
+# the copy vendored in the reference checkout.  The plugin is built only where they exist.
+ORT_INCLUDE_DEFAULT = "/root/reference/docker/environment/third_party/onnxruntime/include"
+ORT_LIB = PKG / "librxmet_ort_ops.so"
+
+
+def ort_include() -> Path | None:
+    cand = Path(os.environ.get("RXMET_ORT_INCLUDE", ORT_INCLUDE_DEFAULT))
+    return cand if (cand / "onnxruntime_lite_custom_op.h").is_file() else None
+
+
+def build_ort_ops(verbose: bool = True) -> Path | None:
+    """The ONNX Runtime plugin over librxmet.so (host code only, g++), when ORT's headers are
+    available; returns its path or None."""
+    inc = ort_include()
+    if inc is None:
+        if verbose:
+            print("ONNX Runtime headers not found; librxmet_ort_ops.so not rebuilt")
+        return None
+    tmp = ORT_LIB.with_suffix(".so.tmp")
+    cmd = [shutil.which("g++") or "g++", "-std=c++17", "-O2", "-fPIC", "-shared", "-Wall",
+           f"-I{inc}", f"-I{ROOT / 'include'}", "-o", str(tmp),
+           str(PKG / "ort" / "qc_quantize_op.cpp"), f"-L{PKG}", "-lrxmet",
+           "-Wl,-rpath,$ORIGIN", "-Wl,--no-undefined"]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"ORT plugin build failed: {' '.join(cmd)}\n{proc.stdout}\n"
+                           f"{proc.stderr}")
+    os.replace(tmp, ORT_LIB)
+    if verbose:
+        print(f"built {ORT_LIB}")
+    return ORT_LIB
+
+
 def build(verbose: bool = True) -> Path:
     BUILD.mkdir(exist_ok=True)
     sources = sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.cpp")))
@@ -81,6 +115,7 @@ def build(verbose: bool = True) -> Path:
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB} from {len(sources)} sources")
+    build_ort_ops(verbose)
     return LIB
 
 

@@ -429,7 +429,7 @@ static int backward_impl(int op, const void *x, const void *g, void *dx, float *
 }
 
 static int minmax_impl(const void *x, int32_t io, const rxmet_qdq_layout *l, float *out_min,
-                       float *out_max, void *workspace, void *stream) {
+                       float *out_max, void *workspace, void *stream, bool skip_nan = false) {
   RXMET_CHECK_ARG(l != nullptr, "layout must be non-null");
   if (int rc = check_layout(l->outer, l->C0, l->mid, l->C1, l->inner)) return rc;
   RXMET_CHECK_ARG(is_io(io), "io_dtype must be RXMET_QDQ_F32, F16 or BF16");
@@ -443,11 +443,33 @@ static int minmax_impl(const void *x, int32_t io, const rxmet_qdq_layout *l, flo
   rxmet_qdq_numerics nm{io, io, 0.0, 0, 0};
   const Call c{&p, OP_QDQ_LEARN, nm.internal_dtype, x, nullptr, nullptr, nullptr, nullptr,
                make_params(0, 0, nm), workspace, s};
-  if (int rc = dispatch(c, io, WHAT_MINMAX)) return rc;
+  if (int rc = dispatch(c, io, skip_nan ? WHAT_MINMAX_SKIP_NAN : WHAT_MINMAX)) return rc;
   launch_fold_minmax(static_cast<const MinMax *>(workspace), p.fold, l->C0 * l->C1, out_min,
                      out_max, s);
   RXMET_CHECK_LAUNCH();
   return 0;
+}
+
+// Shared with the ONNX Runtime op core (qc_quantize.hip).
+int minmax_stats(const void *x, int32_t io, const rxmet_qdq_layout &l, float *out_min,
+                 float *out_max, void *workspace, hipStream_t s) {
+  return minmax_impl(x, io, &l, out_min, out_max, workspace, s, true);
+}
+
+int forward_tf(int op, const void *x, void *y, int32_t io, const rxmet_qdq_layout &l,
+               const TfEnc32 *enc, hipStream_t s) {
+  RXMET_CHECK_ARG(op == OP_NATIVE || op == OP_FP16, "forward_tf: OP_NATIVE or OP_FP16");
+  RXMET_CHECK_ARG(io == RXMET_QDQ_F32 || io == RXMET_QDQ_F16, "io_dtype must be F32 or F16");
+  if (int rc = check_layout(l.outer, l.C0, l.mid, l.C1, l.inner)) return rc;
+  RXMET_CHECK_ARG(op == OP_FP16 || enc != nullptr, "encodings must be non-null");
+  const Plan p = make_plan(l.outer, l.C0, l.mid, l.C1, l.inner, esize_of(io), kVecQdq);
+  if (p.n == 0) return 0;
+  RXMET_CHECK_ARG(x != nullptr && y != nullptr, "input/output must be non-null");
+  const rxmet_qdq_numerics nm{io, RXMET_QDQ_F32, 0.0, 0, 0};
+  const Call c{&p, op, RXMET_QDQ_F32, x, nullptr, y, reinterpret_cast<const float *>(enc),
+               nullptr, make_params(0, 0, nm), nullptr, s, MinMaxSrc{}};
+  rxmet::prof::Scope ps__(op == OP_NATIVE ? "qc_qdq_native" : "qc_qdq_fp16", s);
+  return dispatch(c, io, WHAT_FORWARD);
 }
 
 // The three-argument fp32 layout [outer, C, inner] of the original entry points.

@@ -36,7 +36,16 @@
 namespace rxmet {
 namespace qdq {
 
-enum Op { OP_QDQ_LEARN = 0, OP_QDQ_FROZEN = 1, OP_Q = 2, OP_DQ = 3 };
+// OP_NATIVE: the libpymo form stableQuantizeDequantize (quantize_dequantize.hpp:35-46) on a
+// TfEncoding, as the ONNX Runtime custom op runs it (trim_functions.cpp:646-668).  OP_FP16:
+// the float16 round trip of a float quantizer (AimetOpUtils.cpp:60-66).  Forward only.
+enum Op { OP_QDQ_LEARN = 0, OP_QDQ_FROZEN = 1, OP_Q = 2, OP_DQ = 3, OP_NATIVE = 4, OP_FP16 = 5 };
+
+// One TfEncoding as OP_NATIVE reads it: min, max and delta rounded to fp32 (the reference
+// casts the double encoding to the tensor type) and the correctly rounded fp32 1 / delta.
+struct alignas(16) TfEnc32 {
+  float mn, mx, delta, inv_delta;
+};
 
 constexpr int kThreads = 256;
 // 16-byte vectors per thread per chunk (runs decomposition), per kind of pass.  Measured on
@@ -64,8 +73,13 @@ struct bf16_t {
 __device__ __forceinline__ float f16_to_f(uint32_t b) {
   return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(b)));
 }
+// Round an fp32 value to fp16, nearest even.  The empty asm makes v an fp32 register first:
+// without it the compiler folds the multiply or fma that produced v into the conversion
+// (v_fma_mixlo_f16), which rounds the exact result to fp16 once instead of rounding it to
+// fp32 and then to fp16 as the reference does — different on fp16 ties.
 __device__ __forceinline__ uint32_t f_to_f16(float v) {
-  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));  // round to nearest even
+  __asm__("" : "+v"(v));
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
 }
 __device__ __forceinline__ float bf16_to_f(uint32_t b) {
   return __builtin_bit_cast(float, (b & 0xFFFFu) << 16);
@@ -290,6 +304,14 @@ __device__ __forceinline__ float fwd_elem(float x, const typename Elem<T, R>::En
   } else if constexpr (OP == OP_Q) {
     const A t = El::r(A(x) / e.s);
     return static_cast<float>(clamp_a(El::r(rint_a(t) - e.o), e.qmin, e.qmax));
+  } else if constexpr (OP == OP_NATIVE) {
+    // NaN kept; clip in value space (fmax(fmin(v, max), min)); times fl(1 / delta); round
+    // half to even; times delta
+    if (x != x) return x;
+    const float c = fmaxf(fminf(x, e.hi), e.lo);
+    return rintf(c * e.inv_s) * e.fs;
+  } else if constexpr (OP == OP_FP16) {
+    return static_cast<float>(static_cast<_Float16>(x));  // round to nearest even, and back
   } else {
     return static_cast<float>(El::r(El::r(A(x) + e.o) * e.s));
   }
@@ -395,7 +417,22 @@ struct FwdW {
   Params p;
   MinMaxSrc mm;
 
-  __device__ Enc enc(int64_t c) const { return El::enc(scale, offset, mm, c, p); }
+  __device__ Enc enc(int64_t c) const {
+    if constexpr (OP == OP_NATIVE) {
+      // `scale` holds the TfEnc32 array of the launch
+      const TfEnc32 t = reinterpret_cast<const TfEnc32 *>(scale)[c];
+      Enc e{};
+      e.lo = t.mn;
+      e.hi = t.mx;
+      e.fs = t.delta;
+      e.inv_s = t.inv_delta;
+      return e;
+    } else if constexpr (OP == OP_FP16) {
+      return Enc{};
+    } else {
+      return El::enc(scale, offset, mm, c, p);
+    }
+  }
   __device__ static Acc zero() { return Sum2{0.0, 0.0}; }
   __device__ void elem(const Enc &e, int64_t i, Acc &) const {
     Io<T>::st(y, i, fwd_elem<OP, T, R>(Io<T>::ld(x, i), e, p));
@@ -484,7 +521,10 @@ struct BwdW {
   }
 };
 
-template <typename T>
+// SKIP_NAN: NaN never replaces a running value, as the reference's CPU statistics
+// (math_functions.cpp:356-375: val = min(val, x) from +-max) — a block of NaN only keeps
+// +inf / -inf.  Otherwise NaN propagates (torch.aminmax).
+template <typename T, bool SKIP_NAN = false>
 struct MinMaxW {
   struct Enc {};
   using Acc = MinMax;
@@ -496,8 +536,13 @@ struct MinMaxW {
   __device__ Enc enc(int64_t) const { return Enc{}; }
   __device__ static Acc zero() { return MinMax{INFINITY, -INFINITY}; }
   __device__ static void take(Acc &acc, float v) {
-    acc.mn = nan_min(acc.mn, v);
-    acc.mx = nan_max(acc.mx, v);
+    if constexpr (SKIP_NAN) {
+      acc.mn = v < acc.mn ? v : acc.mn;
+      acc.mx = acc.mx < v ? v : acc.mx;
+    } else {
+      acc.mn = nan_min(acc.mn, v);
+      acc.mx = nan_max(acc.mx, v);
+    }
   }
   __device__ void elem(const Enc &, int64_t i, Acc &acc) const { take(acc, Io<T>::ld(x, i)); }
   __device__ static void take_vec(const u4 &v, Acc &acc) {
@@ -715,18 +760,24 @@ static int run_backward(const Call &c) {
   return launch_decomp(*c.plan, w, al, nullptr, c.stream);
 }
 
-template <typename T>
+template <typename T, bool SKIP_NAN>
 static int run_minmax(const Call &c) {
-  MinMaxW<T> w{static_cast<const T *>(c.x)};
+  MinMaxW<T, SKIP_NAN> w{static_cast<const T *>(c.x)};
   return launch_decomp(*c.plan, w, aligned16(c.x), c.partial, c.stream);
 }
 
-enum What { WHAT_FORWARD = 0, WHAT_BACKWARD = 1, WHAT_MINMAX = 2 };
+enum What { WHAT_FORWARD = 0, WHAT_BACKWARD = 1, WHAT_MINMAX = 2, WHAT_MINMAX_SKIP_NAN = 3 };
 
 // The internal types each io type pairs with: R = T, fp32 or fp64 (fp32 io: fp32, fp64).
 template <typename T>
 static int run_typed(const Call &c, int what) {
-  if (what == WHAT_MINMAX) return run_minmax<T>(c);
+  if (what == WHAT_MINMAX) return run_minmax<T, false>(c);
+  if (what == WHAT_MINMAX_SKIP_NAN) return run_minmax<T, true>(c);
+  if (c.op == OP_NATIVE || c.op == OP_FP16) {  // fp32 arithmetic, forward only
+    if (what != WHAT_FORWARD) return -22;
+    return c.op == OP_NATIVE ? run_forward<OP_NATIVE, T, float>(c)
+                             : run_forward<OP_FP16, T, float>(c);
+  }
   auto go = [&](auto rtag) -> int {
     using R = decltype(rtag);
     auto fw = what == WHAT_FORWARD;
@@ -759,6 +810,14 @@ static int run_typed(const Call &c, int what) {
 int run_f32(const Call &c, int what);
 int run_f16(const Call &c, int what);
 int run_bf16(const Call &c, int what);
+
+// Shared with the ONNX Runtime op core (qc_quantize.hip), defined in qdq.hip:
+// per-encoding min / max of the layout with NaN skipped (the reference's CPU statistics), and
+// the OP_NATIVE / OP_FP16 forward (f32 or f16 tensors).
+int minmax_stats(const void *x, int32_t io, const rxmet_qdq_layout &l, float *out_min,
+                 float *out_max, void *workspace, hipStream_t s);
+int forward_tf(int op, const void *x, void *y, int32_t io, const rxmet_qdq_layout &l,
+               const TfEnc32 *enc, hipStream_t s);
 
 }  // namespace qdq
 }  // namespace rxmet

@@ -4,6 +4,7 @@ from pathlib import Path
 
 import rxmet_gru_abi  # noqa: F401  (registers the GRU signatures)
 import rxmet_lstm_abi  # noqa: F401  (registers the LSTM signatures)
+import rxmet_qc_abi  # noqa: F401  (registers the QcQuantizeOp signatures)
 import rxmet_lib
 
 ROOT = Path(__file__).resolve().parents[1]

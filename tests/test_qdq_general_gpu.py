@@ -343,22 +343,27 @@ def test_block_quantization_matches_torch_reference(cuda, dtype, block_size, ssh
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("per_channel", [False, True])
 def test_frozen_fast_path_matches_torch_fake_quantize(cuda, dtype, per_channel):
-    """Frozen encodings on a 16-bit tensor: torch.fake_quantize on the GPU is the
-    reference's own path (torch_builtins.py:287-361), NaN restored (:249)."""
+    """Frozen encodings on a 16-bit tensor: torch.fake_quantize is the reference's own path
+    (torch_builtins.py:287-361), NaN restored (:249).  It computes the result in fp32 and
+    rounds that to the tensor's type; the checker is torch's CPU kernel, because the ROCm build
+    of torch's GPU kernel lets the compiler fold the last multiply into the fp16 conversion
+    (v_fma_mixlo_f16: one rounding of the exact product), which differs on fp16 ties — seed 3
+    has three such elements in the per-channel case."""
     gen = torch.Generator().manual_seed(3)
     x = (torch.randn(96, 1000, generator=gen) * 2).to(dtype).to(cuda)
     x[0, :3] = torch.tensor([float("nan"), float("inf"), -float("inf")], dtype=dtype)
+    xc = x.cpu()
     if per_channel:
         scale = (torch.rand(96, 1, generator=gen) * 0.05 + 0.01).to(cuda)
         offset = torch.zeros(96, 1, device=cuda)
         ref = torch.fake_quantize_per_channel_affine(
-            x, scale.flatten(), torch.zeros(96, dtype=torch.int32, device=cuda), 0, -128, 127)
+            xc, scale.flatten().cpu(), torch.zeros(96, dtype=torch.int32), 0, -128, 127)
     else:
         scale = torch.tensor(0.0173, device=cuda)
         offset = torch.tensor(-3.0, device=cuda)
-        ref = torch.fake_quantize_per_tensor_affine(
-            x, scale, torch.tensor(3, dtype=torch.int32, device=cuda), -128, 127)
-    ref = ref.masked_fill_(torch.isnan(x), float("nan"))
+        ref = torch.fake_quantize_per_tensor_affine(xc, scale.cpu(), torch.tensor(3, dtype=torch.int32),
+                                                    -128, 127)
+    ref = ref.masked_fill_(torch.isnan(xc), float("nan")).to(cuda)
     y = Q.quantize_dequantize(x, scale, offset, -128, 127)
     assert y.dtype == dtype
     fin = torch.isfinite(x)
