@@ -216,6 +216,7 @@ def _qdq_leg(torch, steps: int, warmup: int, validate: bool = True):
     _log(f"qdq kernels (bf16 tensor): fwd {t_fh*1e6:.1f} us ({4*n/t_fh/1e9:.0f} GB/s), "
          f"bwd {t_bh*1e6:.1f} us ({6*n/t_bh/1e9:.0f} GB/s)")
     del xh, gh, yh, dxh, dsh, doh, wsh
+    results.update(_qc_op_timings(torch, x, ev_time, max(steps, 20)))
     check = None
     if validate:
         # the timed kernels' outputs on 64 rows against the oracle: y and dx bit-exact, the
@@ -242,6 +243,62 @@ def _qdq_leg(torch, steps: int, warmup: int, validate: bool = True):
             "traffic": _traffic("qdq_bwd_learnable"),
             "algorithmic_bytes_per_launch": 12 * n}
     return results, roof, check
+
+
+def _qc_op_timings(torch, x, ev_time, reps):
+    """The ONNX Runtime op QcQuantizeOp (rxmet_qc_quantize_compute) on the c2 tensor: 8-bit
+    TF encodings per tensor and per row; quantizeDequantize (read x, write y: 8 B/element) and
+    oneShotQuantizeDequantize (statistics pass, encodings, quantize-dequantize: 12 B/element),
+    and quantizeDequantize on a float16 copy (4 B/element).  64 rows of the one-shot result
+    against the oracle, bit for bit."""
+    import ctypes
+
+    import numpy as np
+
+    import rxmet_lib
+    from qc_quantize_op import BlockTensorQuantizer, OpMode, QcQuantizeInfo
+
+    R, Cc = x.shape
+    n = R * Cc
+    sh = torch.cuda.current_stream(x.device).cuda_stream
+    arr = (ctypes.c_int64 * 2)(R, Cc)
+    out = {}
+    y = torch.empty_like(x)
+    xh = x.to(torch.float16)
+    yh = torch.empty_like(xh)
+    for label, eshape in (("per_tensor", ()), ("per_channel", (R, 1))):
+        q = BlockTensorQuantizer(eshape, 8)
+        info = QcQuantizeInfo()
+        info.tensorQuantizerRef = q
+        c = info.c_struct
+
+        def run(mode, src=x, dst=y, io=0):
+            c.op_mode = mode
+            rxmet_lib.call("rxmet_qc_quantize_compute", ctypes.byref(c), src.data_ptr(),
+                           dst.data_ptr(), io, arr, 2, None, sh)
+
+        t_one = ev_time(lambda: run(int(OpMode.oneShotQuantizeDequantize)), reps)
+        if label == "per_channel":
+            import qc_quantize_oracle as QO
+
+            torch.cuda.synchronize()
+            rows = np.sort(np.random.default_rng(3).choice(R, 64, replace=False))
+            xs = x[rows].cpu().numpy()
+            oq = QO.BlockTensorQuantizerOracle((64, 1), 8)
+            oq.update_stats(xs)
+            oq.set_encodings(oq.compute_encodings(False))
+            _check_equal("qc oneShot per row", y[rows].cpu().numpy(), oq.quantize_dequantize(xs))
+        t_q = ev_time(lambda: run(int(OpMode.quantizeDequantize)), reps)
+        t_h = ev_time(lambda: run(int(OpMode.quantizeDequantize), xh, yh, 1), reps)
+        for nm, t, b in (("one_shot", t_one, 12), ("qdq", t_q, 8), ("qdq_f16", t_h, 4)):
+            gbs = b * n / t / 1e9
+            out[f"qc_op_{nm}_{label}"] = {"us": t * 1e6, "GB_s": gbs, "frac": gbs / HBM_PEAK_GBS}
+        _log(f"QcQuantizeOp {label}: oneShot {t_one*1e6:.1f} us ({12*n/t_one/1e9:.0f} GB/s), "
+             f"quantizeDequantize {t_q*1e6:.1f} us ({8*n/t_q/1e9:.0f} GB/s), fp16 "
+             f"{t_h*1e6:.1f} us ({4*n/t_h/1e9:.0f} GB/s)")
+        del q, info
+    del y, xh, yh
+    return out
 
 
 # Algorithmic work per launch of the instrumented GRU kernels (one direction, c3 shapes):
@@ -905,7 +962,41 @@ def _qdq_cpu_baseline(torch, budget_s: float = 8.0):
             "frozen_fake_quantize_GB_s": round(20 * n / dtf / 1e9, 3),
             "frozen_note": "the reference's own frozen-encoding path (aten "
                            "fake_quantize_per_tensor_affine), same tensor and threads",
+            "qc_op_one_shot": _qc_ref_cpu_baseline(x[:1024].contiguous().numpy(), budget_s / 2),
             **_host_info()}
+
+
+def _qc_ref_cpu_baseline(xs, budget_s: float):
+    """QcQuantizeOp's one-shot work on the reference's own CPU code (oracle/_ref/libqc_ref.so:
+    MinMaxEncodingAnalyzer statistics + getComputedEncodings, then quantizeDequantizeBroadcast;
+    one thread, as the reference runs them), 8-bit encodings per row of a [1024, 8192] slice of
+    c2; GB/s on the GPU leg's byte formula (12 bytes per element).  None where the reference
+    checker was not built."""
+    import ctypes
+
+    import numpy as np
+
+    path = ROOT / "oracle" / "_ref" / "libqc_ref.so"
+    if not path.exists():
+        return None
+    lib = ctypes.CDLL(str(path))
+    R, Cc = xs.shape
+    ts = np.array([R, Cc], np.int64)
+    es = np.array([R, 1], np.int64)
+    enc = np.zeros(4 * R, np.float64)
+    y = np.empty_like(xs)
+    P = ctypes.c_void_p
+
+    def run():
+        lib.qcref_analyzer(P(xs.ctypes.data), P(ts.ctypes.data), 2, P(es.ctypes.data), 2, 1, 8,
+                           0, 0, 0, P(enc.ctypes.data))
+        lib.qcref_qdq(P(xs.ctypes.data), P(y.ctypes.data), P(ts.ctypes.data), 2,
+                      P(es.ctypes.data), 2, P(enc.ctypes.data), 8)
+    dt, reps = _timed_cpu(run, budget_s)
+    return {"value": round(12 * xs.size / dt / 1e9, 3), "unit": "GB/s", "cores": 1,
+            "kind": "reference",
+            "sample": f"QcQuantizeOp oneShot, 8-bit per-row encodings, [{R}, {Cc}] slice of c2, "
+                      f"{reps} run(s) of {dt:.3f} s"}
 
 
 def _c1_leg(torch, steps: int, warmup: int):

@@ -9,10 +9,10 @@
 //
 // The reference keeps statistics and encodings on the host and, on the GPU, synchronizes for
 // every statistics update (GetMinMax_gpu copies each reduction back).  Here they stay in HBM
-// next to the op: a oneShot call is four launches on the caller's stream and no host round
-// trip — the streaming min / max of the QDQ kernels (NaN skipped), a per-encoding fold into the
-// running statistics that also derives the TfEncodings in double arithmetic, and the
-// stableQuantizeDequantize streaming pass.
+// next to the op: a oneShot call runs on the caller's stream with no host round
+// trip — the streaming min / max of the QDQ kernels (NaN skipped), their per-encoding fold,
+// which also replaces the running statistics and derives the TfEncodings in double arithmetic,
+// and the stableQuantizeDequantize streaming pass: three launches.
 #include <algorithm>
 #include <cfloat>
 #include <climits>
@@ -30,10 +30,10 @@ struct rxmet_block_tensor_quantizer {
   bool strict = false, unsigned_sym = false;
   bool valid_stats = false, encoding_valid = false;
   int device = 0;
-  // device memory, one allocation: running min / max, this call's min / max (fp32), the
-  // encodings as TfEncoding (double) and as the fp32 form the QDQ pass reads
+  // device memory, one allocation: running min / max (fp32), the encodings as TfEncoding
+  // (double) and as the fp32 form the QDQ pass reads
   void *mem = nullptr;
-  float *st_min = nullptr, *st_max = nullptr, *cur_min = nullptr, *cur_max = nullptr;
+  float *st_min = nullptr, *st_max = nullptr;
   rxmet_tf_encoding *enc = nullptr;
   TfEnc32 *enc32 = nullptr;
   void *ws = nullptr;  // the quantizer's own workspace (update_stats with none given)
@@ -45,9 +45,6 @@ namespace qc {
 
 constexpr int kThreads = 256;
 
-// MinMaxEncodingAnalyzer<float>::MIN_RANGE: the float nearest 0.01, added in double.
-constexpr float kMinRange = 0.01f;
-
 // running statistics reset: (numeric_limits<float>::max(), lowest()) as resetStats
 __global__ __launch_bounds__(kThreads) void stats_reset(int64_t n, float *mn, float *mx) {
   const int64_t c = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -56,78 +53,13 @@ __global__ __launch_bounds__(kThreads) void stats_reset(int64_t n, float *mn, fl
   mx[c] = -FLT_MAX;
 }
 
-// _minStats = std::min(_minStats, currMin); _maxStats = std::max(_maxStats, currMax)
-__global__ __launch_bounds__(kThreads) void stats_fold(int64_t n, const float *cmn,
-                                                       const float *cmx, float *mn, float *mx) {
-  const int64_t c = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (c >= n) return;
-  const float a = mn[c], b = cmn[c];
-  mn[c] = b < a ? b : a;
-  const float u = mx[c], v = cmx[c];
-  mx[c] = u < v ? v : u;
-}
-
-__device__ __forceinline__ double dmin(double a, double b) { return b < a ? b : a; }  // std::min
-__device__ __forceinline__ double dmax(double a, double b) { return a < b ? b : a; }  // std::max
-__device__ __forceinline__ double dclamp(double v, double lo, double hi) {            // std::clamp
-  return v < lo ? lo : (hi < v ? hi : v);
-}
-
-__device__ __forceinline__ void put_enc(rxmet_tf_encoding *enc, TfEnc32 *enc32, int64_t c,
-                                        double mn, double mx, double delta, double offset,
-                                        int bw) {
-  rxmet_tf_encoding e;
-  e.min = mn;
-  e.max = mx;
-  e.delta = delta;
-  e.offset = offset;
-  e.bw = bw;
-  e.reserved = 0;
-  enc[c] = e;
-  TfEnc32 t;
-  t.mn = static_cast<float>(mn);
-  t.mx = static_cast<float>(mx);
-  t.delta = static_cast<float>(delta);
-  t.inv_delta = 1.0f / t.delta;  // correctly rounded (qdqReciprocal)
-  enc32[c] = t;
-}
-
-// MinMaxEncodingAnalyzer::computeEncoding + getComputedEncodings, one thread per encoding,
-// every operation a correctly rounded double operation as on the host.
+// MinMaxEncodingAnalyzer::computeEncoding from the running statistics, one thread per encoding.
 __global__ __launch_bounds__(kThreads) void compute_encodings(
     int64_t n, const float *st_min, const float *st_max, int bw, int sym, int strict,
     int unsigned_sym, rxmet_tf_encoding *enc, TfEnc32 *enc32) {
-#pragma clang fp contract(off)
   const int64_t c = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (c >= n) return;
-  // zero inside the range; at least MIN_RANGE wide
-  const float fmn = st_min[c], fmx = st_max[c];
-  double mn = static_cast<double>(fmn < 0.0f ? fmn : 0.0f);
-  double mx = static_cast<double>(0.0f < fmx ? fmx : 0.0f);
-  mx = dmax(mx, mn + static_cast<double>(kMinRange));
-
-  double steps = ldexp(1.0, bw) - 1.0;
-  if (sym && strict) steps -= 1.0;
-  const double f32_lo = static_cast<double>(-FLT_MAX) * 0.99;
-  const double f32_hi = static_cast<double>(FLT_MAX) * 0.99;
-  mn = dclamp(mn, f32_lo, 0.0);
-  mx = dclamp(mx, 0.0, f32_hi);
-  const bool uns = unsigned_sym && mn >= 0.0;
-  double delta, offset;
-  if (sym && !uns) {
-    const unsigned pos = static_cast<unsigned>(floor(steps / 2.0));
-    const unsigned neg = static_cast<unsigned>(steps - static_cast<double>(pos));
-    const unsigned extra = steps == 3.0 ? 1u : 0u;  // all bins usable at 2 bits
-    delta = dmax(mx / static_cast<double>(pos + extra), -mn / static_cast<double>(neg));
-    offset = -static_cast<double>(neg);
-  } else {
-    delta = (mx - mn) / steps;
-    offset = dclamp(round(mn / delta), -steps, 0.0);
-  }
-  // the dequantized grid stays inside [0.99 lowest, 0.99 max] of fp32
-  if (offset < 0.0) delta = dmin(delta, f32_lo / offset);
-  if (offset + steps > 0.0) delta = dmin(delta, f32_hi / (offset + steps));
-  put_enc(enc, enc32, c, delta * offset, delta * (offset + steps), delta, offset, bw);
+  rxmet::qdq::tf_encoding(st_min[c], st_max[c], bw, sym, strict, unsigned_sym, enc, enc32, c);
 }
 
 // fp32 forms of host-set encodings
@@ -248,8 +180,11 @@ static int reset_stats(rxmet_block_tensor_quantizer *q, hipStream_t s) {
   return 0;
 }
 
+// One statistics update folded into the running statistics (reset: in their place), and with
+// enc_sym >= 0 the encodings computed from them and set (symmetric = enc_sym) in the same fold.
 static int update_stats(rxmet_block_tensor_quantizer *q, const void *x, int32_t io,
-                        const int64_t *shape, int32_t ndim, void *workspace, hipStream_t s) {
+                        const int64_t *shape, int32_t ndim, void *workspace, hipStream_t s,
+                        bool reset = false, int enc_sym = -1) {
   if (int rc = check_io(io)) return rc;
   rxmet_qdq_layout l;
   if (int rc = layout_of(q, shape, ndim, l)) return rc;
@@ -266,11 +201,14 @@ static int update_stats(rxmet_block_tensor_quantizer *q, const void *x, int32_t 
     workspace = q->ws;
   }
   rxmet::prof::Scope ps__("qc_update_stats", s);
-  if (int rc = rxmet::qdq::minmax_stats(x, io, l, q->cur_min, q->cur_max, workspace, s)) return rc;
-  hipLaunchKernelGGL(stats_fold, dim3(blocks_for(q->n)), dim3(kThreads), 0, s, q->n, q->cur_min,
-                     q->cur_max, q->st_min, q->st_max);
-  RXMET_CHECK_LAUNCH();
+  const rxmet::qdq::StatsSink sink{q->st_min,   q->st_max,         reset ? 1 : 0,
+                                   enc_sym >= 0, q->bitwidth,       enc_sym > 0 ? 1 : 0,
+                                   q->strict,   q->unsigned_sym,    q->enc,
+                                   q->enc32};
+  if (int rc = rxmet::qdq::minmax_stats(x, io, l, sink, workspace, s)) return rc;
   q->valid_stats = true;
+  if (reset) q->encoding_valid = false;
+  if (enc_sym >= 0) q->encoding_valid = true;
   return 0;
 }
 
@@ -340,11 +278,11 @@ rxmet_block_tensor_quantizer *rxmet_block_tensor_quantizer_create(const int64_t 
     delete q;
     return nullptr;
   }
-  // 4 fp32 arrays, the TfEncodings, the fp32 encodings (each region 256-byte aligned)
+  // 2 fp32 arrays, the TfEncodings, the fp32 encodings (each region 256-byte aligned)
   auto up = [](size_t b) { return (b + 255) & ~size_t(255); };
   const size_t f = up(sizeof(float) * n), e = up(sizeof(rxmet_tf_encoding) * n),
                e32 = up(sizeof(TfEnc32) * n);
-  if (hipMalloc(&q->mem, 4 * f + e + e32) != hipSuccess) {
+  if (hipMalloc(&q->mem, 2 * f + e + e32) != hipSuccess) {
     set_error("hipMalloc of the quantizer state failed");
     delete q;
     return nullptr;
@@ -352,10 +290,8 @@ rxmet_block_tensor_quantizer *rxmet_block_tensor_quantizer_create(const int64_t 
   char *p = static_cast<char *>(q->mem);
   q->st_min = reinterpret_cast<float *>(p);
   q->st_max = reinterpret_cast<float *>(p + f);
-  q->cur_min = reinterpret_cast<float *>(p + 2 * f);
-  q->cur_max = reinterpret_cast<float *>(p + 3 * f);
-  q->enc = reinterpret_cast<rxmet_tf_encoding *>(p + 4 * f);
-  q->enc32 = reinterpret_cast<TfEnc32 *>(p + 4 * f + e);
+  q->enc = reinterpret_cast<rxmet_tf_encoding *>(p + 2 * f);
+  q->enc32 = reinterpret_cast<TfEnc32 *>(p + 2 * f + e);
   // statistics start reset, as the analyzer's constructor leaves them
   if (reset_stats(q, nullptr) != 0 || hipStreamSynchronize(nullptr) != hipSuccess) {
     (void)hipFree(q->mem);
@@ -526,9 +462,11 @@ int rxmet_qc_quantize_compute(rxmet_qc_quantize_info *info, const void *x, void 
       if ((rc = check_q(q))) return rc;
     switch (mode) {
       case RXMET_QC_ONE_SHOT_QUANTIZE_DEQUANTIZE:
-        if ((rc = reset_stats(q, s))) return rc;
-        if ((rc = update_stats(q, x, io_dtype, shape, ndim, workspace, s))) return rc;
-        if ((rc = compute_and_set(q, info->use_symmetric_encoding != 0, s))) return rc;
+        // resetEncodingStats, updateStats, computeEncodings + setEncodings: one statistics
+        // pass whose fold replaces the statistics and derives the encodings
+        if ((rc = update_stats(q, x, io_dtype, shape, ndim, workspace, s, true,
+                               info->use_symmetric_encoding ? 1 : 0)))
+          return rc;
         [[fallthrough]];
       case RXMET_QC_QUANTIZE_DEQUANTIZE:
         rc = qc::qdq(q, x, y, io_dtype, shape, ndim, s);

@@ -98,11 +98,32 @@ struct PutMinMaxGrad {
   }
 };
 
-__device__ __forceinline__ void put_minmax(const MinMax &v, int64_t c, float *out_min,
-                                           float *out_max) {
-  out_min[c] = v.mn;
-  out_max[c] = v.mx;
-}
+// Folded min / max written out.
+struct PutMinMax {
+  float *out_min, *out_max;
+  __device__ void operator()(const MinMax &v, int64_t c) const {
+    out_min[c] = v.mn;
+    out_max[c] = v.mx;
+  }
+};
+
+// Folded min / max of one statistics update taken into a TF-scheme quantizer's running
+// statistics (std::min / std::max with the previous ones, or in their place after a reset),
+// and optionally its TfEncodings derived from them in the same thread.
+struct PutStats {
+  StatsSink k;
+  __device__ void operator()(const MinMax &v, int64_t c) const {
+    float mn = v.mn, mx = v.mx;
+    if (!k.reset) {
+      const float a = k.st_min[c], u = k.st_max[c];
+      mn = mn < a ? mn : a;
+      mx = u < mx ? mx : u;
+    }
+    k.st_min[c] = mn;
+    k.st_max[c] = mx;
+    if (k.enc) tf_encoding(mn, mx, k.bw, k.sym, k.strict, k.unsigned_sym, k.enc64, k.enc32, c);
+  }
+};
 
 struct AddSum {
   __device__ void operator()(Sum2 &a, const Sum2 &v) const { acc_add(a, v); }
@@ -135,12 +156,10 @@ __global__ __launch_bounds__(NT) void fold_sum(const Sum2 *__restrict__ partial,
   fold_block<NT>(partial, f, Sum2{0.0, 0.0}, AddSum{}, put);
 }
 
-template <int NT>
+template <int NT, typename Put>
 __global__ __launch_bounds__(NT) void fold_minmax(const MinMax *__restrict__ partial, FoldMap f,
-                                                  float *__restrict__ out_min,
-                                                  float *__restrict__ out_max) {
-  fold_block<NT>(partial, f, MinMax{INFINITY, -INFINITY}, AddMinMax{},
-                 [&](const MinMax &v, int64_t c) { put_minmax(v, c, out_min, out_max); });
+                                                  Put put) {
+  fold_block<NT>(partial, f, MinMax{INFINITY, -INFINITY}, AddMinMax{}, put);
 }
 
 // One thread per encoding, its partials in order.
@@ -152,14 +171,12 @@ __global__ __launch_bounds__(256) void fold_sum_thread(const Sum2 *__restrict__ 
   put(fold_strided(partial, f, c, 0, 1, Sum2{0.0, 0.0}, AddSum{}), c);
 }
 
+template <typename Put>
 __global__ __launch_bounds__(256) void fold_minmax_thread(const MinMax *__restrict__ partial,
-                                                          FoldMap f, int64_t C,
-                                                          float *__restrict__ out_min,
-                                                          float *__restrict__ out_max) {
+                                                          FoldMap f, int64_t C, Put put) {
   const int64_t c = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (c >= C) return;
-  put_minmax(fold_strided(partial, f, c, 0, 1, MinMax{INFINITY, -INFINITY}, AddMinMax{}), c,
-             out_min, out_max);
+  put(fold_strided(partial, f, c, 0, 1, MinMax{INFINITY, -INFINITY}, AddMinMax{}), c);
 }
 
 // Launch the fold of C encodings' partials with the shape their count calls for.
@@ -181,21 +198,22 @@ static void launch_fold_sum(const Sum2 *ws, const FoldMap &f, int64_t C, Put put
                        dim3(256), 0, s, ws, f, C, put);
 }
 
-static void launch_fold_minmax(const MinMax *ws, const FoldMap &f, int64_t C, float *out_min,
-                               float *out_max, hipStream_t s) {
+template <typename Put>
+static void launch_fold_minmax(const MinMax *ws, const FoldMap &f, int64_t C, Put put,
+                               hipStream_t s) {
   const int64_t n = f.n0 * f.n1 * f.n2;
   if (n >= 8192)
-    hipLaunchKernelGGL(fold_minmax<16 * kWave>, dim3(static_cast<unsigned>(C)), dim3(16 * kWave),
-                       0, s, ws, f, out_min, out_max);
+    hipLaunchKernelGGL((fold_minmax<16 * kWave, Put>), dim3(static_cast<unsigned>(C)),
+                       dim3(16 * kWave), 0, s, ws, f, put);
   else if (n >= 1024)
-    hipLaunchKernelGGL(fold_minmax<4 * kWave>, dim3(static_cast<unsigned>(C)), dim3(4 * kWave), 0,
-                       s, ws, f, out_min, out_max);
+    hipLaunchKernelGGL((fold_minmax<4 * kWave, Put>), dim3(static_cast<unsigned>(C)),
+                       dim3(4 * kWave), 0, s, ws, f, put);
   else if (n >= 64)
-    hipLaunchKernelGGL(fold_minmax<kWave>, dim3(static_cast<unsigned>(C)), dim3(kWave), 0, s, ws,
-                       f, out_min, out_max);
+    hipLaunchKernelGGL((fold_minmax<kWave, Put>), dim3(static_cast<unsigned>(C)), dim3(kWave), 0,
+                       s, ws, f, put);
   else
-    hipLaunchKernelGGL(fold_minmax_thread, dim3(static_cast<unsigned>((C + 255) / 256)), dim3(256),
-                       0, s, ws, f, C, out_min, out_max);
+    hipLaunchKernelGGL((fold_minmax_thread<Put>), dim3(static_cast<unsigned>((C + 255) / 256)),
+                       dim3(256), 0, s, ws, f, C, put);
 }
 
 __global__ __launch_bounds__(256) void zero_enc_grads(int64_t C, float *dscale, float *doffset) {
@@ -428,12 +446,13 @@ static int backward_impl(int op, const void *x, const void *g, void *dx, float *
   return 0;
 }
 
-static int minmax_impl(const void *x, int32_t io, const rxmet_qdq_layout *l, float *out_min,
-                       float *out_max, void *workspace, void *stream, bool skip_nan = false) {
+// Min / max of every encoding's elements; `put` receives each folded pair.
+template <typename Put>
+static int minmax_impl(const void *x, int32_t io, const rxmet_qdq_layout *l, Put put,
+                       void *workspace, void *stream, bool skip_nan = false) {
   RXMET_CHECK_ARG(l != nullptr, "layout must be non-null");
   if (int rc = check_layout(l->outer, l->C0, l->mid, l->C1, l->inner)) return rc;
   RXMET_CHECK_ARG(is_io(io), "io_dtype must be RXMET_QDQ_F32, F16 or BF16");
-  RXMET_CHECK_ARG(out_min && out_max, "out_min/out_max must be non-null");
   const Plan p = make_plan(l->outer, l->C0, l->mid, l->C1, l->inner, esize_of(io), kVecMinMax);
   RXMET_CHECK_ARG(p.n > 0, "min/max of an empty tensor");
   RXMET_CHECK_ARG(x != nullptr, "x must be non-null");
@@ -444,16 +463,17 @@ static int minmax_impl(const void *x, int32_t io, const rxmet_qdq_layout *l, flo
   const Call c{&p, OP_QDQ_LEARN, nm.internal_dtype, x, nullptr, nullptr, nullptr, nullptr,
                make_params(0, 0, nm), workspace, s};
   if (int rc = dispatch(c, io, skip_nan ? WHAT_MINMAX_SKIP_NAN : WHAT_MINMAX)) return rc;
-  launch_fold_minmax(static_cast<const MinMax *>(workspace), p.fold, l->C0 * l->C1, out_min,
-                     out_max, s);
+  launch_fold_minmax(static_cast<const MinMax *>(workspace), p.fold, l->C0 * l->C1, put, s);
   RXMET_CHECK_LAUNCH();
   return 0;
 }
 
 // Shared with the ONNX Runtime op core (qc_quantize.hip).
-int minmax_stats(const void *x, int32_t io, const rxmet_qdq_layout &l, float *out_min,
-                 float *out_max, void *workspace, hipStream_t s) {
-  return minmax_impl(x, io, &l, out_min, out_max, workspace, s, true);
+int minmax_stats(const void *x, int32_t io, const rxmet_qdq_layout &l, const StatsSink &sink,
+                 void *workspace, hipStream_t s) {
+  RXMET_CHECK_ARG(sink.st_min && sink.st_max, "statistics must be non-null");
+  RXMET_CHECK_ARG(!sink.enc || (sink.enc64 && sink.enc32), "encodings must be non-null");
+  return minmax_impl(x, io, &l, PutStats{sink}, workspace, s, true);
 }
 
 int forward_tf(int op, const void *x, void *y, int32_t io, const rxmet_qdq_layout &l,
@@ -569,13 +589,15 @@ int rxmet_qdq_minmax(const float *x, int64_t outer, int64_t C, int64_t inner, fl
   clear_error();
   if (int rc = check_layout3(outer, C, inner)) return rc;
   const rxmet_qdq_layout l = layout3(outer, C, inner);
-  return minmax_impl(x, RXMET_QDQ_F32, &l, out_min, out_max, workspace, stream);
+  RXMET_CHECK_ARG(out_min && out_max, "out_min/out_max must be non-null");
+  return minmax_impl(x, RXMET_QDQ_F32, &l, PutMinMax{out_min, out_max}, workspace, stream);
 }
 
 int rxmet_qdq_minmax_ex(const void *x, int32_t io_dtype, const rxmet_qdq_layout *layout,
                         float *out_min, float *out_max, void *workspace, void *stream) {
   clear_error();
-  return minmax_impl(x, io_dtype, layout, out_min, out_max, workspace, stream);
+  RXMET_CHECK_ARG(out_min && out_max, "out_min/out_max must be non-null");
+  return minmax_impl(x, io_dtype, layout, PutMinMax{out_min, out_max}, workspace, stream);
 }
 
 static int qdq_op(int mode) {

@@ -31,6 +31,7 @@
 #include <type_traits>
 
 #include "rxmet_common.h"
+#include "rxmet_qc.h"
 #include "rxmet_qdq.h"
 
 namespace rxmet {
@@ -46,6 +47,62 @@ enum Op { OP_QDQ_LEARN = 0, OP_QDQ_FROZEN = 1, OP_Q = 2, OP_DQ = 3, OP_NATIVE = 
 struct alignas(16) TfEnc32 {
   float mn, mx, delta, inv_delta;
 };
+
+__device__ __forceinline__ double dmin_std(double a, double b) { return b < a ? b : a; }
+__device__ __forceinline__ double dmax_std(double a, double b) { return a < b ? b : a; }
+__device__ __forceinline__ double dclamp_std(double v, double lo, double hi) {
+  return v < lo ? lo : (hi < v ? hi : v);
+}
+
+// The TfEncoding of encoding c from its fp32 running statistics:
+// MinMaxEncodingAnalyzer<float>::computeEncoding (MinMaxEncodingAnalyzer.cpp:72-96) and
+// getComputedEncodings (quantization_utils.cpp:59-119), each step the correctly rounded double
+// operation (std::min / max / clamp as their comparisons define them, C round), written as the
+// double encoding and its fp32 form.
+__device__ __forceinline__ void tf_encoding(float st_min, float st_max, int bw, int sym,
+                                            int strict, int unsigned_sym, rxmet_tf_encoding *enc,
+                                            TfEnc32 *enc32, int64_t c) {
+  // zero inside the range; at least MIN_RANGE (the float 0.01) wide
+  double mn = static_cast<double>(st_min < 0.0f ? st_min : 0.0f);
+  double mx = static_cast<double>(0.0f < st_max ? st_max : 0.0f);
+  mx = dmax_std(mx, mn + static_cast<double>(0.01f));
+
+  double steps = ldexp(1.0, bw) - 1.0;
+  if (sym && strict) steps -= 1.0;
+  const double f32_lo = static_cast<double>(-3.40282346638528859812e+38f) * 0.99;
+  const double f32_hi = static_cast<double>(3.40282346638528859812e+38f) * 0.99;
+  mn = dclamp_std(mn, f32_lo, 0.0);
+  mx = dclamp_std(mx, 0.0, f32_hi);
+  const bool uns = unsigned_sym && mn >= 0.0;
+  double delta, offset;
+  if (sym && !uns) {
+    const unsigned pos = static_cast<unsigned>(floor(steps / 2.0));
+    const unsigned neg = static_cast<unsigned>(steps - static_cast<double>(pos));
+    const unsigned extra = steps == 3.0 ? 1u : 0u;  // all bins usable at 2 bits
+    delta = dmax_std(mx / static_cast<double>(pos + extra), -mn / static_cast<double>(neg));
+    offset = -static_cast<double>(neg);
+  } else {
+    delta = (mx - mn) / steps;
+    offset = dclamp_std(round(mn / delta), -steps, 0.0);
+  }
+  // the dequantized grid stays inside [0.99 lowest, 0.99 max] of fp32
+  if (offset < 0.0) delta = dmin_std(delta, f32_lo / offset);
+  if (offset + steps > 0.0) delta = dmin_std(delta, f32_hi / (offset + steps));
+  rxmet_tf_encoding e;
+  e.min = delta * offset;
+  e.max = delta * (offset + steps);
+  e.delta = delta;
+  e.offset = offset;
+  e.bw = bw;
+  e.reserved = 0;
+  enc[c] = e;
+  TfEnc32 t;
+  t.mn = static_cast<float>(e.min);
+  t.mx = static_cast<float>(e.max);
+  t.delta = static_cast<float>(delta);
+  t.inv_delta = 1.0f / t.delta;  // correctly rounded (qdqReciprocal)
+  enc32[c] = t;
+}
 
 constexpr int kThreads = 256;
 // 16-byte vectors per thread per chunk (runs decomposition), per kind of pass.  Measured on
@@ -811,11 +868,21 @@ int run_f32(const Call &c, int what);
 int run_f16(const Call &c, int what);
 int run_bf16(const Call &c, int what);
 
+// Where a TF-scheme quantizer's statistics update lands (ONNX Runtime op): the running
+// min / max (replaced after a reset), and with enc set the TfEncodings derived from them.
+struct StatsSink {
+  float *st_min, *st_max;
+  int reset, enc;
+  int bw, sym, strict, unsigned_sym;
+  rxmet_tf_encoding *enc64;
+  TfEnc32 *enc32;
+};
+
 // Shared with the ONNX Runtime op core (qc_quantize.hip), defined in qdq.hip:
 // per-encoding min / max of the layout with NaN skipped (the reference's CPU statistics), and
 // the OP_NATIVE / OP_FP16 forward (f32 or f16 tensors).
-int minmax_stats(const void *x, int32_t io, const rxmet_qdq_layout &l, float *out_min,
-                 float *out_max, void *workspace, hipStream_t s);
+int minmax_stats(const void *x, int32_t io, const rxmet_qdq_layout &l, const StatsSink &sink,
+                 void *workspace, hipStream_t s);
 int forward_tf(int op, const void *x, void *y, int32_t io, const rxmet_qdq_layout &l,
                const TfEnc32 *enc, hipStream_t s);
 
