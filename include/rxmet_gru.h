@@ -330,6 +330,33 @@ int rxmet_gru_forward_int_io(int32_t T, int32_t B, int32_t I, int32_t H, const f
                              void *stream);
 
 /*
+ * Both directions of a bidirectional layer on the int32 carrier in one call.  No counterpart
+ * in the reference, which calls forward_quant_int_storage / forward_quantized_int_io once per
+ * direction (quant_gru.py:2207-2288, 2482-2537): the per-direction prologues run first, then
+ * one clustered recurrence launch covers both directions so their sequential steps overlap
+ * (each direction stepped where the clustered form does not apply).  dirs[k] holds exactly the
+ * arguments of one rxmet_gru_forward_quant_int call (x_q_in == null) or one
+ * rxmet_gru_forward_int_io call (x_q_in != null: x_q_in, h0_q_in, h_q as x_q, h0_q, h_q there;
+ * is_training must be 0), with its own workspace of rxmet_gru_forward_int_workspace_bytes
+ * bytes; the results equal ndir separate calls.  ndir is 1 or 2; both directions have the same
+ * kind.
+ */
+typedef struct rxmet_gru_int_dir {
+  const float *W, *R, *bw, *br, *x, *h0;
+  const int32_t *x_q_in, *h0_q_in;
+  const rxmet_gru_qparams *params;
+  float *h, *v;
+  int32_t *h_q, *W_q, *R_q, *bw_q, *br_q, *x_q;
+  uint8_t *x_mask, *h0_mask, *W_mask, *R_mask, *bw_mask, *br_mask, *ih_mask, *hh_mask,
+      *gate_in_mask, *gate_out_mask, *h_mask;
+  void *workspace;
+} rxmet_gru_int_dir;
+
+int rxmet_gru_forward_quant_int_dirs(int32_t ndir, int32_t is_training, int32_t T, int32_t B,
+                                     int32_t I, int32_t H, const rxmet_gru_int_dir *dirs,
+                                     void *stream);
+
+/*
  * Float GRU forward with MinMax calibration statistics: forwardWithCalibrationGPU
  * (src/gru_interface.cc:930-1024) / forwardWithCalibrationCPU
  * (src/gru_forward_cpu.cc:58-151).  Writes h [T+1,B,H] and v [T,B,4H] (float values)

@@ -710,13 +710,16 @@ __device__ __forceinline__ void recurrence_cl_pair(const RecArgs &a, const StepP
   const int *tab = nullptr;
   if (!STAGE && cl.gate_tab) {
     __syncthreads();  // the LUT is in LDS
-    const Bounds gin[3] = {p.zin, p.rin, p.nin}, gout[3] = {p.zout, p.rout, p.nout};
     for (int i = tid; i < 3 * kGateTabMax; i += blockDim.x) {
       const int g = i / kGateTabMax, e = i % kGateTabMax;
-      if (e <= static_cast<int>(gin[g].hi - gin[g].lo)) {
+      // selected, not indexed: a local array indexed by g would live in scratch memory
+      const Bounds gi = g == 0 ? p.zin : (g == 1 ? p.rin : p.nin);
+      const Bounds go = g == 0 ? p.zout : (g == 1 ? p.rout : p.nout);
+      const float zpx = g == 0 ? p.lut[0].zp_x : (g == 1 ? p.lut[1].zp_x : p.lut[2].zp_x);
+      if (e <= static_cast<int>(gi.hi - gi.lo)) {
         uint8_t k = 0;
-        const float v = pwl_eval(gin[g].lo + static_cast<float>(e), lut_f + 48 * g, lut_f + 48 * g + 16,
-                                 lut_n + 16 * g, lut_f + 48 * g + 32, p.lut[g].zp_x, gout[g], k);
+        const float v = pwl_eval(gi.lo + static_cast<float>(e), lut_f + 48 * g, lut_f + 48 * g + 16,
+                                 lut_n + 16 * g, lut_f + 48 * g + 32, zpx, go, k);
         gtab[i] = static_cast<int>(v) * 2 | k;
       }
     }

@@ -314,10 +314,10 @@ __global__ __launch_bounds__(256) void int_point(IPointArgs a, IntStepParams p, 
 constexpr int kITile = 16;
 constexpr int kIMaxKPerWave = 4;  // K-steps per wave: H <= 1024
 
-struct IClArgs {
-  int T, B, H, KS, Bpad;
-  int G, UT, ncl, ntiles;
+// One direction of the clustered recurrence.
+struct IClDir {
   int h_offset;                 // 0 (signed h grid) or 2^(bits-1) (unsigned): centred codes
+  int gate_tab;                 // gate activations by table (every gate grid fits)
   const int32_t *wx;            // [T, B, 3H] weight_ih_linear codes
   const v4i *rfrag;             // R_q as int8 MFMA B fragments, [H/16][3][KS][64]
   const int32_t *rcol;          // [3H] column sums of R_q
@@ -328,10 +328,16 @@ struct IClArgs {
   int32_t *hq;                  // h codes [T+1, B, H] (row 0 written), or null
   uint8_t *hh_m, *gin_m, *gout_m, *h_m;  // training masks, or null
   int8_t *hx;                   // [2][NPL][Bpad / 16][KS][16][64] exchanged h codes (see ihx_offset)
+};
+
+// The launch: clusters walk (direction, batch tile) pairs, so both directions of a
+// bidirectional layer run in one launch and their sequential steps overlap.
+struct IClArgs {
+  int T, B, H, KS, Bpad;
+  int G, UT, ncl, ntiles, ndir;
   unsigned *counters;           // [ncl]
   int *timeout;
   unsigned spin_limit;  // polls before a wait gives up (cluster::spin_limit())
-  int gate_tab;                 // gate activations by table (every gate grid fits)
 };
 
 // Gate activations by table: a gate input is clamped to its grid, so when the grid has at most
@@ -385,30 +391,34 @@ __device__ __forceinline__ void publish_h(int8_t *hx, unsigned plane_stride, int
                                   NPL == 1 ? hcv : (q == 0 ? (hcv & 255) - 128 : hcv >> 8));
 }
 
+// One (direction, batch tile) pair of the launch: the direction's LUT, gate tables and R_q
+// fragments are loaded, then its T steps run.
 template <int NPL>
-__global__ __launch_bounds__(512) void int_recurrence_cl(IClArgs a, IntStepParams p) {
-  extern __shared__ __align__(16) unsigned char smem[];
+__device__ __forceinline__ void int_cl_pair(const IClDir &a, const IntStepParams &p,
+                                            const IClArgs &s, int tile, int member,
+                                            unsigned *counter, unsigned &epoch, bool &alive,
+                                            unsigned char *smem) {
   ILut *lut = reinterpret_cast<ILut *>(smem);
   v4i *red = reinterpret_cast<v4i *>(smem + (3 * sizeof(ILut) + 15) / 16 * 16);  // [UT][4][3][NPL][64]
-  int32_t *gtab = reinterpret_cast<int32_t *>(red + static_cast<size_t>(a.UT) * 4 * 3 * NPL * 64);
-  const cluster::Place pl = cluster::place(a.G, a.ncl);
-  unsigned *counter = a.counters + pl.cluster;
-  const int H = a.H, C = 3 * H, B = a.B, KS = a.KS;
+  int32_t *gtab = reinterpret_cast<int32_t *>(red + static_cast<size_t>(s.UT) * 4 * 3 * NPL * 64);
+  const int H = s.H, C = 3 * H, B = s.B, KS = s.KS;
   const int tid = threadIdx.x, w = tid / 64, l = tid % 64;
   const int utl = w / 4, kq = w % 4;
-  const int ut = pl.member * a.UT + utl;
+  const int ut = member * s.UT + utl;
   const int j = 16 * ut + l % 16;
   const int nr = 4 * (l / 16) + kq;  // batch row finished by this lane
   for (int i = tid; i < 3 * static_cast<int>(sizeof(ILut) / 4); i += blockDim.x)
     reinterpret_cast<int32_t *>(lut)[i] = reinterpret_cast<const int32_t *>(p.lut)[i];
   if (a.gate_tab) {
     __syncthreads();  // the LUT is in LDS; the tables are read after the first cluster barrier
-    const IGrid gin[3] = {p.zin, p.rin, p.nin}, gout[3] = {p.zout, p.rout, p.nout};
     for (int i = tid; i < 3 * kIGateTabMax; i += blockDim.x) {
       const int g = i / kIGateTabMax, e = i % kIGateTabMax;
-      if (e <= gin[g].hi - gin[g].lo) {
+      // selected, not indexed: a local array indexed by g would live in scratch memory
+      const IGrid gi = g == 0 ? p.zin : (g == 1 ? p.rin : p.nin);
+      const IGrid go = g == 0 ? p.zout : (g == 1 ? p.rout : p.nout);
+      if (e <= gi.hi - gi.lo) {
         uint8_t k = 0;
-        const int32_t v = clampi(pwl_i(gin[g].lo + e, lut[g]), gout[g], k);
+        const int32_t v = clampi(pwl_i(gi.lo + e, lut[g]), go, k);
         gtab[i] = v * 2 | k;
       }
     }
@@ -425,10 +435,10 @@ __global__ __launch_bounds__(512) void int_recurrence_cl(IClArgs a, IntStepParam
   v4i rfr[kIMaxKPerWave][3];
 #pragma unroll
   for (int i = 0; i < kIMaxKPerWave; ++i) {
-    const int s = kq + 4 * i;
+    const int ks = kq + 4 * i;
 #pragma unroll
     for (int g = 0; g < 3; ++g)
-      rfr[i][g] = s < KS ? a.rfrag[((ut * 3 + g) * KS + s) * 64 + l] : v4i{0, 0, 0, 0};
+      rfr[i][g] = ks < KS ? a.rfrag[((ut * 3 + g) * KS + ks) * 64 + l] : v4i{0, 0, 0, 0};
   }
   // S = sum_k R (h - zp_h) = (plane sums) + (centring - zp_h) colsum
   const long long centre = (NPL == 2 ? 128 : 0) + a.h_offset - p.zp_h;
@@ -441,15 +451,12 @@ __global__ __launch_bounds__(512) void int_recurrence_cl(IClArgs a, IntStepParam
     bias[g] = a.bias[c];
     rs[g] = a.rs[c];
   }
-  const unsigned plane_stride = static_cast<unsigned>(a.Bpad) * KS * 64;
+  const unsigned plane_stride = static_cast<unsigned>(s.Bpad) * KS * 64;
   // the exchange buffer, 2 NPL planes (32-bit byte offsets: checked by the launcher)
   const auto xr = cluster::buffer_rsrc(a.hx, 2u * NPL * plane_stride);
   const size_t NH = static_cast<size_t>(B) * H;
   v4i *myred = red + (static_cast<size_t>(utl) * 4 + kq) * 3 * NPL * 64;
-  unsigned epoch = 0;
-  bool alive = true;
-  for (int tile = pl.cluster; tile < a.ntiles && alive; tile += a.ncl) {
-    __syncthreads();  // the previous tile's readers of the partial-sum buffer are done
+  {
     const int b0 = tile * kITile, b = b0 + nr;
     const bool valid = b < B;
     int32_t hold = valid ? a.h0q[static_cast<size_t>(b) * H + j] : p.zp_h;
@@ -461,8 +468,8 @@ __global__ __launch_bounds__(512) void int_recurrence_cl(IClArgs a, IntStepParam
         wn_[g] = valid ? a.wx[(static_cast<size_t>(t) * B + b) * C + g * H + j] : 0;
     };
     load_wx(0);
-    alive = cluster::sync(counter, ++epoch * a.G, a.timeout, a.spin_limit);
-    for (int t = 0; t < a.T && alive; ++t) {
+    alive = cluster::sync(counter, ++epoch * s.G, s.timeout, s.spin_limit);
+    for (int t = 0; t < s.T && alive; ++t) {
       const int par = t & 1;
       const unsigned hin = par * NPL * plane_stride;  // byte offset of the step's planes
       int8_t *hnext = a.hx + (par ^ 1) * NPL * plane_stride;
@@ -576,9 +583,27 @@ __global__ __launch_bounds__(512) void int_recurrence_cl(IClArgs a, IntStepParam
           a.h_m[static_cast<size_t>(t) * NH + e] = k_h;
         }
       }
-      if (t + 1 < a.T) load_wx(t + 1);
-      alive = cluster::wait(counter, epoch * a.G, a.timeout, a.spin_limit);
+      if (t + 1 < s.T) load_wx(t + 1);
+      alive = cluster::wait(counter, epoch * s.G, s.timeout, s.spin_limit);
     }
+  }
+}
+
+template <int NPL>
+__global__ __launch_bounds__(512) void int_recurrence_cl(IClDir a0, IClDir a1,
+                                                         const IntStepParams *__restrict__ ps,
+                                                         IClArgs s) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const cluster::Place pl = cluster::place(s.G, s.ncl);
+  unsigned *counter = s.counters + pl.cluster;
+  unsigned epoch = 0;
+  bool alive = true;
+  for (int pair = pl.cluster; pair < s.ndir * s.ntiles && alive; pair += s.ncl) {
+    const int d = pair / s.ntiles, tile = pair % s.ntiles;
+    // the previous pair's readers of the LUT, the gate tables and the partial-sum buffer are
+    // done
+    __syncthreads();
+    int_cl_pair<NPL>(d == 0 ? a0 : a1, ps[d], s, tile, pl.member, counter, epoch, alive, smem);
   }
 }
 
@@ -595,7 +620,8 @@ __global__ __launch_bounds__(256) void poison_codes(const int *timeout, int64_t 
 // host
 // ---------------------------------------------------------------------------------
 struct IntWorkspace {
-  size_t hostblk, bias, wx, rh, hq, xa, bfrag, colsum, flag, rfrag, rcol, hx, sync, total;
+  size_t hostblk, bias, wx, rh, hq, xa, bfrag, colsum, flag, rfrag, rcol, hx, sync, sparams,
+      total;
   IntWorkspace(int T, int B, int I, int H) {
     const size_t C = 3 * static_cast<size_t>(H);
     const size_t Kp = static_cast<size_t>(xgemm::pad_k(I));
@@ -617,7 +643,8 @@ struct IntWorkspace {
     rfrag = o; o += al(sizeof(v4i) * 64 * (static_cast<size_t>(H) / 16) * 3 * KS);
     rcol = o; o += al(sizeof(int32_t) * C);
     hx = o; o += al(2 * 2 * Bpad * KS * 64);
-    sync = o; o += al(sizeof(unsigned) * (Bpad / kITile + 2));
+    sync = o; o += al(sizeof(unsigned) * (2 * Bpad / kITile + 2));  // counters of up to 2 directions
+    sparams = o; o += al(2 * sizeof(IntStepParams));
     total = o;
   }
 };
@@ -673,18 +700,32 @@ struct IntCall {
   void *workspace;
 };
 
-// The clustered recurrence when R_q fits signed 8 bits, h spans at most 16 bits, H is a
-// multiple of 16 up to 1024 and the grid can be resident at once; returns 1 when launched,
-// 0 when the caller must step, negative on error.
-static int int_recurrence_clustered(const IntCall &k, const IntStepParams &sp,
-                                    const IWeightArgs &wa, const int32_t *wx, const int32_t *hq0,
-                                    const IntWorkspace &ws, hipStream_t stream) {
-  const int T = k.T, B = k.B, H = k.H, C = 3 * H;
-  if (H % 16 != 0 || H > 1024 || wa.gR.lo < -128 || wa.gR.hi > 127 ||
-      std::getenv("RXMET_NO_CLUSTER") != nullptr)
-    return 0;
-  const rxmet_grid &gh = k.params->g[RXMET_GRU_H];
-  const int npl = gh.bits <= 8 ? 1 : 2;
+// One direction's call after its prologue (weights and inputs quantised, the input
+// projection done): what the recurrence reads and writes.
+struct IntPlan {
+  IntCall k;
+  IntStepParams sp;
+  IWeightArgs wa;
+  long long *bias;
+  IRescale *rs;
+  int32_t *wx, *rh, *hqb, *hq0;
+  char *wsb;
+};
+
+// The clustered recurrence for ndir directions in one launch, when R_q fits signed 8 bits,
+// h spans at most 16 bits (the same plane count in every direction), H is a multiple of 16 up
+// to 1024 and the grid can be resident at once; returns 1 when launched, 0 when the caller
+// must step, negative on error.
+static int int_recurrence_clustered(IntPlan *plans, int ndir, hipStream_t stream) {
+  const IntCall &k0 = plans[0].k;
+  const int T = k0.T, B = k0.B, H = k0.H, C = 3 * H;
+  if (H % 16 != 0 || H > 1024 || std::getenv("RXMET_NO_CLUSTER") != nullptr) return 0;
+  const int npl = k0.params->g[RXMET_GRU_H].bits <= 8 ? 1 : 2;
+  for (int d = 0; d < ndir; ++d) {
+    const IGrid &gR = plans[d].wa.gR;
+    if (gR.lo < -128 || gR.hi > 127) return 0;
+    if ((plans[d].k.params->g[RXMET_GRU_H].bits <= 8 ? 1 : 2) != npl) return 0;
+  }
   // the exchange buffer (2 npl planes of Bpad KS 64 bytes) is addressed with 32-bit offsets
   if (2.0 * npl * ((B + kITile - 1) / kITile * kITile) * ((H + 63) / 64 * 64) >= 2147483648.0) return 0;
   const void *fn = npl == 1 ? reinterpret_cast<const void *>(&int_recurrence_cl<1>)
@@ -692,89 +733,112 @@ static int int_recurrence_clustered(const IntCall &k, const IntStepParams &sp,
   int device = 0, ncu = 0;
   RXMET_CHECK_HIP(hipGetDevice(&device));
   RXMET_CHECK_HIP(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, device));
-  IClArgs a{};
-  a.T = T; a.B = B; a.H = H; a.KS = (H + 63) / 64;
-  a.ntiles = (B + kITile - 1) / kITile;
-  a.Bpad = a.ntiles * kITile;
+  IClArgs s{};
+  s.T = T; s.B = B; s.H = H; s.KS = (H + 63) / 64;
+  s.ndir = ndir;
+  s.ntiles = (B + kITile - 1) / kITile;
+  s.Bpad = s.ntiles * kITile;
+  const int pairs = ndir * s.ntiles;
   // the smallest unit slice per workgroup whose grid fits one workgroup per CU, else two tiles
-  a.UT = (H / 16) % 2 == 0 && static_cast<int64_t>(a.ntiles) * (H / 16) > ncu ? 2 : 1;
-  a.G = H / (16 * a.UT);
-  a.gate_tab = 1;
-  for (const IGrid &g : {sp.zin, sp.rin, sp.nin})
-    if (static_cast<int64_t>(g.hi) - g.lo >= kIGateTabMax) a.gate_tab = 0;
+  s.UT = (H / 16) % 2 == 0 && static_cast<int64_t>(pairs) * (H / 16) > ncu ? 2 : 1;
+  s.G = H / (16 * s.UT);
   const size_t lds = (3 * sizeof(ILut) + 15) / 16 * 16 +
-                     sizeof(v4i) * static_cast<size_t>(a.UT) * 4 * 3 * npl * 64 +
+                     sizeof(v4i) * static_cast<size_t>(s.UT) * 4 * 3 * npl * 64 +
                      sizeof(int32_t) * 3 * kIGateTabMax;
   RXMET_CHECK_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                       static_cast<int>(lds)));
   int per_cu = 0;
-  RXMET_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256 * a.UT, lds));
-  int ncl = per_cu * ncu / a.G;
+  RXMET_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256 * s.UT, lds));
+  int ncl = per_cu * ncu / s.G;
   if (ncl < 1) return 0;
-  if (ncl > a.ntiles) ncl = a.ntiles;
+  if (ncl > pairs) ncl = pairs;
   if (ncl >= 8) ncl -= ncl % 8;
-  a.ncl = ncl;
-  a.h_offset = gh.bits < 32 && gh.is_unsigned ? 1 << (gh.bits - 1) : 0;
-  char *wsb = static_cast<char *>(k.workspace);
-  v4i *rfrag = reinterpret_cast<v4i *>(wsb + ws.rfrag);
-  int32_t *rcol = reinterpret_cast<int32_t *>(wsb + ws.rcol);
-  hipLaunchKernelGGL(cluster::zero_words, dim3(1), dim3(256), 0, stream,
-                     reinterpret_cast<unsigned *>(rcol), C);
+  s.ncl = ncl;
+  const IntWorkspace ws(T, B, k0.I, H);
+  IClDir dirs[2]{};
+  IntStepParams host_ps[2];
+  for (int d = 0; d < ndir; ++d) {
+    IntPlan &pl = plans[d];
+    const IntCall &k = pl.k;
+    const rxmet_grid &gh = k.params->g[RXMET_GRU_H];
+    IClDir &a = dirs[d];
+    a.h_offset = gh.bits < 32 && gh.is_unsigned ? 1 << (gh.bits - 1) : 0;
+    a.gate_tab = 1;
+    for (const IGrid &g : {pl.sp.zin, pl.sp.rin, pl.sp.nin})
+      if (static_cast<int64_t>(g.hi) - g.lo >= kIGateTabMax) a.gate_tab = 0;
+    v4i *rfrag = reinterpret_cast<v4i *>(pl.wsb + ws.rfrag);
+    int32_t *rcol = reinterpret_cast<int32_t *>(pl.wsb + ws.rcol);
+    hipLaunchKernelGGL(cluster::zero_words, dim3(1), dim3(256), 0, stream,
+                       reinterpret_cast<unsigned *>(rcol), C);
+    RXMET_CHECK_LAUNCH();
+    hipLaunchKernelGGL(pack_r_frags_i32, dim3((H / 16) * 3 * s.KS), dim3(64), 0, stream, H, s.KS,
+                       k.Rq, rfrag, rcol);
+    RXMET_CHECK_LAUNCH();
+    a.wx = pl.wx;
+    a.rfrag = rfrag;
+    a.rcol = rcol;
+    a.bias = pl.wa.bias + C;
+    a.rs = pl.wa.rs + 2 * C;
+    a.h0q = pl.hq0;
+    a.hout = k.h;
+    a.v = k.v;
+    a.hq = k.hq_out;
+    a.hh_m = k.training ? k.hh_m : nullptr;
+    a.gin_m = k.training ? k.gin_m : nullptr;
+    a.gout_m = k.training ? k.gout_m : nullptr;
+    a.h_m = k.training ? k.h_m : nullptr;
+    if (a.gin_m && !(a.gout_m && a.h_m)) a.gin_m = nullptr;
+    a.hx = reinterpret_cast<int8_t *>(pl.wsb + ws.hx);
+    host_ps[d] = pl.sp;
+  }
+  if (ndir == 1) {
+    dirs[1] = dirs[0];
+    host_ps[1] = host_ps[0];
+  }
+  // both directions' step parameters in device memory (read with scalar loads)
+  IntStepParams *ps = reinterpret_cast<IntStepParams *>(plans[0].wsb + ws.sparams);
+  if (int rc = upload(ps, host_ps, sizeof(host_ps), stream)) return rc;
+  s.counters = reinterpret_cast<unsigned *>(plans[0].wsb + ws.sync);
+  s.timeout = reinterpret_cast<int *>(s.counters + ncl);
+  s.spin_limit = cluster::spin_limit();
+  hipLaunchKernelGGL(cluster::zero_words, dim3(1), dim3(256), 0, stream, s.counters, ncl + 1);
   RXMET_CHECK_LAUNCH();
-  hipLaunchKernelGGL(pack_r_frags_i32, dim3((H / 16) * 3 * a.KS), dim3(64), 0, stream, H, a.KS,
-                     k.Rq, rfrag, rcol);
-  RXMET_CHECK_LAUNCH();
-  a.wx = wx;
-  a.rfrag = rfrag;
-  a.rcol = rcol;
-  a.bias = wa.bias + C;
-  a.rs = wa.rs + 2 * C;
-  a.h0q = hq0;
-  a.hout = k.h;
-  a.v = k.v;
-  a.hq = k.hq_out;
-  a.hh_m = k.training ? k.hh_m : nullptr;
-  a.gin_m = k.training ? k.gin_m : nullptr;
-  a.gout_m = k.training ? k.gout_m : nullptr;
-  a.h_m = k.training ? k.h_m : nullptr;
-  if (a.gin_m && !(a.gout_m && a.h_m)) a.gin_m = nullptr;
-  a.hx = reinterpret_cast<int8_t *>(wsb + ws.hx);
-  a.counters = reinterpret_cast<unsigned *>(wsb + ws.sync);
-  a.timeout = reinterpret_cast<int *>(a.counters + ncl);
-  a.spin_limit = cluster::spin_limit();
-  hipLaunchKernelGGL(cluster::zero_words, dim3(1), dim3(256), 0, stream, a.counters, ncl + 1);
-  RXMET_CHECK_LAUNCH();
-  IntStepParams spc = sp;
-  void *args[] = {&a, &spc};
+  void *args[] = {&dirs[0], &dirs[1], &ps, &s};
   {
     rxmet::prof::Scope ps__("gru_int_recurrence", stream);
-    RXMET_CHECK_HIP(cluster::launch(fn, dim3(ncl * a.G), dim3(256 * a.UT), args,
+    RXMET_CHECK_HIP(cluster::launch(fn, dim3(ncl * s.G), dim3(256 * s.UT), args,
                                     static_cast<unsigned>(lds), stream));
   }
   // a wait that timed out: every output after row 0 becomes NaN (codes: INT32_MIN)
   const size_t NH = static_cast<size_t>(B) * H;
   cluster::PoisonList pl{};
-  if (k.h) {
-    pl.p[pl.count] = k.h + NH;
-    pl.n[pl.count++] = static_cast<int64_t>(T) * NH;
-  }
-  if (k.v) {
-    pl.p[pl.count] = k.v;
-    pl.n[pl.count++] = static_cast<int64_t>(T) * NH * 4;
+  for (int d = 0; d < ndir; ++d) {
+    const IntCall &k = plans[d].k;
+    if (k.h) {
+      pl.p[pl.count] = k.h + NH;
+      pl.n[pl.count++] = static_cast<int64_t>(T) * NH;
+    }
+    if (k.v) {
+      pl.p[pl.count] = k.v;
+      pl.n[pl.count++] = static_cast<int64_t>(T) * NH * 4;
+    }
   }
   if (pl.count) {
-    hipLaunchKernelGGL(cluster::poison_list, dim3(256), dim3(256), 0, stream, a.timeout, pl);
+    hipLaunchKernelGGL(cluster::poison_list, dim3(256), dim3(256), 0, stream, s.timeout, pl);
     RXMET_CHECK_LAUNCH();
   }
-  if (k.hq_out) {
-    hipLaunchKernelGGL(poison_codes, dim3(256), dim3(256), 0, stream, a.timeout,
-                       static_cast<int64_t>(T) * NH, k.hq_out + NH);
-    RXMET_CHECK_LAUNCH();
-  }
+  for (int d = 0; d < ndir; ++d)
+    if (plans[d].k.hq_out) {
+      hipLaunchKernelGGL(poison_codes, dim3(256), dim3(256), 0, stream, s.timeout,
+                         static_cast<int64_t>(T) * NH, plans[d].k.hq_out + NH);
+      RXMET_CHECK_LAUNCH();
+    }
   return 1;
 }
 
-static int forward_int(const IntCall &k, hipStream_t stream) {
+// Checks, parameters, weight and input quantisation and the input projection of one
+// direction.
+static int prologue_int(const IntCall &k, hipStream_t stream, IntPlan &plan) {
   const int T = k.T, B = k.B, I = k.I, H = k.H;
   RXMET_CHECK_ARG(k.params != nullptr && k.workspace != nullptr, "params and workspace must be non-null");
   RXMET_CHECK_ARG(T >= 1 && B >= 1 && I >= 1 && H >= 1, "dimensions must be positive");
@@ -802,10 +866,8 @@ static int forward_int(const IntCall &k, hipStream_t stream) {
   IRescale *rs = reinterpret_cast<IRescale *>(wsb + ws.hostblk + 4 * static_cast<size_t>(C) * sizeof(float));
   long long *bias = reinterpret_cast<long long *>(wsb + ws.bias);
   int32_t *wx = reinterpret_cast<int32_t *>(wsb + ws.wx);
-  int32_t *rh = reinterpret_cast<int32_t *>(wsb + ws.rh);
-  int32_t *hqb = reinterpret_cast<int32_t *>(wsb + ws.hq);
 
-  IntStepParams sp;
+  IntStepParams &sp = plan.sp;
   std::vector<char> host(4 * static_cast<size_t>(C) * (sizeof(float) + sizeof(IRescale)));
   try {
     make_int_step_params(P, H, &sp);
@@ -840,8 +902,8 @@ static int forward_int(const IntCall &k, hipStream_t stream) {
     RXMET_CHECK_ARG(bad == 0, "x_q / h0_q hold codes outside the x / h grids");
   }
 
-  RXMET_CHECK_HIP(hipMemcpyAsync(wsb + ws.hostblk, host.data(), host.size(), hipMemcpyHostToDevice, stream));
-  IWeightArgs wa;
+  if (int rc = upload(wsb + ws.hostblk, host.data(), host.size(), stream)) return rc;
+  IWeightArgs &wa = plan.wa;
   wa.W = k.W; wa.R = k.R; wa.bw = k.bw; wa.br = k.br;
   wa.eff = eff; wa.rs = rs;
   wa.gW = igrid_of(P.chan_bits[RXMET_GRU_W], P.chan_unsigned[RXMET_GRU_W]);
@@ -863,7 +925,8 @@ static int forward_int(const IntCall &k, hipStream_t stream) {
   RXMET_CHECK_LAUNCH();
 
   const int64_t nx = k.xq_in ? 0 : static_cast<int64_t>(T) * B * I, nh = static_cast<int64_t>(B) * H;
-  int32_t *hq0 = k.hq_out ? k.hq_out : hqb;
+  plan.hqb = reinterpret_cast<int32_t *>(wsb + ws.hq);
+  int32_t *hq0 = k.hq_out ? k.hq_out : plan.hqb;
   {
     rxmet::prof::Scope ps__("gru_int_quant_input", stream);
     const int64_t blocks = std::min<int64_t>((nx + nh + 255) / 256, 8192);
@@ -885,31 +948,41 @@ static int forward_int(const IntCall &k, hipStream_t stream) {
                                k.Wq, C, C, pb, e, wsb, ws, stream))
       return rc;
   }
+  plan.k = k;
+  plan.bias = bias;
+  plan.rs = rs;
+  plan.wx = wx;
+  plan.rh = reinterpret_cast<int32_t *>(wsb + ws.rh);
+  plan.hq0 = hq0;
+  plan.wsb = wsb;
+  return 0;
+}
 
-  // recurrence: clustered when it applies, else per step R_q (h - zp_h) + br ->
-  // weight_hh_linear codes, then the gates
+// The stepped recurrence of one direction: per step R_q (h - zp_h) + br -> weight_hh_linear
+// codes, then the gates.
+static int stepped_int(const IntPlan &plan, hipStream_t stream) {
+  const IntCall &k = plan.k;
+  const IntStepParams &sp = plan.sp;
+  const int T = k.T, B = k.B, I = k.I, H = k.H, C = 3 * H;
+  const IntWorkspace ws(T, B, I, H);
+  const int64_t nh = static_cast<int64_t>(B) * H;
   const double hlo = sp.h.lo, hhi = sp.h.hi;
-  {
-    const int rc = int_recurrence_clustered(k, sp, wa, wx, hq0, ws, stream);
-    if (rc < 0) return rc;
-    if (rc == 1) return 0;
-  }
   const float hoff = xgemm::a_shift(hlo, hhi);
-  const int hpa = xgemm::a_planes(hlo, hhi), rpb = xgemm::b_planes(wa.gR.lo, wa.gR.hi);
+  const int hpa = xgemm::a_planes(hlo, hhi), rpb = xgemm::b_planes(plan.wa.gR.lo, plan.wa.gR.hi);
   IPointArgs pa;
   pa.T = T; pa.B = B; pa.H = H;
-  pa.wx = wx; pa.rh = rh; pa.hout = k.h; pa.v = k.v;
+  pa.wx = plan.wx; pa.rh = plan.rh; pa.hout = k.h; pa.v = k.v;
   pa.gin_m = k.training ? k.gin_m : nullptr;
   pa.gout_m = k.training ? k.gout_m : nullptr;
   pa.h_m = k.training ? k.h_m : nullptr;
   if (pa.gin_m && !(pa.gout_m && pa.h_m)) pa.gin_m = nullptr;
   const dim3 pgrid(static_cast<unsigned>((nh + 255) / 256));
   rxmet::prof::Scope ps__("gru_int_recurrence", stream);
-  const int32_t *hcur = hq0;
+  const int32_t *hcur = plan.hq0;
   for (int t = 0; t < T; ++t) {
     int32_t *hnext = k.hq_out ? k.hq_out + (static_cast<size_t>(t) + 1) * nh
-                              : hqb + static_cast<size_t>((t + 1) & 1) * nh;
-    LinearOut e{bias + C, rs + 2 * C, sp.zp_rh, sp.rh, rh,
+                              : plan.hqb + static_cast<size_t>((t + 1) & 1) * nh;
+    LinearOut e{plan.bias + C, plan.rs + 2 * C, sp.zp_rh, sp.rh, plan.rh,
                 k.training && k.hh_m ? k.hh_m + static_cast<size_t>(t) * B * C : nullptr, C};
     if (int rc = launch_linear(hcur, H, B, H, hoff, static_cast<long long>(hoff) - sp.zp_h, hpa,
                                k.Rq, C, C, rpb, e, nullptr, ws, stream))
@@ -919,6 +992,31 @@ static int forward_int(const IntCall &k, hipStream_t stream) {
     hcur = hnext;
   }
   return 0;
+}
+
+// ndir directions with the same shapes (each with its own workspace): the prologues, then
+// one clustered launch for all of them, or each direction stepped.
+static int forward_int_dirs(const IntCall *calls, int ndir, hipStream_t stream) {
+  RXMET_CHECK_ARG(ndir == 1 || ndir == 2, "ndir must be 1 or 2");
+  IntPlan plans[2];
+  for (int d = 0; d < ndir; ++d) {
+    if (d > 0)
+      RXMET_CHECK_ARG(calls[d].T == calls[0].T && calls[d].B == calls[0].B &&
+                          calls[d].I == calls[0].I && calls[d].H == calls[0].H &&
+                          calls[d].training == calls[0].training,
+                      "the directions must have the same shapes and mode");
+    if (int rc = prologue_int(calls[d], stream, plans[d])) return rc;
+  }
+  const int rc = int_recurrence_clustered(plans, ndir, stream);
+  if (rc < 0) return rc;
+  if (rc == 1) return 0;
+  for (int d = 0; d < ndir; ++d)
+    if (int r = stepped_int(plans[d], stream)) return r;
+  return 0;
+}
+
+static int forward_int(const IntCall &k, hipStream_t stream) {
+  return forward_int_dirs(&k, 1, stream);
 }
 
 }  // namespace
@@ -962,6 +1060,47 @@ int rxmet_gru_forward_quant_int(int32_t is_training, int32_t T, int32_t B, int32
   k.gout_m = gate_out_mask; k.h_m = h_mask;
   k.workspace = workspace;
   return forward_int(k, static_cast<hipStream_t>(stream));
+}
+
+int rxmet_gru_forward_quant_int_dirs(int32_t ndir, int32_t is_training, int32_t T, int32_t B,
+                                     int32_t I, int32_t H, const rxmet_gru_int_dir *dirs,
+                                     void *stream) {
+  clear_error();
+  RXMET_CHECK_ARG(ndir == 1 || ndir == 2, "ndir must be 1 or 2");
+  RXMET_CHECK_ARG(dirs != nullptr, "dirs must be non-null");
+  IntCall calls[2]{};
+  const bool io = dirs[0].x_q_in != nullptr;
+  for (int d = 0; d < ndir; ++d) {
+    const rxmet_gru_int_dir &a = dirs[d];
+    RXMET_CHECK_ARG((a.x_q_in != nullptr) == io, "both directions must be int-IO or neither");
+    IntCall &k = calls[d];
+    k.T = T; k.B = B; k.I = I; k.H = H;
+    k.W = a.W; k.R = a.R; k.bw = a.bw; k.br = a.br;
+    k.params = a.params;
+    k.Wq = a.W_q; k.Rq = a.R_q; k.bwq = a.bw_q; k.brq = a.br_q;
+    k.workspace = a.workspace;
+    if (io) {
+      RXMET_CHECK_ARG(!is_training, "int-IO directions run without training outputs");
+      RXMET_CHECK_ARG(a.h_q != nullptr, "x_q_in and h_q must be non-null");
+      k.training = false;
+      k.xq_in = a.x_q_in; k.h0q_in = a.h0_q_in;
+      k.hq_out = a.h_q;
+    } else {
+      RXMET_CHECK_ARG(a.x && a.h && a.x_q, "x, h and x_q must be non-null");
+      if (is_training)
+        RXMET_CHECK_ARG(a.v && a.x_mask && a.W_mask && a.R_mask && a.bw_mask && a.br_mask &&
+                            a.ih_mask && a.hh_mask && a.gate_in_mask && a.gate_out_mask &&
+                            a.h_mask && (a.h0 == nullptr || a.h0_mask),
+                        "training needs v and every mask output");
+      k.training = is_training != 0;
+      k.x = a.x; k.h0 = a.h0;
+      k.h = a.h; k.v = a.v; k.xq = a.x_q;
+      k.x_m = a.x_mask; k.h0_m = a.h0_mask; k.W_m = a.W_mask; k.R_m = a.R_mask;
+      k.bw_m = a.bw_mask; k.br_m = a.br_mask; k.ih_m = a.ih_mask; k.hh_m = a.hh_mask;
+      k.gin_m = a.gate_in_mask; k.gout_m = a.gate_out_mask; k.h_m = a.h_mask;
+    }
+  }
+  return forward_int_dirs(calls, ndir, static_cast<hipStream_t>(stream));
 }
 
 int rxmet_gru_forward_int_io(int32_t T, int32_t B, int32_t I, int32_t H, const float *W,

@@ -574,12 +574,13 @@ def forward_quant_float_storage_dirs_x(is_training, time_steps, batch_size, inpu
 
 def bidir_assemble(h_f, h_r, batch_first: bool):
     """(output, h_n) of a bidirectional layer from both directions' h [T+1, B, H]
-    (rxmet_gru_bidir_assemble): output [T, B, 2H], or [B, T, 2H] when batch_first."""
+    (rxmet_gru_bidir_assemble): output [T, B, 2H], or [B, T, 2H] when batch_first.  The
+    assembly copies 4-byte elements, so float32 states and int32 codes alike."""
     T1, B, H = h_f.shape
     T = T1 - 1
     shape = (B, T, 2 * H) if batch_first else (T, B, 2 * H)
-    out = torch.empty(shape, dtype=torch.float32, device=h_f.device)
-    h_n = torch.empty((2, B, H), dtype=torch.float32, device=h_f.device)
+    out = torch.empty(shape, dtype=h_f.dtype, device=h_f.device)
+    h_n = torch.empty((2, B, H), dtype=h_f.dtype, device=h_f.device)
     st, sb = (out.stride(1), out.stride(0)) if batch_first else (out.stride(0), out.stride(1))
     _rx.call("rxmet_gru_bidir_assemble", T, B, H, h_f.data_ptr(), h_r.data_ptr(), out.data_ptr(),
              st, sb, h_n.data_ptr(), _stream(h_f.device))
@@ -750,6 +751,62 @@ def forward_quant_int_storage(is_training, time_steps, batch_size, input_size, h
              v.data_ptr(), W_q.data_ptr(), R_q.data_ptr(), bw_q.data_ptr(), br_q.data_ptr(),
              x_q.data_ptr(), *mp, ws.data_ptr(), _stream(dev))
     return (h, v, W_q, R_q, bw_q, br_q, x_q, *masks)
+
+
+def _int_dir_struct(**fields):
+    d = A.IntDir()
+    for k, v in fields.items():
+        setattr(d, k, v)
+    return d
+
+
+def forward_int_bidir(T, B, I, H, dirs, int_io=False):
+    """Both directions of a bidirectional layer on the int32 carrier in one call
+    (rxmet_gru_forward_quant_int_dirs; no counterpart in the reference, which calls the
+    per-direction wrappers): one clustered recurrence launch covers both directions.  dirs: two
+    tuples (W, R, bw, br, x, h0, quant_params), each direction's x in its own time order (x
+    int32 codes when int_io).  Inference only: returns, per direction, h [T+1,B,H] float32
+    (int_io: h_q [T+1,B,H] int32 codes)."""
+    dev = dirs[0][4].device
+    C = 3 * H
+    i32 = dict(dtype=torch.int32, device=dev)
+    f32 = dict(dtype=torch.float32, device=dev)
+    structs, keep, outs = [], [], []
+    for W, R, bw, br, x, h0, qp in dirs:
+        for n, t in (("W", W), ("R", R), ("bw", bw), ("br", br)):
+            _check_f32_cuda(n, t)
+        (_check_i32_cuda if int_io else _check_f32_cuda)("x", x)
+        if tuple(x.shape) != (T, B, I):
+            raise RuntimeError("x must have shape [time_steps, batch_size, input_size]")
+        has_h0 = h0 is not None and h0.numel() > 0
+        if has_h0:
+            (_check_i32_cuda if int_io else _check_f32_cuda)("h0", h0)
+            if tuple(h0.shape) != (B, H):
+                raise RuntimeError("h0 must have shape [batch_size, hidden_size]")
+        codes = [torch.empty(s_, **i32) for s_ in ((I, C), (H, C), (C,), (C,))]
+        ws = _ws(_rx.load().rxmet_gru_forward_int_workspace_bytes(T, B, I, H), dev)
+        x = x.contiguous()
+        h0c = h0.contiguous() if has_h0 else None
+        f = dict(W=W.data_ptr(), R=R.data_ptr(), bw=bw.data_ptr(), br=br.data_ptr(),
+                 params=ctypes.addressof(qp.struct),
+                 W_q=codes[0].data_ptr(), R_q=codes[1].data_ptr(), bw_q=codes[2].data_ptr(),
+                 br_q=codes[3].data_ptr(), workspace=ws.data_ptr())
+        if int_io:
+            h = torch.empty((T + 1, B, H), **i32)
+            f.update(x_q_in=x.data_ptr(), h0_q_in=h0c.data_ptr() if has_h0 else None,
+                     h_q=h.data_ptr())
+            keep += [x, h0c, ws, codes]
+        else:
+            h = torch.empty((T + 1, B, H), **f32)
+            x_q = torch.empty((T, B, I), **i32)
+            f.update(x=x.data_ptr(), h0=h0c.data_ptr() if has_h0 else None, h=h.data_ptr(),
+                     x_q=x_q.data_ptr())
+            keep += [x, h0c, ws, codes, x_q]
+        structs.append(_int_dir_struct(**f))
+        outs.append(h)
+    arr = (A.IntDir * 2)(*structs)
+    _rx.call("rxmet_gru_forward_quant_int_dirs", 2, 0, T, B, I, H, arr, _stream(dev))
+    return outs
 
 
 def backward_quant_int_storage(time_steps, batch_size, input_size, hidden_size, W_q, R_q, bw_q,

@@ -1157,6 +1157,9 @@ class QuantGRU(nn.Module):
         input = ensure_cuda_float32(input, device)
         h0f, h0r = self._parse_initial_state(hx, B)
         save_state = self._save_state(input, hx)
+        if (self.bidirectional and self.use_quantization and not save_state
+                and self.quant_storage_dtype == "int32" and self.hidden_size % 4 == 0):
+            return self._forward_int_bidir(input, h0f, h0r, device)
         b = self.bias
         out_f, hn_f = GRUFunction.apply(
             input, self.weight_ih_l0, self.weight_hh_l0, self.bias_ih_l0 if b else None,
@@ -1171,6 +1174,23 @@ class QuantGRU(nn.Module):
                 self.quant_storage_dtype)
             out_r = out_r.flip(0)
         return self._combine_bidirectional_outputs(out_f, hn_f, out_r, hn_r)
+
+    def _forward_int_bidir(self, input, h0f, h0r, device, int_io=False):
+        """Inference of both directions on the int32 carrier in one library call (one clustered
+        recurrence launch for the two directions) and the output assembled in the library; the
+        reverse direction reads a time-flipped copy of the input.  Replaces the per-direction
+        calls with flip / cat of the reference (quant_gru.py:2207-2288, 2482-2537)."""
+        T, B, I = input.shape
+        H = self.hidden_size
+        dirs = []
+        for reverse, h0 in ((False, h0f), (True, h0r)):
+            if h0 is not None and not int_io:
+                h0 = ensure_cuda_float32(h0, device).contiguous()
+            W, R, bw, br = self._direction_weights(reverse, device)
+            qp = self.quant_params_reverse if reverse else self.quant_params
+            dirs.append((W, R, bw, br, input.flip(0) if reverse else input, h0, qp))
+        h_f, h_r = gru_ops.forward_int_bidir(T, B, I, H, dirs, int_io=int_io)
+        return gru_ops.bidir_assemble(h_f, h_r, False)
 
     def _save_state(self, input, hx) -> bool:
         """Gate values and masks are kept whenever a backward may follow
@@ -1304,6 +1324,11 @@ class QuantGRU(nn.Module):
             hx = hx.to(device=device, dtype=torch.int32)
             h0f = hx[0].contiguous()
             h0r = hx[1].contiguous() if self.bidirectional else None
+        if self.bidirectional and self.hidden_size % 4 == 0:
+            output_q, h_n_q = self._forward_int_bidir(input, h0f, h0r, device, int_io=True)
+            if self.batch_first:
+                output_q = output_q.transpose(0, 1).contiguous()
+            return output_q, h_n_q
         out_f, hn_f = self._forward_quantized_dir(input, h0f, False, device)
         out_r = hn_r = None
         if self.bidirectional:

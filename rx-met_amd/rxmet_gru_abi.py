@@ -78,6 +78,17 @@ class FwdDir(ctypes.Structure):
     _fields_ = [(n, _p) for n in FWD_DIR_FIELDS]
 
 
+INT_DIR_FIELDS = ("W", "R", "bw", "br", "x", "h0", "x_q_in", "h0_q_in", "params", "h", "v", "h_q",
+                  "W_q", "R_q", "bw_q", "br_q", "x_q", "x_mask", "h0_mask", "W_mask", "R_mask",
+                  "bw_mask", "br_mask", "ih_mask", "hh_mask", "gate_in_mask", "gate_out_mask",
+                  "h_mask", "workspace")
+
+
+class IntDir(ctypes.Structure):
+    """rxmet_gru_int_dir: the arguments of one rxmet_gru_forward_quant_int (or int-IO) call."""
+    _fields_ = [(n, _p) for n in INT_DIR_FIELDS]
+
+
 class BwdDir(ctypes.Structure):
     """rxmet_gru_bwd_dir: the arguments of one rxmet_gru_backward_quant call."""
     _fields_ = [(n, _p) for n in BWD_DIR_FIELDS]
@@ -109,6 +120,7 @@ _SIGS = {
                                     [ctypes.POINTER(GruQParams)] + [_p] * 18 + [_p, _p]),
     "rxmet_gru_forward_int_io": (ctypes.c_int, [_i32] * 4 + [_p] * 6 +
                                  [ctypes.POINTER(GruQParams)] + [_p] * 5 + [_p, _p]),
+    "rxmet_gru_forward_quant_int_dirs": (ctypes.c_int, [_i32] * 6 + [ctypes.POINTER(IntDir), _p]),
 }
 for _name, (_res, _args) in _SIGS.items():
     _rx.register(_name, _res, _args)

@@ -177,3 +177,43 @@ def test_forward_quantized_equals_int32_storage_forward(cuda, bidirectional, bat
             np.testing.assert_array_equal(deq.cpu().numpy(), ref.cpu().numpy(), err_msg=f"dir{d}")
     with pytest.raises(TypeError, match="integer codes"):
         m.forward_quantized(x.to(cuda))
+
+
+@pytest.mark.parametrize("with_hx", [False, True])
+@pytest.mark.parametrize("cfg", ["c3", "po2-16b"])
+@pytest.mark.parametrize("shape", [(7, 160, 12, 64), (6, 24, 10, 36), (5, 40, 8, 256)], ids=str)
+def test_int32_inference_both_directions_in_one_call(cuda, with_hx, cfg, shape):
+    """Bidirectional PTQ inference on the int32 carrier (eval, no autograd) runs both directions
+    through rxmet_gru_forward_quant_int_dirs — one clustered recurrence launch for the two
+    (H = 64: ten batch tiles, several per cluster; H = 256; H = 36, not a multiple of 16, steps
+    each direction) — and assembles the output in the library: output and h_n equal the oracle's
+    int32 carrier of each direction bit for bit, and the int-IO form equals it too."""
+    print(f"[quantgru int32 bidir inference] hx={with_hx} cfg={cfg} shape={shape}", flush=True)
+    m, x_tbi, hx = _module_case(True, False, with_hx, cfg, 29, shape=shape)
+    m.quant_storage_dtype = "int32"
+    m = m.to(cuda)
+    x_in = x_tbi.to(cuda)
+    hx_d = hx.to(cuda) if hx is not None else None
+    with m.calibration_context():
+        m(x_in, hx_d)
+    m.use_quantization = True
+    m.eval()
+    with torch.no_grad():
+        out, hn = m(x_in, hx_d)
+    torch.cuda.synchronize()
+    H = m.hidden_size
+    xn = x_tbi.numpy()
+    outn = out.cpu().numpy()
+    for d in range(2):
+        sfx = "_reverse" if d else ""
+        qp = (m.quant_params_reverse if d else m.quant_params).struct
+        pn = lambda n: getattr(m, n + sfx).detach().cpu().numpy()
+        W, R, bw, br = _haste(pn("weight_ih_l0"), pn("weight_hh_l0"), pn("bias_ih_l0"),
+                              pn("bias_hh_l0"))
+        xs = xn[::-1].copy() if d else xn
+        h0 = hx[d].numpy() if hx is not None else None
+        fwd = GO.forward_int(W, R, bw, br, xs, qp, h0=h0, training=False)
+        h = GO.dequant_int(fwd["h_q"], qp.g[A.GRID["h"]], bool(qp.use_pot2))
+        o = h[1:][::-1] if d else h[1:]
+        np.testing.assert_array_equal(outn[..., d * H:(d + 1) * H], o, err_msg=f"out dir{d}")
+        np.testing.assert_array_equal(hn[d].cpu().numpy(), h[-1], err_msg=f"h_n dir{d}")
