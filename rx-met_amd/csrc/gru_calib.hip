@@ -14,7 +14,10 @@
 // running ranges; per-channel ranges of W, R, bw and br are reduced
 // by a separate kernel.
 #include <cfloat>
+#include <cstdlib>
 
+#include "cluster.h"
+#include "mfma_frag.h"
 #include "rxmet_common.h"
 #include "rxmet_gru.h"
 
@@ -160,6 +163,439 @@ __global__ void stats_merge(const unsigned *o, float *s) {
   }
 }
 
+// ---------------------------------------------------------------------------------
+// MFMA form (H a multiple of 16, H <= 1024): the input projection of every step as one fp32
+// MFMA GEMM, then the recurrence as a clustered persistent kernel with R resident in VGPRs.
+// Products and sums are fp32 (v_mfma_f32_16x16x4f32) in another order than the sequential
+// sums above; results agree to rounding (the calibration is held to 1e-5, not bit-exactness).
+// Statistics: every workgroup writes its (min, max) partials to the workspace and one small
+// kernel folds them, in a fixed order, into this call's ordered ranges (no contended atomics).
+// ---------------------------------------------------------------------------------
+constexpr int kCT = 16;      // batch rows of a tile
+constexpr int kCMaxW = 16;   // waves of a recurrence workgroup
+constexpr int kGemmRBMax = 8;  // 64-row tiles per input-projection workgroup, at most
+
+// Block-wide (min, max) of n statistics, written by thread 0 to part[0..n) / part[n..2n).
+__device__ __forceinline__ void block_stats(const float *mn, const float *mx, int n, float *part) {
+  __shared__ float smn[kCMaxW][kNStat], smx[kCMaxW][kNStat];
+  const int w = threadIdx.x / kWave, nw = blockDim.x / kWave;
+  for (int i = 0; i < n; ++i) {
+    const float lo = wave_min(mn[i]), hi = wave_max(mx[i]);
+    if (threadIdx.x % kWave == 0) {
+      smn[w][i] = lo;
+      smx[w][i] = hi;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < n) {
+    float lo = smn[0][threadIdx.x], hi = smx[0][threadIdx.x];
+    for (int ww = 1; ww < nw; ++ww) {
+      lo = fminf(lo, smn[ww][threadIdx.x]);
+      hi = fmaxf(hi, smx[ww][threadIdx.x]);
+    }
+    part[threadIdx.x] = lo;
+    part[n + threadIdx.x] = hi;
+  }
+}
+
+// Fold P partial blocks of 2 n floats (n statistics starting at i0) into the ordered ranges
+// (statistics a block did not observe hold FLT_MAX / -FLT_MAX and change nothing).
+__global__ __launch_bounds__(256) void stats_fold(const float *__restrict__ part, int P, int n,
+                                                  int i0, unsigned *__restrict__ ostat) {
+  __shared__ float smn[4][kNStat], smx[4][kNStat];
+  const int w = threadIdx.x / kWave;
+  for (int i = 0; i < n; ++i) {
+    float lo = FLT_MAX, hi = -FLT_MAX;
+    for (int p = threadIdx.x; p < P; p += blockDim.x) {
+      lo = fminf(lo, part[static_cast<size_t>(p) * 2 * n + i]);
+      hi = fmaxf(hi, part[static_cast<size_t>(p) * 2 * n + n + i]);
+    }
+    lo = wave_min(lo);
+    hi = wave_max(hi);
+    if (threadIdx.x % kWave == 0) {
+      smn[w][i] = lo;
+      smx[w][i] = hi;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < n) {
+    float lo = smn[0][threadIdx.x], hi = smx[0][threadIdx.x];
+    for (int ww = 1; ww < 4; ++ww) {
+      lo = fminf(lo, smn[ww][threadIdx.x]);
+      hi = fmaxf(hi, smx[ww][threadIdx.x]);
+    }
+    if (lo <= hi) {  // merged: one thread per statistic, so no contention
+      atomicMin(&ostat[i0 + threadIdx.x], f2ord(lo));
+      atomicMax(&ostat[kNStat + i0 + threadIdx.x], f2ord(hi));
+    }
+  }
+}
+
+// wx[m][c] = sum_k x[m][k] W[k][c] + bw[c] for m < M = T B, c < C = 3H, with the X and WX
+// statistics.  A workgroup covers 64 columns of RB 64-row tiles; each of its four waves a
+// 32 x 32 block of 2 x 2 MFMA tiles per row tile.  The contraction runs in blocks of 16 k, lane
+// group g taking k = k0 + 4 g + s at sub-step s, so a lane reads four consecutive x of a row
+// (one 16-byte load where K allows) and four rows of one W column.
+template <bool STATS>
+__global__ __launch_bounds__(256) void calib_input_gemm(int M, int K, int C, int RB,
+                                                        const float *__restrict__ x,
+                                                        const float *__restrict__ W,
+                                                        const float *__restrict__ bw,
+                                                        float *__restrict__ wx,
+                                                        float *__restrict__ part) {
+  const int w = threadIdx.x / kWave, l = threadIdx.x % kWave, r = l % 16, g = l / 16;
+  const int n0 = blockIdx.x * 64 + (w % 2) * 32;
+  const bool see_x = STATS && blockIdx.x == 0, vec = K % 4 == 0;
+  float st_mn[kNStat], st_mx[kNStat];  // X and WX observed here
+#pragma unroll
+  for (int i = 0; i < kNStat; ++i) {
+    st_mn[i] = FLT_MAX;
+    st_mx[i] = -FLT_MAX;
+  }
+  for (int rt = 0; rt < RB; ++rt) {
+    const int m0 = (blockIdx.y * RB + rt) * 64 + (w / 2) * 32;
+    if (m0 >= M) break;
+    v4f acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int k0 = 0; k0 < K; k0 += 16) {
+      float a[2][4], b[2][4];
+      const int kb = k0 + 4 * g;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int row = m0 + 16 * i + r;
+        const float *xr = x + static_cast<size_t>(row) * K + kb;
+        if (row < M && vec && kb + 3 < K) {
+          const float4 v = *reinterpret_cast<const float4 *>(xr);
+          a[i][0] = v.x; a[i][1] = v.y; a[i][2] = v.z; a[i][3] = v.w;
+        } else {
+#pragma unroll
+          for (int s = 0; s < 4; ++s) a[i][s] = row < M && kb + s < K ? xr[s] : 0.0f;
+        }
+        if (see_x && row < M)
+#pragma unroll
+          for (int s = 0; s < 4; ++s)
+            if (kb + s < K) observe(a[i][s], st_mn[RXMET_GRU_X], st_mx[RXMET_GRU_X]);
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int col = n0 + 16 * j + r;
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          b[j][s] = col < C && kb + s < K ? W[static_cast<size_t>(kb + s) * C + col] : 0.0f;
+      }
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) acc[i][j] = mfma_f32(a[i][s], b[j][s], acc[i][j]);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int col = n0 + 16 * j + r;
+        if (col >= C) continue;
+        const float bias = bw[col];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int row = m0 + 16 * i + 4 * g + q;
+          if (row < M) {
+            const float v = acc[i][j][q] + bias;
+            wx[static_cast<size_t>(row) * C + col] = v;
+            if (STATS) observe(v, st_mn[RXMET_GRU_WX], st_mx[RXMET_GRU_WX]);
+          }
+        }
+      }
+  }
+  if (STATS)
+    block_stats(st_mn, st_mx, kNStat,
+                part + (static_cast<size_t>(blockIdx.y) * gridDim.x + blockIdx.x) * 2 * kNStat);
+}
+
+struct CalClArgs {
+  int T, B, H, NC, NWG, ntiles, Bpad, Hpad, G, ncl;
+  const float *wx;   // [T, B, 3H] input projection with bw
+  const float *R;    // [H, 3H]
+  const float *br;   // [3H]
+  const float *h0;   // [B, H] or null
+  float *hout;       // [T+1, B, H]
+  float *v;          // [T, B, 4H] or null
+  float *hx;         // [2][Bpad][Hpad] exchanged h (padding columns zero)
+  float *part;       // [ncl G][2 x 13] partial statistics
+  unsigned *counters;
+  int *timeout;
+  unsigned spin_limit;
+};
+
+// Member m of a cluster owns units 16 m .. 16 m + 15 of one 16-row batch tile.  The recurrent
+// product splits into items (k chunk c of 64, gate): 3 NC items, dealt to the workgroup's NWG
+// waves (wave w takes items w, w + NWG, ...: IPW at most).  An item is sixteen MFMAs, MFMA s
+// taking k = 64 c + 16 g + s for lane group g, so a lane's A values are 16 consecutive h of its
+// row (four 16-byte coherent loads) and its B values (R) stay in VGPRs for the whole launch.
+// The items' partial tiles meet in LDS; each of the tile's 256 (row, unit) elements is then
+// finished by one thread (the gates, the new h and the statistics), its previous h kept in a
+// register.  NWG >= 4, so the 256 elements have threads of their own.
+template <bool STATS, int IPW>
+__global__ __launch_bounds__(64 * kCMaxW) void calib_recurrence_cl(CalClArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  v4f *red = reinterpret_cast<v4f *>(smem);  // [3 NC][64]
+  const cluster::Place pl = cluster::place(a.G, a.ncl);
+  unsigned *counter = a.counters + pl.cluster;
+  const int H = a.H, C = 3 * H, B = a.B, NC = a.NC, NWG = a.NWG;
+  const int tid = threadIdx.x, w = tid / kWave, l = tid % kWave, r16 = l % 16, g = l / 16;
+  const int u0 = 16 * pl.member;
+  const int nitems = 3 * NC;
+  float rfr[IPW][16];
+#pragma unroll
+  for (int it = 0; it < IPW; ++it) {
+    const int item = w + it * NWG, ch = item / 3, gate = item % 3;
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+      const int k = 64 * ch + 16 * g + s;
+      rfr[it][s] = item < nitems && k < H
+                       ? a.R[static_cast<size_t>(k) * C + gate * H + u0 + r16] : 0.0f;
+    }
+  }
+  // the finishing element of this thread (tid < 256): row 4 (tid % 64 / 16) + tid / 64 and
+  // unit u0 + tid % 16 of the tile, which lane tid % 64 holds as accumulator tid / 64
+  const bool fin = tid < 256;
+  const int fl = tid % 64, fq = tid / 64;
+  const int frow = 4 * (fl / 16) + fq, fu = u0 + fl % 16;
+  const float bz = fin ? a.br[fu] : 0.0f, brr = fin ? a.br[H + fu] : 0.0f,
+              bn = fin ? a.br[2 * H + fu] : 0.0f;
+  float mn[kNStat], mx[kNStat];
+#pragma unroll
+  for (int i = 0; i < kNStat; ++i) {
+    mn[i] = FLT_MAX;
+    mx[i] = -FLT_MAX;
+  }
+  const unsigned plane = static_cast<unsigned>(a.Bpad) * a.Hpad;  // floats per parity
+  const auto xr = cluster::buffer_rsrc(a.hx, 2u * plane * 4u);
+  unsigned *hxw = reinterpret_cast<unsigned *>(a.hx);
+  const size_t BH = static_cast<size_t>(B) * H;
+  unsigned epoch = 0;
+  bool alive = true;
+  for (int tile = pl.cluster; tile < a.ntiles && alive; tile += a.ncl) {
+    __syncthreads();  // the previous tile's readers of the partial tiles are done
+    const int b = tile * kCT + frow;
+    const bool valid = fin && b < B;
+    float hold = 0.0f;
+    if (fin) {
+      hold = valid && a.h0 ? a.h0[static_cast<size_t>(b) * H + fu] : 0.0f;
+      cluster::store_coherent(hxw + b * a.Hpad + fu, __float_as_uint(hold));
+      if (valid) a.hout[static_cast<size_t>(b) * H + fu] = hold;
+    }
+    // the step's weight_ih_linear values, loaded one step ahead (they do not depend on h)
+    float wz = 0.0f, wr = 0.0f, wn = 0.0f;
+    auto load_wx = [&](int t) {
+      if (valid) {
+        const float *wp = a.wx + (static_cast<size_t>(t) * B + b) * C + fu;
+        wz = wp[0];
+        wr = wp[H];
+        wn = wp[2 * H];
+      }
+    };
+    load_wx(0);
+    alive = cluster::sync(counter, ++epoch * a.G, a.timeout, a.spin_limit);
+    for (int t = 0; t < a.T && alive; ++t) {
+      const int par = t & 1;
+      const unsigned rowoff = par * plane + static_cast<unsigned>(tile * kCT + r16) * a.Hpad;
+#pragma unroll
+      for (int it = 0; it < IPW; ++it) {
+        const int item = w + it * NWG;
+        if (item >= nitems) break;
+        const int ch = item / 3;
+        // A: row tile*16 + r16, h[64 ch + 16 g .. + 15]
+        float hv[16];
+        const unsigned off = 4u * (rowoff + 64 * ch + 16 * g);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int4 v = cluster::load_coherent16(xr, off + 16u * q);
+          hv[4 * q] = __int_as_float(v.x);
+          hv[4 * q + 1] = __int_as_float(v.y);
+          hv[4 * q + 2] = __int_as_float(v.z);
+          hv[4 * q + 3] = __int_as_float(v.w);
+        }
+        v4f acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < 16; ++s) acc = mfma_f32(hv[s], rfr[it][s], acc);
+        red[item * kWave + l] = acc;
+      }
+      __syncthreads();
+      if (fin) {
+        float rh[3] = {bz, brr, bn};
+        for (int ch = 0; ch < NC; ++ch)
+#pragma unroll
+          for (int gate = 0; gate < 3; ++gate) rh[gate] += red[(ch * 3 + gate) * kWave + fl][fq];
+        const float zp = wz + rh[0];
+        const float rp = wr + rh[1];
+        const float z = static_cast<float>(1.0 / (1.0 + exp(-static_cast<double>(zp))));
+        const float r = static_cast<float>(1.0 / (1.0 + exp(-static_cast<double>(rp))));
+        const float rhm = r * rh[2];
+        const float np = wn + rhm;
+        const float n = tanhf(np);
+        const float oldc = z * hold;
+        const float newc = (1.0f - z) * n;
+        const float hn = oldc + newc;
+        hold = hn;
+        cluster::store_coherent(hxw + (par ^ 1) * plane + b * a.Hpad + fu, __float_as_uint(hn));
+        if (STATS && valid) {
+          observe(rh[0], mn[RXMET_GRU_RH], mx[RXMET_GRU_RH]);
+          observe(rh[1], mn[RXMET_GRU_RH], mx[RXMET_GRU_RH]);
+          observe(rh[2], mn[RXMET_GRU_RH], mx[RXMET_GRU_RH]);
+          observe(zp, mn[RXMET_GRU_Z_IN], mx[RXMET_GRU_Z_IN]);
+          observe(rp, mn[RXMET_GRU_R_IN], mx[RXMET_GRU_R_IN]);
+          observe(np, mn[RXMET_GRU_N_IN], mx[RXMET_GRU_N_IN]);
+          observe(z, mn[RXMET_GRU_Z_OUT], mx[RXMET_GRU_Z_OUT]);
+          observe(r, mn[RXMET_GRU_R_OUT], mx[RXMET_GRU_R_OUT]);
+          observe(n, mn[RXMET_GRU_N_OUT], mx[RXMET_GRU_N_OUT]);
+          observe(rhm, mn[RXMET_GRU_MUL_RH], mx[RXMET_GRU_MUL_RH]);
+          observe(newc, mn[RXMET_GRU_MUL_NEW], mx[RXMET_GRU_MUL_NEW]);
+          observe(oldc, mn[RXMET_GRU_MUL_OLD], mx[RXMET_GRU_MUL_OLD]);
+          observe(hn, mn[RXMET_GRU_H], mx[RXMET_GRU_H]);
+        }
+        cluster::arrive(counter);
+        ++epoch;
+        if (valid) {
+          a.hout[(static_cast<size_t>(t) + 1) * BH + static_cast<size_t>(b) * H + fu] = hn;
+          if (a.v) {
+            float *vb = a.v + (static_cast<size_t>(t) * B + b) * 4 * H + fu;
+            vb[0] = z;
+            vb[H] = r;
+            vb[2 * H] = n;
+            vb[3 * H] = rh[2];
+          }
+        }
+        if (t + 1 < a.T) load_wx(t + 1);
+      } else {
+        cluster::arrive(counter);
+        ++epoch;
+      }
+      alive = cluster::wait(counter, epoch * a.G, a.timeout, a.spin_limit);
+    }
+  }
+  if (STATS) {
+    __syncthreads();
+    block_stats(mn, mx, kNStat,
+                a.part + (static_cast<size_t>(blockIdx.x)) * 2 * kNStat);
+  }
+}
+
+struct CalWorkspace {
+  size_t ord, wx, hx, part, sync, total;
+  int Bpad, Hpad, ntiles;
+  int64_t nparts;
+  CalWorkspace(int T, int B, int H) {
+    auto al = [](size_t v) { return (v + 255) & ~static_cast<size_t>(255); };
+    ntiles = (B + kCT - 1) / kCT;
+    Bpad = ntiles * kCT;
+    Hpad = (H + 63) / 64 * 64;
+    const int64_t M = static_cast<int64_t>(T) * B;
+    const int64_t gemm_blocks = (3 * static_cast<int64_t>(H) + 63) / 64 * ((M + 63) / 64);
+    const int64_t rec_blocks = static_cast<int64_t>(ntiles) * (H / 16 > 0 ? H / 16 : 1);
+    nparts = 2 * kNStat * (gemm_blocks > rec_blocks ? gemm_blocks : rec_blocks);
+    size_t o = 0;
+    ord = o; o += al(sizeof(unsigned) * 2 * kNStat);
+    wx = o; o += al(sizeof(float) * static_cast<size_t>(T) * B * 3 * H);
+    hx = o; o += al(sizeof(float) * 2 * static_cast<size_t>(Bpad) * Hpad);
+    part = o; o += al(sizeof(float) * static_cast<size_t>(nparts));
+    sync = o; o += al(sizeof(unsigned) * (ntiles + 2));
+    total = o;
+  }
+};
+
+// The MFMA form when it applies (H a multiple of 16 up to 1024, the clusters resident);
+// returns 1 when launched, 0 when the caller must use the per-sequence kernel.
+template <bool STATS>
+static int calibrate_mfma(int T, int B, int I, int H, const float *W, const float *R,
+                          const float *bw, const float *br, const float *x, const float *h0,
+                          float *h, float *v, void *workspace, hipStream_t stream) {
+  if (H % 16 != 0 || H > 1024 || std::getenv("RXMET_NO_CLUSTER") != nullptr) return 0;
+  const CalWorkspace ws(T, B, H);
+  if (2.0 * ws.Bpad * ws.Hpad * 4 >= 2147483648.0) return 0;  // 32-bit exchange offsets
+  CalClArgs a{};
+  a.T = T; a.B = B; a.H = H;
+  a.NC = (H + 63) / 64;
+  a.NWG = std::min(kCMaxW, std::max(4, 3 * a.NC));
+  const int ipw = (3 * a.NC + a.NWG - 1) / a.NWG;  // 1 (H <= 320) .. 3
+  a.ntiles = ws.ntiles; a.Bpad = ws.Bpad; a.Hpad = ws.Hpad;
+  a.G = H / 16;
+  const void *fn = ipw == 1 ? reinterpret_cast<const void *>(&calib_recurrence_cl<STATS, 1>)
+                 : ipw == 2 ? reinterpret_cast<const void *>(&calib_recurrence_cl<STATS, 2>)
+                            : reinterpret_cast<const void *>(&calib_recurrence_cl<STATS, 3>);
+  const size_t lds = sizeof(v4f) * kWave * 3 * static_cast<size_t>(a.NC);
+  RXMET_CHECK_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      static_cast<int>(lds)));
+  int device = 0, ncu = 0, per_cu = 0;
+  RXMET_CHECK_HIP(hipGetDevice(&device));
+  RXMET_CHECK_HIP(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, device));
+  RXMET_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kWave * a.NWG, lds));
+  int ncl = per_cu * ncu / a.G;
+  if (ncl < 1) return 0;
+  if (ncl > a.ntiles) ncl = a.ntiles;
+  if (ncl >= 8) ncl -= ncl % 8;
+  a.ncl = ncl;
+  char *wsb = static_cast<char *>(workspace);
+  unsigned *ord = reinterpret_cast<unsigned *>(wsb + ws.ord);
+  float *wx = reinterpret_cast<float *>(wsb + ws.wx);
+  float *part = reinterpret_cast<float *>(wsb + ws.part);
+  a.hx = reinterpret_cast<float *>(wsb + ws.hx);
+  a.counters = reinterpret_cast<unsigned *>(wsb + ws.sync);
+  a.timeout = reinterpret_cast<int *>(a.counters + ncl);
+  a.spin_limit = cluster::spin_limit();
+  const int C = 3 * H;
+  const int M = T * B;
+  {
+    rxmet::prof::Scope ps__("gru_calibrate_input_gemm", stream);
+    // row tiles per workgroup: as many as keep about 2048 workgroups (fewer partials to fold)
+    const int64_t tiles = (M + 63) / 64, cblocks = (C + 63) / 64;
+    int RB = 1;
+    while (RB < kGemmRBMax && tiles * cblocks / (2 * RB) >= 2048) RB *= 2;
+    const dim3 grid(static_cast<unsigned>(cblocks), static_cast<unsigned>((tiles + RB - 1) / RB));
+    hipLaunchKernelGGL(calib_input_gemm<STATS>, grid, dim3(256), 0, stream, M, I, C, RB, x, W, bw,
+                       wx, part);
+    RXMET_CHECK_LAUNCH();
+    if (STATS) {
+      hipLaunchKernelGGL(stats_fold, dim3(1), dim3(256), 0, stream, part,
+                         static_cast<int>(grid.x * grid.y), kNStat, 0, ord);
+      RXMET_CHECK_LAUNCH();
+    }
+  }
+  // the exchange buffer's padding columns must read as zero
+  hipLaunchKernelGGL(cluster::zero_words, dim3(1), dim3(1024), 0, stream,
+                     reinterpret_cast<unsigned *>(a.hx), 2 * ws.Bpad * ws.Hpad);
+  RXMET_CHECK_LAUNCH();
+  hipLaunchKernelGGL(cluster::zero_words, dim3(1), dim3(256), 0, stream, a.counters, ncl + 1);
+  RXMET_CHECK_LAUNCH();
+  a.wx = wx; a.R = R; a.br = br; a.h0 = h0; a.hout = h; a.v = v; a.part = part;
+  void *args[] = {&a};
+  {
+    rxmet::prof::Scope ps__("gru_calibrate_forward", stream);
+    RXMET_CHECK_HIP(cluster::launch(fn, dim3(ncl * a.G), dim3(kWave * a.NWG), args,
+                                    static_cast<unsigned>(lds), stream));
+    if (STATS) {
+      hipLaunchKernelGGL(stats_fold, dim3(1), dim3(256), 0, stream, part, ncl * a.G, kNStat, 0,
+                         ord);
+      RXMET_CHECK_LAUNCH();
+    }
+  }
+  // a wait that timed out: the outputs become NaN (the statistics skip non-finite values)
+  cluster::PoisonList pl{};
+  pl.p[pl.count] = h;
+  pl.n[pl.count++] = static_cast<int64_t>(T + 1) * B * H;
+  if (v) {
+    pl.p[pl.count] = v;
+    pl.n[pl.count++] = static_cast<int64_t>(T) * B * 4 * H;
+  }
+  hipLaunchKernelGGL(cluster::poison_list, dim3(256), dim3(256), 0, stream, a.timeout, pl);
+  RXMET_CHECK_LAUNCH();
+  return 1;
+}
+
 // Per-channel min/max of W [I,3H], R [H,3H], bw, br merged into the running ranges.
 __global__ __launch_bounds__(256) void calib_params(int I, int H, const float *W, const float *R,
                                                     const float *bw, const float *br,
@@ -194,8 +630,9 @@ using namespace rxmet::gru;
 extern "C" {
 
 int64_t rxmet_gru_calibrate_workspace_bytes(int32_t T, int32_t B, int32_t I, int32_t H) {
-  (void)T; (void)B; (void)I; (void)H;
-  return static_cast<int64_t>(sizeof(unsigned) * 2 * kNStat);
+  (void)I;
+  if (T < 1 || B < 1 || H < 1) return static_cast<int64_t>(sizeof(unsigned) * 2 * kNStat);
+  return static_cast<int64_t>(CalWorkspace(T, B, H).total);
 }
 
 int rxmet_gru_forward_calibrate(int32_t T, int32_t B, int32_t I, int32_t H, const float *W,
@@ -207,15 +644,17 @@ int rxmet_gru_forward_calibrate(int32_t T, int32_t B, int32_t I, int32_t H, cons
   RXMET_CHECK_ARG(H <= 4096, "hidden_size above 4096 is not supported by the calibration pass");
   RXMET_CHECK_ARG(W && R && bw && br && x && h && stats && workspace, "required pointer is null");
   hipStream_t stream = static_cast<hipStream_t>(stream_);
-  unsigned *ord = static_cast<unsigned *>(workspace);
+  unsigned *ord = static_cast<unsigned *>(workspace);  // the workspace's first region
   hipLaunchKernelGGL(stats_init, dim3(1), dim3(64), 0, stream, ord);
   RXMET_CHECK_LAUNCH();
-  const size_t lds = sizeof(float) * 8 * static_cast<size_t>(H);
-  if (lds > 64 * 1024)
-    RXMET_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&calib_forward<true>),
-                                        hipFuncAttributeMaxDynamicSharedMemorySize,
-                                        static_cast<int>(lds)));
-  {
+  const int mf = calibrate_mfma<true>(T, B, I, H, W, R, bw, br, x, h0, h, v, workspace, stream);
+  if (mf < 0) return mf;
+  if (mf == 0) {
+    const size_t lds = sizeof(float) * 8 * static_cast<size_t>(H);
+    if (lds > 64 * 1024)
+      RXMET_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&calib_forward<true>),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize,
+                                          static_cast<int>(lds)));
     rxmet::prof::Scope ps__("gru_calibrate_forward", stream);
     hipLaunchKernelGGL(calib_forward<true>, dim3(B), dim3(kCalThreads), lds, stream, T, B, I, H, W, R, bw,
                        br, x, h0, h, v, ord);
