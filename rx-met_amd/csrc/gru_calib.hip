@@ -179,7 +179,8 @@ constexpr int kGemmRBMax = 8;  // 64-row tiles per input-projection workgroup, a
 __device__ __forceinline__ void block_stats(const float *mn, const float *mx, int n, float *part) {
   __shared__ float smn[kCMaxW][kNStat], smx[kCMaxW][kNStat];
   const int w = threadIdx.x / kWave, nw = blockDim.x / kWave;
-  for (int i = 0; i < n; ++i) {
+#pragma unroll
+  for (int i = 0; i < n; ++i) {  // unrolled (n is a constant where inlined): mn, mx stay in registers
     const float lo = wave_min(mn[i]), hi = wave_max(mx[i]);
     if (threadIdx.x % kWave == 0) {
       smn[w][i] = lo;
