@@ -15,7 +15,9 @@ Prints ONE JSON line.  Legs (all run by default):
 * gint — the c3 model on the int32 carrier, PTQ inference of both directions (the work the
          reference's CPU int carrier does, timed by the c3 CPU baseline), float and int-IO: seq/s;
 * lstmpub — the reference's published QuantLSTM inference profiles ([50, 64, 128, 256] and
-         [16, 128, 64, 128], cuda-performance.md), P50 / P95 over 200 calls, beside its numbers.
+         [16, 128, 64, 128], cuda-performance.md), P50 / P95 over 200 calls, beside its numbers;
+* calib — the MinMax calibration forwards at c3 (GRU, both directions), c4 (LSTM) and c5 (GRU):
+         ms per calibration forward over the whole batch.
 
 The roofline object describes the dominant kernel of the headline leg, timed with
 hipEvents that the library records around its own launches on the stream they run on
@@ -620,7 +622,7 @@ def _lstm_kernel_work(B, T, I, H):
     }
 
 
-def _timed_steps(torch, step, steps, warmup, work):
+def _timed_steps(torch, step, steps, warmup, work, timed=None):
     """Run warmup + timed steps; per-step events, per-kernel library timings, roofline of the
     dominant instrumented kernel.
 
@@ -635,7 +637,8 @@ def _timed_steps(torch, step, steps, warmup, work):
         step()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream(dev)
-    timed = sorted(k for k in work if "recurrence" in k)
+    if timed is None:
+        timed = sorted(k for k in work if "recurrence" in k)
     evs = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
     rxmet_lib.prof_filter(timed)
     rxmet_lib.prof_reset()
@@ -999,6 +1002,123 @@ def _qc_ref_cpu_baseline(xs, budget_s: float):
                       f"{reps} run(s) of {dt:.3f} s"}
 
 
+FP32_MFMA_PEAK = 157.3
+
+
+def _calib_leg(torch, steps: int, warmup: int):
+    """calib: the MinMax calibration forwards (float recurrence plus the statistics of every
+    grid, rxmet_gru_forward_calibrate / rxmet_lstm_forward_calibrate) at the benchmark shapes:
+    c3 GRU (bidirectional, both directions per step), c4 LSTM and c5 GRU.  One step = one
+    calibration forward over the whole batch, merged into the module's running ranges as a
+    calibration loop over batches does."""
+    import quant_gru as QG
+    import quant_lstm as QL
+
+    dev = torch.device("cuda:0")
+    res, keep = {}, {}
+    cases = (("gru_c3", "gru", 256, 200, 80, 256, True),
+             ("lstm_c4", "lstm", 512, 100, 64, 512, False),
+             ("gru_c5", "gru", 1024, 50, 256, 1024, False))
+    for name, kind, B, T, I, H, bidir in cases:
+        torch.manual_seed(6)
+        if kind == "gru":
+            x = torch.randn(T, B, I)
+            m = QG.QuantGRU(I, H, bidirectional=bidir)
+            C = 3 * H
+        else:
+            x = torch.rand(T, B, I) * 2 - 1
+            m = QL.QuantLSTM(I, H)
+            C = 4 * H
+        m = m.to(dev)
+        x = x.to(dev)
+        D = 2 if bidir else 1
+
+        def step(m=m, x=x):
+            m.calibrating = True
+            with torch.no_grad():
+                m(x)
+            m.calibrating = False
+
+        M = T * B
+        rec, gemm = f"{kind}_calibrate_forward", f"{kind}_calibrate_input_gemm"
+        work = {rec: (D * 2.0 * M * H * C, FP32_MFMA_PEAK,
+                      "recurrent GEMM h R of every direction over T steps on fp32 MFMA (one "
+                      "clustered launch per direction: gates and statistics fused)"),
+                gemm: (D * 2.0 * M * C * I, FP32_MFMA_PEAK,
+                       "input projection x W of every direction (fp32 MFMA, statistics fused)")}
+        dt, p50, p95, kernels, roof = _timed_steps(torch, step, steps, warmup, work,
+                                                   timed=[rec])
+        _log(f"calibration {name}: {dt*1e3:.3f} ms/step wall, P50 {p50:.3f} ms, {B/dt:.1f} "
+             f"seq/s; " + ", ".join(f"{k} {v['ms_per_step']:.3f} ms/step"
+                                    for k, v in kernels.items()))
+        res[name] = {"ms_per_step": dt * 1e3, "p50_ms": p50, "p95_ms": p95, "seq_per_s": B / dt,
+                     "shape_TBIH": [T, B, I, H], "directions": D,
+                     "kernels_ms_per_step": {k: round(v["ms_per_step"], 4)
+                                             for k, v in kernels.items()},
+                     "recurrence_roofline": {k: roof[k] for k in ("achieved", "peak", "unit",
+                                                                  "frac", "us_per_launch")}}
+        keep[name] = (kind, m, x)
+    return res, keep
+
+
+def _validate_calib(torch, keep, rows=(0, -1)):
+    """One more calibration forward of each benchmarked module: every output finite, the
+    input range equal to the tensor's own min / max, and the sampled sequences' output equal
+    to the oracle's float calibration forward run on those sequences alone (rtol 1e-4)."""
+    import numpy as np
+
+    import gru_oracle as GO
+    import lstm_oracle as LO
+    import rxmet_lstm_abi as L
+
+    out = {}
+    for name, (kind, m, x) in keep.items():
+        m.calibrating = True
+        with torch.no_grad():
+            y = m(x)[0]
+        m.calibrating = False
+        torch.cuda.synchronize()
+        if not bool(torch.isfinite(y).all()):
+            raise ValidationError(f"{name} calibration: non-finite output")
+        B = x.shape[1]
+        rws = sorted({r % B for r in rows})
+        xs = x[:, rws].contiguous().cpu().numpy()
+        got = y[:, rws].cpu().numpy()
+        H = m.hidden_size
+        err = 0.0
+        if kind == "gru":
+            lo, hi = float(x.min()), float(x.max())
+            rg = m.quant_ranges
+            if rg.min_x_ != lo or rg.max_x_ != hi:
+                raise ValidationError(f"{name} calibration: x range [{rg.min_x_}, {rg.max_x_}] "
+                                      f"is not the input's [{lo}, {hi}]")
+            for d in range(m.num_directions):
+                sfx = "_reverse" if d else ""
+                p = lambda n: getattr(m, n + sfx).detach().cpu().numpy()
+                W = np.ascontiguousarray(_swap_gates(p("weight_ih_l0")).T)
+                R = np.ascontiguousarray(_swap_gates(p("weight_hh_l0")).T)
+                bw, br = _swap_gates(p("bias_ih_l0")), _swap_gates(p("bias_hh_l0"))
+                xd = np.ascontiguousarray(xs[::-1]) if d else xs
+                h, _, _ = GO.forward_calibrate(W, R, bw, br, xd)
+                exp = h[1:][::-1] if d else h[1:]
+                err = max(err, _check_close(f"{name} calibration output (direction {d})",
+                                            got[..., d * H:(d + 1) * H], exp))
+        else:
+            lo, hi = float(x.min()), float(x.max())
+            st = m._stats[0].cpu().numpy()
+            n = L.NOPS  # minima of the operators, then maxima; "input" first
+            if float(st[0]) != lo or float(st[n]) != hi:
+                raise ValidationError(f"{name} calibration: input range [{st[0]}, {st[n]}] is "
+                                      f"not the input's [{lo}, {hi}]")
+            Wi, Wh, bi, bh = (p.detach().cpu().numpy() for p in m._direction_params(False))
+            exp, _, _ = LO.forward_float(Wi, Wh, bi, bh, xs, mode=LO.ACT_CR)
+            err = _check_close(f"{name} calibration output", got, exp)
+        out[name] = {"sequences": rws,
+                     "output_vs_oracle": f"rtol 1e-4; max |err| / max |ref| = {err:.3g}",
+                     "input_range": "exact"}
+    return out
+
+
 def _c1_leg(torch, steps: int, warmup: int):
     """c1: the PTQ calibration pass of a unidirectional QuantGRU (B=32, T=98, I=40, H=64):
     MinMax calibration forward on the GPU, parameter derivation, then the PTQ (quantised,
@@ -1100,8 +1220,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-validate", action="store_true",
                     help="skip the oracle comparison of the benchmarked outputs (profiling runs)")
-    ap.add_argument("--legs", default="gru,lstm,qdq,c1,c5,gint,lstmpub",
-                    help="comma-separated subset of gru,lstm,qdq,c1,c5,gint,lstmpub")
+    ap.add_argument("--legs", default="gru,lstm,qdq,c1,c5,gint,lstmpub,calib",
+                    help="comma-separated subset of gru,lstm,qdq,c1,c5,gint,lstmpub,calib")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run a plain elementwise copy over MIB MiB (scales HBM byte "
                          "counters in profiling runs)")
@@ -1121,7 +1241,7 @@ def main() -> int:
     validate = not args.no_validate
     checks = {}
     gru = roof = lstm = lstm_roof = qdq = qdq_roof = c5 = c1 = gint = gint_roof = None
-    lstmpub = None
+    lstmpub = calib = None
     try:
         if "gru" in legs:
             gru, roof, m, x = _gru_leg(torch, args.steps, args.warmup)
@@ -1148,6 +1268,12 @@ def main() -> int:
                 _log(f"gint validation: {checks['gint']}")
         if "lstmpub" in legs:
             lstmpub = _lstm_published_leg(torch)
+        if "calib" in legs:
+            calib, ckeep = _calib_leg(torch, args.steps, args.warmup)
+            if validate:
+                checks["calibration"] = _validate_calib(torch, ckeep)
+                _log(f"calibration validation: {checks['calibration']}")
+            del ckeep
         if "c5" in legs:
             c5, c5m, c5x = _gru_c5_leg(torch, args.steps, args.warmup)
             if validate:
@@ -1202,6 +1328,7 @@ def main() -> int:
         "gru_c5": rnd(c5),
         "gru_int32_c3": rnd(gint),
         "gru_int32_roofline": gint_roof,
+        "calibration_forward": calib,
         "lstm_published_inference": lstmpub,
         "qdq": None if qdq is None else {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv)
                                              for kk, vv in v.items()} for k, v in qdq.items()},

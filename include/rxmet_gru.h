@@ -289,6 +289,48 @@ int rxmet_gru_backward_quant_dirs_x(int32_t ndir, int32_t T, int32_t B, int32_t 
                                     const rxmet_gru_bwd_dir *dirs, int32_t flags, void *stream);
 
 /*
+ * Saved state as codes, for callers that keep the forward's state only to hand it to the
+ * backward (the module path).  No counterpart in the reference, whose forward returns v in
+ * fp32 and one byte per mask value (gru_interface_binding.cc:306-448); the gradients equal
+ * those of the reference-format pair bit for bit (v is dequantised in the backward with the
+ * same (code - zero point) * effective scale).  Per direction, in blocks of 16 sequences x 16
+ * units so that a recurrence workgroup writes each step's codes as one contiguous run: block
+ * k = (t Bt + b / 16) (H / 16) + j / 16, Bt = ceil(B / 16), row r = b % 16, unit e = j % 16:
+ *   v_codes   [T Bt 16 4H]: element (t, b, field f, j) at 1024 k + 64 r + 16 f + e; fields
+ *             f = 0..3 the update, reset and new gate outputs and the new gate's recurrent
+ *             linear (z, r, n, hh_n), each as its code minus its grid's minimum;
+ *   mask_bits [T Bt 16 H]: element (t, b, j) at 256 k + 16 r + e; bit g (gate g = z, r, n) the
+ *             weight_ih_linear mask, 3 + g the weight_hh_linear mask, 6 + g the gate input
+ *             mask, 9 + g the gate output mask, 12 the h mask.
+ * Both 16-byte aligned; rows past B hold unspecified values.  The four grids must span at most
+ * 16 bits.  H a multiple of 16.
+ */
+typedef struct rxmet_gru_saved_codes {
+  uint16_t *v_codes;
+  uint16_t *mask_bits;
+} rxmet_gru_saved_codes;
+
+/*
+ * rxmet_gru_forward_quant_dirs_x (x_layout may be null: [T, B, I] contiguous per direction)
+ * writing, when is_training, codes[k] instead of dirs[k].v and the five per-step mask
+ * families (ih, hh, gate in, gate out, h), which may then be null; the x, h0, W, R, bw and br
+ * masks and every other output as before.
+ */
+int rxmet_gru_forward_quant_dirs_codes(int32_t ndir, int32_t is_training, int32_t T, int32_t B,
+                                       int32_t I, int32_t H, const rxmet_gru_fwd_dir *dirs,
+                                       const int64_t *x_layout, const rxmet_gru_saved_codes *codes,
+                                       void *stream);
+
+/*
+ * rxmet_gru_backward_quant_dirs_x (flags as there) reading codes[k] from
+ * rxmet_gru_forward_quant_dirs_codes instead of dirs[k].v and the five per-step mask families
+ * (which may be null).
+ */
+int rxmet_gru_backward_quant_dirs_codes(int32_t ndir, int32_t T, int32_t B, int32_t I, int32_t H,
+                                        const rxmet_gru_bwd_dir *dirs, int32_t flags,
+                                        const rxmet_gru_saved_codes *codes, void *stream);
+
+/*
  * Quantised forward, int32 carrier: quantGRUForwardInt (src/gru_interface.cc:443-559) behind
  * forward_quant_int_storage_wrapper (gru_interface_binding.cc:451-586), i.e. ForwardPassQuant
  * (src/gru_forward_gpu_quant.cu) and the reference's CPU carrier (src/gru_forward_cpu_quant.cc:

@@ -16,6 +16,13 @@ namespace cluster {
 
 constexpr unsigned kSpinLimit = 1u << 20;  // about a second of polling
 
+// Words between two clusters' barrier counters: each counter has a 256-byte line of its own.
+// Counters sharing a line serialise every cluster's arrivals and polls at that line; with the
+// 32 clusters of the two-direction c3 GRU forward on one line, a step whose workgroups reach
+// the barrier early took 1.55 ms against 0.82 ms with the counters apart.  A launch of n
+// clusters takes kCounterStride * n + 1 words: the counters, then the timeout flag.
+constexpr int kCounterStride = 64;
+
 // The poll limit a launch passes to its waits: kSpinLimit, or RXMET_TEST_SPIN_LIMIT from the
 // environment.  Tests of the timeout path set it to 0, so that a wait that has to poll gives
 // up at once: the launch then takes the path of a real timeout (flag raised, members stop

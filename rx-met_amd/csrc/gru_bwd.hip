@@ -94,6 +94,11 @@ struct BwdArgs {
   float *dh0;                // [B, H]
   float *xch;                // clustered path: [2][Bpad][KP] exchanged dq * scale_R
   const uint4 *rt;           // clustered path: packed R_q codes, see pack_rt_bf16
+  // saved state as codes (instead of v and the five per-step masks; the per-tile kernel
+  // does not read them): v_codes [T, B, 4H] and mask_bits [T, B, H] of the forward; field q
+  // of v is (v_codes - vzl[q]) * veff[q], vzl = zero point - grid minimum
+  const uint16_t *vc, *mb;
+  float vzl[4], veff[4];
 };
 
 constexpr int kPlanes = 3;
@@ -381,6 +386,30 @@ __device__ __forceinline__ void bwd_load_step(const BwdArgs &a, const BwdMasks &
   const uint32_t v0 = 4u * tH + 4u * static_cast<uint32_t>(b) * H + j;
   r[0] = a.dh_new[tH + BH + oH];
   r[1] = a.h[tH + oH];
+  if (a.vc) {
+    // blocked codes: block ((t ceil(B/16) + b / 16) H/16 + j / 16) of 16 rows x 16 units, v as
+    // [16][4][16], mask bits as [16][16]; the forward's (code - zero point) * effective scale,
+    // from code - minimum: the same fp32 operations on the same values
+    const uint32_t nt = static_cast<uint32_t>(a.B + 15) / 16;
+    const uint32_t row = ((static_cast<uint32_t>(t) * nt + static_cast<uint32_t>(b) / 16) *
+                              (static_cast<uint32_t>(H) / 16) + static_cast<uint32_t>(j) / 16) * 16 +
+                         static_cast<uint32_t>(b) % 16;
+    const uint32_t e = static_cast<uint32_t>(j) % 16;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      r[2 + q] = (static_cast<float>(a.vc[64 * row + 16 * q + e]) - a.vzl[q]) * a.veff[q];
+    const unsigned bits = a.mb[16 * row + e];
+    auto bit = [&](int k) { return static_cast<float>((bits >> k) & 1u); };
+    r[6] = bit(12);
+#pragma unroll
+    for (int gg = 0; gg < 3; ++gg) {
+      r[7 + gg] = bit(9 + gg);
+      r[10 + gg] = bit(6 + gg);
+      r[13 + gg] = bit(3 + gg);
+      r[16 + gg] = bit(gg);
+    }
+    return;
+  }
 #pragma unroll
   for (int q = 0; q < 4; ++q) r[2 + q] = a.v[v0 + q * H];
   r[6] = mk.h.at(tH + oH);
@@ -601,7 +630,7 @@ __device__ __forceinline__ void bwd_cl_pair(const BwdArgs &a, const BwdClArgs &c
 template <int UT, int NPL>
 __global__ __launch_bounds__(256 * UT) void bwd_recurrence_cl(BwdArgs a0, BwdArgs a1, BwdClArgs cl) {
   const cluster::Place pl = cluster::place(cl.G, cl.ncl);
-  unsigned *counter = cl.counters + pl.cluster;
+  unsigned *counter = cl.counters + cluster::kCounterStride * pl.cluster;
   unsigned epoch = 0;
   bool alive = true;
   for (int pair = pl.cluster; pair < cl.ndir * cl.ntiles && alive; pair += cl.ncl) {
@@ -777,7 +806,7 @@ struct BwdWorkspace {
     const size_t Bpad = nwg * kBTile;
     xch = o; o += al(sizeof(float) * 2 * Bpad * KS2 * 64);
     rt = o; o += al(sizeof(uint4) * 2 * ((H + 15) / 16) * 4 * ((KS2 + 1) / 2) * 64);
-    sync = o; o += al(sizeof(unsigned) * (2 * nwg + 2));  // clusters of both directions
+    sync = o; o += al(sizeof(unsigned) * cluster::kCounterStride * (2 * nwg + 2));  // clusters of both directions
     // stepped recurrence: R codes as bf16 planes [H][Cp], the dh GEMM output, dhl
     Cp = static_cast<int>((C + 31) / 32 * 32);
     rb = o; o += al(sizeof(__bf16) * 2 * H * static_cast<size_t>(Cp));
@@ -797,13 +826,16 @@ struct BwdPlan {
 };
 
 static int backward_prologue(int T, int B, int I, int H, const rxmet_gru_bwd_dir &d,
-                             hipStream_t stream, BwdPlan *plan) {
+                             const rxmet_gru_saved_codes *codes, hipStream_t stream,
+                             BwdPlan *plan) {
   const rxmet_gru_qparams *params = d.params;
   RXMET_CHECK_ARG(params != nullptr, "params must be non-null");
   RXMET_CHECK_ARG(params->hidden == H, "params.hidden != hidden_size");
-  RXMET_CHECK_ARG(d.W_q && d.R_q && d.x_q && d.dh_new && d.h && d.v && d.dx && d.dW && d.dR &&
-                      d.dbw && d.dbr && d.dh0 && d.workspace,
+  RXMET_CHECK_ARG(d.W_q && d.R_q && d.x_q && d.dh_new && d.h && (codes || d.v) && d.dx && d.dW &&
+                      d.dR && d.dbw && d.dbr && d.dh0 && d.workspace,
                   "required pointer is null");
+  RXMET_CHECK_ARG(!codes || (codes->v_codes && codes->mask_bits),
+                  "v_codes and mask_bits must be non-null");
   {
     const Bounds brq = bounds_of(params->chan_bits[RXMET_GRU_R], params->chan_unsigned[RXMET_GRU_R]);
     RXMET_CHECK_ARG(brq.lo >= -32768.0f && brq.hi <= 32767.0f,
@@ -866,6 +898,22 @@ static int backward_prologue(int T, int B, int I, int H, const rxmet_gru_bwd_dir
   ba.dh_new = d.dh_new; ba.h = d.h; ba.v = d.v;
   ba.ih_m = d.ih_mask; ba.hh_m = d.hh_mask; ba.gin_m = d.gate_in_mask; ba.gout_m = d.gate_out_mask;
   ba.h_m = d.h_mask; ba.bw_m = d.bw_mask; ba.br_m = d.br_mask; ba.h0_m = d.h0_mask;
+  ba.vc = nullptr; ba.mb = nullptr;
+  if (codes) {
+    ba.v = nullptr;
+    ba.ih_m = ba.hh_m = ba.gin_m = ba.gout_m = ba.h_m = nullptr;
+    ba.vc = codes->v_codes;
+    ba.mb = codes->mask_bits;
+    const int fields[4] = {RXMET_GRU_Z_OUT, RXMET_GRU_R_OUT, RXMET_GRU_N_OUT, RXMET_GRU_RH};
+    for (int q = 0; q < 4; ++q) {
+      const rxmet_grid &g = params->g[fields[q]];
+      const Bounds b = bounds_of(g.bits, g.is_unsigned);
+      RXMET_CHECK_ARG(b.hi - b.lo <= 65535.0f,
+                      "saved codes need gate output and weight_hh_linear grids of at most 16 bits");
+      ba.vzl[q] = static_cast<float>(g.zero_point) - b.lo;
+      ba.veff[q] = effective_scale(g.scale, params->use_pot2 != 0);
+    }
+  }
   ba.rfrag = reinterpret_cast<v4i *>(wsb + ws.rfrag);
   ba.rowsum = reinterpret_cast<float *>(wsb + ws.rowsum);
   ba.eff_r = effr;
@@ -933,7 +981,7 @@ static int backward_recurrence_clustered(BwdPlan *plans, int ndir, int T, int B,
   cl.ncl = ncl;
   const BwdWorkspace ws(T, B, I, H);
   cl.counters = reinterpret_cast<unsigned *>(plans[0].wsb + ws.sync);
-  cl.timeout = reinterpret_cast<int *>(cl.counters + ncl);
+  cl.timeout = reinterpret_cast<int *>(cl.counters + cluster::kCounterStride * ncl);
   cl.spin_limit = cluster::spin_limit();
   for (int k = 0; k < ndir; ++k) {
     hipLaunchKernelGGL(pack_rt_bf16, dim3((H / 16) * 4 * ((KS2 + 1) / 2)), dim3(64), 0, stream, H, KS2,
@@ -944,7 +992,8 @@ static int backward_recurrence_clustered(BwdPlan *plans, int ndir, int T, int B,
     hipLaunchKernelGGL(zero_floats, dim3(256), dim3(256), 0, stream, nx, plans[k].ba.xch);
     RXMET_CHECK_LAUNCH();
   }
-  hipLaunchKernelGGL(cluster::zero_words, dim3(1), dim3(256), 0, stream, cl.counters, ncl + 1);
+  hipLaunchKernelGGL(cluster::zero_words, dim3(1), dim3(256), 0, stream, cl.counters,
+                     cluster::kCounterStride * ncl + 1);
   RXMET_CHECK_LAUNCH();
   BwdArgs &a1 = plans[ndir > 1 ? 1 : 0].ba;
   void *args[] = {&plans[0].ba, &a1, &cl};
@@ -1080,7 +1129,8 @@ static int backward_epilogue(int T, int B, int I, int H, BwdPlan &plan, hipStrea
 }
 
 static int backward_dirs(int ndir, int T, int B, int I, int H, const rxmet_gru_bwd_dir *dirs,
-                         bool torch_layout, hipStream_t stream) {
+                         bool torch_layout, hipStream_t stream,
+                         const rxmet_gru_saved_codes *codes = nullptr) {
   RXMET_CHECK_ARG(ndir == 1 || ndir == 2, "ndir must be 1 or 2");
   RXMET_CHECK_ARG(dirs != nullptr, "dirs must be non-null");
   RXMET_CHECK_ARG(T >= 1 && B >= 1 && I >= 1 && H >= 1, "dimensions must be positive");
@@ -1090,7 +1140,9 @@ static int backward_dirs(int ndir, int T, int B, int I, int H, const rxmet_gru_b
                   "T*B*H too large for the recurrence's 32-bit element offsets");
   BwdPlan plans[2];
   for (int k = 0; k < ndir; ++k)
-    if (int rc = backward_prologue(T, B, I, H, dirs[k], stream, &plans[k])) return rc;
+    if (int rc = backward_prologue(T, B, I, H, dirs[k], codes ? &codes[k] : nullptr, stream,
+                                   &plans[k]))
+      return rc;
   for (int k = 0; k < ndir; ++k) plans[k].torch_layout = torch_layout;
   // H > 256 (more R values than the clustered and per-tile kernels keep in registers), or
   // RXMET_BWD_STEPPED set: one pointwise and one GEMM launch per step
@@ -1107,7 +1159,7 @@ static int backward_dirs(int ndir, int T, int B, int I, int H, const rxmet_gru_b
              dirs[k].params->chan_unsigned[RXMET_GRU_R] != 0;
   if (rc == 0)
     for (int k = 0; k < ndir; ++k)
-      if (int r = (stepped || wide_r) ? backward_recurrence_stepped(plans[k], T, B, I, H, stream)
+      if (int r = (stepped || wide_r || codes) ? backward_recurrence_stepped(plans[k], T, B, I, H, stream)
                                       : backward_recurrence_tiles(plans[k], B, H, stream))
         return r;
   for (int k = 0; k < ndir; ++k)
@@ -1174,6 +1226,15 @@ int rxmet_gru_backward_quant_dirs_x(int32_t ndir, int32_t T, int32_t B, int32_t 
   clear_error();
   return backward_dirs(ndir, T, B, I, H, dirs, (flags & 1) != 0,
                        static_cast<hipStream_t>(stream_));
+}
+
+int rxmet_gru_backward_quant_dirs_codes(int32_t ndir, int32_t T, int32_t B, int32_t I, int32_t H,
+                                        const rxmet_gru_bwd_dir *dirs, int32_t flags,
+                                        const rxmet_gru_saved_codes *codes, void *stream_) {
+  clear_error();
+  RXMET_CHECK_ARG(codes != nullptr, "codes must be non-null");
+  return backward_dirs(ndir, T, B, I, H, dirs, (flags & 1) != 0,
+                       static_cast<hipStream_t>(stream_), codes);
 }
 
 }  // extern "C"

@@ -345,7 +345,7 @@ __global__ __launch_bounds__(64 * kCMaxW) void calib_recurrence_cl(CalClArgs a) 
   extern __shared__ __align__(16) unsigned char smem[];
   v4f *red = reinterpret_cast<v4f *>(smem);  // [3 NC][64]
   const cluster::Place pl = cluster::place(a.G, a.ncl);
-  unsigned *counter = a.counters + pl.cluster;
+  unsigned *counter = a.counters + cluster::kCounterStride * pl.cluster;
   const int H = a.H, C = 3 * H, B = a.B, NC = a.NC, NWG = a.NWG;
   const int tid = threadIdx.x, w = tid / kWave, l = tid % kWave, r16 = l % 16, g = l / 16;
   const int u0 = 16 * pl.member;
@@ -504,7 +504,7 @@ struct CalWorkspace {
     wx = o; o += al(sizeof(float) * static_cast<size_t>(T) * B * 3 * H);
     hx = o; o += al(sizeof(float) * 2 * static_cast<size_t>(Bpad) * Hpad);
     part = o; o += al(sizeof(float) * static_cast<size_t>(nparts));
-    sync = o; o += al(sizeof(unsigned) * (ntiles + 2));
+    sync = o; o += al(sizeof(unsigned) * cluster::kCounterStride * (ntiles + 2));
     total = o;
   }
 };
@@ -546,7 +546,7 @@ static int calibrate_mfma(int T, int B, int I, int H, const float *W, const floa
   float *part = reinterpret_cast<float *>(wsb + ws.part);
   a.hx = reinterpret_cast<float *>(wsb + ws.hx);
   a.counters = reinterpret_cast<unsigned *>(wsb + ws.sync);
-  a.timeout = reinterpret_cast<int *>(a.counters + ncl);
+  a.timeout = reinterpret_cast<int *>(a.counters + cluster::kCounterStride * ncl);
   a.spin_limit = cluster::spin_limit();
   const int C = 3 * H;
   const int M = T * B;
@@ -570,7 +570,8 @@ static int calibrate_mfma(int T, int B, int I, int H, const float *W, const floa
   hipLaunchKernelGGL(cluster::zero_words, dim3(1), dim3(1024), 0, stream,
                      reinterpret_cast<unsigned *>(a.hx), 2 * ws.Bpad * ws.Hpad);
   RXMET_CHECK_LAUNCH();
-  hipLaunchKernelGGL(cluster::zero_words, dim3(1), dim3(256), 0, stream, a.counters, ncl + 1);
+  hipLaunchKernelGGL(cluster::zero_words, dim3(1), dim3(256), 0, stream, a.counters,
+                     cluster::kCounterStride * ncl + 1);
   RXMET_CHECK_LAUNCH();
   a.wx = wx; a.R = R; a.br = br; a.h0 = h0; a.hout = h; a.v = v; a.part = part;
   void *args[] = {&a};

@@ -301,6 +301,9 @@ struct RecArgs {
   float *hout;              // [T+1, B, H] dequantised (row 0 written by quant_input)
   float *v;                 // [T, B, 4H] dequantised
   uint8_t *ih_m, *hh_m, *gin_m, *gout_m, *h_m;
+  // saved state as codes (training, instead of v and the five mask arrays above): v_codes
+  // [T, B, 4H] code minus grid minimum of z, r, n, hh_n; mask_bits [T, B, H] (code_mask_bits)
+  uint16_t *vc, *mb;
   int8_t *hx;               // clustered path: [2][NPL][Bpad / 16][KS][16][64] exchanged h codes
                             // (1 KB blocks of 16 rows x 64 units, see hx_offset)
   int wide_out;             // clustered path: outputs 16-byte aligned (H % 16 == 0), stored
@@ -430,15 +433,50 @@ __device__ __forceinline__ PointOut gru_point(const float gih[3], const float gh
   return o;
 }
 
+// The 13 mask values of one element as bits: gate g's weight_ih_linear mask at bit g, its
+// weight_hh_linear mask at 3 + g, gate input 6 + g, gate output 9 + g, the h mask at 12.
+__device__ __forceinline__ unsigned code_mask_bits(const PointOut &o) {
+  unsigned m = static_cast<unsigned>(o.k_h) << 12;
+#pragma unroll
+  for (int g = 0; g < 3; ++g)
+    m |= static_cast<unsigned>(o.k_ih[g]) << g | static_cast<unsigned>(o.k_hh[g]) << (3 + g) |
+         static_cast<unsigned>(o.k_gi[g]) << (6 + g) | static_cast<unsigned>(o.k_go[g]) << (9 + g);
+  return m;
+}
+
+// A saved code as its offset from the grid's minimum (grids of at most 16 bits).
+__device__ __forceinline__ unsigned code_u16(float code, float lo) {
+  return static_cast<unsigned>(static_cast<int>(code - lo));
+}
+
+// Saved codes are blocked so that a workgroup's outputs of one step are contiguous: block
+// ((t ceil(B/16) + b / 16) H/16 + j / 16) holds 16 rows (b % 16) of 16 units (j % 16); v codes
+// as [16 rows][4 fields][16 units] (1024 per block), mask bits as [16 rows][16 units] (256).
+// Returns block * 16 + b % 16: the row's index in units of 64 v codes / 16 mask words.
+__device__ __forceinline__ uint32_t codes_row(int t, int b, int j, int B, int H) {
+  const uint32_t nt = static_cast<uint32_t>(B + 15) / 16;
+  return ((static_cast<uint32_t>(t) * nt + static_cast<uint32_t>(b) / 16) *
+              (static_cast<uint32_t>(H) / 16) + static_cast<uint32_t>(j) / 16) * 16 +
+         static_cast<uint32_t>(b) % 16;
+}
+
 // The outputs of one (step t, sequence b, unit j): dequantised h at row t + 1, and in
-// training v (z, r, n, hh_n dequantised) and the five mask families, one element at a time.
+// training v (z, r, n, hh_n dequantised) and the five mask families, one element at a time
+// (or their codes, with a.vc set).
 __device__ __forceinline__ void store_point(const RecArgs &a, const StepParams &p, int t, int b,
                                             int j, const PointOut &o) {
   const uint32_t H = static_cast<uint32_t>(a.H), B = static_cast<uint32_t>(a.B), C = 3u * H;
   const uint32_t stepH = static_cast<uint32_t>(t) * B * H;
   const uint32_t oH = static_cast<uint32_t>(b) * H + j;
   a.hout[stepH + B * H + oH] = (o.h - p.zp_h) * p.eff_h;
-  if (a.training) {
+  if (a.training && a.vc) {
+    const uint32_t row = codes_row(t, b, j, a.B, a.H), e = static_cast<uint32_t>(j) % 16;
+    a.vc[64 * row + e] = static_cast<uint16_t>(code_u16(o.z, p.zout.lo));
+    a.vc[64 * row + 16 + e] = static_cast<uint16_t>(code_u16(o.r, p.rout.lo));
+    a.vc[64 * row + 32 + e] = static_cast<uint16_t>(code_u16(o.n, p.nout.lo));
+    a.vc[64 * row + 48 + e] = static_cast<uint16_t>(code_u16(o.rh_n, p.rh.lo));
+    a.mb[16 * row + e] = static_cast<uint16_t>(code_mask_bits(o));
+  } else if (a.training) {
     const uint32_t v0 = 4u * stepH + 4u * static_cast<uint32_t>(b) * H + j;
     a.v[v0] = (o.z - p.zp_zout) * p.eff_zout;
     a.v[v0 + H] = (o.r - p.zp_rout) * p.eff_rout;
@@ -645,7 +683,7 @@ struct ClArgs {
   int ncl, G, UT, ntiles, Bpad, ndir;  // clusters walk (direction, batch tile) pairs
   int stage_h;                         // h tile staged in LDS once per workgroup (large H)
   int gate_tab;                        // gate activations by table (every gate grid fits)
-  unsigned *counters;                  // [ncl]
+  unsigned *counters;                  // [ncl], kCounterStride words apart
   int *timeout;
   unsigned spin_limit;  // polls before a wait gives up (cluster::spin_limit())
 };
@@ -876,7 +914,17 @@ __device__ __forceinline__ void recurrence_cl_pair(const RecArgs &a, const StepP
       if (a.wide_out) {
         float *f = sf + nr * 5 * UW + jj;
         f[0] = (h2 - p.zp_h) * p.eff_h;
-        if (a.training) {
+        if (a.training && a.vc) {
+          // codes in their blocked layout (codes_row), over the mask bytes: the member's UT
+          // v-code blocks, then its UT mask-bit blocks
+          uint16_t *c16 = reinterpret_cast<uint16_t *>(sb) + (utl * 16 + nr) * 64 + l % 16;
+          c16[0] = static_cast<uint16_t>(code_u16(o.z, p.zout.lo));
+          c16[16] = static_cast<uint16_t>(code_u16(o.r, p.rout.lo));
+          c16[32] = static_cast<uint16_t>(code_u16(o.n, p.nout.lo));
+          c16[48] = static_cast<uint16_t>(code_u16(o.rh_n, p.rh.lo));
+          reinterpret_cast<uint16_t *>(sb)[1024 * cl.UT + (utl * 16 + nr) * 16 + l % 16] =
+              static_cast<uint16_t>(code_mask_bits(o));
+        } else if (a.training) {
           f[UW] = (o.z - p.zp_zout) * p.eff_zout;
           f[2 * UW] = (o.r - p.zp_rout) * p.eff_rout;
           f[3 * UW] = (o.n - p.zp_nout) * p.eff_nout;
@@ -908,7 +956,18 @@ __device__ __forceinline__ void recurrence_cl_pair(const RecArgs &a, const StepP
                                         member * UW + 4 * q) =
                 *reinterpret_cast<const float4 *>(sf + row * 5 * UW + 4 * q);
         }
-        if (a.training) {
+        if (a.training && a.vc) {
+          // one contiguous run of UT blocks per array (the batch tile's padding rows too)
+          const uint4 *c16 = reinterpret_cast<const uint4 *>(sb);
+          const size_t blk = (static_cast<size_t>(t) * cl.ntiles + tile) * (H / 16) +
+                             static_cast<size_t>(member) * cl.UT;
+          uint4 *dv = reinterpret_cast<uint4 *>(a.vc + blk * 1024);
+          uint4 *dm = reinterpret_cast<uint4 *>(a.mb + blk * 256);
+          const int nv = 128 * cl.UT, nm = 32 * cl.UT;  // 16-byte chunks
+          for (int c = (tid + nthr - (16 * fq) % nthr) % nthr; c < nv; c += nthr) dv[c] = c16[c];
+          for (int c = (tid + nthr - (16 * fq + nv) % nthr) % nthr; c < nm; c += nthr)
+            dm[c] = c16[nv + c];
+        } else if (a.training) {
           for (int c = (tid + nthr - (16 * fq) % nthr) % nthr; c < 64 * fq; c += nthr) {
             const int row = c / (4 * fq), fld = (c / fq) % 4, q = c % fq, bb = b0 + row;
             if (bb < B)
@@ -937,7 +996,7 @@ __global__ __launch_bounds__(512) void recurrence_cl(RecArgs a0, RecArgs a1,
                                                      const StepParams *__restrict__ ps,
                                                      ClArgs cl) {
   const cluster::Place pl = cluster::place(cl.G, cl.ncl);
-  unsigned *counter = cl.counters + pl.cluster;
+  unsigned *counter = cl.counters + cluster::kCounterStride * pl.cluster;
   unsigned epoch = 0;
   bool alive = true;
   for (int pair = pl.cluster; pair < cl.ndir * cl.ntiles && alive; pair += cl.ncl) {
@@ -978,7 +1037,7 @@ struct FwdWorkspace {
     rfrag = o; o += al(sizeof(v4i) * 64 * static_cast<size_t>(H / 16) * 3 * ((H + 63) / 64));
     const size_t Bpad = (static_cast<size_t>(B) + kTileB - 1) / kTileB * kTileB;
     hx = o; o += al(2 * 2 * Bpad * ((H + 63) / 64) * 64);
-    sync = o; o += al(sizeof(unsigned) * (2 * (Bpad / kTileB) + 2));  // clusters of both directions
+    sync = o; o += al(sizeof(unsigned) * cluster::kCounterStride * (2 * (Bpad / kTileB) + 2));  // clusters of both directions
     sparams = o; o += al(2 * sizeof(StepParams));
     // packed operands of the input projection (I <= 256): x planes, W fragments, W column sums
     const size_t ip = static_cast<size_t>(I) <= kPackedMaxK ? 1 : 0;
@@ -1025,7 +1084,7 @@ struct FwdPlan {
 };
 
 static int forward_prologue(bool training, int T, int B, int I, int H, const rxmet_gru_fwd_dir &d,
-                            const XLayout &xl,
+                            const XLayout &xl, const rxmet_gru_saved_codes *codes,
                             hipStream_t stream, FwdPlan *plan) {
   const rxmet_gru_qparams *params = d.params;
   RXMET_CHECK_ARG(params != nullptr, "params must be non-null");
@@ -1034,7 +1093,19 @@ static int forward_prologue(bool training, int T, int B, int I, int H, const rxm
                       d.x_q && d.workspace,
                   "required pointer is null");
   if (int rc = host_bits_check(*params)) return rc;
-  if (training) {
+  if (training && codes) {
+    RXMET_CHECK_ARG(codes->v_codes && codes->mask_bits && d.x_mask && d.W_mask && d.R_mask &&
+                        d.bw_mask && d.br_mask && (d.h0 == nullptr || d.h0_mask),
+                    "training needs the saved codes and the x, W, R and bias mask outputs");
+    auto a16 = [](const void *q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; };
+    RXMET_CHECK_ARG(a16(codes->v_codes) && a16(codes->mask_bits),
+                    "v_codes and mask_bits must be 16-byte aligned");
+    for (int gi : {RXMET_GRU_Z_OUT, RXMET_GRU_R_OUT, RXMET_GRU_N_OUT, RXMET_GRU_RH}) {
+      const Bounds b = bounds_of(params->g[gi].bits, params->g[gi].is_unsigned);
+      RXMET_CHECK_ARG(b.hi - b.lo <= 65535.0f,
+                      "saved codes need gate output and weight_hh_linear grids of at most 16 bits");
+    }
+  } else if (training) {
     RXMET_CHECK_ARG(d.v && d.x_mask && d.W_mask && d.R_mask && d.bw_mask && d.br_mask &&
                         d.ih_mask && d.hh_mask && d.gate_in_mask && d.gate_out_mask && d.h_mask &&
                         (d.h0 == nullptr || d.h0_mask),
@@ -1184,11 +1255,20 @@ static int forward_prologue(bool training, int T, int B, int I, int H, const rxm
   ra.gih = gih; ra.rfrag = rfrag; ra.chan = chan; ra.h0codes = h0codes; ra.hout = d.h; ra.v = d.v;
   ra.ih_m = d.ih_mask; ra.hh_m = d.hh_mask; ra.gin_m = d.gate_in_mask;
   ra.gout_m = d.gate_out_mask; ra.h_m = d.h_mask;
+  ra.vc = nullptr; ra.mb = nullptr;
+  if (training && codes) {
+    ra.v = nullptr;
+    ra.ih_m = ra.hh_m = ra.gin_m = ra.gout_m = ra.h_m = nullptr;
+    ra.vc = codes->v_codes;
+    ra.mb = codes->mask_bits;
+  }
   ra.hx = reinterpret_cast<int8_t *>(wsb + ws.hx);
   {
     auto a16 = [](const void *q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; };
     bool wide = H % 16 == 0 && a16(ra.hout);
-    if (training)
+    if (training && ra.vc)
+      wide = wide && a16(ra.vc) && a16(ra.mb);
+    else if (training)
       wide = wide && a16(ra.v) && a16(ra.ih_m) && a16(ra.hh_m) && a16(ra.gin_m) &&
              a16(ra.gout_m) && a16(ra.h_m);
     ra.wide_out = wide ? 1 : 0;
@@ -1257,9 +1337,10 @@ static int forward_recurrence_clustered(FwdPlan *plans, int ndir, int T, int B, 
   cl.ncl = ncl;
   const FwdWorkspace ws(T, B, I, H);
   cl.counters = reinterpret_cast<unsigned *>(plans[0].wsb + ws.sync);
-  cl.timeout = reinterpret_cast<int *>(cl.counters + ncl);
+  cl.timeout = reinterpret_cast<int *>(cl.counters + cluster::kCounterStride * ncl);
   cl.spin_limit = cluster::spin_limit();
-  hipLaunchKernelGGL(cluster::zero_words, dim3(1), dim3(256), 0, stream, cl.counters, ncl + 1);
+  hipLaunchKernelGGL(cluster::zero_words, dim3(1), dim3(256), 0, stream, cl.counters,
+                     cluster::kCounterStride * ncl + 1);
   RXMET_CHECK_LAUNCH();
   RecArgs &a1 = plans[ndir > 1 ? 1 : 0].ra;
   // both directions' step parameters in device memory (read with scalar loads)
@@ -1277,8 +1358,10 @@ static int forward_recurrence_clustered(FwdPlan *plans, int ndir, int T, int B, 
   for (int k = 0; k < ndir; ++k) {
     pl.p[pl.count] = plans[k].ra.hout;
     pl.n[pl.count++] = static_cast<int64_t>(T + 1) * B * H;
-    pl.p[pl.count] = plans[k].ra.v;
-    pl.n[pl.count++] = static_cast<int64_t>(T) * B * 4 * H;
+    if (plans[k].ra.v) {
+      pl.p[pl.count] = plans[k].ra.v;
+      pl.n[pl.count++] = static_cast<int64_t>(T) * B * 4 * H;
+    }
   }
   hipLaunchKernelGGL(cluster::poison_list, dim3(256), dim3(256), 0, stream, cl.timeout, pl);
   RXMET_CHECK_LAUNCH();
@@ -1347,7 +1430,7 @@ static int forward_recurrence_tiles(FwdPlan &plan, int B, int H, hipStream_t str
 
 static int forward_dirs(int ndir, bool training, int T, int B, int I, int H,
                         const rxmet_gru_fwd_dir *dirs, const int64_t *x_layout,
-                        hipStream_t stream) {
+                        hipStream_t stream, const rxmet_gru_saved_codes *codes = nullptr) {
   RXMET_CHECK_ARG(ndir == 1 || ndir == 2, "ndir must be 1 or 2");
   RXMET_CHECK_ARG(dirs != nullptr, "dirs must be non-null");
   RXMET_CHECK_ARG(T >= 1 && B >= 1 && I >= 1 && H >= 1, "dimensions must be positive");
@@ -1364,7 +1447,9 @@ static int forward_dirs(int ndir, bool training, int T, int B, int I, int H,
       RXMET_CHECK_ARG(static_cast<double>(T) * B * I < 4294967295.0 && xl.st >= 0 && xl.sb >= 0,
                       "strided x: T*B*I must be below 2^32 and the strides non-negative");
     }
-    if (int rc = forward_prologue(training, T, B, I, H, dirs[k], xl, stream, &plans[k])) return rc;
+    if (int rc = forward_prologue(training, T, B, I, H, dirs[k], xl, codes ? &codes[k] : nullptr,
+                                  stream, &plans[k]))
+      return rc;
   }
   bool stepped = false;
   for (int k = 0; k < ndir; ++k) stepped = stepped || plans[k].stepped;
@@ -1426,6 +1511,16 @@ int rxmet_gru_forward_quant_dirs_x(int32_t ndir, int32_t is_training, int32_t T,
   RXMET_CHECK_ARG(x_layout != nullptr, "x_layout must be non-null");
   return forward_dirs(ndir, is_training != 0, T, B, I, H, dirs, x_layout,
                       static_cast<hipStream_t>(stream_));
+}
+
+int rxmet_gru_forward_quant_dirs_codes(int32_t ndir, int32_t is_training, int32_t T, int32_t B,
+                                       int32_t I, int32_t H, const rxmet_gru_fwd_dir *dirs,
+                                       const int64_t *x_layout, const rxmet_gru_saved_codes *codes,
+                                       void *stream_) {
+  clear_error();
+  RXMET_CHECK_ARG(codes != nullptr || !is_training, "codes must be non-null in training");
+  return forward_dirs(ndir, is_training != 0, T, B, I, H, dirs, x_layout,
+                      static_cast<hipStream_t>(stream_), is_training ? codes : nullptr);
 }
 
 }  // extern "C"

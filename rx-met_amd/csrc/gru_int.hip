@@ -335,7 +335,7 @@ struct IClDir {
 struct IClArgs {
   int T, B, H, KS, Bpad;
   int G, UT, ncl, ntiles, ndir;
-  unsigned *counters;           // [ncl]
+  unsigned *counters;           // [ncl], kCounterStride words apart
   int *timeout;
   unsigned spin_limit;  // polls before a wait gives up (cluster::spin_limit())
 };
@@ -595,7 +595,7 @@ __global__ __launch_bounds__(512) void int_recurrence_cl(IClDir a0, IClDir a1,
                                                          IClArgs s) {
   extern __shared__ __align__(16) unsigned char smem[];
   const cluster::Place pl = cluster::place(s.G, s.ncl);
-  unsigned *counter = s.counters + pl.cluster;
+  unsigned *counter = s.counters + cluster::kCounterStride * pl.cluster;
   unsigned epoch = 0;
   bool alive = true;
   for (int pair = pl.cluster; pair < s.ndir * s.ntiles && alive; pair += s.ncl) {
@@ -643,7 +643,7 @@ struct IntWorkspace {
     rfrag = o; o += al(sizeof(v4i) * 64 * (static_cast<size_t>(H) / 16) * 3 * KS);
     rcol = o; o += al(sizeof(int32_t) * C);
     hx = o; o += al(2 * 2 * Bpad * KS * 64);
-    sync = o; o += al(sizeof(unsigned) * (2 * Bpad / kITile + 2));  // counters of up to 2 directions
+    sync = o; o += al(sizeof(unsigned) * cluster::kCounterStride * (2 * Bpad / kITile + 2));  // counters of up to 2 directions
     sparams = o; o += al(2 * sizeof(IntStepParams));
     total = o;
   }
@@ -799,9 +799,10 @@ static int int_recurrence_clustered(IntPlan *plans, int ndir, hipStream_t stream
   IntStepParams *ps = reinterpret_cast<IntStepParams *>(plans[0].wsb + ws.sparams);
   if (int rc = upload(ps, host_ps, sizeof(host_ps), stream)) return rc;
   s.counters = reinterpret_cast<unsigned *>(plans[0].wsb + ws.sync);
-  s.timeout = reinterpret_cast<int *>(s.counters + ncl);
+  s.timeout = reinterpret_cast<int *>(s.counters + cluster::kCounterStride * ncl);
   s.spin_limit = cluster::spin_limit();
-  hipLaunchKernelGGL(cluster::zero_words, dim3(1), dim3(256), 0, stream, s.counters, ncl + 1);
+  hipLaunchKernelGGL(cluster::zero_words, dim3(1), dim3(256), 0, stream, s.counters,
+                     cluster::kCounterStride * ncl + 1);
   RXMET_CHECK_LAUNCH();
   void *args[] = {&dirs[0], &dirs[1], &ps, &s};
   {

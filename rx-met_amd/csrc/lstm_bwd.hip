@@ -500,7 +500,7 @@ __global__ __launch_bounds__(512) void lstm_bwd_recurrence_cl(BwdArgs a, BwdClAr
     zc[0][ut] = s0;
     zc[1][ut] = s1;
   }
-  unsigned *counter = cl.counters + pl.cluster;
+  unsigned *counter = cl.counters + cluster::kCounterStride * pl.cluster;
   unsigned epoch = 0;
   bool alive = true;
   const uint32_t BC = static_cast<uint32_t>(B) * C;
@@ -811,7 +811,7 @@ struct BwdWorkspace {
     csum = o; o += al(sizeof(float) * KS2 * H);
     xp = o; o += al(2 * 3 * Bpad * C);
     xe = o; o += al(sizeof(int) * 2 * Bpad * G);
-    sync = o; o += al(sizeof(unsigned) * (Bpad / kBB + 1));
+    sync = o; o += al(sizeof(unsigned) * cluster::kCounterStride * (Bpad / kBB + 1));
     // stepped recurrence: K-split parts of dh, the cell gradient, W_hh codes as bf16 planes
     dhr = o; o += al(sizeof(float) * kBStepMaxSplit * static_cast<size_t>(B) * H);
     dcs = o; o += al(sizeof(float) * static_cast<size_t>(B) * H);
@@ -996,12 +996,13 @@ int rxmet_lstm_backward_quant(int32_t T, int32_t B, int32_t I, int32_t H,
       cl.xp = reinterpret_cast<int8_t *>(wsb + ws.xp);
       cl.xe = reinterpret_cast<int *>(wsb + ws.xe);
       cl.counters = reinterpret_cast<unsigned *>(wsb + ws.sync);
-      cl.timeout = reinterpret_cast<int *>(cl.counters + ncl);
+      cl.timeout = reinterpret_cast<int *>(cl.counters + cluster::kCounterStride * ncl);
       cl.spin_limit = cluster::spin_limit();
       hipLaunchKernelGGL(lstm_pack_whh_t_cl, dim3((H / 16) * KS2), dim3(64), 0, stream, H, KS2,
                          sv.w_hh_q, wf, cs);
       RXMET_CHECK_LAUNCH();
-      hipLaunchKernelGGL(cluster::zero_words, dim3(1), dim3(256), 0, stream, cl.counters, ncl + 1);
+      hipLaunchKernelGGL(cluster::zero_words, dim3(1), dim3(256), 0, stream, cl.counters,
+                     cluster::kCounterStride * ncl + 1);
       RXMET_CHECK_LAUNCH();
       void *args[] = {&ba, &cl};
       {

@@ -655,7 +655,7 @@ __device__ __forceinline__ float lut_code(const uint32_t *t, int idx, int out_lo
 struct ClusterArgs {
   int ncl, G, ntiles, Bpad;
   int8_t *hx;          // [2][NPL][Bpad][H] centred h codes as int8 planes
-  unsigned *counters;  // [ncl] barrier arrivals
+  unsigned *counters;  // [ncl] barrier arrivals, kCounterStride words apart
   int *timeout;        // set by a member whose barrier wait gave up
   unsigned spin_limit; // polls before a wait gives up (cluster::spin_limit())
   ActLut lut;
@@ -782,7 +782,7 @@ __global__ __launch_bounds__(512) void lstm_recurrence_cl(RecArgs a, StepParams 
     hk64[q] = (static_cast<int64_t>(r.hh_k_hi) << 32) | static_cast<uint32_t>(r.hh_k);
   }
   const v4i ones = v4i{0x01010101, 0x01010101, 0x01010101, 0x01010101};
-  unsigned *counter = cl.counters + pl.cluster;
+  unsigned *counter = cl.counters + cluster::kCounterStride * pl.cluster;
   unsigned epoch = 0;
   bool alive = true;
   const bool train = a.hidden != nullptr;
@@ -1097,7 +1097,7 @@ struct FwdWorkspace {
     // clustered recurrence: h exchange planes (two parities, up to two planes) and counters
     const size_t Bpad = (static_cast<size_t>(B) + 15) / 16 * 16;
     hx = o; o += al(2 * 2 * Bpad * H);
-    sync = o; o += al(sizeof(unsigned) * (Bpad / 16 + 1));
+    sync = o; o += al(sizeof(unsigned) * cluster::kCounterStride * (Bpad / 16 + 1));
     lut = o; o += al(sizeof(uint32_t) * 2 * kLutMaxEntries);
     glut = o; o += al(sizeof(uint32_t) * 5 * static_cast<size_t>(kGlobalLutMaxCodes));
     // reference activation exceptions: keys, then entries, of at most 5 full 16-bit grids
@@ -1448,10 +1448,11 @@ int rxmet_lstm_forward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const f
       cl.ncl = ncl;
       cl.hx = reinterpret_cast<int8_t *>(wsb + ws.hx);
       cl.counters = reinterpret_cast<unsigned *>(wsb + ws.sync);
-      cl.timeout = reinterpret_cast<int *>(cl.counters + ncl);
+      cl.timeout = reinterpret_cast<int *>(cl.counters + cluster::kCounterStride * ncl);
       cl.spin_limit = cluster::spin_limit();
       cl.lut = lut;
-      hipLaunchKernelGGL(cluster::zero_words, dim3(1), dim3(256), 0, stream, cl.counters, ncl + 1);
+      hipLaunchKernelGGL(cluster::zero_words, dim3(1), dim3(256), 0, stream, cl.counters,
+                     cluster::kCounterStride * ncl + 1);
       RXMET_CHECK_LAUNCH();
       const int n_exc = static_cast<int>(exc.key.size());
       if (lut.total > 0) {

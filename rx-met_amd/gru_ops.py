@@ -478,8 +478,11 @@ MASK_NAMES = ("x_mask", "h0_mask", "W_mask", "R_mask", "bw_mask", "br_mask",
               "gate_output_mask", "h_mask")
 
 
-def _forward_dir(is_training, T, B, I, H, W, R, bw, br, x, h0, quant_params):
-    """Check one direction's inputs and allocate its outputs; returns (outputs, FwdDir)."""
+def _forward_dir(is_training, T, B, I, H, W, R, bw, br, x, h0, quant_params, codes=False):
+    """Check one direction's inputs and allocate its outputs; returns (outputs, FwdDir,
+    workspace), and with ``codes`` (training) the SavedCodes of the direction as well: the
+    outputs are then (h, v_codes, W_q, .., x_q, the six x / h0 / W / R / bias masks,
+    mask_bits)."""
     for n, t in (("W", W), ("R", R), ("bw", bw), ("br", br), ("x", x)):
         _check_f32_cuda(n, t)
     has_h0 = h0 is not None and h0.numel() > 0
@@ -492,7 +495,8 @@ def _forward_dir(is_training, T, B, I, H, W, R, bw, br, x, h0, quant_params):
     f32 = dict(dtype=torch.float32, device=dev)
     u8 = dict(dtype=torch.uint8, device=dev)
     h = torch.empty((T + 1, B, H), **f32)
-    v = torch.empty((T, B, 4 * H), **f32) if is_training else torch.empty((0,), **f32)
+    codes = codes and is_training
+    v = torch.empty((T, B, 4 * H), **f32) if is_training and not codes else torch.empty((0,), **f32)
     W_q = torch.empty((I, C), **f32)
     R_q = torch.empty((H, C), **f32)
     bw_q = torch.empty((C,), **f32)
@@ -502,7 +506,11 @@ def _forward_dir(is_training, T, B, I, H, W, R, bw, br, x, h0, quant_params):
         masks = [torch.empty((T, B, I), **u8),
                  torch.empty((B, H), **u8) if has_h0 else torch.empty((0,), **u8),
                  torch.empty((I, C), **u8), torch.empty((H, C), **u8), torch.empty((C,), **u8),
-                 torch.empty((C,), **u8)] + [torch.empty((T, B, C), **u8) for _ in range(4)] + \
+                 torch.empty((C,), **u8)]
+        if codes:
+            masks += [torch.empty((0,), **u8) for _ in range(5)]
+        else:
+            masks += [torch.empty((T, B, C), **u8) for _ in range(4)] + \
                 [torch.empty((T, B, H), **u8)]
     else:
         masks = [torch.empty((0,), **u8) for _ in range(11)]
@@ -510,9 +518,16 @@ def _forward_dir(is_training, T, B, I, H, W, R, bw, br, x, h0, quant_params):
     mp = [m.data_ptr() if m.numel() > 0 else None for m in masks]
     d = A.FwdDir(W.data_ptr(), R.data_ptr(), bw.data_ptr(), br.data_ptr(), x.data_ptr(),
                  h0.data_ptr() if has_h0 else None, ctypes.addressof(quant_params.struct),
-                 h.data_ptr(), v.data_ptr() if is_training else None, W_q.data_ptr(),
+                 h.data_ptr(), v.data_ptr() if v.numel() else None, W_q.data_ptr(),
                  R_q.data_ptr(), bw_q.data_ptr(), br_q.data_ptr(), x_q.data_ptr(), *mp,
                  ws.data_ptr())
+    if codes:
+        i16 = dict(dtype=torch.int16, device=dev)
+        Bp = (B + 15) // 16 * 16
+        vc = torch.empty((T, Bp * 4 * H), **i16)
+        mb = torch.empty((T, Bp * H), **i16)
+        sc = A.SavedCodes(vc.data_ptr(), mb.data_ptr())
+        return (h, vc, W_q, R_q, bw_q, br_q, x_q, *masks[:6], mb), d, ws, sc
     outs = (h, v, W_q, R_q, bw_q, br_q, x_q, *masks)
     return outs, d, ws
 
@@ -572,6 +587,73 @@ def forward_quant_float_storage_dirs_x(is_training, time_steps, batch_size, inpu
     return [m[0] for m in made]
 
 
+def forward_quant_codes_dirs(is_training, time_steps, batch_size, input_size, hidden_size, dirs,
+                             x_layouts=None):
+    """forward_quant_float_storage_dirs(_x) keeping the saved state as codes
+    (rxmet_gru_forward_quant_dirs_codes), for callers that only hand it to
+    backward_quant_codes_dirs.  Per direction (h, v_codes [T, Bp 4H] int16, W_q, R_q, bw_q,
+    br_q, x_q, x_mask, h0_mask, W_mask, R_mask, bw_mask, br_mask, mask_bits [T, Bp H] int16),
+    Bp = B rounded up to 16; v_codes holds each of z, r, n, hh_n as code minus grid minimum
+    (read as unsigned 16 bits), mask_bits the 13 per-step masks of an element, both in blocks
+    of 16 sequences x 16 units (rxmet_gru_saved_codes; ``unblock_codes`` restores [T, B, .]).
+    Not training: as the float-storage call.
+    ``x_layouts`` as in forward_quant_float_storage_dirs_x, or None for [T, B, I] inputs."""
+    T, B, I, H = time_steps, batch_size, input_size, hidden_size
+    if H % _UNIT_TILE:
+        raise RuntimeError("the saved-codes entry points need hidden_size % 16 == 0")
+    made = [_forward_dir(is_training, T, B, I, H, *d, codes=True) for d in dirs]
+    arr = (A.FwdDir * len(made))(*[m[1] for m in made])
+    lay = None
+    if x_layouts is not None:
+        lay = (ctypes.c_int64 * (4 * len(made)))(*[int(v) for xl in x_layouts for v in xl])
+    codes = None
+    if is_training:
+        codes = (A.SavedCodes * len(made))(*[m[3] for m in made])
+    _rx.call("rxmet_gru_forward_quant_dirs_codes", len(made), int(bool(is_training)), T, B, I, H,
+             arr, lay, codes, _stream(dirs[0][4].device))
+    return [m[0] for m in made]
+
+
+def backward_quant_codes_dirs(time_steps, batch_size, input_size, hidden_size, dirs,
+                              torch_layout=True):
+    """The backward of forward_quant_codes_dirs (rxmet_gru_backward_quant_dirs_codes): ``dirs``
+    is a list of (W_q, R_q, bw_q, br_q, x_q, dh_new, h, v_codes, quant_params, masks) with
+    masks = (x_mask, h0_mask, W_mask, R_mask, bw_mask, br_mask, mask_bits); returns one
+    (dx, dW, dR, dbw, dbr, dh) tuple per direction, the weight gradients in PyTorch's layout
+    and gate order unless ``torch_layout`` is False."""
+    T, B, I, H = time_steps, batch_size, input_size, hidden_size
+    made, codes = [], []
+    Bp = (B + 15) // 16 * 16
+    for (W_q, R_q, bw_q, br_q, x_q, dh_new, h, vc, qp, masks) in dirs:
+        if vc.dtype != torch.int16 or tuple(vc.shape) != (T, Bp * 4 * H) or not vc.is_contiguous():
+            raise RuntimeError("v_codes must be a contiguous int16 tensor of shape [T, Bp 4H]")
+        mb = masks[6]
+        if mb.dtype != torch.int16 or tuple(mb.shape) != (T, Bp * H) or not mb.is_contiguous():
+            raise RuntimeError("mask_bits must be a contiguous int16 tensor of shape [T, Bp H]")
+        outs, d, keep = _backward_dir(T, B, I, H, W_q, R_q, bw_q, br_q, x_q, dh_new, h, None,
+                                      qp, tuple(masks[:6]) + (None,) * 5,
+                                      torch_layout=torch_layout)
+        made.append((outs, d, keep))
+        codes.append(A.SavedCodes(vc.data_ptr(), mb.data_ptr()))
+    arr = (A.BwdDir * len(made))(*[m[1] for m in made])
+    carr = (A.SavedCodes * len(made))(*codes)
+    _rx.call("rxmet_gru_backward_quant_dirs_codes", len(made), T, B, I, H, arr,
+             1 if torch_layout else 0, carr, _stream(dirs[0][4].device))
+    return [m[0] for m in made]
+
+
+def unblock_codes(codes, B, H, fields):
+    """[T, B, fields H] view order of blocked saved codes (forward_quant_codes_dirs): ``codes``
+    [T, Bp fields H] with blocks of [16 rows][fields][16 units] (fields 4 for v_codes, 1 for
+    mask_bits).  Works on torch tensors and numpy arrays."""
+    T = codes.shape[0]
+    nt = (B + 15) // 16
+    blk = codes.reshape(T, nt, H // 16, 16, fields, 16)
+    perm = (0, 1, 3, 4, 2, 5)
+    blk = blk.permute(*perm) if isinstance(blk, torch.Tensor) else blk.transpose(perm)
+    return blk.reshape(T, nt * 16, fields * H)[:, :B]
+
+
 def bidir_assemble(h_f, h_r, batch_first: bool):
     """(output, h_n) of a bidirectional layer from both directions' h [T+1, B, H]
     (rxmet_gru_bidir_assemble): output [T, B, 2H], or [B, T, 2H] when batch_first.  The
@@ -628,6 +710,8 @@ def _backward_dir(T, B, I, H, W_q, R_q, bw_q, br_q, x_q, dh_new, h, v, quant_par
                       ("br_q", br_q, (C,)), ("x_q", x_q, (T, B, I)),
                       ("dh_new", dh_new, (T + 1, B, H)), ("h", h, (T + 1, B, H)),
                       ("v", v, (T, B, 4 * H))):
+        if t is None and n == "v":  # saved codes instead (backward_quant_codes_dirs)
+            continue
         _check_f32_cuda(n, t)
         if tuple(t.shape) != shp:
             raise RuntimeError(f"{n} must have shape {list(shp)}")
@@ -640,7 +724,7 @@ def _backward_dir(T, B, I, H, W_q, R_q, bw_q, br_q, x_q, dh_new, h, v, quant_par
     dh_new = dh_new.contiguous()
     ws = _ws(_rx.load().rxmet_gru_backward_workspace_bytes(T, B, I, H), dev)
     d = A.BwdDir(W_q.data_ptr(), R_q.data_ptr(), bw_q.data_ptr(), br_q.data_ptr(), x_q.data_ptr(),
-                 dh_new.data_ptr(), h.data_ptr(), v.data_ptr(),
+                 dh_new.data_ptr(), h.data_ptr(), v.data_ptr() if v is not None else None,
                  ctypes.addressof(quant_params.struct), *mp, *[o.data_ptr() for o in outs],
                  ws.data_ptr())
     return outs, d, (ws, dh_new)

@@ -418,6 +418,20 @@ def _aimet_split(op: dict, parts: int) -> list:
 # ------------------------------------------------------------------------------------
 
 
+# Training forwards of the module keep their saved state as codes (gru_ops.
+# forward_quant_codes_dirs: v as 16-bit codes, the 13 per-step masks as bits) rather than in
+# the reference's float / byte format, which only the gru_ops entry points hand out; the
+# gradients are the same bit for bit.  False: the reference format throughout.
+SAVE_STATE_AS_CODES = True
+
+
+def _codes_fit(quant_params) -> bool:
+    """The saved codes hold grids of at most 16 bits (gate outputs and weight_hh_linear)."""
+    g = quant_params.struct.g
+    return all(int(g[A.GRID[n]].bits) <= 16 for n in ("update_gate_output", "reset_gate_output",
+                                                       "new_gate_output", "weight_hh_linear"))
+
+
 class GRUFunction(torch.autograd.Function):
     """One direction of a quantised GRU.  forward: weight reorder -> forward_quant_float_storage
     (or forward_quant_int_storage for quant_storage_dtype='int32'); backward: dh_new [T+1,B,H]
@@ -447,16 +461,31 @@ class GRUFunction(torch.autograd.Function):
                              f"{quant_storage_dtype}")
         device = _require_device(input)
         input = ensure_cuda_float32(input, device).contiguous()
-        W, R, bw, br = convert_weights_to_haste_format(weight_ih, weight_hh, bias_ih, bias_hh, H,
-                                                       device)
         h0_t = (ensure_cuda_float32(h0, device).contiguous() if h0 is not None
                 else torch.empty(0, device=device, dtype=torch.float32))
-        # float32: codes stored as fp32 (FP32 carrier); int32: the int32 carrier
-        forward_fn = (gru_ops.forward_quant_int_storage if quant_storage_dtype == "int32"
-                      else gru_ops.forward_quant_float_storage)
-        outs = forward_fn(
-            is_training=is_training, time_steps=T, batch_size=B, input_size=I, hidden_size=H,
-            W=W, R=R, bw=bw, br=br, x=input, h0=h0_t, quant_params=quant_params)
+        ctx.codes = bool(is_training and quant_storage_dtype == "float32" and H % 16 == 0
+                         and SAVE_STATE_AS_CODES and _codes_fit(quant_params))
+        if ctx.codes:
+            # weights read in PyTorch's layout by the library; saved state as codes
+            W = ensure_cuda_float32(weight_ih, device).contiguous()
+            R = ensure_cuda_float32(weight_hh, device).contiguous()
+            if bias_ih is not None and bias_hh is not None:
+                bw = ensure_cuda_float32(bias_ih, device).contiguous()
+                br = ensure_cuda_float32(bias_hh, device).contiguous()
+            else:
+                bw = br = _zeros(3 * H, device)
+            outs = gru_ops.forward_quant_codes_dirs(
+                True, T, B, I, H, [(W, R, bw, br, input, h0_t, quant_params)],
+                [(B * I, I, 0, 1)])[0]
+        else:
+            W, R, bw, br = convert_weights_to_haste_format(weight_ih, weight_hh, bias_ih, bias_hh,
+                                                           H, device)
+            # float32: codes stored as fp32 (FP32 carrier); int32: the int32 carrier
+            forward_fn = (gru_ops.forward_quant_int_storage if quant_storage_dtype == "int32"
+                          else gru_ops.forward_quant_float_storage)
+            outs = forward_fn(
+                is_training=is_training, time_steps=T, batch_size=B, input_size=I, hidden_size=H,
+                W=W, R=R, bw=bw, br=br, x=input, h0=h0_t, quant_params=quant_params)
         h_full = outs[0]
         ctx.quant_storage_dtype = quant_storage_dtype
         ctx.bias_none = (bias_ih is None, bias_hh is None)
@@ -464,7 +493,8 @@ class GRUFunction(torch.autograd.Function):
         ctx.quant_params = quant_params
         ctx.saved_state = bool(is_training)
         if is_training:
-            # (W_q, R_q, bw_q, br_q, x_q, h, v, 11 masks) as the backward consumes them
+            # (W_q, R_q, bw_q, br_q, x_q, h, v, 11 masks) as the backward consumes them, or
+            # (.., h, v_codes, 6 masks, mask_bits)
             ctx.save_for_backward(outs[2], outs[3], outs[4], outs[5], outs[6], h_full, outs[1],
                                   *outs[7:])
         return h_full[1:], h_full[-1:]
@@ -486,6 +516,13 @@ class GRUFunction(torch.autograd.Function):
             dh_new[1:] = grad_output
         if grad_h_n is not None and grad_h_n.numel() > 0:
             dh_new[-1] += grad_h_n[0]
+        if ctx.codes:
+            dx, dW, dR, dbw, dbr, dh = gru_ops.backward_quant_codes_dirs(
+                T, B, I, H, [(W_q, R_q, bw_q, br_q, x_q, dh_new, h, v, ctx.quant_params,
+                              masks)])[0]
+            return (dx, dW, dR, None if ctx.bias_none[0] else dbw,
+                    None if ctx.bias_none[1] else dbr, None if ctx.h0_is_none else dh,
+                    None, None, None, None)
         backward_fn = (gru_ops.backward_quant_int_storage if ctx.quant_storage_dtype == "int32"
                        else gru_ops.backward_quant_float_storage)
         dx, dW, dR, dbw, dbr, dh = backward_fn(
@@ -541,8 +578,11 @@ class GRUBidirectionalFunction(torch.autograd.Function):
             h0_t = (ensure_cuda_float32(h0, device).contiguous() if h0 is not None
                     else torch.empty(0, device=device, dtype=torch.float32))
             dirs.append((W, R, bw, br, x, h0_t, qp))
-        outs = gru_ops.forward_quant_float_storage_dirs_x(is_training, T, B, I, H, dirs,
-                                                          [(st, sb, 0, 1), (st, sb, 1, 1)])
+        ctx.codes = bool(is_training and SAVE_STATE_AS_CODES and _codes_fit(qp_f)
+                         and _codes_fit(qp_r))
+        fwd = (gru_ops.forward_quant_codes_dirs if ctx.codes
+               else gru_ops.forward_quant_float_storage_dirs_x)
+        outs = fwd(is_training, T, B, I, H, dirs, [(st, sb, 0, 1), (st, sb, 1, 1)])
         ctx.bias_none = (bi_f is None, bh_f is None)
         ctx.h0_none = (h0_f is None, h0_r is None)
         ctx.quant_params = (qp_f, qp_r)
@@ -570,7 +610,8 @@ class GRUBidirectionalFunction(torch.autograd.Function):
             masks = saved[k * n + 7:(k + 1) * n]
             dirs.append((W_q, R_q, bw_q, br_q, x_q, dh_new, h, v, ctx.quant_params[k], masks))
         # weight gradients come back in PyTorch's layout and gate order
-        res = gru_ops.backward_quant_float_storage_dirs_x(T, B, I, H, dirs)
+        res = (gru_ops.backward_quant_codes_dirs(T, B, I, H, dirs) if ctx.codes
+               else gru_ops.backward_quant_float_storage_dirs_x(T, B, I, H, dirs))
         grads = []
         for k, (dx, dW, dR, dbw, dbr, dh) in enumerate(res):
             grads.append((dW, dR, None if ctx.bias_none[0] else dbw,

@@ -94,6 +94,11 @@ class BwdDir(ctypes.Structure):
     _fields_ = [(n, _p) for n in BWD_DIR_FIELDS]
 
 
+class SavedCodes(ctypes.Structure):
+    """rxmet_gru_saved_codes: one direction's v codes [T, B, 4H] and mask bits [T, B, H]."""
+    _fields_ = [("v_codes", _p), ("mask_bits", _p)]
+
+
 _SIGS = {
     "rxmet_gru_make_params": (ctypes.c_int, [ctypes.POINTER(GruRanges), ctypes.POINTER(GruConfig),
                                              ctypes.POINTER(GruQParams)]),
@@ -121,6 +126,10 @@ _SIGS = {
     "rxmet_gru_forward_int_io": (ctypes.c_int, [_i32] * 4 + [_p] * 6 +
                                  [ctypes.POINTER(GruQParams)] + [_p] * 5 + [_p, _p]),
     "rxmet_gru_forward_quant_int_dirs": (ctypes.c_int, [_i32] * 6 + [ctypes.POINTER(IntDir), _p]),
+    "rxmet_gru_forward_quant_dirs_codes": (ctypes.c_int, [_i32] * 6 + [ctypes.POINTER(FwdDir), _p,
+                                                                     ctypes.POINTER(SavedCodes), _p]),
+    "rxmet_gru_backward_quant_dirs_codes": (ctypes.c_int, [_i32] * 5 + [ctypes.POINTER(BwdDir), _i32,
+                                                                      ctypes.POINTER(SavedCodes), _p]),
 }
 for _name, (_res, _args) in _SIGS.items():
     _rx.register(_name, _res, _args)
