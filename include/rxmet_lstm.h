@@ -183,6 +183,48 @@ int rxmet_lstm_backward_quant(int32_t T, int32_t B, int32_t I, int32_t H,
                               float *db_ih, float *db_hh, float *dh0, float *dc0,
                               void *workspace, void *stream);
 
+/*
+ * Saved state as codes, for callers that keep a training forward's state only to hand it to
+ * the backward (the module path).  No counterpart in the reference, whose forward returns the
+ * checkpoints as fp32 codes and every mask as a byte (lstm_interface_binding.cc:437-480); the
+ * gradients equal those of the reference-format pair bit for bit.  In blocks of 16 sequences x
+ * 16 units, block k = (t Bt + b / 16) (H / 16) + j / 16, Bt = ceil(B / 16), row r = b % 16,
+ * unit e = j % 16, of 3840 bytes each (blocks: T Bt H/16 of them):
+ *   bytes [0, 2048):     u16 [16 r][4 gates][16 e] the gate outputs, code - grid minimum;
+ *   bytes [2048, 3072):  u8 [4 gates][16 r][16 e] bit 0 hh-linear mask, bit 1 gate-input mask,
+ *                        bit 2 gate-output mask (1 = clamped);
+ *   bytes [3072, 3584):  u16 [16 r][16 e] tanh(c), code - grid minimum;
+ *   bytes [3584, 3840):  u8 [16 r][16 e] bit 0 cell mask, bit 1 cell-tanh mask, bit 2 hidden mask.
+ * cell_codes: u16 [16 r][16 e] per block (code - grid minimum) for T + 1 steps: step 0 c0,
+ * step t + 1 the cell after step t ((T + 1) Bt H/16 blocks).  Rows past B are unspecified.
+ * Both 16-byte aligned; the gate-output, cell and tanh grids at most 16 bits; H % 16 == 0.
+ */
+typedef struct {
+  uint8_t *blocks;
+  uint16_t *cell_codes;
+} rxmet_lstm_saved_codes;
+
+/* rxmet_lstm_forward_quant writing codes (non-null with saved) instead of saved->gate_out,
+ * cell, cell_tanh and the six recurrence masks (hh_linear_m, gate_in_m, gate_out_m, cell_m,
+ * cell_tanh_m, hidden_m), which may be null; every other saved tensor as before. */
+int rxmet_lstm_forward_quant_codes(int32_t T, int32_t B, int32_t I, int32_t H, const float *W_ih,
+                                   const float *W_hh, const float *b_ih, const float *b_hh,
+                                   const float *x, const float *h0, const float *c0,
+                                   const rxmet_lstm_params *params, float *output, float *h_n,
+                                   float *c_n, const rxmet_lstm_saved *saved,
+                                   const rxmet_lstm_saved_codes *codes, void *workspace,
+                                   void *stream);
+
+/* rxmet_lstm_backward_quant reading the codes of rxmet_lstm_forward_quant_codes instead of
+ * saved->gate_out, cell, cell_tanh and the six recurrence masks. */
+int rxmet_lstm_backward_quant_codes(int32_t T, int32_t B, int32_t I, int32_t H,
+                                    const rxmet_lstm_params *params, const rxmet_lstm_saved *saved,
+                                    const rxmet_lstm_saved_codes *codes,
+                                    const float *grad_output, const float *grad_h_n,
+                                    const float *grad_c_n, float *dx, float *dW_ih, float *dW_hh,
+                                    float *db_ih, float *db_hh, float *dh0, float *dc0,
+                                    void *workspace, void *stream);
+
 int64_t rxmet_lstm_calibrate_workspace_bytes(int32_t T, int32_t B, int32_t I, int32_t H);
 
 /* Float LSTM forward that merges MinMax statistics into `stats` (layout above): x, h

@@ -95,6 +95,11 @@ struct BwdArgs {
   double s_gout[4], zp_gout[4], s_c, zp_c, s_t, zp_t;
   float *dli, *dlh;      // [T, B, 4H]
   float *dh0, *dc0;      // [B, H]
+  // saved codes (lck_block; instead of gate_out, cell, cell_tanh and the six recurrence masks)
+  // and the grid minima their offsets are taken from
+  const uint8_t *ckb;
+  const uint16_t *cellc;
+  int32_t lo_gout[4], lo_c, lo_t;
 };
 
 // The STE backward of one (step t, sequence b, unit j) given dh and dc arriving from step t + 1
@@ -105,12 +110,72 @@ struct LstmBwdPoint {
   float li[4], lh[4], dc_prev;
 };
 
+// The saved codes of (step t, sequence b, unit j) in the reference format: gate outputs,
+// tanh(c) and the previous cell as fp32 codes, the masks as bytes (1 = clamped).
+struct LstmCk {
+  float go[4], ct, pc;
+  uint8_t m_go[4], m_gi[4], m_hh[4], m_c, m_t, m_h;
+};
+__device__ __forceinline__ LstmCk lstm_ck_codes(const BwdArgs &a, int t, int b, int j) {
+  LstmCk k;
+  const uint8_t *blk = a.ckb + static_cast<size_t>(lck_block(t, b, j, a.B, a.H)) * kLckBlock;
+  const int R = b % 16, e = j % 16;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    k.go[g] = static_cast<float>(reinterpret_cast<const uint16_t *>(blk)[(R * 4 + g) * 16 + e] +
+                                 a.lo_gout[g]);
+    const uint8_t m = blk[kLckGm + (g * 16 + R) * 16 + e];
+    k.m_hh[g] = m & 1;
+    k.m_gi[g] = (m >> 1) & 1;
+    k.m_go[g] = (m >> 2) & 1;
+  }
+  k.ct = static_cast<float>(reinterpret_cast<const uint16_t *>(blk + kLckTanh)[R * 16 + e] + a.lo_t);
+  const uint8_t m = blk[kLckCm + R * 16 + e];
+  k.m_c = m & 1;
+  k.m_t = (m >> 1) & 1;
+  k.m_h = (m >> 2) & 1;
+  k.pc = static_cast<float>(
+      a.cellc[static_cast<size_t>(lck_block(t, b, j, a.B, a.H)) * kLcellBlock + R * 16 + e] + a.lo_c);
+  return k;
+}
+
 __device__ __forceinline__ LstmBwdPoint lstm_bwd_point(const BwdArgs &a, int t, int b, int j,
                                                        float dh_in, float dc_in) {
   const uint32_t H = static_cast<uint32_t>(a.H), C = 4u * H, B = static_cast<uint32_t>(a.B);
   const uint32_t BH = B * H, BC = B * C;
   const uint32_t e = static_cast<uint32_t>(t) * BH + static_cast<uint32_t>(b) * H + j;
   const uint32_t gb = static_cast<uint32_t>(t) * BC + static_cast<uint32_t>(b) * C + j;
+  if (a.ckb) {
+    // the same arithmetic on the decoded codes
+    const LstmCk k = lstm_ck_codes(a, t, b, j);
+    const auto kp = [](uint8_t m) { return m == 0 ? 1.0f : 0.0f; };
+    const float ig = deq(k.go[0], a.s_gout[0], a.zp_gout[0]);
+    const float fg = deq(k.go[1], a.s_gout[1], a.zp_gout[1]);
+    const float gg = deq(k.go[2], a.s_gout[2], a.zp_gout[2]);
+    const float og = deq(k.go[3], a.s_gout[3], a.zp_gout[3]);
+    const float ct = deq(k.ct, a.s_t, a.zp_t);
+    const float pc = deq(k.pc, a.s_c, a.zp_c);
+    const float dht = (dh_in + a.grad_out[e]) * kp(k.m_h);
+    const float d_o = dht * ct;
+    const float dct = dht * og * kp(k.m_t);
+    const float dc = dc_in + dct * (1.0f - ct * ct);
+    const float mdc = dc * kp(k.m_c);
+    const float dfg = mdc * pc;
+    const float dig = mdc * gg, dgg = mdc * ig;
+    const float go0 = dig * kp(k.m_go[0]), go1 = dfg * kp(k.m_go[1]);
+    const float go2 = dgg * kp(k.m_go[2]), go3 = d_o * kp(k.m_go[3]);
+    const float gi[4] = {go0 * ig * (1.0f - ig), go1 * fg * (1.0f - fg), go2 * (1.0f - gg * gg),
+                         go3 * og * (1.0f - og)};
+    LstmBwdPoint o;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const float grad = gi[g] * kp(k.m_gi[g]);
+      o.li[g] = grad * keepf(a.ih_m, gb + g * H);
+      o.lh[g] = grad * kp(k.m_hh[g]);
+    }
+    o.dc_prev = mdc * fg;
+    return o;
+  }
   const float ig = deq(a.gate_out[gb], a.s_gout[0], a.zp_gout[0]);
   const float fg = deq(a.gate_out[gb + H], a.s_gout[1], a.zp_gout[1]);
   const float gg = deq(a.gate_out[gb + 2 * H], a.s_gout[2], a.zp_gout[2]);
@@ -449,6 +514,42 @@ __device__ __forceinline__ void ck_issue(const BwdArgs &a, int t, int b0, int u0
   }
 }
 
+// With saved codes the step's block in LDS is instead (16-byte chunks):
+//   the member's four code blocks  bytes 0..15359      chunks    0..959  (lck_block layout)
+//   its four cell blocks of step t bytes 15360..17407  chunks  960..1087 (the previous cell)
+//   grad_out floats [16 rows][64]  bytes 17408..21503  chunks 1088..1343
+//   ih masks bytes [16][4 gates][64] bytes 21504..25599 chunks 1344..1599
+constexpr int kCkcInst = 25;
+constexpr int kCkcCell = 15360, kCkcGrad = 17408, kCkcIh = 21504;
+
+__device__ __forceinline__ void ck_issue_codes(const BwdArgs &a, int t, int tile, int b0, int u0,
+                                               unsigned char *ck, int w, int l) {
+  if (w == 0) return;
+  const int H = a.H, C = 4 * H;
+  const uint32_t BH = static_cast<uint32_t>(a.B) * H, BC = static_cast<uint32_t>(a.B) * C;
+  const size_t nt = static_cast<size_t>(a.B + 15) / 16;
+  const size_t blk0 = (static_cast<size_t>(t) * nt + tile) * (H / 16) + u0 / 16;
+  for (int k = w - 1; k < kCkcInst; k += 7) {
+    const int q = k * 64 + l;
+    const void *src;
+    if (k < 15) {
+      src = a.ckb + blk0 * kLckBlock + 16 * q;
+    } else if (k < 17) {
+      src = reinterpret_cast<const unsigned char *>(a.cellc + blk0 * kLcellBlock) + 16 * (q - 960);
+    } else if (k < 21) {
+      const int q3 = q - 1088, R = q3 / 16, c = q3 % 16;
+      const uint32_t row = static_cast<uint32_t>(min(b0 + R, a.B - 1)) * H + u0 + 4 * c;
+      src = a.grad_out + (static_cast<uint32_t>(t) * BH + row);
+    } else {
+      const int q4 = q - 1344, R = q4 / 16, g = (q4 / 4) % 4, c = q4 % 4;
+      const int b = min(b0 + R, a.B - 1);
+      src = a.ih_m + (static_cast<uint32_t>(t) * BC + static_cast<uint32_t>(b) * C + g * H + u0 + 16 * c);
+    }
+    __builtin_amdgcn_global_load_lds(src, (lds_void *)(ck + 1024 * k), 16, 0, 0);
+  }
+}
+
+template <bool CK>
 __global__ __launch_bounds__(512) void lstm_bwd_recurrence_cl(BwdArgs a, BwdClArgs cl) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int H = a.H, C = 4 * H, B = a.B, KS2 = a.KS2, G = cl.G;
@@ -509,7 +610,10 @@ __global__ __launch_bounds__(512) void lstm_bwd_recurrence_cl(BwdArgs a, BwdClAr
 
   for (int tile = pl.cluster; tile < cl.ntiles && alive; tile += cl.ncl) {
     const int b0 = tile * kBB;
-    ck_issue(a, a.T - 1, b0, kBcUnits * m0, ck, w, l);
+    if constexpr (CK)
+      ck_issue_codes(a, a.T - 1, tile, b0, kBcUnits * m0, ck, w, l);
+    else
+      ck_issue(a, a.T - 1, b0, kBcUnits * m0, ck, w, l);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     float dh[2], dc[2];
@@ -532,6 +636,29 @@ __global__ __launch_bounds__(512) void lstm_bwd_recurrence_cl(BwdArgs a, BwdClAr
         const int R = nrow0 + 2 * kh + rr, uu = 16 * utl + l % 16;
         float r_go[4], r_ct, r_pc, r_gd;
         uint8_t r_hid, r_tanh, r_cell, r_gm[4], r_gin[4], r_ih[4], r_hh[4];
+        if constexpr (CK) {
+          // codes: block utl of the member, e = l % 16
+          const unsigned char *bk = ck + utl * kLckBlock;
+          const int e = l % 16;
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            r_go[g] = static_cast<float>(
+                reinterpret_cast<const uint16_t *>(bk)[(R * 4 + g) * 16 + e] + a.lo_gout[g]);
+            const uint8_t m = bk[kLckGm + (g * 16 + R) * 16 + e];
+            r_hh[g] = m & 1;
+            r_gin[g] = (m >> 1) & 1;
+            r_gm[g] = (m >> 2) & 1;
+            r_ih[g] = ck[kCkcIh + (R * 4 + g) * 64 + uu];
+          }
+          r_ct = static_cast<float>(reinterpret_cast<const uint16_t *>(bk + kLckTanh)[R * 16 + e] + a.lo_t);
+          r_pc = static_cast<float>(
+              reinterpret_cast<const uint16_t *>(ck + kCkcCell + utl * 2 * kLcellBlock)[R * 16 + e] + a.lo_c);
+          r_gd = ckf[kCkcGrad / 4 + R * 64 + uu];
+          const uint8_t m = bk[kLckCm + R * 16 + e];
+          r_cell = m & 1;
+          r_tanh = (m >> 1) & 1;
+          r_hid = (m >> 2) & 1;
+        } else {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           r_go[g] = ckf[(R * 4 + g) * 64 + uu];
@@ -546,6 +673,7 @@ __global__ __launch_bounds__(512) void lstm_bwd_recurrence_cl(BwdArgs a, BwdClAr
         r_hid = ck[kCkBitOff + (0 * 16 + R) * 64 + uu];
         r_tanh = ck[kCkBitOff + (1 * 16 + R) * 64 + uu];
         r_cell = ck[kCkBitOff + (2 * 16 + R) * 64 + uu];
+        }
         const auto kp = [](uint8_t m) { return m == 0 ? 1.0f : 0.0f; };
         const float ig = deq(r_go[0], a.s_gout[0], a.zp_gout[0]);
         const float fg = deq(r_go[1], a.s_gout[1], a.zp_gout[1]);
@@ -642,7 +770,12 @@ __global__ __launch_bounds__(512) void lstm_bwd_recurrence_cl(BwdArgs a, BwdClAr
       ++epoch;
       // the next step's checkpoint block (the block of this step was read before the exponent
       // barriers above); complete before the partial-sum barrier below
-      if (t > 0) ck_issue(a, t - 1, b0, kBcUnits * m0, ck, w, l);
+      if (t > 0) {
+        if constexpr (CK)
+          ck_issue_codes(a, t - 1, tile, b0, kBcUnits * m0, ck, w, l);
+        else
+          ck_issue(a, t - 1, b0, kBcUnits * m0, ck, w, l);
+      }
       {
         const size_t tb = static_cast<size_t>(t) * BC;
         const int u0 = kBcUnits * m0;
@@ -833,13 +966,13 @@ int64_t rxmet_lstm_backward_workspace_bytes(int32_t T, int32_t B, int32_t I, int
   return static_cast<int64_t>(BwdWorkspace(T, B, I, H).total);
 }
 
-int rxmet_lstm_backward_quant(int32_t T, int32_t B, int32_t I, int32_t H,
+static int lstm_backward_impl(int32_t T, int32_t B, int32_t I, int32_t H,
                               const rxmet_lstm_params *params, const rxmet_lstm_saved *saved,
+                              const rxmet_lstm_saved_codes *codes,
                               const float *grad_output, const float *grad_h_n,
                               const float *grad_c_n, float *dx, float *dW_ih, float *dW_hh,
                               float *db_ih, float *db_hh, float *dh0, float *dc0,
                               void *workspace, void *stream_) {
-  clear_error();
   RXMET_CHECK_ARG(T >= 1 && B >= 1 && I >= 1 && H >= 1, "dimensions must be positive");
   RXMET_CHECK_ARG(H % 16 == 0, "hidden_size must be a multiple of 16");
   RXMET_CHECK_ARG(params && saved && grad_output && dx && dW_ih && dW_hh && dh0 && dc0 && workspace,
@@ -848,11 +981,18 @@ int rxmet_lstm_backward_quant(int32_t T, int32_t B, int32_t I, int32_t H,
   const bool bias = params->bias_enabled != 0;
   RXMET_CHECK_ARG(!bias || (db_ih && db_hh), "bias gradients requested but pointers are null");
   const rxmet_lstm_saved &sv = *saved;
-  RXMET_CHECK_ARG(sv.x_q && sv.w_ih_q && sv.w_hh_q && sv.h0_q && sv.c0_q && sv.x_m && sv.w_ih_m &&
-                      sv.w_hh_m && sv.h0_m && sv.c0_m && sv.gate_out && sv.cell && sv.cell_tanh &&
-                      sv.hidden && sv.ih_linear_m && sv.hh_linear_m && sv.gate_in_m &&
-                      sv.gate_out_m && sv.cell_m && sv.cell_tanh_m && sv.hidden_m,
-                  "backward needs every saved tensor");
+  if (codes)
+    RXMET_CHECK_ARG(sv.x_q && sv.w_ih_q && sv.w_hh_q && sv.h0_q && sv.c0_q && sv.x_m &&
+                        sv.w_ih_m && sv.w_hh_m && sv.h0_m && sv.c0_m && sv.hidden &&
+                        sv.ih_linear_m && codes->blocks && codes->cell_codes,
+                    "backward needs the masters, hidden, ih_linear_m and the saved codes");
+  else
+    RXMET_CHECK_ARG(sv.x_q && sv.w_ih_q && sv.w_hh_q && sv.h0_q && sv.c0_q && sv.x_m &&
+                        sv.w_ih_m && sv.w_hh_m && sv.h0_m && sv.c0_m && sv.gate_out && sv.cell &&
+                        sv.cell_tanh && sv.hidden && sv.ih_linear_m && sv.hh_linear_m &&
+                        sv.gate_in_m && sv.gate_out_m && sv.cell_m && sv.cell_tanh_m &&
+                        sv.hidden_m,
+                    "backward needs every saved tensor");
   RXMET_CHECK_ARG(!bias || (sv.b_ih_m && sv.b_hh_m), "backward with bias needs the bias masks");
   const Grid gwh_b = grid_of(params->config.op[RXMET_LSTM_W_HH], 1.0f, 0);
   RXMET_CHECK_ARG(gwh_b.lo >= -32768 && gwh_b.hi <= 32767, "W_hh codes must fit signed 16 bits");
@@ -927,6 +1067,16 @@ int rxmet_lstm_backward_quant(int32_t T, int32_t B, int32_t I, int32_t H,
   }
   ba.s_c = sp.c.dscale; ba.zp_c = sp.c.dzp; ba.s_t = sp.tanh_c.dscale; ba.zp_t = sp.tanh_c.dzp;
   ba.dli = dli; ba.dlh = dlh; ba.dh0 = dh0; ba.dc0 = dc0;
+  ba.ckb = nullptr; ba.cellc = nullptr;
+  if (codes) {
+    ba.gate_out = ba.cell = ba.cell_tanh = nullptr;
+    ba.hh_m = ba.gin_m = ba.gout_m = ba.cell_m = ba.tanh_m = ba.hid_m = nullptr;
+    ba.ckb = codes->blocks;
+    ba.cellc = codes->cell_codes;
+    for (int g = 0; g < 4; ++g) ba.lo_gout[g] = sp.gout[g].lo;
+    ba.lo_c = sp.c.lo;
+    ba.lo_t = sp.tanh_c.lo;
+  }
   bool recurrence_done = false;  // set by the stepped or the clustered recurrence
   int *timeout_flag = nullptr;
   if (stepped) {
@@ -965,14 +1115,17 @@ int rxmet_lstm_backward_quant(int32_t T, int32_t B, int32_t I, int32_t H,
   // (the exchange buffer, 6 Bpad C bytes, is addressed with 32-bit buffer offsets; checkpoint
   // rows are copied into LDS as 16-byte chunks)
   const auto a16 = [](const void *p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
-  const bool ck_aligned = a16(sv.gate_out) && a16(sv.cell) && a16(sv.cell_tanh) && a16(sv.c0_q) &&
-                          a16(grad_output) && a16(sv.ih_linear_m) && a16(sv.hh_linear_m) &&
-                          a16(sv.gate_in_m) && a16(sv.gate_out_m) && a16(sv.cell_m) &&
-                          a16(sv.cell_tanh_m) && a16(sv.hidden_m);
+  const bool ck_aligned =
+      codes ? a16(codes->blocks) && a16(codes->cell_codes) && a16(grad_output) && a16(sv.ih_linear_m)
+            : a16(sv.gate_out) && a16(sv.cell) && a16(sv.cell_tanh) && a16(sv.c0_q) &&
+                  a16(grad_output) && a16(sv.ih_linear_m) && a16(sv.hh_linear_m) &&
+                  a16(sv.gate_in_m) && a16(sv.gate_out_m) && a16(sv.cell_m) &&
+                  a16(sv.cell_tanh_m) && a16(sv.hidden_m);
   if (!stepped && H % (2 * kBcUnits) == 0 && KS2 <= 8 * kBcMaxKs && ck_aligned &&
       6.0 * ((B + kBB - 1) / kBB * kBB) * C < 2147483648.0 &&
       std::getenv("RXMET_NO_CLUSTER") == nullptr) {
-    const void *fn = reinterpret_cast<const void *>(&lstm_bwd_recurrence_cl);
+    const void *fn = codes ? reinterpret_cast<const void *>(&lstm_bwd_recurrence_cl<true>)
+                           : reinterpret_cast<const void *>(&lstm_bwd_recurrence_cl<false>);
     const size_t lds_cl = bwd_cl_lds();
     int device = 0, ncu = 0, per_cu = 0;
     RXMET_CHECK_HIP(hipGetDevice(&device));
@@ -1080,6 +1233,30 @@ int rxmet_lstm_backward_quant(int32_t T, int32_t B, int32_t I, int32_t H,
     RXMET_CHECK_LAUNCH();
   }
   return 0;
+}
+
+int rxmet_lstm_backward_quant(int32_t T, int32_t B, int32_t I, int32_t H,
+                              const rxmet_lstm_params *params, const rxmet_lstm_saved *saved,
+                              const float *grad_output, const float *grad_h_n,
+                              const float *grad_c_n, float *dx, float *dW_ih, float *dW_hh,
+                              float *db_ih, float *db_hh, float *dh0, float *dc0,
+                              void *workspace, void *stream_) {
+  clear_error();
+  return lstm_backward_impl(T, B, I, H, params, saved, nullptr, grad_output, grad_h_n, grad_c_n,
+                            dx, dW_ih, dW_hh, db_ih, db_hh, dh0, dc0, workspace, stream_);
+}
+
+int rxmet_lstm_backward_quant_codes(int32_t T, int32_t B, int32_t I, int32_t H,
+                                    const rxmet_lstm_params *params, const rxmet_lstm_saved *saved,
+                                    const rxmet_lstm_saved_codes *codes,
+                                    const float *grad_output, const float *grad_h_n,
+                                    const float *grad_c_n, float *dx, float *dW_ih, float *dW_hh,
+                                    float *db_ih, float *db_hh, float *dh0, float *dc0,
+                                    void *workspace, void *stream_) {
+  clear_error();
+  RXMET_CHECK_ARG(codes != nullptr, "codes must be non-null");
+  return lstm_backward_impl(T, B, I, H, params, saved, codes, grad_output, grad_h_n, grad_c_n,
+                            dx, dW_ih, dW_hh, db_ih, db_hh, dh0, dc0, workspace, stream_);
 }
 
 }  // extern "C"

@@ -353,8 +353,40 @@ struct RecArgs {
   // checkpoints (null in inference)
   float *gate_out, *cell, *cell_tanh, *hidden;
   uint8_t *hh_lin_m, *gate_in_m, *gate_out_m, *cell_m, *cell_tanh_m, *hidden_m;
+  // saved state as codes (training; instead of gate_out, cell, cell_tanh and the six masks
+  // above): the blocks and the cell codes of lck_block
+  uint8_t *ckb;
+  uint16_t *cellc;
   int wide_out;  // clustered path: outputs 16-byte aligned, stored as 16-byte rows through LDS
 };
+
+// A saved code as its offset from the grid's minimum (grids of at most 16 bits).
+__device__ __forceinline__ uint32_t lck_u16(float code, int32_t lo) {
+  return static_cast<uint32_t>(static_cast<int32_t>(code) - lo) & 0xFFFFu;
+}
+
+// One gate output of (step t, sequence b, unit j) and its three gate masks into its block.
+__device__ __forceinline__ void lck_store_gate(const RecArgs &a, int t, int b, int j, int g,
+                                               float go, int32_t lo, uint32_t bits) {
+  uint8_t *blk = a.ckb + static_cast<size_t>(lck_block(t, b, j, a.B, a.H)) * kLckBlock;
+  const int R = b % 16, e = j % 16;
+  reinterpret_cast<uint16_t *>(blk)[(R * 4 + g) * 16 + e] = static_cast<uint16_t>(lck_u16(go, lo));
+  blk[kLckGm + (g * 16 + R) * 16 + e] = static_cast<uint8_t>(bits);
+}
+
+// The cell-phase codes of (step t, sequence b, unit j): tanh(c) and the three masks into the
+// step's block, the cell into the cell codes at step t + 1.
+__device__ __forceinline__ void lck_store_cell(const RecArgs &a, const StepParams &sp, int t, int b,
+                                               int j, float cn, float ct, uint32_t bits) {
+  const uint32_t k = lck_block(t, b, j, a.B, a.H);
+  uint8_t *blk = a.ckb + static_cast<size_t>(k) * kLckBlock;
+  const int R = b % 16, e = j % 16;
+  reinterpret_cast<uint16_t *>(blk + kLckTanh)[R * 16 + e] =
+      static_cast<uint16_t>(lck_u16(ct, sp.tanh_c.lo));
+  blk[kLckCm + R * 16 + e] = static_cast<uint8_t>(bits);
+  a.cellc[static_cast<size_t>(lck_block(t + 1, b, j, a.B, a.H)) * kLcellBlock + R * 16 + e] =
+      static_cast<uint16_t>(lck_u16(cn, sp.c.lo));
+}
 
 // One (sequence, unit) step of the q-carrier (forward_quantized_fp_cpu.cc:18-44, 116-190): per
 // gate the recurrent linear from its exact centred sum plus the rescaled bias (accf), its
@@ -400,7 +432,14 @@ __device__ __forceinline__ void lstm_store(const RecArgs &a, const StepParams &s
   const uint32_t row = static_cast<uint32_t>(t) * a.B + b;
   const uint32_t oh = row * H + j;
   a.output[oh] = dequant(o.hv, sp.h.scale, sp.h.zp);
-  if (a.hidden != nullptr) {
+  if (a.hidden != nullptr && a.ckb != nullptr) {
+    a.hidden[oh] = o.hv;
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      lck_store_gate(a, t, b, j, g, o.gout[g], sp.gout[g].lo,
+                     o.m_hl[g] | (o.m_gi[g] << 1) | (o.m_go[g] << 2));
+    lck_store_cell(a, sp, t, b, j, o.cn, o.ct, o.m_c | (o.m_t << 1) | (o.m_h << 2));
+  } else if (a.hidden != nullptr) {
     a.cell[oh] = o.cn;
     a.cell_tanh[oh] = o.ct;
     a.hidden[oh] = o.hv;
@@ -740,10 +779,82 @@ __device__ __forceinline__ void flush_step(const RecArgs &a, const StepParams &s
   }
 }
 
+// Two codes as one word: code - lo of each, low half first.
+__device__ __forceinline__ uint32_t lck_pair(float a, float b, int32_t lo) {
+  return lck_u16(a, lo) | (lck_u16(b, lo) << 16);
+}
+
+// flush_step for the saved codes: the member's four blocks of the step (one contiguous run)
+// and its four cell-code blocks of step t + 1, besides the output and the hidden codes.
+__device__ __forceinline__ void flush_step_codes(const RecArgs &a, const StepParams &sp, int t,
+                                                 int tile, int b0, int u0, float *xg,
+                                                 const uint8_t *gm, const uint8_t *cm,
+                                                 const float (&hvs)[2], const float (&cst)[2],
+                                                 const float (&cts)[2], int srow, int su) {
+  const int H = a.H, B = a.B, tid = threadIdx.x, nthr = blockDim.x;
+  const size_t nt = static_cast<size_t>(B + 15) / 16;
+  uint8_t *blk = a.ckb + ((static_cast<size_t>(t) * nt + tile) * (H / 16) + u0 / 16) * kLckBlock;
+  uint16_t *cel = a.cellc + ((static_cast<size_t>(t + 1) * nt + tile) * (H / 16) + u0 / 16) * kLcellBlock;
+  // gate codes [ut][16 rows][4 gates][16 units] from xg [(ut * 4 + g) * 16 + row][16], four
+  // codes (8 bytes) per store
+  for (int c = tid; c < 1024; c += nthr) {
+    const int ut = c >> 8, R = (c >> 4) & 15, g = (c >> 2) & 3, qq = c & 3;
+    // selected, not indexed: a kernel-argument array indexed at run time goes through scratch
+    const int32_t lo = g == 0 ? sp.gout[0].lo : g == 1 ? sp.gout[1].lo : g == 2 ? sp.gout[2].lo
+                                                                            : sp.gout[3].lo;
+    const float4 v = *reinterpret_cast<const float4 *>(xg + ((ut * 4 + g) * 16 + R) * 16 + 4 * qq);
+    *reinterpret_cast<uint2 *>(blk + ut * kLckBlock + ((R * 4 + g) * 16 + 4 * qq) * 2) =
+        make_uint2(lck_pair(v.x, v.y, lo), lck_pair(v.z, v.w, lo));
+  }
+  // gate masks [ut][4 gates][16 rows][16 units], cell-phase masks [ut][16 rows][16 units]
+  for (int c = (tid + nthr - 1024 % nthr) % nthr; c < 256 + 64; c += nthr) {
+    if (c < 256) {
+      const int ut = c >> 6, g = (c >> 4) & 3, R = c & 15;
+      *reinterpret_cast<uint4 *>(blk + ut * kLckBlock + kLckGm + (g * 16 + R) * 16) =
+          *reinterpret_cast<const uint4 *>(gm + (g * 16 + R) * kClUnits + 16 * ut);
+    } else {
+      const int ut = (c - 256) >> 4, R = (c - 256) & 15;
+      *reinterpret_cast<uint4 *>(blk + ut * kLckBlock + kLckCm + R * 16) =
+          *reinterpret_cast<const uint4 *>(cm + R * kClUnits + 16 * ut);
+    }
+  }
+  __syncthreads();  // every read of xg is done
+#pragma unroll
+  for (int rr = 0; rr < 2; ++rr) {
+    float *d = xg + (srow + rr) * kClUnits + su;
+    d[0] = hvs[rr];
+    d[16 * kClUnits] = cst[rr];
+    d[32 * kClUnits] = cts[rr];
+  }
+  __syncthreads();
+  flush_rows(a.output, xg, t, b0, B, H, u0, tid, nthr, true, sp.h.scale, sp.h.zp);
+  flush_rows(a.hidden, xg, t, b0, B, H, u0, (tid + nthr - 256 % nthr) % nthr, nthr, false, 0.f, 0);
+  // tanh(c) codes into the blocks, the cell codes into step t + 1's cell blocks
+  for (int c = tid; c < 512; c += nthr) {
+    const int k = c >> 8, ut = (c >> 6) & 3, R = (c >> 2) & 15, qq = c & 3;
+    const float4 v = *reinterpret_cast<const float4 *>(xg + (k == 0 ? 32 : 16) * kClUnits +
+                                                       R * kClUnits + 16 * ut + 4 * qq);
+    const int32_t lo = k == 0 ? sp.tanh_c.lo : sp.c.lo;
+    uint2 *dst = k == 0 ? reinterpret_cast<uint2 *>(blk + ut * kLckBlock + kLckTanh + (R * 16 + 4 * qq) * 2)
+                        : reinterpret_cast<uint2 *>(cel + ut * kLcellBlock + R * 16 + 4 * qq);
+    *dst = make_uint2(lck_pair(v.x, v.y, lo), lck_pair(v.z, v.w, lo));
+  }
+}
+
+// The cell codes of c0 (step 0 of the cell-code array) from the c0 codes [B, H].
+__global__ __launch_bounds__(256) void lstm_c0_codes(int B, int H, const float *__restrict__ c0q,
+                                                     int32_t c_lo, uint16_t *__restrict__ cellc) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= static_cast<int64_t>(B) * H) return;
+  const int b = static_cast<int>(i / H), j = static_cast<int>(i % H);
+  cellc[static_cast<size_t>(lck_block(0, b, j, B, H)) * kLcellBlock + (b % 16) * 16 + j % 16] =
+      static_cast<uint16_t>(lck_u16(c0q[i], c_lo));
+}
+
 // PW = 2: W_hh of up to 16 bits as two int8 planes, W = 256 bh + bl + 128 (lstm_pack_whh), so
 // sum_k W y = 256 sum bh y + sum bl y + 128 sum_k y for each h plane y; the row sums sum_k y come
 // from one more MFMA against a fragment of ones, and the planes are recombined in int64.
-template <int NPL, int PW, bool EXC>
+template <int NPL, int PW, bool EXC, bool CK>
 __global__ __launch_bounds__(512) void lstm_recurrence_cl(RecArgs a, StepParams sp,
                                                           ClusterArgs cl) {
   extern __shared__ __align__(16) unsigned char smem[];
@@ -956,7 +1067,8 @@ __global__ __launch_bounds__(512) void lstm_recurrence_cl(RecArgs a, StepParams 
                                       static_cast<int>(gi) - gin.lo, gout.lo, m_go)
                            : real_act<EXC>(gi, gin, gout, g == 2, sp, g, m_go));
             xg[((ut * 4 + g) * 16 + nr) * 16 + l % 16] = go;
-            if (a.wide_out) {
+            // (the codes kernel always stages: the launcher runs it only with wide_out set)
+            if (CK || a.wide_out) {
               if (train)
                 gm[(g * 16 + nr) * kClUnits + 16 * ut + l % 16] =
                     static_cast<uint8_t>(m_hl | (m_gi << 1) | (m_go << 2));
@@ -997,7 +1109,7 @@ __global__ __launch_bounds__(512) void lstm_recurrence_cl(RecArgs a, StepParams 
                                   : real_act<EXC>(cn, sp.c, sp.tanh_c, true, sp, 4, mts[rr]));
         const float raw = center_f(gout[3], sp.gout[3].zp) * center_f(cts[rr], sp.tanh_c.zp);
         hvs[rr] = clamp_grid_f(rescale(raw, sp.hidden.mult, sp.hidden.shift), sp.h, mhs[rr]);
-        if (a.wide_out && train)
+        if ((CK || a.wide_out) && train)
           cm[nr * kClUnits + 16 * ut + l % 16] =
               static_cast<uint8_t>(mcs[rr] | (mts[rr] << 1) | (mhs[rr] << 2));
         const int hc = static_cast<int>(hvs[rr] - a.h_offset);
@@ -1010,8 +1122,13 @@ __global__ __launch_bounds__(512) void lstm_recurrence_cl(RecArgs a, StepParams 
       // the other members only read the h codes: arrive, then store outputs while waiting
       cluster::arrive(counter);
       ++epoch;
-      if (a.wide_out) {
-        flush_step(a, sp, t, b0, u0, train, xg, gm, cm, hvs, cst, cts, nrow0 + 2 * gp, 16 * ut + l % 16);
+      if (CK || a.wide_out) {
+        if constexpr (CK)
+          flush_step_codes(a, sp, t, tile, b0, u0, xg, gm, cm, hvs, cst, cts, nrow0 + 2 * gp,
+                           16 * ut + l % 16);
+        else
+          flush_step(a, sp, t, b0, u0, train, xg, gm, cm, hvs, cst, cts, nrow0 + 2 * gp,
+                     16 * ut + l % 16);
         if (t == a.T - 1) {
 #pragma unroll
           for (int rr = 0; rr < 2; ++rr) {
@@ -1129,13 +1246,12 @@ int64_t rxmet_lstm_forward_workspace_bytes(int32_t T, int32_t B, int32_t I, int3
   return static_cast<int64_t>(FwdWorkspace(T, B, I, H).total);
 }
 
-int rxmet_lstm_forward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const float *W_ih,
+static int lstm_forward_impl(int32_t T, int32_t B, int32_t I, int32_t H, const float *W_ih,
                              const float *W_hh, const float *b_ih, const float *b_hh,
                              const float *x, const float *h0, const float *c0,
                              const rxmet_lstm_params *params, float *output, float *h_n,
-                             float *c_n, const rxmet_lstm_saved *saved, void *workspace,
-                             void *stream_) {
-  clear_error();
+                             float *c_n, const rxmet_lstm_saved *saved,
+                             const rxmet_lstm_saved_codes *codes, void *workspace, void *stream_) {
   RXMET_CHECK_ARG(T >= 1 && B >= 1 && I >= 1 && H >= 1, "dimensions must be positive");
   RXMET_CHECK_ARG(H % 16 == 0, "hidden_size must be a multiple of 16");
   RXMET_CHECK_ARG(W_ih && W_hh && x && params && output && h_n && c_n && workspace,
@@ -1148,7 +1264,16 @@ int rxmet_lstm_forward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const f
   RXMET_CHECK_ARG(h_t.bits <= 16, "output (h) wider than 16 bits is not supported");
   RXMET_CHECK_ARG(static_cast<double>(T) * B * 4 * H < 4294967295.0,
                   "T*B*4H too large for 32-bit element offsets");
-  if (saved) {
+  if (saved && codes) {
+    RXMET_CHECK_ARG(saved->x_q && saved->w_ih_q && saved->w_hh_q && saved->h0_q && saved->c0_q &&
+                        saved->x_m && saved->w_ih_m && saved->w_hh_m && saved->h0_m &&
+                        saved->c0_m && saved->hidden && saved->ih_linear_m && codes->blocks &&
+                        codes->cell_codes,
+                    "training forward needs the masters, hidden, ih_linear_m and the codes");
+    auto a16 = [](const void *q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; };
+    RXMET_CHECK_ARG(a16(codes->blocks) && a16(codes->cell_codes),
+                    "the saved codes must be 16-byte aligned");
+  } else if (saved) {
     RXMET_CHECK_ARG(saved->x_q && saved->w_ih_q && saved->w_hh_q && saved->h0_q && saved->c0_q &&
                         saved->x_m && saved->w_ih_m && saved->w_hh_m && saved->h0_m &&
                         saved->c0_m && saved->gate_out && saved->cell && saved->cell_tanh &&
@@ -1162,6 +1287,11 @@ int rxmet_lstm_forward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const f
   StepParams sp;
   ChannelParams cp;
   if (int rc = derive(*params, &sp, &cp)) return rc;
+  if (saved && codes) {
+    bool fit = sp.c.hi - sp.c.lo <= 65535 && sp.tanh_c.hi - sp.tanh_c.lo <= 65535;
+    for (int g = 0; g < 4; ++g) fit = fit && sp.gout[g].hi - sp.gout[g].lo <= 65535;
+    RXMET_CHECK_ARG(fit, "saved codes need gate-output, cell and tanh grids of at most 16 bits");
+  }
   const int C = 4 * H, KS = (H + 63) / 64, UT = H / 16;
   // the input branch is an exact byte-plane GEMM; the recurrent MFMA sum must fit int32
   RXMET_CHECK_ARG(I < (1 << 17), "input_size must be below 131072 for the exact input GEMM");
@@ -1318,10 +1448,23 @@ int rxmet_lstm_forward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const f
   ra.gate_out = sv.gate_out; ra.cell = sv.cell; ra.cell_tanh = sv.cell_tanh; ra.hidden = sv.hidden;
   ra.hh_lin_m = sv.hh_linear_m; ra.gate_in_m = sv.gate_in_m; ra.gate_out_m = sv.gate_out_m;
   ra.cell_m = sv.cell_m; ra.cell_tanh_m = sv.cell_tanh_m; ra.hidden_m = sv.hidden_m;
+  ra.ckb = nullptr; ra.cellc = nullptr;
+  if (saved && codes) {
+    ra.gate_out = ra.cell = ra.cell_tanh = nullptr;
+    ra.hh_lin_m = ra.gate_in_m = ra.gate_out_m = ra.cell_m = ra.cell_tanh_m = ra.hidden_m = nullptr;
+    ra.ckb = codes->blocks;
+    ra.cellc = codes->cell_codes;
+    const int64_t n = static_cast<int64_t>(B) * H;
+    hipLaunchKernelGGL(lstm_c0_codes, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
+                       stream, B, H, c0q, sp.c.lo, ra.cellc);
+    RXMET_CHECK_LAUNCH();
+  }
   {
     auto a16 = [](const void *q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; };
     bool wide = H % 16 == 0 && a16(ra.output);
-    if (ra.hidden != nullptr)
+    if (ra.ckb != nullptr)
+      wide = wide && a16(ra.hidden);
+    else if (ra.hidden != nullptr)
       wide = wide && a16(ra.gate_out) && a16(ra.cell) && a16(ra.cell_tanh) && a16(ra.hidden) &&
              a16(ra.hh_lin_m) && a16(ra.gate_in_m) && a16(ra.gate_out_m) && a16(ra.cell_m) &&
              a16(ra.cell_tanh_m) && a16(ra.hidden_m);
@@ -1367,16 +1510,16 @@ int rxmet_lstm_forward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const f
   if (may_cluster) {
     // clustered path when the whole grid can be resident at once
     const bool has_exc = !exc.key.empty();
-    const void *fns[2][2][2] = {
-        {{reinterpret_cast<const void *>(&lstm_recurrence_cl<1, 1, false>),
-          reinterpret_cast<const void *>(&lstm_recurrence_cl<1, 1, true>)},
-         {reinterpret_cast<const void *>(&lstm_recurrence_cl<1, 2, false>),
-          reinterpret_cast<const void *>(&lstm_recurrence_cl<1, 2, true>)}},
-        {{reinterpret_cast<const void *>(&lstm_recurrence_cl<2, 1, false>),
-          reinterpret_cast<const void *>(&lstm_recurrence_cl<2, 1, true>)},
-         {reinterpret_cast<const void *>(&lstm_recurrence_cl<2, 2, false>),
-          reinterpret_cast<const void *>(&lstm_recurrence_cl<2, 2, true>)}}};
-    const void *fn = fns[npl - 1][pw - 1][has_exc ? 1 : 0];
+#define RXMET_LSTM_CL(N, P, E)                                                         \
+  {reinterpret_cast<const void *>(&lstm_recurrence_cl<N, P, E, false>),              \
+   reinterpret_cast<const void *>(&lstm_recurrence_cl<N, P, E, true>)}
+    const void *fns[2][2][2][2] = {
+        {{RXMET_LSTM_CL(1, 1, false), RXMET_LSTM_CL(1, 1, true)},
+         {RXMET_LSTM_CL(1, 2, false), RXMET_LSTM_CL(1, 2, true)}},
+        {{RXMET_LSTM_CL(2, 1, false), RXMET_LSTM_CL(2, 1, true)},
+         {RXMET_LSTM_CL(2, 2, false), RXMET_LSTM_CL(2, 2, true)}}};
+#undef RXMET_LSTM_CL
+    const void *fn = fns[npl - 1][pw - 1][has_exc ? 1 : 0][ra.ckb != nullptr ? 1 : 0];
     ActLut lut{};
     uint32_t *lut_table = reinterpret_cast<uint32_t *>(wsb + ws.lut);
     int dev_lds = 0;
@@ -1444,7 +1587,8 @@ int rxmet_lstm_forward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const f
     if (ncl > cl.ntiles) ncl = cl.ntiles;
     if (ncl >= 8) ncl -= ncl % 8;
     // (the exchange buffer, 2 npl planes of Bpad H bytes, is addressed with 32-bit offsets)
-    if (ncl >= 1 && 4.0 * cl.Bpad * H < 2147483648.0 && std::getenv("RXMET_NO_CLUSTER") == nullptr) {
+    if (ncl >= 1 && 4.0 * cl.Bpad * H < 2147483648.0 && std::getenv("RXMET_NO_CLUSTER") == nullptr &&
+        (ra.ckb == nullptr || ra.wide_out)) {
       cl.ncl = ncl;
       cl.hx = reinterpret_cast<int8_t *>(wsb + ws.hx);
       cl.counters = reinterpret_cast<unsigned *>(wsb + ws.sync);
@@ -1516,6 +1660,30 @@ int rxmet_lstm_forward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const f
   }
   RXMET_CHECK_LAUNCH();
   return 0;
+}
+
+int rxmet_lstm_forward_quant(int32_t T, int32_t B, int32_t I, int32_t H, const float *W_ih,
+                             const float *W_hh, const float *b_ih, const float *b_hh,
+                             const float *x, const float *h0, const float *c0,
+                             const rxmet_lstm_params *params, float *output, float *h_n,
+                             float *c_n, const rxmet_lstm_saved *saved, void *workspace,
+                             void *stream_) {
+  clear_error();
+  return lstm_forward_impl(T, B, I, H, W_ih, W_hh, b_ih, b_hh, x, h0, c0, params, output, h_n,
+                           c_n, saved, nullptr, workspace, stream_);
+}
+
+int rxmet_lstm_forward_quant_codes(int32_t T, int32_t B, int32_t I, int32_t H, const float *W_ih,
+                                   const float *W_hh, const float *b_ih, const float *b_hh,
+                                   const float *x, const float *h0, const float *c0,
+                                   const rxmet_lstm_params *params, float *output, float *h_n,
+                                   float *c_n, const rxmet_lstm_saved *saved,
+                                   const rxmet_lstm_saved_codes *codes, void *workspace,
+                                   void *stream_) {
+  clear_error();
+  RXMET_CHECK_ARG(saved == nullptr || codes != nullptr, "codes must be non-null with saved");
+  return lstm_forward_impl(T, B, I, H, W_ih, W_hh, b_ih, b_hh, x, h0, c0, params, output, h_n,
+                           c_n, saved, saved ? codes : nullptr, workspace, stream_);
 }
 
 }  // extern "C"

@@ -72,5 +72,24 @@ ActExceptions act_exceptions(const StepParams &sp);
 // core's arithmetic (reference = true) or the kernels' double evaluation.
 uint32_t act_entry(const StepParams &sp, int k, int32_t q, bool reference);
 
+// Saved state as codes (the module path's training forward, rxmet_lstm_saved_codes): per
+// (step t, 16-sequence tile, 16-unit tile) one block of kLckBlock bytes at index
+// lck_block(t, b, j): the four gate outputs as code - grid minimum, u16 [16 rows][4 gates][16
+// units]; the gate masks (bit 0 hh linear, bit 1 gate input, bit 2 gate output, 1 = clamped),
+// u8 [4 gates][16 rows][16 units] at kLckGm; tanh(c) as code - minimum, u16 [16][16] at
+// kLckTanh; the cell-phase masks (bit 0 cell, bit 1 tanh, bit 2 hidden), u8 [16][16] at kLckCm.
+// The cell codes (code - minimum, u16 [16][16], kLcellBlock per block) are a second array of
+// T + 1 steps: step 0 holds c0, step t + 1 the cell after step t.  A recurrence member's 64
+// units are four consecutive blocks.
+constexpr int kLckBlock = 3840, kLckGm = 2048, kLckTanh = 3072, kLckCm = 3584, kLcellBlock = 256;
+
+#if defined(__HIP__)
+__host__ __device__ inline uint32_t lck_block(int t, int b, int j, int B, int H) {
+  const uint32_t nt = static_cast<uint32_t>(B + 15) / 16;
+  return (static_cast<uint32_t>(t) * nt + static_cast<uint32_t>(b) / 16) *
+             (static_cast<uint32_t>(H) / 16) + static_cast<uint32_t>(j) / 16;
+}
+#endif
+
 }  // namespace lstm
 }  // namespace rxmet

@@ -164,7 +164,14 @@ def forward_float(x, W_ih, W_hh, b_ih, b_hh, h0, c0):
     return out, hn, cn
 
 
-def _saved_tensors(T, B, I, H, bias, dev) -> dict:
+# the saved-codes form's entries (rxmet_lstm_saved_codes) and the reference-format entries they
+# replace
+CODE_KEYS = ("codes_blocks", "cell_codes")
+CODED_FIELDS = ("gate_out", "cell", "cell_tanh", "hh_linear_m", "gate_in_m", "gate_out_m",
+                "cell_m", "cell_tanh_m", "hidden_m")
+
+
+def _saved_tensors(T, B, I, H, bias, dev, codes=False) -> dict:
     C = 4 * H
     f = dict(dtype=_F32, device=dev)
     u = dict(dtype=torch.uint8, device=dev)
@@ -173,12 +180,18 @@ def _saved_tensors(T, B, I, H, bias, dev) -> dict:
          "c0_q": torch.empty((B, H), **f), "x_m": torch.empty((T, B, I), **u),
          "w_ih_m": torch.empty((C, I), **u), "w_hh_m": torch.empty((C, H), **u),
          "h0_m": torch.empty((B, H), **u), "c0_m": torch.empty((B, H), **u),
-         "gate_out": torch.empty((T, B, C), **f), "cell": torch.empty((T, B, H), **f),
-         "cell_tanh": torch.empty((T, B, H), **f), "hidden": torch.empty((T, B, H), **f)}
-    for k in ("ih_linear_m", "hh_linear_m", "gate_in_m", "gate_out_m"):
-        s[k] = torch.empty((T, B, C), **u)
-    for k in ("cell_m", "cell_tanh_m", "hidden_m"):
-        s[k] = torch.empty((T, B, H), **u)
+         "hidden": torch.empty((T, B, H), **f), "ih_linear_m": torch.empty((T, B, C), **u)}
+    if codes:
+        nb = (B + 15) // 16 * (H // 16)
+        s["codes_blocks"] = torch.empty((T * nb * L.CODES_BLOCK,), **u)
+        s["cell_codes"] = torch.empty(((T + 1) * nb * L.CELL_BLOCK,), dtype=torch.int16, device=dev)
+    else:
+        s.update({"gate_out": torch.empty((T, B, C), **f), "cell": torch.empty((T, B, H), **f),
+                  "cell_tanh": torch.empty((T, B, H), **f)})
+        for k in ("hh_linear_m", "gate_in_m", "gate_out_m"):
+            s[k] = torch.empty((T, B, C), **u)
+        for k in ("cell_m", "cell_tanh_m", "hidden_m"):
+            s[k] = torch.empty((T, B, H), **u)
     if bias:
         s["b_ih_q"] = torch.empty((C,), **f)
         s["b_hh_q"] = torch.empty((C,), **f)
@@ -193,6 +206,58 @@ def _saved_struct(saved: dict) -> L.Saved:
         t = saved.get(k)
         setattr(s, k, None if t is None else t.data_ptr())
     return s
+
+
+def _codes_struct(saved: dict):
+    if "codes_blocks" not in saved:
+        return None
+    return L.SavedCodes(saved["codes_blocks"].data_ptr(), saved["cell_codes"].data_ptr())
+
+
+def codes_fit(params: LstmQuantParams) -> bool:
+    """The saved codes hold the gate-output, cell and tanh grids (at most 16 bits)."""
+    op = params.struct.config.op
+    return all(int(op[L.OP[n]].bits) <= 16 for n in _GATE_OUTPUTS + ("cell_state", "cell_tanh_output"))
+
+
+_GATE_OUTPUTS = ("input_gate_output", "forget_gate_output", "cell_gate_output",
+                 "output_gate_output")
+
+
+def _grid_lo(params: LstmQuantParams, name: str) -> int:
+    t = params.struct.config.op[L.OP[name]]
+    return 0 if t.is_unsigned else -(1 << (int(t.bits) - 1))
+
+
+def decode_saved_codes(saved: dict, params: LstmQuantParams, B: int) -> dict:
+    """The reference-format entries (gate_out, cell, cell_tanh as fp32 codes; the six masks as
+    uint8, 1 = clamped) of a saved-codes forward, from its blocks (rxmet_lstm_saved_codes)."""
+    T, H = saved["hidden"].shape[0], saved["hidden"].shape[2]
+    nt, nu = (B + 15) // 16, H // 16
+    blk = saved["codes_blocks"].view(T, nt, nu, L.CODES_BLOCK)
+    u16 = lambda t: t.contiguous().view(torch.int16).to(torch.int32) & 0xFFFF
+
+    def unblock(x, fields):  # [T, nt, nu, 16 r, fields, 16 e] -> [T, B, fields H]
+        y = x.reshape(T, nt, nu, 16, fields, 16).permute(0, 1, 3, 4, 2, 5)
+        return y.reshape(T, nt * 16, fields * H)[:, :B]
+
+    gates = u16(blk[..., :2048]).view(T, nt, nu, 16, 4, 16)
+    lo_g = torch.tensor([_grid_lo(params, n) for n in _GATE_OUTPUTS], dtype=torch.int32,
+                        device=gates.device).view(1, 1, 1, 1, 4, 1)
+    out = {"gate_out": unblock(gates + lo_g, 4).to(_F32)}
+    gm = blk[..., 2048:3072].reshape(T, nt, nu, 4, 16, 16).permute(0, 1, 2, 4, 3, 5)
+    for bit, k in enumerate(("hh_linear_m", "gate_in_m", "gate_out_m")):
+        out[k] = unblock((gm >> bit) & 1, 4).contiguous()
+    tanh = u16(blk[..., 3072:3584]).view(T, nt, nu, 16, 1, 16) + _grid_lo(params, "cell_tanh_output")
+    out["cell_tanh"] = unblock(tanh, 1).to(_F32)
+    cm = blk[..., 3584:].reshape(T, nt, nu, 16, 1, 16)
+    for bit, k in enumerate(("cell_m", "cell_tanh_m", "hidden_m")):
+        out[k] = unblock((cm >> bit) & 1, 1).contiguous()
+    cells = u16(saved["cell_codes"].view(T + 1, nt, nu, L.CELL_BLOCK)).view(T + 1, nt, nu, 16, 1, 16)
+    cells = cells + _grid_lo(params, "cell_state")
+    y = cells.permute(0, 1, 3, 4, 2, 5).reshape(T + 1, nt * 16, H)[:, :B]
+    out["cell"] = y[1:].to(_F32).contiguous()
+    return out
 
 
 # ---------------------------------------------------------------------------------------
@@ -290,10 +355,13 @@ def _backward_padded(saved, params, grad_output, grad_h_n, grad_c_n):
 
 
 def forward_quant(x, W_ih, W_hh, b_ih, b_hh, h0, c0, params: LstmQuantParams,
-                  save_checkpoints: bool):
+                  save_checkpoints: bool, codes: bool = False):
     """Quantised FP32-carrier forward (lstm_forward_quantized).  Returns (output, h_n, c_n,
     saved) where ``saved`` holds the masters, checkpoints and clamp masks (1 = clamped) when
-    ``save_checkpoints`` is set, else None."""
+    ``save_checkpoints`` is set, else None.  With ``codes`` the checkpoints other than hidden
+    and the recurrence masks are kept as the blocked codes of rxmet_lstm_forward_quant_codes
+    (``codes_blocks``, ``cell_codes``; decode_saved_codes restores them), for backward_quant
+    only."""
     T, B, I = x.shape
     H = W_hh.shape[1]
     if H % _UNIT_TILE:
@@ -310,13 +378,18 @@ def forward_quant(x, W_ih, W_hh, b_ih, b_hh, h0, c0, params: LstmQuantParams,
     out = torch.empty((T, B, H), dtype=_F32, device=dev)
     hn = torch.empty((B, H), dtype=_F32, device=dev)
     cn = torch.empty((B, H), dtype=_F32, device=dev)
-    saved = _saved_tensors(T, B, I, H, bias, dev) if save_checkpoints else None
+    codes = bool(codes and save_checkpoints)
+    saved = _saved_tensors(T, B, I, H, bias, dev, codes) if save_checkpoints else None
     sv = _saved_struct(saved) if saved is not None else None
     ws = _ws(_rx.load().rxmet_lstm_forward_workspace_bytes(T, B, I, H), dev)
-    _rx.call("rxmet_lstm_forward_quant", T, B, I, H, _ptr(W_ih), _ptr(W_hh), _ptr(b_ih),
-             _ptr(b_hh), _ptr(x), _ptr(h0), _ptr(c0), ctypes.byref(params.struct), _ptr(out),
-             _ptr(hn), _ptr(cn), ctypes.byref(sv) if sv is not None else None, _ptr(ws),
-             _stream(dev))
+    head = (T, B, I, H, _ptr(W_ih), _ptr(W_hh), _ptr(b_ih), _ptr(b_hh), _ptr(x), _ptr(h0),
+            _ptr(c0), ctypes.byref(params.struct), _ptr(out), _ptr(hn), _ptr(cn),
+            ctypes.byref(sv) if sv is not None else None)
+    if codes:
+        cs = _codes_struct(saved)
+        _rx.call("rxmet_lstm_forward_quant_codes", *head, ctypes.byref(cs), _ptr(ws), _stream(dev))
+    else:
+        _rx.call("rxmet_lstm_forward_quant", *head, _ptr(ws), _stream(dev))
     return out, hn, cn, saved
 
 
@@ -343,9 +416,14 @@ def backward_quant(saved: dict, params: LstmQuantParams, grad_output, grad_h_n=N
     dh0 = torch.empty((B, H), **f)
     dc0 = torch.empty((B, H), **f)
     sv = _saved_struct(saved)
+    cs = _codes_struct(saved)
     ws = _ws(_rx.load().rxmet_lstm_backward_workspace_bytes(T, B, I, H), dev)
-    _rx.call("rxmet_lstm_backward_quant", T, B, I, H, ctypes.byref(params.struct),
-             ctypes.byref(sv), _ptr(grad_output), _ptr(grad_h_n), _ptr(grad_c_n), _ptr(dx),
-             _ptr(dwi), _ptr(dwh), _ptr(dbi), _ptr(dbh), _ptr(dh0), _ptr(dc0), _ptr(ws),
-             _stream(dev))
+    tail = (_ptr(grad_output), _ptr(grad_h_n), _ptr(grad_c_n), _ptr(dx), _ptr(dwi), _ptr(dwh),
+            _ptr(dbi), _ptr(dbh), _ptr(dh0), _ptr(dc0), _ptr(ws), _stream(dev))
+    if cs is not None:
+        _rx.call("rxmet_lstm_backward_quant_codes", T, B, I, H, ctypes.byref(params.struct),
+                 ctypes.byref(sv), ctypes.byref(cs), *tail)
+    else:
+        _rx.call("rxmet_lstm_backward_quant", T, B, I, H, ctypes.byref(params.struct),
+                 ctypes.byref(sv), *tail)
     return dx, dwi, dwh, dbi, dbh, dh0, dc0

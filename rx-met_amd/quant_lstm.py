@@ -328,21 +328,32 @@ def import_operators(ops: dict, hidden: int, bias: bool, scale_mode: str):
 # autograd bridge (lstm_autograd.py:139-258)
 # ------------------------------------------------------------------------------------------
 
+# Training forwards of the module keep the checkpoints other than hidden and the recurrence
+# masks as blocked codes (lstm_ops.forward_quant(codes=True), 16-bit codes and mask bits)
+# rather than the reference's fp32 / byte format; qat_saved_state() decodes them on request and
+# the gradients are the same bit for bit.  False: the reference format throughout.
+SAVE_STATE_AS_CODES = True
+
+
 class _QuantizedLSTMFunction(torch.autograd.Function):
     """One direction, time-major.  Saves the 25 backward tensors (7 masters, 7 master masks,
-    4 checkpoints, 7 checkpoint masks) when ``save_checkpoints`` is set."""
+    4 checkpoints, 7 checkpoint masks) when ``save_checkpoints`` is set, or with the saved
+    codes the masters, hidden, the ih-linear mask and the two code arrays."""
 
     @staticmethod
     def forward(ctx, x, W_ih, W_hh, b_ih, b_hh, h0, c0, params, save_checkpoints, sink):
+        codes = bool(save_checkpoints and SAVE_STATE_AS_CODES and W_hh.shape[1] % 16 == 0
+                     and lstm_ops.codes_fit(params))
         out, hn, cn, saved = lstm_ops.forward_quant(x, W_ih, W_hh, b_ih, b_hh, h0, c0, params,
-                                                    save_checkpoints)
+                                                    save_checkpoints, codes=codes)
         ctx.has_checkpoints = saved is not None
         ctx.params = params
         ctx.has_bias = b_ih is not None
         ctx.has_state = h0 is not None
         if saved is not None:
             sink["saved"] = saved
-            ctx.names = [k for k in L.SAVED_FIELDS if saved.get(k) is not None]
+            sink["batch"] = x.shape[1]
+            ctx.names = [k for k in L.SAVED_FIELDS + lstm_ops.CODE_KEYS if saved.get(k) is not None]
             ctx.save_for_backward(*(saved[k] for k in ctx.names))
         return out, hn, cn
 
@@ -370,8 +381,11 @@ class _FloatLSTMFunction(torch.autograd.Function):
                                   "train with use_quantization=True (QAT) after calibration")
 
 
-def _qat_state(saved: dict) -> dict:
-    """The reference's qat_saved_state layout (masks as bool views of the uint8 masks)."""
+def _qat_state(saved: dict, params=None, batch: int = 0) -> dict:
+    """The reference's qat_saved_state layout (masks as bool views of the uint8 masks); saved
+    codes are decoded into it first."""
+    if "codes_blocks" in saved:
+        saved = {**saved, **lstm_ops.decode_saved_codes(saved, params, batch)}
     m = lambda k: None if saved.get(k) is None else saved[k].view(torch.bool)
     master = {"input": "x", "weight_ih": "w_ih", "weight_hh": "w_hh", "bias_ih": "b_ih",
               "bias_hh": "b_hh", "h_0": "h0", "c_0": "c0"}
@@ -657,7 +671,10 @@ class QuantLSTM(nn.Module):
         return self._directions(x, hx, run)
 
     def qat_saved_state(self):
-        return self._qat_saved_state
+        st = self._qat_saved_state
+        if callable(st):  # saved codes: decoded on the first request
+            st = self._qat_saved_state = st()
+        return st
 
     def _quantized_forward(self, x: Tensor, hx):
         if not self.is_calibrated():
@@ -674,9 +691,14 @@ class QuantLSTM(nn.Module):
 
         result = self._directions(x, hx, run)
         if self.training and save:
-            states = [_qat_state(s["saved"]) if "saved" in s else None for s in sinks]
-            self._qat_saved_state = (states[0] if not self.bidirectional else
-                                     {"forward": states[0], "reverse": states[1]})
+            params = list(self._params)
+
+            def build(sinks=sinks, params=params, bidir=self.bidirectional):
+                states = [_qat_state(s["saved"], params[d], s["batch"]) if "saved" in s else None
+                          for d, s in enumerate(sinks)]
+                return states[0] if not bidir else {"forward": states[0], "reverse": states[1]}
+
+            self._qat_saved_state = build
         else:
             self._qat_saved_state = None
         return result

@@ -57,6 +57,16 @@ class Saved(ctypes.Structure):
     _fields_ = [(n, ctypes.c_void_p) for n in SAVED_FIELDS]
 
 
+class SavedCodes(ctypes.Structure):
+    """rxmet_lstm_saved_codes: the saved-codes blocks and the cell codes."""
+    _fields_ = [("blocks", ctypes.c_void_p), ("cell_codes", ctypes.c_void_p)]
+
+
+# bytes of one saved-codes block and u16 codes of one cell-code block (rxmet_lstm_saved_codes)
+CODES_BLOCK = 3840
+CELL_BLOCK = 256
+
+
 def default_config() -> Config:
     """The reference's default profile (config/defaults/lstm_quant_default_v1.json): all
     8-bit, affine, sigmoid gate outputs unsigned, everything symmetric, parameters
@@ -116,6 +126,13 @@ _SIGS = {
     "rxmet_lstm_backward_quant": (ctypes.c_int, [_i32] * 4 + [ctypes.POINTER(Params),
                                                               ctypes.POINTER(Saved)] +
                                   [_p] * 3 + [_p] * 7 + [_p, _p]),
+    "rxmet_lstm_forward_quant_codes": (ctypes.c_int, [_i32] * 4 + [_p] * 7 + [ctypes.POINTER(Params)] +
+                                       [_p] * 3 + [ctypes.POINTER(Saved), ctypes.POINTER(SavedCodes),
+                                                   _p, _p]),
+    "rxmet_lstm_backward_quant_codes": (ctypes.c_int, [_i32] * 4 + [ctypes.POINTER(Params),
+                                                                    ctypes.POINTER(Saved),
+                                                                    ctypes.POINTER(SavedCodes)] +
+                                        [_p] * 3 + [_p] * 7 + [_p, _p]),
     "rxmet_lstm_forward_calibrate": (ctypes.c_int, [_i32] * 4 + [_p] * 7 + [_p] * 4 + [_p, _p]),
     "rxmet_lstm_forward_float": (ctypes.c_int, [_i32] * 4 + [_p] * 7 + [_p] * 3 + [_p]),
     "rxmet_lstm_activation_table": (_i32, [ctypes.POINTER(Params), _i32, _i32, _p, _i32]),
