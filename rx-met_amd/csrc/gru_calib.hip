@@ -199,38 +199,57 @@ __device__ __forceinline__ void block_stats(const float *mn, const float *mx, in
   }
 }
 
-// Fold P partial blocks of 2 n floats (n statistics starting at i0) into the ordered ranges
-// (statistics a block did not observe hold FLT_MAX / -FLT_MAX and change nothing).
-__global__ __launch_bounds__(256) void stats_fold(const float *__restrict__ part, int P, int n,
-                                                  int i0, unsigned *__restrict__ ostat) {
-  __shared__ float smn[4][kNStat], smx[4][kNStat];
+// Fold P partial blocks of 2 N floats (N statistics starting at i0) into the ordered ranges
+// (statistics a block did not observe hold FLT_MAX / -FLT_MAX and change nothing).  Each
+// thread takes whole partial blocks, all of a block's loads issued together, so the pass over
+// P blocks is one latency per 256 blocks rather than one per statistic and block.
+template <int N>
+__global__ __launch_bounds__(256) void stats_fold(const float *__restrict__ part, int P, int i0,
+                                                  unsigned *__restrict__ ostat) {
+  __shared__ float smn[4][N], smx[4][N];
   const int w = threadIdx.x / kWave;
-  for (int i = 0; i < n; ++i) {
-    float lo = FLT_MAX, hi = -FLT_MAX;
-    for (int p = threadIdx.x; p < P; p += blockDim.x) {
-      lo = fminf(lo, part[static_cast<size_t>(p) * 2 * n + i]);
-      hi = fmaxf(hi, part[static_cast<size_t>(p) * 2 * n + n + i]);
+  float lo[N], hi[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    lo[i] = FLT_MAX;
+    hi[i] = -FLT_MAX;
+  }
+  for (int p = threadIdx.x; p < P; p += blockDim.x) {
+    const float *q = part + static_cast<size_t>(p) * 2 * N;
+    float v[2 * N];
+#pragma unroll
+    for (int i = 0; i < 2 * N; ++i) v[i] = q[i];
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      lo[i] = fminf(lo[i], v[i]);
+      hi[i] = fmaxf(hi[i], v[N + i]);
     }
-    lo = wave_min(lo);
-    hi = wave_max(hi);
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const float a = wave_min(lo[i]), b = wave_max(hi[i]);
     if (threadIdx.x % kWave == 0) {
-      smn[w][i] = lo;
-      smx[w][i] = hi;
+      smn[w][i] = a;
+      smx[w][i] = b;
     }
   }
   __syncthreads();
-  if (threadIdx.x < n) {
-    float lo = smn[0][threadIdx.x], hi = smx[0][threadIdx.x];
+  if (threadIdx.x < N) {
+    float a = smn[0][threadIdx.x], b = smx[0][threadIdx.x];
     for (int ww = 1; ww < 4; ++ww) {
-      lo = fminf(lo, smn[ww][threadIdx.x]);
-      hi = fmaxf(hi, smx[ww][threadIdx.x]);
+      a = fminf(a, smn[ww][threadIdx.x]);
+      b = fmaxf(b, smx[ww][threadIdx.x]);
     }
-    if (lo <= hi) {  // merged: one thread per statistic, so no contention
-      atomicMin(&ostat[i0 + threadIdx.x], f2ord(lo));
-      atomicMax(&ostat[kNStat + i0 + threadIdx.x], f2ord(hi));
+    if (a <= b) {  // merged: one thread per statistic, so no contention
+      atomicMin(&ostat[i0 + threadIdx.x], f2ord(a));
+      atomicMax(&ostat[kNStat + i0 + threadIdx.x], f2ord(b));
     }
   }
 }
+
+// The statistics the input GEMM observes, x and the input linear, lie among the first three.
+constexpr int kGemmStat = 3;
+static_assert(RXMET_GRU_X < kGemmStat && RXMET_GRU_WX < kGemmStat, "GEMM statistics layout");
 
 // wx[m][c] = sum_k x[m][k] W[k][c] + bw[c] for m < M = T B, c < C = 3H, with the X and WX
 // statistics.  A workgroup covers 64 columns of RB 64-row tiles; each of its four waves a
@@ -261,8 +280,8 @@ __global__ __launch_bounds__(256) void calib_input_gemm(int M, int K, int C, int
     for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int j = 0; j < 2; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-    for (int k0 = 0; k0 < K; k0 += 16) {
-      float a[2][4], b[2][4];
+    // operands of one 16-wide K step; the next step's are in flight during this one's MFMAs
+    auto load = [&](int k0, float (&a)[2][4], float (&b)[2][4]) {
       const int kb = k0 + 4 * g;
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
@@ -275,10 +294,6 @@ __global__ __launch_bounds__(256) void calib_input_gemm(int M, int K, int C, int
 #pragma unroll
           for (int s = 0; s < 4; ++s) a[i][s] = row < M && kb + s < K ? xr[s] : 0.0f;
         }
-        if (see_x && row < M)
-#pragma unroll
-          for (int s = 0; s < 4; ++s)
-            if (kb + s < K) observe(a[i][s], st_mn[RXMET_GRU_X], st_mx[RXMET_GRU_X]);
       }
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
@@ -287,12 +302,31 @@ __global__ __launch_bounds__(256) void calib_input_gemm(int M, int K, int C, int
         for (int s = 0; s < 4; ++s)
           b[j][s] = col < C && kb + s < K ? W[static_cast<size_t>(kb + s) * C + col] : 0.0f;
       }
+    };
+    auto step = [&](int k0, const float (&a)[2][4], const float (&b)[2][4]) {
+      // the zeros loaded past M and K are not values of x: only in-range entries are observed
+      if (see_x)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+          if (m0 + 16 * i + r < M)
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+              if (k0 + 4 * g + s < K) observe(a[i][s], st_mn[RXMET_GRU_X], st_mx[RXMET_GRU_X]);
 #pragma unroll
       for (int s = 0; s < 4; ++s)
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
           for (int j = 0; j < 2; ++j) acc[i][j] = mfma_f32(a[i][s], b[j][s], acc[i][j]);
+    };
+    float a0[2][4], b0[2][4], a1[2][4], b1[2][4];
+    load(0, a0, b0);
+    for (int k0 = 0; k0 < K; k0 += 32) {
+      if (k0 + 16 < K) load(k0 + 16, a1, b1);
+      step(k0, a0, b0);
+      if (k0 + 16 >= K) break;
+      if (k0 + 32 < K) load(k0 + 32, a0, b0);
+      step(k0 + 16, a1, b1);
     }
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -313,8 +347,8 @@ __global__ __launch_bounds__(256) void calib_input_gemm(int M, int K, int C, int
       }
   }
   if (STATS)
-    block_stats(st_mn, st_mx, kNStat,
-                part + (static_cast<size_t>(blockIdx.y) * gridDim.x + blockIdx.x) * 2 * kNStat);
+    block_stats(st_mn, st_mx, kGemmStat,
+                part + (static_cast<size_t>(blockIdx.y) * gridDim.x + blockIdx.x) * 2 * kGemmStat);
 }
 
 struct CalClArgs {
@@ -561,8 +595,8 @@ static int calibrate_mfma(int T, int B, int I, int H, const float *W, const floa
                        wx, part);
     RXMET_CHECK_LAUNCH();
     if (STATS) {
-      hipLaunchKernelGGL(stats_fold, dim3(1), dim3(256), 0, stream, part,
-                         static_cast<int>(grid.x * grid.y), kNStat, 0, ord);
+      hipLaunchKernelGGL(stats_fold<kGemmStat>, dim3(1), dim3(256), 0, stream, part,
+                         static_cast<int>(grid.x * grid.y), 0, ord);
       RXMET_CHECK_LAUNCH();
     }
   }
@@ -580,7 +614,7 @@ static int calibrate_mfma(int T, int B, int I, int H, const float *W, const floa
     RXMET_CHECK_HIP(cluster::launch(fn, dim3(ncl * a.G), dim3(kWave * a.NWG), args,
                                     static_cast<unsigned>(lds), stream));
     if (STATS) {
-      hipLaunchKernelGGL(stats_fold, dim3(1), dim3(256), 0, stream, part, ncl * a.G, kNStat, 0,
+      hipLaunchKernelGGL(stats_fold<kNStat>, dim3(1), dim3(256), 0, stream, part, ncl * a.G, 0,
                          ord);
       RXMET_CHECK_LAUNCH();
     }

@@ -186,14 +186,17 @@ constexpr int kCMaxW = 8;  // waves of a recurrence workgroup (256 VGPRs: W_hh, 
 constexpr int kGemmRBMax = 8;
 constexpr int kPart = 2 * kN + 1;  // floats per partial block: min[18], max[18], non-finite
 
+// The block's ranges of the first N statistics and its non-finite count as one partial block
+// of 2 N + 1 floats: min[N], max[N], count.
+template <int N = kN>
 __device__ __forceinline__ void obs_block(const Obs &o, float *part) {
-  __shared__ float smn[kCMaxW][kN], smx[kCMaxW][kN];
+  __shared__ float smn[kCMaxW][N], smx[kCMaxW][N];
   __shared__ unsigned sbad;
   const int w = threadIdx.x / kWave, nw = blockDim.x / kWave;
   if (threadIdx.x == 0) sbad = 0;
   __syncthreads();
 #pragma unroll
-  for (int i = 0; i < kN; ++i) {  // unrolled: o stays in registers
+  for (int i = 0; i < N; ++i) {  // unrolled: o stays in registers
     const float lo = wave_min(o.mn[i]), hi = wave_max(o.mx[i]);
     if (threadIdx.x % kWave == 0) {
       smn[w][i] = lo;
@@ -202,16 +205,16 @@ __device__ __forceinline__ void obs_block(const Obs &o, float *part) {
   }
   if (o.bad) atomicAdd(&sbad, o.bad);
   __syncthreads();
-  if (threadIdx.x < kN) {
+  if (threadIdx.x < N) {
     float lo = smn[0][threadIdx.x], hi = smx[0][threadIdx.x];
     for (int ww = 1; ww < nw; ++ww) {
       lo = fminf(lo, smn[ww][threadIdx.x]);
       hi = fmaxf(hi, smx[ww][threadIdx.x]);
     }
     part[threadIdx.x] = lo;
-    part[kN + threadIdx.x] = hi;
+    part[N + threadIdx.x] = hi;
   }
-  if (threadIdx.x == 0) part[2 * kN] = static_cast<float>(sbad);  // exact: far below 2^24
+  if (threadIdx.x == 0) part[2 * N] = static_cast<float>(sbad);  // exact: far below 2^24
 }
 
 __device__ __forceinline__ void obs_init(Obs &o) {
@@ -223,44 +226,64 @@ __device__ __forceinline__ void obs_init(Obs &o) {
   o.bad = 0;
 }
 
-// P partial blocks folded in a fixed order into this call's ordered ranges and count.
+// P partial blocks of the first N statistics (obs_block<N>) folded into this call's ordered
+// ranges and count.  Each thread takes whole partial blocks, all of a block's loads issued
+// together: one load latency per 256 blocks rather than one per statistic and block.
+template <int N>
 __global__ __launch_bounds__(256) void lstm_stats_fold(const float *__restrict__ part, int P,
                                                        unsigned *__restrict__ ostat) {
-  __shared__ float smn[4][kN], smx[4][kN];
+  __shared__ float smn[4][N], smx[4][N];
   __shared__ unsigned sbad;
   const int w = threadIdx.x / kWave;
   if (threadIdx.x == 0) sbad = 0;
   __syncthreads();
+  float lo[N], hi[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    lo[i] = INFINITY;
+    hi[i] = -INFINITY;
+  }
   unsigned bad = 0;
-  for (int i = 0; i < kN; ++i) {
-    float lo = INFINITY, hi = -INFINITY;
-    for (int p = threadIdx.x; p < P; p += blockDim.x) {
-      lo = fminf(lo, part[static_cast<size_t>(p) * kPart + i]);
-      hi = fmaxf(hi, part[static_cast<size_t>(p) * kPart + kN + i]);
-      if (i == 0) bad += static_cast<unsigned>(part[static_cast<size_t>(p) * kPart + 2 * kN]);
+  for (int p = threadIdx.x; p < P; p += blockDim.x) {
+    const float *q = part + static_cast<size_t>(p) * (2 * N + 1);
+    float v[2 * N + 1];
+#pragma unroll
+    for (int i = 0; i < 2 * N + 1; ++i) v[i] = q[i];
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      lo[i] = fminf(lo[i], v[i]);
+      hi[i] = fmaxf(hi[i], v[N + i]);
     }
-    lo = wave_min(lo);
-    hi = wave_max(hi);
+    bad += static_cast<unsigned>(v[2 * N]);
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const float a = wave_min(lo[i]), b = wave_max(hi[i]);
     if (threadIdx.x % kWave == 0) {
-      smn[w][i] = lo;
-      smx[w][i] = hi;
+      smn[w][i] = a;
+      smx[w][i] = b;
     }
   }
   if (bad) atomicAdd(&sbad, bad);
   __syncthreads();
-  if (threadIdx.x < kN) {
-    float lo = smn[0][threadIdx.x], hi = smx[0][threadIdx.x];
+  if (threadIdx.x < N) {
+    float a = smn[0][threadIdx.x], b = smx[0][threadIdx.x];
     for (int ww = 1; ww < 4; ++ww) {
-      lo = fminf(lo, smn[ww][threadIdx.x]);
-      hi = fmaxf(hi, smx[ww][threadIdx.x]);
+      a = fminf(a, smn[ww][threadIdx.x]);
+      b = fmaxf(b, smx[ww][threadIdx.x]);
     }
-    if (lo <= hi) {  // one thread per operator: no contention
-      atomicMin(&ostat[threadIdx.x], f2ord(lo));
-      atomicMax(&ostat[kN + threadIdx.x], f2ord(hi));
+    if (a <= b) {  // one thread per operator: no contention
+      atomicMin(&ostat[threadIdx.x], f2ord(a));
+      atomicMax(&ostat[kN + threadIdx.x], f2ord(b));
     }
   }
   if (threadIdx.x == 0 && sbad) atomicAdd(&ostat[2 * kN], sbad);
 }
+
+// The statistics the input GEMM observes, the input and the input linear, lie among the first
+// kGemmStat operators.
+constexpr int kGemmStat = RXMET_LSTM_IH_LINEAR + 1;
+static_assert(RXMET_LSTM_INPUT < kGemmStat, "GEMM statistics layout");
 
 // li[m][c] = sum_k x[m][k] W_ih[c][k] + b_ih[c] for m < M = T B, c < C = 4H, with the INPUT
 // and IH_LINEAR observations.  The GRU projection's tiling (gru_calib.hip): 64 columns of RB
@@ -286,8 +309,8 @@ __global__ __launch_bounds__(256) void lstm_input_gemm(int M, int K, int C, int 
     for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int j = 0; j < 2; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-    for (int k0 = 0; k0 < K; k0 += 16) {
-      float a[2][4], b[2][4];
+    // operands of one 16-wide K step; the next step's are in flight during this one's MFMAs
+    auto load = [&](int k0, float (&a)[2][4], float (&b)[2][4]) {
       const int kb = k0 + 4 * g;
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
@@ -300,11 +323,6 @@ __global__ __launch_bounds__(256) void lstm_input_gemm(int M, int K, int C, int 
 #pragma unroll
           for (int s = 0; s < 4; ++s) a[i][s] = row < M && kb + s < K ? xr[s] : 0.0f;
         }
-        // x observed by the lanes of one column half (each row once)
-        if (see_x && (w % 2) == 0 && row < M)
-#pragma unroll
-          for (int s = 0; s < 4; ++s)
-            if (kb + s < K) observe(o, RXMET_LSTM_INPUT, a[i][s]);
       }
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
@@ -318,12 +336,32 @@ __global__ __launch_bounds__(256) void lstm_input_gemm(int M, int K, int C, int 
           for (int s = 0; s < 4; ++s) b[j][s] = col < C && kb + s < K ? wr[s] : 0.0f;
         }
       }
+    };
+    auto step = [&](int k0, const float (&a)[2][4], const float (&b)[2][4]) {
+      // x observed by the lanes of one column half (each row once); the zeros loaded past M
+      // and K are not values of x
+      if (see_x && (w % 2) == 0)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+          if (m0 + 16 * i + r < M)
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+              if (k0 + 4 * g + s < K) observe(o, RXMET_LSTM_INPUT, a[i][s]);
 #pragma unroll
       for (int s = 0; s < 4; ++s)
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
           for (int j = 0; j < 2; ++j) acc[i][j] = mfma_f32(a[i][s], b[j][s], acc[i][j]);
+    };
+    float a0[2][4], b0[2][4], a1[2][4], b1[2][4];
+    load(0, a0, b0);
+    for (int k0 = 0; k0 < K; k0 += 32) {
+      if (k0 + 16 < K) load(k0 + 16, a1, b1);
+      step(k0, a0, b0);
+      if (k0 + 16 >= K) break;
+      if (k0 + 32 < K) load(k0 + 32, a0, b0);
+      step(k0 + 16, a1, b1);
     }
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -343,7 +381,9 @@ __global__ __launch_bounds__(256) void lstm_input_gemm(int M, int K, int C, int 
         }
       }
   }
-  if (STATS) obs_block(o, part + (static_cast<size_t>(blockIdx.y) * gridDim.x + blockIdx.x) * kPart);
+  if (STATS)
+    obs_block<kGemmStat>(o, part + (static_cast<size_t>(blockIdx.y) * gridDim.x + blockIdx.x) *
+                                       (2 * kGemmStat + 1));
 }
 
 struct LCalArgs {
@@ -574,7 +614,7 @@ static int lstm_float_mfma(int T, int B, int I, int H, const float *Wi, const fl
                        li, part);
     RXMET_CHECK_LAUNCH();
     if (STATS) {
-      hipLaunchKernelGGL(lstm_stats_fold, dim3(1), dim3(256), 0, stream, part,
+      hipLaunchKernelGGL(lstm_stats_fold<kGemmStat>, dim3(1), dim3(256), 0, stream, part,
                          static_cast<int>(grid.x * grid.y), ord);
       RXMET_CHECK_LAUNCH();
     }
@@ -593,7 +633,7 @@ static int lstm_float_mfma(int T, int B, int I, int H, const float *Wi, const fl
     RXMET_CHECK_HIP(cluster::launch(fn, dim3(ncl * a.G), dim3(kWave * a.NWG), args,
                                     static_cast<unsigned>(lds), stream));
     if (STATS) {
-      hipLaunchKernelGGL(lstm_stats_fold, dim3(1), dim3(256), 0, stream, part, ncl * a.G, ord);
+      hipLaunchKernelGGL(lstm_stats_fold<kN>, dim3(1), dim3(256), 0, stream, part, ncl * a.G, ord);
       RXMET_CHECK_LAUNCH();
     }
   }

@@ -1145,8 +1145,9 @@ class QuantGRU(nn.Module):
             self.quant_ranges = gru_ops.GRUQuantizationRanges(H, device=device)
         W, R, bw, br = self._direction_weights(False, device)
         with torch.no_grad():
+            # the gate values (v) are not needed for the ranges: not materialised
             h, _ = gru_ops.forward_calibrate(
-                is_training=True, time_steps=T, batch_size=B, input_size=I, hidden_size=H,
+                is_training=False, time_steps=T, batch_size=B, input_size=I, hidden_size=H,
                 W=W, R=R, bw=bw, br=br, x=input,
                 h0=ensure_cuda_float32(h0f, device).contiguous() if h0f is not None else empty,
                 calib_method=self.calibration_method, bitwidth_config=self._bitwidth_config,
@@ -1159,7 +1160,7 @@ class QuantGRU(nn.Module):
             W, R, bw, br = self._direction_weights(True, device)
             with torch.no_grad():
                 h_r, _ = gru_ops.forward_calibrate(
-                    is_training=True, time_steps=T, batch_size=B, input_size=I, hidden_size=H,
+                    is_training=False, time_steps=T, batch_size=B, input_size=I, hidden_size=H,
                     W=W, R=R, bw=bw, br=br, x=input.flip(0).contiguous(),
                     h0=ensure_cuda_float32(h0r, device).contiguous() if h0r is not None else empty,
                     calib_method=self.calibration_method, bitwidth_config=self._bitwidth_config,
