@@ -366,28 +366,74 @@ struct CalClArgs {
   unsigned spin_limit;
 };
 
+// The recurrent product of one member for one tile: wave w takes the consecutive items
+// w IPW .. w IPW + IPW - 1 (item = 3 chunk + gate), so the three gates of a K chunk share one
+// load of its h values; every chunk the wave needs is loaded before the first MFMA.  Partial
+// tiles go to red[item][64].
+template <int IPW>
+__device__ __forceinline__ void calib_items(const float (&rfr)[IPW][16], int w, int l, int g,
+                                            int nitems, __amdgpu_buffer_rsrc_t xr, unsigned rowoff,
+                                            v4f *red) {
+  // chunks a run of IPW items spans (IPW items from a multiple of 3 when IPW is one)
+  constexpr int NCH = IPW % 3 == 0 ? IPW / 3 : (IPW + 1) / 3 + 1;
+  const int first = (w * IPW) / 3;
+  float hv[NCH][16];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int ch = first + c;
+    if (3 * ch < nitems) {
+      const unsigned off = 4u * (rowoff + 64 * ch + 16 * g);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int4 v = cluster::load_coherent16(xr, off + 16u * q);
+        hv[c][4 * q] = __int_as_float(v.x);
+        hv[c][4 * q + 1] = __int_as_float(v.y);
+        hv[c][4 * q + 2] = __int_as_float(v.z);
+        hv[c][4 * q + 3] = __int_as_float(v.w);
+      }
+    }
+  }
+#pragma unroll
+  for (int it = 0; it < IPW; ++it) {
+    const int item = w * IPW + it;
+    if (item >= nitems) break;
+    // the item's chunk among the loaded ones: static when IPW is a multiple of 3, else selected
+    // (a register array indexed at run time would live in scratch memory)
+    const int c = IPW % 3 == 0 ? it / 3 : item / 3 - first;
+    v4f acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+      float hs = hv[0][s];
+#pragma unroll
+      for (int cc = 1; cc < NCH; ++cc) hs = c == cc ? hv[cc][s] : hs;
+      acc = mfma_f32(hs, rfr[it][s], acc);
+    }
+    red[item * kWave + l] = acc;
+  }
+}
+
 // Member m of a cluster owns units 16 m .. 16 m + 15 of one 16-row batch tile.  The recurrent
 // product splits into items (k chunk c of 64, gate): 3 NC items, dealt to the workgroup's NWG
-// waves (wave w takes items w, w + NWG, ...: IPW at most).  An item is sixteen MFMAs, MFMA s
+// waves (wave w takes IPW consecutive items, calib_items).  An item is sixteen MFMAs, MFMA s
 // taking k = 64 c + 16 g + s for lane group g, so a lane's A values are 16 consecutive h of its
 // row (four 16-byte coherent loads) and its B values (R) stay in VGPRs for the whole launch.
 // The items' partial tiles meet in LDS; each of the tile's 256 (row, unit) elements is then
 // finished by one thread (the gates, the new h and the statistics), its previous h kept in a
 // register.  NWG >= 4, so the 256 elements have threads of their own.
-template <bool STATS, int IPW>
-__global__ __launch_bounds__(64 * kCMaxW) void calib_recurrence_cl(CalClArgs a) {
+template <bool STATS, int IPW, int MAXW = kCMaxW>
+__global__ __launch_bounds__(64 * MAXW) void calib_recurrence_cl(CalClArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   v4f *red = reinterpret_cast<v4f *>(smem);  // [3 NC][64]
   const cluster::Place pl = cluster::place(a.G, a.ncl);
   unsigned *counter = a.counters + cluster::kCounterStride * pl.cluster;
-  const int H = a.H, C = 3 * H, B = a.B, NC = a.NC, NWG = a.NWG;
+  const int H = a.H, C = 3 * H, B = a.B, NC = a.NC;
   const int tid = threadIdx.x, w = tid / kWave, l = tid % kWave, r16 = l % 16, g = l / 16;
   const int u0 = 16 * pl.member;
   const int nitems = 3 * NC;
   float rfr[IPW][16];
 #pragma unroll
   for (int it = 0; it < IPW; ++it) {
-    const int item = w + it * NWG, ch = item / 3, gate = item % 3;
+    const int item = w * IPW + it, ch = item / 3, gate = item % 3;
 #pragma unroll
     for (int s = 0; s < 16; ++s) {
       const int k = 64 * ch + 16 * g + s;
@@ -439,27 +485,8 @@ __global__ __launch_bounds__(64 * kCMaxW) void calib_recurrence_cl(CalClArgs a) 
     for (int t = 0; t < a.T && alive; ++t) {
       const int par = t & 1;
       const unsigned rowoff = par * plane + static_cast<unsigned>(tile * kCT + r16) * a.Hpad;
-#pragma unroll
-      for (int it = 0; it < IPW; ++it) {
-        const int item = w + it * NWG;
-        if (item >= nitems) break;
-        const int ch = item / 3;
-        // A: row tile*16 + r16, h[64 ch + 16 g .. + 15]
-        float hv[16];
-        const unsigned off = 4u * (rowoff + 64 * ch + 16 * g);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int4 v = cluster::load_coherent16(xr, off + 16u * q);
-          hv[4 * q] = __int_as_float(v.x);
-          hv[4 * q + 1] = __int_as_float(v.y);
-          hv[4 * q + 2] = __int_as_float(v.z);
-          hv[4 * q + 3] = __int_as_float(v.w);
-        }
-        v4f acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int s = 0; s < 16; ++s) acc = mfma_f32(hv[s], rfr[it][s], acc);
-        red[item * kWave + l] = acc;
-      }
+      // A: row tile*16 + r16, h[64 ch + 16 g .. + 15] of each item's chunk
+      calib_items<IPW>(rfr, w, l, g, nitems, xr, rowoff, red);
       __syncthreads();
       if (fin) {
         float rh[3] = {bz, brr, bn};
@@ -520,6 +547,145 @@ __global__ __launch_bounds__(64 * kCMaxW) void calib_recurrence_cl(CalClArgs a) 
   }
 }
 
+// The multi-tile form of calib_recurrence_cl, for clusters that own several batch tiles
+// (ntiles > ncl; c5: 64 tiles over 4 clusters): each step runs all of the cluster's tiles, one
+// after another, and meets the other members once, so a step pays one cluster barrier for up
+// to kMtMax tiles instead of one per tile.  Each tile's previous h (one per finishing thread)
+// waits in LDS between steps; the next tile's input linear is loaded while this one computes.
+constexpr int kMtMax = 16;
+
+template <bool STATS, int IPW, int MAXW = kCMaxW>
+__global__ __launch_bounds__(64 * MAXW) void calib_recurrence_mt(CalClArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  v4f *red = reinterpret_cast<v4f *>(smem);                             // [3 NC][64]
+  float *hl = reinterpret_cast<float *>(red + 3 * a.NC * kWave);        // [kMtMax][256]
+  const cluster::Place pl = cluster::place(a.G, a.ncl);
+  unsigned *counter = a.counters + cluster::kCounterStride * pl.cluster;
+  const int H = a.H, C = 3 * H, B = a.B, NC = a.NC;
+  const int tid = threadIdx.x, w = tid / kWave, l = tid % kWave, r16 = l % 16, g = l / 16;
+  const int u0 = 16 * pl.member;
+  const int nitems = 3 * NC;
+  const int nT = (a.ntiles - pl.cluster + a.ncl - 1) / a.ncl;  // <= kMtMax (launcher)
+  float rfr[IPW][16];
+#pragma unroll
+  for (int it = 0; it < IPW; ++it) {
+    const int item = w * IPW + it, ch = item / 3, gate = item % 3;
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+      const int k = 64 * ch + 16 * g + s;
+      rfr[it][s] = item < nitems && k < H
+                       ? a.R[static_cast<size_t>(k) * C + gate * H + u0 + r16] : 0.0f;
+    }
+  }
+  const bool fin = tid < 256;
+  const int fl = tid % 64, fq = tid / 64;
+  const int frow = 4 * (fl / 16) + fq, fu = u0 + fl % 16;
+  const float bz = fin ? a.br[fu] : 0.0f, brr = fin ? a.br[H + fu] : 0.0f,
+              bn = fin ? a.br[2 * H + fu] : 0.0f;
+  float mn[kNStat], mx[kNStat];
+#pragma unroll
+  for (int i = 0; i < kNStat; ++i) {
+    mn[i] = FLT_MAX;
+    mx[i] = -FLT_MAX;
+  }
+  const unsigned plane = static_cast<unsigned>(a.Bpad) * a.Hpad;  // floats per parity
+  const auto xr = cluster::buffer_rsrc(a.hx, 2u * plane * 4u);
+  unsigned *hxw = reinterpret_cast<unsigned *>(a.hx);
+  const size_t BH = static_cast<size_t>(B) * H;
+  // initial states of every tile
+  for (int k = 0; k < nT; ++k) {
+    const int b = (pl.cluster + k * a.ncl) * kCT + frow;
+    if (fin) {
+      const float h0 = b < B && a.h0 ? a.h0[static_cast<size_t>(b) * H + fu] : 0.0f;
+      cluster::store_coherent(hxw + b * a.Hpad + fu, __float_as_uint(h0));
+      if (b < B) a.hout[static_cast<size_t>(b) * H + fu] = h0;
+      hl[k * 256 + tid] = h0;
+    }
+  }
+  float wz = 0.0f, wr = 0.0f, wn = 0.0f;
+  auto load_wx = [&](int t, int k) {
+    const int b = (pl.cluster + k * a.ncl) * kCT + frow;
+    if (fin && b < B) {
+      const float *wp = a.wx + (static_cast<size_t>(t) * B + b) * C + fu;
+      wz = wp[0];
+      wr = wp[H];
+      wn = wp[2 * H];
+    }
+  };
+  load_wx(0, 0);
+  unsigned epoch = 0;
+  bool alive = cluster::sync(counter, ++epoch * a.G, a.timeout, a.spin_limit);
+  for (int t = 0; t < a.T && alive; ++t) {
+    const int par = t & 1;
+    for (int k = 0; k < nT; ++k) {
+      const int tile = pl.cluster + k * a.ncl;
+      const int b = tile * kCT + frow;
+      const bool valid = fin && b < B;
+      const unsigned rowoff = par * plane + static_cast<unsigned>(tile * kCT + r16) * a.Hpad;
+      calib_items<IPW>(rfr, w, l, g, nitems, xr, rowoff, red);
+      __syncthreads();
+      if (fin) {
+        const float cz = wz, cr = wr, cn = wn;
+        // the next tile's (or the next step's first tile's) input linear, in flight meanwhile
+        if (k + 1 < nT)
+          load_wx(t, k + 1);
+        else if (t + 1 < a.T)
+          load_wx(t + 1, 0);
+        float rh[3] = {bz, brr, bn};
+        for (int ch = 0; ch < NC; ++ch)
+#pragma unroll
+          for (int gate = 0; gate < 3; ++gate) rh[gate] += red[(ch * 3 + gate) * kWave + fl][fq];
+        const float hold = hl[k * 256 + tid];
+        const float zp = cz + rh[0];
+        const float rp = cr + rh[1];
+        const float z = static_cast<float>(1.0 / (1.0 + exp(-static_cast<double>(zp))));
+        const float r = static_cast<float>(1.0 / (1.0 + exp(-static_cast<double>(rp))));
+        const float rhm = r * rh[2];
+        const float np = cn + rhm;
+        const float n = tanhf(np);
+        const float oldc = z * hold;
+        const float newc = (1.0f - z) * n;
+        const float hn = oldc + newc;
+        hl[k * 256 + tid] = hn;
+        cluster::store_coherent(hxw + (par ^ 1) * plane + b * a.Hpad + fu, __float_as_uint(hn));
+        if (STATS && valid) {
+          observe(rh[0], mn[RXMET_GRU_RH], mx[RXMET_GRU_RH]);
+          observe(rh[1], mn[RXMET_GRU_RH], mx[RXMET_GRU_RH]);
+          observe(rh[2], mn[RXMET_GRU_RH], mx[RXMET_GRU_RH]);
+          observe(zp, mn[RXMET_GRU_Z_IN], mx[RXMET_GRU_Z_IN]);
+          observe(rp, mn[RXMET_GRU_R_IN], mx[RXMET_GRU_R_IN]);
+          observe(np, mn[RXMET_GRU_N_IN], mx[RXMET_GRU_N_IN]);
+          observe(z, mn[RXMET_GRU_Z_OUT], mx[RXMET_GRU_Z_OUT]);
+          observe(r, mn[RXMET_GRU_R_OUT], mx[RXMET_GRU_R_OUT]);
+          observe(n, mn[RXMET_GRU_N_OUT], mx[RXMET_GRU_N_OUT]);
+          observe(rhm, mn[RXMET_GRU_MUL_RH], mx[RXMET_GRU_MUL_RH]);
+          observe(newc, mn[RXMET_GRU_MUL_NEW], mx[RXMET_GRU_MUL_NEW]);
+          observe(oldc, mn[RXMET_GRU_MUL_OLD], mx[RXMET_GRU_MUL_OLD]);
+          observe(hn, mn[RXMET_GRU_H], mx[RXMET_GRU_H]);
+        }
+        if (valid) {
+          a.hout[(static_cast<size_t>(t) + 1) * BH + static_cast<size_t>(b) * H + fu] = hn;
+          if (a.v) {
+            float *vb = a.v + (static_cast<size_t>(t) * B + b) * 4 * H + fu;
+            vb[0] = z;
+            vb[H] = r;
+            vb[2 * H] = n;
+            vb[3 * H] = rh[2];
+          }
+        }
+      }
+      __syncthreads();  // the partial tiles are read before the next tile rewrites them
+    }
+    cluster::arrive(counter);
+    ++epoch;
+    alive = cluster::wait(counter, epoch * a.G, a.timeout, a.spin_limit);
+  }
+  if (STATS) {
+    __syncthreads();
+    block_stats(mn, mx, kNStat, a.part + static_cast<size_t>(blockIdx.x) * 2 * kNStat);
+  }
+}
+
 struct CalWorkspace {
   size_t ord, wx, hx, part, sync, total;
   int Bpad, Hpad, ntiles;
@@ -555,14 +721,30 @@ static int calibrate_mfma(int T, int B, int I, int H, const float *W, const floa
   CalClArgs a{};
   a.T = T; a.B = B; a.H = H;
   a.NC = (H + 63) / 64;
-  a.NWG = std::min(kCMaxW, std::max(4, 3 * a.NC));
-  const int ipw = (3 * a.NC + a.NWG - 1) / a.NWG;  // 1 (H <= 320) .. 3
+  // up to 320 units: 4..16 waves of one item (1024 threads, 128 VGPRs); above, 8 waves of
+  // 3..6 items (512 threads, 256 VGPRs: two or three items per wave at 1024 threads spilled)
+  const bool wide = 3 * a.NC > kCMaxW;
+  a.NWG = wide ? 8 : std::max(4, 3 * a.NC);
+  const int ipw = (3 * a.NC + a.NWG - 1) / a.NWG;  // 1, or 3..6 when wide
   a.ntiles = ws.ntiles; a.Bpad = ws.Bpad; a.Hpad = ws.Hpad;
   a.G = H / 16;
-  const void *fn = ipw == 1 ? reinterpret_cast<const void *>(&calib_recurrence_cl<STATS, 1>)
-                 : ipw == 2 ? reinterpret_cast<const void *>(&calib_recurrence_cl<STATS, 2>)
-                            : reinterpret_cast<const void *>(&calib_recurrence_cl<STATS, 3>);
-  const size_t lds = sizeof(v4f) * kWave * 3 * static_cast<size_t>(a.NC);
+  using K = const void *;
+  const K cl_fns[7] = {nullptr,
+                       reinterpret_cast<K>(&calib_recurrence_cl<STATS, 1>),
+                       nullptr,
+                       reinterpret_cast<K>(&calib_recurrence_cl<STATS, 3, 8>),
+                       reinterpret_cast<K>(&calib_recurrence_cl<STATS, 4, 8>),
+                       reinterpret_cast<K>(&calib_recurrence_cl<STATS, 5, 8>),
+                       reinterpret_cast<K>(&calib_recurrence_cl<STATS, 6, 8>)};
+  const K mt_fns[7] = {nullptr,
+                       reinterpret_cast<K>(&calib_recurrence_mt<STATS, 1>),
+                       nullptr,
+                       reinterpret_cast<K>(&calib_recurrence_mt<STATS, 3, 8>),
+                       reinterpret_cast<K>(&calib_recurrence_mt<STATS, 4, 8>),
+                       reinterpret_cast<K>(&calib_recurrence_mt<STATS, 5, 8>),
+                       reinterpret_cast<K>(&calib_recurrence_mt<STATS, 6, 8>)};
+  const void *fn = cl_fns[ipw];
+  size_t lds = sizeof(v4f) * kWave * 3 * static_cast<size_t>(a.NC);
   RXMET_CHECK_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                       static_cast<int>(lds)));
   int device = 0, ncu = 0, per_cu = 0;
@@ -574,6 +756,22 @@ static int calibrate_mfma(int T, int B, int I, int H, const float *W, const floa
   if (ncl > a.ntiles) ncl = a.ntiles;
   if (ncl >= 8) ncl -= ncl % 8;
   a.ncl = ncl;
+  // clusters owning several tiles run them all in each step (one barrier per step), when
+  // the multi-tile kernel's occupancy allows the same cluster count
+  if (a.ntiles > ncl && (a.ntiles + ncl - 1) / ncl <= kMtMax &&
+      std::getenv("RXMET_CALIB_TILEWISE") == nullptr) {
+    const void *mt = mt_fns[ipw];
+    const size_t lds_mt = lds + sizeof(float) * kMtMax * 256;
+    RXMET_CHECK_HIP(hipFuncSetAttribute(mt, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        static_cast<int>(lds_mt)));
+    int per_cu_mt = 0;
+    RXMET_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu_mt, mt, kWave * a.NWG,
+                                                                 lds_mt));
+    if (per_cu_mt >= per_cu) {
+      fn = mt;
+      lds = lds_mt;
+    }
+  }
   char *wsb = static_cast<char *>(workspace);
   unsigned *ord = reinterpret_cast<unsigned *>(wsb + ws.ord);
   float *wx = reinterpret_cast<float *>(wsb + ws.wx);

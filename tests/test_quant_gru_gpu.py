@@ -50,8 +50,11 @@ def _close(a, e, name, atol=2e-6, rtol=1e-5):
     np.testing.assert_allclose(a, e, rtol=rtol, atol=atol, err_msg=name)
 
 
+# H = 336 .. 1024 take the 8-wave recurrence (3 .. 6 items per wave); B = 300 at H = 528 and
+# B = 200 at H = 1024 give clusters several batch tiles (the multi-tile recurrence)
 @pytest.mark.parametrize("shape", [(5, 20, 7, 32), (4, 16, 80, 256), (3, 9, 40, 48),
-                                   (2, 3, 1, 5), (3, 4, 6, 300)])
+                                   (2, 3, 1, 5), (3, 4, 6, 300), (3, 40, 16, 336),
+                                   (2, 300, 8, 528), (2, 48, 8, 704), (2, 200, 8, 1024)])
 @pytest.mark.parametrize("with_h0", [False, True])
 def test_calibration_matches_oracle(cuda, shape, with_h0):
     T, B, I, H = shape
