@@ -170,7 +170,7 @@ int rxmet_qdq_encoding_backward(const float *mn, const float *mx, const float *g
  * zero_point_shift, and encodings over two separated groups of axes.
  * ------------------------------------------------------------------------------------- */
 
-/* Element types (tensors: F32, F16, BF16; internal arithmetic: also F64). */
+/* Element types (tensors and internal arithmetic; an F64 tensor computes in F64). */
 enum {
   RXMET_QDQ_F32 = 0,
   RXMET_QDQ_F16 = 1,
@@ -192,13 +192,17 @@ typedef struct rxmet_qdq_layout {
 
 /*
  * Arithmetic of one call, as the reference's backend evaluates it:
- *   io_dtype        element type of x, y, g and dx (F32, F16 or BF16);
+ *   io_dtype        element type of x, y, g and dx (F32, F16, BF16 or F64; F64 pairs with
+ *                   internal_dtype F64 only, the reference's internal type for an fp64
+ *                   tensor);
  *   internal_dtype  type QuantizeFunc / QuantDequantFunc compute in (io_dtype, F32 or F64:
  *                   torch_builtins.py:171-174, 255-262 widen it while the grid is not
  *                   numerically stable in the narrower type); every operation's result is
  *                   rounded to it, and the result to io_dtype.  Dequantize computes in
  *                   io_dtype (internal_dtype must equal it); the frozen mode computes as
- *                   torch.fake_quantize does, in fp32, whatever the io type.
+ *                   torch.fake_quantize does, in fp32, whatever the io type (an F64 tensor's
+ *                   x * (1 / scale) and its rounding in fp64, as aten's kernel promotes it).
+ *                   Min / max statistics of an F64 tensor are fp32 (each value rounded).
  *   zero_point_shift  quantize_dequantize only (learnable mode): y = qdq(x - shift * s) +
  *                   shift * s (torch_builtins.py:276-284); 0 for none.
  *   scalar_scale    the reference's scale is a 0-dim tensor.  PyTorch then evaluates binary

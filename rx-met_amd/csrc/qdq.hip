@@ -307,7 +307,9 @@ static int check_layout(int64_t outer, int64_t C0, int64_t mid, int64_t C1, int6
   return 0;
 }
 
-static int esize_of(int32_t io) { return io == RXMET_QDQ_F32 ? 4 : 2; }
+static int esize_of(int32_t io) {
+  return io == RXMET_QDQ_F64 ? 8 : io == RXMET_QDQ_F32 ? 4 : 2;
+}
 
 static int mantissa_bits(int32_t t) {
   return t == RXMET_QDQ_F64 ? 53 : t == RXMET_QDQ_F32 ? 24 : t == RXMET_QDQ_F16 ? 11 : 8;
@@ -324,7 +326,7 @@ static int check_grid(int64_t qmin, int64_t qmax, int32_t type) {
 }
 
 static bool is_io(int32_t t) {
-  return t == RXMET_QDQ_F32 || t == RXMET_QDQ_F16 || t == RXMET_QDQ_BF16;
+  return t == RXMET_QDQ_F32 || t == RXMET_QDQ_F16 || t == RXMET_QDQ_BF16 || t == RXMET_QDQ_F64;
 }
 
 // Which internal type an op computes in under these numerics.
@@ -335,7 +337,7 @@ static int32_t arithmetic_type(int op, const rxmet_qdq_numerics &nm) {
 }
 
 static int check_numerics(int op, const rxmet_qdq_numerics &nm) {
-  RXMET_CHECK_ARG(is_io(nm.io_dtype), "io_dtype must be RXMET_QDQ_F32, F16 or BF16");
+  RXMET_CHECK_ARG(is_io(nm.io_dtype), "io_dtype must be RXMET_QDQ_F32, F16, BF16 or F64");
   const int32_t r = nm.internal_dtype;
   RXMET_CHECK_ARG(r == nm.io_dtype || r == RXMET_QDQ_F32 || r == RXMET_QDQ_F64,
                   "internal_dtype must be io_dtype, RXMET_QDQ_F32 or RXMET_QDQ_F64");
@@ -361,6 +363,7 @@ static int dispatch(const Call &c, int32_t io, int what) {
   if (io == RXMET_QDQ_F32) rc = run_f32(c, what);
   else if (io == RXMET_QDQ_F16) rc = run_f16(c, what);
   else if (io == RXMET_QDQ_BF16) rc = run_bf16(c, what);
+  else if (io == RXMET_QDQ_F64) rc = run_f64(c, what);
   if (rc != 0) {
     set_error("qdq: no kernel for this op / io type / internal type combination");
     return rc;
@@ -452,7 +455,7 @@ static int minmax_impl(const void *x, int32_t io, const rxmet_qdq_layout *l, Put
                        void *workspace, void *stream, bool skip_nan = false) {
   RXMET_CHECK_ARG(l != nullptr, "layout must be non-null");
   if (int rc = check_layout(l->outer, l->C0, l->mid, l->C1, l->inner)) return rc;
-  RXMET_CHECK_ARG(is_io(io), "io_dtype must be RXMET_QDQ_F32, F16 or BF16");
+  RXMET_CHECK_ARG(is_io(io), "io_dtype must be RXMET_QDQ_F32, F16, BF16 or F64");
   const Plan p = make_plan(l->outer, l->C0, l->mid, l->C1, l->inner, esize_of(io), kVecMinMax);
   RXMET_CHECK_ARG(p.n > 0, "min/max of an empty tensor");
   RXMET_CHECK_ARG(x != nullptr, "x must be non-null");

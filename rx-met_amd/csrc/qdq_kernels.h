@@ -155,6 +155,7 @@ struct Io;
 
 template <>
 struct Io<float> {
+  using V = float;             // the value type elements are computed in
   static constexpr int E = 4;  // elements per 16-byte vector
   __device__ static float ld(const float *p, int64_t i) { return p[i]; }
   __device__ static void st(float *p, int64_t i, float v) { p[i] = v; }
@@ -179,6 +180,7 @@ struct Io<float> {
 // 16-bit io types: BF selects bf16 (else fp16).
 template <typename Tag, bool BF>
 struct Io16 {
+  using V = float;
   static constexpr int E = 8;
   __device__ static float to_f(uint32_t b) { return BF ? bf16_to_f(b) : f16_to_f(b); }
   __device__ static uint32_t from_f(float v) { return BF ? f_to_bf16(v) : f_to_f16(v); }
@@ -208,6 +210,33 @@ template <>
 struct Io<half_t> : Io16<half_t, false> {};
 template <>
 struct Io<bf16_t> : Io16<bf16_t, true> {};
+
+// fp64 tensors: elements stay in double (the reference computes in the tensor's own type).
+template <>
+struct Io<double> {
+  using V = double;
+  static constexpr int E = 2;
+  __device__ static double ld(const double *p, int64_t i) { return p[i]; }
+  __device__ static void st(double *p, int64_t i, double v) { p[i] = v; }
+  __device__ static void unpack(const u4 &v, double (&a)[E]) {
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const unsigned lo = v[2 * k], hi = v[2 * k + 1];
+      a[k] = __builtin_bit_cast(double, (static_cast<unsigned long long>(hi) << 32) | lo);
+    }
+  }
+  __device__ static u4 pack(const double (&a)[E]) {
+    u4 v;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const unsigned long long b = __builtin_bit_cast(unsigned long long, a[k]);
+      v[2 * k] = static_cast<unsigned>(b);
+      v[2 * k + 1] = static_cast<unsigned>(b >> 32);
+    }
+    return v;
+  }
+  __device__ static double round(double v) { return v; }
+};
 
 // Rounding of an intermediate result to the internal type R, in R's compute type A.
 template <typename R>
@@ -327,9 +356,10 @@ struct Elem {
   // The tensor QuantDequantFunc receives: x, or torch.sub(x, scale, alpha=shift).  With a
   // 0-dim scale and R wider than T, type promotion keeps that subtraction in T (the scale
   // is rounded to T first); otherwise it runs in R.
-  __device__ static A shifted(float x, const Enc &e, const Params &p) {
+  __device__ static A shifted(typename Io<T>::V x, const Enc &e, const Params &p) {
     if (p.alpha == 0.0) return A(x);
-    if (p.scalar_scale) return A(Io<T>::round(fmaf(-static_cast<float>(p.alpha), e.s_io, x)));
+    if constexpr (std::is_same<typename Io<T>::V, float>::value)
+      if (p.scalar_scale) return A(Io<T>::round(fmaf(-static_cast<float>(p.alpha), e.s_io, x)));
     return r(fma_a(A(-p.alpha), e.s, A(x)));
   }
 
@@ -346,21 +376,29 @@ struct Elem {
   }
 };
 
-// Forward value of one element (as fp32; the store rounds it to T).
-template <int OP, typename T, typename R>
-__device__ __forceinline__ float fwd_elem(float x, const typename Elem<T, R>::Enc &e,
-                                          const Params &p) {
+// Forward value of one element (in the io type's value type V; the store rounds it to T).
+template <int OP, typename T, typename R, typename V = typename Io<T>::V>
+__device__ __forceinline__ V fwd_elem(V x, const typename Elem<T, R>::Enc &e, const Params &p) {
   using El = Elem<T, R>;
   using A = typename El::A;
   if constexpr (OP == OP_QDQ_LEARN) {
-    return static_cast<float>(El::unshift(El::qdq(El::shifted(x, e, p), e), e, p));
+    return static_cast<V>(El::unshift(El::qdq(El::shifted(x, e, p), e), e, p));
   } else if constexpr (OP == OP_QDQ_FROZEN) {
-    const float q = rintf(x * e.inv_s) + e.zp;
-    return (clamp_keep_nan(q, static_cast<float>(p.qmin), static_cast<float>(p.qmax)) - e.zp) *
-           e.fs;
+    if constexpr (std::is_same<V, double>::value) {
+      // torch's fake_quantize on an fp64 tensor: the code from x times the fp32 1 / scale in
+      // double, then the clamp, zero point and scale in fp32
+      const double qd = rint(x * static_cast<double>(e.inv_s)) + static_cast<double>(e.zp);
+      const float q = static_cast<float>(qd);
+      return static_cast<double>(
+          (clamp_keep_nan(q, static_cast<float>(p.qmin), static_cast<float>(p.qmax)) - e.zp) * e.fs);
+    } else {
+      const float q = rintf(x * e.inv_s) + e.zp;
+      return (clamp_keep_nan(q, static_cast<float>(p.qmin), static_cast<float>(p.qmax)) - e.zp) *
+             e.fs;
+    }
   } else if constexpr (OP == OP_Q) {
     const A t = El::r(A(x) / e.s);
-    return static_cast<float>(clamp_a(El::r(rint_a(t) - e.o), e.qmin, e.qmax));
+    return static_cast<V>(clamp_a(El::r(rint_a(t) - e.o), e.qmin, e.qmax));
   } else if constexpr (OP == OP_NATIVE) {
     // NaN kept; clip in value space (fmax(fmin(v, max), min)); times fl(1 / delta); round
     // half to even; times delta
@@ -368,17 +406,17 @@ __device__ __forceinline__ float fwd_elem(float x, const typename Elem<T, R>::En
     const float c = fmaxf(fminf(x, e.hi), e.lo);
     return rintf(c * e.inv_s) * e.fs;
   } else if constexpr (OP == OP_FP16) {
-    return static_cast<float>(static_cast<_Float16>(x));  // round to nearest even, and back
+    return static_cast<V>(static_cast<_Float16>(x));  // round to nearest even, and back
   } else {
-    return static_cast<float>(El::r(El::r(A(x) + e.o) * e.s));
+    return static_cast<V>(El::r(El::r(A(x) + e.o) * e.s));
   }
 }
 
 // One element of the backward: returns dx and adds this element's encoding-gradient terms
 // (as the reference rounds them, in R) to (ds, dof).
-template <int OP, typename T, typename R>
-__device__ __forceinline__ float bwd_elem(float x, float g, const typename Elem<T, R>::Enc &e,
-                                          const Params &p, double &ds, double &dof) {
+template <int OP, typename T, typename R, typename V = typename Io<T>::V>
+__device__ __forceinline__ V bwd_elem(V x, V g, const typename Elem<T, R>::Enc &e, const Params &p,
+                                      double &ds, double &dof) {
   using El = Elem<T, R>;
   using A = typename El::A;
   const A ga = A(g);
@@ -392,11 +430,16 @@ __device__ __forceinline__ float bwd_elem(float x, float g, const typename Elem<
     dof += static_cast<double>(El::r(ga * El::r(nm * e.s)));
     // the shift's own scale terms: +alpha*g from the add, -alpha*g*mask through the sub
     if (p.alpha != 0.0) ds += static_cast<double>(A(p.alpha)) * static_cast<double>(ga * nm);
-    return static_cast<float>(ga * m);
+    return static_cast<V>(ga * m);
   } else if constexpr (OP == OP_QDQ_FROZEN) {
-    const float q = rintf(x * e.inv_s) + e.zp;
-    const float m = (q >= p.qmin && q <= p.qmax) ? 1.0f : 0.0f;
-    return g * m;
+    if constexpr (std::is_same<V, double>::value) {
+      const double q = rint(x * static_cast<double>(e.inv_s)) + static_cast<double>(e.zp);
+      return (q >= p.qmin && q <= p.qmax) ? g : g * 0.0;
+    } else {
+      const float q = rintf(x * e.inv_s) + e.zp;
+      const float m = (q >= p.qmin && q <= p.qmax) ? 1.0f : 0.0f;
+      return g * m;
+    }
   } else if constexpr (OP == OP_Q) {
     const A t = El::r(A(x) / e.s);
     const A q = El::r(rint_a(t) - e.o);
@@ -408,12 +451,12 @@ __device__ __forceinline__ float bwd_elem(float x, float g, const typename Elem<
     const A xs = p.scalar_scale ? A(Io<T>::round(x / e.s_io)) : t;
     ds += static_cast<double>(El::r(-gs * xs));
     dof += static_cast<double>(-mg);
-    return static_cast<float>(gs);
+    return static_cast<V>(gs);
   } else {
     const A gs = El::r(ga * e.s);
     ds += static_cast<double>(El::r(ga * El::r(A(x) + e.o)));
     dof += static_cast<double>(gs);
-    return static_cast<float>(gs);
+    return static_cast<V>(gs);
   }
 }
 
@@ -498,7 +541,7 @@ struct FwdW {
   // pass, but leave the output in the caches to be written back during the next pass: a
   // forward + backward training step measured 255-263 us with them against 236-240 us.
   __device__ void compute(const Enc &e, const u4 &v, int64_t vi) const {
-    float a[E];
+    typename Io<T>::V a[E];
     Io<T>::unpack(v, a);
 #pragma unroll
     for (int k = 0; k < E; ++k) a[k] = fwd_elem<OP, T, R>(a[k], e, p);
@@ -546,7 +589,7 @@ struct BwdW {
   }
   __device__ void compute(const Enc &e, const u4 &xv, const u4 &gv, int64_t vi,
                           Acc &acc) const {
-    float a[E], b[E];
+    typename Io<T>::V a[E], b[E];
     Io<T>::unpack(xv, a);
     Io<T>::unpack(gv, b);
 #pragma unroll
@@ -601,12 +644,16 @@ struct MinMaxW {
       acc.mx = nan_max(acc.mx, v);
     }
   }
-  __device__ void elem(const Enc &, int64_t i, Acc &acc) const { take(acc, Io<T>::ld(x, i)); }
+  // fp64 values are rounded to fp32 first: rounding is monotone, so the fp32 min / max equal
+  // the rounded fp64 min / max (the statistics are fp32)
+  __device__ void elem(const Enc &, int64_t i, Acc &acc) const {
+    take(acc, static_cast<float>(Io<T>::ld(x, i)));
+  }
   __device__ static void take_vec(const u4 &v, Acc &acc) {
-    float a[E];
+    typename Io<T>::V a[E];
     Io<T>::unpack(v, a);
 #pragma unroll
-    for (int k = 0; k < E; ++k) take(acc, a[k]);
+    for (int k = 0; k < E; ++k) take(acc, static_cast<float>(a[k]));
   }
   __device__ void vec1(const Enc &, int64_t vi, Acc &acc) const {
     take_vec(__builtin_nontemporal_load(reinterpret_cast<const u4 *>(x) + vi), acc);
@@ -852,6 +899,10 @@ static int run_typed(const Call &c, int what) {
                                 : run_backward<OP_QDQ_FROZEN, T, float>(c);
   if (c.op == OP_DQ)  // DequantizeFunc runs in the tensor's own type
     return what == WHAT_FORWARD ? run_forward<OP_DQ, T, T>(c) : run_backward<OP_DQ, T, T>(c);
+  if constexpr (std::is_same<T, double>::value) {
+    if (c.internal != RXMET_QDQ_F64) return -22;  // an fp64 tensor computes in fp64
+    return go(double{});
+  }
   switch (c.internal) {
     case RXMET_QDQ_F64:
       return go(double{});
@@ -867,6 +918,7 @@ static int run_typed(const Call &c, int what) {
 int run_f32(const Call &c, int what);
 int run_f16(const Call &c, int what);
 int run_bf16(const Call &c, int what);
+int run_f64(const Call &c, int what);
 
 // Where a TF-scheme quantizer's statistics update lands (ONNX Runtime op): the running
 // min / max (replaced after a reset), and with enc set the TfEncodings derived from them.

@@ -127,7 +127,7 @@ def reshape_tensor_for_blocks(tensor, encoding_shape, block_size):
 # view (encoding c0 * C1 + c1 of row-major element (o, c0, m, c1, k)).
 # ---------------------------------------------------------------------------------
 
-_IO_CODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+_IO_CODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2, torch.float64: 3}
 _INTERNAL_CODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2, torch.float64: 3}
 
 
@@ -210,7 +210,8 @@ def _require(tensor: torch.Tensor, what: str):
         raise RuntimeError(f"mi355x backend: {what} must be a GPU tensor")
     if tensor.dtype not in _IO_CODE:
         raise NotImplementedError(
-            f"mi355x backend: {what} must be float32, float16 or bfloat16 (got {tensor.dtype})")
+            f"mi355x backend: {what} must be float32, float16, bfloat16 or float64 "
+            f"(got {tensor.dtype})")
 
 
 def _numerics(io: torch.dtype, internal: torch.dtype, shift: float = 0.0,

@@ -261,6 +261,9 @@ BACKEND_CASES = [  # tensor dtype, grid, scale shape, tensor shape
     (torch.float32, (-128, 127), (), (64, 257)),
     (torch.float32, (-(1 << 22), (1 << 22) - 1), (), (64, 257)),
     (torch.float16, (-8, 7), (4, 1, 8), (4, 33, 8)),
+    (torch.float64, (-128, 127), (), (64, 257)),
+    (torch.float64, (-8, 7), (64, 1), (64, 257)),
+    (torch.float64, (-(1 << 22), (1 << 22) - 1), (1, 257), (64, 257)),
 ]
 
 
@@ -376,6 +379,71 @@ def test_frozen_fast_path_matches_torch_fake_quantize(cuda, dtype, per_channel):
     zp = 3 if not per_channel else 0
     assert y[0, 1].item() == torch.tensor((127 - zp) * s0).to(dtype).item()
     assert y[0, 2].item() == torch.tensor((-128 - zp) * s0).to(dtype).item()
+
+
+@pytest.mark.parametrize("per_channel", [False, True])
+def test_frozen_fast_path_on_fp64_matches_torch_fake_quantize(cuda, per_channel):
+    """Frozen encodings on an fp64 tensor: the reference's torch.fake_quantize on the GPU
+    (aten's kernel: x times the fp32 1 / scale and its rounding in fp64, the clamp, zero point
+    and scale in fp32), NaN restored.  Checked against that very kernel."""
+    gen = torch.Generator().manual_seed(5)
+    x = (torch.randn(96, 1000, generator=gen, dtype=torch.float64) * 2).to(cuda)
+    x[0, :1] = float("nan")
+    if per_channel:
+        scale = (torch.rand(96, 1, generator=gen) * 0.05 + 0.01).to(cuda)
+        offset = torch.zeros(96, 1, device=cuda)
+        ref = torch.fake_quantize_per_channel_affine(
+            x, scale.flatten(), torch.zeros(96, dtype=torch.int32, device=cuda), 0, -128, 127)
+    else:
+        scale = torch.tensor(0.0173, device=cuda)
+        offset = torch.tensor(-3.0, device=cuda)
+        ref = torch.fake_quantize_per_tensor_affine(
+            x, scale, torch.tensor(3, dtype=torch.int32, device=cuda), -128, 127)
+    ref = ref.masked_fill_(torch.isnan(x), float("nan"))
+    y = Q.quantize_dequantize(x, scale, offset, -128, 127)
+    assert y.dtype == torch.float64
+    assert torch.equal(torch.isnan(y), torch.isnan(x))
+    fin = torch.isfinite(x)
+    assert torch.equal(y[fin], ref[fin])
+    # the gradient is the fake_quantize mask
+    xs = x.clone().requires_grad_(True)
+    g = torch.randn(x.shape, generator=gen, dtype=torch.float64).to(cuda)
+    Q.quantize_dequantize(xs, scale, offset, -128, 127).backward(g)
+    xr = x.clone().requires_grad_(True)
+    if per_channel:
+        torch.fake_quantize_per_channel_affine(
+            xr, scale.flatten(), torch.zeros(96, dtype=torch.int32, device=cuda), 0, -128,
+            127).backward(g)
+    else:
+        torch.fake_quantize_per_tensor_affine(
+            xr, scale, torch.tensor(3, dtype=torch.int32, device=cuda), -128, 127).backward(g)
+    assert torch.equal(xs.grad[fin], xr.grad[fin])
+
+
+def test_fp64_module_forward_backward_matches_torch_reference(cuda):
+    """aimet's QuantizeDequantize on an fp64 input (fp32 learnable min / max): the tensor
+    computes in fp64, as the reference's backend does; checked against the reference's
+    operations run by torch on the GPU with the module's own encodings."""
+    import aimet_affine as A
+
+    gen = torch.Generator().manual_seed(9)
+    x = (torch.randn(64, 300, generator=gen, dtype=torch.float64) * 1.3).to(cuda)
+    g = torch.randn(64, 300, generator=gen, dtype=torch.float64).to(cuda)
+    for shape, bits, sym in (((), 8, False), ((64, 1), 4, True)):
+        q = A.QuantizeDequantize(shape, bits, sym).to(cuda)
+        with q.compute_encodings():
+            q(x)
+        xs = x.clone().requires_grad_(True)
+        y = q(xs)
+        y.backward(g)
+        assert y.dtype == torch.float64 and xs.grad.dtype == torch.float64
+        scale, offset = q.get_scale().detach(), q.get_offset().detach()
+        xr = x.clone().requires_grad_(True)
+        yr = _torch_reference(xr, scale, offset, q.qmin, q.qmax, 0.0)
+        yr.backward(g)
+        assert torch.equal(torch.isnan(y), torch.isnan(yr))
+        assert torch.equal(y.detach(), yr.detach()), (shape, bits)
+        assert torch.equal(xs.grad, xr.grad), (shape, bits)
 
 
 def test_backend_quantize_dequantize_16bit(cuda):
