@@ -65,39 +65,6 @@ __device__ __forceinline__ Acc fold_strided(const Acc *__restrict__ partial, con
   return a;
 }
 
-// Rounding of a folded encoding gradient to the internal type (0: fp32, 1: fp16, 2: bf16),
-// as the reference's gradient tensors carry it.
-__device__ __forceinline__ float round_internal(float v, int round16) {
-  if (round16 == 1) return Io<half_t>::round(v);
-  if (round16 == 2) return Io<bf16_t>::round(v);
-  return v;
-}
-
-// Folded encoding gradients, written as the gradients of scale and offset.
-struct PutScaleOffset {
-  float *dscale, *doffset;
-  int round16;
-  __device__ void operator()(const Sum2 &v, int64_t c) const {
-    if (dscale) dscale[c] = round_internal(static_cast<float>(v.a), round16);
-    if (doffset) doffset[c] = round_internal(static_cast<float>(v.b), round16);
-  }
-};
-
-// Folded encoding gradients taken on to the min / max they were derived from.
-struct PutMinMaxGrad {
-  MinMaxSrc mm;
-  float *d_min, *d_max;
-  int round16;
-  __device__ void operator()(const Sum2 &v, int64_t c) const {
-    const float gs = round_internal(static_cast<float>(v.a), round16);
-    const float go = round_internal(static_cast<float>(v.b), round16);
-    float a, b;
-    minmax_encoding_grad(mm, c, gs, &go, a, b);
-    d_min[c] = a;
-    d_max[c] = b;
-  }
-};
-
 // Folded min / max written out.
 struct PutMinMax {
   float *out_min, *out_max;
@@ -263,8 +230,17 @@ static Plan make_plan(int64_t outer, int64_t C0, int64_t mid, int64_t C1, int64_
   const int64_t chunk = int64_t(kThreads) * vec * (16 / esize);
   if ((C0 == 1 && C1 == 1) || inner >= kMinRun) {
     p.kind = KIND_RUNS;
-    p.splits = inner > 0 ? (inner + chunk - 1) / chunk : 1;
+    // many encodings of one run each, runs of a few chunks: whole runs per workgroup; one
+    // long run (the forward / backward passes): two chunks per workgroup
+    const int64_t nchunks = inner > 0 ? (inner + chunk - 1) / chunk : 1;
+    if (outer * mid == 1 && p.runs >= kWholeRunMinRuns && nchunks > 1 &&
+        nchunks <= kWholeRunChunks)
+      p.passes = static_cast<int>(nchunks);
+    else if (p.runs == 1 && vec == kVecQdq && nchunks >= kSingleRunMinChunks)
+      p.passes = kSingleRunPasses;
+    p.splits = (nchunks + p.passes - 1) / p.passes;
     p.partial_slots = p.runs * p.splits;
+    p.direct = p.splits == 1 && outer * mid == 1;
     p.fold = FoldMap{outer, mid, p.splits, C0 * mid * C1 * p.splits, C1 * p.splits, 1,
                      C1, mid * C1 * p.splits, p.splits};
   } else if (inner >= kMinSeg) {
@@ -428,16 +404,22 @@ static int backward_impl(int op, const void *x, const void *g, void *dx, float *
   }
   RXMET_CHECK_ARG(x != nullptr && g != nullptr && dx != nullptr, "x, g and dx must be non-null");
   if (enc) RXMET_CHECK_ARG(workspace != nullptr, "encoding gradients need a workspace");
-  const Call c{&p, op, nm->internal_dtype, x, g, dx, scale, offset,
-               make_params(qmin, qmax, *nm), enc ? workspace : nullptr, s,
-               mm ? *mm : MinMaxSrc{}};
+  Call c{&p, op, nm->internal_dtype, x, g, dx, scale, offset,
+         make_params(qmin, qmax, *nm), enc ? workspace : nullptr, s,
+         mm ? *mm : MinMaxSrc{}};
+  const int32_t r = arithmetic_type(op, *nm);
+  const int round16 = r == RXMET_QDQ_F16 ? 1 : (r == RXMET_QDQ_BF16 ? 2 : 0);
+  if (enc && p.kind == KIND_RUNS && p.direct) {
+    c.ff.direct = 1;
+    c.ff.use_mm = mm != nullptr;
+    c.ff.so = PutScaleOffset{dscale, doffset, round16};
+    if (mm != nullptr) c.ff.mg = PutMinMaxGrad{*mm, d_min, d_max, round16};
+  }
   {
     rxmet::prof::Scope ps__("qdq_backward_stream", s);
     if (int rc = dispatch(c, nm->io_dtype, WHAT_BACKWARD)) return rc;
   }
-  if (enc) {
-    const int32_t r = arithmetic_type(op, *nm);
-    const int round16 = r == RXMET_QDQ_F16 ? 1 : (r == RXMET_QDQ_BF16 ? 2 : 0);
+  if (enc && !c.ff.direct) {
     rxmet::prof::Scope ps__("qdq_backward_fold", s);
     const Sum2 *ws = static_cast<const Sum2 *>(workspace);
     if (mm != nullptr)
@@ -582,7 +564,8 @@ int64_t rxmet_qdq_workspace_bytes_ex(const rxmet_qdq_layout *l, int32_t io_dtype
   if (l == nullptr || !is_io(io_dtype) || l->outer < 0 || l->mid < 0 || l->inner < 0 ||
       l->C0 < 1 || l->C1 < 1)
     return 0;
-  // the forward / backward passes' chunks are the smaller ones, so they have the most partials
+  // the forward / backward plan has at least as many partials as the min / max plan (its
+  // chunks are half as long; it takes two per workgroup only where min / max takes one)
   const Plan p = make_plan(l->outer, l->C0, l->mid, l->C1, l->inner, esize_of(io_dtype), kVecQdq);
   return p.partial_slots * static_cast<int64_t>(sizeof(Sum2));
 }

@@ -23,7 +23,8 @@
 //          rows of one band, several rows in parallel when the matrix is narrow.
 // Reductions write one fp64 (or min/max) partial per workgroup, run or column chunk; a
 // second kernel folds the partials of each encoding in a fixed order, so results are
-// deterministic and need no atomics.
+// deterministic and need no atomics.  A backward whose workgroups each hold one whole
+// encoding (per-channel runs of a few chunks) writes the encoding gradients itself.
 #pragma once
 
 #include <stdint.h>
@@ -114,6 +115,17 @@ constexpr int kVecMinMax = 8;
 constexpr int64_t kMinRun = 1024;  // runs at least this long use the runs decomposition
 constexpr int64_t kMinSeg = 16;    // shorter runs use the column decomposition
 constexpr int kColTargetBlocks = 2048;
+// Runs decomposition with many encodings (at least kWholeRunMinRuns runs, one per encoding):
+// a run of up to kWholeRunChunks chunks is one workgroup's, so its encoding gradients are
+// complete in that workgroup and no fold follows.  One long run (a single encoding, at least
+// kSingleRunMinChunks chunks): kSingleRunPasses chunks per workgroup, interleaved.  Measured on
+// c2 as a QuantizeDequantize training step, per tensor: 232 us with 2 chunks against 236
+// with 1, 236 with 4 and 241 with 8 (the separate fold kernel reads half the partials); per
+// channel with whole rows (two chunks): 226 us against 231 with one chunk per workgroup.
+constexpr int kWholeRunChunks = 4;
+constexpr int64_t kWholeRunMinRuns = 1024;
+constexpr int kSingleRunPasses = 2;
+constexpr int64_t kSingleRunMinChunks = 2048;
 
 typedef unsigned int u4 __attribute__((ext_vector_type(4)));
 
@@ -485,6 +497,54 @@ __device__ __forceinline__ MinMax acc_shfl(const MinMax &x, int off) {
   return MinMax{__shfl_xor(x.mn, off, kWave), __shfl_xor(x.mx, off, kWave)};
 }
 
+// Rounding of a folded encoding gradient to the internal type (0: fp32, 1: fp16, 2: bf16),
+// as the reference's gradient tensors carry it.
+__device__ __forceinline__ float round_internal(float v, int round16) {
+  if (round16 == 1) return Io<half_t>::round(v);
+  if (round16 == 2) return Io<bf16_t>::round(v);
+  return v;
+}
+
+// Folded encoding gradients, written as the gradients of scale and offset.
+struct PutScaleOffset {
+  float *dscale, *doffset;
+  int round16;
+  __device__ void operator()(const Sum2 &v, int64_t c) const {
+    if (dscale) dscale[c] = round_internal(static_cast<float>(v.a), round16);
+    if (doffset) doffset[c] = round_internal(static_cast<float>(v.b), round16);
+  }
+};
+
+// Folded encoding gradients taken on to the min / max they were derived from.
+struct PutMinMaxGrad {
+  MinMaxSrc mm;
+  float *d_min, *d_max;
+  int round16;
+  __device__ void operator()(const Sum2 &v, int64_t c) const {
+    const float gs = round_internal(static_cast<float>(v.a), round16);
+    const float go = round_internal(static_cast<float>(v.b), round16);
+    float a, b;
+    minmax_encoding_grad(mm, c, gs, &go, a, b);
+    d_min[c] = a;
+    d_max[c] = b;
+  }
+};
+
+// A backward launch with encoding gradients completes them by a separate fold kernel over the
+// partials, or (direct: one workgroup per encoding) each workgroup writes its own encoding's.
+struct FusedFold {
+  int direct;
+  int use_mm;  // min / max gradients instead of scale / offset gradients
+  PutScaleOffset so;
+  PutMinMaxGrad mg;
+  __device__ void put(const Sum2 &v, int64_t c) const {
+    if (use_mm)
+      mg(v, c);
+    else
+      so(v, c);
+  }
+};
+
 // Whole-block reduction; thread 0 ends with the block's value (fixed order).
 template <typename Acc>
 __device__ __forceinline__ void block_reduce(Acc &a) {
@@ -509,6 +569,7 @@ struct FwdW {
   using Enc = typename El::Enc;
   using Acc = Sum2;  // unused
   static constexpr bool kReduce = false;
+  static constexpr bool kFold = false;
   static constexpr int E = Io<T>::E;
   static constexpr int V = kVecQdq;
   const T *x;
@@ -573,6 +634,7 @@ struct BwdW {
   using Enc = typename El::Enc;
   using Acc = Sum2;
   static constexpr bool kReduce = ENC;
+  static constexpr bool kFold = ENC;
   static constexpr int E = Io<T>::E;
   static constexpr int V = kVecQdq;
   const T *x, *g;
@@ -580,6 +642,7 @@ struct BwdW {
   const float *scale, *offset;
   Params p;
   MinMaxSrc mm;
+  FusedFold ff;  // how the encoding gradients complete (ENC)
 
   __device__ Enc enc(int64_t c) const { return El::enc(scale, offset, mm, c, p); }
   __device__ static Acc zero() { return Sum2{0.0, 0.0}; }
@@ -629,6 +692,7 @@ struct MinMaxW {
   struct Enc {};
   using Acc = MinMax;
   static constexpr bool kReduce = true;
+  static constexpr bool kFold = false;
   static constexpr int E = Io<T>::E;
   static constexpr int V = kVecMinMax;
   const T *x;
@@ -691,26 +755,40 @@ struct ColGeo {
   int kt_shift;                    // log2 of the threads per row (the rest walk rows)
 };
 
-// runs: block b handles chunk (b % splits) of run (b / splits); one partial per block.
+// runs: block b handles chunks sp, sp + splits, ... (`passes` of them, sp = b % splits) of
+// run b / splits, so that the blocks in flight read adjacent memory; one partial per block,
+// or (kFold, direct) the block's encoding gradients.
 template <class W>
-__global__ __launch_bounds__(kThreads) void k_runs(W w, Geo geo, int64_t splits, int vec,
+__global__ __launch_bounds__(kThreads) void k_runs(W w, Geo geo, int64_t splits, int passes,
+                                                   int vec,
                                                    typename W::Acc *__restrict__ partial) {
   constexpr int64_t kChunk = int64_t(kThreads) * W::V * W::E;
   const int64_t b = blockIdx.x;
   const int64_t run = b / splits, sp = b % splits;
-  const auto e = w.enc(enc_of_run(geo, run));
-  const int64_t beg = sp * kChunk;
-  const int64_t end = min(geo.inner, beg + kChunk);
-  const int64_t base = run * geo.inner + beg;
+  const int64_t c = enc_of_run(geo, run);
+  const auto e = w.enc(c);
+  const int64_t first = sp * kChunk, step = kChunk * splits;
+  const int64_t rb = run * geo.inner;
   typename W::Acc acc = W::zero();
-  if (vec) {
-    w.vec_block(e, base / W::E, static_cast<int>((end - beg) / W::E), acc);
-  } else {
-    const int n = static_cast<int>(end - beg);
-    for (int i = threadIdx.x; i < n; i += kThreads) w.elem(e, base + i, acc);
+  for (int q = 0; q < passes; ++q) {
+    const int64_t beg = first + q * step;
+    if (beg >= geo.inner) break;
+    const int64_t end = min(geo.inner, beg + kChunk);
+    if (vec) {
+      w.vec_block(e, (rb + beg) / W::E, static_cast<int>((end - beg) / W::E), acc);
+    } else {
+      const int n = static_cast<int>(end - beg);
+      for (int i = threadIdx.x; i < n; i += kThreads) w.elem(e, rb + beg + i, acc);
+    }
   }
   if constexpr (W::kReduce) {
     block_reduce(acc);
+    if constexpr (W::kFold) {
+      if (w.ff.direct) {
+        if (threadIdx.x == 0) w.ff.put(acc, c);
+        return;
+      }
+    }
     if (threadIdx.x == 0) partial[b] = acc;
   }
 }
@@ -792,6 +870,8 @@ struct Plan {
   int64_t outer = 0, C0 = 1, mid = 1, C1 = 1, inner = 0;  // normalized layout
   int64_t n = 0;                                           // elements
   int64_t runs = 0, splits = 0;                            // runs / segs
+  int passes = 1;                                          // runs: chunks per block
+  bool direct = false;  // runs: one block per encoding (its gradients need no fold)
   Geo geo{};
   ColGeo cg{};
   int64_t col_blocks = 0;
@@ -811,6 +891,7 @@ struct Call {
   void *partial;           // Sum2 / MinMax partials, or null
   hipStream_t stream;
   MinMaxSrc mm;            // mm.mn != null: encodings derived from min / max in the kernels
+  FusedFold ff;            // backward with encoding gradients: how they complete
 };
 
 template <class W>
@@ -821,7 +902,7 @@ static int launch_decomp(const Plan &pl, const W &w, bool aligned, void *partial
   const bool vec = aligned && pl.inner % W::E == 0;
   if (pl.kind == KIND_RUNS) {
     hipLaunchKernelGGL(k_runs<W>, dim3(static_cast<unsigned>(pl.runs * pl.splits)),
-                       dim3(kThreads), 0, s, w, pl.geo, pl.splits, int(vec), part);
+                       dim3(kThreads), 0, s, w, pl.geo, pl.splits, pl.passes, int(vec), part);
   } else if (pl.kind == KIND_SEGS) {
     const int64_t nv = vec ? pl.inner / W::E : pl.inner;
     int shift = 0;
@@ -856,7 +937,7 @@ static int run_backward(const Call &c) {
   const bool al = aligned16(c.x) && aligned16(c.g) && aligned16(c.out);
   if (c.partial) {
     BwdW<OP, T, R, true> w{static_cast<const T *>(c.x), static_cast<const T *>(c.g),
-                           static_cast<T *>(c.out), c.scale, c.offset, c.p, c.mm};
+                           static_cast<T *>(c.out), c.scale, c.offset, c.p, c.mm, c.ff};
     return launch_decomp(*c.plan, w, al, c.partial, c.stream);
   }
   BwdW<OP, T, R, false> w{static_cast<const T *>(c.x), static_cast<const T *>(c.g),

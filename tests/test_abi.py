@@ -38,11 +38,15 @@ def test_python_signatures_cover_headers():
 def test_host_only_calls_work_without_gpu():
     lib = rxmet_lib.load()
     assert lib.rxmet_abi_version() >= 1
-    # [8192, 8192] per-channel on dim 0: a 4096-element chunk per block (256 threads x four
-    # 16-byte vectors of fp32), two partials of 16 bytes per channel row; per-tensor the same
-    # 16384 chunks
-    assert lib.rxmet_qdq_workspace_bytes(1, 8192, 8192) == 8192 * 2 * 16
-    assert lib.rxmet_qdq_workspace_bytes(1, 1, 8192 * 8192) == 16384 * 16
+    # [8192, 8192] per-channel on dim 0: 4096-element chunks (256 threads x four 16-byte vectors
+    # of fp32); 8192 rows of two chunks are one workgroup each, one 16-byte partial per row.
+    # Per-tensor: 16384 chunks, two per workgroup
+    assert lib.rxmet_qdq_workspace_bytes(1, 8192, 8192) == 8192 * 16
+    assert lib.rxmet_qdq_workspace_bytes(1, 1, 8192 * 8192) == 8192 * 16
+    # 64 rows: too few for whole-row workgroups, two chunks per row
+    assert lib.rxmet_qdq_workspace_bytes(1, 64, 8192) == 64 * 2 * 16
+    # per-tensor below 2048 chunks: one chunk per workgroup
+    assert lib.rxmet_qdq_workspace_bytes(1, 1, 4096 * 2047) == 2047 * 16
 
 
 def test_noalloc_backward_rejects_layouts_beyond_its_scratch():

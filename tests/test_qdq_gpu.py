@@ -93,6 +93,61 @@ def test_forward_backward_match_oracle(cuda, layout, grid, mode):
         np.testing.assert_allclose(do.cpu().numpy(), edo, rtol=1e-6, atol=1e-6, equal_nan=True)
 
 
+def _backward(cuda, x, g, s, o, layout, qmin, qmax):
+    xd, gd, sd, od = _t(x, cuda), _t(g, cuda), _t(s, cuda), _t(o, cuda)
+    C = layout[1]
+    dx, ds, do = torch.empty_like(xd), torch.empty(C, device=cuda), torch.empty(C, device=cuda)
+    rxmet_lib.call("rxmet_qdq_backward", xd.data_ptr(), gd.data_ptr(), dx.data_ptr(),
+                   ds.data_ptr(), do.data_ptr(), *layout, sd.data_ptr(), od.data_ptr(), qmin,
+                   qmax, Q.LEARNABLE, _ws(layout, cuda).data_ptr(), _stream(cuda))
+    torch.cuda.synchronize()
+    return dx, ds, do
+
+
+# Plans of the c2 shapes: per-channel rows of 2, 3 and 4 chunks held whole by one workgroup
+# (1024+ rows; the workgroup writes its encoding gradients, no fold), and single runs of 2048+
+# chunks taken two interleaved chunks per workgroup (the last chunk partial: 16-byte vector
+# path, and the element path of an odd length)
+FOLD_LAYOUTS = [(1, 1024, 8192), (1, 1030, 12284), (1, 1024, 16384), (1, 1, 4096 * 2051 + 8),
+                (1, 1, 4096 * 2049 + 7)]
+
+
+@pytest.mark.parametrize("layout", FOLD_LAYOUTS)
+def test_whole_run_and_two_chunk_plans_match_oracle(cuda, layout):
+    qmin, qmax = -128, 127
+    n = int(np.prod(layout))
+    print(f"[qdq] plan layout={layout}", flush=True)
+    x, g = _data(n, 41), np.random.default_rng(42).standard_normal(n).astype(f32)
+    s, o = _enc(layout[1], 43, qmin, qmax, False)
+    xd, sd, od = _t(x, cuda), _t(s, cuda), _t(o, cuda)
+    y = torch.empty_like(xd)
+    rxmet_lib.call("rxmet_qdq_forward", xd.data_ptr(), y.data_ptr(), *layout, sd.data_ptr(),
+                   od.data_ptr(), qmin, qmax, Q.LEARNABLE, _stream(cuda))
+    dx, ds, do = _backward(cuda, x, g, s, o, layout, qmin, qmax)
+    ey, _ = O.qdq_learnable(x, s, o, qmin, qmax, layout)
+    edx, eds, edo = O.qdq_learnable_backward(x, g, s, o, qmin, qmax, layout)
+    np.testing.assert_array_equal(y.cpu().numpy(), ey)
+    np.testing.assert_array_equal(dx.cpu().numpy(), edx)
+    np.testing.assert_allclose(ds.cpu().numpy(), eds, rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(do.cpu().numpy(), edo, rtol=1e-6, atol=1e-6)
+
+
+def test_per_tensor_encoding_gradients_at_scale(cuda):
+    """Per-tensor over 20000 chunks (10000 workgroups of two interleaved chunks, folded by the
+    1024-thread fold): the tensor repeats one 16384-element block 5000 times, so its encoding
+    gradients are 5000 times the oracle's over the block, and dx is the block's dx repeated."""
+    qmin, qmax = -128, 127
+    blk, reps = 16384, 5000
+    xb, gb = _data(blk, 51), np.random.default_rng(52).standard_normal(blk).astype(f32)
+    s, o = _enc(1, 53, qmin, qmax, False)
+    edx, eds, edo = O.qdq_learnable_backward(xb, gb, s, o, qmin, qmax, (1, 1, blk))
+    dx, ds, do = _backward(cuda, np.tile(xb, reps), np.tile(gb, reps), s, o,
+                           (1, 1, blk * reps), qmin, qmax)
+    assert torch.equal(dx.view(reps, blk), _t(edx, cuda).expand(reps, blk))
+    np.testing.assert_allclose(ds.cpu().numpy(), eds.astype(np.float64) * reps, rtol=1e-6)
+    np.testing.assert_allclose(do.cpu().numpy(), edo.astype(np.float64) * reps, rtol=1e-6)
+
+
 @pytest.mark.parametrize("layout", LAYOUTS)
 def test_minmax_matches_oracle(cuda, layout):
     outer, C, inner = layout
