@@ -312,19 +312,21 @@ INT8_MFMA_PEAK = 5000.0
 BF16_MFMA_PEAK = 2500.0
 
 
-def _gru_kernel_work(B, T, I, H, D=2):
-    """Algorithmic FLOPs per step of the instrumented c3 kernels (D directions): GEMM FLOPs
+def _gru_kernel_work(B, T, I, H, D=2, stepped_bwd=False):
+    """Algorithmic FLOPs per step of the instrumented GRU kernels (D directions): GEMM FLOPs
     2*M*N*K as counted for the metric; peaks are MI355X's dense figures in TFLOP/s."""
     C = 3 * H
     M = T * B
+    dirs = "both directions in one clustered launch" if D == 2 else "one clustered launch"
+    bwd = ("one direction, stepped: per time step one dh GEMM launch (bf16 MFMA: dq split into "
+           "three bf16 terms against the R codes) and one pointwise launch" if stepped_bwd else
+           f"{dirs} (bf16 MFMA: dq split into three bf16 terms against the R codes)")
     return {
         "gru_fwd_recurrence": (D * 2.0 * M * H * C, INT8_MFMA_PEAK,
-                               "recurrent GEMM R_q.h_q over T steps, both directions in one "
-                               "clustered launch (int8 MFMA, 16-bit h as two byte planes)"),
+                               f"recurrent GEMM R_q.h_q over T steps, {dirs} (int8 MFMA, 16-bit "
+                               "h as two byte planes)"),
         "gru_bwd_recurrence": (D * 2.0 * M * H * C, BF16_MFMA_PEAK,
-                               "dh GEMM R_deq.dq over T steps, both directions in one clustered "
-                               "launch (bf16 MFMA: dq split into three bf16 terms against the "
-                               "R codes)"),
+                               f"dh GEMM R_deq.dq over T steps, {bwd}"),
         "gru_bwd_weight_gemms": (D * 2.0 * M * C * (2 * I + H), BF16_MFMA_PEAK,
                                  "dx, dW, dR GEMMs (float gradient split into three bf16 "
                                  "terms against exact bf16 code planes, MFMA)"),
@@ -594,7 +596,9 @@ def _gru_c5_leg(torch, steps: int, warmup: int):
         out.mean().backward()
 
     dt, p50, p95, kernels, roof = _timed_steps(torch, step, steps, warmup,
-                                               _gru_kernel_work(B, T, I, H, D=1))
+                                               _gru_kernel_work(B, T, I, H, D=1,
+                                                                stepped_bwd=True),
+                                               traffic_prefix="c5_")
     _log(f"gru c5: {dt*1e3:.2f} ms/step wall, P50 {p50:.2f} ms, {B/dt:.1f} seq/s")
     for k, v in sorted(kernels.items(), key=lambda kv: -kv[1]["ms_per_step"]):
         _log(f"  {k}: {v['ms_per_step']:.3f} ms/step, {v['us_per_launch']:.1f} us/launch")
@@ -622,7 +626,7 @@ def _lstm_kernel_work(B, T, I, H):
     }
 
 
-def _timed_steps(torch, step, steps, warmup, work, timed=None):
+def _timed_steps(torch, step, steps, warmup, work, timed=None, traffic_prefix=""):
     """Run warmup + timed steps; per-step events, per-kernel library timings, roofline of the
     dominant instrumented kernel.
 
@@ -681,7 +685,8 @@ def _timed_steps(torch, step, steps, warmup, work, timed=None):
     flops = flops_step / live[dom]["launches_per_step"]
     achieved = flops / (live[dom]["us_per_launch"] * 1e-6) / 1e12
     roof = {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 3), "peak": peak,
-            "unit": "TFLOP/s", "frac": round(achieved / peak, 6), "traffic": _traffic(dom),
+            "unit": "TFLOP/s", "frac": round(achieved / peak, 6),
+            "traffic": _traffic(traffic_prefix + dom),
             "algorithmic_flops_per_launch": flops, "work": what,
             "us_per_launch": round(live[dom]["us_per_launch"], 2)}
     return dt, p50, p95, kernels, roof
@@ -1047,7 +1052,7 @@ def _calib_leg(torch, steps: int, warmup: int):
                 gemm: (D * 2.0 * M * C * I, FP32_MFMA_PEAK,
                        "input projection x W of every direction (fp32 MFMA, statistics fused)")}
         dt, p50, p95, kernels, roof = _timed_steps(torch, step, steps, warmup, work,
-                                                   timed=[rec])
+                                                   timed=[rec], traffic_prefix=f"{name}_")
         _log(f"calibration {name}: {dt*1e3:.3f} ms/step wall, P50 {p50:.3f} ms, {B/dt:.1f} "
              f"seq/s; " + ", ".join(f"{k} {v['ms_per_step']:.3f} ms/step"
                                     for k, v in kernels.items()))
@@ -1056,7 +1061,8 @@ def _calib_leg(torch, steps: int, warmup: int):
                      "kernels_ms_per_step": {k: round(v["ms_per_step"], 4)
                                              for k, v in kernels.items()},
                      "recurrence_roofline": {k: roof[k] for k in ("achieved", "peak", "unit",
-                                                                  "frac", "us_per_launch")}}
+                                                                  "frac", "us_per_launch",
+                                                                  "traffic")}}
         keep[name] = (kind, m, x)
     return res, keep
 

@@ -686,11 +686,15 @@ __global__ __launch_bounds__(64 * MAXW) void calib_recurrence_mt(CalClArgs a) {
   }
 }
 
+// Rows of W and R (concatenated) per workgroup of the parameter ranges.
+constexpr int kPrmRows = 64;
+
 struct CalWorkspace {
-  size_t ord, wx, hx, part, sync, total;
+  size_t ord, wx, hx, part, sync, prm, total;
   int Bpad, Hpad, ntiles;
   int64_t nparts;
-  CalWorkspace(int T, int B, int H) {
+  int prm_slabs;
+  CalWorkspace(int T, int B, int I, int H) {
     auto al = [](size_t v) { return (v + 255) & ~static_cast<size_t>(255); };
     ntiles = (B + kCT - 1) / kCT;
     Bpad = ntiles * kCT;
@@ -705,6 +709,8 @@ struct CalWorkspace {
     hx = o; o += al(sizeof(float) * 2 * static_cast<size_t>(Bpad) * Hpad);
     part = o; o += al(sizeof(float) * static_cast<size_t>(nparts));
     sync = o; o += al(sizeof(unsigned) * cluster::kCounterStride * (ntiles + 2));
+    prm_slabs = (I + H + kPrmRows - 1) / kPrmRows;
+    prm = o; o += al(sizeof(float) * 4 * static_cast<size_t>(prm_slabs) * 3 * H);
     total = o;
   }
 };
@@ -716,7 +722,7 @@ static int calibrate_mfma(int T, int B, int I, int H, const float *W, const floa
                           const float *bw, const float *br, const float *x, const float *h0,
                           float *h, float *v, void *workspace, hipStream_t stream) {
   if (H % 16 != 0 || H > 1024 || std::getenv("RXMET_NO_CLUSTER") != nullptr) return 0;
-  const CalWorkspace ws(T, B, H);
+  const CalWorkspace ws(T, B, I, H);
   if (2.0 * ws.Bpad * ws.Hpad * 4 >= 2147483648.0) return 0;  // 32-bit exchange offsets
   CalClArgs a{};
   a.T = T; a.B = B; a.H = H;
@@ -830,28 +836,80 @@ static int calibrate_mfma(int T, int B, int I, int H, const float *W, const floa
   return 1;
 }
 
-// Per-channel min/max of W [I,3H], R [H,3H], bw, br merged into the running ranges.
-__global__ __launch_bounds__(256) void calib_params(int I, int H, const float *W, const float *R,
-                                                    const float *bw, const float *br,
-                                                    float *chan /* 4 x (min[C], max[C]) */) {
+// Per-channel min / max over the finite values of W, R and the two biases, merged into the
+// running ranges (a channel with no finite value contributes 0 to both).  calib_params_part:
+// workgroup (x, s) takes 64 columns of rows [s kPrmRows, +kPrmRows) of W and R stacked, its four
+// waves on interleaved rows, and writes the slab's min / max per column; calib_params_fold
+// folds the slabs of a column and merges.
+__global__ __launch_bounds__(256) void calib_params_part(int I, int H, const float *W,
+                                                         const float *R,
+                                                         float *part /* [S][2][2][C] */) {
+  const int C = 3 * H;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int c = blockIdx.x * 64 + lane;
+  const int r0 = blockIdx.y * kPrmRows, r1 = min(I + H, r0 + kPrmRows);
+  float lw = FLT_MAX, hw = -FLT_MAX, lr = FLT_MAX, hr = -FLT_MAX;
+  if (c < C) {
+    for (int r = r0 + w; r < r1; r += 4) {
+      const bool in_w = r < I;
+      const float v = in_w ? W[static_cast<size_t>(r) * C + c]
+                           : R[static_cast<size_t>(r - I) * C + c];
+      if (!isfinite(v)) continue;
+      if (in_w) {
+        lw = fminf(lw, v);
+        hw = fmaxf(hw, v);
+      } else {
+        lr = fminf(lr, v);
+        hr = fmaxf(hr, v);
+      }
+    }
+  }
+  __shared__ float red[4][4][64];
+  red[w][0][lane] = lw;
+  red[w][1][lane] = hw;
+  red[w][2][lane] = lr;
+  red[w][3][lane] = hr;
+  __syncthreads();
+  if (w != 0 || c >= C) return;
+  for (int q = 1; q < 4; ++q) {
+    lw = fminf(lw, red[q][0][lane]);
+    hw = fmaxf(hw, red[q][1][lane]);
+    lr = fminf(lr, red[q][2][lane]);
+    hr = fmaxf(hr, red[q][3][lane]);
+  }
+  float *p = part + static_cast<size_t>(blockIdx.y) * 4 * C;
+  p[c] = lw;
+  p[C + c] = hw;
+  p[2 * C + c] = lr;
+  p[3 * C + c] = hr;
+}
+
+__global__ __launch_bounds__(256) void calib_params_fold(int H, int S, const float *part,
+                                                         const float *bw, const float *br,
+                                                         float *chan /* 4 x (min[C], max[C]) */) {
   const int C = 3 * H;
   const int c = blockIdx.x * blockDim.x + threadIdx.x;
   if (c >= C) return;
-  const float *src[4] = {W, R, bw, br};
-  const int rows[4] = {I, H, 1, 1};
+  float lo[4], hi[4];
+  lo[0] = lo[1] = FLT_MAX;
+  hi[0] = hi[1] = -FLT_MAX;
+  for (int s = 0; s < S; ++s) {
+    const float *p = part + static_cast<size_t>(s) * 4 * C;
+    lo[0] = fminf(lo[0], p[c]);
+    hi[0] = fmaxf(hi[0], p[C + c]);
+    lo[1] = fminf(lo[1], p[2 * C + c]);
+    hi[1] = fmaxf(hi[1], p[3 * C + c]);
+  }
+  const float b0 = bw[c], b1 = br[c];
+  lo[2] = hi[2] = isfinite(b0) ? b0 : 0.0f;
+  lo[3] = hi[3] = isfinite(b1) ? b1 : 0.0f;
+#pragma unroll
   for (int k = 0; k < 4; ++k) {
-    float lo = FLT_MAX, hi = -FLT_MAX;
-    for (int r = 0; r < rows[k]; ++r) {
-      const float v = src[k][static_cast<size_t>(r) * C + c];
-      if (isfinite(v)) {
-        lo = fminf(lo, v);
-        hi = fmaxf(hi, v);
-      }
-    }
-    if (lo > hi) lo = hi = 0.0f;
+    float l = lo[k], h = hi[k];
+    if (l > h) l = h = 0.0f;
     float *mn = chan + static_cast<size_t>(k) * 2 * C, *mx = mn + C;
-    mn[c] = lo < mn[c] ? lo : mn[c];
-    mx[c] = hi > mx[c] ? hi : mx[c];
+    mn[c] = l < mn[c] ? l : mn[c];
+    mx[c] = h > mx[c] ? h : mx[c];
   }
 }
 
@@ -866,7 +924,7 @@ extern "C" {
 int64_t rxmet_gru_calibrate_workspace_bytes(int32_t T, int32_t B, int32_t I, int32_t H) {
   (void)I;
   if (T < 1 || B < 1 || H < 1) return static_cast<int64_t>(sizeof(unsigned) * 2 * kNStat);
-  return static_cast<int64_t>(CalWorkspace(T, B, H).total);
+  return static_cast<int64_t>(CalWorkspace(T, B, I, H).total);
 }
 
 int rxmet_gru_forward_calibrate(int32_t T, int32_t B, int32_t I, int32_t H, const float *W,
@@ -896,8 +954,13 @@ int rxmet_gru_forward_calibrate(int32_t T, int32_t B, int32_t I, int32_t H, cons
   RXMET_CHECK_LAUNCH();
   hipLaunchKernelGGL(stats_merge, dim3(1), dim3(64), 0, stream, ord, stats);
   RXMET_CHECK_LAUNCH();
-  hipLaunchKernelGGL(calib_params, dim3((3 * H + 255) / 256), dim3(256), 0, stream, I, H, W, R, bw,
-                     br, stats + 2 * kNStat);
+  const CalWorkspace cw(T, B, I, H);
+  float *prm = reinterpret_cast<float *>(static_cast<char *>(workspace) + cw.prm);
+  hipLaunchKernelGGL(calib_params_part, dim3((3 * H + 63) / 64, cw.prm_slabs), dim3(256), 0,
+                     stream, I, H, W, R, prm);
+  RXMET_CHECK_LAUNCH();
+  hipLaunchKernelGGL(calib_params_fold, dim3((3 * H + 255) / 256), dim3(256), 0, stream, H,
+                     cw.prm_slabs, prm, bw, br, stats + 2 * kNStat);
   RXMET_CHECK_LAUNCH();
   return 0;
 }

@@ -86,6 +86,28 @@ def test_calibration_merges_batches_and_ignores_non_finite(cuda):
     _close(got, s, "merged stats")
 
 
+@pytest.mark.parametrize("shape", [(2, 8, 40, 64), (2, 4, 300, 128)])
+def test_parameter_ranges_skip_non_finite_weights(cuda, shape):
+    """Per-channel ranges of W, R, bw, br (the stats after the 2 x 13 activation grids): W and R
+    taken in 64-row slabs (I + H = 104 and 428 rows), non-finite entries skipped, a channel with
+    no finite entry contributing 0; merged into ranges from an earlier batch."""
+    T, B, I, H = shape
+    W, R, bw, br = _haste(*_weights(I, H, 15))
+    W[3, 5], W[I - 1, 7], R[H - 1, 2] = np.nan, np.inf, -np.inf
+    R[:, 9] = np.inf          # one recurrent channel with no finite value
+    bw[4], br[11] = np.nan, -np.inf
+    x = np.random.default_rng(16).standard_normal((T, B, I)).astype(f32)
+    W1, R1, bw1, br1 = _haste(*_weights(I, H, 17, amp=3.0))
+    _, _, s = GO.forward_calibrate(W1, R1, bw1, br1, x)
+    _, _, s = GO.forward_calibrate(W, R, bw, br, x, stats=s)
+    _, _, ranges = _gpu_calibrate(cuda, W1, R1, bw1, br1, x, None)
+    _, _, ranges = _gpu_calibrate(cuda, W, R, bw, br, x, None, ranges)
+    n = 2 * A.NGRIDS
+    got = ranges.stats.cpu().numpy()[n:]
+    assert np.isfinite(got).all()
+    np.testing.assert_array_equal(got, s[n:])
+
+
 def _module_case(bidirectional, batch_first, with_hx, cfg, seed, shape=(6, 24, 10, 32)):
     T, B, I, H = shape
     torch.manual_seed(seed)
