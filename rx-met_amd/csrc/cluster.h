@@ -166,7 +166,14 @@ __device__ __forceinline__ void store_bytes_coherent(unsigned char *dst4, int by
 // Zero `n` words (counters and flags) on the stream; used instead of a memset node so the
 // sequence stays capturable.
 [[maybe_unused]] static __global__ void zero_words(unsigned *p, int n) {
-  for (int i = threadIdx.x; i < n; i += blockDim.x) p[i] = 0u;
+  const int stride = gridDim.x * blockDim.x;
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = 0u;
+}
+
+// Blocks of 256 threads for zero_words over n words (grid-strided, at most 1024 blocks).
+[[maybe_unused]] static inline unsigned zero_blocks(int64_t n) {
+  const int64_t b = (n + 1023) / 1024;
+  return static_cast<unsigned>(b < 1 ? 1 : (b > 1024 ? 1024 : b));
 }
 
 // A launch whose cluster wait timed out leaves untrustworthy outputs: overwrite `n` floats

@@ -16,6 +16,7 @@
 #include <cfloat>
 #include <cstdlib>
 
+#include "calib_gemm.h"
 #include "cluster.h"
 #include "mfma_frag.h"
 #include "rxmet_common.h"
@@ -173,7 +174,6 @@ __global__ void stats_merge(const unsigned *o, float *s) {
 // ---------------------------------------------------------------------------------
 constexpr int kCT = 16;      // batch rows of a tile
 constexpr int kCMaxW = 16;   // waves of a recurrence workgroup
-constexpr int kGemmRBMax = 8;  // 64-row tiles per input-projection workgroup, at most
 
 // Block-wide (min, max) of n statistics, written by thread 0 to part[0..n) / part[n..2n).
 __device__ __forceinline__ void block_stats(const float *mn, const float *mx, int n, float *part) {
@@ -251,101 +251,30 @@ __global__ __launch_bounds__(256) void stats_fold(const float *__restrict__ part
 constexpr int kGemmStat = 3;
 static_assert(RXMET_GRU_X < kGemmStat && RXMET_GRU_WX < kGemmStat, "GEMM statistics layout");
 
-// wx[m][c] = sum_k x[m][k] W[k][c] + bw[c] for m < M = T B, c < C = 3H, with the X and WX
-// statistics.  A workgroup covers 64 columns of RB 64-row tiles; each of its four waves a
-// 32 x 32 block of 2 x 2 MFMA tiles per row tile.  The contraction runs in blocks of 16 k, lane
-// group g taking k = k0 + 4 g + s at sub-step s, so a lane reads four consecutive x of a row
-// (one 16-byte load where K allows) and four rows of one W column.
+// wx[m][c] = sum_k x[m][k] W[k][c] + bw[c] for m < M = T B, c < C = 3H (W [I][3H], K-major),
+// with the X and WX statistics: the LDS-tiled fp32 MFMA block of calib_gemm.h, one partial
+// block of statistics per workgroup.
 template <bool STATS>
-__global__ __launch_bounds__(256) void calib_input_gemm(int M, int K, int C, int RB,
+__global__ __launch_bounds__(256) void calib_input_gemm(int M, int K, int C,
                                                         const float *__restrict__ x,
                                                         const float *__restrict__ W,
                                                         const float *__restrict__ bw,
                                                         float *__restrict__ wx,
                                                         float *__restrict__ part) {
-  const int w = threadIdx.x / kWave, l = threadIdx.x % kWave, r = l % 16, g = l / 16;
-  const int n0 = blockIdx.x * 64 + (w % 2) * 32;
-  const bool see_x = STATS && blockIdx.x == 0, vec = K % 4 == 0;
-  float st_mn[kNStat], st_mx[kNStat];  // X and WX observed here
+  float st_mn[kGemmStat], st_mx[kGemmStat];
 #pragma unroll
-  for (int i = 0; i < kNStat; ++i) {
+  for (int i = 0; i < kGemmStat; ++i) {
     st_mn[i] = FLT_MAX;
     st_mx[i] = -FLT_MAX;
   }
-  for (int rt = 0; rt < RB; ++rt) {
-    const int m0 = (blockIdx.y * RB + rt) * 64 + (w / 2) * 32;
-    if (m0 >= M) break;
-    v4f acc[2][2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-    // operands of one 16-wide K step; the next step's are in flight during this one's MFMAs
-    auto load = [&](int k0, float (&a)[2][4], float (&b)[2][4]) {
-      const int kb = k0 + 4 * g;
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int row = m0 + 16 * i + r;
-        const float *xr = x + static_cast<size_t>(row) * K + kb;
-        if (row < M && vec && kb + 3 < K) {
-          const float4 v = *reinterpret_cast<const float4 *>(xr);
-          a[i][0] = v.x; a[i][1] = v.y; a[i][2] = v.z; a[i][3] = v.w;
-        } else {
-#pragma unroll
-          for (int s = 0; s < 4; ++s) a[i][s] = row < M && kb + s < K ? xr[s] : 0.0f;
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int col = n0 + 16 * j + r;
-#pragma unroll
-        for (int s = 0; s < 4; ++s)
-          b[j][s] = col < C && kb + s < K ? W[static_cast<size_t>(kb + s) * C + col] : 0.0f;
-      }
-    };
-    auto step = [&](int k0, const float (&a)[2][4], const float (&b)[2][4]) {
-      // the zeros loaded past M and K are not values of x: only in-range entries are observed
-      if (see_x)
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-          if (m0 + 16 * i + r < M)
-#pragma unroll
-            for (int s = 0; s < 4; ++s)
-              if (k0 + 4 * g + s < K) observe(a[i][s], st_mn[RXMET_GRU_X], st_mx[RXMET_GRU_X]);
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-          for (int j = 0; j < 2; ++j) acc[i][j] = mfma_f32(a[i][s], b[j][s], acc[i][j]);
-    };
-    float a0[2][4], b0[2][4], a1[2][4], b1[2][4];
-    load(0, a0, b0);
-    for (int k0 = 0; k0 < K; k0 += 32) {
-      if (k0 + 16 < K) load(k0 + 16, a1, b1);
-      step(k0, a0, b0);
-      if (k0 + 16 >= K) break;
-      if (k0 + 32 < K) load(k0 + 32, a0, b0);
-      step(k0 + 16, a1, b1);
-    }
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int col = n0 + 16 * j + r;
-        if (col >= C) continue;
-        const float bias = bw[col];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int row = m0 + 16 * i + 4 * g + q;
-          if (row < M) {
-            const float v = acc[i][j][q] + bias;
-            wx[static_cast<size_t>(row) * C + col] = v;
-            if (STATS) observe(v, st_mn[RXMET_GRU_WX], st_mx[RXMET_GRU_WX]);
-          }
-        }
-      }
-  }
+  calgemm::gemm_block<true>(
+      M, C, K, x, W, bw, wx, STATS && blockIdx.x == 0,
+      [&](float v) {
+        if (STATS) observe(v, st_mn[RXMET_GRU_X], st_mx[RXMET_GRU_X]);
+      },
+      [&](float v) {
+        if (STATS) observe(v, st_mn[RXMET_GRU_WX], st_mx[RXMET_GRU_WX]);
+      });
   if (STATS)
     block_stats(st_mn, st_mx, kGemmStat,
                 part + (static_cast<size_t>(blockIdx.y) * gridDim.x + blockIdx.x) * 2 * kGemmStat);
@@ -790,12 +719,9 @@ static int calibrate_mfma(int T, int B, int I, int H, const float *W, const floa
   const int M = T * B;
   {
     rxmet::prof::Scope ps__("gru_calibrate_input_gemm", stream);
-    // row tiles per workgroup: as many as keep about 2048 workgroups (fewer partials to fold)
-    const int64_t tiles = (M + 63) / 64, cblocks = (C + 63) / 64;
-    int RB = 1;
-    while (RB < kGemmRBMax && tiles * cblocks / (2 * RB) >= 2048) RB *= 2;
-    const dim3 grid(static_cast<unsigned>(cblocks), static_cast<unsigned>((tiles + RB - 1) / RB));
-    hipLaunchKernelGGL(calib_input_gemm<STATS>, grid, dim3(256), 0, stream, M, I, C, RB, x, W, bw,
+    const dim3 grid(static_cast<unsigned>((C + calgemm::kBN - 1) / calgemm::kBN),
+                    static_cast<unsigned>((M + calgemm::kBM - 1) / calgemm::kBM));
+    hipLaunchKernelGGL(calib_input_gemm<STATS>, grid, dim3(256), 0, stream, M, I, C, x, W, bw,
                        wx, part);
     RXMET_CHECK_LAUNCH();
     if (STATS) {
@@ -805,8 +731,9 @@ static int calibrate_mfma(int T, int B, int I, int H, const float *W, const floa
     }
   }
   // the exchange buffer's padding columns must read as zero
-  hipLaunchKernelGGL(cluster::zero_words, dim3(1), dim3(1024), 0, stream,
-                     reinterpret_cast<unsigned *>(a.hx), 2 * ws.Bpad * ws.Hpad);
+  hipLaunchKernelGGL(cluster::zero_words, dim3(cluster::zero_blocks(2 * ws.Bpad * ws.Hpad)),
+                     dim3(256), 0, stream, reinterpret_cast<unsigned *>(a.hx),
+                     2 * ws.Bpad * ws.Hpad);
   RXMET_CHECK_LAUNCH();
   hipLaunchKernelGGL(cluster::zero_words, dim3(1), dim3(256), 0, stream, a.counters,
                      cluster::kCounterStride * ncl + 1);

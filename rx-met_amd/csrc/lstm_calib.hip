@@ -14,6 +14,7 @@
 #include <cfloat>
 #include <cstdlib>
 
+#include "calib_gemm.h"
 #include "cluster.h"
 #include "mfma_frag.h"
 #include "rxmet_common.h"
@@ -183,7 +184,6 @@ __global__ void lstm_stats_merge(const unsigned *o, float *s, int64_t count_inde
 constexpr int kCT = 16;
 constexpr int kCMaxW = 8;  // waves of a recurrence workgroup (256 VGPRs: W_hh, h and the 18
                            // operators' statistics stay in registers)
-constexpr int kGemmRBMax = 8;
 constexpr int kPart = 2 * kN + 1;  // floats per partial block: min[18], max[18], non-finite
 
 // The block's ranges of the first N statistics and its non-finite count as one partial block
@@ -285,102 +285,26 @@ __global__ __launch_bounds__(256) void lstm_stats_fold(const float *__restrict__
 constexpr int kGemmStat = RXMET_LSTM_IH_LINEAR + 1;
 static_assert(RXMET_LSTM_INPUT < kGemmStat, "GEMM statistics layout");
 
-// li[m][c] = sum_k x[m][k] W_ih[c][k] + b_ih[c] for m < M = T B, c < C = 4H, with the INPUT
-// and IH_LINEAR observations.  The GRU projection's tiling (gru_calib.hip): 64 columns of RB
-// 64-row tiles per workgroup, a lane reading four consecutive x of a row and four consecutive
-// weights of one W_ih row (both 16-byte loads where K allows).
+// li[m][c] = sum_k x[m][k] W_ih[c][k] + b_ih[c] for m < M = T B, c < C = 4H (W_ih [4H][I],
+// N-major), with the INPUT and IH_LINEAR statistics: the LDS-tiled fp32 MFMA block of
+// calib_gemm.h, one partial block of statistics per workgroup.
 template <bool STATS>
-__global__ __launch_bounds__(256) void lstm_input_gemm(int M, int K, int C, int RB,
+__global__ __launch_bounds__(256) void lstm_input_gemm(int M, int K, int C,
                                                        const float *__restrict__ x,
                                                        const float *__restrict__ Wi,
                                                        const float *__restrict__ bi,
                                                        float *__restrict__ li,
                                                        float *__restrict__ part) {
-  const int w = threadIdx.x / kWave, l = threadIdx.x % kWave, r = l % 16, g = l / 16;
-  const int n0 = blockIdx.x * 64 + (w % 2) * 32;
-  const bool see_x = STATS && blockIdx.x == 0, vec = K % 4 == 0;
   Obs o;
   obs_init(o);
-  for (int rt = 0; rt < RB; ++rt) {
-    const int m0 = (blockIdx.y * RB + rt) * 64 + (w / 2) * 32;
-    if (m0 >= M) break;
-    v4f acc[2][2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-    // operands of one 16-wide K step; the next step's are in flight during this one's MFMAs
-    auto load = [&](int k0, float (&a)[2][4], float (&b)[2][4]) {
-      const int kb = k0 + 4 * g;
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int row = m0 + 16 * i + r;
-        const float *xr = x + static_cast<size_t>(row) * K + kb;
-        if (row < M && vec && kb + 3 < K) {
-          const float4 v = *reinterpret_cast<const float4 *>(xr);
-          a[i][0] = v.x; a[i][1] = v.y; a[i][2] = v.z; a[i][3] = v.w;
-        } else {
-#pragma unroll
-          for (int s = 0; s < 4; ++s) a[i][s] = row < M && kb + s < K ? xr[s] : 0.0f;
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int col = n0 + 16 * j + r;
-        const float *wr = Wi + static_cast<size_t>(col) * K + kb;
-        if (col < C && vec && kb + 3 < K) {
-          const float4 v = *reinterpret_cast<const float4 *>(wr);
-          b[j][0] = v.x; b[j][1] = v.y; b[j][2] = v.z; b[j][3] = v.w;
-        } else {
-#pragma unroll
-          for (int s = 0; s < 4; ++s) b[j][s] = col < C && kb + s < K ? wr[s] : 0.0f;
-        }
-      }
-    };
-    auto step = [&](int k0, const float (&a)[2][4], const float (&b)[2][4]) {
-      // x observed by the lanes of one column half (each row once); the zeros loaded past M
-      // and K are not values of x
-      if (see_x && (w % 2) == 0)
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-          if (m0 + 16 * i + r < M)
-#pragma unroll
-            for (int s = 0; s < 4; ++s)
-              if (k0 + 4 * g + s < K) observe(o, RXMET_LSTM_INPUT, a[i][s]);
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-          for (int j = 0; j < 2; ++j) acc[i][j] = mfma_f32(a[i][s], b[j][s], acc[i][j]);
-    };
-    float a0[2][4], b0[2][4], a1[2][4], b1[2][4];
-    load(0, a0, b0);
-    for (int k0 = 0; k0 < K; k0 += 32) {
-      if (k0 + 16 < K) load(k0 + 16, a1, b1);
-      step(k0, a0, b0);
-      if (k0 + 16 >= K) break;
-      if (k0 + 32 < K) load(k0 + 32, a0, b0);
-      step(k0 + 16, a1, b1);
-    }
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int col = n0 + 16 * j + r;
-        if (col >= C) continue;
-        const float bias = bi ? bi[col] : 0.0f;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int row = m0 + 16 * i + 4 * g + q;
-          if (row < M) {
-            const float v = acc[i][j][q] + bias;
-            li[static_cast<size_t>(row) * C + col] = v;
-            if (STATS) observe(o, RXMET_LSTM_IH_LINEAR, v);
-          }
-        }
-      }
-  }
+  calgemm::gemm_block<false>(
+      M, C, K, x, Wi, bi, li, STATS && blockIdx.x == 0,
+      [&](float v) {
+        if (STATS) observe(o, RXMET_LSTM_INPUT, v);
+      },
+      [&](float v) {
+        if (STATS) observe(o, RXMET_LSTM_IH_LINEAR, v);
+      });
   if (STATS)
     obs_block<kGemmStat>(o, part + (static_cast<size_t>(blockIdx.y) * gridDim.x + blockIdx.x) *
                                        (2 * kGemmStat + 1));
@@ -606,11 +530,9 @@ static int lstm_float_mfma(int T, int B, int I, int H, const float *Wi, const fl
   const int C = 4 * H, M = T * B;
   {
     rxmet::prof::Scope ps__("lstm_calibrate_input_gemm", stream);
-    const int64_t tiles = (M + 63) / 64, cblocks = (C + 63) / 64;
-    int RB = 1;
-    while (RB < kGemmRBMax && tiles * cblocks / (2 * RB) >= 2048) RB *= 2;
-    const dim3 grid(static_cast<unsigned>(cblocks), static_cast<unsigned>((tiles + RB - 1) / RB));
-    hipLaunchKernelGGL(lstm_input_gemm<STATS>, grid, dim3(256), 0, stream, M, I, C, RB, x, Wi, bi,
+    const dim3 grid(static_cast<unsigned>((C + calgemm::kBN - 1) / calgemm::kBN),
+                    static_cast<unsigned>((M + calgemm::kBM - 1) / calgemm::kBM));
+    hipLaunchKernelGGL(lstm_input_gemm<STATS>, grid, dim3(256), 0, stream, M, I, C, x, Wi, bi,
                        li, part);
     RXMET_CHECK_LAUNCH();
     if (STATS) {
@@ -619,8 +541,9 @@ static int lstm_float_mfma(int T, int B, int I, int H, const float *Wi, const fl
       RXMET_CHECK_LAUNCH();
     }
   }
-  hipLaunchKernelGGL(cluster::zero_words, dim3(1), dim3(1024), 0, stream,
-                     reinterpret_cast<unsigned *>(a.hx), 2 * ws.Bpad * ws.Hpad);
+  hipLaunchKernelGGL(cluster::zero_words, dim3(cluster::zero_blocks(2 * ws.Bpad * ws.Hpad)),
+                     dim3(256), 0, stream, reinterpret_cast<unsigned *>(a.hx),
+                     2 * ws.Bpad * ws.Hpad);
   RXMET_CHECK_LAUNCH();
   hipLaunchKernelGGL(cluster::zero_words, dim3(1), dim3(256), 0, stream, a.counters,
                      cluster::kCounterStride * ncl + 1);
