@@ -108,6 +108,21 @@ _RANGE_GRID.update(Wx="weight_ih_linear", Rh="weight_hh_linear")
 del _RANGE_GRID["weight_ih_linear"], _RANGE_GRID["weight_hh_linear"]
 
 
+_EMPTY_STATS = {}
+
+
+def _empty_stats(hidden: int, device) -> torch.Tensor:
+    """A fresh empty statistics vector; on a GPU a copy of a cached device template, so that
+    a new calibration does not wait for the stream on a pageable host copy."""
+    if device is None or torch.device(device).type == "cpu":
+        return torch.from_numpy(A.empty_stats(hidden))
+    key = (hidden, str(device))
+    t = _EMPTY_STATS.get(key)
+    if t is None:
+        t = _EMPTY_STATS[key] = torch.from_numpy(A.empty_stats(hidden)).to(device)
+    return t.clone()
+
+
 class GRUQuantizationRanges:
     """MinMax statistics of one direction (GRUQuantizationRanges, gru_interface_binding.cc:
     1365-1410): a flat vector in the layout of rxmet_gru_forward_calibrate, kept on the device
@@ -117,14 +132,12 @@ class GRUQuantizationRanges:
 
     def __init__(self, hidden_size: int = 0, device=None):
         object.__setattr__(self, "hidden_", int(hidden_size))
-        object.__setattr__(self, "stats", torch.from_numpy(A.empty_stats(self.hidden_)))
-        if device is not None:
-            self.stats = self.stats.to(device)
+        object.__setattr__(self, "stats", _empty_stats(self.hidden_, device))
 
     def reset(self, hidden: int = -1):
         if hidden > 0:
             object.__setattr__(self, "hidden_", int(hidden))
-        self.stats = torch.from_numpy(A.empty_stats(self.hidden_)).to(self.stats.device)
+        self.stats = _empty_stats(self.hidden_, self.stats.device)
 
     def to_struct(self):
         return A.make_ranges(self.stats.detach().cpu().numpy(), self.hidden_)

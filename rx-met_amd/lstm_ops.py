@@ -96,9 +96,20 @@ class LstmQuantParams:
         return p
 
 
+_EMPTY_STATS = {}
+
+
 def new_stats(hidden: int, device) -> torch.Tensor:
-    """Empty MinMax statistics (layout of rxmet_lstm_stats_size) on ``device``."""
-    return torch.from_numpy(L.empty_stats(hidden)).to(device)
+    """Empty MinMax statistics (layout of rxmet_lstm_stats_size) on ``device``; on a GPU a copy
+    of a cached device template, so that a new calibration does not wait for the stream on a
+    pageable host copy."""
+    if torch.device(device).type == "cpu":
+        return torch.from_numpy(L.empty_stats(hidden))
+    key = (hidden, str(device))
+    t = _EMPTY_STATS.get(key)
+    if t is None:
+        t = _EMPTY_STATS[key] = torch.from_numpy(L.empty_stats(hidden)).to(device)
+    return t.clone()
 
 
 def forward_calibrate(x, W_ih, W_hh, b_ih, b_hh, h0, c0, stats: torch.Tensor):
