@@ -1,5 +1,7 @@
 // exact_gemm.hip — operand packing for the pre-packed exact GEMM (exact_gemm.h), for codes
 // stored as fp32 or int32.
+#include <type_traits>
+
 #include "exact_gemm.h"
 
 #include "rxmet_common.h"
@@ -14,14 +16,35 @@ __global__ __launch_bounds__(256) void pack_a_kernel(const E *__restrict__ A, in
                                                      int Kp) {
   const int64_t words = static_cast<int64_t>(M) * (Kp / 4), plane = static_cast<int64_t>(M) * Kp;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  const unsigned kq = static_cast<unsigned>(Kp / 4);
+  // whole 4-element groups of a row as one 16-byte load where the rows allow it
+  const bool vec = std::is_same<E, float>::value && lda % 4 == 0 &&
+                   (reinterpret_cast<uintptr_t>(A) & 15) == 0;
   for (int64_t w = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; w < words; w += stride) {
-    const int64_t m = w / (Kp / 4);
-    const int k0 = static_cast<int>(w % (Kp / 4)) * 4;
+    // 32-bit division where the word index fits (a 64-bit one is a long software sequence)
+    int64_t m;
+    int k0;
+    if (words <= 0x7fffffff) {
+      const unsigned mw = static_cast<unsigned>(w) / kq;
+      m = mw;
+      k0 = static_cast<int>(static_cast<unsigned>(w) - mw * kq) * 4;
+    } else {
+      m = w / kq;
+      k0 = static_cast<int>(w % kq) * 4;
+    }
+    E a4[4];
+    if (vec && k0 + 3 < K) {
+      const float4 v4 = *reinterpret_cast<const float4 *>(A + m * lda + k0);
+      a4[0] = v4.x; a4[1] = v4.y; a4[2] = v4.z; a4[3] = v4.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) a4[e] = k0 + e < K ? A[m * lda + k0 + e] : E(0);
+    }
     unsigned lo = 0, hi = 0;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int k = k0 + e;
-      const int v = k < K ? static_cast<int>(A[m * lda + k]) - static_cast<int>(off) : 0;
+      const int v = k < K ? static_cast<int>(a4[e]) - static_cast<int>(off) : 0;
       if (PA == 1) {
         lo |= static_cast<unsigned>(v & 255) << (8 * e);
       } else {
@@ -67,10 +90,17 @@ __global__ __launch_bounds__(64) void pack_b_kernel(const E *__restrict__ B, int
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * 64 + l;
   frag[idx] = v4i{w0[0], w0[1], w0[2], w0[3]};
   if (PB == 2) frag[fplane + idx] = v4i{w1[0], w1[1], w1[2], w1[3]};
-  if (s == 0 && l < 16 && n < N) {
+  // column sums (exact in int64, so the order does not matter): the wave of K-step 0, lane
+  // group l / 16 taking every fourth k of column n, then the four groups added by shuffles
+  if (s == 0) {
     long long sum = 0;
-    for (int k = 0; k < K; ++k) sum += static_cast<long long>(B[k * sbk + n * sbn]);
-    colsum[n] = sum;
+    if (n < N) {
+#pragma unroll 4
+      for (int k = l / 16; k < K; k += 4) sum += static_cast<long long>(B[k * sbk + n * sbn]);
+    }
+    sum += __shfl_xor(sum, 16, 64);
+    sum += __shfl_xor(sum, 32, 64);
+    if (l < 16 && n < N) colsum[n] = sum;
   }
 }
 
