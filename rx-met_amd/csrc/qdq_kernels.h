@@ -31,6 +31,7 @@
 
 #include <type_traits>
 
+#include "div_rn.h"
 #include "rxmet_common.h"
 #include "rxmet_qc.h"
 #include "rxmet_qdq.h"
@@ -266,6 +267,11 @@ __device__ __forceinline__ float rint_a(float v) { return rintf(v); }
 __device__ __forceinline__ double rint_a(double v) { return rint(v); }
 __device__ __forceinline__ float fma_a(float a, float b, float c) { return fmaf(a, b, c); }
 __device__ __forceinline__ double fma_a(double a, double b, double c) { return fma(a, b, c); }
+
+// x / s in the internal type: fp32 by the correctly rounded reciprocal (div_rn.h), fp64 by
+// the division.
+__device__ __forceinline__ float div_a(float x, float s, float rs) { return div_rn(x, s, rs); }
+__device__ __forceinline__ double div_a(double x, double s, float) { return x / s; }
 template <typename A>
 __device__ __forceinline__ A clamp_a(A v, A lo, A hi) {
   return v < lo ? lo : (v > hi ? hi : v);  // NaN falls through (torch.clamp)
@@ -359,7 +365,9 @@ struct Elem {
     e.lo = r(e.o + e.qmin);
     e.hi = r(e.o + e.qmax);
     e.fs = s;
-    e.inv_s = 1.0f / s;  // torch's fake_quantize kernels multiply by fp32 1/scale
+    // torch's fake_quantize kernels multiply by fp32 1/scale; with A = fp32 it is also the
+    // correctly rounded reciprocal of e.s that div_a takes
+    e.inv_s = 1.0f / s;
     e.zp = -truncf(o);   // zero point = -offset.to(int32)
     e.s_io = Io<T>::round(s);
     return e;
@@ -377,7 +385,7 @@ struct Elem {
 
   // QuantDequantFunc.forward: (clamp(rint(v / s) - o) + o) * s, each step rounded to R.
   __device__ static A qdq(A v, const Enc &e) {
-    const A t = r(v / e.s);
+    const A t = r(div_a(v, e.s, e.inv_s));
     const A q = r(rint_a(t) - e.o);
     return r(r(clamp_a(q, e.qmin, e.qmax) + e.o) * e.s);
   }
@@ -409,7 +417,7 @@ __device__ __forceinline__ V fwd_elem(V x, const typename Elem<T, R>::Enc &e, co
              e.fs;
     }
   } else if constexpr (OP == OP_Q) {
-    const A t = El::r(A(x) / e.s);
+    const A t = El::r(div_a(A(x), e.s, e.inv_s));
     return static_cast<V>(clamp_a(El::r(rint_a(t) - e.o), e.qmin, e.qmax));
   } else if constexpr (OP == OP_NATIVE) {
     // NaN kept; clip in value space (fmax(fmin(v, max), min)); times fl(1 / delta); round
@@ -425,7 +433,7 @@ __device__ __forceinline__ V fwd_elem(V x, const typename Elem<T, R>::Enc &e, co
 }
 
 // One element of the backward: returns dx and adds this element's encoding-gradient terms
-// (as the reference rounds them, in R) to (ds, dof).
+// (as the reference rounds them, in R) to the fp64 sums (ds, dof).
 template <int OP, typename T, typename R, typename V = typename Io<T>::V>
 __device__ __forceinline__ V bwd_elem(V x, V g, const typename Elem<T, R>::Enc &e, const Params &p,
                                       double &ds, double &dof) {
@@ -433,7 +441,7 @@ __device__ __forceinline__ V bwd_elem(V x, V g, const typename Elem<T, R>::Enc &
   using A = typename El::A;
   const A ga = A(g);
   if constexpr (OP == OP_QDQ_LEARN) {
-    const A t = El::r(El::shifted(x, e, p) / e.s);
+    const A t = El::r(div_a(El::shifted(x, e, p), e.s, e.inv_s));
     const A rr = rint_a(t);
     const A q = El::r(rr - e.o);
     const A m = (q >= e.qmin && q <= e.qmax) ? A(1) : A(0);
@@ -441,7 +449,8 @@ __device__ __forceinline__ V bwd_elem(V x, V g, const typename Elem<T, R>::Enc &
     ds += static_cast<double>(El::r(ga * El::r(clamp_a(rr, e.lo, e.hi) - t * m)));
     dof += static_cast<double>(El::r(ga * El::r(nm * e.s)));
     // the shift's own scale terms: +alpha*g from the add, -alpha*g*mask through the sub
-    if (p.alpha != 0.0) ds += static_cast<double>(A(p.alpha)) * static_cast<double>(ga * nm);
+    if (p.alpha != 0.0)
+      ds += static_cast<double>(A(p.alpha)) * static_cast<double>(ga * nm);
     return static_cast<V>(ga * m);
   } else if constexpr (OP == OP_QDQ_FROZEN) {
     if constexpr (std::is_same<V, double>::value) {
@@ -453,11 +462,11 @@ __device__ __forceinline__ V bwd_elem(V x, V g, const typename Elem<T, R>::Enc &
       return g * m;
     }
   } else if constexpr (OP == OP_Q) {
-    const A t = El::r(A(x) / e.s);
+    const A t = El::r(div_a(A(x), e.s, e.inv_s));
     const A q = El::r(rint_a(t) - e.o);
     const A m = (q >= e.qmin && q <= e.qmax) ? A(1) : A(0);
     const A mg = ga * m;
-    const A gs = El::r(mg / e.s);
+    const A gs = El::r(div_a(mg, e.s, e.inv_s));
     // QuantizeFunc.backward divides the saved input (type T) by the scale: in T when the
     // scale is 0-dim, in R otherwise
     const A xs = p.scalar_scale ? A(Io<T>::round(x / e.s_io)) : t;

@@ -169,6 +169,59 @@ def test_minmax_matches_oracle(cuda, layout):
     np.testing.assert_array_equal(mx.cpu().numpy(), emx)
 
 
+def _bits_equal(a, e, msg):
+    """Bit-for-bit equality (signed zeros told apart), NaN matching NaN."""
+    a, e = np.asarray(a, f32), np.asarray(e, f32)
+    na, ne = np.isnan(a), np.isnan(e)
+    np.testing.assert_array_equal(na, ne, err_msg=msg)
+    np.testing.assert_array_equal(a[~na].view(np.uint32), e[~ne].view(np.uint32), err_msg=msg)
+
+
+def test_quotients_are_correctly_rounded(cuda):
+    """x / s as the kernels evaluate it (a product by the rounded reciprocal with one fma
+    correction inside [2^-100, 2^100], the division elsewhere) against IEEE division: the
+    quantized codes of values within two ulps of every rounding tie (k + 1/2) s, and
+    dx = g m / s of QuantizeFunc's backward, which is the quotient itself, for scales with
+    all-ones and minimal significands, powers of two, tiny and huge scales, and operands at
+    and beyond the fast range (zeros, denormals, 2^-110 .. 2^110, inf, NaN)."""
+    fb = lambda u: np.array([u], np.uint32).view(f32)[0]
+    scales = np.array([0.0173, 0.1, 3.0, 1.0, 0.5, fb(0x3fffffff), fb(0x3f7fffff), fb(0x3f800001),
+                       fb(0x3fc00001), 1e-30, 1e30, 2.0 ** -120, 2.0 ** -126, 2.0 ** 120], f32)
+    C, n = len(scales), 6000
+    rng = np.random.default_rng(71)
+    x = np.empty((C, n), f32)
+    g = np.empty((C, n), f32)
+    edge = np.array([0.0, -0.0, 1e-40, -1e-40, 2.0 ** -110, -(2.0 ** -110), 2.0 ** -100,
+                     2.0 ** 100, 2.0 ** 110, 3e38, -3e38, np.inf, -np.inf, np.nan], f32)
+    for c, s in enumerate(scales):
+        k = rng.integers(-(1 << 20), 1 << 20, n // 5)
+        tie = ((k + 0.5) * np.float64(s)).astype(f32)
+        row = [tie, np.nextafter(tie, np.inf, dtype=f32), np.nextafter(tie, -np.inf, dtype=f32),
+               np.nextafter(np.nextafter(tie, np.inf, dtype=f32), np.inf, dtype=f32),
+               np.nextafter(np.nextafter(tie, -np.inf, dtype=f32), -np.inf, dtype=f32)]
+        x[c] = np.concatenate(row)[:n]
+        x[c, :len(edge)] = edge
+        gr = rng.standard_normal(n).astype(f32) * (10.0 ** rng.integers(-38, 38, n)).astype(f32)
+        gr[:len(edge)] = edge
+        g[c] = gr
+    o = np.zeros(C, f32)
+    qmin, qmax = -(1 << 23), (1 << 23) - 1
+    layout = (1, C, n)
+    xd, gd, sd, od = (_t(a, cuda) for a in (x.reshape(-1), g.reshape(-1), scales, o))
+    q, dx = torch.empty_like(xd), torch.empty_like(xd)
+    ds, do = torch.empty(C, device=cuda), torch.empty(C, device=cuda)
+    rxmet_lib.call("rxmet_quantize_forward", xd.data_ptr(), q.data_ptr(), *layout, sd.data_ptr(),
+                   od.data_ptr(), qmin, qmax, _stream(cuda))
+    rxmet_lib.call("rxmet_quantize_backward", xd.data_ptr(), gd.data_ptr(), dx.data_ptr(),
+                   ds.data_ptr(), do.data_ptr(), *layout, sd.data_ptr(), od.data_ptr(), qmin, qmax,
+                   _ws(layout, cuda).data_ptr(), _stream(cuda))
+    torch.cuda.synchronize()
+    eq = O.quantize(x.reshape(-1), scales, o, qmin, qmax, layout)
+    edx, _, _ = O.quantize_backward(x.reshape(-1), g.reshape(-1), scales, o, qmin, qmax, layout)
+    _bits_equal(q.cpu().numpy(), eq, "codes")
+    _bits_equal(dx.cpu().numpy(), edx, "dx = g m / s")
+
+
 @pytest.mark.parametrize("layout", [(1, 1, 5001), (1, 4, 3000), (30, 6, 1)])
 def test_quantize_dequantize_kernels(cuda, layout):
     outer, C, inner = layout
