@@ -57,7 +57,7 @@ def test_noalloc_backward_rejects_layouts_beyond_its_scratch():
     lib = rxmet_lib.load()
     buf = (ctypes.c_float * 4)()
     p = ctypes.cast(buf, ctypes.c_void_p)
-    n = 1 << 33  # per-tensor: 2^33 / 4096 partials of 16 bytes = 32 MiB
+    n = 1 << 33  # per-tensor: 2^33 / 8192 partials (two 4096-element chunks each) of 16 bytes = 16 MiB
     need = lib.rxmet_qdq_workspace_bytes(1, 1, n)
     assert need > 4 << 20
     rc = lib.rxmet_qdq_backward_noalloc(p, p, p, p, p, 1, 1, n, p, p, -128, 127, 0, None)
