@@ -5,14 +5,16 @@
 //
 // Reference: forwardWithCalibrationCPU (operators/quant-gru/src/gru_forward_cpu.cc:58-151)
 // and its GPU counterpart forwardWithCalibrationGPU (src/gru_interface.cc:930-1024).
-// One workgroup per sequence keeps h in LDS and walks the T steps; the two linears use
-// the reference's sequential fp32 summation order (sum over k, then + bias), sigmoid is
-// evaluated in double as the reference's CPU template does, so h, v and the statistics
-// match the CPU reference up to the device's tanhf/exp last-ulp behaviour.  Statistics
-// of the 13 activations ignore non-finite values, are reduced with atomic min/max on
-// order-preserving integer images of the floats and then merged into the caller's
-// running ranges; per-channel ranges of W, R, bw and br are reduced
-// by a separate kernel.
+// Main form (H a multiple of 16 up to 1024): the input projection of every step as one fp32
+// MFMA GEMM (calib_gemm.h) and the recurrence as a clustered persistent kernel with R resident
+// in VGPRs, the 13 activation ranges observed in registers and folded from per-workgroup
+// partials.  Fallback (other H) and the float forward: one workgroup per sequence keeps h in
+// LDS and walks the T steps with the reference's sequential fp32 summation order (sum over k,
+// then + bias) and sigmoid in double, as the reference's CPU template does; its statistics
+// are reduced with atomic min/max on order-preserving integer images of the floats.  Either
+// way non-finite values are not observed, this call's ranges are merged into the caller's
+// running ones, and the per-channel ranges of W, R, bw and br come from calib_params_part /
+// calib_params_fold.
 #include <cfloat>
 #include <cstdlib>
 

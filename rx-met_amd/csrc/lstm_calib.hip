@@ -4,9 +4,11 @@
 // Reference: CalibrationSession.collect -> LstmCalibrationCollector::collect
 // (src/lstm/calibration.cc:154-240) over lstmForwardFloatCpu (src/lstm/forward_float_cpu.cc:
 // 57-153); the CUDA session runs the same observation set on device traces
-// (src/lstm/calibration_cuda.cu:372-480).  One workgroup per sequence keeps h and c in LDS
-// and walks the T steps with the reference's summation order (bias first, then the
-// products in index order); exp and tanh are evaluated in double and rounded once to float.
+// (src/lstm/calibration_cuda.cu:372-480).  Main form (H a multiple of 16 up to 512): the
+// input projection on fp32 MFMA (calib_gemm.h) and a clustered recurrence with W_hh resident
+// in VGPRs.  Fallback (other H): one workgroup per sequence keeps h and c in LDS and walks
+// the T steps with the reference's summation order (bias first, then the products in index
+// order).  In both, exp and tanh are evaluated in double and rounded once to float.
 // Observed: x, h (h0 or zeros, then every h_t), c (c0 or zeros, then every c_t), both
 // linears, the four gate inputs and outputs, tanh(c), and per-channel parameter ranges.
 // Non-finite values are counted (the reference rejects them) instead of entering a range.
