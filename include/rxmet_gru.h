@@ -326,9 +326,26 @@ int rxmet_gru_forward_quant_dirs_codes(int32_t ndir, int32_t is_training, int32_
  * rxmet_gru_forward_quant_dirs_codes instead of dirs[k].v and the five per-step mask families
  * (which may be null).
  */
+/*
+ * A direction's incoming gradient read in place from the layer's output gradient instead of a
+ * dh_new buffer [T+1, B, H]: row s + 1 of dh_new is g at element (t, b, col0 + j), t = s (or
+ * T - 1 - s for a reverse direction), element (t, b, k) at g[t st + b sb + k sk] (any strides,
+ * zero included), plus g_hn[b H + j] (the gradient of the direction's h_n, [B, H] contiguous)
+ * at s = T - 1; row 0 is zero.  g or g_hn may be null (zero).  No counterpart in the reference,
+ * which builds dh_new with tensor copies (quant_gru.py:2207-2288).
+ */
+typedef struct rxmet_gru_grad_view {
+  const float *g;
+  int64_t st, sb, sk;
+  int32_t col0, reverse;
+  const float *g_hn;
+} rxmet_gru_grad_view;
+
+/* views: null, or one per direction (dirs[k].dh_new is then not read and may be null). */
 int rxmet_gru_backward_quant_dirs_codes(int32_t ndir, int32_t T, int32_t B, int32_t I, int32_t H,
                                         const rxmet_gru_bwd_dir *dirs, int32_t flags,
-                                        const rxmet_gru_saved_codes *codes, void *stream);
+                                        const rxmet_gru_saved_codes *codes,
+                                        const rxmet_gru_grad_view *views, void *stream);
 
 /*
  * Quantised forward, int32 carrier: quantGRUForwardInt (src/gru_interface.cc:443-559) behind

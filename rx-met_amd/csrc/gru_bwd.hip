@@ -98,6 +98,10 @@ struct BwdArgs {
   // does not read them): v_codes [T, B, 4H] and mask_bits [T, B, H] of the forward; field q
   // of v is (v_codes - vzl[q]) * veff[q], vzl = zero point - grid minimum
   const uint16_t *vc, *mb;
+  // dh_new read in place from the layer's output gradient (rxmet_gru_grad_view), when gv_on
+  const float *gv, *gv_hn;
+  int64_t gv_t, gv_b, gv_k;
+  int gv_col0, gv_rev, gv_on;
   float vzl[4], veff[4];
 };
 
@@ -384,7 +388,17 @@ __device__ __forceinline__ void bwd_load_step(const BwdArgs &a, const BwdMasks &
   const uint32_t tH = static_cast<uint32_t>(t) * BH;
   const uint32_t m = 3u * tH + 3u * static_cast<uint32_t>(b) * H + j;
   const uint32_t v0 = 4u * tH + 4u * static_cast<uint32_t>(b) * H + j;
-  r[0] = a.dh_new[tH + BH + oH];
+  if (a.gv_on) {
+    float g = 0.0f;
+    if (a.gv) {
+      const int64_t tt = a.gv_rev ? a.T - 1 - t : t;
+      g = a.gv[tt * a.gv_t + b * a.gv_b + (a.gv_col0 + j) * a.gv_k];
+    }
+    if (t == a.T - 1 && a.gv_hn) g += a.gv_hn[oH];
+    r[0] = g;
+  } else {
+    r[0] = a.dh_new[tH + BH + oH];
+  }
   r[1] = a.h[tH + oH];
   if (a.vc) {
     // blocked codes: block ((t ceil(B/16) + b / 16) H/16 + j / 16) of 16 rows x 16 units, v as
@@ -827,11 +841,11 @@ struct BwdPlan {
 
 static int backward_prologue(int T, int B, int I, int H, const rxmet_gru_bwd_dir &d,
                              const rxmet_gru_saved_codes *codes, hipStream_t stream,
-                             BwdPlan *plan) {
+                             BwdPlan *plan, const rxmet_gru_grad_view *view = nullptr) {
   const rxmet_gru_qparams *params = d.params;
   RXMET_CHECK_ARG(params != nullptr, "params must be non-null");
   RXMET_CHECK_ARG(params->hidden == H, "params.hidden != hidden_size");
-  RXMET_CHECK_ARG(d.W_q && d.R_q && d.x_q && d.dh_new && d.h && (codes || d.v) && d.dx && d.dW &&
+  RXMET_CHECK_ARG(d.W_q && d.R_q && d.x_q && (view || d.dh_new) && d.h && (codes || d.v) && d.dx && d.dW &&
                       d.dR && d.dbw && d.dbr && d.dh0 && d.workspace,
                   "required pointer is null");
   RXMET_CHECK_ARG(!codes || (codes->v_codes && codes->mask_bits),
@@ -896,6 +910,13 @@ static int backward_prologue(int T, int B, int I, int H, const rxmet_gru_bwd_dir
   BwdArgs &ba = plan->ba;
   ba.T = T; ba.B = B; ba.H = H; ba.KS2 = KS2;
   ba.dh_new = d.dh_new; ba.h = d.h; ba.v = d.v;
+  ba.gv_on = view != nullptr;
+  if (view) {
+    RXMET_CHECK_ARG(view->col0 >= 0, "grad view: col0 must be non-negative");
+    ba.gv = view->g; ba.gv_hn = view->g_hn;
+    ba.gv_t = view->st; ba.gv_b = view->sb; ba.gv_k = view->sk;
+    ba.gv_col0 = view->col0; ba.gv_rev = view->reverse != 0;
+  }
   ba.ih_m = d.ih_mask; ba.hh_m = d.hh_mask; ba.gin_m = d.gate_in_mask; ba.gout_m = d.gate_out_mask;
   ba.h_m = d.h_mask; ba.bw_m = d.bw_mask; ba.br_m = d.br_mask; ba.h0_m = d.h0_mask;
   ba.vc = nullptr; ba.mb = nullptr;
@@ -1130,7 +1151,8 @@ static int backward_epilogue(int T, int B, int I, int H, BwdPlan &plan, hipStrea
 
 static int backward_dirs(int ndir, int T, int B, int I, int H, const rxmet_gru_bwd_dir *dirs,
                          bool torch_layout, hipStream_t stream,
-                         const rxmet_gru_saved_codes *codes = nullptr) {
+                         const rxmet_gru_saved_codes *codes = nullptr,
+                         const rxmet_gru_grad_view *views = nullptr) {
   RXMET_CHECK_ARG(ndir == 1 || ndir == 2, "ndir must be 1 or 2");
   RXMET_CHECK_ARG(dirs != nullptr, "dirs must be non-null");
   RXMET_CHECK_ARG(T >= 1 && B >= 1 && I >= 1 && H >= 1, "dimensions must be positive");
@@ -1141,7 +1163,7 @@ static int backward_dirs(int ndir, int T, int B, int I, int H, const rxmet_gru_b
   BwdPlan plans[2];
   for (int k = 0; k < ndir; ++k)
     if (int rc = backward_prologue(T, B, I, H, dirs[k], codes ? &codes[k] : nullptr, stream,
-                                   &plans[k]))
+                                   &plans[k], views ? &views[k] : nullptr))
       return rc;
   for (int k = 0; k < ndir; ++k) plans[k].torch_layout = torch_layout;
   // H > 256 (more R values than the clustered and per-tile kernels keep in registers), or
@@ -1230,11 +1252,12 @@ int rxmet_gru_backward_quant_dirs_x(int32_t ndir, int32_t T, int32_t B, int32_t 
 
 int rxmet_gru_backward_quant_dirs_codes(int32_t ndir, int32_t T, int32_t B, int32_t I, int32_t H,
                                         const rxmet_gru_bwd_dir *dirs, int32_t flags,
-                                        const rxmet_gru_saved_codes *codes, void *stream_) {
+                                        const rxmet_gru_saved_codes *codes,
+                                        const rxmet_gru_grad_view *views, void *stream_) {
   clear_error();
   RXMET_CHECK_ARG(codes != nullptr, "codes must be non-null");
   return backward_dirs(ndir, T, B, I, H, dirs, (flags & 1) != 0,
-                       static_cast<hipStream_t>(stream_), codes);
+                       static_cast<hipStream_t>(stream_), codes, views);
 }
 
 }  // extern "C"

@@ -627,13 +627,35 @@ def forward_quant_codes_dirs(is_training, time_steps, batch_size, input_size, hi
     return [m[0] for m in made]
 
 
+def grad_views(g_out, g_hn, T, B, H, batch_first: bool, ndir: int):
+    """Each direction's rxmet_gru_grad_view of the layer's output gradient ([T, B, D H], or
+    [B, T, D H] batch-first; any strides, or None) and of the h_n gradient [D, B, H] (or None):
+    the backward reads its dh in place instead of a dh_new buffer.  Returns (views, keep)."""
+    gp, st, sb, sk = None, 0, 0, 0
+    if g_out is not None:
+        _check_f32_cuda("grad_output", g_out)
+        gp = g_out.data_ptr()
+        st, sb = (g_out.stride(1), g_out.stride(0)) if batch_first else (g_out.stride(0),
+                                                                          g_out.stride(1))
+        sk = g_out.stride(2)
+    hp = None
+    if g_hn is not None and g_hn.numel() > 0:
+        _check_f32_cuda("grad_h_n", g_hn)
+        g_hn = g_hn.contiguous()
+        hp = g_hn.data_ptr()
+    views = [A.GradView(gp, st, sb, sk, k * H, k, None if hp is None else hp + 4 * k * B * H)
+             for k in range(ndir)]
+    return views, (g_out, g_hn)
+
+
 def backward_quant_codes_dirs(time_steps, batch_size, input_size, hidden_size, dirs,
-                              torch_layout=True):
+                              torch_layout=True, views=None):
     """The backward of forward_quant_codes_dirs (rxmet_gru_backward_quant_dirs_codes): ``dirs``
     is a list of (W_q, R_q, bw_q, br_q, x_q, dh_new, h, v_codes, quant_params, masks) with
     masks = (x_mask, h0_mask, W_mask, R_mask, bw_mask, br_mask, mask_bits); returns one
     (dx, dW, dR, dbw, dbr, dh) tuple per direction, the weight gradients in PyTorch's layout
-    and gate order unless ``torch_layout`` is False."""
+    and gate order unless ``torch_layout`` is False.  With ``views`` (grad_views), each
+    direction reads its dh from the output gradient and its dh_new entry may be None."""
     T, B, I, H = time_steps, batch_size, input_size, hidden_size
     made, codes = [], []
     Bp = (B + 15) // 16 * 16
@@ -650,8 +672,13 @@ def backward_quant_codes_dirs(time_steps, batch_size, input_size, hidden_size, d
         codes.append(A.SavedCodes(vc.data_ptr(), mb.data_ptr()))
     arr = (A.BwdDir * len(made))(*[m[1] for m in made])
     carr = (A.SavedCodes * len(made))(*codes)
+    varr = None
+    if views is not None:
+        if len(views) != len(made):
+            raise RuntimeError("one grad view per direction")
+        varr = (A.GradView * len(made))(*views)
     _rx.call("rxmet_gru_backward_quant_dirs_codes", len(made), T, B, I, H, arr,
-             1 if torch_layout else 0, carr, _stream(dirs[0][4].device))
+             1 if torch_layout else 0, carr, varr, _stream(dirs[0][4].device))
     return [m[0] for m in made]
 
 
@@ -723,7 +750,7 @@ def _backward_dir(T, B, I, H, W_q, R_q, bw_q, br_q, x_q, dh_new, h, v, quant_par
                       ("br_q", br_q, (C,)), ("x_q", x_q, (T, B, I)),
                       ("dh_new", dh_new, (T + 1, B, H)), ("h", h, (T + 1, B, H)),
                       ("v", v, (T, B, 4 * H))):
-        if t is None and n == "v":  # saved codes instead (backward_quant_codes_dirs)
+        if t is None and n in ("v", "dh_new"):  # saved codes / a grad view instead
             continue
         _check_f32_cuda(n, t)
         if tuple(t.shape) != shp:
@@ -734,10 +761,11 @@ def _backward_dir(T, B, I, H, W_q, R_q, bw_q, br_q, x_q, dh_new, h, v, quant_par
             torch.empty((C, H) if torch_layout else (H, C), **f32),
             torch.empty((C,), **f32), torch.empty((C,), **f32), torch.empty((B, H), **f32))
     mp = [m.data_ptr() if (m is not None and m.numel() > 0) else None for m in masks]
-    dh_new = dh_new.contiguous()
+    dh_new = dh_new.contiguous() if dh_new is not None else None
     ws = _ws(_rx.load().rxmet_gru_backward_workspace_bytes(T, B, I, H), dev)
     d = A.BwdDir(W_q.data_ptr(), R_q.data_ptr(), bw_q.data_ptr(), br_q.data_ptr(), x_q.data_ptr(),
-                 dh_new.data_ptr(), h.data_ptr(), v.data_ptr() if v is not None else None,
+                 dh_new.data_ptr() if dh_new is not None else None, h.data_ptr(),
+                 v.data_ptr() if v is not None else None,
                  ctypes.addressof(quant_params.struct), *mp, *[o.data_ptr() for o in outs],
                  ws.data_ptr())
     return outs, d, (ws, dh_new)

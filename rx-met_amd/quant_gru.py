@@ -511,18 +511,20 @@ class GRUFunction(torch.autograd.Function):
         saved = ctx.saved_tensors
         W_q, R_q, bw_q, br_q, x_q, h, v = saved[:7]
         masks = saved[7:]
+        if ctx.codes:
+            # dh read in place from grad_output / grad_h_n (no dh_new buffer)
+            views, _keep = gru_ops.grad_views(grad_output, grad_h_n, T, B, H, False, 1)
+            dx, dW, dR, dbw, dbr, dh = gru_ops.backward_quant_codes_dirs(
+                T, B, I, H, [(W_q, R_q, bw_q, br_q, x_q, None, h, v, ctx.quant_params,
+                              masks)], views=views)[0]
+            return (dx, dW, dR, None if ctx.bias_none[0] else dbw,
+                    None if ctx.bias_none[1] else dbr, None if ctx.h0_is_none else dh,
+                    None, None, None, None)
         dh_new = torch.zeros((T + 1, B, H), device=h.device, dtype=torch.float32)
         if grad_output is not None:
             dh_new[1:] = grad_output
         if grad_h_n is not None and grad_h_n.numel() > 0:
             dh_new[-1] += grad_h_n[0]
-        if ctx.codes:
-            dx, dW, dR, dbw, dbr, dh = gru_ops.backward_quant_codes_dirs(
-                T, B, I, H, [(W_q, R_q, bw_q, br_q, x_q, dh_new, h, v, ctx.quant_params,
-                              masks)])[0]
-            return (dx, dW, dR, None if ctx.bias_none[0] else dbw,
-                    None if ctx.bias_none[1] else dbr, None if ctx.h0_is_none else dh,
-                    None, None, None, None)
         backward_fn = (gru_ops.backward_quant_int_storage if ctx.quant_storage_dtype == "int32"
                        else gru_ops.backward_quant_float_storage)
         dx, dW, dR, dbw, dbr, dh = backward_fn(
@@ -602,15 +604,22 @@ class GRUBidirectionalFunction(torch.autograd.Function):
         T, B, I, H = ctx.dims
         saved = ctx.saved_tensors
         n = len(saved) // 2
-        dh_f, dh_r, _ = gru_ops.bidir_split_grad(g_out, g_hn, T, B, H, ctx.batch_first,
-                                                 saved[5].device)
+        if ctx.codes:
+            # each direction reads its dh in place from g_out / g_hn (no split copies)
+            views, _keep = gru_ops.grad_views(g_out, g_hn, T, B, H, ctx.batch_first, 2)
+            dhs = (None, None)
+        else:
+            views = None
+            dh_f, dh_r, _ = gru_ops.bidir_split_grad(g_out, g_hn, T, B, H, ctx.batch_first,
+                                                     saved[5].device)
+            dhs = (dh_f, dh_r)
         dirs = []
-        for k, dh_new in enumerate((dh_f, dh_r)):
+        for k, dh_new in enumerate(dhs):
             W_q, R_q, bw_q, br_q, x_q, h, v = saved[k * n:k * n + 7]
             masks = saved[k * n + 7:(k + 1) * n]
             dirs.append((W_q, R_q, bw_q, br_q, x_q, dh_new, h, v, ctx.quant_params[k], masks))
         # weight gradients come back in PyTorch's layout and gate order
-        res = (gru_ops.backward_quant_codes_dirs(T, B, I, H, dirs) if ctx.codes
+        res = (gru_ops.backward_quant_codes_dirs(T, B, I, H, dirs, views=views) if ctx.codes
                else gru_ops.backward_quant_float_storage_dirs_x(T, B, I, H, dirs))
         grads = []
         for k, (dx, dW, dR, dbw, dbr, dh) in enumerate(res):

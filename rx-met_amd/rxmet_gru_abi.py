@@ -99,6 +99,12 @@ class SavedCodes(ctypes.Structure):
     _fields_ = [("v_codes", _p), ("mask_bits", _p)]
 
 
+class GradView(ctypes.Structure):
+    """rxmet_gru_grad_view: a direction's dh read in place from the layer's output gradient."""
+    _fields_ = [("g", _p), ("st", ctypes.c_int64), ("sb", ctypes.c_int64), ("sk", ctypes.c_int64),
+                ("col0", ctypes.c_int32), ("reverse", ctypes.c_int32), ("g_hn", _p)]
+
+
 _SIGS = {
     "rxmet_gru_make_params": (ctypes.c_int, [ctypes.POINTER(GruRanges), ctypes.POINTER(GruConfig),
                                              ctypes.POINTER(GruQParams)]),
@@ -129,7 +135,8 @@ _SIGS = {
     "rxmet_gru_forward_quant_dirs_codes": (ctypes.c_int, [_i32] * 6 + [ctypes.POINTER(FwdDir), _p,
                                                                      ctypes.POINTER(SavedCodes), _p]),
     "rxmet_gru_backward_quant_dirs_codes": (ctypes.c_int, [_i32] * 5 + [ctypes.POINTER(BwdDir), _i32,
-                                                                      ctypes.POINTER(SavedCodes), _p]),
+                                                                      ctypes.POINTER(SavedCodes),
+                                                                      ctypes.POINTER(GradView), _p]),
 }
 for _name, (_res, _args) in _SIGS.items():
     _rx.register(_name, _res, _args)

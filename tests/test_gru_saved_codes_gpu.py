@@ -86,9 +86,12 @@ def test_saved_codes_decode_to_reference_format_and_gradients_equal(cuda, case):
 
 
 @pytest.mark.parametrize("bidirectional", [False, True])
-def test_module_gradients_equal_with_and_without_saved_codes(cuda, monkeypatch, bidirectional):
-    """QuantGRU training step (c3 grids) with the saved state as codes and in the reference
-    format: output and every parameter and input gradient bit for bit."""
+@pytest.mark.parametrize("loss", ["square_mean", "sum"])
+def test_module_gradients_equal_with_and_without_saved_codes(cuda, monkeypatch, bidirectional,
+                                                             loss):
+    """QuantGRU training step (c3 grids) with the saved state as codes (dh read in place from the
+    output gradient: a dense one, and the zero-stride one of a sum) and in the reference format
+    (dh_new built by copies): output and every parameter and input gradient bit for bit."""
     torch.manual_seed(3)
     T, B, I, H = 6, 37, 12, 64
     m = QG.QuantGRU(I, H, batch_first=True, bidirectional=bidirectional)
@@ -108,7 +111,10 @@ def test_module_gradients_equal_with_and_without_saved_codes(cuda, monkeypatch, 
         xl = x.clone().requires_grad_(True)
         hl = h0.clone().requires_grad_(True)
         out, hn = m(xl, hl)
-        (out.square().mean() + hn.sum()).backward()
+        if loss == "sum":
+            (out.sum() + 0.5 * hn.sum()).backward()
+        else:
+            (out.square().mean() + hn.sum()).backward()
         torch.cuda.synchronize()
         res.append([out.detach(), hn.detach(), xl.grad, hl.grad] +
                    [p.grad.clone() for p in m.parameters()])
