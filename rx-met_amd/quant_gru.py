@@ -434,7 +434,9 @@ def _codes_fit(quant_params) -> bool:
 
 class GRUFunction(torch.autograd.Function):
     """One direction of a quantised GRU.  forward: weight reorder -> forward_quant_float_storage
-    (or forward_quant_int_storage for quant_storage_dtype='int32'); backward: dh_new [T+1,B,H]
+    (or forward_quant_int_storage for quant_storage_dtype='int32'; inference on the FP32
+    carrier and training with the state saved as codes read PyTorch's weight layout in the
+    library instead); backward: dh_new [T+1,B,H]
     (dh_new[0]=0, dh_new[1:]=grad_output, grad_h_n added to the last step) ->
     backward_quant_float_storage (backward_quant_int_storage) -> gradients reordered back to
     (r, z, n)."""
@@ -465,8 +467,11 @@ class GRUFunction(torch.autograd.Function):
                 else torch.empty(0, device=device, dtype=torch.float32))
         ctx.codes = bool(is_training and quant_storage_dtype == "float32" and H % 16 == 0
                          and SAVE_STATE_AS_CODES and _codes_fit(quant_params))
-        if ctx.codes:
-            # weights read in PyTorch's layout by the library; saved state as codes
+        # inference on the FP32 carrier reads the weights as they are too (no reorder kernels)
+        eval_torch_w = (not is_training and quant_storage_dtype == "float32"
+                        and H % 16 == 0)
+        if ctx.codes or eval_torch_w:
+            # weights read in PyTorch's layout by the library; in training the state saved as codes
             W = ensure_cuda_float32(weight_ih, device).contiguous()
             R = ensure_cuda_float32(weight_hh, device).contiguous()
             if bias_ih is not None and bias_hh is not None:
@@ -474,9 +479,10 @@ class GRUFunction(torch.autograd.Function):
                 br = ensure_cuda_float32(bias_hh, device).contiguous()
             else:
                 bw = br = _zeros(3 * H, device)
-            outs = gru_ops.forward_quant_codes_dirs(
-                True, T, B, I, H, [(W, R, bw, br, input, h0_t, quant_params)],
-                [(B * I, I, 0, 1)])[0]
+            fwd = (gru_ops.forward_quant_codes_dirs if ctx.codes
+                   else gru_ops.forward_quant_float_storage_dirs_x)
+            outs = fwd(bool(is_training), T, B, I, H, [(W, R, bw, br, input, h0_t, quant_params)],
+                       [(B * I, I, 0, 1)])[0]
         else:
             W, R, bw, br = convert_weights_to_haste_format(weight_ih, weight_hh, bias_ih, bias_hh,
                                                            H, device)
