@@ -462,14 +462,17 @@ class GRUFunction(torch.autograd.Function):
             raise ValueError(f"quant_storage_dtype must be 'float32' or 'int32', got "
                              f"{quant_storage_dtype}")
         device = _require_device(input)
-        input = ensure_cuda_float32(input, device).contiguous()
+        # inference on the FP32 carrier reads the weights as they are too (no reorder kernels),
+        # and x in place when its feature stride is 1 (a batch-first caller's transposed view)
+        eval_torch_w = (not is_training and quant_storage_dtype == "float32"
+                        and H % 16 == 0)
+        input = ensure_cuda_float32(input, device)
+        if not (eval_torch_w and input.stride(2) == 1):
+            input = input.contiguous()
         h0_t = (ensure_cuda_float32(h0, device).contiguous() if h0 is not None
                 else torch.empty(0, device=device, dtype=torch.float32))
         ctx.codes = bool(is_training and quant_storage_dtype == "float32" and H % 16 == 0
                          and SAVE_STATE_AS_CODES and _codes_fit(quant_params))
-        # inference on the FP32 carrier reads the weights as they are too (no reorder kernels)
-        eval_torch_w = (not is_training and quant_storage_dtype == "float32"
-                        and H % 16 == 0)
         if ctx.codes or eval_torch_w:
             # weights read in PyTorch's layout by the library; in training the state saved as codes
             W = ensure_cuda_float32(weight_ih, device).contiguous()
@@ -482,7 +485,7 @@ class GRUFunction(torch.autograd.Function):
             fwd = (gru_ops.forward_quant_codes_dirs if ctx.codes
                    else gru_ops.forward_quant_float_storage_dirs_x)
             outs = fwd(bool(is_training), T, B, I, H, [(W, R, bw, br, input, h0_t, quant_params)],
-                       [(B * I, I, 0, 1)])[0]
+                       [(input.stride(0), input.stride(1), 0, 1)])[0]
         else:
             W, R, bw, br = convert_weights_to_haste_format(weight_ih, weight_hh, bias_ih, bias_hh,
                                                            H, device)
@@ -1282,7 +1285,10 @@ class QuantGRU(nn.Module):
                 and self.quant_storage_dtype == "float32" and self.hidden_size % 16 == 0):
             return self._forward_bidirectional(input, hx)
         if self.batch_first:
-            input = input.transpose(0, 1).contiguous()
+            input = input.transpose(0, 1)
+            if (self.calibrating or self.bidirectional or not self.use_quantization
+                    or self.quant_storage_dtype != "float32" or self._save_state(input, hx)):
+                input = input.contiguous()  # else GRUFunction reads the [B, T, I] rows in place
         if self.calibrating:
             output, h_n = self._forward_with_calibration(input, hx)
         else:

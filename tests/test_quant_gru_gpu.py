@@ -258,6 +258,29 @@ def test_module_no_grad_eval_saves_nothing_and_matches_training(cuda):
     assert torch.equal(y_tr.detach(), y_ev) and torch.equal(h_tr.detach(), h_ev)
 
 
+@pytest.mark.parametrize("shape", [(6, 24, 10, 32), (5, 12, 6, 48), (4, 9, 7, 33)])
+@pytest.mark.parametrize("with_hx", [False, True])
+def test_batch_first_eval_reads_x_in_place_and_matches_training(cuda, shape, with_hx):
+    """Unidirectional batch-first inference reads the [B, T, I] input through its strides and
+    PyTorch-layout weights (H % 16 == 0; H = 33 takes the reordering path): the output equals
+    the training forward's on the same grids bit for bit."""
+    print(f"[quantgru bf eval] shape={shape} hx={with_hx}", flush=True)
+    m, x_tbi, hx = _module_case(False, True, with_hx, "c3", 41, shape=shape)
+    m = m.to(cuda)
+    x = x_tbi.transpose(0, 1).contiguous().to(cuda)
+    hx = hx.to(cuda) if with_hx else None
+    with m.calibration_context():
+        m(x, hx)
+    m.use_quantization = True
+    m.train()
+    y_tr, h_tr = m(x, hx)
+    m.eval()
+    with torch.no_grad():
+        y_ev, h_ev = m(x, hx)
+    assert y_ev.is_contiguous() and y_ev.shape == y_tr.shape
+    assert torch.equal(y_tr.detach(), y_ev) and torch.equal(h_tr.detach(), h_ev)
+
+
 def test_lock_keeps_grids_across_recalibration(cuda):
     m, x, _ = _module_case(False, False, False, "c3", 41)
     m = m.to(cuda)
